@@ -1,0 +1,619 @@
+// Test infrastructure only: the CPU oracle (see tlq_oracle.h). Compiled with
+// -ffp-contract=off so every a*b+c below rounds twice, as the reference's
+// x86-64 build (no FMA) does.
+#include "tlq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+// ---------------------------------------------------------------- geometry
+// ggml-common.h:194-198 (q4_0: f16 d + 16 nibble bytes), :251-255 (q8_0: f16 d
+// + 32 int8), :325-337 (q4_K: f16 d, f16 dmin, 12 packed 6-bit scale/min
+// bytes, 128 nibble bytes), :370-375 (q8_K: f32 d, 256 int8, 16 int16 sums).
+enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q8_K_B = 292 };
+
+int64_t tlq_block_elems(int type) {
+    switch (type) {
+    case TLQ_F32: case TLQ_F16: return 1;
+    case TLQ_Q4_0: case TLQ_Q8_0: return QK32;
+    case TLQ_Q4_K: case TLQ_Q8_K: return QKK;
+    default: return 0;
+    }
+}
+
+int64_t tlq_block_bytes(int type) {
+    switch (type) {
+    case TLQ_F32: return 4;
+    case TLQ_F16: return 2;
+    case TLQ_Q4_0: return Q4_0_B;
+    case TLQ_Q8_0: return Q8_0_B;
+    case TLQ_Q4_K: return Q4_K_B;
+    case TLQ_Q8_K: return Q8_K_B;
+    default: return 0;
+    }
+}
+
+int64_t tlq_row_bytes(int type, int64_t k) {
+    int64_t be = tlq_block_elems(type);
+    return be ? (k / be) * tlq_block_bytes(type) : 0;
+}
+
+int tlq_vec_dot_type(int wtype) {
+    switch (wtype) {
+    case TLQ_Q4_0: case TLQ_Q8_0: return TLQ_Q8_0;
+    case TLQ_Q4_K: return TLQ_Q8_K;
+    default: return -1;
+    }
+}
+
+// Little-endian field access on packed block bytes.
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline void wr16(uint8_t *p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
+static inline float rdf32(const uint8_t *p) { float f; memcpy(&f, p, 4); return f; }
+static inline void wrf32(uint8_t *p, float f) { memcpy(p, &f, 4); }
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bitsf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+// ------------------------------------------------------------------- fp16
+// IEEE binary16 conversions (semantics of ggml-impl.h:384-430), written from
+// the IEEE 754 encodings: half = s | e5 | m10, bias 15; float bias 127.
+float tlq_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    if (e == 0x1f) return bitsf(sign | 0x7f800000u | (m << 13) | (m ? 0x00400000u : 0));
+    if (e != 0) return bitsf(sign | ((e + (127 - 15)) << 23) | (m << 13));
+    // zero or subnormal: m * 2^-24, exact in binary32
+    return bitsf(sign | fbits((float)m * 0x1p-24f));
+}
+
+uint16_t tlq_fp32_to_fp16(float f) {
+    const uint32_t x = fbits(f);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return sign | 0x7e00u;   // NaN -> canonical quiet NaN
+    if (ax >= 0x477ff000u) return sign | 0x7c00u;  // |f| >= 65520 rounds to infinity
+    if (ax >= 0x38800000u) {                       // normal half: |f| >= 2^-14
+        const uint32_t r = ax - ((uint32_t)(127 - 15) << 23);
+        const uint32_t rounded = r + 0x0fffu + ((r >> 13) & 1u);  // round to nearest even on 13 dropped bits
+        return sign | (uint16_t)(rounded >> 13);
+    }
+    // subnormal half (or zero): count of 2^-24 units, rounded to nearest even
+    const int e = (int)(ax >> 23);
+    if (e < 102) return sign;  // |f| < 2^-25 (or a binary32 subnormal): rounds to 0
+    const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+    const int shift = 126 - e;  // value/2^-24 = mant * 2^(e-126), shift in [14, 24]
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return sign | (uint16_t)q;
+}
+
+void tlq_fp16_to_fp32_row(const uint16_t *h, float *f, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) f[i] = tlq_fp16_to_fp32(h[i]);
+}
+
+void tlq_fp32_to_fp16_row(const float *f, uint16_t *h, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) h[i] = tlq_fp32_to_fp16(f[i]);
+}
+
+// Round to nearest, ties to even, for |v| < 2^22: what ggml's nearest_int
+// (ggml-quants.c:621-626) computes with its 1.5*2^23 addend.
+static inline int round_even(float v) { return (int)rintf(v); }
+
+// ------------------------------------------------------ weight quantizers
+// ggml-quants.c:113-147. Scale from the signed value of largest magnitude
+// (first one wins ties), d = max/-8, codes trunc(x/d + 8.5) clamped to 15.
+void tlq_quantize_row_q4_0(const float *x, void *vy, int64_t k) {
+    uint8_t *y = (uint8_t *)vy;
+    for (int64_t b = 0; b < k / QK32; ++b, x += QK32, y += Q4_0_B) {
+        float amax = 0.0f, smax = 0.0f;
+        for (int j = 0; j < QK32; ++j) {
+            if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); smax = x[j]; }
+        }
+        const float d = smax / -8;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        wr16(y, tlq_fp32_to_fp16(d));
+        for (int j = 0; j < QK32 / 2; ++j) {
+            int lo = (int8_t)(x[j] * id + 8.5f);
+            int hi = (int8_t)(x[j + QK32 / 2] * id + 8.5f);
+            if (lo > 15) lo = 15;
+            if (hi > 15) hi = 15;
+            y[2 + j] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+}
+
+// make_qkx2_quants (ggml-quants.c:799-878): asymmetric 4-bit fit of n values
+// with weights: a grid fit from [min, max], then nstep+1 least-squares refits
+// with perturbed inverse scales, keeping the lowest weighted squared error.
+// Returns the scale; *neg_min receives -min.
+static float fit_scale_min(int n, int nmax, const float *x, const float *w, uint8_t *L, float *neg_min,
+                           uint8_t *Laux, float rmin, float rdelta, int nstep) {
+    float lo = x[0], hi = x[0];
+    float sw = w[0];
+    float sx = sw * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+        sw += w[i];
+        sx += w[i] * x[i];
+    }
+    if (lo > 0) lo = 0;
+    if (hi == lo) {
+        memset(L, 0, (size_t)n);
+        *neg_min = -lo;
+        return 0.0f;
+    }
+    float iscale = nmax / (hi - lo);
+    float scale = 1 / iscale;
+    float best = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = round_even(iscale * (x[i] - lo));
+        l = l < 0 ? 0 : (l > nmax ? nmax : l);
+        L[i] = (uint8_t)l;
+        float diff = scale * L[i] + lo - x[i];
+        best += w[i] * (diff * diff);
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (hi - lo);
+        float sl = 0, sl2 = 0, sxl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = round_even(iscale * (x[i] - lo));
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            Laux[i] = (uint8_t)l;
+            sl += w[i] * l;
+            sl2 += w[i] * l * l;
+            sxl += w[i] * l * x[i];
+        }
+        const float D = sw * sl2 - sl * sl;
+        if (D > 0) {
+            float s = (sw * sxl - sx * sl) / D;
+            float m = (sl2 * sx - sl * sxl) / D;
+            if (m > 0) {
+                m = 0;
+                s = sxl / sl2;
+            }
+            float err = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = s * Laux[i] + m - x[i];
+                err += w[i] * (diff * diff);
+            }
+            if (err < best) {
+                memcpy(L, Laux, (size_t)n);
+                best = err;
+                scale = s;
+                lo = m;
+            }
+        }
+    }
+    *neg_min = -lo;
+    return scale;
+}
+
+// The 12-byte q4_K scale field (ggml-quants.c:880-887): sub-blocks 0..3 keep
+// their 6-bit scale/min in the low 6 bits of bytes 0..3 / 4..7; sub-blocks
+// 4..7 keep their low 4 bits in bytes 8..11 (scale low nibble, min high
+// nibble) and their top 2 bits in bits 6..7 of bytes 0..3 / 4..7.
+static inline void q4k_scale_min(int j, const uint8_t *s, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *mn = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 0x0f) | ((s[j - 4] >> 6) << 4);
+        *mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static inline void q4k_put_scale_min(int j, uint8_t *s, int sc, int mn) {
+    if (j < 4) {
+        s[j] = (uint8_t)sc;
+        s[j + 4] = (uint8_t)mn;
+    } else {
+        s[j + 4] = (uint8_t)((sc & 0x0f) | ((mn & 0x0f) << 4));
+        s[j - 4] |= (uint8_t)((sc >> 4) << 6);
+        s[j] |= (uint8_t)((mn >> 4) << 6);
+    }
+}
+
+// ggml-quants.c:1457-1527: per 32-element sub-block an importance-weighted
+// fit (weights sqrt(mean x^2) + |x|), 6-bit quantized scales and mins against
+// the super-block maxima, then codes re-derived from the stored scales.
+void tlq_quantize_row_q4_K(const float *x, void *vy, int64_t k) {
+    uint8_t *y = (uint8_t *)vy;
+    uint8_t L[QKK], Laux[32];
+    float w[32], mins[8], scales[8];
+    for (int64_t b = 0; b < k / QKK; ++b, x += QKK, y += Q4_K_B) {
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < 8; ++j) {
+            const float *xs = x + 32 * j;
+            float s2 = 0;
+            for (int l = 0; l < 32; ++l) s2 += xs[l] * xs[l];
+            const float av = sqrtf(s2 / 32);
+            for (int l = 0; l < 32; ++l) w[l] = av + fabsf(xs[l]);
+            scales[j] = fit_scale_min(32, 15, xs, w, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+        const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+        uint8_t *sfield = y + 4;
+        for (int j = 0; j < 8; ++j) {
+            int ls = (uint8_t)round_even(inv_scale * scales[j]);
+            int lm = (uint8_t)round_even(inv_min * mins[j]);
+            if (ls > 63) ls = 63;
+            if (lm > 63) lm = 63;
+            q4k_put_scale_min(j, sfield, ls, lm);
+        }
+        const uint16_t dh = tlq_fp32_to_fp16(max_scale / 63.f);
+        const uint16_t mh = tlq_fp32_to_fp16(max_min / 63.f);
+        wr16(y, dh);
+        wr16(y + 2, mh);
+        for (int j = 0; j < 8; ++j) {
+            int sc, mn;
+            q4k_scale_min(j, sfield, &sc, &mn);
+            const float d = tlq_fp16_to_fp32(dh) * sc;
+            if (d == 0.0f) continue;
+            const float dm = tlq_fp16_to_fp32(mh) * mn;
+            for (int i = 0; i < 32; ++i) {
+                int l = round_even((x[32 * j + i] + dm) / d);
+                L[32 * j + i] = (uint8_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+            }
+        }
+        uint8_t *q = y + 16;
+        for (int c = 0; c < 4; ++c)
+            for (int l = 0; l < 32; ++l) q[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+    }
+}
+
+// -------------------------------------------------- activation quantizers
+// ggml-quants.c:276-297: symmetric int8 with d = amax/127 stored as f16, the
+// multiplier computed from the unrounded f32 d, codes roundf (ties away).
+void tlq_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
+    uint8_t *y = (uint8_t *)vy;
+    for (int64_t b = 0; b < k / QK32; ++b, x += QK32, y += Q8_0_B) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK32; ++j) {
+            const float a = fabsf(x[j]);
+            if (a > amax) amax = a;
+        }
+        const float d = amax / 127;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        wr16(y, tlq_fp32_to_fp16(d));
+        for (int j = 0; j < QK32; ++j) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+    }
+}
+
+// ggml-quants.c:2768-2804: iscale = -127/(signed value of largest magnitude,
+// first wins), codes round-half-even clamped to 127, 16-element code sums,
+// d = 1/iscale in f32. An all-zero block stores d = 0 and zero codes; the
+// reference leaves its bsums untouched there, we store zeros.
+void tlq_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
+    uint8_t *y = (uint8_t *)vy;
+    for (int64_t b = 0; b < k / QKK; ++b, x += QKK, y += Q8_K_B) {
+        float amax = 0, smax = 0;
+        for (int j = 0; j < QKK; ++j) {
+            const float a = fabsf(x[j]);
+            if (a > amax) { amax = a; smax = x[j]; }
+        }
+        int8_t *qs = (int8_t *)(y + 4);
+        if (amax == 0) {
+            wrf32(y, 0.0f);
+            memset(y + 4, 0, Q8_K_B - 4);
+            continue;
+        }
+        const float iscale = -127.f / smax;
+        for (int j = 0; j < QKK; ++j) {
+            int v = round_even(iscale * x[j]);
+            qs[j] = (int8_t)(v > 127 ? 127 : v);
+        }
+        for (int g = 0; g < 16; ++g) {
+            int s = 0;
+            for (int i = 0; i < 16; ++i) s += qs[16 * g + i];
+            int16_t s16 = (int16_t)s;
+            memcpy(y + 4 + QKK + 2 * g, &s16, 2);
+        }
+        wrf32(y, 1 / iscale);
+    }
+}
+
+int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k) {
+    switch (tlq_vec_dot_type(wtype)) {
+    case TLQ_Q8_0: tlq_quantize_row_q8_0(x, y, k); return 0;
+    case TLQ_Q8_K: tlq_quantize_row_q8_K(x, y, k); return 0;
+    default: return -1;
+    }
+}
+
+// ----------------------------------------------------------- dequantizers
+// ggml-quants.c:459-476
+void tlq_dequantize_row_q4_0(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q4_0_B, y += QK32) {
+        const float d = tlq_fp16_to_fp32(rd16(x));
+        for (int j = 0; j < 16; ++j) {
+            y[j] = ((x[2 + j] & 0x0f) - 8) * d;
+            y[j + 16] = ((x[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+// ggml-quants.c:553-565
+void tlq_dequantize_row_q8_0(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q8_0_B, y += QK32) {
+        const float d = tlq_fp16_to_fp32(rd16(x));
+        for (int j = 0; j < QK32; ++j) y[j] = (int8_t)x[2 + j] * d;
+    }
+}
+
+// ggml-quants.c:1529-1550: per 64 elements, two sub-blocks sharing 32 code
+// bytes (low nibbles first); y = (d*sc)*q - (dmin*m), rounded after each step.
+void tlq_dequantize_row_q4_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q4_K_B) {
+        const float d = tlq_fp16_to_fp32(rd16(x));
+        const float dmin = tlq_fp16_to_fp32(rd16(x + 2));
+        const uint8_t *q = x + 16;
+        for (int c = 0; c < 4; ++c, q += 32) {
+            int sc, mn;
+            q4k_scale_min(2 * c, x + 4, &sc, &mn);
+            const float d1 = d * sc, m1 = dmin * mn;
+            q4k_scale_min(2 * c + 1, x + 4, &sc, &mn);
+            const float d2 = d * sc, m2 = dmin * mn;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (q[l] & 0x0f) - m1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (q[l] >> 4) - m2;
+        }
+    }
+}
+
+void tlq_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q8_K_B, y += QKK) {
+        const float d = rdf32(x);
+        for (int j = 0; j < QKK; ++j) y[j] = d * (int8_t)x[4 + j];
+    }
+}
+
+int tlq_dequantize_row(int type, const void *x, float *y, int64_t k) {
+    switch (type) {
+    case TLQ_Q4_0: tlq_dequantize_row_q4_0(x, y, k); return 0;
+    case TLQ_Q8_0: tlq_dequantize_row_q8_0(x, y, k); return 0;
+    case TLQ_Q4_K: tlq_dequantize_row_q4_K(x, y, k); return 0;
+    case TLQ_Q8_K: tlq_dequantize_row_q8_K(x, y, k); return 0;
+    default: return -1;
+    }
+}
+
+// ----------------------------------------------------------- dot products
+// ggml-cpu/quants.c:225-258 (and the identical scalar tail of the x86 entry,
+// arch/x86/quants.c:839-853): f32 accumulation of (sumi * dx) * dy per block.
+float tlq_vec_dot_q4_0_q8_0(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float acc = 0;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q4_0_B, y += Q8_0_B) {
+        int s = 0;
+        for (int j = 0; j < 16; ++j) {
+            s += ((x[2 + j] & 0x0f) - 8) * (int8_t)y[2 + j];
+            s += ((x[2 + j] >> 4) - 8) * (int8_t)y[2 + 16 + j];
+        }
+        acc += s * tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y));
+    }
+    return acc;
+}
+
+// ggml-cpu/quants.c:451-476: f32 accumulation of sumi * (dx * dy).
+float tlq_vec_dot_q8_0_q8_0(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float acc = 0;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q8_0_B, y += Q8_0_B) {
+        int s = 0;
+        for (int j = 0; j < QK32; ++j) s += (int8_t)x[2 + j] * (int8_t)y[2 + j];
+        acc += s * (tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y)));
+    }
+    return acc;
+}
+
+void tlq_block_ints_q4_K(const void *vx, const void *vy, int32_t *sum_q, int32_t *sum_m) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    const int8_t *q8 = (const int8_t *)(y + 4);
+    int32_t sq = 0, sm = 0;
+    for (int s = 0; s < 8; ++s) {
+        int sc, mn;
+        q4k_scale_min(s, x + 4, &sc, &mn);
+        const uint8_t *q = x + 16 + 32 * (s / 2);
+        int dot = 0, sum8 = 0;
+        for (int l = 0; l < 32; ++l) {
+            const int c = (s & 1) ? (q[l] >> 4) : (q[l] & 0x0f);
+            dot += c * q8[32 * s + l];
+            sum8 += q8[32 * s + l];
+        }
+        sq += sc * dot;
+        sm += mn * sum8;
+    }
+    *sum_q = sq;
+    *sum_m = sm;
+}
+
+// ggml-cpu/quants.c:696-773. Integer part per super-block: eight int32 lane
+// accumulators (element e feeds lane e % 8) of scale_s * q4 * q8, and the min
+// correction sum_g bsums[g] * m_{g/2}. Float part: sums[lane] += (dx*dy) *
+// lane, acc -= (dminx*dy) * minsum per block, then acc += sums[0..7] in order.
+float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float lanes_f[8] = {0};
+    float acc = 0;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q4_K_B, y += Q8_K_B) {
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int32_t lanes[8] = {0};
+        int32_t msum = 0;
+        for (int g = 0; g < 16; ++g) {
+            int16_t bs;
+            memcpy(&bs, y + 4 + QKK + 2 * g, 2);
+            int sc, mn;
+            q4k_scale_min(g / 2, x + 4, &sc, &mn);
+            msum += bs * mn;
+        }
+        for (int s = 0; s < 8; ++s) {
+            int sc, mn;
+            q4k_scale_min(s, x + 4, &sc, &mn);
+            const uint8_t *q = x + 16 + 32 * (s / 2);
+            for (int l = 0; l < 32; ++l) {
+                const int c = (s & 1) ? (q[l] >> 4) : (q[l] & 0x0f);
+                lanes[l % 8] += sc * (c * q8[32 * s + l]);
+            }
+        }
+        const float dy = rdf32(y);
+        const float d = tlq_fp16_to_fp32(rd16(x)) * dy;
+        for (int l = 0; l < 8; ++l) lanes_f[l] += d * lanes[l];
+        const float dmin = tlq_fp16_to_fp32(rd16(x + 2)) * dy;
+        acc -= dmin * msum;
+    }
+    for (int l = 0; l < 8; ++l) acc += lanes_f[l];
+    return acc;
+}
+
+// -------------------------------------------------------------- mul_mat
+typedef float (*dot_fn)(int64_t, const void *, const void *);
+
+struct mm_job {
+    dot_fn dot;
+    const uint8_t *w;
+    const uint8_t *xq;
+    int64_t M, K, N, wrow, xrow;
+    float *y;
+    int64_t m0, m1;
+};
+
+static void *mm_worker(void *p) {
+    struct mm_job *j = (struct mm_job *)p;
+    for (int64_t n = 0; n < j->N; ++n)
+        for (int64_t m = j->m0; m < j->m1; ++m)
+            j->y[n * j->M + m] = j->dot(j->K, j->w + m * j->wrow, j->xq + n * j->xrow);
+    return NULL;
+}
+
+int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
+                int nthreads) {
+    dot_fn dot;
+    switch (wtype) {
+    case TLQ_Q4_0: dot = tlq_vec_dot_q4_0_q8_0; break;
+    case TLQ_Q8_0: dot = tlq_vec_dot_q8_0_q8_0; break;
+    case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
+    default: return -1;
+    }
+    const int at = tlq_vec_dot_type(wtype);
+    if (K % tlq_block_elems(wtype) != 0) return -2;
+    const int64_t xrow = tlq_row_bytes(at, K);
+    uint8_t *xq = (uint8_t *)malloc((size_t)(xrow * (N > 0 ? N : 1)));
+    if (!xq) return -3;
+    for (int64_t n = 0; n < N; ++n) tlq_quantize_act(wtype, x + n * K, xq + n * xrow, K);
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if (nthreads > M) nthreads = (int)(M > 0 ? M : 1);
+    struct mm_job jobs[256];
+    pthread_t th[256];
+    int joinable[256] = {0};
+    const int64_t per = (M + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; ++t) {
+        const int64_t m0 = t * per, m1 = (t + 1) * per < M ? (t + 1) * per : M;
+        jobs[t] = (struct mm_job){dot, (const uint8_t *)w, xq, M, K, N, tlq_row_bytes(wtype, K), xrow, y, m0, m1};
+    }
+    for (int t = 1; t < nthreads; ++t) {
+        if (jobs[t].m0 >= jobs[t].m1) continue;
+        joinable[t] = pthread_create(&th[t], NULL, mm_worker, &jobs[t]) == 0;
+        if (!joinable[t]) mm_worker(&jobs[t]);
+    }
+    mm_worker(&jobs[0]);
+    for (int t = 1; t < nthreads; ++t)
+        if (joinable[t]) pthread_join(th[t], NULL);
+    free(xq);
+    return 0;
+}
+
+// ------------------------------------------------------- paged attention
+// Key cache element (block, kv head, dim i, slot s) sits at
+// [block][kvh][i/8][s][i%8]; value cache at [block][kvh][i][s]
+// (crates/kernels/src/cuda/paged_attn.rs:9-11, x = 16 bytes / sizeof(f16) = 8).
+static inline int64_t kidx(int64_t blk, int h, int i, int s, int kvh, int hs, int bs) {
+    return (((blk * kvh + h) * (hs / 8) + i / 8) * bs + s) * 8 + (i % 8);
+}
+static inline int64_t vidx(int64_t blk, int h, int i, int s, int kvh, int hs, int bs) {
+    return ((blk * kvh + h) * (int64_t)hs + i) * bs + s;
+}
+
+int tlq_paged_attention(uint16_t *out, const uint16_t *q, const uint16_t *kc, const uint16_t *vc, int kvh,
+                        float scale, const int32_t *tables, const int32_t *lens, int max_blocks, int seqs,
+                        int heads, int hs, int bs) {
+    if (kvh <= 0 || heads % kvh != 0 || hs % 8 != 0) return -1;
+    int maxlen = 0;
+    for (int s = 0; s < seqs; ++s) maxlen = lens[s] > maxlen ? lens[s] : maxlen;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)(maxlen > 0 ? maxlen : 1));
+    float *qf = (float *)malloc(sizeof(float) * (size_t)hs);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)hs);
+    if (!logits || !qf || !acc) return -2;
+    const int group = heads / kvh;
+    for (int s = 0; s < seqs; ++s) {
+        const int L = lens[s];
+        const int32_t *bt = tables + (int64_t)s * max_blocks;
+        for (int h = 0; h < heads; ++h) {
+            const int g = h / group;
+            for (int i = 0; i < hs; ++i) qf[i] = tlq_fp16_to_fp32(q[((int64_t)s * heads + h) * hs + i]);
+            float mx = -INFINITY;
+            for (int t = 0; t < L; ++t) {
+                const int64_t blk = bt[t / bs];
+                float dot = 0;
+                for (int i = 0; i < hs; ++i) dot += qf[i] * tlq_fp16_to_fp32(kc[kidx(blk, g, i, t % bs, kvh, hs, bs)]);
+                logits[t] = scale * dot;
+                if (logits[t] > mx) mx = logits[t];
+            }
+            float sum = 0;
+            for (int t = 0; t < L; ++t) {
+                logits[t] = expf(logits[t] - mx);
+                sum += logits[t];
+            }
+            const float inv = 1.f / (sum + 1e-6f);
+            for (int i = 0; i < hs; ++i) acc[i] = 0;
+            for (int t = 0; t < L; ++t) {
+                const float p = tlq_fp16_to_fp32(tlq_fp32_to_fp16(logits[t] * inv));
+                const int64_t blk = bt[t / bs];
+                for (int i = 0; i < hs; ++i) acc[i] += p * tlq_fp16_to_fp32(vc[vidx(blk, g, i, t % bs, kvh, hs, bs)]);
+            }
+            for (int i = 0; i < hs; ++i) out[((int64_t)s * heads + h) * hs + i] = tlq_fp32_to_fp16(acc[i]);
+        }
+    }
+    free(logits);
+    free(qf);
+    free(acc);
+    return 0;
+}
+
+void tlq_reshape_and_cache(const uint16_t *key, const uint16_t *value, uint16_t *kc, uint16_t *vc,
+                           const int64_t *slots, int tokens, int kvh, int hs, int bs) {
+    for (int t = 0; t < tokens; ++t) {
+        const int64_t slot = slots[t];
+        if (slot < 0) continue;
+        const int64_t blk = slot / bs;
+        const int off = (int)(slot % bs);
+        for (int h = 0; h < kvh; ++h)
+            for (int i = 0; i < hs; ++i) {
+                kc[kidx(blk, h, i, off, kvh, hs, bs)] = key[((int64_t)t * kvh + h) * hs + i];
+                vc[vidx(blk, h, i, off, kvh, hs, bs)] = value[((int64_t)t * kvh + h) * hs + i];
+            }
+    }
+}
+
+void tlq_gather_kv(const uint16_t *kc, const uint16_t *vc, const int32_t *bt, int L, int kvh, int hs, int bs,
+                   uint16_t *k_out, uint16_t *v_out) {
+    for (int h = 0; h < kvh; ++h)
+        for (int t = 0; t < L; ++t) {
+            const int64_t blk = bt[t / bs];
+            for (int i = 0; i < hs; ++i) {
+                k_out[((int64_t)h * L + t) * hs + i] = kc[kidx(blk, h, i, t % bs, kvh, hs, bs)];
+                v_out[((int64_t)h * L + t) * hs + i] = vc[vidx(blk, h, i, t % bs, kvh, hs, bs)];
+            }
+        }
+}

@@ -1,0 +1,113 @@
+// Test infrastructure only. The CPU oracle of the quantized MUL_MAT and
+// paged-attention hot path: a plain-C restatement of the arithmetic the
+// reference runs on its CPU backend (vendored ggml) and in its paged-attention
+// kernels (vendored vLLM via crates/kernels/src/cuda/shaders). Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+// only as a checker: the product library never links or calls it.
+//
+// Every function cites the reference file:line it follows (paths relative to
+// the reference repository root). How each one is pinned (against the compiled
+// reference ggml in oracle/_ref, closed forms, invariants, brute force) is
+// recorded next to its test under tests/.
+#ifndef TLQ_ORACLE_H
+#define TLQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ggml type numbers, vendor/ggml/include/ggml.h:390-405.
+enum {
+    TLQ_F32 = 0,
+    TLQ_F16 = 1,
+    TLQ_Q4_0 = 2,
+    TLQ_Q8_0 = 8,
+    TLQ_Q4_K = 12,
+    TLQ_Q8_K = 15,
+};
+
+// Block geometry, vendor/ggml/src/ggml-common.h:89-90,194-198,251-255,325-337,370-375.
+int64_t tlq_block_elems(int type);
+int64_t tlq_block_bytes(int type);
+int64_t tlq_row_bytes(int type, int64_t k);
+// vec_dot_type of a weight type on x86 (ggml-cpu.c:239-319): Q8_0 for Q4_0
+// and Q8_0 weights, Q8_K for Q4_K; -1 otherwise.
+int tlq_vec_dot_type(int wtype);
+
+// IEEE binary16 <-> binary32 (round to nearest even), the semantics of
+// ggml_compute_fp16_to_fp32 / ggml_compute_fp32_to_fp16 (ggml-impl.h:384-430).
+float tlq_fp16_to_fp32(uint16_t h);
+uint16_t tlq_fp32_to_fp16(float f);
+void tlq_fp16_to_fp32_row(const uint16_t *h, float *f, int64_t n);
+void tlq_fp32_to_fp16_row(const float *f, uint16_t *h, int64_t n);
+
+// Weight quantizers (offline, host only; ggml_quantize_chunk with imatrix NULL):
+// quantize_row_q4_0_ref ggml-quants.c:113-147, quantize_row_q8_0_ref :276-297,
+// quantize_row_q4_K_ref :1457-1527 (make_qkx2_quants :799-878).
+void tlq_quantize_row_q4_0(const float *x, void *y, int64_t k);
+void tlq_quantize_row_q4_K(const float *x, void *y, int64_t k);
+// Activation quantizers the CPU mul_mat applies to src1
+// (ggml-cpu.c:1318-1359 with from_float of type_traits_cpu):
+// quantize_row_q8_0 -> _ref on x86 without AVX (arch/x86/quants.c:395-398,
+// ggml-quants.c:276-297); quantize_row_q8_K -> _ref (arch/x86/quants.c:505-507,
+// ggml-quants.c:2768-2804).
+void tlq_quantize_row_q8_0(const float *x, void *y, int64_t k);
+void tlq_quantize_row_q8_K(const float *x, void *y, int64_t k);
+// Quantize one activation row into the weight type's vec_dot type.
+int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k);
+
+// Dequantizers: dequantize_row_q4_0 ggml-quants.c:459-476, _q8_0 :553-565,
+// _q4_K :1529-1550; q8_K has no dequantizer on the path (d * q per element).
+void tlq_dequantize_row_q4_0(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q8_0(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q4_K(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q8_K(const void *x, float *y, int64_t k);
+int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
+
+// Dot products of one weight row with one quantized activation row:
+// ggml_vec_dot_q4_0_q8_0_generic ggml-cpu/quants.c:225-258,
+// _q8_0_q8_0_generic :451-476, _q4_K_q8_K_generic :696-773.
+float tlq_vec_dot_q4_0_q8_0(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q8_0_q8_0(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *x, const void *y);
+
+// Exact integer parts of one block product (for pinning GPU partial sums):
+// q4_K: *sum_q = sum_s sc_s * sum_{e in s} q4_e*q8_e, *sum_m = sum_s m_s * sum_{e in s} q8_e.
+void tlq_block_ints_q4_K(const void *x_block, const void *y_block, int32_t *sum_q, int32_t *sum_m);
+
+// GGML_OP_MUL_MAT on the CPU backend's algorithm (ggml-cpu.c:1254-1457 with
+// the one-chunk loop :1164-1252): quantize every activation column to the
+// vec_dot type, then y[n*M + m] = vec_dot(W row m, column n). `nthreads`
+// splits rows; the result does not depend on it.
+int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
+                int nthreads);
+
+// Paged-attention decode following the vLLM v1 kernel
+// (crates/kernels/src/cuda/shaders/pagedattention.cuh:113-486, launched by
+// crates/kernels/src/cuda/paged_attn.rs:326-417): f16 q [seqs][heads][hs],
+// key cache [blocks][kvh][hs/8][bs][8] f16, value cache [blocks][kvh][hs][bs]
+// f16, block tables i32 [seqs][max_blocks], context lens i32 [seqs]; out f16
+// [seqs][heads][hs]. Logits scale*q.k in f32, softmax with 1/(sum + 1e-6),
+// probabilities rounded to f16 before the f32 P.V accumulation, as the kernel
+// does.
+int tlq_paged_attention(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                        int num_kv_heads, float scale, const int32_t *block_tables, const int32_t *context_lens,
+                        int max_blocks, int num_seqs, int num_heads, int head_size, int block_size);
+
+// reshape_and_cache (crates/kernels/src/cuda/shaders/reshape_and_cache_kernel.cu:31-84):
+// key/value f16 [tokens][kvh*hs] scattered to slot = block*bs + offset;
+// negative slots are skipped.
+void tlq_reshape_and_cache(const uint16_t *key, const uint16_t *value, uint16_t *k_cache, uint16_t *v_cache,
+                           const int64_t *slots, int num_tokens, int num_kv_heads, int head_size, int block_size);
+// The inverse read (gather_kv_cache_kernel.cu:40): dense f16 [kvh][L][hs] K and
+// V of one sequence from its block table.
+void tlq_gather_kv(const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_table, int context_len,
+                   int num_kv_heads, int head_size, int block_size, uint16_t *k_out, uint16_t *v_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
