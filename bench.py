@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Workload: the decode GEMV sweep at 8B-class shapes,
+Q4_0 and Q4_K weights, batch 1 and 8:
+  M x K in 4096x4096, 6144x4096, 14336x4096, 4096x14336, 128256x4096.
+One "step" is one pass over all 20 (type, shape, N) GGML_OP_MUL_MAT nodes,
+each through the C ABI (activation quantization + GEMV) on its own stream
+order. Weights are resident in HBM before timing and every node rotates over
+enough distinct weight copies (>= 640 MB per node) that no launch finds its
+weights in the 256 MB Infinity Cache (MALL) or L2.
+
+value  = whole-sweep algorithmic bytes (M*row_bytes + N*K*4 + N*M*4 per node)
+         / wall time of the timed steps, GB/s.
+roofline = the dominant kernel (the Q4_K GEMV at N = 1 on the 128256 x 4096
+         lm_head shape): its algorithmic bytes / its mean duration from HIP
+         events on the launch stream, against 8 TB/s.
+cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, compiled from
+         the reference sources) on the same sweep, timed on this host.
+Also reported: an 8B Llama Q4_K bs=1 decode token rate counting only its
+matmuls (32 x (QKV, O, gate, up, down) + lm_head), from the per-node times.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode tokens/sec (8B Q4_K, bs=1) + quant GEMV HBM GB/s (% of 8 TB/s)"
+HBM_PEAK_GBS = 8000.0
+SHAPES = [(4096, 4096), (6144, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+ROTATE_BYTES = 640 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gpu_blocks(torch, wtype, M, K, gen):
+    """Structurally valid random weight blocks generated on the GPU (finite f16 scales)."""
+    from tensorlisp_amd import native as N
+
+    be, bb = N.BLOCK[wtype]
+    nb = M * (K // be)
+    raw = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device="cuda", generator=gen)
+    nscale = 2 if wtype == N.Q4_K else 1
+    d = (torch.randn((nb, nscale), device="cuda", generator=gen).abs() * (0.02 / 63)).to(torch.float16)
+    raw[:, : 2 * nscale] = d.view(torch.uint8).reshape(nb, 2 * nscale)
+    return raw.reshape(M, (K // be) * bb)
+
+
+def algorithmic_bytes(wtype, M, K, n):
+    from tensorlisp_amd import native as N
+
+    return M * N.row_bytes(wtype, K) + n * K * 4 + n * M * 4
+
+
+def cpu_baseline(host_weights, cases, seconds: float):
+    """The reference's ggml CPU backend (oracle/_ref) on the same sweep; falls back to
+    our C port of it (oracle/liboracle.so) where the reference was not built."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import numpy as np
+
+    import refs
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    threads = max(1, min(threads, 16))
+    r = refs.ref()
+    kind = "reference" if r is not None else "port"
+    xs = {c: np.random.default_rng(1).standard_normal((c[3], c[2])).astype(np.float32) for c in cases}
+    total_bytes, total_s, passes = 0, 0.0, 0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or passes == 0:
+        for c in cases:
+            t, M, K, n = c
+            if r is not None:
+                _, s = r.mul_mat(t, host_weights[(t, M, K)], M, K, xs[c], nthreads=threads)
+            else:
+                t0 = time.perf_counter()
+                refs.oracle().mul_mat(t, host_weights[(t, M, K)], M, K, xs[c], nthreads=threads)
+                s = time.perf_counter() - t0
+            total_s += s
+            total_bytes += algorithmic_bytes(t, M, K, n)
+        passes += 1
+    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{passes} pass(es) of the full 20-node sweep (same shapes, N in 1,8), "
+                      f"ggml_graph_compute wall time, {threads} threads, {total_s:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tensorlisp_amd import native as N
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    props = N.device_props(0)
+    log(f"device {props['name']} {props['arch']} CUs={props['compute_units']}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+
+    cases = [(t, M, K, n) for t in (N.Q4_0, N.Q4_K) for (M, K) in SHAPES for n in (1, 8)]
+    weights, nodes, xs, ys, bytes_per = {}, {}, {}, {}, {}
+    for t in (N.Q4_0, N.Q4_K):
+        for (M, K) in SHAPES:
+            base = gpu_blocks(torch, t, M, K, gen)
+            copies = max(2, math.ceil(ROTATE_BYTES / base.numel()))
+            weights[(t, M, K)] = [base] + [base.clone() for _ in range(copies - 1)]
+    for c in cases:
+        t, M, K, n = c
+        nodes[c] = N.MulMat(t, M, K, n)
+        xs[c] = torch.randn((n, K), device="cuda", generator=gen)
+        ys[c] = torch.empty((n, M), dtype=torch.float32, device="cuda")
+        bytes_per[c] = algorithmic_bytes(t, M, K, n)
+    torch.cuda.synchronize()
+    log(f"setup: {len(cases)} nodes, {sum(w[0].numel() * len(w) for w in weights.values()) / 2**30:.1f} GiB "
+        "of rotated weights resident")
+
+    stream = torch.cuda.current_stream()
+    ev = {c: [] for c in cases}
+
+    def step(i: int, record: bool) -> None:
+        # one MUL_MAT node = activation quantization + GEMV (tlh_mul_mat's two phases);
+        # with `record`, HIP events on the launch stream bracket the GEMV kernel alone
+        for c in cases:
+            t, M, K, _ = c
+            ws = weights[(t, M, K)]
+            nodes[c].quantize(xs[c], stream)
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+            nodes[c].compute(ws[i % len(ws)], ys[c], stream)
+            if record:
+                e1.record(stream)
+                ev[c].append((e0, e1))
+
+    for i in range(args.warmup):
+        step(i, False)
+    torch.cuda.synchronize()
+    log(f"warmup: {args.warmup} steps")
+
+    # wall-clock timed region: exactly K steps, synchronized on both sides
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, False)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    log(f"timed: {args.steps} steps in {wall * 1e3:.1f} ms")
+
+    # per-node GEMV kernel durations (a separate pass, events around each GEMV launch)
+    for i in range(args.steps):
+        step(args.warmup + args.steps + i, True)
+    torch.cuda.synchronize()
+    node_ms = {c: sum(a.elapsed_time(b) for a, b in ev[c]) / len(ev[c]) for c in cases}
+    for c in cases:
+        t, M, K, n = c
+        log(f"  {N.TYPE_NAMES[t]:5s} {M:6d}x{K:<5d} n={n}: {node_ms[c] * 1e3:8.1f} us  "
+            f"{bytes_per[c] / node_ms[c] / 1e6:7.0f} GB/s")
+
+    sweep_bytes = sum(bytes_per.values())
+    value = sweep_bytes * args.steps / wall / 1e9
+
+    dom = (N.Q4_K, 128256, 4096, 1)
+    dom_gbs = bytes_per[dom] / node_ms[dom] / 1e6
+    # matmul-only decode token rate of an 8B Llama with Q4_K weights at bs = 1
+    q = lambda M, K: node_ms[(N.Q4_K, M, K, 1)]  # noqa: E731
+    tok_ms = 32 * (q(6144, 4096) + q(4096, 4096) + 2 * q(14336, 4096) + q(4096, 14336)) + q(128256, 4096)
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("gemv_q4_K_128256x4096_n1_bytes")
+        except (ValueError, OSError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: ggml CPU backend on the same sweep (~{args.cpu_seconds:.0f} s)")
+        host_w = {k: v[0].cpu().numpy() for k, v in weights.items()}
+        cpu = cpu_baseline(host_w, cases, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.1f} GB/s ({cpu['kind']}, {cpu['cores']} threads)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "configs[1] decode GEMV sweep: {q4_0,q4_K} x {4096x4096, 6144x4096, 14336x4096, "
+                        "4096x14336, 128256x4096} x N {1, 8}; GGML_OP_MUL_MAT incl. Q8_0/Q8_K activation "
+                        "quantization; weights rotated over >= 640 MB of HBM copies per node",
+            "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+            "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "q4_K GEMV N=1, 128256x4096 (k_gemv<12,1,R>), per launch",
+            "achieved": round(dom_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,194 @@
+/*
+ * tlhip.h — C ABI of the MI355X (gfx950) executor for tensorlisp's quantized
+ * hot path: GGML_OP_MUL_MAT over GGUF block-quantized weights (Q8_0, Q4_0,
+ * Q4_K; decode GEMV for N <= 8 columns, MFMA GEMM for prefill) and
+ * paged-attention decode over an f16 block-table KV cache.
+ *
+ * This is the surface a `native-hip` feature binds from Rust
+ * (crates/kernels/src/hip/ + crates/tensorlisp/src/native_hip.rs), in place of
+ * the NVRTC launcher of crates/kernels/src/cuda/{mod,exec,lower}.rs. Plain C:
+ * pointers, sizes and PODs; no torch or HIP types in the signatures (a stream
+ * is an opaque `void*` that is a hipStream_t, NULL = the null stream).
+ *
+ * Conventions (mirroring crates/kernels/src/lib.rs:44-61 and
+ * crates/kernels/src/cuda/mod.rs):
+ *  - every call returns a tlh_status; tlh_last_error() gives this thread's
+ *    text for the last failure;
+ *  - work calls are stream-ordered and asynchronous; nothing allocates behind
+ *    the caller's back except where a function says so (tlh_alloc);
+ *  - device pointers are plain device addresses on the current device.
+ */
+#ifndef TLHIP_H
+#define TLHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error kinds of tensorlisp_kernels::Error (crates/kernels/src/lib.rs:44-61):
+ * NoDevice, Unsupported{op,node,why}, Invalid, Alloc(bytes), Execution(msg). */
+typedef enum tlh_status {
+    TLH_OK = 0,
+    TLH_NO_DEVICE = 1,
+    TLH_UNSUPPORTED = 2,
+    TLH_INVALID = 3,
+    TLH_ALLOC = 4,
+    TLH_EXECUTION = 5
+} tlh_status;
+
+/* ggml type numbers (vendor/ggml/include/ggml.h:390-405). */
+enum {
+    TLH_TYPE_F32 = 0,
+    TLH_TYPE_F16 = 1,
+    TLH_TYPE_Q4_0 = 2,
+    TLH_TYPE_Q8_0 = 8,
+    TLH_TYPE_Q4_K = 12,
+    TLH_TYPE_Q8_K = 15
+};
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+const char *tlh_last_error(void);
+const char *tlh_status_name(tlh_status s);
+/* Library version string, e.g. "tlhip 0.1 gfx950". */
+const char *tlh_version(void);
+
+/* ------------------------------------------------------------------ device
+ * Replaces Device::system_default / name (crates/kernels/src/cuda/mod.rs:244-277):
+ * TLH_NO_DEVICE when no GPU is present (not fatal at probe time). Opening
+ * makes the device current on the calling thread. */
+typedef struct tlh_device_props {
+    char name[64];
+    char arch[32];       /* e.g. "gfx950" */
+    int compute_units;
+    int wave_size;       /* 64 on CDNA */
+    int lds_bytes;       /* per workgroup */
+    int clock_khz;
+    int64_t hbm_bytes;
+} tlh_device_props;
+
+tlh_status tlh_device_count(int *count);
+tlh_status tlh_device_open(int ordinal, tlh_device_props *props);
+
+/* ------------------------------------------------------------------ memory
+ * Replaces Buffer (crates/kernels/src/cuda/mod.rs:39-133): alloc/free and
+ * blocking copies, plus a stream-ordered sync (mod.rs:544-548). */
+tlh_status tlh_alloc(size_t bytes, void **ptr);
+tlh_status tlh_free(void *ptr);
+tlh_status tlh_h2d(void *dst, const void *src, size_t bytes);
+tlh_status tlh_d2h(void *dst, const void *src, size_t bytes);
+tlh_status tlh_stream_sync(void *stream);
+
+/* ---------------------------------------------------------- op descriptor
+ * struct T / struct Op of crates/kernels/src/cuda/native/common.cuh:14-26, as
+ * packed by OpBlob (crates/kernels/src/cuda/lower.rs:67-99): 5 tensors (slots
+ * 0..3 sources, 4 the destination) of ggml ne/nb/type, then 12 scalar slots
+ * (ints, or floats as their bit pattern). 456 bytes. */
+typedef struct tlh_tensor {
+    int64_t ne[4];
+    int64_t nb[4];
+    int32_t ty;
+    int32_t pad_;
+} tlh_tensor;
+
+typedef struct tlh_op {
+    tlh_tensor t[5];
+    int64_t x[12];
+} tlh_op;
+
+/* --------------------------------------------------------------- MUL_MAT
+ * GGML_OP_MUL_MAT, replacing Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
+ * and its mm_vec / mm_tile kernels (crates/kernels/src/cuda/native/mm.cu:16-103),
+ * computed the way the ggml CPU backend does (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457):
+ *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K, ne [K, M, ne02, ne03],
+ *                  nb[0] = block bytes (rows must not be transposed);
+ *   op->t[1] src1: f32 activations, ne [K, N, ne12, ne13], nb[0] = 4;
+ *   op->t[4] dst:  f32 [M, N, ne12, ne13], nb[0] = 4;
+ *   op->x[0] = r2 = ne12 / ne02, op->x[1] = r3 = ne13 / ne03 (broadcast).
+ * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0 and
+ * Q8_0, Q8_K for Q4_K) into `scratch` (at least tlh_mul_mat_scratch_bytes);
+ * then N <= 8 runs the decode GEMV, larger N the int8-MFMA GEMM. Integer block
+ * sums are exact; the f32 result agrees with the CPU backend to rounding of
+ * the f32 accumulation order. TLH_UNSUPPORTED (with the reason in
+ * tlh_last_error) for any other type or layout. */
+tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes);
+tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,
+                       size_t scratch_bytes, void *stream);
+
+/* The two phases of tlh_mul_mat, which the CPU backend separates with a
+ * barrier (ggml-cpu.c:1318-1359 quantize src1 into wdata; :1366 barrier;
+ * :1426-1451 the dot products). Splitting them lets an executor quantize an
+ * activation once for several weights that consume it (e.g. Q, K and V
+ * projections of one input: same src1 shape and weight type, one scratch).
+ * tlh_mul_mat_compute reads the scratch a matching tlh_mul_mat_quantize
+ * filled (same op shape for src1, same vec_dot type). */
+tlh_status tlh_mul_mat_quantize(const tlh_op *op, const void *src1, void *scratch, size_t scratch_bytes,
+                                void *stream);
+tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *scratch, size_t scratch_bytes,
+                               void *dst, void *stream);
+
+/* Activation quantizer alone: `rows` rows of `k` f32 (row stride x_row_bytes)
+ * into ggml's block layout of the vec_dot type of `wtype` — the from_float the
+ * CPU mul_mat applies (quantize_row_q8_0 / quantize_row_q8_K:
+ * vendor/ggml/src/ggml-cpu/arch/x86/quants.c:302-398, :505-507), bit-exact.
+ * Output: rows * row_size(vec_dot_type, k) bytes, rows packed. A block whose
+ * values are all zero gets d = 0, zero codes and zero bsums (the reference
+ * leaves a zero Q8_K block's bsums unwritten). */
+tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, int64_t x_row_bytes, void *y,
+                            void *stream);
+
+/* dequantize_row_{q4_0,q8_0,q4_K} (vendor/ggml/src/ggml-quants.c:459-476,
+ * :553-565, :1529-1550), bit-exact: `rows` rows of `k` elements (row stride
+ * w_row_bytes) into f32 [rows][k]. The to_f32 of DType (crates/tensorlisp/src/dtype.rs:80-95). */
+tlh_status tlh_dequantize(int type, const void *w, int64_t k, int64_t rows, int64_t w_row_bytes, float *y,
+                          void *stream);
+
+/* ------------------------------------------------------- paged attention
+ * The `paged-attention` custom node (crates/tensorlisp/src/scheme/core.ss:251-258),
+ * lowered by Ctx::custom kind 1 (crates/kernels/src/cuda/lower.rs:672-731) to
+ * vLLM's paged_attention_v1/v2 (crates/kernels/src/cuda/paged_attn.rs:326-417).
+ * Layouts (f16 elements, x = 8):
+ *   q        [num_seqs][num_heads][head_size] (contiguous)
+ *   k_cache  [num_blocks][num_kv_heads][head_size/8][block_size][8]
+ *   v_cache  [num_blocks][num_kv_heads][head_size][block_size]
+ *   block_tables i32 [num_seqs][max_blocks_per_seq], context_lens i32 [num_seqs]
+ *   out      [num_seqs][num_heads][head_size]
+ * head_size in {64, 80, 96, 112, 128, 192, 256}, block_size in {8, 16, 32},
+ * num_heads % num_kv_heads == 0, context lens <= max_context_len.
+ * `scratch` holds split-context partials (tlh_paged_attention_scratch_bytes);
+ * it may be NULL when that size is 0. */
+typedef struct tlh_paged_attention_args {
+    void *out;
+    const void *q;
+    const void *k_cache;
+    const void *v_cache;
+    const int32_t *block_tables;
+    const int32_t *context_lens;
+    int32_t num_seqs;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_size;
+    int32_t block_size;
+    int32_t max_blocks_per_seq;
+    int32_t max_context_len;
+    float scale;
+} tlh_paged_attention_args;
+
+tlh_status tlh_paged_attention_scratch_bytes(const tlh_paged_attention_args *a, size_t *bytes);
+tlh_status tlh_paged_attention(const tlh_paged_attention_args *a, void *scratch, size_t scratch_bytes,
+                               void *stream);
+
+/* The `paged-cache-write` custom node (core.ss:265-272), Ctx::custom kind 2
+ * (lower.rs:732-753) -> reshape_and_cache (crates/kernels/src/cuda/shaders/
+ * reshape_and_cache_kernel.cu:31-84): key/value f16 [num_tokens][num_kv_heads*head_size]
+ * into the caches at slot = block * block_size + offset; negative slots skip. */
+tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
+                                 const int64_t *slots, int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
+                                 int32_t block_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TLHIP_H */

@@ -1,0 +1,119 @@
+// Shared device-side definitions of the gfx950 executor: block formats,
+// conversions, the quantized-activation scratch layout and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tlhip.h"
+
+namespace tlh {
+
+// ----------------------------------------------------------- block formats
+// vendor/ggml/src/ggml-common.h:194-198 (q4_0), :251-255 (q8_0), :325-337
+// (q4_K), :370-375 (q8_K). Byte sizes per block and elements per block.
+constexpr int QK = 32;    // q4_0 / q8_0 block
+constexpr int QKK = 256;  // k-quant super-block
+constexpr int Q4_0_BYTES = 18;
+constexpr int Q8_0_BYTES = 34;
+constexpr int Q4_K_BYTES = 144;
+constexpr int Q8_K_BYTES = 292;
+
+__host__ __device__ constexpr int block_elems(int t) {
+    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q8_K) ? QKK : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0) ? QK : 1;
+}
+__host__ __device__ constexpr int block_bytes(int t) {
+    return t == TLH_TYPE_Q4_0   ? Q4_0_BYTES
+           : t == TLH_TYPE_Q8_0 ? Q8_0_BYTES
+           : t == TLH_TYPE_Q4_K ? Q4_K_BYTES
+           : t == TLH_TYPE_Q8_K ? Q8_K_BYTES
+           : t == TLH_TYPE_F16  ? 2
+                                : 4;
+}
+// vec_dot_type on x86 (vendor/ggml/src/ggml-cpu/ggml-cpu.c:239-319).
+__host__ __device__ constexpr int vec_dot_type(int wtype) {
+    return wtype == TLH_TYPE_Q4_K ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
+}
+
+// ---------------------------------------------------------- conversions
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// v_cvt_f16_f32: round to nearest even, f16 denormals kept (kernel default mode).
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// q4_K packed 6-bit scale/min of sub-block j from the 12-byte field
+// (ggml-quants.c:880-887), given the field as three little-endian words.
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &mn) {
+    // bytes 0..3 = s0, 4..7 = s1, 8..11 = s2
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63;
+        mn = (s1 >> (8 * j)) & 63;
+    } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (s2 >> (8 * jj)) & 0xff;
+        sc = (b8 & 0x0f) | (((s0 >> (8 * jj)) >> 6 & 3) << 4);
+        mn = (b8 >> 4) | (((s1 >> (8 * jj)) >> 6 & 3) << 4);
+    }
+}
+
+// ------------------------------------------------ quantized activation scratch
+// The CPU backend quantizes src1 into `wdata` in ggml's block layout
+// (ggml-cpu.c:1318-1359). Here the same values (bit-exact d and codes) go to
+// a split layout the kernels can stream with aligned 128-bit loads: for R
+// activation rows of K values,
+//   qs  : int8  [R][K]            codes, 64-byte aligned rows
+//   d   : f32   [R][K/blk]        block scales (q8_0: the f16-rounded d as f32)
+//   sum : int32 [R][K/32] (q8_0)  per-block code sums
+//         int16 [R][K/16] (q8_K)  bsums
+struct ActView {
+    const int8_t *qs;
+    const float *d;
+    const int32_t *sum32;  // q8_0 only
+    const int16_t *bsums;  // q8_K only
+    int64_t K;
+};
+
+struct ActLayout {
+    int64_t qs_off, d_off, sum_off, total;
+};
+
+__host__ __device__ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+__host__ __device__ inline ActLayout act_layout(int act_type, int64_t K, int64_t rows) {
+    ActLayout L;
+    L.qs_off = 0;
+    L.d_off = align_up(rows * K, 256);
+    const int64_t nblk = K / block_elems(act_type);
+    L.sum_off = align_up(L.d_off + rows * nblk * 4, 256);
+    const int64_t sum_bytes = act_type == TLH_TYPE_Q8_K ? rows * (K / 16) * 2 : rows * (K / 32) * 4;
+    L.total = align_up(L.sum_off + sum_bytes, 256);
+    return L;
+}
+
+__host__ __device__ inline ActView act_view(const void *base, int act_type, int64_t K, int64_t rows) {
+    const ActLayout L = act_layout(act_type, K, rows);
+    const char *b = (const char *)base;
+    ActView v;
+    v.qs = (const int8_t *)(b + L.qs_off);
+    v.d = (const float *)(b + L.d_off);
+    v.sum32 = (const int32_t *)(b + L.sum_off);
+    v.bsums = (const int16_t *)(b + L.sum_off);
+    v.K = K;
+    return v;
+}
+
+// ------------------------------------------------------- wave64 reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// int8x4 dot product with accumulate (v_dot4c_i32_i8).
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+}  // namespace tlh

@@ -1,0 +1,46 @@
+// Internal interface between the C ABI (tlhip.cpp) and the kernel files.
+#pragma once
+
+#include "common.hpp"
+
+namespace tlh {
+
+// Thread-local error text + status (defined in tlhip.cpp).
+tlh_status set_error(tlh_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// hipGetLastError after a launch, mapped to TLH_EXECUTION with `what` in the text.
+tlh_status check_launch(const char *what);
+
+// rows of x (stride x_row_bytes) -> activation rows row_off.. of an output of
+// total_rows rows, in ggml's block layout or the split scratch layout.
+tlh_status launch_quantize_act(int wtype, const float *x, int64_t K, int64_t rows, int64_t x_row_bytes, void *out,
+                               bool ggml_layout, int64_t row_off, int64_t total_rows, hipStream_t stream);
+tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, int64_t w_row_bytes, float *y,
+                             hipStream_t stream);
+
+// One batch slice of MUL_MAT with pre-quantized activations:
+//   dst[n*d_nb1 + m*4] = sum_k W[m][k] * act[n][k],  m < M, n < N
+// over `batches` = ne12*ne13 slices (grid z), weights broadcast by r2/r3.
+struct MatmulArgs {
+    int wtype;
+    const uint8_t *w;
+    int64_t w_nb1, w_nb2, w_nb3;  // weight row / matrix strides (bytes)
+    int64_t M, K, N;              // N: columns handled by this launch
+    int64_t n0, N_total;          // first column; columns per batch slice in act/dst
+    int64_t ne12, ne13, r2, r3;
+    const void *act;              // split-layout scratch, N_total*ne12*ne13 rows:
+                                  // column n of slice b is row n + N_total*b
+    float *dst;
+    int64_t d_nb1, d_nb2, d_nb3;  // dst strides (bytes), nb0 = 4
+};
+
+tlh_status launch_gemv(const MatmulArgs &a, hipStream_t stream);  // N <= 8
+tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N
+
+tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
+                                  hipStream_t stream);
+size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
+tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
+                                    const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,
+                                    int block_size, hipStream_t stream);
+
+}  // namespace tlh

@@ -1,0 +1,217 @@
+// Activation quantizers (f32 -> Q8_0 / Q8_K, bit-exact with the CPU backend's
+// from_float) and weight dequantizers (Q4_0 / Q8_0 / Q4_K -> f32, bit-exact
+// with ggml's dequantize_row_*), for gfx950.
+//
+// Bit-exactness rules kept here: no a*b+c contraction where the reference
+// rounds twice (#pragma clang fp contract(off)), IEEE-correct f32 division
+// (hipcc's default), f16 conversion by v_cvt_f16_f32 (round to nearest even,
+// denormals kept), roundf = ties away from zero, rintf = ties to even.
+#include "kernels.hpp"
+
+
+namespace tlh {
+
+// ------------------------------------------------------------------ Q8_0
+// quantize_row_q8_0_ref (vendor/ggml/src/ggml-quants.c:276-297), reached on
+// x86 without AVX through quantize_row_q8_0 (arch/x86/quants.c:395-398).
+// One lane per element, 32 lanes per block (two blocks per wave64):
+// amax over the block, d = amax/127, f16(d) stored, codes roundf(x * (1/d))
+// with the multiplier taken from the unrounded f32 d.
+// `rows` rows of x (stride x_row_bytes) become activation rows row_off.. of
+// an output holding total_rows rows.
+template <bool GGML_LAYOUT>
+__global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__ x, int64_t K, int64_t rows,
+                                                       int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
+                                                       int64_t total_rows) {
+#pragma clang fp contract(off)
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = K * rows;
+    if (gid >= total) return;  // K % 32 == 0, so whole 32-lane groups exit together
+    const int64_t row = gid / K;
+    const int64_t col = gid - row * K;
+    const float v = *(const float *)((const char *)x + row * x_row_bytes + col * 4);
+    float amax = fabsf(v);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q = (int)roundf(v * id);
+    const uint16_t dh = f2h(d);
+    const int lane32 = threadIdx.x & 31;
+    const int64_t blk = col / QK;
+    const int64_t orow = row + row_off;
+    if (GGML_LAYOUT) {
+        uint8_t *b = (uint8_t *)out + orow * (K / QK) * Q8_0_BYTES + blk * Q8_0_BYTES;
+        b[2 + lane32] = (uint8_t)(int8_t)q;
+        if (lane32 == 0) *(uint16_t *)b = dh;
+    } else {
+        const ActLayout L = act_layout(TLH_TYPE_Q8_0, K, total_rows);
+        int8_t *qs = (int8_t *)out + L.qs_off;
+        qs[orow * K + col] = (int8_t)q;
+        int s = q;
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) s += __shfl_xor(s, m, 32);
+        if (lane32 == 0) {
+            ((float *)((char *)out + L.d_off))[orow * (K / QK) + blk] = h2f(dh);
+            ((int32_t *)((char *)out + L.sum_off))[orow * (K / QK) + blk] = s;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ Q8_K
+// quantize_row_q8_K_ref (ggml-quants.c:2768-2804), the x86 entry
+// (arch/x86/quants.c:505-507). One wave per 256-element block, four
+// consecutive elements per lane: the signed value of largest magnitude (the
+// first one on ties), iscale = -127/max, codes rint(iscale*x) clamped to 127,
+// bsums of 16, d = 1/iscale. An all-zero block gets d = 0 and zero codes and sums.
+template <bool GGML_LAYOUT>
+__global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__ x, int64_t K, int64_t rows,
+                                                       int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
+                                                       int64_t total_rows) {
+#pragma clang fp contract(off)
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t nblk = K / QKK;
+    if (wave >= nblk * rows) return;
+    const int64_t row = wave / nblk;
+    const int64_t blk = wave - row * nblk;
+    const float *src = (const float *)((const char *)x + row * x_row_bytes) + blk * QKK + 4 * lane;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[i];
+    float ba = 0.0f, bv = 0.0f;
+    int bi = 1 << 30;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > ba) { ba = a; bv = v[i]; bi = 4 * lane + i; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float oa = __shfl_xor(ba, m, 64);
+        const float ov = __shfl_xor(bv, m, 64);
+        const int oi = __shfl_xor(bi, m, 64);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
+    }
+    uint32_t packed = 0;
+    int psum = 0;
+    float d = 0.0f;
+    if (ba != 0.0f) {
+        const float iscale = -127.0f / bv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int q = (int)rintf(iscale * v[i]);
+            q = q > 127 ? 127 : q;
+            packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
+            psum += q;
+        }
+        d = 1.0f / iscale;
+    }
+    psum += __shfl_xor(psum, 1, 64);
+    psum += __shfl_xor(psum, 2, 64);
+    const int64_t orow = row + row_off;
+    if (GGML_LAYOUT) {
+        uint8_t *b = (uint8_t *)out + orow * nblk * Q8_K_BYTES + blk * Q8_K_BYTES;
+        *(uint32_t *)(b + 4 + 4 * lane) = packed;
+        if ((lane & 3) == 0) *(int16_t *)(b + 4 + QKK + 2 * (lane >> 2)) = (int16_t)psum;
+        if (lane == 0) *(float *)b = d;
+    } else {
+        const ActLayout L = act_layout(TLH_TYPE_Q8_K, K, total_rows);
+        *(uint32_t *)((char *)out + L.qs_off + orow * K + blk * QKK + 4 * lane) = packed;
+        if ((lane & 3) == 0)
+            ((int16_t *)((char *)out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
+        if (lane == 0) ((float *)((char *)out + L.d_off))[orow * nblk + blk] = d;
+    }
+}
+
+// ------------------------------------------------------------- dequantize
+// One thread per output element; integer codes convert exactly, so the only
+// roundings are the reference's own: q4_0 ((q-8)*d, ggml-quants.c:459-476),
+// q8_0 (q*d, :553-565), q4_K ((d*sc)*q - (dmin*m), :1529-1550).
+template <int WT>
+__global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ w, int64_t K, int64_t rows,
+                                                    int64_t w_row_bytes, float *__restrict__ y) {
+#pragma clang fp contract(off)
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= K * rows) return;
+    const int64_t row = gid / K;
+    const int64_t col = gid - row * K;
+    const uint8_t *r = w + row * w_row_bytes;
+    float out;
+    if constexpr (WT == TLH_TYPE_Q4_0) {
+        const uint8_t *b = r + (col / QK) * Q4_0_BYTES;
+        const int j = (int)(col % QK);
+        const float d = h2f(*(const uint16_t *)b);
+        const int code = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
+        out = (float)(code - 8) * d;
+    } else if constexpr (WT == TLH_TYPE_Q8_0) {
+        const uint8_t *b = r + (col / QK) * Q8_0_BYTES;
+        const float d = h2f(*(const uint16_t *)b);
+        out = (float)(int8_t)b[2 + col % QK] * d;
+    } else {
+        const uint8_t *b = r + (col / QKK) * Q4_K_BYTES;
+        const int i = (int)(col % QKK);
+        const int c = i / 64, pos = i % 64, hi = pos >= 32, l = pos & 31;
+        const uint32_t *s = (const uint32_t *)(b + 4);
+        int sc, mn;
+        q4k_scale_min(2 * c + hi, s[0], s[1], s[2], sc, mn);
+        const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
+        const uint8_t byte = b[16 + 32 * c + l];
+        const int code = hi ? byte >> 4 : byte & 0x0f;
+        const float d1 = d * (float)sc;
+        const float m1 = dmin * (float)mn;
+        out = d1 * (float)code - m1;
+    }
+    y[gid] = out;
+}
+
+// --------------------------------------------------------------- launchers
+static inline unsigned grid_for(int64_t threads, int per_block) {
+    return (unsigned)((threads + per_block - 1) / per_block);
+}
+
+tlh_status launch_quantize_act(int wtype, const float *x, int64_t K, int64_t rows, int64_t x_row_bytes, void *out,
+                               bool ggml_layout, int64_t row_off, int64_t total_rows, hipStream_t stream) {
+    if (rows == 0 || K == 0) return TLH_OK;
+    if (vec_dot_type(wtype) == TLH_TYPE_Q8_0) {
+        const unsigned g = grid_for(K * rows, 256);
+        if (ggml_layout)
+            hipLaunchKernelGGL(k_quantize_q8_0<true>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
+                               row_off, total_rows);
+        else
+            hipLaunchKernelGGL(k_quantize_q8_0<false>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
+                               row_off, total_rows);
+    } else {
+        const unsigned g = grid_for((K / QKK) * rows * 64, 256);
+        if (ggml_layout)
+            hipLaunchKernelGGL(k_quantize_q8_K<true>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
+                               row_off, total_rows);
+        else
+            hipLaunchKernelGGL(k_quantize_q8_K<false>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
+                               row_off, total_rows);
+    }
+    return check_launch("quantize_act");
+}
+
+tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, int64_t w_row_bytes, float *y,
+                             hipStream_t stream) {
+    if (rows == 0 || K == 0) return TLH_OK;
+    const unsigned g = grid_for(K * rows, 256);
+    const uint8_t *wb = (const uint8_t *)w;
+    switch (type) {
+    case TLH_TYPE_Q4_0:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_0>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q8_0:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q8_0>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q4_K:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    default:
+        return set_error(TLH_UNSUPPORTED, "dequantize: unsupported type %d", type);
+    }
+    return check_launch("dequantize");
+}
+
+}  // namespace tlh

@@ -1,0 +1,363 @@
+// C ABI of the gfx950 executor (include/tlhip.h): validation, dispatch policy
+// and error reporting around the kernels. Host code only.
+//
+// The MUL_MAT policy mirrors Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
+// in what it accepts and how it reports refusals, and the ggml CPU backend
+// (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457) in what it computes:
+// quantize src1 to the vec_dot type, then N <= 8 -> GEMV, else GEMM.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "kernels.hpp"
+
+namespace tlh {
+
+static thread_local std::string g_last_error;
+
+tlh_status set_error(tlh_status s, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return s;
+}
+
+tlh_status check_launch(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(TLH_EXECUTION, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return TLH_OK;
+}
+
+static tlh_status hip_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return TLH_OK;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+        return set_error(TLH_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+    if (e == hipErrorOutOfMemory) return set_error(TLH_ALLOC, "%s: %s", what, hipGetErrorString(e));
+    return set_error(TLH_EXECUTION, "%s: %s", what, hipGetErrorString(e));
+}
+
+static bool weight_type_ok(int t) { return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K; }
+
+static const char *type_name(int t) {
+    switch (t) {
+    case TLH_TYPE_F32: return "f32";
+    case TLH_TYPE_F16: return "f16";
+    case TLH_TYPE_Q4_0: return "q4_0";
+    case TLH_TYPE_Q8_0: return "q8_0";
+    case TLH_TYPE_Q4_K: return "q4_K";
+    case TLH_TYPE_Q8_K: return "q8_K";
+    default: return "?";
+    }
+}
+
+// Validates a MUL_MAT descriptor; fills the derived sizes.
+struct MulMatShape {
+    int64_t K, M, N, ne12, ne13, r2, r3, act_rows;
+    int act_type;
+};
+
+static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
+    if (!op) return set_error(TLH_INVALID, "mul_mat: null op");
+    const tlh_tensor &a = op->t[0], &b = op->t[1], &d = op->t[4];
+    if (!weight_type_ok(a.ty))
+        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K", a.ty,
+                         type_name(a.ty));
+    if (b.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: activations must be f32 (got type %d)", b.ty);
+    if (d.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: the destination must be f32");
+    for (int i = 0; i < 4; ++i)
+        if (a.ne[i] < 0 || b.ne[i] < 0 || d.ne[i] < 0) return set_error(TLH_INVALID, "mul_mat: negative extent");
+    if (a.ne[0] != b.ne[0] || d.ne[0] != a.ne[1] || d.ne[1] != b.ne[1] || d.ne[2] != b.ne[2] || d.ne[3] != b.ne[3] ||
+        a.ne[2] == 0 || a.ne[3] == 0)
+        return set_error(TLH_UNSUPPORTED, "mul_mat: inconsistent shapes");
+    if (b.ne[2] % a.ne[2] != 0 || b.ne[3] % a.ne[3] != 0)
+        return set_error(TLH_UNSUPPORTED, "mul_mat: src1 batch dims are not multiples of src0's");
+    s.K = a.ne[0];
+    s.M = a.ne[1];
+    s.N = b.ne[1];
+    s.ne12 = b.ne[2];
+    s.ne13 = b.ne[3];
+    s.r2 = s.ne12 / a.ne[2];
+    s.r3 = s.ne13 / a.ne[3];
+    if ((op->x[0] != 0 && op->x[0] != s.r2) || (op->x[1] != 0 && op->x[1] != s.r3))
+        return set_error(TLH_INVALID, "mul_mat: broadcast factors x[0]=%lld x[1]=%lld disagree with the shapes",
+                         (long long)op->x[0], (long long)op->x[1]);
+    const int be = block_elems(a.ty);
+    if (s.K % be != 0)
+        return set_error(TLH_UNSUPPORTED, "mul_mat: K=%lld is not a multiple of the %s block (%d)", (long long)s.K,
+                         type_name(a.ty), be);
+    if (a.nb[0] != block_bytes(a.ty))
+        return set_error(TLH_UNSUPPORTED, "mul_mat: src0 must not be permuted (nb0=%lld)", (long long)a.nb[0]);
+    const int64_t rb = s.K / be * block_bytes(a.ty);
+    if (a.nb[1] < rb || (a.nb[1] & 1) || (a.nb[2] & 1) || (a.nb[3] & 1))
+        return set_error(TLH_UNSUPPORTED, "mul_mat: src0 row stride %lld (row is %lld bytes, 2-byte aligned)",
+                         (long long)a.nb[1], (long long)rb);
+    if (b.nb[0] != 4 || (b.nb[1] & 3) || (b.nb[2] & 3) || (b.nb[3] & 3))
+        return set_error(TLH_UNSUPPORTED, "mul_mat: src1 must have contiguous f32 rows");
+    if (d.nb[0] != 4 || d.nb[1] < 4 * s.M || (d.nb[1] & 3) || d.nb[2] < d.nb[1] || d.nb[3] < d.nb[2])
+        return set_error(TLH_UNSUPPORTED, "mul_mat: dst must be f32 with ordered strides");
+    s.act_type = vec_dot_type(a.ty);
+    s.act_rows = s.N * s.ne12 * s.ne13;
+    return TLH_OK;
+}
+
+}  // namespace tlh
+
+using namespace tlh;
+
+extern "C" {
+
+const char *tlh_last_error(void) { return g_last_error.c_str(); }
+
+const char *tlh_status_name(tlh_status s) {
+    switch (s) {
+    case TLH_OK: return "OK";
+    case TLH_NO_DEVICE: return "NO_DEVICE";
+    case TLH_UNSUPPORTED: return "UNSUPPORTED";
+    case TLH_INVALID: return "INVALID";
+    case TLH_ALLOC: return "ALLOC";
+    case TLH_EXECUTION: return "EXECUTION";
+    default: return "?";
+    }
+}
+
+const char *tlh_version(void) { return "tlhip 0.1 gfx950"; }
+
+tlh_status tlh_device_count(int *count) {
+    if (!count) return set_error(TLH_INVALID, "device_count: null pointer");
+    *count = 0;
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice || (e == hipSuccess && n == 0)) {
+        (void)hipGetLastError();
+        return TLH_OK;
+    }
+    if (e != hipSuccess) return hip_check(e, "hipGetDeviceCount");
+    *count = n;
+    return TLH_OK;
+}
+
+tlh_status tlh_device_open(int ordinal, tlh_device_props *props) {
+    int n = 0;
+    tlh_status st = tlh_device_count(&n);
+    if (st != TLH_OK) return st;
+    if (n == 0) return set_error(TLH_NO_DEVICE, "no HIP device");
+    if (ordinal < 0 || ordinal >= n) return set_error(TLH_NO_DEVICE, "device %d of %d", ordinal, n);
+    st = hip_check(hipSetDevice(ordinal), "hipSetDevice");
+    if (st != TLH_OK || !props) return st;
+    hipDeviceProp_t p;
+    st = hip_check(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    if (st != TLH_OK) return st;
+    memset(props, 0, sizeof *props);
+    snprintf(props->name, sizeof props->name, "%s", p.name);
+    snprintf(props->arch, sizeof props->arch, "%s", p.gcnArchName);
+    props->compute_units = p.multiProcessorCount;
+    props->wave_size = p.warpSize;
+    props->lds_bytes = (int)p.sharedMemPerBlock;
+    props->clock_khz = p.clockRate;
+    props->hbm_bytes = (int64_t)p.totalGlobalMem;
+    return TLH_OK;
+}
+
+tlh_status tlh_alloc(size_t bytes, void **ptr) {
+    if (!ptr) return set_error(TLH_INVALID, "alloc: null pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return TLH_OK;
+    const hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(TLH_ALLOC, "alloc of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+    }
+    return TLH_OK;
+}
+
+tlh_status tlh_free(void *ptr) { return ptr ? hip_check(hipFree(ptr), "hipFree") : TLH_OK; }
+
+tlh_status tlh_h2d(void *dst, const void *src, size_t bytes) {
+    return bytes ? hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "h2d") : TLH_OK;
+}
+
+tlh_status tlh_d2h(void *dst, const void *src, size_t bytes) {
+    return bytes ? hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "d2h") : TLH_OK;
+}
+
+tlh_status tlh_stream_sync(void *stream) {
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes) {
+    if (!bytes) return set_error(TLH_INVALID, "mul_mat_scratch_bytes: null pointer");
+    MulMatShape s;
+    const tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK) return st;
+    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows).total;
+    return TLH_OK;
+}
+
+static tlh_status mm_check_scratch(const MulMatShape &s, const void *scratch, size_t scratch_bytes) {
+    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows).total;
+    if (!scratch || scratch_bytes < need)
+        return set_error(TLH_INVALID, "mul_mat: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    if ((uintptr_t)scratch & 255) return set_error(TLH_INVALID, "mul_mat: scratch must be 256-byte aligned");
+    return TLH_OK;
+}
+
+// Phase 1: src1 -> vec_dot-type codes in scratch (the CPU's wdata, ggml-cpu.c:1318-1359).
+static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void *src1, void *scratch,
+                              hipStream_t hs) {
+    const tlh_tensor &a = op->t[0], &b = op->t[1];
+    if ((uintptr_t)src1 & 3) return set_error(TLH_INVALID, "mul_mat: src1 must be 4-byte aligned");
+    const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
+    if (packed)
+        return launch_quantize_act(a.ty, (const float *)src1, s.K, s.act_rows, b.nb[1], scratch, false, 0,
+                                   s.act_rows, hs);
+    for (int64_t i13 = 0; i13 < s.ne13; ++i13)
+        for (int64_t i12 = 0; i12 < s.ne12; ++i12) {
+            const float *x = (const float *)((const char *)src1 + i12 * b.nb[2] + i13 * b.nb[3]);
+            const tlh_status st = launch_quantize_act(a.ty, x, s.K, s.N, b.nb[1], scratch, false,
+                                                      s.N * (i12 + s.ne12 * i13), s.act_rows, hs);
+            if (st != TLH_OK) return st;
+        }
+    return TLH_OK;
+}
+
+// Phase 2: the products, N <= 8 -> GEMV, else GEMM.
+static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void *src0, const void *scratch,
+                             void *dst, hipStream_t hs) {
+    const tlh_tensor &a = op->t[0], &d = op->t[4];
+    if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
+        return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
+    MatmulArgs m;
+    m.wtype = a.ty;
+    m.w = (const uint8_t *)src0;
+    m.w_nb1 = a.nb[1];
+    m.w_nb2 = a.nb[2];
+    m.w_nb3 = a.nb[3];
+    m.M = s.M;
+    m.K = s.K;
+    m.N = s.N;
+    m.n0 = 0;
+    m.N_total = s.N;
+    m.ne12 = s.ne12;
+    m.ne13 = s.ne13;
+    m.r2 = s.r2;
+    m.r3 = s.r3;
+    m.act = scratch;
+    m.dst = (float *)dst;
+    m.d_nb1 = d.nb[1];
+    m.d_nb2 = d.nb[2];
+    m.d_nb3 = d.nb[3];
+    return s.N <= 8 ? launch_gemv(m, hs) : launch_gemm(m, hs);
+}
+
+static bool mm_empty(const MulMatShape &s) { return s.M == 0 || s.N == 0 || s.ne12 == 0 || s.ne13 == 0; }
+
+tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,
+                       size_t scratch_bytes, void *stream) {
+    MulMatShape s;
+    tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK || mm_empty(s)) return st;
+    if (!src0 || !src1 || !dst) return set_error(TLH_INVALID, "mul_mat: null tensor pointer");
+    if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
+    if ((st = mm_quantize(op, s, src1, scratch, (hipStream_t)stream)) != TLH_OK) return st;
+    return mm_compute(op, s, src0, scratch, dst, (hipStream_t)stream);
+}
+
+tlh_status tlh_mul_mat_quantize(const tlh_op *op, const void *src1, void *scratch, size_t scratch_bytes,
+                                void *stream) {
+    MulMatShape s;
+    tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK || mm_empty(s)) return st;
+    if (!src1) return set_error(TLH_INVALID, "mul_mat_quantize: null src1");
+    if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
+    return mm_quantize(op, s, src1, scratch, (hipStream_t)stream);
+}
+
+tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *scratch, size_t scratch_bytes,
+                               void *dst, void *stream) {
+    MulMatShape s;
+    tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK || mm_empty(s)) return st;
+    if (!src0 || !dst) return set_error(TLH_INVALID, "mul_mat_compute: null tensor pointer");
+    if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
+    return mm_compute(op, s, src0, scratch, dst, (hipStream_t)stream);
+}
+
+tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, int64_t x_row_bytes, void *y,
+                            void *stream) {
+    if (!weight_type_ok(wtype)) return set_error(TLH_UNSUPPORTED, "quantize_act: weight type %d", wtype);
+    if (k < 0 || rows < 0 || k % block_elems(vec_dot_type(wtype)) != 0)
+        return set_error(TLH_INVALID, "quantize_act: k=%lld is not a multiple of the %s block", (long long)k,
+                         type_name(vec_dot_type(wtype)));
+    if ((!x || !y) && k * rows > 0) return set_error(TLH_INVALID, "quantize_act: null pointer");
+    if (x_row_bytes < 4 * k || (x_row_bytes & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
+        return set_error(TLH_INVALID, "quantize_act: rows must be 4-byte aligned f32 with stride >= 4k");
+    return launch_quantize_act(wtype, x, k, rows, x_row_bytes, y, true, 0, rows, (hipStream_t)stream);
+}
+
+tlh_status tlh_dequantize(int type, const void *w, int64_t k, int64_t rows, int64_t w_row_bytes, float *y,
+                          void *stream) {
+    if (!weight_type_ok(type)) return set_error(TLH_UNSUPPORTED, "dequantize: type %d", type);
+    if (k < 0 || rows < 0 || k % block_elems(type) != 0)
+        return set_error(TLH_INVALID, "dequantize: k=%lld is not a multiple of the %s block", (long long)k,
+                         type_name(type));
+    if ((!w || !y) && k * rows > 0) return set_error(TLH_INVALID, "dequantize: null pointer");
+    if (w_row_bytes < k / block_elems(type) * block_bytes(type) || (w_row_bytes & 1) || ((uintptr_t)w & 1))
+        return set_error(TLH_INVALID, "dequantize: row stride too small or misaligned");
+    return launch_dequantize(type, w, k, rows, w_row_bytes, y, (hipStream_t)stream);
+}
+
+static tlh_status check_paged(const tlh_paged_attention_args *a) {
+    if (!a) return set_error(TLH_INVALID, "paged_attention: null args");
+    static const int head_sizes[] = {64, 80, 96, 112, 128, 192, 256};
+    bool hs_ok = false;
+    for (int h : head_sizes) hs_ok |= a->head_size == h;
+    if (!hs_ok) return set_error(TLH_INVALID, "paged_attention: unsupported head_size %d", a->head_size);
+    if (a->block_size != 8 && a->block_size != 16 && a->block_size != 32)
+        return set_error(TLH_INVALID, "paged_attention: unsupported block_size %d (have 8, 16, 32)", a->block_size);
+    if (a->num_kv_heads <= 0 || a->num_heads <= 0 || a->num_heads % a->num_kv_heads != 0)
+        return set_error(TLH_INVALID, "paged_attention: num_heads must be a multiple of num_kv_heads");
+    if (a->num_seqs < 0 || a->max_blocks_per_seq < 0 || a->max_context_len < 0 ||
+        (int64_t)a->max_blocks_per_seq * a->block_size < a->max_context_len)
+        return set_error(TLH_INVALID, "paged_attention: max_blocks_per_seq * block_size < max_context_len");
+    return TLH_OK;
+}
+
+tlh_status tlh_paged_attention_scratch_bytes(const tlh_paged_attention_args *a, size_t *bytes) {
+    if (!bytes) return set_error(TLH_INVALID, "paged_attention_scratch_bytes: null pointer");
+    const tlh_status st = check_paged(a);
+    if (st != TLH_OK) return st;
+    *bytes = paged_attention_scratch_bytes(*a);
+    return TLH_OK;
+}
+
+tlh_status tlh_paged_attention(const tlh_paged_attention_args *a, void *scratch, size_t scratch_bytes,
+                               void *stream) {
+    const tlh_status st = check_paged(a);
+    if (st != TLH_OK) return st;
+    if (a->num_seqs == 0) return TLH_OK;
+    if (!a->out || !a->q || !a->k_cache || !a->v_cache || !a->block_tables || !a->context_lens)
+        return set_error(TLH_INVALID, "paged_attention: null pointer");
+    const size_t need = paged_attention_scratch_bytes(*a);
+    if (need > 0 && (!scratch || scratch_bytes < need))
+        return set_error(TLH_INVALID, "paged_attention: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    return launch_paged_attention(*a, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
+                                 const int64_t *slots, int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
+                                 int32_t block_size, void *stream) {
+    if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || head_size % 8 != 0 || block_size <= 0)
+        return set_error(TLH_INVALID, "reshape_and_cache: bad geometry");
+    if (num_tokens == 0) return TLH_OK;
+    if (!key || !value || !k_cache || !v_cache || !slots) return set_error(TLH_INVALID, "reshape_and_cache: null pointer");
+    return launch_reshape_and_cache(key, value, k_cache, v_cache, slots, num_tokens, num_kv_heads, head_size,
+                                    block_size, (hipStream_t)stream);
+}
+
+}  // extern "C"

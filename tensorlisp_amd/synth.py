@@ -1,0 +1,99 @@
+"""Deterministic synthetic inputs for parity tests and the benchmark.
+
+A counter-based generator (splitmix64 of seed and element index) so any slice
+of any input can be regenerated independently of numpy's RNG stream policy:
+uniform in [0, 1) from the top 24 bits, N(0, 1) by Box-Muller. BASELINE's
+configs fix distributions but no RNG; this one is ours, and fixtures record
+the seeds they were made with.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _splitmix64(x: np.ndarray) -> np.ndarray:
+    x = x + np.uint64(0x9E3779B97F4A7C15)
+    z = x
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def bits(seed: int, n: int, offset: int = 0) -> np.ndarray:
+    """n pseudo-random uint64 for stream `seed`, elements offset..offset+n-1."""
+    with np.errstate(over="ignore"):
+        idx = np.arange(offset, offset + n, dtype=np.uint64)
+        base = _splitmix64(np.array([seed], dtype=np.uint64))[0]
+        return _splitmix64(idx ^ base)
+
+
+def uniform(seed: int, n: int, offset: int = 0) -> np.ndarray:
+    """float64 in [0, 1) with 24 random bits (exact in float32)."""
+    return (bits(seed, n, offset) >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+
+
+def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
+    """float32 N(0, std^2) of `shape` by Box-Muller on pairs of uniforms."""
+    n = int(np.prod(shape))
+    m = (n + 1) // 2
+    u = uniform(seed, 2 * m)
+    u1 = 1.0 - u[0::2]  # (0, 1]
+    u2 = u[1::2]
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.empty(2 * m)
+    z[0::2] = r * np.cos(2 * np.pi * u2)
+    z[1::2] = r * np.sin(2 * np.pi * u2)
+    return (z[:n] * std).astype(np.float32).reshape(shape)
+
+
+def integers(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+    """int64 uniform in [lo, hi] (inclusive)."""
+    span = np.uint64(hi - lo + 1)
+    return (bits(seed, n) % span).astype(np.int64) + lo
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+# ------------------------------------------------------------ weight blocks
+def q8_0_config1(seed: int, M: int, K: int) -> np.ndarray:
+    """BASELINE config 1's Q8_0 weight built directly: codes uniform in [-127, 127],
+    f16 scale |N(0, 0.02)| / 127 (about 30% of them f16-subnormal). uint8 [M, K/32*34]."""
+    nb = M * (K // 32)
+    qs = integers(seed, -127, 127, nb * 32).astype(np.int8).view(np.uint8).reshape(nb, 32)
+    d = f16_bits(np.abs(normal(seed + 1, (nb,), 0.02)) / np.float32(127))
+    blocks = np.empty((nb, 34), np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = qs
+    return blocks.reshape(M, (K // 32) * 34)
+
+
+def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> np.ndarray:
+    """Structurally valid random blocks of a weight type, sized like weights
+    quantized from N(0, std) (finite f16 scales, random codes). Used where
+    quantizing full-size f32 weights on the host would dominate run time."""
+    from .native import Q4_0, Q8_0, Q4_K
+
+    if wtype == Q8_0:
+        return q8_0_config1(seed, M, K)
+    if wtype == Q4_0:
+        nb = M * (K // 32)
+        d = f16_bits(normal(seed + 1, (nb,), std) / np.float32(8))
+        qs = (bits(seed, nb * 2) & np.uint64(0xFFFFFFFFFFFFFFFF)).view(np.uint8).reshape(nb, 16)
+        blocks = np.empty((nb, 18), np.uint8)
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = qs
+        return blocks.reshape(M, (K // 32) * 18)
+    if wtype == Q4_K:
+        nb = M * (K // 256)
+        d = f16_bits(np.abs(normal(seed + 1, (nb,), std)) / np.float32(63 * 4))
+        dmin = f16_bits(np.abs(normal(seed + 2, (nb,), std)) / np.float32(63 * 2))
+        raw = bits(seed, nb * 18).view(np.uint8).reshape(nb, 144)
+        blocks = raw.copy()
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+        return blocks.reshape(M, (K // 256) * 144)
+    raise ValueError(wtype)

@@ -1,0 +1,137 @@
+"""Writes the golden fixtures of this directory from the reference's own
+compiled ggml CPU code (oracle/_ref/libggml_ref.so, built in place from
+/root/reference by oracle/Makefile).
+
+The reference commits no golden vectors (its tests compute expectations at run
+time from ggml's CPU backend: crates/tensorlisp/tests/native.rs:61-107), so
+these are the reference's outputs on fixed inputs, captured once:
+
+  fp16.npz         ggml_fp16_to_fp32_row over all 65536 halves; ggml_fp32_to_fp16_row
+                   over refs.fp16_probe_values() (every rounding boundary between
+                   adjacent halves +-1 ulp, and a random sample over all exponents)
+  quant.npz        ggml_quantize_chunk (q4_0, q8_0, q4_K; imatrix NULL, the path of
+                   DType::from_f32, crates/tensorlisp/src/dtype.rs:98-124) and
+                   dequantize_row_* on the same rows
+  act.npz          quantize_row_q8_0 / quantize_row_q8_K (the x86 from_float of the
+                   CPU mul_mat) on random and edge-case rows
+  mul_mat.npz      one GGML_OP_MUL_MAT on the CPU backend for the reference test's
+                   cases (native.rs:73-107: 96 x 256 weights from noise(seed 1),
+                   x = noise(seed 10 + n), n in 1,3,5,8,9,40) per weight type
+  config1.npz      BASELINE config 1 (Q8_0 4096 x 4096, N = 1, seed 0): input hashes
+                   and the CPU backend's output vector
+  flash_attn.npz   GGML_OP_FLASH_ATTN_EXT (ops.cpp:8468) on dense f16 K/V, the
+                   dense-cache counterpart of paged attention
+
+Run: python tests/golden/make_golden.py   (needs oracle/_ref built)
+"""
+from __future__ import annotations
+
+import hashlib
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent))
+sys.path.insert(0, str(HERE.parents[1]))
+
+from refs import Q4_0, Q4_K, Q8_0, Ref, fp16_probe_values, xorshift_noise  # noqa: E402
+from tensorlisp_amd import synth  # noqa: E402
+
+
+def edge_rows_act(k: int) -> np.ndarray:
+    """Rows that exercise the activation quantizers' corner cases."""
+    rows = []
+    rows.append(np.zeros(k, np.float32))  # all-zero blocks: d = 0
+    rows.append(np.full(k, 0.37, np.float32))  # constant blocks
+    r = synth.normal(101, (k,))
+    r[::32] = 3.0
+    r[16::32] = -3.0  # |max| ties with opposite signs: the first one wins (q8_K)
+    rows.append(r)
+    r = synth.normal(102, (k,))
+    r[::256] = -5.0
+    r[128::256] = 5.0
+    rows.append(r)
+    # codes landing exactly on .5 after scaling: amax 127 -> id = 1, x = n + 0.5
+    r = (np.arange(k) % 64 - 32).astype(np.float32) + np.float32(0.5)
+    r[::32] = 127.0
+    rows.append(r)
+    r = (np.arange(k) % 64 - 32).astype(np.float32) + np.float32(0.5)
+    r[::256] = -127.0
+    rows.append(r)
+    rows.append(synth.normal(103, (k,)) * np.float32(1e-30))  # tiny: subnormal f16 d
+    rows.append(synth.normal(104, (k,)) * np.float32(1e4))  # large
+    r = synth.normal(105, (k,))
+    r[32:64] = 0.0  # one zero block among others
+    r[256:512] = 0.0
+    rows.append(r)
+    return np.stack(rows).astype(np.float32)
+
+
+def main() -> None:
+    ref = Ref()
+    # ---------------------------------------------------------------- fp16
+    halves = np.arange(65536, dtype=np.uint16)
+    h2f = ref.f16_to_f32(halves)
+    f = fp16_probe_values()
+    np.savez_compressed(HERE / "fp16.npz", h2f_bits=h2f.view(np.uint32), f2h=ref.f32_to_f16(f))
+
+    # ------------------------------------------------------ weight quantization
+    K = 512
+    w = synth.normal(11, (12, K), 0.02)
+    w[0] = 0.0
+    w[1] = 0.01
+    w[2, :256] = synth.normal(12, (256,), 1.0)
+    w[3] = np.abs(w[3])  # non-negative rows: min > 0 is clamped to 0 in q4_K
+    out = {"w": w}
+    for t, name in ((Q4_0, "q4_0"), (Q8_0, "q8_0"), (Q4_K, "q4_K")):
+        q = ref.quantize_weights(t, w)
+        out[f"{name}_bytes"] = q
+        out[f"{name}_deq"] = ref.dequantize(t, q, K)
+    np.savez_compressed(HERE / "quant.npz", **out)
+
+    # ----------------------------------------------- activation quantization
+    K = 1024
+    x = np.concatenate([edge_rows_act(K), synth.normal(13, (6, K))]).astype(np.float32)
+    np.savez_compressed(HERE / "act.npz", x=x, q8_0=ref.quantize_act(Q4_0, x), q8_K=ref.quantize_act(Q4_K, x))
+
+    # ------------------------------------------ mul_mat, the reference test's cases
+    rows, k = 96, 256
+    wn = xorshift_noise((rows, k), 1)
+    ns = [1, 3, 5, 8, 9, 40]
+    out = {"w_f32": wn, "ns": np.array(ns)}
+    for n in ns:
+        out[f"x{n}"] = xorshift_noise((n, k), 10 + n)
+    for t, name in ((Q4_0, "q4_0"), (Q8_0, "q8_0"), (Q4_K, "q4_K")):
+        q = ref.quantize_weights(t, wn)
+        out[f"{name}_w"] = q
+        for n in ns:
+            y, _ = ref.mul_mat(t, q, rows, k, out[f"x{n}"])
+            out[f"{name}_y{n}"] = y
+    np.savez_compressed(HERE / "mul_mat.npz", **out)
+
+    # ------------------------------------------------------------ config 1
+    M = K1 = 4096
+    wq = synth.q8_0_config1(0, M, K1)
+    x1 = synth.normal(1000, (1, K1))
+    y1, _ = ref.mul_mat(Q8_0, wq, M, K1, x1, nthreads=8)
+    np.savez_compressed(HERE / "config1.npz", w_sha256=np.frombuffer(hashlib.sha256(wq.tobytes()).digest(), np.uint8),
+                        x_sha256=np.frombuffer(hashlib.sha256(x1.tobytes()).digest(), np.uint8), y=y1,
+                        seeds=np.array([0, 1000]))
+
+    # ----------------------------------------------------------- flash attn
+    out = {}
+    for i, (H, Hkv, D, L) in enumerate(((4, 1, 128, 70), (8, 2, 64, 33), (8, 2, 128, 515), (4, 4, 256, 5))):
+        q = synth.normal(200 + i, (H, D))
+        kk = synth.f16_bits(synth.normal(300 + i, (Hkv, L, D)))
+        vv = synth.f16_bits(synth.normal(400 + i, (Hkv, L, D)))
+        o, _ = ref.flash_attn(q, kk, vv, 1.0 / np.sqrt(D))
+        out.update({f"q{i}": q, f"k{i}": kk, f"v{i}": vv, f"o{i}": o})
+    np.savez_compressed(HERE / "flash_attn.npz", **out)
+    for p in sorted(HERE.glob("*.npz")):
+        print(f"{p.name}: {p.stat().st_size} bytes")
+
+
+if __name__ == "__main__":
+    main()

@@ -278,6 +278,25 @@ def ref():
     return _ref
 
 
+def fp16_probe_values() -> np.ndarray:
+    """f32 inputs that pin an f32 -> f16 conversion: every midpoint between adjacent
+    finite halves and its two f32 neighbours, a random sample over all exponents,
+    and the overflow / underflow edges."""
+    import sys
+
+    sys.path.insert(0, str(ROOT))
+    from tensorlisp_amd import synth
+
+    h = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float64)
+    hv = np.unique(h[np.isfinite(h)])
+    mids = ((hv[1:] + hv[:-1]) / 2).astype(np.float32)
+    rnd = synth.normal(7, (1 << 14,)) * np.float32(2.0) ** synth.integers(8, -30, 17, 1 << 14).astype(np.float32)
+    edges = np.array([0.0, -0.0, 65504, 65519.996, 65520, -65520, 1e-8, 2.0 ** -25, 2.0 ** -24, 3 * 2.0 ** -26,
+                      np.inf, -np.inf], np.float32)
+    return np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf)),
+                           rnd, edges]).astype(np.float32)
+
+
 def xorshift_noise(shape, seed: int) -> np.ndarray:
     """The reference tests' input generator (crates/tensorlisp/tests/native.rs:10-18):
     xorshift64 seeded with seed * 0x9e3779b97f4a7c15 | 1, values in [-1, 1)."""

@@ -1,0 +1,144 @@
+"""The C ABI (include/tlhip.h) without touching a GPU: the library loads, exports
+every declared symbol, and validates descriptors the way Ctx::mul_mat
+(crates/kernels/src/cuda/lower.rs:543-571) and PagedGeometry::prepare
+(crates/kernels/src/cuda/paged_attn.rs:223-250) refuse them: unsupported types
+and shapes are named errors, not crashes (the reference's
+native.rs:241-250 "unsupported op reported by name")."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from tensorlisp_amd import native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tlhip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tlh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    decl = declared_functions()
+    assert decl, "no declarations parsed"
+    missing = [f for f in decl if not hasattr(lib, f)]
+    assert not missing, missing
+    assert sorted(N.EXPORTS) == decl
+
+
+def test_descriptor_layout():
+    assert C.sizeof(N.TlhTensor) == 72
+    assert C.sizeof(N.TlhOp) == 5 * 72 + 12 * 8  # OP_BYTES of lower.rs:67
+    assert N.TlhOp.x.offset == 360
+
+
+def test_version_and_device_count_without_gpu():
+    assert N.lib().tlh_version().decode().startswith("tlhip")
+    assert N.device_count() >= 0
+
+
+def _status(fn, *args):
+    st = fn(*args)
+    return N.STATUS[st], N.lib().tlh_last_error().decode()
+
+
+def scratch_status(op):
+    n = C.c_size_t()
+    st, msg = _status(N.lib().tlh_mul_mat_scratch_bytes, C.byref(op), C.byref(n))
+    return st, msg, n.value
+
+
+@pytest.mark.parametrize("wt", [N.Q4_0, N.Q8_0, N.Q4_K])
+@pytest.mark.parametrize("n", [1, 8, 9, 512])
+def test_mul_mat_scratch_sizes(wt, n):
+    K, M = 4096, 1024
+    st, msg, nbytes = scratch_status(N.mul_mat_op(wt, M, K, n))
+    assert st == "OK", msg
+    # codes + f32 scales + per-block sums, each region 256-byte aligned
+    at = N.VEC_DOT_TYPE[wt]
+    be = N.BLOCK[at][0]
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    sums = n * (K // 16) * 2 if at == N.Q8_K else n * (K // 32) * 4
+    assert nbytes == al(al(al(n * K) + n * (K // be) * 4) + sums)
+
+
+def test_mul_mat_unsupported_weight_type_is_named():
+    op = N.mul_mat_op(N.Q4_0, 64, 256, 1)
+    op.t[0].ty = 14  # q6_K
+    st, msg, _ = scratch_status(op)
+    assert st == "UNSUPPORTED" and "type 14" in msg
+
+
+def test_mul_mat_rejects_bad_shapes_and_layouts():
+    op = N.mul_mat_op(N.Q4_K, 64, 512, 2)
+    op.t[1].ne[0] = 256  # K mismatch
+    assert scratch_status(op)[0] == "UNSUPPORTED"
+    op = N.mul_mat_op(N.Q4_K, 64, 320, 2)  # K not a multiple of 256
+    st, msg, _ = scratch_status(op)
+    assert st == "UNSUPPORTED" and "multiple" in msg
+    op = N.mul_mat_op(N.Q8_0, 64, 256, 2)
+    op.t[1].ty = N.F16
+    assert scratch_status(op)[0] == "UNSUPPORTED"
+    op = N.mul_mat_op(N.Q8_0, 64, 256, 2)
+    op.t[0].nb[0] = 17  # permuted src0
+    assert scratch_status(op)[0] == "UNSUPPORTED"
+    op = N.mul_mat_op(N.Q8_0, 64, 256, 4, ne2=3, w_ne2=2)  # 3 % 2 != 0
+    assert scratch_status(op)[0] == "UNSUPPORTED"
+    op = N.mul_mat_op(N.Q8_0, 64, 256, 4, ne2=4, w_ne2=2)
+    op.x[0] = 3  # disagrees with ne12 / ne02 = 2
+    assert scratch_status(op)[0] == "INVALID"
+
+
+def test_mul_mat_null_pointers_are_invalid_not_crashes():
+    op = N.mul_mat_op(N.Q8_0, 64, 256, 1)
+    st, msg = _status(N.lib().tlh_mul_mat, C.byref(op), None, None, None, None, 0, None)
+    assert st == "INVALID", msg
+
+
+def test_quantize_and_dequantize_validation():
+    L = N.lib()
+    st, msg = _status(L.tlh_quantize_act, 14, None, 256, 1, 1024, None, None)
+    assert st == "UNSUPPORTED"
+    st, msg = _status(L.tlh_quantize_act, N.Q4_K, None, 300, 1, 1200, None, None)
+    assert st == "INVALID" and "multiple" in msg
+    st, msg = _status(L.tlh_dequantize, N.Q4_0, None, 33, 1, 18, None, None)
+    assert st == "INVALID"
+
+
+def paged_args(**kw):
+    a = N.TlhPagedArgs()
+    a.num_seqs, a.num_heads, a.num_kv_heads, a.head_size = 32, 32, 8, 128
+    a.block_size, a.max_blocks_per_seq, a.max_context_len, a.scale = 16, 512, 8192, 128 ** -0.5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status", [
+    ({}, "OK"),
+    ({"head_size": 100}, "INVALID"),
+    ({"block_size": 64}, "INVALID"),
+    ({"num_kv_heads": 3}, "INVALID"),
+    ({"max_blocks_per_seq": 10}, "INVALID"),
+])
+def test_paged_attention_geometry_validation(kw, status):
+    n = C.c_size_t()
+    st, msg = _status(N.lib().tlh_paged_attention_scratch_bytes, C.byref(paged_args(**kw)), C.byref(n))
+    assert st == status, msg
+    if status == "OK":
+        assert n.value == 32 * 32 * (8192 // 512) * (128 + 2) * 4
+
+
+def test_no_device_is_reported_not_fatal():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(N.TlhError) as e:
+        N.device_props(0)
+    assert e.value.status == "NO_DEVICE"

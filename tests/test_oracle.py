@@ -1,0 +1,330 @@
+"""Pins the CPU oracle (oracle/tlq_oracle.c) before anything is checked against it.
+
+Each oracle function is pinned by at least one check that a plausible mistake
+(dropped term, wrong sign or index, swapped nibble halves, wrong rounding tie)
+fails:
+  * the golden vectors of tests/golden/ (outputs of the reference's own compiled
+    ggml, written by make_golden.py) -- bit-exact;
+  * the compiled reference itself on fresh random inputs, where oracle/_ref is
+    built (this container) -- bit-exact;
+  * mathematics: numpy's IEEE float16 conversion, float64 brute-force sums of the
+    dequantized operands, quantizer invariants, softmax brute force.
+"""
+from __future__ import annotations
+
+import hashlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from refs import NAMES, Q4_0, Q4_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
+from tensorlisp_amd import synth
+
+GOLD = Path(__file__).resolve().parent / "golden"
+WTYPES = (Q4_0, Q8_0, Q4_K)
+
+
+def gold(name):
+    return np.load(GOLD / f"{name}.npz")
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+# ------------------------------------------------------------------- fp16
+def test_fp16_to_fp32_all_halves_golden_and_numpy():
+    o = oracle()
+    halves = np.arange(65536, dtype=np.uint16)
+    got = o.f16_to_f32(halves)
+    want = gold("fp16")["h2f_bits"].view(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert same_bits(got[~nan], want[~nan])
+    # independent: numpy's IEEE binary16 decoder
+    assert same_bits(got[~nan], halves.view(np.float16).astype(np.float32)[~nan])
+
+
+def test_fp32_to_fp16_rounding_boundaries():
+    o = oracle()
+    f = fp16_probe_values()
+    got = o.f32_to_f16(f)
+    assert np.array_equal(got, gold("fp16")["f2h"])
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, f.astype(np.float16).view(np.uint16))  # IEEE round-to-nearest-even
+    nan = np.array([np.nan, -np.nan], np.float32)
+    assert np.array_equal(o.f32_to_f16(nan) & 0x7FFF, np.array([0x7E00, 0x7E00], np.uint16))
+
+
+# ------------------------------------------------------ weight quantization
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_weight_quantize_and_dequantize_golden(t):
+    o, g = oracle(), gold("quant")
+    q = o.quantize(t, g["w"])
+    assert np.array_equal(q, g[f"{NAMES[t]}_bytes"])
+    assert same_bits(o.dequantize(t, q, g["w"].shape[1]), g[f"{NAMES[t]}_deq"])
+
+
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_weight_quantize_error_bounds(t):
+    """Round-to-nearest quantization: each dequantized value lies within its block's
+    step of the input (q8_0/q4_0: |d|/2 plus the f16 rounding of d; q4_K: the stored
+    sub-block scale)."""
+    o = oracle()
+    w = synth.normal(21, (16, 512), 0.02)
+    deq = o.dequantize(t, o.quantize(t, w), 512)
+    err = np.abs(deq - w)
+    amax = np.abs(w).reshape(16, -1, 32).max(-1, keepdims=True)
+    eb = err.reshape(16, -1, 32)
+    if t == Q8_0:
+        assert np.all(eb <= amax / 127 * (0.5 + 127 * 2.0 ** -11))  # d/2 plus the f16 rounding of d
+    elif t == Q4_0:
+        # d = max/-8: codes span [-8, 7], so the opposite-sign extreme clamps at 7 (error <= |d|)
+        assert np.all(eb <= amax / 8 * 1.001)
+        assert np.mean(eb <= amax / 16 * 1.001) > 0.9
+    else:
+        assert err.max() < 0.25 * np.abs(w).max()
+    # dequantized values are exactly code * scale: q8_0 codes recovered as integers
+    if t == Q8_0:
+        q = o.quantize(t, w).reshape(-1, 34)
+        d = q[:, :2].copy().view(np.float16).astype(np.float32)
+        codes = q[:, 2:].view(np.int8).astype(np.float32)
+        assert same_bits((codes * d).reshape(deq.shape), deq)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("scale", [0.02, 1.0, 300.0])
+def test_weight_quantize_matches_reference_random(t, scale):
+    o, r = oracle(), ref()
+    w = synth.normal(31 + int(scale), (64, 1024), scale)
+    q = o.quantize(t, w)
+    assert np.array_equal(q, r.quantize_weights(t, w))
+    assert same_bits(o.dequantize(t, q, 1024), r.dequantize(t, q, 1024))
+
+
+# ------------------------------------------------- activation quantization
+def test_act_quantize_golden():
+    o, g = oracle(), gold("act")
+    assert np.array_equal(o.quantize(Q8_0, g["x"]), g["q8_0"])
+    assert np.array_equal(o.quantize(Q8_K, g["x"]), g["q8_K"])
+
+
+def _q8_0_fields(q, k):
+    b = q.reshape(-1, 34)
+    return b[:, :2].copy().view(np.float16).astype(np.float32).ravel(), b[:, 2:].view(np.int8)
+
+
+def _q8_K_fields(q):
+    b = q.reshape(-1, 292)
+    d = b[:, :4].copy().view(np.float32).ravel()
+    qs = b[:, 4:260].view(np.int8)
+    bs = b[:, 260:].copy().view(np.int16)
+    return d, qs, bs
+
+
+def test_act_quantize_invariants():
+    o = oracle()
+    x = np.concatenate([gold("act")["x"], synth.normal(41, (8, 1024), 3.0)])
+    d, qs = _q8_0_fields(o.quantize(Q8_0, x), 1024)
+    xb = x.reshape(-1, 32)
+    assert np.abs(qs.astype(int)).max() <= 127
+    amax = np.abs(xb).max(1)
+    assert np.array_equal(d, (amax / np.float32(127)).astype(np.float16).astype(np.float32))
+    dd = (amax / np.float32(127)).astype(np.float32)
+    nz = dd > 0
+    assert np.all(np.abs(xb[nz] - qs[nz] * dd[nz, None]) <= dd[nz, None] * 0.5 * (1 + 1e-5))
+    assert np.all(qs[~nz] == 0)
+    d, qs, bs = _q8_K_fields(o.quantize(Q8_K, x))
+    assert np.array_equal(bs, qs.reshape(-1, 16, 16).astype(np.int32).sum(-1).astype(np.int16))
+    xk = x.reshape(-1, 256)
+    nz = np.abs(xk).max(1) > 0
+    assert np.all(d[~nz] == 0) and np.all(qs[~nz] == 0)
+    assert np.all(np.abs(xk[nz] - qs[nz] * d[nz, None]) <= np.abs(d[nz, None]) * 0.5 * (1 + 1e-5))
+    # the element of largest magnitude maps to -127 * sign-convention: d carries -max/127
+    i = np.abs(xk[nz]).argmax(1)
+    assert np.all(qs[nz][np.arange(nz.sum()), i] == -127)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("wt", [Q4_0, Q4_K], ids=["q8_0", "q8_K"])
+def test_act_quantize_matches_reference_random(wt):
+    o, r = oracle(), ref()
+    for seed, s in ((51, 1.0), (52, 1e-3), (53, 1e5)):
+        x = synth.normal(seed, (32, 2048), s)
+        x[3, 100:400] = 0.0
+        assert np.array_equal(o.quantize_act(wt, x), r.quantize_act(wt, x))
+
+
+# ----------------------------------------------------------- dot products
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_vec_dot_against_f64_bruteforce(t):
+    """vec_dot = sum of the dequantized operands, to f32 accumulation error."""
+    o = oracle()
+    K = 4096
+    w = o.quantize(t, synth.normal(61, (8, K), 0.02))
+    x = synth.normal(62, (4, K))
+    xq = o.quantize_act(t, x)
+    at = Q8_K if t == Q4_K else Q8_0
+    wd = o.dequantize(t, w, K).astype(np.float64)
+    xd = o.dequantize(at, xq, K).astype(np.float64)
+    want = wd @ xd.T
+    got = np.array([[o.vec_dot(t, K, w[i], xq[j]) for j in range(4)] for i in range(8)])
+    scale = np.abs(wd).sum(1)[:, None] * np.abs(xd).max()
+    assert np.all(np.abs(got - want) <= 1e-6 * scale)
+
+
+def test_q4_K_block_integer_sums():
+    """The integer parts of a q4_K x q8_K block: sum_s sc*dot and sum_s m*sum(q8),
+    against codes recovered independently from dequantized values."""
+    o = oracle()
+    w = o.quantize(Q4_K, synth.normal(71, (4, 256), 0.02))
+    xq = o.quantize(Q8_K, synth.normal(72, (4, 256)))
+    for i in range(4):
+        sq, sm = o.block_ints_q4_K(w[i], xq[i])
+        blk = w[i]
+        d = blk[0:2].copy().view(np.float16).astype(np.float64)[0]
+        dmin = blk[2:4].copy().view(np.float16).astype(np.float64)[0]
+        y = o.dequantize(Q4_K, blk, 256).astype(np.float64)
+        q8 = xq[i][4:260].view(np.int8).astype(np.int64)
+        # y = d*sc*q - dmin*m  => sum(y*q8) = d*sq - dmin*sm (up to f32 rounding of y)
+        lhs = (y * q8).sum()
+        assert abs(lhs - (d * sq - dmin * sm)) <= 1e-5 * (abs(d * sq) + abs(dmin * sm) + 1)
+
+
+# ---------------------------------------------------------------- mul_mat
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_mul_mat_golden_reference_cases(t):
+    """The reference test's shapes (native.rs:73-107), CPU backend outputs, bit-exact."""
+    o, g = oracle(), gold("mul_mat")
+    for n in g["ns"]:
+        y = o.mul_mat(t, g[f"{NAMES[t]}_w"], 96, 256, g[f"x{n}"])
+        assert same_bits(y, g[f"{NAMES[t]}_y{n}"]), n
+
+
+def test_mul_mat_config1_golden():
+    """BASELINE config 1 through the oracle equals the CPU backend's output bit for bit;
+    the input hashes pin the synthetic generator."""
+    o, g = oracle(), gold("config1")
+    w = synth.q8_0_config1(int(g["seeds"][0]), 4096, 4096)
+    x = synth.normal(int(g["seeds"][1]), (1, 4096))
+    assert hashlib.sha256(w.tobytes()).digest() == g["w_sha256"].tobytes()
+    assert hashlib.sha256(x.tobytes()).digest() == g["x_sha256"].tobytes()
+    assert same_bits(o.mul_mat(Q8_0, w, 4096, 4096, x), g["y"])
+    # ~30% of the f16 scales are subnormal, as the config states
+    d = w.reshape(-1, 34)[:, :2].copy().view(np.uint16)
+    frac = np.mean((d & 0x7C00) == 0)
+    assert 0.2 < frac < 0.4, frac
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_mul_mat_matches_reference_random_blocks(t):
+    o, r = oracle(), ref()
+    M, K = 200, 1024
+    w = synth.random_blocks(t, 81, M, K)
+    for n in (1, 8, 17):
+        x = synth.normal(82 + n, (n, K))
+        y, _ = r.mul_mat(t, w, M, K, x)
+        assert same_bits(o.mul_mat(t, w, M, K, x), y)
+
+
+# -------------------------------------------------------- paged attention
+def _random_paged(seqs, heads, kvh, hs, bs, lens, seed, pool=None):
+    """Random paged KV cache with scattered block tables (as BASELINE config 4)."""
+    maxb = max(1, max((L + bs - 1) // bs for L in lens))
+    need = sum((L + bs - 1) // bs for L in lens)
+    nblocks = pool or max(need * 2, 4)
+    perm = synth.bits(seed, nblocks).argsort()[:need]
+    tables = np.zeros((seqs, maxb), np.int32)
+    c = 0
+    for s, L in enumerate(lens):
+        nb = (L + bs - 1) // bs
+        tables[s, :nb] = perm[c:c + nb]
+        c += nb
+    kc = synth.f16_bits(synth.normal(seed + 1, (nblocks, kvh, hs // 8, bs, 8)))
+    vc = synth.f16_bits(synth.normal(seed + 2, (nblocks, kvh, hs, bs)))
+    q = synth.f16_bits(synth.normal(seed + 3, (seqs, heads, hs)))
+    return q, kc, vc, tables, np.array(lens, np.int32)
+
+
+def attention_f64(q, kc, vc, tables, lens, kvh, bs, scale):
+    """Brute-force softmax(scale q k^T) v in float64 over exactly the f16 K/V."""
+    o = oracle()
+    seqs, heads, hs = q.shape
+    out = np.zeros((seqs, heads, hs))
+    qf = q.view(np.float16).astype(np.float64)
+    for s in range(seqs):
+        L = int(lens[s])
+        if L == 0:
+            continue
+        k, v = o.gather_kv(kc, vc, tables[s], L, kvh, hs, bs)
+        k = k.view(np.float16).astype(np.float64)
+        v = v.view(np.float16).astype(np.float64)
+        for h in range(heads):
+            g = h // (heads // kvh)
+            lg = scale * (k[g] @ qf[s, h])
+            p = np.exp(lg - lg.max())
+            out[s, h] = (p / p.sum()) @ v[g]
+    return out
+
+
+@pytest.mark.parametrize("hs,bs,kvh,heads,lens", [
+    (128, 16, 2, 8, [70, 33, 5]),
+    (64, 8, 1, 4, [1, 17, 64]),
+    (256, 32, 4, 4, [100, 1]),
+    (80, 16, 1, 2, [40]),
+])
+def test_paged_attention_oracle_vs_bruteforce(hs, bs, kvh, heads, lens):
+    o = oracle()
+    q, kc, vc, tables, L = _random_paged(len(lens), heads, kvh, hs, bs, lens, 90)
+    scale = 1.0 / np.sqrt(hs)
+    got = o.paged_attention(q, kc, vc, kvh, scale, tables, L, bs).view(np.float16).astype(np.float64)
+    want = attention_f64(q, kc, vc, tables, L, kvh, bs, scale)
+    # f16 probabilities and f16 output: ~1e-3 of the output scale
+    assert np.abs(got - want).max() <= 3e-3 * np.abs(want).max()
+
+
+def test_paged_attention_oracle_vs_ggml_flash_attn_golden():
+    """The oracle on a one-sequence paged cache holding the golden dense K/V equals
+    ggml's CPU FLASH_ATTN_EXT (f16 Q and f16 V accumulation there) within f16 error."""
+    o, g = oracle(), gold("flash_attn")
+    for i in range(4):
+        q32, k, v, want = g[f"q{i}"], g[f"k{i}"], g[f"v{i}"], g[f"o{i}"]
+        Hkv, L, D = k.shape
+        H = q32.shape[0]
+        bs = 16
+        nb = (L + bs - 1) // bs
+        kc = np.zeros((nb, Hkv, D // 8, bs, 8), np.uint16)
+        vc = np.zeros((nb, Hkv, D, bs), np.uint16)
+        key = k.transpose(1, 0, 2).reshape(L, Hkv * D)
+        val = v.transpose(1, 0, 2).reshape(L, Hkv * D)
+        o.reshape_and_cache(key, val, kc, vc, np.arange(L, dtype=np.int64), Hkv, D, bs)
+        q16 = synth.f16_bits(q32)[None]
+        got = o.paged_attention(q16, kc, vc, Hkv, 1.0 / np.sqrt(D), np.arange(nb, dtype=np.int32)[None],
+                                np.array([L], np.int32), bs)
+        got = got.view(np.float16).astype(np.float32)[0]
+        assert np.abs(got - want).max() <= 4e-3 * np.abs(want).max(), i
+
+
+def test_reshape_and_cache_gather_roundtrip():
+    """Scatter through slots (negative = skip) then gather: bit-exact."""
+    o = oracle()
+    kvh, hs, bs, T = 2, 64, 8, 40
+    nblocks = 12
+    key = synth.f16_bits(synth.normal(95, (T, kvh * hs)))
+    val = synth.f16_bits(synth.normal(96, (T, kvh * hs)))
+    table = (synth.bits(97, nblocks).argsort()[:5]).astype(np.int32)
+    slots = np.array([table[t // bs] * bs + t % bs for t in range(T)], np.int64)
+    slots[7] = -1
+    kc = np.zeros((nblocks, kvh, hs // 8, bs, 8), np.uint16)
+    vc = np.zeros((nblocks, kvh, hs, bs), np.uint16)
+    o.reshape_and_cache(key, val, kc, vc, slots, kvh, hs, bs)
+    k, v = o.gather_kv(kc, vc, table, T, kvh, hs, bs)
+    kk = key.reshape(T, kvh, hs).transpose(1, 0, 2)
+    vv = val.reshape(T, kvh, hs).transpose(1, 0, 2)
+    keep = np.ones(T, bool)
+    keep[7] = False
+    assert np.array_equal(k[:, keep], kk[:, keep]) and np.array_equal(v[:, keep], vv[:, keep])
+    assert np.all(k[:, 7] == 0) and np.all(v[:, 7] == 0)
