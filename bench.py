@@ -140,16 +140,16 @@ def main() -> int:
     ev = {c: [] for c in cases}
 
     def step(i: int, record: bool) -> None:
-        # one MUL_MAT node = activation quantization + GEMV (tlh_mul_mat's two phases);
-        # with `record`, HIP events on the launch stream bracket the GEMV kernel alone
+        # one MUL_MAT node per case through tlh_mul_mat (activation quantization fused
+        # into the GEMV when N*K is small, else a quantize launch + the GEMV); with
+        # `record`, HIP events on the launch stream bracket each node
         for c in cases:
             t, M, K, _ = c
             ws = weights[(t, M, K)]
-            nodes[c].quantize(xs[c], stream)
             if record:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
-            nodes[c].compute(ws[i % len(ws)], ys[c], stream)
+            nodes[c](ws[i % len(ws)], xs[c], ys[c], stream)
             if record:
                 e1.record(stream)
                 ev[c].append((e0, e1))
@@ -168,7 +168,7 @@ def main() -> int:
     wall = time.perf_counter() - t0
     log(f"timed: {args.steps} steps in {wall * 1e3:.1f} ms")
 
-    # per-node GEMV kernel durations (a separate pass, events around each GEMV launch)
+    # per-node durations (a separate pass, events around each node; a fused node is one kernel)
     for i in range(args.steps):
         step(args.warmup + args.steps + i, True)
     torch.cuda.synchronize()
@@ -224,7 +224,8 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "q4_K GEMV N=1, 128256x4096 (k_gemv<12,1,R>), per launch",
+            "kernel": "q4_K GEMV N=1 with fused Q8_K activation quantization, 128256x4096 "
+                      "(tlh::k_gemv<12, 1, 4, 256, true>), per launch",
             "achieved": round(dom_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -12,7 +12,7 @@ tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
         MatmulArgs s = a;
         s.n0 = a.n0 + c;
         s.N = a.N - c < 8 ? a.N - c : 8;
-        const tlh_status st = launch_gemv(s, stream);
+        const tlh_status st = launch_gemv(s, nullptr, 0, stream);
         if (st != TLH_OK) return st;
     }
     return TLH_OK;

@@ -33,8 +33,12 @@ struct MatmulArgs {
     int64_t d_nb1, d_nb2, d_nb3;  // dst strides (bytes), nb0 = 4
 };
 
-tlh_status launch_gemv(const MatmulArgs &a, hipStream_t stream);  // N <= 8
-tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N
+// N <= 8. With x != nullptr (src1 rows in activation-row order, stride
+// x_row_bytes) and a small N*K the GEMV quantizes x itself and the scratch is
+// not read; otherwise it reads the scratch a quantize launch filled.
+tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
+bool gemv_fuses_quantize(const MatmulArgs &a);
+tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
                                   hipStream_t stream);

@@ -226,12 +226,8 @@ static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void
     return TLH_OK;
 }
 
-// Phase 2: the products, N <= 8 -> GEMV, else GEMM.
-static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void *src0, const void *scratch,
-                             void *dst, hipStream_t hs) {
+static MatmulArgs mm_args(const tlh_op *op, const MulMatShape &s, const void *src0, const void *scratch, void *dst) {
     const tlh_tensor &a = op->t[0], &d = op->t[4];
-    if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
-        return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
     MatmulArgs m;
     m.wtype = a.ty;
     m.w = (const uint8_t *)src0;
@@ -252,7 +248,16 @@ static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void 
     m.d_nb1 = d.nb[1];
     m.d_nb2 = d.nb[2];
     m.d_nb3 = d.nb[3];
-    return s.N <= 8 ? launch_gemv(m, hs) : launch_gemm(m, hs);
+    return m;
+}
+
+// Phase 2: the products from the scratch, N <= 8 -> GEMV, else GEMM.
+static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void *src0, const void *scratch,
+                             void *dst, hipStream_t hs) {
+    if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
+        return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
+    const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
+    return s.N <= 8 ? launch_gemv(m, nullptr, 0, hs) : launch_gemm(m, hs);
 }
 
 static bool mm_empty(const MulMatShape &s) { return s.M == 0 || s.N == 0 || s.ne12 == 0 || s.ne13 == 0; }
@@ -264,8 +269,20 @@ tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, voi
     if (st != TLH_OK || mm_empty(s)) return st;
     if (!src0 || !src1 || !dst) return set_error(TLH_INVALID, "mul_mat: null tensor pointer");
     if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
-    if ((st = mm_quantize(op, s, src1, scratch, (hipStream_t)stream)) != TLH_OK) return st;
-    return mm_compute(op, s, src0, scratch, dst, (hipStream_t)stream);
+    const hipStream_t hs = (hipStream_t)stream;
+    // Decode with a small activation: the GEMV quantizes src1 itself (one launch).
+    const tlh_tensor &b = op->t[1];
+    const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
+    if (s.N <= 8 && packed && !((uintptr_t)src1 & 3)) {
+        const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
+        if (gemv_fuses_quantize(m)) {
+            if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
+                return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
+            return launch_gemv(m, (const float *)src1, b.nb[1], hs);
+        }
+    }
+    if ((st = mm_quantize(op, s, src1, scratch, hs)) != TLH_OK) return st;
+    return mm_compute(op, s, src0, scratch, dst, hs);
 }
 
 tlh_status tlh_mul_mat_quantize(const tlh_op *op, const void *src1, void *scratch, size_t scratch_bytes,

@@ -109,7 +109,7 @@ def test_config4_full(gpu):
     seqs, heads, kvh, hs, bs, pool = 32, 32, 8, 128, 16, 65536
     lens = synth.integers(1300, 512, 8192, seqs).astype(np.int32)
     pages = [(int(L) + bs - 1) // bs for L in lens]
-    maxb = max(pages)
+    maxb = 8192 // bs  # max_blocks_per_seq * block_size covers max_context_len
     order = synth.bits(1301, pool).argsort()[: sum(pages)].astype(np.int32)
     tables = np.zeros((seqs, maxb), np.int32)
     c = 0
