@@ -1,4 +1,7 @@
-// Decode GEMV for GGML_OP_MUL_MAT with N <= 8 activation columns, gfx950.
+// Decode GEMV for GGML_OP_MUL_MAT with N <= 8 activation columns, gfx950:
+// the LDS-staged variant, used for K the register-resident kernel
+// (gemv_reg.hip) does not cover (K > 16384 or K not a multiple of 64), and
+// the GEMV dispatch.
 //
 // Replaces mm_vec (crates/kernels/src/cuda/native/mm.cu:16-42), which
 // dequantized every weight to f32. Here the activations are quantized to the
@@ -399,39 +402,44 @@ static bool fits_lds(int wtype, int64_t K, int nc) {
 }
 
 template <int WT, int NC>
-static tlh_status launch_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
+static tlh_status launch_nc(const MatmulArgs &a, hipStream_t stream) {
     constexpr int R = NC <= 2 ? 4 : 2;
-    // fuse the quantization when each workgroup's re-read of the f32 input is small
-    const bool fused = x != nullptr && a.N * a.K * 4 <= 64 * 1024;
-    if (fused) return launch_cfg<WT, NC, R, 256, true>(a, x, x_row_bytes, stream);
-    return launch_cfg<WT, NC, R, 512, false>(a, x, x_row_bytes, stream);
+    return launch_cfg<WT, NC, R, 512, false>(a, nullptr, 0, stream);
 }
 
 template <int WT>
-static tlh_status launch_wt(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
+static tlh_status launch_wt(const MatmulArgs &a, hipStream_t stream) {
     switch (a.N) {
-    case 1: return launch_nc<WT, 1>(a, x, x_row_bytes, stream);
-    case 2: return launch_nc<WT, 2>(a, x, x_row_bytes, stream);
-    case 3: return launch_nc<WT, 3>(a, x, x_row_bytes, stream);
-    case 4: return launch_nc<WT, 4>(a, x, x_row_bytes, stream);
-    case 5: return launch_nc<WT, 5>(a, x, x_row_bytes, stream);
-    case 6: return launch_nc<WT, 6>(a, x, x_row_bytes, stream);
-    case 7: return launch_nc<WT, 7>(a, x, x_row_bytes, stream);
-    default: return launch_nc<WT, 8>(a, x, x_row_bytes, stream);
+    case 1: return launch_nc<WT, 1>(a, stream);
+    case 2: return launch_nc<WT, 2>(a, stream);
+    case 3: return launch_nc<WT, 3>(a, stream);
+    case 4: return launch_nc<WT, 4>(a, stream);
+    case 5: return launch_nc<WT, 5>(a, stream);
+    case 6: return launch_nc<WT, 6>(a, stream);
+    case 7: return launch_nc<WT, 7>(a, stream);
+    default: return launch_nc<WT, 8>(a, stream);
     }
 }
 
-bool gemv_fuses_quantize(const MatmulArgs &a) { return a.N * a.K * 4 <= 64 * 1024; }
+bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_bytes) {
+    int ksplit, upw;
+    return x != nullptr && a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw) && ((uintptr_t)x & 15) == 0 &&
+           (x_row_bytes & 15) == 0;
+}
 
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
     if (a.N < 1 || a.N > 8) return set_error(TLH_INVALID, "gemv: N=%lld outside 1..8", (long long)a.N);
+    int ksplit, upw;
+    if (gemv_reg_geometry(a.K, ksplit, upw)) return launch_gemv_reg(a, x, x_row_bytes, stream);
+    if (x != nullptr) return set_error(TLH_INVALID, "gemv: fused quantization needs K <= 16384, K %% 64 == 0");
+    // other K: activation codes staged in LDS from the scratch
     if (!fits_lds(a.wtype, a.K, (int)a.N))
         return set_error(TLH_UNSUPPORTED, "gemv: K=%lld x N=%lld activations exceed LDS", (long long)a.K,
                          (long long)a.N);
     switch (a.wtype) {
-    case TLH_TYPE_Q4_0: return launch_wt<TLH_TYPE_Q4_0>(a, x, x_row_bytes, stream);
-    case TLH_TYPE_Q8_0: return launch_wt<TLH_TYPE_Q8_0>(a, x, x_row_bytes, stream);
-    case TLH_TYPE_Q4_K: return launch_wt<TLH_TYPE_Q4_K>(a, x, x_row_bytes, stream);
+    case TLH_TYPE_Q4_0: return launch_wt<TLH_TYPE_Q4_0>(a, stream);
+    case TLH_TYPE_Q8_0: return launch_wt<TLH_TYPE_Q8_0>(a, stream);
+    case TLH_TYPE_Q4_K: return launch_wt<TLH_TYPE_Q4_K>(a, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
     }
 }

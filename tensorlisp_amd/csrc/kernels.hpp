@@ -37,7 +37,10 @@ struct MatmulArgs {
 // x_row_bytes) and a small N*K the GEMV quantizes x itself and the scratch is
 // not read; otherwise it reads the scratch a quantize launch filled.
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
-bool gemv_fuses_quantize(const MatmulArgs &a);
+bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_bytes);
+// register-resident GEMV (gemv_reg.hip): K <= 16384, K % 64 == 0
+bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
+tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,

@@ -275,7 +275,7 @@ tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, voi
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
     if (s.N <= 8 && packed && !((uintptr_t)src1 & 3)) {
         const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
-        if (gemv_fuses_quantize(m)) {
+        if (gemv_fuses_quantize(m, (const float *)src1, b.nb[1])) {
             if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
                 return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
             return launch_gemv(m, (const float *)src1, b.nb[1], hs);

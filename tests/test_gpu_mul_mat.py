@@ -164,3 +164,59 @@ def test_repeated_launches_are_deterministic(gpu):
         mm(w, x, y1)
     torch.cuda.synchronize()
     assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
+
+
+@pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 16416)],
+                         ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K16416"])
+@pytest.mark.parametrize("n", [1, 2, 5, 8])
+def test_lds_staged_gemv_shapes(gpu, t, K, n):
+    """K outside the register-resident GEMV (K % 64 != 0 or K > 16384): the LDS-staged kernel."""
+    M = 77
+    w = synth.random_blocks(t, 980 + K, M, K)
+    x = synth.normal(981 + n, (n, K))
+    y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
+    close(y, oracle().mul_mat(t, w, M, K, x), f"{NAMES[t]} K={K} n={n}")
+
+
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("n", [1, 2])
+def test_unaligned_activation_rows_take_the_quantize_launch(gpu, t, n):
+    """Rows whose stride is not 16-byte aligned cannot use the fused in-register
+    quantization; the node falls back to a quantize launch with the same result."""
+    import ctypes as C
+
+    import torch
+
+    M, K = 130, 1024
+    xpad = K + 1
+    w = synth.random_blocks(t, 990, M, K)
+    x = synth.normal(991, (n, xpad))
+    op = N.mul_mat_op(t, M, K, n, x_nb=[4, xpad * 4, xpad * 4 * n, xpad * 4 * n])
+    nbytes = N.mul_mat_scratch_bytes(op)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    y = torch.empty((n, M), dtype=torch.float32, device="cuda")
+    wd, xd = dev(w), dev(x)
+    N.check(N.lib().tlh_mul_mat(C.byref(op), C.c_void_p(wd.data_ptr()), C.c_void_p(xd.data_ptr()),
+                                C.c_void_p(y.data_ptr()), C.c_void_p(scratch.data_ptr()), nbytes,
+                                C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    close(host(y), oracle().mul_mat(t, w, M, K, x[:, :K]), NAMES[t])
+
+
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+def test_split_phases_match_fused_node(gpu, t):
+    """tlh_mul_mat_quantize + tlh_mul_mat_compute (the CPU's two phases) equal the
+    single-call node, which fuses the quantization for N <= 2."""
+    import torch
+
+    M, K = 300, 4096
+    w = dev(synth.random_blocks(t, 995, M, K))
+    for n in (1, 2, 8):
+        x = dev(synth.normal(996 + n, (n, K)))
+        mm = N.MulMat(t, M, K, n)
+        y0 = torch.empty((n, M), dtype=torch.float32, device="cuda")
+        y1 = torch.empty_like(y0)
+        mm(w, x, y0)
+        mm.quantize(x)
+        mm.compute(w, y1)
+        torch.cuda.synchronize()
+        close(y1.cpu().numpy(), y0.cpu().numpy(), f"{NAMES[t]} n={n}")
