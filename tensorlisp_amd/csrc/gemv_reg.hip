@@ -1,4 +1,4 @@
-// Decode GEMV with register-resident activations, gfx950 (N <= 8, K <= 16384,
+// Decode GEMV with register-resident activations, gfx950 (N <= 2, K <= 16384,
 // K a multiple of 64).
 //
 // Each lane owns one 64-element unit of K for the whole kernel: its slice of
@@ -9,7 +9,7 @@
 // contiguous load; for larger K, KSPLIT (2 or 4) waves of a workgroup take
 // contiguous K ranges of the same rows and merge their partials through LDS.
 //
-// FUSED (N <= 2): every wave quantizes its own activation slice in registers
+// FUSED: every wave quantizes its own activation slice in registers
 // from the f32 input (the rules of quantize_row_q8_0_ref, ggml-quants.c:276-297,
 // and quantize_row_q8_K_ref, :2768-2804; a q8_K super-block is 4 lanes, which
 // agree on its signed maximum with two butterflies), so a decode MUL_MAT is
@@ -409,24 +409,13 @@ static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_r
     return launch_reg_cfg<WT, NC, R, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
 }
 
+// N = 1 or 2 only: more columns of register-resident activations (20 VGPRs
+// per column) leave too few registers and spill.
 template <int WT, bool FUSED>
 static tlh_status launch_reg_wt(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
                                 hipStream_t stream) {
-    if constexpr (FUSED) {
-        if (a.N == 1) return launch_reg_nc<WT, 1, true>(a, x, x_row_bytes, ksplit, upw, stream);
-        return launch_reg_nc<WT, 2, true>(a, x, x_row_bytes, ksplit, upw, stream);
-    } else {
-        switch (a.N) {
-        case 1: return launch_reg_nc<WT, 1, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 2: return launch_reg_nc<WT, 2, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 3: return launch_reg_nc<WT, 3, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 4: return launch_reg_nc<WT, 4, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 5: return launch_reg_nc<WT, 5, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 6: return launch_reg_nc<WT, 6, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        case 7: return launch_reg_nc<WT, 7, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        default: return launch_reg_nc<WT, 8, false>(a, x, x_row_bytes, ksplit, upw, stream);
-        }
-    }
+    if (a.N == 1) return launch_reg_nc<WT, 1, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
+    return launch_reg_nc<WT, 2, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
 }
 
 // Geometry of the register-resident GEMV for K: waves per row group and
