@@ -104,14 +104,15 @@ def test_every_column_count(gpu, t, n):
 
 
 @pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
-def test_broadcast_batches_and_strides(gpu, t):
+@pytest.mark.parametrize("n", [3, 20])
+def test_broadcast_batches_and_strides(gpu, t, n):
     """src0 [K, M, 2, 1] broadcast over src1 [K, N, 4, 3] (r2 = 2, r3 = 3), src1 rows
-    padded (non-contiguous), dst with a padded row stride."""
+    padded (non-contiguous), dst with a padded row stride; GEMV (n=3) and GEMM (n=20)."""
     import ctypes as C
 
     import torch
 
-    M, K, n, w_ne2, w_ne3, ne2, ne3 = 64, 512, 3, 2, 1, 4, 3
+    M, K, w_ne2, w_ne3, ne2, ne3 = 64, 512, 2, 1, 4, 3
     rb = N.row_bytes(t, K)
     w = synth.random_blocks(t, 950, M * w_ne2 * w_ne3, K)
     xpad = K + 64
@@ -220,3 +221,13 @@ def test_split_phases_match_fused_node(gpu, t):
         mm.compute(w, y1)
         torch.cuda.synchronize()
         close(y1.cpu().numpy(), y0.cpu().numpy(), f"{NAMES[t]} n={n}")
+
+
+@pytest.mark.parametrize("M,K,n", [(128, 256, 128), (256, 512, 129), (300, 2304, 257), (1000, 4096, 64)])
+def test_q4K_mfma_gemm_tiles(gpu, M, K, n):
+    """The q4_K MFMA GEMM on exact tile multiples and ragged edges, weights quantized
+    from f32 by the ggml quantizer (so scales/mins span their real ranges)."""
+    w = oracle().quantize(Q4_K, synth.normal(1010 + M, (M, K), 0.02))
+    x = synth.normal(1011 + n, (n, K))
+    y = host(N.mul_mat(Q4_K, dev(w), M, K, dev(x)))
+    close(y, oracle().mul_mat(Q4_K, w, M, K, x), f"{M}x{K} n={n}")
