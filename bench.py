@@ -223,37 +223,7 @@ def main() -> int:
         try:
             traffic = json.loads(tfile.read_text()).get("gemv_q4_K_128256x4096_n1_bytes")
         except (ValueError, OSError):
-            # prefill GEMM: q4_K 14336x4096 and 4096x14336, N = 512 / 2048, GEMM kernel
-    # alone (the activation quantization runs first as its own phase), rotated weights
-    prefill = []
-    for (M, K) in ((14336, 4096), (4096, 14336)):
-        base = gpu_blocks(torch, N.Q4_K, M, K, gen)
-        ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
-        for n in (512, 2048):
-            node = N.MulMat(N.Q4_K, M, K, n)
-            x = torch.randn((n, K), device="cuda", generator=gen)
-            y = torch.empty((n, M), dtype=torch.float32, device="cuda")
-            node.quantize(x, stream)
-            for i in range(2):
-                node.compute(ws[i % len(ws)], y, stream)
-            reps = 6
-            evs = []
-            for i in range(reps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                node.compute(ws[i % len(ws)], y, stream)
-                e1.record(stream)
-                evs.append((e0, e1))
-            torch.cuda.synchronize()
-            ms = sum(a.elapsed_time(b) for a, b in evs) / reps
-            tflops = 2.0 * M * n * K / (ms * 1e-3) / 1e12
-            prefill.append({"M": M, "K": K, "N": n, "us": round(ms * 1e3, 1), "tflops": round(tflops, 1),
-                            "frac_of_f16_mfma_peak": round(tflops / 2500.0, 4)})
-            log(f"  prefill q4_K {M}x{K} N={n}: {ms * 1e3:8.1f} us  {tflops:7.1f} TFLOP/s")
-        del ws, base
-    torch.cuda.empty_cache()
-
-    traffic = None
+            traffic = None
 
     cpu = None
     if not args.no_cpu:
