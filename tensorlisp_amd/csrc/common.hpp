@@ -64,28 +64,35 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
 //   d   : f32   [R][K/blk]        block scales (q8_0: the f16-rounded d as f32)
 //   sum : int32 [R][K/32] (q8_0)  per-block code sums
 //         int16 [R][K/16] (q8_K)  bsums
+//   q16 : f16   [R][K]            (GEMM launches only) the codes as f16,
+//         exact, so the MFMA operand needs no conversion
 struct ActView {
     const int8_t *qs;
     const float *d;
     const int32_t *sum32;  // q8_0 only
     const int16_t *bsums;  // q8_K only
+    const _Float16 *q16;   // GEMM launches only
     int64_t K;
 };
 
 struct ActLayout {
-    int64_t qs_off, d_off, sum_off, total;
+    int64_t qs_off, d_off, sum_off, q16_off, total;
 };
+
+// GEMM launches (more than 8 activation columns) also get f16 codes.
+__host__ __device__ constexpr bool act_has_f16(int64_t n_cols) { return n_cols > 8; }
 
 __host__ __device__ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-__host__ __device__ inline ActLayout act_layout(int act_type, int64_t K, int64_t rows) {
+__host__ __device__ inline ActLayout act_layout(int act_type, int64_t K, int64_t rows, bool f16 = false) {
     ActLayout L;
     L.qs_off = 0;
     L.d_off = align_up(rows * K, 256);
     const int64_t nblk = K / block_elems(act_type);
     L.sum_off = align_up(L.d_off + rows * nblk * 4, 256);
     const int64_t sum_bytes = act_type == TLH_TYPE_Q8_K ? rows * (K / 16) * 2 : rows * (K / 32) * 4;
-    L.total = align_up(L.sum_off + sum_bytes, 256);
+    L.q16_off = align_up(L.sum_off + sum_bytes, 256);
+    L.total = align_up(L.q16_off + (f16 ? rows * K * 2 : 0), 256);
     return L;
 }
 
@@ -97,6 +104,7 @@ __host__ __device__ inline ActView act_view(const void *base, int act_type, int6
     v.d = (const float *)(b + L.d_off);
     v.sum32 = (const int32_t *)(b + L.sum_off);
     v.bsums = (const int16_t *)(b + L.sum_off);
+    v.q16 = (const _Float16 *)(b + L.q16_off);
     v.K = K;
     return v;
 }

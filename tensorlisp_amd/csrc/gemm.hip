@@ -19,9 +19,11 @@
 // Tiling: 128 (weight rows) x 128 (tokens) per workgroup of 4 waves, each
 // wave 64 x 64 as 2 x 2 MFMA tiles of 32 x 32; K advances in stages of one
 // 64-element q4_K chunk. Each stage is converted once per workgroup into f16
-// LDS tiles (nibble -> (1024 + n) * sc - 1024 * sc with one packed FMA; codes
-// -> (1152 + q) - 1152), the next stage's global loads are in flight while the
-// current one is multiplied.
+// LDS tiles (nibble -> (1024 + n) * sc - 1024 * sc with one packed FMA; the
+// activation codes arrive as exact f16 from the quantize pass). LDS holds two
+// stage buffers: while the waves multiply stage s, the threads write stage
+// s + 1 (fetched one stage earlier) into the other buffer and fetch s + 2, one
+// barrier per stage.
 //
 // q4_0 / q8_0 weights with N > 8 run through the GEMV kernels in slabs of 8
 // columns (correct for any N; not tuned).
@@ -34,36 +36,32 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int GBM = 128, GBN = 128, GBK = 64;
-constexpr int GLD = GBK + 8;  // halves per LDS row: 144 bytes, 16-byte aligned, conflict-free for b128 reads
 
+// LDS: two stage buffers of f16 tiles (row = 64 halves = 8 chunks of 16 bytes,
+// chunk c of row r stored at chunk position c ^ (r & 7) so the b128 operand
+// reads of 8 consecutive rows hit distinct banks), and two buffers of the
+// per-super-block metadata (by super-block parity).
 struct __attribute__((aligned(16))) GemmSmem {
-    __attribute__((aligned(16))) _Float16 A[GBM][GLD];
-    _Float16 B[GBN][GLD];
-    _Float16 Amin[GBM][16];  // m_{k/2} of the current super-block, per weight row
-    _Float16 Bsum[GBN][16];  // bsums of the current super-block, per token
-    float dA[GBM], dminA[GBM], dB[GBN];
+    _Float16 A[2][GBM][GBK];
+    _Float16 B[2][GBN][GBK];
+    uint8_t Amin[2][GBM][8];    // the 8 sub-block mins per weight row
+    _Float16 Bsum[2][GBN][16];  // bsums per token
+    float dA[2][GBM], dminA[2][GBM], dB[2][GBN];
 };
+
+__device__ __forceinline__ int swz(int row, int chunk) { return ((chunk ^ (row & 7)) << 3); }  // halves
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// 4 nibbles (one per byte of v) -> two half2 of sc * n, exact.
+// 4 nibbles (one per byte of v) -> two half2 of sc * n, exact:
+// (1024 + n) * sc - 1024 * sc in one packed FMA (the product is exact inside the FMA).
 __device__ __forceinline__ void nib4_to_h(uint32_t v, half2_t sc2, half2_t nsc2, uint32_t &o01, uint32_t &o23) {
     const half2_t a = __builtin_bit_cast(half2_t, perm(0x64646464u, v, 0x04010400u));  // 1024 + n0, 1024 + n1
     const half2_t b = __builtin_bit_cast(half2_t, perm(0x64646464u, v, 0x04030402u));  // 1024 + n2, 1024 + n3
     o01 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc2, nsc2));
     o23 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc2, nsc2));
-}
-
-// 4 int8 codes -> two half2, exact: bytes q ^ 0x80 = q + 128, then (1024 + q + 128) - 1152.
-__device__ __forceinline__ void q8x4_to_h(uint32_t v, uint32_t &o01, uint32_t &o23) {
-    const uint32_t u = v ^ 0x80808080u;
-    const half2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const half2_t a = __builtin_bit_cast(half2_t, perm(0x64646464u, u, 0x04010400u));
-    const half2_t b = __builtin_bit_cast(half2_t, perm(0x64646464u, u, 0x04030402u));
-    o01 = __builtin_bit_cast(uint32_t, a + bias);
-    o23 = __builtin_bit_cast(uint32_t, b + bias);
 }
 
 __device__ __forceinline__ void q4k_sm_g(int s, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &mn) {
@@ -79,16 +77,18 @@ __device__ __forceinline__ uint4 ldg16(const void *p) {
     return v;
 }
 
-// What one thread fetches from global memory for a stage.
+// What one thread fetches from global memory for a stage: its weight row's
+// 16 code bytes (half h of the chunk) and super-block header, its token's 32
+// f16 codes (half h of the chunk); at a super-block's first chunk also the
+// token's scale and 16 bsums.
 struct StageRegs {
-    uint4 wq;      // 16 code bytes of its weight row (half h of the chunk)
-    uint4 hdr;     // the row's super-block header (d, dmin, scales)
-    uint4 x0, x1;  // 32 activation codes of its token (half h of the chunk)
-    float dx;      // the token's super-block scale
-    uint4 bs0, bs1;  // the token's 16 bsums (int16)
+    uint4 wq, hdr;
+    uint4 x[4];
+    uint4 bs0, bs1;
+    float dx;
 };
 
-__global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_gemm_q4k(const MatmulArgs a) {
     __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -102,13 +102,13 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
     const int64_t m_base = (int64_t)blockIdx.y * GBM;
     const int64_t n_base = (int64_t)blockIdx.x * GBN;
 
-    // staging roles: row / token t >> 1, half h = t & 1 of the 64-element chunk
+    // staging roles: weight row / token tid >> 1, half h = tid & 1 of the 64-element chunk
     const int srow = tid >> 1, sh = tid & 1;
-    const int64_t grow = m_base + srow < a.M ? m_base + srow : a.M - 1;   // clamped: loads in bounds
+    const int64_t grow = m_base + srow < a.M ? m_base + srow : a.M - 1;  // clamped: loads in bounds
     const int64_t gcol = n_base + srow < a.N ? n_base + srow : a.N - 1;
     const uint8_t *wrow = W + grow * a.w_nb1;
     const int64_t arow = a.n0 + gcol + a.N_total * batch;
-    const int8_t *xrow = act.qs + arow * K;
+    const _Float16 *xrow = act.q16 + arow * K;
 
     auto fetch = [&](int64_t stage, StageRegs &r) {
         const int64_t sb = stage >> 2;
@@ -116,9 +116,9 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
         const uint8_t *blk = wrow + sb * Q4_K_BYTES;
         r.hdr = ldg16(blk);
         r.wq = ldg16(blk + 16 + 32 * j + 16 * sh);
-        const int8_t *xq = xrow + sb * QKK + 64 * j + 32 * sh;
-        r.x0 = *(const uint4 *)xq;
-        r.x1 = *(const uint4 *)(xq + 16);
+        const _Float16 *xq = xrow + sb * QKK + 64 * j + 32 * sh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.x[i] = *(const uint4 *)(xq + 8 * i);
         if (j == 0) {
             r.dx = act.d[arow * nsb + sb];
             const int16_t *bs = act.bsums + arow * (K / 16) + sb * 16;
@@ -128,6 +128,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
     };
 
     auto commit = [&](int64_t stage, const StageRegs &r) {
+        const int buf = (int)(stage & 1), mb = (int)((stage >> 2) & 1);
         const int j = (int)(stage & 3);
         int sclo, mnlo, schi, mnhi;
         q4k_sm_g(2 * j, r.hdr.y, r.hdr.z, r.hdr.w, sclo, mnlo);
@@ -143,43 +144,36 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
             nib4_to_h(w[i] & 0x0f0f0f0fu, sl2, nsl2, lo[2 * i], lo[2 * i + 1]);
             nib4_to_h((w[i] >> 4) & 0x0f0f0f0fu, sh2, nsh2, hi[2 * i], hi[2 * i + 1]);
         }
-        // low nibbles: k = 16h + i; high nibbles: k = 32 + 16h + i
-        *(uint4 *)&sm.A[srow][16 * sh] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *(uint4 *)&sm.A[srow][16 * sh + 8] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-        *(uint4 *)&sm.A[srow][32 + 16 * sh] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *(uint4 *)&sm.A[srow][32 + 16 * sh + 8] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-        const uint32_t xv[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
-        uint32_t xb[16];
+        // low nibbles: k = 16h + i (chunks 2h, 2h+1); high nibbles: k = 32 + 16h + i (chunks 4+2h, 5+2h)
+        _Float16 *ar = sm.A[buf][srow];
+        *(uint4 *)(ar + swz(srow, 2 * sh)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *(uint4 *)(ar + swz(srow, 2 * sh + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+        *(uint4 *)(ar + swz(srow, 4 + 2 * sh)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *(uint4 *)(ar + swz(srow, 5 + 2 * sh)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+        _Float16 *br = sm.B[buf][srow];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q8x4_to_h(xv[i], xb[2 * i], xb[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) *(uint4 *)(br + swz(srow, 4 * sh + i)) = r.x[i];
+        if (j == 0 && sh == 0) {
+            sm.dA[mb][srow] = h2f((uint16_t)(r.hdr.x & 0xffff));
+            sm.dminA[mb][srow] = h2f((uint16_t)(r.hdr.x >> 16));
+            uint32_t mv[2] = {0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(uint4 *)&sm.B[srow][32 * sh + 8 * i] = make_uint4(xb[4 * i], xb[4 * i + 1], xb[4 * i + 2], xb[4 * i + 3]);
-        if (j == 0) {
-            if (sh == 0) {
-                sm.dA[srow] = h2f((uint16_t)(r.hdr.x & 0xffff));
-                sm.dminA[srow] = h2f((uint16_t)(r.hdr.x >> 16));
-                uint32_t mv[8];
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    int sc, mn;
-                    q4k_sm_g(s, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
-                    const uint32_t h = f2h((float)mn);
-                    mv[s] = h | (h << 16);  // m_s at k = 2s and 2s + 1
-                }
-                *(uint4 *)&sm.Amin[srow][0] = make_uint4(mv[0], mv[1], mv[2], mv[3]);
-                *(uint4 *)&sm.Amin[srow][8] = make_uint4(mv[4], mv[5], mv[6], mv[7]);
-                sm.dB[srow] = r.dx;
-                const uint32_t bw[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
-                uint32_t bh[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int lo16 = (int)(int16_t)(bw[i] & 0xffff), hi16 = (int)(int16_t)(bw[i] >> 16);
-                    bh[i] = (uint32_t)f2h((float)lo16) | ((uint32_t)f2h((float)hi16) << 16);
-                }
-                *(uint4 *)&sm.Bsum[srow][0] = make_uint4(bh[0], bh[1], bh[2], bh[3]);
-                *(uint4 *)&sm.Bsum[srow][8] = make_uint4(bh[4], bh[5], bh[6], bh[7]);
+            for (int s = 0; s < 8; ++s) {
+                int sc, mn;
+                q4k_sm_g(s, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+                mv[s >> 2] |= (uint32_t)mn << (8 * (s & 3));
             }
+            *(uint2 *)&sm.Amin[mb][srow][0] = make_uint2(mv[0], mv[1]);
+            sm.dB[mb][srow] = r.dx;
+            const uint32_t bw[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
+            uint32_t bh[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int lo16 = (int)(int16_t)(bw[i] & 0xffff), hi16 = (int)(int16_t)(bw[i] >> 16);
+                bh[i] = (uint32_t)f2h((float)lo16) | ((uint32_t)f2h((float)hi16) << 16);
+            }
+            *(uint4 *)&sm.Bsum[mb][srow][0] = make_uint4(bh[0], bh[1], bh[2], bh[3]);
+            *(uint4 *)&sm.Bsum[mb][srow][8] = make_uint4(bh[4], bh[5], bh[6], bh[7]);
         }
     };
 
@@ -194,19 +188,21 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
 
     const int lr = lane & 31, lg = lane >> 5;  // MFMA operand row/col and k-group
     const int64_t stages = nsb * 4;
-    StageRegs cur, nxt;
-    fetch(0, cur);
+    StageRegs pre;
+    fetch(0, pre);
+    commit(0, pre);
+    if (stages > 1) fetch(1, pre);
+    __syncthreads();
     for (int64_t st = 0; st < stages; ++st) {
-        commit(st, cur);
-        if (st + 1 < stages) fetch(st + 1, nxt);
-        __syncthreads();
+        const int buf = (int)(st & 1);
 #pragma unroll
         for (int t = 0; t < GBK / 16; ++t) {
             half8_t av[2], bv[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                av[i] = *(const half8_t *)&sm.A[64 * wm + 32 * i + lr][16 * t + 8 * lg];
-                bv[i] = *(const half8_t *)&sm.B[64 * wn + 32 * i + lr][16 * t + 8 * lg];
+                const int ra = 64 * wm + 32 * i + lr, rb = 64 * wn + 32 * i + lr;
+                av[i] = *(const half8_t *)&sm.A[buf][ra][swz(ra, 2 * t + lg)];
+                bv[i] = *(const half8_t *)&sm.B[buf][rb][swz(rb, 2 * t + lg)];
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -216,42 +212,53 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(const MatmulArgs a) {
         }
         if ((st & 3) == 3) {
             // super-block finalize: acc += dy * (d * S - dmin * Mn)
+            const int mb = (int)((st >> 2) & 1);
+            // Mn operands: A'[m][k] = m_{k/2}, k = 8g..8g+7 -> mins 4g..4g+3, each twice
             half8_t am[2], bm[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                am[i] = *(const half8_t *)&sm.Amin[64 * wm + 32 * i + lr][8 * lg];
-                bm[i] = *(const half8_t *)&sm.Bsum[64 * wn + 32 * i + lr][8 * lg];
+                const uint32_t mw = *(const uint32_t *)&sm.Amin[mb][64 * wm + 32 * i + lr][4 * lg];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const _Float16 h = (_Float16)(float)((mw >> (8 * e)) & 0xff);
+                    am[i][2 * e] = h;
+                    am[i][2 * e + 1] = h;
+                }
+                bm[i] = *(const half8_t *)&sm.Bsum[mb][64 * wn + 32 * i + lr][8 * lg];
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                float dv[16], dmv[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int m0 = 64 * wm + 32 * i + 8 * q + 4 * lg;
-                    const float4 d4 = *(const float4 *)&sm.dA[m0];
-                    const float4 dm4 = *(const float4 *)&sm.dminA[m0];
-                    dv[4 * q] = d4.x; dv[4 * q + 1] = d4.y; dv[4 * q + 2] = d4.z; dv[4 * q + 3] = d4.w;
-                    dmv[4 * q] = dm4.x; dmv[4 * q + 1] = dm4.y; dmv[4 * q + 2] = dm4.z; dmv[4 * q + 3] = dm4.w;
-                }
 #pragma unroll
                 for (int jn = 0; jn < 2; ++jn) {
-                    const float16_t Mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[jn], (float16_t){}, 0, 0, 0);
-                    const float dy = sm.dB[64 * wn + 32 * jn + lr];
+                    const float16_t Mn =
+                        __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[jn], (float16_t){}, 0, 0, 0);
+                    const float dy = sm.dB[mb][64 * wn + 32 * jn + lr];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float t1 = dv[r] * S[i][jn][r] - dmv[r] * Mn[r];
-                        acc[i][jn][r] += dy * t1;
+                    for (int q = 0; q < 4; ++q) {
+                        const int m0 = 64 * wm + 32 * i + 8 * q + 4 * lg;
+                        const float4 d4 = *(const float4 *)&sm.dA[mb][m0];
+                        const float4 dm4 = *(const float4 *)&sm.dminA[mb][m0];
+                        const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, dmv[4] = {dm4.x, dm4.y, dm4.z, dm4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * q + e;
+                            acc[i][jn][r] += dy * (dv[e] * S[i][jn][r] - dmv[e] * Mn[r]);
+                        }
                     }
                     S[i][jn] = (float16_t){};
                 }
             }
         }
+        // stage st + 1 goes to the other buffer (free since the last barrier),
+        // stage st + 2 is fetched behind this stage's products
+        if (st + 1 < stages) {
+            commit(st + 1, pre);
+            if (st + 2 < stages) fetch(st + 2, pre);
+        }
         __syncthreads();
-        cur = nxt;
     }
 
-    // store: lane holds token n = lane % 32 of each 32 x 32 tile and rows
-    // 8q + 4g + (0..3)
+    // store: lane holds token n = lane % 32 of each 32 x 32 tile and rows 8q + 4g + (0..3)
     char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
 #pragma unroll
     for (int i = 0; i < 2; ++i)

@@ -12,8 +12,9 @@ tlh_status check_launch(const char *what);
 
 // rows of x (stride x_row_bytes) -> activation rows row_off.. of an output of
 // total_rows rows, in ggml's block layout or the split scratch layout.
+// f16: also write the codes as f16 (the scratch of a GEMM launch).
 tlh_status launch_quantize_act(int wtype, const float *x, int64_t K, int64_t rows, int64_t x_row_bytes, void *out,
-                               bool ggml_layout, int64_t row_off, int64_t total_rows, hipStream_t stream);
+                               bool ggml_layout, int64_t row_off, int64_t total_rows, bool f16, hipStream_t stream);
 tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, int64_t w_row_bytes, float *y,
                              hipStream_t stream);
 

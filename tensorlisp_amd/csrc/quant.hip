@@ -22,7 +22,7 @@ namespace tlh {
 template <bool GGML_LAYOUT>
 __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__ x, int64_t K, int64_t rows,
                                                        int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
-                                                       int64_t total_rows) {
+                                                       int64_t total_rows, bool f16) {
 #pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t total = K * rows;
@@ -45,9 +45,10 @@ __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__
         b[2 + lane32] = (uint8_t)(int8_t)q;
         if (lane32 == 0) *(uint16_t *)b = dh;
     } else {
-        const ActLayout L = act_layout(TLH_TYPE_Q8_0, K, total_rows);
+        const ActLayout L = act_layout(TLH_TYPE_Q8_0, K, total_rows, f16);
         int8_t *qs = (int8_t *)out + L.qs_off;
         qs[orow * K + col] = (int8_t)q;
+        if (f16) ((_Float16 *)((char *)out + L.q16_off))[orow * K + col] = (_Float16)q;
         int s = q;
 #pragma unroll
         for (int m = 16; m >= 1; m >>= 1) s += __shfl_xor(s, m, 32);
@@ -67,7 +68,7 @@ __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__
 template <bool GGML_LAYOUT>
 __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__ x, int64_t K, int64_t rows,
                                                        int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
-                                                       int64_t total_rows) {
+                                                       int64_t total_rows, bool f16) {
 #pragma clang fp contract(off)
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
@@ -116,8 +117,17 @@ __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__
         if ((lane & 3) == 0) *(int16_t *)(b + 4 + QKK + 2 * (lane >> 2)) = (int16_t)psum;
         if (lane == 0) *(float *)b = d;
     } else {
-        const ActLayout L = act_layout(TLH_TYPE_Q8_K, K, total_rows);
+        const ActLayout L = act_layout(TLH_TYPE_Q8_K, K, total_rows, f16);
         *(uint32_t *)((char *)out + L.qs_off + orow * K + blk * QKK + 4 * lane) = packed;
+        if (f16) {
+            uint32_t h[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int c0 = (int)(int8_t)(packed >> (16 * i)), c1 = (int)(int8_t)(packed >> (16 * i + 8));
+                h[i] = (uint32_t)f2h((float)c0) | ((uint32_t)f2h((float)c1) << 16);
+            }
+            *(uint2 *)((char *)out + L.q16_off + (orow * K + blk * QKK + 4 * lane) * 2) = make_uint2(h[0], h[1]);
+        }
         if ((lane & 3) == 0)
             ((int16_t *)((char *)out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
         if (lane == 0) ((float *)((char *)out + L.d_off))[orow * nblk + blk] = d;
@@ -171,24 +181,24 @@ static inline unsigned grid_for(int64_t threads, int per_block) {
 }
 
 tlh_status launch_quantize_act(int wtype, const float *x, int64_t K, int64_t rows, int64_t x_row_bytes, void *out,
-                               bool ggml_layout, int64_t row_off, int64_t total_rows, hipStream_t stream) {
+                               bool ggml_layout, int64_t row_off, int64_t total_rows, bool f16, hipStream_t stream) {
     if (rows == 0 || K == 0) return TLH_OK;
     if (vec_dot_type(wtype) == TLH_TYPE_Q8_0) {
         const unsigned g = grid_for(K * rows, 256);
         if (ggml_layout)
             hipLaunchKernelGGL(k_quantize_q8_0<true>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows);
+                               row_off, total_rows, f16);
         else
             hipLaunchKernelGGL(k_quantize_q8_0<false>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows);
+                               row_off, total_rows, f16);
     } else {
         const unsigned g = grid_for((K / QKK) * rows * 64, 256);
         if (ggml_layout)
             hipLaunchKernelGGL(k_quantize_q8_K<true>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows);
+                               row_off, total_rows, f16);
         else
             hipLaunchKernelGGL(k_quantize_q8_K<false>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows);
+                               row_off, total_rows, f16);
     }
     return check_launch("quantize_act");
 }

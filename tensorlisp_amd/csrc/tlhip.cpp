@@ -195,12 +195,12 @@ tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes) {
     MulMatShape s;
     const tlh_status st = check_mul_mat(op, s);
     if (st != TLH_OK) return st;
-    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows).total;
+    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.N)).total;
     return TLH_OK;
 }
 
 static tlh_status mm_check_scratch(const MulMatShape &s, const void *scratch, size_t scratch_bytes) {
-    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows).total;
+    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.N)).total;
     if (!scratch || scratch_bytes < need)
         return set_error(TLH_INVALID, "mul_mat: scratch of %zu bytes, need %zu", scratch_bytes, need);
     if ((uintptr_t)scratch & 255) return set_error(TLH_INVALID, "mul_mat: scratch must be 256-byte aligned");
@@ -215,12 +215,12 @@ static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
     if (packed)
         return launch_quantize_act(a.ty, (const float *)src1, s.K, s.act_rows, b.nb[1], scratch, false, 0,
-                                   s.act_rows, hs);
+                                   s.act_rows, act_has_f16(s.N), hs);
     for (int64_t i13 = 0; i13 < s.ne13; ++i13)
         for (int64_t i12 = 0; i12 < s.ne12; ++i12) {
             const float *x = (const float *)((const char *)src1 + i12 * b.nb[2] + i13 * b.nb[3]);
             const tlh_status st = launch_quantize_act(a.ty, x, s.K, s.N, b.nb[1], scratch, false,
-                                                      s.N * (i12 + s.ne12 * i13), s.act_rows, hs);
+                                                      s.N * (i12 + s.ne12 * i13), s.act_rows, act_has_f16(s.N), hs);
             if (st != TLH_OK) return st;
         }
     return TLH_OK;
@@ -314,7 +314,7 @@ tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, 
     if ((!x || !y) && k * rows > 0) return set_error(TLH_INVALID, "quantize_act: null pointer");
     if (x_row_bytes < 4 * k || (x_row_bytes & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
         return set_error(TLH_INVALID, "quantize_act: rows must be 4-byte aligned f32 with stride >= 4k");
-    return launch_quantize_act(wtype, x, k, rows, x_row_bytes, y, true, 0, rows, (hipStream_t)stream);
+    return launch_quantize_act(wtype, x, k, rows, x_row_bytes, y, true, 0, rows, false, (hipStream_t)stream);
 }
 
 tlh_status tlh_dequantize(int type, const void *w, int64_t k, int64_t rows, int64_t w_row_bytes, float *y,
