@@ -217,6 +217,47 @@ def main() -> int:
         del ws, base
     torch.cuda.empty_cache()
 
+    # paged-attention decode: 32 sequences, 32 q / 8 kv heads, hs 128, 16-token
+    # pages scattered over a 65,536-page pool (2 GiB per cache), lens ~ U[512, 8192]
+    seqs, heads, kvh, hs, bs, pool = 32, 32, 8, 128, 16, 65536
+    lens = torch.randint(512, 8193, (seqs,), device="cuda", generator=gen, dtype=torch.int32)
+    maxb = 8192 // bs
+    kc = torch.randn((pool, kvh, hs // 8, bs, 8), device="cuda", generator=gen, dtype=torch.float16)
+    vc = torch.randn((pool, kvh, hs, bs), device="cuda", generator=gen, dtype=torch.float16)
+    tables = torch.randperm(pool, device="cuda", generator=gen)[: seqs * maxb].to(torch.int32).reshape(seqs, maxb)
+    qa = torch.randn((seqs, heads, hs), device="cuda", generator=gen, dtype=torch.float16)
+    oa = torch.empty_like(qa)
+    pa = N.PagedAttention(seqs, heads, kvh, hs, bs, maxb, 8192, hs ** -0.5)
+    lsum = int(lens.sum().item())
+    pages = int(((lens + bs - 1) // bs).sum().item())
+    attn_bytes = lsum * kvh * hs * 2 * 2 + 2 * seqs * heads * hs * 2 + pages * 4 + seqs * 4
+    for _ in range(2):
+        pa(oa, qa, kc, vc, tables, lens, stream)
+    evs = []
+    for _ in range(10):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        pa(oa, qa, kc, vc, tables, lens, stream)
+        e1.record(stream)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    attn_gbs = attn_bytes / attn_ms / 1e6
+    attention = {"seqs": seqs, "heads": heads, "kv_heads": kvh, "head_size": hs, "block_size": bs,
+                 "context_tokens": lsum, "bytes": attn_bytes, "us": round(attn_ms * 1e3, 1),
+                 "gbs": round(attn_gbs, 1), "frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4)}
+    log(f"  paged attention {seqs} seqs, {lsum} tokens: {attn_ms * 1e3:8.1f} us  {attn_gbs:7.0f} GB/s")
+    del kc, vc
+    torch.cuda.empty_cache()
+
+    # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
+    # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
@@ -252,6 +293,7 @@ def main() -> int:
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
             "prefill_gemm_q4k": prefill,
+            "paged_attention_decode": attention,
         },
         "roofline": {
             "bound": "hbm",
