@@ -258,13 +258,15 @@ def main() -> int:
     torch.cuda.synchronize()
     del src, dst
 
+    # HBM bytes per launch of the roofline kernel, as measured by the rocprofv3 PMC runs
+    # summarised in profiles/ (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size)
     traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
+    tfile = ROOT / "profiles" / "traffic.txt"
     if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("gemv_q4_K_128256x4096_n1_bytes")
-        except (ValueError, OSError):
-            traffic = None
+        for ln in tfile.read_text().splitlines():
+            key, _, val = ln.partition("=")
+            if key.strip() == "gemv_q4_K_128256x4096_n1_bytes" and val.strip().isdigit():
+                traffic = int(val.strip())
 
     cpu = None
     if not args.no_cpu:
