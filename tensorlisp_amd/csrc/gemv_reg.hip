@@ -204,7 +204,134 @@ __device__ __forceinline__ float treduce(float (&v)[1 << LV], int lane, int &vid
 template <int X> struct L2 { static constexpr int v = 1 + L2<X / 2>::v; };
 template <> struct L2<1> { static constexpr int v = 0; };
 
-template <int WT, int NC, int R, bool FUSED>
+// One lane's weight bytes for its unit u of R rows, and their products with
+// the lane's activation slice.
+template <int WT, int R> struct WRegs;
+
+template <int R> struct WRegs<TLH_TYPE_Q4_K, R> {
+    uint4 hd[R], q0[R], q1[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+        const int64_t sb = u >> 2;
+        const int j = (int)(u & 3);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + sb * Q4_K_BYTES;
+            hd[r] = ldu16(blk);
+            q0[r] = ldu16(blk + 16 + 32 * j);
+            q1[r] = ldu16(blk + 32 + 32 * j);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t u, float (&acc)[R][NC]) const {
+        const int j = (int)(u & 3);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            int lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                lo[i] = (int)(w[i] & 0x0f0f0f0fu);
+                hi[i] = (int)((w[i] >> 4) & 0x0f0f0f0fu);
+            }
+            int sclo, mnlo, schi, mnhi;
+            q4k_sm_r(2 * j, hd[r].y, hd[r].z, hd[r].w, sclo, mnlo);
+            q4k_sm_r(2 * j + 1, hd[r].y, hd[r].z, hd[r].w, schi, mnhi);
+            const float d = h2f((uint16_t)(hd[r].x & 0xffff));
+            const float dmin = h2f((uint16_t)(hd[r].x >> 16));
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    dl = dot4(lo[i], act[n].q[i], dl);
+                    dh = dot4(hi[i], act[n].q[8 + i], dh);
+                }
+                const int S = sclo * dl + schi * dh;
+                const int Mn = mnlo * act[n].s0 + mnhi * act[n].s1;
+                acc[r][n] += (d * act[n].d0) * (float)S - (dmin * act[n].d0) * (float)Mn;
+            }
+        }
+    }
+};
+
+template <int R> struct WRegs<TLH_TYPE_Q4_0, R> {
+    uint4 w0[R], w1[R];
+    float dw0[R], dw1[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + u * (2 * Q4_0_BYTES);
+            dw0[r] = h2f(*(const uint16_t *)blk);
+            w0[r] = ldu16(blk + 2);
+            dw1[r] = h2f(*(const uint16_t *)(blk + Q4_0_BYTES));
+            w1[r] = ldu16(blk + Q4_0_BYTES + 2);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t, float (&acc)[R][NC]) const {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t wa[4] = {w0[r].x, w0[r].y, w0[r].z, w0[r].w};
+            const uint32_t wb[4] = {w1[r].x, w1[r].y, w1[r].z, w1[r].w};
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int s0 = 0, s1 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    s0 = dot4((int)(wa[i] & 0x0f0f0f0fu), act[n].q[i], s0);
+                    s0 = dot4((int)((wa[i] >> 4) & 0x0f0f0f0fu), act[n].q[4 + i], s0);
+                    s1 = dot4((int)(wb[i] & 0x0f0f0f0fu), act[n].q[8 + i], s1);
+                    s1 = dot4((int)((wb[i] >> 4) & 0x0f0f0f0fu), act[n].q[12 + i], s1);
+                }
+                s0 -= 8 * act[n].s0;  // codes are nibble - 8
+                s1 -= 8 * act[n].s1;
+                acc[r][n] += ((float)s0 * dw0[r]) * act[n].d0;
+                acc[r][n] += ((float)s1 * dw1[r]) * act[n].d1;
+            }
+        }
+    }
+};
+
+template <int R> struct WRegs<TLH_TYPE_Q8_0, R> {
+    uint4 w0[R], w1[R], w2[R], w3[R];
+    float dw0[R], dw1[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + u * (2 * Q8_0_BYTES);
+            dw0[r] = h2f(*(const uint16_t *)blk);
+            w0[r] = ldu16(blk + 2);
+            w1[r] = ldu16(blk + 18);
+            dw1[r] = h2f(*(const uint16_t *)(blk + Q8_0_BYTES));
+            w2[r] = ldu16(blk + Q8_0_BYTES + 2);
+            w3[r] = ldu16(blk + Q8_0_BYTES + 18);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t, float (&acc)[R][NC]) const {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t wv[16] = {w0[r].x, w0[r].y, w0[r].z, w0[r].w, w1[r].x, w1[r].y, w1[r].z, w1[r].w,
+                                     w2[r].x, w2[r].y, w2[r].z, w2[r].w, w3[r].x, w3[r].y, w3[r].z, w3[r].w};
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int s0 = 0, s1 = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    s0 = dot4((int)wv[i], act[n].q[i], s0);
+                    s1 = dot4((int)wv[8 + i], act[n].q[8 + i], s1);
+                }
+                acc[r][n] += (float)s0 * (dw0[r] * act[n].d0);
+                acc[r][n] += (float)s1 * (dw1[r] * act[n].d1);
+            }
+        }
+    }
+};
+
+// PIPE: double-buffer the weight registers so the next row block's loads are
+// in flight while this one is multiplied (for grids that loop over many row
+// blocks; it costs the registers of a second weight set).
+template <int WT, int NC, int R, bool FUSED, bool PIPE>
 __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const float *__restrict__ x,
                                                   int64_t x_row_bytes, int ksplit, int upw) {
     constexpr int AT = vec_dot_type(WT);
@@ -224,6 +351,27 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
     const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
     const int64_t arow0 = a.n0 + a.N_total * batch;
+    const int64_t rows_per_block = (int64_t)groups * R;
+
+    auto row_ptrs = [&](int64_t rb, const uint8_t *(&wrow)[R]) {
+        const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // clamp: loads in bounds, store skipped
+            wrow[r] = W + m * a.w_nb1;
+        }
+    };
+
+    // the first row block's weights are requested before the activation
+    // slice is read and quantized, so the two memory latencies overlap
+    WRegs<WT, R> cur;
+    int64_t rb = blockIdx.x;
+    bool have = rb * rows_per_block < a.M;
+    if (have && uvalid) {
+        const uint8_t *wrow[R];
+        row_ptrs(rb, wrow);
+        cur.load(wrow, u);
+    }
 
     AUnit act[NC];
 #pragma unroll
@@ -238,122 +386,25 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     }
 
     char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
-    const int64_t rows_per_block = (int64_t)groups * R;
-    for (int64_t rb = blockIdx.x; rb * rows_per_block < a.M; rb += gridDim.x) {
-        const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
+    while (have) {
+        const int64_t rb_next = rb + gridDim.x;
+        const bool have_next = rb_next * rows_per_block < a.M;
+        WRegs<WT, R> nxt;
+        if constexpr (PIPE) {
+            if (have_next && uvalid) {
+                const uint8_t *wrow[R];
+                row_ptrs(rb_next, wrow);
+                nxt.load(wrow, u);
+            }
+        }
         float acc[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int n = 0; n < NC; ++n) acc[r][n] = 0.0f;
-        if (uvalid) {
-            const uint8_t *wrow[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // clamp: loads in bounds, store skipped
-                wrow[r] = W + m * a.w_nb1;
-            }
-            if constexpr (WT == TLH_TYPE_Q4_K) {
-                const int64_t sb = u >> 2;
-                const int j = (int)(u & 3);
-                uint4 hd[R], q0[R], q1[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint8_t *blk = wrow[r] + sb * Q4_K_BYTES;
-                    hd[r] = ldu16(blk);
-                    q0[r] = ldu16(blk + 16 + 32 * j);
-                    q1[r] = ldu16(blk + 32 + 32 * j);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint32_t w[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
-                    int lo[8], hi[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        lo[i] = (int)(w[i] & 0x0f0f0f0fu);
-                        hi[i] = (int)((w[i] >> 4) & 0x0f0f0f0fu);
-                    }
-                    int sclo, mnlo, schi, mnhi;
-                    q4k_sm_r(2 * j, hd[r].y, hd[r].z, hd[r].w, sclo, mnlo);
-                    q4k_sm_r(2 * j + 1, hd[r].y, hd[r].z, hd[r].w, schi, mnhi);
-                    const float d = h2f((uint16_t)(hd[r].x & 0xffff));
-                    const float dmin = h2f((uint16_t)(hd[r].x >> 16));
-#pragma unroll
-                    for (int n = 0; n < NC; ++n) {
-                        int dl = 0, dh = 0;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            dl = dot4(lo[i], act[n].q[i], dl);
-                            dh = dot4(hi[i], act[n].q[8 + i], dh);
-                        }
-                        const int S = sclo * dl + schi * dh;
-                        const int Mn = mnlo * act[n].s0 + mnhi * act[n].s1;
-                        acc[r][n] += (d * act[n].d0) * (float)S - (dmin * act[n].d0) * (float)Mn;
-                    }
-                }
-            } else if constexpr (WT == TLH_TYPE_Q4_0) {
-                uint4 w0[R], w1[R];
-                float dw0[R], dw1[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint8_t *blk = wrow[r] + u * (2 * Q4_0_BYTES);
-                    dw0[r] = h2f(*(const uint16_t *)blk);
-                    w0[r] = ldu16(blk + 2);
-                    dw1[r] = h2f(*(const uint16_t *)(blk + Q4_0_BYTES));
-                    w1[r] = ldu16(blk + Q4_0_BYTES + 2);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint32_t wa[4] = {w0[r].x, w0[r].y, w0[r].z, w0[r].w};
-                    const uint32_t wb[4] = {w1[r].x, w1[r].y, w1[r].z, w1[r].w};
-#pragma unroll
-                    for (int n = 0; n < NC; ++n) {
-                        int s0 = 0, s1 = 0;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            s0 = dot4((int)(wa[i] & 0x0f0f0f0fu), act[n].q[i], s0);
-                            s0 = dot4((int)((wa[i] >> 4) & 0x0f0f0f0fu), act[n].q[4 + i], s0);
-                            s1 = dot4((int)(wb[i] & 0x0f0f0f0fu), act[n].q[8 + i], s1);
-                            s1 = dot4((int)((wb[i] >> 4) & 0x0f0f0f0fu), act[n].q[12 + i], s1);
-                        }
-                        s0 -= 8 * act[n].s0;  // codes are nibble - 8
-                        s1 -= 8 * act[n].s1;
-                        acc[r][n] += ((float)s0 * dw0[r]) * act[n].d0;
-                        acc[r][n] += ((float)s1 * dw1[r]) * act[n].d1;
-                    }
-                }
-            } else {  // Q8_0
-                uint4 w0[R], w1[R], w2[R], w3[R];
-                float dw0[R], dw1[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint8_t *blk = wrow[r] + u * (2 * Q8_0_BYTES);
-                    dw0[r] = h2f(*(const uint16_t *)blk);
-                    w0[r] = ldu16(blk + 2);
-                    w1[r] = ldu16(blk + 18);
-                    dw1[r] = h2f(*(const uint16_t *)(blk + Q8_0_BYTES));
-                    w2[r] = ldu16(blk + Q8_0_BYTES + 2);
-                    w3[r] = ldu16(blk + Q8_0_BYTES + 18);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint32_t wv[16] = {w0[r].x, w0[r].y, w0[r].z, w0[r].w, w1[r].x, w1[r].y, w1[r].z, w1[r].w,
-                                             w2[r].x, w2[r].y, w2[r].z, w2[r].w, w3[r].x, w3[r].y, w3[r].z, w3[r].w};
-#pragma unroll
-                    for (int n = 0; n < NC; ++n) {
-                        int s0 = 0, s1 = 0;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            s0 = dot4((int)wv[i], act[n].q[i], s0);
-                            s1 = dot4((int)wv[8 + i], act[n].q[8 + i], s1);
-                        }
-                        acc[r][n] += (float)s0 * (dw0[r] * act[n].d0);
-                        acc[r][n] += (float)s1 * (dw1[r] * act[n].d1);
-                    }
-                }
-            }
-        }
+        if (uvalid) cur.template compute<NC>(act, u, acc);
 
+        const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
         float vals[VP];
 #pragma unroll
         for (int i = 0; i < VP; ++i) vals[i] = i < V ? acc[i / NC][i % NC] : 0.0f;
@@ -370,36 +421,62 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             __syncthreads();
             if (kw == 0 && holder && vi < V) {
                 float t = 0.0f;
-                for (int s = 0; s < ksplit; ++s) t += part[grp * ksplit + s][vi];
+                for (int s2 = 0; s2 < ksplit; ++s2) t += part[grp * ksplit + s2][vi];
                 const int r = vi / NC, n = vi % NC;
                 if (m0 + r < a.M && n < a.N) *(float *)(dbase + (a.n0 + n) * a.d_nb1 + (m0 + r) * 4) = t;
             }
             __syncthreads();
         }
+        if constexpr (PIPE) {
+            cur = nxt;
+        } else if (have_next && uvalid) {
+            const uint8_t *wrow[R];
+            row_ptrs(rb_next, wrow);
+            cur.load(wrow, u);
+        }
+        rb = rb_next;
+        have = have_next;
     }
 }
 
-template <int WT, int NC, int R, bool FUSED>
-static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
-                                 hipStream_t stream) {
-    auto kern = k_gemv_reg<WT, NC, R, FUSED>;
-    static int blocks_per_cu = -1, cus = 0;
-    if (blocks_per_cu < 0) {
-        int dev = 0;
+// Workgroups of `kern` that the device holds at once (cached per kernel).
+template <typename Kern> static int64_t resident_blocks(Kern kern, int &cache) {
+    if (cache < 0) {
+        int dev = 0, cus = 0, nb = 0;
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
-        blocks_per_cu = nb;
+        cache = cus * nb;
     }
-    const int groups = 4 / ksplit;
-    const int64_t row_blocks = (a.M + (int64_t)groups * R - 1) / ((int64_t)groups * R);
+    return cache;
+}
+
+template <int WT, int NC, int R, bool FUSED, bool PIPE>
+static tlh_status launch_reg_pipe(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
+                                  int64_t row_blocks, hipStream_t stream) {
+    auto kern = k_gemv_reg<WT, NC, R, FUSED, PIPE>;
+    static int slots = -1;
     const int64_t batches = a.ne12 * a.ne13;
-    int64_t resident = (int64_t)cus * blocks_per_cu / (batches > 0 ? batches : 1);
+    int64_t resident = resident_blocks(kern, slots) / (batches > 0 ? batches : 1);
     if (resident < 1) resident = 1;
     const unsigned gx = (unsigned)(row_blocks < resident ? row_blocks : resident);
     hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(256), 0, stream, a, x, x_row_bytes, ksplit, upw);
     return check_launch("gemv");
+}
+
+// A persistent grid walks the row blocks; once each workgroup has several to
+// walk, the double-buffered kernel keeps the weight stream busy.
+template <int WT, int NC, int R, bool FUSED>
+static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
+                                 hipStream_t stream) {
+    static int slots = -1;
+    const int groups = 4 / ksplit;
+    const int64_t row_blocks = (a.M + (int64_t)groups * R - 1) / ((int64_t)groups * R);
+    const int64_t batches = a.ne12 * a.ne13 > 0 ? a.ne12 * a.ne13 : 1;
+    const int64_t resident = resident_blocks(k_gemv_reg<WT, NC, R, FUSED, false>, slots);
+    if (row_blocks * batches > 2 * resident)
+        return launch_reg_pipe<WT, NC, R, FUSED, true>(a, x, x_row_bytes, ksplit, upw, row_blocks, stream);
+    return launch_reg_pipe<WT, NC, R, FUSED, false>(a, x, x_row_bytes, ksplit, upw, row_blocks, stream);
 }
 
 template <int WT, int NC, bool FUSED>
