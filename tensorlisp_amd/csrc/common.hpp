@@ -79,8 +79,8 @@ struct ActLayout {
     int64_t qs_off, d_off, sum_off, q16_off, total;
 };
 
-// GEMM launches (more than 8 activation columns) also get f16 codes.
-__host__ __device__ constexpr bool act_has_f16(int64_t n_cols) { return n_cols > 8; }
+// q4_K GEMM launches (more than 16 activation columns) also get f16 codes.
+__host__ __device__ constexpr bool act_has_f16(int wtype, int64_t n_cols) { return wtype == TLH_TYPE_Q4_K && n_cols > 16; }
 
 __host__ __device__ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
@@ -120,6 +120,14 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
     return v;
 }
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
+// and meets the other waves, but leaves its global loads in flight.
+// __syncthreads() also drains the outstanding global loads (its workgroup
+// fence waits for vmcnt 0), which would stall every load issued ahead of a
+// barrier as a prefetch. Global memory written before this barrier is not
+// made visible to the other waves.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // int8x4 dot product with accumulate (v_dot4c_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -25,8 +25,9 @@
 // s + 1 (fetched one stage earlier) into the other buffer and fetch s + 2, one
 // barrier per stage.
 //
-// q4_0 / q8_0 weights with N > 8 run through the GEMV kernels in slabs of 8
-// columns (correct for any N; not tuned).
+// q4_0 / q8_0 weights with N > 16 run through the int8-MFMA few-column kernel
+// (gemv_mfma.hip) in slabs of 16 columns (correct for any N; each slab
+// re-reads the weights).
 #include "kernels.hpp"
 
 namespace tlh {
@@ -192,7 +193,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     fetch(0, pre);
     commit(0, pre);
     if (stages > 1) fetch(1, pre);
-    __syncthreads();
+    lds_barrier();
     for (int64_t st = 0; st < stages; ++st) {
         const int buf = (int)(st & 1);
 #pragma unroll
@@ -255,7 +256,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             commit(st + 1, pre);
             if (st + 2 < stages) fetch(st + 2, pre);
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // store: lane holds token n = lane % 32 of each 32 x 32 tile and rows 8q + 4g + (0..3)
@@ -284,11 +285,11 @@ tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(256), 0, stream, a);
         return check_launch("gemm_q4k");
     }
-    for (int64_t c = 0; c < a.N; c += 8) {
+    for (int64_t c = 0; c < a.N; c += 16) {
         MatmulArgs s = a;
         s.n0 = a.n0 + c;
-        s.N = a.N - c < 8 ? a.N - c : 8;
-        const tlh_status st = launch_gemv(s, nullptr, 0, stream);
+        s.N = a.N - c < 16 ? a.N - c : 16;
+        const tlh_status st = launch_gemv_mfma(s, stream);
         if (st != TLH_OK) return st;
     }
     return TLH_OK;

@@ -428,10 +428,11 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 }
 
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
-    if (a.N < 1 || a.N > 8) return set_error(TLH_INVALID, "gemv: N=%lld outside 1..8", (long long)a.N);
+    if (a.N < 1 || a.N > 16) return set_error(TLH_INVALID, "gemv: N=%lld outside 1..16", (long long)a.N);
     int ksplit, upw;
     if (a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw)) return launch_gemv_reg(a, x, x_row_bytes, stream);
     if (x != nullptr) return set_error(TLH_INVALID, "gemv: fused quantization needs N <= 2, K <= 16384, K %% 64 == 0");
+    return launch_gemv_mfma(a, stream);
     // other K: activation codes staged in LDS from the scratch
     if (!fits_lds(a.wtype, a.K, (int)a.N))
         return set_error(TLH_UNSUPPORTED, "gemv: K=%lld x N=%lld activations exceed LDS", (long long)a.K,

@@ -1,0 +1,507 @@
+// Few-column GEMM for GGML_OP_MUL_MAT with 3..16 activation columns, gfx950:
+// integer matrix cores (v_mfma_i32_16x16x32_i8) instead of v_dot4.
+//
+// With more than two columns the dot4 GEMV needs every activation column in
+// every lane, so it streams them from LDS, about ten LDS bytes per weight
+// byte, and LDS bandwidth, not HBM, sets its speed. An MFMA shares its
+// operands across the wave: the 16 x 32 activation operand of one step is
+// 8 bytes per lane. Here each wave keeps the activation operands of its own
+// slice of K in registers for the whole launch and streams weight row groups
+// past them, so activations cost no memory traffic after the first read.
+//
+// The MFMA is oriented so that each lane's outputs share one weight row:
+//   D[i][j] = sum_k A[i][k] * B[k][j],  A = activation codes (i = column,
+//   16 columns, the ones past N zero), B = weight codes (j = weight row of a
+//   16-row group), k = 32 elements of one block / sub-block.
+// Operand lane layout (16x16x32 int8): lane l holds A[l % 16][8g .. 8g+7] and
+// B[8g .. 8g+7][l % 16] with g = l / 16; D lane l holds D[4g + r][l % 16],
+// r = 0..3. So the weight row's scales, read by the lane that holds its
+// codes, are also the scales of that lane's outputs.
+//
+// Per block the integer sums are exactly those of the CPU's vec_dot
+// (ggml-cpu/quants.c): q4_0 / q8_0 blocks of 32 elements are one MFMA each
+// (sumi), scaled in f32 as the CPU does (:255, :475); a q4_K super-block is
+// eight sub-block MFMAs, each S_s folded into an int32 as sum sc_s * S_s, and
+// the min term Mn = sum_s m_s * (sum of q8 in s) is eight more MFMAs whose
+// weight operand is m_s broadcast over the sub-block (:696-773).
+//
+// Work split: a unit is 256 elements (one q4_K super-block or eight q4_0 /
+// q8_0 blocks). A launch covers units [u_begin, u_end); wave w of a
+// workgroup owns KS of them; the workgroup walks 16-row groups (persistent
+// grid), loading the next group's weights while it multiplies this one. The
+// waves' 16 x 16 partials meet in LDS and are summed in wave order
+// (deterministic). A K longer than one launch covers (16 waves x KS units)
+// runs as consecutive launches on the stream, each adding its part to the
+// output of the previous one.
+//
+// Weight loads (STAGED, K a multiple of 256): the operand layout wants 8
+// bytes from each of several places in 16 different rows per instruction, and
+// a load instruction costs the address unit about as many cycles as cache
+// lines it touches, which made such loads, not HBM, the limit. So a wave
+// reads its 16-row x KS-unit slice as consecutive 16-byte pieces per lane
+// (each row's slice is contiguous), writes them to a wave-private LDS buffer
+// and reads the operand layout back from there. Other K: direct loads.
+#include "kernels.hpp"
+
+namespace tlh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int SK_COLS = 16;
+constexpr int SK_MAXW = 16;
+constexpr int SK_OUTBUF = 16;  // row groups of outputs held in LDS between stores
+
+__device__ __forceinline__ v4i mfma_i8(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
+    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+template <typename T> __device__ __forceinline__ T ldu(const void *p) {
+    T v;
+    __builtin_memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+// Four nibbles n (one per byte) -> the int8 bytes n - 8 (q4_0 codes):
+// (n | 0x80) - 8 stays in 0x78..0x87 without borrows, ^ 0x80 recentres it.
+__device__ __forceinline__ uint32_t nib_minus8(uint32_t x) {
+    return ((x | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+}
+
+// 4 / 8 bytes from a 2-byte aligned LDS address, by aligned dword reads.
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) {
+    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], (uint32_t)((uintptr_t)p & 3));
+}
+__device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
+    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t a0 = q[0], a1 = q[1], a2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(a2, a1, sh));
+}
+
+// Bytes of one row per unit.
+template <int WT> constexpr int unit_bytes() {
+    return WT == TLH_TYPE_Q4_K ? Q4_K_BYTES : WT == TLH_TYPE_Q4_0 ? 8 * Q4_0_BYTES : 8 * Q8_0_BYTES;
+}
+
+// One lane's weight data of one unit in operand form: q4_K the super-block
+// header and bytes 8g..8g+7 of each 32-byte chunk; q8_0 / q4_0 per block the
+// scale and codes 8g..8g+7 / nibble bytes 4g..4g+3.
+template <int WT> struct UnitW;
+
+template <> struct UnitW<TLH_TYPE_Q4_K> {
+    uint4 hdr;
+    uint2 q[4];
+    // blk: the unit's 144 bytes; global (unaligned) or LDS (16-byte aligned)
+    __device__ __forceinline__ void load(const uint8_t *blk, int g) {
+        hdr = ldu<uint4>(blk);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) q[c] = ldu<uint2>(blk + 16 + 32 * c + 8 * g);
+    }
+    __device__ __forceinline__ void load_lds(const uint8_t *blk, int g) {
+        hdr = *(const uint4 *)blk;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) q[c] = *(const uint2 *)(blk + 16 + 32 * c + 8 * g);
+    }
+};
+
+template <> struct UnitW<TLH_TYPE_Q8_0> {
+    uint2 q[8];
+    uint16_t d[8];
+    // blk0: the unit's first block; blocks past `nb` valid ones are not read (global) / garbage (LDS)
+    __device__ __forceinline__ void load(const uint8_t *blk0, int g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            d[j] = ldu<uint16_t>(blk0 + j * Q8_0_BYTES);
+            q[j] = ldu<uint2>(blk0 + j * Q8_0_BYTES + 2 + 8 * g);
+        }
+    }
+    __device__ __forceinline__ void load_lds(const uint8_t *blk0, int g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            d[j] = *(const uint16_t *)(blk0 + j * Q8_0_BYTES);
+            q[j] = lds_u64(blk0 + j * Q8_0_BYTES + 2 + 8 * g);
+        }
+    }
+};
+
+template <> struct UnitW<TLH_TYPE_Q4_0> {
+    uint32_t q[8];
+    uint16_t d[8];
+    __device__ __forceinline__ void load(const uint8_t *blk0, int g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            d[j] = ldu<uint16_t>(blk0 + j * Q4_0_BYTES);
+            q[j] = ldu<uint32_t>(blk0 + j * Q4_0_BYTES + 2 + 4 * g);
+        }
+    }
+    __device__ __forceinline__ void load_lds(const uint8_t *blk0, int g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            d[j] = *(const uint16_t *)(blk0 + j * Q4_0_BYTES);
+            q[j] = lds_u32(blk0 + j * Q4_0_BYTES + 2 + 4 * g);
+        }
+    }
+};
+
+// One q4_0 / q8_0 block: y[r] += its integer dot product (one MFMA) scaled
+// as the CPU scales it; sdb: the block's activation scales [16 columns].
+template <int WT>
+__device__ __forceinline__ void block_mma(long A, long B, uint16_t dwh, const float *sdb, int g, float (&y)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    const v4i Sb = mfma_i8(A, B, zero);
+    const float dw = h2f(dwh);
+    const float4 d8 = *(const float4 *)(sdb + 4 * g);
+    const float d8r[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        if constexpr (WT == TLH_TYPE_Q4_0)
+            y[r] += ((float)Sb[r] * dw) * d8r[r];  // quants.c:255
+        else
+            y[r] += (float)Sb[r] * (dw * d8r[r]);  // quants.c:475
+    }
+}
+
+// y[r] += the unit's contribution to output (column 4g + r, the lane's weight
+// row). A: the unit's activation operands; sdu: its activation scales in LDS
+// (q4_K one slot, q4_0 / q8_0 one per block) as [slot][16 columns];
+// nvalid: blocks of the unit inside K (q4_0 / q8_0).
+template <int WT>
+__device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8], const float *sdu, int g,
+                                         int nvalid, float (&y)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    if constexpr (WT == TLH_TYPE_Q4_K) {
+        const uint4 h = w.hdr;
+        v4i S = {0, 0, 0, 0}, Mn = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint2 qv = w.q[j >> 1];
+            const int sh = (j & 1) ? 4 : 0;
+            const long B = pack2((qv.x >> sh) & 0x0f0f0f0fu, (qv.y >> sh) & 0x0f0f0f0fu);
+            const v4i Sj = mfma_i8(A[j], B, zero);
+            // 6-bit scale / min of sub-block j (get_scale_min_k4, ggml-quants.c:880-887)
+            const int bj = 8 * (j & 3);
+            const int s = j < 4 ? (int)((h.y >> bj) & 63) : (int)(((h.w >> bj) & 15) | (((h.y >> (bj + 6)) & 3) << 4));
+            const uint32_t m = j < 4 ? ((h.z >> bj) & 63) : (((h.w >> (bj + 4)) & 15) | (((h.z >> (bj + 6)) & 3) << 4));
+            const uint32_t m4 = m * 0x01010101u;
+            Mn = mfma_i8(A[j], pack2(m4, m4), Mn);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] += s * Sj[r];
+        }
+        const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
+        const float4 d8 = *(const float4 *)(sdu + 4 * g);
+        const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j >= nvalid) continue;  // wave-uniform
+            long B;
+            if constexpr (WT == TLH_TYPE_Q4_0) {
+                const uint32_t v = w.q[j];
+                B = pack2(nib_minus8(v & 0x0f0f0f0fu), nib_minus8((v >> 4) & 0x0f0f0f0fu));
+            } else {
+                B = pack2(w.q[j].x, w.q[j].y);
+            }
+            block_mma<WT>(A[j], B, w.d[j], sdu + j * SK_COLS, g, y);
+        }
+    }
+}
+
+// Staging of one row group's slice: lane l loads pieces 64i + l (16 bytes
+// each) of the 16 rows x KS units, row-major; NL loads per lane.
+template <int WT, int KS> struct Stage {
+    static constexpr int RB = KS * unit_bytes<WT>();  // slice bytes per row (a multiple of 16)
+    static constexpr int PR = RB / 16;                 // pieces per row
+    static constexpr int NL = (16 * PR + 63) / 64;
+    static constexpr int BUF = NL * 64 * 16 + 16;      // LDS bytes per wave (with read slack)
+    uint4 v[NL];
+};
+
+// Direct loads of KS units (prefetch set of the unstaged kernel). Units
+// past `last` reread unit `last` (their products are skipped).
+template <int WT, int KS> struct DirectW {
+    UnitW<WT> u[KS];
+    __device__ __forceinline__ void load(const uint8_t *row, int64_t u0, int64_t last, int g) {
+#pragma unroll
+        for (int t = 0; t < KS; ++t) u[t].load(row + (u0 + t < last ? u0 + t : last) * unit_bytes<WT>(), g);
+    }
+};
+
+template <int WT, int KS, bool STAGED>
+__global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t u_begin, int64_t u_end,
+                                                    int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) char sk_lds[];
+    constexpr int AT = vec_dot_type(WT);
+    constexpr bool KQ = WT == TLH_TYPE_Q4_K;
+    constexpr int UB = unit_bytes<WT>();
+    using St = Stage<WT, KS>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int g = lane >> 4, wr = lane & 15;  // k group; weight row in the group / activation column
+    const int64_t K = a.K;
+    const int64_t nblk = K / block_elems(AT);  // activation blocks per row (q8_K: super-blocks)
+    const int64_t u0 = u_begin + (int64_t)wave * KS;
+    // scale slots of the launch: q4_K one per unit, q4_0 / q8_0 one per block
+    const int64_t s_begin = KQ ? u_begin : 8 * u_begin;
+    const int64_t s_end = KQ ? u_end : (8 * u_end < nblk ? 8 * u_end : nblk);
+    const int64_t batch = blockIdx.z;
+    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
+    const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
+    const int64_t arow0 = a.n0 + a.N_total * batch;
+    const ActView act = act_view(a.act, AT, K, a.N_total * a.ne12 * a.ne13);
+    const int N = (int)a.N;
+
+    // LDS: partials [2][nw][64] float4, the activation scales of the
+    // launch's scale slots [s_end - s_begin][16 columns], the outputs of up
+    // to SK_OUTBUF row groups [SK_OUTBUF][256], then (STAGED) one weight
+    // buffer per wave.
+    float4 *red = (float4 *)sk_lds;
+    float *sd = (float *)(sk_lds + 2 * nw * 64 * sizeof(float4));
+    float *obuf = sd + (s_end - s_begin) * SK_COLS;
+    uint8_t *wbuf = (uint8_t *)(obuf + SK_OUTBUF * 256) + (size_t)wave * St::BUF;
+
+    const int64_t groups = (a.M + 15) / 16;
+    int64_t rg = blockIdx.x;
+    const int64_t row_bytes = K / block_elems(WT) * block_bytes(WT);
+
+    // STAGED: piece i of this lane is row p / PR of the group at byte
+    // u0 * UB + 16 * (p % PR) of the row (p = 64i + lane; offsets past the row
+    // end, of units past K, are clamped to the row start)
+    auto stage_load = [&](St &s, int64_t grp) {
+#pragma unroll
+        for (int i = 0; i < St::NL; ++i) {
+            const int p = 64 * i + lane;
+            const int pc = p < 16 * St::PR ? p : 0;
+            const int r = pc / St::PR;
+            const int64_t off = u0 * UB + 16 * (pc - r * St::PR);
+            const int64_t m = grp * 16 + r < a.M ? grp * 16 + r : a.M - 1;
+            s.v[i] = ldu<uint4>(W + m * a.w_nb1 + (off + 16 <= row_bytes ? off : 0));
+        }
+    };
+    auto wrow_of = [&](int64_t grp) {
+        const int64_t m = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;  // clamp: loads in bounds
+        return W + m * a.w_nb1;
+    };
+
+    // the first row group's weights go out before the activations are read
+    St st;
+    DirectW<WT, KS> da, db;
+    const int64_t rg0 = rg < groups ? rg : groups - 1;
+    if constexpr (STAGED) stage_load(st, rg0);
+    else da.load(wrow_of(rg0), u0, (s_end - 1) / (KQ ? 1 : 8), g);
+
+    // activation operands of this wave's units (zero past N and past the range)
+    long A[KS][8];
+    const bool col_ok = wr < N;
+    const int8_t *aq = act.qs + (arow0 + (col_ok ? wr : 0)) * K;
+#pragma unroll
+    for (int t = 0; t < KS; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
+            const bool ok = col_ok && e < 256 * u_end && e < K;
+            const int64_t ec = ok ? e : 0;
+            long v;
+            if constexpr (WT == TLH_TYPE_Q4_0) {
+                // the lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16+4g.. (high)
+                v = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
+            } else {
+                v = ldu<long>(aq + ec + 8 * g);
+            }
+            A[t][j] = ok ? v : 0;
+        }
+    for (int64_t i = threadIdx.x; i < (s_end - s_begin) * SK_COLS; i += blockDim.x) {
+        const int64_t b = s_begin + (i >> 4);
+        const int c = (int)(i & 15);
+        sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
+    }
+    lds_barrier();
+
+    char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
+    // output element o = threadIdx.x (< 256) of a row group: column o / 16, row o % 16
+    const int ocol = threadIdx.x >> 4, orow = threadIdx.x & 15;
+    auto out_ptr = [&](int64_t grp) { return (float *)(dbase + (a.n0 + ocol) * a.d_nb1 + (grp * 16 + orow) * 4); };
+
+    // Outputs wait in LDS (each thread rereads only what it wrote) and go to
+    // memory every SK_OUTBUF row groups: a store in flight would make the next
+    // wait for prefetched weights a wait for everything (loads and stores
+    // share one completion counter that is not in order across the two).
+    int nbuf = 0;
+    int64_t buf_rg = rg;
+    // Accumulate launches add the previous launch's partial here.
+    auto flush = [&]() {
+        if (threadIdx.x < 16 * SK_COLS)
+            for (int k = 0; k < nbuf; ++k) {
+                const int64_t grp = buf_rg + (int64_t)k * gridDim.x;
+                if (ocol < N && grp * 16 + orow < a.M) {
+                    float *o = out_ptr(grp);
+                    const float v = obuf[k * 256 + threadIdx.x];
+                    *o = accumulate ? *o + v : v;
+                }
+            }
+        nbuf = 0;
+        // the stores complete here, so no later wait for loads is widened by them
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    };
+
+    // reduce the waves' partials through LDS buffer `parity`, buffer the result
+    auto finish = [&](const float (&y)[4], int64_t grp, int parity) {
+        float4 *slot = red + parity * nw * 64;
+        slot[wave * 64 + lane] = make_float4(y[0], y[1], y[2], y[3]);
+        lds_barrier();
+        if (nbuf == 0) buf_rg = grp;
+        if (threadIdx.x < 16 * SK_COLS) {
+            const int l = orow + 16 * (ocol >> 2), r = ocol & 3;
+            const float *sl = (const float *)slot + 4 * l + r;
+            float s = 0.0f;
+            for (int wv = 0; wv < nw; ++wv) s += sl[256 * wv];
+            obuf[nbuf * 256 + threadIdx.x] = s;
+        }
+        if (++nbuf == SK_OUTBUF) flush();
+    };
+
+    auto unit_slots = [&](int t) { return sd + (KQ ? (u0 + t - s_begin) : 8 * (u0 + t) - s_begin) * SK_COLS; };
+    auto unit_nvalid = [&](int t) {
+        const int64_t v = s_end - 8 * (u0 + t);
+        return KQ ? 8 : (int)(v < 0 ? 0 : v > 8 ? 8 : v);
+    };
+    // multiply one row group from the wave's LDS buffer
+    auto process_staged = [&](int64_t grp, int parity) {
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+            if (u0 + t >= u_end) continue;  // wave-uniform
+            const uint8_t *ub = wbuf + wr * St::RB + t * UB;
+            if constexpr (KQ) {
+                UnitW<WT> w;
+                w.load_lds(ub, g);
+                unit_mma<WT>(w, A[t], unit_slots(t), g, 8, y);
+            } else {
+                // block by block: the operands of one block live at a time
+                const int nv = unit_nvalid(t);
+                const float *sdu = unit_slots(t);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (j >= nv) continue;  // wave-uniform
+                    const uint8_t *blk = ub + j * block_bytes(WT);
+                    long B;
+                    if constexpr (WT == TLH_TYPE_Q4_0) {
+                        const uint32_t v = lds_u32(blk + 2 + 4 * g);
+                        B = pack2(nib_minus8(v & 0x0f0f0f0fu), nib_minus8((v >> 4) & 0x0f0f0f0fu));
+                    } else {
+                        const uint2 v = lds_u64(blk + 2 + 8 * g);
+                        B = pack2(v.x, v.y);
+                    }
+                    block_mma<WT>(A[t][j], B, *(const uint16_t *)blk, sdu + j * SK_COLS, g, y);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            // one unit's operands live at a time
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        finish(y, grp, parity);
+    };
+    // ... or direct registers
+    auto process_direct = [&](const DirectW<WT, KS> &d, int64_t grp, int parity) {
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+            if (u0 + t >= u_end) continue;  // wave-uniform
+            unit_mma<WT>(d.u[t], A[t], unit_slots(t), g, unit_nvalid(t), y);
+        }
+        finish(y, grp, parity);
+    };
+
+    // The loads of the next row group are in flight while this one is
+    // multiplied. Staged: the registers hold only loads in flight (this
+    // group's bytes are in LDS by then), one set. Direct: two register sets
+    // in turn, so no register copy makes the wave wait for the loads early.
+    // The prefetch is unconditional (past the last group it rereads the
+    // current one, a cache hit) so that the compiler can count the loads in
+    // flight and wait only for the ones it needs.
+    if constexpr (STAGED) {
+        for (int it = 0; rg < groups; ++it) {
+            const int64_t r1 = rg + gridDim.x;
+#pragma unroll
+            for (int i = 0; i < St::NL; ++i) *(uint4 *)(wbuf + 1024 * i + 16 * lane) = st.v[i];
+            stage_load(st, r1 < groups ? r1 : rg);
+            process_staged(rg, it & 1);
+            rg = r1;
+        }
+    } else {
+        const int64_t dlast = (s_end - 1) / (KQ ? 1 : 8);
+        for (;;) {
+            if (rg >= groups) break;
+            const int64_t r1 = rg + gridDim.x;
+            db.load(wrow_of(r1 < groups ? r1 : rg), u0, dlast, g);
+            process_direct(da, rg, 0);
+            if (r1 >= groups) break;
+            const int64_t r2 = r1 + gridDim.x;
+            da.load(wrow_of(r2 < groups ? r2 : r1), u0, dlast, g);
+            process_direct(db, r1, 1);
+            rg = r2;
+        }
+    }
+    flush();
+}
+
+// Units per wave: one (16 activation-operand registers); a launch covers up
+// to 16 units (K = 4096); longer K takes several launches.
+template <int WT> constexpr int sk_ks() { return 1; }
+
+bool gemv_mfma_supported(int64_t N) { return N >= 1 && N <= SK_COLS; }
+
+template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream) {
+    constexpr int KS = sk_ks<WT>();
+    auto kern = k_gemv_mfma<WT, KS, STAGED>;
+    const int64_t units = (a.K + 255) / 256;
+    const int64_t per_launch = (int64_t)SK_MAXW * KS;
+    const int64_t launches = (units + per_launch - 1) / per_launch;
+    // equal shares, so no launch is left with a sliver
+    const int64_t share = (units + launches - 1) / launches;
+    // at least 4 waves: the first 256 threads each own one of a row group's outputs
+    const int nw = (int)((share + KS - 1) / KS) > 4 ? (int)((share + KS - 1) / KS) : 4;
+    const size_t lds = (size_t)2 * nw * 64 * 16 + (size_t)(WT == TLH_TYPE_Q4_K ? share : 8 * share) * SK_COLS * 4 +
+                       (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0);
+    static int cached_nw = -1, blocks_per_cu = 1, cus = 0;
+    if (cached_nw != nw) {
+        int dev = 0, nb = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * nw, lds) != hipSuccess || nb < 1) nb = 1;
+        blocks_per_cu = nb;
+        cached_nw = nw;
+    }
+    const int64_t groups = (a.M + 15) / 16;
+    const int64_t batches = a.ne12 * a.ne13;
+    int64_t resident = (int64_t)cus * blocks_per_cu / (batches > 0 ? batches : 1);
+    if (resident < 1) resident = 1;
+    const unsigned gx = (unsigned)(groups < resident ? groups : resident);
+    for (int64_t l = 0; l < launches; ++l) {
+        const int64_t ub = l * share, ue = ub + share < units ? ub + share : units;
+        hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(64 * nw), lds, stream, a, ub, ue, (int)(l > 0));
+        const tlh_status st = check_launch("gemv_mfma");
+        if (st != TLH_OK) return st;
+    }
+    return TLH_OK;
+}
+
+tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
+    if (!gemv_mfma_supported(a.N)) return set_error(TLH_INVALID, "gemv_mfma: N=%lld", (long long)a.N);
+    // whole units per row: every staged piece lies inside its row
+    const bool staged = a.K % 256 == 0;
+    switch (a.wtype) {
+    case TLH_TYPE_Q4_0: return staged ? launch_sk<TLH_TYPE_Q4_0, true>(a, stream) : launch_sk<TLH_TYPE_Q4_0, false>(a, stream);
+    case TLH_TYPE_Q8_0: return staged ? launch_sk<TLH_TYPE_Q8_0, true>(a, stream) : launch_sk<TLH_TYPE_Q8_0, false>(a, stream);
+    case TLH_TYPE_Q4_K: return launch_sk<TLH_TYPE_Q4_K, true>(a, stream);  // K is a multiple of 256
+    default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: weight type %d", a.wtype);
+    }
+}
+
+}  // namespace tlh

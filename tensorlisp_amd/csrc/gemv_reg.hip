@@ -418,14 +418,14 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             }
         } else {
             if (holder) part[wave][vi] = tot;
-            __syncthreads();
+            lds_barrier();
             if (kw == 0 && holder && vi < V) {
                 float t = 0.0f;
                 for (int s2 = 0; s2 < ksplit; ++s2) t += part[grp * ksplit + s2][vi];
                 const int r = vi / NC, n = vi % NC;
                 if (m0 + r < a.M && n < a.N) *(float *)(dbase + (a.n0 + n) * a.d_nb1 + (m0 + r) * 4) = t;
             }
-            __syncthreads();
+            lds_barrier();
         }
         if constexpr (PIPE) {
             cur = nxt;

@@ -34,7 +34,7 @@ struct MatmulArgs {
     int64_t d_nb1, d_nb2, d_nb3;  // dst strides (bytes), nb0 = 4
 };
 
-// N <= 8. With x != nullptr (src1 rows in activation-row order, stride
+// N <= 16. With x != nullptr (src1 rows in activation-row order, stride
 // x_row_bytes) and a small N*K the GEMV quantizes x itself and the scratch is
 // not read; otherwise it reads the scratch a quantize launch filled.
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
@@ -42,6 +42,9 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 // register-resident GEMV (gemv_reg.hip): K <= 16384, K % 64 == 0
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
+// few-column GEMM on int8 MFMA (gemv_mfma.hip): 1 <= N <= 16, any K
+bool gemv_mfma_supported(int64_t N);
+tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,

@@ -4,7 +4,8 @@
 // The MUL_MAT policy mirrors Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
 // in what it accepts and how it reports refusals, and the ggml CPU backend
 // (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457) in what it computes:
-// quantize src1 to the vec_dot type, then N <= 8 -> GEMV, else GEMM.
+// quantize src1 to the vec_dot type, then N <= 2 -> register GEMV,
+// N <= 16 -> int8-MFMA few-column kernel, else the GEMM.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -59,7 +60,7 @@ static const char *type_name(int t) {
 // Validates a MUL_MAT descriptor; fills the derived sizes.
 struct MulMatShape {
     int64_t K, M, N, ne12, ne13, r2, r3, act_rows;
-    int act_type;
+    int wtype, act_type;
 };
 
 static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
@@ -101,6 +102,7 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
         return set_error(TLH_UNSUPPORTED, "mul_mat: src1 must have contiguous f32 rows");
     if (d.nb[0] != 4 || d.nb[1] < 4 * s.M || (d.nb[1] & 3) || d.nb[2] < d.nb[1] || d.nb[3] < d.nb[2])
         return set_error(TLH_UNSUPPORTED, "mul_mat: dst must be f32 with ordered strides");
+    s.wtype = a.ty;
     s.act_type = vec_dot_type(a.ty);
     s.act_rows = s.N * s.ne12 * s.ne13;
     return TLH_OK;
@@ -195,12 +197,12 @@ tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes) {
     MulMatShape s;
     const tlh_status st = check_mul_mat(op, s);
     if (st != TLH_OK) return st;
-    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.N)).total;
+    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
     return TLH_OK;
 }
 
 static tlh_status mm_check_scratch(const MulMatShape &s, const void *scratch, size_t scratch_bytes) {
-    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.N)).total;
+    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
     if (!scratch || scratch_bytes < need)
         return set_error(TLH_INVALID, "mul_mat: scratch of %zu bytes, need %zu", scratch_bytes, need);
     if ((uintptr_t)scratch & 255) return set_error(TLH_INVALID, "mul_mat: scratch must be 256-byte aligned");
@@ -215,12 +217,12 @@ static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
     if (packed)
         return launch_quantize_act(a.ty, (const float *)src1, s.K, s.act_rows, b.nb[1], scratch, false, 0,
-                                   s.act_rows, act_has_f16(s.N), hs);
+                                   s.act_rows, act_has_f16(s.wtype, s.N), hs);
     for (int64_t i13 = 0; i13 < s.ne13; ++i13)
         for (int64_t i12 = 0; i12 < s.ne12; ++i12) {
             const float *x = (const float *)((const char *)src1 + i12 * b.nb[2] + i13 * b.nb[3]);
             const tlh_status st = launch_quantize_act(a.ty, x, s.K, s.N, b.nb[1], scratch, false,
-                                                      s.N * (i12 + s.ne12 * i13), s.act_rows, act_has_f16(s.N), hs);
+                                                      s.N * (i12 + s.ne12 * i13), s.act_rows, act_has_f16(s.wtype, s.N), hs);
             if (st != TLH_OK) return st;
         }
     return TLH_OK;
@@ -257,7 +259,7 @@ static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void 
     if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
         return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
     const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
-    return s.N <= 8 ? launch_gemv(m, nullptr, 0, hs) : launch_gemm(m, hs);
+    return s.N <= 16 ? launch_gemv(m, nullptr, 0, hs) : launch_gemm(m, hs);
 }
 
 static bool mm_empty(const MulMatShape &s) { return s.M == 0 || s.N == 0 || s.ne12 == 0 || s.ne13 == 0; }

@@ -64,7 +64,7 @@ def test_mul_mat_scratch_sizes(wt, n):
     be = N.BLOCK[at][0]
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
     sums = n * (K // 16) * 2 if at == N.Q8_K else n * (K // 32) * 4
-    f16_codes = n * K * 2 if n > 8 else 0  # GEMM launches also stage the codes as f16
+    f16_codes = n * K * 2 if wt == N.Q4_K and n > 16 else 0  # q4_K GEMM launches also stage f16 codes
     assert nbytes == al(al(al(al(n * K) + n * (K // be) * 4) + sums) + f16_codes)
 
 
