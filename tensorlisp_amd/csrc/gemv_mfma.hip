@@ -71,14 +71,16 @@ __device__ __forceinline__ uint32_t nib_minus8(uint32_t x) {
     return ((x | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
 }
 
-// 4 / 8 bytes from a 2-byte aligned LDS address, by aligned dword reads.
-__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) {
-    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
-    return __builtin_amdgcn_alignbyte(q[1], q[0], (uint32_t)((uintptr_t)p & 3));
+// 4 / 8 bytes at byte offset `off` (2-byte aligned) of a 4-byte aligned LDS
+// buffer, by aligned dword reads. (Offsets, not integer-cast pointers, keep
+// the accesses in the LDS address space.)
+__device__ __forceinline__ uint32_t lds_u32(const uint32_t *base, uint32_t off) {
+    const uint32_t *q = base + (off >> 2);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], off & 3);
 }
-__device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
-    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+__device__ __forceinline__ uint2 lds_u64(const uint32_t *base, uint32_t off) {
+    const uint32_t *q = base + (off >> 2);
+    const uint32_t sh = off & 3;
     const uint32_t a0 = q[0], a1 = q[1], a2 = q[2];
     return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(a2, a1, sh));
 }
@@ -120,13 +122,6 @@ template <> struct UnitW<TLH_TYPE_Q8_0> {
             q[j] = ldu<uint2>(blk0 + j * Q8_0_BYTES + 2 + 8 * g);
         }
     }
-    __device__ __forceinline__ void load_lds(const uint8_t *blk0, int g) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            d[j] = *(const uint16_t *)(blk0 + j * Q8_0_BYTES);
-            q[j] = lds_u64(blk0 + j * Q8_0_BYTES + 2 + 8 * g);
-        }
-    }
 };
 
 template <> struct UnitW<TLH_TYPE_Q4_0> {
@@ -137,13 +132,6 @@ template <> struct UnitW<TLH_TYPE_Q4_0> {
         for (int j = 0; j < 8; ++j) {
             d[j] = ldu<uint16_t>(blk0 + j * Q4_0_BYTES);
             q[j] = ldu<uint32_t>(blk0 + j * Q4_0_BYTES + 2 + 4 * g);
-        }
-    }
-    __device__ __forceinline__ void load_lds(const uint8_t *blk0, int g) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            d[j] = *(const uint16_t *)(blk0 + j * Q4_0_BYTES);
-            q[j] = lds_u32(blk0 + j * Q4_0_BYTES + 2 + 4 * g);
         }
     }
 };
@@ -176,6 +164,10 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
     const v4i zero = {0, 0, 0, 0};
     if constexpr (WT == TLH_TYPE_Q4_K) {
         const uint4 h = w.hdr;
+        // the 6-bit scales / mins of the 8 sub-blocks as bytes, sub-blocks
+        // 0..3 and 4..7 (get_scale_min_k4, ggml-quants.c:880-887)
+        const uint32_t sc[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
         v4i S = {0, 0, 0, 0}, Mn = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -183,14 +175,12 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
             const int sh = (j & 1) ? 4 : 0;
             const long B = pack2((qv.x >> sh) & 0x0f0f0f0fu, (qv.y >> sh) & 0x0f0f0f0fu);
             const v4i Sj = mfma_i8(A[j], B, zero);
-            // 6-bit scale / min of sub-block j (get_scale_min_k4, ggml-quants.c:880-887)
-            const int bj = 8 * (j & 3);
-            const int s = j < 4 ? (int)((h.y >> bj) & 63) : (int)(((h.w >> bj) & 15) | (((h.y >> (bj + 6)) & 3) << 4));
-            const uint32_t m = j < 4 ? ((h.z >> bj) & 63) : (((h.w >> (bj + 4)) & 15) | (((h.z >> (bj + 6)) & 3) << 4));
-            const uint32_t m4 = m * 0x01010101u;
+            const int s = (int)__builtin_amdgcn_ubfe(sc[j >> 2], 8 * (j & 3), 8);
+            // m_j in all four bytes (byte j & 3 of the word, selected four times)
+            const uint32_t m4 = __builtin_amdgcn_perm(0u, mn[j >> 2], 0x01010101u * (uint32_t)(j & 3));
             Mn = mfma_i8(A[j], pack2(m4, m4), Mn);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] += s * Sj[r];
+            for (int r = 0; r < 4; ++r) S[r] += __mul24(s, Sj[r]);  // |Sj| < 2^16, s < 64
         }
         const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
         const float4 d8 = *(const float4 *)(sdu + 4 * g);
@@ -270,18 +260,28 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     int64_t rg = blockIdx.x;
     const int64_t row_bytes = K / block_elems(WT) * block_bytes(WT);
 
-    // STAGED: piece i of this lane is row p / PR of the group at byte
+    // STAGED: piece i of this lane is row pr[i] = p / PR of the group at byte
     // u0 * UB + 16 * (p % PR) of the row (p = 64i + lane; offsets past the row
-    // end, of units past K, are clamped to the row start)
+    // end, of units past K, are clamped to the row start). pofs[i]: that
+    // piece's byte offset from the group's first row; rows past M read row M-1.
+    int pr[St::NL];
+    int64_t pofs[St::NL];
+#pragma unroll
+    for (int i = 0; i < St::NL; ++i) {
+        const int p = 64 * i + lane;
+        const int pc = p < 16 * St::PR ? p : 0;
+        pr[i] = pc / St::PR;
+        const int64_t off = u0 * UB + 16 * (pc - pr[i] * St::PR);
+        pofs[i] = pr[i] * a.w_nb1 + (off + 16 <= row_bytes ? off : 0);
+    }
+    const uint8_t *wlast = W + (a.M - 1) * a.w_nb1;
     auto stage_load = [&](St &s, int64_t grp) {
+        const uint8_t *gb = W + grp * 16 * a.w_nb1;  // wave-uniform
+        const int rows_left = (int)(a.M - grp * 16);
 #pragma unroll
         for (int i = 0; i < St::NL; ++i) {
-            const int p = 64 * i + lane;
-            const int pc = p < 16 * St::PR ? p : 0;
-            const int r = pc / St::PR;
-            const int64_t off = u0 * UB + 16 * (pc - r * St::PR);
-            const int64_t m = grp * 16 + r < a.M ? grp * 16 + r : a.M - 1;
-            s.v[i] = ldu<uint4>(W + m * a.w_nb1 + (off + 16 <= row_bytes ? off : 0));
+            const uint8_t *q = pr[i] < rows_left ? gb + pofs[i] : wlast + (pofs[i] - pr[i] * a.w_nb1);
+            s.v[i] = ldu<uint4>(q);
         }
     };
     auto wrow_of = [&](int64_t grp) {
@@ -377,28 +377,30 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
-            const uint8_t *ub = wbuf + wr * St::RB + t * UB;
+            const uint32_t ub = (uint32_t)(wr * St::RB + t * UB);  // byte offset of the row's unit in wbuf
             if constexpr (KQ) {
                 UnitW<WT> w;
-                w.load_lds(ub, g);
+                w.load_lds(wbuf + ub, g);
                 unit_mma<WT>(w, A[t], unit_slots(t), g, 8, y);
             } else {
                 // block by block: the operands of one block live at a time
                 const int nv = unit_nvalid(t);
                 const float *sdu = unit_slots(t);
+                const uint32_t *w32 = (const uint32_t *)wbuf;
+                const uint16_t *w16 = (const uint16_t *)wbuf;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (j >= nv) continue;  // wave-uniform
-                    const uint8_t *blk = ub + j * block_bytes(WT);
+                    const uint32_t blk = ub + j * block_bytes(WT);
                     long B;
                     if constexpr (WT == TLH_TYPE_Q4_0) {
-                        const uint32_t v = lds_u32(blk + 2 + 4 * g);
+                        const uint32_t v = lds_u32(w32, blk + 2 + 4 * g);
                         B = pack2(nib_minus8(v & 0x0f0f0f0fu), nib_minus8((v >> 4) & 0x0f0f0f0fu));
                     } else {
-                        const uint2 v = lds_u64(blk + 2 + 8 * g);
+                        const uint2 v = lds_u64(w32, blk + 2 + 8 * g);
                         B = pack2(v.x, v.y);
                     }
-                    block_mma<WT>(A[t][j], B, *(const uint16_t *)blk, sdu + j * SK_COLS, g, y);
+                    block_mma<WT>(A[t][j], B, w16[blk >> 1], sdu + j * SK_COLS, g, y);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
