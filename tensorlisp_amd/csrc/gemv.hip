@@ -427,22 +427,18 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
            (x_row_bytes & 15) == 0;
 }
 
+bool gemv_uses_reg(const MatmulArgs &a) {
+    int ksplit, upw;
+    return a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw);
+}
+
+// N <= 2 with K the register kernel covers: the register-resident GEMV
+// (fused quantization when x is given); otherwise the int8-MFMA kernel.
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
     if (a.N < 1 || a.N > 16) return set_error(TLH_INVALID, "gemv: N=%lld outside 1..16", (long long)a.N);
-    int ksplit, upw;
-    if (a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw)) return launch_gemv_reg(a, x, x_row_bytes, stream);
+    if (gemv_uses_reg(a)) return launch_gemv_reg(a, x, x_row_bytes, stream);
     if (x != nullptr) return set_error(TLH_INVALID, "gemv: fused quantization needs N <= 2, K <= 16384, K %% 64 == 0");
     return launch_gemv_mfma(a, stream);
-    // other K: activation codes staged in LDS from the scratch
-    if (!fits_lds(a.wtype, a.K, (int)a.N))
-        return set_error(TLH_UNSUPPORTED, "gemv: K=%lld x N=%lld activations exceed LDS", (long long)a.K,
-                         (long long)a.N);
-    switch (a.wtype) {
-    case TLH_TYPE_Q4_0: return launch_wt<TLH_TYPE_Q4_0>(a, stream);
-    case TLH_TYPE_Q8_0: return launch_wt<TLH_TYPE_Q8_0>(a, stream);
-    case TLH_TYPE_Q4_K: return launch_wt<TLH_TYPE_Q4_K>(a, stream);
-    default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
-    }
 }
 
 }  // namespace tlh

@@ -30,9 +30,9 @@
 // workgroup owns KS of them; the workgroup walks 16-row groups (persistent
 // grid), loading the next group's weights while it multiplies this one. The
 // waves' 16 x 16 partials meet in LDS and are summed in wave order
-// (deterministic). A K longer than one launch covers (16 waves x KS units)
-// runs as consecutive launches on the stream, each adding its part to the
-// output of the previous one.
+// (deterministic). A K longer than one workgroup covers (16 waves x KS
+// units) is split into chunks (grid y); each chunk writes its partial sums to
+// the scratch and a second kernel adds the chunks in order.
 //
 // Weight loads (STAGED, K a multiple of 256): the operand layout wants 8
 // bytes from each of several places in 16 different rows per instruction, and
@@ -224,8 +224,7 @@ template <int WT, int KS> struct DirectW {
 };
 
 template <int WT, int KS, bool STAGED>
-__global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t u_begin, int64_t u_end,
-                                                    int accumulate) {
+__global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share) {
     extern __shared__ __attribute__((aligned(16))) char sk_lds[];
     constexpr int AT = vec_dot_type(WT);
     constexpr bool KQ = WT == TLH_TYPE_Q4_K;
@@ -236,6 +235,10 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     const int g = lane >> 4, wr = lane & 15;  // k group; weight row in the group / activation column
     const int64_t K = a.K;
     const int64_t nblk = K / block_elems(AT);  // activation blocks per row (q8_K: super-blocks)
+    // K chunk blockIdx.y: units [u_begin, u_end)
+    const int64_t units_all = (K + 255) / 256;
+    const int64_t u_begin = (int64_t)blockIdx.y * share;
+    const int64_t u_end = u_begin + share < units_all ? u_begin + share : units_all;
     const int64_t u0 = u_begin + (int64_t)wave * KS;
     // scale slots of the launch: q4_K one per unit, q4_0 / q8_0 one per block
     const int64_t s_begin = KQ ? u_begin : 8 * u_begin;
@@ -299,34 +302,41 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // activation operands of this wave's units (zero past N and past the range)
     long A[KS][8];
     const bool col_ok = wr < N;
-    const int8_t *aq = act.qs + (arow0 + (col_ok ? wr : 0)) * K;
+    {
+        const int8_t *aq = act.qs + (arow0 + (col_ok ? wr : 0)) * K;
 #pragma unroll
-    for (int t = 0; t < KS; ++t)
+        for (int t = 0; t < KS; ++t)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
-            const bool ok = col_ok && e < 256 * u_end && e < K;
-            const int64_t ec = ok ? e : 0;
-            long v;
-            if constexpr (WT == TLH_TYPE_Q4_0) {
-                // the lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16+4g.. (high)
-                v = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
-            } else {
-                v = ldu<long>(aq + ec + 8 * g);
+            for (int j = 0; j < 8; ++j) {
+                const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
+                const bool ok = col_ok && e < 256 * u_end && e < K;
+                const int64_t ec = ok ? e : 0;
+                long v;
+                if constexpr (WT == TLH_TYPE_Q4_0) {
+                    // the lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16+4g.. (high)
+                    v = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
+                } else {
+                    v = ldu<long>(aq + ec + 8 * g);
+                }
+                A[t][j] = ok ? v : 0;
             }
-            A[t][j] = ok ? v : 0;
+        for (int64_t i = threadIdx.x; i < (s_end - s_begin) * SK_COLS; i += blockDim.x) {
+            const int64_t b = s_begin + (i >> 4);
+            const int c = (int)(i & 15);
+            sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
         }
-    for (int64_t i = threadIdx.x; i < (s_end - s_begin) * SK_COLS; i += blockDim.x) {
-        const int64_t b = s_begin + (i >> 4);
-        const int c = (int)(i & 15);
-        sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
     }
     lds_barrier();
 
     char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
-    // output element o = threadIdx.x (< 256) of a row group: column o / 16, row o % 16
+    // output element o = threadIdx.x (< 256) of a row group: column o / 16,
+    // row o % 16; to dst, or with several K chunks to this chunk's partials
+    // [chunk][batch][N][M]
     const int ocol = threadIdx.x >> 4, orow = threadIdx.x & 15;
-    auto out_ptr = [&](int64_t grp) { return (float *)(dbase + (a.n0 + ocol) * a.d_nb1 + (grp * 16 + orow) * 4); };
+    float *pbase = a.part ? a.part + (((int64_t)blockIdx.y * gridDim.z + batch) * a.N + ocol) * a.M : nullptr;
+    auto out_ptr = [&](int64_t grp) {
+        return pbase ? pbase + grp * 16 + orow : (float *)(dbase + (a.n0 + ocol) * a.d_nb1 + (grp * 16 + orow) * 4);
+    };
 
     // Outputs wait in LDS (each thread rereads only what it wrote) and go to
     // memory every SK_OUTBUF row groups: a store in flight would make the next
@@ -334,16 +344,11 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // share one completion counter that is not in order across the two).
     int nbuf = 0;
     int64_t buf_rg = rg;
-    // Accumulate launches add the previous launch's partial here.
     auto flush = [&]() {
         if (threadIdx.x < 16 * SK_COLS)
             for (int k = 0; k < nbuf; ++k) {
                 const int64_t grp = buf_rg + (int64_t)k * gridDim.x;
-                if (ocol < N && grp * 16 + orow < a.M) {
-                    float *o = out_ptr(grp);
-                    const float v = obuf[k * 256 + threadIdx.x];
-                    *o = accumulate ? *o + v : v;
-                }
+                if (ocol < N && grp * 16 + orow < a.M) *out_ptr(grp) = obuf[k * 256 + threadIdx.x];
             }
         nbuf = 0;
         // the stores complete here, so no later wait for loads is widened by them
@@ -453,20 +458,45 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     flush();
 }
 
-// Units per wave: one (16 activation-operand registers); a launch covers up
-// to 16 units (K = 4096); longer K takes several launches.
+// Units per wave: one (16 activation-operand registers); a workgroup covers
+// up to 16 units (K = 4096); longer K takes several chunks.
 template <int WT> constexpr int sk_ks() { return 1; }
-
 bool gemv_mfma_supported(int64_t N) { return N >= 1 && N <= SK_COLS; }
+
+
+// dst (strided, columns n0..) = sum over the K chunks of the partials, in chunk order
+__global__ void __launch_bounds__(256) k_gemv_mfma_reduce(const MatmulArgs a, int chunks) {
+    const int64_t batches = a.ne12 * a.ne13;
+    const int64_t per_batch = a.N * a.M;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= per_batch * batches) return;
+    const int64_t batch = i / per_batch, r = i - batch * per_batch;
+    const int64_t n = r / a.M, m = r - n * a.M;
+    float s = 0.0f;
+    for (int c = 0; c < chunks; ++c) s += a.part[(c * batches + batch) * per_batch + r];
+    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
+    *(float *)((char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3 + (a.n0 + n) * a.d_nb1 + m * 4) = s;
+}
+
+static int64_t sk_share(int64_t K, int64_t &chunks) {
+    const int64_t units = (K + 255) / 256;
+    const int64_t per = (int64_t)SK_MAXW * sk_ks<TLH_TYPE_Q4_K>();
+    chunks = (units + per - 1) / per;
+    return (units + chunks - 1) / chunks;  // equal shares, so no chunk is left with a sliver
+}
+
+int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches) {
+    int64_t chunks = 1;
+    (void)sk_share(K, chunks);
+    return chunks > 1 ? chunks * batches * (N < SK_COLS ? N : SK_COLS) * M * 4 : 0;
+}
 
 template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream) {
     constexpr int KS = sk_ks<WT>();
     auto kern = k_gemv_mfma<WT, KS, STAGED>;
-    const int64_t units = (a.K + 255) / 256;
-    const int64_t per_launch = (int64_t)SK_MAXW * KS;
-    const int64_t launches = (units + per_launch - 1) / per_launch;
-    // equal shares, so no launch is left with a sliver
-    const int64_t share = (units + launches - 1) / launches;
+    int64_t chunks = 1;
+    const int64_t share = sk_share(a.K, chunks);
+    if (chunks > 1 && !a.part) return set_error(TLH_INVALID, "gemv_mfma: K=%lld needs a partials buffer", (long long)a.K);
     // at least 4 waves: the first 256 threads each own one of a row group's outputs
     const int nw = (int)((share + KS - 1) / KS) > 4 ? (int)((share + KS - 1) / KS) : 4;
     const size_t lds = (size_t)2 * nw * 64 * 16 + (size_t)(WT == TLH_TYPE_Q4_K ? share : 8 * share) * SK_COLS * 4 +
@@ -482,16 +512,25 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     }
     const int64_t groups = (a.M + 15) / 16;
     const int64_t batches = a.ne12 * a.ne13;
-    int64_t resident = (int64_t)cus * blocks_per_cu / (batches > 0 ? batches : 1);
+    int64_t resident = (int64_t)cus * blocks_per_cu / (batches * chunks > 0 ? batches * chunks : 1);
     if (resident < 1) resident = 1;
     const unsigned gx = (unsigned)(groups < resident ? groups : resident);
-    for (int64_t l = 0; l < launches; ++l) {
-        const int64_t ub = l * share, ue = ub + share < units ? ub + share : units;
-        hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(64 * nw), lds, stream, a, ub, ue, (int)(l > 0));
-        const tlh_status st = check_launch("gemv_mfma");
-        if (st != TLH_OK) return st;
+    MatmulArgs k = a;
+    if (chunks == 1) k.part = nullptr;
+    hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share);
+    tlh_status st = check_launch("gemv_mfma");
+    if (st != TLH_OK || chunks == 1) return st;
+    const int64_t total = a.N * a.M * batches;
+    hipLaunchKernelGGL(k_gemv_mfma_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, (int)chunks);
+    return check_launch("gemv_mfma_reduce");
+}
+
+template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool staged, hipStream_t stream) {
+    if constexpr (WT == TLH_TYPE_Q4_K) {
+        return launch_sk<WT, true>(a, stream);  // K is a multiple of 256
+    } else {
+        return staged ? launch_sk<WT, true>(a, stream) : launch_sk<WT, false>(a, stream);
     }
-    return TLH_OK;
 }
 
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
@@ -499,9 +538,9 @@ tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     // whole units per row: every staged piece lies inside its row
     const bool staged = a.K % 256 == 0;
     switch (a.wtype) {
-    case TLH_TYPE_Q4_0: return staged ? launch_sk<TLH_TYPE_Q4_0, true>(a, stream) : launch_sk<TLH_TYPE_Q4_0, false>(a, stream);
-    case TLH_TYPE_Q8_0: return staged ? launch_sk<TLH_TYPE_Q8_0, true>(a, stream) : launch_sk<TLH_TYPE_Q8_0, false>(a, stream);
-    case TLH_TYPE_Q4_K: return launch_sk<TLH_TYPE_Q4_K, true>(a, stream);  // K is a multiple of 256
+    case TLH_TYPE_Q4_0: return launch_sk_wt<TLH_TYPE_Q4_0>(a, staged, stream);
+    case TLH_TYPE_Q8_0: return launch_sk_wt<TLH_TYPE_Q8_0>(a, staged, stream);
+    case TLH_TYPE_Q4_K: return launch_sk_wt<TLH_TYPE_Q4_K>(a, staged, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: weight type %d", a.wtype);
     }
 }

@@ -32,6 +32,8 @@ struct MatmulArgs {
                                   // column n of slice b is row n + N_total*b
     float *dst;
     int64_t d_nb1, d_nb2, d_nb3;  // dst strides (bytes), nb0 = 4
+    float *part;                  // few-column kernel with K split in chunks: partial
+                                  // sums [chunk][batch][N][M] (scratch), else null
 };
 
 // N <= 16. With x != nullptr (src1 rows in activation-row order, stride
@@ -42,8 +44,10 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 // register-resident GEMV (gemv_reg.hip): K <= 16384, K % 64 == 0
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
-// few-column GEMM on int8 MFMA (gemv_mfma.hip): 1 <= N <= 16, any K
+// few-column GEMM on int8 MFMA (gemv_mfma.hip): 1 <= N <= 16, any K, from
+// the scratch. K > 4096 needs a.part: gemv_mfma_partial_bytes of scratch.
 bool gemv_mfma_supported(int64_t N);
+int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches);
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 

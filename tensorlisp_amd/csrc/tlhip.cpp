@@ -192,17 +192,29 @@ tlh_status tlh_stream_sync(void *stream) {
     return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
 }
 
+// Scratch: the quantized activations, then (when the int8-MFMA few-column
+// kernel runs with K split in chunks) its partial sums.
+static int64_t mm_act_bytes(const MulMatShape &s) {
+    return act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
+}
+static int64_t mm_partial_bytes(const MulMatShape &s) {
+    int ksplit, upw;
+    const bool reg = s.N <= 2 && gemv_reg_geometry(s.K, ksplit, upw);
+    const bool mfma = s.N <= 16 ? !reg : s.wtype != TLH_TYPE_Q4_K;
+    return mfma ? align_up(gemv_mfma_partial_bytes(s.K, s.M, s.N, s.ne12 * s.ne13), 256) : 0;
+}
+
 tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes) {
     if (!bytes) return set_error(TLH_INVALID, "mul_mat_scratch_bytes: null pointer");
     MulMatShape s;
     const tlh_status st = check_mul_mat(op, s);
     if (st != TLH_OK) return st;
-    *bytes = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
+    *bytes = (size_t)(mm_act_bytes(s) + mm_partial_bytes(s));
     return TLH_OK;
 }
 
 static tlh_status mm_check_scratch(const MulMatShape &s, const void *scratch, size_t scratch_bytes) {
-    const size_t need = (size_t)act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
+    const size_t need = (size_t)(mm_act_bytes(s) + mm_partial_bytes(s));
     if (!scratch || scratch_bytes < need)
         return set_error(TLH_INVALID, "mul_mat: scratch of %zu bytes, need %zu", scratch_bytes, need);
     if ((uintptr_t)scratch & 255) return set_error(TLH_INVALID, "mul_mat: scratch must be 256-byte aligned");
@@ -250,6 +262,7 @@ static MatmulArgs mm_args(const tlh_op *op, const MulMatShape &s, const void *sr
     m.d_nb1 = d.nb[1];
     m.d_nb2 = d.nb[2];
     m.d_nb3 = d.nb[3];
+    m.part = mm_partial_bytes(s) > 0 ? (float *)((char *)scratch + mm_act_bytes(s)) : nullptr;
     return m;
 }
 
@@ -275,7 +288,7 @@ tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, voi
     // Decode with a small activation: the GEMV quantizes src1 itself (one launch).
     const tlh_tensor &b = op->t[1];
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
-    if (s.N <= 8 && packed && !((uintptr_t)src1 & 3)) {
+    if (s.N <= 2 && packed && !((uintptr_t)src1 & 3)) {
         const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
         if (gemv_fuses_quantize(m, (const float *)src1, b.nb[1])) {
             if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
