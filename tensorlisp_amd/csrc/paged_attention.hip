@@ -44,187 +44,181 @@ __device__ __forceinline__ float *part_slot(float *scratch, int seq, int head, i
     return scratch + ((int64_t)(seq * num_heads + head) * P + part) * (HS + 2);
 }
 
-template <int HS, int BS, int GC>
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16(half4_t a, half4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// One wave works on 16-token tiles with v_mfma_f32_16x16x16_f16 (lane l,
+// g = l / 16, c = l % 16; A lane holds A[c][4g..4g+3], B lane B[4g..4g+3][c],
+// D lane D[4g + r][c]):
+//   S = K_tile (16 tokens x HS) . Q^T (HS x 16 heads), HS / 16 steps: the key
+//       cache layout [HS/8][BS][8] makes the A operand (token c, dims
+//       16s + 4g..+3) 8 contiguous bytes, and a step's 64 lanes read 512
+//       contiguous bytes of the page;
+//   P = softmax numerators, f16: lane (token 4g + r, head c) of S is exactly
+//       the A operand (head c, tokens 4g..4g+3) of
+//   O += P (16 heads x 16 tokens) . V_tile (16 tokens x 16 dims), HS / 16
+//       tiles: the value layout [HS][BS] makes the B operand (tokens 4g..+3,
+//       dim c) 8 contiguous bytes.
+// Heads past the group (c >= gc) have zero q and are dropped; one MFMA serves
+// up to 16 query heads of a kv head, so a page is read once per group.
+template <int HS, int BS, bool PIPE>
 __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                                                     const uint16_t *__restrict__ vc,
                                                     const int32_t *__restrict__ tables,
                                                     const int32_t *__restrict__ lens, int num_heads, int num_kv_heads,
-                                                    int max_blocks, float scale, int P, float *__restrict__ scratch) {
-    constexpr int CH = HS / 8;            // 8-dim chunks per key
-    constexpr int PIECES = CH * BS;       // 16-byte pieces per page (keys or values)
-    constexpr int NP = (PIECES + 63) / 64;  // pieces per lane
-    constexpr int REP = 64 / BS;          // lanes sharing one slot (key layout)
-    constexpr int SG = BS / 8;            // 8-slot groups per value row
+                                                    int gc, int max_blocks, float scale, int P,
+                                                    float *__restrict__ scratch) {
+    constexpr int KS = HS / 16;  // QK steps = PV output tiles
+    __shared__ int s_bt[PA_PART / 8];
+    __shared__ float s_m[PA_WAVES][16], s_l[PA_WAVES][16];
+    __shared__ float s_acc[PA_WAVES][16][HS];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int G = num_heads / num_kv_heads;
+    const int kvh = blockIdx.x / (G / gc);
+    const int head0 = kvh * G + (blockIdx.x % (G / gc)) * gc;
     const int seq = blockIdx.y;
-    const int kvh = blockIdx.x / ((num_heads / num_kv_heads) / GC);
-    const int hg = blockIdx.x % ((num_heads / num_kv_heads) / GC);
-    const int head0 = kvh * (num_heads / num_kv_heads) + hg * GC;
     const int part = blockIdx.z;
     const int L = lens[seq];
     const int t0 = part * PA_PART;
     if (t0 >= L && !(part == 0 && L == 0)) return;  // the reduce kernel ignores partitions past the context
     const int t1 = min(L, t0 + PA_PART);
-    const int pages0 = t0 / BS, pages1 = (t1 + BS - 1) / BS;
-
-    // q chunks this lane multiplies: chunk c_i = lane / BS + REP * i (key layout).
-    uint32_t qv[NP][GC][4];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int c = lane / BS + REP * i;
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-            const uint16_t *qh = q + ((int64_t)seq * num_heads + head0 + g) * HS;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (c < CH) v = *(const uint4 *)(qh + 8 * c);
-            qv[i][g][0] = v.x;
-            qv[i][g][1] = v.y;
-            qv[i][g][2] = v.z;
-            qv[i][g][3] = v.w;
-        }
-    }
-
-    const int slot = lane % BS;     // key layout: this lane's slot
-    const int vsg = lane % SG;      // value layout: this lane's 8-slot group
-    float m_run[GC], l_run[GC], acc[NP][GC];
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-        m_run[g] = -INFINITY;
-        l_run[g] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) acc[i][g] = 0.0f;
-    }
-
-    const int32_t *bt = tables + (int64_t)seq * max_blocks;
-    const int64_t kv_stride_blk = (int64_t)num_kv_heads * HS * BS;  // elements per block (keys or values)
-    for (int pg = pages0 + wave; pg < pages1; pg += PA_WAVES) {
-        const int64_t blk = (int64_t)__builtin_amdgcn_readfirstlane(bt[pg]);
-        const uint16_t *kp = kc + blk * kv_stride_blk + (int64_t)kvh * HS * BS;
-        const uint16_t *vp = vc + blk * kv_stride_blk + (int64_t)kvh * HS * BS;
-        uint4 kv[NP], vv[NP];
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int p = lane + 64 * i;
-            kv[i] = make_uint4(0, 0, 0, 0);
-            vv[i] = make_uint4(0, 0, 0, 0);
-            if (p < PIECES) {
-                kv[i] = *(const uint4 *)(kp + 8 * p);
-                vv[i] = *(const uint4 *)(vp + 8 * p);
-            }
-        }
-        // logits of slot `slot` for each head of the group
-        float lg[GC];
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                s = fdot2(kv[i].x, qv[i][g][0], s);
-                s = fdot2(kv[i].y, qv[i][g][1], s);
-                s = fdot2(kv[i].z, qv[i][g][2], s);
-                s = fdot2(kv[i].w, qv[i][g][3], s);
-            }
-#pragma unroll
-            for (int m = BS; m < 64; m <<= 1) s += __shfl_xor(s, m, 64);
-            lg[g] = s * scale;
-        }
-        const int tok = pg * BS + slot;
-        const bool valid = tok < t1;
-        float p[GC];
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-            float x = valid ? lg[g] : -INFINITY;
-            float mx = x;
-#pragma unroll
-            for (int m = 1; m < BS; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-            const float m_new = fmaxf(m_run[g], mx);  // finite: every page holds >= 1 valid token
-            const float alpha = __expf(m_run[g] - m_new);
-            m_run[g] = m_new;
-            p[g] = valid ? __expf(x - m_new) : 0.0f;
-            l_run[g] = l_run[g] * alpha + p[g];  // per-lane partial sum over this lane's slot
-#pragma unroll
-            for (int i = 0; i < NP; ++i) acc[i][g] *= alpha;
-        }
-        // p for the 8 slots of this lane's value group, as f16 pairs, per head
-        uint32_t pk[GC][4];
-#pragma unroll
-        for (int g = 0; g < GC; ++g)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float a = __shfl(p[g], 8 * vsg + 2 * j, 64);
-                const float b = __shfl(p[g], 8 * vsg + 2 * j + 1, 64);
-                pk[g][j] = pack_h2(a, b);
-            }
-        if (pg * BS + BS > t1) {  // last, partial page: zero values past the context (they may be NaN)
-#pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                uint32_t w[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int s0 = pg * BS + 8 * vsg + 2 * j;
-                    if (s0 >= t1) w[j] &= 0xffff0000u;
-                    if (s0 + 1 >= t1) w[j] &= 0x0000ffffu;
-                }
-                vv[i] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < GC; ++g)
-#pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                float s = acc[i][g];
-                s = fdot2(vv[i].x, pk[g][0], s);
-                s = fdot2(vv[i].y, pk[g][1], s);
-                s = fdot2(vv[i].z, pk[g][2], s);
-                s = fdot2(vv[i].w, pk[g][3], s);
-                acc[i][g] = s;
-            }
-    }
-
-    // per-wave totals: sum over slots, acc over slot groups
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-#pragma unroll
-        for (int m = 1; m < BS; m <<= 1) l_run[g] += __shfl_xor(l_run[g], m, 64);
-#pragma unroll
-        for (int i = 0; i < NP; ++i)
-#pragma unroll
-            for (int m = 1; m < SG; m <<= 1) acc[i][g] += __shfl_xor(acc[i][g], m, 64);
-    }
-
-    // merge the waves through LDS: max, sum, acc[HS] per head
-    __shared__ float s_m[PA_WAVES][GC], s_l[PA_WAVES][GC];
-    __shared__ float s_acc[PA_WAVES][GC][HS];
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-            s_m[wave][g] = m_run[g];
-            s_l[wave][g] = l_run[g];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int pidx = lane + 64 * i;
-        const int d = pidx / SG;
-        if (pidx < PIECES && vsg == 0)
-#pragma unroll
-            for (int g = 0; g < GC; ++g) s_acc[wave][g][d] = acc[i][g];
-    }
+    const int page0 = t0 / BS;
+    const int npages = (t1 + BS - 1) / BS - page0;
+    for (int i = threadIdx.x; i < npages; i += blockDim.x) s_bt[i] = tables[(int64_t)seq * max_blocks + page0 + i];
     __syncthreads();
-    for (int e = threadIdx.x; e < GC * HS; e += blockDim.x) {
-        const int g = e / HS, d = e % HS;
+
+    // Q^T operand: head c, dims 16s + 4g..+3 (zero past the group)
+    half4_t qb[KS];
+    {
+        const uint16_t *qh = q + ((int64_t)seq * num_heads + head0 + (c < gc ? c : 0)) * HS + 4 * g;
+#pragma unroll
+        for (int st = 0; st < KS; ++st) {
+            const uint2 v = *(const uint2 *)(qh + 16 * st);
+            qb[st] = c < gc ? __builtin_bit_cast(half4_t, v) : (half4_t){};
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;  // head c: running max; this lane's partial sum
+    f32x4_t o[KS];
+#pragma unroll
+    for (int n = 0; n < KS; ++n) o[n] = (f32x4_t){};
+
+    const int64_t kv_stride_blk = (int64_t)num_kv_heads * HS * BS;  // elements per block
+    const int64_t head_off = (int64_t)kvh * HS * BS;
+    const int ntiles = (t1 - t0 + 15) / 16;
+    const int my_tiles = ntiles > wave ? (ntiles - wave + PA_WAVES - 1) / PA_WAVES : 0;
+    // tile k of this wave: tokens t0 + 16 * (wave + PA_WAVES * k) ...
+    auto load_tile = [&](int k, half4_t (&ka)[KS], half4_t (&vb)[KS]) {
+        const int tk = 16 * (wave + PA_WAVES * k);  // first token of the tile, relative to t0
+        // keys: token tk + c at slot (t0 + tk + c) % BS of partition page
+        // (t0 % BS + tk + c) / BS. A tile's tokens past the context can lie on
+        // a page past the sequence's last (block size 8): those read the last
+        // page instead (their logits are masked, their values zeroed).
+        const int kt = (t0 % BS) + tk + c;
+        const int kpg = kt / BS < npages ? kt / BS : npages - 1;
+        const uint16_t *kp = kc + (int64_t)s_bt[kpg] * kv_stride_blk + head_off + (kt % BS) * 8 + 4 * (g & 1);
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+            ka[st] = __builtin_bit_cast(half4_t, *(const uint2 *)(kp + (2 * st + (g >> 1)) * BS * 8));
+        // values: tokens tk + 4g..+3 (one 4-aligned run of slots), dim 16n + c
+        const int vt = (t0 % BS) + tk + 4 * g;
+        const int vpg = vt / BS < npages ? vt / BS : npages - 1;
+        const uint16_t *vp = vc + (int64_t)s_bt[vpg] * kv_stride_blk + head_off + c * BS + (vt % BS);
+#pragma unroll
+        for (int n = 0; n < KS; ++n) vb[n] = __builtin_bit_cast(half4_t, *(const uint2 *)(vp + 16 * n * BS));
+    };
+    auto compute_tile = [&](int k, const half4_t (&ka)[KS], const half4_t (&vin)[KS]) {
+        const int tk = t0 + 16 * (wave + PA_WAVES * k);
+        f32x4_t S = (f32x4_t){};
+#pragma unroll
+        for (int st = 0; st < KS; ++st) S = mfma16(ka[st], qb[st], S);
+        float x[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            x[r] = tk + 4 * g + r < t1 ? S[r] * scale : -INFINITY;
+            mx = fmaxf(mx, x[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);  // finite: every tile holds >= 1 valid token
+        const float alpha = __expf(m_run - m_new);
+        m_run = m_new;
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = tk + 4 * g + r < t1 ? __expf(x[r] - m_new) : 0.0f;
+        l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        const half4_t pa = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+        // O rows are heads 4g + r: their alphas live in lanes c = 4g + r
+        float ao[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ao[r] = __shfl(alpha, 4 * g + r, 64);
+        const bool partial = tk + 16 > t1;  // zero values past the context (they may be NaN)
+#pragma unroll
+        for (int n = 0; n < KS; ++n) {
+            half4_t v = vin[n];
+            if (partial) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (tk + 4 * g + r >= t1) v[r] = (_Float16)0.0f;
+            }
+            f32x4_t on = o[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) on[r] *= ao[r];
+            o[n] = mfma16(pa, v, on);
+        }
+    };
+    half4_t ka[KS], va[KS];
+    if (my_tiles > 0) load_tile(0, ka, va);
+    if constexpr (PIPE) {
+        // two register sets in turn: the next tile's loads are in flight while
+        // this one is multiplied (past the last tile it rereads its own, a
+        // cache hit, so the compiler can count the loads)
+        half4_t kb[KS], vb[KS];
+        for (int k = 0; k < my_tiles; k += 2) {
+            load_tile(k + 1 < my_tiles ? k + 1 : k, kb, vb);
+            compute_tile(k, ka, va);
+            if (k + 1 >= my_tiles) break;
+            load_tile(k + 2 < my_tiles ? k + 2 : k + 1, ka, va);
+            compute_tile(k + 1, kb, vb);
+        }
+    } else {
+        for (int k = 0; k < my_tiles; ++k) {
+            compute_tile(k, ka, va);
+            if (k + 1 < my_tiles) load_tile(k + 1, ka, va);
+        }
+    }
+
+    // this wave's sum per head (over the 4 token groups), then merge the
+    // waves through LDS: max, sum, acc[HS] per head
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (g == 0) {
+        s_m[wave][c] = m_run;
+        s_l[wave][c] = l_run;
+    }
+#pragma unroll
+    for (int n = 0; n < KS; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_acc[wave][4 * g + r][16 * n + c] = o[n][r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < gc * HS; e += blockDim.x) {
+        const int h = e / HS, d = e % HS;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < PA_WAVES; ++w) M = fmaxf(M, s_m[w][g]);
+        for (int w = 0; w < PA_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
         float lsum = 0.0f, a = 0.0f;
 #pragma unroll
         for (int w = 0; w < PA_WAVES; ++w) {
-            const float f = s_m[w][g] == -INFINITY ? 0.0f : __expf(s_m[w][g] - M);
-            lsum += f * s_l[w][g];
-            a += f * s_acc[w][g][d];
+            const float f = s_m[w][h] == -INFINITY ? 0.0f : __expf(s_m[w][h] - M);
+            lsum += f * s_l[w][h];
+            a += f * s_acc[w][h][d];
         }
-        float *slotp = part_slot<HS>(scratch, seq, head0 + g, part, num_heads, P);
+        float *slotp = part_slot<HS>(scratch, seq, head0 + h, part, num_heads, P);
         slotp[2 + d] = a;
         if (d == 0) {
             slotp[0] = M;
@@ -268,27 +262,19 @@ size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
     return (size_t)a.num_seqs * a.num_heads * pa_partitions(a) * (a.head_size + 2) * sizeof(float);
 }
 
-template <int HS, int BS, int GC>
-static void launch_pa3(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream) {
-    const int P = pa_partitions(a);
-    const int groups = (a.num_heads / a.num_kv_heads) / GC;
-    hipLaunchKernelGGL((k_paged_attn<HS, BS, GC>), dim3(a.num_kv_heads * groups, a.num_seqs, P), dim3(256), 0,
-                       stream, (const uint16_t *)a.q, (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache,
-                       a.block_tables, a.context_lens, a.num_heads, a.num_kv_heads, a.max_blocks_per_seq, a.scale, P,
-                       scratch);
-    hipLaunchKernelGGL((k_paged_attn_reduce<HS>), dim3(a.num_heads, a.num_seqs), dim3(HS < 256 ? HS : 256), 0, stream,
-                       (uint16_t *)a.out, (const float *)scratch, a.context_lens, a.num_heads, P);
-}
-
 template <int HS, int BS>
 static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream) {
+    const int P = pa_partitions(a);
     const int G = a.num_heads / a.num_kv_heads;
-    if (G % 4 == 0)
-        launch_pa3<HS, BS, 4>(a, scratch, stream);
-    else if (G % 2 == 0)
-        launch_pa3<HS, BS, 2>(a, scratch, stream);
-    else
-        launch_pa3<HS, BS, 1>(a, scratch, stream);
+    int gc = G < 16 ? G : 16;  // query heads per workgroup: a divisor of G, at most 16
+    while (G % gc) --gc;
+    constexpr bool PIPE = HS <= 128;  // two register sets fit
+    hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE>), dim3(a.num_kv_heads * (G / gc), a.num_seqs, P), dim3(256), 0,
+                       stream, (const uint16_t *)a.q, (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache,
+                       a.block_tables, a.context_lens, a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale,
+                       P, scratch);
+    hipLaunchKernelGGL((k_paged_attn_reduce<HS>), dim3(a.num_heads, a.num_seqs), dim3(HS < 256 ? HS : 256), 0, stream,
+                       (uint16_t *)a.out, (const float *)scratch, a.context_lens, a.num_heads, P);
 }
 
 template <int HS>
