@@ -84,13 +84,17 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
     const int head0 = kvh * G + (blockIdx.x % (G / gc)) * gc;
     const int seq = blockIdx.y;
     const int part = blockIdx.z;
-    const int L = lens[seq];
     const int t0 = part * PA_PART;
+    const int page0 = t0 / BS;
+    // the partition's block ids are read together with the context length
+    // (entries past the table are clamped to its last one and never used)
+    if (max_blocks > 0)
+        for (int i = threadIdx.x; i < PA_PART / BS; i += blockDim.x)
+            s_bt[i] = tables[(int64_t)seq * max_blocks + min(page0 + i, max_blocks - 1)];
+    const int L = lens[seq];
     if (t0 >= L && !(part == 0 && L == 0)) return;  // the reduce kernel ignores partitions past the context
     const int t1 = min(L, t0 + PA_PART);
-    const int page0 = t0 / BS;
     const int npages = (t1 + BS - 1) / BS - page0;
-    for (int i = threadIdx.x; i < npages; i += blockDim.x) s_bt[i] = tables[(int64_t)seq * max_blocks + page0 + i];
     __syncthreads();
 
     // Q^T operand: head c, dims 16s + 4g..+3 (zero past the group)
@@ -227,30 +231,46 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
     }
 }
 
-// Merge the partitions of one (sequence, head) and write f16 output.
+// Merge the partitions of one (sequence, head) and write f16 output. Each
+// thread reads the maxima, sums and its dims of up to 16 partitions in one
+// round of independent loads and forms the weights itself; longer contexts
+// take further rounds.
 template <int HS>
 __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, const float *__restrict__ scratch,
                                                            const int32_t *__restrict__ lens, int num_heads, int P) {
+    constexpr int CHUNK = 16;
     const int head = blockIdx.x, seq = blockIdx.y;
     const int L = lens[seq];
     // partitions holding this sequence's context (never more than were written)
     const int np = min(P, L > 0 ? (L + PA_PART - 1) / PA_PART : 1);
     const float *base = scratch + (int64_t)(seq * num_heads + head) * P * (HS + 2);
-    float M = -INFINITY;
-    for (int p = 0; p < np; ++p) M = fmaxf(M, base[(int64_t)p * (HS + 2)]);
-    float lsum = 0.0f;
-    for (int p = 0; p < np; ++p) {
-        const float m = base[(int64_t)p * (HS + 2)];
-        lsum += m == -INFINITY ? 0.0f : __expf(m - M) * base[(int64_t)p * (HS + 2) + 1];
-    }
-    const float inv = 1.0f / (lsum + 1e-6f);
     for (int d = threadIdx.x; d < HS; d += blockDim.x) {
-        float a = 0.0f;
-        for (int p = 0; p < np; ++p) {
-            const float m = base[(int64_t)p * (HS + 2)];
-            if (m != -INFINITY) a += __expf(m - M) * base[(int64_t)p * (HS + 2) + 2 + d];
+        float M = -INFINITY;
+        for (int p0 = 0; p0 < np; p0 += CHUNK) {
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i)
+                if (p0 + i < np) M = fmaxf(M, base[(int64_t)(p0 + i) * (HS + 2)]);
         }
-        out[((int64_t)seq * num_heads + head) * HS + d] = f2h(a * inv);
+        float lsum = 0.0f, a = 0.0f;
+        for (int p0 = 0; p0 < np; p0 += CHUNK) {
+            float m[CHUNK], l[CHUNK], v[CHUNK];
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) {
+                const int64_t o = (int64_t)(p0 + i < np ? p0 + i : 0) * (HS + 2);
+                m[i] = base[o];
+                l[i] = base[o + 1];
+                v[i] = base[o + 2 + d];
+            }
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) {
+                if (p0 + i < np && m[i] != -INFINITY) {
+                    const float w = __expf(m[i] - M);
+                    lsum += w * l[i];
+                    a += w * v[i];
+                }
+            }
+        }
+        out[((int64_t)seq * num_heads + head) * HS + d] = f2h(a * (1.0f / (lsum + 1e-6f)));
     }
 }
 
