@@ -300,7 +300,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": "q4_K GEMV N=1 with fused Q8_K activation quantization, 128256x4096 "
-                      "(tlh::k_gemv<12, 1, 4, 256, true>), per launch",
+                      "(tlh::k_gemv_reg<12, 1, 4, true, true>), per launch",
             "achieved": round(dom_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -68,6 +68,24 @@ def test_mul_mat_scratch_sizes(wt, n):
     assert nbytes == al(al(al(al(n * K) + n * (K // be) * 4) + sums) + f16_codes)
 
 
+@pytest.mark.parametrize("wt", [N.Q4_0, N.Q8_0, N.Q4_K])
+@pytest.mark.parametrize("n,K,parts", [(1, 14336, 0), (8, 4096, 0), (8, 14336, 4), (16, 8192, 2), (1, 16640, 5)])
+def test_mul_mat_scratch_has_mfma_partials_for_long_K(wt, n, K, parts):
+    """The few-column MFMA kernel (N <= 16 outside the register GEMV) with K above 4096
+    keeps per-chunk partial sums [chunks][batches][N][M] after the activations."""
+    M = 1000
+    if K % 256:
+        pytest.skip("K multiple of 256 here")
+    st, msg, nbytes = scratch_status(N.mul_mat_op(wt, M, K, n))
+    assert st == "OK", msg
+    at = N.VEC_DOT_TYPE[wt]
+    be = N.BLOCK[at][0]
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    sums = n * (K // 16) * 2 if at == N.Q8_K else n * (K // 32) * 4
+    act = al(al(al(al(n * K) + n * (K // be) * 4) + sums))
+    assert nbytes == act + al(parts * n * M * 4)
+
+
 def test_mul_mat_unsupported_weight_type_is_named():
     op = N.mul_mat_op(N.Q4_0, 64, 256, 1)
     op.t[0].ty = 14  # q6_K

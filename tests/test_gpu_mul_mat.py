@@ -1,4 +1,4 @@
-"""GPU parity: GGML_OP_MUL_MAT (decode GEMV N <= 8, prefill GEMM N > 8) through the C ABI
+"""GPU parity: GGML_OP_MUL_MAT (decode GEMV N <= 16, prefill GEMM N > 16) through the C ABI
 against the ggml CPU backend's results (golden vectors) and the oracle.
 
 Tolerance: f32 outputs within 1e-3 relative / 1e-4 absolute,
@@ -170,13 +170,27 @@ def test_repeated_launches_are_deterministic(gpu):
 @pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 8224)],
                          ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K8224"])
 @pytest.mark.parametrize("n", [1, 2, 5, 8])
-def test_lds_staged_gemv_shapes(gpu, t, K, n):
-    """K outside the register-resident GEMV (K % 64 != 0 or K > 16384): the LDS-staged kernel."""
+def test_other_K_shapes(gpu, t, K, n):
+    """K outside the register-resident GEMV (K % 64 != 0 or K > 16384), so every N runs on
+    the int8-MFMA kernel: K % 256 != 0 takes its direct weight loads, K > 4096 its chunked
+    K with the ordered partial-sum merge."""
     M = 77
     w = synth.random_blocks(t, 980 + K, M, K)
     x = synth.normal(981 + n, (n, K))
     y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
     close(y, oracle().mul_mat(t, w, M, K, x), f"{NAMES[t]} K={K} n={n}")
+
+
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("K,n", [(8192, 3), (14336, 8), (14336, 16), (16384, 11)])
+def test_mfma_long_K_chunks(gpu, t, K, n):
+    """The few-column MFMA kernel splits K above 4096 into chunks whose partial sums a
+    second kernel adds in order; odd M leaves a partial 16-row group."""
+    M = 261
+    w = synth.random_blocks(t, 1020 + K + n, M, K)
+    x = synth.normal(1021 + n, (n, K))
+    y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
+    close(y, oracle().mul_mat(t, w, M, K, x, nthreads=16), f"{NAMES[t]} K={K} n={n}")
 
 
 @pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
