@@ -1,8 +1,9 @@
 /*
  * tlhip.h — C ABI of the MI355X (gfx950) executor for tensorlisp's quantized
  * hot path: GGML_OP_MUL_MAT over GGUF block-quantized weights (Q8_0, Q4_0,
- * Q4_K; decode GEMV for N <= 8 columns, MFMA GEMM for prefill) and
- * paged-attention decode over an f16 block-table KV cache.
+ * Q4_K; decode GEMV for N <= 16 columns, MFMA GEMM for prefill),
+ * paged-attention decode over an f16 block-table KV cache, and dense
+ * GGML_OP_FLASH_ATTN_EXT over f16 K/V.
  *
  * This is the surface a `native-hip` feature binds from Rust
  * (crates/kernels/src/hip/ + crates/tensorlisp/src/native_hip.rs), in place of
@@ -109,7 +110,8 @@ typedef struct tlh_op {
  *   op->x[0] = r2 = ne12 / ne02, op->x[1] = r3 = ne13 / ne03 (broadcast).
  * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0 and
  * Q8_0, Q8_K for Q4_K) into `scratch` (at least tlh_mul_mat_scratch_bytes);
- * then N <= 8 runs the decode GEMV, larger N the int8-MFMA GEMM. Integer block
+ * then N <= 16 runs the decode GEMV (register kernel for N <= 2, int8-MFMA
+ * few-column kernel above), larger N the MFMA GEMM. Integer block
  * sums are exact; the f32 result agrees with the CPU backend to rounding of
  * the f32 accumulation order. TLH_UNSUPPORTED (with the reason in
  * tlh_last_error) for any other type or layout. */
@@ -144,6 +146,32 @@ tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, 
  * w_row_bytes) into f32 [rows][k]. The to_f32 of DType (crates/tensorlisp/src/dtype.rs:80-95). */
 tlh_status tlh_dequantize(int type, const void *w, int64_t k, int64_t rows, int64_t w_row_bytes, float *y,
                           void *stream);
+
+/* ------------------------------------------------------- FLASH_ATTN_EXT
+ * GGML_OP_FLASH_ATTN_EXT, replacing Ctx::flash_attn_ext and its fa_main /
+ * fa_split + fa_reduce kernels (crates/kernels/src/cuda/lower.rs:575-657,
+ * split plan :764-792; crates/kernels/src/cuda/native/fa.cu:21-232), computed
+ * as the ggml CPU backend does (vendor/ggml/src/ggml-cpu/ops.cpp:8468-8700):
+ *   op->t[0] q:    f32 [D, nq, nh, nb], nb[0] = 4;
+ *   op->t[1] k:    f16 [D, L, nhkv, nbk], nb[0] = 2, nh % nhkv == 0, nb % nbk == 0;
+ *   op->t[2] v:    f16 [DV, L, nhkv, nbk], nb[0] = 2;
+ *   op->t[3] mask: f16 [>= L, >= nq, mne2, mne3] (read only when `mask` is
+ *                  non-NULL), broadcast over heads (nh % mne2 == 0) and batch;
+ *   op->t[4] dst:  f32 [DV, nh, nq, nb], nb[0] = 4;
+ *   op->x[0] scale (divided by softcap when softcap != 0), x[1] max_bias,
+ *   x[2] m0, x[3] m1 (floats as their bit pattern, sign-extended), x[4]
+ *   n_head_log2, x[5] softcap: the OpBlob lower.rs:615-620 packs.
+ * K/V base pointers and strides must be 16-byte multiples; head sizes D = DV
+ * in {32, 40, 64, 72, 80, 96, 112, 128, 192, 256} or D = 192, DV = 128. No
+ * attention sinks (the reference lowering refuses them too). q is rounded to
+ * f16 (as the CPU backend does for f16 keys); scores and the softmax are f32,
+ * P.V accumulates in f32 (the CPU backend accumulates P.V in f16), so the
+ * result agrees with the CPU backend to f16 rounding. Keys with a -inf mask are
+ * skipped; a row with every key masked gives 0. `scratch` holds split-key
+ * partials (tlh_flash_attn_ext_scratch_bytes; may be NULL when that is 0). */
+tlh_status tlh_flash_attn_ext_scratch_bytes(const tlh_op *op, size_t *bytes);
+tlh_status tlh_flash_attn_ext(const tlh_op *op, const void *q, const void *k, const void *v, const void *mask,
+                              void *dst, void *scratch, size_t scratch_bytes, void *stream);
 
 /* ------------------------------------------------------- paged attention
  * The `paged-attention` custom node (crates/tensorlisp/src/scheme/core.ss:251-258),

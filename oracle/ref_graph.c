@@ -12,6 +12,9 @@
 //                    CPU kernel ggml-cpu.c:1254-1457).
 //   ref_flash_attn   GGML_OP_FLASH_ATTN_EXT over dense f16 K/V (ops.cpp:8468),
 //                    the dense-cache attention the paged kernel is compared to.
+//   ref_flash_attn_ext  the same op in full: q [D, nq, nh, nb], K/V
+//                    [D|DV, L, nhkv, nb], optional f16 mask [Lm, nqm, mne2,
+//                    mne3], max_bias and logit softcap (ggml.c:5402-5444).
 //
 // Tensor data points at caller memory (no copies); the work buffer is
 // allocated per call.
@@ -100,3 +103,30 @@ int ref_flash_attn(const float *q, const uint16_t *k, const uint16_t *v, int64_t
 }
 
 size_t ref_row_size(int wtype, int64_t K) { return ggml_row_size((enum ggml_type)wtype, K); }
+
+// Contiguous tensors; mask may be NULL. out: [DV, nh, nq, nb] f32.
+int ref_flash_attn_ext(const float *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask, int64_t D,
+                       int64_t DV, int64_t nq, int64_t nh, int64_t nb, int64_t L, int64_t nhkv, int64_t Lm,
+                       int64_t nqm, int64_t mne2, int64_t mne3, float scale, float max_bias, float softcap,
+                       float *out, int nthreads, int reps, double *secs) {
+    struct ggml_context *ctx = meta_ctx();
+    if (!ctx) return -1;
+    struct ggml_tensor *tq = ggml_new_tensor_4d(ctx, GGML_TYPE_F32, D, nq, nh, nb);
+    struct ggml_tensor *tk = ggml_new_tensor_4d(ctx, GGML_TYPE_F16, D, L, nhkv, nb);
+    struct ggml_tensor *tv = ggml_new_tensor_4d(ctx, GGML_TYPE_F16, DV, L, nhkv, nb);
+    struct ggml_tensor *tm = NULL;
+    tq->data = (void *)q;
+    tk->data = (void *)k;
+    tv->data = (void *)v;
+    if (mask) {
+        tm = ggml_new_tensor_4d(ctx, GGML_TYPE_F16, Lm, nqm, mne2, mne3);
+        tm->data = (void *)mask;
+    }
+    struct ggml_tensor *o = ggml_flash_attn_ext(ctx, tq, tk, tv, tm, scale, max_bias, softcap);
+    o->data = out;
+    struct ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, o);
+    int rc = compute(gf, nthreads, reps < 1 ? 1 : reps, secs);
+    ggml_free(ctx);
+    return rc;
+}

@@ -534,6 +534,131 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     return 0;
 }
 
+// ------------------------------------------------------- FLASH_ATTN_EXT
+// ops.cpp:8468-8700: one query row over keys [ic0, ic1) (no sinks). Leaves the
+// running max M, sum S and the f16 accumulator VKQ16 (DV values).
+struct fa_shape {
+    const void *q, *k, *v, *mask;
+    const int64_t *q_nb, *k_nb, *v_nb, *m_ne, *m_nb;
+    int64_t DK, DV, rk2, rk3, rv2, rv3;
+    float scale, max_bias, softcap, m0, m1;
+    uint32_t n_head_log2;
+};
+
+static void fa_row_chunk(const struct fa_shape *f, int64_t iq1, int64_t iq2, int64_t iq3, int64_t ic0, int64_t ic1,
+                         uint16_t *Q16, uint16_t *VKQ16, float *Mout, float *Sout) {
+    const uint32_t h = (uint32_t)iq2;
+    const uint32_t nhl2 = f->n_head_log2;
+    const float slope = (f->max_bias > 0.0f) ? h < nhl2 ? powf(f->m0, h + 1) : powf(f->m1, 2 * (h - nhl2) + 1)
+                                             : 1.0f;
+    float S = 0.0f, M = -INFINITY;
+    memset(VKQ16, 0, sizeof(uint16_t) * (size_t)f->DV);
+    const uint16_t *mp = f->mask ? (const uint16_t *)((const char *)f->mask + iq1 * f->m_nb[1] +
+                                                      (iq2 % f->m_ne[2]) * f->m_nb[2] + (iq3 % f->m_ne[3]) * f->m_nb[3])
+                                 : NULL;
+    const int64_t ik3 = iq3 / f->rk3, ik2 = iq2 / f->rk2, iv3 = iq3 / f->rv3, iv2 = iq2 / f->rv2;
+    const float *pq =
+        (const float *)((const char *)f->q + iq1 * f->q_nb[1] + iq2 * f->q_nb[2] + iq3 * f->q_nb[3]);
+    tlq_fp32_to_fp16_row(pq, Q16, f->DK);  // q_to_vec_dot: f16 for f16 keys
+    for (int64_t ic = ic0; ic < ic1; ++ic) {
+        const float mv = mp ? slope * tlq_fp16_to_fp32(mp[ic]) : 0.0f;
+        if (mv == -INFINITY) continue;
+        // ggml_vec_dot_f16, scalar: double sum of f32 products
+        const uint16_t *kr =
+            (const uint16_t *)((const char *)f->k + ic * f->k_nb[1] + ik2 * f->k_nb[2] + ik3 * f->k_nb[3]);
+        double sumf = 0.0;
+        for (int64_t d = 0; d < f->DK; ++d) sumf += (double)(tlq_fp16_to_fp32(kr[d]) * tlq_fp16_to_fp32(Q16[d]));
+        float s = (float)sumf;
+        s = s * f->scale;
+        if (f->softcap != 0.0f) s = f->softcap * tanhf(s);
+        s += mv;
+        const float Mold = M;
+        float ms = 1.0f, vs = 1.0f;
+        const uint16_t *vr =
+            (const uint16_t *)((const char *)f->v + ic * f->v_nb[1] + iv2 * f->v_nb[2] + iv3 * f->v_nb[3]);
+        if (s > M) {
+            M = s;
+            ms = expf(Mold - M);
+            for (int64_t d = 0; d < f->DV; ++d)  // ggml_vec_scale_f16
+                VKQ16[d] = tlq_fp32_to_fp16(tlq_fp16_to_fp32(VKQ16[d]) * ms);
+        } else {
+            vs = expf(s - M);
+        }
+        for (int64_t d = 0; d < f->DV; ++d)  // ggml_vec_mad_f16
+            VKQ16[d] = tlq_fp32_to_fp16(tlq_fp16_to_fp32(VKQ16[d]) + tlq_fp16_to_fp32(vr[d]) * vs);
+        S = S * ms + vs;
+    }
+    *Mout = M;
+    *Sout = S;
+}
+
+int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[4], const void *k,
+                       const int64_t k_ne[4], const int64_t k_nb[4], const void *v, const int64_t v_ne[4],
+                       const int64_t v_nb[4], const void *mask, const int64_t m_ne[4], const int64_t m_nb[4],
+                       void *dst, const int64_t d_nb[4], float scale, float max_bias, float softcap, int nthreads) {
+    const int64_t DK = k_ne[0], DV = v_ne[0], N = q_ne[1], nh = q_ne[2], nb = q_ne[3], L = k_ne[1];
+    if (q_ne[0] != DK || v_ne[1] != L || nh % k_ne[2] || nb % k_ne[3] || nh % v_ne[2] || nb % v_ne[3]) return -1;
+    struct fa_shape f = {q, k, v, mask, q_nb, k_nb, v_nb, m_ne, m_nb, DK, DV, nh / k_ne[2], nb / k_ne[3],
+                         nh / v_ne[2], nb / v_ne[3], scale, max_bias, softcap, 0, 0, 0};
+    // ops.cpp:8523-8533
+    if (softcap != 0) f.scale /= softcap;
+    f.n_head_log2 = 1u << (uint32_t)floor(log2((double)(uint32_t)nh));
+    f.m0 = powf(2.0f, -(max_bias) / f.n_head_log2);
+    f.m1 = powf(2.0f, -(max_bias / 2.0f) / f.n_head_log2);
+    const int nth = nthreads > 0 ? nthreads : 1;
+    uint16_t *Q16 = malloc(sizeof(uint16_t) * (size_t)(DK > 0 ? DK : 1));
+    uint16_t *VKQ16 = malloc(sizeof(uint16_t) * (size_t)(DV > 0 ? DV : 1));
+    float *acc = malloc(sizeof(float) * (size_t)(DV > 0 ? DV : 1));
+    if (!Q16 || !VKQ16 || !acc) {
+        free(Q16);
+        free(VKQ16);
+        free(acc);
+        return -2;
+    }
+    if (N == 1 && nb == 1 && L >= 512) {
+        // split-KV decode (ops.cpp:9115-9145): thread t covers keys
+        // [t*chunk, (t+1)*chunk) and leaves (M, S, VKQ) partials, merged in
+        // chunk order by ggml_flash_attn_ext_reduce_partials (ops.cpp:8996-9063)
+        const int64_t chunk = (L + nth - 1) / nth;
+        for (int64_t h = 0; h < nh; ++h) {
+            float Mf = -INFINITY, Sf = 0.0f;
+            for (int64_t d = 0; d < DV; ++d) acc[d] = 0.0f;
+            for (int t = 0; t < nth; ++t) {
+                const int64_t ic0 = t * chunk;
+                if (ic0 >= L) continue;
+                const int64_t ic1 = ic0 + chunk < L ? ic0 + chunk : L;
+                float Mc, Sc;
+                fa_row_chunk(&f, 0, h, 0, ic0, ic1, Q16, VKQ16, &Mc, &Sc);
+                if (Sc == 0.0f) continue;
+                const float Mn = fmaxf(Mf, Mc);
+                const float so = expf(Mf - Mn), sn = expf(Mc - Mn);
+                for (int64_t d = 0; d < DV; ++d) acc[d] = acc[d] * so + tlq_fp16_to_fp32(VKQ16[d]) * sn;
+                Sf = Sf * so + Sc * sn;
+                Mf = Mn;
+            }
+            if (Sf != 0.0f) {
+                const float S_inv = 1.0f / Sf;
+                for (int64_t d = 0; d < DV; ++d) acc[d] *= S_inv;
+            }
+            memcpy((char *)dst + h * d_nb[1], acc, sizeof(float) * (size_t)DV);
+        }
+    } else {
+        for (int64_t iq3 = 0; iq3 < nb; ++iq3)
+            for (int64_t iq2 = 0; iq2 < nh; ++iq2)
+                for (int64_t iq1 = 0; iq1 < N; ++iq1) {
+                    float M, S;
+                    fa_row_chunk(&f, iq1, iq2, iq3, 0, L, Q16, VKQ16, &M, &S);
+                    const float S_inv = S == 0.0f ? 0.0f : 1.0f / S;
+                    float *out = (float *)((char *)dst + iq2 * d_nb[1] + iq1 * d_nb[2] + iq3 * d_nb[3]);
+                    for (int64_t d = 0; d < DV; ++d) out[d] = tlq_fp16_to_fp32(VKQ16[d]) * S_inv;
+                }
+    }
+    free(Q16);
+    free(VKQ16);
+    free(acc);
+    return 0;
+}
+
 // ------------------------------------------------------- paged attention
 // Key cache element (block, kv head, dim i, slot s) sits at
 // [block][kvh][i/8][s][i%8]; value cache at [block][kvh][i][s]

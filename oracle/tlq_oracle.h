@@ -1,5 +1,5 @@
-// Test infrastructure only. The CPU oracle of the quantized MUL_MAT and
-// paged-attention hot path: a plain-C restatement of the arithmetic the
+// Test infrastructure only. The CPU oracle of the quantized MUL_MAT,
+// FLASH_ATTN_EXT and paged-attention hot path: a plain-C restatement of the arithmetic the
 // reference runs on its CPU backend (vendored ggml) and in its paged-attention
 // kernels (vendored vLLM via crates/kernels/src/cuda/shaders). Only tests/,
 // __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
@@ -96,6 +96,27 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
 int tlq_paged_attention(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                         int num_kv_heads, float scale, const int32_t *block_tables, const int32_t *context_lens,
                         int max_blocks, int num_seqs, int num_heads, int head_size, int block_size);
+
+// GGML_OP_FLASH_ATTN_EXT on the CPU backend's vec path
+// (vendor/ggml/src/ggml-cpu/ops.cpp:8468-8700, ggml_compute_forward_flash_attn_ext_f16_one_chunk)
+// for f32 q and f16 K/V, with the scalar helpers an x86-64 build without
+// -march compiles (vec.h:570-580 ggml_vec_mad_f16, :845-850 ggml_vec_scale_f16,
+// vec.cpp:264-352 ggml_vec_dot_f16): q rounded to f16, q.k summed in double,
+// the P.V accumulator kept in f16 and rounded after every key. Shapes and
+// byte strides are ggml's: q [D, nq, nh, nb], k [D, L, nhkv, nbk],
+// v [DV, L, nhkv, nbk], mask [>= L, >= nq, mne2, mne3] (NULL = none),
+// dst [DV, nh, nq, nb]. m0, m1 and n_head_log2 are derived from max_bias as
+// ops.cpp:8527-8533 does. One query per batch with L >= 512 keys takes the
+// backend's split-KV decode path instead (ops.cpp:9115-9145, reduce
+// :8996-9063): `nthreads` key chunks with their own f16 accumulators, merged
+// in f32 in chunk order, so the result depends on nthreads there as it does
+// in the backend. (The backend's tiled path for >= 64 queries,
+// ops.cpp:8706, accumulates in f32 and is not restated: its results are
+// compared within f16 tolerance.)
+int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[4], const void *k,
+                       const int64_t k_ne[4], const int64_t k_nb[4], const void *v, const int64_t v_ne[4],
+                       const int64_t v_nb[4], const void *mask, const int64_t m_ne[4], const int64_t m_nb[4],
+                       void *dst, const int64_t d_nb[4], float scale, float max_bias, float softcap, int nthreads);
 
 // reshape_and_cache (crates/kernels/src/cuda/shaders/reshape_and_cache_kernel.cu:31-84):
 // key/value f16 [tokens][kvh*hs] scattered to slot = block*bs + offset;

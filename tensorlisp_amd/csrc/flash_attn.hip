@@ -1,0 +1,483 @@
+// Dense-cache GGML_OP_FLASH_ATTN_EXT over f16 K/V, gfx950.
+//
+// Computes what ggml's CPU backend computes for FLASH_ATTN_EXT
+// (vendor/ggml/src/ggml-cpu/ops.cpp:8468-8700) and what the reference's CUDA
+// executor dispatches as fa_main / fa_split + fa_reduce
+// (crates/kernels/src/cuda/native/fa.cu:21-232, lowered at
+// crates/kernels/src/cuda/lower.rs:575-657):
+//   q    f32 [D, nq, nh, nb]           (nb0 = 4)
+//   k    f16 [D, L, nhkv, nbk]         (nb0 = 2), head h reads kv head h / (nh / nhkv)
+//   v    f16 [DV, L, nhkv, nbk]        (nb0 = 2)
+//   mask f16 [>= L, >= nq, mne2, mne3] optional, broadcast over heads and batch
+//   dst  f32 [DV, nh, nq, nb]          (nb0 = 4)
+// per (query, head): s_j = scale * q.k_j, soft-capped (softcap * tanh), plus
+// slope(h) * mask_j (ALiBi slopes from m0, m1, n_head_log2); keys whose mask
+// is -inf are skipped; out = sum_j softmax(s)_j v_j (0 when every key is
+// masked). q is rounded to f16 first, as the CPU backend does for f16 keys.
+//
+// Design (MI355X-first, not the CUDA block-per-query structure):
+//  * a workgroup (4 waves) owns a tile of up to 16 query rows that share one
+//    kv head: gc query heads of the GQA group x qr queries (gc * qr <= 16),
+//    so each K/V row is read once for the whole group; a long key range is
+//    split into partitions across workgroups (flash-decoding) and merged by a
+//    second kernel;
+//  * each wave streams 16-key tiles and runs v_mfma_f32_16x16x16_f16 (lane l,
+//    g = l / 16, c = l % 16; A lane holds A[c][4g..4g+3], B lane
+//    B[4g..4g+3][c], D lane D[4g + r][c]):
+//      S^T = K_tile (16 keys x D) . Q^T (D x 16 rows): the A operand (key c,
+//            four dims) comes from 16-byte loads of the key row, 64
+//            contiguous bytes per key for each group of 4 lanes;
+//      P   = softmax numerators (f16): lane (key 4g + r, row c) of S^T is the
+//            A operand (row c, keys 4g..4g+3) of
+//      O  += P (16 rows x 16 keys) . V_tile (16 keys x DV): lane (c, g) loads
+//            the 16-byte pieces of keys 4g..4g+3 at dims 8c..8c+7 (a
+//            contiguous 256-byte row per 16 lanes), and its B operand for
+//            output tile m is element m of each of the four pieces (two byte
+//            permutes), so output tile m holds dims 8c + m;
+//  * online softmax in f32 (running max and sum per row), f32 accumulation;
+//    waves merge through LDS.
+#include "kernels.hpp"
+
+namespace tlh {
+
+constexpr int FA_WAVES = 4;
+constexpr int FA_TARGET_WGS = 2048;  // workgroups a split launch aims for
+constexpr int FA_MIN_PART = 128;     // fewest keys per partition when split
+
+typedef _Float16 fa_half4 __attribute__((ext_vector_type(4)));
+typedef float fa_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ fa_f32x4 fa_mfma(fa_half4 a, fa_half4 b, fa_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ fa_half4 as_h4(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(fa_half4, make_uint2(lo, hi));
+}
+
+__device__ __forceinline__ uint32_t word(const uint4 &v, int w) { return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w; }
+
+// Key-row geometry: full 32-dim chunks (one 16-byte load, two MFMA steps
+// with dims 32i + 8g + 4s..+3), then a 16-dim step (8-byte load, dims
+// 32F + 4g..+3), then an 8-dim step (lanes g < 2 only).
+template <int D>
+struct KGeom {
+    static constexpr int F = D / 32;
+    static constexpr bool R16 = (D % 32) >= 16;
+    static constexpr bool R8 = (D % 16) == 8;
+    static constexpr int STEPS = 2 * F + R16 + R8;
+    static constexpr int B16 = 32 * F, B8 = B16 + 16 * R16;
+};
+
+// Value-row geometry: 128-dim chunks (16-byte pieces, 8 output tiles with
+// dims 128f + 8c + m), then 64 (8-byte, dims 4c + m), 32 (4-byte, 2c + m),
+// 16 (2-byte, c) and 8 dims (2-byte, c < 8).
+template <int DV>
+struct VGeom {
+    static constexpr int F = DV / 128;
+    static constexpr int REM = DV % 128;
+    static constexpr bool R64 = REM >= 64, R32 = (REM % 64) >= 32, R16 = (REM % 32) >= 16, R8 = (REM % 16) == 8;
+    static constexpr int B64 = 128 * F, B32 = B64 + 64 * R64, B16 = B32 + 32 * R32, B8 = B16 + 16 * R16;
+    static constexpr int T64 = 8 * F, T32 = T64 + 4 * R64, T16 = T32 + 2 * R32, T8 = T16 + R16;
+    static constexpr int NO = T8 + R8;  // output tiles
+    // output dim of tile n in column c
+    __device__ static constexpr int dim(int n, int c) {
+        return n < T64   ? 128 * (n / 8) + 8 * c + n % 8
+               : n < T32 ? B64 + 4 * c + (n - T64)
+               : n < T16 ? B32 + 2 * c + (n - T32)
+               : n < T8  ? B16 + c
+                         : B8 + c;
+    }
+    __device__ static constexpr bool live(int n, int c) { return n < T8 || c < 8; }
+};
+
+struct FaArgs {
+    const char *q, *k, *v, *mask;
+    char *dst;
+    float *part;  // partials [nb][nh][nq][P][DV + 2] when P > 1
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int64_t d_nb1, d_nb2, d_nb3;
+    int m_ne2, m_ne3;
+    int nq, nh, nb, L, nhkv, rk3;  // rk3 = nb / nbk
+    int G, gc, qr, HC, QC;         // heads per kv head; tile = gc heads x qr queries
+    int P, part_len;
+    float scale, max_bias, m0, m1, softcap;
+    int nhl2;
+};
+
+template <int D, int DV, bool MASK>
+struct FaRegs {
+    using KG = KGeom<D>;
+    using VG = VGeom<DV>;
+    uint4 kf[KG::F > 0 ? KG::F : 1];
+    uint2 k16, k8;
+    uint4 vf[VG::F > 0 ? VG::F : 1][4];
+    uint2 v64[4];
+    uint32_t v32[4], v16[4], v8[4];
+    uint32_t mk[4];
+};
+
+template <int D, int DV, bool MASK, bool PIPE>
+__global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
+    using KG = KGeom<D>;
+    using VG = VGeom<DV>;
+    using Regs = FaRegs<D, DV, MASK>;
+    __shared__ float s_m[FA_WAVES][16], s_l[FA_WAVES][16];
+    __shared__ float s_acc[FA_WAVES][16][DV];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+
+    // workgroup -> (query chunk, head chunk, partition); kv head; batch
+    const int qc = blockIdx.x % a.QC;
+    const int hc = (blockIdx.x / a.QC) % a.HC;
+    const int p = blockIdx.x / (a.QC * a.HC);
+    const int hk = blockIdx.y, ib = blockIdx.z;
+    const int j0 = p * a.part_len;
+    const int j1 = min(a.L, j0 + a.part_len);
+    const int nrows = min(a.qr, a.nq - qc * a.qr) * a.gc;  // live rows: a prefix of the tile
+
+    // row c of the tile: query qc*qr + c/gc, head hk*G + hc*gc + c%gc
+    const bool rlive = c < nrows;
+    const int rr = rlive ? c : 0;
+    const int iq = qc * a.qr + rr / a.gc;
+    const int h = hk * a.G + hc * a.gc + rr % a.gc;
+
+    // Q^T operand (row c, dims of step st for group g), rounded to f16
+    fa_half4 qb[KG::STEPS];
+    {
+        const float *qrow = (const float *)(a.q + iq * a.q_nb1 + h * a.q_nb2 + ib * a.q_nb3);
+#pragma unroll
+        for (int st = 0; st < KG::STEPS; ++st) {
+            const int d0 = st < 2 * KG::F ? 32 * (st / 2) + 8 * g + 4 * (st % 2)
+                           : (KG::R16 && st == 2 * KG::F) ? KG::B16 + 4 * g
+                                                          : KG::B8 + 4 * (g & 1);
+            const bool ok = rlive && !(KG::R8 && st == KG::STEPS - 1 && g >= 2);
+            fa_half4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (_Float16)qrow[d0 + e];
+            qb[st] = ok ? v : (fa_half4){};
+        }
+    }
+    float slope = 1.0f;
+    const uint16_t *mrow = nullptr;
+    if constexpr (MASK) {
+        if (a.max_bias > 0.0f)
+            slope = h < a.nhl2 ? powf(a.m0, (float)(h + 1)) : powf(a.m1, (float)(2 * (h - a.nhl2) + 1));
+        mrow = (const uint16_t *)(a.mask + iq * a.m_nb1 + (h % a.m_ne2) * a.m_nb2 + (ib % a.m_ne3) * a.m_nb3);
+    }
+    const float scale = a.scale, softcap = a.softcap;
+
+    const char *kb = a.k + hk * a.k_nb2 + (ib / a.rk3) * a.k_nb3;
+    const char *vb = a.v + hk * a.v_nb2 + (ib / a.rk3) * a.v_nb3;
+    const int64_t k_nb1 = a.k_nb1, v_nb1 = a.v_nb1;
+
+    float m_run = -INFINITY, l_run = 0.0f;  // row c: running max; this lane's partial sum
+    fa_f32x4 o[VG::NO];
+#pragma unroll
+    for (int n = 0; n < VG::NO; ++n) o[n] = (fa_f32x4){};
+
+    const int ntiles = j1 > j0 ? (j1 - j0 + 15) / 16 : 0;
+    const int my_tiles = ntiles > wave ? (ntiles - wave + FA_WAVES - 1) / FA_WAVES : 0;
+
+    // Loads of tile k of this wave (keys t..t+15, t = j0 + 16 (wave + 4k)).
+    // Rows past the partition read its last row instead (their scores are
+    // masked), so every load is unconditional and in bounds.
+    auto load_tile = [&](int k, Regs &R) {
+        const int t = j0 + 16 * (wave + FA_WAVES * k);
+        const char *kr = kb + (int64_t)min(t + c, j1 - 1) * k_nb1;
+#pragma unroll
+        for (int i = 0; i < KG::F; ++i) R.kf[i] = *(const uint4 *)(kr + 64 * i + 16 * g);
+        if constexpr (KG::R16) R.k16 = *(const uint2 *)(kr + 2 * KG::B16 + 8 * g);
+        if constexpr (KG::R8) R.k8 = *(const uint2 *)(kr + 2 * KG::B8 + 8 * (g & 1));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = min(t + 4 * g + j, j1 - 1);
+            const char *vr = vb + (int64_t)key * v_nb1;
+#pragma unroll
+            for (int f = 0; f < VG::F; ++f) R.vf[f][j] = *(const uint4 *)(vr + 256 * f + 16 * c);
+            if constexpr (VG::R64) R.v64[j] = *(const uint2 *)(vr + 2 * VG::B64 + 8 * c);
+            if constexpr (VG::R32) R.v32[j] = *(const uint32_t *)(vr + 2 * VG::B32 + 4 * c);
+            if constexpr (VG::R16) R.v16[j] = *(const uint16_t *)(vr + 2 * VG::B16 + 2 * c);
+            if constexpr (VG::R8) R.v8[j] = *(const uint16_t *)(vr + 2 * VG::B8 + 2 * (c & 7));
+            if constexpr (MASK) R.mk[j] = mrow[key];
+        }
+    };
+    auto compute_tile = [&](int k, const Regs &R) {
+        const int t = j0 + 16 * (wave + FA_WAVES * k);
+        fa_f32x4 S = (fa_f32x4){};
+#pragma unroll
+        for (int i = 0; i < KG::F; ++i) {
+            S = fa_mfma(as_h4(R.kf[i].x, R.kf[i].y), qb[2 * i], S);
+            S = fa_mfma(as_h4(R.kf[i].z, R.kf[i].w), qb[2 * i + 1], S);
+        }
+        if constexpr (KG::R16) S = fa_mfma(as_h4(R.k16.x, R.k16.y), qb[2 * KG::F], S);
+        if constexpr (KG::R8) {
+            const uint2 kk = g < 2 ? R.k8 : make_uint2(0, 0);
+            S = fa_mfma(as_h4(kk.x, kk.y), qb[KG::STEPS - 1], S);
+        }
+        // lane (row c, keys t + 4g + r)
+        float x[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float s = S[r] * scale;
+            if (softcap != 0.0f) s = softcap * tanhf(s);
+            if constexpr (MASK) {
+                const float mv = slope * h2f((uint16_t)R.mk[r]);
+                s = mv == -INFINITY ? -INFINITY : s + mv;
+            }
+            x[r] = t + 4 * g + r < j1 ? s : -INFINITY;
+            mx = fmaxf(mx, x[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        // exp(-inf - (-inf)) is NaN: a row with every key so far masked keeps 0
+        const bool none = m_new == -INFINITY;
+        const float alpha = none ? 1.0f : __expf(m_run - m_new);
+        m_run = m_new;
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = none ? 0.0f : __expf(x[r] - m_new);
+        l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+        const fa_half4 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
+        // output rows are tile rows 4g + r: their alphas live in lanes 4g + r
+        float ao[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ao[r] = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+        for (int n = 0; n < VG::NO; ++n) {
+            uint32_t lo, hi;
+            if (n < VG::T64) {
+                const int f = n / 8, w = (n % 8) / 2;
+                const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+                lo = __builtin_amdgcn_perm(word(R.vf[f][1], w), word(R.vf[f][0], w), sel);
+                hi = __builtin_amdgcn_perm(word(R.vf[f][3], w), word(R.vf[f][2], w), sel);
+            } else if (n < VG::T32) {
+                const int m = n - VG::T64, w = m / 2;
+                const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t a0 = w ? R.v64[0].y : R.v64[0].x, a1 = w ? R.v64[1].y : R.v64[1].x;
+                const uint32_t a2 = w ? R.v64[2].y : R.v64[2].x, a3 = w ? R.v64[3].y : R.v64[3].x;
+                lo = __builtin_amdgcn_perm(a1, a0, sel);
+                hi = __builtin_amdgcn_perm(a3, a2, sel);
+            } else if (n < VG::T16) {
+                const uint32_t sel = ((n - VG::T32) & 1) ? 0x07060302u : 0x05040100u;
+                lo = __builtin_amdgcn_perm(R.v32[1], R.v32[0], sel);
+                hi = __builtin_amdgcn_perm(R.v32[3], R.v32[2], sel);
+            } else if (n < VG::T8) {
+                lo = (R.v16[0] & 0xffffu) | (R.v16[1] << 16);
+                hi = (R.v16[2] & 0xffffu) | (R.v16[3] << 16);
+            } else {
+                lo = (R.v8[0] & 0xffffu) | (R.v8[1] << 16);
+                hi = (R.v8[2] & 0xffffu) | (R.v8[3] << 16);
+            }
+            fa_f32x4 on = o[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) on[r] *= ao[r];
+            o[n] = fa_mfma(pa, as_h4(lo, hi), on);
+        }
+    };
+
+    Regs ra;
+    if (my_tiles > 0) load_tile(0, ra);
+    if constexpr (PIPE) {
+        // two register sets in turn: the next tile's loads are in flight while
+        // this one is multiplied (past the last tile it rereads its own, a
+        // cache hit, so the compiler can count the loads)
+        Regs rb;
+        for (int k = 0; k < my_tiles; k += 2) {
+            load_tile(k + 1 < my_tiles ? k + 1 : k, rb);
+            compute_tile(k, ra);
+            if (k + 1 >= my_tiles) break;
+            load_tile(k + 2 < my_tiles ? k + 2 : k + 1, ra);
+            compute_tile(k + 1, rb);
+        }
+    } else {
+        for (int k = 0; k < my_tiles; ++k) {
+            compute_tile(k, ra);
+            if (k + 1 < my_tiles) load_tile(k + 1, ra);
+        }
+    }
+
+    // row sums over the 4 key groups, then merge the waves through LDS
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (g == 0) {
+        s_m[wave][c] = m_run;
+        s_l[wave][c] = l_run;
+    }
+#pragma unroll
+    for (int n = 0; n < VG::NO; ++n)
+        if (VG::live(n, c))
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s_acc[wave][4 * g + r][VG::dim(n, c)] = o[n][r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < nrows * DV; e += blockDim.x) {
+        const int row = e / DV, d = e % DV;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < FA_WAVES; ++w) M = fmaxf(M, s_m[w][row]);
+        float lsum = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < FA_WAVES; ++w) {
+            const float f = s_m[w][row] == -INFINITY ? 0.0f : __expf(s_m[w][row] - M);
+            lsum += f * s_l[w][row];
+            acc += f * s_acc[w][row][d];
+        }
+        const int riq = qc * a.qr + row / a.gc;
+        const int rh = hk * a.G + hc * a.gc + row % a.gc;
+        if (a.P == 1) {
+            const float inv = lsum == 0.0f ? 0.0f : 1.0f / lsum;
+            float *out = (float *)(a.dst + rh * a.d_nb1 + riq * a.d_nb2 + ib * a.d_nb3);
+            out[d] = acc * inv;
+        } else {
+            float *slot = a.part + ((((int64_t)ib * a.nh + rh) * a.nq + riq) * a.P + p) * (DV + 2);
+            slot[2 + d] = acc;
+            if (d == 0) {
+                slot[0] = M;
+                slot[1] = lsum;
+            }
+        }
+    }
+}
+
+// Merge the partitions of one (batch, head, query) row: every partition was
+// written (an empty one as max -inf, sum 0). Each thread reads the maxima,
+// sums and its dims of up to 16 partitions in one round of loads.
+template <int DV>
+__global__ void __launch_bounds__(256) k_flash_attn_reduce(const FaArgs a) {
+    constexpr int CHUNK = 16;
+    const int iq = blockIdx.x, h = blockIdx.y, ib = blockIdx.z;
+    const int P = a.P;
+    const float *base = a.part + (((int64_t)ib * a.nh + h) * a.nq + iq) * P * (DV + 2);
+    float *out = (float *)(a.dst + h * a.d_nb1 + iq * a.d_nb2 + ib * a.d_nb3);
+    for (int d = threadIdx.x; d < DV; d += blockDim.x) {
+        float M = -INFINITY;
+        for (int p0 = 0; p0 < P; p0 += CHUNK) {
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i)
+                if (p0 + i < P) M = fmaxf(M, base[(int64_t)(p0 + i) * (DV + 2)]);
+        }
+        float lsum = 0.0f, acc = 0.0f;
+        for (int p0 = 0; p0 < P; p0 += CHUNK) {
+            float m[CHUNK], l[CHUNK], v[CHUNK];
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) {
+                const int64_t o = (int64_t)(p0 + i < P ? p0 + i : 0) * (DV + 2);
+                m[i] = base[o];
+                l[i] = base[o + 1];
+                v[i] = base[o + 2 + d];
+            }
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) {
+                if (p0 + i < P && m[i] != -INFINITY) {
+                    const float w = __expf(m[i] - M);
+                    lsum += w * l[i];
+                    acc += w * v[i];
+                }
+            }
+        }
+        out[d] = acc * (lsum == 0.0f ? 0.0f : 1.0f / lsum);
+    }
+}
+
+// ------------------------------------------------------------------ host
+bool flash_attn_head_sizes_ok(int64_t D, int64_t DV) {
+    if (D == 192 && DV == 128) return true;
+    if (D != DV) return false;
+    switch (D) {
+    case 32: case 40: case 64: case 72: case 80: case 96: case 112: case 128: case 192: case 256: return true;
+    default: return false;
+    }
+}
+
+// Row tiles and key partitions of a launch (a pure function of the shape,
+// so the scratch size can be planned ahead).
+struct FaPlan {
+    int G, gc, qr, HC, QC, P, part_len;
+};
+
+static FaPlan fa_plan(int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L) {
+    FaPlan pl;
+    pl.G = (int)(nh / nhkv);
+    pl.gc = pl.G < 16 ? pl.G : 16;  // a divisor of G, at most 16
+    while (pl.G % pl.gc) --pl.gc;
+    pl.qr = nq > 1 ? 16 / pl.gc : 1;
+    if (pl.qr > nq) pl.qr = (int)nq;
+    pl.HC = pl.G / pl.gc;
+    pl.QC = (int)((nq + pl.qr - 1) / pl.qr);
+    const int64_t tiles = (int64_t)pl.QC * pl.HC * nhkv * nb;
+    int64_t P = (FA_TARGET_WGS + tiles - 1) / tiles;
+    const int64_t maxP = L / FA_MIN_PART;
+    if (P > maxP) P = maxP;
+    if (P < 1) P = 1;
+    int64_t part = (L + P - 1) / P;
+    part = (part + 63) / 64 * 64;
+    if (part < 64) part = 64;
+    pl.part_len = (int)part;
+    pl.P = L > 0 ? (int)((L + part - 1) / part) : 1;
+    return pl;
+}
+
+int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L) {
+    const FaPlan pl = fa_plan(nq, nh, nhkv, nb, L);
+    return pl.P > 1 ? nb * nh * nq * pl.P * (DV + 2) * (int64_t)sizeof(float) : 0;
+}
+
+template <int D, int DV>
+static void launch_fa(const FaArgs &a, bool mask, hipStream_t stream) {
+    constexpr bool PIPE = D <= 128 && DV <= 128;  // two register sets fit
+    const dim3 grid(a.QC * a.HC * a.P, a.nhkv, a.nb);
+    if (mask)
+        hipLaunchKernelGGL((k_flash_attn<D, DV, true, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
+    else
+        hipLaunchKernelGGL((k_flash_attn<D, DV, false, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
+    if (a.P > 1)
+        hipLaunchKernelGGL((k_flash_attn_reduce<DV>), dim3(a.nq, a.nh, a.nb), dim3(DV < 256 ? DV : 256), 0, stream,
+                           a);
+}
+
+tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
+    FaArgs a;
+    a.q = (const char *)d.q;
+    a.k = (const char *)d.k;
+    a.v = (const char *)d.v;
+    a.mask = (const char *)d.mask;
+    a.dst = (char *)d.dst;
+    a.part = (float *)d.scratch;
+    a.q_nb1 = d.q_nb[1], a.q_nb2 = d.q_nb[2], a.q_nb3 = d.q_nb[3];
+    a.k_nb1 = d.k_nb[1], a.k_nb2 = d.k_nb[2], a.k_nb3 = d.k_nb[3];
+    a.v_nb1 = d.v_nb[1], a.v_nb2 = d.v_nb[2], a.v_nb3 = d.v_nb[3];
+    a.m_nb1 = d.m_nb[1], a.m_nb2 = d.m_nb[2], a.m_nb3 = d.m_nb[3];
+    a.d_nb1 = d.d_nb[1], a.d_nb2 = d.d_nb[2], a.d_nb3 = d.d_nb[3];
+    a.m_ne2 = (int)d.m_ne2, a.m_ne3 = (int)d.m_ne3;
+    a.nq = (int)d.nq, a.nh = (int)d.nh, a.nb = (int)d.nb, a.L = (int)d.L, a.nhkv = (int)d.nhkv;
+    a.rk3 = (int)(d.nb / d.nbk);
+    const FaPlan pl = fa_plan(d.nq, d.nh, d.nhkv, d.nb, d.L);
+    a.G = pl.G, a.gc = pl.gc, a.qr = pl.qr, a.HC = pl.HC, a.QC = pl.QC, a.P = pl.P, a.part_len = pl.part_len;
+    a.scale = d.scale, a.max_bias = d.max_bias, a.m0 = d.m0, a.m1 = d.m1, a.softcap = d.softcap;
+    a.nhl2 = d.n_head_log2;
+    const bool mask = d.mask != nullptr;
+    switch (d.D * 1000 + d.DV) {
+    case 32032: launch_fa<32, 32>(a, mask, stream); break;
+    case 40040: launch_fa<40, 40>(a, mask, stream); break;
+    case 64064: launch_fa<64, 64>(a, mask, stream); break;
+    case 72072: launch_fa<72, 72>(a, mask, stream); break;
+    case 80080: launch_fa<80, 80>(a, mask, stream); break;
+    case 96096: launch_fa<96, 96>(a, mask, stream); break;
+    case 112112: launch_fa<112, 112>(a, mask, stream); break;
+    case 128128: launch_fa<128, 128>(a, mask, stream); break;
+    case 192192: launch_fa<192, 192>(a, mask, stream); break;
+    case 192128: launch_fa<192, 128>(a, mask, stream); break;
+    case 256256: launch_fa<256, 256>(a, mask, stream); break;
+    default:
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: head sizes D=%lld DV=%lld", (long long)d.D,
+                         (long long)d.DV);
+    }
+    return check_launch("flash_attn_ext");
+}
+
+}  // namespace tlh

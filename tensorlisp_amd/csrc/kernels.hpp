@@ -51,6 +51,22 @@ int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
+// Dense FLASH_ATTN_EXT over f16 K/V (flash_attn.hip). Strides in bytes;
+// scale already divided by softcap when softcap != 0; mask may be null.
+struct FlashAttnDesc {
+    const void *q, *k, *v, *mask;
+    void *dst;
+    void *scratch;  // flash_attn_scratch_bytes of partials (may be null when 0)
+    int64_t D, DV, nq, nh, nb, L, nhkv, nbk;
+    int64_t q_nb[4], k_nb[4], v_nb[4], m_nb[4], d_nb[4];
+    int64_t m_ne2, m_ne3;
+    float scale, max_bias, m0, m1, softcap;
+    int n_head_log2;
+};
+bool flash_attn_head_sizes_ok(int64_t D, int64_t DV);
+int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L);
+tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
+
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
                                   hipStream_t stream);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);

@@ -112,6 +112,71 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
 
 using namespace tlh;
 
+// Validates a FLASH_ATTN_EXT descriptor the way Ctx::flash_attn_ext
+// (crates/kernels/src/cuda/lower.rs:575-657) and ggml_flash_attn_ext
+// (vendor/ggml/src/ggml.c:5402-5444) do, narrowed to what the kernels run:
+// f32 q and dst, f16 K/V with 16-byte aligned rows, f16 mask.
+static float op_float(int64_t x) {
+    const int32_t i = (int32_t)x;
+    float f;
+    memcpy(&f, &i, sizeof f);
+    return f;
+}
+
+static tlh_status check_flash_attn(const tlh_op *op, bool has_mask, FlashAttnDesc &d) {
+    if (!op) return set_error(TLH_INVALID, "flash_attn_ext: null op");
+    const tlh_tensor &q = op->t[0], &k = op->t[1], &v = op->t[2], &m = op->t[3], &o = op->t[4];
+    if (q.ty != TLH_TYPE_F32 || o.ty != TLH_TYPE_F32)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: needs f32 queries and destination");
+    if (k.ty != TLH_TYPE_F16 || v.ty != TLH_TYPE_F16)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: K/V of type %s/%s; have f16", type_name(k.ty),
+                         type_name(v.ty));
+    if (has_mask && m.ty != TLH_TYPE_F16) return set_error(TLH_UNSUPPORTED, "flash_attn_ext: mask must be f16");
+    for (int i = 0; i < 4; ++i)
+        if (q.ne[i] < 0 || k.ne[i] < 0 || v.ne[i] < 0 || o.ne[i] < 0 || (has_mask && m.ne[i] < 0))
+            return set_error(TLH_INVALID, "flash_attn_ext: negative extent");
+    d.D = q.ne[0], d.nq = q.ne[1], d.nh = q.ne[2], d.nb = q.ne[3];
+    d.L = k.ne[1], d.nhkv = k.ne[2], d.nbk = k.ne[3], d.DV = v.ne[0];
+    if (k.ne[0] != d.D || v.ne[1] != d.L || v.ne[2] != d.nhkv || v.ne[3] != d.nbk || d.nhkv == 0 || d.nbk == 0 ||
+        d.nh % d.nhkv != 0 || d.nb % d.nbk != 0)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: inconsistent head shapes");
+    if (o.ne[0] != d.DV || o.ne[1] != d.nh || o.ne[2] != d.nq || o.ne[3] != d.nb)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: destination must be [DV, heads, queries, batch]");
+    if (!flash_attn_head_sizes_ok(d.D, d.DV))
+        return set_error(TLH_UNSUPPORTED,
+                         "flash_attn_ext: head sizes D=%lld DV=%lld (have D = DV in {32, 40, 64, 72, 80, 96, 112, 128, "
+                         "192, 256} and D=192 DV=128)",
+                         (long long)d.D, (long long)d.DV);
+    if (q.nb[0] != 4 || o.nb[0] != 4 || k.nb[0] != 2 || v.nb[0] != 2 || (has_mask && m.nb[0] != 2))
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: rows must be contiguous (nb[0] = element size)");
+    for (int i = 1; i < 4; ++i) {
+        if ((k.nb[i] | v.nb[i]) & 15)
+            return set_error(TLH_UNSUPPORTED, "flash_attn_ext: K/V strides must be multiples of 16 bytes");
+        if ((q.nb[i] | o.nb[i]) & 3 || (has_mask && (m.nb[i] & 1)))
+            return set_error(TLH_INVALID, "flash_attn_ext: misaligned q/dst/mask strides");
+    }
+    if (has_mask) {
+        if (m.ne[0] < d.L || m.ne[1] < d.nq || m.ne[2] == 0 || m.ne[3] == 0 || d.nh % m.ne[2] != 0 ||
+            d.nb % m.ne[3] != 0)
+            return set_error(TLH_UNSUPPORTED, "flash_attn_ext: mask must be [>= keys, >= queries, heads/n, batch/n]");
+    }
+    for (int i = 0; i < 4; ++i) {
+        d.q_nb[i] = q.nb[i], d.k_nb[i] = k.nb[i], d.v_nb[i] = v.nb[i], d.d_nb[i] = o.nb[i];
+        d.m_nb[i] = has_mask ? m.nb[i] : 0;
+    }
+    d.m_ne2 = has_mask ? m.ne[2] : 1;
+    d.m_ne3 = has_mask ? m.ne[3] : 1;
+    d.scale = op_float(op->x[0]);
+    d.max_bias = op_float(op->x[1]);
+    d.m0 = op_float(op->x[2]);
+    d.m1 = op_float(op->x[3]);
+    d.n_head_log2 = (int)op->x[4];
+    d.softcap = op_float(op->x[5]);
+    if (d.nq > INT32_MAX || d.L > INT32_MAX || d.nh > 65535 || d.nhkv > 65535 || d.nb > 65535)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: extents beyond the launch grid");
+    return TLH_OK;
+}
+
 extern "C" {
 
 const char *tlh_last_error(void) { return g_last_error.c_str(); }
@@ -390,6 +455,35 @@ tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cac
     if (!key || !value || !k_cache || !v_cache || !slots) return set_error(TLH_INVALID, "reshape_and_cache: null pointer");
     return launch_reshape_and_cache(key, value, k_cache, v_cache, slots, num_tokens, num_kv_heads, head_size,
                                     block_size, (hipStream_t)stream);
+}
+
+tlh_status tlh_flash_attn_ext_scratch_bytes(const tlh_op *op, size_t *bytes) {
+    if (!bytes) return set_error(TLH_INVALID, "flash_attn_ext_scratch_bytes: null pointer");
+    FlashAttnDesc d;
+    const tlh_status st = check_flash_attn(op, false, d);
+    if (st != TLH_OK) return st;
+    *bytes = (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L);
+    return TLH_OK;
+}
+
+tlh_status tlh_flash_attn_ext(const tlh_op *op, const void *q, const void *k, const void *v, const void *mask,
+                              void *dst, void *scratch, size_t scratch_bytes, void *stream) {
+    FlashAttnDesc d;
+    const tlh_status st = check_flash_attn(op, mask != nullptr, d);
+    if (st != TLH_OK) return st;
+    if (d.max_bias > 0.0f && !mask) return set_error(TLH_INVALID, "flash_attn_ext: max_bias needs a mask");
+    if (d.nq == 0 || d.nh == 0 || d.nb == 0 || d.DV == 0) return TLH_OK;
+    if (!q || !dst || (d.L > 0 && (!k || !v))) return set_error(TLH_INVALID, "flash_attn_ext: null tensor pointer");
+    if (((uintptr_t)k | (uintptr_t)v) & 15)
+        return set_error(TLH_UNSUPPORTED, "flash_attn_ext: K/V must be 16-byte aligned");
+    if (((uintptr_t)q | (uintptr_t)dst) & 3 || ((uintptr_t)mask & 1))
+        return set_error(TLH_INVALID, "flash_attn_ext: misaligned q, dst or mask");
+    const size_t need = (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L);
+    if (need > 0 && (!scratch || scratch_bytes < need))
+        return set_error(TLH_INVALID, "flash_attn_ext: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    if (need > 0 && ((uintptr_t)scratch & 3)) return set_error(TLH_INVALID, "flash_attn_ext: misaligned scratch");
+    d.q = q, d.k = k, d.v = v, d.mask = mask, d.dst = dst, d.scratch = scratch;
+    return launch_flash_attn(d, (hipStream_t)stream);
 }
 
 }  // extern "C"

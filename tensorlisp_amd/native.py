@@ -31,8 +31,8 @@ EXPORTS = (
     "tlh_last_error", "tlh_status_name", "tlh_version", "tlh_device_count", "tlh_device_open", "tlh_alloc",
     "tlh_free", "tlh_h2d", "tlh_d2h", "tlh_stream_sync", "tlh_mul_mat_scratch_bytes", "tlh_mul_mat",
     "tlh_mul_mat_quantize", "tlh_mul_mat_compute",
-    "tlh_quantize_act", "tlh_dequantize", "tlh_paged_attention_scratch_bytes", "tlh_paged_attention",
-    "tlh_reshape_and_cache",
+    "tlh_quantize_act", "tlh_dequantize", "tlh_flash_attn_ext_scratch_bytes", "tlh_flash_attn_ext",
+    "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
 )
 
 
@@ -90,6 +90,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_mul_mat_compute.argtypes = [C.POINTER(TlhOp), vp, vp, C.c_size_t, vp, vp]
     L.tlh_quantize_act.argtypes = [C.c_int, vp, i64, i64, i64, vp, vp]
     L.tlh_dequantize.argtypes = [C.c_int, vp, i64, i64, i64, vp, vp]
+    L.tlh_flash_attn_ext_scratch_bytes.argtypes = [C.POINTER(TlhOp), C.POINTER(C.c_size_t)]
+    L.tlh_flash_attn_ext.argtypes = [C.POINTER(TlhOp), vp, vp, vp, vp, vp, vp, C.c_size_t, vp]
     L.tlh_paged_attention_scratch_bytes.argtypes = [C.POINTER(TlhPagedArgs), C.POINTER(C.c_size_t)]
     L.tlh_paged_attention.argtypes = [C.POINTER(TlhPagedArgs), vp, C.c_size_t, vp]
     L.tlh_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]
@@ -244,6 +246,104 @@ def dequantize(wtype: int, w, k: int, stream=None):
     y = torch.empty((rows, k), dtype=torch.float32, device=w.device)
     check(lib().tlh_dequantize(wtype, _ptr(w), k, rows, w.stride(0), _ptr(y), _stream(stream)))
     return y
+
+
+def _f32_bits(x: float) -> int:
+    """A float op parameter as OpBlob::float stores it (lower.rs:96-98): the f32
+    bit pattern, sign-extended to 64 bits."""
+    import struct
+
+    return struct.unpack("<i", struct.pack("<f", x))[0]
+
+
+def flash_attn_params(n_head: int, scale: float, max_bias: float = 0.0, softcap: float = 0.0):
+    """(scale, max_bias, m0, m1, n_head_log2, softcap) as Ctx::flash_attn_ext derives
+    them (lower.rs:604-620), in f32 arithmetic."""
+    import numpy as np
+
+    f = np.float32
+    scale, max_bias, softcap = f(scale), f(max_bias), f(softcap)
+    if softcap != 0:
+        scale = f(scale / softcap)
+    nhl2 = 1 << int(np.floor(np.log2(f(n_head))))
+    m0 = f(np.power(f(2.0), f(-max_bias / f(nhl2))))
+    m1 = f(np.power(f(2.0), f(-(max_bias / f(2.0)) / f(nhl2))))
+    return float(scale), float(max_bias), float(m0), float(m1), nhl2, float(softcap)
+
+
+def _ggml_type(t) -> int:
+    import torch
+
+    return {torch.float32: F32, torch.float16: F16}.get(t.dtype, -1)
+
+
+def tensor_desc(t, ty: int) -> TlhTensor:
+    """The ggml descriptor of a torch tensor whose shape is ggml's ne reversed
+    (torch (n3, n2, n1, n0) <-> ggml [n0, n1, n2, n3]); strides follow the view."""
+    shape = list(t.shape)[::-1] + [1] * (4 - t.dim())
+    if t.numel() == 0:  # an empty view's strides are arbitrary: use ggml's contiguous ones
+        strides = [t.element_size()]
+        for i in range(1, 4):
+            strides.append(strides[-1] * max(shape[i - 1], 1))
+        return ggml_tensor(ty, shape, strides)
+    strides = [s * t.element_size() for s in list(t.stride())[::-1]]
+    for i in range(t.dim(), 4):
+        strides.append(strides[-1] * shape[i - 1] if strides else t.element_size())
+    return ggml_tensor(ty, shape, strides)
+
+
+def flash_attn_op(q, k, v, mask, dst, scale: float, max_bias: float = 0.0, softcap: float = 0.0) -> TlhOp:
+    """The FLASH_ATTN_EXT descriptor Ctx::flash_attn_ext packs (lower.rs:611-621):
+    t0 q, t1 k, t2 v, t3 mask (zeros when absent), t4 dst; x0..x5 the parameters."""
+    op = TlhOp()
+    op.t[0] = tensor_desc(q, _ggml_type(q))
+    op.t[1] = tensor_desc(k, _ggml_type(k))
+    op.t[2] = tensor_desc(v, _ggml_type(v))
+    if mask is not None:
+        op.t[3] = tensor_desc(mask, _ggml_type(mask))
+    op.t[4] = tensor_desc(dst, _ggml_type(dst))
+    sc, mb, m0, m1, nhl2, cap = flash_attn_params(int(op.t[0].ne[2]), scale, max_bias, softcap)
+    op.x[0], op.x[1], op.x[2], op.x[3] = _f32_bits(sc), _f32_bits(mb), _f32_bits(m0), _f32_bits(m1)
+    op.x[4] = nhl2
+    op.x[5] = _f32_bits(cap)
+    return op
+
+
+def flash_attn_scratch_bytes(op: TlhOp) -> int:
+    n = C.c_size_t()
+    check(lib().tlh_flash_attn_ext_scratch_bytes(C.byref(op), C.byref(n)))
+    return n.value
+
+
+class FlashAttnExt:
+    """One GGML_OP_FLASH_ATTN_EXT node with its split-key scratch. Tensors are torch
+    views whose shapes are ggml's ne reversed: q f32 (nb, nh, nq, D), k f16
+    (nbk, nhkv, L, D), v f16 (nbk, nhkv, L, DV), mask f16 (mne3, mne2, >= nq, >= L)
+    or None, dst f32 (nb, nq, nh, DV)."""
+
+    def __init__(self, q, k, v, mask, dst, scale: float, max_bias: float = 0.0, softcap: float = 0.0):
+        import torch
+
+        self.op = flash_attn_op(q, k, v, mask, dst, scale, max_bias, softcap)
+        self.scratch_bytes = flash_attn_scratch_bytes(self.op)
+        self.scratch = torch.empty(max(self.scratch_bytes, 4), dtype=torch.uint8, device=q.device)
+
+    def __call__(self, q, k, v, mask, dst, stream=None):
+        check(lib().tlh_flash_attn_ext(C.byref(self.op), _ptr(q), _ptr(k), _ptr(v),
+                                       _ptr(mask) if mask is not None else None, _ptr(dst), _ptr(self.scratch),
+                                       self.scratch_bytes, _stream(stream)))
+        return dst
+
+
+def flash_attn_ext(q, k, v, mask=None, scale: float = 1.0, max_bias: float = 0.0, softcap: float = 0.0,
+                   stream=None):
+    """ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, softcap) on torch views
+    (shapes as in FlashAttnExt) -> dst f32 (nb, nq, nh, DV), ggml [DV, nh, nq, nb]."""
+    import torch
+
+    nb, nh, nq, _ = q.shape
+    dst = torch.empty((nb, nq, nh, v.shape[-1]), dtype=torch.float32, device=q.device)
+    return FlashAttnExt(q, k, v, mask, dst, scale, max_bias, softcap)(q, k, v, mask, dst, stream)
 
 
 class PagedAttention:

@@ -21,8 +21,13 @@ these are the reference's outputs on fixed inputs, captured once:
                    and the CPU backend's output vector
   flash_attn.npz   GGML_OP_FLASH_ATTN_EXT (ops.cpp:8468) on dense f16 K/V, the
                    dense-cache counterpart of paged attention
+  flash_attn_ext.npz  GGML_OP_FLASH_ATTN_EXT with masks, GQA, batch, soft cap and
+                   ALiBi on the shapes of the reference's attention tests
+                   (refs.FA_CASES, native.rs:156-345), 8 CPU threads, outputs of the
+                   first and last 6 queries; inputs are regenerated from the
+                   stored seeds by refs.fa_case_inputs
 
-Run: python tests/golden/make_golden.py   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -36,7 +41,7 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import Q4_0, Q4_K, Q8_0, Ref, fp16_probe_values, xorshift_noise  # noqa: E402
+from refs import FA_CASES, Q4_0, Q4_K, Q8_0, Ref, fa_case_inputs, fp16_probe_values, xorshift_noise  # noqa: E402
 from tensorlisp_amd import synth  # noqa: E402
 
 
@@ -69,8 +74,25 @@ def edge_rows_act(k: int) -> np.ndarray:
     return np.stack(rows).astype(np.float32)
 
 
+def flash_attn_ext_golden(ref) -> None:
+    out = {}
+    for i, case in enumerate(FA_CASES):
+        seed = 500 + 10 * i
+        q, k, v, m, scale, max_bias, softcap = fa_case_inputs(case, seed)
+        o, _ = ref.flash_attn_ext(q, k, v, m, scale, max_bias, softcap, nthreads=8)
+        nq = o.shape[1]
+        rows = np.unique(np.r_[np.arange(min(nq, 6)), np.arange(max(nq - 6, 0), nq)])  # first and last queries
+        out[f"{case[0]}/seed"] = np.array([seed])
+        out[f"{case[0]}/rows"] = rows
+        out[f"{case[0]}/out"] = o[:, rows]
+    np.savez_compressed(HERE / "flash_attn_ext.npz", **out)
+
+
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["flash_attn_ext"]:  # only the FLASH_ATTN_EXT fixture
+        flash_attn_ext_golden(ref)
+        return
     # ---------------------------------------------------------------- fp16
     halves = np.arange(65536, dtype=np.uint16)
     h2f = ref.f16_to_f32(halves)
@@ -129,6 +151,7 @@ def main() -> None:
         o, _ = ref.flash_attn(q, kk, vv, 1.0 / np.sqrt(D))
         out.update({f"q{i}": q, f"k{i}": kk, f"v{i}": vv, f"o{i}": o})
     np.savez_compressed(HERE / "flash_attn.npz", **out)
+    flash_attn_ext_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

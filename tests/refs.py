@@ -42,6 +42,23 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def _ne(a: np.ndarray) -> np.ndarray:
+    """ggml ne of an array whose shape is ne reversed."""
+    return np.array(list(a.shape)[::-1] + [1] * (4 - a.ndim), np.int64)
+
+
+def _nb(a: np.ndarray) -> np.ndarray:
+    """ggml byte strides of such an array."""
+    st = list(a.strides)[::-1]
+    while len(st) < 4:
+        st.append(st[-1] * a.shape[0] if st else a.itemsize)
+    return np.array(st, np.int64)
+
+
+def _i64p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_int64))
+
+
 class Oracle:
     def __init__(self, path: Path = ORACLE_SO):
         if not path.exists():
@@ -65,6 +82,10 @@ class Oracle:
                                           C.c_int, C.c_int]
         L.tlq_paged_attention.restype = C.c_int
         L.tlq_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]
+        arr4 = C.POINTER(C.c_int64)
+        L.tlq_flash_attn_ext.argtypes = [vp, arr4, arr4, vp, arr4, arr4, vp, arr4, arr4, vp, arr4, arr4, vp, arr4,
+                                         C.c_float, C.c_float, C.c_float, C.c_int]
+        L.tlq_flash_attn_ext.restype = C.c_int
         L.tlq_gather_kv.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp]
 
     # -- fp16
@@ -138,6 +159,28 @@ class Oracle:
         assert rc == 0, rc
         return out
 
+    def flash_attn_ext(self, q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0,
+                       nthreads: int = 8) -> np.ndarray:
+        """GGML_OP_FLASH_ATTN_EXT on numpy arrays whose shapes are ggml's ne reversed
+        (any strides): q f32 (nb, nh, nq, D), k/v f16 bits (nb, nhkv, L, D|DV),
+        mask f16 bits (mne3, mne2, >= nq, >= L) or None -> f32 (nb, nq, nh, DV).
+        nthreads matters only on the backend's split-KV decode path."""
+        nb, nh, nq, _ = q.shape
+        DV = v.shape[-1]
+        out = np.zeros((nb, nq, nh, DV), np.float32)
+        zero = np.zeros(4, np.int64)
+        args = []
+        for a, dt in ((q, np.float32), (k, np.uint16), (v, np.uint16), (mask, np.uint16)):
+            if a is None:
+                args += [None, _i64p(zero), _i64p(zero)]
+                continue
+            assert a.dtype == dt, (a.dtype, dt)
+            args += [_p(a), _i64p(_ne(a)), _i64p(_nb(a))]
+        rc = self.lib.tlq_flash_attn_ext(*args, _p(out), _i64p(_nb(out)), float(scale), float(max_bias),
+                                         float(softcap), nthreads)
+        assert rc == 0, rc
+        return out
+
     def reshape_and_cache(self, key, value, k_cache, v_cache, slots, num_kv_heads, head_size, block_size):
         key = np.ascontiguousarray(key, dtype=np.uint16)
         value = np.ascontiguousarray(value, dtype=np.uint16)
@@ -181,6 +224,9 @@ class Ref:
         L.ref_flash_attn.argtypes = [vp, vp, vp, i64, i64, i64, i64, C.c_float, vp, C.c_int, C.c_int,
                                      C.POINTER(C.c_double)]
         L.ref_flash_attn.restype = C.c_int
+        L.ref_flash_attn_ext.argtypes = [vp, vp, vp, vp] + [i64] * 11 + [C.c_float] * 3 + [
+            vp, C.c_int, C.c_int, C.POINTER(C.c_double)]
+        L.ref_flash_attn_ext.restype = C.c_int
         L.ggml_cpu_init.argtypes = []
         L.ggml_cpu_init()
 
@@ -257,6 +303,140 @@ class Ref:
                                      C.byref(secs))
         assert rc == 0, rc
         return out, secs.value
+
+    def flash_attn_ext(self, q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0, nthreads: int = 8,
+                       reps: int = 1):
+        """ggml_flash_attn_ext on the CPU backend, contiguous inputs shaped as in
+        Oracle.flash_attn_ext. Returns (out f32 (nb, nq, nh, DV), seconds)."""
+        q = _f32(q)
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        nb, nh, nq, D = q.shape
+        _, nhkv, L, DV = v.shape
+        out = np.empty((nb, nq, nh, DV), np.float32)
+        if mask is not None:
+            mask = np.ascontiguousarray(mask, dtype=np.uint16)
+            mne3, mne2, nqm, Lm = mask.shape
+        else:
+            mne3 = mne2 = nqm = Lm = 0
+        secs = C.c_double()
+        rc = self.lib.ref_flash_attn_ext(_p(q), _p(k), _p(v), _p(mask) if mask is not None else None, D, DV, nq, nh,
+                                         nb, L, nhkv, Lm, nqm, mne2, mne3, float(scale), float(max_bias),
+                                         float(softcap), _p(out), nthreads, reps, C.byref(secs))
+        assert rc == 0, rc
+        return out, secs.value
+
+
+def flash_attn_f64(q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0) -> np.ndarray:
+    """FLASH_ATTN_EXT in float64 on exactly the f16 inputs (q rounded to f16 first,
+    as the CPU backend does for f16 keys): the mathematical value every
+    implementation approximates. Shapes as in Oracle.flash_attn_ext."""
+    nb, nh, nq, D = q.shape
+    _, nhkv, L, DV = v.shape
+    q16 = np.asarray(q, np.float32).astype(np.float16).astype(np.float64)
+    kk = np.asarray(k).view(np.float16).astype(np.float64)
+    vv = np.asarray(v).view(np.float16).astype(np.float64)
+    sc = np.float32(scale)
+    if softcap != 0:
+        sc = np.float32(sc / np.float32(softcap))
+    nhl2 = 1 << int(np.floor(np.log2(nh)))
+    m0 = 2.0 ** (-max_bias / nhl2)
+    m1 = 2.0 ** (-(max_bias / 2.0) / nhl2)
+    out = np.zeros((nb, nq, nh, DV), np.float64)
+    for b in range(nb):
+        for h in range(nh):
+            hk = h // (nh // nhkv)
+            bk = b // (nb // k.shape[0])
+            s = (q16[b, h] @ kk[bk, hk].T) * float(sc)  # (nq, L)
+            if softcap != 0:
+                s = softcap * np.tanh(s)
+            if mask is not None:
+                slope = 1.0 if max_bias <= 0 else (m0 ** (h + 1) if h < nhl2 else m1 ** (2 * (h - nhl2) + 1))
+                mv = np.asarray(mask).view(np.float16)[b % mask.shape[0], h % mask.shape[1], :nq, :L]
+                mv = mv.astype(np.float64) * slope
+                s = np.where(np.isneginf(mv), -np.inf, s + mv)
+            m = s.max(axis=1, keepdims=True)
+            live = np.isfinite(m)
+            e = np.where(live, np.exp(s - np.where(live, m, 0.0)), 0.0)
+            den = e.sum(axis=1, keepdims=True)
+            out[b, :, h] = np.where(den > 0, (e @ vv[bk, hk]) / np.where(den > 0, den, 1.0), 0.0)
+    return out
+
+
+# FLASH_ATTN_EXT cases of the reference's own tests (crates/tensorlisp/tests/native.rs:156-345)
+# plus ALiBi: (name, nb, nh, nhkv, nq, L, D, DV, mask kind, max_bias, softcap).
+# Mask kinds build the f16 padding masks those tests use ([L, nq, 1, nb]: 0 or -inf):
+#   "flash"  native.rs:175-181  batch 0 masks keys >= 3L/4, batch 1 keys >= 5
+#   "split"  native.rs:202-208  batch 0 keeps keys < v0, batch 1 keys < v1 (v0, v1 in the name)
+#   "holes"  native.rs:290-293  keys < 3L/4 with j % 3 != 1
+#   "many"   native.rs:336-344  batch 0 masks the first L/4 and [L/2, L/2 + 7), batch 1 keys >= 3
+#   "bias"   finite position biases -0.05 * |distance| (what ALiBi slopes scale) and
+#            -inf on every fifth key
+#   "none"   no mask
+FA_CASES = (
+    [(f"flash-{nq}-{nk}-{m}", 2, 4, 2, nq, nk, 64, 64, m, 0.0, 0.0)
+     for nq, nk in ((5, 6), (40, 70), (40, 64), (3, 100), (1, 1000), (1, 777)) for m in ("flash", "none")]
+    + [(f"split-{nk}-{v0}-{v1}", 2, 4, 2, 1, nk, 64, 64, "split", 0.0, 0.0)
+       for nk, v0, v1 in ((300, 300, 300), (1000, 750, 5), (512, 129, 128), (777, 1, 777))]
+    + [(f"hs-{hs}-{nq}-{nk}", 1, 4, 1, nq, nk, hs, hs, "holes", 0.0, 0.0)
+       for hs, nq, nk in ((128, 1, 300), (256, 1, 1000), (256, 1, 100), (256, 5, 60), (256, 40, 70))]
+    + [(f"many-{hs}-{nq}-{nk}", 2, 4, 2, nq, nk, hs, hs, "many", 0.0, sc)
+       for hs, nq, nk, sc in ((72, 16, 1, 0.0), (72, 17, 17, 0.0), (72, 100, 300, 0.0), (80, 33, 129, 0.0),
+                              (64, 130, 70, 30.0), (96, 20, 5000, 0.0), (112, 50, 33, 0.0), (128, 64, 256, 20.0))]
+    + [("alibi-6-2", 1, 6, 2, 3, 90, 64, 64, "bias", 8.0, 0.0),
+       ("alibi-12-4", 2, 12, 4, 2, 40, 128, 128, "bias", 4.0, 10.0),
+       ("dv-192-128", 1, 8, 2, 4, 50, 192, 128, "holes", 0.0, 0.0)]
+)
+
+
+def fa_mask(kind: str, nb: int, nq: int, L: int):
+    """f16 bits (nb, 1, nq, L) of a padding mask, or None."""
+    if kind == "none":
+        return None
+    if kind == "bias":
+        iq = np.arange(nq)[:, None] + (L - nq)
+        j = np.arange(L)[None, :]
+        m = np.where(j % 5 == 4, -np.inf, -0.05 * np.abs(j - iq)).astype(np.float32)
+        m = m[None, None] + np.float32(0.25) * np.arange(nb, dtype=np.float32)[:, None, None, None]
+        return np.ascontiguousarray(m.astype(np.float16)).view(np.uint16)
+    valid = np.ones((nb, L), bool)
+    if kind == "flash":
+        valid[0, L * 3 // 4:] = False
+        valid[1, 5:] = False
+    elif kind.startswith("split"):
+        v0, v1 = (int(t) for t in kind.split(":")[1:])
+        valid[:] = False
+        valid[0, :v0] = True
+        valid[1, :v1] = True
+    elif kind == "holes":
+        j = np.arange(L)
+        valid[:] = (j < L * 3 // 4) & (j % 3 != 1)
+    elif kind == "many":
+        valid[0, :L // 4] = False
+        valid[1, 3:] = False
+        valid[0, L // 2:min(L // 2 + 7, L)] = False
+    else:
+        raise ValueError(kind)
+    m = np.where(valid, np.float32(0.0), np.float32(-np.inf)).astype(np.float16)
+    return np.ascontiguousarray(np.broadcast_to(m[:, None, None, :], (nb, 1, nq, L))).view(np.uint16)
+
+
+def fa_case_inputs(case, seed: int):
+    """(q, k, v, mask, scale, max_bias, softcap) of one FA_CASES entry: q f32 and K/V
+    f16 bits from tensorlisp_amd.synth normal draws seeded by `seed`."""
+    import sys
+
+    sys.path.insert(0, str(ROOT))
+    from tensorlisp_amd import synth
+
+    name, nb, nh, nhkv, nq, L, D, DV, mkind, max_bias, softcap = case
+    if mkind == "split":
+        _, nk, v0, v1 = name.split("-")
+        mkind = f"split:{v0}:{v1}"
+    q = synth.normal(seed, (nb, nh, nq, D))
+    k = synth.f16_bits(synth.normal(seed + 1, (nb, nhkv, L, D)))
+    v = synth.f16_bits(synth.normal(seed + 2, (nb, nhkv, L, DV)))
+    return q, k, v, fa_mask(mkind, nb, nq, L), 1.0 / np.sqrt(D), max_bias, softcap
 
 
 _oracle = None

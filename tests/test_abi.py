@@ -153,6 +153,64 @@ def test_paged_attention_geometry_validation(kw, status):
         assert n.value == 32 * 32 * (8192 // 512) * (128 + 2) * 4
 
 
+def _fa_op(nb=2, nh=8, nhkv=2, nq=1, L=1000, D=128, DV=None, kdt="f16", mask=True, **kw):
+    import torch
+
+    DV = D if DV is None else DV
+    dt = {"f16": torch.float16, "f32": torch.float32}[kdt]
+    q = torch.zeros((nb, nh, nq, D))
+    k = torch.zeros((nb, nhkv, L, D), dtype=dt)
+    v = torch.zeros((nb, nhkv, L, DV), dtype=dt)
+    m = torch.zeros((nb, 1, nq, L), dtype=torch.float16) if mask else None
+    d = torch.zeros((nb, nq, nh, DV))
+    return N.flash_attn_op(q, k, v, m, d, 0.1, **kw)
+
+
+def fa_scratch_status(op):
+    n = C.c_size_t()
+    st, msg = _status(N.lib().tlh_flash_attn_ext_scratch_bytes, C.byref(op), C.byref(n))
+    return st, msg, n.value
+
+
+def test_flash_attn_op_packs_the_lowering_parameters():
+    """x0..x5 as Ctx::flash_attn_ext packs them (lower.rs:604-620): scale divided by
+    softcap, n_head_log2 = 8 for 12 heads, m0 = 2^(-8/8), m1 = 2^(-4/8)."""
+    import struct
+
+    op = _fa_op(nh=12, nhkv=4, softcap=20.0, max_bias=8.0)
+    f = [struct.unpack("<f", struct.pack("<i", op.x[i]))[0] for i in (0, 1, 2, 3, 5)]
+    assert f[0] == pytest.approx(0.1 / 20.0, rel=1e-6) and f[1] == 8.0 and f[4] == 20.0
+    assert op.x[4] == 8 and f[2] == pytest.approx(0.5, rel=1e-6) and f[3] == pytest.approx(2 ** -0.5, rel=1e-6)
+    assert list(op.t[3].ne) == [1000, 1, 1, 2] and op.t[3].ty == N.F16
+    assert list(op.t[4].ne) == [128, 12, 1, 2]
+
+
+def test_flash_attn_scratch_sizes():
+    """Partials [nb][nh][nq][P][DV + 2] f32 when the keys are split, else none."""
+    st, msg, n = fa_scratch_status(_fa_op(nb=32, nh=32, nhkv=8, L=4096))
+    assert st == "OK", msg
+    assert n == 32 * 32 * 8 * (128 + 2) * 4  # the bench shape: 8 partitions of 512 keys
+    st, msg, n = fa_scratch_status(_fa_op(L=100))
+    assert st == "OK" and n == 0  # too short to split
+    st, msg, n = fa_scratch_status(_fa_op(nb=1, nh=8, nhkv=8, nq=3, L=5000, D=64))
+    assert st == "OK" and n > 0 and n % (1 * 8 * 3 * (64 + 2) * 4) == 0
+
+
+@pytest.mark.parametrize("kw,status,text", [
+    ({"kdt": "f32"}, "UNSUPPORTED", "K/V of type f32"),
+    ({"D": 48}, "UNSUPPORTED", "head sizes"),
+    ({"D": 128, "DV": 64}, "UNSUPPORTED", "head sizes"),
+    ({"D": 576, "DV": 512}, "UNSUPPORTED", "head sizes"),
+    ({"nhkv": 3}, "UNSUPPORTED", "inconsistent"),
+    ({"D": 192, "DV": 128}, "OK", ""),
+    ({"D": 72}, "OK", ""),
+])
+def test_flash_attn_validation(kw, status, text):
+    st, msg, _ = fa_scratch_status(_fa_op(**kw))
+    assert st == status, msg
+    assert text in msg
+
+
 def test_no_device_is_reported_not_fatal():
     import torch
 

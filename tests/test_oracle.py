@@ -328,3 +328,113 @@ def test_reshape_and_cache_gather_roundtrip():
     keep[7] = False
     assert np.array_equal(k[:, keep], kk[:, keep]) and np.array_equal(v[:, keep], vv[:, keep])
     assert np.all(k[:, 7] == 0) and np.all(v[:, 7] == 0)
+
+
+# --------------------------------------------------------- FLASH_ATTN_EXT
+# tlq_flash_attn_ext restates the CPU backend's vec path (ops.cpp:8468-8700) and
+# split-KV decode path (ops.cpp:9115-9145, :8996-9063). Pins: the reference's own
+# outputs on its test shapes (golden, bit-exact where the backend takes those two
+# paths; its tiled path for >= 64 queries accumulates in f32 instead), the compiled
+# reference live, and a float64 brute force (f16 accumulator error only).
+from refs import FA_CASES, fa_case_inputs, flash_attn_f64  # noqa: E402
+
+
+def _fa_tiled(case):
+    return case[4] >= 64  # ggml_fa_tile_config::Q (common.h:9): the backend's tiled path
+
+
+@pytest.mark.parametrize("case", FA_CASES, ids=[c[0] for c in FA_CASES])
+def test_flash_attn_oracle_golden(case):
+    g = gold("flash_attn_ext")
+    name = case[0]
+    q, k, v, m, scale, max_bias, softcap = fa_case_inputs(case, int(g[f"{name}/seed"][0]))
+    got = oracle().flash_attn_ext(q, k, v, m, scale, max_bias, softcap, nthreads=8)[:, g[f"{name}/rows"]]
+    want = g[f"{name}/out"]
+    if _fa_tiled(case):
+        assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max() + 1e-6
+    else:
+        assert same_bits(got, want), np.abs(got - want).max()
+
+
+def test_flash_attn_oracle_dense_golden_of_paged_tests():
+    """The one-query dense goldens (flash_attn.npz: L = 70, 33, 515, 5), bit-exact;
+    L = 515 takes the split-KV path with 8 chunks."""
+    g = gold("flash_attn")
+    for i in range(4):
+        q32, k, v, want = g[f"q{i}"], g[f"k{i}"], g[f"v{i}"], g[f"o{i}"]
+        Hkv, L, D = k.shape
+        H = q32.shape[0]
+        got = oracle().flash_attn_ext(q32.reshape(1, H, 1, D), k[None], v[None], None, 1.0 / np.sqrt(D),
+                                      nthreads=8)
+        assert same_bits(got.reshape(H, D), want), i
+
+
+FA_RANDOM = [
+    # nb, nh, nhkv, nq, L, D, DV, mask kind, max_bias, softcap
+    (1, 4, 1, 1, 70, 128, 128, "none", 0.0, 0.0),
+    (2, 8, 2, 7, 45, 64, 64, "holes", 0.0, 0.0),
+    (1, 6, 3, 3, 33, 80, 80, "bias", 8.0, 0.0),  # ALiBi, heads past n_head_log2 = 4 use m1
+    (2, 4, 4, 5, 20, 96, 96, "many", 0.0, 50.0),
+    (1, 8, 1, 1, 900, 112, 112, "holes", 0.0, 0.0),  # split-KV decode
+    (2, 4, 2, 2, 64, 192, 128, "bias", 2.0, 0.0),
+]
+
+
+@pytest.mark.parametrize("nthreads", [8, 3])
+@pytest.mark.parametrize("shape", FA_RANDOM)
+def test_flash_attn_oracle_vs_reference_live(shape, nthreads):
+    r = ref()
+    if r is None:
+        pytest.skip("oracle/_ref is not built here (needs /root/reference)")
+    case = ("live",) + shape
+    q, k, v, m, scale, max_bias, softcap = fa_case_inputs(case, 4242 + shape[4])
+    got = oracle().flash_attn_ext(q, k, v, m, scale, max_bias, softcap, nthreads=nthreads)
+    want, _ = r.flash_attn_ext(q, k, v, m, scale, max_bias, softcap, nthreads=nthreads)
+    assert same_bits(got, want), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("shape", FA_RANDOM)
+def test_flash_attn_oracle_vs_f64(shape):
+    """Within the f16 accumulator's error of the exact softmax over the f16 inputs:
+    a dropped soft cap, slope, mask term or scale moves results by O(1) of the scale."""
+    case = ("f64",) + shape
+    q, k, v, m, scale, max_bias, softcap = fa_case_inputs(case, 777 + shape[5])
+    got = oracle().flash_attn_ext(q, k, v, m, scale, max_bias, softcap)
+    want = flash_attn_f64(q, k, v, m, scale, max_bias, softcap)
+    assert np.abs(got - want).max() <= 8e-3 * np.abs(want).max()
+
+
+def test_flash_attn_f64_pins_against_closed_forms():
+    """The brute force itself: a single key gives v exactly; identical keys give the
+    mean of the values; a fully masked row gives 0; softcap -> tanh bound."""
+    rng = np.random.default_rng(5)
+    D = 64
+    q = rng.standard_normal((1, 2, 3, D)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 1, D)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((1, 1, 1, D)).astype(np.float16).view(np.uint16)
+    o = flash_attn_f64(q, k, v, None, 0.3)
+    assert np.allclose(o, v.view(np.float16).astype(np.float64)[0, 0, 0])
+    k4 = np.repeat(k, 5, axis=2)
+    v4 = rng.standard_normal((1, 1, 5, D)).astype(np.float16).view(np.uint16)
+    o = flash_attn_f64(q, k4, v4, None, 0.3)
+    assert np.allclose(o, v4.view(np.float16).astype(np.float64)[0, 0].mean(0))
+    m = np.full((1, 1, 3, 5), np.float16(-np.inf)).view(np.uint16)
+    assert np.all(flash_attn_f64(q, k4, v4, m, 0.3) == 0)
+    # the oracle agrees on those three closed forms too
+    got = oracle().flash_attn_ext(q, k4, v4, m, 0.3)
+    assert np.all(got == 0)
+
+
+def test_flash_attn_oracle_catches_planted_mistakes():
+    """Mistakes planted in the inputs the oracle sees (on the CPU): a wrong scale, a
+    dropped soft cap or a dropped ALiBi slope each move the result far outside the
+    f64 tolerance the oracle meets."""
+    case = ("plant", 1, 6, 2, 2, 40, 64, 64, "bias", 8.0, 1.5)  # a cap that saturates tanh
+    q, k, v, m, scale, max_bias, softcap = fa_case_inputs(case, 99)
+    want = flash_attn_f64(q, k, v, m, scale, max_bias, softcap)
+    tol = 8e-3 * np.abs(want).max()
+    o = oracle()
+    assert np.abs(o.flash_attn_ext(q, k, v, m, scale, max_bias, softcap) - want).max() <= tol
+    assert np.abs(o.flash_attn_ext(q, k, v, m, scale * 1.5, max_bias, softcap) - want).max() > 10 * tol
+    assert np.abs(o.flash_attn_ext(q, k, v, m, scale, 0.0, softcap) - want).max() > 10 * tol
+    assert np.abs(o.flash_attn_ext(q, k, v, m, scale, max_bias, 0.0) - want).max() > 10 * tol
