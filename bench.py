@@ -18,7 +18,9 @@ roofline = the dominant kernel (the Q4_K GEMV at N = 1 on the 128256 x 4096
 cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, compiled from
          the reference sources) on the same sweep, timed on this host.
 Also reported: an 8B Llama Q4_K bs=1 decode token rate counting only its
-matmuls (32 x (QKV, O, gate, up, down) + lm_head), from the per-node times.
+matmuls (32 x (QKV, O, gate, up, down) + lm_head), from the per-node times;
+the q4_K prefill GEMM; paged-attention decode; dense
+FLASH_ATTN_EXT decode (32 sequences x 4096 keys) and a causal 512-token prefill.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -250,6 +252,42 @@ def main() -> int:
     del kc, vc
     torch.cuda.empty_cache()
 
+    # dense FLASH_ATTN_EXT decode: the same 32 sequences x 32 q / 8 kv heads x 128 with a
+    # per-sequence f16 cache of 4096 keys (ggml k/v [128, 4096, 8, 32]), one query each;
+    # and a causal 512-token prefill of one sequence (q [128, 512, 32, 1], mask [512, 512])
+    fa = {}
+    for name, nb, nq, L, causal in (("decode", 32, 1, 4096, False), ("prefill_causal", 1, 512, 512, True)):
+        fq = torch.randn((nb, heads, nq, hs), device="cuda", generator=gen, dtype=torch.float32)
+        fk = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
+        fv = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
+        fm = None
+        if causal:
+            fm = torch.full((nq, L), float("-inf"), device="cuda").triu(1 + L - nq).to(torch.float16)[None, None]
+            fm = fm.contiguous()
+        fo = torch.empty((nb, nq, heads, hs), device="cuda", dtype=torch.float32)
+        node = N.FlashAttnExt(fq, fk, fv, fm, fo, hs ** -0.5)
+        for _ in range(2):
+            node(fq, fk, fv, fm, fo, stream)
+        evs = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            node(fq, fk, fv, fm, fo, stream)
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        fms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        fbytes = nb * kvh * L * hs * 2 * 2 + 2 * nb * nq * heads * hs * 4 + (nq * L * 2 if causal else 0)
+        flops = 4.0 * nb * heads * nq * L * hs  # QK and PV over every key the kernel visits
+        fa[name] = {"batch": nb, "queries": nq, "keys": L, "heads": heads, "kv_heads": kvh, "head_size": hs,
+                    "causal_mask": causal, "bytes": fbytes, "us": round(fms * 1e3, 1),
+                    "gbs": round(fbytes / fms / 1e6, 1), "frac_of_hbm_peak": round(fbytes / fms / 1e6 / HBM_PEAK_GBS, 4),
+                    "tflops": round(flops / (fms * 1e-3) / 1e12, 1)}
+        log(f"  flash_attn_ext {name}: {fms * 1e3:8.1f} us  {fbytes / fms / 1e6:7.0f} GB/s  "
+            f"{flops / (fms * 1e-3) / 1e12:6.1f} TFLOP/s")
+        del fq, fk, fv, fm, fo, node
+    torch.cuda.empty_cache()
+
     # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
     # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -296,6 +334,7 @@ def main() -> int:
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
             "prefill_gemm_q4k": prefill,
             "paged_attention_decode": attention,
+            "flash_attn_ext": fa,
         },
         "roofline": {
             "bound": "hbm",

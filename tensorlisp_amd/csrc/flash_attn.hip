@@ -41,7 +41,7 @@
 namespace tlh {
 
 constexpr int FA_WAVES = 4;
-constexpr int FA_TARGET_WGS = 2048;  // workgroups a split launch aims for
+constexpr int FA_TARGET_WGS = 1024;  // workgroups a split launch aims for
 constexpr int FA_MIN_PART = 128;     // fewest keys per partition when split
 
 typedef _Float16 fa_half4 __attribute__((ext_vector_type(4)));
@@ -94,7 +94,8 @@ struct VGeom {
 struct FaArgs {
     const char *q, *k, *v, *mask;
     char *dst;
-    float *part;  // partials [nb][nh][nq][P][DV + 2] when P > 1
+    float *part;   // partials [nb][nh][nq][P][DV + 2] when P > 1
+    int2 *ranges;  // masked launches: live keys [lo, hi) of each mask row [mne3][mne2][nq]
     int64_t q_nb1, q_nb2, q_nb3;
     int64_t k_nb1, k_nb2, k_nb3;
     int64_t v_nb1, v_nb2, v_nb3;
@@ -136,8 +137,8 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
     const int hc = (blockIdx.x / a.QC) % a.HC;
     const int p = blockIdx.x / (a.QC * a.HC);
     const int hk = blockIdx.y, ib = blockIdx.z;
-    const int j0 = p * a.part_len;
-    const int j1 = min(a.L, j0 + a.part_len);
+    int j0 = p * a.part_len;
+    int j1 = min(a.L, j0 + a.part_len);
     const int nrows = min(a.qr, a.nq - qc * a.qr) * a.gc;  // live rows: a prefix of the tile
 
     // row c of the tile: query qc*qr + c/gc, head hk*G + hc*gc + c%gc
@@ -145,6 +146,18 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
     const int rr = rlive ? c : 0;
     const int iq = qc * a.qr + rr / a.gc;
     const int h = hk * a.G + hc * a.gc + rr % a.gc;
+    if constexpr (MASK) {
+        // keys outside every row's live range are -inf for the whole tile: skip them
+        int2 rg = a.ranges[((int64_t)(ib % a.m_ne3) * a.m_ne2 + h % a.m_ne2) * a.nq + iq];
+        if (!rlive) rg = make_int2(INT32_MAX, 0);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            rg.x = min(rg.x, __shfl_xor(rg.x, o, 64));
+            rg.y = max(rg.y, __shfl_xor(rg.y, o, 64));
+        }
+        j0 = max(j0, rg.x);
+        j1 = min(j1, rg.y);
+    }
 
     // Q^T operand (row c, dims of step st for group g), rounded to f16
     fa_half4 qb[KG::STEPS];
@@ -346,7 +359,8 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
 
 // Merge the partitions of one (batch, head, query) row: every partition was
 // written (an empty one as max -inf, sum 0). Each thread reads the maxima,
-// sums and its dims of up to 16 partitions in one round of loads.
+// sums and its dims of up to 16 partitions in one round of loads and folds
+// them into a running (max, sum, acc) rescaled online.
 template <int DV>
 __global__ void __launch_bounds__(256) k_flash_attn_reduce(const FaArgs a) {
     constexpr int CHUNK = 16;
@@ -355,33 +369,66 @@ __global__ void __launch_bounds__(256) k_flash_attn_reduce(const FaArgs a) {
     const float *base = a.part + (((int64_t)ib * a.nh + h) * a.nq + iq) * P * (DV + 2);
     float *out = (float *)(a.dst + h * a.d_nb1 + iq * a.d_nb2 + ib * a.d_nb3);
     for (int d = threadIdx.x; d < DV; d += blockDim.x) {
-        float M = -INFINITY;
-        for (int p0 = 0; p0 < P; p0 += CHUNK) {
-#pragma unroll
-            for (int i = 0; i < CHUNK; ++i)
-                if (p0 + i < P) M = fmaxf(M, base[(int64_t)(p0 + i) * (DV + 2)]);
-        }
-        float lsum = 0.0f, acc = 0.0f;
+        float M = -INFINITY, lsum = 0.0f, acc = 0.0f;
         for (int p0 = 0; p0 < P; p0 += CHUNK) {
             float m[CHUNK], l[CHUNK], v[CHUNK];
 #pragma unroll
             for (int i = 0; i < CHUNK; ++i) {
-                const int64_t o = (int64_t)(p0 + i < P ? p0 + i : 0) * (DV + 2);
+                const int64_t o = (int64_t)(p0 + i < P ? p0 + i : p0) * (DV + 2);
                 m[i] = base[o];
                 l[i] = base[o + 1];
                 v[i] = base[o + 2 + d];
             }
+            float cm = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) cm = fmaxf(cm, m[i]);  // repeats of p0 change nothing
+            const float Mn = fmaxf(M, cm);
+            if (Mn == -INFINITY) continue;
+            const float so = __expf(M - Mn);  // 0 while M is -inf (then lsum and acc are 0)
+            lsum *= so;
+            acc *= so;
 #pragma unroll
             for (int i = 0; i < CHUNK; ++i) {
-                if (p0 + i < P && m[i] != -INFINITY) {
-                    const float w = __expf(m[i] - M);
-                    lsum += w * l[i];
-                    acc += w * v[i];
-                }
+                const float w = p0 + i < P ? __expf(m[i] - Mn) : 0.0f;  // exp(-inf) = 0: empty partitions
+                lsum += w * l[i];
+                acc += w * v[i];
             }
+            M = Mn;
         }
         out[d] = acc * (lsum == 0.0f ? 0.0f : 1.0f / lsum);
     }
+}
+
+// Live key range [lo, hi) of each mask row (first and one past the last entry
+// that is not -inf; lo = L, hi = 0 when there is none), one wave per row of
+// [mne3][mne2][nq]: the attention kernels clip their key loops to the union
+// over their rows, so causal, padding and window masks skip whole key ranges.
+__global__ void __launch_bounds__(256) k_fa_mask_range(const FaArgs a, int rows) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int iq = r % a.nq, mh = (r / a.nq) % a.m_ne2, mb = r / (a.nq * a.m_ne2);
+    const uint16_t *mrow = (const uint16_t *)(a.mask + iq * a.m_nb1 + mh * a.m_nb2 + mb * a.m_nb3);
+    int lo = a.L, hi = 0;
+    for (int j0 = 0; j0 < a.L; j0 += 8 * 64) {
+        uint16_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = mrow[min(j0 + 64 * u + lane, a.L - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + 64 * u + lane;
+            if (j < a.L && v[u] != 0xfc00u) {  // f16 -inf
+                lo = min(lo, j);
+                hi = max(hi, j + 1);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        lo = min(lo, __shfl_xor(lo, o, 64));
+        hi = max(hi, __shfl_xor(hi, o, 64));
+    }
+    if (lane == 0) a.ranges[r] = make_int2(lo, hi);
 }
 
 // ------------------------------------------------------------------ host
@@ -422,17 +469,26 @@ static FaPlan fa_plan(int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t 
     return pl;
 }
 
-int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L) {
+static int64_t fa_partial_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L) {
     const FaPlan pl = fa_plan(nq, nh, nhkv, nb, L);
-    return pl.P > 1 ? nb * nh * nq * pl.P * (DV + 2) * (int64_t)sizeof(float) : 0;
+    const int64_t b = pl.P > 1 ? nb * nh * nq * pl.P * (DV + 2) * (int64_t)sizeof(float) : 0;
+    return (b + 255) / 256 * 256;
+}
+
+int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L,
+                                 int64_t mask_rows) {
+    return fa_partial_bytes(DV, nq, nh, nhkv, nb, L) + (L > 0 ? mask_rows * (int64_t)sizeof(int2) : 0);
 }
 
 template <int D, int DV>
 static void launch_fa(const FaArgs &a, bool mask, hipStream_t stream) {
     constexpr bool PIPE = D <= 128 && DV <= 128;  // two register sets fit
     const dim3 grid(a.QC * a.HC * a.P, a.nhkv, a.nb);
-    if (mask)
+    if (mask) {
+        const int rows = a.nq * a.m_ne2 * a.m_ne3;
+        hipLaunchKernelGGL(k_fa_mask_range, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows);
         hipLaunchKernelGGL((k_flash_attn<D, DV, true, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
+    }
     else
         hipLaunchKernelGGL((k_flash_attn<D, DV, false, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
     if (a.P > 1)
@@ -448,6 +504,7 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
     a.mask = (const char *)d.mask;
     a.dst = (char *)d.dst;
     a.part = (float *)d.scratch;
+    a.ranges = (int2 *)((char *)d.scratch + fa_partial_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L));
     a.q_nb1 = d.q_nb[1], a.q_nb2 = d.q_nb[2], a.q_nb3 = d.q_nb[3];
     a.k_nb1 = d.k_nb[1], a.k_nb2 = d.k_nb[2], a.k_nb3 = d.k_nb[3];
     a.v_nb1 = d.v_nb[1], a.v_nb2 = d.v_nb[2], a.v_nb3 = d.v_nb[3];
@@ -460,7 +517,7 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
     a.G = pl.G, a.gc = pl.gc, a.qr = pl.qr, a.HC = pl.HC, a.QC = pl.QC, a.P = pl.P, a.part_len = pl.part_len;
     a.scale = d.scale, a.max_bias = d.max_bias, a.m0 = d.m0, a.m1 = d.m1, a.softcap = d.softcap;
     a.nhl2 = d.n_head_log2;
-    const bool mask = d.mask != nullptr;
+    const bool mask = d.mask != nullptr && d.L > 0;
     switch (d.D * 1000 + d.DV) {
     case 32032: launch_fa<32, 32>(a, mask, stream); break;
     case 40040: launch_fa<40, 40>(a, mask, stream); break;

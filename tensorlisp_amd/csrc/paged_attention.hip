@@ -13,12 +13,12 @@
 //  * one workgroup (4 waves) per (sequence, kv head, 512-token partition);
 //    it serves every query head of the GQA group from one read of each KV
 //    page (vLLM v1 re-reads a kv head once per query head);
-//  * each wave streams whole pages with 16-byte loads: a page of keys for one
-//    kv head is head_size*block_size*2 contiguous bytes, lane l owns slot
-//    l % block_size and 8-dim chunks l/block_size + (64/block_size)*i;
-//    values are read the same way along [dim][slot];
-//  * q.k and p.v run on v_dot2_f32_f16 (f16 pairs into f32), the softmax is
-//    online (running max / sum per head, f32) so a page is touched once;
+//  * each wave streams 16-token tiles of its partition's pages (the key and
+//    value operands are 8-byte loads from the cache layouts, see the MFMA
+//    operand notes below);
+//  * q.k and p.v run on v_mfma_f32_16x16x16_f16 over 16-token tiles (below),
+//    the softmax is online (running max / sum per head, f32) so a page is
+//    touched once;
 //  * waves merge their (max, sum, acc) through LDS; partitions are merged by
 //    a second kernel (flash-decoding) into the f16 output.
 #include "kernels.hpp"
@@ -27,16 +27,6 @@ namespace tlh {
 
 constexpr int PA_PART = 512;  // tokens per partition (a multiple of every block size)
 constexpr int PA_WAVES = 4;
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-    return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
-}
 
 // Scratch per (seq, head, partition): max, sum, acc[HS] (f32).
 template <int HS>
@@ -233,8 +223,8 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
 
 // Merge the partitions of one (sequence, head) and write f16 output. Each
 // thread reads the maxima, sums and its dims of up to 16 partitions in one
-// round of independent loads and forms the weights itself; longer contexts
-// take further rounds.
+// round of independent loads and folds them into a running (max, sum, acc)
+// rescaled online; longer contexts take further rounds.
 template <int HS>
 __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, const float *__restrict__ scratch,
                                                            const int32_t *__restrict__ lens, int num_heads, int P) {
@@ -245,30 +235,31 @@ __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict_
     const int np = min(P, L > 0 ? (L + PA_PART - 1) / PA_PART : 1);
     const float *base = scratch + (int64_t)(seq * num_heads + head) * P * (HS + 2);
     for (int d = threadIdx.x; d < HS; d += blockDim.x) {
-        float M = -INFINITY;
-        for (int p0 = 0; p0 < np; p0 += CHUNK) {
-#pragma unroll
-            for (int i = 0; i < CHUNK; ++i)
-                if (p0 + i < np) M = fmaxf(M, base[(int64_t)(p0 + i) * (HS + 2)]);
-        }
-        float lsum = 0.0f, a = 0.0f;
+        float M = -INFINITY, lsum = 0.0f, a = 0.0f;
         for (int p0 = 0; p0 < np; p0 += CHUNK) {
             float m[CHUNK], l[CHUNK], v[CHUNK];
 #pragma unroll
             for (int i = 0; i < CHUNK; ++i) {
-                const int64_t o = (int64_t)(p0 + i < np ? p0 + i : 0) * (HS + 2);
+                const int64_t o = (int64_t)(p0 + i < np ? p0 + i : p0) * (HS + 2);
                 m[i] = base[o];
                 l[i] = base[o + 1];
                 v[i] = base[o + 2 + d];
             }
+            float cm = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < CHUNK; ++i) cm = fmaxf(cm, m[i]);  // repeats of p0 change nothing
+            const float Mn = fmaxf(M, cm);
+            if (Mn == -INFINITY) continue;
+            const float so = __expf(M - Mn);  // 0 while M is -inf (then lsum and a are 0)
+            lsum *= so;
+            a *= so;
 #pragma unroll
             for (int i = 0; i < CHUNK; ++i) {
-                if (p0 + i < np && m[i] != -INFINITY) {
-                    const float w = __expf(m[i] - M);
-                    lsum += w * l[i];
-                    a += w * v[i];
-                }
+                const float w = p0 + i < np ? __expf(m[i] - Mn) : 0.0f;
+                lsum += w * l[i];
+                a += w * v[i];
             }
+            M = Mn;
         }
         out[((int64_t)seq * num_heads + head) * HS + d] = f2h(a * (1.0f / (lsum + 1e-6f)));
     }

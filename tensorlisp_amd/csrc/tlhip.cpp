@@ -460,9 +460,11 @@ tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cac
 tlh_status tlh_flash_attn_ext_scratch_bytes(const tlh_op *op, size_t *bytes) {
     if (!bytes) return set_error(TLH_INVALID, "flash_attn_ext_scratch_bytes: null pointer");
     FlashAttnDesc d;
-    const tlh_status st = check_flash_attn(op, false, d);
+    // a mask descriptor in slot 3 (OpBlob leaves it zeroed without a mask)
+    const bool has_mask = op && op->t[3].ne[0] > 0;
+    const tlh_status st = check_flash_attn(op, has_mask, d);
     if (st != TLH_OK) return st;
-    *bytes = (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L);
+    *bytes = (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L, has_mask ? d.nq * d.m_ne2 * d.m_ne3 : 0);
     return TLH_OK;
 }
 
@@ -478,10 +480,11 @@ tlh_status tlh_flash_attn_ext(const tlh_op *op, const void *q, const void *k, co
         return set_error(TLH_UNSUPPORTED, "flash_attn_ext: K/V must be 16-byte aligned");
     if (((uintptr_t)q | (uintptr_t)dst) & 3 || ((uintptr_t)mask & 1))
         return set_error(TLH_INVALID, "flash_attn_ext: misaligned q, dst or mask");
-    const size_t need = (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L);
+    const size_t need =
+        (size_t)flash_attn_scratch_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L, mask ? d.nq * d.m_ne2 * d.m_ne3 : 0);
     if (need > 0 && (!scratch || scratch_bytes < need))
         return set_error(TLH_INVALID, "flash_attn_ext: scratch of %zu bytes, need %zu", scratch_bytes, need);
-    if (need > 0 && ((uintptr_t)scratch & 3)) return set_error(TLH_INVALID, "flash_attn_ext: misaligned scratch");
+    if (need > 0 && ((uintptr_t)scratch & 7)) return set_error(TLH_INVALID, "flash_attn_ext: misaligned scratch");
     d.q = q, d.k = k, d.v = v, d.mask = mask, d.dst = dst, d.scratch = scratch;
     return launch_flash_attn(d, (hipStream_t)stream);
 }

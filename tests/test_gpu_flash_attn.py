@@ -226,3 +226,27 @@ def test_refusals(gpu):
     k3 = torch.zeros((1, 3, 10, 64), device="cuda", dtype=torch.float16)
     with pytest.raises(N.TlhError, match="UNSUPPORTED.*inconsistent"):
         N.flash_attn_ext(q, k3, k3, None, 1.0)
+
+
+def test_window_and_causal_masks_clip_key_ranges(gpu):
+    """Per-head sliding windows and causal masks: each row's live keys are a window
+    that starts past 0 and ends before L, different across the rows of a tile and
+    across heads (mask per head, mne2 = nh), so the kernels' key loops are clipped
+    to per-tile ranges that do not line up with 16-key tiles or partitions."""
+    nb, nh, nhkv, nq, L, D = 2, 8, 2, 100, 700, 64
+    q = synth.normal(101, (nb, nh, nq, D))
+    k = synth.f16_bits(synth.normal(102, (nb, nhkv, L, D)))
+    v = synth.f16_bits(synth.normal(103, (nb, nhkv, L, D)))
+    pos = np.arange(nq)[:, None] + (L - nq)  # query i sits at position L - nq + i
+    j = np.arange(L)[None, :]
+    mf = np.full((nb, nh, nq, L), -np.inf, np.float32)
+    for h in range(nh):
+        w = 13 + 29 * h  # window per head
+        mf[:, h] = np.where((j <= pos) & (j > pos - w), 0.0, -np.inf)
+    mf[1, :, :, :350] = -np.inf  # batch 1: also a padding prefix
+    m = mf.astype(np.float16).view(np.uint16)
+    check(run_gpu(q, k, v, m, 0.125), q, k, v, m, 0.125, what="windows")
+    # causal decode-style rows: one query per batch at the last position, split path
+    q1 = np.ascontiguousarray(q[:, :, -1:])
+    m1 = np.ascontiguousarray(m[:, :, -1:])
+    check(run_gpu(q1, k, v, m1, 0.125), q1, k, v, m1, 0.125, what="windows, one query")
