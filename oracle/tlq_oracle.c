@@ -11,14 +11,16 @@
 // ---------------------------------------------------------------- geometry
 // ggml-common.h:194-198 (q4_0: f16 d + 16 nibble bytes), :251-255 (q8_0: f16 d
 // + 32 int8), :325-337 (q4_K: f16 d, f16 dmin, 12 packed 6-bit scale/min
-// bytes, 128 nibble bytes), :370-375 (q8_K: f32 d, 256 int8, 16 int16 sums).
-enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q8_K_B = 292 };
+// bytes, 128 nibble bytes), :362-368 (q6_K: 128 low-nibble bytes, 64 bytes of
+// 2-bit high parts, 16 int8 scales, f16 d), :370-375 (q8_K: f32 d, 256 int8,
+// 16 int16 sums).
+enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q6_K_B = 210, Q8_K_B = 292 };
 
 int64_t tlq_block_elems(int type) {
     switch (type) {
     case TLQ_F32: case TLQ_F16: return 1;
     case TLQ_Q4_0: case TLQ_Q8_0: return QK32;
-    case TLQ_Q4_K: case TLQ_Q8_K: return QKK;
+    case TLQ_Q4_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
     default: return 0;
     }
 }
@@ -30,6 +32,7 @@ int64_t tlq_block_bytes(int type) {
     case TLQ_Q4_0: return Q4_0_B;
     case TLQ_Q8_0: return Q8_0_B;
     case TLQ_Q4_K: return Q4_K_B;
+    case TLQ_Q6_K: return Q6_K_B;
     case TLQ_Q8_K: return Q8_K_B;
     default: return 0;
     }
@@ -43,7 +46,7 @@ int64_t tlq_row_bytes(int type, int64_t k) {
 int tlq_vec_dot_type(int wtype) {
     switch (wtype) {
     case TLQ_Q4_0: case TLQ_Q8_0: return TLQ_Q8_0;
-    case TLQ_Q4_K: return TLQ_Q8_K;
+    case TLQ_Q4_K: case TLQ_Q6_K: return TLQ_Q8_K;
     default: return -1;
     }
 }
@@ -370,6 +373,25 @@ void tlq_dequantize_row_q4_K(const void *vx, float *y, int64_t k) {
     }
 }
 
+// ggml-quants.c:1939-1968: per 128-element half, element 32q + l has its low
+// 4 bits in ql[l + 32 (q & 1)] (high nibble for q >= 2) and its high 2 bits
+// in qh[l] at bit 2q; y = (d * scale) * (code - 32), scale per 16 elements.
+static int q6k_code(const uint8_t *blk, int i) {
+    const int h = i / 128, e = i % 128, q = e / 32, l = e % 32;
+    const uint8_t lo = blk[64 * h + l + 32 * (q & 1)];
+    const uint8_t hi = blk[128 + 32 * h + l];
+    return (int)(((q >= 2 ? lo >> 4 : lo & 0x0f) | (((hi >> (2 * q)) & 3) << 4))) - 32;
+}
+
+void tlq_dequantize_row_q6_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q6_K_B) {
+        const float d = tlq_fp16_to_fp32(rd16(x + 208));
+        const int8_t *sc = (const int8_t *)(x + 192);
+        for (int i = 0; i < QKK; ++i) *y++ = d * sc[i / 16] * q6k_code(x, i);
+    }
+}
+
 void tlq_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
     const uint8_t *x = (const uint8_t *)vx;
     for (int64_t b = 0; b < k / QKK; ++b, x += Q8_K_B, y += QKK) {
@@ -383,6 +405,7 @@ int tlq_dequantize_row(int type, const void *x, float *y, int64_t k) {
     case TLQ_Q4_0: tlq_dequantize_row_q4_0(x, y, k); return 0;
     case TLQ_Q8_0: tlq_dequantize_row_q8_0(x, y, k); return 0;
     case TLQ_Q4_K: tlq_dequantize_row_q4_K(x, y, k); return 0;
+    case TLQ_Q6_K: tlq_dequantize_row_q6_K(x, y, k); return 0;
     case TLQ_Q8_K: tlq_dequantize_row_q8_K(x, y, k); return 0;
     default: return -1;
     }
@@ -476,6 +499,30 @@ float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *vx, const void *vy) {
     return acc;
 }
 
+// ggml-cpu/quants.c:851-904. Per super-block: codes in element order, eight
+// int32 lane accumulators (element e of each 16-element sub-block feeds lane
+// e % 8) of scale_j * (code * q8); float part sums[lane] += (dx * dy) * lane,
+// then sumf = sums[0] + ... + sums[7].
+float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float sums[8] = {0};
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q6_K_B, y += Q8_K_B) {
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        const int8_t *sc = (const int8_t *)(x + 192);
+        int32_t aux32[8] = {0};
+        for (int j = 0; j < 16; ++j)
+            for (int l = 0; l < 16; ++l) {
+                const int e = 16 * j + l;
+                aux32[l % 8] += sc[j] * (int16_t)(q6k_code(x, e) * q8[e]);
+            }
+        const float d = tlq_fp16_to_fp32(rd16(x + 208)) * rdf32(y);
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    }
+    float sumf = 0;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
 // -------------------------------------------------------------- mul_mat
 typedef float (*dot_fn)(int64_t, const void *, const void *);
 
@@ -503,6 +550,7 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     case TLQ_Q4_0: dot = tlq_vec_dot_q4_0_q8_0; break;
     case TLQ_Q8_0: dot = tlq_vec_dot_q8_0_q8_0; break;
     case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
+    case TLQ_Q6_K: dot = tlq_vec_dot_q6_K_q8_K; break;
     default: return -1;
     }
     const int at = tlq_vec_dot_type(wtype);

@@ -26,6 +26,7 @@ enum {
     TLQ_Q4_0 = 2,
     TLQ_Q8_0 = 8,
     TLQ_Q4_K = 12,
+    TLQ_Q6_K = 14,
     TLQ_Q8_K = 15,
 };
 
@@ -64,6 +65,7 @@ int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k);
 void tlq_dequantize_row_q4_0(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q8_0(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q4_K(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q8_K(const void *x, float *y, int64_t k);
 int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
 
@@ -73,6 +75,7 @@ int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
 float tlq_vec_dot_q4_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q8_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *x, const void *y);
 
 // Exact integer parts of one block product (for pinning GPU partial sums):
 // q4_K: *sum_q = sum_s sc_s * sum_{e in s} q4_e*q8_e, *sum_m = sum_s m_s * sum_{e in s} q8_e.

@@ -11,28 +11,33 @@ namespace tlh {
 
 // ----------------------------------------------------------- block formats
 // vendor/ggml/src/ggml-common.h:194-198 (q4_0), :251-255 (q8_0), :325-337
-// (q4_K), :370-375 (q8_K). Byte sizes per block and elements per block.
+// (q4_K), :362-368 (q6_K), :370-375 (q8_K). Byte sizes per block and
+// elements per block.
 constexpr int QK = 32;    // q4_0 / q8_0 block
 constexpr int QKK = 256;  // k-quant super-block
 constexpr int Q4_0_BYTES = 18;
 constexpr int Q8_0_BYTES = 34;
 constexpr int Q4_K_BYTES = 144;
+constexpr int Q6_K_BYTES = 210;  // ql[128] (low 4 bits), qh[64] (high 2 bits), int8 scales[16], f16 d
 constexpr int Q8_K_BYTES = 292;
 
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q8_K) ? QKK : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0) ? QK : 1;
+    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q6_K || t == TLH_TYPE_Q8_K) ? QKK
+           : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0)                      ? QK
+                                                                             : 1;
 }
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == TLH_TYPE_Q4_0   ? Q4_0_BYTES
            : t == TLH_TYPE_Q8_0 ? Q8_0_BYTES
            : t == TLH_TYPE_Q4_K ? Q4_K_BYTES
+           : t == TLH_TYPE_Q6_K ? Q6_K_BYTES
            : t == TLH_TYPE_Q8_K ? Q8_K_BYTES
            : t == TLH_TYPE_F16  ? 2
                                 : 4;
 }
 // vec_dot_type on x86 (vendor/ggml/src/ggml-cpu/ggml-cpu.c:239-319).
 __host__ __device__ constexpr int vec_dot_type(int wtype) {
-    return wtype == TLH_TYPE_Q4_K ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
+    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
 }
 
 // ---------------------------------------------------------- conversions

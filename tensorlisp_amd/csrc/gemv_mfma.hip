@@ -85,10 +85,18 @@ __device__ __forceinline__ uint2 lds_u64(const uint32_t *base, uint32_t off) {
     return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(a2, a1, sh));
 }
 
-// Bytes of one row per unit.
+// Bytes of one row per unit (the stride between units).
 template <int WT> constexpr int unit_bytes() {
-    return WT == TLH_TYPE_Q4_K ? Q4_K_BYTES : WT == TLH_TYPE_Q4_0 ? 8 * Q4_0_BYTES : 8 * Q8_0_BYTES;
+    return WT == TLH_TYPE_Q4_K   ? Q4_K_BYTES
+           : WT == TLH_TYPE_Q6_K ? Q6_K_BYTES
+           : WT == TLH_TYPE_Q4_0 ? 8 * Q4_0_BYTES
+                                 : 8 * Q8_0_BYTES;
 }
+// Bytes of a unit staged through LDS (a multiple of 16): all of it, but for
+// q6_K its first 208 (ql, qh, scales; d, the last 2 bytes, is loaded apart).
+template <int WT> constexpr int staged_bytes() { return WT == TLH_TYPE_Q6_K ? 208 : unit_bytes<WT>(); }
+// Types whose unit is one k-quant super-block (one activation scale slot).
+template <int WT> constexpr bool kquant() { return WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q6_K; }
 
 // One lane's weight data of one unit in operand form: q4_K the super-block
 // header and bytes 8g..8g+7 of each 32-byte chunk; q8_0 / q4_0 per block the
@@ -108,6 +116,23 @@ template <> struct UnitW<TLH_TYPE_Q4_K> {
         hdr = *(const uint4 *)blk;
 #pragma unroll
         for (int c = 0; c < 4; ++c) q[c] = *(const uint2 *)(blk + 16 + 32 * c + 8 * g);
+    }
+};
+
+// q6_K from the staged LDS copy: lane g's operand bytes of 32-element step m
+// (elements 32m + 8g..+7; half h = m / 4, m' = m % 4, e = 32m' + 8g) are the
+// 8 ql bytes at 64h + 32 (m' & 1) + 8g (low nibbles for m' < 2, else high)
+// and the 8 qh bytes at 128 + 32h + 8g (2-bit fields 2m'); all 16 scales.
+template <> struct UnitW<TLH_TYPE_Q6_K> {
+    uint2 ql[4];  // [2h + (m' & 1)]
+    uint2 qh[2];  // [h]
+    uint4 sc;
+    __device__ __forceinline__ void load_lds(const uint8_t *blk, int g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ql[i] = *(const uint2 *)(blk + 32 * i + 8 * g);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) qh[h] = *(const uint2 *)(blk + 128 + 32 * h + 8 * g);
+        sc = *(const uint4 *)(blk + 192);
     }
 };
 
@@ -152,6 +177,46 @@ __device__ __forceinline__ void block_mma(long A, long B, uint16_t dwh, const fl
         else
             y[r] += (float)Sb[r] * (dw * d8r[r]);  // quants.c:475
     }
+}
+
+// q6_K super-block (vec_dot_q6_K_q8_K_generic, ggml-cpu/quants.c:851-904):
+// 16 sub-blocks of 16 with int8 scales. A 32-element MFMA step holds two
+// sub-blocks (lanes g < 2 the first, g >= 2 the second), so each step runs
+// twice with the other sub-block's lanes of the weight operand zeroed; codes
+// are (ql | qh << 4) - 32 as signed bytes. S = sum scale_s * S_s in int32,
+// scaled by d * d8 in f32 (the CPU splits the int32 sums in 8 lanes before its
+// f32 products; the difference is f32 rounding). dq: the unit's f16 d.
+__device__ __forceinline__ void unit_mma_q6k(const UnitW<TLH_TYPE_Q6_K> &w, uint32_t dq, const long (&A)[8],
+                                             const float *sdu, int g, float (&y)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    v4i S = {0, 0, 0, 0};
+    const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int h = m >> 2, mp = m & 3;
+        const uint2 l = w.ql[2 * h + (mp & 1)], hq = w.qh[h];
+        const int nsh = mp >= 2 ? 4 : 0, hsh = 2 * mp;
+        uint32_t b[2];
+        const uint32_t lv[2] = {l.x, l.y}, hv[2] = {hq.x, hq.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u = ((lv[i] >> nsh) & 0x0f0f0f0fu) | (((hv[i] >> hsh) & 0x03030303u) << 4);
+            b[i] = ((u | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // u - 32 per byte, no borrows
+        }
+        const long B = pack2(b[0], b[1]);
+        const v4i S0 = mfma_i8(A[m], g < 2 ? B : 0, zero);   // sub-block 2m
+        const v4i S1 = mfma_i8(A[m], g >= 2 ? B : 0, zero);  // sub-block 2m + 1
+        const uint32_t sw = scw[m >> 1];
+        const int s0 = (int)(int8_t)((sw >> (16 * (m & 1))) & 0xff);
+        const int s1 = (int)(int8_t)((sw >> (16 * (m & 1) + 8)) & 0xff);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[r] += __mul24(s0, S0[r]) + __mul24(s1, S1[r]);  // |S_s| < 2^16
+    }
+    const float d = h2f((uint16_t)dq);
+    const float4 d8 = *(const float4 *)(sdu + 4 * g);
+    const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r];
 }
 
 // y[r] += the unit's contribution to output (column 4g + r, the lane's weight
@@ -206,11 +271,12 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
 // Staging of one row group's slice: lane l loads pieces 64i + l (16 bytes
 // each) of the 16 rows x KS units, row-major; NL loads per lane.
 template <int WT, int KS> struct Stage {
-    static constexpr int RB = KS * unit_bytes<WT>();  // slice bytes per row (a multiple of 16)
-    static constexpr int PR = RB / 16;                 // pieces per row
+    static constexpr int RB = KS * staged_bytes<WT>();  // slice bytes per row (a multiple of 16)
+    static constexpr int PR = RB / 16;                   // pieces per row
     static constexpr int NL = (16 * PR + 63) / 64;
-    static constexpr int BUF = NL * 64 * 16 + 16;      // LDS bytes per wave (with read slack)
+    static constexpr int BUF = NL * 64 * 16 + 16;        // LDS bytes per wave (with read slack)
     uint4 v[NL];
+    uint32_t dq;  // q6_K: the lane's row's d (KS = 1)
 };
 
 // Direct loads of KS units (prefetch set of the unstaged kernel). Units
@@ -227,8 +293,9 @@ template <int WT, int KS, bool STAGED>
 __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share) {
     extern __shared__ __attribute__((aligned(16))) char sk_lds[];
     constexpr int AT = vec_dot_type(WT);
-    constexpr bool KQ = WT == TLH_TYPE_Q4_K;
+    constexpr bool KQ = kquant<WT>();
     constexpr int UB = unit_bytes<WT>();
+    static_assert(WT != TLH_TYPE_Q6_K || KS == 1, "q6_K staging keeps one d per lane");
     using St = Stage<WT, KS>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
@@ -274,10 +341,14 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         const int p = 64 * i + lane;
         const int pc = p < 16 * St::PR ? p : 0;
         pr[i] = pc / St::PR;
-        const int64_t off = u0 * UB + 16 * (pc - pr[i] * St::PR);
+        const int64_t off = u0 * UB + 16 * (pc - pr[i] * St::PR);  // (KS = 1 for the staged q6_K bytes)
         pofs[i] = pr[i] * a.w_nb1 + (off + 16 <= row_bytes ? off : 0);
     }
     const uint8_t *wlast = W + (a.M - 1) * a.w_nb1;
+    auto wrow_of = [&](int64_t grp) {
+        const int64_t m = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;  // clamp: loads in bounds
+        return W + m * a.w_nb1;
+    };
     auto stage_load = [&](St &s, int64_t grp) {
         const uint8_t *gb = W + grp * 16 * a.w_nb1;  // wave-uniform
         const int rows_left = (int)(a.M - grp * 16);
@@ -286,10 +357,10 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const uint8_t *q = pr[i] < rows_left ? gb + pofs[i] : wlast + (pofs[i] - pr[i] * a.w_nb1);
             s.v[i] = ldu<uint4>(q);
         }
-    };
-    auto wrow_of = [&](int64_t grp) {
-        const int64_t m = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;  // clamp: loads in bounds
-        return W + m * a.w_nb1;
+        if constexpr (WT == TLH_TYPE_Q6_K) {
+            const int64_t ud = u0 < u_end ? u0 : u_begin;  // a unit of the row (products past u_end are skipped)
+            s.dq = ldu<uint16_t>(wrow_of(grp) + ud * UB + 208);
+        }
     };
 
     // the first row group's weights go out before the activations are read
@@ -377,13 +448,17 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         return KQ ? 8 : (int)(v < 0 ? 0 : v > 8 ? 8 : v);
     };
     // multiply one row group from the wave's LDS buffer
-    auto process_staged = [&](int64_t grp, int parity) {
+    auto process_staged = [&](int64_t grp, int parity, uint32_t dq) {
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
-            const uint32_t ub = (uint32_t)(wr * St::RB + t * UB);  // byte offset of the row's unit in wbuf
-            if constexpr (KQ) {
+            const uint32_t ub = (uint32_t)(wr * St::RB + t * staged_bytes<WT>());  // the row's unit in wbuf
+            if constexpr (WT == TLH_TYPE_Q6_K) {
+                UnitW<WT> w;
+                w.load_lds(wbuf + ub, g);
+                unit_mma_q6k(w, dq, A[t], unit_slots(t), g, y);
+            } else if constexpr (KQ) {
                 UnitW<WT> w;
                 w.load_lds(wbuf + ub, g);
                 unit_mma<WT>(w, A[t], unit_slots(t), g, 8, y);
@@ -420,7 +495,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
-            unit_mma<WT>(d.u[t], A[t], unit_slots(t), g, unit_nvalid(t), y);
+            if constexpr (WT != TLH_TYPE_Q6_K) unit_mma<WT>(d.u[t], A[t], unit_slots(t), g, unit_nvalid(t), y);
         }
         finish(y, grp, parity);
     };
@@ -437,8 +512,9 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const int64_t r1 = rg + gridDim.x;
 #pragma unroll
             for (int i = 0; i < St::NL; ++i) *(uint4 *)(wbuf + 1024 * i + 16 * lane) = st.v[i];
+            const uint32_t dq = st.dq;  // this group's (read with its weight bytes above)
             stage_load(st, r1 < groups ? r1 : rg);
-            process_staged(rg, it & 1);
+            process_staged(rg, it & 1, dq);
             rg = r1;
         }
     } else {
@@ -499,7 +575,7 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     if (chunks > 1 && !a.part) return set_error(TLH_INVALID, "gemv_mfma: K=%lld needs a partials buffer", (long long)a.K);
     // at least 4 waves: the first 256 threads each own one of a row group's outputs
     const int nw = (int)((share + KS - 1) / KS) > 4 ? (int)((share + KS - 1) / KS) : 4;
-    const size_t lds = (size_t)2 * nw * 64 * 16 + (size_t)(WT == TLH_TYPE_Q4_K ? share : 8 * share) * SK_COLS * 4 +
+    const size_t lds = (size_t)2 * nw * 64 * 16 + (size_t)(kquant<WT>() ? share : 8 * share) * SK_COLS * 4 +
                        (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0);
     static int cached_nw = -1, blocks_per_cu = 1, cus = 0;
     if (cached_nw != nw) {
@@ -526,7 +602,7 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
 }
 
 template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool staged, hipStream_t stream) {
-    if constexpr (WT == TLH_TYPE_Q4_K) {
+    if constexpr (kquant<WT>()) {
         return launch_sk<WT, true>(a, stream);  // K is a multiple of 256
     } else {
         return staged ? launch_sk<WT, true>(a, stream) : launch_sk<WT, false>(a, stream);
@@ -541,6 +617,7 @@ tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     case TLH_TYPE_Q4_0: return launch_sk_wt<TLH_TYPE_Q4_0>(a, staged, stream);
     case TLH_TYPE_Q8_0: return launch_sk_wt<TLH_TYPE_Q8_0>(a, staged, stream);
     case TLH_TYPE_Q4_K: return launch_sk_wt<TLH_TYPE_Q4_K>(a, staged, stream);
+    case TLH_TYPE_Q6_K: return launch_sk_wt<TLH_TYPE_Q6_K>(a, staged, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: weight type %d", a.wtype);
     }
 }

@@ -39,23 +39,39 @@ __device__ __forceinline__ uint4 ldu16(const void *p) {
     return v;
 }
 
-// One lane's 64 activation codes with their scales and 32-element code sums.
-// q8_0: d0/d1 are the two blocks' (f16-rounded) scales; q8_K: d0 is the
-// super-block scale.
+// One lane's 64 activation codes with their scales and code sums.
+// q8_0: d0/d1 are the two blocks' (f16-rounded) scales, s0/s1 their sums;
+// q8_K: d0 is the super-block scale, s0/s1 the sums of the two 32-element
+// halves and b[0..3] of the four 16-element quarters.
 struct AUnit {
     int q[16];
     float d0, d1;
     int s0, s1;
+    int b[4];
 };
 
-template <int AT>
+// The elements of unit u: two runs of 32 at e0 and e0 + off1. Contiguous 64
+// for every type but q6_K, whose 128-element halves keep element e's low 4
+// bits in ql[e % 64] (high nibble from e = 64) and its high 2 bits in
+// qh[e % 32]: there a unit is the 32-element runs at 32c and 64 + 32c of half
+// h, which share ql bytes 32c..32c+31 and all of qh[0..31], so a lane loads
+// 64 weight bytes for 64 elements (u = 4 * super-block + 2h + c).
+template <int WT> __device__ __forceinline__ int64_t unit_e0(int64_t u) {
+    if constexpr (WT == TLH_TYPE_Q6_K) return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * (u & 1);
+    return 64 * u;
+}
+template <int WT> constexpr int unit_off1() { return WT == TLH_TYPE_Q6_K ? 64 : 32; }
+
+template <int AT, int WT>
 __device__ __forceinline__ void quantize_unit(const float *xr, int64_t u, bool valid, AUnit &o) {
 #pragma clang fp contract(off)
+    const int64_t e0 = unit_e0<WT>(u);
+    constexpr int OFF1 = unit_off1<WT>();
     float v[64];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (valid) f = *(const float4 *)(xr + 64 * u + 4 * i);
+        if (valid) f = *(const float4 *)(xr + e0 + (i < 8 ? 4 * i : OFF1 + 4 * (i - 8)));
         v[4 * i] = f.x;
         v[4 * i + 1] = f.y;
         v[4 * i + 2] = f.z;
@@ -91,17 +107,18 @@ __device__ __forceinline__ void quantize_unit(const float *xr, int64_t u, bool v
         }
     } else {
         // signed value of largest magnitude in the 256-element super-block,
-        // first index on ties: in-lane over 64, then across the 4 lanes
+        // first index on ties: in-lane over 64 (in element order), then across
+        // the 4 lanes
         float ba = 0.0f, bv = 0.0f;
         int bi = 1 << 30;
-        const int base = 64 * (int)(u & 3);
+        const int base = (int)(e0 & 255);
 #pragma unroll
         for (int i = 0; i < 64; ++i) {
             const float a = fabsf(v[i]);
             if (a > ba) {
                 ba = a;
                 bv = v[i];
-                bi = base + i;
+                bi = base + (i < 32 ? i : OFF1 + i - 32);
             }
         }
 #pragma unroll
@@ -120,7 +137,7 @@ __device__ __forceinline__ void quantize_unit(const float *xr, int64_t u, bool v
             iscale = -127.0f / bv;
             d = 1.0f / iscale;
         }
-        int s[2] = {0, 0};
+        int s[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int w = 0; w < 16; ++w) {
             uint32_t packed = 0;
@@ -132,46 +149,55 @@ __device__ __forceinline__ void quantize_unit(const float *xr, int64_t u, bool v
                     c = c > 127 ? 127 : c;
                 }
                 packed |= (uint32_t)(uint8_t)(int8_t)c << (8 * i);
-                s[w / 8] += c;
+                s[w / 4] += c;
             }
             o.q[w] = (int)packed;
         }
         o.d0 = d;
         o.d1 = 0.0f;
-        o.s0 = s[0];
-        o.s1 = s[1];
+        o.s0 = s[0] + s[1];
+        o.s1 = s[2] + s[3];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o.b[k] = s[k];
     }
 }
 
-template <int AT>
+// Lanes past K read unit 0 (in bounds) and keep zeros: branch-free, so the
+// unit stays in registers.
+template <int AT, int WT>
 __device__ __forceinline__ void load_unit(const ActView g, int64_t arow, int64_t K, int64_t u, bool valid, AUnit &o) {
-    if (!valid) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o.q[i] = 0;
-        o.d0 = o.d1 = 0.0f;
-        o.s0 = o.s1 = 0;
-        return;
-    }
-    const int8_t *qs = g.qs + arow * K + 64 * u;
+    const int64_t uc = valid ? u : 0;
+    const int64_t e0 = unit_e0<WT>(uc);
+    const int8_t *qs = g.qs + arow * K + e0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int4 t = *(const int4 *)(qs + 16 * i);
-        o.q[4 * i] = t.x;
-        o.q[4 * i + 1] = t.y;
-        o.q[4 * i + 2] = t.z;
-        o.q[4 * i + 3] = t.w;
+        const int4 t = *(const int4 *)(qs + (i < 2 ? 16 * i : unit_off1<WT>() + 16 * (i - 2)));
+        o.q[4 * i] = valid ? t.x : 0;
+        o.q[4 * i + 1] = valid ? t.y : 0;
+        o.q[4 * i + 2] = valid ? t.z : 0;
+        o.q[4 * i + 3] = valid ? t.w : 0;
     }
     if constexpr (AT == TLH_TYPE_Q8_0) {
-        o.d0 = g.d[arow * (K / 32) + 2 * u];
-        o.d1 = g.d[arow * (K / 32) + 2 * u + 1];
-        o.s0 = g.sum32[arow * (K / 32) + 2 * u];
-        o.s1 = g.sum32[arow * (K / 32) + 2 * u + 1];
+        const float d0 = g.d[arow * (K / 32) + 2 * uc], d1 = g.d[arow * (K / 32) + 2 * uc + 1];
+        const int s0 = g.sum32[arow * (K / 32) + 2 * uc], s1 = g.sum32[arow * (K / 32) + 2 * uc + 1];
+        o.d0 = valid ? d0 : 0.0f;
+        o.d1 = valid ? d1 : 0.0f;
+        o.s0 = valid ? s0 : 0;
+        o.s1 = valid ? s1 : 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o.b[k] = 0;
     } else {
-        o.d0 = g.d[arow * (K / QKK) + u / 4];
+        const float d0 = g.d[arow * (K / QKK) + uc / 4];
+        o.d0 = valid ? d0 : 0.0f;
         o.d1 = 0.0f;
-        const int16_t *b = g.bsums + arow * (K / 16) + 4 * u;
-        o.s0 = (int)b[0] + (int)b[1];
-        o.s1 = (int)b[2] + (int)b[3];
+        const int16_t *b = g.bsums + arow * (K / 16) + e0 / 16;
+        const int off = unit_off1<WT>() / 16;  // quarters 2 and 3 start this many bsums further
+        o.b[0] = valid ? b[0] : 0;
+        o.b[1] = valid ? b[1] : 0;
+        o.b[2] = valid ? b[off] : 0;
+        o.b[3] = valid ? b[off + 1] : 0;
+        o.s0 = o.b[0] + o.b[1];
+        o.s1 = o.b[2] + o.b[3];
     }
 }
 
@@ -249,6 +275,67 @@ template <int R> struct WRegs<TLH_TYPE_Q4_K, R> {
                 const int S = sclo * dl + schi * dh;
                 const int Mn = mnlo * act[n].s0 + mnhi * act[n].s1;
                 acc[r][n] += (d * act[n].d0) * (float)S - (dmin * act[n].d0) * (float)Mn;
+            }
+        }
+    }
+};
+
+// q6_K (vec_dot_q6_K_q8_K_generic, ggml-cpu/quants.c:851-904): the lane's 32
+// ql bytes (low nibbles: its first run, high nibbles: its second), the half's
+// 32 qh bytes (2-bit fields 2c and 4 + 2c), the 8 scales of the half and d.
+// codes = ql | qh << 4 in 0..63; per 16-element sub-block k
+// sum (code - 32) * q8 = dot(code, q8) - 32 * bsum_k, then sum scale_k * that
+// in int32 and one f32 scaling by d * d8 as the CPU does per super-block.
+template <int R> struct WRegs<TLH_TYPE_Q6_K, R> {
+    uint4 l0[R], l1[R], h0[R], h1[R];
+    uint2 sc[R];
+    uint32_t dq[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+        const int64_t sb = u >> 2;
+        const int h = (int)((u >> 1) & 1), c = (int)(u & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + sb * Q6_K_BYTES;
+            l0[r] = ldu16(blk + 64 * h + 32 * c);
+            l1[r] = ldu16(blk + 64 * h + 32 * c + 16);
+            h0[r] = ldu16(blk + 128 + 32 * h);
+            h1[r] = ldu16(blk + 128 + 32 * h + 16);
+            uint2 s;
+            __builtin_memcpy(&s, blk + 192 + 8 * h, 8);
+            sc[r] = s;
+            uint16_t d;
+            __builtin_memcpy(&d, blk + 208, 2);
+            dq[r] = d;
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t u, float (&acc)[R][NC]) const {
+        const int c = (int)(u & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t ql[8] = {l0[r].x, l0[r].y, l0[r].z, l0[r].w, l1[r].x, l1[r].y, l1[r].z, l1[r].w};
+            const uint32_t qh[8] = {h0[r].x, h0[r].y, h0[r].z, h0[r].w, h1[r].x, h1[r].y, h1[r].z, h1[r].w};
+            int code[16];
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                code[w] = (int)((ql[w] & 0x0f0f0f0fu) | (((qh[w] >> (2 * c)) & 0x03030303u) << 4));
+                code[8 + w] = (int)(((ql[w] >> 4) & 0x0f0f0f0fu) | (((qh[w] >> (4 + 2 * c)) & 0x03030303u) << 4));
+            }
+            // this unit's sub-blocks: 2c, 2c + 1 (first run) and 4 + 2c, 5 + 2c (second) of the half
+            const uint32_t sw = c ? (sc[r].x >> 16) | (sc[r].y & 0xffff0000u) : (sc[r].x & 0xffffu) | (sc[r].y << 16);
+            const float d = h2f((uint16_t)dq[r]);
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int tot = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int s = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s = dot4(code[4 * k + i], act[n].q[4 * k + i], s);
+                    const int scale = (int)(int8_t)((sw >> (8 * k)) & 0xff);
+                    tot += scale * (s - 32 * act[n].b[k]);
+                }
+                acc[r][n] += (d * act[n].d0) * (float)tot;
             }
         }
     }
@@ -378,10 +465,10 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     for (int n = 0; n < NC; ++n) {
         const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
         if constexpr (FUSED) {
-            quantize_unit<AT>((const float *)((const char *)x + arow * x_row_bytes), u, uvalid, act[n]);
+            quantize_unit<AT, WT>((const float *)((const char *)x + arow * x_row_bytes), u, uvalid, act[n]);
         } else {
             const ActView g = act_view(a.act, AT, K, a.N_total * a.ne12 * a.ne13);
-            load_unit<AT>(g, arow, K, u, uvalid, act[n]);
+            load_unit<AT, WT>(g, arow, K, u, uvalid, act[n]);
         }
     }
 
@@ -482,7 +569,8 @@ static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_
 template <int WT, int NC, bool FUSED>
 static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
                                 hipStream_t stream) {
-    constexpr int R = NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
+    // q6_K holds 19 weight registers per row: two columns take 2 rows per wave
+    constexpr int R = (WT == TLH_TYPE_Q6_K && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
     return launch_reg_cfg<WT, NC, R, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
 }
 
@@ -520,6 +608,9 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     case TLH_TYPE_Q4_K:
         return fused ? launch_reg_wt<TLH_TYPE_Q4_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
                      : launch_reg_wt<TLH_TYPE_Q4_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
+    case TLH_TYPE_Q6_K:
+        return fused ? launch_reg_wt<TLH_TYPE_Q6_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
+                     : launch_reg_wt<TLH_TYPE_Q6_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
     }
 }

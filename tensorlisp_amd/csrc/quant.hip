@@ -137,7 +137,8 @@ __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__
 // ------------------------------------------------------------- dequantize
 // One thread per output element; integer codes convert exactly, so the only
 // roundings are the reference's own: q4_0 ((q-8)*d, ggml-quants.c:459-476),
-// q8_0 (q*d, :553-565), q4_K ((d*sc)*q - (dmin*m), :1529-1550).
+// q8_0 (q*d, :553-565), q4_K ((d*sc)*q - (dmin*m), :1529-1550), q6_K ((d*sc)*q,
+// :1939-1968).
 template <int WT>
 __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ w, int64_t K, int64_t rows,
                                                     int64_t w_row_bytes, float *__restrict__ y) {
@@ -158,6 +159,18 @@ __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ 
         const uint8_t *b = r + (col / QK) * Q8_0_BYTES;
         const float d = h2f(*(const uint16_t *)b);
         out = (float)(int8_t)b[2 + col % QK] * d;
+    } else if constexpr (WT == TLH_TYPE_Q6_K) {
+        // element e of a 128-element half: low 4 bits in ql[l + 32 * (q & 1)]
+        // (high nibble for q >= 2), high 2 bits in qh[l] at 2q; e = 32q + l
+        const uint8_t *b = r + (col / QKK) * Q6_K_BYTES;
+        const int i = (int)(col % QKK);
+        const int h = i >> 7, e = i & 127, q = e >> 5, l = e & 31;
+        const uint8_t lo = b[64 * h + l + 32 * (q & 1)];
+        const uint8_t hi2 = b[128 + 32 * h + l];
+        const int code = (int)(((q >= 2 ? lo >> 4 : lo & 0x0f) | (((hi2 >> (2 * q)) & 3) << 4))) - 32;
+        const float d = h2f(*(const uint16_t *)(b + 208));
+        const int sc = (int)(int8_t)b[192 + 8 * h + (e >> 4)];
+        out = (d * (float)sc) * (float)code;
     } else {
         const uint8_t *b = r + (col / QKK) * Q4_K_BYTES;
         const int i = (int)(col % QKK);
@@ -217,6 +230,9 @@ tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, i
         break;
     case TLH_TYPE_Q4_K:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q6_K:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q6_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
         break;
     default:
         return set_error(TLH_UNSUPPORTED, "dequantize: unsupported type %d", type);

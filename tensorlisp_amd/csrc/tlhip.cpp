@@ -43,7 +43,9 @@ static tlh_status hip_check(hipError_t e, const char *what) {
     return set_error(TLH_EXECUTION, "%s: %s", what, hipGetErrorString(e));
 }
 
-static bool weight_type_ok(int t) { return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K; }
+static bool weight_type_ok(int t) {
+    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q6_K;
+}
 
 static const char *type_name(int t) {
     switch (t) {
@@ -52,6 +54,7 @@ static const char *type_name(int t) {
     case TLH_TYPE_Q4_0: return "q4_0";
     case TLH_TYPE_Q8_0: return "q8_0";
     case TLH_TYPE_Q4_K: return "q4_K";
+    case TLH_TYPE_Q6_K: return "q6_K";
     case TLH_TYPE_Q8_K: return "q8_K";
     default: return "?";
     }
@@ -67,7 +70,7 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     if (!op) return set_error(TLH_INVALID, "mul_mat: null op");
     const tlh_tensor &a = op->t[0], &b = op->t[1], &d = op->t[4];
     if (!weight_type_ok(a.ty))
-        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K", a.ty,
+        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q6_K", a.ty,
                          type_name(a.ty));
     if (b.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: activations must be f32 (got type %d)", b.ty);
     if (d.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: the destination must be f32");

@@ -21,13 +21,18 @@ these are the reference's outputs on fixed inputs, captured once:
                    and the CPU backend's output vector
   flash_attn.npz   GGML_OP_FLASH_ATTN_EXT (ops.cpp:8468) on dense f16 K/V, the
                    dense-cache counterpart of paged attention
+  q6_K.npz         q6_K weights from ggml_quantize_chunk on the reference test's
+                   96 x 256 noise matrix (native.rs:73-107, the same inputs as
+                   mul_mat.npz), their dequantize_row_q6_K, and one
+                   GGML_OP_MUL_MAT per n in 1,3,5,8,9,40; plus structurally
+                   random q6_K blocks (synth seed 61) against x (seed 62)
   flash_attn_ext.npz  GGML_OP_FLASH_ATTN_EXT with masks, GQA, batch, soft cap and
                    ALiBi on the shapes of the reference's attention tests
                    (refs.FA_CASES, native.rs:156-345), 8 CPU threads, outputs of the
                    first and last 6 queries; inputs are regenerated from the
                    stored seeds by refs.fa_case_inputs
 
-Run: python tests/golden/make_golden.py [flash_attn_ext]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -41,7 +46,7 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import FA_CASES, Q4_0, Q4_K, Q8_0, Ref, fa_case_inputs, fp16_probe_values, xorshift_noise  # noqa: E402
+from refs import FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, fa_case_inputs, fp16_probe_values, xorshift_noise  # noqa: E402
 from tensorlisp_amd import synth  # noqa: E402
 
 
@@ -88,10 +93,30 @@ def flash_attn_ext_golden(ref) -> None:
     np.savez_compressed(HERE / "flash_attn_ext.npz", **out)
 
 
+def q6_K_golden(ref) -> None:
+    rows, k = 96, 256
+    wn = xorshift_noise((rows, k), 1)
+    ns = [1, 3, 5, 8, 9, 40]
+    q = ref.quantize_weights(Q6_K, wn)
+    out = {"w": q, "deq": ref.dequantize(Q6_K, q, k), "ns": np.array(ns)}
+    for n in ns:
+        y, _ = ref.mul_mat(Q6_K, q, rows, k, xorshift_noise((n, k), 10 + n))
+        out[f"y{n}"] = y
+    M, K = 40, 1024
+    wr = synth.random_blocks(Q6_K, 61, M, K)
+    xr = synth.normal(62, (3, K))
+    y, _ = ref.mul_mat(Q6_K, wr, M, K, xr)
+    out.update({"rand_w": wr, "rand_y": y, "rand_deq": ref.dequantize(Q6_K, wr, K)})
+    np.savez_compressed(HERE / "q6_K.npz", **out)
+
+
 def main() -> None:
     ref = Ref()
     if sys.argv[1:] == ["flash_attn_ext"]:  # only the FLASH_ATTN_EXT fixture
         flash_attn_ext_golden(ref)
+        return
+    if sys.argv[1:] == ["q6_K"]:  # only the q6_K fixture
+        q6_K_golden(ref)
         return
     # ---------------------------------------------------------------- fp16
     halves = np.arange(65536, dtype=np.uint16)
@@ -152,6 +177,7 @@ def main() -> None:
         out.update({f"q{i}": q, f"k{i}": kk, f"v{i}": vv, f"o{i}": o})
     np.savez_compressed(HERE / "flash_attn.npz", **out)
     flash_attn_ext_golden(ref)
+    q6_K_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

@@ -88,9 +88,9 @@ def test_mul_mat_scratch_has_mfma_partials_for_long_K(wt, n, K, parts):
 
 def test_mul_mat_unsupported_weight_type_is_named():
     op = N.mul_mat_op(N.Q4_0, 64, 256, 1)
-    op.t[0].ty = 14  # q6_K
+    op.t[0].ty = 13  # q5_K
     st, msg, _ = scratch_status(op)
-    assert st == "UNSUPPORTED" and "type 14" in msg
+    assert st == "UNSUPPORTED" and "type 13" in msg
 
 
 def test_mul_mat_rejects_bad_shapes_and_layouts():
@@ -121,7 +121,7 @@ def test_mul_mat_null_pointers_are_invalid_not_crashes():
 
 def test_quantize_and_dequantize_validation():
     L = N.lib()
-    st, msg = _status(L.tlh_quantize_act, 14, None, 256, 1, 1024, None, None)
+    st, msg = _status(L.tlh_quantize_act, 13, None, 256, 1, 1024, None, None)  # q5_K
     assert st == "UNSUPPORTED"
     st, msg = _status(L.tlh_quantize_act, N.Q4_K, None, 300, 1, 1200, None, None)
     assert st == "INVALID" and "multiple" in msg

@@ -12,14 +12,15 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q8_0, oracle
+from refs import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, oracle
 from tensorlisp_amd import native as N
 from tensorlisp_amd import synth
 
 pytestmark = pytest.mark.gpu
 GOLD = Path(__file__).resolve().parent / "golden"
 RTOL, ATOL = 1e-3, 1e-4
-WTYPES = (Q4_0, Q8_0, Q4_K)
+WTYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
+GOLD_TYPES = (Q4_0, Q8_0, Q4_K)  # mul_mat.npz; q6_K has q6_K.npz
 
 
 def dev(a):
@@ -41,7 +42,7 @@ def close(got, want, what=""):
     assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tol, max err {err.max():.3e}"
 
 
-@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("t", GOLD_TYPES, ids=[NAMES[t] for t in GOLD_TYPES])
 def test_reference_cases_golden(gpu, t):
     """crates/tensorlisp/tests/native.rs:73-107 shapes: 96 x 256, N in 1,3,5,8,9,40."""
     g = np.load(GOLD / "mul_mat.npz")
@@ -49,6 +50,34 @@ def test_reference_cases_golden(gpu, t):
     for n in g["ns"]:
         y = host(N.mul_mat(t, w, 96, 256, dev(g[f"x{n}"])))
         close(y, g[f"{NAMES[t]}_y{n}"], f"{NAMES[t]} n={n}")
+
+
+def test_q6_K_reference_cases_golden(gpu):
+    """q6_K weights from ggml_quantize_chunk on the reference test's 96 x 256 matrix
+    and structurally random q6_K blocks: the CPU backend's outputs (q6_K.npz)."""
+    from refs import xorshift_noise
+
+    g = np.load(GOLD / "q6_K.npz")
+    w = dev(g["w"])
+    for n in g["ns"]:
+        y = host(N.mul_mat(Q6_K, w, 96, 256, dev(xorshift_noise((int(n), 256), 10 + int(n)))))
+        close(y, g[f"y{n}"], f"q6_K n={n}")
+    y = host(N.mul_mat(Q6_K, dev(g["rand_w"]), 40, 1024, dev(synth.normal(62, (3, 1024)))))
+    close(y, g["rand_y"], "q6_K random blocks")
+
+
+@pytest.mark.parametrize("n", [1, 2, 8, 40])
+def test_q6_K_lm_head_row_sample(gpu, n):
+    """The q6_K output projection of a Q4_K_M 8B model (128256 x 4096): register GEMV
+    (n <= 2), MFMA few-column kernel (n = 8) and its 16-column slabs (n = 40), checked
+    by the oracle on 96 rows spread over M."""
+    M, K = 128256, 4096
+    w = synth.random_blocks(Q6_K, 610 + n, M, K)
+    x = synth.normal(611 + n, (n, K))
+    y = host(N.mul_mat(Q6_K, dev(w), M, K, dev(x)))
+    rows = np.unique(synth.integers(612, 0, M - 1, 96))
+    want = oracle().mul_mat(Q6_K, w[rows], len(rows), K, x, nthreads=16)
+    close(y[:, rows], want, f"q6_K lm_head n={n}")
 
 
 def test_config1_q8_0_4096_golden(gpu):
@@ -167,8 +196,8 @@ def test_repeated_launches_are_deterministic(gpu):
     assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
 
 
-@pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 8224)],
-                         ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K8224"])
+@pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 8224), (Q6_K, 16640)],
+                         ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K8224", "q6_K-K16640"])
 @pytest.mark.parametrize("n", [1, 2, 5, 8])
 def test_other_K_shapes(gpu, t, K, n):
     """K outside the register-resident GEMV (K % 64 != 0 or K > 16384), so every N runs on

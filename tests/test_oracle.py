@@ -18,7 +18,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
+from refs import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
 from tensorlisp_amd import synth
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -228,6 +228,72 @@ def test_mul_mat_matches_reference_random_blocks(t):
         x = synth.normal(82 + n, (n, K))
         y, _ = r.mul_mat(t, w, M, K, x)
         assert same_bits(o.mul_mat(t, w, M, K, x), y)
+
+
+# ------------------------------------------------------------------ q6_K
+# tlq_dequantize_row_q6_K (ggml-quants.c:1939-1968) and tlq_vec_dot_q6_K_q8_K
+# (ggml-cpu/quants.c:851-904): pinned by the compiled reference's outputs
+# (q6_K.npz, from ggml_quantize_chunk weights and random blocks), bit-exact;
+# the live reference; and float64 brute force over the dequantized operands.
+def test_q6_K_golden_dequantize_and_mul_mat():
+    o, g = oracle(), gold("q6_K")
+    assert same_bits(o.dequantize(Q6_K, g["w"], 256), g["deq"])
+    assert same_bits(o.dequantize(Q6_K, g["rand_w"], 1024), g["rand_deq"])
+    from refs import xorshift_noise
+
+    for n in g["ns"]:
+        y = o.mul_mat(Q6_K, g["w"], 96, 256, xorshift_noise((int(n), 256), 10 + int(n)))
+        assert same_bits(y, g[f"y{n}"]), n
+    assert same_bits(o.mul_mat(Q6_K, g["rand_w"], 40, 1024, synth.normal(62, (3, 1024))), g["rand_y"])
+
+
+def test_q6_K_codes_against_an_independent_unpacking():
+    """dequantize = d * scale * (code - 32) with code rebuilt here from ql / qh by
+    a different route (numpy bit fields over the whole block at once)."""
+    o = oracle()
+    w = synth.random_blocks(Q6_K, 91, 6, 512).reshape(-1, 210)
+    ql, qh = w[:, :128].astype(np.int64), w[:, 128:192].astype(np.int64)
+    sc = w[:, 192:208].view(np.int8).astype(np.float64)
+    d = w[:, 208:210].copy().view(np.float16).astype(np.float64)[:, 0]
+    codes = np.zeros((w.shape[0], 256), np.int64)
+    for h in range(2):
+        for q in range(4):
+            lo = ql[:, 64 * h + 32 * (q & 1): 64 * h + 32 * (q & 1) + 32]
+            nib = (lo >> 4) if q >= 2 else (lo & 15)
+            hi = (qh[:, 32 * h: 32 * h + 32] >> (2 * q)) & 3
+            codes[:, 128 * h + 32 * q: 128 * h + 32 * q + 32] = (nib | (hi << 4)) - 32
+    want = d[:, None] * np.repeat(sc, 16, axis=1) * codes
+    got = o.dequantize(Q6_K, w, 256).astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-6, atol=0)
+
+
+def test_q6_K_vec_dot_against_f64_bruteforce():
+    o = oracle()
+    K = 2048
+    w = synth.random_blocks(Q6_K, 93, 8, K)
+    x = synth.normal(94, (4, K))
+    xq = o.quantize_act(Q6_K, x)
+    wd = o.dequantize(Q6_K, w, K).astype(np.float64)
+    xd = o.dequantize(Q8_K, xq, K).astype(np.float64)
+    want = wd @ xd.T
+    got = np.array([[o.vec_dot(Q6_K, K, w[i], xq[j]) for j in range(4)] for i in range(8)])
+    scale = np.abs(wd).sum(1)[:, None] * np.abs(xd).max()
+    assert np.all(np.abs(got - want) <= 1e-6 * scale)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+def test_q6_K_matches_reference_live():
+    o, r = oracle(), ref()
+    M, K = 120, 2048
+    w = synth.random_blocks(Q6_K, 95, M, K)
+    assert same_bits(o.dequantize(Q6_K, w, K), r.dequantize(Q6_K, w, K))
+    wq = r.quantize_weights(Q6_K, synth.normal(96, (8, K), 0.02))
+    for n in (1, 2, 9):
+        x = synth.normal(97 + n, (n, K))
+        y, _ = r.mul_mat(Q6_K, w, M, K, x)
+        assert same_bits(o.mul_mat(Q6_K, w, M, K, x), y)
+        y, _ = r.mul_mat(Q6_K, wq, 8, K, x)
+        assert same_bits(o.mul_mat(Q6_K, wq, 8, K, x), y)
 
 
 # -------------------------------------------------------- paged attention
