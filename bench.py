@@ -56,7 +56,10 @@ def gpu_blocks(torch, wtype, M, K, gen):
     raw = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device="cuda", generator=gen)
     nscale = 2 if wtype == N.Q4_K else 1
     d = (torch.randn((nb, nscale), device="cuda", generator=gen).abs() * (0.02 / 63)).to(torch.float16)
-    raw[:, : 2 * nscale] = d.view(torch.uint8).reshape(nb, 2 * nscale)
+    if wtype == N.Q6_K:  # d is the block's last field
+        raw[:, bb - 2:] = d.view(torch.uint8).reshape(nb, 2)
+    else:
+        raw[:, : 2 * nscale] = d.view(torch.uint8).reshape(nb, 2 * nscale)
     return raw.reshape(M, (K // be) * bb)
 
 
@@ -219,6 +222,32 @@ def main() -> int:
         del ws, base
     torch.cuda.empty_cache()
 
+    # q6_K output projection (the lm_head of Q4_K_M files), 128256 x 4096, N = 1 and 8
+    q6 = []
+    base = gpu_blocks(torch, N.Q6_K, 128256, 4096, gen)
+    ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
+    for n in (1, 8):
+        node = N.MulMat(N.Q6_K, 128256, 4096, n)
+        x = torch.randn((n, 4096), device="cuda", generator=gen)
+        y = torch.empty((n, 128256), dtype=torch.float32, device="cuda")
+        for i in range(2):
+            node(ws[i % len(ws)], x, y, stream)
+        evs = []
+        for i in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            node(ws[i % len(ws)], x, y, stream)
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        b = algorithmic_bytes(N.Q6_K, 128256, 4096, n)
+        q6.append({"M": 128256, "K": 4096, "N": n, "us": round(ms * 1e3, 1), "gbs": round(b / ms / 1e6, 1),
+                   "frac_of_hbm_peak": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)})
+        log(f"  q6_K  128256x4096  n={n}: {ms * 1e3:8.1f} us  {b / ms / 1e6:7.0f} GB/s")
+    del ws, base
+    torch.cuda.empty_cache()
+
     # paged-attention decode: 32 sequences, 32 q / 8 kv heads, hs 128, 16-token
     # pages scattered over a 65,536-page pool (2 GiB per cache), lens ~ U[512, 8192]
     seqs, heads, kvh, hs, bs, pool = 32, 32, 8, 128, 16, 65536
@@ -333,6 +362,7 @@ def main() -> int:
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
             "prefill_gemm_q4k": prefill,
+            "gemv_q6k_lm_head": q6,
             "paged_attention_decode": attention,
             "flash_attn_ext": fa,
         },
