@@ -174,6 +174,50 @@ tlh_status tlh_flash_attn_ext_scratch_bytes(const tlh_op *op, size_t *bytes);
 tlh_status tlh_flash_attn_ext(const tlh_op *op, const void *q, const void *k, const void *v, const void *mask,
                               void *dst, void *scratch, size_t scratch_bytes, void *stream);
 
+/* ------------------------------------------------------------ core ops
+ * The ggml ops around MUL_MAT and attention in a decoder step (token
+ * embedding, norms, residuals, activations, RoPE, KV-cache writes, softmax,
+ * greedy sampling), replacing the reference's core kernels
+ * (crates/kernels/src/cuda/native/core.cu) as Ctx::lower dispatches them
+ * (crates/kernels/src/cuda/lower.rs:175-213, 219-500), computed as the ggml CPU
+ * backend does (vendor/ggml/src/ggml-cpu/binary-ops.cpp, unary-ops.cpp,
+ * ops.cpp). `op` is the blob the reference's lowering packs: t[0..2] sources,
+ * t[4] the destination, x[] the op's parameters (floats as their bit
+ * pattern). Data types f32 / f16; index tensors i32 / i64. Results are
+ * bit-exact for BIN, CPY, GET_ROWS, SET_ROWS, ARGMAX and the unary ops
+ * without a transcendental function; NORM sums in double like the CPU (equal
+ * up to the order of the double additions); the others use the GPU's
+ * expf/sinf/... (within a few ulp of the CPU's libm; GELU and GELU_QUICK go
+ * through f16 like the CPU's tables). A SOFT_MAX row whose every entry is -inf
+ * gives zeros (the CPU gives NaN).
+ * tlh_core_check validates a node without launching (for planning);
+ * tlh_core runs it. A GET_ROWS index outside src0 reads the nearest row and a
+ * SET_ROWS index outside dst writes nothing (ggml asserts instead). */
+typedef enum tlh_core_kind {
+    TLH_CORE_BIN = 1,      /* ADD/SUB/MUL/DIV: x0 = 0/1/2/3; t0 op t1, t1 repeated to t0's shape */
+    TLH_CORE_UNARY = 2,    /* UNARY (x0 = ggml_unary_op) and SCALE 100 (x1 s, x2 b), FILL 101 (x1),
+                              CLAMP 102 (x1, x2), LEAKY_RELU 103 (x1), SQR 104, SQRT 105, SIN 106,
+                              COS 107, LOG 108 (lower.rs:250-290) */
+    TLH_CORE_NORM = 3,     /* NORM (x0 = 0) / RMS_NORM (x0 = 1), x1 = eps; f32 rows, unit element stride */
+    TLH_CORE_GET_ROWS = 4, /* t0 f32/f16/q4_0/q8_0/q4_K/q6_K rows, t1 indices -> t4 f32/f16 */
+    TLH_CORE_SET_ROWS = 5, /* t0 f32/f16 rows to the t4 rows named by t1 */
+    TLH_CORE_CPY = 6,      /* DUP/CPY/CONT: equal element counts, any shapes/strides */
+    TLH_CORE_ROPE = 7,     /* x0 n_dims, x1 mode (0 normal, 2 neox), x2 freq_scale, x3 ext_factor,
+                              x4 attn_factor, x5 freq_base^(-2/n_dims), x6/x7 YaRN corr dims,
+                              x8 = 1 with f32 frequency factors in src2; t1 i32 positions */
+    TLH_CORE_SOFT_MAX = 8, /* x0 scale, x1 max_bias, x2 m0, x3 m1, x4 n_head_log2; t0 f32; mask src1
+                              f32/f16, optional (lower.rs:314-341) */
+    TLH_CORE_ARGMAX = 9,   /* t0 f32 [n, rows] -> t4 i32 [rows] (last index of the maximum) */
+    TLH_CORE_GLU = 10      /* GGML_OP_GLU, f32: x0 = ggml_glu_op (0 reglu, 1 geglu, 2 swiglu, 4 geglu_erf,
+                              5 geglu_quick), x1 = swapped; t0 [2n, ...] halves, or t0 and t1 [n, ...]
+                              (split form). No counterpart in the reference's lowering, which leaves
+                              GLU unsupported; computed as ops.cpp ggml_compute_forward_glu does */
+} tlh_core_kind;
+
+tlh_status tlh_core_check(int kind, const tlh_op *op, int has_src1, int has_src2);
+tlh_status tlh_core(int kind, const tlh_op *op, const void *src0, const void *src1, const void *src2, void *dst,
+                    void *stream);
+
 /* ------------------------------------------------------- paged attention
  * The `paged-attention` custom node (crates/tensorlisp/src/scheme/core.ss:251-258),
  * lowered by Ctx::custom kind 1 (crates/kernels/src/cuda/lower.rs:672-731) to

@@ -15,6 +15,10 @@
 //   ref_flash_attn_ext  the same op in full: q [D, nq, nh, nb], K/V
 //                    [D|DV, L, nhkv, nb], optional f16 mask [Lm, nqm, mne2,
 //                    mne3], max_bias and logit softcap (ggml.c:5402-5444).
+//   ref_core         one of the ops around them in a decoder step (add/sub/
+//                    mul/div, unary ops, norm/rms_norm, get_rows, set_rows,
+//                    cpy of a permuted view, rope_ext, soft_max_ext, argmax,
+//                    glu).
 //
 // Tensor data points at caller memory (no copies); the work buffer is
 // allocated per call.
@@ -127,6 +131,81 @@ int ref_flash_attn_ext(const float *q, const uint16_t *k, const uint16_t *v, con
     struct ggml_cgraph *gf = ggml_new_graph(ctx);
     ggml_build_forward_expand(gf, o);
     int rc = compute(gf, nthreads, reps < 1 ? 1 : reps, secs);
+    ggml_free(ctx);
+    return rc;
+}
+
+// One core op (kind numbering as tlh_core_kind) on contiguous caller buffers:
+// tensor i (0 src0, 1 src1, 2 src2, 3 destination) has ggml type ty[i], extents
+// ne[4*i .. 4*i+3] and data data[i] (NULL: absent). ip[] / fp[] hold the
+// integer / float arguments of the ggml constructor:
+//   BIN 1      ip0 = 0 add, 1 sub, 2 mul, 3 div
+//   UNARY 2    ip0 = ggml_unary_op, or 100 scale_bias(fp0, fp1), 101 fill(fp0),
+//              102 clamp(fp0, fp1), 103 leaky_relu(fp0), 104 sqr, 105 sqrt,
+//              106 sin, 107 cos, 108 log
+//   NORM 3     ip0 = 1 rms_norm / 0 norm, eps fp0
+//   GET_ROWS 4 / SET_ROWS 5 (destination holds the rows not written)
+//   CPY 6      src0 permuted by ip0..ip3 first when ip4 != 0
+//   ROPE 7     n_dims ip0, mode ip1, n_ctx_orig ip2; freq_base, freq_scale,
+//              ext_factor, attn_factor, beta_fast, beta_slow fp0..fp5
+//   SOFT_MAX 8 scale fp0, max_bias fp1 (src1 mask optional)
+//   ARGMAX 9
+//   GLU 10     ip0 = ggml_glu_op, ip1 = swapped (src1 present: ggml_glu_split)
+int ref_core(int kind, const int *ty, const int64_t *ne, void *const *data, const int32_t *ip, const float *fp,
+             int nthreads) {
+    struct ggml_context *ctx = meta_ctx();
+    if (!ctx) return -1;
+    struct ggml_tensor *t[4] = {NULL, NULL, NULL, NULL};
+    for (int i = 0; i < 4; ++i) {
+        if (!data[i]) continue;
+        t[i] = ggml_new_tensor_4d(ctx, (enum ggml_type)ty[i], ne[4 * i], ne[4 * i + 1], ne[4 * i + 2], ne[4 * i + 3]);
+        t[i]->data = data[i];
+    }
+    struct ggml_tensor *o = NULL;
+    switch (kind) {
+    case 1: {
+        struct ggml_tensor *(*f[4])(struct ggml_context *, struct ggml_tensor *, struct ggml_tensor *) = {
+            ggml_add, ggml_sub, ggml_mul, ggml_div};
+        o = f[ip[0] & 3](ctx, t[0], t[1]);
+        break;
+    }
+    case 2:
+        switch (ip[0]) {
+        case 100: o = ggml_scale_bias(ctx, t[0], fp[0], fp[1]); break;
+        case 101: o = ggml_fill(ctx, t[0], fp[0]); break;
+        case 102: o = ggml_clamp(ctx, t[0], fp[0], fp[1]); break;
+        case 103: o = ggml_leaky_relu(ctx, t[0], fp[0], false); break;
+        case 104: o = ggml_sqr(ctx, t[0]); break;
+        case 105: o = ggml_sqrt(ctx, t[0]); break;
+        case 106: o = ggml_sin(ctx, t[0]); break;
+        case 107: o = ggml_cos(ctx, t[0]); break;
+        case 108: o = ggml_log(ctx, t[0]); break;
+        default: o = ggml_unary(ctx, t[0], (enum ggml_unary_op)ip[0]); break;
+        }
+        break;
+    case 3: o = ip[0] ? ggml_rms_norm(ctx, t[0], fp[0]) : ggml_norm(ctx, t[0], fp[0]); break;
+    case 4: o = ggml_get_rows(ctx, t[0], t[1]); break;
+    case 5: o = ggml_set_rows(ctx, t[3], t[0], t[1]); break;
+    case 6: {
+        struct ggml_tensor *a = ip[4] ? ggml_permute(ctx, t[0], ip[0], ip[1], ip[2], ip[3]) : t[0];
+        o = ggml_cpy(ctx, a, t[3]);
+        break;
+    }
+    case 7:
+        o = ggml_rope_ext(ctx, t[0], t[1], t[2], ip[0], ip[1], ip[2], fp[0], fp[1], fp[2], fp[3], fp[4], fp[5]);
+        break;
+    case 8: o = ggml_soft_max_ext(ctx, t[0], t[1], fp[0], fp[1]); break;
+    case 9: o = ggml_argmax(ctx, t[0]); break;
+    case 10:
+        o = t[1] ? ggml_glu_split(ctx, t[0], t[1], (enum ggml_glu_op)ip[0])
+                 : ggml_glu(ctx, t[0], (enum ggml_glu_op)ip[0], ip[1] != 0);
+        break;
+    default: ggml_free(ctx); return -4;
+    }
+    o->data = data[3];
+    struct ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, o);
+    int rc = compute(gf, nthreads, 1, NULL);
     ggml_free(ctx);
     return rc;
 }

@@ -707,6 +707,311 @@ int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[
     return 0;
 }
 
+// ------------------------------------------------------------ core ops
+// The ggml CPU backend's ops around MUL_MAT in a decoder step, on ggml tensors
+// given as (data, ne[4], nb[4], type). f32/f16 data, i32/i64 indices.
+static float t_ld(const tlq_t *t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+    const char *p = (const char *)t->data + i0 * t->nb[0] + i1 * t->nb[1] + i2 * t->nb[2] + i3 * t->nb[3];
+    if (t->ty == TLQ_F16) return tlq_fp16_to_fp32(rd16((const uint8_t *)p));
+    float f;
+    memcpy(&f, p, 4);
+    return f;
+}
+static void t_st(const tlq_t *t, int64_t i0, int64_t i1, int64_t i2, int64_t i3, float v) {
+    char *p = (char *)t->data + i0 * t->nb[0] + i1 * t->nb[1] + i2 * t->nb[2] + i3 * t->nb[3];
+    if (t->ty == TLQ_F16) {
+        const uint16_t h = tlq_fp32_to_fp16(v);
+        memcpy(p, &h, 2);
+    } else {
+        memcpy(p, &v, 4);
+    }
+}
+static int64_t t_idx(const tlq_t *t, int64_t i0, int64_t i1, int64_t i2) {
+    const char *p = (const char *)t->data + i0 * t->nb[0] + i1 * t->nb[1] + i2 * t->nb[2];
+    if (t->ty == 27) {
+        int64_t v;
+        memcpy(&v, p, 8);
+        return v;
+    }
+    int32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+
+#define FOR4(t) \
+    for (int64_t i3 = 0; i3 < (t)->ne[3]; ++i3) \
+        for (int64_t i2 = 0; i2 < (t)->ne[2]; ++i2) \
+            for (int64_t i1 = 0; i1 < (t)->ne[1]; ++i1)
+
+// binary-ops.cpp: dst = a (op) b, b repeated; code 0 add, 1 sub, 2 mul, 3 div.
+void tlq_core_bin(int code, const tlq_t *a, const tlq_t *b, const tlq_t *d) {
+    FOR4(d) for (int64_t i0 = 0; i0 < d->ne[0]; ++i0) {
+        const float x = t_ld(a, i0, i1, i2, i3);
+        const float y = t_ld(b, i0 % b->ne[0], i1 % b->ne[1], i2 % b->ne[2], i3 % b->ne[3]);
+        t_st(d, i0, i1, i2, i3, code == 0 ? x + y : code == 1 ? x - y : code == 2 ? x * y : x / y);
+    }
+}
+
+// unary-ops.cpp:3-97 op_* and vec.h's ggml_vec_*_f32 (gelu and gelu_quick
+// through the f16 tables of ggml-cpu.c:3840-3849, GGML_GELU_FP16), plus the
+// lowering's 100 scale (x*s, or x*s + b when b != 0; ops.cpp:4568-4620),
+// 101 fill, 102 clamp MAX(MIN(x, max), min), 103 leaky relu, 104 sqr,
+// 105 sqrt, 106 sin, 107 cos, 108 log.
+static float gelu_f(float x) {
+    return 0.5f * x * (1.0f + tanhf(0.79788456080286535587989211986876f * x * (1.0f + 0.044715f * x * x)));
+}
+static float via_f16(float x) { return tlq_fp16_to_fp32(tlq_fp32_to_fp16(x)); }
+static float unary1(int code, float x, float p1, float p2) {
+    switch (code) {
+    case 0: return fabsf(x);
+    case 1: return (x > 0.f) ? 1.f : ((x < 0.f) ? -1.f : 0.f);
+    case 2: return -x;
+    case 3: return (x > 0.f) ? 1.f : 0.f;
+    case 4: return tanhf(x);
+    case 5: return (x > 0.f) ? x : expm1f(x);
+    case 6: return (x > 0.f) ? x : 0.f;
+    case 7: return 1.f / (1.f + expf(-x));
+    case 8: return x <= -10.0f ? 0.0f : x >= 10.0f ? x : via_f16(gelu_f(via_f16(x)));
+    case 9: {
+        const float h = via_f16(x);
+        return via_f16(h * (1.0f / (1.0f + expf(-1.702f * h))));
+    }
+    case 10: return x / (1.0f + expf(-x));
+    case 11: return x * fminf(1.0f, fmaxf(0.0f, (x + 3.0f) / 6.0f));
+    case 12: return fminf(1.0f, fmaxf(0.0f, (x + 3.0f) / 6.0f));
+    case 13: return expf(x);
+    case 14: return expf(x) - 1.0f;
+    case 15: return (x > 20.0f) ? x : logf(1.0f + expf(x));
+    case 16: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+    case 18: return floorf(x);
+    case 19: return ceilf(x);
+    case 20: return roundf(x);
+    case 21: return truncf(x);
+    case 100: return p2 == 0.0f ? x * p1 : x * p1 + p2;
+    case 101: return p1;
+    case 102: {
+        const float t = x < p2 ? x : p2;
+        return t > p1 ? t : p1;
+    }
+    case 103: return ((x > 0.f) ? x : 0.f) + p1 * ((x < 0.f) ? x : 0.f);
+    case 104: return x * x;
+    case 105: return sqrtf(x);
+    case 106: return sinf(x);
+    case 107: return cosf(x);
+    case 108: return logf(x);
+    default: return NAN;
+    }
+}
+// On f16 data the CPU reads the gelu table for every input (vec.h ggml_vec_gelu_f16),
+// without the f32 path's +-10 cut-offs.
+void tlq_core_unary(int code, float p1, float p2, const tlq_t *a, const tlq_t *d) {
+    FOR4(d) for (int64_t i0 = 0; i0 < d->ne[0]; ++i0) {
+        const float x = t_ld(a, i0, i1, i2, i3);
+        t_st(d, i0, i1, i2, i3, code == 8 && a->ty == TLQ_F16 ? via_f16(gelu_f(x)) : unary1(code, x, p1, p2));
+    }
+}
+
+// ops.cpp:3795-3840 rms_norm_f32: sum of x*x in double, mean = (float)(sum/n).
+// ops.cpp:3698-3740 norm_f32 (contiguous rows): mean = (float)sum / n with the
+// sum in double (ggml_vec_sum_f32); the variance as ggml_vec_cvar_f32's SSE2
+// build forms it (vec.cpp): ((d0^2 + d1^2) + (d2^2 + d3^2)) per group of four
+// in f32, accumulated in double, the tail element by element, / n in double.
+void tlq_core_norm(int rms, float eps, const tlq_t *a, const tlq_t *d) {
+    const int64_t n = a->ne[0];
+    FOR4(a) {
+        float mean = 0.0f;
+        double s2 = 0.0;
+        if (rms) {
+            for (int64_t i = 0; i < n; ++i) {
+                const float v = t_ld(a, i, i1, i2, i3);
+                s2 += (double)(v * v);
+            }
+        } else {
+            double s = 0.0;
+            for (int64_t i = 0; i < n; ++i) s += (double)t_ld(a, i, i1, i2, i3);
+            mean = (float)s / (float)n;
+            int64_t i = 0;
+            for (; i + 3 < n; i += 4) {
+                float q[4];
+                for (int j = 0; j < 4; ++j) {
+                    const float v = t_ld(a, i + j, i1, i2, i3) - mean;
+                    q[j] = v * v;
+                }
+                s2 += (double)((q[0] + q[1]) + (q[2] + q[3]));
+            }
+            for (; i < n; ++i) {
+                const float v = t_ld(a, i, i1, i2, i3) - mean;
+                s2 += (double)(v * v);
+            }
+        }
+        const float var = (float)(s2 / n);
+        const float scale = 1.0f / sqrtf(var + eps);
+        for (int64_t i = 0; i < n; ++i) t_st(d, i, i1, i2, i3, (t_ld(a, i, i1, i2, i3) - mean) * scale);
+    }
+}
+
+// ops.cpp get_rows: dst row (i1, i2, i3) = src row idx[i1, i2, i3] of plane (i2, i3).
+void tlq_core_get_rows(const tlq_t *a, const tlq_t *idx, const tlq_t *d) {
+    float *tmp = malloc(sizeof(float) * (size_t)(a->ne[0] > 0 ? a->ne[0] : 1));
+    FOR4(d) {
+        const int64_t r = t_idx(idx, i1, i2, i3);
+        const char *row = (const char *)a->data + r * a->nb[1] + i2 * a->nb[2] + i3 * a->nb[3];
+        if (a->ty == TLQ_F32 || a->ty == TLQ_F16) {
+            for (int64_t i = 0; i < d->ne[0]; ++i) {
+                tlq_t one = *a;
+                one.data = (void *)row;
+                t_st(d, i, i1, i2, i3, t_ld(&one, i, 0, 0, 0));
+            }
+        } else {
+            tlq_dequantize_row(a->ty, row, tmp, a->ne[0]);
+            for (int64_t i = 0; i < d->ne[0]; ++i) t_st(d, i, i1, i2, i3, tmp[i]);
+        }
+    }
+    free(tmp);
+}
+
+// ops.cpp set_rows: src row (i1, i2, i3) to dst row idx[i1, i2 % n1, i3 % n2] of plane (i2, i3).
+void tlq_core_set_rows(const tlq_t *a, const tlq_t *idx, const tlq_t *d) {
+    FOR4(a) {
+        const int64_t r = t_idx(idx, i1, i2 % idx->ne[1], i3 % idx->ne[2]);
+        for (int64_t i = 0; i < a->ne[0]; ++i) t_st(d, i, r, i2, i3, t_ld(a, i, i1, i2, i3));
+    }
+}
+
+// ops.cpp dup: element k of a in row-major order to element k of d.
+void tlq_core_cpy(const tlq_t *a, const tlq_t *d) {
+    float *tmp = malloc(sizeof(float) * (size_t)(a->ne[0] > 0 ? a->ne[0] : 1));
+    int64_t k = 0;
+    FOR4(a) {
+        const char *row = (const char *)a->data + i1 * a->nb[1] + i2 * a->nb[2] + i3 * a->nb[3];
+        if (a->ty == TLQ_F32 || a->ty == TLQ_F16) {
+            tlq_t one = *a;
+            one.data = (void *)row;
+            for (int64_t i = 0; i < a->ne[0]; ++i) tmp[i] = t_ld(&one, i, 0, 0, 0);
+        } else {
+            tlq_dequantize_row(a->ty, row, tmp, a->ne[0]);
+        }
+        for (int64_t i = 0; i < a->ne[0]; ++i, ++k) {
+            int64_t j = k;
+            const int64_t j0 = j % d->ne[0];
+            j /= d->ne[0];
+            const int64_t j1 = j % d->ne[1];
+            j /= d->ne[1];
+            t_st(d, j0, j1, j % d->ne[2], j / d->ne[2], tmp[i]);
+        }
+    }
+    free(tmp);
+}
+
+// ops.cpp:5822-5860 (rope_yarn_ramp, rope_yarn, ggml_rope_cache_init) and
+// :5934-6100 (rope_flt, rotate_pairs): mode 0 normal, 2 neox.
+void tlq_core_rope(int mode, int n_dims, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                   float attn_factor, float beta_fast, float beta_slow, const tlq_t *a, const int32_t *pos,
+                   const float *ff, const tlq_t *d) {
+    const float theta_scale = powf(freq_base, -2.0f / n_dims);
+    // ggml_rope_yarn_corr_dims (ggml.c)
+    const float pi = 3.14159265358979323846f;
+    const float start = floorf(n_dims * logf(n_ctx_orig / (beta_fast * 2 * pi)) / (2 * logf(freq_base)));
+    const float end = ceilf(n_dims * logf(n_ctx_orig / (beta_slow * 2 * pi)) / (2 * logf(freq_base)));
+    const float c0 = fmaxf(0, start), c1 = fminf(n_dims - 1, end);
+    const int64_t ne0 = a->ne[0];
+    float *cache = malloc(sizeof(float) * (size_t)(ne0 + 2));
+    FOR4(a) {
+        float theta = (float)pos[i2];
+        for (int64_t i0 = 0; i0 < ne0; i0 += 2) {
+            const float f = ff ? ff[i0 / 2] : 1.0f;
+            const float theta_extrap = theta / f;
+            float theta_interp = freq_scale * theta_extrap, th = theta_interp, mscale = attn_factor;
+            if (ext_factor != 0.0f) {
+                const float y = (i0 / 2 - c0) / fmaxf(0.001f, c1 - c0);
+                const float ramp = (1 - fminf(1, fmaxf(0, y))) * ext_factor;
+                th = theta_interp * (1 - ramp) + theta_extrap * ramp;
+                mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+            }
+            cache[i0] = cosf(th) * mscale;
+            cache[i0 + 1] = sinf(th) * mscale;
+            theta *= theta_scale;
+        }
+        for (int64_t i0 = 0; i0 < n_dims; i0 += 2) {
+            const int64_t ia = mode == 0 ? i0 : i0 / 2, ib = mode == 0 ? i0 + 1 : i0 / 2 + n_dims / 2;
+            const float x0 = t_ld(a, ia, i1, i2, i3), x1 = t_ld(a, ib, i1, i2, i3);
+            t_st(d, ia, i1, i2, i3, x0 * cache[i0] - x1 * cache[i0 + 1]);
+            t_st(d, ib, i1, i2, i3, x0 * cache[i0 + 1] + x1 * cache[i0]);
+        }
+        for (int64_t i0 = n_dims; i0 < ne0; ++i0) t_st(d, i0, i1, i2, i3, t_ld(a, i0, i1, i2, i3));
+    }
+    free(cache);
+}
+
+// ops.cpp soft_max_f32 (:5460-5560): w = x*scale + slope*mask; y = expf(w - max)
+// * (float)(1.0 / sum), sum in double; mask row i1, broadcast over i2/i3.
+void tlq_core_soft_max(float scale, float max_bias, const tlq_t *a, const tlq_t *mask, const tlq_t *d) {
+    const uint32_t n_head = (uint32_t)a->ne[2];
+    const uint32_t nhl2 = 1u << (uint32_t)floor(log2((double)n_head));
+    const float m0 = powf(2.0f, -(max_bias) / nhl2), m1 = powf(2.0f, -(max_bias / 2.0f) / nhl2);
+    const int64_t n = a->ne[0];
+    float *w = malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    FOR4(a) {
+        const uint32_t h = (uint32_t)i2;
+        const float slope = max_bias > 0.0f ? (h < nhl2 ? powf(m0, h + 1) : powf(m1, 2 * (h - nhl2) + 1)) : 1.0f;
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < n; ++i) {
+            w[i] = t_ld(a, i, i1, i2, i3) * scale;
+            if (mask) w[i] += slope * t_ld(mask, i, i1, i2 % mask->ne[2], i3 % mask->ne[3]);
+            mx = w[i] > mx ? w[i] : mx;
+        }
+        double sum = 0.0;
+        for (int64_t i = 0; i < n; ++i) {
+            w[i] = expf(w[i] - mx);
+            sum += (double)w[i];
+        }
+        const float inv = (float)(1.0 / sum);
+        for (int64_t i = 0; i < n; ++i) t_st(d, i, i1, i2, i3, w[i] * inv);
+    }
+    free(w);
+}
+
+// ops.cpp ggml_compute_forward_glu (reglu/geglu/swiglu/geglu_erf/geglu_quick f32)
+// with vec.h's ggml_vec_*glu_f32: y = act(x) * g; x, g = a, b (split) or the
+// halves of a's rows (x first unless swapped).
+void tlq_core_glu(int code, int swapped, const tlq_t *a, const tlq_t *b, const tlq_t *d) {
+    const int64_t nc = d->ne[0];
+    FOR4(d) for (int64_t i = 0; i < nc; ++i) {
+        float x, g;
+        if (b) {
+            x = t_ld(a, i, i1, i2, i3);
+            g = t_ld(b, i, i1, i2, i3);
+        } else {
+            x = t_ld(a, i + (swapped ? nc : 0), i1, i2, i3);
+            g = t_ld(a, i + (swapped ? 0 : nc), i1, i2, i3);
+        }
+        float y;
+        switch (code) {
+        case 0: y = x > 0.f ? x * g : 0.f; break;
+        case 1: y = x <= -10.0f ? 0.0f : x >= 10.0f ? x * g : via_f16(gelu_f(via_f16(x))) * g; break;
+        case 2: y = (x / (1.0f + expf(-x))) * g; break;
+        case 4: y = 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)) * g; break;
+        case 5: y = unary1(9, x, 0, 0) * g; break;
+        default: y = NAN;
+        }
+        t_st(d, i, i1, i2, i3, y);
+    }
+}
+
+// vec.h ggml_vec_argmax_f32: the last index of the maximum.
+void tlq_core_argmax(const tlq_t *a, int32_t *out) {
+    for (int64_t r = 0; r < a->ne[1]; ++r) {
+        float mx = -INFINITY;
+        int idx = 0;
+        for (int64_t i = 0; i < a->ne[0]; ++i) {
+            const float v = t_ld(a, i, r, 0, 0);
+            mx = mx > v ? mx : v;
+            if (mx == v) idx = (int)i;
+        }
+        out[r] = idx;
+    }
+}
+
 // ------------------------------------------------------- paged attention
 // Key cache element (block, kv head, dim i, slot s) sits at
 // [block][kvh][i/8][s][i%8]; value cache at [block][kvh][i][s]

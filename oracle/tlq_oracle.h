@@ -121,6 +121,29 @@ int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[
                        const int64_t v_nb[4], const void *mask, const int64_t m_ne[4], const int64_t m_nb[4],
                        void *dst, const int64_t d_nb[4], float scale, float max_bias, float softcap, int nthreads);
 
+// Core ops of a decoder step, as the ggml CPU backend computes them
+// (vendor/ggml/src/ggml-cpu/binary-ops.cpp, unary-ops.cpp, ops.cpp; each
+// function in tlq_oracle.c cites its lines). Tensors as ggml describes them:
+// data, ne[4], byte strides nb[4], type (f32, f16; i32 = 26 / i64 = 27 indices;
+// GET_ROWS / CPY sources also q4_0, q8_0, q4_K, q6_K).
+typedef struct tlq_t {
+    void *data;
+    int64_t ne[4], nb[4];
+    int ty;
+} tlq_t;
+void tlq_core_bin(int code, const tlq_t *a, const tlq_t *b, const tlq_t *d);
+void tlq_core_unary(int code, float p1, float p2, const tlq_t *a, const tlq_t *d);
+void tlq_core_norm(int rms, float eps, const tlq_t *a, const tlq_t *d);
+void tlq_core_get_rows(const tlq_t *a, const tlq_t *idx, const tlq_t *d);
+void tlq_core_set_rows(const tlq_t *a, const tlq_t *idx, const tlq_t *d);
+void tlq_core_cpy(const tlq_t *a, const tlq_t *d);
+void tlq_core_rope(int mode, int n_dims, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                   float attn_factor, float beta_fast, float beta_slow, const tlq_t *a, const int32_t *pos,
+                   const float *ff, const tlq_t *d);
+void tlq_core_soft_max(float scale, float max_bias, const tlq_t *a, const tlq_t *mask, const tlq_t *d);
+void tlq_core_argmax(const tlq_t *a, int32_t *out);
+void tlq_core_glu(int code, int swapped, const tlq_t *a, const tlq_t *b, const tlq_t *d);
+
 // reshape_and_cache (crates/kernels/src/cuda/shaders/reshape_and_cache_kernel.cu:31-84):
 // key/value f16 [tokens][kvh*hs] scattered to slot = block*bs + offset;
 // negative slots are skipped.

@@ -60,6 +60,52 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
+// ------------------------------------------------------ element dequantizers
+// Element `col` of a row of ggml blocks of type WT, rounded as the reference's
+// dequantize_row_* rounds it (integer codes convert exactly): q4_0
+// (q-8)*d (ggml-quants.c:459-476), q8_0 q*d (:553-565), q4_K (d*sc)*q -
+// (dmin*m) (:1529-1550), q6_K (d*sc)*q (:1939-1968).
+template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r, int64_t col) {
+#pragma clang fp contract(off)
+    if constexpr (WT == TLH_TYPE_Q4_0) {
+        const uint8_t *b = r + (col / QK) * Q4_0_BYTES;
+        const int j = (int)(col % QK);
+        const float d = h2f(*(const uint16_t *)b);
+        const int code = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
+        return (float)(code - 8) * d;
+    } else if constexpr (WT == TLH_TYPE_Q8_0) {
+        const uint8_t *b = r + (col / QK) * Q8_0_BYTES;
+        const float d = h2f(*(const uint16_t *)b);
+        return (float)(int8_t)b[2 + col % QK] * d;
+    } else if constexpr (WT == TLH_TYPE_Q6_K) {
+        // element e of a 128-element half: low 4 bits in ql[l + 32 * (q & 1)]
+        // (high nibble for q >= 2), high 2 bits in qh[l] at 2q; e = 32q + l
+        const uint8_t *b = r + (col / QKK) * Q6_K_BYTES;
+        const int i = (int)(col % QKK);
+        const int h = i >> 7, e = i & 127, q = e >> 5, l = e & 31;
+        const uint8_t lo = b[64 * h + l + 32 * (q & 1)];
+        const uint8_t hi2 = b[128 + 32 * h + l];
+        const int code = (int)(((q >= 2 ? lo >> 4 : lo & 0x0f) | (((hi2 >> (2 * q)) & 3) << 4))) - 32;
+        const float d = h2f(*(const uint16_t *)(b + 208));
+        const int sc = (int)(int8_t)b[192 + 8 * h + (e >> 4)];
+        return (d * (float)sc) * (float)code;
+    } else {
+        static_assert(WT == TLH_TYPE_Q4_K, "dequant_elem: type");
+        const uint8_t *b = r + (col / QKK) * Q4_K_BYTES;
+        const int i = (int)(col % QKK);
+        const int c = i / 64, pos = i % 64, hi = pos >= 32, l = pos & 31;
+        const uint32_t *s = (const uint32_t *)(b + 4);
+        int sc, mn;
+        q4k_scale_min(2 * c + hi, s[0], s[1], s[2], sc, mn);
+        const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
+        const uint8_t byte = b[16 + 32 * c + l];
+        const int code = hi ? byte >> 4 : byte & 0x0f;
+        const float d1 = d * (float)sc;
+        const float m1 = dmin * (float)mn;
+        return d1 * (float)code - m1;
+    }
+}
+
 // ------------------------------------------------ quantized activation scratch
 // The CPU backend quantizes src1 into `wdata` in ggml's block layout
 // (ggml-cpu.c:1318-1359). Here the same values (bit-exact d and codes) go to

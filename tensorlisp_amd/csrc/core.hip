@@ -1,0 +1,597 @@
+// The rest of a decoder step on gfx950: the ggml ops around MUL_MAT and
+// attention that a tensorlisp program runs per token.
+//
+// Each kernel computes what ggml's CPU backend computes for the op
+// (vendor/ggml/src/ggml-cpu/binary-ops.cpp, unary-ops.cpp, ops.cpp) on ggml
+// tensors addressed through their ne/nb (views work unchanged), with the
+// parameters the reference's lowering packs for its core kernels
+// (crates/kernels/src/cuda/lower.rs:219-500; kernels in
+// crates/kernels/src/cuda/native/core.cu). Element types: f32 and f16 data,
+// i32/i64 indices; GET_ROWS and CPY also read q4_0, q8_0, q4_K and q6_K rows.
+//
+// Layout on the GPU: rows of ne0 elements. Kernels that map one element per
+// thread walk a row per workgroup y-index (row -> i1, i2, i3 decomposed once)
+// with consecutive threads on consecutive elements, so contiguous rows are
+// read and written in full cache lines; reductions (norms, softmax, argmax)
+// give each row one workgroup and reduce in registers, then across waves.
+#include "kernels.hpp"
+
+// The CPU backend rounds every product and sum (its x86-64 build has no FMA);
+// contracting a*b+c into one fma here would change results in the last bit.
+#pragma clang fp contract(off)
+
+namespace tlh {
+
+constexpr int CORE_I32 = 26, CORE_I64 = 27;
+
+__device__ __forceinline__ float ld_f(const char *p, int ty) {
+    return ty == TLH_TYPE_F16 ? h2f(*(const uint16_t *)p) : *(const float *)p;
+}
+__device__ __forceinline__ void st_f(char *p, int ty, float v) {
+    if (ty == TLH_TYPE_F16)
+        *(uint16_t *)p = f2h(v);
+    else
+        *(float *)p = v;
+}
+__device__ __forceinline__ int64_t ld_idx(const char *p, int ty) {
+    return ty == CORE_I64 ? *(const int64_t *)p : (int64_t)*(const int32_t *)p;
+}
+
+struct CoreArgs {
+    tlh_op op;
+    const char *s0, *s1, *s2;
+    char *dst;
+};
+
+// rows of a tensor: row r -> (i1, i2, i3)
+__device__ __forceinline__ void row_coords(int64_t r, const tlh_tensor &t, int64_t &i1, int64_t &i2, int64_t &i3) {
+    i1 = r % t.ne[1];
+    i2 = (r / t.ne[1]) % t.ne[2];
+    i3 = r / (t.ne[1] * t.ne[2]);
+}
+__device__ __forceinline__ int64_t offs(const tlh_tensor &t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+    return i0 * t.nb[0] + i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
+}
+
+// grid: (chunks of CORE_CHUNK elements along ne0, rows); 256 threads, 4 elements each
+constexpr int CORE_CHUNK = 1024;
+
+// ------------------------------------------------------------------- binary
+// binary-ops.cpp: dst = src0 (op) src1 with src1 repeated to src0's shape
+// (ggml_can_repeat), in f32.
+__global__ void __launch_bounds__(256) k_core_bin(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &y = a.op.t[1], &d = a.op.t[4];
+    const int code = (int)a.op.x[0];
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, d, i1, i2, i3);
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    const char *yr = a.s1 + offs(y, 0, i1 % y.ne[1], i2 % y.ne[2], i3 % y.ne[3]);
+    char *dr = a.dst + offs(d, 0, i1, i2, i3);
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= d.ne[0]) break;
+        const float p = ld_f(xr + i0 * x.nb[0], x.ty);
+        const float q = ld_f(yr + (i0 % y.ne[0]) * y.nb[0], y.ty);
+        const float r = code == 0 ? p + q : code == 1 ? p - q : code == 2 ? p * q : p / q;
+        st_f(dr + i0 * d.nb[0], d.ty, r);
+    }
+}
+
+// -------------------------------------------------------------------- unary
+// unary-ops.cpp / vec.h per element, in f32. Codes: ggml_unary_op 0..21 and
+// the reference's 100 scale (x * s + b), 101 fill, 102 clamp, 103 leaky relu,
+// 104 sqr, 105 sqrt, 106 sin, 107 cos, 108 log.
+// ggml_gelu_f32 / ggml_gelu_quick_f32 (vec.h:966-1019) as the CPU applies
+// them to f32 data: through 64K-entry f16 tables (GGML_GELU_FP16), i.e. x
+// rounded to f16, the function of that, rounded to f16 again.
+__device__ __forceinline__ float gelu_f16(float h) {
+    const float c = 0.044715f, s2pi = 0.79788456080286535587989211986876f;
+    return h2f(f2h(0.5f * h * (1.0f + tanhf(s2pi * h * (1.0f + c * h * h)))));
+}
+__device__ __forceinline__ float gelu_tab(float v) {
+    if (v <= -10.0f) return 0.0f;
+    if (v >= 10.0f) return v;
+    return gelu_f16(h2f(f2h(v)));
+}
+__device__ __forceinline__ float gelu_quick_tab(float v) {
+    const float h = h2f(f2h(v));
+    return h2f(f2h(h * (1.0f / (1.0f + expf(-1.702f * h)))));
+}
+
+__device__ __forceinline__ float unary_val(int code, float v, float p1, float p2) {
+    switch (code) {  // unary-ops.cpp:3-97 op_* and vec.h for the ops.cpp ones
+    case 0: return fabsf(v);
+    case 1: return (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+    case 2: return -v;
+    case 3: return (v > 0.f) ? 1.f : 0.f;
+    case 4: return tanhf(v);
+    case 5: return (v > 0.f) ? v : expm1f(v);
+    case 6: return (v > 0.f) ? v : 0.f;
+    case 7: return 1.f / (1.f + expf(-v));
+    case 8: return gelu_tab(v);
+    case 9: return gelu_quick_tab(v);
+    case 10: return v / (1.0f + expf(-v));  // silu
+    case 11: return v * fminf(1.0f, fmaxf(0.0f, (v + 3.0f) / 6.0f));
+    case 12: return fminf(1.0f, fmaxf(0.0f, (v + 3.0f) / 6.0f));
+    case 13: return expf(v);
+    case 14: return expf(v) - 1.0f;
+    case 15: return (v > 20.0f) ? v : logf(1.0f + expf(v));  // softplus
+    case 16: return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+    case 18: return floorf(v);
+    case 19: return ceilf(v);
+    case 20: return roundf(v);
+    case 21: return truncf(v);
+    case 100: return p2 == 0.0f ? v * p1 : v * p1 + p2;  // ggml_vec_scale_f32 / ggml_vec_mad1_f32
+    case 101: return p1;
+    case 102: {  // MAX(MIN(x, max), min)
+        const float t = v < p2 ? v : p2;
+        return t > p1 ? t : p1;
+    }
+    case 103: return ((v > 0.f) ? v : 0.f) + p1 * ((v < 0.f) ? v : 0.f);
+    case 104: return v * v;
+    case 105: return sqrtf(v);
+    case 106: return sinf(v);
+    case 107: return cosf(v);
+    case 108: return logf(v);
+    default: return v;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_core_unary(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &d = a.op.t[4];
+    const int code = (int)a.op.x[0];
+    const float p1 = __int_as_float((int)a.op.x[1]), p2 = __int_as_float((int)a.op.x[2]);
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, d, i1, i2, i3);
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    char *dr = a.dst + offs(d, 0, i1, i2, i3);
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= d.ne[0]) break;
+        const float v = ld_f(xr + i0 * x.nb[0], x.ty);
+        // f16 data reads the CPU's gelu table for every value (no +-10 cut-offs)
+        st_f(dr + i0 * d.nb[0], d.ty, code == 8 && x.ty == TLH_TYPE_F16 ? gelu_f16(v) : unary_val(code, v, p1, p2));
+    }
+}
+
+// ----------------------------------------------------------------- get_rows
+// ops.cpp get_rows: dst [ne0, n_idx, i11, i12] row (i, j, k) = src0 row
+// idx[i, j, k] of src0 plane (j, k); quantized rows are dequantized.
+template <int ST>
+__global__ void __launch_bounds__(256) k_core_get_rows(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &ix = a.op.t[1], &d = a.op.t[4];
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, d, i1, i2, i3);
+    int64_t r = ld_idx(a.s1 + i1 * ix.nb[0] + i2 * ix.nb[1] + i3 * ix.nb[2], ix.ty);
+    r = r < 0 ? 0 : r >= x.ne[1] ? x.ne[1] - 1 : r;  // an index outside src0 reads its nearest row
+    const char *xr = a.s0 + r * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
+    char *dr = a.dst + offs(d, 0, i1, i2, i3);
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= d.ne[0]) break;
+        float v;
+        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16)
+            v = ld_f(xr + i0 * x.nb[0], ST);
+        else
+            v = dequant_elem<ST>((const uint8_t *)xr, i0);
+        st_f(dr + i0 * d.nb[0], d.ty, v);
+    }
+}
+
+// ----------------------------------------------------------------- set_rows
+// ops.cpp set_rows: src0 row (i, j, k) goes to dst row idx[i, j % n1, k % n2]
+// of dst plane (j, k), converted to dst's type.
+__global__ void __launch_bounds__(256) k_core_set_rows(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &ix = a.op.t[1], &d = a.op.t[4];
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, x, i1, i2, i3);
+    const int64_t r = ld_idx(a.s1 + i1 * ix.nb[0] + (i2 % ix.ne[1]) * ix.nb[1] + (i3 % ix.ne[2]) * ix.nb[2], ix.ty);
+    if (r < 0 || r >= d.ne[1]) return;  // an index outside dst writes nothing
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    char *dr = a.dst + r * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3];
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= x.ne[0]) break;
+        st_f(dr + i0 * d.nb[0], d.ty, ld_f(xr + i0 * x.nb[0], x.ty));
+    }
+}
+
+// ---------------------------------------------------------------------- cpy
+// ops.cpp dup / cpy: element i of src0 in row-major order to element i of dst
+// (shapes may differ, element counts are equal), converted; quantized sources
+// dequantized (src0 rows of whole blocks).
+template <int ST>
+__global__ void __launch_bounds__(256) k_core_cpy(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &d = a.op.t[4];
+    int64_t i1, i2, i3;
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
+    row_coords(row, x, i1, i2, i3);
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= x.ne[0]) break;
+        float v;
+        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16)
+            v = ld_f(xr + i0 * x.nb[0], ST);
+        else
+            v = dequant_elem<ST>((const uint8_t *)xr, i0);
+        // linear index in src0's logical order -> dst coordinates
+        int64_t li = row * x.ne[0] + i0;
+        const int64_t j0 = li % d.ne[0];
+        li /= d.ne[0];
+        const int64_t j1 = li % d.ne[1];
+        li /= d.ne[1];
+        const int64_t j2 = li % d.ne[2], j3 = li / d.ne[2];
+        st_f(a.dst + offs(d, j0, j1, j2, j3), d.ty, v);
+    }
+}
+
+// ---------------------------------------------------------------------- glu
+// ops.cpp ggml_compute_forward_{reglu,geglu,swiglu,geglu_erf,geglu_quick}_f32
+// with vec.h's ggml_vec_*glu_f32: y = act(x) * g over nc = ne0 of dst; x and g
+// are src0 and src1 (split form) or the two halves of a src0 row (x first
+// unless swapped). Codes are ggml_glu_op: 0 reglu, 1 geglu, 2 swiglu,
+// 4 geglu_erf, 5 geglu_quick.
+__device__ __forceinline__ float glu_val(int code, float x, float g) {
+    switch (code) {
+    case 0: return (x > 0.f) ? x * g : 0.f;
+    case 1: return x <= -10.0f ? 0.0f : x >= 10.0f ? x * g : gelu_f16(h2f(f2h(x))) * g;
+    case 2: return (x / (1.0f + expf(-x))) * g;
+    case 4: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)) * g;
+    default: return gelu_quick_tab(x) * g;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &y = a.op.t[1], &d = a.op.t[4];
+    const int code = (int)a.op.x[0];
+    const bool swapped = a.op.x[1] != 0;
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, d, i1, i2, i3);
+    const int64_t nc = d.ne[0];
+    const float *xr = (const float *)(a.s0 + offs(x, 0, i1, i2, i3));
+    const float *gr;
+    if (a.s1) {
+        gr = (const float *)(a.s1 + offs(y, 0, i1, i2, i3));
+    } else {
+        gr = xr + (swapped ? 0 : nc);
+        xr += swapped ? nc : 0;
+    }
+    float *dr = (float *)(a.dst + offs(d, 0, i1, i2, i3));
+    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < CORE_CHUNK / 256; ++u) {
+        const int64_t i0 = e0 + 256 * u;
+        if (i0 >= nc) break;
+        dr[i0] = glu_val(code, xr[i0], gr[i0]);
+    }
+}
+
+// ------------------------------------------------------------ block reduces
+template <typename T> __device__ __forceinline__ T wave_sum_t(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+// sum over the 256 threads, order fixed by the lane and wave layout
+template <typename T> __device__ __forceinline__ T block_sum_t(T v, T *sh) {
+    v = wave_sum_t(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const T r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ float block_max_f(float v, float *sh) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return r;
+}
+
+// --------------------------------------------------------------------- norm
+// ops.cpp rms_norm_f32 (:3795-3840): sum of x*x (f32 products) in double,
+// mean = (float)(sum / n), scale = 1/sqrtf(mean + eps), y = x * scale.
+// ops.cpp norm_f32 (:3698-3740): mean = (float)sum / n with the sum in double;
+// the centred variance as ggml_vec_cvar_f32's x86-64 (SSE2) build forms it
+// (vec.cpp): per group of four, ((d0^2 + d1^2) + (d2^2 + d3^2)) in f32 added
+// in double, the n % 4 tail element by element, divided by n in double.
+// Contiguous f32 rows; one workgroup per row, so only the order of the double
+// additions differs from the CPU's.
+__global__ void __launch_bounds__(256) k_core_norm(const CoreArgs a) {
+    __shared__ double shd[4];
+    const tlh_tensor &x = a.op.t[0], &d = a.op.t[4];
+    const bool rms = a.op.x[0] != 0;
+    const float eps = __int_as_float((int)a.op.x[1]);
+    int64_t i1, i2, i3;
+    row_coords(blockIdx.x + (int64_t)gridDim.x * blockIdx.y, x, i1, i2, i3);
+    const float *xr = (const float *)(a.s0 + offs(x, 0, i1, i2, i3));
+    float *dr = (float *)(a.dst + offs(d, 0, i1, i2, i3));
+    const int64_t n = x.ne[0];
+    float mean = 0.0f;
+    double s2 = 0.0;
+    if (rms) {
+        for (int64_t i = threadIdx.x; i < n; i += 256) s2 += (double)(xr[i] * xr[i]);
+    } else {
+        double s = 0.0;
+        for (int64_t i = threadIdx.x; i < n; i += 256) s += (double)xr[i];
+        mean = (float)block_sum_t(s, shd) / (float)n;
+        const int64_t n4 = n / 4;
+        for (int64_t g = threadIdx.x; g < n4; g += 256) {
+            const float *v = xr + 4 * g;  // rows need not be 16-byte aligned
+            const float d0 = v[0] - mean, d1 = v[1] - mean, d2 = v[2] - mean, d3 = v[3] - mean;
+            s2 += (double)((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3));
+        }
+        for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += 256) {
+            const float v = xr[i] - mean;
+            s2 += (double)(v * v);
+        }
+    }
+    const float var = (float)(block_sum_t(s2, shd) / (double)n);
+    const float scale = 1.0f / sqrtf(var + eps);
+    for (int64_t i = threadIdx.x; i < n; i += 256) dr[i] = (xr[i] - mean) * scale;
+}
+
+// ----------------------------------------------------------------- soft_max
+// ops.cpp soft_max_f32: v = x * scale + slope * mask, y = exp(v - max) / sum
+// (sum in double), slope from ALiBi (m0, m1, n_head_log2) per head i2.
+// One workgroup per row.
+__global__ void __launch_bounds__(256) k_core_soft_max(const CoreArgs a) {
+    __shared__ float shf[4];
+    __shared__ double shd[4];
+    const tlh_tensor &x = a.op.t[0], &m = a.op.t[1], &d = a.op.t[4];
+    const float scale = __int_as_float((int)a.op.x[0]), max_bias = __int_as_float((int)a.op.x[1]);
+    const float m0 = __int_as_float((int)a.op.x[2]), m1 = __int_as_float((int)a.op.x[3]);
+    const int nhl2 = (int)a.op.x[4];
+    int64_t i1, i2, i3;
+    row_coords(blockIdx.x + (int64_t)gridDim.x * blockIdx.y, x, i1, i2, i3);
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    const char *mr = a.s1 ? a.s1 + i1 * m.nb[1] + (i2 % m.ne[2]) * m.nb[2] + (i3 % m.ne[3]) * m.nb[3] : nullptr;
+    char *dr = a.dst + offs(d, 0, i1, i2, i3);
+    float slope = 1.0f;
+    if (max_bias > 0.0f) {
+        const int h = (int)i2;
+        slope = h < nhl2 ? powf(m0, (float)(h + 1)) : powf(m1, (float)(2 * (h - nhl2) + 1));
+    }
+    const int64_t n = x.ne[0];
+    auto val = [&](int64_t i) {
+        float v = ld_f(xr + i * x.nb[0], x.ty) * scale;
+        if (mr) v += slope * ld_f(mr + i * m.nb[0], m.ty);
+        return v;
+    };
+    float mx = -INFINITY;
+    for (int64_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, val(i));
+    mx = block_max_f(mx, shf);
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) s += (double)expf(val(i) - mx);
+    s = block_sum_t(s, shd);
+    const float inv = (float)(1.0 / s);
+    for (int64_t i = threadIdx.x; i < n; i += 256)
+        st_f(dr + i * d.nb[0], d.ty, mx == -INFINITY ? 0.0f : expf(val(i) - mx) * inv);
+}
+
+// ------------------------------------------------------------------- argmax
+// ops.cpp argmax_f32 / vec.h ggml_vec_argmax_f32: the last index of the
+// maximum (max = MAX(max, x); if max == x then idx = i). One workgroup per row.
+__global__ void __launch_bounds__(256) k_core_argmax(const CoreArgs a) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const tlh_tensor &x = a.op.t[0], &d = a.op.t[4];
+    const int64_t row = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+    const char *xr = a.s0 + row * x.nb[1];
+    float best = -INFINITY;
+    int bi = 0;
+    for (int64_t i = threadIdx.x; i < x.ne[0]; i += 256) {
+        const float v = ld_f(xr + i * x.nb[0], x.ty);
+        if (v >= best) {
+            best = v;
+            bi = (int)i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > best || (ov == best && oi > bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] > bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        *(int32_t *)(a.dst + row * d.nb[0]) = bi;
+    }
+}
+
+// --------------------------------------------------------------------- rope
+// ops.cpp rope_flt (:5953-6100; normal mode 0: pairs (2p, 2p+1); neox mode
+// 2: (p, p + n_dims/2)) with ggml's YaRN angle (rope_yarn, :5829-5844):
+// theta = pos * theta_scale^p / freq_factor, mixed with its interpolation by
+// the ramp over [corr0, corr1] when ext_factor != 0; dims past n_dims pass
+// through. One thread per pair.
+__global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
+    const tlh_tensor &x = a.op.t[0], &ps = a.op.t[1], &d = a.op.t[4];
+    const int n_dims = (int)a.op.x[0], mode = (int)a.op.x[1];
+    const float freq_scale = __int_as_float((int)a.op.x[2]), ext_factor = __int_as_float((int)a.op.x[3]);
+    const float attn_factor = __int_as_float((int)a.op.x[4]), theta_scale = __int_as_float((int)a.op.x[5]);
+    const float corr0 = __int_as_float((int)a.op.x[6]), corr1 = __int_as_float((int)a.op.x[7]);
+    const bool has_ff = a.op.x[8] != 0;
+    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
+    if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
+    int64_t i1, i2, i3;
+    row_coords(row, x, i1, i2, i3);
+    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    char *dr = a.dst + offs(d, 0, i1, i2, i3);
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;  // pair index
+    if (p >= x.ne[0] / 2) return;
+    if (2 * p >= n_dims) {  // past the rotated dims: copy both elements of the pair
+        st_f(dr + 2 * p * d.nb[0], d.ty, ld_f(xr + 2 * p * x.nb[0], x.ty));
+        st_f(dr + (2 * p + 1) * d.nb[0], d.ty, ld_f(xr + (2 * p + 1) * x.nb[0], x.ty));
+        return;
+    }
+    const float ff = has_ff ? *(const float *)(a.s2 + p * 4) : 1.0f;
+    // theta_p = pos * theta_scale^p by repeated f32 products, in the order
+    // ggml_rope_cache_init (ops.cpp:5846-5860) forms it, so the angles match
+    // the CPU's bit for bit (a powf would differ in the last bits, which at
+    // positions in the thousands moves the angle visibly)
+    float tp = (float)*(const int32_t *)(a.s1 + i2 * ps.nb[0]);
+    for (int64_t k = 0; k < p; ++k) tp *= theta_scale;
+    const float theta_extrap = tp / ff;
+    float theta = freq_scale * theta_extrap;
+    float mscale = attn_factor;
+    if (ext_factor != 0.0f) {
+        const float y = ((float)p - corr0) / fmaxf(0.001f, corr1 - corr0);
+        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * ext_factor;
+        theta = freq_scale * theta_extrap * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+    }
+    const float cs = cosf(theta) * mscale, sn = sinf(theta) * mscale;
+    const int64_t ia = mode == 0 ? 2 * p : p;
+    const int64_t ib = mode == 0 ? 2 * p + 1 : p + n_dims / 2;
+    const float x0 = ld_f(xr + ia * x.nb[0], x.ty), x1 = ld_f(xr + ib * x.nb[0], x.ty);
+    st_f(dr + ia * d.nb[0], d.ty, x0 * cs - x1 * sn);
+    st_f(dr + ib * d.nb[0], d.ty, x0 * sn + x1 * cs);
+}
+
+// ------------------------------------------------------------------ launchers
+static dim3 row_grid(int64_t chunks, int64_t rows) {
+    // rows over (y, z) so that more than 65535 rows fit
+    const int64_t gy = rows < 65535 ? rows : 65535;
+    return dim3((unsigned)chunks, (unsigned)gy, (unsigned)((rows + gy - 1) / gy));
+}
+static dim3 red_grid(int64_t rows) {
+    const int64_t gx = rows < 2147483647 ? rows : 2147483647;
+    return dim3((unsigned)gx, 1, 1);
+}
+static int64_t nrows(const tlh_tensor &t) { return t.ne[1] * t.ne[2] * t.ne[3]; }
+
+tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,
+                       hipStream_t stream) {
+    CoreArgs a;
+    a.op = op;
+    a.s0 = (const char *)s0;
+    a.s1 = (const char *)s1;
+    a.s2 = (const char *)s2;
+    a.dst = (char *)dst;
+    const tlh_tensor &x = op.t[0], &d = op.t[4];
+    switch (kind) {
+    case TLH_CORE_BIN: {
+        const int64_t rows = nrows(d);
+        if (rows == 0 || d.ne[0] == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_bin, row_grid((d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows), dim3(256), 0,
+                           stream, a);
+        break;
+    }
+    case TLH_CORE_UNARY: {
+        const int64_t rows = nrows(d);
+        if (rows == 0 || d.ne[0] == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_unary, row_grid((d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows), dim3(256), 0,
+                           stream, a);
+        break;
+    }
+    case TLH_CORE_GET_ROWS: {
+        const int64_t rows = nrows(d);
+        if (rows == 0 || d.ne[0] == 0) return TLH_OK;
+        const dim3 g = row_grid((d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows);
+        switch (x.ty) {
+        case TLH_TYPE_F32: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_F32>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
+        }
+        break;
+    }
+    case TLH_CORE_SET_ROWS: {
+        const int64_t rows = nrows(x);
+        if (rows == 0 || x.ne[0] == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_set_rows, row_grid((x.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows), dim3(256), 0,
+                           stream, a);
+        break;
+    }
+    case TLH_CORE_CPY: {
+        const int64_t rows = nrows(x);
+        if (rows == 0 || x.ne[0] == 0) return TLH_OK;
+        const dim3 g = row_grid((x.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows);
+        switch (x.ty) {
+        case TLH_TYPE_F32: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_F32>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
+        }
+        break;
+    }
+    case TLH_CORE_NORM: {
+        const int64_t rows = nrows(x);
+        if (rows == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_norm, red_grid(rows), dim3(256), 0, stream, a);
+        break;
+    }
+    case TLH_CORE_SOFT_MAX: {
+        const int64_t rows = nrows(x);
+        if (rows == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_soft_max, red_grid(rows), dim3(256), 0, stream, a);
+        break;
+    }
+    case TLH_CORE_ARGMAX: {
+        const int64_t rows = x.ne[1];
+        if (rows == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_argmax, red_grid(rows), dim3(256), 0, stream, a);
+        break;
+    }
+    case TLH_CORE_GLU: {
+        const int64_t rows = nrows(d);
+        if (rows == 0 || d.ne[0] == 0) return TLH_OK;
+        hipLaunchKernelGGL(k_core_glu, row_grid((d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows), dim3(256), 0,
+                           stream, a);
+        break;
+    }
+    case TLH_CORE_ROPE: {
+        const int64_t rows = nrows(x);
+        if (rows == 0 || x.ne[0] < 2) return TLH_OK;
+        hipLaunchKernelGGL(k_core_rope, row_grid((x.ne[0] / 2 + 255) / 256, rows), dim3(256), 0, stream, a);
+        break;
+    }
+    default: return set_error(TLH_INVALID, "core: unknown kind %d", kind);
+    }
+    return check_launch("core");
+}
+
+}  // namespace tlh

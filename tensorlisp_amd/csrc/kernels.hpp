@@ -70,6 +70,10 @@ int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhk
                                  int64_t mask_rows);
 tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
 
+// core ops (core.hip): kind is a tlh_core_kind; op validated by the caller
+tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,
+                       hipStream_t stream);
+
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
                                   hipStream_t stream);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);

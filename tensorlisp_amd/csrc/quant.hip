@@ -142,50 +142,11 @@ __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__
 template <int WT>
 __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ w, int64_t K, int64_t rows,
                                                     int64_t w_row_bytes, float *__restrict__ y) {
-#pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= K * rows) return;
     const int64_t row = gid / K;
     const int64_t col = gid - row * K;
-    const uint8_t *r = w + row * w_row_bytes;
-    float out;
-    if constexpr (WT == TLH_TYPE_Q4_0) {
-        const uint8_t *b = r + (col / QK) * Q4_0_BYTES;
-        const int j = (int)(col % QK);
-        const float d = h2f(*(const uint16_t *)b);
-        const int code = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
-        out = (float)(code - 8) * d;
-    } else if constexpr (WT == TLH_TYPE_Q8_0) {
-        const uint8_t *b = r + (col / QK) * Q8_0_BYTES;
-        const float d = h2f(*(const uint16_t *)b);
-        out = (float)(int8_t)b[2 + col % QK] * d;
-    } else if constexpr (WT == TLH_TYPE_Q6_K) {
-        // element e of a 128-element half: low 4 bits in ql[l + 32 * (q & 1)]
-        // (high nibble for q >= 2), high 2 bits in qh[l] at 2q; e = 32q + l
-        const uint8_t *b = r + (col / QKK) * Q6_K_BYTES;
-        const int i = (int)(col % QKK);
-        const int h = i >> 7, e = i & 127, q = e >> 5, l = e & 31;
-        const uint8_t lo = b[64 * h + l + 32 * (q & 1)];
-        const uint8_t hi2 = b[128 + 32 * h + l];
-        const int code = (int)(((q >= 2 ? lo >> 4 : lo & 0x0f) | (((hi2 >> (2 * q)) & 3) << 4))) - 32;
-        const float d = h2f(*(const uint16_t *)(b + 208));
-        const int sc = (int)(int8_t)b[192 + 8 * h + (e >> 4)];
-        out = (d * (float)sc) * (float)code;
-    } else {
-        const uint8_t *b = r + (col / QKK) * Q4_K_BYTES;
-        const int i = (int)(col % QKK);
-        const int c = i / 64, pos = i % 64, hi = pos >= 32, l = pos & 31;
-        const uint32_t *s = (const uint32_t *)(b + 4);
-        int sc, mn;
-        q4k_scale_min(2 * c + hi, s[0], s[1], s[2], sc, mn);
-        const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
-        const uint8_t byte = b[16 + 32 * c + l];
-        const int code = hi ? byte >> 4 : byte & 0x0f;
-        const float d1 = d * (float)sc;
-        const float m1 = dmin * (float)mn;
-        out = d1 * (float)code - m1;
-    }
-    y[gid] = out;
+    y[gid] = dequant_elem<WT>(w + row * w_row_bytes, col);
 }
 
 // --------------------------------------------------------------- launchers

@@ -180,6 +180,115 @@ static tlh_status check_flash_attn(const tlh_op *op, bool has_mask, FlashAttnDes
     return TLH_OK;
 }
 
+// Validates a core-op node (tlh_core_kind) the way Ctx::lower and its helpers
+// (crates/kernels/src/cuda/lower.rs:175-500) refuse nodes, narrowed to what
+// core.hip runs: f32/f16 data, i32/i64 indices, quantized rows for GET_ROWS
+// and CPY.
+static bool data_ty(int t) { return t == TLH_TYPE_F32 || t == TLH_TYPE_F16; }
+static bool idx_ty(int t) { return t == 26 || t == 27; }
+static bool same_shape(const tlh_tensor &a, const tlh_tensor &b) {
+    for (int i = 0; i < 4; ++i)
+        if (a.ne[i] != b.ne[i]) return false;
+    return true;
+}
+static int64_t nel(const tlh_tensor &t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; }
+static bool rows_of_blocks(const tlh_tensor &t) {  // quantized tensor read by whole blocks
+    return weight_type_ok(t.ty) && t.ne[0] % block_elems(t.ty) == 0 && t.nb[0] == block_bytes(t.ty);
+}
+static bool elem_strides_ok(const tlh_tensor &t) {
+    const int64_t es = t.ty == TLH_TYPE_F16 ? 2 : t.ty == 27 ? 8 : 4;
+    for (int i = 0; i < 4; ++i)
+        if (t.nb[i] % es) return false;
+    return true;
+}
+
+static tlh_status check_core(int kind, const tlh_op *op, bool has1, bool has2) {
+    if (!op) return set_error(TLH_INVALID, "core: null op");
+    const tlh_tensor &a = op->t[0], &b = op->t[1], &c = op->t[2], &d = op->t[4];
+    for (int i = 0; i < 4; ++i)
+        if (a.ne[i] < 0 || b.ne[i] < 0 || d.ne[i] < 0) return set_error(TLH_INVALID, "core: negative extent");
+    auto unsup = [](const char *why) { return set_error(TLH_UNSUPPORTED, "core: %s", why); };
+    const bool a_data = data_ty(a.ty) && elem_strides_ok(a);
+    const bool d_data = data_ty(d.ty) && elem_strides_ok(d);
+    switch (kind) {
+    case TLH_CORE_BIN:
+        if (!a_data || !data_ty(b.ty) || !elem_strides_ok(b) || !d_data) return unsup("BIN: f32/f16 operands");
+        if (!same_shape(a, d)) return unsup("BIN: destination shape differs from src0");
+        for (int i = 0; i < 4 && nel(a) > 0; ++i)  // ggml_can_repeat: an empty src1 repeats to an empty src0
+            if (b.ne[i] == 0 || a.ne[i] % b.ne[i] != 0) return unsup("BIN: src1 does not repeat to src0");
+        if (op->x[0] < 0 || op->x[0] > 3) return set_error(TLH_INVALID, "core: BIN code %lld", (long long)op->x[0]);
+        return TLH_OK;
+    case TLH_CORE_UNARY: {
+        if (!a_data || !d_data) return unsup("UNARY: f32/f16 operands");
+        if (!same_shape(a, d)) return unsup("UNARY: destination shape differs from src0");
+        const int64_t code = op->x[0];
+        if (!((code >= 0 && code <= 16) || (code >= 18 && code <= 21) || (code >= 100 && code <= 108)))
+            return set_error(TLH_UNSUPPORTED, "core: unary op %lld", (long long)code);
+        return TLH_OK;
+    }
+    case TLH_CORE_NORM:
+        if (a.ty != TLH_TYPE_F32 || d.ty != TLH_TYPE_F32 || a.nb[0] != 4 || d.nb[0] != 4 || !elem_strides_ok(a) ||
+            !elem_strides_ok(d))
+            return unsup("NORM: f32 rows with unit element stride");
+        if (!same_shape(a, d)) return unsup("NORM: destination shape differs from src0");
+        return TLH_OK;
+    case TLH_CORE_GET_ROWS:
+        if (!(a_data || rows_of_blocks(a)) || !idx_ty(b.ty) || !elem_strides_ok(b) || !d_data)
+            return unsup("GET_ROWS: f32/f16/q4_0/q8_0/q4_K/q6_K rows, i32/i64 indices, f32/f16 destination");
+        if (d.ne[0] != a.ne[0] || d.ne[1] != b.ne[0] || d.ne[2] != b.ne[1] || d.ne[3] != b.ne[2] ||
+            a.ne[2] != b.ne[1] || a.ne[3] != b.ne[2] || (a.ne[1] == 0 && nel(d) > 0))
+            return unsup("GET_ROWS: shapes");
+        return TLH_OK;
+    case TLH_CORE_SET_ROWS:
+        if (!a_data || !idx_ty(b.ty) || !elem_strides_ok(b) || !d_data)
+            return unsup("SET_ROWS: f32/f16 rows, i32/i64 indices, f32/f16 destination");
+        if (d.ne[0] != a.ne[0] || d.ne[2] != a.ne[2] || d.ne[3] != a.ne[3] || b.ne[0] != a.ne[1] || b.ne[1] == 0 ||
+            b.ne[2] == 0 || a.ne[2] % b.ne[1] != 0 || a.ne[3] % b.ne[2] != 0)
+            return unsup("SET_ROWS: shapes");
+        return TLH_OK;
+    case TLH_CORE_CPY:
+        if (!(a_data || rows_of_blocks(a)) || !d_data) return unsup("CPY: f32/f16 (or quantized) to f32/f16");
+        if (nel(a) != nel(d)) return unsup("CPY: element counts differ");
+        return TLH_OK;
+    case TLH_CORE_ROPE: {
+        if (!a_data || !d_data || !same_shape(a, d)) return unsup("ROPE: f32/f16 operands of one shape");
+        const int64_t n_dims = op->x[0], mode = op->x[1];
+        if (mode != 0 && mode != 2) return unsup("ROPE: only normal and neox modes");
+        if (b.ty != 26 || b.ne[0] != a.ne[2] || b.nb[0] != 4) return unsup("ROPE: one i32 position per token");
+        if (n_dims <= 0 || n_dims > a.ne[0] || n_dims % 2) return set_error(TLH_INVALID, "core: ROPE n_dims");
+        if (op->x[8] && (!has2 || c.ty != TLH_TYPE_F32 || c.nb[0] != 4 || c.ne[0] < n_dims / 2))
+            return unsup("ROPE: frequency factors must be f32 [n_dims/2]");
+        return TLH_OK;
+    }
+    case TLH_CORE_SOFT_MAX:
+        if (a.ty != TLH_TYPE_F32 || !a_data || !d_data || !same_shape(a, d))
+            return unsup("SOFT_MAX: f32 source, f32/f16 destination of its shape");
+        if (has1 && (!data_ty(b.ty) || !elem_strides_ok(b) || b.ne[0] < a.ne[0] || b.ne[1] < a.ne[1] ||
+                     b.ne[2] == 0 || b.ne[3] == 0 || a.ne[2] % b.ne[2] || a.ne[3] % b.ne[3]))
+            return unsup("SOFT_MAX: mask must be f32/f16 [>= n, >= rows, broadcast]");
+        return TLH_OK;
+    case TLH_CORE_ARGMAX:
+        if (a.ty != TLH_TYPE_F32 || !a_data || d.ty != 26 || d.nb[0] != 4) return unsup("ARGMAX: f32 rows to i32");
+        if (a.ne[2] != 1 || a.ne[3] != 1 || d.ne[0] != a.ne[1] || a.ne[0] > INT32_MAX)
+            return unsup("ARGMAX: 2-D source, one i32 per row");
+        return TLH_OK;
+    case TLH_CORE_GLU: {
+        const bool rows_ok = a.ty == TLH_TYPE_F32 && d.ty == TLH_TYPE_F32 && a.nb[0] == 4 && d.nb[0] == 4 &&
+                             elem_strides_ok(a) && elem_strides_ok(d) &&
+                             (!has1 || (b.ty == TLH_TYPE_F32 && b.nb[0] == 4 && elem_strides_ok(b)));
+        if (!rows_ok) return unsup("GLU: f32 rows with unit element stride");
+        const int64_t code = op->x[0];
+        if (code < 0 || code > 5 || code == 3) return set_error(TLH_UNSUPPORTED, "core: glu op %lld", (long long)code);
+        if (has1 ? !(same_shape(a, b) && same_shape(a, d))
+                 : (a.ne[0] % 2 != 0 || d.ne[0] != a.ne[0] / 2 || d.ne[1] != a.ne[1] || d.ne[2] != a.ne[2] ||
+                    d.ne[3] != a.ne[3]))
+            return unsup("GLU: shapes");
+        return TLH_OK;
+    }
+    default: return set_error(TLH_INVALID, "core: unknown kind %d", kind);
+    }
+}
+
 extern "C" {
 
 const char *tlh_last_error(void) { return g_last_error.c_str(); }
@@ -490,6 +599,21 @@ tlh_status tlh_flash_attn_ext(const tlh_op *op, const void *q, const void *k, co
     if (need > 0 && ((uintptr_t)scratch & 7)) return set_error(TLH_INVALID, "flash_attn_ext: misaligned scratch");
     d.q = q, d.k = k, d.v = v, d.mask = mask, d.dst = dst, d.scratch = scratch;
     return launch_flash_attn(d, (hipStream_t)stream);
+}
+
+tlh_status tlh_core_check(int kind, const tlh_op *op, int has_src1, int has_src2) {
+    return check_core(kind, op, has_src1 != 0, has_src2 != 0);
+}
+
+tlh_status tlh_core(int kind, const tlh_op *op, const void *src0, const void *src1, const void *src2, void *dst,
+                    void *stream) {
+    const tlh_status st = check_core(kind, op, src1 != nullptr, src2 != nullptr);
+    if (st != TLH_OK) return st;
+    if (nel(op->t[4]) == 0 || (kind == TLH_CORE_SET_ROWS && nel(op->t[0]) == 0)) return TLH_OK;  // nothing to do
+    const bool needs1 = kind == TLH_CORE_BIN || kind == TLH_CORE_GET_ROWS || kind == TLH_CORE_SET_ROWS ||
+                        kind == TLH_CORE_ROPE;
+    if (!src0 || !dst || (needs1 && !src1)) return set_error(TLH_INVALID, "core: null tensor pointer");
+    return launch_core(kind, *op, src0, src1, src2, dst, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -33,6 +33,7 @@ EXPORTS = (
     "tlh_mul_mat_quantize", "tlh_mul_mat_compute",
     "tlh_quantize_act", "tlh_dequantize", "tlh_flash_attn_ext_scratch_bytes", "tlh_flash_attn_ext",
     "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
+    "tlh_core_check", "tlh_core",
 )
 
 
@@ -95,6 +96,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_paged_attention_scratch_bytes.argtypes = [C.POINTER(TlhPagedArgs), C.POINTER(C.c_size_t)]
     L.tlh_paged_attention.argtypes = [C.POINTER(TlhPagedArgs), vp, C.c_size_t, vp]
     L.tlh_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]
+    L.tlh_core_check.argtypes = [C.c_int, C.POINTER(TlhOp), C.c_int, C.c_int]
+    L.tlh_core.argtypes = [C.c_int, C.POINTER(TlhOp), vp, vp, vp, vp, vp]
     for name in EXPORTS:
         if name not in ("tlh_last_error", "tlh_status_name", "tlh_version"):
             getattr(L, name).restype = st
@@ -132,7 +135,7 @@ def ggml_tensor(ty: int, ne, nb=None) -> TlhTensor:
             be, bb = BLOCK[ty]
             nb0, nb1 = bb, ne[0] // be * bb
         else:
-            nb0 = 4 if ty == F32 else 2
+            nb0 = {F32: 4, F16: 2, 26: 4, 27: 8}[ty]  # f32, f16, i32, i64
             nb1 = nb0 * ne[0]
         nb = [nb0, nb1, nb1 * ne[1], nb1 * ne[1] * ne[2]]
     for i in range(4):
@@ -389,3 +392,223 @@ def reshape_and_cache(key, value, k_cache, v_cache, slots, num_kv_heads, block_s
     hs = key.shape[1] // num_kv_heads
     check(lib().tlh_reshape_and_cache(_ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slots), tokens,
                                       num_kv_heads, hs, block_size, _stream(stream)))
+
+
+# ------------------------------------------------------------------ core ops
+# The ops around MUL_MAT and attention in a decoder step, packed as the
+# reference's lowering packs them for its core kernels
+# (crates/kernels/src/cuda/lower.rs:175-500) and run by tlh_core.
+(CORE_BIN, CORE_UNARY, CORE_NORM, CORE_GET_ROWS, CORE_SET_ROWS, CORE_CPY, CORE_ROPE, CORE_SOFT_MAX, CORE_ARGMAX,
+ CORE_GLU) = range(1, 11)
+I32, I64 = 26, 27
+# ggml_unary_op codes (ggml.h) and the lowering's extra element-wise codes
+UNARY = {"abs": 0, "sgn": 1, "neg": 2, "step": 3, "tanh": 4, "elu": 5, "relu": 6, "sigmoid": 7, "gelu": 8,
+         "gelu_quick": 9, "silu": 10, "hardswish": 11, "hardsigmoid": 12, "exp": 13, "expm1": 14, "softplus": 15,
+         "gelu_erf": 16, "floor": 18, "ceil": 19, "round": 20, "trunc": 21, "scale": 100, "fill": 101,
+         "clamp": 102, "leaky_relu": 103, "sqr": 104, "sqrt": 105, "sin": 106, "cos": 107, "log": 108}
+# ggml_glu_op codes (ggml.h:623-630); swiglu_oai is not supported
+GLU = {"reglu": 0, "geglu": 1, "swiglu": 2, "geglu_erf": 4, "geglu_quick": 5}
+
+_libm = None
+
+
+def _f32_fn(name: str):
+    """The C library's single-precision `name` (powf, logf, ...): the host-side
+    parameters below are derived with the same f32 functions the CPU backend
+    and the reference's lowering call, so they match bit for bit."""
+    global _libm
+    if _libm is None:
+        _libm = C.CDLL("libm.so.6")
+    f = getattr(_libm, name)
+    f.restype = C.c_float
+    f.argtypes = [C.c_float] * (2 if name == "powf" else 1)
+    return f
+
+
+def _f32(x) -> float:
+    import struct
+
+    return struct.unpack("<f", struct.pack("<f", x))[0]
+
+
+def core_type(t) -> int:
+    import torch
+
+    return {torch.float32: F32, torch.float16: F16, torch.int32: I32, torch.int64: I64}.get(t.dtype, -1)
+
+
+def quant_desc(t, wtype: int, k: int) -> TlhTensor:
+    """The ggml descriptor of quantized rows held as a uint8 torch tensor of shape
+    (..., rows, row_bytes): ne [k, rows, ...], nb from the tensor's byte strides."""
+    rb = row_bytes(wtype, k)
+    if t.shape[-1] != rb or t.stride(-1) != 1:
+        raise ValueError(f"rows must be {rb} contiguous bytes for {TYPE_NAMES[wtype]} k={k}")
+    lead = list(t.shape[:-1])[::-1] + [1] * (4 - t.dim())
+    nbs = [s for s in list(t.stride()[:-1])[::-1]]
+    while len(nbs) < 3:
+        nbs.append(nbs[-1] * lead[len(nbs) - 1] if nbs else rb)
+    return ggml_tensor(wtype, [k] + lead[:3], [BLOCK[wtype][1]] + nbs[:3])
+
+
+def core_op(srcs, dst, x=()) -> TlhOp:
+    """t[0..2] = the sources (torch tensors, TlhTensor descriptors or None),
+    t[4] = dst, x[] = the op's parameters."""
+    op = TlhOp()
+    for i, t in enumerate(srcs):
+        if t is None:
+            continue
+        op.t[i] = t if isinstance(t, TlhTensor) else tensor_desc(t, core_type(t))
+    op.t[4] = dst if isinstance(dst, TlhTensor) else tensor_desc(dst, core_type(dst))
+    for i, v in enumerate(x):
+        op.x[i] = v
+    return op
+
+
+class CoreOp:
+    """One core node, validated once (tlh_core_check) and run on each call."""
+
+    def __init__(self, kind: int, op: TlhOp, has_src1: bool, has_src2: bool):
+        self.kind, self.op = kind, op
+        check(lib().tlh_core_check(kind, C.byref(op), int(has_src1), int(has_src2)))
+
+    def __call__(self, src0, src1, src2, dst, stream=None):
+        p = lambda t: _ptr(t) if t is not None else None  # noqa: E731
+        check(lib().tlh_core(self.kind, C.byref(self.op), p(src0), p(src1), p(src2), _ptr(dst), _stream(stream)))
+        return dst
+
+
+def _run(kind, srcs, dst, x=(), descs=None, stream=None):
+    op = core_op(descs if descs is not None else srcs, dst, x)
+    s = list(srcs) + [None] * (3 - len(srcs))
+    return CoreOp(kind, op, s[1] is not None, s[2] is not None)(s[0], s[1], s[2], dst, stream)
+
+
+def _out(like, out, dtype=None):
+    import torch
+
+    return out if out is not None else torch.empty(like.shape, dtype=dtype or like.dtype, device=like.device)
+
+
+def binary(code: int, a, b, out=None, stream=None):
+    """ADD/SUB/MUL/DIV (code 0..3) with b repeated to a's shape (lower.rs:219-248)."""
+    return _run(CORE_BIN, [a, b], _out(a, out), (code,), stream=stream)
+
+
+def add(a, b, out=None, stream=None):
+    return binary(0, a, b, out, stream)
+
+
+def mul(a, b, out=None, stream=None):
+    return binary(2, a, b, out, stream)
+
+
+def unary(op, a, p1: float = 0.0, p2: float = 0.0, out=None, stream=None):
+    """A ggml unary op or the lowering's element-wise extras (lower.rs:250-290),
+    by name or code: scale (p1 s, p2 b), fill (p1), clamp (p1 min, p2 max),
+    leaky_relu (p1 slope)."""
+    code = UNARY[op] if isinstance(op, str) else int(op)
+    return _run(CORE_UNARY, [a], _out(a, out), (code, _f32_bits(p1), _f32_bits(p2)), stream=stream)
+
+
+def norm(a, eps: float, rms: bool = False, out=None, stream=None):
+    """ggml_norm / ggml_rms_norm over ne0 (lower.rs:292-312)."""
+    return _run(CORE_NORM, [a], _out(a, out), (int(rms), _f32_bits(eps)), stream=stream)
+
+
+def rms_norm(a, eps: float, out=None, stream=None):
+    return norm(a, eps, True, out, stream)
+
+
+def get_rows(a, idx, wtype: int = None, k: int = None, out=None, stream=None):
+    """ggml_get_rows: out (i3, i2, i1) row = a's row idx[i3, i2, i1] of plane
+    (i2, i3). `a` is f32/f16, or quantized rows (uint8, (..., rows, row_bytes))
+    with `wtype` and their element count `k`. out is f32 (..., n_idx, ne0)."""
+    import torch
+
+    ad = quant_desc(a, wtype, k) if wtype is not None else tensor_desc(a, core_type(a))
+    ne0 = k if wtype is not None else a.shape[-1]
+    if out is None:
+        out = torch.empty(tuple(idx.shape) + (ne0,), dtype=torch.float32, device=idx.device)
+    return _run(CORE_GET_ROWS, [a, idx], out, descs=[ad, idx], stream=stream)
+
+
+def set_rows(dst, src, idx, stream=None):
+    """ggml_set_rows: src row (i3, i2, i1) to dst row idx[i3 % n2, i2 % n1, i1]."""
+    return _run(CORE_SET_ROWS, [src, idx], dst, stream=stream)
+
+
+def cpy(src, dst, wtype: int = None, k: int = None, stream=None):
+    """ggml_cpy / ggml_cont / ggml_dup: element i of src (row-major over ggml's
+    ne) to element i of dst, converted to dst's type."""
+    sd = quant_desc(src, wtype, k) if wtype is not None else tensor_desc(src, core_type(src))
+    return _run(CORE_CPY, [src], dst, descs=[sd], stream=stream)
+
+
+def rope_params(n_dims: int, mode: int, n_ctx_orig: int, freq_base: float, freq_scale: float, ext_factor: float,
+                attn_factor: float, beta_fast: float, beta_slow: float, has_ff: bool):
+    """x[] of Ctx::rope (lower.rs:422-466): the YaRN corr dims of
+    ggml_rope_yarn_corr_dims (ggml.c:4369-4381) and theta_scale =
+    freq_base^(-2/n_dims), all in f32."""
+    import numpy as np
+
+    powf, logf = _f32_fn("powf"), _f32_fn("logf")
+    f = np.float32
+    with np.errstate(all="ignore"):  # beta 0 or n_ctx_orig 0 give inf / nan, as in C
+        def corr(beta):
+            ratio = f(n_ctx_orig) / (f(beta) * f(2.0) * f(np.pi))
+            return f(f(n_dims) * f(logf(float(ratio)))) / f(f(2.0) * f(logf(freq_base)))
+
+        start, end = np.floor(corr(beta_fast)), np.ceil(corr(beta_slow))
+    c0 = 0.0 if 0.0 > start else float(start)  # MAX(0, start) and MIN(n_dims - 1, end) of ggml.c
+    c1 = float(n_dims - 1) if n_dims - 1 < end else float(end)
+    ts = powf(freq_base, _f32(-2.0 / n_dims))
+    return (n_dims, mode, _f32_bits(freq_scale), _f32_bits(ext_factor), _f32_bits(attn_factor), _f32_bits(ts),
+            _f32_bits(c0), _f32_bits(c1), int(has_ff))
+
+
+def rope(a, pos, n_dims: int, mode: int = 0, n_ctx_orig: int = 0, freq_base: float = 10000.0,
+         freq_scale: float = 1.0, ext_factor: float = 0.0, attn_factor: float = 1.0, beta_fast: float = 32.0,
+         beta_slow: float = 1.0, freq_factors=None, out=None, stream=None):
+    """ggml_rope_ext on a (ggml [ne0, heads, tokens, ne3]) with i32 positions [tokens]."""
+    x = rope_params(n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor, beta_fast,
+                    beta_slow, freq_factors is not None)
+    return _run(CORE_ROPE, [a, pos, freq_factors], _out(a, out), x, stream=stream)
+
+
+def soft_max_params(n_head: int, scale: float, max_bias: float):
+    """x[] of Ctx::soft_max (lower.rs:314-341): scale, max_bias, m0, m1, n_head_log2."""
+    import math
+
+    powf = _f32_fn("powf")
+    nhl2 = 1 << int(math.floor(math.log2(n_head))) if n_head > 0 else 1
+    m0 = powf(2.0, _f32(_f32(-max_bias) / nhl2))
+    m1 = powf(2.0, _f32(_f32(-_f32(max_bias / 2.0)) / nhl2))
+    return (_f32_bits(scale), _f32_bits(max_bias), _f32_bits(m0), _f32_bits(m1), nhl2)
+
+
+def soft_max(a, mask=None, scale: float = 1.0, max_bias: float = 0.0, out=None, stream=None):
+    """ggml_soft_max_ext over ne0 of f32 a, with an optional f16/f32 mask
+    (ggml [ne0, >= rows, broadcast over heads / batches])."""
+    n_head = a.shape[-3] if a.dim() >= 3 else 1
+    return _run(CORE_SOFT_MAX, [a, mask], _out(a, out), soft_max_params(n_head, scale, max_bias), stream=stream)
+
+
+def argmax(a, out=None, stream=None):
+    """ggml_argmax of f32 a (rows, n) -> i32 (rows,): the last index of each row's maximum."""
+    import torch
+
+    if out is None:
+        out = torch.empty((a.shape[0],), dtype=torch.int32, device=a.device)
+    return _run(CORE_ARGMAX, [a], out, stream=stream)
+
+
+def glu(op, a, b=None, swapped: bool = False, out=None, stream=None):
+    """GGML_OP_GLU on f32 rows: act(x) * g with x, g = a, b (ggml_glu_split) or
+    the two halves of a's rows (ggml_glu; x first unless swapped)."""
+    import torch
+
+    code = GLU[op] if isinstance(op, str) else int(op)
+    if out is None:
+        shape = tuple(a.shape) if b is not None else tuple(a.shape[:-1]) + (a.shape[-1] // 2,)
+        out = torch.empty(shape, dtype=torch.float32, device=a.device)
+    return _run(CORE_GLU, [a, b], out, (code, int(swapped)), stream=stream)

@@ -31,8 +31,14 @@ these are the reference's outputs on fixed inputs, captured once:
                    (refs.FA_CASES, native.rs:156-345), 8 CPU threads, outputs of the
                    first and last 6 queries; inputs are regenerated from the
                    stored seeds by refs.fa_case_inputs
+  core.npz         the ops around them in a decoder step (add/sub/mul/div, every
+                   unary op, norm/rms_norm, get_rows of every weight type,
+                   set_rows, cpy, rope_ext normal/neox/YaRN, soft_max_ext,
+                   argmax) on refs.core_cases(): the reference tests' shapes and
+                   inputs (native.rs:109-498) and decoder-sized ones; inputs are
+                   regenerated from seeds, the file keeps the outputs
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | core]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -46,7 +52,8 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, fa_case_inputs, fp16_probe_values, xorshift_noise  # noqa: E402
+from refs import (FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, core_cases, core_ref, fa_case_inputs,  # noqa: E402
+                  fp16_probe_values, xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
 
 
@@ -110,8 +117,15 @@ def q6_K_golden(ref) -> None:
     np.savez_compressed(HERE / "q6_K.npz", **out)
 
 
+def core_golden(ref) -> None:
+    np.savez_compressed(HERE / "core.npz", **{c["name"]: core_ref(ref, c) for c in core_cases()})
+
+
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["core"]:  # only the core-op fixture
+        core_golden(ref)
+        return
     if sys.argv[1:] == ["flash_attn_ext"]:  # only the FLASH_ATTN_EXT fixture
         flash_attn_ext_golden(ref)
         return
@@ -178,6 +192,7 @@ def main() -> None:
     np.savez_compressed(HERE / "flash_attn.npz", **out)
     flash_attn_ext_golden(ref)
     q6_K_golden(ref)
+    core_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

@@ -59,6 +59,38 @@ def _i64p(a: np.ndarray):
     return a.ctypes.data_as(C.POINTER(C.c_int64))
 
 
+I32, I64 = 26, 27
+NP_OF = {F32: np.float32, F16: np.uint16, I32: np.int32, I64: np.int64}
+
+
+class TlqT(C.Structure):
+    """tlq_t of oracle/tlq_oracle.h: a ggml tensor view over caller memory."""
+    _fields_ = [("data", C.c_void_p), ("ne", C.c_int64 * 4), ("nb", C.c_int64 * 4), ("ty", C.c_int)]
+
+
+def tlq_t(a: np.ndarray, ty: int, k: int = None) -> TlqT:
+    """The view of numpy array `a` (shape = ggml ne reversed, any strides) as
+    ggml type `ty`; quantized rows are uint8 (..., rows, row_bytes) with `k`
+    elements per row."""
+    t = TlqT()
+    t.data = a.ctypes.data
+    if ty in BLOCK:
+        assert a.dtype == np.uint8 and a.shape[-1] == row_bytes(ty, k) and a.strides[-1] == 1
+        lead = list(a.shape[:-1])[::-1]
+        st = list(a.strides[:-1])[::-1]
+        while len(lead) < 3:
+            st.append(st[-1] * lead[-1] if st else a.shape[-1])
+            lead.append(1)
+        ne, nb = [k] + lead[:3], [BLOCK[ty][1]] + st[:3]
+    else:
+        assert a.dtype == NP_OF[ty], (a.dtype, ty)
+        ne, nb = list(_ne(a)), list(_nb(a))
+    for i in range(4):
+        t.ne[i], t.nb[i] = int(ne[i]), int(nb[i])
+    t.ty = ty
+    return t
+
+
 class Oracle:
     def __init__(self, path: Path = ORACLE_SO):
         if not path.exists():
@@ -87,6 +119,17 @@ class Oracle:
         L.tlq_flash_attn_ext.argtypes = [vp, arr4, arr4, vp, arr4, arr4, vp, arr4, arr4, vp, arr4, arr4, vp, arr4,
                                          C.c_float, C.c_float, C.c_float, C.c_int]
         L.tlq_flash_attn_ext.restype = C.c_int
+        tp = C.POINTER(TlqT)
+        L.tlq_core_bin.argtypes = [C.c_int, tp, tp, tp]
+        L.tlq_core_unary.argtypes = [C.c_int, C.c_float, C.c_float, tp, tp]
+        L.tlq_core_norm.argtypes = [C.c_int, C.c_float, tp, tp]
+        L.tlq_core_get_rows.argtypes = [tp, tp, tp]
+        L.tlq_core_set_rows.argtypes = [tp, tp, tp]
+        L.tlq_core_cpy.argtypes = [tp, tp]
+        L.tlq_core_rope.argtypes = [C.c_int, C.c_int, C.c_int] + [C.c_float] * 6 + [tp, vp, vp, tp]
+        L.tlq_core_soft_max.argtypes = [C.c_float, C.c_float, tp, tp, tp]
+        L.tlq_core_argmax.argtypes = [tp, vp]
+        L.tlq_core_glu.argtypes = [C.c_int, C.c_int, tp, tp, tp]
         L.tlq_gather_kv.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp]
 
     # -- fp16
@@ -183,6 +226,71 @@ class Oracle:
         assert rc == 0, rc
         return out
 
+    # ----------------------------------------------------------- core ops
+    # numpy arrays shaped as ggml's ne reversed: f32 float32, f16 uint16 bits,
+    # i32/i64 indices; the destination type is F32 unless given.
+    def core_bin(self, code: int, a, ta: int, b, tb: int, td: int = F32) -> np.ndarray:
+        d = np.zeros(a.shape, NP_OF[td])
+        self.lib.tlq_core_bin(code, C.byref(tlq_t(a, ta)), C.byref(tlq_t(b, tb)), C.byref(tlq_t(d, td)))
+        return d
+
+    def core_unary(self, code: int, a, ta: int, p1: float = 0.0, p2: float = 0.0, td: int = F32) -> np.ndarray:
+        d = np.zeros(a.shape, NP_OF[td])
+        self.lib.tlq_core_unary(code, p1, p2, C.byref(tlq_t(a, ta)), C.byref(tlq_t(d, td)))
+        return d
+
+    def core_norm(self, rms: bool, eps: float, a) -> np.ndarray:
+        d = np.zeros(a.shape, np.float32)
+        self.lib.tlq_core_norm(int(rms), eps, C.byref(tlq_t(a, F32)), C.byref(tlq_t(d, F32)))
+        return d
+
+    def core_get_rows(self, a, ta: int, idx, ti: int, k: int = None, td: int = F32) -> np.ndarray:
+        ne0 = k if ta in BLOCK else a.shape[-1]
+        d = np.zeros(tuple(idx.shape) + (ne0,), NP_OF[td])
+        self.lib.tlq_core_get_rows(C.byref(tlq_t(a, ta, k)), C.byref(tlq_t(idx, ti)), C.byref(tlq_t(d, td)))
+        return d
+
+    def core_set_rows(self, dst, td: int, src, ts: int, idx, ti: int) -> np.ndarray:
+        d = np.array(dst, copy=True)
+        self.lib.tlq_core_set_rows(C.byref(tlq_t(src, ts)), C.byref(tlq_t(idx, ti)), C.byref(tlq_t(d, td)))
+        return d
+
+    def core_cpy(self, a, ta: int, shape, td: int, k: int = None) -> np.ndarray:
+        d = np.zeros(shape, NP_OF[td])
+        self.lib.tlq_core_cpy(C.byref(tlq_t(a, ta, k)), C.byref(tlq_t(d, td)))
+        return d
+
+    def core_rope(self, a, ta: int, pos, n_dims: int, mode: int, n_ctx_orig: int, freq_base: float,
+                  freq_scale: float, ext_factor: float, attn_factor: float, beta_fast: float, beta_slow: float,
+                  ff=None) -> np.ndarray:
+        d = np.zeros(a.shape, NP_OF[ta])
+        pos = np.ascontiguousarray(pos, np.int32)
+        ffp = None
+        if ff is not None:
+            ff = np.ascontiguousarray(ff, np.float32)
+            ffp = _p(ff)
+        self.lib.tlq_core_rope(mode, n_dims, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor, beta_fast,
+                               beta_slow, C.byref(tlq_t(a, ta)), _p(pos), ffp, C.byref(tlq_t(d, ta)))
+        return d
+
+    def core_soft_max(self, a, scale: float, max_bias: float, mask=None, tm: int = F16) -> np.ndarray:
+        d = np.zeros(a.shape, np.float32)
+        m = C.byref(tlq_t(mask, tm)) if mask is not None else None
+        self.lib.tlq_core_soft_max(scale, max_bias, C.byref(tlq_t(a, F32)), m, C.byref(tlq_t(d, F32)))
+        return d
+
+    def core_glu(self, code: int, swapped: bool, a, b=None) -> np.ndarray:
+        shape = a.shape if b is not None else a.shape[:-1] + (a.shape[-1] // 2,)
+        d = np.zeros(shape, np.float32)
+        bp = C.byref(tlq_t(b, F32)) if b is not None else None
+        self.lib.tlq_core_glu(code, int(swapped), C.byref(tlq_t(a, F32)), bp, C.byref(tlq_t(d, F32)))
+        return d
+
+    def core_argmax(self, a) -> np.ndarray:
+        out = np.zeros(a.shape[0], np.int32)
+        self.lib.tlq_core_argmax(C.byref(tlq_t(a, F32)), _p(out))
+        return out
+
     def reshape_and_cache(self, key, value, k_cache, v_cache, slots, num_kv_heads, head_size, block_size):
         key = np.ascontiguousarray(key, dtype=np.uint16)
         value = np.ascontiguousarray(value, dtype=np.uint16)
@@ -230,6 +338,7 @@ class Ref:
         L.ref_flash_attn_ext.argtypes = [vp, vp, vp, vp] + [i64] * 11 + [C.c_float] * 3 + [
             vp, C.c_int, C.c_int, C.POINTER(C.c_double)]
         L.ref_flash_attn_ext.restype = C.c_int
+        L.ref_core.argtypes = [C.c_int, vp, vp, vp, vp, vp, C.c_int]
         L.ggml_cpu_init.argtypes = []
         L.ggml_cpu_init()
 
@@ -328,6 +437,40 @@ class Ref:
                                          float(softcap), _p(out), nthreads, reps, C.byref(secs))
         assert rc == 0, rc
         return out, secs.value
+
+
+    def core(self, kind: int, srcs, dst, td: int, ip=(), fp=(), nthreads: int = 4) -> np.ndarray:
+        """One core op on the CPU backend (ref_core in oracle/ref_graph.c).
+        srcs: up to three (array, ggml type[, k]) or None, contiguous; dst an
+        array (its contents are the rows SET_ROWS leaves) of type td."""
+        ty = np.zeros(4, np.int32)
+        ne = np.zeros(16, np.int64)
+        ptrs = (C.c_void_p * 4)()
+        keep = []
+        for i, src in enumerate(list(srcs) + [None] * (3 - len(srcs))):
+            if src is None:
+                continue
+            a, t = np.ascontiguousarray(src[0]), src[1]
+            keep.append(a)
+            ty[i] = t
+            if t in BLOCK:
+                k = src[2]
+                lead = list(a.shape[:-1])[::-1] + [1] * (4 - a.ndim)
+                ne[4 * i:4 * i + 4] = [k] + lead[:3]
+            else:
+                ne[4 * i:4 * i + 4] = _ne(a)
+            ptrs[i] = a.ctypes.data
+        assert dst.flags.c_contiguous
+        ty[3] = td
+        ne[12:16] = _ne(dst)
+        ptrs[3] = dst.ctypes.data
+        ipa = np.zeros(16, np.int32)
+        ipa[:len(ip)] = ip
+        fpa = np.zeros(16, np.float32)
+        fpa[:len(fp)] = fp
+        rc = self.lib.ref_core(kind, _p(ty), _p(ne), C.cast(ptrs, C.c_void_p), _p(ipa), _p(fpa), nthreads)
+        assert rc == 0, rc
+        return dst
 
 
 def flash_attn_f64(q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0) -> np.ndarray:
@@ -494,3 +637,224 @@ def xorshift_noise(shape, seed: int) -> np.ndarray:
         s ^= (s << 17) & mask
         out[i] = np.float32((s >> 40) / float(1 << 23) - 1.0)
     return out.reshape(shape)
+
+
+# ------------------------------------------------------------------ core ops
+CORE_KINDS = {"bin": 1, "unary": 2, "norm": 3, "get_rows": 4, "set_rows": 5, "cpy": 6, "rope": 7, "soft_max": 8,
+              "argmax": 9, "glu": 10}
+# ggml_unary_op codes (ggml.h:596-619) and the lowering's element-wise extras
+UNARY_CODES = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 18, 19, 20, 21, 100, 101, 102, 103, 104,
+               105, 106, 107, 108]
+# the CPU's x86-64 build evaluates exp in soft_max and silu with a polynomial
+# (vec.h:1278-1316); the oracle and the GPU call expf, a few ulp away
+CORE_INEXACT_UNARY = {10}
+ROPE_ARGS = ("n_dims", "mode", "n_ctx_orig", "freq_base", "freq_scale", "ext_factor", "attn_factor", "beta_fast",
+             "beta_slow")
+
+
+def _special_row() -> np.ndarray:
+    return np.array([0.0, -0.0, 10.0, -10.0, 9.99, -9.99, 20.0, 20.5, -20.0, 1e-3, -1e-3, 80.0, -80.0, 100.0,
+                     -100.0, 0.5, -0.5, 1.5, 2.5, -2.5, 3.0, -3.0, 6.0, 1e-30, -1e-30, 60000.0, -60000.0],
+                    np.float32)
+
+
+def core_cases():
+    """The core-op cases pinned against the reference's CPU backend: the
+    shapes and inputs of the reference's own tests
+    (crates/tensorlisp/tests/native.rs:109-154 elementwise/norms, 252-281 rope
+    and argmax, 416-435 argmax of long rows, 437-469 set_rows, 471-498 norm
+    and rope chains) and decoder-sized ones (rows of 4096, 32 heads of 128,
+    a 32000-entry vocabulary). Inputs are regenerated from seeds; the golden
+    file keeps the reference's outputs. Each case: name, kind, srcs [(array,
+    ggml type[, k])], dst (shape, type), ip / fp (ref_core's arguments), init
+    (SET_ROWS' destination before the op), perm (CPY of a permuted view),
+    exact (bit-equal to the reference)."""
+    from tensorlisp_amd import synth
+
+    f16 = lambda a: synth.f16_bits(np.asarray(a, np.float32))  # noqa: E731
+    cases = []
+
+    def add(name, kind, srcs, dst, ip=(), fp=(), init=None, perm=None, exact=True):
+        cases.append(dict(name=name, kind=CORE_KINDS[kind], srcs=srcs, dst=dst, ip=tuple(ip), fp=tuple(fp),
+                          init=init, perm=perm, exact=exact))
+
+    # native.rs elementwise_norms_and_reductions
+    x = xorshift_noise([5, 8], 5) * np.float32(3.0)
+    y = xorshift_noise([5, 8], 6)
+    add("t_rms", "norm", [(x, F32)], ((5, 8), F32), (1,), (1e-6,))
+    add("t_norm", "norm", [(x, F32)], ((5, 8), F32), (0,), (1e-6,))
+    for nm, code in (("gelu", 8), ("gelu_erf", 16), ("relu", 6), ("silu", 10), ("sqr", 104), ("exp", 13),
+                     ("sin", 106)):
+        add(f"t_{nm}", "unary", [(x, F32)], ((5, 8), F32), (code,), exact=code not in CORE_INEXACT_UNARY)
+    add("t_cos_y", "unary", [(y, F32)], ((5, 8), F32), (107,))
+    add("t_bias", "unary", [(x, F32)], ((5, 8), F32), (100,), (0.5, 3.0))
+    add("t_scale_bias_exp", "unary", [(np.exp(y).astype(np.float32), F32)], ((5, 8), F32), (100,), (1.0, 2.0))
+    for nm, code in (("add", 0), ("sub", 1), ("mul", 2), ("div", 3)):
+        add(f"t_{nm}", "bin", [(x, F32), (y + np.float32(1.5), F32)], ((5, 8), F32), (code,))
+    # embedding: an f16 table [4, 10] read at ids [[1,7,3],[0,9,9]], flattened
+    table = f16(xorshift_noise([10, 4], 4))
+    add("t_embed", "get_rows", [(table, F16), (np.array([1, 7, 3, 0, 9, 9], np.int32), I32)], ((6, 4), F32))
+    # rope_pooling_depthwise_argmax: neox base 100 scale 0.5 and the normal rope_ext
+    rx = xorshift_noise([3, 2, 8], 4)
+    pos = np.array([0, 3, 7], np.int32)
+    add("t_rope_neox", "rope", [(rx, F32), (pos, I32)], ((3, 2, 8), F32), (8, 2, 0), (100.0, 0.5, 0.0, 1.0, 0.0, 0.0))
+    add("t_rope_norm", "rope", [(rx, F32), (pos, I32)], ((3, 2, 8), F32), (8, 0, 0), (100.0, 1.0, 0.0, 1.0, 0.0, 0.0))
+    ax = xorshift_noise([2, 3, 7, 9], 5).reshape(42, 9)
+    add("t_argmax_pool", "argmax", [(ax, F32)], ((42,), I32))
+    # argmax_of_long_rows (the 262144 case is in the GPU tests only)
+    for n in (100, 16384, 20000):
+        a = xorshift_noise([3, n], 5)
+        for j in (n // 3, n // 2 + 1, n - 1):
+            a[0, j] = 5.0
+        a[1, n - 1] = 9.0
+        add(f"t_argmax_{n}", "argmax", [(a, F32)], ((3,), I32))
+    # state_and_set_rows_persist_between_runs: a [2] row into row `at` of [2, 3]
+    for step, at in enumerate((0, 2, 1, 2)):
+        x1 = xorshift_noise([1, 4], 20 + step)[:, :2].copy()
+        for ty, npty in ((F32, np.float32), (F16, np.uint16)):
+            init = np.zeros((3, 2), npty)
+            add(f"t_set_rows_{TYPE_SUFFIX[ty]}_{step}", "set_rows", [(x1, F32), (np.array([at], np.int32), I32)],
+                ((3, 2), ty), init=init)
+    # norm_weight_rope_chains_match_unfused
+    cx = xorshift_noise([5, 2, 64], 13)
+    cpos = np.array([0, 1, 5, 6, 31], np.int32)
+    add("t_chain_rms", "norm", [(cx, F32)], ((5, 2, 64), F32), (1,), (1e-6,))
+    add("t_chain_mulw", "bin", [(cx, F32), (xorshift_noise([64], 11), F32)], ((5, 2, 64), F32), (2,))
+    add("t_chain_rope_neox", "rope", [(cx, F32), (cpos, I32)], ((5, 2, 64), F32), (64, 2, 0),
+        (1000.0, 1.0, 0.0, 1.0, 0.0, 0.0))
+    add("t_chain_rope_norm", "rope", [(cx, F32), (cpos, I32)], ((5, 2, 64), F32), (64, 0, 0),
+        (1000.0, 1.0, 0.0, 1.0, 0.0, 0.0))
+
+    # every unary op over random values and the special ones
+    u = np.concatenate([synth.normal(201, (3 * 256,)) * np.float32(4.0), _special_row()]).reshape(1, -1)
+    for code in UNARY_CODES:
+        src = np.abs(u) + np.float32(0.1) if code in (105, 108) else u
+        p = (-1.5, 2.0) if code == 102 else (0.7, -0.3)
+        add(f"u_{code}", "unary", [(src, F32)], (src.shape, F32), (code,), p, exact=code not in CORE_INEXACT_UNARY)
+    uh = f16(u)
+    add("u_f16_gelu", "unary", [(uh, F16)], (u.shape, F16), (8,))
+
+    # decoder-sized (llama-7B shapes: 2 tokens, 4096 wide, 32 heads of 128)
+    h = synth.normal(211, (2, 4096))
+    add("d_rms", "norm", [(h, F32)], ((2, 4096), F32), (1,), (1e-5,))
+    add("d_norm", "norm", [(h + np.float32(0.3), F32)], ((2, 4096), F32), (0,), (1e-5,))
+    add("d_mul_w", "bin", [(h, F32), (synth.normal(212, (4096,)), F32)], ((2, 4096), F32), (2,))
+    add("d_add", "bin", [(h, F32), (synth.normal(213, (2, 4096)), F32)], ((2, 4096), F32), (0,))
+    add("d_silu", "unary", [(h, F32)], ((2, 4096), F32), (10,), exact=False)
+    qh = synth.normal(214, (2, 32, 128))
+    dpos = np.array([37, 4095], np.int32)
+    add("d_rope_neox", "rope", [(qh, F32), (dpos, I32)], ((2, 32, 128), F32), (128, 2, 4096),
+        (10000.0, 1.0, 0.0, 1.0, 32.0, 1.0))
+    add("d_rope_norm", "rope", [(qh, F32), (dpos, I32)], ((2, 32, 128), F32), (128, 0, 4096),
+        (500000.0, 1.0, 0.0, 1.0, 32.0, 1.0))
+    ff = (np.float32(1.0) + np.abs(synth.normal(215, (64,)))).astype(np.float32)
+    ypos = np.array([5, 30000], np.int32)
+    add("d_rope_yarn_ff", "rope", [(qh, F32), (ypos, I32), (ff, F32)], ((2, 32, 128), F32), (96, 2, 4096),
+        (10000.0, 0.25, 1.0, 1.0, 32.0, 1.0))
+    add("d_rope_f16", "rope", [(f16(qh), F16), (dpos, I32)], ((2, 32, 128), F16), (128, 2, 4096),
+        (10000.0, 1.0, 0.0, 1.0, 32.0, 1.0))
+    s = synth.normal(216, (1, 32, 2, 300)) * np.float32(3.0)
+    m = np.where(synth.uniform(217, 8 * 300).reshape(1, 1, 8, 300) < 0.25, -np.inf, 0.0).astype(np.float32)
+    add("d_soft_max_f16mask", "soft_max", [(s, F32), (f16(m), F16)], (s.shape, F32), (), (0.088388, 0.0),
+        exact=False)
+    mb = (m + synth.normal(218, (1, 1, 8, 300))).astype(np.float32)
+    add("d_soft_max_alibi", "soft_max", [(s, F32), (mb, F32)], (s.shape, F32), (), (0.125, 8.0), exact=False)
+    add("d_soft_max_plain", "soft_max", [(s, F32)], (s.shape, F32), (), (1.0, 0.0), exact=False)
+    for t in (F32, F16, Q4_0, Q8_0, Q4_K, Q6_K):
+        K = 512
+        if t == F32:
+            tab = synth.normal(220, (64, K))
+            src = (tab, t)
+        elif t == F16:
+            src = (f16(synth.normal(220, (64, K))), t)
+        else:
+            src = (synth.random_blocks(t, 221 + t, 64, K), t, K)
+        ids = np.array([3, 63, 0, 17, 17, 42, 8], np.int32)
+        add(f"d_get_rows_{TYPE_SUFFIX[t]}", "get_rows", [src, (ids, I32)], ((7, K), F32))
+    kv = synth.normal(222, (5, 512))
+    slots = np.array([9, 0, 63, 31, 32], np.int64)
+    add("d_set_rows_kv_f16", "set_rows", [(kv, F32), (slots, I64)], ((64, 512), F16),
+        init=f16(synth.normal(223, (64, 512))))
+    add("d_set_rows_kv_f32", "set_rows", [(kv, F32), (slots.astype(np.int32), I32)], ((64, 512), F32),
+        init=synth.normal(224, (64, 512)))
+    add("d_cpy_f16", "cpy", [(h, F32)], ((2, 4096), F16))
+    add("d_cpy_f16_f32", "cpy", [(f16(h), F16)], ((2, 4096), F32))
+    add("d_cpy_perm", "cpy", [(qh, F32)], ((32, 2, 128), F32), perm=(0, 2, 1, 3))
+    add("d_cpy_reshape", "cpy", [(qh, F32)], ((16, 4, 128), F32))
+    add("d_cpy_q8_0", "cpy", [(synth.random_blocks(Q8_0, 225, 6, 512), Q8_0, 512)], ((6, 512), F32))
+    gx = synth.normal(227, (2, 2 * 1376)) * np.float32(3.0)
+    gx[0, :27] = _special_row()[:27] / np.float32(1000.0) * np.float32(400.0)
+    for code, nm in ((0, "reglu"), (1, "geglu"), (2, "swiglu"), (4, "geglu_erf"), (5, "geglu_quick")):
+        add(f"d_glu_{nm}", "glu", [(gx, F32)], ((2, 1376), F32), (code, 0), exact=code != 2)
+    add("d_glu_swiglu_swapped", "glu", [(gx, F32)], ((2, 1376), F32), (2, 1), exact=False)
+    add("d_glu_geglu_split", "glu", [(gx[:, :1376].copy(), F32), (gx[:, 1376:].copy(), F32)], ((2, 1376), F32),
+        (1, 0))
+    add("d_glu_swiglu_split", "glu", [(gx[:, :1376].copy(), F32), (gx[:, 1376:].copy(), F32)], ((2, 1376), F32),
+        (2, 0), exact=False)
+    logits = synth.normal(226, (4, 32000))
+    logits[1, 7] = logits[1, 31999] = logits[1].max() + np.float32(1.0)
+    logits[2, :] = np.float32(0.25)
+    add("d_argmax", "argmax", [(logits, F32)], ((4,), I32))
+    return cases
+
+
+TYPE_SUFFIX = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q6_K: "q6_K"}
+
+
+def core_ref(r, case) -> np.ndarray:
+    """The reference's CPU backend on a case (Ref.core)."""
+    shape, td = case["dst"]
+    dst = np.array(case["init"], copy=True) if case["init"] is not None else np.zeros(shape, NP_OF[td])
+    ip = case["ip"]
+    if case["kind"] == CORE_KINDS["cpy"] and case["perm"] is not None:
+        ip = tuple(case["perm"]) + (1,)
+    return r.core(case["kind"], case["srcs"], dst, td, ip=ip, fp=case["fp"])
+
+
+def core_oracle(o, case) -> np.ndarray:
+    """Our C restatement on a case."""
+    k, srcs = case["kind"], case["srcs"]
+    shape, td = case["dst"]
+    ip, fp = case["ip"], case["fp"]
+    a = srcs[0]
+    if k == CORE_KINDS["bin"]:
+        return o.core_bin(ip[0], a[0], a[1], srcs[1][0], srcs[1][1], td)
+    if k == CORE_KINDS["unary"]:
+        p = tuple(fp) + (0.0, 0.0)
+        return o.core_unary(ip[0], a[0], a[1], p[0], p[1], td)
+    if k == CORE_KINDS["norm"]:
+        return o.core_norm(bool(ip[0]), fp[0], a[0])
+    if k == CORE_KINDS["get_rows"]:
+        return o.core_get_rows(a[0], a[1], srcs[1][0], srcs[1][1], k=a[2] if len(a) > 2 else None, td=td)
+    if k == CORE_KINDS["set_rows"]:
+        return o.core_set_rows(case["init"], td, a[0], a[1], srcs[1][0], srcs[1][1])
+    if k == CORE_KINDS["cpy"]:
+        src = a[0]
+        if case["perm"] is not None:
+            src = core_perm_view(src, case["perm"])
+        return o.core_cpy(src, a[1], shape, td, k=a[2] if len(a) > 2 else None)
+    if k == CORE_KINDS["rope"]:
+        ff = srcs[2][0] if len(srcs) > 2 else None
+        return o.core_rope(a[0], a[1], srcs[1][0], ip[0], ip[1], ip[2], *fp, ff=ff)
+    if k == CORE_KINDS["soft_max"]:
+        m = srcs[1] if len(srcs) > 1 else None
+        return o.core_soft_max(a[0], fp[0], fp[1], m[0] if m else None, m[1] if m else F16)
+    if k == CORE_KINDS["argmax"]:
+        return o.core_argmax(a[0])
+    if k == CORE_KINDS["glu"]:
+        return o.core_glu(ip[0], bool(ip[1]), a[0], srcs[1][0] if len(srcs) > 1 else None)
+    raise ValueError(k)
+
+
+def core_perm_view(a: np.ndarray, perm):
+    """ggml_permute(a, *perm) as a numpy view (a's shape is ggml's ne reversed):
+    ggml axis i of a becomes axis perm[i] of the view."""
+    nd = a.ndim
+    ax = [0] * 4
+    for i in range(4):
+        ax[perm[i]] = i
+    # numpy axis j <-> ggml axis nd - 1 - j; pad a to 4 dims first
+    a4 = a.reshape((1,) * (4 - nd) + a.shape)
+    v = a4.transpose([3 - ax[3 - j] for j in range(4)])
+    assert all(s == 1 for s in v.shape[:4 - nd]), "the permutation must keep the padding axes"
+    return v[(0,) * (4 - nd)]

@@ -222,3 +222,77 @@ def test_no_device_is_reported_not_fatal():
     with pytest.raises(N.TlhError) as e:
         N.device_props(0)
     assert e.value.status == "NO_DEVICE"
+
+
+# ------------------------------------------------------------------ core ops
+def _core(kind, srcs, dst, x=(), has1=None, has2=None):
+    op = N.core_op(srcs, dst, x)
+    has1 = len(srcs) > 1 and srcs[1] is not None if has1 is None else has1
+    has2 = len(srcs) > 2 and srcs[2] is not None if has2 is None else has2
+    return _status(N.lib().tlh_core_check, kind, C.byref(op), int(has1), int(has2))
+
+
+def test_core_params_pack_as_the_lowering_does():
+    """Ctx::rope (lower.rs:422-466) and Ctx::soft_max (:314-341): theta_scale =
+    freq_base^(-2/n_dims), YaRN corr dims from ggml_rope_yarn_corr_dims (for
+    n_dims 128, n_ctx_orig 4096, base 10000, beta 32/1: [20, 46]); ALiBi m0/m1
+    for 12 heads and max_bias 8: n_head_log2 8, m0 = 2^-1, m1 = 2^-0.5."""
+    import struct
+
+    f = lambda b: struct.unpack("<f", struct.pack("<i", b))[0]  # noqa: E731
+    x = N.rope_params(128, 2, 4096, 10000.0, 1.0, 1.0, 1.0, 32.0, 1.0, False)
+    assert x[0] == 128 and x[1] == 2 and x[8] == 0
+    assert f(x[5]) == pytest.approx(10000.0 ** (-2 / 128), rel=1e-7)
+    assert (f(x[6]), f(x[7])) == (20.0, 46.0)
+    sm = N.soft_max_params(12, 0.125, 8.0)
+    assert f(sm[0]) == 0.125 and f(sm[1]) == 8.0 and sm[4] == 8
+    assert f(sm[2]) == 0.5 and f(sm[3]) == pytest.approx(2 ** -0.5, rel=1e-7)
+
+
+def test_core_validation():
+    """What tlh_core_check accepts and refuses, by kind, without a GPU."""
+    f32 = lambda *ne: N.ggml_tensor(N.F32, ne)  # noqa: E731
+    f16 = lambda *ne: N.ggml_tensor(N.F16, ne)  # noqa: E731
+    i32 = lambda *ne: N.ggml_tensor(N.I32, ne)  # noqa: E731
+    ok = [
+        (N.CORE_BIN, [f32(64, 5), f32(64, 1)], f32(64, 5), (0,)),
+        (N.CORE_BIN, [f16(64, 5), f32(64, 5)], f16(64, 5), (3,)),
+        (N.CORE_UNARY, [f32(9, 2)], f32(9, 2), (10,)),
+        (N.CORE_UNARY, [f16(9, 2)], f32(9, 2), (108,)),
+        (N.CORE_NORM, [f32(4096, 2)], f32(4096, 2), (1,)),
+        (N.CORE_GET_ROWS, [N.ggml_tensor(N.Q4_K, [512, 40]), i32(7)], f32(512, 7), ()),
+        (N.CORE_SET_ROWS, [f32(512, 5), i32(5)], f16(512, 64), ()),
+        (N.CORE_CPY, [f32(128, 32, 2)], f16(4096, 2), ()),
+        (N.CORE_ROPE, [f32(128, 32, 2), i32(2)], f32(128, 32, 2), (128, 2)),
+        (N.CORE_SOFT_MAX, [f32(300, 5, 32), f16(300, 8)], f32(300, 5, 32), ()),
+        (N.CORE_ARGMAX, [f32(32000, 4)], N.ggml_tensor(N.I32, [4]), ()),
+        (N.CORE_GLU, [f32(2752, 2)], f32(1376, 2), (2, 0)),
+        (N.CORE_GLU, [f32(1376, 2), f32(1376, 2)], f32(1376, 2), (1, 0)),
+    ]
+    for kind, srcs, dst, x in ok:
+        st, msg = _core(kind, srcs, dst, x)
+        assert st == "OK", (kind, msg)
+    bad = [
+        (N.CORE_BIN, [f32(64, 5), f32(64, 2)], f32(64, 5), (0,), "UNSUPPORTED", "repeat"),
+        (N.CORE_BIN, [f32(64, 5), f32(64, 5)], f32(64, 5), (4,), "INVALID", "BIN code"),
+        (N.CORE_UNARY, [f32(9, 2)], f32(9, 2), (17,), "UNSUPPORTED", "unary op 17"),
+        (N.CORE_NORM, [f16(64, 2)], f32(64, 2), (1,), "UNSUPPORTED", "NORM"),
+        (N.CORE_GET_ROWS, [N.ggml_tensor(13, [512, 40], [176, 352, 14080, 14080]), i32(7)], f32(512, 7), (),
+         "UNSUPPORTED", "GET_ROWS"),
+        (N.CORE_GET_ROWS, [f32(512, 40), i32(7)], f32(512, 6), (), "UNSUPPORTED", "shapes"),
+        (N.CORE_SET_ROWS, [f32(512, 5), i32(4)], f32(512, 64), (), "UNSUPPORTED", "shapes"),
+        (N.CORE_CPY, [f32(128, 32)], f32(128, 31), (), "UNSUPPORTED", "element counts"),
+        (N.CORE_ROPE, [f32(128, 32, 2), i32(2)], f32(128, 32, 2), (128, 1), "UNSUPPORTED", "modes"),
+        (N.CORE_ROPE, [f32(128, 32, 2), i32(3)], f32(128, 32, 2), (128, 2), "UNSUPPORTED", "position"),
+        (N.CORE_ROPE, [f32(128, 32, 2), i32(2)], f32(128, 32, 2), (130, 2), "INVALID", "n_dims"),
+        (N.CORE_SOFT_MAX, [f32(300, 5), f16(299, 5)], f32(300, 5), (), "UNSUPPORTED", "mask"),
+        (N.CORE_ARGMAX, [f32(100, 4, 2)], N.ggml_tensor(N.I32, [4]), (), "UNSUPPORTED", "2-D"),
+        (N.CORE_GLU, [f32(2752, 2)], f32(1375, 2), (2, 0), "UNSUPPORTED", "shapes"),
+        (N.CORE_GLU, [f32(2752, 2)], f32(1376, 2), (3, 0), "UNSUPPORTED", "glu op 3"),
+        (99, [f32(4)], f32(4), (), "INVALID", "unknown kind"),
+    ]
+    for kind, srcs, dst, x, status, text in bad:
+        st, msg = _core(kind, srcs, dst, x)
+        assert st == status and text in msg, (kind, st, msg)
+    st, msg = _core(N.CORE_ROPE, [f32(128, 32, 2), i32(2)], f32(128, 32, 2), (128, 2, 0, 0, 0, 0, 0, 0, 1))
+    assert st == "UNSUPPORTED" and "frequency factors" in msg

@@ -504,3 +504,98 @@ def test_flash_attn_oracle_catches_planted_mistakes():
     assert np.abs(o.flash_attn_ext(q, k, v, m, scale * 1.5, max_bias, softcap) - want).max() > 10 * tol
     assert np.abs(o.flash_attn_ext(q, k, v, m, scale, 0.0, softcap) - want).max() > 10 * tol
     assert np.abs(o.flash_attn_ext(q, k, v, m, scale, max_bias, 0.0) - want).max() > 10 * tol
+
+
+# ------------------------------------------------------------------ core ops
+from refs import (CORE_KINDS, F16, F32, I32, core_cases, core_oracle, core_ref)  # noqa: E402
+
+CORE = core_cases()
+
+
+def _as_f32(o, a):
+    return o.f16_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float64)
+
+
+@pytest.mark.parametrize("case", CORE, ids=[c["name"] for c in CORE])
+def test_core_oracle_golden(case):
+    """The restated core ops against the reference CPU backend's outputs:
+    bit-exact, except where that backend's x86 build takes a polynomial exp
+    (silu, soft_max), where a few ulp separate them."""
+    o = oracle()
+    want = gold("core")[case["name"]]
+    got = core_oracle(o, case)
+    assert got.shape == want.shape and got.dtype == want.dtype
+    if case["exact"]:
+        np.testing.assert_array_equal(got, want)
+    else:
+        g, w = _as_f32(o, got), _as_f32(o, want)
+        assert np.all(np.abs(g - w) <= 1e-6 * np.abs(w) + 1e-9), np.abs(g - w).max()
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_core_oracle_vs_reference_live(seed):
+    """Fresh shapes and parameters through both: norms of odd widths, rope with
+    random bases / YaRN parameters, get_rows of every weight type."""
+    o, r = oracle(), ref()
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 3000))
+    x = (rng.standard_normal((3, n)) * rng.uniform(0.1, 10) + rng.uniform(-2, 2)).astype(np.float32)
+    for rms in (0, 1):
+        c = dict(kind=CORE_KINDS["norm"], srcs=[(x, F32)], dst=(x.shape, F32), ip=(rms,), fp=(1e-5,), init=None,
+                 perm=None)
+        np.testing.assert_array_equal(core_oracle(o, c), core_ref(r, c))
+    nd = int(rng.integers(1, 33)) * 2
+    a = rng.standard_normal((4, 3, nd + 2 * int(rng.integers(0, 4)))).astype(np.float32)
+    pos = rng.integers(0, 40000, 4).astype(np.int32)
+    fp = (float(rng.uniform(100, 1e6)), float(rng.uniform(0.1, 1)), float(rng.integers(0, 2)),
+          float(rng.uniform(0.5, 2)), float(rng.uniform(16, 64)), float(rng.uniform(0.5, 2)))
+    for mode in (0, 2):
+        c = dict(kind=CORE_KINDS["rope"], srcs=[(a, F32), (pos, I32)], dst=(a.shape, F32),
+                 ip=(nd, mode, int(rng.integers(512, 8192))), fp=fp, init=None, perm=None)
+        np.testing.assert_array_equal(core_oracle(o, c), core_ref(r, c))
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+        k = 256 * int(rng.integers(1, 4))
+        w = synth.random_blocks(t, seed + t, 9, k)
+        ids = rng.integers(0, 9, 5).astype(np.int32)
+        c = dict(kind=CORE_KINDS["get_rows"], srcs=[(w, t, k), (ids, I32)], dst=((5, k), F32), ip=(), fp=(),
+                 init=None, perm=None)
+        np.testing.assert_array_equal(core_oracle(o, c), core_ref(r, c))
+
+
+def test_core_oracle_against_the_mathematics():
+    """What the mathematics fixes, independent of the reference: rms_norm and norm
+    against float64, softmax rows against float64 (and summing to one), rope
+    as a rotation by pos * base^(-2p/n) (neox pairs p, p + n/2), argmax as the
+    last maximum, get_rows of q8_0 as the dequantized rows, cpy of a permuted
+    view as numpy's transpose."""
+    o = oracle()
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((4, 1000)) * 3 + 1).astype(np.float32)
+    xd = x.astype(np.float64)
+    rms = xd / np.sqrt((xd * xd).mean(1, keepdims=True) + 1e-5)
+    np.testing.assert_allclose(o.core_norm(True, 1e-5, x), rms, rtol=2e-6, atol=1e-6)
+    c = xd - xd.mean(1, keepdims=True)
+    np.testing.assert_allclose(o.core_norm(False, 1e-5, x), c / np.sqrt((c * c).mean(1, keepdims=True) + 1e-5),
+                               rtol=2e-6, atol=1e-5)
+    s = rng.standard_normal((1, 3, 2, 50)).astype(np.float32)
+    m = rng.standard_normal((1, 1, 2, 50)).astype(np.float32)
+    got = o.core_soft_max(s, 0.5, 0.0, m, F32)
+    e = np.exp(s.astype(np.float64) * 0.5 + m - (s.astype(np.float64) * 0.5 + m).max(-1, keepdims=True))
+    np.testing.assert_allclose(got, e / e.sum(-1, keepdims=True), rtol=1e-6, atol=1e-8)
+    a = rng.standard_normal((3, 2, 16)).astype(np.float32)
+    pos = np.array([0, 5, 300], np.int32)
+    got = o.core_rope(a, F32, pos, 16, 2, 0, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+    th = pos[:, None].astype(np.float64) * 10000.0 ** (-2.0 * np.arange(8) / 16)
+    x0, x1 = a[..., :8].astype(np.float64), a[..., 8:].astype(np.float64)
+    cs, sn = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+    np.testing.assert_allclose(got[..., :8], x0 * cs - x1 * sn, atol=2e-5)
+    np.testing.assert_allclose(got[..., 8:], x0 * sn + x1 * cs, atol=2e-5)
+    b = rng.integers(0, 4, (5, 64)).astype(np.float32)
+    want = b.shape[1] - 1 - np.argmax(b[:, ::-1], axis=1)
+    np.testing.assert_array_equal(o.core_argmax(b), want)
+    w = synth.random_blocks(Q8_0, 9, 6, 256)
+    ids = np.array([5, 0, 5], np.int32)
+    np.testing.assert_array_equal(o.core_get_rows(w, Q8_0, ids, I32, k=256), o.dequantize(Q8_0, w, 256)[ids])
+    q = rng.standard_normal((2, 3, 4)).astype(np.float32)
+    np.testing.assert_array_equal(o.core_cpy(q.transpose(1, 0, 2), F32, (3, 2, 4), F32), q.transpose(1, 0, 2))
