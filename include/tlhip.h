@@ -261,6 +261,84 @@ tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cac
                                  const int64_t *slots, int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
                                  int32_t block_size, void *stream);
 
+/* ------------------------------------------------------------ executor
+ * A graph of ggml nodes compiled once into a recorded list of launches on this
+ * library's kernels and replayed per run, replacing the reference's
+ * Executor::compile / Program::run (crates/kernels/src/cuda/exec.rs:27-226)
+ * over its IR (crates/kernels/src/graph.rs:72-229) and memory plan
+ * (crates/kernels/src/plan.rs:56-189). The caller hands over the IR the
+ * reference builds from a ggml graph (native_ir.rs lower_graph): one record
+ * per tensor, the node order and the tensors that must outlive the run.
+ *
+ * Memory: weights stay where the caller put them (a device pointer per weight
+ * index); state tensors live in one caller buffer at fixed byte offsets (per
+ * state index), handed over per run so sessions can swap blocks; inputs live
+ * in an io buffer and temporaries in an arena, both owned by the program. The
+ * arena reuses a tensor's bytes once its last reader has run (first fit by
+ * start position, 256-byte alignment), and holds each node's scratch.
+ * MUL_MAT nodes that read the same activation with the same weight type
+ * quantize it once: the first one writes the q8 blocks into a scratch block
+ * that lives until the last of them has run (when the activation has more
+ * than two columns; at one or two the GEMV quantizes on the fly, which saves
+ * a launch).
+ *
+ * Lowering follows the reference's Ctx::lower (lower.rs:175-213): view ops
+ * and empty tensors produce nothing; MUL_MAT, FLASH_ATTN_EXT and the core ops
+ * go to the entry points above with the blobs Ctx packs. Every node is lowered
+ * before failing, and one TLH_UNSUPPORTED names each missing op with a count
+ * and an example, as exec.rs:39-58 reports them.
+ *
+ * Runs: tlh_program_run enqueues the launches on `stream`; with `graph` != 0
+ * the launches are captured once into a hipGraph (per state buffer and stream)
+ * and replayed with one hipGraphLaunch. Calls on one program must not overlap. */
+typedef enum tlh_storage {
+    TLH_STORE_TEMP = 0,   /* computed in the arena */
+    TLH_STORE_WEIGHT = 1, /* weights[storage_index] */
+    TLH_STORE_STATE = 2,  /* state buffer + state_offsets[storage_index] */
+    TLH_STORE_INPUT = 3   /* input storage_index, in the program's io buffer */
+} tlh_storage;
+
+typedef struct tlh_ir_tensor {
+    char op[24];            /* ggml op name ("MUL_MAT", "RMS_NORM", ...; "NONE" for leaves) */
+    int32_t ty;             /* ggml type */
+    int32_t storage;        /* tlh_storage; meaningful for roots */
+    int32_t storage_index;
+    int32_t view_src;       /* -1, or the root tensor whose storage this view aliases */
+    int64_t view_offs;      /* byte offset into view_src */
+    int64_t ne[4];
+    int64_t nb[4];
+    int32_t op_params[16];  /* as ggml stores them */
+    int32_t src[10];        /* tensor ids, -1 = none */
+} tlh_ir_tensor;
+
+typedef struct tlh_program tlh_program;
+
+/* Plans and lowers; allocates the arena and io buffer on the current device.
+ * weights: n_weights device pointers; state_offsets: byte offset of each state
+ * tensor in the state buffer given to tlh_program_run. */
+tlh_status tlh_program_compile(const tlh_ir_tensor *tensors, int32_t n_tensors, const int32_t *nodes,
+                               int32_t n_nodes, const int32_t *keep, int32_t n_keep, const void *const *weights,
+                               int32_t n_weights, const int64_t *state_offsets, int32_t n_states,
+                               tlh_program **program);
+tlh_status tlh_program_destroy(tlh_program *p);
+/* Stream-ordered copy between any two device (or pinned host) addresses. */
+tlh_status tlh_copy(void *dst, const void *src, size_t bytes, void *stream);
+/* Device address and byte size of graph input i in the io buffer. */
+tlh_status tlh_program_input(const tlh_program *p, int32_t i, void **ptr, size_t *bytes);
+/* Device address of tensor `id` (any storage; `state` is the run's state buffer). */
+tlh_status tlh_program_tensor(const tlh_program *p, int32_t id, void *state, void **ptr);
+tlh_status tlh_program_run(tlh_program *p, void *state, void *stream, int32_t graph);
+/* Sizes: arena bytes, io bytes, and the number of recorded dispatches (one
+ * per lowered node, plus one quantization per MUL_MAT group; a dispatch may
+ * launch more than one kernel). */
+tlh_status tlh_program_stats(const tlh_program *p, size_t *arena_bytes, size_t *io_bytes, int32_t *launches);
+/* The plan without a device (for checking it): arena offset per tensor (-1 if
+ * not in the arena), per-node scratch offset (-1 if none) and the arena size.
+ * Scratch sizes come from the same entry points compile uses. */
+tlh_status tlh_program_plan(const tlh_ir_tensor *tensors, int32_t n_tensors, const int32_t *nodes, int32_t n_nodes,
+                            const int32_t *keep, int32_t n_keep, int64_t *tensor_offsets, int64_t *scratch_offsets,
+                            size_t *arena_bytes);
+
 #ifdef __cplusplus
 }
 #endif

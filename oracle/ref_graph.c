@@ -209,3 +209,125 @@ int ref_core(int kind, const int *ty, const int64_t *ne, void *const *data, cons
     ggml_free(ctx);
     return rc;
 }
+
+// ------------------------------------------------------------ IR graphs
+// ref_ir_run: rebuilds a tlh_ir_tensor graph (include/tlhip.h) with the ggml
+// constructors each record names, checks that ggml gives every tensor the same
+// ne, nb and view placement as the record (so the IR is the graph ggml builds
+// from those calls), and computes it on the CPU backend. Leaves point at the
+// caller's host arrays by storage index (weights, states -- updated in place
+// by SET_ROWS / CPY -- and inputs); `outs` receive copies of the tensors
+// `out_ids` (contiguous). Returns 0, or -(1000 + id) for the first tensor whose
+// shape, strides or placement differ, or -(2000 + id) for an op it cannot
+// rebuild.
+#include "../include/tlhip.h"
+
+static int64_t ir_param_offset(const tlh_ir_tensor *r) {
+    return (int64_t)(uint32_t)r->op_params[0] | ((int64_t)r->op_params[1] << 32);
+}
+static float ir_f(const tlh_ir_tensor *r, int i) {
+    float f;
+    memcpy(&f, &r->op_params[i], 4);
+    return f;
+}
+
+int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_nodes, void *const *weights,
+               void *const *states, void *const *inputs, const int32_t *out_ids, void *const *outs, int n_outs,
+               int nthreads) {
+    ggml_cpu_init();
+    size_t mem = ggml_graph_overhead_custom(4096 > n ? 4096 : (size_t)n * 2, false) + 1024 * 1024;
+    for (int i = 0; i < n; ++i) {
+        mem += ggml_tensor_overhead() + 64;
+        if (rec[i].view_src < 0 && strcmp(rec[i].op, "NONE") != 0) {
+            const int64_t ne = rec[i].ne[0] * rec[i].ne[1] * rec[i].ne[2] * rec[i].ne[3];
+            mem += (size_t)(ne * 8 + 256);  // at most 8 bytes an element (i64)
+        }
+    }
+    struct ggml_init_params ip = {.mem_size = mem, .mem_buffer = NULL, .no_alloc = false};
+    struct ggml_context *ctx = ggml_init(ip);
+    if (!ctx) return -1;
+    struct ggml_tensor **t = calloc((size_t)n, sizeof *t);
+    int rc = 0;
+    for (int i = 0; i < n && rc == 0; ++i) {
+        const tlh_ir_tensor *r = &rec[i];
+        struct ggml_tensor *s0 = r->src[0] >= 0 ? t[r->src[0]] : NULL, *s1 = r->src[1] >= 0 ? t[r->src[1]] : NULL,
+                           *s2 = r->src[2] >= 0 ? t[r->src[2]] : NULL, *s3 = r->src[3] >= 0 ? t[r->src[3]] : NULL;
+        const char *op = r->op;
+        struct ggml_tensor *x = NULL;
+        if (!strcmp(op, "NONE")) {
+            x = ggml_new_tensor_4d(ctx, (enum ggml_type)r->ty, r->ne[0], r->ne[1], r->ne[2], r->ne[3]);
+            void *const *leaf = r->storage == TLH_STORE_WEIGHT ? weights : r->storage == TLH_STORE_STATE ? states
+                                : r->storage == TLH_STORE_INPUT ? inputs : NULL;
+            if (!leaf) {
+                rc = -(2000 + i);
+                break;
+            }
+            x->data = leaf[r->storage_index];
+        } else if (!strcmp(op, "VIEW")) {
+            x = ggml_view_4d(ctx, s0, r->ne[0], r->ne[1], r->ne[2], r->ne[3], r->nb[1], r->nb[2], r->nb[3],
+                             (size_t)ir_param_offset(r));
+        } else if (!strcmp(op, "RESHAPE")) {
+            x = ggml_reshape_4d(ctx, s0, r->ne[0], r->ne[1], r->ne[2], r->ne[3]);
+        } else if (!strcmp(op, "PERMUTE")) {
+            x = ggml_permute(ctx, s0, r->op_params[0], r->op_params[1], r->op_params[2], r->op_params[3]);
+        } else if (!strcmp(op, "TRANSPOSE")) {
+            x = ggml_transpose(ctx, s0);
+        } else if (!strcmp(op, "CONT")) {
+            x = ggml_cont_4d(ctx, s0, r->ne[0], r->ne[1], r->ne[2], r->ne[3]);
+        } else if (!strcmp(op, "CPY")) {
+            x = ggml_cpy(ctx, s0, s1);
+        } else if (!strcmp(op, "MUL_MAT")) {
+            x = ggml_mul_mat(ctx, s0, s1);
+        } else if (!strcmp(op, "ADD")) {
+            x = ggml_add(ctx, s0, s1);
+        } else if (!strcmp(op, "SUB")) {
+            x = ggml_sub(ctx, s0, s1);
+        } else if (!strcmp(op, "MUL")) {
+            x = ggml_mul(ctx, s0, s1);
+        } else if (!strcmp(op, "DIV")) {
+            x = ggml_div(ctx, s0, s1);
+        } else if (!strcmp(op, "RMS_NORM")) {
+            x = ggml_rms_norm(ctx, s0, ir_f(r, 0));
+        } else if (!strcmp(op, "NORM")) {
+            x = ggml_norm(ctx, s0, ir_f(r, 0));
+        } else if (!strcmp(op, "UNARY")) {
+            x = ggml_unary(ctx, s0, (enum ggml_unary_op)r->op_params[0]);
+        } else if (!strcmp(op, "SCALE")) {
+            x = ggml_scale_bias(ctx, s0, ir_f(r, 0), ir_f(r, 1));
+        } else if (!strcmp(op, "GET_ROWS")) {
+            x = ggml_get_rows(ctx, s0, s1);
+        } else if (!strcmp(op, "SET_ROWS")) {
+            x = ggml_set_rows(ctx, t[r->view_src], s0, s1);
+        } else if (!strcmp(op, "ROPE")) {
+            x = ggml_rope_ext(ctx, s0, s1, s2, r->op_params[1], r->op_params[2], r->op_params[4], ir_f(r, 5),
+                              ir_f(r, 6), ir_f(r, 7), ir_f(r, 8), ir_f(r, 9), ir_f(r, 10));
+        } else if (!strcmp(op, "SOFT_MAX")) {
+            x = ggml_soft_max_ext(ctx, s0, s1, ir_f(r, 0), ir_f(r, 1));
+        } else if (!strcmp(op, "FLASH_ATTN_EXT")) {
+            x = ggml_flash_attn_ext(ctx, s0, s1, s2, s3, ir_f(r, 0), ir_f(r, 1), ir_f(r, 2));
+        } else if (!strcmp(op, "GLU")) {
+            x = s1 ? ggml_glu_split(ctx, s0, s1, (enum ggml_glu_op)r->op_params[0])
+                   : ggml_glu(ctx, s0, (enum ggml_glu_op)r->op_params[0], r->op_params[1] != 0);
+        } else if (!strcmp(op, "ARGMAX")) {
+            x = ggml_argmax(ctx, s0);
+        } else {
+            rc = -(2000 + i);
+            break;
+        }
+        t[i] = x;
+        int same = x->type == (enum ggml_type)r->ty;
+        for (int d = 0; d < 4; ++d) same = same && x->ne[d] == r->ne[d] && (int64_t)x->nb[d] == r->nb[d];
+        if (r->view_src >= 0) same = same && x->view_src == t[r->view_src] && (int64_t)x->view_offs == r->view_offs;
+        else same = same && x->view_src == NULL;
+        if (!same) rc = -(1000 + i);
+    }
+    if (rc == 0) {
+        struct ggml_cgraph *gf = ggml_new_graph_custom(ctx, 4096 > n ? 4096 : (size_t)n * 2, false);
+        for (int k = 0; k < n_nodes; ++k) ggml_build_forward_expand(gf, t[nodes[k]]);
+        rc = compute(gf, nthreads, 1, NULL);
+        for (int k = 0; k < n_outs && rc == 0; ++k) memcpy(outs[k], t[out_ids[k]]->data, ggml_nbytes(t[out_ids[k]]));
+    }
+    free(t);
+    ggml_free(ctx);
+    return rc;
+}

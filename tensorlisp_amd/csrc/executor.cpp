@@ -1,0 +1,758 @@
+// The graph executor (include/tlhip.h, "executor"): ggml IR in, a recorded
+// list of launches on this library's entry points out, replayed per run
+// eagerly or as one captured hipGraph. Host code only.
+//
+// It takes the place of the reference's Executor::compile / Program::run
+// (crates/kernels/src/cuda/exec.rs:27-226) over its IR (graph.rs:72-229) and
+// memory plan (plan.rs:56-189): lowering per node as Ctx::lower decides
+// (lower.rs:175-213), then a liveness plan of one arena, then replay.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "kernels.hpp"
+
+namespace tlh {
+namespace {
+
+constexpr int64_t ALIGN = 256;
+int64_t align_up(int64_t n) { return (n + ALIGN - 1) / ALIGN * ALIGN; }
+
+enum BufKind { B_NONE, B_ARENA, B_IO, B_STATE, B_WEIGHT };
+struct Place {
+    int buf = B_NONE;
+    int32_t index = -1;  // weight index for B_WEIGHT
+    int64_t off = 0;
+};
+
+enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE };
+struct Dispatch {
+    DispatchKind kind;
+    int core_kind = 0;
+    tlh_op op;
+    Place src[4];
+    Place dst;
+    int pos = 0;            // node position
+    int block = -1;         // scratch block index
+    size_t scratch_bytes = 0;
+};
+
+// ggml type traits used for byte sizes: (block elements, block bytes)
+bool type_traits(int ty, int64_t &blck, int64_t &size) {
+    switch (ty) {
+    case TLH_TYPE_F32: blck = 1, size = 4; return true;
+    case TLH_TYPE_F16: blck = 1, size = 2; return true;
+    case TLH_TYPE_Q4_0: blck = 32, size = 18; return true;
+    case 3: blck = 32, size = 20; return true;   // q4_1
+    case 6: blck = 32, size = 22; return true;   // q5_0
+    case 7: blck = 32, size = 24; return true;   // q5_1
+    case TLH_TYPE_Q8_0: blck = 32, size = 34; return true;
+    case 9: blck = 32, size = 36; return true;   // q8_1
+    case 10: blck = 256, size = 84; return true;   // q2_K
+    case 11: blck = 256, size = 110; return true;  // q3_K
+    case TLH_TYPE_Q4_K: blck = 256, size = 144; return true;
+    case 13: blck = 256, size = 176; return true;  // q5_K
+    case TLH_TYPE_Q6_K: blck = 256, size = 210; return true;
+    case TLH_TYPE_Q8_K: blck = 256, size = 292; return true;
+    case 24: blck = 1, size = 1; return true;  // i8
+    case 25: blck = 1, size = 2; return true;  // i16
+    case 26: blck = 1, size = 4; return true;  // i32
+    case 27: blck = 1, size = 8; return true;  // i64
+    case 28: blck = 1, size = 8; return true;  // f64
+    case 30: blck = 1, size = 2; return true;  // bf16
+    default: return false;
+    }
+}
+
+int64_t nelements(const tlh_ir_tensor &t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; }
+
+// ggml_nbytes (graph.rs Tensor::nbytes)
+int64_t nbytes(const tlh_ir_tensor &t) {
+    if (nelements(t) == 0) return 0;
+    int64_t blck = 1, size = 4;
+    type_traits(t.ty, blck, size);
+    int64_t n = blck == 1 ? size + (t.ne[0] - 1) * t.nb[0] : t.ne[0] * t.nb[0] / blck;
+    for (int i = 1; i < 4; ++i) n += (t.ne[i] - 1) * t.nb[i];
+    return n;
+}
+
+bool is_view_op(const tlh_ir_tensor &t) {
+    return !strcmp(t.op, "NONE") || !strcmp(t.op, "RESHAPE") || !strcmp(t.op, "VIEW") || !strcmp(t.op, "TRANSPOSE") ||
+           !strcmp(t.op, "PERMUTE");
+}
+
+float f32_of(int32_t bits) {
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+int64_t bits_of(float f) {
+    int32_t b;
+    memcpy(&b, &f, 4);
+    return b;  // sign-extended, as OpBlob::float stores it
+}
+
+struct Graph {
+    const tlh_ir_tensor *t = nullptr;
+    int32_t n = 0;
+    std::vector<int32_t> nodes, keep;
+
+    int32_t root(int32_t id, int64_t &extra) const {
+        extra = t[id].view_src >= 0 ? t[id].view_offs : 0;
+        return t[id].view_src >= 0 ? t[id].view_src : id;
+    }
+    const char *name(int32_t id) const { return t[id].op; }
+};
+
+struct Unsupported {
+    std::string op, example;
+    int count = 0;
+};
+
+struct Block {
+    int64_t first, last, size;
+    int32_t tensor;  // arena root, or -1 for a scratch block
+    int64_t off = 0;
+};
+
+// One program: the lowered launches and the plan.
+struct Lowered {
+    std::vector<Dispatch> d;
+    std::vector<Block> blocks;        // arena blocks (tensor roots, then scratch)
+    std::vector<int64_t> arena_off;   // per tensor root (-1: not in the arena)
+    std::vector<int64_t> node_scratch;  // per node position (-1: none)
+    std::vector<int32_t> node_ids;      // tensor id per node position
+    int64_t arena = 0;
+};
+
+class Lowering {
+  public:
+    Lowering(const Graph &g) : g_(g) {}
+
+    tlh_status run(Lowered &out) {
+        out.d.clear();
+        out.node_ids = g_.nodes;
+        for (size_t pos = 0; pos < g_.nodes.size(); ++pos) {
+            const int32_t id = g_.nodes[pos];
+            const tlh_ir_tensor &t = g_.t[id];
+            if (is_view_op(t) || nelements(t) == 0) continue;
+            std::string why;
+            if (!lower_node((int)pos, id, out.d, why)) {
+                bool found = false;
+                for (auto &u : missing_)
+                    if (u.op == t.op) {
+                        ++u.count;
+                        found = true;
+                    }
+                if (!found) missing_.push_back({t.op, "node " + std::to_string(id) + ": " + why, 1});
+            }
+        }
+        if (!missing_.empty()) {
+            std::string list;
+            for (auto &u : missing_) {
+                if (!list.empty()) list += "; ";
+                list += u.op + " x" + std::to_string(u.count) + " (e.g. " + u.example + ")";
+            }
+            return set_error(TLH_UNSUPPORTED, "native HIP: not implemented: %s", list.c_str());
+        }
+        group_mul_mats(out.d);
+        plan(out);
+        return TLH_OK;
+    }
+
+  private:
+    const Graph &g_;
+    std::vector<Unsupported> missing_;
+
+    static tlh_tensor desc(const tlh_ir_tensor &t) {
+        tlh_tensor d;
+        memset(&d, 0, sizeof d);
+        for (int i = 0; i < 4; ++i) d.ne[i] = t.ne[i], d.nb[i] = t.nb[i];
+        d.ty = t.ty;
+        return d;
+    }
+
+    Place place_of(int32_t id) const {
+        int64_t extra = 0;
+        const int32_t r = g_.root(id, extra);
+        Place p;
+        p.off = extra;
+        switch (g_.t[r].storage) {
+        case TLH_STORE_WEIGHT: p.buf = B_WEIGHT, p.index = g_.t[r].storage_index; break;
+        case TLH_STORE_STATE: p.buf = B_STATE, p.index = g_.t[r].storage_index; break;
+        case TLH_STORE_INPUT: p.buf = B_IO, p.index = g_.t[r].storage_index; break;
+        default: p.buf = B_ARENA, p.index = r; break;
+        }
+        return p;
+    }
+
+    Dispatch base(int pos, int32_t id, std::initializer_list<int> srcs) const {
+        Dispatch d;
+        memset(&d.op, 0, sizeof d.op);
+        int i = 0;
+        for (int s : srcs) {
+            const int32_t sid = s >= 0 ? g_.t[id].src[s] : -1;
+            if (sid >= 0) {
+                d.op.t[i] = desc(g_.t[sid]);
+                d.src[i] = place_of(sid);
+            }
+            ++i;
+        }
+        d.op.t[4] = desc(g_.t[id]);
+        d.dst = place_of(id);
+        d.pos = pos;
+        return d;
+    }
+
+    bool core(std::vector<Dispatch> &out, Dispatch d, int kind, std::string &why) {
+        d.kind = D_CORE;
+        d.core_kind = kind;
+        const tlh_status st = tlh_core_check(kind, &d.op, d.src[1].buf != B_NONE, d.src[2].buf != B_NONE);
+        if (st != TLH_OK) {
+            why = tlh_last_error();
+            return false;
+        }
+        out.push_back(d);
+        return true;
+    }
+
+    // Ctx::lower's table (lower.rs:188-211) for the ops this library runs.
+    bool lower_node(int pos, int32_t id, std::vector<Dispatch> &out, std::string &why) {
+        const tlh_ir_tensor &t = g_.t[id];
+        const std::string op = t.op;
+        const int32_t *p = t.op_params;
+        auto src = [&](int i) { return t.src[i]; };
+        if (op == "MUL_MAT") {
+            if (src(0) < 0 || src(1) < 0) return why = "missing source", false;
+            Dispatch d = base(pos, id, {0, 1});
+            const tlh_ir_tensor &a = g_.t[src(0)];
+            d.op.x[0] = a.ne[2] ? t.ne[2] / a.ne[2] : 0;  // r2, r3 (lower.rs:556-559)
+            d.op.x[1] = a.ne[3] ? t.ne[3] / a.ne[3] : 0;
+            size_t bytes = 0;
+            if (tlh_mul_mat_scratch_bytes(&d.op, &bytes) != TLH_OK) return why = tlh_last_error(), false;
+            d.kind = D_MUL_MAT;
+            d.scratch_bytes = bytes;
+            out.push_back(d);
+            return true;
+        }
+        if (op == "FLASH_ATTN_EXT") {
+            if (src(4) >= 0) return why = "attention sinks", false;
+            Dispatch d = base(pos, id, {0, 1, 2, 3});
+            float scale = f32_of(p[0]);
+            const float max_bias = f32_of(p[1]), softcap = f32_of(p[2]);
+            if (softcap != 0.0f) scale /= softcap;
+            const int64_t nh = g_.t[src(0)].ne[2];
+            const uint32_t nhl2 = 1u << (uint32_t)floorf(log2f((float)nh));
+            d.op.x[0] = bits_of(scale);
+            d.op.x[1] = bits_of(max_bias);
+            d.op.x[2] = bits_of(powf(2.0f, -max_bias / (float)nhl2));
+            d.op.x[3] = bits_of(powf(2.0f, -(max_bias / 2.0f) / (float)nhl2));
+            d.op.x[4] = nhl2;
+            d.op.x[5] = bits_of(softcap);
+            size_t bytes = 0;
+            if (tlh_flash_attn_ext_scratch_bytes(&d.op, &bytes) != TLH_OK) return why = tlh_last_error(), false;
+            d.kind = D_FLASH_ATTN;
+            d.scratch_bytes = bytes;
+            out.push_back(d);
+            return true;
+        }
+        if (op == "ADD" || op == "SUB" || op == "MUL" || op == "DIV") {
+            Dispatch d = base(pos, id, {0, 1});
+            d.op.x[0] = op == "ADD" ? 0 : op == "SUB" ? 1 : op == "MUL" ? 2 : 3;
+            return core(out, d, TLH_CORE_BIN, why);
+        }
+        static const std::map<std::string, int> unary = {{"SCALE", 100}, {"FILL", 101}, {"CLAMP", 102},
+                                                         {"LEAKY_RELU", 103}, {"SQR", 104}, {"SQRT", 105},
+                                                         {"SIN", 106}, {"COS", 107}, {"LOG", 108}, {"UNARY", -1}};
+        if (auto u = unary.find(op); u != unary.end()) {  // lower.rs:253-290
+            Dispatch d = base(pos, id, {0});
+            int code = u->second;
+            if (code == -1) {
+                code = p[0];
+                if (code == 17) return why = "xielu", false;
+            }
+            if (code == 100 || code == 102) d.op.x[1] = bits_of(f32_of(p[0])), d.op.x[2] = bits_of(f32_of(p[1]));
+            if (code == 101 || code == 103) d.op.x[1] = bits_of(f32_of(p[0]));
+            d.op.x[0] = code;
+            return core(out, d, TLH_CORE_UNARY, why);
+        }
+        if (op == "NORM" || op == "RMS_NORM") {
+            Dispatch d = base(pos, id, {0});
+            d.op.x[0] = op == "RMS_NORM";
+            d.op.x[1] = bits_of(f32_of(p[0]));
+            return core(out, d, TLH_CORE_NORM, why);
+        }
+        if (op == "GET_ROWS") return core(out, base(pos, id, {0, 1}), TLH_CORE_GET_ROWS, why);
+        if (op == "SET_ROWS") return core(out, base(pos, id, {0, 1}), TLH_CORE_SET_ROWS, why);
+        if (op == "CPY" || op == "DUP" || op == "CONT") return core(out, base(pos, id, {0}), TLH_CORE_CPY, why);
+        if (op == "ARGMAX") return core(out, base(pos, id, {0}), TLH_CORE_ARGMAX, why);
+        if (op == "GLU") {
+            Dispatch d = base(pos, id, {0, 1});
+            d.op.x[0] = p[0];
+            d.op.x[1] = p[1];
+            return core(out, d, TLH_CORE_GLU, why);
+        }
+        if (op == "SOFT_MAX") {  // lower.rs:314-341
+            if (src(2) >= 0) return why = "sinks are not supported by the soft_max lowering", false;
+            Dispatch d = base(pos, id, {0, 1});
+            const float scale = f32_of(p[0]), max_bias = f32_of(p[1]);
+            const uint32_t nhl2 = 1u << (uint32_t)floorf(log2f((float)g_.t[src(0)].ne[2]));
+            d.op.x[0] = bits_of(scale);
+            d.op.x[1] = bits_of(max_bias);
+            d.op.x[2] = bits_of(powf(2.0f, -max_bias / (float)nhl2));
+            d.op.x[3] = bits_of(powf(2.0f, -(max_bias / 2.0f) / (float)nhl2));
+            d.op.x[4] = nhl2;
+            return core(out, d, TLH_CORE_SOFT_MAX, why);
+        }
+        if (op == "ROPE") {  // lower.rs:422-466 with ggml_rope_yarn_corr_dims (ggml.c:4369-4381)
+            Dispatch d = base(pos, id, {0, 1, 2});
+            const int n_dims = p[1], mode = p[2], n_ctx_orig = p[4];
+            const float freq_base = f32_of(p[5]), freq_scale = f32_of(p[6]), ext_factor = f32_of(p[7]);
+            const float attn_factor = f32_of(p[8]), beta_fast = f32_of(p[9]), beta_slow = f32_of(p[10]);
+            auto corr = [&](float beta) {
+                return n_dims * logf(n_ctx_orig / (beta * 2 * 3.14159265358979323846f)) / (2 * logf(freq_base));
+            };
+            const float start = floorf(corr(beta_fast)), end = ceilf(corr(beta_slow));
+            const float c0 = 0.0f > start ? 0.0f : start;
+            const float c1 = (float)(n_dims - 1) < end ? (float)(n_dims - 1) : end;
+            d.op.x[0] = n_dims;
+            d.op.x[1] = mode;
+            d.op.x[2] = bits_of(freq_scale);
+            d.op.x[3] = bits_of(ext_factor);
+            d.op.x[4] = bits_of(attn_factor);
+            d.op.x[5] = bits_of(powf(freq_base, -2.0f / n_dims));
+            d.op.x[6] = bits_of(c0);
+            d.op.x[7] = bits_of(c1);
+            d.op.x[8] = src(2) >= 0;
+            return core(out, d, TLH_CORE_ROPE, why);
+        }
+        why = "op not implemented in the native HIP executor";
+        return false;
+    }
+
+    // MUL_MAT nodes with more than two activation columns that read the same
+    // bytes with the same weight type (so the same q8 layout) share one
+    // quantization: the first of them writes the blocks into a scratch block
+    // that lives until the last has run. A node that writes into the
+    // activation's storage in between ends the group.
+    void group_mul_mats(std::vector<Dispatch> &d) {
+        using Key = std::tuple<int, int32_t, int64_t, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                               int64_t>;
+        std::map<Key, int> open;  // key -> index of the group's first dispatch
+        std::vector<Dispatch> out;
+        out.reserve(d.size() * 2);
+        std::vector<int> leader(d.size(), -1);
+        for (size_t i = 0; i < d.size(); ++i) {
+            const Dispatch &x = d[i];
+            // a write into storage an open group reads closes that group
+            for (auto it = open.begin(); it != open.end();) {
+                const Place &s1 = d[it->second].src[1];
+                if (x.dst.buf == s1.buf && x.dst.index == s1.index) it = open.erase(it);
+                else ++it;
+            }
+            if (x.kind != D_MUL_MAT || x.op.t[1].ne[1] <= 2) continue;
+            const tlh_tensor &b = x.op.t[1];
+            const Key k{x.src[1].buf, x.src[1].index, x.src[1].off, x.op.t[0].ty, b.ne[0], b.ne[1], b.ne[2], b.ne[3],
+                        b.nb[1], b.nb[2], b.nb[3], x.op.t[0].ne[2]};
+            auto it = open.find(k);
+            if (it == open.end()) {
+                open[k] = (int)i;
+                leader[i] = (int)i;
+            } else {
+                leader[i] = it->second;
+            }
+        }
+        // members per leader
+        std::map<int, std::vector<int>> members;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (leader[i] >= 0) members[leader[i]].push_back((int)i);
+        group_of_.assign(d.size(), -1);
+        groups_.clear();
+        for (auto &[l, m] : members) {
+            if (m.size() < 2) continue;
+            Group gr;
+            gr.first = d[m.front()].pos;
+            gr.last = d[m.back()].pos;
+            for (int i : m) gr.bytes = std::max(gr.bytes, d[i].scratch_bytes);
+            for (int i : m) group_of_[i] = (int)groups_.size();
+            gr.leader = l;
+            groups_.push_back(gr);
+        }
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch x = d[i];
+            const int gi = group_of_[i];
+            if (gi < 0) {
+                out.push_back(x);
+                continue;
+            }
+            x.scratch_bytes = groups_[gi].bytes;
+            x.block = -2 - gi;  // resolved to the group's block by plan()
+            if (groups_[gi].leader == (int)i) {
+                Dispatch q = x;
+                q.kind = D_MM_QUANTIZE;
+                out.push_back(q);
+            }
+            x.kind = D_MM_COMPUTE;
+            out.push_back(x);
+        }
+        d.swap(out);
+    }
+
+    struct Group {
+        int64_t first = 0, last = 0;
+        size_t bytes = 0;
+        int leader = -1;
+    };
+    std::vector<Group> groups_;
+    std::vector<int> group_of_;
+
+    // plan.rs:63-189: liveness of arena roots by node position, then first
+    // fit by start position over the lowest free offset.
+    void plan(Lowered &out) {
+        const int64_t n = (int64_t)g_.nodes.size();
+        std::vector<int64_t> first(g_.n, INT64_MAX), last(g_.n, -1);
+        auto touch = [&](int32_t id, int64_t pos) {
+            int64_t extra;
+            const int32_t r = g_.root(id, extra);
+            first[r] = std::min(first[r], pos);
+            last[r] = std::max(last[r], pos);
+        };
+        for (int64_t pos = 0; pos < n; ++pos) {
+            const int32_t id = g_.nodes[pos];
+            touch(id, pos);
+            for (int s = 0; s < 10; ++s)
+                if (g_.t[id].src[s] >= 0) touch(g_.t[id].src[s], pos);
+        }
+        for (int32_t id : g_.keep) {
+            int64_t extra;
+            const int32_t r = g_.root(id, extra);
+            if (first[r] == INT64_MAX) first[r] = n;
+            last[r] = n;
+        }
+        out.blocks.clear();
+        out.arena_off.assign(g_.n, -1);
+        for (int32_t id = 0; id < g_.n; ++id)
+            if (g_.t[id].view_src < 0 && g_.t[id].storage == TLH_STORE_TEMP && first[id] != INT64_MAX)
+                out.blocks.push_back({first[id], last[id], align_up(std::max<int64_t>(nbytes(g_.t[id]), 1)), id});
+        const size_t n_tensor_blocks = out.blocks.size();
+        // scratch: one block per ungrouped dispatch that asks for it, one per group
+        std::vector<int> disp_block(out.d.size(), -1);
+        for (size_t i = 0; i < out.d.size(); ++i) {
+            Dispatch &x = out.d[i];
+            if (x.block <= -2 || x.scratch_bytes == 0) continue;
+            disp_block[i] = (int)out.blocks.size();
+            out.blocks.push_back({x.pos, x.pos, align_up((int64_t)x.scratch_bytes), -1});
+        }
+        std::vector<int> group_block(groups_.size());
+        for (size_t gi = 0; gi < groups_.size(); ++gi) {
+            group_block[gi] = (int)out.blocks.size();
+            out.blocks.push_back({groups_[gi].first, groups_[gi].last, align_up((int64_t)groups_[gi].bytes), -1});
+        }
+        for (size_t i = 0; i < out.d.size(); ++i) {
+            Dispatch &x = out.d[i];
+            if (x.block <= -2) x.block = group_block[-2 - x.block];
+            else if (disp_block[i] >= 0) x.block = disp_block[i];
+        }
+        // order: (first, tensor blocks before scratch, index)
+        std::vector<int> order(out.blocks.size());
+        for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+        std::sort(order.begin(), order.end(), [&](int a, int b) {
+            const bool sa = (size_t)a >= n_tensor_blocks, sb = (size_t)b >= n_tensor_blocks;
+            return std::make_tuple(out.blocks[a].first, sa, a) < std::make_tuple(out.blocks[b].first, sb, b);
+        });
+        struct Live {
+            int64_t off, size, last;
+        };
+        std::vector<Live> live;
+        int64_t arena = 0;
+        for (int bi : order) {
+            Block &b = out.blocks[bi];
+            live.erase(std::remove_if(live.begin(), live.end(), [&](const Live &l) { return l.last < b.first; }),
+                       live.end());
+            std::sort(live.begin(), live.end(), [](const Live &x, const Live &y) { return x.off < y.off; });
+            int64_t off = 0;
+            for (const Live &l : live) {
+                if (l.off >= off + b.size) break;
+                off = std::max(off, l.off + l.size);
+            }
+            b.off = off;
+            live.push_back({off, b.size, b.last});
+            arena = std::max(arena, off + b.size);
+        }
+        for (size_t i = 0; i < n_tensor_blocks; ++i) out.arena_off[out.blocks[i].tensor] = out.blocks[i].off;
+        out.node_scratch.assign(n, -1);
+        for (const Dispatch &x : out.d)
+            if (x.block >= 0) out.node_scratch[x.pos] = out.blocks[x.block].off;
+        out.arena = arena;
+    }
+};
+
+tlh_status read_graph(const tlh_ir_tensor *tensors, int32_t n_tensors, const int32_t *nodes, int32_t n_nodes,
+                      const int32_t *keep, int32_t n_keep, Graph &g) {
+    if (!tensors || n_tensors < 0 || n_nodes < 0 || n_keep < 0 || (n_nodes && !nodes) || (n_keep && !keep))
+        return set_error(TLH_INVALID, "program: null or negative graph arrays");
+    g.t = tensors;
+    g.n = n_tensors;
+    g.nodes.assign(nodes, nodes + n_nodes);
+    g.keep.assign(keep, keep + n_keep);
+    for (int32_t id = 0; id < n_tensors; ++id) {
+        const tlh_ir_tensor &t = tensors[id];
+        if (memchr(t.op, 0, sizeof t.op) == nullptr) return set_error(TLH_INVALID, "tensor %d: op name not terminated", id);
+        for (int s = 0; s < 10; ++s)
+            if (t.src[s] < -1 || t.src[s] >= n_tensors) return set_error(TLH_INVALID, "tensor %d: source %d out of range", id, s);
+        if (t.view_src >= n_tensors || t.view_src < -1 || (t.view_src >= 0 && tensors[t.view_src].view_src >= 0))
+            return set_error(TLH_INVALID, "tensor %d: view_src must be a root tensor", id);
+        if (t.view_src < 0 && (t.storage < TLH_STORE_TEMP || t.storage > TLH_STORE_INPUT))
+            return set_error(TLH_INVALID, "tensor %d: storage %d", id, t.storage);
+        for (int i = 0; i < 4; ++i)
+            if (t.ne[i] < 0 || t.nb[i] < 0) return set_error(TLH_INVALID, "tensor %d: negative extent or stride", id);
+        int64_t blck, size;
+        if (!type_traits(t.ty, blck, size)) return set_error(TLH_UNSUPPORTED, "tensor %d: ggml type %d", id, t.ty);
+    }
+    for (int32_t id : g.nodes)
+        if (id < 0 || id >= n_tensors) return set_error(TLH_INVALID, "program: node id %d out of range", id);
+    for (int32_t id : g.keep)
+        if (id < 0 || id >= n_tensors) return set_error(TLH_INVALID, "program: kept id %d out of range", id);
+    return TLH_OK;
+}
+
+}  // namespace
+}  // namespace tlh
+
+using namespace tlh;
+
+struct tlh_program {
+    std::vector<tlh_ir_tensor> tensors;
+    Lowered low;
+    std::vector<const void *> weights;
+    std::vector<int64_t> state_offsets;
+    std::vector<std::pair<int64_t, int64_t>> inputs;  // (io offset, bytes) per input index
+    int64_t io_bytes = 0;
+    char *arena = nullptr, *io = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void *exec_state = nullptr;
+    hipStream_t exec_stream = nullptr;
+    int device = 0;
+
+    void *resolve(const Place &p, void *state) const {
+        switch (p.buf) {
+        case B_ARENA: return arena + low.arena_off[p.index] + p.off;
+        case B_IO: return io + inputs[p.index].first + p.off;
+        case B_STATE: return (char *)state + state_offsets[p.index] + p.off;
+        case B_WEIGHT: return (char *)weights[p.index] + p.off;
+        default: return nullptr;
+        }
+    }
+
+    tlh_status enqueue(void *state, hipStream_t s) const {
+        for (const Dispatch &x : low.d) {
+            void *src[4];
+            for (int i = 0; i < 4; ++i) src[i] = resolve(x.src[i], state);
+            void *dst = resolve(x.dst, state);
+            void *scratch = x.block >= 0 ? arena + low.blocks[x.block].off : nullptr;
+            tlh_status st;
+            switch (x.kind) {
+            case D_MUL_MAT: st = tlh_mul_mat(&x.op, src[0], src[1], dst, scratch, x.scratch_bytes, s); break;
+            case D_MM_QUANTIZE: st = tlh_mul_mat_quantize(&x.op, src[1], scratch, x.scratch_bytes, s); break;
+            case D_MM_COMPUTE: st = tlh_mul_mat_compute(&x.op, src[0], scratch, x.scratch_bytes, dst, s); break;
+            case D_FLASH_ATTN:
+                st = tlh_flash_attn_ext(&x.op, src[0], src[1], src[2], src[3], dst, scratch, x.scratch_bytes, s);
+                break;
+            default: st = tlh_core(x.core_kind, &x.op, src[0], src[1], src[2], dst, s); break;
+            }
+            if (st != TLH_OK) {
+                const int32_t id = low.node_ids[x.pos];
+                const std::string msg = tlh_last_error();
+                return set_error(st, "launching `%s` (tensor %d): %s", tensors[id].op, id, msg.c_str());
+            }
+        }
+        return TLH_OK;
+    }
+
+    void drop_graph() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        exec = nullptr;
+        exec_state = nullptr;
+        exec_stream = nullptr;
+    }
+};
+
+namespace {
+
+tlh_status hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return TLH_OK;
+    (void)hipGetLastError();
+    if (e == hipErrorOutOfMemory) return set_error(TLH_ALLOC, "%s: %s", what, hipGetErrorString(e));
+    return set_error(TLH_EXECUTION, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+tlh_status tlh_program_plan(const tlh_ir_tensor *tensors, int32_t n_tensors, const int32_t *nodes, int32_t n_nodes,
+                            const int32_t *keep, int32_t n_keep, int64_t *tensor_offsets, int64_t *scratch_offsets,
+                            size_t *arena_bytes) {
+    Graph g;
+    tlh_status st = read_graph(tensors, n_tensors, nodes, n_nodes, keep, n_keep, g);
+    if (st != TLH_OK) return st;
+    Lowered low;
+    if ((st = Lowering(g).run(low)) != TLH_OK) return st;
+    if (tensor_offsets)
+        for (int32_t id = 0; id < n_tensors; ++id) {
+            int64_t extra = 0;
+            const int32_t r = g.root(id, extra);
+            tensor_offsets[id] = low.arena_off[r] >= 0 ? low.arena_off[r] + extra : -1;
+        }
+    if (scratch_offsets)
+        for (int32_t i = 0; i < n_nodes; ++i) scratch_offsets[i] = low.node_scratch[i];
+    if (arena_bytes) *arena_bytes = (size_t)low.arena;
+    return TLH_OK;
+}
+
+tlh_status tlh_program_compile(const tlh_ir_tensor *tensors, int32_t n_tensors, const int32_t *nodes,
+                               int32_t n_nodes, const int32_t *keep, int32_t n_keep, const void *const *weights,
+                               int32_t n_weights, const int64_t *state_offsets, int32_t n_states,
+                               tlh_program **program) {
+    if (!program) return set_error(TLH_INVALID, "program_compile: null result pointer");
+    *program = nullptr;
+    if (n_weights < 0 || n_states < 0 || (n_weights && !weights) || (n_states && !state_offsets))
+        return set_error(TLH_INVALID, "program_compile: null or negative leaf arrays");
+    Graph g;
+    tlh_status st = read_graph(tensors, n_tensors, nodes, n_nodes, keep, n_keep, g);
+    if (st != TLH_OK) return st;
+    // leaves must exist for every root that names them
+    int32_t n_inputs = 0;
+    for (int32_t id = 0; id < n_tensors; ++id) {
+        const tlh_ir_tensor &t = tensors[id];
+        if (t.view_src >= 0) continue;
+        const int32_t k = t.storage_index;
+        if (t.storage == TLH_STORE_WEIGHT && (k < 0 || k >= n_weights))
+            return set_error(TLH_INVALID, "tensor %d: weight index %d of %d", id, k, n_weights);
+        if (t.storage == TLH_STORE_STATE && (k < 0 || k >= n_states))
+            return set_error(TLH_INVALID, "tensor %d: state index %d of %d", id, k, n_states);
+        if (t.storage == TLH_STORE_INPUT) {
+            if (k < 0 || k >= n_tensors) return set_error(TLH_INVALID, "tensor %d: input index %d", id, k);
+            n_inputs = std::max(n_inputs, k + 1);
+        }
+    }
+    tlh_program *p = new tlh_program;
+    p->tensors.assign(tensors, tensors + n_tensors);
+    g.t = p->tensors.data();
+    if ((st = Lowering(g).run(p->low)) != TLH_OK) {
+        delete p;
+        return st;
+    }
+    p->weights.assign(weights, weights + n_weights);
+    p->state_offsets.assign(state_offsets, state_offsets + n_states);
+    // inputs live in the io buffer, by input index (plan.rs:155-167)
+    p->inputs.assign(n_inputs, {0, 0});
+    std::vector<int64_t> in_bytes(n_inputs, -1);
+    for (int32_t id = 0; id < n_tensors; ++id) {
+        const tlh_ir_tensor &t = tensors[id];
+        if (t.view_src < 0 && t.storage == TLH_STORE_INPUT) in_bytes[t.storage_index] = nbytes(t);
+    }
+    for (int32_t i = 0; i < n_inputs; ++i) {
+        p->inputs[i] = {p->io_bytes, std::max<int64_t>(in_bytes[i], 0)};
+        p->io_bytes += align_up(std::max<int64_t>(in_bytes[i], 1));
+    }
+    (void)hipGetDevice(&p->device);
+    if ((st = hip_ok(hipMalloc((void **)&p->arena, (size_t)std::max<int64_t>(p->low.arena, ALIGN)), "arena")) !=
+            TLH_OK ||
+        (st = hip_ok(hipMalloc((void **)&p->io, (size_t)std::max<int64_t>(p->io_bytes, ALIGN)), "io buffer")) !=
+            TLH_OK) {
+        tlh_program_destroy(p);
+        return st;
+    }
+    *program = p;
+    return TLH_OK;
+}
+
+tlh_status tlh_program_destroy(tlh_program *p) {
+    if (!p) return TLH_OK;
+    p->drop_graph();
+    if (p->arena) (void)hipFree(p->arena);
+    if (p->io) (void)hipFree(p->io);
+    delete p;
+    return TLH_OK;
+}
+
+tlh_status tlh_copy(void *dst, const void *src, size_t bytes, void *stream) {
+    if (!bytes) return TLH_OK;
+    if (!dst || !src) return set_error(TLH_INVALID, "copy: null pointer");
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, (hipStream_t)stream), "copy");
+}
+
+tlh_status tlh_program_input(const tlh_program *p, int32_t i, void **ptr, size_t *bytes) {
+    if (!p || !ptr) return set_error(TLH_INVALID, "program_input: null pointer");
+    if (i < 0 || i >= (int32_t)p->inputs.size()) return set_error(TLH_INVALID, "program_input: no graph input %d", i);
+    *ptr = p->io + p->inputs[i].first;
+    if (bytes) *bytes = (size_t)p->inputs[i].second;
+    return TLH_OK;
+}
+
+tlh_status tlh_program_tensor(const tlh_program *p, int32_t id, void *state, void **ptr) {
+    if (!p || !ptr) return set_error(TLH_INVALID, "program_tensor: null pointer");
+    if (id < 0 || id >= (int32_t)p->tensors.size()) return set_error(TLH_INVALID, "program_tensor: id %d", id);
+    const tlh_ir_tensor &t = p->tensors[id];
+    const int32_t r = t.view_src >= 0 ? t.view_src : id;
+    const int64_t extra = t.view_src >= 0 ? t.view_offs : 0;
+    const tlh_ir_tensor &rt = p->tensors[r];
+    switch (rt.storage) {
+    case TLH_STORE_WEIGHT: *ptr = (char *)p->weights[rt.storage_index] + extra; break;
+    case TLH_STORE_STATE:
+        if (!state) return set_error(TLH_INVALID, "program_tensor: tensor %d is state; pass the state buffer", id);
+        *ptr = (char *)state + p->state_offsets[rt.storage_index] + extra;
+        break;
+    case TLH_STORE_INPUT: *ptr = p->io + p->inputs[rt.storage_index].first + extra; break;
+    default:
+        if (p->low.arena_off[r] < 0) return set_error(TLH_INVALID, "program_tensor: tensor %d is never computed", id);
+        *ptr = p->arena + p->low.arena_off[r] + extra;
+    }
+    return TLH_OK;
+}
+
+tlh_status tlh_program_run(tlh_program *p, void *state, void *stream, int32_t graph) {
+    if (!p) return set_error(TLH_INVALID, "program_run: null program");
+    if (!p->state_offsets.empty() && !state) return set_error(TLH_INVALID, "program_run: the graph has state; pass its buffer");
+    const hipStream_t s = (hipStream_t)stream;
+    if (!graph) return p->enqueue(state, s);
+    if (!s) return set_error(TLH_INVALID, "program_run: graph replay needs a stream other than the null stream");
+    if (!p->exec || p->exec_state != state || p->exec_stream != s) {
+        p->drop_graph();
+        tlh_status st = hip_ok(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+        if (st != TLH_OK) return st;
+        st = p->enqueue(state, s);
+        hipGraph_t gr = nullptr;
+        const hipError_t e = hipStreamEndCapture(s, &gr);
+        if (st != TLH_OK) {
+            if (gr) (void)hipGraphDestroy(gr);
+            return st;
+        }
+        if ((st = hip_ok(e, "hipStreamEndCapture")) != TLH_OK) return st;
+        hipGraphExec_t ex = nullptr;
+        st = hip_ok(hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0), "hipGraphInstantiate");
+        (void)hipGraphDestroy(gr);
+        if (st != TLH_OK) return st;
+        p->exec = ex;
+        p->exec_state = state;
+        p->exec_stream = s;
+    }
+    return hip_ok(hipGraphLaunch(p->exec, s), "hipGraphLaunch");
+}
+
+tlh_status tlh_program_stats(const tlh_program *p, size_t *arena_bytes, size_t *io_bytes, int32_t *launches) {
+    if (!p) return set_error(TLH_INVALID, "program_stats: null program");
+    if (arena_bytes) *arena_bytes = (size_t)p->low.arena;
+    if (io_bytes) *io_bytes = (size_t)p->io_bytes;
+    if (launches) *launches = (int32_t)p->low.d.size();
+    return TLH_OK;
+}
+
+}  // extern "C"

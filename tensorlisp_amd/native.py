@@ -33,7 +33,8 @@ EXPORTS = (
     "tlh_mul_mat_quantize", "tlh_mul_mat_compute",
     "tlh_quantize_act", "tlh_dequantize", "tlh_flash_attn_ext_scratch_bytes", "tlh_flash_attn_ext",
     "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
-    "tlh_core_check", "tlh_core",
+    "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_program_input",
+    "tlh_program_tensor", "tlh_program_run", "tlh_program_stats", "tlh_program_plan",
 )
 
 
@@ -98,6 +99,17 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]
     L.tlh_core_check.argtypes = [C.c_int, C.POINTER(TlhOp), C.c_int, C.c_int]
     L.tlh_core.argtypes = [C.c_int, C.POINTER(TlhOp), vp, vp, vp, vp, vp]
+    i32p, i64p = C.POINTER(C.c_int32), C.POINTER(C.c_int64)
+    L.tlh_program_compile.argtypes = [vp, C.c_int32, i32p, C.c_int32, i32p, C.c_int32, C.POINTER(C.c_void_p),
+                                      C.c_int32, i64p, C.c_int32, C.POINTER(C.c_void_p)]
+    L.tlh_program_destroy.argtypes = [vp]
+    L.tlh_copy.argtypes = [vp, vp, C.c_size_t, vp]
+    L.tlh_program_input.argtypes = [vp, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+    L.tlh_program_tensor.argtypes = [vp, C.c_int32, vp, C.POINTER(C.c_void_p)]
+    L.tlh_program_run.argtypes = [vp, vp, vp, C.c_int32]
+    L.tlh_program_stats.argtypes = [vp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]
+    L.tlh_program_plan.argtypes = [vp, C.c_int32, i32p, C.c_int32, i32p, C.c_int32, i64p, i64p,
+                                   C.POINTER(C.c_size_t)]
     for name in EXPORTS:
         if name not in ("tlh_last_error", "tlh_status_name", "tlh_version"):
             getattr(L, name).restype = st

@@ -38,7 +38,14 @@ these are the reference's outputs on fixed inputs, captured once:
                    inputs (native.rs:109-498) and decoder-sized ones; inputs are
                    regenerated from seeds, the file keeps the outputs
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | core]   (needs oracle/_ref built)
+  decoder.npz      a llama-style decoder step graph (tensorlisp_amd.graph.decoder_step,
+                   refs.decoder_tiny_config: 2 layers, 4 heads of 64, 2 KV heads,
+                   q4_K / q6_K weights from refs.decoder_weights) run on the CPU
+                   backend for refs.DECODER_STEPS (a 5-token prompt, three
+                   single-token steps, a 3-token chunk): logits and argmax per
+                   step and the f16 KV caches after the last one
+
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | core | decoder]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -52,8 +59,8 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import (FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, core_cases, core_ref, fa_case_inputs,  # noqa: E402
-                  fp16_probe_values, xorshift_noise)
+from refs import (FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
+                  decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
 
 
@@ -121,8 +128,20 @@ def core_golden(ref) -> None:
     np.savez_compressed(HERE / "core.npz", **{c["name"]: core_ref(ref, c) for c in core_cases()})
 
 
+def decoder_golden(ref) -> None:
+    c = decoder_tiny_config()
+    logits, ams, caches = decoder_ref_run(ref, c, decoder_weights(c))
+    out = {f"logits{i}": lg for i, lg in enumerate(logits)}
+    out.update({f"argmax{i}": a for i, a in enumerate(ams)})
+    out.update({f"cache{i}": s for i, s in enumerate(caches)})
+    np.savez_compressed(HERE / "decoder.npz", **out)
+
+
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["decoder"]:  # only the decoder-step fixture
+        decoder_golden(ref)
+        return
     if sys.argv[1:] == ["core"]:  # only the core-op fixture
         core_golden(ref)
         return
@@ -193,6 +212,7 @@ def main() -> None:
     flash_attn_ext_golden(ref)
     q6_K_golden(ref)
     core_golden(ref)
+    decoder_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

@@ -339,6 +339,7 @@ class Ref:
             vp, C.c_int, C.c_int, C.POINTER(C.c_double)]
         L.ref_flash_attn_ext.restype = C.c_int
         L.ref_core.argtypes = [C.c_int, vp, vp, vp, vp, vp, C.c_int]
+        L.ref_ir_run.argtypes = [vp, C.c_int, vp, C.c_int, vp, vp, vp, vp, vp, C.c_int, C.c_int]
         L.ggml_cpu_init.argtypes = []
         L.ggml_cpu_init()
 
@@ -471,6 +472,29 @@ class Ref:
         rc = self.lib.ref_core(kind, _p(ty), _p(ne), C.cast(ptrs, C.c_void_p), _p(ipa), _p(fpa), nthreads)
         assert rc == 0, rc
         return dst
+
+
+    def ir_run(self, builder, weights, states, inputs, outs, nthreads: int = 8):
+        """Runs a tensorlisp_amd.graph.Builder graph through ggml (ref_ir_run in
+        oracle/ref_graph.c): weights / states / inputs are contiguous numpy arrays
+        by storage index (states are updated in place); `outs` are (tensor,
+        numpy dtype); returns their values. Fails if ggml shapes any tensor
+        differently from the builder."""
+        recs = builder.records()
+        nodes = np.array(builder.nodes, np.int32)
+        arrs = [np.ascontiguousarray(a) for a in weights] + list(inputs)
+        for a in states:
+            assert a.flags.c_contiguous
+        ptrs = lambda xs: (C.c_void_p * max(len(xs), 1))(*[x.ctypes.data for x in xs])  # noqa: E731
+        inputs = [np.ascontiguousarray(a) for a in inputs]
+        res = [np.empty(t.ne[::-1], dt) for t, dt in outs]
+        ids = np.array([t.id for t, _ in outs], np.int32)
+        rc = self.lib.ref_ir_run(C.cast(recs, C.c_void_p), len(builder.t), _p(nodes), len(nodes),
+                                 C.cast(ptrs(arrs[:len(weights)]), C.c_void_p), C.cast(ptrs(states), C.c_void_p),
+                                 C.cast(ptrs(inputs), C.c_void_p), _p(ids), C.cast(ptrs(res), C.c_void_p), len(res),
+                                 nthreads)
+        assert rc == 0, (rc, builder.t[-rc % 1000].op if rc < -999 else "")
+        return res
 
 
 def flash_attn_f64(q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0) -> np.ndarray:
@@ -858,3 +882,55 @@ def core_perm_view(a: np.ndarray, perm):
     v = a4.transpose([3 - ax[3 - j] for j in range(4)])
     assert all(s == 1 for s in v.shape[:4 - nd]), "the permutation must keep the padding axes"
     return v[(0,) * (4 - nd)]
+
+
+# ------------------------------------------------------------ decoder steps
+def decoder_tiny_config():
+    from tensorlisp_amd import graph as G
+
+    return G.DecoderConfig(n_embd=256, n_head=4, n_head_kv=2, n_ff=512, n_layer=2, n_vocab=1000, n_ctx=64)
+
+
+def decoder_weights(c, seed=100):
+    """Host weights for a decoder config: structurally valid random blocks and
+    norm weights near one (synth, seeded by weight index)."""
+    from tensorlisp_amd import native as N
+    from tensorlisp_amd import synth
+
+    out = []
+    for i, (_, ty, ne) in enumerate(c.weight_shapes()):
+        if ty == N.F32:
+            out.append((1.0 + 0.1 * synth.normal(seed + i, (ne[0],))).astype(np.float32))
+        else:
+            out.append(synth.random_blocks(ty, seed + i, ne[1], ne[0], 0.05))
+    return out
+
+
+# (tokens, first position, attended cache rows, logits of every token?): a
+# 5-token prompt, then three single-token steps, then a 3-token chunk
+DECODER_STEPS = [([1, 7, 3, 999, 0], 0, 8, False), ([42], 5, 8, False), ([17], 6, 8, False), ([500], 7, 8, False),
+                 ([3, 4, 5], 8, 16, True)]
+
+
+def decoder_step_inputs(step):
+    from tensorlisp_amd import graph as G
+
+    toks, p0, n_kv, _ = step
+    pos = np.arange(len(toks), dtype=np.int32) + p0
+    return [np.array(toks, np.int32), pos, pos.astype(np.int64), G.causal_mask(pos, n_kv)]
+
+
+def decoder_ref_run(r, c, weights):
+    """DECODER_STEPS through the reference CPU backend; returns (logits per
+    step, argmax per step, final caches)."""
+    from tensorlisp_amd import graph as G
+
+    states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
+    logits, ams = [], []
+    for step in DECODER_STEPS:
+        st = G.decoder_step(c, len(step[0]), step[2], last_only=not step[3])
+        lg, am = r.ir_run(st.builder, weights, states, decoder_step_inputs(step),
+                          [(st.logits, np.float32), (st.argmax, np.int32)])
+        logits.append(lg.reshape(-1, c.n_vocab))
+        ams.append(am.reshape(-1))
+    return logits, ams, states

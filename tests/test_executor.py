@@ -1,0 +1,178 @@
+"""The executor's host side without a GPU: the memory plan (tlh_program_plan),
+IR validation and unsupported-op reporting, and the graph builder against ggml.
+
+Plan properties follow the reference's own planner tests
+(crates/kernels/src/plan.rs:196-315): a chain of adds reuses two blocks, a
+view keeps its source alive until the view's last reader, and on random graphs
+no two tensors that are alive at the same node share bytes, no node writes
+over its own source, and every scratch block is 256-byte aligned. The builder
+is pinned by rebuilding its graphs with the ggml constructors in the compiled
+reference (oracle/ref_graph.c ref_ir_run), which must give every tensor the
+same ne, nb and view placement.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from refs import decoder_tiny_config, decoder_weights, ref
+from tensorlisp_amd import graph as G
+from tensorlisp_amd import native as N
+
+
+def lcg(state):
+    state[0] = (state[0] * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+    return state[0] >> 33
+
+
+def test_a_chain_reuses_two_blocks():
+    b = G.Builder()
+    x = b.input(N.F32, [256])
+    t = x
+    for _ in range(6):
+        t = b.add(t, x)
+    b.expand(t)
+    offs, _, size = G.plan(b, [t])
+    assert size == 2 * 1024  # each add reads its predecessor while writing: two blocks
+    assert offs[x.id] == -1  # the input lives in the io buffer
+
+
+def test_views_extend_the_life_of_their_source():
+    b = G.Builder()
+    x = b.input(N.F32, [256])
+    a = b.add(x, x)
+    tail = b.view(a, [128], offset=512)
+    c1 = b.add(x, x)
+    c2 = b.add(c1, c1)
+    late = b.add(tail, tail)
+    for t in (a, tail, c1, c2, late):
+        b.expand(t)
+    offs, _, _ = G.plan(b, [late])
+    assert offs[tail.id] == offs[a.id] + 512
+    over = lambda p, q: p < q + 1024 and q < p + 1024  # noqa: E731
+    assert not over(offs[a.id], offs[c1.id]) and not over(offs[a.id], offs[c2.id])
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_graphs_never_overlap_live_tensors(seed):
+    st = [seed * 7919 + 7]
+    b = G.Builder()
+    x = b.input(N.F32, [64])
+    ts = [x]
+    for _ in range(5 + lcg(st) % 40):
+        a, c = ts[lcg(st) % len(ts)], ts[lcg(st) % len(ts)]
+        size = 16 * (1 + lcg(st) % 40)
+        va = b.view(a, [min(size, a.ne[0])]) if a.ne[0] >= size else a
+        vc = b.view(c, [min(size, c.ne[0])]) if c.ne[0] >= size else c
+        if va.ne[0] != vc.ne[0]:
+            vc = va
+        t = b.add(va, vc)
+        b.expand(t)
+        ts.append(t)
+    offs, _, _ = G.plan(b, [ts[-1]])
+    nodes = b.nodes
+    pos = {n: i for i, n in enumerate(nodes)}
+    root = lambda t: t if t.view_src < 0 else b.t[t.view_src]  # noqa: E731
+    live = {}
+    for p, n in enumerate(nodes):
+        for tid in [n] + b.t[n].src:
+            r = root(b.t[tid])
+            if r.storage != G.STORE_TEMP:
+                continue
+            lo, hi = live.get(r.id, (p, p))
+            live[r.id] = (min(lo, p), max(hi, p))
+    r_last = root(ts[-1]).id
+    live[r_last] = (live[r_last][0], len(nodes))
+    items = [(rid, lo, hi, offs[rid], b.t[rid].ne[0] * 4) for rid, (lo, hi) in live.items()]
+    for i, x1 in enumerate(items):
+        for x2 in items[i + 1:]:
+            time = x1[1] <= x2[2] and x2[1] <= x1[2]
+            space = x1[3] < x2[3] + x2[4] and x2[3] < x1[3] + x1[4]
+            assert not (time and space), (x1, x2)
+    del pos
+
+
+def _mm_graph(n_cols):
+    """Q, K and V projections of one normed activation, then their sum."""
+    b = G.Builder()
+    wq = b.weight(N.Q4_K, [512, 256])
+    wk = b.weight(N.Q4_K, [512, 256])
+    wv = b.weight(N.Q6_K, [512, 256])
+    x = b.input(N.F32, [512, n_cols])
+    h = b.rms_norm(x, 1e-5)
+    q, k, v = b.mul_mat(wq, h), b.mul_mat(wk, h), b.mul_mat(wv, h)
+    out = b.add(b.add(q, k), v)
+    b.expand(out)
+    return b, out, (q, k, v)
+
+
+def test_mul_mats_of_one_activation_share_its_quantization():
+    """Q and K (same weight type) read one quantized copy of the normed activation:
+    one scratch block that lives from the first to the second; V (q6_K) has its
+    own. At one or two columns each GEMV quantizes on the fly instead."""
+    b, out, (q, k, v) = _mm_graph(8)
+    _, scr, _ = G.plan(b, [out])
+    pos = {n: i for i, n in enumerate(b.nodes)}
+    assert scr[pos[q.id]] >= 0 and scr[pos[q.id]] == scr[pos[k.id]]
+    assert scr[pos[v.id]] >= 0
+    b1, out1, (q1, k1, v1) = _mm_graph(1)
+    _, scr1, _ = G.plan(b1, [out1])
+    pos1 = {n: i for i, n in enumerate(b1.nodes)}
+    assert scr1[pos1[q1.id]] != scr1[pos1[k1.id]] or scr1[pos1[q1.id]] < 0
+
+
+def test_unsupported_ops_are_reported_by_name():
+    """Every node is lowered before failing; the error counts each missing op and
+    gives an example (the reference's exec.rs:39-58)."""
+    b = G.Builder()
+    x = b.input(N.F32, [64, 4])
+    y = b.add(x, x)
+    s1 = b._new(N.F32, [64, 4], "IM2COL", [y])
+    s2 = b._new(N.F32, [64, 4], "IM2COL", [s1])
+    z = b._new(N.F32, [64, 4], "POOL_2D", [s2])
+    b.expand(z)
+    with pytest.raises(N.TlhError, match=r"IM2COL x2 .*POOL_2D x1"):
+        G.plan(b, [z])
+    b = G.Builder()
+    w = b._new(13, [256, 8], nb=[176, 176, 1408, 1408], storage=G.STORE_WEIGHT, index=0)  # q5_K: not taken
+    x = b.input(N.F32, [256, 1])
+    b.expand(b.mul_mat(w, x))
+    with pytest.raises(N.TlhError, match="MUL_MAT x1"):
+        G.plan(b, [b.t[-1]])
+
+
+def test_ir_validation():
+    b = G.Builder()
+    x = b.input(N.F32, [64])
+    y = b.add(x, x)
+    b.expand(y)
+    recs = b.records()
+    recs[1].src[0] = 99
+    nodes = (C.c_int32 * 1)(y.id)
+    st = N.lib().tlh_program_plan(recs, 2, nodes, 1, nodes, 1, None, None, None)
+    assert N.STATUS[st] == "INVALID" and "out of range" in N.lib().tlh_last_error().decode()
+    recs = b.records()
+    recs[0].ty = 99
+    st = N.lib().tlh_program_plan(recs, 2, nodes, 1, nodes, 1, None, None, None)
+    assert N.STATUS[st] == "UNSUPPORTED"
+
+
+TINY = decoder_tiny_config()
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("T,n_kv,last_only", [(5, 8, True), (1, 8, True), (3, 64, False)])
+def test_decoder_graph_is_the_graph_ggml_builds(T, n_kv, last_only):
+    """ggml's constructors, called as each record says, give every tensor of the
+    decoder step the builder's ne, nb and view placement; the CPU backend then
+    runs it (finite logits)."""
+    st = G.decoder_step(TINY, T, n_kv, last_only)
+    states = [np.zeros((TINY.n_ctx, TINY.n_embd_kv), np.uint16) for _ in range(2 * TINY.n_layer)]
+    pos = np.arange(T, dtype=np.int32) + (n_kv - T)
+    inputs = [np.arange(T, dtype=np.int32) * 7 % 1000, pos, pos.astype(np.int64), G.causal_mask(pos, n_kv)]
+    logits, am = ref().ir_run(st.builder, decoder_weights(TINY), states, inputs,
+                              [(st.logits, np.float32), (st.argmax, np.int32)])
+    assert np.all(np.isfinite(logits)) and am.size == (1 if last_only else T)
+    assert np.any(states[0] != 0)  # SET_ROWS wrote the cache
