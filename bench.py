@@ -63,6 +63,104 @@ def gpu_blocks(torch, wtype, M, K, gen):
     return raw.reshape(M, (K // be) * bb)
 
 
+def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32):
+    """configs[4] at batch 1 through the executor (tlh_program_*): Llama-3-8B
+    shapes with q4_K matrices, a q4_K token embedding and a q6_K lm_head, f16 KV
+    caches written with SET_ROWS and read with FLASH_ATTN_EXT. A 512-token
+    prefill, then greedy decode steps whose next token is the previous step's
+    argmax, copied on the device into the next step's input (no host round
+    trip). Decode attends a cache view padded to 768 rows (the mask hides the
+    rows not yet written) so one program, captured once as a hipGraph, serves
+    every step. Returns a dict of timings."""
+    import numpy as np
+
+    from tensorlisp_amd import graph as G
+    from tensorlisp_amd import native as N
+
+    c = G.DecoderConfig(n_ctx=1024)
+    W = []
+    for _, ty, ne in c.weight_shapes():
+        if ty == N.F32:
+            W.append(1.0 + 0.1 * torch.randn(ne[0], device="cuda", generator=gen))
+        else:
+            W.append(gpu_blocks(torch, ty, ne[1], ne[0], gen))
+    offs, total = c.state_bytes()
+    state = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    weight_bytes = sum(w.numel() * w.element_size() for w in W)
+    stream = torch.cuda.Stream()
+    copy = lambda dst, src, n: N.check(N.lib().tlh_copy(dst, src, n, N._stream(stream)))  # noqa: E731
+
+    # prefill: 512 tokens at positions 0..511, logits of the last one
+    T = prefill_tokens
+    pre = G.decoder_step(c, T, T)
+    P = G.Program(pre.builder, pre.keep, W, offs)
+    toks = torch.randint(0, c.n_vocab, (T,), device="cuda", generator=gen, dtype=torch.int32)
+    pos = torch.arange(T, device="cuda", dtype=torch.int32)
+    mask = torch.from_numpy(G.causal_mask(np.arange(T), T).view(np.int16)).cuda()
+    with torch.cuda.stream(stream):
+        for i, a in enumerate((toks, pos, pos.to(torch.int64), mask)):
+            P.write_input(i, a, stream)
+    P.run(state, stream)  # warm
+    stream.synchronize()
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        P.run(state, stream, graph=True)
+    stream.synchronize()
+    prefill_ms = (time.perf_counter() - t0) / reps * 1e3
+
+    # decode: one token a step at positions 512.., over a 768-row cache view
+    n_kv = 768
+    dec = G.decoder_step(c, 1, n_kv)
+    D = G.Program(dec.builder, dec.keep, W, offs)
+    steps = decode_steps
+    dpos = torch.arange(T, T + steps, device="cuda", dtype=torch.int32)
+    dslot = dpos.to(torch.int64)
+    dmask = torch.from_numpy(G.causal_mask(np.arange(T, T + steps), n_kv).view(np.int16)).cuda()
+    inp = [D.input(i)[0] for i in range(4)]
+    am_dec = D.tensor_ptr(dec.argmax, state)
+    am_pre = P.tensor_ptr(pre.argmax, state)
+
+    def run_decode(n, graph):
+        copy(inp[0], am_pre, 4)  # the prompt's greedy token starts the decode
+        for i in range(n):
+            copy(inp[1], dpos.data_ptr() + 4 * i, 4)
+            copy(inp[2], dslot.data_ptr() + 8 * i, 8)
+            copy(inp[3], dmask.data_ptr() + 2 * n_kv * i, 2 * n_kv)
+            D.run(state, stream, graph)
+            copy(inp[0], am_dec, 4)
+
+    run_decode(4, True)  # capture and warm
+    stream.synchronize()
+    t0 = time.perf_counter()
+    run_decode(steps, True)
+    stream.synchronize()
+    graph_ms = (time.perf_counter() - t0) / steps * 1e3
+    t0 = time.perf_counter()
+    run_decode(eager_steps, False)
+    stream.synchronize()
+    eager_ms = (time.perf_counter() - t0) / eager_steps * 1e3
+    kv_bytes = 2 * c.n_layer * n_kv * c.n_embd_kv * 2  # every cache row the padded view attends
+    tok_bytes = weight_bytes - W[0].numel() + c.n_embd * 2 + kv_bytes  # embedding: one row
+    out = {
+        "model": "Llama-3-8B shapes: 32 layers, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 128256, "
+                 "RoPE 500000; q4_K matrices and token embedding, q6_K lm_head; random weights",
+        "batch": 1, "prefill_tokens": T, "decode_steps": steps,
+        "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(T / prefill_ms * 1e3, 1),
+        "decode_ms_per_token_hipgraph": round(graph_ms, 4), "decode_tokens_per_s": round(1e3 / graph_ms, 1),
+        "decode_ms_per_token_eager": round(eager_ms, 4),
+        "decode_bytes_per_token": tok_bytes, "decode_gbs": round(tok_bytes / graph_ms / 1e6, 1),
+        "decode_frac_of_hbm_peak": round(tok_bytes / graph_ms / 1e6 / HBM_PEAK_GBS, 4),
+        "dispatches_per_decode_step": D.stats()["launches"],
+    }
+    log(f"  e2e 8B q4_K: prefill {T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} tok/s); decode "
+        f"{graph_ms:.3f} ms/tok graph, {eager_ms:.3f} eager -> {out['decode_tokens_per_s']} tok/s, "
+        f"{out['decode_gbs']} GB/s")
+    del P, D, W, state
+    torch.cuda.empty_cache()
+    return out
+
+
 def algorithmic_bytes(wtype, M, K, n):
     from tensorlisp_amd import native as N
 
@@ -317,6 +415,8 @@ def main() -> int:
         del fq, fk, fv, fm, fo, node
     torch.cuda.empty_cache()
 
+    e2e = e2e_decoder(torch, gen)
+
     # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
     # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -360,6 +460,8 @@ def main() -> int:
                         "4096x14336, 128256x4096} x N {1, 8}; GGML_OP_MUL_MAT incl. Q8_0/Q8_K activation "
                         "quantization; weights rotated over >= 640 MB of HBM copies per node",
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+            "decode_tokens_per_s_8b_q4k_bs1": e2e["decode_tokens_per_s"],
+            "e2e_decoder_8b_q4k": e2e,
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
             "prefill_gemm_q4k": prefill,
             "gemv_q6k_lm_head": q6,
