@@ -437,6 +437,88 @@ __global__ void __launch_bounds__(256) k_core_argmax(const CoreArgs a) {
     }
 }
 
+// Long rows (a vocabulary of logits): the row in chunks over many
+// workgroups, each leaving (max, last index of it) in scratch, then one
+// workgroup per row folds the chunks in order. Same result as k_core_argmax.
+struct ArgmaxPart {
+    float v;
+    int i;
+};
+constexpr int ARGMAX_CHUNK = 2048;
+
+__device__ __forceinline__ void argmax_fold(float &best, int &bi, float ov, int oi) {
+    if (ov > best || (ov == best && oi > bi)) {
+        best = ov;
+        bi = oi;
+    }
+}
+
+__device__ __forceinline__ void argmax_block(float &best, int &bi, float *sv, int *si) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) argmax_fold(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64));
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    best = sv[0];
+    bi = si[0];
+    for (int w = 1; w < 4; ++w) argmax_fold(best, bi, sv[w], si[w]);
+}
+
+__global__ void __launch_bounds__(256) k_argmax_chunks(const CoreArgs a, ArgmaxPart *part, int nchunks) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const tlh_tensor &x = a.op.t[0];
+    const int64_t row = blockIdx.y;
+    const char *xr = a.s0 + row * x.nb[1];
+    const int64_t lo = (int64_t)blockIdx.x * ARGMAX_CHUNK;
+    const int64_t hi = lo + ARGMAX_CHUNK < x.ne[0] ? lo + ARGMAX_CHUNK : x.ne[0];
+    float best = -INFINITY;
+    int bi = (int)lo;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+        const float v = ld_f(xr + i * x.nb[0], x.ty);
+        if (v >= best) {
+            best = v;
+            bi = (int)i;
+        }
+    }
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) part[row * nchunks + blockIdx.x] = {best, bi};
+}
+
+__global__ void __launch_bounds__(256) k_argmax_fold(const CoreArgs a, const ArgmaxPart *part, int nchunks) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int64_t row = blockIdx.x;
+    float best = -INFINITY;
+    int bi = 0;
+    for (int c = threadIdx.x; c < nchunks; c += 256) argmax_fold(best, bi, part[row * nchunks + c].v, part[row * nchunks + c].i);
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) *(int32_t *)(a.dst + row * a.op.t[4].nb[0]) = bi;
+}
+
+size_t argmax_split_scratch_bytes(const tlh_op &op) {
+    const int64_t nchunks = (op.t[0].ne[0] + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    return (size_t)(op.t[0].ne[1] * nchunks * sizeof(ArgmaxPart));
+}
+
+tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void *scratch, hipStream_t stream) {
+    CoreArgs a;
+    a.op = op;
+    a.s0 = (const char *)x;
+    a.s1 = a.s2 = nullptr;
+    a.dst = (char *)dst;
+    const int64_t rows = op.t[0].ne[1];
+    const int nchunks = (int)((op.t[0].ne[0] + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK);
+    if (rows == 0 || nchunks == 0) return TLH_OK;
+    hipLaunchKernelGGL(k_argmax_chunks, dim3((unsigned)nchunks, (unsigned)rows), dim3(256), 0, stream, a,
+                       (ArgmaxPart *)scratch, nchunks);
+    hipLaunchKernelGGL(k_argmax_fold, dim3((unsigned)rows), dim3(256), 0, stream, a, (const ArgmaxPart *)scratch,
+                       nchunks);
+    return check_launch("argmax");
+}
+
 // --------------------------------------------------------------------- rope
 // ops.cpp rope_flt (:5953-6100; normal mode 0: pairs (2p, 2p+1); neox mode
 // 2: (p, p + n_dims/2)) with ggml's YaRN angle (rope_yarn, :5829-5844):
@@ -592,6 +674,119 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
     default: return set_error(TLH_INVALID, "core: unknown kind %d", kind);
     }
     return check_launch("core");
+}
+
+// ---------------------------------------------------------- norm chains
+// [ADD ->] RMS_NORM / NORM -> MUL(weight) in one pass per row, for the
+// executor: s = p + q (written: it is read again as the residual), the norm
+// of s (or of x without the ADD), times a weight row that repeats over rows.
+// Every value is the one the separate BIN, NORM and BIN kernels produce:
+// s_i = p_i + q_i, t_i = (s_i - mean) * scale, y_i = t_i * w_i, with the
+// same sums (double; the variance in groups of four as k_core_norm forms it).
+// f32 rows with unit element stride. op: t0 p (or x), t1 q, t2 w, t3 s,
+// t4 y; x0 = 1 for RMS_NORM, x1 eps, x2 = 1 with the ADD.
+struct NormChainArgs {
+    tlh_op op;
+    const float *p, *q, *w;
+    float *s, *y;
+};
+
+constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows up to 4096 in one read
+
+// The weight row has the norm's length (the executor fuses only then), so
+// element i of a row multiplies w[i].
+__global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
+    __shared__ double shd[4];
+    const tlh_tensor &tp = a.op.t[0], &tq = a.op.t[1], &tw = a.op.t[2], &ts = a.op.t[3], &ty = a.op.t[4];
+    const bool rms = a.op.x[0] != 0, add = a.op.x[2] != 0;
+    const float eps = __int_as_float((int)a.op.x[1]);
+    int64_t i1, i2, i3;
+    row_coords(blockIdx.x + (int64_t)gridDim.x * blockIdx.y, tp, i1, i2, i3);
+    const float *pr = (const float *)((const char *)a.p + offs(tp, 0, i1, i2, i3));
+    const float *qr = add ? (const float *)((const char *)a.q + offs(tq, 0, i1, i2, i3)) : nullptr;
+    float *sr = add ? (float *)((char *)a.s + offs(ts, 0, i1, i2, i3)) : nullptr;
+    const float *wr = (const float *)((const char *)a.w + offs(tw, 0, i1 % tw.ne[1], i2 % tw.ne[2], i3 % tw.ne[3]));
+    float *yr = (float *)((char *)a.y + offs(ty, 0, i1, i2, i3));
+    const int n = (int)tp.ne[0];
+    const int t = threadIdx.x;
+    auto value = [&](int i) { return add ? pr[i] + qr[i] : pr[i]; };
+    // thread t owns groups of four: elements 4 (t + 256 j) .. + 3
+    float c[NC_CACHE][4];
+#pragma unroll
+    for (int j = 0; j < NC_CACHE; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * (t + 256 * j) + e;
+            c[j][e] = i < n ? value(i) : 0.0f;
+        }
+    double s1 = 0.0;
+#pragma unroll
+    for (int j = 0; j < NC_CACHE; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * (t + 256 * j) + e;
+            if (i < n) {
+                if (add) sr[i] = c[j][e];
+                s1 += rms ? (double)(c[j][e] * c[j][e]) : (double)c[j][e];
+            }
+        }
+    for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)  // rows past the registers
+        for (int e = 0; e < 4 && i + e < n; ++e) {
+            const float v = value(i + e);
+            if (add) sr[i + e] = v;
+            s1 += rms ? (double)(v * v) : (double)v;
+        }
+    float mean = 0.0f, var;
+    if (rms) {
+        var = (float)(block_sum_t(s1, shd) / (double)n);
+    } else {
+        mean = (float)block_sum_t(s1, shd) / (float)n;
+        double s2 = 0.0;
+        auto group = [&](int i, float v0, float v1, float v2, float v3) {
+            const float d0 = v0 - mean, d1 = v1 - mean, d2 = v2 - mean, d3 = v3 - mean;
+            if (i + 3 < n) {
+                s2 += (double)((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3));
+            } else {  // the row's tail, element by element
+                if (i < n) s2 += (double)(d0 * d0);
+                if (i + 1 < n) s2 += (double)(d1 * d1);
+                if (i + 2 < n) s2 += (double)(d2 * d2);
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < NC_CACHE; ++j) {
+            const int i = 4 * (t + 256 * j);
+            if (i < n) group(i, c[j][0], c[j][1], c[j][2], c[j][3]);
+        }
+        for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)
+            group(i, value(i), i + 1 < n ? value(i + 1) : 0.0f, i + 2 < n ? value(i + 2) : 0.0f,
+                  i + 3 < n ? value(i + 3) : 0.0f);
+        var = (float)(block_sum_t(s2, shd) / (double)n);
+    }
+    const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int j = 0; j < NC_CACHE; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * (t + 256 * j) + e;
+            if (i < n) yr[i] = ((c[j][e] - mean) * scale) * wr[i];
+        }
+    for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)
+        for (int e = 0; e < 4 && i + e < n; ++e) yr[i + e] = ((value(i + e) - mean) * scale) * wr[i + e];
+}
+
+tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
+                             hipStream_t stream) {
+    NormChainArgs a;
+    a.op = op;
+    a.p = (const float *)p;
+    a.q = (const float *)q;
+    a.w = (const float *)w;
+    a.s = (float *)s;
+    a.y = (float *)y;
+    const int64_t rows = nrows(op.t[0]);
+    if (rows == 0) return TLH_OK;
+    hipLaunchKernelGGL(k_norm_chain, red_grid(rows), dim3(256), 0, stream, a);
+    return check_launch("norm_chain");
 }
 
 }  // namespace tlh

@@ -31,16 +31,22 @@ struct Place {
     int64_t off = 0;
 };
 
-enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE };
+enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
+                    D_ARGMAX_SPLIT };
 struct Dispatch {
     DispatchKind kind;
     int core_kind = 0;
     tlh_op op;
     Place src[4];
     Place dst;
-    int pos = 0;            // node position
+    int pos = 0;            // node position (the first one, for fused nodes)
+    int pos_last = 0;       // last node position a fused dispatch covers
     int block = -1;         // scratch block index
     size_t scratch_bytes = 0;
+    // D_MULTI_GEMV: the member MUL_MATs (shared activation in src[1])
+    int nmem = 0;
+    tlh_op mop[3];
+    Place mw[3], mdst[3];
 };
 
 // ggml type traits used for byte sizes: (block elements, block bytes)
@@ -161,6 +167,9 @@ class Lowering {
             }
             return set_error(TLH_UNSUPPORTED, "native HIP: not implemented: %s", list.c_str());
         }
+        for (Dispatch &x : out.d) x.pos_last = x.pos;
+        fuse_norm_chains(out.d);
+        fuse_multi_gemv(out.d);
         group_mul_mats(out.d);
         plan(out);
         return TLH_OK;
@@ -291,7 +300,15 @@ class Lowering {
         if (op == "GET_ROWS") return core(out, base(pos, id, {0, 1}), TLH_CORE_GET_ROWS, why);
         if (op == "SET_ROWS") return core(out, base(pos, id, {0, 1}), TLH_CORE_SET_ROWS, why);
         if (op == "CPY" || op == "DUP" || op == "CONT") return core(out, base(pos, id, {0}), TLH_CORE_CPY, why);
-        if (op == "ARGMAX") return core(out, base(pos, id, {0}), TLH_CORE_ARGMAX, why);
+        if (op == "ARGMAX") {
+            Dispatch d = base(pos, id, {0});
+            if (!core(out, d, TLH_CORE_ARGMAX, why)) return false;
+            if (d.op.t[0].ne[0] >= 8192) {  // a vocabulary: chunks over many workgroups
+                out.back().kind = D_ARGMAX_SPLIT;
+                out.back().scratch_bytes = argmax_split_scratch_bytes(d.op);
+            }
+            return true;
+        }
         if (op == "GLU") {
             Dispatch d = base(pos, id, {0, 1});
             d.op.x[0] = p[0];
@@ -334,6 +351,141 @@ class Lowering {
         }
         why = "op not implemented in the native HIP executor";
         return false;
+    }
+
+    int32_t node_of(const Dispatch &x) const { return g_.nodes[x.pos]; }
+
+    void count_readers() {
+        readers_.assign(g_.n, 0);
+        for (int32_t id : g_.nodes)
+            for (int s = 0; s < 10; ++s)
+                if (g_.t[id].src[s] >= 0) ++readers_[g_.t[id].src[s]];
+        for (int32_t id : g_.keep) ++readers_[id];
+    }
+    std::vector<int> readers_;
+
+    static bool f32_rows(const tlh_tensor &t) { return t.ty == TLH_TYPE_F32 && t.nb[0] == 4; }
+    static bool same_ne(const tlh_tensor &a, const tlh_tensor &b) {
+        return a.ne[0] == b.ne[0] && a.ne[1] == b.ne[1] && a.ne[2] == b.ne[2] && a.ne[3] == b.ne[3];
+    }
+
+    // [ADD ->] RMS_NORM / NORM -> MUL(weight) -> one k_norm_chain launch, when the
+    // norm's result has no other reader, the MUL broadcasts a weight row over
+    // it, and the ADD (if fused) feeds the norm directly with operands of its
+    // own shape. The ADD's result is still written (it is read again later).
+    void fuse_norm_chains(std::vector<Dispatch> &d) {
+        count_readers();
+        std::vector<Dispatch> out;
+        out.reserve(d.size());
+        for (size_t i = 0; i < d.size(); ++i) {
+            const Dispatch &x = d[i];
+            const bool is_norm = x.kind == D_CORE && x.core_kind == TLH_CORE_NORM;
+            if (!is_norm || i + 1 >= d.size()) {
+                out.push_back(x);
+                continue;
+            }
+            const Dispatch &m = d[i + 1];
+            const int32_t nid = node_of(x);
+            const bool mul_ok = m.kind == D_CORE && m.core_kind == TLH_CORE_BIN && m.op.x[0] == 2 &&
+                                g_.t[node_of(m)].src[0] == nid && readers_[nid] == 1 && f32_rows(m.op.t[1]) &&
+                                m.op.t[1].ne[0] == x.op.t[0].ne[0] && f32_rows(m.op.t[4]) && same_ne(m.op.t[4], x.op.t[0]);
+            if (!mul_ok) {
+                out.push_back(x);
+                continue;
+            }
+            bool with_add = false;
+            if (!out.empty()) {
+                const Dispatch &a = out.back();
+                with_add = a.kind == D_CORE && a.core_kind == TLH_CORE_BIN && a.op.x[0] == 0 &&
+                           node_of(a) == g_.t[nid].src[0] && f32_rows(a.op.t[0]) && f32_rows(a.op.t[1]) &&
+                           f32_rows(a.op.t[4]) && same_ne(a.op.t[0], a.op.t[4]) && same_ne(a.op.t[1], a.op.t[4]);
+            }
+            Dispatch f;
+            f.kind = D_NORM_CHAIN;
+            memset(&f.op, 0, sizeof f.op);
+            if (with_add) {
+                const Dispatch a = out.back();
+                out.pop_back();
+                f.op.t[0] = a.op.t[0], f.op.t[1] = a.op.t[1], f.op.t[3] = a.op.t[4];
+                f.src[0] = a.src[0], f.src[1] = a.src[1], f.src[3] = a.dst;
+                f.pos = a.pos;
+            } else {
+                f.op.t[0] = x.op.t[0];
+                f.src[0] = x.src[0];
+                f.pos = x.pos;
+            }
+            f.op.t[2] = m.op.t[1];
+            f.src[2] = m.src[1];
+            f.op.t[4] = m.op.t[4];
+            f.dst = m.dst;
+            f.op.x[0] = x.op.x[0];
+            f.op.x[1] = x.op.x[1];
+            f.op.x[2] = with_add;
+            f.pos_last = m.pos;
+            out.push_back(f);
+            ++i;  // the MUL is part of it
+        }
+        d.swap(out);
+    }
+
+    // MUL_MATs at N = 1 that read the same activation with weights of one type
+    // and K -> one multi-segment register GEMV at the first one's place (up to
+    // three: Q, K and V, or gate and up). Later members move up: their weights
+    // are leaves and their activation is the first one's, so only their
+    // outputs' lifetimes grow, which the plan sees through the dispatch's
+    // position range. A write into the activation's storage ends the search.
+    void fuse_multi_gemv(std::vector<Dispatch> &d) {
+        auto single_ok = [&](const Dispatch &x) {
+            const tlh_op *o = &x.op;
+            return x.kind == D_MUL_MAT && x.src[0].buf == B_WEIGHT && x.dst.buf == B_ARENA && mul_mat_multi_ok(&o, 1);
+        };
+        std::vector<char> taken(d.size(), 0);
+        std::vector<Dispatch> out;
+        out.reserve(d.size());
+        for (size_t i = 0; i < d.size(); ++i) {
+            if (taken[i]) continue;
+            const Dispatch &x = d[i];
+            if (!single_ok(x)) {
+                out.push_back(x);
+                continue;
+            }
+            std::vector<size_t> mem{i};
+            const Place &a = x.src[1];
+            for (size_t j = i + 1; j < d.size() && mem.size() < 3; ++j) {
+                const Dispatch &y = d[j];
+                if (y.dst.buf == a.buf && y.dst.index == a.index) break;  // the activation is overwritten
+                if (y.kind == D_NORM_CHAIN && y.src[3].buf == a.buf && y.src[3].index == a.index) break;
+                if (taken[j] || !single_ok(y)) continue;
+                const tlh_tensor &b0 = x.op.t[1], &b1 = y.op.t[1];
+                bool same = y.src[1].buf == a.buf && y.src[1].index == a.index && y.src[1].off == a.off &&
+                            y.op.t[0].ty == x.op.t[0].ty && same_ne(b0, b1);
+                for (int k = 0; k < 4 && same; ++k) same = b0.nb[k] == b1.nb[k];
+                if (!same) continue;
+                const tlh_op *ops[3];
+                for (size_t k = 0; k < mem.size(); ++k) ops[k] = &d[mem[k]].op;
+                ops[mem.size()] = &y.op;
+                if (mul_mat_multi_ok(ops, (int)mem.size() + 1)) mem.push_back(j);
+            }
+            if (mem.size() < 2) {
+                out.push_back(x);
+                continue;
+            }
+            Dispatch f = x;
+            f.kind = D_MULTI_GEMV;
+            f.nmem = (int)mem.size();
+            f.scratch_bytes = 0;
+            for (size_t k = 0; k < mem.size(); ++k) {
+                const Dispatch &y = d[mem[k]];
+                f.mop[k] = y.op;
+                f.mw[k] = y.src[0];
+                f.mdst[k] = y.dst;
+                f.scratch_bytes = std::max(f.scratch_bytes, y.scratch_bytes);
+                f.pos_last = std::max(f.pos_last, y.pos_last);
+                taken[mem[k]] = 1;
+            }
+            out.push_back(f);
+        }
+        d.swap(out);
     }
 
     // MUL_MAT nodes with more than two activation columns that read the same
@@ -434,6 +586,21 @@ class Lowering {
             const int32_t r = g_.root(id, extra);
             if (first[r] == INT64_MAX) first[r] = n;
             last[r] = n;
+        }
+        // a fused dispatch reads and writes all its tensors over its whole
+        // position range: none of them may share bytes with another there
+        auto touch_place = [&](const Place &p, int64_t pos) {
+            if (p.buf != B_ARENA) return;
+            first[p.index] = std::min(first[p.index], pos);
+            last[p.index] = std::max(last[p.index], pos);
+        };
+        for (const Dispatch &x : out.d) {
+            if (x.pos_last == x.pos) continue;
+            for (int64_t pos : {(int64_t)x.pos, (int64_t)x.pos_last}) {
+                for (int k = 0; k < 4; ++k) touch_place(x.src[k], pos);
+                touch_place(x.dst, pos);
+                for (int k = 0; k < x.nmem; ++k) touch_place(x.mdst[k], pos);
+            }
         }
         out.blocks.clear();
         out.arena_off.assign(g_.n, -1);
@@ -564,6 +731,23 @@ struct tlh_program {
             case D_FLASH_ATTN:
                 st = tlh_flash_attn_ext(&x.op, src[0], src[1], src[2], src[3], dst, scratch, x.scratch_bytes, s);
                 break;
+            case D_NORM_CHAIN: st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s); break;
+            case D_ARGMAX_SPLIT: st = launch_argmax_split(x.op, src[0], dst, scratch, s); break;
+            case D_MULTI_GEMV: {
+                const tlh_op *ops[3];
+                const void *w[3];
+                void *dsts[3];
+                for (int k = 0; k < x.nmem; ++k) {
+                    ops[k] = &x.mop[k];
+                    w[k] = resolve(x.mw[k], state);
+                    dsts[k] = resolve(x.mdst[k], state);
+                }
+                st = mul_mat_multi(ops, w, dsts, x.nmem, src[1], s);
+                if (st == TLH_UNSUPPORTED)  // pointers the fused launch cannot take: one launch per node
+                    for (int k = 0; k < x.nmem && (k == 0 || st == TLH_OK); ++k)
+                        st = tlh_mul_mat(ops[k], w[k], src[1], dsts[k], scratch, x.scratch_bytes, s);
+                break;
+            }
             default: st = tlh_core(x.core_kind, &x.op, src[0], src[1], src[2], dst, s); break;
             }
             if (st != TLH_OK) {

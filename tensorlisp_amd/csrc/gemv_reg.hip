@@ -440,14 +440,22 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     const int64_t arow0 = a.n0 + a.N_total * batch;
     const int64_t rows_per_block = (int64_t)groups * R;
 
+    // segment of launch row m (a.nseg > 0): which matrix it belongs to
+    auto seg_of = [&](int64_t m) { return (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]); };
     auto row_ptrs = [&](int64_t rb, const uint8_t *(&wrow)[R]) {
         const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // clamp: loads in bounds, store skipped
-            wrow[r] = W + m * a.w_nb1;
+            if (a.nseg > 0) {
+                const int sg = seg_of(m);
+                wrow[r] = a.seg_w[sg] + (m - a.seg_m0[sg]) * a.seg_w_nb1[sg];
+            } else {
+                wrow[r] = W + m * a.w_nb1;
+            }
         }
     };
+
 
     // the first row block's weights are requested before the activation
     // slice is read and quantized, so the two memory latencies overlap
@@ -472,7 +480,15 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         }
     }
 
-    char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
+    char *dbase = a.nseg > 0 ? nullptr : (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
+    auto store = [&](int64_t m, int n, float v) {
+        if (a.nseg > 0) {
+            const int sg = seg_of(m);
+            a.seg_dst[sg][m - a.seg_m0[sg]] = v;
+        } else {
+            *(float *)(dbase + (a.n0 + n) * a.d_nb1 + m * 4) = v;
+        }
+    };
     while (have) {
         const int64_t rb_next = rb + gridDim.x;
         const bool have_next = rb_next * rows_per_block < a.M;
@@ -501,7 +517,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         if (ksplit == 1) {
             if (holder && vi < V) {
                 const int r = vi / NC, n = vi % NC;
-                if (m0 + r < a.M && n < a.N) *(float *)(dbase + (a.n0 + n) * a.d_nb1 + (m0 + r) * 4) = tot;
+                if (m0 + r < a.M && n < a.N) store(m0 + r, n, tot);
             }
         } else {
             if (holder) part[wave][vi] = tot;
@@ -510,7 +526,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
                 float t = 0.0f;
                 for (int s2 = 0; s2 < ksplit; ++s2) t += part[grp * ksplit + s2][vi];
                 const int r = vi / NC, n = vi % NC;
-                if (m0 + r < a.M && n < a.N) *(float *)(dbase + (a.n0 + n) * a.d_nb1 + (m0 + r) * 4) = t;
+                if (m0 + r < a.M && n < a.N) store(m0 + r, n, t);
             }
             lds_barrier();
         }

@@ -34,6 +34,15 @@ struct MatmulArgs {
     int64_t d_nb1, d_nb2, d_nb3;  // dst strides (bytes), nb0 = 4
     float *part;                  // few-column kernel with K split in chunks: partial
                                   // sums [chunk][batch][N][M] (scratch), else null
+    // Register GEMV at N = 1 and one batch slice only: with nseg > 0 the
+    // launch's M rows are the rows of up to three weight matrices read with
+    // the same activation -- rows seg_m0[s] .. seg_m0[s+1] come from seg_w[s]
+    // (row stride seg_w_nb1[s]) and go to seg_dst[s]; w / dst above are unused.
+    int nseg;
+    const uint8_t *seg_w[3];
+    int64_t seg_w_nb1[3];
+    float *seg_dst[3];
+    int64_t seg_m0[4];
 };
 
 // N <= 16. With x != nullptr (src1 rows in activation-row order, stride
@@ -71,6 +80,20 @@ int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhk
 tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
 
 // core ops (core.hip): kind is a tlh_core_kind; op validated by the caller
+// Up to three MUL_MAT nodes at N = 1 reading one activation with weights of one
+// type and K as one register-GEMV launch (tlhip.cpp); TLH_UNSUPPORTED when the
+// pointers do not allow it.
+bool mul_mat_multi_ok(const tlh_op *const *ops, int n);
+tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n, const void *x,
+                         hipStream_t stream);
+// [ADD ->] RMS_NORM / NORM -> MUL(weight) in one kernel (core.hip k_norm_chain);
+// op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
+tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
+                             hipStream_t stream);
+// ARGMAX of long rows in chunks over many workgroups (executor): scratch of
+// argmax_split_scratch_bytes; same result as the core ARGMAX.
+size_t argmax_split_scratch_bytes(const tlh_op &op);
+tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void *scratch, hipStream_t stream);
 tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,
                        hipStream_t stream);
 

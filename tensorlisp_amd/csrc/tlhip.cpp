@@ -419,7 +419,7 @@ static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void
 
 static MatmulArgs mm_args(const tlh_op *op, const MulMatShape &s, const void *src0, const void *scratch, void *dst) {
     const tlh_tensor &a = op->t[0], &d = op->t[4];
-    MatmulArgs m;
+    MatmulArgs m{};
     m.wtype = a.ty;
     m.w = (const uint8_t *)src0;
     m.w_nb1 = a.nb[1];
@@ -453,6 +453,59 @@ static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void 
 }
 
 static bool mm_empty(const MulMatShape &s) { return s.M == 0 || s.N == 0 || s.ne12 == 0 || s.ne13 == 0; }
+
+}  // extern "C"
+
+// Up to three MUL_MAT nodes at N = 1 (one batch slice) reading one activation
+// with weights of one type and K, as one register-GEMV launch that quantizes
+// the activation once. mul_mat_multi_ok checks the shapes; mul_mat_multi
+// returns TLH_UNSUPPORTED when the pointers do not allow the fused launch
+// (the caller then runs the nodes one by one).
+bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
+    if (n < 1 || n > 3) return false;
+    MulMatShape first;
+    for (int i = 0; i < n; ++i) {
+        MulMatShape s;
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.N != 1 || s.ne12 * s.ne13 != 1) return false;
+        int ks, upw;
+        if (!gemv_reg_geometry(s.K, ks, upw)) return false;
+        if (i == 0) first = s;
+        else if (s.K != first.K || s.wtype != first.wtype) return false;
+    }
+    return true;
+}
+
+tlh_status tlh::mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
+                              const void *x, hipStream_t stream) {
+    if (!mul_mat_multi_ok(ops, n)) return set_error(TLH_UNSUPPORTED, "mul_mat_multi: shapes");
+    MulMatShape s;
+    check_mul_mat(ops[0], s);
+    MatmulArgs m = mm_args(ops[0], s, w[0], nullptr, dst[0]);
+    m.nseg = n;
+    int64_t rows = 0;
+    for (int i = 0; i < 3; ++i) {
+        m.seg_m0[i] = rows;
+        if (i < n) {
+            if (!w[i] || !dst[i] || ((uintptr_t)w[i] & 1) || ((uintptr_t)dst[i] & 3))
+                return set_error(TLH_UNSUPPORTED, "mul_mat_multi: pointers");
+            m.seg_w[i] = (const uint8_t *)w[i];
+            m.seg_w_nb1[i] = ops[i]->t[0].nb[1];
+            m.seg_dst[i] = (float *)dst[i];
+            rows += ops[i]->t[0].ne[1];
+        } else {
+            m.seg_w[i] = nullptr;
+            m.seg_w_nb1[i] = 0;
+            m.seg_dst[i] = nullptr;
+        }
+    }
+    m.seg_m0[3] = rows;
+    m.M = rows;
+    if (!x || !gemv_fuses_quantize(m, (const float *)x, ops[0]->t[1].nb[1]))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_multi: activation alignment");
+    return launch_gemv_reg(m, (const float *)x, ops[0]->t[1].nb[1], stream);
+}
+
+extern "C" {
 
 tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,
                        size_t scratch_bytes, void *stream) {

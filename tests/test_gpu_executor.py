@@ -172,3 +172,63 @@ def test_program_refusals(gpu):
         prog.run(None)
     with pytest.raises(N.TlhError, match="null stream"):
         N.check(N.lib().tlh_program_run(prog.ptr, dec.state.data_ptr(), None, 1))
+
+
+@pytest.mark.parametrize("n,rms,add", [(4096, True, True), (4096, False, True), (8195, True, True), (8195, False, False),
+                                       (100, False, True), (256, True, False)])
+def test_fused_norm_chains_match_unfused(gpu, n, rms, add):
+    """[ADD ->] RMS_NORM / NORM -> MUL(weight) runs as one kernel in a program;
+    its outputs (the ADD's, which stays readable, and the MUL's) are bit-identical
+    to the three core ops run one by one. Rows past the 4096 held in registers
+    and tails of fewer than four elements included."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    b = G.Builder()
+    p = b.input(N.F32, [n, 3])
+    q = b.input(N.F32, [n, 3])
+    w = b.weight(N.F32, [n])
+    s = b.add(p, q) if add else p
+    t = b.rms_norm(s, 1e-5) if rms else b.norm(s, 1e-5)
+    y = b.mul(t, w)
+    b.expand(y)
+    keep = [y, s] if add else [y]
+    wd = dev(synth.normal(61, (n,)))
+    prog = G.Program(b, keep, [wd])
+    pv, qv = dev(synth.normal(62, (3, n)) * 2 + 0.5), dev(synth.normal(63, (3, n)))
+    prog.write_input(0, pv)
+    prog.write_input(1, qv)
+    prog.run()
+    sv = N.add(pv, qv) if add else pv
+    tv = N.norm(sv, 1e-5, rms=rms)
+    want = N.mul(tv, wd)
+    got = prog.read(y, torch.float32).reshape(want.shape)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+    if add:
+        np.testing.assert_array_equal(prog.read(s, torch.float32).reshape(sv.shape).cpu().numpy(), sv.cpu().numpy())
+    assert prog.stats()["launches"] == 1
+
+
+def test_argmax_of_a_vocabulary(gpu):
+    """ARGMAX over 128256 logits runs in chunks over many workgroups in a
+    program; the last index of equal maxima wins, as on the CPU."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    b = G.Builder()
+    lg = b.input(N.F32, [128256, 4])
+    am = b.argmax(lg)
+    b.expand(am)
+    prog = G.Program(b, [am], [])
+    x = synth.normal(64, (4, 128256))
+    x[1, 5] = x[1, 70000] = x[1, 128255] = 50.0
+    x[2, :] = 1.0
+    x[3, 2047:2049] = 60.0  # a tie across the chunk boundary
+    prog.write_input(0, dev(x))
+    prog.run()
+    got = prog.read(am, torch.int32).cpu().numpy().reshape(-1)
+    np.testing.assert_array_equal(got, oracle().core_argmax(x))
+    assert list(got[1:]) == [128255, 128255, 2048]
