@@ -41,6 +41,7 @@ struct CoreArgs {
     tlh_op op;
     const char *s0, *s1, *s2;
     char *dst;
+    const char *s3;  // ROPE writing rows of a cache: the row index of each token
 };
 
 // rows of a tensor: row r -> (i1, i2, i3)
@@ -59,17 +60,16 @@ constexpr int CORE_CHUNK = 1024;
 // ------------------------------------------------------------------- binary
 // binary-ops.cpp: dst = src0 (op) src1 with src1 repeated to src0's shape
 // (ggml_can_repeat), in f32.
-__global__ void __launch_bounds__(256) k_core_bin(const CoreArgs a) {
+__device__ __forceinline__ void body_bin(const CoreArgs &a, int64_t bx, int64_t row) {
     const tlh_tensor &x = a.op.t[0], &y = a.op.t[1], &d = a.op.t[4];
     const int code = (int)a.op.x[0];
-    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
     if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
     int64_t i1, i2, i3;
     row_coords(row, d, i1, i2, i3);
     const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
     const char *yr = a.s1 + offs(y, 0, i1 % y.ne[1], i2 % y.ne[2], i3 % y.ne[3]);
     char *dr = a.dst + offs(d, 0, i1, i2, i3);
-    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+    const int64_t e0 = bx * CORE_CHUNK + threadIdx.x;
 #pragma unroll
     for (int u = 0; u < CORE_CHUNK / 256; ++u) {
         const int64_t i0 = e0 + 256 * u;
@@ -79,6 +79,9 @@ __global__ void __launch_bounds__(256) k_core_bin(const CoreArgs a) {
         const float r = code == 0 ? p + q : code == 1 ? p - q : code == 2 ? p * q : p / q;
         st_f(dr + i0 * d.nb[0], d.ty, r);
     }
+}
+__global__ void __launch_bounds__(256) k_core_bin(const CoreArgs a) {
+    body_bin(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 
 // -------------------------------------------------------------------- unary
@@ -141,17 +144,16 @@ __device__ __forceinline__ float unary_val(int code, float v, float p1, float p2
     }
 }
 
-__global__ void __launch_bounds__(256) k_core_unary(const CoreArgs a) {
+__device__ __forceinline__ void body_unary(const CoreArgs &a, int64_t bx, int64_t row) {
     const tlh_tensor &x = a.op.t[0], &d = a.op.t[4];
     const int code = (int)a.op.x[0];
     const float p1 = __int_as_float((int)a.op.x[1]), p2 = __int_as_float((int)a.op.x[2]);
-    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
     if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
     int64_t i1, i2, i3;
     row_coords(row, d, i1, i2, i3);
     const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
     char *dr = a.dst + offs(d, 0, i1, i2, i3);
-    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+    const int64_t e0 = bx * CORE_CHUNK + threadIdx.x;
 #pragma unroll
     for (int u = 0; u < CORE_CHUNK / 256; ++u) {
         const int64_t i0 = e0 + 256 * u;
@@ -160,6 +162,9 @@ __global__ void __launch_bounds__(256) k_core_unary(const CoreArgs a) {
         // f16 data reads the CPU's gelu table for every value (no +-10 cut-offs)
         st_f(dr + i0 * d.nb[0], d.ty, code == 8 && x.ty == TLH_TYPE_F16 ? gelu_f16(v) : unary_val(code, v, p1, p2));
     }
+}
+__global__ void __launch_bounds__(256) k_core_unary(const CoreArgs a) {
+    body_unary(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 
 // ----------------------------------------------------------------- get_rows
@@ -193,9 +198,8 @@ __global__ void __launch_bounds__(256) k_core_get_rows(const CoreArgs a) {
 // ----------------------------------------------------------------- set_rows
 // ops.cpp set_rows: src0 row (i, j, k) goes to dst row idx[i, j % n1, k % n2]
 // of dst plane (j, k), converted to dst's type.
-__global__ void __launch_bounds__(256) k_core_set_rows(const CoreArgs a) {
+__device__ __forceinline__ void body_set_rows(const CoreArgs &a, int64_t bx, int64_t row) {
     const tlh_tensor &x = a.op.t[0], &ix = a.op.t[1], &d = a.op.t[4];
-    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
     if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
     int64_t i1, i2, i3;
     row_coords(row, x, i1, i2, i3);
@@ -203,13 +207,16 @@ __global__ void __launch_bounds__(256) k_core_set_rows(const CoreArgs a) {
     if (r < 0 || r >= d.ne[1]) return;  // an index outside dst writes nothing
     const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
     char *dr = a.dst + r * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3];
-    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+    const int64_t e0 = bx * CORE_CHUNK + threadIdx.x;
 #pragma unroll
     for (int u = 0; u < CORE_CHUNK / 256; ++u) {
         const int64_t i0 = e0 + 256 * u;
         if (i0 >= x.ne[0]) break;
         st_f(dr + i0 * d.nb[0], d.ty, ld_f(xr + i0 * x.nb[0], x.ty));
     }
+}
+__global__ void __launch_bounds__(256) k_core_set_rows(const CoreArgs a) {
+    body_set_rows(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 
 // ---------------------------------------------------------------------- cpy
@@ -261,11 +268,10 @@ __device__ __forceinline__ float glu_val(int code, float x, float g) {
     }
 }
 
-__global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
+__device__ __forceinline__ void body_glu(const CoreArgs &a, int64_t bx, int64_t row) {
     const tlh_tensor &x = a.op.t[0], &y = a.op.t[1], &d = a.op.t[4];
     const int code = (int)a.op.x[0];
     const bool swapped = a.op.x[1] != 0;
-    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
     if (row >= d.ne[1] * d.ne[2] * d.ne[3]) return;
     int64_t i1, i2, i3;
     row_coords(row, d, i1, i2, i3);
@@ -279,13 +285,16 @@ __global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
         xr += swapped ? nc : 0;
     }
     float *dr = (float *)(a.dst + offs(d, 0, i1, i2, i3));
-    const int64_t e0 = (int64_t)blockIdx.x * CORE_CHUNK + threadIdx.x;
+    const int64_t e0 = bx * CORE_CHUNK + threadIdx.x;
 #pragma unroll
     for (int u = 0; u < CORE_CHUNK / 256; ++u) {
         const int64_t i0 = e0 + 256 * u;
         if (i0 >= nc) break;
         dr[i0] = glu_val(code, xr[i0], gr[i0]);
     }
+}
+__global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
+    body_glu(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 
 // ------------------------------------------------------------ block reduces
@@ -525,20 +534,22 @@ tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void 
 // theta = pos * theta_scale^p / freq_factor, mixed with its interpolation by
 // the ramp over [corr0, corr1] when ext_factor != 0; dims past n_dims pass
 // through. One thread per pair.
-__global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
+__device__ __forceinline__ void body_rope(const CoreArgs &a, int64_t bx, int64_t row) {
     const tlh_tensor &x = a.op.t[0], &ps = a.op.t[1], &d = a.op.t[4];
     const int n_dims = (int)a.op.x[0], mode = (int)a.op.x[1];
     const float freq_scale = __int_as_float((int)a.op.x[2]), ext_factor = __int_as_float((int)a.op.x[3]);
     const float attn_factor = __int_as_float((int)a.op.x[4]), theta_scale = __int_as_float((int)a.op.x[5]);
     const float corr0 = __int_as_float((int)a.op.x[6]), corr1 = __int_as_float((int)a.op.x[7]);
     const bool has_ff = a.op.x[8] != 0;
-    const int64_t row = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
     if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
     int64_t i1, i2, i3;
     row_coords(row, x, i1, i2, i3);
     const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
-    char *dr = a.dst + offs(d, 0, i1, i2, i3);
-    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;  // pair index
+    // x9 = 1: the rotated row of token i2 lands in row idx[i2] of a cache whose
+    // rows hold every head of a token (the SET_ROWS of the reshaped result)
+    char *dr = a.op.x[9] ? a.dst + ld_idx(a.s3 + i2 * a.op.t[3].nb[0], a.op.t[3].ty) * d.nb[1] + i1 * x.ne[0] * d.nb[0]
+                         : a.dst + offs(d, 0, i1, i2, i3);
+    const int64_t p = bx * 256 + threadIdx.x;  // pair index
     if (p >= x.ne[0] / 2) return;
     if (2 * p >= n_dims) {  // past the rotated dims: copy both elements of the pair
         st_f(dr + 2 * p * d.nb[0], d.ty, ld_f(xr + 2 * p * x.nb[0], x.ty));
@@ -568,6 +579,9 @@ __global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
     st_f(dr + ia * d.nb[0], d.ty, x0 * cs - x1 * sn);
     st_f(dr + ib * d.nb[0], d.ty, x0 * sn + x1 * cs);
 }
+__global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
+    body_rope(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+}
 
 // ------------------------------------------------------------------ launchers
 static dim3 row_grid(int64_t chunks, int64_t rows) {
@@ -589,6 +603,7 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
     a.s1 = (const char *)s1;
     a.s2 = (const char *)s2;
     a.dst = (char *)dst;
+    a.s3 = nullptr;
     const tlh_tensor &x = op.t[0], &d = op.t[4];
     switch (kind) {
     case TLH_CORE_BIN: {
@@ -676,6 +691,81 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
     return check_launch("core");
 }
 
+// --------------------------------------------------------- several ops at once
+// Up to four independent element-wise ops (BIN, UNARY, SET_ROWS, GLU, ROPE)
+// in one launch, for the executor: the flattened grid is cut into each op's
+// own (chunk, row) blocks, and every block runs the op's body as its own
+// kernel would. Saves the fixed cost of the launches it replaces.
+constexpr int MULTI_MAX = 4;
+struct MultiArgs {
+    int n;
+    int kind[MULTI_MAX];
+    int64_t start[MULTI_MAX + 1];  // first flattened block of each op
+    int64_t gx[MULTI_MAX];         // blocks along a row
+    CoreArgs sub[MULTI_MAX];
+};
+
+__global__ void __launch_bounds__(256) k_core_multi(const MultiArgs m) {
+    const int64_t b = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+    int k = 0;
+    while (k + 1 < m.n && b >= m.start[k + 1]) ++k;
+    const int64_t local = b - m.start[k];
+    const int64_t bx = local % m.gx[k], row = local / m.gx[k];
+    switch (m.kind[k]) {
+    case TLH_CORE_BIN: body_bin(m.sub[k], bx, row); break;
+    case TLH_CORE_UNARY: body_unary(m.sub[k], bx, row); break;
+    case TLH_CORE_SET_ROWS: body_set_rows(m.sub[k], bx, row); break;
+    case TLH_CORE_GLU: body_glu(m.sub[k], bx, row); break;
+    default: body_rope(m.sub[k], bx, row); break;
+    }
+}
+
+// blocks along a row and rows of an element-wise op's grid
+static bool ew_grid(int kind, const tlh_op &op, int64_t &gx, int64_t &rows) {
+    const tlh_tensor &x = op.t[0], &d = op.t[4];
+    switch (kind) {
+    case TLH_CORE_BIN: case TLH_CORE_UNARY: case TLH_CORE_GLU:
+        gx = (d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows = nrows(d);
+        return true;
+    case TLH_CORE_SET_ROWS: gx = (x.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows = nrows(x); return true;
+    case TLH_CORE_ROPE: gx = (x.ne[0] / 2 + 255) / 256, rows = nrows(x); return true;
+    default: return false;
+    }
+}
+
+bool core_multi_kind(int kind) {
+    return kind == TLH_CORE_BIN || kind == TLH_CORE_UNARY || kind == TLH_CORE_SET_ROWS || kind == TLH_CORE_GLU ||
+           kind == TLH_CORE_ROPE;
+}
+
+tlh_status launch_core_multi(int n, const int *kinds, const tlh_op *ops, const void *const (*srcs)[4],
+                             void *const *dsts, hipStream_t stream) {
+    if (n < 1 || n > MULTI_MAX) return set_error(TLH_INVALID, "core_multi: %d ops", n);
+    MultiArgs m;
+    m.n = n;
+    int64_t total = 0;
+    for (int k = 0; k < n; ++k) {
+        int64_t gx = 0, rows = 0;
+        if (!ew_grid(kinds[k], ops[k], gx, rows)) return set_error(TLH_INVALID, "core_multi: kind %d", kinds[k]);
+        m.kind[k] = kinds[k];
+        m.start[k] = total;
+        m.gx[k] = gx > 0 ? gx : 1;
+        total += gx * rows;
+        CoreArgs &a = m.sub[k];
+        a.op = ops[k];
+        a.s0 = (const char *)srcs[k][0];
+        a.s1 = (const char *)srcs[k][1];
+        a.s2 = (const char *)srcs[k][2];
+        a.s3 = (const char *)srcs[k][3];
+        a.dst = (char *)dsts[k];
+    }
+    m.start[n] = total;
+    if (total == 0) return TLH_OK;
+    const int64_t gxx = total < 65535 ? total : 65535;
+    hipLaunchKernelGGL(k_core_multi, dim3((unsigned)gxx, (unsigned)((total + gxx - 1) / gxx)), dim3(256), 0, stream, m);
+    return check_launch("core_multi");
+}
+
 // ---------------------------------------------------------- norm chains
 // [ADD ->] RMS_NORM / NORM -> MUL(weight) in one pass per row, for the
 // executor: s = p + q (written: it is read again as the residual), the norm
@@ -710,14 +800,16 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     const int n = (int)tp.ne[0];
     const int t = threadIdx.x;
     auto value = [&](int i) { return add ? pr[i] + qr[i] : pr[i]; };
-    // thread t owns groups of four: elements 4 (t + 256 j) .. + 3
-    float c[NC_CACHE][4];
+    // thread t owns groups of four: elements 4 (t + 256 j) .. + 3; the weight
+    // row is fetched with the values, so its latency overlaps the reduction
+    float c[NC_CACHE][4], wv[NC_CACHE][4];
 #pragma unroll
     for (int j = 0; j < NC_CACHE; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * (t + 256 * j) + e;
             c[j][e] = i < n ? value(i) : 0.0f;
+            wv[j][e] = i < n ? wr[i] : 0.0f;
         }
     double s1 = 0.0;
 #pragma unroll
@@ -768,7 +860,7 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * (t + 256 * j) + e;
-            if (i < n) yr[i] = ((c[j][e] - mean) * scale) * wr[i];
+            if (i < n) yr[i] = ((c[j][e] - mean) * scale) * wv[j][e];
         }
     for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)
         for (int e = 0; e < 4 && i + e < n; ++e) yr[i + e] = ((value(i + e) - mean) * scale) * wr[i + e];

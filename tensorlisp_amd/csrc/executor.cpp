@@ -32,7 +32,7 @@ struct Place {
 };
 
 enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
-                    D_ARGMAX_SPLIT };
+                    D_ARGMAX_SPLIT, D_CORE_MULTI };
 struct Dispatch {
     DispatchKind kind;
     int core_kind = 0;
@@ -47,6 +47,11 @@ struct Dispatch {
     int nmem = 0;
     tlh_op mop[3];
     Place mw[3], mdst[3];
+    // D_CORE_MULTI: independent element-wise ops in one launch
+    int nsub = 0;
+    int sub_kind[4];
+    tlh_op sop[4];
+    Place ssrc[4][4], sdst[4];
 };
 
 // ggml type traits used for byte sizes: (block elements, block bytes)
@@ -170,6 +175,8 @@ class Lowering {
         for (Dispatch &x : out.d) x.pos_last = x.pos;
         fuse_norm_chains(out.d);
         fuse_multi_gemv(out.d);
+        fuse_rope_rows(out.d);
+        group_elementwise(out.d);
         group_mul_mats(out.d);
         plan(out);
         return TLH_OK;
@@ -357,12 +364,14 @@ class Lowering {
 
     void count_readers() {
         readers_.assign(g_.n, 0);
+        reader_.assign(g_.n, -1);
         for (int32_t id : g_.nodes)
             for (int s = 0; s < 10; ++s)
-                if (g_.t[id].src[s] >= 0) ++readers_[g_.t[id].src[s]];
+                if (g_.t[id].src[s] >= 0) ++readers_[g_.t[id].src[s]], reader_[g_.t[id].src[s]] = id;
         for (int32_t id : g_.keep) ++readers_[id];
     }
     std::vector<int> readers_;
+    std::vector<int32_t> reader_;  // the (last) node reading each tensor
 
     static bool f32_rows(const tlh_tensor &t) { return t.ty == TLH_TYPE_F32 && t.nb[0] == 4; }
     static bool same_ne(const tlh_tensor &a, const tlh_tensor &b) {
@@ -488,6 +497,119 @@ class Lowering {
         d.swap(out);
     }
 
+    static bool same_root(const Place &a, const Place &b) {
+        return a.buf != B_NONE && a.buf != B_WEIGHT && a.buf == b.buf && a.index == b.index;
+    }
+    // every place a dispatch reads, and the ones it writes
+    static void places(const Dispatch &x, std::vector<Place> &rd, std::vector<Place> &wr) {
+        rd.clear(), wr.clear();
+        for (int k = 0; k < 4; ++k) rd.push_back(x.src[k]);
+        wr.push_back(x.dst);
+        for (int k = 0; k < x.nmem; ++k) rd.push_back(x.mw[k]), wr.push_back(x.mdst[k]);
+        for (int k = 0; k < x.nsub; ++k) {
+            for (int j = 0; j < 4; ++j) rd.push_back(x.ssrc[k][j]);
+            wr.push_back(x.sdst[k]);
+        }
+        if (x.kind == D_NORM_CHAIN) wr.push_back(x.src[3]);  // the ADD's result
+    }
+    static bool independent(const Dispatch &a, const Dispatch &b) {
+        std::vector<Place> ra, wa, rb, wb;
+        places(a, ra, wa);
+        places(b, rb, wb);
+        for (const Place &w : wa) {
+            for (const Place &r : rb)
+                if (same_root(w, r)) return false;
+            for (const Place &w2 : wb)
+                if (same_root(w, w2)) return false;
+        }
+        for (const Place &w : wb)
+            for (const Place &r : ra)
+                if (same_root(w, r)) return false;
+        return true;
+    }
+
+    // ROPE whose result is only reshaped into the rows a SET_ROWS writes (a
+    // K cache write): the rotation writes those cache rows itself, in the
+    // cache's type, and the SET_ROWS goes away. Nothing in between may touch
+    // the cache.
+    void fuse_rope_rows(std::vector<Dispatch> &d) {
+        std::vector<char> gone(d.size(), 0);
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &r = d[i];
+            if (!(r.kind == D_CORE && r.core_kind == TLH_CORE_ROPE)) continue;
+            const int32_t rn = node_of(r);
+            if (readers_[rn] != 1) continue;
+            const int32_t v = reader_[rn];
+            if (v < 0 || strcmp(g_.t[v].op, "RESHAPE") != 0 || readers_[v] != 1) continue;
+            const int32_t sr = reader_[v];
+            if (sr < 0 || strcmp(g_.t[sr].op, "SET_ROWS") != 0 || g_.t[sr].src[0] != v) continue;
+            size_t j = i + 1;
+            while (j < d.size() && !(d[j].kind == D_CORE && node_of(d[j]) == sr)) ++j;
+            if (j == d.size()) continue;
+            const Dispatch &w = d[j];
+            const tlh_tensor &x = r.op.t[0], &y = r.op.t[4], &cache = w.op.t[4], &ix = w.op.t[1];
+            bool ok = x.ne[3] == 1 && same_ne(x, y) && y.nb[0] == (y.ty == TLH_TYPE_F32 ? 4 : 2) &&
+                      y.nb[1] == y.nb[0] * y.ne[0] && y.nb[2] == y.nb[1] * y.ne[1] &&
+                      w.op.t[0].ne[0] == y.ne[0] * y.ne[1] && w.op.t[0].ne[1] == y.ne[2] && w.op.t[0].ne[2] == 1 &&
+                      w.op.t[0].ne[3] == 1 && ix.ne[0] == y.ne[2] && cache.ne[0] == y.ne[0] * y.ne[1] &&
+                      cache.nb[0] == (cache.ty == TLH_TYPE_F32 ? 4 : 2) && cache.ne[2] == 1 && cache.ne[3] == 1;
+            for (size_t k = i + 1; k < j && ok; ++k) {
+                std::vector<Place> rd, wr;
+                places(d[k], rd, wr);
+                for (const Place &p : rd) ok = ok && !same_root(p, w.dst);
+                for (const Place &p : wr) ok = ok && !same_root(p, w.dst);
+            }
+            if (!ok) continue;
+            r.op.t[3] = ix;
+            r.op.t[4] = cache;
+            r.op.x[9] = 1;
+            r.src[3] = w.src[1];
+            r.dst = w.dst;
+            r.pos_last = std::max(r.pos_last, w.pos_last);
+            gone[j] = 1;
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
+    // consecutive independent element-wise dispatches -> one launch (up to 4)
+    void group_elementwise(std::vector<Dispatch> &d) {
+        auto ew = [](const Dispatch &x) { return x.kind == D_CORE && core_multi_kind(x.core_kind); };
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size();) {
+            size_t j = i + 1;
+            if (ew(d[i]))
+                while (j < d.size() && j - i < 4 && ew(d[j])) {
+                    bool ind = true;
+                    for (size_t k = i; k < j && ind; ++k) ind = independent(d[k], d[j]);
+                    if (!ind) break;
+                    ++j;
+                }
+            if (j - i < 2) {
+                out.push_back(d[i++]);
+                continue;
+            }
+            Dispatch f = d[i];
+            f.kind = D_CORE_MULTI;
+            f.nsub = (int)(j - i);
+            for (size_t k = i; k < j; ++k) {
+                const int q = (int)(k - i);
+                f.sub_kind[q] = d[k].core_kind;
+                f.sop[q] = d[k].op;
+                for (int m = 0; m < 4; ++m) f.ssrc[q][m] = d[k].src[m];
+                f.sdst[q] = d[k].dst;
+                f.pos_last = std::max(f.pos_last, d[k].pos_last);
+            }
+            for (int m = 0; m < 4; ++m) f.src[m] = Place();
+            f.dst = Place();
+            out.push_back(f);
+            i = j;
+        }
+        d.swap(out);
+    }
+
     // MUL_MAT nodes with more than two activation columns that read the same
     // bytes with the same weight type (so the same q8 layout) share one
     // quantization: the first of them writes the blocks into a scratch block
@@ -600,6 +722,10 @@ class Lowering {
                 for (int k = 0; k < 4; ++k) touch_place(x.src[k], pos);
                 touch_place(x.dst, pos);
                 for (int k = 0; k < x.nmem; ++k) touch_place(x.mdst[k], pos);
+                for (int k = 0; k < x.nsub; ++k) {
+                    for (int m = 0; m < 4; ++m) touch_place(x.ssrc[k][m], pos);
+                    touch_place(x.sdst[k], pos);
+                }
             }
         }
         out.blocks.clear();
@@ -733,6 +859,16 @@ struct tlh_program {
                 break;
             case D_NORM_CHAIN: st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s); break;
             case D_ARGMAX_SPLIT: st = launch_argmax_split(x.op, src[0], dst, scratch, s); break;
+            case D_CORE_MULTI: {
+                const void *ss[4][4];
+                void *dd[4];
+                for (int k = 0; k < x.nsub; ++k) {
+                    for (int m = 0; m < 4; ++m) ss[k][m] = resolve(x.ssrc[k][m], state);
+                    dd[k] = resolve(x.sdst[k], state);
+                }
+                st = launch_core_multi(x.nsub, x.sub_kind, x.sop, ss, dd, s);
+                break;
+            }
             case D_MULTI_GEMV: {
                 const tlh_op *ops[3];
                 const void *w[3];
@@ -748,7 +884,14 @@ struct tlh_program {
                         st = tlh_mul_mat(ops[k], w[k], src[1], dsts[k], scratch, x.scratch_bytes, s);
                 break;
             }
-            default: st = tlh_core(x.core_kind, &x.op, src[0], src[1], src[2], dst, s); break;
+            default:
+                if (x.core_kind == TLH_CORE_ROPE && x.op.x[9]) {  // rope into cache rows
+                    const void *ss[1][4] = {{src[0], src[1], src[2], src[3]}};
+                    st = launch_core_multi(1, &x.core_kind, &x.op, ss, &dst, s);
+                } else {
+                    st = tlh_core(x.core_kind, &x.op, src[0], src[1], src[2], dst, s);
+                }
+                break;
             }
             if (st != TLH_OK) {
                 const int32_t id = low.node_ids[x.pos];
