@@ -785,6 +785,7 @@ constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows
 
 // The weight row has the norm's length (the executor fuses only then), so
 // element i of a row multiplies w[i].
+template <bool VEC>  // VEC: every row 16-byte aligned with n % 4 == 0, groups move as float4
 __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     __shared__ double shd[4];
     const tlh_tensor &tp = a.op.t[0], &tq = a.op.t[1], &tw = a.op.t[2], &ts = a.op.t[3], &ty = a.op.t[4];
@@ -803,25 +804,46 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     // thread t owns groups of four: elements 4 (t + 256 j) .. + 3; the weight
     // row is fetched with the values, so its latency overlaps the reduction
     float c[NC_CACHE][4], wv[NC_CACHE][4];
+    if constexpr (VEC) {
 #pragma unroll
-    for (int j = 0; j < NC_CACHE; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = 4 * (t + 256 * j) + e;
-            c[j][e] = i < n ? value(i) : 0.0f;
-            wv[j][e] = i < n ? wr[i] : 0.0f;
+        for (int j = 0; j < NC_CACHE; ++j) {
+            const int i = 4 * (t + 256 * j);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f), ww = v;
+            if (i < n) {
+                v = *(const float4 *)(pr + i);
+                if (add) {
+                    const float4 g = *(const float4 *)(qr + i);
+                    v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);
+                }
+                ww = *(const float4 *)(wr + i);
+            }
+            c[j][0] = v.x, c[j][1] = v.y, c[j][2] = v.z, c[j][3] = v.w;
+            wv[j][0] = ww.x, wv[j][1] = ww.y, wv[j][2] = ww.z, wv[j][3] = ww.w;
         }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NC_CACHE; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = 4 * (t + 256 * j) + e;
+                c[j][e] = i < n ? value(i) : 0.0f;
+                wv[j][e] = i < n ? wr[i] : 0.0f;
+            }
+    }
     double s1 = 0.0;
 #pragma unroll
-    for (int j = 0; j < NC_CACHE; ++j)
+    for (int j = 0; j < NC_CACHE; ++j) {
+        const int i0 = 4 * (t + 256 * j);
+        if (VEC && add && i0 < n) *(float4 *)(sr + i0) = make_float4(c[j][0], c[j][1], c[j][2], c[j][3]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int i = 4 * (t + 256 * j) + e;
+            const int i = i0 + e;
             if (i < n) {
-                if (add) sr[i] = c[j][e];
+                if (!VEC && add) sr[i] = c[j][e];
                 s1 += rms ? (double)(c[j][e] * c[j][e]) : (double)c[j][e];
             }
         }
+    }
     for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)  // rows past the registers
         for (int e = 0; e < 4 && i + e < n; ++e) {
             const float v = value(i + e);
@@ -856,12 +878,19 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     }
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
-    for (int j = 0; j < NC_CACHE; ++j)
+    for (int j = 0; j < NC_CACHE; ++j) {
+        const int i0 = 4 * (t + 256 * j);
+        float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = 4 * (t + 256 * j) + e;
-            if (i < n) yr[i] = ((c[j][e] - mean) * scale) * wv[j][e];
+        for (int e = 0; e < 4; ++e) o[e] = ((c[j][e] - mean) * scale) * wv[j][e];
+        if (VEC) {
+            if (i0 < n) *(float4 *)(yr + i0) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (i0 + e < n) yr[i0 + e] = o[e];
         }
+    }
     for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)
         for (int e = 0; e < 4 && i + e < n; ++e) yr[i + e] = ((value(i + e) - mean) * scale) * wr[i + e];
 }
@@ -877,7 +906,18 @@ tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, con
     a.y = (float *)y;
     const int64_t rows = nrows(op.t[0]);
     if (rows == 0) return TLH_OK;
-    hipLaunchKernelGGL(k_norm_chain, red_grid(rows), dim3(256), 0, stream, a);
+    const tlh_tensor *ts[5] = {&op.t[0], &op.t[1], &op.t[2], &op.t[3], &op.t[4]};
+    const void *ps[5] = {p, q, w, s, y};
+    bool vec = op.t[0].ne[0] % 4 == 0;
+    for (int k = 0; k < 5 && vec; ++k) {
+        if (!ps[k]) continue;
+        vec = ((uintptr_t)ps[k] & 15) == 0;
+        for (int i = 1; i < 4; ++i) vec = vec && ts[k]->nb[i] % 16 == 0;
+    }
+    if (vec)
+        hipLaunchKernelGGL(k_norm_chain<true>, red_grid(rows), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k_norm_chain<false>, red_grid(rows), dim3(256), 0, stream, a);
     return check_launch("norm_chain");
 }
 
