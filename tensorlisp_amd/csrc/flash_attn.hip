@@ -95,7 +95,7 @@ struct FaArgs {
     const char *q, *k, *v, *mask;
     char *dst;
     float *part;   // partials [nb][nh][nq][P][DV + 2] when P > 1
-    int2 *ranges;  // masked launches: live keys [lo, hi) of each mask row [mne3][mne2][nq]
+    int mask_vec;  // mask rows 16-byte aligned: scanned in 16-byte runs
     int64_t q_nb1, q_nb2, q_nb3;
     int64_t k_nb1, k_nb2, k_nb3;
     int64_t v_nb1, v_nb2, v_nb3;
@@ -147,16 +147,43 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
     const int iq = qc * a.qr + rr / a.gc;
     const int h = hk * a.G + hc * a.gc + rr % a.gc;
     if constexpr (MASK) {
-        // keys outside every row's live range are -inf for the whole tile: skip them
-        int2 rg = a.ranges[((int64_t)(ib % a.m_ne3) * a.m_ne2 + h % a.m_ne2) * a.nq + iq];
-        if (!rlive) rg = make_int2(INT32_MAX, 0);
+        // keys that are -inf in every mask row of the tile are skipped: the
+        // live range [lo, hi) of the tile's rows inside [j0, j1), lane (g, c)
+        // scanning row c in runs of 8 keys j0 + 8 (g + 4 k), then the union
+        // over the 16 rows and 4 groups
+        int lo = INT32_MAX, hi = 0;
+        if (rlive) {
+            const uint16_t *mr = (const uint16_t *)(a.mask + iq * a.m_nb1 + (int64_t)(h % a.m_ne2) * a.m_nb2 +
+                                                    (int64_t)(ib % a.m_ne3) * a.m_nb3);
+            int jt = j0;  // keys past the 16-byte runs, one by one
+            if (a.mask_vec) {
+                const int jv = j0 + (j1 - j0) / 8 * 8;
+                for (int jb = j0 + 8 * g; jb < jv; jb += 32) {
+                    const uint4 w = *(const uint4 *)(mr + jb);
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            rg.x = min(rg.x, __shfl_xor(rg.x, o, 64));
-            rg.y = max(rg.y, __shfl_xor(rg.y, o, 64));
+                    for (int e = 0; e < 8; ++e)
+                        if (((ws[e / 2] >> (16 * (e & 1))) & 0xffffu) != 0xfc00u) {  // not f16 -inf
+                            lo = min(lo, jb + e);
+                            hi = max(hi, jb + e + 1);
+                        }
+                }
+                jt = jv;
+            }
+#pragma unroll 8
+            for (int j = jt + g; j < j1; j += 4)
+                if (mr[j] != 0xfc00u) {
+                    lo = min(lo, j);
+                    hi = max(hi, j + 1);
+                }
         }
-        j0 = max(j0, rg.x);
-        j1 = min(j1, rg.y);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            lo = min(lo, __shfl_xor(lo, o, 64));
+            hi = max(hi, __shfl_xor(hi, o, 64));
+        }
+        j0 = max(j0, lo);
+        j1 = min(j1, hi);
     }
 
     // Q^T operand (row c, dims of step st for group g), rounded to f16
@@ -399,38 +426,6 @@ __global__ void __launch_bounds__(256) k_flash_attn_reduce(const FaArgs a) {
     }
 }
 
-// Live key range [lo, hi) of each mask row (first and one past the last entry
-// that is not -inf; lo = L, hi = 0 when there is none), one wave per row of
-// [mne3][mne2][nq]: the attention kernels clip their key loops to the union
-// over their rows, so causal, padding and window masks skip whole key ranges.
-__global__ void __launch_bounds__(256) k_fa_mask_range(const FaArgs a, int rows) {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
-    const int lane = threadIdx.x & 63;
-    const int iq = r % a.nq, mh = (r / a.nq) % a.m_ne2, mb = r / (a.nq * a.m_ne2);
-    const uint16_t *mrow = (const uint16_t *)(a.mask + iq * a.m_nb1 + mh * a.m_nb2 + mb * a.m_nb3);
-    int lo = a.L, hi = 0;
-    for (int j0 = 0; j0 < a.L; j0 += 8 * 64) {
-        uint16_t v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = mrow[min(j0 + 64 * u + lane, a.L - 1)];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = j0 + 64 * u + lane;
-            if (j < a.L && v[u] != 0xfc00u) {  // f16 -inf
-                lo = min(lo, j);
-                hi = max(hi, j + 1);
-            }
-        }
-    }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        lo = min(lo, __shfl_xor(lo, o, 64));
-        hi = max(hi, __shfl_xor(hi, o, 64));
-    }
-    if (lane == 0) a.ranges[r] = make_int2(lo, hi);
-}
-
 // ------------------------------------------------------------------ host
 bool flash_attn_head_sizes_ok(int64_t D, int64_t DV) {
     if (D == 192 && DV == 128) return true;
@@ -477,18 +472,16 @@ static int64_t fa_partial_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv
 
 int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L,
                                  int64_t mask_rows) {
-    return fa_partial_bytes(DV, nq, nh, nhkv, nb, L) + (L > 0 ? mask_rows * (int64_t)sizeof(int2) : 0);
+    (void)mask_rows;  // the kernels scan the mask themselves
+    return fa_partial_bytes(DV, nq, nh, nhkv, nb, L);
 }
 
 template <int D, int DV>
 static void launch_fa(const FaArgs &a, bool mask, hipStream_t stream) {
     constexpr bool PIPE = D <= 128 && DV <= 128;  // two register sets fit
     const dim3 grid(a.QC * a.HC * a.P, a.nhkv, a.nb);
-    if (mask) {
-        const int rows = a.nq * a.m_ne2 * a.m_ne3;
-        hipLaunchKernelGGL(k_fa_mask_range, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows);
+    if (mask)
         hipLaunchKernelGGL((k_flash_attn<D, DV, true, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
-    }
     else
         hipLaunchKernelGGL((k_flash_attn<D, DV, false, PIPE>), grid, dim3(64 * FA_WAVES), 0, stream, a);
     if (a.P > 1)
@@ -504,7 +497,7 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
     a.mask = (const char *)d.mask;
     a.dst = (char *)d.dst;
     a.part = (float *)d.scratch;
-    a.ranges = (int2 *)((char *)d.scratch + fa_partial_bytes(d.DV, d.nq, d.nh, d.nhkv, d.nb, d.L));
+    a.mask_vec = !((uintptr_t)d.mask & 15) && d.m_nb[1] % 16 == 0 && d.m_nb[2] % 16 == 0 && d.m_nb[3] % 16 == 0;
     a.q_nb1 = d.q_nb[1], a.q_nb2 = d.q_nb[2], a.q_nb3 = d.q_nb[3];
     a.k_nb1 = d.k_nb[1], a.k_nb2 = d.k_nb[2], a.k_nb3 = d.k_nb[3];
     a.v_nb1 = d.v_nb[1], a.v_nb2 = d.v_nb[2], a.v_nb3 = d.v_nb[3];

@@ -73,8 +73,7 @@ struct FlashAttnDesc {
     int n_head_log2;
 };
 bool flash_attn_head_sizes_ok(int64_t D, int64_t DV);
-// split-key partials, then (mask_rows = nq * mne2 * mne3 when masked) the
-// live key range of each mask row
+// split-key partials (mask_rows is not used: the kernels scan the mask)
 int64_t flash_attn_scratch_bytes(int64_t DV, int64_t nq, int64_t nh, int64_t nhkv, int64_t nb, int64_t L,
                                  int64_t mask_rows);
 tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
