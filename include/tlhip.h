@@ -339,6 +339,45 @@ tlh_status tlh_program_plan(const tlh_ir_tensor *tensors, int32_t n_tensors, con
                             const int32_t *keep, int32_t n_keep, int64_t *tensor_offsets, int64_t *scratch_offsets,
                             size_t *arena_bytes);
 
+/* ------------------------------------------------------------------ GGUF
+ * Reading a GGUF model and loading its tensors into device memory, in place
+ * of the reference's load for its native executors
+ * (crates/tensorlisp/src/native_cuda.rs:44-82, reading through ggml's
+ * gguf.cpp as crates/tensorlisp/src/gguf.rs:79-320 does). The file is checked
+ * with ggml's rules (versions 2-3; general.alignment a u32 power of two,
+ * default 32; tensor names under 64 bytes, unique; at most 4 dimensions; rows
+ * of whole blocks; tensor offsets consecutive at the alignment); a refusal is
+ * TLH_INVALID (TLH_UNSUPPORTED for a ggml type this loader cannot size) with
+ * the reason. Key-value pairs keep their GGUF types (gguf_type numbering);
+ * numeric values and arrays come back as their raw little-endian bytes.
+ * tlh_gguf_layout places every tensor 256-byte aligned in one buffer of
+ * `total` bytes; tlh_gguf_upload copies the file's tensor data there through
+ * pinned staging buffers (a synchronous call on `stream`). */
+typedef struct tlh_gguf tlh_gguf;
+typedef struct tlh_gguf_tensor_info {
+    char name[64];
+    int32_t ty;      /* ggml type */
+    int32_t n_dims;
+    int64_t ne[4];
+    uint64_t offset; /* in the data section */
+    uint64_t bytes;
+} tlh_gguf_tensor_info;
+
+tlh_status tlh_gguf_open(const char *path, tlh_gguf **g);
+tlh_status tlh_gguf_close(tlh_gguf *g);
+tlh_status tlh_gguf_counts(const tlh_gguf *g, uint32_t *version, int64_t *n_tensors, int64_t *n_kv,
+                           uint64_t *alignment, uint64_t *data_offset);
+tlh_status tlh_gguf_tensor(const tlh_gguf *g, int64_t i, tlh_gguf_tensor_info *info);
+tlh_status tlh_gguf_find_tensor(const tlh_gguf *g, const char *name, int64_t *i); /* -1 when absent */
+tlh_status tlh_gguf_find_key(const tlh_gguf *g, const char *key, int64_t *i);     /* -1 when absent */
+/* type: gguf_type of the value; for arrays (9) also the element type and count */
+tlh_status tlh_gguf_key(const tlh_gguf *g, int64_t i, const char **key, int32_t *type, int32_t *arr_type,
+                        uint64_t *n);
+tlh_status tlh_gguf_value(const tlh_gguf *g, int64_t i, const void **data, size_t *bytes); /* numeric / bool */
+tlh_status tlh_gguf_string(const tlh_gguf *g, int64_t i, uint64_t j, const char **s, uint64_t *len);
+tlh_status tlh_gguf_layout(const tlh_gguf *g, uint64_t *offsets, uint64_t *total);
+tlh_status tlh_gguf_upload(const tlh_gguf *g, void *dev, const uint64_t *offsets, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

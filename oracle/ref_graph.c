@@ -331,3 +331,115 @@ int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_node
     ggml_free(ctx);
     return rc;
 }
+
+// ------------------------------------------------------------------ GGUF
+// ggml's own GGUF reader and writer (vendor/ggml/src/gguf.cpp), to pin the
+// product's reader: ref_gguf_* describe a file as ggml parses it, and
+// ref_gguf_write_sample writes one with ggml's writer.
+#include "gguf.h"
+
+typedef struct {
+    struct gguf_context *g;
+    struct ggml_context *ctx;
+} ref_gguf;
+
+void *ref_gguf_open(const char *path) {
+    ref_gguf *h = calloc(1, sizeof *h);
+    struct gguf_init_params p = {.no_alloc = true, .ctx = &h->ctx};
+    h->g = gguf_init_from_file(path, p);
+    if (!h->g) {
+        free(h);
+        return NULL;
+    }
+    return h;
+}
+void ref_gguf_close(void *hp) {
+    ref_gguf *h = hp;
+    if (!h) return;
+    gguf_free(h->g);
+    if (h->ctx) ggml_free(h->ctx);
+    free(h);
+}
+void ref_gguf_info(void *hp, int64_t *n_tensors, int64_t *n_kv, size_t *alignment, size_t *data_offset,
+                   uint32_t *version) {
+    ref_gguf *h = hp;
+    *n_tensors = gguf_get_n_tensors(h->g);
+    *n_kv = gguf_get_n_kv(h->g);
+    *alignment = gguf_get_alignment(h->g);
+    *data_offset = gguf_get_data_offset(h->g);
+    *version = gguf_get_version(h->g);
+}
+void ref_gguf_tensor(void *hp, int64_t i, char *name, int *type, int64_t *ne, size_t *offset, size_t *bytes) {
+    ref_gguf *h = hp;
+    const char *n = gguf_get_tensor_name(h->g, i);
+    strncpy(name, n, 63);
+    name[63] = 0;
+    *type = (int)gguf_get_tensor_type(h->g, i);
+    *offset = gguf_get_tensor_offset(h->g, i);
+    *bytes = gguf_get_tensor_size(h->g, i);
+    const struct ggml_tensor *t = ggml_get_tensor(h->ctx, n);
+    for (int d = 0; d < 4; ++d) ne[d] = t->ne[d];
+}
+const char *ref_gguf_key(void *hp, int64_t i, int *type, int *arr_type, size_t *n) {
+    ref_gguf *h = hp;
+    *type = (int)gguf_get_kv_type(h->g, i);
+    *arr_type = *type == GGUF_TYPE_ARRAY ? (int)gguf_get_arr_type(h->g, i) : -1;
+    *n = *type == GGUF_TYPE_ARRAY ? gguf_get_arr_n(h->g, i) : 1;
+    return gguf_get_key(h->g, i);
+}
+const void *ref_gguf_data(void *hp, int64_t i) {
+    ref_gguf *h = hp;
+    return gguf_get_kv_type(h->g, i) == GGUF_TYPE_ARRAY ? gguf_get_arr_data(h->g, i) : gguf_get_val_data(h->g, i);
+}
+const char *ref_gguf_str(void *hp, int64_t i, int64_t j) {
+    ref_gguf *h = hp;
+    return gguf_get_kv_type(h->g, i) == GGUF_TYPE_ARRAY ? gguf_get_arr_str(h->g, i, j) : gguf_get_val_str(h->g, i);
+}
+
+// A file written by ggml's writer: every scalar type, strings, arrays of
+// u32 / f32 / strings, general.alignment when `alignment` != 0, and tensors of
+// several types and ranks with deterministic contents.
+int ref_gguf_write_sample(const char *path, uint32_t alignment) {
+    struct gguf_context *g = gguf_init_empty();
+    gguf_set_val_u8(g, "t.u8", 200);
+    gguf_set_val_i8(g, "t.i8", -100);
+    gguf_set_val_u16(g, "t.u16", 60000);
+    gguf_set_val_i16(g, "t.i16", -30000);
+    gguf_set_val_u32(g, "t.u32", 4000000000u);
+    gguf_set_val_i32(g, "t.i32", -2000000000);
+    gguf_set_val_f32(g, "t.f32", 3.25f);
+    gguf_set_val_bool(g, "t.bool", true);
+    gguf_set_val_str(g, "t.str", "a string, unicode \\xc3\\xa9");
+    gguf_set_val_u64(g, "t.u64", 18000000000000000000ull);
+    gguf_set_val_i64(g, "t.i64", -9000000000000000000ll);
+    gguf_set_val_f64(g, "t.f64", -1.0e300);
+    const uint32_t au[5] = {1, 2, 3, 4, 5};
+    gguf_set_arr_data(g, "t.arr_u32", GGUF_TYPE_UINT32, au, 5);
+    const float af[3] = {0.5f, -1.5f, 1e-20f};
+    gguf_set_arr_data(g, "t.arr_f32", GGUF_TYPE_FLOAT32, af, 3);
+    const char *as[3] = {"x", "", "longer string"};
+    gguf_set_arr_str(g, "t.arr_str", as, 3);
+    if (alignment) gguf_set_val_u32(g, "general.alignment", alignment);
+    struct ggml_init_params ip = {.mem_size = 1 << 20, .mem_buffer = NULL, .no_alloc = false};
+    struct ggml_context *ctx = ggml_init(ip);
+    const struct {
+        const char *name;
+        enum ggml_type ty;
+        int nd;
+        int64_t ne[4];
+    } ts[] = {{"w.f32", GGML_TYPE_F32, 2, {7, 3}},    {"w.f16", GGML_TYPE_F16, 1, {64}},
+              {"w.q4_0", GGML_TYPE_Q4_0, 2, {64, 2}}, {"w.q8_0", GGML_TYPE_Q8_0, 3, {32, 3, 2}},
+              {"w.q4_K", GGML_TYPE_Q4_K, 2, {256, 2}}, {"w.q6_K", GGML_TYPE_Q6_K, 1, {512}},
+              {"w.i32", GGML_TYPE_I32, 4, {5, 1, 1, 2}}};
+    for (size_t k = 0; k < sizeof ts / sizeof ts[0]; ++k) {
+        struct ggml_tensor *t = ggml_new_tensor(ctx, ts[k].ty, ts[k].nd, ts[k].ne);
+        ggml_set_name(t, ts[k].name);
+        uint8_t *d = t->data;
+        for (size_t b = 0; b < ggml_nbytes(t); ++b) d[b] = (uint8_t)(b * 31 + k * 7);
+        gguf_add_tensor(g, t);
+    }
+    const bool ok = gguf_write_to_file(g, path, false);
+    ggml_free(ctx);
+    gguf_free(g);
+    return ok ? 0 : -1;
+}

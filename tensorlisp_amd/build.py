@@ -38,7 +38,7 @@ COMMON = [
 
 
 def sources():
-    return sorted(CSRC.glob("*.hip")) + [CSRC / "tlhip.cpp", CSRC / "executor.cpp"]
+    return sorted(CSRC.glob("*.hip")) + [CSRC / "tlhip.cpp", CSRC / "executor.cpp", CSRC / "gguf.cpp"]
 
 
 def _compile(src: Path) -> Path:

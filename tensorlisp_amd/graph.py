@@ -339,6 +339,7 @@ class DecoderConfig:
     wtype: int = N.Q4_K       # attention and FFN matrices
     embd_type: int = N.Q4_K   # token embedding (read with GET_ROWS)
     out_type: int = N.Q6_K    # lm_head
+    types: dict = None        # per-weight types (a GGUF file's), overriding the three above
 
     @property
     def head_dim(self) -> int:
@@ -359,6 +360,8 @@ class DecoderConfig:
                     (f"l{i}.w_gate", c.wtype, [c.n_embd, c.n_ff]), (f"l{i}.w_up", c.wtype, [c.n_embd, c.n_ff]),
                     (f"l{i}.w_down", c.wtype, [c.n_ff, c.n_embd])]
         out += [("out_norm", N.F32, [c.n_embd]), ("output", c.out_type, [c.n_embd, c.n_vocab])]
+        if c.types:
+            out = [(name, c.types.get(name, ty), ne) for name, ty, ne in out]
         return out
 
     def state_bytes(self):

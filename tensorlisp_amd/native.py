@@ -35,6 +35,8 @@ EXPORTS = (
     "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
     "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_program_input",
     "tlh_program_tensor", "tlh_program_run", "tlh_program_stats", "tlh_program_plan",
+    "tlh_gguf_open", "tlh_gguf_close", "tlh_gguf_counts", "tlh_gguf_tensor", "tlh_gguf_find_tensor",
+    "tlh_gguf_find_key", "tlh_gguf_key", "tlh_gguf_value", "tlh_gguf_string", "tlh_gguf_layout", "tlh_gguf_upload",
 )
 
 
@@ -110,6 +112,18 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_program_stats.argtypes = [vp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]
     L.tlh_program_plan.argtypes = [vp, C.c_int32, i32p, C.c_int32, i32p, C.c_int32, i64p, i64p,
                                    C.POINTER(C.c_size_t)]
+    u64p, cpp = C.POINTER(C.c_uint64), C.POINTER(C.c_char_p)
+    L.tlh_gguf_open.argtypes = [C.c_char_p, C.POINTER(C.c_void_p)]
+    L.tlh_gguf_close.argtypes = [vp]
+    L.tlh_gguf_counts.argtypes = [vp, C.POINTER(C.c_uint32), i64p, i64p, u64p, u64p]
+    L.tlh_gguf_tensor.argtypes = [vp, C.c_int64, vp]
+    L.tlh_gguf_find_tensor.argtypes = [vp, C.c_char_p, i64p]
+    L.tlh_gguf_find_key.argtypes = [vp, C.c_char_p, i64p]
+    L.tlh_gguf_key.argtypes = [vp, C.c_int64, cpp, C.POINTER(C.c_int32), C.POINTER(C.c_int32), u64p]
+    L.tlh_gguf_value.argtypes = [vp, C.c_int64, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+    L.tlh_gguf_string.argtypes = [vp, C.c_int64, C.c_uint64, cpp, u64p]
+    L.tlh_gguf_layout.argtypes = [vp, u64p, u64p]
+    L.tlh_gguf_upload.argtypes = [vp, vp, u64p, vp]
     for name in EXPORTS:
         if name not in ("tlh_last_error", "tlh_status_name", "tlh_version"):
             getattr(L, name).restype = st

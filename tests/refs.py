@@ -340,6 +340,17 @@ class Ref:
         L.ref_flash_attn_ext.restype = C.c_int
         L.ref_core.argtypes = [C.c_int, vp, vp, vp, vp, vp, C.c_int]
         L.ref_ir_run.argtypes = [vp, C.c_int, vp, C.c_int, vp, vp, vp, vp, vp, C.c_int, C.c_int]
+        L.ref_gguf_open.argtypes, L.ref_gguf_open.restype = [C.c_char_p], vp
+        L.ref_gguf_close.argtypes = [vp]
+        L.ref_gguf_info.argtypes = [vp] + [C.POINTER(C.c_int64)] * 2 + [C.POINTER(C.c_size_t)] * 2 + [
+            C.POINTER(C.c_uint32)]
+        L.ref_gguf_tensor.argtypes = [vp, C.c_int64, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int64),
+                                      C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        L.ref_gguf_key.argtypes = [vp, C.c_int64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_size_t)]
+        L.ref_gguf_key.restype = C.c_char_p
+        L.ref_gguf_data.argtypes, L.ref_gguf_data.restype = [vp, C.c_int64], vp
+        L.ref_gguf_str.argtypes, L.ref_gguf_str.restype = [vp, C.c_int64, C.c_int64], C.c_char_p
+        L.ref_gguf_write_sample.argtypes = [C.c_char_p, C.c_uint32]
         L.ggml_cpu_init.argtypes = []
         L.ggml_cpu_init()
 
@@ -495,6 +506,46 @@ class Ref:
                                  nthreads)
         assert rc == 0, (rc, builder.t[-rc % 1000].op if rc < -999 else "")
         return res
+
+
+    def gguf_describe(self, path):
+        """A GGUF file as ggml's reader sees it: None if it refuses the file, else
+        dict(version, alignment, data_offset, tensors [(name, type, ne, offset,
+        bytes)], kv {key: (gguf type, value)})."""
+        L = self.lib
+        h = L.ref_gguf_open(str(path).encode())
+        if not h:
+            return None
+        try:
+            nt, nk, al, do, ver = C.c_int64(), C.c_int64(), C.c_size_t(), C.c_size_t(), C.c_uint32()
+            L.ref_gguf_info(h, C.byref(nt), C.byref(nk), C.byref(al), C.byref(do), C.byref(ver))
+            tensors = []
+            for i in range(nt.value):
+                name = C.create_string_buffer(64)
+                ty, ne, off, nb = C.c_int(), (C.c_int64 * 4)(), C.c_size_t(), C.c_size_t()
+                L.ref_gguf_tensor(h, i, name, C.byref(ty), ne, C.byref(off), C.byref(nb))
+                tensors.append((name.value.decode(), ty.value, list(ne), off.value, nb.value))
+            kv = {}
+            sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+            npt = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32,
+                   7: np.bool_, 10: np.uint64, 11: np.int64, 12: np.float64}
+            for i in range(nk.value):
+                ty, aty, n = C.c_int(), C.c_int(), C.c_size_t()
+                key = L.ref_gguf_key(h, i, C.byref(ty), C.byref(aty), C.byref(n)).decode()
+                t = ty.value
+                if t == 8 or (t == 9 and aty.value == 8):
+                    vals = [L.ref_gguf_str(h, i, j).decode("utf-8", "replace") for j in range(n.value)]
+                    kv[key] = (t, vals[0] if t == 8 else vals)
+                else:
+                    et = aty.value if t == 9 else t
+                    raw = np.frombuffer(C.string_at(L.ref_gguf_data(h, i), n.value * sizes[et]), npt[et])
+                    kv[key] = (t, raw.copy() if t == 9 else raw[0].item())
+            return dict(version=ver.value, alignment=al.value, data_offset=do.value, tensors=tensors, kv=kv)
+        finally:
+            L.ref_gguf_close(h)
+
+    def gguf_write_sample(self, path, alignment: int = 0):
+        assert self.lib.ref_gguf_write_sample(str(path).encode(), alignment) == 0
 
 
 def flash_attn_f64(q, k, v, mask=None, scale=1.0, max_bias=0.0, softcap=0.0) -> np.ndarray:

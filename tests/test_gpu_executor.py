@@ -47,11 +47,11 @@ def dev(a):
 
 
 class GpuDecoder:
-    def __init__(self, c, weights):
+    def __init__(self, c, weights, on_device=False):
         import torch
 
         self.c = c
-        self.w = [dev(w) for w in weights]
+        self.w = list(weights) if on_device else [dev(w) for w in weights]
         self.offs, total = c.state_bytes()
         self.state = torch.zeros(total, dtype=torch.uint8, device="cuda")
 
@@ -232,3 +232,4 @@ def test_argmax_of_a_vocabulary(gpu):
     got = prog.read(am, torch.int32).cpu().numpy().reshape(-1)
     np.testing.assert_array_equal(got, oracle().core_argmax(x))
     assert list(got[1:]) == [128255, 128255, 2048]
+
