@@ -1,7 +1,7 @@
 /*
  * tlhip.h — C ABI of the MI355X (gfx950) executor for tensorlisp's quantized
  * hot path: GGML_OP_MUL_MAT over GGUF block-quantized weights (Q8_0, Q4_0,
- * Q4_K, Q6_K; decode GEMV for N <= 16 columns, MFMA GEMM for prefill),
+ * Q4_K, Q5_K, Q6_K; decode GEMV for N <= 16 columns, MFMA GEMM for prefill),
  * paged-attention decode over an f16 block-table KV cache, and dense
  * GGML_OP_FLASH_ATTN_EXT over f16 K/V.
  *
@@ -47,6 +47,7 @@ enum {
     TLH_TYPE_Q4_0 = 2,
     TLH_TYPE_Q8_0 = 8,
     TLH_TYPE_Q4_K = 12,
+    TLH_TYPE_Q5_K = 13,
     TLH_TYPE_Q6_K = 14,
     TLH_TYPE_Q8_K = 15
 };
@@ -104,13 +105,13 @@ typedef struct tlh_op {
  * GGML_OP_MUL_MAT, replacing Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
  * and its mm_vec / mm_tile kernels (crates/kernels/src/cuda/native/mm.cu:16-103),
  * computed the way the ggml CPU backend does (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457):
- *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K | Q6_K, ne [K, M, ne02, ne03],
+ *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K | Q5_K | Q6_K, ne [K, M, ne02, ne03],
  *                  nb[0] = block bytes (rows must not be transposed);
  *   op->t[1] src1: f32 activations, ne [K, N, ne12, ne13], nb[0] = 4;
  *   op->t[4] dst:  f32 [M, N, ne12, ne13], nb[0] = 4;
  *   op->x[0] = r2 = ne12 / ne02, op->x[1] = r3 = ne13 / ne03 (broadcast).
  * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0 and
- * Q8_0, Q8_K for Q4_K and Q6_K) into `scratch` (at least tlh_mul_mat_scratch_bytes);
+ * Q8_0, Q8_K for Q4_K, Q5_K and Q6_K) into `scratch` (at least tlh_mul_mat_scratch_bytes);
  * then N <= 16 runs the decode GEMV (register kernel for N <= 2, int8-MFMA
  * few-column kernel above), larger N the MFMA GEMM. Integer block
  * sums are exact; the f32 result agrees with the CPU backend to rounding of
@@ -142,8 +143,8 @@ tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *s
 tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, int64_t x_row_bytes, void *y,
                             void *stream);
 
-/* dequantize_row_{q4_0,q8_0,q4_K,q6_K} (vendor/ggml/src/ggml-quants.c:459-476,
- * :553-565, :1529-1550, :1939-1968), bit-exact: `rows` rows of `k` elements (row stride
+/* dequantize_row_{q4_0,q8_0,q4_K,q5_K,q6_K} (vendor/ggml/src/ggml-quants.c:459-476,
+ * :553-565, :1529-1550, :1731-1756, :1939-1968), bit-exact: `rows` rows of `k` elements (row stride
  * w_row_bytes) into f32 [rows][k]. The to_f32 of DType (crates/tensorlisp/src/dtype.rs:80-95). */
 tlh_status tlh_dequantize(int type, const void *w, int64_t k, int64_t rows, int64_t w_row_bytes, float *y,
                           void *stream);
@@ -199,7 +200,7 @@ typedef enum tlh_core_kind {
                               CLAMP 102 (x1, x2), LEAKY_RELU 103 (x1), SQR 104, SQRT 105, SIN 106,
                               COS 107, LOG 108 (lower.rs:250-290) */
     TLH_CORE_NORM = 3,     /* NORM (x0 = 0) / RMS_NORM (x0 = 1), x1 = eps; f32 rows, unit element stride */
-    TLH_CORE_GET_ROWS = 4, /* t0 f32/f16/q4_0/q8_0/q4_K/q6_K rows, t1 indices -> t4 f32/f16 */
+    TLH_CORE_GET_ROWS = 4, /* t0 f32/f16/q4_0/q8_0/q4_K/q5_K/q6_K rows, t1 indices -> t4 f32/f16 */
     TLH_CORE_SET_ROWS = 5, /* t0 f32/f16 rows to the t4 rows named by t1 */
     TLH_CORE_CPY = 6,      /* DUP/CPY/CONT: equal element counts, any shapes/strides */
     TLH_CORE_ROPE = 7,     /* x0 n_dims, x1 mode (0 normal, 2 neox), x2 freq_scale, x3 ext_factor,

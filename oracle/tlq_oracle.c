@@ -11,16 +11,17 @@
 // ---------------------------------------------------------------- geometry
 // ggml-common.h:194-198 (q4_0: f16 d + 16 nibble bytes), :251-255 (q8_0: f16 d
 // + 32 int8), :325-337 (q4_K: f16 d, f16 dmin, 12 packed 6-bit scale/min
-// bytes, 128 nibble bytes), :362-368 (q6_K: 128 low-nibble bytes, 64 bytes of
+// bytes, 128 nibble bytes), :345-352 (q5_K: q4_K's header, 32 bytes of fifth
+// bits, 128 nibble bytes), :362-368 (q6_K: 128 low-nibble bytes, 64 bytes of
 // 2-bit high parts, 16 int8 scales, f16 d), :370-375 (q8_K: f32 d, 256 int8,
 // 16 int16 sums).
-enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q6_K_B = 210, Q8_K_B = 292 };
+enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q5_K_B = 176, Q6_K_B = 210, Q8_K_B = 292 };
 
 int64_t tlq_block_elems(int type) {
     switch (type) {
     case TLQ_F32: case TLQ_F16: return 1;
     case TLQ_Q4_0: case TLQ_Q8_0: return QK32;
-    case TLQ_Q4_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
+    case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
     default: return 0;
     }
 }
@@ -32,6 +33,7 @@ int64_t tlq_block_bytes(int type) {
     case TLQ_Q4_0: return Q4_0_B;
     case TLQ_Q8_0: return Q8_0_B;
     case TLQ_Q4_K: return Q4_K_B;
+    case TLQ_Q5_K: return Q5_K_B;
     case TLQ_Q6_K: return Q6_K_B;
     case TLQ_Q8_K: return Q8_K_B;
     default: return 0;
@@ -46,7 +48,7 @@ int64_t tlq_row_bytes(int type, int64_t k) {
 int tlq_vec_dot_type(int wtype) {
     switch (wtype) {
     case TLQ_Q4_0: case TLQ_Q8_0: return TLQ_Q8_0;
-    case TLQ_Q4_K: case TLQ_Q6_K: return TLQ_Q8_K;
+    case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: return TLQ_Q8_K;
     default: return -1;
     }
 }
@@ -373,6 +375,28 @@ void tlq_dequantize_row_q4_K(const void *vx, float *y, int64_t k) {
     }
 }
 
+// ggml-quants.c:1731-1756: q4_K's arithmetic on 5-bit codes. Element l of
+// sub-block s (32 elements, s = 0..7) has its low 4 bits in nibble s & 1 of
+// qs[32 (s / 2) + l] (qs at byte 48) and its fifth bit at bit s of qh[l].
+static int q5k_code(const uint8_t *blk, int s, int l) {
+    const uint8_t q = blk[48 + 32 * (s / 2) + l];
+    return ((s & 1) ? (q >> 4) : (q & 0x0f)) | (((blk[16 + l] >> s) & 1) << 4);
+}
+
+void tlq_dequantize_row_q5_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q5_K_B) {
+        const float d = tlq_fp16_to_fp32(rd16(x));
+        const float dmin = tlq_fp16_to_fp32(rd16(x + 2));
+        for (int s = 0; s < 8; ++s) {
+            int sc, mn;
+            q4k_scale_min(s, x + 4, &sc, &mn);
+            const float d1 = d * sc, m1 = dmin * mn;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * q5k_code(x, s, l) - m1;
+        }
+    }
+}
+
 // ggml-quants.c:1939-1968: per 128-element half, element 32q + l has its low
 // 4 bits in ql[l + 32 (q & 1)] (high nibble for q >= 2) and its high 2 bits
 // in qh[l] at bit 2q; y = (d * scale) * (code - 32), scale per 16 elements.
@@ -405,6 +429,7 @@ int tlq_dequantize_row(int type, const void *x, float *y, int64_t k) {
     case TLQ_Q4_0: tlq_dequantize_row_q4_0(x, y, k); return 0;
     case TLQ_Q8_0: tlq_dequantize_row_q8_0(x, y, k); return 0;
     case TLQ_Q4_K: tlq_dequantize_row_q4_K(x, y, k); return 0;
+    case TLQ_Q5_K: tlq_dequantize_row_q5_K(x, y, k); return 0;
     case TLQ_Q6_K: tlq_dequantize_row_q6_K(x, y, k); return 0;
     case TLQ_Q8_K: tlq_dequantize_row_q8_K(x, y, k); return 0;
     default: return -1;
@@ -499,6 +524,41 @@ float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *vx, const void *vy) {
     return acc;
 }
 
+// ggml-cpu/quants.c:771-850: the q4_K arithmetic of tlq_vec_dot_q4_K_q8_K on
+// 5-bit codes. Per super-block eight int32 lane accumulators (element e feeds
+// lane e % 8) of scale_s * (int16)(code * q8), the min correction
+// sum_g bsums[g] * m_{g/2}; sums[lane] += (dx*dy) * lane, sumf -= (dminx*dy) *
+// minsum, and sums[0..7] added to sumf at the end.
+float tlq_vec_dot_q5_K_q8_K(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float sums[8] = {0};
+    float sumf = 0;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q5_K_B, y += Q8_K_B) {
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int32_t aux32[8] = {0};
+        int32_t sumi = 0;
+        for (int g = 0; g < 16; ++g) {
+            int16_t bs;
+            memcpy(&bs, y + 4 + QKK + 2 * g, 2);
+            int sc, mn;
+            q4k_scale_min(g / 2, x + 4, &sc, &mn);
+            sumi += bs * mn;
+        }
+        for (int s = 0; s < 8; ++s) {
+            int sc, mn;
+            q4k_scale_min(s, x + 4, &sc, &mn);
+            for (int l = 0; l < 32; ++l) aux32[l % 8] += sc * (int16_t)(q5k_code(x, s, l) * q8[32 * s + l]);
+        }
+        const float dy = rdf32(y);
+        const float d = tlq_fp16_to_fp32(rd16(x)) * dy;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+        const float dmin = tlq_fp16_to_fp32(rd16(x + 2)) * dy;
+        sumf -= dmin * sumi;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
 // ggml-cpu/quants.c:851-904. Per super-block: codes in element order, eight
 // int32 lane accumulators (element e of each 16-element sub-block feeds lane
 // e % 8) of scale_j * (code * q8); float part sums[lane] += (dx * dy) * lane,
@@ -550,6 +610,7 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     case TLQ_Q4_0: dot = tlq_vec_dot_q4_0_q8_0; break;
     case TLQ_Q8_0: dot = tlq_vec_dot_q8_0_q8_0; break;
     case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
+    case TLQ_Q5_K: dot = tlq_vec_dot_q5_K_q8_K; break;
     case TLQ_Q6_K: dot = tlq_vec_dot_q6_K_q8_K; break;
     default: return -1;
     }

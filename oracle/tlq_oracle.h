@@ -26,6 +26,7 @@ enum {
     TLQ_Q4_0 = 2,
     TLQ_Q8_0 = 8,
     TLQ_Q4_K = 12,
+    TLQ_Q5_K = 13,
     TLQ_Q6_K = 14,
     TLQ_Q8_K = 15,
 };
@@ -61,20 +62,23 @@ void tlq_quantize_row_q8_K(const float *x, void *y, int64_t k);
 int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k);
 
 // Dequantizers: dequantize_row_q4_0 ggml-quants.c:459-476, _q8_0 :553-565,
-// _q4_K :1529-1550; q8_K has no dequantizer on the path (d * q per element).
+// _q4_K :1529-1550, _q5_K :1731-1756, _q6_K :1939-1968; q8_K has no dequantizer on the path (d * q per element).
 void tlq_dequantize_row_q4_0(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q8_0(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q4_K(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q5_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q8_K(const void *x, float *y, int64_t k);
 int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
 
 // Dot products of one weight row with one quantized activation row:
 // ggml_vec_dot_q4_0_q8_0_generic ggml-cpu/quants.c:225-258,
-// _q8_0_q8_0_generic :451-476, _q4_K_q8_K_generic :696-773.
+// _q8_0_q8_0_generic :451-476, _q4_K_q8_K_generic :696-773,
+// _q5_K_q8_K_generic :771-850, _q6_K_q8_K_generic :851-904.
 float tlq_vec_dot_q4_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q8_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q5_K_q8_K(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *x, const void *y);
 
 // Exact integer parts of one block product (for pinning GPU partial sums):
@@ -125,7 +129,7 @@ int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[
 // (vendor/ggml/src/ggml-cpu/binary-ops.cpp, unary-ops.cpp, ops.cpp; each
 // function in tlq_oracle.c cites its lines). Tensors as ggml describes them:
 // data, ne[4], byte strides nb[4], type (f32, f16; i32 = 26 / i64 = 27 indices;
-// GET_ROWS / CPY sources also q4_0, q8_0, q4_K, q6_K).
+// GET_ROWS / CPY sources also q4_0, q8_0, q4_K, q5_K, q6_K).
 typedef struct tlq_t {
     void *data;
     int64_t ne[4], nb[4];

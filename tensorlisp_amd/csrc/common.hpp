@@ -11,18 +11,20 @@ namespace tlh {
 
 // ----------------------------------------------------------- block formats
 // vendor/ggml/src/ggml-common.h:194-198 (q4_0), :251-255 (q8_0), :325-337
-// (q4_K), :362-368 (q6_K), :370-375 (q8_K). Byte sizes per block and
+// (q4_K), :345-352 (q5_K), :362-368 (q6_K), :370-375 (q8_K). Byte sizes per
+// block and
 // elements per block.
 constexpr int QK = 32;    // q4_0 / q8_0 block
 constexpr int QKK = 256;  // k-quant super-block
 constexpr int Q4_0_BYTES = 18;
 constexpr int Q8_0_BYTES = 34;
 constexpr int Q4_K_BYTES = 144;
+constexpr int Q5_K_BYTES = 176;  // f16 d, dmin; scales[12] as q4_K; qh[32] (fifth bits); qs[128] (low nibbles)
 constexpr int Q6_K_BYTES = 210;  // ql[128] (low 4 bits), qh[64] (high 2 bits), int8 scales[16], f16 d
 constexpr int Q8_K_BYTES = 292;
 
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q6_K || t == TLH_TYPE_Q8_K) ? QKK
+    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K || t == TLH_TYPE_Q8_K) ? QKK
            : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0)                      ? QK
                                                                              : 1;
 }
@@ -30,6 +32,7 @@ __host__ __device__ constexpr int block_bytes(int t) {
     return t == TLH_TYPE_Q4_0   ? Q4_0_BYTES
            : t == TLH_TYPE_Q8_0 ? Q8_0_BYTES
            : t == TLH_TYPE_Q4_K ? Q4_K_BYTES
+           : t == TLH_TYPE_Q5_K ? Q5_K_BYTES
            : t == TLH_TYPE_Q6_K ? Q6_K_BYTES
            : t == TLH_TYPE_Q8_K ? Q8_K_BYTES
            : t == TLH_TYPE_F16  ? 2
@@ -37,7 +40,7 @@ __host__ __device__ constexpr int block_bytes(int t) {
 }
 // vec_dot_type on x86 (vendor/ggml/src/ggml-cpu/ggml-cpu.c:239-319).
 __host__ __device__ constexpr int vec_dot_type(int wtype) {
-    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
+    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
 }
 
 // ---------------------------------------------------------- conversions
@@ -64,7 +67,8 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
 // Element `col` of a row of ggml blocks of type WT, rounded as the reference's
 // dequantize_row_* rounds it (integer codes convert exactly): q4_0
 // (q-8)*d (ggml-quants.c:459-476), q8_0 q*d (:553-565), q4_K (d*sc)*q -
-// (dmin*m) (:1529-1550), q6_K (d*sc)*q (:1939-1968).
+// (dmin*m) (:1529-1550), q5_K the same with a fifth code bit (:1731-1756),
+// q6_K (d*sc)*q (:1939-1968).
 template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r, int64_t col) {
 #pragma clang fp contract(off)
     if constexpr (WT == TLH_TYPE_Q4_0) {
@@ -90,16 +94,19 @@ template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r
         const int sc = (int)(int8_t)b[192 + 8 * h + (e >> 4)];
         return (d * (float)sc) * (float)code;
     } else {
-        static_assert(WT == TLH_TYPE_Q4_K, "dequant_elem: type");
-        const uint8_t *b = r + (col / QKK) * Q4_K_BYTES;
+        static_assert(WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K, "dequant_elem: type");
+        constexpr bool Q5 = WT == TLH_TYPE_Q5_K;
+        const uint8_t *b = r + (col / QKK) * (Q5 ? Q5_K_BYTES : Q4_K_BYTES);
         const int i = (int)(col % QKK);
         const int c = i / 64, pos = i % 64, hi = pos >= 32, l = pos & 31;
-        const uint32_t *s = (const uint32_t *)(b + 4);
         int sc, mn;
+        uint32_t s[3];
+        __builtin_memcpy(s, b + 4, 12);
         q4k_scale_min(2 * c + hi, s[0], s[1], s[2], sc, mn);
         const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
-        const uint8_t byte = b[16 + 32 * c + l];
-        const int code = hi ? byte >> 4 : byte & 0x0f;
+        const uint8_t byte = b[(Q5 ? 48 : 16) + 32 * c + l];
+        int code = hi ? byte >> 4 : byte & 0x0f;
+        if constexpr (Q5) code |= ((b[16 + l] >> (2 * c + hi)) & 1) << 4;
         const float d1 = d * (float)sc;
         const float m1 = dmin * (float)mn;
         return d1 * (float)code - m1;

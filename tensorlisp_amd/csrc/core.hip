@@ -7,7 +7,7 @@
 // parameters the reference's lowering packs for its core kernels
 // (crates/kernels/src/cuda/lower.rs:219-500; kernels in
 // crates/kernels/src/cuda/native/core.cu). Element types: f32 and f16 data,
-// i32/i64 indices; GET_ROWS and CPY also read q4_0, q8_0, q4_K and q6_K rows.
+// i32/i64 indices; GET_ROWS and CPY also read q4_0, q8_0, q4_K, q5_K and q6_K rows.
 //
 // Layout on the GPU: rows of ne0 elements. Kernels that map one element per
 // thread walk a row per workgroup y-index (row -> i1, i2, i3 decomposed once)
@@ -630,6 +630,7 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;
         default: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
         }
         break;
@@ -651,6 +652,7 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;
         default: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
         }
         break;

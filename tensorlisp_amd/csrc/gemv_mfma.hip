@@ -88,6 +88,7 @@ __device__ __forceinline__ uint2 lds_u64(const uint32_t *base, uint32_t off) {
 // Bytes of one row per unit (the stride between units).
 template <int WT> constexpr int unit_bytes() {
     return WT == TLH_TYPE_Q4_K   ? Q4_K_BYTES
+           : WT == TLH_TYPE_Q5_K ? Q5_K_BYTES
            : WT == TLH_TYPE_Q6_K ? Q6_K_BYTES
            : WT == TLH_TYPE_Q4_0 ? 8 * Q4_0_BYTES
                                  : 8 * Q8_0_BYTES;
@@ -96,7 +97,7 @@ template <int WT> constexpr int unit_bytes() {
 // q6_K its first 208 (ql, qh, scales; d, the last 2 bytes, is loaded apart).
 template <int WT> constexpr int staged_bytes() { return WT == TLH_TYPE_Q6_K ? 208 : unit_bytes<WT>(); }
 // Types whose unit is one k-quant super-block (one activation scale slot).
-template <int WT> constexpr bool kquant() { return WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q6_K; }
+template <int WT> constexpr bool kquant() { return WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K || WT == TLH_TYPE_Q6_K; }
 
 // One lane's weight data of one unit in operand form: q4_K the super-block
 // header and bytes 8g..8g+7 of each 32-byte chunk; q8_0 / q4_0 per block the
@@ -116,6 +117,26 @@ template <> struct UnitW<TLH_TYPE_Q4_K> {
         hdr = *(const uint4 *)blk;
 #pragma unroll
         for (int c = 0; c < 4; ++c) q[c] = *(const uint2 *)(blk + 16 + 32 * c + 8 * g);
+    }
+};
+
+// q5_K: q4_K's header and lane bytes (nibbles at 48 + 32c + 8g) plus qh bytes
+// 16 + 8g, whose bit j is the fifth bit of those elements in sub-block j.
+template <> struct UnitW<TLH_TYPE_Q5_K> {
+    uint4 hdr;
+    uint2 q[4];
+    uint2 qh;
+    __device__ __forceinline__ void load(const uint8_t *blk, int g) {
+        hdr = ldu<uint4>(blk);
+        qh = ldu<uint2>(blk + 16 + 8 * g);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) q[c] = ldu<uint2>(blk + 48 + 32 * c + 8 * g);
+    }
+    __device__ __forceinline__ void load_lds(const uint8_t *blk, int g) {
+        hdr = *(const uint4 *)blk;
+        qh = *(const uint2 *)(blk + 16 + 8 * g);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) q[c] = *(const uint2 *)(blk + 48 + 32 * c + 8 * g);
     }
 };
 
@@ -227,7 +248,7 @@ template <int WT>
 __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8], const float *sdu, int g,
                                          int nvalid, float (&y)[4]) {
     const v4i zero = {0, 0, 0, 0};
-    if constexpr (WT == TLH_TYPE_Q4_K) {
+    if constexpr (WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K) {
         const uint4 h = w.hdr;
         // the 6-bit scales / mins of the 8 sub-blocks as bytes, sub-blocks
         // 0..3 and 4..7 (get_scale_min_k4, ggml-quants.c:880-887)
@@ -238,7 +259,12 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
         for (int j = 0; j < 8; ++j) {
             const uint2 qv = w.q[j >> 1];
             const int sh = (j & 1) ? 4 : 0;
-            const long B = pack2((qv.x >> sh) & 0x0f0f0f0fu, (qv.y >> sh) & 0x0f0f0f0fu);
+            uint32_t b0 = (qv.x >> sh) & 0x0f0f0f0fu, b1 = (qv.y >> sh) & 0x0f0f0f0fu;
+            if constexpr (WT == TLH_TYPE_Q5_K) {
+                b0 |= ((w.qh.x >> j) & 0x01010101u) << 4;
+                b1 |= ((w.qh.y >> j) & 0x01010101u) << 4;
+            }
+            const long B = pack2(b0, b1);
             const v4i Sj = mfma_i8(A[j], B, zero);
             const int s = (int)__builtin_amdgcn_ubfe(sc[j >> 2], 8 * (j & 3), 8);
             // m_j in all four bytes (byte j & 3 of the word, selected four times)
@@ -617,6 +643,7 @@ tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     case TLH_TYPE_Q4_0: return launch_sk_wt<TLH_TYPE_Q4_0>(a, staged, stream);
     case TLH_TYPE_Q8_0: return launch_sk_wt<TLH_TYPE_Q8_0>(a, staged, stream);
     case TLH_TYPE_Q4_K: return launch_sk_wt<TLH_TYPE_Q4_K>(a, staged, stream);
+    case TLH_TYPE_Q5_K: return launch_sk_wt<TLH_TYPE_Q5_K>(a, staged, stream);
     case TLH_TYPE_Q6_K: return launch_sk_wt<TLH_TYPE_Q6_K>(a, staged, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: weight type %d", a.wtype);
     }

@@ -280,6 +280,58 @@ template <int R> struct WRegs<TLH_TYPE_Q4_K, R> {
     }
 };
 
+// q5_K (vec_dot_q5_K_q8_K_generic, ggml-cpu/quants.c:771-850): q4_K's
+// header and nibbles (at byte 48 + 32j) plus the 32 qh bytes, whose bits 2j
+// and 2j + 1 are the fifth bits of the unit's two runs; codes 0..31.
+template <int R> struct WRegs<TLH_TYPE_Q5_K, R> {
+    uint4 hd[R], q0[R], q1[R], h0[R], h1[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+        const int64_t sb = u >> 2;
+        const int j = (int)(u & 3);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + sb * Q5_K_BYTES;
+            hd[r] = ldu16(blk);
+            h0[r] = ldu16(blk + 16);
+            h1[r] = ldu16(blk + 32);
+            q0[r] = ldu16(blk + 48 + 32 * j);
+            q1[r] = ldu16(blk + 64 + 32 * j);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t u, float (&acc)[R][NC]) const {
+        const int j = (int)(u & 3);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            const uint32_t h[8] = {h0[r].x, h0[r].y, h0[r].z, h0[r].w, h1[r].x, h1[r].y, h1[r].z, h1[r].w};
+            int lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                lo[i] = (int)((w[i] & 0x0f0f0f0fu) | (((h[i] >> (2 * j)) & 0x01010101u) << 4));
+                hi[i] = (int)(((w[i] >> 4) & 0x0f0f0f0fu) | (((h[i] >> (2 * j + 1)) & 0x01010101u) << 4));
+            }
+            int sclo, mnlo, schi, mnhi;
+            q4k_sm_r(2 * j, hd[r].y, hd[r].z, hd[r].w, sclo, mnlo);
+            q4k_sm_r(2 * j + 1, hd[r].y, hd[r].z, hd[r].w, schi, mnhi);
+            const float d = h2f((uint16_t)(hd[r].x & 0xffff));
+            const float dmin = h2f((uint16_t)(hd[r].x >> 16));
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    dl = dot4(lo[i], act[n].q[i], dl);
+                    dh = dot4(hi[i], act[n].q[8 + i], dh);
+                }
+                const int S = sclo * dl + schi * dh;
+                const int Mn = mnlo * act[n].s0 + mnhi * act[n].s1;
+                acc[r][n] += (d * act[n].d0) * (float)S - (dmin * act[n].d0) * (float)Mn;
+            }
+        }
+    }
+};
+
 // q6_K (vec_dot_q6_K_q8_K_generic, ggml-cpu/quants.c:851-904): the lane's 32
 // ql bytes (low nibbles: its first run, high nibbles: its second), the half's
 // 32 qh bytes (2-bit fields 2c and 4 + 2c), the 8 scales of the half and d.
@@ -586,7 +638,7 @@ template <int WT, int NC, bool FUSED>
 static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
                                 hipStream_t stream) {
     // q6_K holds 19 weight registers per row: two columns take 2 rows per wave
-    constexpr int R = (WT == TLH_TYPE_Q6_K && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
+    constexpr int R = ((WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q5_K) && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
     return launch_reg_cfg<WT, NC, R, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
 }
 
@@ -624,6 +676,9 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     case TLH_TYPE_Q4_K:
         return fused ? launch_reg_wt<TLH_TYPE_Q4_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
                      : launch_reg_wt<TLH_TYPE_Q4_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
+    case TLH_TYPE_Q5_K:
+        return fused ? launch_reg_wt<TLH_TYPE_Q5_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
+                     : launch_reg_wt<TLH_TYPE_Q5_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
     case TLH_TYPE_Q6_K:
         return fused ? launch_reg_wt<TLH_TYPE_Q6_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
                      : launch_reg_wt<TLH_TYPE_Q6_K, false>(a, x, x_row_bytes, ksplit, upw, stream);

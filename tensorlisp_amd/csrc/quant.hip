@@ -192,6 +192,9 @@ tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, i
     case TLH_TYPE_Q4_K:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
         break;
+    case TLH_TYPE_Q5_K:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q5_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
     case TLH_TYPE_Q6_K:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q6_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
         break;

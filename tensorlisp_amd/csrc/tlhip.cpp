@@ -44,7 +44,7 @@ static tlh_status hip_check(hipError_t e, const char *what) {
 }
 
 static bool weight_type_ok(int t) {
-    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q6_K;
+    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K;
 }
 
 static const char *type_name(int t) {
@@ -54,6 +54,7 @@ static const char *type_name(int t) {
     case TLH_TYPE_Q4_0: return "q4_0";
     case TLH_TYPE_Q8_0: return "q8_0";
     case TLH_TYPE_Q4_K: return "q4_K";
+    case TLH_TYPE_Q5_K: return "q5_K";
     case TLH_TYPE_Q6_K: return "q6_K";
     case TLH_TYPE_Q8_K: return "q8_K";
     default: return "?";
@@ -70,7 +71,7 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     if (!op) return set_error(TLH_INVALID, "mul_mat: null op");
     const tlh_tensor &a = op->t[0], &b = op->t[1], &d = op->t[4];
     if (!weight_type_ok(a.ty))
-        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q6_K", a.ty,
+        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K", a.ty,
                          type_name(a.ty));
     if (b.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: activations must be f32 (got type %d)", b.ty);
     if (d.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: the destination must be f32");
@@ -234,7 +235,7 @@ static tlh_status check_core(int kind, const tlh_op *op, bool has1, bool has2) {
         return TLH_OK;
     case TLH_CORE_GET_ROWS:
         if (!(a_data || rows_of_blocks(a)) || !idx_ty(b.ty) || !elem_strides_ok(b) || !d_data)
-            return unsup("GET_ROWS: f32/f16/q4_0/q8_0/q4_K/q6_K rows, i32/i64 indices, f32/f16 destination");
+            return unsup("GET_ROWS: f32/f16/q4_0/q8_0/q4_K/q5_K/q6_K rows, i32/i64 indices, f32/f16 destination");
         if (d.ne[0] != a.ne[0] || d.ne[1] != b.ne[0] || d.ne[2] != b.ne[1] || d.ne[3] != b.ne[2] ||
             a.ne[2] != b.ne[1] || a.ne[3] != b.ne[2] || (a.ne[1] == 0 && nel(d) > 0))
             return unsup("GET_ROWS: shapes");

@@ -75,7 +75,7 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
     """Structurally valid random blocks of a weight type, sized like weights
     quantized from N(0, std) (finite f16 scales, random codes). Used where
     quantizing full-size f32 weights on the host would dominate run time."""
-    from .native import Q4_0, Q8_0, Q4_K, Q6_K
+    from .native import Q4_0, Q8_0, Q4_K, Q5_K, Q6_K
 
     if wtype == Q8_0:
         return q8_0_config1(seed, M, K)
@@ -96,6 +96,15 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
         blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
         return blocks.reshape(M, (K // 256) * 144)
+    if wtype == Q5_K:
+        # q4_K's header statistics, random qh / qs bytes (codes 0..31)
+        nb = M * (K // 256)
+        d = f16_bits(np.abs(normal(seed + 1, (nb,), std)) / np.float32(63 * 8))
+        dmin = f16_bits(np.abs(normal(seed + 2, (nb,), std)) / np.float32(63 * 2))
+        blocks = bits(seed, nb * 22).view(np.uint8).reshape(nb, 176).copy()
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+        return blocks.reshape(M, (K // 256) * 176)
     if wtype == Q6_K:
         # random ql/qh bytes, int8 scales over the whole range the quantizer
         # emits (|scale| <= 127 plus -128), f16 d ~ |N(0, std)| / (32 * 127)

@@ -26,6 +26,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    mul_mat.npz), their dequantize_row_q6_K, and one
                    GGML_OP_MUL_MAT per n in 1,3,5,8,9,40; plus structurally
                    random q6_K blocks (synth seed 61) against x (seed 62)
+  q5_K.npz         the same for q5_K (random blocks: synth seed 71, x seed 72)
   flash_attn_ext.npz  GGML_OP_FLASH_ATTN_EXT with masks, GQA, batch, soft cap and
                    ALiBi on the shapes of the reference's attention tests
                    (refs.FA_CASES, native.rs:156-345), 8 CPU threads, outputs of the
@@ -45,7 +46,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    single-token steps, a 3-token chunk): logits and argmax per
                    step and the f16 KV caches after the last one
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | core | decoder]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -59,7 +60,7 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import (FA_CASES, Q4_0, Q4_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
+from refs import (FA_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
                   decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
 
@@ -107,21 +108,29 @@ def flash_attn_ext_golden(ref) -> None:
     np.savez_compressed(HERE / "flash_attn_ext.npz", **out)
 
 
-def q6_K_golden(ref) -> None:
+def kquant_golden(ref, t: int, name: str, wseed: int, xseed: int) -> None:
     rows, k = 96, 256
     wn = xorshift_noise((rows, k), 1)
     ns = [1, 3, 5, 8, 9, 40]
-    q = ref.quantize_weights(Q6_K, wn)
-    out = {"w": q, "deq": ref.dequantize(Q6_K, q, k), "ns": np.array(ns)}
+    q = ref.quantize_weights(t, wn)
+    out = {"w": q, "deq": ref.dequantize(t, q, k), "ns": np.array(ns)}
     for n in ns:
-        y, _ = ref.mul_mat(Q6_K, q, rows, k, xorshift_noise((n, k), 10 + n))
+        y, _ = ref.mul_mat(t, q, rows, k, xorshift_noise((n, k), 10 + n))
         out[f"y{n}"] = y
     M, K = 40, 1024
-    wr = synth.random_blocks(Q6_K, 61, M, K)
-    xr = synth.normal(62, (3, K))
-    y, _ = ref.mul_mat(Q6_K, wr, M, K, xr)
-    out.update({"rand_w": wr, "rand_y": y, "rand_deq": ref.dequantize(Q6_K, wr, K)})
-    np.savez_compressed(HERE / "q6_K.npz", **out)
+    wr = synth.random_blocks(t, wseed, M, K)
+    xr = synth.normal(xseed, (3, K))
+    y, _ = ref.mul_mat(t, wr, M, K, xr)
+    out.update({"rand_w": wr, "rand_y": y, "rand_deq": ref.dequantize(t, wr, K)})
+    np.savez_compressed(HERE / f"{name}.npz", **out)
+
+
+def q6_K_golden(ref) -> None:
+    kquant_golden(ref, Q6_K, "q6_K", 61, 62)
+
+
+def q5_K_golden(ref) -> None:
+    kquant_golden(ref, Q5_K, "q5_K", 71, 72)
 
 
 def core_golden(ref) -> None:
@@ -150,6 +159,9 @@ def main() -> None:
         return
     if sys.argv[1:] == ["q6_K"]:  # only the q6_K fixture
         q6_K_golden(ref)
+        return
+    if sys.argv[1:] == ["q5_K"]:  # only the q5_K fixture
+        q5_K_golden(ref)
         return
     # ---------------------------------------------------------------- fp16
     halves = np.arange(65536, dtype=np.uint16)
@@ -211,6 +223,7 @@ def main() -> None:
     np.savez_compressed(HERE / "flash_attn.npz", **out)
     flash_attn_ext_golden(ref)
     q6_K_golden(ref)
+    q5_K_golden(ref)
     core_golden(ref)
     decoder_golden(ref)
     for p in sorted(HERE.glob("*.npz")):

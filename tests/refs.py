@@ -22,10 +22,10 @@ ORACLE_SO = ROOT / "oracle" / "liboracle.so"
 REF_SO = ROOT / "oracle" / "_ref" / "libggml_ref.so"
 
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 14, 15
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292)}
-VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q6_K: Q8_K}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q6_K: "q6_K", Q8_K: "q8_K"}
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
 
 
 def row_bytes(t: int, k: int) -> int:
@@ -99,11 +99,12 @@ class Oracle:
         vp, i64 = C.c_void_p, C.c_int64
         for name in ("tlq_quantize_row_q4_0", "tlq_quantize_row_q4_K", "tlq_quantize_row_q8_0",
                      "tlq_quantize_row_q8_K", "tlq_dequantize_row_q4_0", "tlq_dequantize_row_q8_0",
-                     "tlq_dequantize_row_q4_K", "tlq_dequantize_row_q6_K", "tlq_dequantize_row_q8_K"):
+                     "tlq_dequantize_row_q4_K", "tlq_dequantize_row_q5_K", "tlq_dequantize_row_q6_K",
+                     "tlq_dequantize_row_q8_K"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("tlq_vec_dot_q4_0_q8_0", "tlq_vec_dot_q8_0_q8_0", "tlq_vec_dot_q4_K_q8_K",
-                     "tlq_vec_dot_q6_K_q8_K"):
+                     "tlq_vec_dot_q5_K_q8_K", "tlq_vec_dot_q6_K_q8_K"):
             getattr(L, name).argtypes = [i64, vp, vp]
             getattr(L, name).restype = C.c_float
         L.tlq_fp16_to_fp32_row.argtypes = [vp, vp, i64]
@@ -163,7 +164,8 @@ class Oracle:
         rows = q.size // row_bytes(t, k)
         out = np.empty((rows, k), np.float32)
         fn = {Q4_0: self.lib.tlq_dequantize_row_q4_0, Q8_0: self.lib.tlq_dequantize_row_q8_0,
-              Q4_K: self.lib.tlq_dequantize_row_q4_K, Q6_K: self.lib.tlq_dequantize_row_q6_K,
+              Q4_K: self.lib.tlq_dequantize_row_q4_K, Q5_K: self.lib.tlq_dequantize_row_q5_K,
+              Q6_K: self.lib.tlq_dequantize_row_q6_K,
               Q8_K: self.lib.tlq_dequantize_row_q8_K}[t]
         fn(_p(q), _p(out), rows * k)
         return out
@@ -172,7 +174,8 @@ class Oracle:
         xrow = np.ascontiguousarray(xrow, dtype=np.uint8)
         yrow = np.ascontiguousarray(yrow, dtype=np.uint8)
         fn = {Q4_0: self.lib.tlq_vec_dot_q4_0_q8_0, Q8_0: self.lib.tlq_vec_dot_q8_0_q8_0,
-              Q4_K: self.lib.tlq_vec_dot_q4_K_q8_K, Q6_K: self.lib.tlq_vec_dot_q6_K_q8_K}[wtype]
+              Q4_K: self.lib.tlq_vec_dot_q4_K_q8_K, Q5_K: self.lib.tlq_vec_dot_q5_K_q8_K,
+              Q6_K: self.lib.tlq_vec_dot_q6_K_q8_K}[wtype]
         return float(fn(k, _p(xrow), _p(yrow)))
 
     def block_ints_q4_K(self, xblock, yblock):
@@ -318,11 +321,11 @@ class Ref:
         vp, i64 = C.c_void_p, C.c_int64
         for name in ("quantize_row_q8_0", "quantize_row_q8_K", "quantize_row_q8_0_ref", "quantize_row_q8_K_ref",
                      "quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "dequantize_row_q4_0",
-                     "dequantize_row_q8_0", "dequantize_row_q4_K", "dequantize_row_q6_K"):
+                     "dequantize_row_q8_0", "dequantize_row_q4_K", "dequantize_row_q5_K", "dequantize_row_q6_K"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("ggml_vec_dot_q4_0_q8_0", "ggml_vec_dot_q8_0_q8_0", "ggml_vec_dot_q4_K_q8_K",
-                     "ggml_vec_dot_q6_K_q8_K"):
+                     "ggml_vec_dot_q5_K_q8_K", "ggml_vec_dot_q6_K_q8_K"):
             getattr(L, name).argtypes = [C.c_int, C.POINTER(C.c_float), C.c_size_t, vp, C.c_size_t, vp, C.c_size_t,
                                          C.c_int]
             getattr(L, name).restype = None
@@ -390,7 +393,8 @@ class Ref:
         rows = q.size // row_bytes(t, k)
         out = np.empty((rows, k), np.float32)
         fn = {Q4_0: self.lib.dequantize_row_q4_0, Q8_0: self.lib.dequantize_row_q8_0,
-              Q4_K: self.lib.dequantize_row_q4_K, Q6_K: self.lib.dequantize_row_q6_K}[t]
+              Q4_K: self.lib.dequantize_row_q4_K, Q5_K: self.lib.dequantize_row_q5_K,
+              Q6_K: self.lib.dequantize_row_q6_K}[t]
         fn(_p(q), _p(out), rows * k)
         return out
 
@@ -399,7 +403,8 @@ class Ref:
         yrow = np.ascontiguousarray(yrow, dtype=np.uint8)
         s = C.c_float()
         fn = {Q4_0: self.lib.ggml_vec_dot_q4_0_q8_0, Q8_0: self.lib.ggml_vec_dot_q8_0_q8_0,
-              Q4_K: self.lib.ggml_vec_dot_q4_K_q8_K, Q6_K: self.lib.ggml_vec_dot_q6_K_q8_K}[wtype]
+              Q4_K: self.lib.ggml_vec_dot_q4_K_q8_K, Q5_K: self.lib.ggml_vec_dot_q5_K_q8_K,
+              Q6_K: self.lib.ggml_vec_dot_q6_K_q8_K}[wtype]
         fn(k, C.byref(s), 0, _p(xrow), 0, _p(yrow), 0, 1)
         return float(s.value)
 
@@ -873,7 +878,7 @@ def core_cases():
     return cases
 
 
-TYPE_SUFFIX = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q6_K: "q6_K"}
+TYPE_SUFFIX = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K"}
 
 
 def core_ref(r, case) -> np.ndarray:

@@ -88,9 +88,9 @@ def test_mul_mat_scratch_has_mfma_partials_for_long_K(wt, n, K, parts):
 
 def test_mul_mat_unsupported_weight_type_is_named():
     op = N.mul_mat_op(N.Q4_0, 64, 256, 1)
-    op.t[0].ty = 13  # q5_K
+    op.t[0].ty = 11  # q3_K
     st, msg, _ = scratch_status(op)
-    assert st == "UNSUPPORTED" and "type 13" in msg
+    assert st == "UNSUPPORTED" and "type 11" in msg
 
 
 def test_mul_mat_rejects_bad_shapes_and_layouts():
@@ -121,7 +121,7 @@ def test_mul_mat_null_pointers_are_invalid_not_crashes():
 
 def test_quantize_and_dequantize_validation():
     L = N.lib()
-    st, msg = _status(L.tlh_quantize_act, 13, None, 256, 1, 1024, None, None)  # q5_K
+    st, msg = _status(L.tlh_quantize_act, 11, None, 256, 1, 1024, None, None)  # q3_K
     assert st == "UNSUPPORTED"
     st, msg = _status(L.tlh_quantize_act, N.Q4_K, None, 300, 1, 1200, None, None)
     assert st == "INVALID" and "multiple" in msg
@@ -277,7 +277,7 @@ def test_core_validation():
         (N.CORE_BIN, [f32(64, 5), f32(64, 5)], f32(64, 5), (4,), "INVALID", "BIN code"),
         (N.CORE_UNARY, [f32(9, 2)], f32(9, 2), (17,), "UNSUPPORTED", "unary op 17"),
         (N.CORE_NORM, [f16(64, 2)], f32(64, 2), (1,), "UNSUPPORTED", "NORM"),
-        (N.CORE_GET_ROWS, [N.ggml_tensor(13, [512, 40], [176, 352, 14080, 14080]), i32(7)], f32(512, 7), (),
+        (N.CORE_GET_ROWS, [N.ggml_tensor(11, [512, 40], [110, 220, 8800, 8800]), i32(7)], f32(512, 7), (),
          "UNSUPPORTED", "GET_ROWS"),
         (N.CORE_GET_ROWS, [f32(512, 40), i32(7)], f32(512, 6), (), "UNSUPPORTED", "shapes"),
         (N.CORE_SET_ROWS, [f32(512, 5), i32(4)], f32(512, 64), (), "UNSUPPORTED", "shapes"),

@@ -136,7 +136,7 @@ def test_unsupported_ops_are_reported_by_name():
     with pytest.raises(N.TlhError, match=r"IM2COL x2 .*POOL_2D x1"):
         G.plan(b, [z])
     b = G.Builder()
-    w = b._new(13, [256, 8], nb=[176, 176, 1408, 1408], storage=G.STORE_WEIGHT, index=0)  # q5_K: not taken
+    w = b._new(11, [256, 8], nb=[110, 110, 880, 880], storage=G.STORE_WEIGHT, index=0)  # q3_K: not taken
     x = b.input(N.F32, [256, 1])
     b.expand(b.mul_mat(w, x))
     with pytest.raises(N.TlhError, match="MUL_MAT x1"):

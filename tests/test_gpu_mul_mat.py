@@ -12,14 +12,14 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, oracle
+from refs import NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, oracle
 from tensorlisp_amd import native as N
 from tensorlisp_amd import synth
 
 pytestmark = pytest.mark.gpu
 GOLD = Path(__file__).resolve().parent / "golden"
 RTOL, ATOL = 1e-3, 1e-4
-WTYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
+WTYPES = (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)
 GOLD_TYPES = (Q4_0, Q8_0, Q4_K)  # mul_mat.npz; q6_K has q6_K.npz
 
 
@@ -52,18 +52,34 @@ def test_reference_cases_golden(gpu, t):
         close(y, g[f"{NAMES[t]}_y{n}"], f"{NAMES[t]} n={n}")
 
 
-def test_q6_K_reference_cases_golden(gpu):
-    """q6_K weights from ggml_quantize_chunk on the reference test's 96 x 256 matrix
-    and structurally random q6_K blocks: the CPU backend's outputs (q6_K.npz)."""
+@pytest.mark.parametrize("t,xseed", [(Q6_K, 62), (Q5_K, 72)], ids=["q6_K", "q5_K"])
+def test_kquant_reference_cases_golden(gpu, t, xseed):
+    """q6_K / q5_K weights from ggml_quantize_chunk on the reference test's 96 x 256
+    matrix and structurally random blocks: the CPU backend's outputs (q6_K.npz,
+    q5_K.npz)."""
     from refs import xorshift_noise
 
-    g = np.load(GOLD / "q6_K.npz")
+    g = np.load(GOLD / f"{NAMES[t]}.npz")
     w = dev(g["w"])
     for n in g["ns"]:
-        y = host(N.mul_mat(Q6_K, w, 96, 256, dev(xorshift_noise((int(n), 256), 10 + int(n)))))
-        close(y, g[f"y{n}"], f"q6_K n={n}")
-    y = host(N.mul_mat(Q6_K, dev(g["rand_w"]), 40, 1024, dev(synth.normal(62, (3, 1024)))))
-    close(y, g["rand_y"], "q6_K random blocks")
+        y = host(N.mul_mat(t, w, 96, 256, dev(xorshift_noise((int(n), 256), 10 + int(n)))))
+        close(y, g[f"y{n}"], f"{NAMES[t]} n={n}")
+    y = host(N.mul_mat(t, dev(g["rand_w"]), 40, 1024, dev(synth.normal(xseed, (3, 1024)))))
+    close(y, g["rand_y"], f"{NAMES[t]} random blocks")
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 40])
+@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 14336)], ids=["up", "down"])
+def test_q5_K_ffn_row_sample(gpu, n, M, K):
+    """q5_K FFN matrices of a Q5_K_M 8B model: register GEMV (n <= 2), MFMA
+    few-column kernel (n = 5, 16; K = 14336 in K chunks) and 16-column slabs
+    (n = 40), checked by the oracle on 64 rows spread over M."""
+    w = synth.random_blocks(Q5_K, 700 + n + K, M, K)
+    x = synth.normal(701 + n, (n, K))
+    y = host(N.mul_mat(Q5_K, dev(w), M, K, dev(x)))
+    rows = np.unique(synth.integers(702 + n, 0, M - 1, 64))
+    want = oracle().mul_mat(Q5_K, w[rows], len(rows), K, x, nthreads=16)
+    close(y[:, rows], want, f"q5_K {M}x{K} n={n}")
 
 
 @pytest.mark.parametrize("n", [1, 2, 8, 40])
@@ -196,8 +212,8 @@ def test_repeated_launches_are_deterministic(gpu):
     assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
 
 
-@pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 8224), (Q6_K, 16640)],
-                         ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K8224", "q6_K-K16640"])
+@pytest.mark.parametrize("t,K", [(Q8_0, 96), (Q4_0, 160), (Q4_K, 16640), (Q8_0, 8224), (Q6_K, 16640), (Q5_K, 16640)],
+                         ids=["q8_0-K96", "q4_0-K160", "q4_K-K16640", "q8_0-K8224", "q6_K-K16640", "q5_K-K16640"])
 @pytest.mark.parametrize("n", [1, 2, 5, 8])
 def test_other_K_shapes(gpu, t, K, n):
     """K outside the register-resident GEMV (K % 64 != 0 or K > 16384), so every N runs on

@@ -7,7 +7,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, oracle
+from refs import NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, oracle
 from tensorlisp_amd import native as N
 from tensorlisp_amd import synth
 
@@ -65,15 +65,16 @@ def test_dequantize_golden(gpu, t):
     assert np.array_equal(got.view(np.uint32), g[f"{NAMES[t]}_deq"].view(np.uint32))
 
 
-def test_dequantize_q6_K_golden(gpu):
-    """dequantize_row_q6_K of the compiled reference (q6_K.npz), bit-exact."""
-    g = np.load(GOLD / "q6_K.npz")
+@pytest.mark.parametrize("t", [Q6_K, Q5_K], ids=["q6_K", "q5_K"])
+def test_dequantize_kquant_golden(gpu, t):
+    """dequantize_row_q6_K / _q5_K of the compiled reference (q6_K.npz, q5_K.npz), bit-exact."""
+    g = np.load(GOLD / f"{NAMES[t]}.npz")
     for key, deq, k in (("w", "deq", 256), ("rand_w", "rand_deq", 1024)):
-        got = host(N.dequantize(Q6_K, dev(g[key]), k))
+        got = host(N.dequantize(t, dev(g[key]), k))
         assert np.array_equal(got.view(np.uint32), g[deq].view(np.uint32)), key
 
 
-@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q6_K], ids=[NAMES[t] for t in (Q4_0, Q8_0, Q4_K, Q6_K)])
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q5_K, Q6_K], ids=[NAMES[t] for t in (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)])
 def test_dequantize_random_blocks(gpu, t):
     """Every code and scale pattern (random bytes, subnormal f16 scales) bit-exact."""
     M, K = 257, 2048

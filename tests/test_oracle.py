@@ -18,7 +18,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
+from refs import NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
 from tensorlisp_amd import synth
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -294,6 +294,76 @@ def test_q6_K_matches_reference_live():
         assert same_bits(o.mul_mat(Q6_K, w, M, K, x), y)
         y, _ = r.mul_mat(Q6_K, wq, 8, K, x)
         assert same_bits(o.mul_mat(Q6_K, wq, 8, K, x), y)
+
+
+# ------------------------------------------------------------------ q5_K
+# tlq_dequantize_row_q5_K (ggml-quants.c:1731-1756) and tlq_vec_dot_q5_K_q8_K
+# (ggml-cpu/quants.c:771-850): pinned by the compiled reference's outputs
+# (q5_K.npz), bit-exact; an independent numpy unpacking of the codes and the
+# 6-bit scale/min field; float64 brute force; the live reference.
+def test_q5_K_golden_dequantize_and_mul_mat():
+    o, g = oracle(), gold("q5_K")
+    assert same_bits(o.dequantize(Q5_K, g["w"], 256), g["deq"])
+    assert same_bits(o.dequantize(Q5_K, g["rand_w"], 1024), g["rand_deq"])
+    from refs import xorshift_noise
+
+    for n in g["ns"]:
+        y = o.mul_mat(Q5_K, g["w"], 96, 256, xorshift_noise((int(n), 256), 10 + int(n)))
+        assert same_bits(y, g[f"y{n}"]), n
+    assert same_bits(o.mul_mat(Q5_K, g["rand_w"], 40, 1024, synth.normal(72, (3, 1024))), g["rand_y"])
+
+
+def test_q5_K_codes_against_an_independent_unpacking():
+    """y = (d * sc) * code - dmin * m in f32, with code = nibble | fifth bit << 4 and
+    the 6-bit sc / m rebuilt here over whole arrays (the block layout of
+    ggml-common.h:345-352), bit-exact."""
+    o = oracle()
+    w = synth.random_blocks(Q5_K, 92, 6, 512).reshape(-1, 176)
+    d = w[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = w[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    s = w[:, 4:16].astype(np.int64)
+    sc = np.concatenate([s[:, 0:4] & 63, (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)], axis=1)
+    mn = np.concatenate([s[:, 4:8] & 63, (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)], axis=1)
+    qh, qs = w[:, 16:48].astype(np.int64), w[:, 48:176].astype(np.int64)
+    codes = np.zeros((w.shape[0], 256), np.int64)
+    for sb in range(8):
+        byte = qs[:, 32 * (sb // 2): 32 * (sb // 2) + 32]
+        nib = (byte >> 4) if sb & 1 else (byte & 15)
+        codes[:, 32 * sb: 32 * sb + 32] = nib | (((qh >> sb) & 1) << 4)
+    d1 = np.repeat(d[:, None] * sc.astype(np.float32), 32, axis=1)
+    m1 = np.repeat(dmin[:, None] * mn.astype(np.float32), 32, axis=1)
+    want = (d1 * codes.astype(np.float32) - m1).astype(np.float32)
+    assert codes.max() == 31 and codes.min() == 0
+    assert same_bits(o.dequantize(Q5_K, w, 256), want)
+
+
+def test_q5_K_vec_dot_against_f64_bruteforce():
+    o = oracle()
+    K = 2048
+    w = synth.random_blocks(Q5_K, 93, 8, K)
+    x = synth.normal(94, (4, K))
+    xq = o.quantize_act(Q5_K, x)
+    wd = o.dequantize(Q5_K, w, K).astype(np.float64)
+    xd = o.dequantize(Q8_K, xq, K).astype(np.float64)
+    want = wd @ xd.T
+    got = np.array([[o.vec_dot(Q5_K, K, w[i], xq[j]) for j in range(4)] for i in range(8)])
+    scale = np.abs(wd).sum(1)[:, None] * np.abs(xd).max()
+    assert np.all(np.abs(got - want) <= 1e-6 * scale)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+def test_q5_K_matches_reference_live():
+    o, r = oracle(), ref()
+    M, K = 120, 2048
+    w = synth.random_blocks(Q5_K, 95, M, K)
+    assert same_bits(o.dequantize(Q5_K, w, K), r.dequantize(Q5_K, w, K))
+    wq = r.quantize_weights(Q5_K, synth.normal(96, (8, K), 0.02))
+    for n in (1, 2, 9):
+        x = synth.normal(97 + n, (n, K))
+        y, _ = r.mul_mat(Q5_K, w, M, K, x)
+        assert same_bits(o.mul_mat(Q5_K, w, M, K, x), y)
+        y, _ = r.mul_mat(Q5_K, wq, 8, K, x)
+        assert same_bits(o.mul_mat(Q5_K, wq, 8, K, x), y)
 
 
 # -------------------------------------------------------- paged attention
