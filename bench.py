@@ -156,7 +156,102 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
     log(f"  e2e 8B q4_K: prefill {T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} tok/s); decode "
         f"{graph_ms:.3f} ms/tok graph, {eager_ms:.3f} eager -> {out['decode_tokens_per_s']} tok/s, "
         f"{out['decode_gbs']} GB/s")
-    del P, D, W, state
+    del P, D, state
+    out["paged_batch16"] = e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_tokens,
+                                             decode_steps)
+    del W
+    torch.cuda.empty_cache()
+    return out
+
+
+def e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_tokens=512, decode_steps=256,
+                      batch=16, block_size=16):
+    """configs[4] at batch 16 with the paged KV cache: each sequence's 512-token
+    prompt runs alone (keys and values into the pools through paged-cache-write,
+    attention over the prompt with FLASH_ATTN_EXT), then all 16 sequences decode
+    together, one token each per step, through the paged-attention node; each
+    step's next tokens are the previous step's argmax, copied on the device.
+    Blocks of a sequence are a random draw from the pool."""
+    import numpy as np
+
+    from tensorlisp_amd import graph as G
+
+    S, T, steps = batch, prefill_tokens, decode_steps
+    per_seq = (T + steps + block_size - 1) // block_size
+    pc = G.PagedConfig(block_size=block_size, n_blocks=S * per_seq, max_blocks=per_seq)
+    offs, total = pc.state_bytes(c)
+    state = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    rng = np.random.default_rng(4)
+    tables = rng.permutation(pc.n_blocks).astype(np.int32).reshape(S, per_seq)
+
+    pre = G.decoder_prefill_paged(c, pc, T)
+    P = G.Program(pre.builder, pre.keep, W, offs)
+    pos = np.arange(T, dtype=np.int32)
+    mask = torch.from_numpy(G.causal_mask(pos, T).view(np.int16)).cuda()
+    toks = torch.randint(0, c.n_vocab, (S, T), device="cuda", generator=gen, dtype=torch.int32)
+    first = torch.empty(S, dtype=torch.int32, device="cuda")
+    slots = [torch.from_numpy(G.paged_slots(tables[s], pos, block_size)).cuda() for s in range(S)]
+    pin = [P.input(i)[0] for i in range(4)]
+    am_pre = P.tensor_ptr(pre.argmax, state)
+    with torch.cuda.stream(stream):
+        P.write_input(1, torch.from_numpy(pos).cuda(), stream)
+        P.write_input(3, mask, stream)
+
+    def prefill_all(graph):
+        for s in range(S):
+            copy(pin[0], toks[s].data_ptr(), 4 * T)
+            copy(pin[2], slots[s].data_ptr(), 8 * T)
+            P.run(state, stream, graph)
+            copy(first.data_ptr() + 4 * s, am_pre, 4)
+
+    prefill_all(True)  # capture and warm
+    stream.synchronize()
+    t0 = time.perf_counter()
+    prefill_all(True)
+    stream.synchronize()
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+
+    dec = G.decoder_decode_paged(c, pc, S)
+    D = G.Program(dec.builder, dec.keep, W, offs)
+    dpos = T + np.arange(steps, dtype=np.int32)[:, None] + np.zeros((1, S), np.int32)
+    dslots = np.stack([np.concatenate([G.paged_slots(tables[s], [p], block_size) for s, p in enumerate(row)])
+                       for row in dpos])
+    dpos_d, dlens_d = torch.from_numpy(dpos).cuda(), torch.from_numpy(dpos + 1).cuda()
+    dslots_d = torch.from_numpy(np.ascontiguousarray(dslots)).cuda()
+    din = [D.input(i)[0] for i in range(5)]
+    am_dec = D.tensor_ptr(dec.argmax, state)
+    with torch.cuda.stream(stream):
+        D.write_input(3, torch.from_numpy(tables).cuda(), stream)
+
+    def run_decode(n, graph):
+        copy(din[0], first.data_ptr(), 4 * S)
+        for i in range(n):
+            copy(din[1], dpos_d.data_ptr() + 4 * S * i, 4 * S)
+            copy(din[2], dslots_d.data_ptr() + 8 * S * i, 8 * S)
+            copy(din[4], dlens_d.data_ptr() + 4 * S * i, 4 * S)
+            D.run(state, stream, graph)
+            copy(din[0], am_dec, 4 * S)
+
+    run_decode(4, True)  # capture and warm (rewrites rows T..T+3, rewritten again below)
+    stream.synchronize()
+    t0 = time.perf_counter()
+    run_decode(steps, True)
+    stream.synchronize()
+    step_ms = (time.perf_counter() - t0) / steps * 1e3
+    # bytes a step reads: the weights once, every sequence's keys and values
+    kv_rows = S * (T + (steps - 1) / 2 + 1)
+    step_bytes = weight_bytes - W[0].numel() + S * c.n_embd * 2 + 2 * c.n_layer * kv_rows * c.n_embd_kv * 2
+    out = {
+        "batch": S, "kv_cache": f"paged, block size {block_size}, {pc.n_blocks} blocks per layer drawn at random",
+        "prefill_tokens_per_seq": T, "decode_steps": steps,
+        "prefill_ms_all_seqs": round(prefill_ms, 1), "prefill_tokens_per_s": round(S * T / prefill_ms * 1e3, 1),
+        "decode_ms_per_step_hipgraph": round(step_ms, 4), "decode_tokens_per_s": round(S / step_ms * 1e3, 1),
+        "decode_gbs": round(step_bytes / step_ms / 1e6, 1),
+        "dispatches_per_decode_step": D.stats()["launches"],
+    }
+    log(f"  e2e 8B q4_K batch {S} paged: prefill {S}x{T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} "
+        f"tok/s); decode {step_ms:.3f} ms/step -> {out['decode_tokens_per_s']} tok/s, {out['decode_gbs']} GB/s")
+    del P, D, state
     torch.cuda.empty_cache()
     return out
 

@@ -40,7 +40,7 @@ typedef enum tlh_status {
     TLH_EXECUTION = 5
 } tlh_status;
 
-/* ggml type numbers (vendor/ggml/include/ggml.h:390-405). */
+/* ggml type numbers (vendor/ggml/include/ggml.h:390-417). */
 enum {
     TLH_TYPE_F32 = 0,
     TLH_TYPE_F16 = 1,
@@ -49,7 +49,9 @@ enum {
     TLH_TYPE_Q4_K = 12,
     TLH_TYPE_Q5_K = 13,
     TLH_TYPE_Q6_K = 14,
-    TLH_TYPE_Q8_K = 15
+    TLH_TYPE_Q8_K = 15,
+    TLH_TYPE_I32 = 26,
+    TLH_TYPE_I64 = 27
 };
 
 /* Thread-local text of the last failure on this thread ("" if none). */

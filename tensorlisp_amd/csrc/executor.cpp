@@ -32,12 +32,13 @@ struct Place {
 };
 
 enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
-                    D_ARGMAX_SPLIT, D_CORE_MULTI };
+                    D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE };
+constexpr int NSRC = 5;  // sources a dispatch reads (the paged nodes have five)
 struct Dispatch {
     DispatchKind kind;
     int core_kind = 0;
     tlh_op op;
-    Place src[4];
+    Place src[NSRC];
     Place dst;
     int pos = 0;            // node position (the first one, for fused nodes)
     int pos_last = 0;       // last node position a fused dispatch covers
@@ -52,6 +53,10 @@ struct Dispatch {
     int sub_kind[4];
     tlh_op sop[4];
     Place ssrc[4][4], sdst[4];
+    // D_PAGED_ATTN: geometry and scale (pointers are set per launch);
+    // D_PAGED_WRITE: tokens, kv heads, head size, block size
+    tlh_paged_attention_args pa{};
+    int32_t pw[4] = {0, 0, 0, 0};
 };
 
 // ggml type traits used for byte sizes: (block elements, block bytes)
@@ -238,6 +243,78 @@ class Lowering {
         return true;
     }
 
+    // A ggml CUSTOM node without a function names a paged-attention kernel in
+    // its userdata (op_params[4..5] as one u64, low to high bits: kind 4,
+    // kv heads 4, block size 8, max context 16, scale f32), as Ctx::custom
+    // decodes it (crates/kernels/src/cuda/lower.rs:660-753):
+    //  kind 1: paged attention, sources q f16 [hs, heads, seqs] (contiguous),
+    //          key pool, value pool (f16), block tables i32 [max_blocks, seqs],
+    //          context lengths i32 [seqs]; the node is f16 [hs, heads, seqs];
+    //  kind 2: cache write, sources key and value f16 [hs * kv_heads, tokens]
+    //          (contiguous rows), the two pools, slots (one i64 per token, as
+    //          two i32); the node is a dummy.
+    bool custom(int pos, int32_t id, std::vector<Dispatch> &out, std::string &why) {
+        const tlh_ir_tensor &t = g_.t[id];
+        const uint64_t ud = (uint64_t)(uint32_t)t.op_params[4] | (uint64_t)(uint32_t)t.op_params[5] << 32;
+        const int kind = (int)(ud & 15), kvh = (int)((ud >> 4) & 15), bs = (int)((ud >> 8) & 255),
+                  max_ctx = (int)((ud >> 16) & 0xffff);
+        const float scale = f32_of((int32_t)(uint32_t)(ud >> 32));
+        for (int i = 0; i < 5; ++i)
+            if (t.src[i] < 0) return why = "a paged node takes five sources", false;
+        auto T = [&](int i) -> const tlh_ir_tensor & { return g_.t[t.src[i]]; };
+        auto is_f16 = [](const tlh_ir_tensor &x) { return x.ty == TLH_TYPE_F16; };
+        Dispatch d = base(pos, id, {0, 1, 2, 3});
+        d.src[4] = place_of(t.src[4]);
+        if (kind == 1) {
+            const tlh_ir_tensor &q = T(0);
+            if (!(is_f16(q) && is_f16(T(1)) && is_f16(T(2)) && is_f16(t)))
+                return why = "paged attention takes f16 q, caches and output", false;
+            if (q.nb[0] != 2 || q.nb[1] != q.ne[0] * 2 || q.nb[2] != q.ne[0] * q.ne[1] * 2 || t.ne[0] != q.ne[0] ||
+                t.ne[1] != q.ne[1] || t.ne[2] != q.ne[2] || t.nb[1] != t.ne[0] * 2 || t.nb[2] != t.ne[0] * t.ne[1] * 2)
+                return why = "paged attention takes a contiguous q and an output of its shape", false;
+            if (T(3).ty != TLH_TYPE_I32 || T(4).ty != TLH_TYPE_I32 || T(3).ne[1] < q.ne[2] || T(4).ne[0] < q.ne[2])
+                return why = "paged attention takes i32 block tables [max_blocks, seqs] and lengths [seqs]", false;
+            tlh_paged_attention_args &a = d.pa;
+            a.num_seqs = (int32_t)q.ne[2];
+            a.num_heads = (int32_t)q.ne[1];
+            a.num_kv_heads = kvh;
+            a.head_size = (int32_t)q.ne[0];
+            a.block_size = bs;
+            a.max_blocks_per_seq = (int32_t)T(3).ne[0];
+            a.max_context_len = max_ctx;
+            a.scale = scale;
+            const int64_t pool = (int64_t)kvh * a.head_size * bs * 2;  // bytes per block of each pool
+            if (kvh < 1 || nbytes(T(1)) < pool || nbytes(T(2)) < pool || nbytes(T(1)) % pool || nbytes(T(2)) % pool)
+                return why = "paged attention: pools are not whole blocks of kv_heads x head_size x block_size", false;
+            size_t bytes = 0;
+            if (tlh_paged_attention_scratch_bytes(&a, &bytes) != TLH_OK) return why = tlh_last_error(), false;
+            d.kind = D_PAGED_ATTN;
+            d.scratch_bytes = bytes;
+        } else if (kind == 2) {
+            const tlh_ir_tensor &k = T(0), &v = T(1);
+            if (!(is_f16(k) && is_f16(v) && is_f16(T(2)) && is_f16(T(3))))
+                return why = "the cache write takes f16 keys, values and caches", false;
+            const int64_t tokens = k.ne[1];
+            int64_t ns = 1;
+            for (int i = 0; i < 4; ++i) ns *= T(4).ne[i];
+            if (ns != 2 * tokens || T(4).ty != TLH_TYPE_I32 || k.nb[1] != k.ne[0] * 2 || v.nb[1] != v.ne[0] * 2 ||
+                v.ne[0] != k.ne[0] || v.ne[1] != tokens || k.nb[0] != 2 || v.nb[0] != 2)
+                return why = "the cache write takes contiguous keys and one i64 slot per token", false;
+            if (kvh < 1 || k.ne[0] % kvh) return why = "the cache write: rows are not kv_heads x head_size", false;
+            d.pw[0] = (int32_t)tokens;
+            d.pw[1] = kvh;
+            d.pw[2] = (int32_t)(k.ne[0] / kvh);
+            d.pw[3] = bs;
+            if (d.pw[2] % 8 || !(bs == 8 || bs == 16 || bs == 32))
+                return why = "the cache write: head size a multiple of 8, block size 8, 16 or 32", false;
+            d.kind = D_PAGED_WRITE;
+        } else {
+            return why = "unknown custom op", false;
+        }
+        out.push_back(d);
+        return true;
+    }
+
     // Ctx::lower's table (lower.rs:188-211) for the ops this library runs.
     bool lower_node(int pos, int32_t id, std::vector<Dispatch> &out, std::string &why) {
         const tlh_ir_tensor &t = g_.t[id];
@@ -278,6 +355,7 @@ class Lowering {
             out.push_back(d);
             return true;
         }
+        if (op == "CUSTOM") return custom(pos, id, out, why);
         if (op == "ADD" || op == "SUB" || op == "MUL" || op == "DIV") {
             Dispatch d = base(pos, id, {0, 1});
             d.op.x[0] = op == "ADD" ? 0 : op == "SUB" ? 1 : op == "MUL" ? 2 : 3;
@@ -503,8 +581,9 @@ class Lowering {
     // every place a dispatch reads, and the ones it writes
     static void places(const Dispatch &x, std::vector<Place> &rd, std::vector<Place> &wr) {
         rd.clear(), wr.clear();
-        for (int k = 0; k < 4; ++k) rd.push_back(x.src[k]);
+        for (int k = 0; k < NSRC; ++k) rd.push_back(x.src[k]);
         wr.push_back(x.dst);
+        if (x.kind == D_PAGED_WRITE) wr.push_back(x.src[2]), wr.push_back(x.src[3]);  // the two pools
         for (int k = 0; k < x.nmem; ++k) rd.push_back(x.mw[k]), wr.push_back(x.mdst[k]);
         for (int k = 0; k < x.nsub; ++k) {
             for (int j = 0; j < 4; ++j) rd.push_back(x.ssrc[k][j]);
@@ -719,7 +798,7 @@ class Lowering {
         for (const Dispatch &x : out.d) {
             if (x.pos_last == x.pos) continue;
             for (int64_t pos : {(int64_t)x.pos, (int64_t)x.pos_last}) {
-                for (int k = 0; k < 4; ++k) touch_place(x.src[k], pos);
+                for (int k = 0; k < NSRC; ++k) touch_place(x.src[k], pos);
                 touch_place(x.dst, pos);
                 for (int k = 0; k < x.nmem; ++k) touch_place(x.mdst[k], pos);
                 for (int k = 0; k < x.nsub; ++k) {
@@ -845,8 +924,8 @@ struct tlh_program {
 
     tlh_status enqueue(void *state, hipStream_t s) const {
         for (const Dispatch &x : low.d) {
-            void *src[4];
-            for (int i = 0; i < 4; ++i) src[i] = resolve(x.src[i], state);
+            void *src[NSRC];
+            for (int i = 0; i < NSRC; ++i) src[i] = resolve(x.src[i], state);
             void *dst = resolve(x.dst, state);
             void *scratch = x.block >= 0 ? arena + low.blocks[x.block].off : nullptr;
             tlh_status st;
@@ -858,6 +937,21 @@ struct tlh_program {
                 st = tlh_flash_attn_ext(&x.op, src[0], src[1], src[2], src[3], dst, scratch, x.scratch_bytes, s);
                 break;
             case D_NORM_CHAIN: st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s); break;
+            case D_PAGED_ATTN: {
+                tlh_paged_attention_args a = x.pa;
+                a.out = dst;
+                a.q = src[0];
+                a.k_cache = src[1];
+                a.v_cache = src[2];
+                a.block_tables = (const int32_t *)src[3];
+                a.context_lens = (const int32_t *)src[4];
+                st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
+                break;
+            }
+            case D_PAGED_WRITE:
+                st = tlh_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4], x.pw[0], x.pw[1],
+                                           x.pw[2], x.pw[3], s);
+                break;
             case D_ARGMAX_SPLIT: st = launch_argmax_split(x.op, src[0], dst, scratch, s); break;
             case D_CORE_MULTI: {
                 const void *ss[4][4];

@@ -209,6 +209,33 @@ class Builder:
     def argmax(self, a: T) -> T:
         return self._new(N.I32, [a.ne[1]], "ARGMAX", [a])
 
+    def cast(self, a: T, ty: int) -> T:
+        """ggml_cast: a copied into a new tensor of type ty."""
+        return self.cpy(a, self._new(ty, a.ne))
+
+    # --------------------------------------------------- paged attention nodes
+    # ggml CUSTOM nodes that nothing computes on ggml; the executor reads the
+    # kernel's parameters from userdata (crates/tensorlisp/src/scheme/core.ss:215-272).
+    def _custom(self, ty, ne, userdata: int, src) -> T:
+        p = [0] * 16
+        lo, hi = userdata & 0xFFFFFFFF, userdata >> 32
+        p[4], p[5] = (lo ^ 0x80000000) - 0x80000000, (hi ^ 0x80000000) - 0x80000000
+        return self._new(ty, ne, "CUSTOM", src, p)
+
+    def paged_attention(self, q: T, kc: T, vc: T, tables: T, lens: T, block_size: int, max_ctx: int, scale: float,
+                        kv_heads: int = 1) -> T:
+        """One query per sequence: q f16 [hs, heads, seqs] (contiguous), block tables
+        i32 [max_blocks, seqs], context lengths i32 [seqs] -> f16 [hs, heads, seqs]
+        (core.ss:247-258)."""
+        return self._custom(N.F16, [q.ne[0], q.ne[1], q.ne[2], 1],
+                            paged_userdata(1, kv_heads, block_size, max_ctx, scale), [q, kc, vc, tables, lens])
+
+    def paged_cache_write(self, k: T, v: T, kc: T, vc: T, slots: T, block_size: int, kv_heads: int = 1) -> T:
+        """key and value f16 [hs * kv_heads, tokens] into the pools at the slots (i32
+        [2 * tokens], one little-endian i64 per token; negative skips), core.ss:260-272.
+        Expand the result before the attention that reads the pools."""
+        return self._custom(N.F16, [1, 1, 1, 1], paged_userdata(2, kv_heads, block_size, 1, 1.0), [k, v, kc, vc, slots])
+
     # ------------------------------------------------------------- ordering
     def expand(self, t: T) -> None:
         """ggml_build_forward_expand: sources first (in slot order), then t; leaves
@@ -242,6 +269,18 @@ class Builder:
             for i in range(10):
                 r.src[i] = t.src[i] if i < len(t.src) else -1
         return arr
+
+
+def paged_userdata(kind: int, kv_heads: int, block_size: int, max_ctx: int, scale: float) -> int:
+    """The u64 a paged CUSTOM node carries (core.ss:240-245): low to high bits kind
+    (4), kv heads (4), block size (8), max context (16), scale (f32 bits)."""
+    if not 0 < kv_heads < 16:
+        raise ValueError(f"kv-heads must be 1..15: {kv_heads}")
+    if block_size not in (8, 16, 32):
+        raise ValueError(f"block-size must be 8, 16 or 32: {block_size}")
+    if not 0 < max_ctx < 65536:
+        raise ValueError(f"max-context must be 1..65535: {max_ctx}")
+    return kind + kv_heads * 16 + block_size * 256 + max_ctx * 65536 + ((_bits(scale) & 0xFFFFFFFF) << 32)
 
 
 def _i32_array(xs):
@@ -382,6 +421,34 @@ class DecoderStep:
     keep: list
 
 
+def _decoder_body(b: Builder, c: DecoderConfig, W, tokens: T, pos: T, T_: int, attend, last_only: bool):
+    """The llama layers around attention (llm_build_llama): attend(i, q, k, v)
+    gets layer i's roped q [hd, heads, T] and k [hd, kv_heads, T] and v
+    [n_embd_kv, T] (f32) and returns the attention output [n_embd, T] (f32)."""
+    x = b.get_rows(W["tok_embd"], tokens)
+    hd = c.head_dim
+    for i in range(c.n_layer):
+        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.attn_norm"])
+        q = b.reshape(b.mul_mat(W[f"l{i}.wq"], cur), hd, c.n_head, T_)
+        k = b.reshape(b.mul_mat(W[f"l{i}.wk"], cur), hd, c.n_head_kv, T_)
+        v = b.mul_mat(W[f"l{i}.wv"], cur)
+        q = b.rope_ext(q, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
+        k = b.rope_ext(k, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
+        att = attend(i, q, k, v)
+        x = b.add(b.mul_mat(W[f"l{i}.wo"], att), x)
+        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.ffn_norm"])
+        h = b.glu_split(b.mul_mat(W[f"l{i}.w_gate"], cur), b.mul_mat(W[f"l{i}.w_up"], cur), "swiglu")
+        x = b.add(b.mul_mat(W[f"l{i}.w_down"], h), x)
+    if last_only and T_ > 1:
+        x = b.view(x, [c.n_embd, 1], [x.nb[1]], (T_ - 1) * x.nb[1])
+    cur = b.mul(b.rms_norm(x, c.eps), W["out_norm"])
+    logits = b.mul_mat(W["output"], cur)
+    am = b.argmax(logits)
+    b.expand(logits)
+    b.expand(am)
+    return logits, am
+
+
 def decoder_step(c: DecoderConfig, n_tokens: int, n_kv: int, last_only: bool = True) -> DecoderStep:
     """One forward step of `n_tokens` new tokens over a cache whose first `n_kv`
     rows are attended (llama.cpp's llm_build_llama with the flash-attention
@@ -397,34 +464,132 @@ def decoder_step(c: DecoderConfig, n_tokens: int, n_kv: int, last_only: bool = T
     pos = b.input(N.I32, [T_], "pos")
     slots = b.input(N.I64, [T_], "slots")
     mask = b.input(N.F16, [n_kv, T_], "mask")
-    x = b.get_rows(W["tok_embd"], tokens)
     scale = 1.0 / float(hd) ** 0.5
-    for i, (kc, vc) in enumerate(caches):
-        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.attn_norm"])
-        q = b.reshape(b.mul_mat(W[f"l{i}.wq"], cur), hd, c.n_head, T_)
-        k = b.reshape(b.mul_mat(W[f"l{i}.wk"], cur), hd, c.n_head_kv, T_)
-        v = b.mul_mat(W[f"l{i}.wv"], cur)
-        q = b.rope_ext(q, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
-        k = b.rope_ext(k, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
+
+    def attend(i, q, k, v):
+        kc, vc = caches[i]
         b.expand(b.set_rows(kc, b.reshape(k, c.n_embd_kv, T_), slots))
         b.expand(b.set_rows(vc, v, slots))
         row = c.n_embd_kv * 2
         K = b.permute(b.view(kc, [hd, c.n_head_kv, n_kv], [hd * 2, row], 0), 0, 2, 1, 3)
         V = b.permute(b.view(vc, [hd, c.n_head_kv, n_kv], [hd * 2, row], 0), 0, 2, 1, 3)
         Q = b.permute(q, 0, 2, 1, 3)
-        att = b.reshape(b.flash_attn_ext(Q, K, V, mask, scale), c.n_embd, T_)
-        x = b.add(b.mul_mat(W[f"l{i}.wo"], att), x)
-        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.ffn_norm"])
-        h = b.glu_split(b.mul_mat(W[f"l{i}.w_gate"], cur), b.mul_mat(W[f"l{i}.w_up"], cur), "swiglu")
-        x = b.add(b.mul_mat(W[f"l{i}.w_down"], h), x)
-    if last_only and T_ > 1:
-        x = b.view(x, [c.n_embd, 1], [x.nb[1]], (T_ - 1) * x.nb[1])
-    cur = b.mul(b.rms_norm(x, c.eps), W["out_norm"])
-    logits = b.mul_mat(W["output"], cur)
-    am = b.argmax(logits)
-    b.expand(logits)
-    b.expand(am)
+        return b.reshape(b.flash_attn_ext(Q, K, V, mask, scale), c.n_embd, T_)
+
+    logits, am = _decoder_body(b, c, W, tokens, pos, T_, attend, last_only)
     return DecoderStep(b, tokens, pos, slots, mask, logits, am, [logits, am])
+
+
+@dataclass
+class PagedConfig:
+    """A paged KV pool per layer: `n_blocks` blocks of `block_size` token rows in
+    vLLM's layouts (keys [blocks, kv_heads, hs/8, block_size, 8], values
+    [blocks, kv_heads, hs, block_size], f16) and `max_blocks` block-table
+    entries per sequence (context at most block_size * max_blocks < 65536)."""
+    block_size: int = 16
+    n_blocks: int = 4096
+    max_blocks: int = 256
+
+    @property
+    def max_ctx(self) -> int:
+        return min(self.block_size * self.max_blocks, 65535)
+
+    def pool_bytes(self, c: DecoderConfig) -> int:
+        return self.n_blocks * c.n_head_kv * c.head_dim * self.block_size * 2
+
+    def state_bytes(self, c: DecoderConfig):
+        """Byte offsets of the per-layer key and value pools in one state buffer."""
+        per = self.pool_bytes(c)
+        return [i * per for i in range(2 * c.n_layer)], 2 * c.n_layer * per
+
+
+@dataclass
+class PagedStep:
+    builder: Builder
+    tokens: T
+    pos: T
+    slots: T
+    mask: T        # prefill only
+    tables: T      # decode only
+    lens: T        # decode only
+    logits: T
+    argmax: T
+    keep: list
+
+
+def _paged_pools(b: Builder, c: DecoderConfig, pc: PagedConfig):
+    n = pc.n_blocks * c.n_head_kv * c.head_dim * pc.block_size
+    return [(b.state(N.F16, [n], f"kpool{i}"), b.state(N.F16, [n], f"vpool{i}")) for i in range(c.n_layer)]
+
+
+def decoder_prefill_paged(c: DecoderConfig, pc: PagedConfig, n_tokens: int) -> PagedStep:
+    """A new sequence's prompt of `n_tokens` tokens: keys and values go to the
+    pools through paged-cache-write and the prompt attends to its own keys with
+    FLASH_ATTN_EXT and a causal mask. Inputs 0 tokens i32 [T], 1 positions i32
+    [T], 2 slots i32 [2T] (one i64 per token), 3 mask f16 [T, T]; logits and
+    argmax of the last token."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    pools = _paged_pools(b, c, pc)
+    T_, hd = n_tokens, c.head_dim
+    tokens = b.input(N.I32, [T_], "tokens")
+    pos = b.input(N.I32, [T_], "pos")
+    slots = b.input(N.I32, [2 * T_], "slots")
+    mask = b.input(N.F16, [T_, T_], "mask")
+    scale = 1.0 / float(hd) ** 0.5
+
+    def attend(i, q, k, v):
+        kc, vc = pools[i]
+        k16 = b.cast(b.reshape(k, c.n_embd_kv, T_), N.F16)
+        v16 = b.cast(v, N.F16)
+        b.expand(b.paged_cache_write(k16, v16, kc, vc, slots, pc.block_size, c.n_head_kv))
+        K = b.permute(b.reshape(k16, hd, c.n_head_kv, T_), 0, 2, 1, 3)
+        V = b.permute(b.reshape(v16, hd, c.n_head_kv, T_), 0, 2, 1, 3)
+        Q = b.permute(q, 0, 2, 1, 3)
+        return b.reshape(b.flash_attn_ext(Q, K, V, mask, scale), c.n_embd, T_)
+
+    logits, am = _decoder_body(b, c, W, tokens, pos, T_, attend, True)
+    return PagedStep(b, tokens, pos, slots, mask, None, None, logits, am, [logits, am])
+
+
+def decoder_decode_paged(c: DecoderConfig, pc: PagedConfig, n_seqs: int) -> PagedStep:
+    """One decode step of `n_seqs` sequences, one token each, over the paged
+    pools (the `paged-attention` node, vLLM's decode kernel). Inputs 0 tokens
+    i32 [S], 1 positions i32 [S], 2 slots i32 [2S], 3 block tables i32
+    [max_blocks, S], 4 context lengths i32 [S] (including the new token);
+    logits [vocab, S] and their argmax [S]."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    pools = _paged_pools(b, c, pc)
+    S, hd = n_seqs, c.head_dim
+    tokens = b.input(N.I32, [S], "tokens")
+    pos = b.input(N.I32, [S], "pos")
+    slots = b.input(N.I32, [2 * S], "slots")
+    tables = b.input(N.I32, [pc.max_blocks, S], "tables")
+    lens = b.input(N.I32, [S], "lens")
+    scale = 1.0 / float(hd) ** 0.5
+
+    def attend(i, q, k, v):
+        kc, vc = pools[i]
+        k16 = b.cast(b.reshape(k, c.n_embd_kv, S), N.F16)
+        v16 = b.cast(v, N.F16)
+        b.expand(b.paged_cache_write(k16, v16, kc, vc, slots, pc.block_size, c.n_head_kv))
+        att = b.paged_attention(b.cast(q, N.F16), kc, vc, tables, lens, pc.block_size, pc.max_ctx, scale,
+                                c.n_head_kv)
+        return b.cast(b.reshape(att, c.n_embd, S), N.F32)
+
+    logits, am = _decoder_body(b, c, W, tokens, pos, S, attend, False)
+    return PagedStep(b, tokens, pos, slots, None, tables, lens, logits, am, [logits, am])
+
+
+def paged_slots(table, positions, block_size: int):
+    """i32 [2T] slot words (one little-endian i64 per token) for token positions of
+    one sequence whose block table is `table` (numpy)."""
+    import numpy as np
+
+    pos = np.asarray(positions, np.int64)
+    tab = np.asarray(table, np.int64)
+    return (tab[pos // block_size] * block_size + pos % block_size).astype(np.int64).view(np.int32)
 
 
 def causal_mask(positions, n_kv: int):

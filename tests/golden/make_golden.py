@@ -39,6 +39,11 @@ these are the reference's outputs on fixed inputs, captured once:
                    inputs (native.rs:109-498) and decoder-sized ones; inputs are
                    regenerated from seeds, the file keeps the outputs
 
+  decoder_paged.npz  refs.PAGED_SEQS (three sequences: a prompt, then three
+                   decode tokens) each alone through the dense-cache decoder
+                   step on the CPU backend (refs.paged_ref_run): the logits
+                   and argmax a batched paged decode must reproduce
+
   decoder.npz      a llama-style decoder step graph (tensorlisp_amd.graph.decoder_step,
                    refs.decoder_tiny_config: 2 layers, 4 heads of 64, 2 KV heads,
                    q4_K / q6_K weights from refs.decoder_weights) run on the CPU
@@ -46,7 +51,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    single-token steps, a 3-token chunk): logits and argmax per
                    step and the f16 KV caches after the last one
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -61,7 +66,8 @@ sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
 from refs import (FA_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
-                  decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, xorshift_noise)
+                  decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, paged_ref_run,
+                  xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
 
 
@@ -133,6 +139,13 @@ def q5_K_golden(ref) -> None:
     kquant_golden(ref, Q5_K, "q5_K", 71, 72)
 
 
+def decoder_paged_golden(ref) -> None:
+    c = decoder_tiny_config()
+    pl, pa, dl, da = paged_ref_run(ref, c, decoder_weights(c))
+    np.savez_compressed(HERE / "decoder_paged.npz", prompt_logits=pl, prompt_argmax=pa, decode_logits=dl,
+                        decode_argmax=da)
+
+
 def core_golden(ref) -> None:
     np.savez_compressed(HERE / "core.npz", **{c["name"]: core_ref(ref, c) for c in core_cases()})
 
@@ -148,6 +161,9 @@ def decoder_golden(ref) -> None:
 
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["decoder_paged"]:  # only the paged-decoder fixture
+        decoder_paged_golden(ref)
+        return
     if sys.argv[1:] == ["decoder"]:  # only the decoder-step fixture
         decoder_golden(ref)
         return
@@ -226,6 +242,7 @@ def main() -> None:
     q5_K_golden(ref)
     core_golden(ref)
     decoder_golden(ref)
+    decoder_paged_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

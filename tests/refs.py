@@ -990,3 +990,38 @@ def decoder_ref_run(r, c, weights):
         logits.append(lg.reshape(-1, c.n_vocab))
         ams.append(am.reshape(-1))
     return logits, ams, states
+
+
+# ------------------------------------------------------- paged decoder steps
+# Three sequences (prompt tokens, then three decode tokens fed one per step),
+# block tables into a 16-block pool of 16-row blocks.
+PAGED_SEQS = [([1, 7, 3, 999, 0], [42, 17, 500]), ([5, 6, 7, 8, 9, 10, 11, 12, 13], [1, 2, 3]),
+              ([250, 251, 252], [9, 99, 999])]
+PAGED_TABLES = [[7, 2, 11, 0], [3, 15, 8, 5], [12, 1, 9, 14]]
+
+
+def paged_ref_run(r, c, weights):
+    """Each PAGED_SEQS sequence alone through the reference CPU backend with the
+    dense-cache decoder step (decoder_step): the prompt as one step, then one
+    step per decode token. Returns (prompt logits [S, vocab], decode logits
+    [steps, S, vocab]) and their argmax."""
+    from tensorlisp_amd import graph as G
+
+    S, steps = len(PAGED_SEQS), len(PAGED_SEQS[0][1])
+    pl = np.zeros((S, c.n_vocab), np.float32)
+    dl = np.zeros((steps, S, c.n_vocab), np.float32)
+    pa = np.zeros(S, np.int32)
+    da = np.zeros((steps, S), np.int32)
+    for s, (prompt, dec) in enumerate(PAGED_SEQS):
+        states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
+        todo = [(prompt, 0)] + [([t], len(prompt) + j) for j, t in enumerate(dec)]
+        for k, (toks, p0) in enumerate(todo):
+            n_kv = p0 + len(toks)
+            st = G.decoder_step(c, len(toks), n_kv)
+            lg, am = r.ir_run(st.builder, weights, states, decoder_step_inputs((toks, p0, n_kv, False)),
+                              [(st.logits, np.float32), (st.argmax, np.int32)])
+            if k == 0:
+                pl[s], pa[s] = lg.reshape(-1), am.reshape(-1)[0]
+            else:
+                dl[k - 1, s], da[k - 1, s] = lg.reshape(-1), am.reshape(-1)[0]
+    return pl, pa, dl, da

@@ -176,3 +176,52 @@ def test_decoder_graph_is_the_graph_ggml_builds(T, n_kv, last_only):
                               [(st.logits, np.float32), (st.argmax, np.int32)])
     assert np.all(np.isfinite(logits)) and am.size == (1 if last_only else T)
     assert np.any(states[0] != 0)  # SET_ROWS wrote the cache
+
+
+# ------------------------------------------------------------ paged nodes
+def test_paged_userdata_packs_as_core_ss():
+    """(+ kind (* kv-heads 16) (* block-size 256) (* max-context 65536) (* scale-bits 2^32)),
+    core.ss:240-245, and its range checks."""
+    ud = G.paged_userdata(1, 8, 16, 4096, 0.08838834764831845)
+    assert ud & 15 == 1 and (ud >> 4) & 15 == 8 and (ud >> 8) & 255 == 16 and (ud >> 16) & 0xFFFF == 4096
+    assert np.array([ud >> 32], np.uint32).view(np.float32)[0] == np.float32(0.08838834764831845)
+    for bad in ((1, 16, 16, 64, 1.0), (1, 8, 12, 64, 1.0), (1, 8, 16, 65536, 1.0), (1, 0, 16, 64, 1.0)):
+        with pytest.raises(ValueError):
+            G.paged_userdata(*bad)
+
+
+def test_paged_decoder_graphs_plan():
+    """The paged prefill and batched decode graphs lower (CUSTOM kinds 1 and 2 next
+    to FLASH_ATTN_EXT and the rest) and get a memory plan."""
+    pc = G.PagedConfig(block_size=16, n_blocks=16, max_blocks=4)
+    for st in (G.decoder_prefill_paged(TINY, pc, 5), G.decoder_decode_paged(TINY, pc, 3)):
+        offs, scr, size = G.plan(st.builder, st.keep)
+        assert size > 0
+        kinds = [st.builder.t[i].op for i in st.builder.nodes]
+        assert kinds.count("CUSTOM") == TINY.n_layer * (2 if st.tables is not None else 1)
+
+
+def _paged_graph(q_ty=N.F16, tab_ty=N.I32, slot_words=2, kvh=2, pool_rows=16 * 2 * 64):
+    b = G.Builder()
+    q = b.input(q_ty, [64, 4, 3])
+    kc = b.state(N.F16, [pool_rows * 4])
+    vc = b.state(N.F16, [pool_rows * 4])
+    tables = b.input(tab_ty, [4, 3])
+    lens = b.input(N.I32, [3])
+    k = b.input(N.F16, [128, 3])
+    slots = b.input(N.I32, [slot_words * 3])
+    b.expand(b.paged_cache_write(k, k, kc, vc, slots, 16, kvh))
+    att = b.paged_attention(q, kc, vc, tables, lens, 16, 64, 0.125, kvh)
+    b.expand(att)
+    return b, att
+
+
+def test_paged_node_validation():
+    b, att = _paged_graph()
+    G.plan(b, [att])
+    for kw, msg in (({"q_ty": N.F32}, "f16 q"), ({"tab_ty": N.I64}, "block tables"),
+                    ({"slot_words": 1}, "one i64 slot"), ({"kvh": 3}, "kv_heads x head_size"),
+                    ({"pool_rows": 100}, "whole blocks")):
+        b, att = _paged_graph(**kw)
+        with pytest.raises(N.TlhError, match=msg):
+            G.plan(b, [att])
