@@ -301,6 +301,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="run only the end-to-end 8B decoder (configs[4]) and print its JSON")
+    ap.add_argument("--decode-steps", type=int, default=256)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -316,6 +319,9 @@ def main() -> int:
     log(f"device {props['name']} {props['arch']} CUs={props['compute_units']}")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
+    if args.e2e_only:
+        print(json.dumps(e2e_decoder(torch, gen, decode_steps=args.decode_steps)), flush=True)
+        return 0
 
     cases = [(t, M, K, n) for t in (N.Q4_0, N.Q4_K) for (M, K) in SHAPES for n in (1, 8)]
     weights, nodes, xs, ys, bytes_per = {}, {}, {}, {}, {}
@@ -510,7 +516,7 @@ def main() -> int:
         del fq, fk, fv, fm, fo, node
     torch.cuda.empty_cache()
 
-    e2e = e2e_decoder(torch, gen)
+    e2e = e2e_decoder(torch, gen, decode_steps=args.decode_steps)
 
     # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
     # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
