@@ -135,6 +135,21 @@ tlh_status tlh_mul_mat_quantize(const tlh_op *op, const void *src1, void *scratc
 tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *scratch, size_t scratch_bytes,
                                void *dst, void *stream);
 
+/* GGML_OP_MUL_MAT_ID (vendor/ggml/src/ggml.c:3329-3353; CPU
+ * ggml_compute_forward_mul_mat_id, ggml-cpu/ggml-cpu.c:1460-1640), which the
+ * reference's native lowering has no kernel for (docs/design/kernel-launcher.md:326)
+ * and runs on the CPU backend. Descriptor slots: t[0] = as, the expert
+ * matrices [K, M, n_as] (q4_0 | q8_0 | q4_K | q5_K | q6_K); t[1] = b f32
+ * [K, n_b1, n_tokens] with n_used % n_b1 == 0; t[2] = ids i32 [n_used, n_tokens];
+ * t[4] = dst f32 [M, n_used, n_tokens]. dst[:, e, t] = as[:, :, ids[e, t]] times
+ * b row (e % n_b1, t), each element the CPU's vec_dot of the quantized row
+ * (so within the MUL_MAT tolerance of the CPU backend). An id outside
+ * [0, n_as) yields NaN in its column (the CPU backend aborts there). Decode
+ * oriented: each (expert, token) pair streams its expert's matrix once. */
+tlh_status tlh_mul_mat_id_scratch_bytes(const tlh_op *op, size_t *bytes);
+tlh_status tlh_mul_mat_id(const tlh_op *op, const void *src0, const void *src1, const void *ids, void *dst,
+                          void *scratch, size_t scratch_bytes, void *stream);
+
 /* Activation quantizer alone: `rows` rows of `k` f32 (row stride x_row_bytes)
  * into ggml's block layout of the vec_dot type of `wtype` — the from_float the
  * CPU mul_mat applies (quantize_row_q8_0 / quantize_row_q8_K:

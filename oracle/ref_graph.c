@@ -278,6 +278,8 @@ int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_node
             x = ggml_cpy(ctx, s0, s1);
         } else if (!strcmp(op, "MUL_MAT")) {
             x = ggml_mul_mat(ctx, s0, s1);
+        } else if (!strcmp(op, "MUL_MAT_ID")) {
+            x = ggml_mul_mat_id(ctx, s0, s1, s2);
         } else if (!strcmp(op, "ADD")) {
             x = ggml_add(ctx, s0, s1);
         } else if (!strcmp(op, "SUB")) {

@@ -32,7 +32,7 @@ struct Place {
 };
 
 enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
-                    D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE };
+                    D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE, D_MUL_MAT_ID };
 constexpr int NSRC = 5;  // sources a dispatch reads (the paged nodes have five)
 struct Dispatch {
     DispatchKind kind;
@@ -330,6 +330,16 @@ class Lowering {
             size_t bytes = 0;
             if (tlh_mul_mat_scratch_bytes(&d.op, &bytes) != TLH_OK) return why = tlh_last_error(), false;
             d.kind = D_MUL_MAT;
+            d.scratch_bytes = bytes;
+            out.push_back(d);
+            return true;
+        }
+        if (op == "MUL_MAT_ID") {
+            if (src(0) < 0 || src(1) < 0 || src(2) < 0) return why = "missing source", false;
+            Dispatch d = base(pos, id, {0, 1, 2});
+            size_t bytes = 0;
+            if (tlh_mul_mat_id_scratch_bytes(&d.op, &bytes) != TLH_OK) return why = tlh_last_error(), false;
+            d.kind = D_MUL_MAT_ID;
             d.scratch_bytes = bytes;
             out.push_back(d);
             return true;
@@ -948,6 +958,9 @@ struct tlh_program {
                 st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
                 break;
             }
+            case D_MUL_MAT_ID:
+                st = tlh_mul_mat_id(&x.op, src[0], src[1], src[2], dst, scratch, x.scratch_bytes, s);
+                break;
             case D_PAGED_WRITE:
                 st = tlh_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4], x.pw[0], x.pw[1],
                                            x.pw[2], x.pw[3], s);

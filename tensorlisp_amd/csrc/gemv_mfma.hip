@@ -339,8 +339,15 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     const int64_t batch = blockIdx.z;
     const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
     const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
-    const int64_t arow0 = a.n0 + a.N_total * batch;
-    const ActView act = act_view(a.act, AT, K, a.N_total * a.ne12 * a.ne13);
+    int64_t arow0 = a.n0 + a.N_total * batch;
+    bool bad_id = false;  // MUL_MAT_ID: an expert id out of range (outputs NaN, loads stay in bounds)
+    if (a.ids) {
+        const int32_t ex = *(const int32_t *)(a.ids + i12 * a.ids_nb0 + i13 * a.ids_nb1);
+        bad_id = ex < 0 || ex >= a.id_nas;
+        W = a.w + (bad_id ? 0 : (int64_t)ex) * a.w_nb2;
+        arow0 = i12 % a.id_b1 + a.id_b1 * i13;
+    }
+    const ActView act = act_view(a.act, AT, K, mm_act_rows(a));
     const int N = (int)a.N;
 
     // LDS: partials [2][nw][64] float4, the activation scales of the
@@ -445,7 +452,8 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         if (threadIdx.x < 16 * SK_COLS)
             for (int k = 0; k < nbuf; ++k) {
                 const int64_t grp = buf_rg + (int64_t)k * gridDim.x;
-                if (ocol < N && grp * 16 + orow < a.M) *out_ptr(grp) = obuf[k * 256 + threadIdx.x];
+                if (ocol < N && grp * 16 + orow < a.M)
+                    *out_ptr(grp) = bad_id ? __builtin_nanf("") : obuf[k * 256 + threadIdx.x];
             }
         nbuf = 0;
         // the stores complete here, so no later wait for loads is widened by them

@@ -43,7 +43,19 @@ struct MatmulArgs {
     int64_t seg_w_nb1[3];
     float *seg_dst[3];
     int64_t seg_m0[4];
+    // MUL_MAT_ID (int8-MFMA few-column kernel only): with ids != null, batch
+    // slice z = (e, t) = (z % ne12, z / ne12) multiplies weight matrix
+    // ids[e * ids_nb0 + t * ids_nb1] (i32, w_nb2 apart; id_nas matrices) by
+    // activation row (e % id_b1) + id_b1 * t of the id_b1 * ne13 quantized rows,
+    // into dst + e * d_nb2 + t * d_nb3. An id outside [0, id_nas) gives NaN.
+    const char *ids;
+    int64_t ids_nb0, ids_nb1, id_b1, id_nas;
 };
+
+// Rows of quantized activations a launch's scratch holds.
+__host__ __device__ inline int64_t mm_act_rows(const MatmulArgs &a) {
+    return a.ids ? a.id_b1 * a.ne13 : a.N_total * a.ne12 * a.ne13;
+}
 
 // N <= 16. With x != nullptr (src1 rows in activation-row order, stride
 // x_row_bytes) and a small N*K the GEMV quantizes x itself and the scratch is

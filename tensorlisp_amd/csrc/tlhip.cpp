@@ -551,6 +551,126 @@ tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *s
     return mm_compute(op, s, src0, scratch, dst, (hipStream_t)stream);
 }
 
+// ------------------------------------------------------------ MUL_MAT_ID
+// ggml_mul_mat_id (ggml.c:3329-3353) computed as the CPU backend does
+// (ggml_compute_forward_mul_mat_id, ggml-cpu/ggml-cpu.c:1460-1640): src1 rows
+// quantized to the vec_dot type once, then output column (e, t) is expert
+// ids[e, t]'s matrix times quantized row (e % ne11) + ne11 * t, each element
+// one vec_dot. Here every (e, t) pair is one batch slice of the int8-MFMA
+// few-column kernel, which reads the expert id on the device.
+struct MulMatIdShape {
+    int64_t K, M, n_as, n_used, n_tok, n_b1;
+    int wtype, act_type;
+};
+
+static tlh_status check_mul_mat_id(const tlh_op *op, MulMatIdShape &s) {
+    if (!op) return set_error(TLH_INVALID, "mul_mat_id: null op");
+    const tlh_tensor &a = op->t[0], &b = op->t[1], &ids = op->t[2], &d = op->t[4];
+    if (!weight_type_ok(a.ty))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K",
+                         a.ty, type_name(a.ty));
+    if (b.ty != TLH_TYPE_F32 || d.ty != TLH_TYPE_F32 || ids.ty != TLH_TYPE_I32)
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: f32 src1 and dst, i32 ids");
+    for (int i = 0; i < 4; ++i)
+        if (a.ne[i] < 0 || b.ne[i] < 0 || d.ne[i] < 0 || ids.ne[i] < 0)
+            return set_error(TLH_INVALID, "mul_mat_id: negative extent");
+    // ggml_mul_mat_id's asserts
+    if (a.ne[3] != 1 || b.ne[3] != 1 || ids.ne[2] != 1 || ids.ne[3] != 1 || ids.ne[1] != b.ne[2] ||
+        a.ne[0] != b.ne[0] || b.ne[1] == 0 || ids.ne[0] % b.ne[1] != 0)
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: shapes (as [K, M, n_as], b [K, n_b1, n_tokens], ids [n_used, "
+                                          "n_tokens] with n_used %% n_b1 == 0)");
+    if (d.ne[0] != a.ne[1] || d.ne[1] != ids.ne[0] || d.ne[2] != b.ne[2] || d.ne[3] != 1)
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: dst must be [M, n_used, n_tokens]");
+    s.K = a.ne[0];
+    s.M = a.ne[1];
+    s.n_as = a.ne[2];
+    s.n_used = ids.ne[0];
+    s.n_tok = ids.ne[1];
+    s.n_b1 = b.ne[1];
+    const int be = block_elems(a.ty);
+    if (s.K % be != 0)
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: K=%lld is not a multiple of the %s block (%d)", (long long)s.K,
+                         type_name(a.ty), be);
+    const int64_t rb = s.K / be * block_bytes(a.ty);
+    if (a.nb[0] != block_bytes(a.ty) || a.nb[1] < rb || (a.nb[1] & 1) || a.nb[2] < a.nb[1] * s.M || (a.nb[2] & 1))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: src0 must hold whole rows, 2-byte aligned, matrices apart");
+    if (b.nb[0] != 4 || (b.nb[1] & 3) || (b.nb[2] & 3))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: src1 must have contiguous f32 rows");
+    if (ids.nb[0] != 4 || (ids.nb[1] & 3))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: ids must be i32 with 4-byte strides");
+    if (d.nb[0] != 4 || d.nb[1] < 4 * s.M || (d.nb[1] & 3) || d.nb[2] < d.nb[1] || (d.nb[2] & 3))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_id: dst must be f32 with ordered strides");
+    if (s.n_used * s.n_tok > 65535) return set_error(TLH_UNSUPPORTED, "mul_mat_id: more than 65535 (expert, token) pairs");
+    s.wtype = a.ty;
+    s.act_type = vec_dot_type(a.ty);
+    return TLH_OK;
+}
+
+static int64_t mmid_act_bytes(const MulMatIdShape &s) { return act_layout(s.act_type, s.K, s.n_b1 * s.n_tok).total; }
+static int64_t mmid_partial_bytes(const MulMatIdShape &s) {
+    return align_up(gemv_mfma_partial_bytes(s.K, s.M, 1, s.n_used * s.n_tok), 256);
+}
+
+tlh_status tlh_mul_mat_id_scratch_bytes(const tlh_op *op, size_t *bytes) {
+    if (!bytes) return set_error(TLH_INVALID, "mul_mat_id_scratch_bytes: null pointer");
+    MulMatIdShape s;
+    const tlh_status st = check_mul_mat_id(op, s);
+    if (st != TLH_OK) return st;
+    *bytes = (size_t)(mmid_act_bytes(s) + mmid_partial_bytes(s));
+    return TLH_OK;
+}
+
+tlh_status tlh_mul_mat_id(const tlh_op *op, const void *src0, const void *src1, const void *ids, void *dst,
+                          void *scratch, size_t scratch_bytes, void *stream) {
+    MulMatIdShape s;
+    tlh_status st = check_mul_mat_id(op, s);
+    if (st != TLH_OK) return st;
+    if (s.M == 0 || s.n_used == 0 || s.n_tok == 0) return TLH_OK;
+    if (!src0 || !src1 || !ids || !dst) return set_error(TLH_INVALID, "mul_mat_id: null tensor pointer");
+    const size_t need = (size_t)(mmid_act_bytes(s) + mmid_partial_bytes(s));
+    if (!scratch || scratch_bytes < need)
+        return set_error(TLH_INVALID, "mul_mat_id: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    if (((uintptr_t)scratch & 255) || ((uintptr_t)src1 & 3) || ((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3) ||
+        ((uintptr_t)ids & 3))
+        return set_error(TLH_INVALID, "mul_mat_id: misaligned pointer (scratch 256, src1/dst/ids 4, src0 2 bytes)");
+    const tlh_tensor &a = op->t[0], &b = op->t[1], &it = op->t[2], &d = op->t[4];
+    const hipStream_t hs = (hipStream_t)stream;
+    const int64_t rows = s.n_b1 * s.n_tok;
+    if (b.nb[2] == b.nb[1] * s.n_b1 || s.n_tok == 1) {
+        st = launch_quantize_act(a.ty, (const float *)src1, s.K, rows, b.nb[1], scratch, false, 0, rows, false, hs);
+    } else {
+        for (int64_t t = 0; t < s.n_tok && st == TLH_OK; ++t)
+            st = launch_quantize_act(a.ty, (const float *)((const char *)src1 + t * b.nb[2]), s.K, s.n_b1, b.nb[1],
+                                     scratch, false, s.n_b1 * t, rows, false, hs);
+    }
+    if (st != TLH_OK) return st;
+    MatmulArgs m{};
+    m.wtype = a.ty;
+    m.w = (const uint8_t *)src0;
+    m.w_nb1 = a.nb[1];
+    m.w_nb2 = a.nb[2];
+    m.w_nb3 = a.nb[2] * s.n_as;
+    m.M = s.M;
+    m.K = s.K;
+    m.N = 1;
+    m.N_total = 1;
+    m.ne12 = s.n_used;
+    m.ne13 = s.n_tok;
+    m.r2 = m.r3 = 1;
+    m.act = scratch;
+    m.dst = (float *)dst;
+    m.d_nb1 = d.nb[1];
+    m.d_nb2 = d.nb[1];
+    m.d_nb3 = d.nb[2];
+    m.part = mmid_partial_bytes(s) > 0 ? (float *)((char *)scratch + mmid_act_bytes(s)) : nullptr;
+    m.ids = (const char *)ids;
+    m.ids_nb0 = it.nb[0];
+    m.ids_nb1 = it.nb[1];
+    m.id_b1 = s.n_b1;
+    m.id_nas = s.n_as;
+    return launch_gemv_mfma(m, hs);
+}
+
 tlh_status tlh_quantize_act(int wtype, const float *x, int64_t k, int64_t rows, int64_t x_row_bytes, void *y,
                             void *stream) {
     if (!weight_type_ok(wtype)) return set_error(TLH_UNSUPPORTED, "quantize_act: weight type %d", wtype);

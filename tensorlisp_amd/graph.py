@@ -147,6 +147,12 @@ class Builder:
         assert a.ne[0] == b.ne[0] and b.ne[2] % a.ne[2] == 0 and b.ne[3] % a.ne[3] == 0
         return self._new(N.F32, [a.ne[1], b.ne[1], b.ne[2], b.ne[3]], "MUL_MAT", [a, b])
 
+    def mul_mat_id(self, a: T, b: T, ids: T) -> T:
+        """ggml_mul_mat_id: experts a [K, M, n_as], b [K, n_b1, n_tokens], ids i32
+        [n_used, n_tokens] -> f32 [M, n_used, n_tokens] (ggml.c:3329-3353)."""
+        assert ids.ty == N.I32 and ids.ne[1] == b.ne[2] and a.ne[0] == b.ne[0] and ids.ne[0] % b.ne[1] == 0
+        return self._new(N.F32, [a.ne[1], ids.ne[0], b.ne[2], 1], "MUL_MAT_ID", [a, b, ids])
+
     def add(self, a, b):
         return self._dup(a, "ADD", [a, b])
 

@@ -39,6 +39,11 @@ these are the reference's outputs on fixed inputs, captured once:
                    inputs (native.rs:109-498) and decoder-sized ones; inputs are
                    regenerated from seeds, the file keeps the outputs
 
+  mul_mat_id.npz   GGML_OP_MUL_MAT_ID on refs.MMID_CASES (every weight type,
+                   broadcast src1, K chunks, repeated experts) through the CPU
+                   backend; inputs are regenerated from the stored seeds by
+                   refs.mmid_case, the file keeps the outputs
+
   decoder_paged.npz  refs.PAGED_SEQS (three sequences: a prompt, then three
                    decode tokens) each alone through the dense-cache decoder
                    step on the CPU backend (refs.paged_ref_run): the logits
@@ -51,7 +56,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    single-token steps, a 3-token chunk): logits and argmax per
                    step and the f16 KV caches after the last one
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -65,8 +70,8 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
-from refs import (FA_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
-                  decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, paged_ref_run,
+from refs import (FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
+                  decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, mmid_case, paged_ref_run,
                   xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
 
@@ -139,6 +144,15 @@ def q5_K_golden(ref) -> None:
     kquant_golden(ref, Q5_K, "q5_K", 71, 72)
 
 
+def mul_mat_id_golden(ref) -> None:
+    out = {}
+    for case in MMID_CASES:
+        b, y, w, inputs = mmid_case(case)
+        (res,) = ref.ir_run(b, w, [], inputs, [(y, np.float32)])
+        out[case[0]] = res
+    np.savez_compressed(HERE / "mul_mat_id.npz", **out)
+
+
 def decoder_paged_golden(ref) -> None:
     c = decoder_tiny_config()
     pl, pa, dl, da = paged_ref_run(ref, c, decoder_weights(c))
@@ -161,6 +175,9 @@ def decoder_golden(ref) -> None:
 
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["mul_mat_id"]:  # only the MUL_MAT_ID fixture
+        mul_mat_id_golden(ref)
+        return
     if sys.argv[1:] == ["decoder_paged"]:  # only the paged-decoder fixture
         decoder_paged_golden(ref)
         return
@@ -243,6 +260,7 @@ def main() -> None:
     core_golden(ref)
     decoder_golden(ref)
     decoder_paged_golden(ref)
+    mul_mat_id_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

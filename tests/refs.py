@@ -1025,3 +1025,38 @@ def paged_ref_run(r, c, weights):
             else:
                 dl[k - 1, s], da[k - 1, s] = lg.reshape(-1), am.reshape(-1)[0]
     return pl, pa, dl, da
+
+
+# ------------------------------------------------------------- MUL_MAT_ID
+# (name, weight type, K, M, n_as, n_used, n_b1, n_tokens, seed): decode-sized
+# (one token, 2 of 6 experts), a token batch with broadcast src1 (n_b1 = 1),
+# K chunks (K > 4096), every weight type, repeated experts within a token.
+MMID_CASES = [
+    ("q4_K_b2_t3", Q4_K, 512, 96, 8, 2, 2, 3, 1),
+    ("q8_0_bcast_t5", Q8_0, 256, 64, 4, 4, 1, 5, 2),
+    ("q6_K_decode", Q6_K, 1024, 40, 6, 2, 1, 1, 3),
+    ("q4_0_kchunks", Q4_0, 4608, 33, 3, 3, 3, 2, 4),
+    ("q5_K_t17_repeats", Q5_K, 256, 17, 5, 2, 2, 17, 5),
+]
+
+
+def mmid_case(case):
+    """(builder, output tensor, host weights [as], inputs [b, ids]) of a MUL_MAT_ID case."""
+    from tensorlisp_amd import graph as G
+    from tensorlisp_amd import synth
+
+    name, t, K, M, n_as, n_used, n_b1, n_tok, seed = case
+    b = G.Builder()
+    w = b.weight(t, [K, M, n_as], "experts")
+    x = b.input(F32, [K, n_b1, n_tok], "b")
+    ids = b.input(I32, [n_used, n_tok], "ids")
+    y = b.mul_mat_id(w, x, ids)
+    b.expand(y)
+    wh = synth.random_blocks(t, 900 + seed, n_as * M, K)
+    xh = synth.normal(910 + seed, (n_tok, n_b1, K))
+    if name.endswith("repeats"):
+        idh = (synth.integers(920 + seed, 0, n_as - 1, n_tok * n_used)).astype(np.int32).reshape(n_tok, n_used)
+    else:
+        rng = np.random.default_rng(930 + seed)
+        idh = np.stack([rng.permutation(n_as)[:n_used] for _ in range(n_tok)]).astype(np.int32)
+    return b, y, [wh], [xh, idh]

@@ -225,3 +225,28 @@ def test_paged_node_validation():
         b, att = _paged_graph(**kw)
         with pytest.raises(N.TlhError, match=msg):
             G.plan(b, [att])
+
+
+# ------------------------------------------------------------- MUL_MAT_ID
+def test_mul_mat_id_plans_and_validates():
+    from refs import MMID_CASES, mmid_case
+
+    for case in MMID_CASES:
+        b, y, _, _ = mmid_case(case)
+        G.plan(b, [y])
+    b = G.Builder()
+    w = b.weight(N.Q4_K, [256, 32, 4])
+    x = b.input(N.F32, [256, 2, 3])
+    ids = b.input(N.F32, [2, 3])
+    y = b._new(N.F32, [32, 2, 3, 1], "MUL_MAT_ID", [w, x, ids])
+    b.expand(y)
+    with pytest.raises(N.TlhError, match="i32 ids"):
+        G.plan(b, [y])
+    b = G.Builder()
+    w = b.weight(N.Q4_K, [256, 32, 4])
+    x = b.input(N.F32, [256, 2, 3])
+    ids = b.input(N.I32, [3, 3])
+    y = b._new(N.F32, [32, 3, 3, 1], "MUL_MAT_ID", [w, x, ids])
+    b.expand(y)
+    with pytest.raises(N.TlhError, match="n_used % n_b1"):
+        G.plan(b, [y])

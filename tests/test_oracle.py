@@ -366,6 +366,25 @@ def test_q5_K_matches_reference_live():
         assert same_bits(o.mul_mat(Q5_K, wq, 8, K, x), y)
 
 
+# ------------------------------------------------------------- MUL_MAT_ID
+def test_mul_mat_id_golden_is_the_per_expert_mul_mat():
+    """The CPU backend's MUL_MAT_ID (mul_mat_id.npz) equals, column by column, the
+    oracle's MUL_MAT of the selected expert's matrix with src1 row (e % n_b1, t),
+    bit for bit (ggml-cpu.c:1460-1640 quantizes src1 once and runs the same vec_dot)."""
+    from refs import MMID_CASES, mmid_case
+
+    o, g = oracle(), gold("mul_mat_id")
+    for case in MMID_CASES:
+        name, t, K, M, n_as, n_used, n_b1, n_tok, _ = case
+        _, _, (wh,), (xh, idh) = mmid_case(case)
+        res = g[name][0]
+        W = wh.reshape(n_as, M, -1)
+        for tt in range(n_tok):
+            for e in range(n_used):
+                want = o.mul_mat(t, W[idh[tt, e]], M, K, xh[tt, e % n_b1][None])
+                assert same_bits(want.reshape(-1), res[tt, e]), (name, tt, e)
+
+
 # -------------------------------------------------------- paged attention
 def _random_paged(seqs, heads, kvh, hs, bs, lens, seed, pool=None):
     """Random paged KV cache with scattered block tables (as BASELINE config 4)."""
