@@ -137,8 +137,15 @@ struct ActLayout {
     int64_t qs_off, d_off, sum_off, q16_off, total;
 };
 
-// q4_K GEMM launches (more than 16 activation columns) also get f16 codes.
-__host__ __device__ constexpr bool act_has_f16(int wtype, int64_t n_cols) { return wtype == TLH_TYPE_Q4_K && n_cols > 16; }
+// Weight types with a tiled prefill GEMM (more than 16 activation columns);
+// the others run it as 16-column slabs of the few-column kernel.
+__host__ __device__ constexpr bool has_gemm(int wtype) {
+    return wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K || wtype == TLH_TYPE_Q8_0 || wtype == TLH_TYPE_Q4_0;
+}
+// q4_K / q5_K GEMM launches also get the activation codes as f16.
+__host__ __device__ constexpr bool act_has_f16(int wtype, int64_t n_cols) {
+    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K) && n_cols > 16;
+}
 
 __host__ __device__ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 

@@ -25,9 +25,11 @@
 // s + 1 (fetched one stage earlier) into the other buffer and fetch s + 2, one
 // barrier per stage.
 //
-// q4_0 / q8_0 weights with N > 16 run through the int8-MFMA few-column kernel
-// (gemv_mfma.hip) in slabs of 16 columns (correct for any N; each slab
-// re-reads the weights).
+// q5_K runs the same kernel with the fifth code bit OR-ed in before the f16
+// conversion (sc * q <= 63 * 31 stays exact). q8_0 / q4_0 have their own
+// int8-MFMA GEMM (gemm_q8.hip). q6_K weights with N > 16 run through the
+// int8-MFMA few-column kernel (gemv_mfma.hip) in slabs of 16 columns (correct
+// for any N; each slab re-reads the weights).
 #include "kernels.hpp"
 
 namespace tlh {
@@ -83,13 +85,17 @@ __device__ __forceinline__ uint4 ldg16(const void *p) {
 // f16 codes (half h of the chunk); at a super-block's first chunk also the
 // token's scale and 16 bsums.
 struct StageRegs {
-    uint4 wq, hdr;
+    uint4 wq, hdr, qh;  // qh: q5_K's fifth bits of the thread's 16 elements of each run
     uint4 x[4];
     uint4 bs0, bs1;
     float dx;
 };
 
+template <int WT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_gemm_q4k(const MatmulArgs a) {
+    constexpr bool Q5 = WT == TLH_TYPE_Q5_K;
+    constexpr int SB = Q5 ? Q5_K_BYTES : Q4_K_BYTES;
+    constexpr int QS = Q5 ? 48 : 16;  // offset of the nibble bytes
     __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -114,9 +120,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto fetch = [&](int64_t stage, StageRegs &r) {
         const int64_t sb = stage >> 2;
         const int j = (int)(stage & 3);
-        const uint8_t *blk = wrow + sb * Q4_K_BYTES;
+        const uint8_t *blk = wrow + sb * SB;
         r.hdr = ldg16(blk);
-        r.wq = ldg16(blk + 16 + 32 * j + 16 * sh);
+        r.wq = ldg16(blk + QS + 32 * j + 16 * sh);
+        if constexpr (Q5) r.qh = ldg16(blk + 16 + 16 * sh);
         const _Float16 *xq = xrow + sb * QKK + 64 * j + 32 * sh;
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.x[i] = *(const uint4 *)(xq + 8 * i);
@@ -139,11 +146,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         const half2_t nsl2 = {(_Float16)(-1024 * sclo), (_Float16)(-1024 * sclo)};
         const half2_t nsh2 = {(_Float16)(-1024 * schi), (_Float16)(-1024 * schi)};
         const uint32_t w[4] = {r.wq.x, r.wq.y, r.wq.z, r.wq.w};
+        const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
         uint32_t lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            nib4_to_h(w[i] & 0x0f0f0f0fu, sl2, nsl2, lo[2 * i], lo[2 * i + 1]);
-            nib4_to_h((w[i] >> 4) & 0x0f0f0f0fu, sh2, nsh2, hi[2 * i], hi[2 * i + 1]);
+            uint32_t cl = w[i] & 0x0f0f0f0fu, ch = (w[i] >> 4) & 0x0f0f0f0fu;
+            if constexpr (Q5) {  // codes 0..31: (1024 + n) stays exact in f16
+                cl |= ((qh[i] >> (2 * j)) & 0x01010101u) << 4;
+                ch |= ((qh[i] >> (2 * j + 1)) & 0x01010101u) << 4;
+            }
+            nib4_to_h(cl, sl2, nsl2, lo[2 * i], lo[2 * i + 1]);
+            nib4_to_h(ch, sh2, nsh2, hi[2 * i], hi[2 * i + 1]);
         }
         // low nibbles: k = 16h + i (chunks 2h, 2h+1); high nibbles: k = 32 + 16h + i (chunks 4+2h, 5+2h)
         _Float16 *ar = sm.A[buf][srow];
@@ -279,10 +292,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 }
 
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
-    if (a.wtype == TLH_TYPE_Q4_K) {
+    if (a.wtype == TLH_TYPE_Q8_0 || a.wtype == TLH_TYPE_Q4_0) return launch_gemm_q8(a, stream);
+    if (a.wtype == TLH_TYPE_Q4_K || a.wtype == TLH_TYPE_Q5_K) {
         const dim3 grid((unsigned)((a.N + GBN - 1) / GBN), (unsigned)((a.M + GBM - 1) / GBM),
                         (unsigned)(a.ne12 * a.ne13));
-        hipLaunchKernelGGL(k_gemm_q4k, grid, dim3(256), 0, stream, a);
+        if (a.wtype == TLH_TYPE_Q4_K) hipLaunchKernelGGL(k_gemm_q4k<TLH_TYPE_Q4_K>, grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(k_gemm_q4k<TLH_TYPE_Q5_K>, grid, dim3(256), 0, stream, a);
         return check_launch("gemm_q4k");
     }
     for (int64_t c = 0; c < a.N; c += 16) {

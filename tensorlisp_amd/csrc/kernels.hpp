@@ -70,6 +70,8 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
 bool gemv_mfma_supported(int64_t N);
 int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches);
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
+// Tiled prefill GEMM for q8_0 / q4_0 weights (gemm_q8.hip), any N.
+tlh_status launch_gemm_q8(const MatmulArgs &a, hipStream_t stream);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
 // Dense FLASH_ATTN_EXT over f16 K/V (flash_attn.hip). Strides in bytes;

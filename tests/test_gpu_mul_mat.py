@@ -290,3 +290,18 @@ def test_q4K_mfma_gemm_tiles(gpu, M, K, n):
     x = synth.normal(1011 + n, (n, K))
     y = host(N.mul_mat(Q4_K, dev(w), M, K, dev(x)))
     close(y, oracle().mul_mat(Q4_K, w, M, K, x), f"{M}x{K} n={n}")
+
+
+@pytest.mark.parametrize("t,M,K", [(Q8_0, 77, 4096), (Q4_0, 77, 4096), (Q8_0, 130, 160), (Q4_0, 64, 8224),
+                                   (Q5_K, 200, 4096), (Q5_K, 77, 14336), (Q8_0, 300, 14336)],
+                         ids=["q8_0", "q4_0", "q8_0-K160", "q4_0-K8224", "q5_K", "q5_K-K14336", "q8_0-K14336"])
+@pytest.mark.parametrize("n", [17, 129, 300])
+def test_prefill_gemm_tiles(gpu, t, M, K, n):
+    """The tiled prefill GEMMs (q8_0 / q4_0: int8 MFMA per 32-element block,
+    gemm_q8.hip; q5_K: the f16-MFMA k-quant GEMM) over row and token tails, K
+    not a multiple of the 128-element stage, and K chunks up to 14336."""
+    w = synth.random_blocks(t, 990 + K + M, M, K)
+    x = synth.normal(991 + n, (n, K))
+    y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
+    rows = np.arange(M) if M <= 130 else np.unique(synth.integers(992, 0, M - 1, 96))
+    close(y[:, rows], oracle().mul_mat(t, w[rows], len(rows), K, x, nthreads=16), f"{NAMES[t]} {M}x{K} n={n}")
