@@ -102,7 +102,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int wm = wave >> 1, wn = wave & 1;  // wave tile position (2 x 2)
     const int64_t K = a.K;
     const int64_t nsb = K / QKK;
-    const int64_t batch = blockIdx.z;
+    const int64_t batches = a.ne12 * a.ne13;
+    const int64_t batch = blockIdx.z % batches, kc = blockIdx.z / batches;  // K chunk kc of gridDim.z / batches
     const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
     const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
     const ActView act = act_view(a.act, TLH_TYPE_Q8_K, K, a.N_total * a.ne12 * a.ne13);
@@ -201,13 +202,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 
     const int lr = lane & 31, lg = lane >> 5;  // MFMA operand row/col and k-group
-    const int64_t stages = nsb * 4;
+    // this workgroup's super-blocks: chunk kc of equal shares (stage indices are global)
+    const int64_t nkc = gridDim.z / batches, share = (nsb + nkc - 1) / nkc;
+    const int64_t sb0 = kc * share, sb1 = sb0 + share < nsb ? sb0 + share : nsb;
+    const int64_t g0 = 4 * sb0, stages = 4 * sb1;
     StageRegs pre;
-    fetch(0, pre);
-    commit(0, pre);
-    if (stages > 1) fetch(1, pre);
+    if (g0 < stages) {
+        fetch(g0, pre);
+        commit(g0, pre);
+        if (g0 + 1 < stages) fetch(g0 + 1, pre);
+    }
     lds_barrier();
-    for (int64_t st = 0; st < stages; ++st) {
+    for (int64_t st = g0; st < stages; ++st) {
         const int buf = (int)(st & 1);
 #pragma unroll
         for (int t = 0; t < GBK / 16; ++t) {
@@ -272,15 +278,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         lds_barrier();
     }
 
-    // store: lane holds token n = lane % 32 of each 32 x 32 tile and rows 8q + 4g + (0..3)
+    // store: lane holds token n = lane % 32 of each 32 x 32 tile and rows 8q + 4g + (0..3);
+    // with K chunks, to this chunk's partials [chunk][batch][N][M]
     char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
+    float *pbase = nkc > 1 ? a.part + (kc * batches + batch) * a.N * a.M : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int jn = 0; jn < 2; ++jn) {
             const int64_t n = n_base + 64 * wn + 32 * jn + lr;
             if (n >= a.N) continue;
-            float *drow = (float *)(dbase + (a.n0 + n) * a.d_nb1);
+            float *drow = pbase ? pbase + n * a.M : (float *)(dbase + (a.n0 + n) * a.d_nb1);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t m = m_base + 64 * wm + 32 * i + 8 * q + 4 * lg;
@@ -291,14 +299,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 }
 
+int gemm_ksplit(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches) {
+    if (!has_gemm(wtype) || N <= 16) return 1;
+    constexpr int64_t CUS = 256;  // MI355X
+    const int64_t tiles = (N + 127) / 128 * ((M + 127) / 128) * batches;
+    if (tiles >= CUS) return 1;  // two workgroups fit a CU: up to 512 tiles run in one wave
+    // stages of 256 elements (k-quants: a super-block; q8_0 / q4_0: 2 stages of 4 blocks)
+    const int64_t units = (K + 255) / 256, min_units = 4;
+    int64_t ks = (2 * CUS + tiles - 1) / tiles;
+    if (ks > units / min_units) ks = units / min_units;
+    if (ks > 16) ks = 16;
+    return ks > 1 ? (int)ks : 1;
+}
+
+int64_t gemm_partial_bytes(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches) {
+    const int ks = gemm_ksplit(wtype, M, N, K, batches);
+    return ks > 1 ? (int64_t)ks * batches * N * M * 4 : 0;
+}
+
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
-    if (a.wtype == TLH_TYPE_Q8_0 || a.wtype == TLH_TYPE_Q4_0) return launch_gemm_q8(a, stream);
+    const int64_t batches = a.ne12 * a.ne13;
+    const int ks = gemm_ksplit(a.wtype, a.M, a.N, a.K, batches);
+    if (ks > 1 && !a.part) return set_error(TLH_INVALID, "gemm: a K split of %d needs a partials buffer", ks);
+    if (a.wtype == TLH_TYPE_Q8_0 || a.wtype == TLH_TYPE_Q4_0) {
+        const tlh_status st = launch_gemm_q8(a, ks, stream);
+        return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
+    }
     if (a.wtype == TLH_TYPE_Q4_K || a.wtype == TLH_TYPE_Q5_K) {
-        const dim3 grid((unsigned)((a.N + GBN - 1) / GBN), (unsigned)((a.M + GBM - 1) / GBM),
-                        (unsigned)(a.ne12 * a.ne13));
+        const dim3 grid((unsigned)((a.N + GBN - 1) / GBN), (unsigned)((a.M + GBM - 1) / GBM), (unsigned)(batches * ks));
         if (a.wtype == TLH_TYPE_Q4_K) hipLaunchKernelGGL(k_gemm_q4k<TLH_TYPE_Q4_K>, grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL(k_gemm_q4k<TLH_TYPE_Q5_K>, grid, dim3(256), 0, stream, a);
-        return check_launch("gemm_q4k");
+        const tlh_status st = check_launch("gemm_q4k");
+        return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
     }
     for (int64_t c = 0; c < a.N; c += 16) {
         MatmulArgs s = a;

@@ -72,7 +72,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int wm = wave >> 1, wn = wave & 1;
     const int64_t K = a.K;
     const int64_t nblk = K / QK;
-    const int64_t batch = blockIdx.z;
+    const int64_t batches = a.ne12 * a.ne13;
+    const int64_t batch = blockIdx.z % batches, kc = blockIdx.z / batches;  // K chunk kc of gridDim.z / batches
     const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
     const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
     const ActView act = act_view(a.act, TLH_TYPE_Q8_0, K, mm_act_rows(a));
@@ -146,14 +147,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             for (int r = 0; r < 16; ++r) acc[i][jn][r] = 0.0f;
 
     const int lr = lane & 31, lg = lane >> 5;  // operand row / column; k half of the block
-    const int64_t stages = (nblk + QSB - 1) / QSB;
+    // this workgroup's stages: chunk kc of equal shares (stage indices are global)
+    const int64_t nst = (nblk + QSB - 1) / QSB, nkc = gridDim.z / batches, share = (nst + nkc - 1) / nkc;
+    const int64_t g0 = kc * share, stages = g0 + share < nst ? g0 + share : nst;
     Q8StageRegs pre;
-    fetch(0, pre);
-    commit(0, pre);
-    if (stages > 1) fetch(1, pre);
+    if (g0 < stages) {
+        fetch(g0, pre);
+        commit(g0, pre);
+        if (g0 + 1 < stages) fetch(g0 + 1, pre);
+    }
     lds_barrier();
     const v16i32 zero = {};
-    for (int64_t st = 0; st < stages; ++st) {
+    for (int64_t st = g0; st < stages; ++st) {
         const int buf = (int)(st & 1);
         // one block at a time: its four products are finished before the next
         // block's MFMAs issue (all of them in flight at once would hold 256
@@ -197,14 +202,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 
     // lane holds token n = lane % 32 of each 32 x 32 tile and rows 8q + 4 lg + (0..3)
+    // (with K chunks, to this chunk's partials [chunk][batch][N][M])
     char *dbase = (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
+    float *pbase = nkc > 1 ? a.part + (kc * batches + batch) * a.N * a.M : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int jn = 0; jn < 2; ++jn) {
             const int64_t n = n_base + 64 * wn + 32 * jn + lr;
             if (n >= a.N) continue;
-            float *drow = (float *)(dbase + (a.n0 + n) * a.d_nb1);
+            float *drow = pbase ? pbase + n * a.M : (float *)(dbase + (a.n0 + n) * a.d_nb1);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t m = m_base + 64 * wm + 32 * i + 8 * q + 4 * lg;
@@ -215,8 +222,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 }
 
-tlh_status launch_gemm_q8(const MatmulArgs &a, hipStream_t stream) {
-    const dim3 grid((unsigned)((a.N + QBN - 1) / QBN), (unsigned)((a.M + QBM - 1) / QBM), (unsigned)(a.ne12 * a.ne13));
+tlh_status launch_gemm_q8(const MatmulArgs &a, int ksplit, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.N + QBN - 1) / QBN), (unsigned)((a.M + QBM - 1) / QBM),
+                    (unsigned)(a.ne12 * a.ne13 * ksplit));
     if (a.wtype == TLH_TYPE_Q8_0) hipLaunchKernelGGL(k_gemm_q8<TLH_TYPE_Q8_0>, grid, dim3(256), 0, stream, a);
     else if (a.wtype == TLH_TYPE_Q4_0) hipLaunchKernelGGL(k_gemm_q8<TLH_TYPE_Q4_0>, grid, dim3(256), 0, stream, a);
     else return set_error(TLH_UNSUPPORTED, "gemm_q8: weight type %d", a.wtype);

@@ -588,6 +588,12 @@ __global__ void __launch_bounds__(256) k_gemv_mfma_reduce(const MatmulArgs a, in
     *(float *)((char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3 + (a.n0 + n) * a.d_nb1 + m * 4) = s;
 }
 
+tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t stream) {
+    const int64_t total = a.N * a.M * a.ne12 * a.ne13;
+    hipLaunchKernelGGL(k_gemv_mfma_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, chunks);
+    return check_launch("partial_reduce");
+}
+
 static int64_t sk_share(int64_t K, int64_t &chunks) {
     const int64_t units = (K + 255) / 256;
     const int64_t per = (int64_t)SK_MAXW * sk_ks<TLH_TYPE_Q4_K>();

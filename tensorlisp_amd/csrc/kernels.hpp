@@ -70,8 +70,16 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
 bool gemv_mfma_supported(int64_t N);
 int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches);
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
-// Tiled prefill GEMM for q8_0 / q4_0 weights (gemm_q8.hip), any N.
-tlh_status launch_gemm_q8(const MatmulArgs &a, hipStream_t stream);
+// Tiled prefill GEMM for q8_0 / q4_0 weights (gemm_q8.hip), any N; with
+// ksplit > 1 each K chunk writes a.part and a reduce launch sums them.
+tlh_status launch_gemm_q8(const MatmulArgs &a, int ksplit, hipStream_t stream);
+// dst (strided, columns n0..) = sum over `chunks` partials [chunk][batch][N][M] of a.part, in chunk order
+tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t stream);
+// K chunks of the tiled prefill GEMMs: a launch of fewer 128 x 128 tiles than
+// CUs splits K into up to 512 / tiles chunks (whole stages per chunk, at least four super-blocks /
+// sixteen q8_0 blocks each), and the bytes of its partial sums.
+int gemm_ksplit(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches);
+int64_t gemm_partial_bytes(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
 
 // Dense FLASH_ATTN_EXT over f16 K/V (flash_attn.hip). Strides in bytes;

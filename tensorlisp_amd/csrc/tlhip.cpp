@@ -378,7 +378,8 @@ static int64_t mm_act_bytes(const MulMatShape &s) {
 static int64_t mm_partial_bytes(const MulMatShape &s) {
     int ksplit, upw;
     const bool reg = s.N <= 2 && gemv_reg_geometry(s.K, ksplit, upw);
-    const bool mfma = s.N <= 16 ? !reg : !has_gemm(s.wtype);
+    if (s.N > 16 && has_gemm(s.wtype)) return align_up(gemm_partial_bytes(s.wtype, s.M, s.N, s.K, s.ne12 * s.ne13), 256);
+    const bool mfma = s.N <= 16 ? !reg : true;
     return mfma ? align_up(gemv_mfma_partial_bytes(s.K, s.M, s.N, s.ne12 * s.ne13), 256) : 0;
 }
 

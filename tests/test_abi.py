@@ -65,7 +65,12 @@ def test_mul_mat_scratch_sizes(wt, n):
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
     sums = n * (K // 16) * 2 if at == N.Q8_K else n * (K // 32) * 4
     f16_codes = n * K * 2 if wt == N.Q4_K and n > 16 else 0  # q4_K GEMM launches also stage f16 codes
-    assert nbytes == al(al(al(al(n * K) + n * (K // be) * 4) + sums) + f16_codes)
+    # a GEMM of fewer 128 x 128 tiles than CUs (256) splits K into up to 512 / tiles
+    # chunks of at least 4 x 256 elements (at most 16) with f32 partials [chunk][N][M]
+    tiles = -(-n // 128) * -(-M // 128)
+    ks = 1 if n <= 16 or tiles >= 256 else max(1, min(-(-512 // tiles), K // 256 // 4, 16))
+    parts = al(ks * n * M * 4) if ks > 1 else 0
+    assert nbytes == al(al(al(al(n * K) + n * (K // be) * 4) + sums) + f16_codes) + parts
 
 
 @pytest.mark.parametrize("wt", [N.Q4_0, N.Q8_0, N.Q4_K])

@@ -305,3 +305,16 @@ def test_prefill_gemm_tiles(gpu, t, M, K, n):
     y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
     rows = np.arange(M) if M <= 130 else np.unique(synth.integers(992, 0, M - 1, 96))
     close(y[:, rows], oracle().mul_mat(t, w[rows], len(rows), K, x, nthreads=16), f"{NAMES[t]} {M}x{K} n={n}")
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q8_0, Q4_0], ids=["q4_K", "q5_K", "q8_0", "q4_0"])
+@pytest.mark.parametrize("M,K,n", [(1024, 4096, 40), (512, 14336, 200), (96, 2560, 33)])
+def test_prefill_gemm_k_chunks(gpu, t, M, K, n):
+    """Few output tiles: the tiled GEMM splits K into chunks whose partial sums are
+    added in chunk order by a second launch (shares of whole stages, trailing
+    chunks possibly empty)."""
+    w = synth.random_blocks(t, 1200 + K + M, M, K)
+    x = synth.normal(1201 + n, (n, K))
+    y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
+    rows = np.unique(synth.integers(1202, 0, M - 1, 64))
+    close(y[:, rows], oracle().mul_mat(t, w[rows], len(rows), K, x, nthreads=16), f"{NAMES[t]} {M}x{K} n={n}")
