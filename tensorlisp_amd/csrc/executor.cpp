@@ -181,6 +181,7 @@ class Lowering {
         fuse_norm_chains(out.d);
         fuse_multi_gemv(out.d);
         fuse_rope_rows(out.d);
+        fuse_rope_cast(out.d);
         group_elementwise(out.d);
         group_mul_mats(out.d);
         plan(out);
@@ -621,6 +622,54 @@ class Lowering {
     // K cache write): the rotation writes those cache rows itself, in the
     // cache's type, and the SET_ROWS goes away. Nothing in between may touch
     // the cache.
+    static bool contiguous(const tlh_tensor &t) {
+        const int64_t es = t.ty == TLH_TYPE_F32 ? 4 : t.ty == TLH_TYPE_F16 ? 2 : 0;
+        return es && t.nb[0] == es && t.nb[1] == t.nb[0] * t.ne[0] && t.nb[2] == t.nb[1] * t.ne[1] &&
+               t.nb[3] == t.nb[2] * t.ne[2];
+    }
+    // ROPE whose only reader is a type cast (CPY of its f32 result, possibly
+    // through a RESHAPE, into a new contiguous f32 / f16 tensor): the rope
+    // writes the cast's destination itself, in its own shape. The values are
+    // the same: the rope's f32 result rounded once to the destination type.
+    void fuse_rope_cast(std::vector<Dispatch> &d) {
+        std::vector<char> gone(d.size(), 0);
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &r = d[i];
+            if (!(r.kind == D_CORE && r.core_kind == TLH_CORE_ROPE) || r.op.x[9]) continue;
+            const int32_t rn = node_of(r);
+            if (readers_[rn] != 1) continue;
+            int32_t v = reader_[rn], from = rn;
+            if (v >= 0 && strcmp(g_.t[v].op, "RESHAPE") == 0 && readers_[v] == 1) from = v, v = reader_[v];
+            if (v < 0 || strcmp(g_.t[v].op, "CPY") != 0 || g_.t[v].src[0] != from) continue;
+            size_t j = i + 1;
+            while (j < d.size() && !(d[j].kind == D_CORE && node_of(d[j]) == v)) ++j;
+            if (j == d.size()) continue;
+            const Dispatch &w = d[j];
+            const tlh_tensor &y = r.op.t[4], &c = w.op.t[4];
+            bool ok = y.ty == TLH_TYPE_F32 && contiguous(y) && contiguous(c) &&
+                      y.ne[0] * y.ne[1] * y.ne[2] * y.ne[3] == c.ne[0] * c.ne[1] * c.ne[2] * c.ne[3];
+            for (size_t k = i + 1; k < j && ok; ++k) {
+                std::vector<Place> rd, wr;
+                places(d[k], rd, wr);
+                for (const Place &p : rd) ok = ok && !same_root(p, w.dst);
+                for (const Place &p : wr) ok = ok && !same_root(p, w.dst);
+            }
+            if (!ok) continue;
+            tlh_tensor out = y;  // the rope's shape, the cast's type and bytes
+            out.ty = c.ty;
+            out.nb[0] = c.nb[0];
+            for (int k = 1; k < 4; ++k) out.nb[k] = out.nb[k - 1] * out.ne[k - 1];
+            r.op.t[4] = out;
+            r.dst = w.dst;
+            r.pos_last = std::max(r.pos_last, w.pos_last);
+            gone[j] = 1;
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
     void fuse_rope_rows(std::vector<Dispatch> &d) {
         std::vector<char> gone(d.size(), 0);
         for (size_t i = 0; i < d.size(); ++i) {
