@@ -56,6 +56,7 @@ struct Dispatch {
     // D_PAGED_ATTN: geometry and scale (pointers are set per launch);
     // D_PAGED_WRITE: tokens, kv heads, head size, block size
     tlh_paged_attention_args pa{};
+    int pa_f32 = 0;  // D_PAGED_ATTN: dst is a fused cast's f32 tensor
     int32_t pw[4] = {0, 0, 0, 0};
 };
 
@@ -182,6 +183,7 @@ class Lowering {
         fuse_multi_gemv(out.d);
         fuse_rope_rows(out.d);
         fuse_rope_cast(out.d);
+        fuse_paged_cast(out.d);
         group_elementwise(out.d);
         group_mul_mats(out.d);
         plan(out);
@@ -670,6 +672,45 @@ class Lowering {
         d.swap(out);
     }
 
+    // paged attention whose only reader is a cast of its f16 result to a
+    // contiguous f32 tensor (possibly through a RESHAPE): the attention's
+    // merge launch writes the widened values there.
+    void fuse_paged_cast(std::vector<Dispatch> &d) {
+        std::vector<char> gone(d.size(), 0);
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &r = d[i];
+            if (r.kind != D_PAGED_ATTN) continue;
+            const int32_t rn = node_of(r);
+            if (readers_[rn] != 1) continue;
+            int32_t v = reader_[rn], from = rn;
+            if (v >= 0 && strcmp(g_.t[v].op, "RESHAPE") == 0 && readers_[v] == 1) from = v, v = reader_[v];
+            if (v < 0 || strcmp(g_.t[v].op, "CPY") != 0 || g_.t[v].src[0] != from) continue;
+            size_t j = i + 1;
+            while (j < d.size() && !(d[j].kind == D_CORE && node_of(d[j]) == v)) ++j;
+            if (j == d.size()) continue;
+            const Dispatch &w = d[j];
+            const tlh_tensor &c = w.op.t[4];
+            bool ok = c.ty == TLH_TYPE_F32 && contiguous(c) && contiguous(r.op.t[4]) &&
+                      c.ne[0] * c.ne[1] * c.ne[2] * c.ne[3] ==
+                          r.op.t[4].ne[0] * r.op.t[4].ne[1] * r.op.t[4].ne[2] * r.op.t[4].ne[3];
+            for (size_t k = i + 1; k < j && ok; ++k) {
+                std::vector<Place> rd, wr;
+                places(d[k], rd, wr);
+                for (const Place &p : rd) ok = ok && !same_root(p, w.dst);
+                for (const Place &p : wr) ok = ok && !same_root(p, w.dst);
+            }
+            if (!ok) continue;
+            r.pa_f32 = 1;
+            r.dst = w.dst;
+            r.pos_last = std::max(r.pos_last, w.pos_last);
+            gone[j] = 1;
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
     void fuse_rope_rows(std::vector<Dispatch> &d) {
         std::vector<char> gone(d.size(), 0);
         for (size_t i = 0; i < d.size(); ++i) {
@@ -1004,7 +1045,12 @@ struct tlh_program {
                 a.v_cache = src[2];
                 a.block_tables = (const int32_t *)src[3];
                 a.context_lens = (const int32_t *)src[4];
-                st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
+                if (x.pa_f32) {
+                    a.out = nullptr;
+                    st = launch_paged_attention(a, scratch, x.scratch_bytes, s, (float *)dst);
+                } else {
+                    st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
+                }
                 break;
             }
             case D_MUL_MAT_ID:

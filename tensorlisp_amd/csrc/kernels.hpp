@@ -124,8 +124,9 @@ tlh_status launch_core_multi(int n, const int *kinds, const tlh_op *ops, const v
 tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,
                        hipStream_t stream);
 
+// out32 != null: the f16 results are written widened to f32 there instead of a.out
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
-                                  hipStream_t stream);
+                                  hipStream_t stream, float *out32 = nullptr);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,

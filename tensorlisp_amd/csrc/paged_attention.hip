@@ -226,7 +226,8 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
 // round of independent loads and folds them into a running (max, sum, acc)
 // rescaled online; longer contexts take further rounds.
 template <int HS>
-__global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, const float *__restrict__ scratch,
+__global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, float *__restrict__ out32,
+                                                           const float *__restrict__ scratch,
                                                            const int32_t *__restrict__ lens, int num_heads, int P) {
     constexpr int CHUNK = 16;
     const int head = blockIdx.x, seq = blockIdx.y;
@@ -261,7 +262,10 @@ __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict_
             }
             M = Mn;
         }
-        out[((int64_t)seq * num_heads + head) * HS + d] = f2h(a * (1.0f / (lsum + 1e-6f)));
+        const uint16_t h = f2h(a * (1.0f / (lsum + 1e-6f)));
+        const int64_t o = ((int64_t)seq * num_heads + head) * HS + d;
+        if (out32) out32[o] = h2f(h);  // the f16 result widened (a cast to f32 fused into this store)
+        else out[o] = h;
     }
 }
 
@@ -274,7 +278,7 @@ size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
 }
 
 template <int HS, int BS>
-static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream) {
+static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32) {
     const int P = pa_partitions(a);
     const int G = a.num_heads / a.num_kv_heads;
     int gc = G < 16 ? G : 16;  // query heads per workgroup: a divisor of G, at most 16
@@ -285,28 +289,29 @@ static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStr
                        a.block_tables, a.context_lens, a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale,
                        P, scratch);
     hipLaunchKernelGGL((k_paged_attn_reduce<HS>), dim3(a.num_heads, a.num_seqs), dim3(HS < 256 ? HS : 256), 0, stream,
-                       (uint16_t *)a.out, (const float *)scratch, a.context_lens, a.num_heads, P);
+                       (uint16_t *)a.out, out32, (const float *)scratch, a.context_lens, a.num_heads, P);
 }
 
 template <int HS>
-static void launch_pa1(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream) {
+static void launch_pa1(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32) {
     switch (a.block_size) {
-    case 8: launch_pa2<HS, 8>(a, scratch, stream); break;
-    case 16: launch_pa2<HS, 16>(a, scratch, stream); break;
-    default: launch_pa2<HS, 32>(a, scratch, stream); break;
+    case 8: launch_pa2<HS, 8>(a, scratch, stream, out32); break;
+    case 16: launch_pa2<HS, 16>(a, scratch, stream, out32); break;
+    default: launch_pa2<HS, 32>(a, scratch, stream, out32); break;
     }
 }
 
-tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t, hipStream_t stream) {
+tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t, hipStream_t stream,
+                                  float *out32) {
     float *s = (float *)scratch;
     switch (a.head_size) {
-    case 64: launch_pa1<64>(a, s, stream); break;
-    case 80: launch_pa1<80>(a, s, stream); break;
-    case 96: launch_pa1<96>(a, s, stream); break;
-    case 112: launch_pa1<112>(a, s, stream); break;
-    case 128: launch_pa1<128>(a, s, stream); break;
-    case 192: launch_pa1<192>(a, s, stream); break;
-    case 256: launch_pa1<256>(a, s, stream); break;
+    case 64: launch_pa1<64>(a, s, stream, out32); break;
+    case 80: launch_pa1<80>(a, s, stream, out32); break;
+    case 96: launch_pa1<96>(a, s, stream, out32); break;
+    case 112: launch_pa1<112>(a, s, stream, out32); break;
+    case 128: launch_pa1<128>(a, s, stream, out32); break;
+    case 192: launch_pa1<192>(a, s, stream, out32); break;
+    case 256: launch_pa1<256>(a, s, stream, out32); break;
     default: return set_error(TLH_INVALID, "paged_attention: head_size %d", a.head_size);
     }
     return check_launch("paged_attention");
