@@ -58,6 +58,7 @@ struct Dispatch {
     tlh_paged_attention_args pa{};
     int pa_f32 = 0;  // D_PAGED_ATTN: dst is a fused cast's f32 tensor
     int32_t pw[4] = {0, 0, 0, 0};
+    int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
 };
 
 // ggml type traits used for byte sizes: (block elements, block bytes)
@@ -184,6 +185,7 @@ class Lowering {
         fuse_rope_rows(out.d);
         fuse_rope_cast(out.d);
         fuse_paged_cast(out.d);
+        fuse_cache_write_cast(out.d);
         group_elementwise(out.d);
         group_mul_mats(out.d);
         plan(out);
@@ -672,6 +674,44 @@ class Lowering {
         d.swap(out);
     }
 
+    // A cache write whose key or value is a cast (CPY) of a contiguous f32
+    // tensor read by nothing else: the write reads the f32 source and rounds it
+    // to f16 itself (the same rounding the cast does).
+    void fuse_cache_write_cast(std::vector<Dispatch> &d) {
+        std::vector<char> gone(d.size(), 0);
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &w = d[i];
+            if (w.kind != D_PAGED_WRITE) continue;
+            const int32_t wn = node_of(w);  // (w.pos moves to the first fused node below)
+            for (int s = 0; s < 2; ++s) {
+                const int32_t cn = g_.t[wn].src[s];
+                if (cn < 0 || strcmp(g_.t[cn].op, "CPY") != 0 || readers_[cn] != 1) continue;
+                size_t j = 0;
+                while (j < i && !(d[j].kind == D_CORE && !gone[j] && node_of(d[j]) == cn)) ++j;
+                if (j == i) continue;
+                const Dispatch &c = d[j];
+                const tlh_tensor &a = c.op.t[0], &b = c.op.t[4];
+                bool ok = c.core_kind == TLH_CORE_CPY && a.ty == TLH_TYPE_F32 && b.ty == TLH_TYPE_F16 &&
+                          contiguous(a) && contiguous(b) &&
+                          a.ne[0] * a.ne[1] * a.ne[2] * a.ne[3] == b.ne[0] * b.ne[1] * b.ne[2] * b.ne[3];
+                for (size_t k = j + 1; k < i && ok; ++k) {  // nothing in between writes the f32 source
+                    std::vector<Place> rd, wr;
+                    places(d[k], rd, wr);
+                    for (const Place &p : wr) ok = ok && !same_root(p, c.src[0]);
+                }
+                if (!ok) continue;
+                w.src[s] = c.src[0];
+                w.pw_f32[s] = 1;
+                w.pos = std::min(w.pos, c.pos);
+                gone[j] = 1;
+            }
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
     // paged attention whose only reader is a cast of its f16 result to a
     // contiguous f32 tensor (possibly through a RESHAPE): the attention's
     // merge launch writes the widened values there.
@@ -1057,8 +1097,14 @@ struct tlh_program {
                 st = tlh_mul_mat_id(&x.op, src[0], src[1], src[2], dst, scratch, x.scratch_bytes, s);
                 break;
             case D_PAGED_WRITE:
-                st = tlh_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4], x.pw[0], x.pw[1],
-                                           x.pw[2], x.pw[3], s);
+                if (x.pw_f32[0] || x.pw_f32[1])
+                    st = x.pw[0] == 0 ? TLH_OK
+                                      : launch_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4],
+                                                                 x.pw[0], x.pw[1], x.pw[2], x.pw[3], s, x.pw_f32[0] != 0,
+                                                                 x.pw_f32[1] != 0);
+                else
+                    st = tlh_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4], x.pw[0],
+                                               x.pw[1], x.pw[2], x.pw[3], s);
                 break;
             case D_ARGMAX_SPLIT: st = launch_argmax_split(x.op, src[0], dst, scratch, s); break;
             case D_CORE_MULTI: {

@@ -128,8 +128,10 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
                                   hipStream_t stream, float *out32 = nullptr);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
+// key_f32 / value_f32: that source is f32 and is rounded to f16 on the way
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,
-                                    int block_size, hipStream_t stream);
+                                    int block_size, hipStream_t stream, bool key_f32 = false,
+                                    bool value_f32 = false);
 
 }  // namespace tlh

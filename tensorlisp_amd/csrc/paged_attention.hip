@@ -320,8 +320,20 @@ tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scrat
 // ------------------------------------------------------- reshape_and_cache
 // reshape_and_cache_kernel.cu:31-84: one workgroup per token, 16-byte pieces
 // of 8 dims; keys land as one contiguous piece, values scatter along slots.
-__global__ void __launch_bounds__(256) k_reshape_and_cache(const uint16_t *__restrict__ key,
-                                                           const uint16_t *__restrict__ value,
+// 8 consecutive elements as f16 bits: an f16 source as is, an f32 source
+// rounded (the executor folds a preceding f32 -> f16 cast into the write)
+template <bool F32> __device__ __forceinline__ uint4 load8_h(const void *base, int64_t e) {
+    if constexpr (!F32) {
+        return *(const uint4 *)((const uint16_t *)base + e);
+    } else {
+        const float4 a = *(const float4 *)((const float *)base + e), b = *(const float4 *)((const float *)base + e + 4);
+        return make_uint4((uint32_t)f2h(a.x) | ((uint32_t)f2h(a.y) << 16), (uint32_t)f2h(a.z) | ((uint32_t)f2h(a.w) << 16),
+                          (uint32_t)f2h(b.x) | ((uint32_t)f2h(b.y) << 16), (uint32_t)f2h(b.z) | ((uint32_t)f2h(b.w) << 16));
+    }
+}
+
+template <bool K32, bool V32>
+__global__ void __launch_bounds__(256) k_reshape_and_cache(const void *__restrict__ key, const void *__restrict__ value,
                                                            uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                                            const int64_t *__restrict__ slots, int kvh, int hs,
                                                            int bs) {
@@ -334,9 +346,9 @@ __global__ void __launch_bounds__(256) k_reshape_and_cache(const uint16_t *__res
     for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
         const int h = c / (hs / 8), ch = c % (hs / 8);
         const int64_t src = (int64_t)t * kvh * hs + 8 * (int64_t)c;
-        const uint4 kk = *(const uint4 *)(key + src);
+        const uint4 kk = load8_h<K32>(key, src);
         *(uint4 *)(kc + (((blk * kvh + h) * (hs / 8) + ch) * bs + off) * 8) = kk;
-        const uint4 vv = *(const uint4 *)(value + src);
+        const uint4 vv = load8_h<V32>(value, src);
         const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
         uint16_t *vdst = vc + ((blk * kvh + h) * (int64_t)hs + 8 * ch) * bs + off;
 #pragma unroll
@@ -349,12 +361,13 @@ __global__ void __launch_bounds__(256) k_reshape_and_cache(const uint16_t *__res
 
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,
-                                    int block_size, hipStream_t stream) {
+                                    int block_size, hipStream_t stream, bool key_f32, bool value_f32) {
     if ((((uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache) & 15) != 0)
         return set_error(TLH_INVALID, "reshape_and_cache: key, value and key cache must be 16-byte aligned");
-    hipLaunchKernelGGL(k_reshape_and_cache, dim3(num_tokens), dim3(128), 0, stream, (const uint16_t *)key,
-                       (const uint16_t *)value, (uint16_t *)k_cache, (uint16_t *)v_cache, slots, num_kv_heads,
-                       head_size, block_size);
+    auto k = key_f32 ? (value_f32 ? k_reshape_and_cache<true, true> : k_reshape_and_cache<true, false>)
+                     : (value_f32 ? k_reshape_and_cache<false, true> : k_reshape_and_cache<false, false>);
+    hipLaunchKernelGGL(k, dim3(num_tokens), dim3(128), 0, stream, key, value, (uint16_t *)k_cache,
+                       (uint16_t *)v_cache, slots, num_kv_heads, head_size, block_size);
     return check_launch("reshape_and_cache");
 }
 
