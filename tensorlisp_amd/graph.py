@@ -577,11 +577,12 @@ def decoder_decode_paged(c: DecoderConfig, pc: PagedConfig, n_seqs: int) -> Page
 
     def attend(i, q, k, v):
         kc, vc = pools[i]
+        q16 = b.cast(q, N.F16)
+        b.expand(q16)  # ahead of the cache write, next to K's rope (one launch for both)
         k16 = b.cast(b.reshape(k, c.n_embd_kv, S), N.F16)
         v16 = b.cast(v, N.F16)
         b.expand(b.paged_cache_write(k16, v16, kc, vc, slots, pc.block_size, c.n_head_kv))
-        att = b.paged_attention(b.cast(q, N.F16), kc, vc, tables, lens, pc.block_size, pc.max_ctx, scale,
-                                c.n_head_kv)
+        att = b.paged_attention(q16, kc, vc, tables, lens, pc.block_size, pc.max_ctx, scale, c.n_head_kv)
         return b.cast(b.reshape(att, c.n_embd, S), N.F32)
 
     logits, am = _decoder_body(b, c, W, tokens, pos, S, attend, False)
