@@ -32,7 +32,8 @@ struct Place {
 };
 
 enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
-                    D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE, D_MUL_MAT_ID };
+                    D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE, D_MUL_MAT_ID,
+                    D_MM_COMPUTE_MULTI };
 constexpr int NSRC = 5;  // sources a dispatch reads (the paged nodes have five)
 struct Dispatch {
     DispatchKind kind;
@@ -46,6 +47,7 @@ struct Dispatch {
     size_t scratch_bytes = 0;
     // D_MULTI_GEMV: the member MUL_MATs (shared activation in src[1])
     int nmem = 0;
+    int mpos[3] = {0, 0, 0};  // D_MM_COMPUTE_MULTI: the members' node positions
     tlh_op mop[3];
     Place mw[3], mdst[3];
     // D_CORE_MULTI: independent element-wise ops in one launch
@@ -188,6 +190,7 @@ class Lowering {
         fuse_cache_write_cast(out.d);
         group_elementwise(out.d);
         group_mul_mats(out.d);
+        merge_mm_computes(out.d);
         plan(out);
         return TLH_OK;
     }
@@ -897,6 +900,40 @@ class Lowering {
         d.swap(out);
     }
 
+    // Consecutive compute halves of one quantization group (3..16 columns,
+    // K <= 4096) become one few-column MFMA launch over their rows.
+    void merge_mm_computes(std::vector<Dispatch> &d) {
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size();) {
+            size_t j = i + 1;
+            if (d[i].kind == D_MM_COMPUTE) {
+                const tlh_op *ops[3] = {&d[i].op, nullptr, nullptr};
+                while (j < d.size() && j - i < 3 && d[j].kind == D_MM_COMPUTE && d[j].block == d[i].block) {
+                    ops[j - i] = &d[j].op;
+                    if (!mul_mat_compute_multi_ok(ops, (int)(j - i + 1))) break;
+                    ++j;
+                }
+            }
+            if (j - i < 2) {
+                out.push_back(d[i++]);
+                continue;
+            }
+            Dispatch f = d[i];
+            f.kind = D_MM_COMPUTE_MULTI;
+            f.nmem = (int)(j - i);
+            for (size_t k = i; k < j; ++k) {
+                f.mop[k - i] = d[k].op;
+                f.mpos[k - i] = d[k].pos;
+                f.mw[k - i] = d[k].src[0];
+                f.mdst[k - i] = d[k].dst;
+                f.pos_last = std::max(f.pos_last, d[k].pos_last);
+            }
+            out.push_back(f);
+            i = j;
+        }
+        d.swap(out);
+    }
+
     struct Group {
         int64_t first = 0, last = 0;
         size_t bytes = 0;
@@ -999,8 +1036,11 @@ class Lowering {
         }
         for (size_t i = 0; i < n_tensor_blocks; ++i) out.arena_off[out.blocks[i].tensor] = out.blocks[i].off;
         out.node_scratch.assign(n, -1);
-        for (const Dispatch &x : out.d)
+        for (const Dispatch &x : out.d) {
             if (x.block >= 0) out.node_scratch[x.pos] = out.blocks[x.block].off;
+            if (x.block >= 0 && x.kind == D_MM_COMPUTE_MULTI)
+                for (int k = 0; k < x.nmem; ++k) out.node_scratch[x.mpos[k]] = out.blocks[x.block].off;
+        }
         out.arena = arena;
     }
 };
@@ -1091,6 +1131,18 @@ struct tlh_program {
                 } else {
                     st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
                 }
+                break;
+            }
+            case D_MM_COMPUTE_MULTI: {
+                const tlh_op *ops[3];
+                const void *w[3];
+                void *dsts[3];
+                for (int k = 0; k < x.nmem; ++k) {
+                    ops[k] = &x.mop[k];
+                    w[k] = resolve(x.mw[k], state);
+                    dsts[k] = resolve(x.mdst[k], state);
+                }
+                st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s);
                 break;
             }
             case D_MUL_MAT_ID:

@@ -377,13 +377,23 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         const int64_t off = u0 * UB + 16 * (pc - pr[i] * St::PR);  // (KS = 1 for the staged q6_K bytes)
         pofs[i] = pr[i] * a.w_nb1 + (off + 16 <= row_bytes ? off : 0);
     }
-    const uint8_t *wlast = W + (a.M - 1) * a.w_nb1;
-    auto wrow_of = [&](int64_t grp) {
-        const int64_t m = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;  // clamp: loads in bounds
+    // segments (a.nseg > 0): row m of the launch is row m - seg_m0[s] of
+    // matrix s; a 16-row group never straddles two
+    auto seg_of = [&](int64_t m) { return (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]); };
+    auto row_base = [&](int64_t m) {
+        if (a.nseg > 0) {
+            const int sg = seg_of(m);
+            return a.seg_w[sg] + (m - a.seg_m0[sg]) * a.w_nb1;
+        }
         return W + m * a.w_nb1;
     };
+    const uint8_t *wlast = row_base(a.M - 1);
+    auto wrow_of = [&](int64_t grp) {
+        const int64_t m = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;  // clamp: loads in bounds
+        return row_base(m);
+    };
     auto stage_load = [&](St &s, int64_t grp) {
-        const uint8_t *gb = W + grp * 16 * a.w_nb1;  // wave-uniform
+        const uint8_t *gb = row_base(grp * 16);  // wave-uniform
         const int rows_left = (int)(a.M - grp * 16);
 #pragma unroll
         for (int i = 0; i < St::NL; ++i) {
@@ -439,6 +449,11 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     const int ocol = threadIdx.x >> 4, orow = threadIdx.x & 15;
     float *pbase = a.part ? a.part + (((int64_t)blockIdx.y * gridDim.z + batch) * a.N + ocol) * a.M : nullptr;
     auto out_ptr = [&](int64_t grp) {
+        if (a.nseg > 0) {
+            const int64_t m = grp * 16 + orow;
+            const int sg = seg_of(grp * 16);
+            return (float *)((char *)a.seg_dst[sg] + (a.n0 + ocol) * a.seg_d_nb1[sg] + (m - a.seg_m0[sg]) * 4);
+        }
         return pbase ? pbase + grp * 16 + orow : (float *)(dbase + (a.n0 + ocol) * a.d_nb1 + (grp * 16 + orow) * 4);
     };
 

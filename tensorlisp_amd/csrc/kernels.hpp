@@ -43,6 +43,10 @@ struct MatmulArgs {
     int64_t seg_w_nb1[3];
     float *seg_dst[3];
     int64_t seg_m0[4];
+    // the few-column MFMA kernel also takes segments (N <= 16, one K chunk,
+    // segment row counts multiples of 16, one weight row stride): segment s's
+    // outputs go to seg_dst[s] + column * seg_d_nb1[s] bytes
+    int64_t seg_d_nb1[3];
     // MUL_MAT_ID (int8-MFMA few-column kernel only): with ids != null, batch
     // slice z = (e, t) = (z % ne12, z / ne12) multiplies weight matrix
     // ids[e * ids_nb0 + t * ids_nb1] (i32, w_nb2 apart; id_nas matrices) by
@@ -104,6 +108,9 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
 // Up to three MUL_MAT nodes at N = 1 reading one activation with weights of one
 // type and K as one register-GEMV launch (tlhip.cpp); TLH_UNSUPPORTED when the
 // pointers do not allow it.
+bool mul_mat_compute_multi_ok(const tlh_op *const *ops, int n);
+tlh_status mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
+                                 const void *scratch, size_t scratch_bytes, hipStream_t stream);
 bool mul_mat_multi_ok(const tlh_op *const *ops, int n);
 tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n, const void *x,
                          hipStream_t stream);

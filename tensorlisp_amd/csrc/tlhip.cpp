@@ -463,6 +463,56 @@ static bool mm_empty(const MulMatShape &s) { return s.M == 0 || s.N == 0 || s.ne
 // the activation once. mul_mat_multi_ok checks the shapes; mul_mat_multi
 // returns TLH_UNSUPPORTED when the pointers do not allow the fused launch
 // (the caller then runs the nodes one by one).
+// Up to three MUL_MATs with 3..16 columns reading one quantized activation
+// (the same scratch a tlh_mul_mat_quantize filled), weights of one type, K
+// (one chunk: K <= 4096) and row stride, as one int8-MFMA few-column launch
+// over their concatenated rows (each a multiple of 16 but the last).
+bool tlh::mul_mat_compute_multi_ok(const tlh_op *const *ops, int n) {
+    if (n < 2 || n > 3) return false;
+    MulMatShape first;
+    for (int i = 0; i < n; ++i) {
+        MulMatShape s;
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.N < 3 || s.N > 16 || s.ne12 * s.ne13 != 1)
+            return false;
+        if (gemv_mfma_partial_bytes(s.K, s.M, s.N, 1) != 0) return false;
+        if (i < n - 1 && s.M % 16 != 0) return false;
+        if (i == 0) first = s;
+        else if (s.K != first.K || s.wtype != first.wtype || s.N != first.N ||
+                 ops[i]->t[0].nb[1] != ops[0]->t[0].nb[1] || ops[i]->t[1].nb[1] != ops[0]->t[1].nb[1])
+            return false;
+    }
+    return true;
+}
+
+tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
+                                      const void *scratch, size_t scratch_bytes, hipStream_t stream) {
+    if (!mul_mat_compute_multi_ok(ops, n)) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: shapes");
+    MulMatShape s;
+    check_mul_mat(ops[0], s);
+    tlh_status st = mm_check_scratch(s, scratch, scratch_bytes);
+    if (st != TLH_OK) return st;
+    MatmulArgs m = mm_args(ops[0], s, w[0], scratch, dst[0]);
+    m.part = nullptr;
+    m.nseg = n;
+    int64_t rows = 0;
+    for (int i = 0; i < 3; ++i) {
+        m.seg_m0[i] = rows;
+        if (i < n) {
+            if (!w[i] || !dst[i] || ((uintptr_t)w[i] & 1) || ((uintptr_t)dst[i] & 3))
+                return set_error(TLH_INVALID, "mul_mat_compute_multi: null or misaligned pointer");
+            m.seg_w[i] = (const uint8_t *)w[i];
+            m.seg_w_nb1[i] = ops[i]->t[0].nb[1];
+            m.seg_dst[i] = (float *)dst[i];
+            m.seg_d_nb1[i] = ops[i]->t[4].nb[1];
+            rows += ops[i]->t[0].ne[1];
+        }
+    }
+    m.seg_m0[3] = rows;
+    for (int i = n; i < 3; ++i) m.seg_m0[i] = rows;
+    m.M = rows;
+    return launch_gemv_mfma(m, stream);
+}
+
 bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
     if (n < 1 || n > 3) return false;
     MulMatShape first;
