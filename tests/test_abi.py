@@ -301,3 +301,38 @@ def test_core_validation():
         assert st == status and text in msg, (kind, st, msg)
     st, msg = _core(N.CORE_ROPE, [f32(128, 32, 2), i32(2)], f32(128, 32, 2), (128, 2, 0, 0, 0, 0, 0, 0, 1))
     assert st == "UNSUPPORTED" and "frequency factors" in msg
+
+
+def _mmid_op(wt=N.Q4_K, K=512, M=64, n_as=8, n_used=2, n_b1=2, n_tok=3, ids_ty=26):
+    op = N.TlhOp()
+    be, bb = N.BLOCK.get(wt, (256, 110))  # q3_K, unsupported: 110-byte super-blocks
+    rb = K // be * bb
+
+    def t(slot, ty, ne, nb):
+        op.t[slot].ty = ty
+        for i in range(4):
+            op.t[slot].ne[i], op.t[slot].nb[i] = ne[i], nb[i]
+    t(0, wt, [K, M, n_as, 1], [bb, rb, rb * M, rb * M * n_as])
+    t(1, N.F32, [K, n_b1, n_tok, 1], [4, 4 * K, 4 * K * n_b1, 4 * K * n_b1 * n_tok])
+    t(2, ids_ty, [n_used, n_tok, 1, 1], [4, 4 * n_used, 4 * n_used * n_tok, 4 * n_used * n_tok])
+    t(4, N.F32, [M, n_used, n_tok, 1], [4, 4 * M, 4 * M * n_used, 4 * M * n_used * n_tok])
+    return op
+
+
+def test_mul_mat_id_scratch_and_validation():
+    """Scratch = src1 quantized once (n_b1 x n_tokens rows) + K-chunk partials per
+    (expert, token) pair; ggml_mul_mat_id's shape asserts (ggml.c:3334-3342) are
+    refusals."""
+    n = C.c_size_t()
+    L = N.lib()
+    st, msg = _status(L.tlh_mul_mat_id_scratch_bytes, C.byref(_mmid_op()), C.byref(n))
+    assert st == "OK", msg
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    rows, K = 2 * 3, 512
+    assert n.value == al(al(al(al(rows * K) + rows * (K // 256) * 4) + rows * (K // 16) * 2))
+    for kw in ({"n_b1": 3}, {"ids_ty": N.F32}, {"wt": 11}):
+        st, msg = _status(L.tlh_mul_mat_id_scratch_bytes, C.byref(_mmid_op(**kw)), C.byref(n))
+        assert st == "UNSUPPORTED", (kw, msg)
+    op = _mmid_op()
+    st, msg = _status(L.tlh_mul_mat_id, C.byref(op), None, None, None, None, None, 0, None)
+    assert st == "INVALID", msg

@@ -264,3 +264,19 @@ def test_refusals(gpu):
         N.rope(torch.zeros((2, 4, 8), device="cuda"), torch.zeros(2, dtype=torch.int32, device="cuda"), 8, 1)
     with pytest.raises(N.TlhError, match="BIN"):
         N.add(x, torch.zeros((4, 3), device="cuda"))
+
+
+def test_get_rows_q5_K_table(gpu):
+    """GET_ROWS from q5_K rows (the token embedding of Q5_K_M files) equals the
+    reference's dequantize_row_q5_K of the picked rows bit for bit (q5_K.npz)."""
+    import torch
+
+    from refs import Q5_K
+
+    g = np.load(Path(__file__).resolve().parent / "golden" / "q5_K.npz")
+    w, deq = g["rand_w"], g["rand_deq"]  # 40 rows of 1024
+    idx = np.array([3, 39, 0, 17, 17, 22], np.int32)
+    out = N.get_rows(torch.from_numpy(np.ascontiguousarray(w)).cuda(), torch.from_numpy(idx).cuda(), Q5_K, 1024)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(len(idx), 1024)
+    assert np.array_equal(got.view(np.uint32), deq[idx].view(np.uint32))
