@@ -900,36 +900,52 @@ class Lowering {
         d.swap(out);
     }
 
-    // Consecutive compute halves of one quantization group (3..16 columns,
-    // K <= 4096) become one few-column MFMA launch over their rows.
+    // Compute halves of one quantization group (3..16 columns, K <= 4096)
+    // become one few-column MFMA launch over their rows, at the first one's
+    // place. A later member moves up only if nothing in between reads or
+    // writes its destination (its weights and the group's activation scratch
+    // are written by nobody else).
     void merge_mm_computes(std::vector<Dispatch> &d) {
+        std::vector<char> taken(d.size(), 0);
         std::vector<Dispatch> out;
-        for (size_t i = 0; i < d.size();) {
-            size_t j = i + 1;
-            if (d[i].kind == D_MM_COMPUTE) {
-                const tlh_op *ops[3] = {&d[i].op, nullptr, nullptr};
-                while (j < d.size() && j - i < 3 && d[j].kind == D_MM_COMPUTE && d[j].block == d[i].block) {
-                    ops[j - i] = &d[j].op;
-                    if (!mul_mat_compute_multi_ok(ops, (int)(j - i + 1))) break;
-                    ++j;
-                }
+        for (size_t i = 0; i < d.size(); ++i) {
+            if (taken[i]) continue;
+            if (d[i].kind != D_MM_COMPUTE) {
+                out.push_back(d[i]);
+                continue;
             }
-            if (j - i < 2) {
-                out.push_back(d[i++]);
+            std::vector<size_t> mem{i};
+            const tlh_op *ops[3] = {&d[i].op, nullptr, nullptr};
+            for (size_t j = i + 1; j < d.size() && j < i + 24 && mem.size() < 3; ++j) {
+                if (taken[j] || d[j].kind != D_MM_COMPUTE || d[j].block != d[i].block) continue;
+                bool ok = true;
+                for (size_t k = i + 1; k < j && ok; ++k) {
+                    if (taken[k]) continue;
+                    std::vector<Place> rd, wr;
+                    places(d[k], rd, wr);
+                    for (const Place &p : rd) ok = ok && !same_root(p, d[j].dst);
+                    for (const Place &p : wr) ok = ok && !same_root(p, d[j].dst);
+                }
+                ops[mem.size()] = &d[j].op;
+                if (ok && mul_mat_compute_multi_ok(ops, (int)mem.size() + 1)) mem.push_back(j);
+            }
+            if (mem.size() < 2) {
+                out.push_back(d[i]);
                 continue;
             }
             Dispatch f = d[i];
             f.kind = D_MM_COMPUTE_MULTI;
-            f.nmem = (int)(j - i);
-            for (size_t k = i; k < j; ++k) {
-                f.mop[k - i] = d[k].op;
-                f.mpos[k - i] = d[k].pos;
-                f.mw[k - i] = d[k].src[0];
-                f.mdst[k - i] = d[k].dst;
-                f.pos_last = std::max(f.pos_last, d[k].pos_last);
+            f.nmem = (int)mem.size();
+            for (size_t k = 0; k < mem.size(); ++k) {
+                const Dispatch &y = d[mem[k]];
+                f.mop[k] = y.op;
+                f.mpos[k] = y.pos;
+                f.mw[k] = y.src[0];
+                f.mdst[k] = y.dst;
+                f.pos_last = std::max(f.pos_last, y.pos_last);
+                taken[mem[k]] = 1;
             }
             out.push_back(f);
-            i = j;
         }
         d.swap(out);
     }
