@@ -191,6 +191,7 @@ class Lowering {
         group_elementwise(out.d);
         group_mul_mats(out.d);
         merge_mm_computes(out.d);
+        group_elementwise(out.d);  // merged computes can leave element-wise launches adjacent
         plan(out);
         return TLH_OK;
     }
