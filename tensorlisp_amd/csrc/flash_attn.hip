@@ -42,7 +42,7 @@ namespace tlh {
 
 constexpr int FA_WAVES = 4;
 constexpr int FA_TARGET_WGS = 1024;  // workgroups a split launch aims for
-constexpr int FA_MIN_PART = 128;     // fewest keys per partition when split
+constexpr int FA_MIN_PART = 64;      // fewest keys per partition when split
 
 typedef _Float16 fa_half4 __attribute__((ext_vector_type(4)));
 typedef float fa_f32x4 __attribute__((ext_vector_type(4)));
