@@ -25,7 +25,9 @@
 
 namespace tlh {
 
-constexpr int PA_PART = 512;  // tokens per partition (a multiple of every block size)
+// tokens per partition (a multiple of every block size): 512, or 256 when
+// sequences x kv heads x 512-token partitions make fewer than 512 workgroups
+constexpr int PA_PART = 512;
 constexpr int PA_WAVES = 4;
 
 // Scratch per (seq, head, partition): max, sum, acc[HS] (f32).
@@ -55,7 +57,7 @@ __device__ __forceinline__ f32x4_t mfma16(half4_t a, half4_t b, f32x4_t c) {
 //       dim c) 8 contiguous bytes.
 // Heads past the group (c >= gc) have zero q and are dropped; one MFMA serves
 // up to 16 query heads of a kv head, so a page is read once per group.
-template <int HS, int BS, bool PIPE>
+template <int HS, int BS, bool PIPE, int PART>
 __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                                                     const uint16_t *__restrict__ vc,
                                                     const int32_t *__restrict__ tables,
@@ -63,7 +65,7 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
                                                     int gc, int max_blocks, float scale, int P,
                                                     float *__restrict__ scratch) {
     constexpr int KS = HS / 16;  // QK steps = PV output tiles
-    __shared__ int s_bt[PA_PART / 8];
+    __shared__ int s_bt[PART / 8];
     __shared__ float s_m[PA_WAVES][16], s_l[PA_WAVES][16];
     __shared__ float s_acc[PA_WAVES][16][HS];
     const int lane = threadIdx.x & 63;
@@ -74,16 +76,16 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
     const int head0 = kvh * G + (blockIdx.x % (G / gc)) * gc;
     const int seq = blockIdx.y;
     const int part = blockIdx.z;
-    const int t0 = part * PA_PART;
+    const int t0 = part * PART;
     const int page0 = t0 / BS;
     // the partition's block ids are read together with the context length
     // (entries past the table are clamped to its last one and never used)
     if (max_blocks > 0)
-        for (int i = threadIdx.x; i < PA_PART / BS; i += blockDim.x)
+        for (int i = threadIdx.x; i < PART / BS; i += blockDim.x)
             s_bt[i] = tables[(int64_t)seq * max_blocks + min(page0 + i, max_blocks - 1)];
     const int L = lens[seq];
     if (t0 >= L && !(part == 0 && L == 0)) return;  // the reduce kernel ignores partitions past the context
-    const int t1 = min(L, t0 + PA_PART);
+    const int t1 = min(L, t0 + PART);
     const int npages = (t1 + BS - 1) / BS - page0;
     __syncthreads();
 
@@ -225,7 +227,7 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
 // thread reads the maxima, sums and its dims of up to 16 partitions in one
 // round of independent loads and folds them into a running (max, sum, acc)
 // rescaled online; longer contexts take further rounds.
-template <int HS>
+template <int HS, int PART>
 __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, float *__restrict__ out32,
                                                            const float *__restrict__ scratch,
                                                            const int32_t *__restrict__ lens, int num_heads, int P) {
@@ -233,7 +235,7 @@ __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict_
     const int head = blockIdx.x, seq = blockIdx.y;
     const int L = lens[seq];
     // partitions holding this sequence's context (never more than were written)
-    const int np = min(P, L > 0 ? (L + PA_PART - 1) / PA_PART : 1);
+    const int np = min(P, L > 0 ? (L + PART - 1) / PART : 1);
     const float *base = scratch + (int64_t)(seq * num_heads + head) * P * (HS + 2);
     for (int d = threadIdx.x; d < HS; d += blockDim.x) {
         float M = -INFINITY, lsum = 0.0f, a = 0.0f;
@@ -269,8 +271,14 @@ __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict_
     }
 }
 
+static int pa_part(const tlh_paged_attention_args &a) {
+    const int64_t p512 = a.max_context_len > 0 ? (a.max_context_len + PA_PART - 1) / PA_PART : 1;
+    return (int64_t)a.num_seqs * a.num_kv_heads * p512 < 512 ? PA_PART / 2 : PA_PART;
+}
+
 static int pa_partitions(const tlh_paged_attention_args &a) {
-    return a.max_context_len > 0 ? (a.max_context_len + PA_PART - 1) / PA_PART : 1;
+    const int part = pa_part(a);
+    return a.max_context_len > 0 ? (a.max_context_len + part - 1) / part : 1;
 }
 
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
@@ -284,12 +292,21 @@ static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStr
     int gc = G < 16 ? G : 16;  // query heads per workgroup: a divisor of G, at most 16
     while (G % gc) --gc;
     constexpr bool PIPE = HS <= 128;  // two register sets fit
-    hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE>), dim3(a.num_kv_heads * (G / gc), a.num_seqs, P), dim3(256), 0,
-                       stream, (const uint16_t *)a.q, (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache,
-                       a.block_tables, a.context_lens, a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale,
-                       P, scratch);
-    hipLaunchKernelGGL((k_paged_attn_reduce<HS>), dim3(a.num_heads, a.num_seqs), dim3(HS < 256 ? HS : 256), 0, stream,
-                       (uint16_t *)a.out, out32, (const float *)scratch, a.context_lens, a.num_heads, P);
+    const dim3 grid(a.num_kv_heads * (G / gc), a.num_seqs, P), rgrid(a.num_heads, a.num_seqs);
+    const dim3 rblock(HS < 256 ? HS : 256);
+    if (pa_part(a) == PA_PART) {
+        hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PA_PART>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
+                           (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
+                           a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch);
+        hipLaunchKernelGGL((k_paged_attn_reduce<HS, PA_PART>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
+                           (const float *)scratch, a.context_lens, a.num_heads, P);
+    } else {
+        hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PA_PART / 2>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
+                           (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
+                           a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch);
+        hipLaunchKernelGGL((k_paged_attn_reduce<HS, PA_PART / 2>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
+                           (const float *)scratch, a.context_lens, a.num_heads, P);
+    }
 }
 
 template <int HS>
