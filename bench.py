@@ -88,6 +88,7 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
     state = torch.zeros(total, dtype=torch.uint8, device="cuda")
     weight_bytes = sum(w.numel() * w.element_size() for w in W)
     stream = torch.cuda.Stream()
+    torch.cuda.synchronize()  # weights and the zeroed state (default stream) before `stream` uses them
     copy = lambda dst, src, n: N.check(N.lib().tlh_copy(dst, src, n, N._stream(stream)))  # noqa: E731
 
     # prefill: 512 tokens at positions 0..511, logits of the last one
@@ -181,6 +182,7 @@ def e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_toke
     pc = G.PagedConfig(block_size=block_size, n_blocks=S * per_seq, max_blocks=per_seq)
     offs, total = pc.state_bytes(c)
     state = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()  # the zeroed pools (default stream) before `stream` uses them
     rng = np.random.default_rng(4)
     tables = rng.permutation(pc.n_blocks).astype(np.int32).reshape(S, per_seq)
 
