@@ -123,6 +123,21 @@ tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes);
 tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,
                        size_t scratch_bytes, void *stream);
 
+/* tlh_mul_mat with no caller scratch and no allocation, for callers that
+ * cannot allocate device memory per call: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference (its launcher allocates nothing per call but always passes
+ * buffers it owns). Same kernels, descriptor and results as tlh_mul_mat; the
+ * scratch is a static device array of TLH_NOALLOC_SCRATCH_BYTES that each GPU
+ * holds for the life of the process, resolved on tlh_device_open (or on the
+ * first call on a device). A node whose tlh_mul_mat_scratch_bytes exceeds it
+ * is refused with TLH_INVALID (nothing is launched). The array keeps the last
+ * call's contents and nothing in it has to start at zero; all calls on one GPU
+ * share it, so calls that overlap in time on one GPU (other streams, other
+ * threads) race: order them on one stream. Calls no hipMalloc/hipFree. */
+#define TLH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+tlh_status tlh_mul_mat_noalloc(const tlh_op *op, const void *src0, const void *src1, void *dst, void *stream);
+
 /* The two phases of tlh_mul_mat, which the CPU backend separates with a
  * barrier (ggml-cpu.c:1318-1359 quantize src1 into wdata; :1366 barrier;
  * :1426-1451 the dot products). Splitting them lets an executor quantize an

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "kernels.hpp"
@@ -42,6 +43,9 @@ static tlh_status hip_check(hipError_t e, const char *what) {
     if (e == hipErrorOutOfMemory) return set_error(TLH_ALLOC, "%s: %s", what, hipGetErrorString(e));
     return set_error(TLH_EXECUTION, "%s: %s", what, hipGetErrorString(e));
 }
+
+// Resolves the no-allocation scratch of tlh_mul_mat_noalloc on the current device (below).
+tlh_status noalloc_setup_current_device();
 
 static bool weight_type_ok(int t) {
     return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K;
@@ -329,6 +333,7 @@ tlh_status tlh_device_open(int ordinal, tlh_device_props *props) {
     if (n == 0) return set_error(TLH_NO_DEVICE, "no HIP device");
     if (ordinal < 0 || ordinal >= n) return set_error(TLH_NO_DEVICE, "device %d of %d", ordinal, n);
     st = hip_check(hipSetDevice(ordinal), "hipSetDevice");
+    if (st == TLH_OK) st = noalloc_setup_current_device();
     if (st != TLH_OK || !props) return st;
     hipDeviceProp_t p;
     st = hip_check(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
@@ -600,6 +605,69 @@ tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *s
     if (!src0 || !dst) return set_error(TLH_INVALID, "mul_mat_compute: null tensor pointer");
     if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
     return mm_compute(op, s, src0, scratch, dst, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------- MUL_MAT without allocation
+// tlh_mul_mat_noalloc runs tlh_mul_mat's kernels with their scratch (the
+// quantized activations and the K-chunk partial sums) in this file-scope
+// device array instead of a caller buffer. Each GPU the library runs on holds
+// its own copy for the life of the process. Host code must not pass the
+// array's name to a kernel or a copy: on the host it is only a stand-in
+// symbol. Its device address is looked up once per device with that device
+// current (hipGetSymbolAddress) and kept in g_noalloc_ptr.
+static __device__ __align__(256) uint8_t scratch[TLH_NOALLOC_SCRATCH_BYTES];
+
+namespace tlh {
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_noalloc_mu;
+static void *g_noalloc_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device (resolved on first use).
+static tlh_status noalloc_scratch(void **ptr) {
+    int dev = 0;
+    tlh_status st = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (st != TLH_OK) return st;
+    if (dev < 0 || dev >= kMaxDevices) return set_error(TLH_UNSUPPORTED, "mul_mat_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        st = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (st != TLH_OK) return st;
+        if (!p || ((uintptr_t)p & 255))
+            return set_error(TLH_EXECUTION, "mul_mat_noalloc: scratch address %p is not 256-byte aligned", p);
+        g_noalloc_ptr[dev] = p;
+    }
+    *ptr = g_noalloc_ptr[dev];
+    return TLH_OK;
+}
+
+// Set-up at device open, so a caller that opens its devices first never has
+// the look-up happen inside a capture.
+tlh_status noalloc_setup_current_device() {
+    void *p = nullptr;
+    return noalloc_scratch(&p);
+}
+
+}  // namespace tlh
+
+extern "C" {
+
+tlh_status tlh_mul_mat_noalloc(const tlh_op *op, const void *src0, const void *src1, void *dst, void *stream) {
+    MulMatShape s;
+    tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK || mm_empty(s)) return st;
+    const size_t need = (size_t)(mm_act_bytes(s) + mm_partial_bytes(s));
+    if (need > (size_t)TLH_NOALLOC_SCRATCH_BYTES)
+        return set_error(TLH_INVALID,
+                         "mul_mat_noalloc: this node needs %zu bytes of scratch, beyond the static %zu "
+                         "(use tlh_mul_mat with a caller buffer)",
+                         need, (size_t)TLH_NOALLOC_SCRATCH_BYTES);
+    void *scr = nullptr;
+    if ((st = noalloc_scratch(&scr)) != TLH_OK) return st;
+    return tlh_mul_mat(op, src0, src1, dst, scr, (size_t)TLH_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 // ------------------------------------------------------------ MUL_MAT_ID

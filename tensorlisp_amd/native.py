@@ -30,7 +30,7 @@ STATUS = {0: "OK", 1: "NO_DEVICE", 2: "UNSUPPORTED", 3: "INVALID", 4: "ALLOC", 5
 EXPORTS = (
     "tlh_last_error", "tlh_status_name", "tlh_version", "tlh_device_count", "tlh_device_open", "tlh_alloc",
     "tlh_free", "tlh_h2d", "tlh_d2h", "tlh_stream_sync", "tlh_mul_mat_scratch_bytes", "tlh_mul_mat",
-    "tlh_mul_mat_quantize", "tlh_mul_mat_compute", "tlh_mul_mat_id_scratch_bytes", "tlh_mul_mat_id",
+    "tlh_mul_mat_noalloc", "tlh_mul_mat_quantize", "tlh_mul_mat_compute", "tlh_mul_mat_id_scratch_bytes", "tlh_mul_mat_id",
     "tlh_quantize_act", "tlh_dequantize", "tlh_flash_attn_ext_scratch_bytes", "tlh_flash_attn_ext",
     "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
     "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_program_input",
@@ -90,6 +90,7 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_stream_sync.argtypes = [vp]
     L.tlh_mul_mat_scratch_bytes.argtypes = [C.POINTER(TlhOp), C.POINTER(C.c_size_t)]
     L.tlh_mul_mat.argtypes = [C.POINTER(TlhOp), vp, vp, vp, vp, C.c_size_t, vp]
+    L.tlh_mul_mat_noalloc.argtypes = [C.POINTER(TlhOp), vp, vp, vp, vp]
     L.tlh_mul_mat_quantize.argtypes = [C.POINTER(TlhOp), vp, vp, C.c_size_t, vp]
     L.tlh_mul_mat_compute.argtypes = [C.POINTER(TlhOp), vp, vp, C.c_size_t, vp, vp]
     L.tlh_mul_mat_id_scratch_bytes.argtypes = [C.POINTER(TlhOp), C.POINTER(C.c_size_t)]
