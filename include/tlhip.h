@@ -263,8 +263,10 @@ tlh_status tlh_core(int kind, const tlh_op *op, const void *src0, const void *sr
  *   out      [num_seqs][num_heads][head_size]
  * head_size in {64, 80, 96, 112, 128, 192, 256}, block_size in {8, 16, 32},
  * num_heads % num_kv_heads == 0, context lens <= max_context_len.
- * `scratch` holds split-context partials (tlh_paged_attention_scratch_bytes);
- * it may be NULL when that size is 0. */
+ * `scratch` holds split-context partials (tlh_paged_attention_scratch_bytes,
+ * which never shrinks as num_seqs or max_context_len grow, so one buffer sized
+ * for the largest batch and context serves every smaller call); it may be
+ * NULL when that size is 0. */
 typedef struct tlh_paged_attention_args {
     void *out;
     const void *q;
@@ -289,10 +291,13 @@ tlh_status tlh_paged_attention(const tlh_paged_attention_args *a, void *scratch,
 /* The `paged-cache-write` custom node (core.ss:265-272), Ctx::custom kind 2
  * (lower.rs:732-753) -> reshape_and_cache (crates/kernels/src/cuda/shaders/
  * reshape_and_cache_kernel.cu:31-84): key/value f16 [num_tokens][num_kv_heads*head_size]
- * into the caches at slot = block * block_size + offset; negative slots skip. */
+ * into the caches at slot = block * block_size + offset; negative slots skip.
+ * num_blocks is the pools' length in blocks (the caller's pool tensors give
+ * it): a slot at or past num_blocks * block_size writes nothing, so a bad
+ * slot cannot write outside the pools. */
 tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                  const int64_t *slots, int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
-                                 int32_t block_size, void *stream);
+                                 int32_t block_size, int64_t num_blocks, void *stream);
 
 /* ------------------------------------------------------------ executor
  * A graph of ggml nodes compiled once into a recorded list of launches on this

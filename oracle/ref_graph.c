@@ -281,7 +281,7 @@ int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_node
         } else if (!strcmp(op, "MUL_MAT_ID")) {
             x = ggml_mul_mat_id(ctx, s0, s1, s2);
         } else if (!strcmp(op, "ADD")) {
-            x = ggml_add(ctx, s0, s1);
+            x = r->view_src >= 0 ? ggml_add_inplace(ctx, s0, s1) : ggml_add(ctx, s0, s1);
         } else if (!strcmp(op, "SUB")) {
             x = ggml_sub(ctx, s0, s1);
         } else if (!strcmp(op, "MUL")) {

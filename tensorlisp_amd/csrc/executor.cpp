@@ -60,6 +60,7 @@ struct Dispatch {
     tlh_paged_attention_args pa{};
     int pa_f32 = 0;  // D_PAGED_ATTN: dst is a fused cast's f32 tensor
     int32_t pw[4] = {0, 0, 0, 0};
+    int64_t pw_blocks = 0;  // D_PAGED_WRITE: blocks in the smaller pool (slots past it are dropped)
     int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
 };
 
@@ -316,6 +317,8 @@ class Lowering {
             d.pw[3] = bs;
             if (d.pw[2] % 8 || !(bs == 8 || bs == 16 || bs == 32))
                 return why = "the cache write: head size a multiple of 8, block size 8, 16 or 32", false;
+            const int64_t block_bytes = (int64_t)kvh * d.pw[2] * bs * 2;
+            d.pw_blocks = std::min(nbytes(T(2)), nbytes(T(3))) / block_bytes;
             d.kind = D_PAGED_WRITE;
         } else {
             return why = "unknown custom op", false;
@@ -499,12 +502,22 @@ class Lowering {
                 out.push_back(x);
                 continue;
             }
+            // The fused kernel reads the row's tail (past its register cache)
+            // from the sources again after writing the ADD's sum and the
+            // output, so no destination may share storage with a source: an
+            // in-place ADD (add-inplace) keeps its own launch.
+            if (same_root(m.dst, x.src[0]) || same_root(m.dst, m.src[1])) {
+                out.push_back(x);
+                continue;
+            }
             bool with_add = false;
             if (!out.empty()) {
                 const Dispatch &a = out.back();
                 with_add = a.kind == D_CORE && a.core_kind == TLH_CORE_BIN && a.op.x[0] == 0 &&
                            node_of(a) == g_.t[nid].src[0] && f32_rows(a.op.t[0]) && f32_rows(a.op.t[1]) &&
-                           f32_rows(a.op.t[4]) && same_ne(a.op.t[0], a.op.t[4]) && same_ne(a.op.t[1], a.op.t[4]);
+                           f32_rows(a.op.t[4]) && same_ne(a.op.t[0], a.op.t[4]) && same_ne(a.op.t[1], a.op.t[4]) &&
+                           !same_root(a.dst, a.src[0]) && !same_root(a.dst, a.src[1]) &&
+                           !same_root(m.dst, a.src[0]) && !same_root(m.dst, a.src[1]);
             }
             Dispatch f;
             f.kind = D_NORM_CHAIN;
@@ -1169,11 +1182,11 @@ struct tlh_program {
                 if (x.pw_f32[0] || x.pw_f32[1])
                     st = x.pw[0] == 0 ? TLH_OK
                                       : launch_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4],
-                                                                 x.pw[0], x.pw[1], x.pw[2], x.pw[3], s, x.pw_f32[0] != 0,
-                                                                 x.pw_f32[1] != 0);
+                                                                 x.pw[0], x.pw[1], x.pw[2], x.pw[3], x.pw_blocks, s,
+                                                                 x.pw_f32[0] != 0, x.pw_f32[1] != 0);
                 else
                     st = tlh_reshape_and_cache(src[0], src[1], src[2], src[3], (const int64_t *)src[4], x.pw[0],
-                                               x.pw[1], x.pw[2], x.pw[3], s);
+                                               x.pw[1], x.pw[2], x.pw[3], x.pw_blocks, s);
                 break;
             case D_ARGMAX_SPLIT: st = launch_argmax_split(x.op, src[0], dst, scratch, s); break;
             case D_CORE_MULTI: {

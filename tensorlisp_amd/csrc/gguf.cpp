@@ -206,18 +206,33 @@ tlh_status tlh_gguf_open(const char *path, tlh_gguf **out) {
                              name.c_str(), ty);
         }
         if (ti.ne[0] % blck) return bad(g, "tensor '%s': rows are not whole blocks", name);
-        const int64_t nel = ti.ne[0] * ti.ne[1] * ti.ne[2] * ti.ne[3];
-        ti.bytes = (uint64_t)(nel / blck * size);
+        // The element count must be an int64, as ggml's reader demands
+        // (vendor/ggml/src/gguf.cpp:691-702); each partial product is
+        // checked before it is formed. Then the byte count and the running
+        // offset must not wrap either.
+        int64_t nel = ti.ne[0];
+        for (int d = 1; d < 4 && nel > 0; ++d) {
+            if (ti.ne[d] > 0 && nel >= INT64_MAX / ti.ne[d])
+                return bad(g, "tensor '%s' has more elements than an int64 holds", name);
+            nel *= ti.ne[d];
+        }
+        if (ti.ne[1] == 0 || ti.ne[2] == 0 || ti.ne[3] == 0) nel = 0;
+        const uint64_t nblocks = (uint64_t)(nel / blck);
+        if (size > 0 && nblocks > UINT64_MAX / 2 / (uint64_t)size)
+            return bad(g, "tensor '%s' has more bytes than a size holds", name);
+        ti.bytes = nblocks * (uint64_t)size;
         if (ti.offset != expect) return bad(g, "tensor '%s' has offset %lld, expected the next aligned slot", name, (long long)ti.offset);
-        expect += (ti.bytes + g->alignment - 1) / g->alignment * g->alignment;
+        const uint64_t padded = (ti.bytes + g->alignment - 1) / g->alignment * g->alignment;
+        if (padded > g->file_size || expect > g->file_size - padded)
+            return bad(g, "tensor '%s': data past the end of the file", name);
+        expect += padded;
         g->by_name[name] = (int64_t)g->tensors.size();
         g->tensors.push_back(ti);
     }
     g->data_offset = n_tensors > 0 ? (r.pos + g->alignment - 1) / g->alignment * g->alignment : r.pos;
-    if (!g->tensors.empty()) {
-        const tlh_gguf_tensor_info &last = g->tensors.back();
-        if (g->data_offset + last.offset + last.bytes > g->file_size) return bad(g, "%stensor data past the end of the file", "");
-    }
+    for (const tlh_gguf_tensor_info &t : g->tensors)  // every tensor, offsets and sizes already bounded above
+        if (g->data_offset > g->file_size || t.offset + t.bytes > g->file_size - g->data_offset)
+            return bad(g, "tensor '%s': data past the end of the file", std::string(t.name));
     *out = g;
     return TLH_OK;
 }

@@ -138,7 +138,7 @@ size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
 // key_f32 / value_f32: that source is f32 and is rounded to f16 on the way
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,
-                                    int block_size, hipStream_t stream, bool key_f32 = false,
+                                    int block_size, int64_t num_blocks, hipStream_t stream, bool key_f32 = false,
                                     bool value_f32 = false);
 
 }  // namespace tlh

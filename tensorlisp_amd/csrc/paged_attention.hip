@@ -281,8 +281,12 @@ static int pa_partitions(const tlh_paged_attention_args &a) {
     return a.max_context_len > 0 ? (a.max_context_len + part - 1) / part : 1;
 }
 
+// Sized for the shorter (256-token) partitions whichever the launch picks, so
+// the size grows with num_seqs and max_context_len: a caller may size its
+// scratch once for its largest batch and context.
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
-    return (size_t)a.num_seqs * a.num_heads * pa_partitions(a) * (a.head_size + 2) * sizeof(float);
+    const int64_t parts = a.max_context_len > 0 ? (a.max_context_len + PA_PART / 2 - 1) / (PA_PART / 2) : 1;
+    return (size_t)a.num_seqs * a.num_heads * parts * (a.head_size + 2) * sizeof(float);
 }
 
 template <int HS, int BS>
@@ -353,10 +357,10 @@ template <bool K32, bool V32>
 __global__ void __launch_bounds__(256) k_reshape_and_cache(const void *__restrict__ key, const void *__restrict__ value,
                                                            uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                                            const int64_t *__restrict__ slots, int kvh, int hs,
-                                                           int bs) {
+                                                           int bs, int64_t pool_slots) {
     const int t = blockIdx.x;
     const int64_t slot = slots[t];
-    if (slot < 0) return;
+    if (slot < 0 || slot >= pool_slots) return;  // negative: skip (the reference); past the pools: dropped
     const int64_t blk = slot / bs;
     const int off = (int)(slot % bs);
     const int chunks = kvh * hs / 8;
@@ -378,13 +382,16 @@ __global__ void __launch_bounds__(256) k_reshape_and_cache(const void *__restric
 
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,
-                                    int block_size, hipStream_t stream, bool key_f32, bool value_f32) {
+                                    int block_size, int64_t num_blocks, hipStream_t stream, bool key_f32,
+                                    bool value_f32) {
+    if (num_blocks < 0 || num_blocks > INT64_MAX / block_size)
+        return set_error(TLH_INVALID, "reshape_and_cache: %lld blocks", (long long)num_blocks);
     if ((((uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache) & 15) != 0)
         return set_error(TLH_INVALID, "reshape_and_cache: key, value and key cache must be 16-byte aligned");
     auto k = key_f32 ? (value_f32 ? k_reshape_and_cache<true, true> : k_reshape_and_cache<true, false>)
                      : (value_f32 ? k_reshape_and_cache<false, true> : k_reshape_and_cache<false, false>);
     hipLaunchKernelGGL(k, dim3(num_tokens), dim3(128), 0, stream, key, value, (uint16_t *)k_cache,
-                       (uint16_t *)v_cache, slots, num_kv_heads, head_size, block_size);
+                       (uint16_t *)v_cache, slots, num_kv_heads, head_size, block_size, num_blocks * block_size);
     return check_launch("reshape_and_cache");
 }
 

@@ -853,13 +853,14 @@ tlh_status tlh_paged_attention(const tlh_paged_attention_args *a, void *scratch,
 
 tlh_status tlh_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                  const int64_t *slots, int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
-                                 int32_t block_size, void *stream) {
-    if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || head_size % 8 != 0 || block_size <= 0)
+                                 int32_t block_size, int64_t num_blocks, void *stream) {
+    if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || head_size % 8 != 0 || block_size <= 0 ||
+        num_blocks < 0)
         return set_error(TLH_INVALID, "reshape_and_cache: bad geometry");
     if (num_tokens == 0) return TLH_OK;
     if (!key || !value || !k_cache || !v_cache || !slots) return set_error(TLH_INVALID, "reshape_and_cache: null pointer");
     return launch_reshape_and_cache(key, value, k_cache, v_cache, slots, num_tokens, num_kv_heads, head_size,
-                                    block_size, (hipStream_t)stream);
+                                    block_size, num_blocks, (hipStream_t)stream);
 }
 
 tlh_status tlh_flash_attn_ext_scratch_bytes(const tlh_op *op, size_t *bytes) {

@@ -156,6 +156,10 @@ class Builder:
     def add(self, a, b):
         return self._dup(a, "ADD", [a, b])
 
+    def add_inplace(self, a, b):
+        """ggml_add_inplace: the sum is written over a (the result is a view of a)."""
+        return self._new(a.ty, a.ne, "ADD", [a, b], view_of=a, nb=a.nb)
+
     def sub(self, a, b):
         return self._dup(a, "SUB", [a, b])
 
@@ -339,10 +343,25 @@ class Program:
                                            C.byref(p)))
         return p.value
 
+    @staticmethod
+    def _order(tensor, stream) -> None:
+        """Orders `stream` after the current stream (which made `tensor` or last used
+        its memory) and tells the caching allocator that `stream` uses `tensor`, so
+        the block is not handed out again before `stream`'s copy has run."""
+        import torch
+
+        if stream is None or not isinstance(stream, torch.cuda.Stream):
+            return
+        cur = torch.cuda.current_stream(tensor.device)
+        if stream != cur:
+            stream.wait_stream(cur)
+            tensor.record_stream(stream)
+
     def write_input(self, i: int, src, stream=None) -> None:
         """Copies a contiguous torch device tensor into graph input i (stream-ordered)."""
         ptr, n = self.input(i)
         assert src.is_contiguous() and src.numel() * src.element_size() == n, (i, n)
+        self._order(src, stream)
         N.check(N.lib().tlh_copy(C.c_void_p(ptr), C.c_void_p(src.data_ptr()), n, N._stream(stream)))
 
     def read(self, t: T, dtype, state=None, stream=None):
@@ -351,12 +370,15 @@ class Program:
 
         out = torch.empty(list(t.ne[::-1]), dtype=dtype, device="cuda")
         n = out.numel() * out.element_size()
+        self._order(out, stream)
         N.check(N.lib().tlh_copy(C.c_void_p(out.data_ptr()), C.c_void_p(self.tensor_ptr(t, state)), n,
                                  N._stream(stream)))
         return out
 
     def run(self, state=None, stream=None, graph: bool = False) -> None:
         st = C.c_void_p(state.data_ptr() if state is not None else None)
+        if state is not None:
+            self._order(state, stream)
         N.check(N.lib().tlh_program_run(self.ptr, st, N._stream(stream), int(graph)))
 
     def stats(self):

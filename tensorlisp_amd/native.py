@@ -101,7 +101,7 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_flash_attn_ext.argtypes = [C.POINTER(TlhOp), vp, vp, vp, vp, vp, vp, C.c_size_t, vp]
     L.tlh_paged_attention_scratch_bytes.argtypes = [C.POINTER(TlhPagedArgs), C.POINTER(C.c_size_t)]
     L.tlh_paged_attention.argtypes = [C.POINTER(TlhPagedArgs), vp, C.c_size_t, vp]
-    L.tlh_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]
+    L.tlh_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int64, vp]
     L.tlh_core_check.argtypes = [C.c_int, C.POINTER(TlhOp), C.c_int, C.c_int]
     L.tlh_core.argtypes = [C.c_int, C.POINTER(TlhOp), vp, vp, vp, vp, vp]
     i32p, i64p = C.POINTER(C.c_int32), C.POINTER(C.c_int64)
@@ -416,11 +416,13 @@ def paged_attention(q, k_cache, v_cache, block_tables, context_lens, block_size,
 
 
 def reshape_and_cache(key, value, k_cache, v_cache, slots, num_kv_heads, block_size, stream=None):
-    """key/value f16 [tokens, kv_heads*hs] scattered into the caches; slots i64 [tokens] (negative = skip)."""
+    """key/value f16 [tokens, kv_heads*hs] scattered into the caches; slots i64 [tokens] (negative = skip;
+    at or past the pools' end = dropped)."""
     tokens = key.shape[0]
     hs = key.shape[1] // num_kv_heads
+    num_blocks = min(k_cache.numel(), v_cache.numel()) // (num_kv_heads * hs * block_size)
     check(lib().tlh_reshape_and_cache(_ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slots), tokens,
-                                      num_kv_heads, hs, block_size, _stream(stream)))
+                                      num_kv_heads, hs, block_size, num_blocks, _stream(stream)))
 
 
 # ------------------------------------------------------------------ core ops

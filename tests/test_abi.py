@@ -154,8 +154,26 @@ def test_paged_attention_geometry_validation(kw, status):
     n = C.c_size_t()
     st, msg = _status(N.lib().tlh_paged_attention_scratch_bytes, C.byref(paged_args(**kw)), C.byref(n))
     assert st == status, msg
-    if status == "OK":
-        assert n.value == 32 * 32 * (8192 // 512) * (128 + 2) * 4
+    if status == "OK":  # partials [seqs][heads][ceil(max_ctx / 256)][head_size + 2] f32
+        assert n.value == 32 * 32 * (8192 // 256) * (128 + 2) * 4
+
+
+def test_paged_attention_scratch_grows_with_batch_and_context():
+    """The scratch size never shrinks as num_seqs or max_context_len grow (it is
+    sized for the shorter of the two partition lengths the launch may pick), so
+    one buffer sized for the largest call serves every smaller one."""
+    def size(seqs, ctx):
+        n = C.c_size_t()
+        a = paged_args(num_seqs=seqs, max_context_len=ctx, max_blocks_per_seq=(ctx + 15) // 16)
+        st, msg = _status(N.lib().tlh_paged_attention_scratch_bytes, C.byref(a), C.byref(n))
+        assert st == "OK", msg
+        return n.value
+    for ctx in (1, 255, 256, 257, 4096, 8192, 8193):
+        sizes = [size(s, ctx) for s in range(1, 40)]
+        assert sizes == sorted(sizes), ctx
+    for s in (1, 3, 4, 32):
+        sizes = [size(s, c) for c in range(1, 9000, 97)]
+        assert sizes == sorted(sizes), s
 
 
 def _fa_op(nb=2, nh=8, nhkv=2, nq=1, L=1000, D=128, DV=None, kdt="f16", mask=True, **kw):

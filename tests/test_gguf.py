@@ -89,6 +89,9 @@ MALFORMED = {
     "five dimensions": _header(3, 1, 0) + _s("a") + struct.pack("<I", 5) + struct.pack("<5q", 1, 1, 1, 1, 1) +
     struct.pack("<iQ", 0, 0) + bytes(64),
     "data past the end": _header(3, 1, 0) + _tensor("a", [1024], 0, 0) + bytes(40),
+    # element counts beyond an int64 (vendor/ggml/src/gguf.cpp:691-702), here in a middle tensor
+    "element count overflows int64": _header(3, 3, 0) + _tensor("a", [8], 0, 0) +
+    _tensor("b", [1 << 32, 1 << 31, 4], 0, 32) + _tensor("c", [8], 0, 64) + bytes(128),
 }
 
 
@@ -123,4 +126,13 @@ def test_unsized_type_is_unsupported(tmp_path):
     p = tmp_path / "iq.gguf"
     p.write_bytes(_header(3, 1, 0) + _tensor("a", [256], 16, 0) + bytes(512))  # 16 = iq2_xxs
     with pytest.raises(N.TlhError, match="UNSUPPORTED"):
+        gguf.GgufFile(p)
+
+
+def test_byte_count_that_would_wrap_is_refused(tmp_path):
+    """2^62 f32 elements fit an int64 but their 2^64 bytes do not: the reader must not
+    wrap the size (and with it every later offset and the layout's total)."""
+    p = tmp_path / "wrap.gguf"
+    p.write_bytes(_header(3, 2, 0) + _tensor("a", [1 << 31, 1 << 31], 0, 0) + _tensor("b", [8], 0, 0) + bytes(64))
+    with pytest.raises(N.TlhError, match="INVALID"):
         gguf.GgufFile(p)

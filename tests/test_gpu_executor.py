@@ -212,6 +212,42 @@ def test_fused_norm_chains_match_unfused(gpu, n, rms, add):
     assert prog.stats()["launches"] == 1
 
 
+@pytest.mark.parametrize("n", [8192, 4100])
+def test_inplace_add_feeding_norm(gpu, n):
+    """An in-place ADD (ggml_add_inplace: the sum overwrites src0) feeding
+    RMS_NORM -> MUL(weight) on rows longer than the fused kernel's register
+    cache: the fused chain would read the row's tail from the overwritten src0,
+    so the ADD keeps its own launch. Results equal the core ops run one by one
+    and the reference backend running the same graph."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    b = G.Builder()
+    p = b.input(N.F32, [n, 2])
+    q = b.input(N.F32, [n, 2])
+    w = b.weight(N.F32, [n])
+    s = b.add_inplace(p, q)
+    y = b.mul(b.rms_norm(s, 1e-5), w)
+    b.expand(y)
+    wn = synth.normal(71, (n,))
+    pn, qn = synth.normal(72, (2, n)) * 2 + 0.5, synth.normal(73, (2, n))
+    prog = G.Program(b, [y, s], [dev(wn)])
+    prog.write_input(0, dev(pn))
+    prog.write_input(1, dev(qn))
+    prog.run()
+    sv = N.add(dev(pn), dev(qn))
+    want = N.mul(N.norm(sv, 1e-5, rms=True), dev(wn))
+    got = prog.read(y, torch.float32).reshape(want.shape)
+    got_s = prog.read(s, torch.float32).reshape(sv.shape)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+    np.testing.assert_array_equal(got_s.cpu().numpy(), sv.cpu().numpy())
+    ry, rs = ref().ir_run(b, [wn], [], [pn.copy(), qn], [(y, np.float32), (s, np.float32)])
+    np.testing.assert_array_equal(got_s.cpu().numpy().reshape(rs.shape), rs)
+    np.testing.assert_allclose(got.cpu().numpy().reshape(ry.shape), ry, rtol=1e-6, atol=1e-7)
+
+
 def test_argmax_of_a_vocabulary(gpu):
     """ARGMAX over 128256 logits runs in chunks over many workgroups in a
     program; the last index of equal maxima wins, as on the CPU."""

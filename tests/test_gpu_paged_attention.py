@@ -59,6 +59,11 @@ CASES = [
     (128, 16, 1, 4, [515, 5]),
     (128, 16, 8, 32, [512, 1, 1024, 513]),
     (128, 8, 2, 6, [77, 300]),  # group of 3 query heads per kv head
+    # 4 sequences x 8 kv heads x ceil(8192 / 512) = 512 workgroups: these take the
+    # 512-token partitions (fewer workgroups would take 256-token ones), at block
+    # sizes 8 and 32 and head sizes 64 and 256
+    (64, 8, 8, 32, [8192, 100, 3000, 511]),
+    (256, 32, 8, 32, [8192, 1, 4097, 512]),
 ]
 
 
@@ -155,6 +160,31 @@ def test_reshape_and_cache_bit_exact(gpu, kvh, hs, bs):
     oracle().reshape_and_cache(key, val, kc, vc, slots, kvh, hs, bs)
     assert np.array_equal(host(kd).view(np.uint16), kc)
     assert np.array_equal(host(vd).view(np.uint16), vc)
+    torch.cuda.synchronize()
+
+
+def test_reshape_and_cache_drops_slots_past_the_pools(gpu):
+    """Slots at or past num_blocks * block_size write nothing (the pools' length
+    comes from the cache tensors). The pools here are the first blocks of larger
+    buffers, and every dropped slot lies inside the spare blocks behind them, so
+    the spare blocks must come back untouched."""
+    import torch
+
+    kvh, hs, bs, nblocks, spare = 2, 64, 16, 8, 4
+    T = 6
+    key = synth.f16_bits(synth.normal(1410, (T, kvh * hs)))
+    val = synth.f16_bits(synth.normal(1411, (T, kvh * hs)))
+    slots = np.array([0, nblocks * bs, 5, nblocks * bs + 17, (nblocks + spare) * bs - 1, nblocks * bs - 1], np.int64)
+    kc = np.full((nblocks + spare, kvh, hs // 8, bs, 8), 0x1234, np.uint16)
+    vc = np.full((nblocks + spare, kvh, hs, bs), 0x4321, np.uint16)
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    N.reshape_and_cache(dev(key.view(np.int16)), dev(val.view(np.int16)), kd[:nblocks], vd[:nblocks], dev(slots),
+                        kvh, bs)
+    kept = np.where(slots < nblocks * bs, slots, -1)
+    oracle().reshape_and_cache(key, val, kc, vc, kept, kvh, hs, bs)
+    assert np.array_equal(host(kd).view(np.uint16), kc)
+    assert np.array_equal(host(vd).view(np.uint16), vc)
+    assert np.all(kc[nblocks:] == 0x1234) and np.all(vc[nblocks:] == 0x4321)
     torch.cuda.synchronize()
 
 
