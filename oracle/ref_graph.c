@@ -238,7 +238,7 @@ int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_node
     size_t mem = ggml_graph_overhead_custom(4096 > n ? 4096 : (size_t)n * 2, false) + 1024 * 1024;
     for (int i = 0; i < n; ++i) {
         mem += ggml_tensor_overhead() + 64;
-        if (rec[i].view_src < 0 && strcmp(rec[i].op, "NONE") != 0) {
+        if (rec[i].view_src < 0 && (strcmp(rec[i].op, "NONE") != 0 || rec[i].storage == TLH_STORE_TEMP)) {
             const int64_t ne = rec[i].ne[0] * rec[i].ne[1] * rec[i].ne[2] * rec[i].ne[3];
             mem += (size_t)(ne * 8 + 256);  // at most 8 bytes an element (i64)
         }
@@ -254,8 +254,14 @@ int ref_ir_run(const tlh_ir_tensor *rec, int n, const int32_t *nodes, int n_node
                            *s2 = r->src[2] >= 0 ? t[r->src[2]] : NULL, *s3 = r->src[3] >= 0 ? t[r->src[3]] : NULL;
         const char *op = r->op;
         struct ggml_tensor *x = NULL;
-        if (!strcmp(op, "NONE")) {
+        if (!strcmp(op, "NONE") && r->storage == TLH_STORE_TEMP) {
+            // a new tensor without a source (ggml_cast's destination): context memory
             x = ggml_new_tensor_4d(ctx, (enum ggml_type)r->ty, r->ne[0], r->ne[1], r->ne[2], r->ne[3]);
+        } else if (!strcmp(op, "NONE")) {
+            // leaves point at the caller's arrays: no context memory for their data
+            ggml_set_no_alloc(ctx, true);
+            x = ggml_new_tensor_4d(ctx, (enum ggml_type)r->ty, r->ne[0], r->ne[1], r->ne[2], r->ne[3]);
+            ggml_set_no_alloc(ctx, false);
             void *const *leaf = r->storage == TLH_STORE_WEIGHT ? weights : r->storage == TLH_STORE_STATE ? states
                                 : r->storage == TLH_STORE_INPUT ? inputs : NULL;
             if (!leaf) {

@@ -447,26 +447,30 @@ class DecoderStep:
     logits: T
     argmax: T
     keep: list
+    taps: list = None  # residual stream after the embedding and after each layer
 
 
-def _decoder_body(b: Builder, c: DecoderConfig, W, tokens: T, pos: T, T_: int, attend, last_only: bool):
-    """The llama layers around attention (llm_build_llama): attend(i, q, k, v)
-    gets layer i's roped q [hd, heads, T] and k [hd, kv_heads, T] and v
-    [n_embd_kv, T] (f32) and returns the attention output [n_embd, T] (f32)."""
-    x = b.get_rows(W["tok_embd"], tokens)
+def _layer(b: Builder, c: DecoderConfig, W, x: T, pos: T, T_: int, attend, i: int) -> T:
+    """Layer i of llm_build_llama: attention block and SwiGLU FFN, each with its
+    RMS_NORM x weight and residual ADD. attend(i, q, k, v) gets the roped q [hd,
+    heads, T] and k [hd, kv_heads, T] and v [n_embd_kv, T] (f32) and returns the
+    attention output [n_embd, T] (f32)."""
     hd = c.head_dim
-    for i in range(c.n_layer):
-        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.attn_norm"])
-        q = b.reshape(b.mul_mat(W[f"l{i}.wq"], cur), hd, c.n_head, T_)
-        k = b.reshape(b.mul_mat(W[f"l{i}.wk"], cur), hd, c.n_head_kv, T_)
-        v = b.mul_mat(W[f"l{i}.wv"], cur)
-        q = b.rope_ext(q, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
-        k = b.rope_ext(k, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
-        att = attend(i, q, k, v)
-        x = b.add(b.mul_mat(W[f"l{i}.wo"], att), x)
-        cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.ffn_norm"])
-        h = b.glu_split(b.mul_mat(W[f"l{i}.w_gate"], cur), b.mul_mat(W[f"l{i}.w_up"], cur), "swiglu")
-        x = b.add(b.mul_mat(W[f"l{i}.w_down"], h), x)
+    cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.attn_norm"])
+    q = b.reshape(b.mul_mat(W[f"l{i}.wq"], cur), hd, c.n_head, T_)
+    k = b.reshape(b.mul_mat(W[f"l{i}.wk"], cur), hd, c.n_head_kv, T_)
+    v = b.mul_mat(W[f"l{i}.wv"], cur)
+    q = b.rope_ext(q, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
+    k = b.rope_ext(k, pos, None, hd, c.rope_mode, c.n_ctx, c.rope_base, 1.0, 0.0, 1.0, 32.0, 1.0)
+    att = attend(i, q, k, v)
+    x = b.add(b.mul_mat(W[f"l{i}.wo"], att), x)
+    cur = b.mul(b.rms_norm(x, c.eps), W[f"l{i}.ffn_norm"])
+    h = b.glu_split(b.mul_mat(W[f"l{i}.w_gate"], cur), b.mul_mat(W[f"l{i}.w_up"], cur), "swiglu")
+    return b.add(b.mul_mat(W[f"l{i}.w_down"], h), x)
+
+
+def _head(b: Builder, c: DecoderConfig, W, x: T, T_: int, last_only: bool):
+    """Final RMS_NORM x weight, lm_head MUL_MAT and ARGMAX (of the last token, or every token)."""
     if last_only and T_ > 1:
         x = b.view(x, [c.n_embd, 1], [x.nb[1]], (T_ - 1) * x.nb[1])
     cur = b.mul(b.rms_norm(x, c.eps), W["out_norm"])
@@ -477,21 +481,22 @@ def _decoder_body(b: Builder, c: DecoderConfig, W, tokens: T, pos: T, T_: int, a
     return logits, am
 
 
-def decoder_step(c: DecoderConfig, n_tokens: int, n_kv: int, last_only: bool = True) -> DecoderStep:
-    """One forward step of `n_tokens` new tokens over a cache whose first `n_kv`
-    rows are attended (llama.cpp's llm_build_llama with the flash-attention
-    path): inputs 0 tokens i32 [T], 1 positions i32 [T], 2 cache rows i64 [T],
-    3 mask f16 [n_kv, T]; logits of the last token (or of every token), and
-    their argmax."""
-    b = Builder()
-    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
-    caches = [(b.state(N.F16, [c.n_embd_kv, c.n_ctx], f"k{i}"), b.state(N.F16, [c.n_embd_kv, c.n_ctx], f"v{i}"))
-              for i in range(c.n_layer)]
-    T_, hd = n_tokens, c.head_dim
-    tokens = b.input(N.I32, [T_], "tokens")
-    pos = b.input(N.I32, [T_], "pos")
-    slots = b.input(N.I64, [T_], "slots")
-    mask = b.input(N.F16, [n_kv, T_], "mask")
+def _decoder_body(b: Builder, c: DecoderConfig, W, tokens: T, pos: T, T_: int, attend, last_only: bool,
+                  taps: list = None):
+    """Token embedding (GET_ROWS), the layers and the head. `taps` (a list)
+    receives the residual stream after the embedding and after each layer."""
+    x = b.get_rows(W["tok_embd"], tokens)
+    if taps is not None:
+        taps.append(x)
+    for i in range(c.n_layer):
+        x = _layer(b, c, W, x, pos, T_, attend, i)
+        if taps is not None:
+            taps.append(x)
+    return _head(b, c, W, x, T_, last_only)
+
+
+def _dense_attend(b: Builder, c: DecoderConfig, caches, slots: T, mask: T, T_: int, n_kv: int, f32_values: bool):
+    hd = c.head_dim
     scale = 1.0 / float(hd) ** 0.5
 
     def attend(i, q, k, v):
@@ -501,11 +506,76 @@ def decoder_step(c: DecoderConfig, n_tokens: int, n_kv: int, last_only: bool = T
         row = c.n_embd_kv * 2
         K = b.permute(b.view(kc, [hd, c.n_head_kv, n_kv], [hd * 2, row], 0), 0, 2, 1, 3)
         V = b.permute(b.view(vc, [hd, c.n_head_kv, n_kv], [hd * 2, row], 0), 0, 2, 1, 3)
+        if f32_values:
+            V = b.cast(V, N.F32)
         Q = b.permute(q, 0, 2, 1, 3)
         return b.reshape(b.flash_attn_ext(Q, K, V, mask, scale), c.n_embd, T_)
 
-    logits, am = _decoder_body(b, c, W, tokens, pos, T_, attend, last_only)
-    return DecoderStep(b, tokens, pos, slots, mask, logits, am, [logits, am])
+    return attend
+
+
+def _dense_caches(b: Builder, c: DecoderConfig):
+    return [(b.state(N.F16, [c.n_embd_kv, c.n_ctx], f"k{i}"), b.state(N.F16, [c.n_embd_kv, c.n_ctx], f"v{i}"))
+            for i in range(c.n_layer)]
+
+
+@dataclass
+class LayerStep:
+    """One layer (or the head) as a graph of its own, fed the residual stream."""
+    builder: Builder
+    x: T        # input 0: residual stream f32 [n_embd, T]
+    out: T      # the layer's residual output, or the logits of the head
+    argmax: T   # the head's argmax (None for a layer)
+    keep: list
+
+
+def decoder_layer_step(c: DecoderConfig, layer: int, n_tokens: int, n_kv: int, f32_values: bool = False) -> LayerStep:
+    """Layer `layer` of decoder_step alone, over the same weights and dense
+    caches: inputs 0 x f32 [n_embd, T], 1 positions i32 [T], 2 cache rows i64
+    [T], 3 mask f16 [n_kv, T]; output the residual stream after the layer."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    caches = _dense_caches(b, c)
+    T_ = n_tokens
+    x = b.input(N.F32, [c.n_embd, T_], "x")
+    pos = b.input(N.I32, [T_], "pos")
+    slots = b.input(N.I64, [T_], "slots")
+    mask = b.input(N.F16, [n_kv, T_], "mask")
+    out = _layer(b, c, W, x, pos, T_, _dense_attend(b, c, caches, slots, mask, T_, n_kv, f32_values), layer)
+    b.expand(out)
+    return LayerStep(b, x, out, None, [out])
+
+
+def decoder_head_step(c: DecoderConfig, n_tokens: int, last_only: bool = True) -> LayerStep:
+    """The decoder's head alone: input 0 x f32 [n_embd, T]; logits and argmax."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    x = b.input(N.F32, [c.n_embd, n_tokens], "x")
+    logits, am = _head(b, c, W, x, n_tokens, last_only)
+    return LayerStep(b, x, logits, am, [logits, am])
+
+
+def decoder_step(c: DecoderConfig, n_tokens: int, n_kv: int, last_only: bool = True,
+                 f32_values: bool = False) -> DecoderStep:
+    """One forward step of `n_tokens` new tokens over a cache whose first `n_kv`
+    rows are attended (llama.cpp's llm_build_llama with the flash-attention
+    path): inputs 0 tokens i32 [T], 1 positions i32 [T], 2 cache rows i64 [T],
+    3 mask f16 [n_kv, T]; logits of the last token (or of every token), and
+    their argmax. f32_values: the attention reads the cached values through an
+    f16 -> f32 cast (the same values; ggml's CPU backend then accumulates P.V in
+    f32 rather than f16)."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    caches = _dense_caches(b, c)
+    T_ = n_tokens
+    tokens = b.input(N.I32, [T_], "tokens")
+    pos = b.input(N.I32, [T_], "pos")
+    slots = b.input(N.I64, [T_], "slots")
+    mask = b.input(N.F16, [n_kv, T_], "mask")
+    taps = []
+    logits, am = _decoder_body(b, c, W, tokens, pos, T_, _dense_attend(b, c, caches, slots, mask, T_, n_kv, f32_values),
+                               last_only, taps)
+    return DecoderStep(b, tokens, pos, slots, mask, logits, am, [logits, am], taps)
 
 
 @dataclass
@@ -589,13 +659,19 @@ def decoder_decode_paged(c: DecoderConfig, pc: PagedConfig, n_seqs: int) -> Page
     b = Builder()
     W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
     pools = _paged_pools(b, c, pc)
-    S, hd = n_seqs, c.head_dim
+    S = n_seqs
     tokens = b.input(N.I32, [S], "tokens")
     pos = b.input(N.I32, [S], "pos")
     slots = b.input(N.I32, [2 * S], "slots")
     tables = b.input(N.I32, [pc.max_blocks, S], "tables")
     lens = b.input(N.I32, [S], "lens")
-    scale = 1.0 / float(hd) ** 0.5
+    attend = _paged_attend(b, c, pc, pools, slots, tables, lens, S)
+    logits, am = _decoder_body(b, c, W, tokens, pos, S, attend, False)
+    return PagedStep(b, tokens, pos, slots, None, tables, lens, logits, am, [logits, am])
+
+
+def _paged_attend(b: Builder, c: DecoderConfig, pc: PagedConfig, pools, slots: T, tables: T, lens: T, S: int):
+    scale = 1.0 / float(c.head_dim) ** 0.5
 
     def attend(i, q, k, v):
         kc, vc = pools[i]
@@ -607,8 +683,25 @@ def decoder_decode_paged(c: DecoderConfig, pc: PagedConfig, n_seqs: int) -> Page
         att = b.paged_attention(q16, kc, vc, tables, lens, pc.block_size, pc.max_ctx, scale, c.n_head_kv)
         return b.cast(b.reshape(att, c.n_embd, S), N.F32)
 
-    logits, am = _decoder_body(b, c, W, tokens, pos, S, attend, False)
-    return PagedStep(b, tokens, pos, slots, None, tables, lens, logits, am, [logits, am])
+    return attend
+
+
+def decoder_layer_decode_paged(c: DecoderConfig, pc: PagedConfig, layer: int, n_seqs: int) -> LayerStep:
+    """Layer `layer` of decoder_decode_paged alone: inputs 0 x f32 [n_embd, S],
+    1 positions i32 [S], 2 slots i32 [2S], 3 block tables i32 [max_blocks, S],
+    4 context lengths i32 [S]; output the residual stream after the layer."""
+    b = Builder()
+    W = {name: b.weight(ty, ne, name) for name, ty, ne in c.weight_shapes()}
+    pools = _paged_pools(b, c, pc)
+    S = n_seqs
+    x = b.input(N.F32, [c.n_embd, S], "x")
+    pos = b.input(N.I32, [S], "pos")
+    slots = b.input(N.I32, [2 * S], "slots")
+    tables = b.input(N.I32, [pc.max_blocks, S], "tables")
+    lens = b.input(N.I32, [S], "lens")
+    out = _layer(b, c, W, x, pos, S, _paged_attend(b, c, pc, pools, slots, tables, lens, S), layer)
+    b.expand(out)
+    return LayerStep(b, x, out, None, [out])
 
 
 def paged_slots(table, positions, block_size: int):

@@ -115,3 +115,53 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
         blocks[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
         return blocks.reshape(M, (K // 256) * 210)
     raise ValueError(wtype)
+
+
+def q4_K_model_blocks(seed: int, M: int, K: int, std: float = 0.02) -> np.ndarray:
+    """Random q4_K blocks that behave like quantized zero-mean weights of
+    standard deviation about `std`: per 32-element sub-block a scale sc in
+    1..63 and a min m = round(15 sc / 16) against dmin = 8 d, so each
+    sub-block's values d sc q - 8 d m (q uniform in 0..15) are centred on zero
+    to within 4 d. (Independent random d, dmin, sc and m, as random_blocks
+    draws them, give every row a large common offset, and with it a model whose
+    logits hardly depend on its input.) uint8 [M, K/256*144]."""
+    nb = M * (K // 256)
+    u = uniform(seed + 1, nb).astype(np.float32)
+    d32 = (np.float32(std) / np.float32(32 * 4.6)) * (np.float32(0.5) + u)
+    d = f16_bits(d32)
+    dmin = f16_bits(d.view(np.float16).astype(np.float32) * np.float32(8))
+    sc = (integers(seed + 2, 1, 63, nb * 8)).astype(np.int64).reshape(nb, 8)
+    mn = np.rint(sc * 15 / 16).astype(np.int64)
+    f = np.zeros((nb, 12), np.uint8)
+    # the 6-bit fields as get_scale_min_k4 reads them (ggml-quants.c:880-887)
+    f[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    f[:, 4:8] = (mn[:, 0:4] & 63) | ((mn[:, 4:8] >> 4) << 6)
+    f[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    blocks = np.empty((nb, 144), np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    blocks[:, 4:16] = f
+    blocks[:, 16:] = bits(seed, nb * 16).view(np.uint8).reshape(nb, 128)
+    return blocks.reshape(M, (K // 256) * 144)
+
+
+def q4_K_model_blocks_gpu(torch, gen, M: int, K: int, std: float = 0.02):
+    """q4_K_model_blocks' distribution drawn on the GPU with a torch generator
+    (for full-size models, where host generation would dominate): a uint8
+    device tensor [M, K/256*144]. Not bit-identical to the host version."""
+    nb = M * (K // 256)
+    dev = gen.device
+    d32 = (std / (32 * 4.6)) * (0.5 + torch.rand(nb, device=dev, generator=gen))
+    d = d32.to(torch.float16)
+    dmin = (d.to(torch.float32) * 8).to(torch.float16)
+    sc = torch.randint(1, 64, (nb, 8), device=dev, generator=gen, dtype=torch.int32)
+    mn = torch.round(sc.to(torch.float32) * 15 / 16).to(torch.int32)
+    f = torch.empty((nb, 12), dtype=torch.int32, device=dev)
+    f[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    f[:, 4:8] = (mn[:, 0:4] & 63) | ((mn[:, 4:8] >> 4) << 6)
+    f[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    blocks = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device=dev, generator=gen)
+    blocks[:, 0:2] = d.view(torch.uint8).reshape(nb, 2)
+    blocks[:, 2:4] = dmin.view(torch.uint8).reshape(nb, 2)
+    blocks[:, 4:16] = f.to(torch.uint8)
+    return blocks.reshape(M, (K // 256) * 144)

@@ -56,7 +56,18 @@ these are the reference's outputs on fixed inputs, captured once:
                    single-token steps, a 3-token chunk): logits and argmax per
                    step and the f16 KV caches after the last one
 
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id]   (needs oracle/_ref built)
+  decoder_8b.npz   BASELINE configs[4]'s decoder at its own shapes (hidden 4096, 32 / 8
+                   heads of 128, FFN 14336, vocab 128256, every matrix q4_K) cut to two
+                   layers (refs.decoder_8b_slice_config, weights refs.decoder_8b_weights):
+                   logits, argmax and written cache rows of refs.DECODER_8B_STEPS on the
+                   CPU backend with the attention's P.V accumulated in f32 (the cached
+                   values read through an f32 cast), and the default run's logits
+                   (f16 P.V accumulation) as f16; the residual stream after the
+                   embedding and each layer, and each layer fed that stream with f16 P.V
+                   accumulation; for refs.paged_8b_seqs, each sequence run alone, the
+                   argmax and 8 largest logits of each step (f32 P.V) and how far the
+                   two accumulations move that step's logits.
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -70,6 +81,8 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 sys.path.insert(0, str(HERE.parents[1]))
 
+from refs import (DECODER_8B_STEPS, decoder_8b_layer_ref, decoder_8b_ref_run, decoder_8b_slice_config,  # noqa: E402
+                  decoder_8b_weights, paged_8b_ref)
 from refs import (FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
                   decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, mmid_case, paged_ref_run,
                   xorshift_noise)
@@ -173,8 +186,43 @@ def decoder_golden(ref) -> None:
     np.savez_compressed(HERE / "decoder.npz", **out)
 
 
+def decoder_8b_golden(ref) -> None:
+    """The 8B-shaped two-layer slice (refs.decoder_8b_slice_config) on the CPU
+    backend, with f32 and with f16 P.V accumulation: logits and argmax of
+    DECODER_8B_STEPS, the cache rows they write, the residual stream per layer
+    (and each layer's output from it with the other accumulation), and the 16
+    paged_8b_seqs sequences each run alone."""
+    c = decoder_8b_slice_config()
+    w = decoder_8b_weights(c)
+    logits, ams, _, _ = decoder_8b_ref_run(ref, c, w)
+    rows = max(p0 + len(t) for t, p0, _, _ in DECODER_8B_STEPS)
+    # the default run's logits as f16 (they bound how far the CPU's own f16 P.V
+    # accumulation moves the logits, a few percent; f16 keeps 3 decimal digits)
+    out = {f"logits{i}": lg.astype(np.float16) for i, lg in enumerate(logits)}
+    out.update({f"argmax{i}": a for i, a in enumerate(ams)})
+    logits32, ams32, caches32, taps32 = decoder_8b_ref_run(ref, c, w, f32_values=True)
+    out.update({f"logits_f32pv{i}": lg for i, lg in enumerate(logits32)})
+    out.update({f"argmax_f32pv{i}": a for i, a in enumerate(ams32)})
+    caches = [s[:rows] for s in caches32]
+    out.update({f"cache{i}": s for i, s in enumerate(caches)})
+    # the residual stream after the embedding and each layer (f32 P.V run), and
+    # each layer fed that stream with f16 P.V accumulation instead (how far the
+    # CPU's own two accumulations put one layer's output apart)
+    for i, step in enumerate(DECODER_8B_STEPS):
+        for layer in range(c.n_layer + 1):
+            out[f"tap{i}_{layer}"] = taps32[i][layer]
+        for layer in range(c.n_layer):
+            out[f"tf16_{i}_{layer}"] = decoder_8b_layer_ref(ref, c, w, caches, step, layer, taps32[i][layer], False)
+    am, ti, tv, spread = paged_8b_ref(ref, c, w)
+    out.update(paged_argmax=am, paged_top_index=ti, paged_top_logit=tv, paged_spread=spread)
+    np.savez_compressed(HERE / "decoder_8b.npz", **out)
+
+
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["decoder_8b"]:  # only the 8B-shaped decoder fixture
+        decoder_8b_golden(ref)
+        return
     if sys.argv[1:] == ["mul_mat_id"]:  # only the MUL_MAT_ID fixture
         mul_mat_id_golden(ref)
         return
@@ -260,6 +308,7 @@ def main() -> None:
     core_golden(ref)
     decoder_golden(ref)
     decoder_paged_golden(ref)
+    decoder_8b_golden(ref)
     mul_mat_id_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")

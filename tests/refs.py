@@ -992,6 +992,123 @@ def decoder_ref_run(r, c, weights):
     return logits, ams, states
 
 
+# --------------------------------------------------- 8B-shaped decoder slice
+def decoder_8b_slice_config():
+    """BASELINE configs[4]'s Llama-style 8B decoder at its own shapes (hidden
+    4096, 32 / 8 heads of 128, SwiGLU FFN 14336, vocab 128256, RoPE theta
+    500000, every matrix q4_K including the token embedding and lm_head) cut to
+    its first two layers, with a 1024-row cache."""
+    from tensorlisp_amd import graph as G
+
+    return G.DecoderConfig(n_layer=2, n_ctx=1024, wtype=Q4_K, embd_type=Q4_K, out_type=Q4_K)
+
+
+def decoder_8b_weights(c, seed=300):
+    """Random-init weights for an 8B-shaped config: q4_K blocks that behave like
+    quantized zero-mean N(0, 0.02) weights (synth.q4_K_model_blocks), f32 norm
+    weights near one."""
+    from tensorlisp_amd import native as N
+    from tensorlisp_amd import synth
+
+    out = []
+    for i, (_, ty, ne) in enumerate(c.weight_shapes()):
+        if ty == N.F32:
+            out.append((1.0 + 0.1 * synth.normal(seed + i, (ne[0],))).astype(np.float32))
+        else:
+            out.append(synth.q4_K_model_blocks(seed + i, ne[1], ne[0], 0.02))
+    return out
+
+
+# (tokens, first position, attended cache rows, logits of every token?): a
+# 6-token prompt, three single-token steps (the last over a 768-row cache view,
+# the bench's padded decode view, which splits the attention into partitions),
+# then a 3-token chunk with every token's logits
+DECODER_8B_STEPS = [([128000, 791, 3938, 315, 279, 1917], 0, 8, False), ([374], 6, 8, False),
+                    ([264], 7, 16, False), ([128255], 8, 768, False), ([0, 65535, 100000], 9, 16, True)]
+
+
+def decoder_8b_ref_run(r, c, weights, steps=DECODER_8B_STEPS, f32_values=False):
+    """`steps` of the 8B slice through the reference CPU backend (one dense
+    cache); returns (logits per step, argmax per step, final caches). With
+    f32_values the attention reads the cached values through an f32 cast, so
+    the CPU accumulates P.V in f32 instead of f16 (same model, same values)."""
+    from tensorlisp_amd import graph as G
+
+    states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
+    logits, ams, taps = [], [], []
+    for step in steps:
+        st = G.decoder_step(c, len(step[0]), step[2], last_only=not step[3], f32_values=f32_values)
+        res = r.ir_run(st.builder, weights, states, decoder_step_inputs(step),
+                       [(st.logits, np.float32), (st.argmax, np.int32)] + [(t, np.float32) for t in st.taps])
+        logits.append(res[0].reshape(-1, c.n_vocab))
+        ams.append(res[1].reshape(-1))
+        taps.append([x.reshape(len(step[0]), c.n_embd) for x in res[2:]])
+    return logits, ams, states, taps
+
+
+def decoder_8b_layer_ref(r, c, weights, caches, step, layer, x, f32_values):
+    """Layer `layer` alone (graph.decoder_layer_step) on the reference CPU backend
+    for decode step `step`, fed the residual stream x [T, n_embd], over dense
+    caches holding `caches` (rows past the step's first position are masked or
+    overwritten); returns the layer's output [T, n_embd]."""
+    from tensorlisp_amd import graph as G
+
+    toks, p0, n_kv, _ = step
+    T_ = len(toks)
+    states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
+    for s, cache in zip(states, caches):
+        s[:len(cache)] = cache
+    ls = G.decoder_layer_step(c, layer, T_, n_kv, f32_values)
+    pos = np.arange(T_, dtype=np.int32) + p0
+    (out,) = r.ir_run(ls.builder, weights, states, [np.ascontiguousarray(x, np.float32), pos, pos.astype(np.int64),
+                                                    G.causal_mask(pos, n_kv)], [(ls.out, np.float32)])
+    return out.reshape(T_, c.n_embd)
+
+
+# 16 sequences of the 8B slice for a batched paged decode: prompts of 1..16
+# tokens, then two decode tokens each
+def paged_8b_seqs():
+    from tensorlisp_amd import synth
+
+    toks = synth.integers(330, 0, 128255, 16 * 18).astype(np.int64).reshape(16, 18)
+    return [([int(t) for t in toks[s, :s + 1]], [int(toks[s, 16]), int(toks[s, 17])]) for s in range(16)]
+
+
+def paged_8b_ref(r, c, weights, top=8):
+    """Each paged_8b_seqs sequence alone through the reference CPU backend with the
+    dense-cache step, with its attention's P.V accumulated in f32 and, again, in
+    f16 (the backend's default). For the prompt and each decode step ([3, S]):
+    the argmax and the `top` largest logits of the f32 run (indices and values,
+    [3, S, top]), and the largest |difference| between the two runs' logits
+    (how far the backend's own accumulation choice moves them)."""
+    from tensorlisp_amd import graph as G
+
+    seqs = paged_8b_seqs()
+    am = np.zeros((3, len(seqs)), np.int32)
+    ti = np.zeros((3, len(seqs), top), np.int32)
+    tv = np.zeros((3, len(seqs), top), np.float32)
+    spread = np.zeros((3, len(seqs)), np.float32)
+    for s, (prompt, dec) in enumerate(seqs):
+        rows = {}
+        for f32v in (True, False):
+            states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
+            todo = [(prompt, 0)] + [([t], len(prompt) + j) for j, t in enumerate(dec)]
+            for k, (toks, p0) in enumerate(todo):
+                n_kv = p0 + len(toks)
+                st = G.decoder_step(c, len(toks), n_kv, f32_values=f32v)
+                lg, a = r.ir_run(st.builder, weights, states, decoder_step_inputs((toks, p0, n_kv, False)),
+                                 [(st.logits, np.float32), (st.argmax, np.int32)])
+                rows[(f32v, k)] = lg.reshape(-1)
+                if f32v:
+                    am[k, s] = a.reshape(-1)[0]
+        for k in range(3):
+            lg = rows[(True, k)]
+            idx = np.argsort(-lg, kind="stable")[:top]
+            ti[k, s], tv[k, s] = idx, lg[idx]
+            spread[k, s] = np.abs(lg - rows[(False, k)]).max()
+    return am, ti, tv, spread
+
+
 # ------------------------------------------------------- paged decoder steps
 # Three sequences (prompt tokens, then three decode tokens fed one per step),
 # block tables into a 16-block pool of 16-row blocks.
