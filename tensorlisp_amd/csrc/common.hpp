@@ -194,6 +194,39 @@ __device__ __forceinline__ float wave_max(float v) {
 // made visible to the other waves.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Sum over the 256 threads of a workgroup, in an order fixed by the lane and
+// wave layout (so every kernel that uses it adds the same values alike).
+template <typename T> __device__ __forceinline__ T wave_sum_t(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+template <typename T> __device__ __forceinline__ T block_sum_t(T v, T *sh) {
+    v = wave_sum_t(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const T r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
+}
+// The same sum with LDS-only barriers: global loads issued before it stay in flight.
+template <typename T> __device__ __forceinline__ T block_sum_lds(T v, T *sh) {
+    v = wave_sum_t(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    lds_barrier();
+    const T r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    lds_barrier();
+    return r;
+}
+
+// ggml's silu in f32 as the CPU's x86-64 build evaluates it (vec.h
+// ggml_silu_f32: x / (1 + expf(-x))), then SwiGLU's product with the gate's
+// partner (vec.h ggml_vec_swiglu_f32).
+__device__ __forceinline__ float swiglu_val(float x, float g) {
+#pragma clang fp contract(off)
+    return (x / (1.0f + expf(-x))) * g;
+}
+
 // int8x4 dot product with accumulate (v_dot4c_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

@@ -262,7 +262,7 @@ __device__ __forceinline__ float glu_val(int code, float x, float g) {
     switch (code) {
     case 0: return (x > 0.f) ? x * g : 0.f;
     case 1: return x <= -10.0f ? 0.0f : x >= 10.0f ? x * g : gelu_f16(h2f(f2h(x))) * g;
-    case 2: return (x / (1.0f + expf(-x))) * g;
+    case 2: return swiglu_val(x, g);
     case 4: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)) * g;
     default: return gelu_quick_tab(x) * g;
     }
@@ -298,20 +298,7 @@ __global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
 }
 
 // ------------------------------------------------------------ block reduces
-template <typename T> __device__ __forceinline__ T wave_sum_t(T v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
-}
-// sum over the 256 threads, order fixed by the lane and wave layout
-template <typename T> __device__ __forceinline__ T block_sum_t(T v, T *sh) {
-    v = wave_sum_t(v);
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const T r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
-    __syncthreads();
-    return r;
-}
+// (wave_sum_t and block_sum_t: common.hpp)
 __device__ __forceinline__ float block_max_f(float v, float *sh) {
     v = wave_max(v);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;

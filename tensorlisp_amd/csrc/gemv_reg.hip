@@ -19,6 +19,8 @@
 //
 // Block products follow the CPU's vec_dot (ggml-cpu/quants.c:225-258,
 // :451-476, :696-773): exact int32 sums on v_dot4, scaled in f32.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace tlh {
@@ -62,103 +64,207 @@ template <int WT> __device__ __forceinline__ int64_t unit_e0(int64_t u) {
 }
 template <int WT> constexpr int unit_off1() { return WT == TLH_TYPE_Q6_K ? 64 : 32; }
 
-template <int AT, int WT>
-__device__ __forceinline__ void quantize_unit(const float *xr, int64_t u, bool valid, AUnit &o) {
+// ------------------------------------------------ in-kernel activation rows
+// A workgroup quantizes each activation column once into LDS, in the layout
+// of the split scratch (codes int8 [K], block scales f32, per-block code sums:
+// int32 per 32 for q8_0, int16 bsums per 16 for q8_K), and every wave then
+// reads its lanes' units from there. Thread t quantizes 16-element groups
+// t, t + 256, ...: a q8_K super-block is a team of 16 consecutive threads, a
+// q8_0 block a pair. The values and rules are quantize_row_q8_K_ref's
+// (ggml-quants.c:2768-2804: the first element of largest magnitude keeps its
+// sign, iscale = -127 / max, codes min(127, round-half-even(iscale * x)),
+// d = 1 / iscale, zero blocks all zero) and quantize_row_q8_0_ref's
+// (:276-297: d = amax / 127, codes roundf(x / d) with the unrounded d, the
+// f16-rounded d stored).
+struct ActLds {
+    int64_t q_off, d_off, s_off, bytes;  // per activation column
+};
+__host__ __device__ inline ActLds act_lds(int act_type, int64_t K) {
+    ActLds L;
+    L.q_off = 0;
+    L.d_off = align_up(K, 16);
+    const int64_t nd = K / (act_type == TLH_TYPE_Q8_K ? QKK : QK);
+    L.s_off = align_up(L.d_off + 4 * nd, 16);
+    L.bytes = align_up(L.s_off + (act_type == TLH_TYPE_Q8_K ? 2 * (K / 16) : 4 * (K / 32)), 16);
+    return L;
+}
+
+// A thread's share of one activation column: 16-element groups t, t + 256,
+// ... (G of them; K <= 4096 * G), loaded into registers before the weight
+// loads are issued, so that quantizing them does not wait for the weights
+// (vector loads complete in order). IN_X: the values of x; IN_NORM: x = p + q
+// and the norm weight w (K <= 4096).
+// IN_X: x with K <= 4096; IN_XL: x with K <= 16384; IN_NORM: the prologue's
+// p, q, w with K <= 4096.
+enum { IN_SCRATCH = 0, IN_X = 1, IN_NORM = 2, IN_XL = 3 };
+
+template <int IN> struct ActRegs {
+    static constexpr int G = IN == IN_XL ? 4 : 1;
+    float v[G][16];
+    float w[IN == IN_NORM ? 16 : 1];
+    __device__ __forceinline__ void load(const float *__restrict__ xr, const float *__restrict__ qr,
+                                         const float *__restrict__ wr, int64_t K) {
 #pragma clang fp contract(off)
-    const int64_t e0 = unit_e0<WT>(u);
-    constexpr int OFF1 = unit_off1<WT>();
-    float v[64];
+        const int t = threadIdx.x;
+        const int64_t groups = K / 16;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (valid) f = *(const float4 *)(xr + e0 + (i < 8 ? 4 * i : OFF1 + 4 * (i - 8)));
-        v[4 * i] = f.x;
-        v[4 * i + 1] = f.y;
-        v[4 * i + 2] = f.z;
-        v[4 * i + 3] = f.w;
+        for (int gi = 0; gi < G; ++gi) {
+            const int64_t g = t + 256 * gi;
+            const int64_t gc = g < groups ? g : 0;  // in bounds; unused
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float4 f = *(const float4 *)(xr + 16 * gc + 4 * k);
+                if constexpr (IN == IN_NORM) {
+                    if (qr) {
+                        const float4 h = *(const float4 *)(qr + 16 * gc + 4 * k);
+                        f = make_float4(f.x + h.x, f.y + h.y, f.z + h.z, f.w + h.w);
+                    }
+                    const float4 ww = *(const float4 *)(wr + 16 * gc + 4 * k);
+                    w[4 * k] = ww.x, w[4 * k + 1] = ww.y, w[4 * k + 2] = ww.z, w[4 * k + 3] = ww.w;
+                }
+                v[gi][4 * k] = f.x, v[gi][4 * k + 1] = f.y, v[gi][4 * k + 2] = f.z, v[gi][4 * k + 3] = f.w;
+            }
+        }
     }
-    if constexpr (AT == TLH_TYPE_Q8_0) {
+    // IN_NORM: y = (x * scale) * w with scale = 1 / sqrtf((float)(sum of x*x
+    // in double / K) + eps), as ggml's RMS_NORM then MUL form it (the double
+    // sum in another order than the CPU's: equal after its rounding to f32 but
+    // for sums within 1e-16 of a rounding boundary); x itself goes to sr.
+    __device__ __forceinline__ void norm(float *__restrict__ sr, int64_t K, float eps, double *shd) {
+#pragma clang fp contract(off)
+        const int t = threadIdx.x;
+        const bool live = t < K / 16;
+        double s1 = 0.0;
+        if (live) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+            for (int i = 0; i < 16; ++i) s1 += (double)(v[0][i] * v[0][i]);
+            if (sr) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    *(float4 *)(sr + 16 * t + 4 * k) = make_float4(v[0][4 * k], v[0][4 * k + 1], v[0][4 * k + 2],
+                                                                   v[0][4 * k + 3]);
+            }
+        }
+        const float mean = (float)(block_sum_lds(s1, shd) / (double)K);
+        const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[0][i] = (v[0][i] * scale) * w[i];
+    }
+};
+
+template <int AT, int IN>
+__device__ void coop_quantize(const ActRegs<IN> &ar, int64_t K, char *lds) {
+#pragma clang fp contract(off)
+    const ActLds L = act_lds(AT, K);
+    int8_t *sq = (int8_t *)(lds + L.q_off);
+    float *sd = (float *)(lds + L.d_off);
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t groups = K / 16;
+#pragma unroll
+    for (int gi = 0; gi < ActRegs<IN>::G; ++gi) {
+        const int64_t g = t + 256 * gi;
+        if (256 * gi + (t & ~(AT == TLH_TYPE_Q8_K ? 15 : 1)) >= groups) continue;  // whole teams drop out
+        const float *v = ar.v[gi];
+        int c[16];
+        if constexpr (AT == TLH_TYPE_Q8_K) {
+            // the first element of largest magnitude: within the thread, then
+            // across the team (on equal magnitudes the lower lane's is earlier)
+            float ba = 0.0f, bv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float a = fabsf(v[i]);
+                if (a > ba) ba = a, bv = v[i];
+            }
+#pragma unroll
+            for (int m = 1; m <= 8; m <<= 1) {
+                const float oa = __shfl_xor(ba, m, 64), ov = __shfl_xor(bv, m, 64);
+                if (oa > ba || (oa == ba && (lane & m))) ba = oa, bv = ov;
+            }
+            float iscale = 0.0f, d = 0.0f;
+            if (ba != 0.0f) {
+                iscale = -127.0f / bv;
+                d = 1.0f / iscale;
+            }
+            int sum = 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                int q = 0;
+                if (ba != 0.0f) {
+                    q = (int)rintf(iscale * v[i]);
+                    q = q > 127 ? 127 : q;
+                }
+                c[i] = q;
+                sum += q;
+            }
+            ((int16_t *)(lds + L.s_off))[g] = (int16_t)sum;
+            if ((lane & 15) == 0) sd[g / 16] = d;
+        } else {
             float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[32 * b + i]));
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             int sum = 0;
 #pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                uint32_t packed = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int c = (int)roundf(v[32 * b + 4 * w + i] * id);
-                    packed |= (uint32_t)(uint8_t)(int8_t)c << (8 * i);
-                    sum += c;
-                }
-                o.q[8 * b + w] = (int)packed;
+            for (int i = 0; i < 16; ++i) {
+                c[i] = (int)roundf(v[i] * id);
+                sum += c[i];
             }
-            if (b == 0) {
-                o.d0 = h2f(f2h(d));
-                o.s0 = sum;
-            } else {
-                o.d1 = h2f(f2h(d));
-                o.s1 = sum;
+            sum += __shfl_xor(sum, 1, 64);
+            if ((lane & 1) == 0) {
+                sd[g / 2] = h2f(f2h(d));
+                ((int32_t *)(lds + L.s_off))[g / 2] = sum;
             }
         }
+        uint32_t w4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w4[k] = (uint32_t)(uint8_t)c[4 * k] | ((uint32_t)(uint8_t)c[4 * k + 1] << 8) |
+                    ((uint32_t)(uint8_t)c[4 * k + 2] << 16) | ((uint32_t)(uint8_t)c[4 * k + 3] << 24);
+        *(uint4 *)(sq + 16 * g) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+}
+
+// A lane's unit u from an LDS activation column (zeros when !valid).
+template <int AT, int WT>
+__device__ __forceinline__ void lds_unit(const char *lds, int64_t K, int64_t u, bool valid, AUnit &o) {
+    const ActLds L = act_lds(AT, K);
+    const int64_t uc = valid ? u : 0;
+    const int e0 = (int)unit_e0<WT>(uc);
+    constexpr int OFF1 = unit_off1<WT>();
+    const int8_t *sq = (const int8_t *)(lds + L.q_off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int4 t = *(const int4 *)(sq + e0 + (i < 2 ? 16 * i : OFF1 + 16 * (i - 2)));
+        o.q[4 * i] = valid ? t.x : 0;
+        o.q[4 * i + 1] = valid ? t.y : 0;
+        o.q[4 * i + 2] = valid ? t.z : 0;
+        o.q[4 * i + 3] = valid ? t.w : 0;
+    }
+    const float *sd = (const float *)(lds + L.d_off);
+    if constexpr (AT == TLH_TYPE_Q8_0) {
+        const int32_t *ss = (const int32_t *)(lds + L.s_off);
+        const float d0 = sd[e0 / 32], d1 = sd[e0 / 32 + 1];
+        const int s0 = ss[e0 / 32], s1 = ss[e0 / 32 + 1];
+        o.d0 = valid ? d0 : 0.0f;
+        o.d1 = valid ? d1 : 0.0f;
+        o.s0 = valid ? s0 : 0;
+        o.s1 = valid ? s1 : 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o.b[k] = 0;
     } else {
-        // signed value of largest magnitude in the 256-element super-block,
-        // first index on ties: in-lane over 64 (in element order), then across
-        // the 4 lanes
-        float ba = 0.0f, bv = 0.0f;
-        int bi = 1 << 30;
-        const int base = (int)(e0 & 255);
-#pragma unroll
-        for (int i = 0; i < 64; ++i) {
-            const float a = fabsf(v[i]);
-            if (a > ba) {
-                ba = a;
-                bv = v[i];
-                bi = base + (i < 32 ? i : OFF1 + i - 32);
-            }
-        }
-#pragma unroll
-        for (int m = 1; m <= 2; m <<= 1) {
-            const float oa = __shfl_xor(ba, m, 64);
-            const float ov = __shfl_xor(bv, m, 64);
-            const int oi = __shfl_xor(bi, m, 64);
-            if (oa > ba || (oa == ba && oi < bi)) {
-                ba = oa;
-                bv = ov;
-                bi = oi;
-            }
-        }
-        float d = 0.0f, iscale = 0.0f;
-        if (ba != 0.0f) {
-            iscale = -127.0f / bv;
-            d = 1.0f / iscale;
-        }
-        int s[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-            uint32_t packed = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int c = 0;
-                if (ba != 0.0f) {
-                    c = (int)rintf(iscale * v[4 * w + i]);
-                    c = c > 127 ? 127 : c;
-                }
-                packed |= (uint32_t)(uint8_t)(int8_t)c << (8 * i);
-                s[w / 4] += c;
-            }
-            o.q[w] = (int)packed;
-        }
-        o.d0 = d;
+        const int16_t *bs = (const int16_t *)(lds + L.s_off);
+        const float d0 = sd[e0 / QKK];
+        const int b0 = bs[e0 / 16], b1 = bs[e0 / 16 + 1], b2 = bs[(e0 + OFF1) / 16], b3 = bs[(e0 + OFF1) / 16 + 1];
+        o.d0 = valid ? d0 : 0.0f;
         o.d1 = 0.0f;
-        o.s0 = s[0] + s[1];
-        o.s1 = s[2] + s[3];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o.b[k] = s[k];
+        o.b[0] = valid ? b0 : 0;
+        o.b[1] = valid ? b1 : 0;
+        o.b[2] = valid ? b2 : 0;
+        o.b[3] = valid ? b3 : 0;
+        o.s0 = o.b[0] + o.b[1];
+        o.s1 = o.b[2] + o.b[3];
     }
 }
 
@@ -201,30 +307,24 @@ __device__ __forceinline__ void load_unit(const ActView g, int64_t arow, int64_t
     }
 }
 
-template <int LV>
-__device__ __forceinline__ float treduce(float (&v)[1 << LV], int lane, int &vidx) {
-    constexpr int V = 1 << LV;
-    float w[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) w[i] = v[i];
-    vidx = 0;
-#pragma unroll
-    for (int step = 0; step < LV; ++step) {
-        const int half = V >> (step + 1);
-        const int mask = 32 >> step;
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int i = 0; i < half; ++i) {
-            const float keep = upper ? w[half + i] : w[i];
-            const float give = upper ? w[i] : w[half + i];
-            w[i] = keep + __shfl_xor(give, mask, 64);
-        }
-        vidx += upper ? half : 0;
-    }
-    float r = w[0];
-#pragma unroll
-    for (int m = 32 >> LV; m >= 1; m >>= 1) r += __shfl_xor(r, m, 64);
-    return r;
+// Sum of v over the 64 lanes of a wave, the same in every lane: each row of
+// 16 lanes adds by DPP row shifts (an inclusive scan: lane 15 of the row ends
+// with the row's sum), then the four row sums are read out of lanes 15, 31,
+// 47 and 63 and added in a fixed order. No LDS round trips.
+template <int CTRL> __device__ __forceinline__ float dpp_row_shr(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_row_shr<0x111>(v);  // row_shr:1
+    v += dpp_row_shr<0x112>(v);  // row_shr:2
+    v += dpp_row_shr<0x114>(v);  // row_shr:4
+    v += dpp_row_shr<0x118>(v);  // row_shr:8
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 47));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 63));
+    return (r0 + r1) + (r2 + r3);
 }
 
 template <int X> struct L2 { static constexpr int v = 1 + L2<X / 2>::v; };
@@ -470,14 +570,19 @@ template <int R> struct WRegs<TLH_TYPE_Q8_0, R> {
 // PIPE: double-buffer the weight registers so the next row block's loads are
 // in flight while this one is multiplied (for grids that loop over many row
 // blocks; it costs the registers of a second weight set).
-template <int WT, int NC, int R, bool FUSED, bool PIPE>
+// IN: where the activation comes from (IN_SCRATCH: the split scratch a
+// quantize launch filled; IN_X: src1 rows, quantized by the workgroup into
+// LDS; IN_NORM: the GemvPro prologue's rows, likewise). GLU: the GemvPro
+// SwiGLU epilogue (rows of a wave pair gate and up rows: R / 2 of each).
+template <int WT, int NC, int R, int IN, bool PIPE, bool GLU>
 __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const float *__restrict__ x,
-                                                  int64_t x_row_bytes, int ksplit, int upw) {
+                                                  int64_t x_row_bytes, int ksplit, int upw, const GemvPro pro) {
     constexpr int AT = vec_dot_type(WT);
     constexpr int V = R * NC;
-    constexpr int LV = L2<V>::v + ((V & (V - 1)) ? 1 : 0);
-    constexpr int VP = 1 << LV;
-    __shared__ float part[4][VP];
+    static_assert(!GLU || R % 2 == 0, "GLU pairs R / 2 gate rows with R / 2 up rows");
+    __shared__ float part[4][V];
+    __shared__ double shd[4];
+    extern __shared__ __align__(16) char s_act[];  // IN != IN_SCRATCH: NC activation columns
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int groups = 4 / ksplit;
@@ -487,110 +592,180 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     const int64_t u = (int64_t)kw * upw + lane;
     const bool uvalid = lane < upw && u < units;
     const int64_t batch = blockIdx.z;
-    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
-    const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
+    int64_t i12 = 0, i13 = 0;
+    const uint8_t *W = a.w;
+    if (gridDim.z > 1) {  // 64-bit divisions only where there are batch slices
+        i12 = batch % a.ne12, i13 = batch / a.ne12;
+        W += (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
+    }
     const int64_t arow0 = a.n0 + a.N_total * batch;
-    const int64_t rows_per_block = (int64_t)groups * R;
+    // output rows a workgroup covers per step (GLU: rows of h, R / 2 per wave)
+    constexpr int RO = GLU ? R / 2 : R;
+    const int64_t rows_per_block = (int64_t)groups * RO;
 
-    // segment of launch row m (a.nseg > 0): which matrix it belongs to
+    // segment of launch row m (a.nseg > 0): which matrix it belongs to. The
+    // segment fields are picked by selects, never indexed by a run-time value
+    // (that would read the kernel arguments with vector loads and a wait).
     auto seg_of = [&](int64_t m) { return (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]); };
+    auto sel = [](int sg, auto x0, auto x1, auto x2) { return sg == 0 ? x0 : sg == 1 ? x1 : x2; };
     auto row_ptrs = [&](int64_t rb, const uint8_t *(&wrow)[R]) {
-        const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
+        const int64_t m0 = rb * rows_per_block + (int64_t)grp * RO;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // clamp: loads in bounds, store skipped
-            if (a.nseg > 0) {
-                const int sg = seg_of(m);
-                wrow[r] = a.seg_w[sg] + (m - a.seg_m0[sg]) * a.seg_w_nb1[sg];
+            if constexpr (GLU) {  // gate rows m0 .. m0 + RO - 1, then the same rows of up
+                const int rr = r % RO;
+                const int64_t m = m0 + rr < a.M ? m0 + rr : a.M - 1;
+                wrow[r] = r < RO ? a.seg_w[0] + m * a.seg_w_nb1[0] : a.seg_w[1] + m * a.seg_w_nb1[1];
             } else {
-                wrow[r] = W + m * a.w_nb1;
+                const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // clamp: loads in bounds, store skipped
+                if (a.nseg > 0) {
+                    const int sg = seg_of(m);
+                    wrow[r] = sel(sg, a.seg_w[0], a.seg_w[1], a.seg_w[2]) +
+                              (m - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2])) *
+                                  sel(sg, a.seg_w_nb1[0], a.seg_w_nb1[1], a.seg_w_nb1[2]);
+                } else {
+                    wrow[r] = W + m * a.w_nb1;
+                }
             }
         }
     };
 
-
-    // the first row block's weights are requested before the activation
-    // slice is read and quantized, so the two memory latencies overlap
+    // In-kernel activations are loaded first, then the first row block's
+    // weights are requested, so quantizing waits only for the activations
+    // while the weights are in flight.
+    ActRegs<IN == IN_SCRATCH ? IN_X : IN> ar[IN == IN_SCRATCH ? 1 : NC];
+    if constexpr (IN != IN_SCRATCH) {
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
+            if constexpr (IN == IN_NORM)
+                ar[n].load((const float *)((const char *)pro.p + arow * pro.p_nb1),
+                           pro.q ? (const float *)((const char *)pro.q + arow * pro.q_nb1) : nullptr, pro.w, K);
+            else
+                ar[n].load((const float *)((const char *)x + arow * x_row_bytes), nullptr, nullptr, K);
+        }
+    }
+    // Weight loads are never predicated: lanes past K load unit 0 (in bounds;
+    // their activations are zero) and rows past M are clamped. A load behind a
+    // branch would make the compiler wait for every outstanding load where the
+    // branch rejoins, instead of only for the ones the next step needs.
     WRegs<WT, R> cur;
-    int64_t rb = blockIdx.x;
-    bool have = rb * rows_per_block < a.M;
-    if (have && uvalid) {
+    const int64_t nblocks = (a.M + rows_per_block - 1) / rows_per_block;
+    int64_t rb = blockIdx.x;  // the launch never has more workgroups than row blocks
+    const int64_t ul = uvalid ? u : 0;
+    {
         const uint8_t *wrow[R];
         row_ptrs(rb, wrow);
-        cur.load(wrow, u);
+        cur.load(wrow, ul);
     }
 
     AUnit act[NC];
+    if constexpr (IN == IN_SCRATCH) {
 #pragma unroll
-    for (int n = 0; n < NC; ++n) {
-        const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
-        if constexpr (FUSED) {
-            quantize_unit<AT, WT>((const float *)((const char *)x + arow * x_row_bytes), u, uvalid, act[n]);
-        } else {
+        for (int n = 0; n < NC; ++n) {
+            const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
             const ActView g = act_view(a.act, AT, K, a.N_total * a.ne12 * a.ne13);
             load_unit<AT, WT>(g, arow, K, u, uvalid, act[n]);
         }
+    } else {
+        const ActLds L = act_lds(AT, K);
+        const bool writer = blockIdx.x == 0 && blockIdx.z == 0;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if constexpr (IN == IN_NORM) {
+                const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
+                float *sr = (writer && pro.s && n < a.N) ? (float *)((char *)pro.s + arow * pro.s_nb1) : nullptr;
+                ar[n].norm(sr, K, pro.eps, shd);
+            }
+            coop_quantize<AT>(ar[n], K, s_act + n * L.bytes);
+        }
+        lds_barrier();
+#pragma unroll
+        for (int n = 0; n < NC; ++n) lds_unit<AT, WT>(s_act + n * L.bytes, K, u, uvalid, act[n]);
     }
 
     char *dbase = a.nseg > 0 ? nullptr : (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
     auto store = [&](int64_t m, int n, float v) {
         if (a.nseg > 0) {
             const int sg = seg_of(m);
-            a.seg_dst[sg][m - a.seg_m0[sg]] = v;
+            sel(sg, a.seg_dst[0], a.seg_dst[1], a.seg_dst[2])[m - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2])] = v;
         } else {
             *(float *)(dbase + (a.n0 + n) * a.d_nb1 + m * 4) = v;
         }
     };
-    while (have) {
-        const int64_t rb_next = rb + gridDim.x;
-        const bool have_next = rb_next * rows_per_block < a.M;
-        WRegs<WT, R> nxt;
-        if constexpr (PIPE) {
-            if (have_next && uvalid) {
-                const uint8_t *wrow[R];
-                row_ptrs(rb_next, wrow);
-                nxt.load(wrow, u);
-            }
-        }
+    // products of row block rbk, their wave sums, the K slices merged, stored
+    auto finish = [&](const WRegs<WT, R> &w, int64_t rbk) {
         float acc[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int n = 0; n < NC; ++n) acc[r][n] = 0.0f;
-        if (uvalid) cur.template compute<NC>(act, u, acc);
+        if (uvalid) w.template compute<NC>(act, u, acc);
 
-        const int64_t m0 = rb * rows_per_block + (int64_t)grp * R;
-        float vals[VP];
+        const int64_t m0 = rbk * rows_per_block + (int64_t)grp * RO;
+        // every lane ends with all V totals (value i = row i / NC, column i % NC)
+        float tot[V];
 #pragma unroll
-        for (int i = 0; i < VP; ++i) vals[i] = i < V ? acc[i / NC][i % NC] : 0.0f;
-        int vi;
-        const float tot = treduce<LV>(vals, lane, vi);
-        const bool holder = (lane & ((64 / VP) - 1)) == 0;
-        if (ksplit == 1) {
-            if (holder && vi < V) {
-                const int r = vi / NC, n = vi % NC;
-                if (m0 + r < a.M && n < a.N) store(m0 + r, n, tot);
+        for (int i = 0; i < V; ++i) tot[i] = wave_total(acc[i / NC][i % NC]);
+        bool emit = ksplit == 1;
+        if (ksplit > 1) {  // the K slices of a row group meet in LDS; the first wave adds them in order
+            if (lane < V) {
+                float mine = tot[0];
+#pragma unroll
+                for (int i = 1; i < V; ++i) mine = lane == i ? tot[i] : mine;
+                part[wave][lane] = mine;
+            }
+            lds_barrier();
+            emit = kw == 0;
+            if (emit) {
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    float t = 0.0f;
+                    for (int s2 = 0; s2 < ksplit; ++s2) t += part[grp * ksplit + s2][i];
+                    tot[i] = t;
+                }
+            }
+            lds_barrier();
+        }
+        // lane i < V (or < V / 2 with the epilogue) stores value i
+        float mine = tot[0], up = GLU ? tot[V / 2] : 0.0f;
+#pragma unroll
+        for (int i = 1; i < V; ++i) mine = lane == i ? tot[i] : mine;
+        if constexpr (GLU) {
+#pragma unroll
+            for (int i = 1; i < V / 2; ++i) up = lane == i ? tot[V / 2 + i] : up;
+            if (emit && lane < V / 2) {
+                const int r = lane / NC, n = lane % NC;
+                if (m0 + r < a.M && n < a.N)
+                    *(float *)((char *)pro.glu + (a.n0 + n) * pro.glu_nb1 + (m0 + r) * 4) = swiglu_val(mine, up);
             }
         } else {
-            if (holder) part[wave][vi] = tot;
-            lds_barrier();
-            if (kw == 0 && holder && vi < V) {
-                float t = 0.0f;
-                for (int s2 = 0; s2 < ksplit; ++s2) t += part[grp * ksplit + s2][vi];
-                const int r = vi / NC, n = vi % NC;
-                if (m0 + r < a.M && n < a.N) store(m0 + r, n, t);
+            if (emit && lane < V) {
+                const int r = lane / NC, n = lane % NC;
+                if (m0 + r < a.M && n < a.N) store(m0 + r, n, mine);
             }
-            lds_barrier();
         }
-        if constexpr (PIPE) {
-            cur = nxt;
-        } else if (have_next && uvalid) {
+    };
+    if constexpr (PIPE) {  // the next block's loads in flight while this one is multiplied
+        for (int64_t rn = rb + gridDim.x; rn < nblocks; rn += gridDim.x) {
+            WRegs<WT, R> nxt;
             const uint8_t *wrow[R];
-            row_ptrs(rb_next, wrow);
-            cur.load(wrow, u);
+            row_ptrs(rn, wrow);
+            nxt.load(wrow, ul);
+            finish(cur, rb);
+            cur = nxt;
+            rb = rn;
         }
-        rb = rb_next;
-        have = have_next;
+        finish(cur, rb);
+    } else {
+        for (;;) {
+            finish(cur, rb);
+            rb += gridDim.x;
+            if (rb >= nblocks) break;
+            const uint8_t *wrow[R];
+            row_ptrs(rb, wrow);
+            cur.load(wrow, ul);
+        }
     }
 }
 
@@ -606,49 +781,58 @@ template <typename Kern> static int64_t resident_blocks(Kern kern, int &cache) {
     return cache;
 }
 
-template <int WT, int NC, int R, bool FUSED, bool PIPE>
-static tlh_status launch_reg_pipe(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
-                                  int64_t row_blocks, hipStream_t stream) {
-    auto kern = k_gemv_reg<WT, NC, R, FUSED, PIPE>;
-    static int slots = -1;
+template <int WT, int NC, int R, int IN, bool PIPE, bool GLU>
+static tlh_status launch_reg_pipe(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
+                                  int ksplit, int upw, unsigned gx, hipStream_t stream) {
+    auto kern = k_gemv_reg<WT, NC, R, IN, PIPE, GLU>;
     const int64_t batches = a.ne12 * a.ne13;
-    int64_t resident = resident_blocks(kern, slots) / (batches > 0 ? batches : 1);
-    if (resident < 1) resident = 1;
-    const unsigned gx = (unsigned)(row_blocks < resident ? row_blocks : resident);
-    hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(256), 0, stream, a, x, x_row_bytes, ksplit, upw);
+    const size_t lds = IN == IN_SCRATCH ? 0 : (size_t)(NC * act_lds(vec_dot_type(WT), a.K).bytes);
+    hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(256), lds, stream, a, x, x_row_bytes, ksplit, upw,
+                       pro);
     return check_launch("gemv");
 }
 
-// A persistent grid walks the row blocks; once each workgroup has several to
-// walk, the double-buffered kernel keeps the weight stream busy.
-template <int WT, int NC, int R, bool FUSED>
-static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
-                                 hipStream_t stream) {
+// A persistent grid walks the row blocks. A workgroup that quantizes its
+// activation itself reads 4 K bytes of it per column (and quantizes them)
+// however few rows it then streams, so the grid is capped to give each
+// workgroup at least twice that in weight bytes. Once each workgroup has
+// several row blocks to walk, the double-buffered kernel keeps the weight
+// stream busy.
+template <int WT, int NC, int R, int IN, bool GLU>
+static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
+                                 int ksplit, int upw, hipStream_t stream) {
     static int slots = -1;
     const int groups = 4 / ksplit;
-    const int64_t row_blocks = (a.M + (int64_t)groups * R - 1) / ((int64_t)groups * R);
+    const int64_t rows_per_block = (int64_t)groups * (GLU ? R / 2 : R);
+    const int64_t row_blocks = (a.M + rows_per_block - 1) / rows_per_block;
     const int64_t batches = a.ne12 * a.ne13 > 0 ? a.ne12 * a.ne13 : 1;
-    const int64_t resident = resident_blocks(k_gemv_reg<WT, NC, R, FUSED, false>, slots);
-    if (row_blocks * batches > 2 * resident)
-        return launch_reg_pipe<WT, NC, R, FUSED, true>(a, x, x_row_bytes, ksplit, upw, row_blocks, stream);
-    return launch_reg_pipe<WT, NC, R, FUSED, false>(a, x, x_row_bytes, ksplit, upw, row_blocks, stream);
+    int64_t gx = resident_blocks(k_gemv_reg<WT, NC, R, IN, false, GLU>, slots) / batches;
+    if (IN != IN_SCRATCH) {
+        const int64_t wbytes = rows_per_block * (GLU ? 2 : 1) * (a.K / block_elems(WT)) * block_bytes(WT);
+        const int64_t per_wg = (2 * 4 * a.K * NC + wbytes - 1) / wbytes;  // row blocks per workgroup, at least
+        gx = std::min(gx, (row_blocks + per_wg - 1) / per_wg);
+    }
+    gx = std::max<int64_t>(1, std::min(gx, row_blocks));
+    if (row_blocks >= 2 * gx)
+        return launch_reg_pipe<WT, NC, R, IN, true, GLU>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
+    return launch_reg_pipe<WT, NC, R, IN, false, GLU>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
 }
 
-template <int WT, int NC, bool FUSED>
-static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
-                                hipStream_t stream) {
+template <int WT, int NC, int IN, bool GLU>
+static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
+                                int ksplit, int upw, hipStream_t stream) {
     // q6_K holds 19 weight registers per row: two columns take 2 rows per wave
     constexpr int R = ((WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q5_K) && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
-    return launch_reg_cfg<WT, NC, R, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
+    return launch_reg_cfg<WT, NC, R, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 // N = 1 or 2 only: more columns of register-resident activations (20 VGPRs
 // per column) leave too few registers and spill.
-template <int WT, bool FUSED>
-static tlh_status launch_reg_wt(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
-                                hipStream_t stream) {
-    if (a.N == 1) return launch_reg_nc<WT, 1, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
-    return launch_reg_nc<WT, 2, FUSED>(a, x, x_row_bytes, ksplit, upw, stream);
+template <int WT, int IN, bool GLU>
+static tlh_status launch_reg_wt(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
+                                int ksplit, int upw, hipStream_t stream) {
+    if (a.N == 1) return launch_reg_nc<WT, 1, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    return launch_reg_nc<WT, 2, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 // Geometry of the register-resident GEMV for K: waves per row group and
@@ -662,28 +846,50 @@ bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw) {
     return upw <= 64;
 }
 
+template <int IN, bool GLU>
+static tlh_status launch_reg_type(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
+                                  int ksplit, int upw, hipStream_t stream) {
+    switch (a.wtype) {
+    case TLH_TYPE_Q4_0: return launch_reg_wt<TLH_TYPE_Q4_0, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q8_0: return launch_reg_wt<TLH_TYPE_Q8_0, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q4_K: return launch_reg_wt<TLH_TYPE_Q4_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q5_K: return launch_reg_wt<TLH_TYPE_Q5_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q6_K: return launch_reg_wt<TLH_TYPE_Q6_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
+    }
+}
+
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
     int ksplit = 1, upw = 64;
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
-    const bool fused = x != nullptr;
-    switch (a.wtype) {
-    case TLH_TYPE_Q4_0:
-        return fused ? launch_reg_wt<TLH_TYPE_Q4_0, true>(a, x, x_row_bytes, ksplit, upw, stream)
-                     : launch_reg_wt<TLH_TYPE_Q4_0, false>(a, x, x_row_bytes, ksplit, upw, stream);
-    case TLH_TYPE_Q8_0:
-        return fused ? launch_reg_wt<TLH_TYPE_Q8_0, true>(a, x, x_row_bytes, ksplit, upw, stream)
-                     : launch_reg_wt<TLH_TYPE_Q8_0, false>(a, x, x_row_bytes, ksplit, upw, stream);
-    case TLH_TYPE_Q4_K:
-        return fused ? launch_reg_wt<TLH_TYPE_Q4_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
-                     : launch_reg_wt<TLH_TYPE_Q4_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
-    case TLH_TYPE_Q5_K:
-        return fused ? launch_reg_wt<TLH_TYPE_Q5_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
-                     : launch_reg_wt<TLH_TYPE_Q5_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
-    case TLH_TYPE_Q6_K:
-        return fused ? launch_reg_wt<TLH_TYPE_Q6_K, true>(a, x, x_row_bytes, ksplit, upw, stream)
-                     : launch_reg_wt<TLH_TYPE_Q6_K, false>(a, x, x_row_bytes, ksplit, upw, stream);
-    default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
+    const GemvPro none;
+    if (!x) return launch_reg_type<IN_SCRATCH, false>(a, nullptr, 0, none, ksplit, upw, stream);
+    return a.K <= 4096 ? launch_reg_type<IN_X, false>(a, x, x_row_bytes, none, ksplit, upw, stream)
+                       : launch_reg_type<IN_XL, false>(a, x, x_row_bytes, none, ksplit, upw, stream);
+}
+
+tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
+                               hipStream_t stream) {
+    int ksplit = 1, upw = 64;
+    if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
+    if (a.ne12 * a.ne13 != 1) return set_error(TLH_INVALID, "gemv_reg: a prologue / epilogue takes one batch slice");
+    const bool glu = pro.glu != nullptr;
+    if (glu && (a.nseg != 2 || a.seg_m0[1] != a.seg_m0[2] - a.seg_m0[1]))
+        return set_error(TLH_INVALID, "gemv_reg: the SwiGLU epilogue needs two segments of equal rows");
+    MatmulArgs b = a;
+    if (glu) b.M = a.seg_m0[1];  // rows of h
+    if (pro.p) {
+        if (x) return set_error(TLH_INVALID, "gemv_reg: a prologue forms the activation itself");
+        if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: the norm prologue takes K <= 4096");
+        return glu ? launch_reg_type<IN_NORM, true>(b, nullptr, 0, pro, ksplit, upw, stream)
+                   : launch_reg_type<IN_NORM, false>(b, nullptr, 0, pro, ksplit, upw, stream);
     }
+    if (!x) return set_error(TLH_INVALID, "gemv_reg: no activation");
+    if (a.K > 4096)
+        return glu ? launch_reg_type<IN_XL, true>(b, x, x_row_bytes, pro, ksplit, upw, stream)
+                   : launch_reg_type<IN_XL, false>(b, x, x_row_bytes, pro, ksplit, upw, stream);
+    return glu ? launch_reg_type<IN_X, true>(b, x, x_row_bytes, pro, ksplit, upw, stream)
+               : launch_reg_type<IN_X, false>(b, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 }  // namespace tlh

@@ -61,6 +61,26 @@ __host__ __device__ inline int64_t mm_act_rows(const MatmulArgs &a) {
     return a.ids ? a.id_b1 * a.ne13 : a.N_total * a.ne12 * a.ne13;
 }
 
+// Optional prologue and epilogue of the register GEMV (N <= 2, one batch
+// slice), for the executor's fusions.
+//  * Prologue (p != nullptr): activation column n is not read from src1 but
+//    formed in the kernel as ggml's [ADD ->] RMS_NORM -> MUL chain does it:
+//    x = p + q (q may be null), scale = 1/sqrtf((float)(sum x*x in double / K)
+//    + eps), y = (x * scale) * w, then quantized like src1; the sum x goes to
+//    s (written by one workgroup) when s is not null. Rows of p, q, s are
+//    p_nb1, q_nb1, s_nb1 bytes apart.
+//  * Epilogue (glu != nullptr): the launch's two segments are a gate and an
+//    up matrix of equal rows; instead of their outputs the kernel stores
+//    h = silu(gate) * up (ggml_vec_swiglu_f32) at glu + n * glu_nb1 bytes.
+struct GemvPro {
+    const float *p = nullptr, *q = nullptr, *w = nullptr;
+    float *s = nullptr;
+    int64_t p_nb1 = 0, q_nb1 = 0, s_nb1 = 0;
+    float eps = 0.0f;
+    float *glu = nullptr;
+    int64_t glu_nb1 = 0;
+};
+
 // N <= 16. With x != nullptr (src1 rows in activation-row order, stride
 // x_row_bytes) and a small N*K the GEMV quantizes x itself and the scratch is
 // not read; otherwise it reads the scratch a quantize launch filled.
@@ -69,6 +89,9 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 // register-resident GEMV (gemv_reg.hip): K <= 16384, K % 64 == 0
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
+// the register GEMV with a prologue and / or epilogue (GemvPro); quantizes in-kernel
+tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
+                               hipStream_t stream);
 // few-column GEMM on int8 MFMA (gemv_mfma.hip): 1 <= N <= 16, any K, from
 // the scratch. K > 4096 needs a.part: gemv_mfma_partial_bytes of scratch.
 bool gemv_mfma_supported(int64_t N);

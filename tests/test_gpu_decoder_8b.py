@@ -250,9 +250,15 @@ def test_8b_slice_paged_batch16_matches_reference_alone(gpu, slice8b):
     tables = [list(perm[2 * s:2 * s + 2]) for s in range(len(seqs))]  # 2 blocks hold up to 32 tokens
     dec = Paged(c, pc, wd)
 
+    # a row whose two CPU runs agree (a one-token prompt: attention over one key
+    # is exact either way) is still as sensitive to the last bit of any other
+    # sum: its allowance is at least the median distance over all rows
+    floor = float(np.median(g["paged_spread"]))
+
     def check(j, s, lg, am):  # j = 0: the prompt, 1 and 2: the decode steps
         idx, val = g["paged_top_index"][j, s], g["paged_top_logit"][j, s]
-        err = within_spread(lg[idx], val, float(g["paged_spread"][j, s]), f"paged step {j} seq {s} (top 8)")
+        spread = max(float(g["paged_spread"][j, s]), floor)
+        err = within_spread(lg[idx], val, spread, f"paged step {j} seq {s} (top 8)")
         argmax_agrees(am, {"index": idx, "value": val}, max(err, 1e-4), f"step {j} seq {s}")
 
     for s, (prompt, _) in enumerate(seqs):

@@ -282,6 +282,51 @@ def test_split_phases_match_fused_node(gpu, t):
         close(y1.cpu().numpy(), y0.cpu().numpy(), f"{NAMES[t]} n={n}")
 
 
+def tie_rows(n, K, seed):
+    """Activations that exercise the quantizers' rules: N(0, 1) rows whose
+    32-element blocks, in turn, hold +-127 as their largest magnitude (so d = 1
+    and half-integers land exactly on rounding ties: roundf away from zero for
+    q8_0, to even for q8_K), the largest magnitude twice with opposite signs
+    (the first one sets q8_K's sign), or nothing but zeros."""
+    x = synth.normal(seed, (n, K))
+    for r in range(n):
+        for b in range(K // 32):
+            kind = (b + r) % 4
+            blk = x[r, 32 * b:32 * b + 32]
+            if kind == 0:
+                blk[:] = np.round(blk * 20) + 0.5
+                blk[5] = -127.0 if (b // 8) % 2 else 127.0
+            elif kind == 1:
+                blk[3], blk[20] = -9.0, 9.0
+            elif kind == 2:
+                blk[:] = 0.0
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("K", [256, 4096, 8192, 14336, 16384])
+def test_in_kernel_quantization_is_the_quantize_launch(gpu, t, K):
+    """For N <= 2 the GEMV quantizes src1 itself (each workgroup into LDS). Its
+    products must be bit-identical to the same GEMV reading the scratch of the
+    separate quantize launch, which is pinned bit-exact to ggml's
+    quantize_row_q8_0 / q8_K (test_gpu_quant.py): so are the in-kernel codes."""
+    import torch
+
+    M = 300
+    w = dev(synth.random_blocks(t, 1990, M, K))
+    for n in (1, 2):
+        x = dev(tie_rows(n, K, 1991 + n))
+        mm = N.MulMat(t, M, K, n)
+        y0 = torch.empty((n, M), dtype=torch.float32, device="cuda")
+        y1 = torch.empty_like(y0)
+        mm(w, x, y0)
+        mm.quantize(x)
+        mm.compute(w, y1)
+        torch.cuda.synchronize()
+        a, b = y0.cpu().numpy(), y1.cpu().numpy()
+        assert np.array_equal(a.view(np.int32), b.view(np.int32)), (NAMES[t], K, n, np.abs(a - b).max())
+
+
 @pytest.mark.parametrize("M,K,n", [(128, 256, 128), (256, 512, 129), (300, 2304, 257), (1000, 4096, 64)])
 def test_q4K_mfma_gemm_tiles(gpu, M, K, n):
     """The q4_K MFMA GEMM on exact tile multiples and ragged edges, weights quantized
