@@ -33,7 +33,7 @@ struct Place {
 
 enum DispatchKind { D_MUL_MAT, D_MM_QUANTIZE, D_MM_COMPUTE, D_FLASH_ATTN, D_CORE, D_NORM_CHAIN, D_MULTI_GEMV,
                     D_ARGMAX_SPLIT, D_CORE_MULTI, D_PAGED_ATTN, D_PAGED_WRITE, D_MUL_MAT_ID,
-                    D_MM_COMPUTE_MULTI };
+                    D_MM_COMPUTE_MULTI, D_GEMV_PRO };
 constexpr int NSRC = 5;  // sources a dispatch reads (the paged nodes have five)
 struct Dispatch {
     DispatchKind kind;
@@ -59,6 +59,13 @@ struct Dispatch {
     // D_PAGED_WRITE: tokens, kv heads, head size, block size
     tlh_paged_attention_args pa{};
     int pa_f32 = 0;  // D_PAGED_ATTN: dst is a fused cast's f32 tensor
+    // D_GEMV_PRO: a register GEMV over the members (as D_MULTI_GEMV) that forms
+    // its activation from the norm chain before it (has_norm: nop, the chain's
+    // p, q, w, s in nsrc[0..3], its output y in ndst) and / or applies the
+    // SwiGLU after it (has_glu: gop, h in gdst)
+    int has_norm = 0, has_glu = 0;
+    tlh_op nop, gop;
+    Place nsrc[4], ndst, gdst;
     int32_t pw[4] = {0, 0, 0, 0};
     int64_t pw_blocks = 0;  // D_PAGED_WRITE: blocks in the smaller pool (slots past it are dropped)
     int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
@@ -185,6 +192,7 @@ class Lowering {
         for (Dispatch &x : out.d) x.pos_last = x.pos;
         fuse_norm_chains(out.d);
         fuse_multi_gemv(out.d);
+        fuse_gemv_pro(out.d);
         fuse_rope_rows(out.d);
         fuse_rope_cast(out.d);
         fuse_paged_cast(out.d);
@@ -607,6 +615,94 @@ class Lowering {
         d.swap(out);
     }
 
+    // A single-column GEMV (D_MULTI_GEMV, or one D_MUL_MAT the register GEMV
+    // runs) takes in its neighbours, in one launch:
+    //  * the [ADD ->] RMS_NORM -> MUL chain right before it when the chain's
+    //    output is read by these MUL_MATs only (K <= 4096): each workgroup forms
+    //    the normalized row itself (the ADD's sum is still written once);
+    //  * a SwiGLU right after a gate / up pair when it alone reads their
+    //    outputs: h = silu(gate) * up is stored instead of the pair.
+    // The pieces' own tensors stay planned: a launch whose pointers the fused
+    // kernel cannot take runs them one by one.
+    static bool same_place(const Place &a, const Place &b) {
+        return a.buf == b.buf && a.index == b.index && a.off == b.off;
+    }
+    void fuse_gemv_pro(std::vector<Dispatch> &d) {
+        count_readers();
+        auto gemv_ok = [&](const Dispatch &x) {
+            if (x.kind == D_MULTI_GEMV) return true;
+            const tlh_op *o = &x.op;
+            return x.kind == D_MUL_MAT && x.src[0].buf == B_WEIGHT && mul_mat_multi_ok(&o, 1);
+        };
+        std::vector<Dispatch> out;
+        out.reserve(d.size());
+        for (size_t i = 0; i < d.size(); ++i) {
+            if (!gemv_ok(d[i])) {
+                out.push_back(d[i]);
+                continue;
+            }
+            Dispatch f = d[i];
+            if (f.kind == D_MUL_MAT) {  // one member
+                f.nmem = 1;
+                f.mop[0] = f.op;
+                f.mw[0] = f.src[0];
+                f.mdst[0] = f.dst;
+            }
+            bool fused = false;
+            // the norm chain before it
+            if (!out.empty()) {
+                const Dispatch &c = out.back();
+                const int32_t y = g_.nodes[c.pos_last];
+                bool ok = c.kind == D_NORM_CHAIN && c.op.x[0] == 1 && readers_[y] == f.nmem &&
+                          std::find(g_.keep.begin(), g_.keep.end(), y) == g_.keep.end() &&
+                          same_place(f.src[1], c.dst) && f.mop[0].t[1].ne[0] <= 4096 &&
+                          f.mop[0].t[1].ne[1] == 1 && c.op.t[0].ne[1] == 1 && c.op.t[0].ne[2] == 1 &&
+                          c.op.t[0].ne[3] == 1;
+                if (ok) {
+                    f.has_norm = 1;
+                    f.nop = c.op;
+                    for (int k = 0; k < 4; ++k) f.nsrc[k] = c.src[k];
+                    f.ndst = c.dst;
+                    f.pos = c.pos;
+                    f.pos_last = std::max(f.pos_last, c.pos_last);
+                    out.pop_back();
+                    fused = true;
+                }
+            }
+            // the SwiGLU after a gate / up pair
+            if (f.nmem == 2 && i + 1 < d.size()) {
+                const Dispatch &gl = d[i + 1];
+                const int32_t m0 = f.mdst[0].index, m1 = f.mdst[1].index;  // arena places: root tensor ids
+                bool ok = f.mdst[0].buf == B_ARENA && f.mdst[1].buf == B_ARENA && gl.kind == D_CORE && gl.core_kind == TLH_CORE_GLU && gl.op.x[0] == 2 && gl.op.x[1] == 0 &&
+                          gl.src[1].buf != B_NONE && f32_rows(gl.op.t[4]) && gl.op.t[4].ne[1] == 1 &&
+                          gl.op.t[4].ne[2] == 1 && gl.op.t[4].ne[3] == 1 &&
+                          f.mop[0].t[0].ne[1] == f.mop[1].t[0].ne[1] && gl.op.t[4].ne[0] == f.mop[0].t[0].ne[1];
+                int gate = -1;
+                if (ok && same_place(gl.src[0], f.mdst[0]) && same_place(gl.src[1], f.mdst[1])) gate = 0;
+                if (ok && same_place(gl.src[0], f.mdst[1]) && same_place(gl.src[1], f.mdst[0])) gate = 1;
+                ok = gate >= 0 && readers_[m0] == 1 && readers_[m1] == 1 &&
+                     std::find(g_.keep.begin(), g_.keep.end(), m0) == g_.keep.end() &&
+                     std::find(g_.keep.begin(), g_.keep.end(), m1) == g_.keep.end();
+                if (ok) {
+                    if (gate == 1) {  // members in gate, up order
+                        std::swap(f.mop[0], f.mop[1]);
+                        std::swap(f.mw[0], f.mw[1]);
+                        std::swap(f.mdst[0], f.mdst[1]);
+                    }
+                    f.has_glu = 1;
+                    f.gop = gl.op;
+                    f.gdst = gl.dst;
+                    f.pos_last = std::max(f.pos_last, gl.pos_last);
+                    ++i;  // the SwiGLU is part of it
+                    fused = true;
+                }
+            }
+            if (fused) f.kind = D_GEMV_PRO;
+            out.push_back(fused ? f : d[i]);
+        }
+        d.swap(out);
+    }
+
     static bool same_root(const Place &a, const Place &b) {
         return a.buf != B_NONE && a.buf != B_WEIGHT && a.buf == b.buf && a.index == b.index;
     }
@@ -622,6 +718,11 @@ class Lowering {
             wr.push_back(x.sdst[k]);
         }
         if (x.kind == D_NORM_CHAIN) wr.push_back(x.src[3]);  // the ADD's result
+        if (x.has_norm) {
+            for (int k = 0; k < 3; ++k) rd.push_back(x.nsrc[k]);
+            wr.push_back(x.nsrc[3]), wr.push_back(x.ndst);
+        }
+        if (x.has_glu) wr.push_back(x.gdst);
     }
     static bool independent(const Dispatch &a, const Dispatch &b) {
         std::vector<Place> ra, wa, rb, wb;
@@ -1008,6 +1109,9 @@ class Lowering {
                 for (int k = 0; k < NSRC; ++k) touch_place(x.src[k], pos);
                 touch_place(x.dst, pos);
                 for (int k = 0; k < x.nmem; ++k) touch_place(x.mdst[k], pos);
+                for (int k = 0; k < 4; ++k) touch_place(x.nsrc[k], pos);
+                touch_place(x.ndst, pos);
+                touch_place(x.gdst, pos);
                 for (int k = 0; k < x.nsub; ++k) {
                     for (int m = 0; m < 4; ++m) touch_place(x.ssrc[k][m], pos);
                     touch_place(x.sdst[k], pos);
@@ -1212,6 +1316,48 @@ struct tlh_program {
                 if (st == TLH_UNSUPPORTED)  // pointers the fused launch cannot take: one launch per node
                     for (int k = 0; k < x.nmem && (k == 0 || st == TLH_OK); ++k)
                         st = tlh_mul_mat(ops[k], w[k], src[1], dsts[k], scratch, x.scratch_bytes, s);
+                break;
+            }
+            case D_GEMV_PRO: {
+                const tlh_op *ops[3];
+                const void *w[3];
+                void *dsts[3];
+                for (int k = 0; k < x.nmem; ++k) {
+                    ops[k] = &x.mop[k];
+                    w[k] = resolve(x.mw[k], state);
+                    dsts[k] = resolve(x.mdst[k], state);
+                }
+                GemvPro pro;
+                if (x.has_norm) {
+                    pro.p = (const float *)resolve(x.nsrc[0], state);
+                    pro.q = x.nop.x[2] ? (const float *)resolve(x.nsrc[1], state) : nullptr;
+                    pro.w = (const float *)resolve(x.nsrc[2], state);
+                    pro.s = x.nop.x[2] ? (float *)resolve(x.nsrc[3], state) : nullptr;
+                    pro.p_nb1 = x.nop.t[0].nb[1];
+                    pro.q_nb1 = x.nop.t[1].nb[1];
+                    pro.s_nb1 = x.nop.t[3].nb[1];
+                    pro.eps = __builtin_bit_cast(float, (int32_t)x.nop.x[1]);
+                }
+                if (x.has_glu) {
+                    pro.glu = (float *)resolve(x.gdst, state);
+                    pro.glu_nb1 = x.gop.t[4].nb[1];
+                }
+                st = mul_mat_multi_pro(ops, w, dsts, x.nmem, pro, x.has_norm ? nullptr : src[1], s);
+                if (st == TLH_UNSUPPORTED) {  // the pieces one by one
+                    const void *act = src[1];
+                    st = TLH_OK;
+                    if (x.has_norm) {
+                        void *y = resolve(x.ndst, state);
+                        st = launch_norm_chain(x.nop, pro.p, pro.q, pro.w, pro.s, y, s);
+                        act = y;
+                    }
+                    if (st == TLH_OK) st = mul_mat_multi(ops, w, dsts, x.nmem, act, s);
+                    if (st == TLH_UNSUPPORTED)
+                        for (int k = 0; k < x.nmem && (k == 0 || st == TLH_OK); ++k)
+                            st = tlh_mul_mat(ops[k], w[k], act, dsts[k], scratch, x.scratch_bytes, s);
+                    if (st == TLH_OK && x.has_glu)
+                        st = tlh_core(TLH_CORE_GLU, &x.gop, dsts[0], dsts[1], nullptr, resolve(x.gdst, state), s);
+                }
                 break;
             }
             default:

@@ -137,6 +137,11 @@ tlh_status mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w,
 bool mul_mat_multi_ok(const tlh_op *const *ops, int n);
 tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n, const void *x,
                          hipStream_t stream);
+// mul_mat_multi with a GemvPro prologue and / or SwiGLU epilogue (executor
+// fusions; x is null with the prologue). TLH_UNSUPPORTED when the pointers do
+// not allow it.
+tlh_status mul_mat_multi_pro(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
+                             const GemvPro &pro, const void *x, hipStream_t stream);
 // [ADD ->] RMS_NORM / NORM -> MUL(weight) in one kernel (core.hip k_norm_chain);
 // op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
 tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,

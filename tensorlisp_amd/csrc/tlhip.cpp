@@ -562,6 +562,52 @@ tlh_status tlh::mul_mat_multi(const tlh_op *const *ops, const void *const *w, vo
     return launch_gemv_reg(m, (const float *)x, ops[0]->t[1].nb[1], stream);
 }
 
+// mul_mat_multi with a GemvPro prologue (the activation formed from an
+// [ADD ->] RMS_NORM -> MUL chain; x is then null) and / or SwiGLU epilogue
+// (two members: gate then up, equal rows; h goes to pro.glu). Shapes as
+// mul_mat_multi_ok; TLH_UNSUPPORTED when the pointers or strides do not allow
+// the fused launch (the executor then runs the pieces one by one).
+tlh_status tlh::mul_mat_multi_pro(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
+                                  const GemvPro &pro, const void *x, hipStream_t stream) {
+    if (!mul_mat_multi_ok(ops, n)) return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: shapes");
+    MulMatShape s;
+    check_mul_mat(ops[0], s);
+    const bool glu = pro.glu != nullptr;
+    if (glu && (n != 2 || ops[0]->t[0].ne[1] != ops[1]->t[0].ne[1]))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: SwiGLU takes a gate and an up matrix of equal rows");
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (pro.p) {
+        if (s.K > 4096 || !a16(pro.p) || !a16(pro.w) || (pro.q && !a16(pro.q)) || (pro.s && !a16(pro.s)) ||
+            ((pro.p_nb1 | pro.q_nb1 | pro.s_nb1) & 15))
+            return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: norm rows (K <= 4096, 16-byte aligned)");
+    } else if (!x || ((uintptr_t)x & 15) || (ops[0]->t[1].nb[1] & 15)) {
+        return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: activation alignment");
+    }
+    if (glu && (((uintptr_t)pro.glu & 3) || (pro.glu_nb1 & 3)))
+        return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: SwiGLU destination alignment");
+    MatmulArgs m = mm_args(ops[0], s, w[0], nullptr, dst[0]);
+    m.nseg = n;
+    int64_t rows = 0;
+    for (int i = 0; i < 3; ++i) {
+        m.seg_m0[i] = rows;
+        if (i < n) {
+            if (!w[i] || ((uintptr_t)w[i] & 1) || (!glu && (!dst[i] || ((uintptr_t)dst[i] & 3))))
+                return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: pointers");
+            m.seg_w[i] = (const uint8_t *)w[i];
+            m.seg_w_nb1[i] = ops[i]->t[0].nb[1];
+            m.seg_dst[i] = (float *)dst[i];
+            rows += ops[i]->t[0].ne[1];
+        } else {
+            m.seg_w[i] = nullptr;
+            m.seg_w_nb1[i] = 0;
+            m.seg_dst[i] = nullptr;
+        }
+    }
+    m.seg_m0[3] = rows;
+    m.M = rows;
+    return launch_gemv_reg_pro(m, pro, (const float *)x, ops[0]->t[1].nb[1], stream);
+}
+
 extern "C" {
 
 tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,

@@ -212,6 +212,76 @@ def test_fused_norm_chains_match_unfused(gpu, n, rms, add):
     assert prog.stats()["launches"] == 1
 
 
+FUSE_TYPES = [N.Q4_K, N.Q4_0, N.Q8_0, N.Q6_K, N.Q5_K]
+
+
+@pytest.mark.parametrize("t", FUSE_TYPES, ids=[N.TYPE_NAMES[t] for t in FUSE_TYPES])
+@pytest.mark.parametrize("K,M,add", [(4096, 1536, True), (4096, 300, False), (256, 1000, True), (2048, 17, True)])
+def test_norm_gemv_swiglu_is_one_launch(gpu, t, K, M, add):
+    """[ADD ->] RMS_NORM -> MUL(weight) feeding a gate / up MUL_MAT pair at one
+    column, then SwiGLU, runs as one register-GEMV launch that forms the
+    normalized row itself and stores silu(gate) * up. Its outputs (h, and the
+    ADD's sum) equal the same ops launched one by one (core ops, MUL_MAT, GLU)."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    b = G.Builder()
+    p = b.input(N.F32, [K, 1])
+    q = b.input(N.F32, [K, 1])
+    nw = b.weight(N.F32, [K])
+    wg = b.weight(t, [K, M])
+    wu = b.weight(t, [K, M])
+    s = b.add(p, q) if add else p
+    cur = b.mul(b.rms_norm(s, 1e-5), nw)
+    h = b.glu_split(b.mul_mat(wg, cur), b.mul_mat(wu, cur), "swiglu")
+    b.expand(h)
+    nwh = (1.0 + 0.1 * synth.normal(81, (K,))).astype(np.float32)
+    gw, uw = (synth.random_blocks(t, 82 + i, M, K) for i in range(2))
+    prog = G.Program(b, [h] + ([s] if add else []), [dev(nwh), dev(gw), dev(uw)])
+    pv, qv = dev(synth.normal(84, (1, K)) * 2 + 0.3), dev(synth.normal(85, (1, K)))
+    prog.write_input(0, pv)
+    prog.write_input(1, qv)
+    prog.run()
+    sv = N.add(pv, qv) if add else pv
+    y = N.mul(N.norm(sv, 1e-5, rms=True), dev(nwh))
+    want = N.glu("swiglu", N.mul_mat(t, dev(gw), M, K, y), N.mul_mat(t, dev(uw), M, K, y))
+    got = prog.read(h, torch.float32).reshape(want.shape)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+    if add:
+        np.testing.assert_array_equal(prog.read(s, torch.float32).reshape(sv.shape).cpu().numpy(), sv.cpu().numpy())
+    assert prog.stats()["launches"] == 1
+
+
+@pytest.mark.parametrize("t", FUSE_TYPES, ids=[N.TYPE_NAMES[t] for t in FUSE_TYPES])
+def test_norm_feeding_one_gemv_is_one_launch(gpu, t):
+    """The head's shape: RMS_NORM -> MUL(weight) -> one MUL_MAT at one column is
+    one launch, equal to the ops launched one by one."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    K, M = 4096, 5000
+    b = G.Builder()
+    x = b.input(N.F32, [K, 1])
+    nw = b.weight(N.F32, [K])
+    wo = b.weight(t, [K, M])
+    out = b.mul_mat(wo, b.mul(b.rms_norm(x, 1e-5), nw))
+    b.expand(out)
+    nwh = (1.0 + 0.1 * synth.normal(86, (K,))).astype(np.float32)
+    ow = synth.random_blocks(t, 87, M, K)
+    prog = G.Program(b, [out], [dev(nwh), dev(ow)])
+    xv = dev(synth.normal(88, (1, K)))
+    prog.write_input(0, xv)
+    prog.run()
+    want = N.mul_mat(t, dev(ow), M, K, N.mul(N.norm(xv, 1e-5, rms=True), dev(nwh)))
+    got = prog.read(out, torch.float32).reshape(want.shape)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+    assert prog.stats()["launches"] == 1
+
+
 @pytest.mark.parametrize("n", [8192, 4100])
 def test_inplace_add_feeding_norm(gpu, n):
     """An in-place ADD (ggml_add_inplace: the sum overwrites src0) feeding
