@@ -94,46 +94,75 @@ __host__ __device__ inline ActLds act_lds(int act_type, int64_t K) {
 // loads are issued, so that quantizing them does not wait for the weights
 // (vector loads complete in order). IN_X: the values of x; IN_NORM: x = p + q
 // and the norm weight w (K <= 4096).
+// Cross-lane moves within a row of 16 lanes by DPP (no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes 1 and 2 apart; row_half_mirror
+// pairs each quad of a half row with the other quad, row_mirror each half row
+// with the other. Applied in that order, every step pairs groups of lanes
+// that already agree, so the four steps reduce a team of 16 lanes (the first
+// step alone a pair).
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL> __device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+// One step of the team search for the first element of largest magnitude:
+// take the partner group's (magnitude, value) when larger, or equal and the
+// partner group comes first (lower lanes hold earlier elements).
+template <int CTRL>
+__device__ __forceinline__ void first_max_step(float &ba, float &bv, bool partner_first) {
+    const float oa = dpp_mov<CTRL>(ba), ov = dpp_mov<CTRL>(bv);
+    if (oa > ba || (oa == ba && partner_first)) ba = oa, bv = ov;
+}
+
 // IN_X: x with K <= 4096; IN_XL: x with K <= 16384; IN_NORM: the prologue's
 // p, q, w with K <= 4096.
 enum { IN_SCRATCH = 0, IN_X = 1, IN_NORM = 2, IN_XL = 3 };
 
 template <int IN> struct ActRegs {
     static constexpr int G = IN == IN_XL ? 4 : 1;
+    static constexpr int NQ = IN == IN_NORM ? 16 : 1;
     float v[G][16];
-    float w[IN == IN_NORM ? 16 : 1];
+    float q[NQ], w[NQ];  // IN_NORM: the ADD's second operand (or x again) and the norm weight
+    // Every load is unconditional (an ADD-less chain loads x twice), so that
+    // using these values waits for these loads only.
     __device__ __forceinline__ void load(const float *__restrict__ xr, const float *__restrict__ qr,
                                          const float *__restrict__ wr, int64_t K) {
-#pragma clang fp contract(off)
         const int t = threadIdx.x;
         const int64_t groups = K / 16;
+        const float *qq = qr ? qr : xr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             const int64_t g = t + 256 * gi;
             const int64_t gc = g < groups ? g : 0;  // in bounds; unused
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                float4 f = *(const float4 *)(xr + 16 * gc + 4 * k);
+                const float4 f = *(const float4 *)(xr + 16 * gc + 4 * k);
+                v[gi][4 * k] = f.x, v[gi][4 * k + 1] = f.y, v[gi][4 * k + 2] = f.z, v[gi][4 * k + 3] = f.w;
                 if constexpr (IN == IN_NORM) {
-                    if (qr) {
-                        const float4 h = *(const float4 *)(qr + 16 * gc + 4 * k);
-                        f = make_float4(f.x + h.x, f.y + h.y, f.z + h.z, f.w + h.w);
-                    }
+                    const float4 h = *(const float4 *)(qq + 16 * gc + 4 * k);
                     const float4 ww = *(const float4 *)(wr + 16 * gc + 4 * k);
+                    q[4 * k] = h.x, q[4 * k + 1] = h.y, q[4 * k + 2] = h.z, q[4 * k + 3] = h.w;
                     w[4 * k] = ww.x, w[4 * k + 1] = ww.y, w[4 * k + 2] = ww.z, w[4 * k + 3] = ww.w;
                 }
-                v[gi][4 * k] = f.x, v[gi][4 * k + 1] = f.y, v[gi][4 * k + 2] = f.z, v[gi][4 * k + 3] = f.w;
             }
         }
     }
-    // IN_NORM: y = (x * scale) * w with scale = 1 / sqrtf((float)(sum of x*x
-    // in double / K) + eps), as ggml's RMS_NORM then MUL form it (the double
-    // sum in another order than the CPU's: equal after its rounding to f32 but
-    // for sums within 1e-16 of a rounding boundary); x itself goes to sr.
-    __device__ __forceinline__ void norm(float *__restrict__ sr, int64_t K, float eps, double *shd) {
+    // IN_NORM: x = p + q (with the ADD), then y = (x * scale) * w with scale =
+    // 1 / sqrtf((float)(sum of x*x in double / K) + eps), as ggml's ADD,
+    // RMS_NORM and MUL form them (the double sum in another order than the
+    // CPU's: equal after its rounding to f32 but for sums within 1e-16 of a
+    // rounding boundary); x goes to sr.
+    __device__ __forceinline__ void norm(bool add, float *__restrict__ sr, int64_t K, float eps, double *shd) {
 #pragma clang fp contract(off)
         const int t = threadIdx.x;
         const bool live = t < K / 16;
+        if (add) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[0][i] = v[0][i] + q[i];
+        }
         double s1 = 0.0;
         if (live) {
 #pragma unroll
@@ -175,11 +204,10 @@ __device__ void coop_quantize(const ActRegs<IN> &ar, int64_t K, char *lds) {
                 const float a = fabsf(v[i]);
                 if (a > ba) ba = a, bv = v[i];
             }
-#pragma unroll
-            for (int m = 1; m <= 8; m <<= 1) {
-                const float oa = __shfl_xor(ba, m, 64), ov = __shfl_xor(bv, m, 64);
-                if (oa > ba || (oa == ba && (lane & m))) ba = oa, bv = ov;
-            }
+            first_max_step<DPP_XOR1>(ba, bv, lane & 1);
+            first_max_step<DPP_XOR2>(ba, bv, lane & 2);
+            first_max_step<DPP_HALF_MIRROR>(ba, bv, lane & 4);
+            first_max_step<DPP_MIRROR>(ba, bv, lane & 8);
             float iscale = 0.0f, d = 0.0f;
             if (ba != 0.0f) {
                 iscale = -127.0f / bv;
@@ -202,7 +230,7 @@ __device__ void coop_quantize(const ActRegs<IN> &ar, int64_t K, char *lds) {
             float amax = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, dpp_mov<DPP_XOR1>(amax));
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             int sum = 0;
@@ -211,7 +239,7 @@ __device__ void coop_quantize(const ActRegs<IN> &ar, int64_t K, char *lds) {
                 c[i] = (int)roundf(v[i] * id);
                 sum += c[i];
             }
-            sum += __shfl_xor(sum, 1, 64);
+            sum += dpp_mov<DPP_XOR1>(sum);
             if ((lane & 1) == 0) {
                 sd[g / 2] = h2f(f2h(d));
                 ((int32_t *)(lds + L.s_off))[g / 2] = sum;
@@ -649,7 +677,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     // their activations are zero) and rows past M are clamped. A load behind a
     // branch would make the compiler wait for every outstanding load where the
     // branch rejoins, instead of only for the ones the next step needs.
-    WRegs<WT, R> cur;
+    WRegs<WT, R> cur, nxt;
     const int64_t nblocks = (a.M + rows_per_block - 1) / rows_per_block;
     int64_t rb = blockIdx.x;  // the launch never has more workgroups than row blocks
     const int64_t ul = uvalid ? u : 0;
@@ -657,6 +685,15 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         const uint8_t *wrow[R];
         row_ptrs(rb, wrow);
         cur.load(wrow, ul);
+    }
+    // double-buffered: every workgroup walks at least two row blocks (the
+    // launcher's rule), so the second block is requested before the
+    // activation work too
+    int64_t rn = rb + gridDim.x;
+    if constexpr (PIPE) {
+        const uint8_t *wrow[R];
+        row_ptrs(rn < nblocks ? rn : rb, wrow);
+        nxt.load(wrow, ul);
     }
 
     AUnit act[NC];
@@ -675,7 +712,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             if constexpr (IN == IN_NORM) {
                 const int64_t arow = arow0 + (n < a.N ? n : a.N - 1);
                 float *sr = (writer && pro.s && n < a.N) ? (float *)((char *)pro.s + arow * pro.s_nb1) : nullptr;
-                ar[n].norm(sr, K, pro.eps, shd);
+                ar[n].norm(pro.q != nullptr, sr, K, pro.eps, shd);
             }
             coop_quantize<AT>(ar[n], K, s_act + n * L.bytes);
         }
@@ -746,17 +783,35 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             }
         }
     };
-    if constexpr (PIPE) {  // the next block's loads in flight while this one is multiplied
-        for (int64_t rn = rb + gridDim.x; rn < nblocks; rn += gridDim.x) {
-            WRegs<WT, R> nxt;
+    if constexpr (PIPE) {
+        // two weight buffers in turn, one block's loads in flight while the
+        // other is multiplied. No register copies and no loads behind a branch
+        // in the steady state: the compiler then waits only for the older
+        // buffer's loads.
+        const int64_t g = gridDim.x, b0 = blockIdx.x;
+        const int64_t mine = (nblocks - b0 + g - 1) / g;  // blocks of this workgroup, >= 2
+        auto blk = [&](int64_t i) { return b0 + i * g; };
+        int64_t i = 0;
+        for (; i + 3 < mine; i += 2) {
             const uint8_t *wrow[R];
-            row_ptrs(rn, wrow);
+            finish(cur, blk(i));
+            row_ptrs(blk(i + 2), wrow);
+            cur.load(wrow, ul);
+            finish(nxt, blk(i + 1));
+            row_ptrs(blk(i + 3), wrow);
             nxt.load(wrow, ul);
-            finish(cur, rb);
-            cur = nxt;
-            rb = rn;
         }
-        finish(cur, rb);
+        if (mine - i == 3) {
+            const uint8_t *wrow[R];
+            finish(cur, blk(i));
+            row_ptrs(blk(i + 2), wrow);
+            cur.load(wrow, ul);
+            finish(nxt, blk(i + 1));
+            finish(cur, blk(i + 2));
+        } else {
+            finish(cur, blk(i));
+            finish(nxt, blk(i + 1));
+        }
     } else {
         for (;;) {
             finish(cur, rb);
