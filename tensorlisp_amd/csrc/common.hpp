@@ -227,6 +227,46 @@ __device__ __forceinline__ float swiglu_val(float x, float g) {
     return (x / (1.0f + expf(-x))) * g;
 }
 
+// ROPE's angle parameters as the lowering derives them from op_params
+// (lower.rs:422-466 with ggml_rope_yarn_corr_dims, ggml.c:4369-4381).
+struct RopeParams {
+    int n_dims = 0, mode = 0;
+    float freq_scale = 1.0f, ext_factor = 0.0f, attn_factor = 1.0f, theta_scale = 1.0f, corr0 = 0.0f, corr1 = 0.0f;
+};
+
+// cos and sin of pair p's angle at position pos, times the YaRN magnitude
+// scale (ggml's rope_yarn, ops.cpp:5820-5835). theta_p = pos * theta_scale^p
+// by repeated f32 products, in the order ggml_rope_cache_init
+// (ops.cpp:5846-5860) forms it, so the angles match the CPU's bit for bit
+// (a powf would differ in the last bits, which at positions in the
+// thousands moves the angle visibly). ff: the pair's frequency factor.
+__device__ __forceinline__ void rope_cs_sn(float pos, int64_t p, float ff, const RopeParams &r, float &cs, float &sn) {
+#pragma clang fp contract(off)
+    float tp = pos;
+    for (int64_t k = 0; k < p; ++k) tp *= r.theta_scale;
+    const float theta_extrap = tp / ff;
+    float theta = r.freq_scale * theta_extrap;
+    float mscale = r.attn_factor;
+    if (r.ext_factor != 0.0f) {
+        const float y = ((float)p - r.corr0) / fmaxf(0.001f, r.corr1 - r.corr0);
+        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * r.ext_factor;
+        theta = r.freq_scale * theta_extrap * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / r.freq_scale);
+    }
+    cs = cosf(theta) * mscale;
+    sn = sinf(theta) * mscale;
+}
+
+// the rotated pair (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos)
+__device__ __forceinline__ float rope_first(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+    return x0 * cs - x1 * sn;
+}
+__device__ __forceinline__ float rope_second(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+    return x0 * sn + x1 * cs;
+}
+
 // int8x4 dot product with accumulate (v_dot4c_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

@@ -544,27 +544,16 @@ __device__ __forceinline__ void body_rope(const CoreArgs &a, int64_t bx, int64_t
         return;
     }
     const float ff = has_ff ? *(const float *)(a.s2 + p * 4) : 1.0f;
-    // theta_p = pos * theta_scale^p by repeated f32 products, in the order
-    // ggml_rope_cache_init (ops.cpp:5846-5860) forms it, so the angles match
-    // the CPU's bit for bit (a powf would differ in the last bits, which at
-    // positions in the thousands moves the angle visibly)
-    float tp = (float)*(const int32_t *)(a.s1 + i2 * ps.nb[0]);
-    for (int64_t k = 0; k < p; ++k) tp *= theta_scale;
-    const float theta_extrap = tp / ff;
-    float theta = freq_scale * theta_extrap;
-    float mscale = attn_factor;
-    if (ext_factor != 0.0f) {
-        const float y = ((float)p - corr0) / fmaxf(0.001f, corr1 - corr0);
-        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * ext_factor;
-        theta = freq_scale * theta_extrap * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
-    }
-    const float cs = cosf(theta) * mscale, sn = sinf(theta) * mscale;
+    RopeParams rp;
+    rp.n_dims = n_dims, rp.mode = mode, rp.freq_scale = freq_scale, rp.ext_factor = ext_factor;
+    rp.attn_factor = attn_factor, rp.theta_scale = theta_scale, rp.corr0 = corr0, rp.corr1 = corr1;
+    float cs, sn;
+    rope_cs_sn((float)*(const int32_t *)(a.s1 + i2 * ps.nb[0]), p, ff, rp, cs, sn);
     const int64_t ia = mode == 0 ? 2 * p : p;
     const int64_t ib = mode == 0 ? 2 * p + 1 : p + n_dims / 2;
     const float x0 = ld_f(xr + ia * x.nb[0], x.ty), x1 = ld_f(xr + ib * x.nb[0], x.ty);
-    st_f(dr + ia * d.nb[0], d.ty, x0 * cs - x1 * sn);
-    st_f(dr + ib * d.nb[0], d.ty, x0 * sn + x1 * cs);
+    st_f(dr + ia * d.nb[0], d.ty, rope_first(x0, x1, cs, sn));
+    st_f(dr + ib * d.nb[0], d.ty, rope_second(x0, x1, cs, sn));
 }
 __global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
     body_rope(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);

@@ -69,6 +69,15 @@ struct Dispatch {
     int32_t pw[4] = {0, 0, 0, 0};
     int64_t pw_blocks = 0;  // D_PAGED_WRITE: blocks in the smaller pool (slots past it are dropped)
     int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
+    // D_GEMV_PRO with has_epi: member rows leave through the store epilogue
+    // (epi: layouts, types, geometry and rotation; its pointers come from
+    // edst / eidx / epos / eff per launch) in place of the `absorbed`
+    // dispatches, which run one by one after a plain GEMV when the fused
+    // launch is refused
+    int has_epi = 0;
+    GemvEpi epi;
+    Place edst[3], eidx[3], epos, eff;
+    std::vector<Dispatch> absorbed;
 };
 
 // ggml type traits used for byte sizes: (block elements, block bytes)
@@ -197,6 +206,7 @@ class Lowering {
         fuse_rope_cast(out.d);
         fuse_paged_cast(out.d);
         fuse_cache_write_cast(out.d);
+        fuse_gemv_epilogue(out.d);
         group_elementwise(out.d);
         group_mul_mats(out.d);
         merge_mm_computes(out.d);
@@ -723,6 +733,16 @@ class Lowering {
             wr.push_back(x.nsrc[3]), wr.push_back(x.ndst);
         }
         if (x.has_glu) wr.push_back(x.gdst);
+        if (x.has_epi) {
+            for (int k = 0; k < 3; ++k) wr.push_back(x.edst[k]), rd.push_back(x.eidx[k]);
+            rd.push_back(x.epos), rd.push_back(x.eff);
+            std::vector<Place> r2, w2;
+            for (const Dispatch &a : x.absorbed) {
+                places(a, r2, w2);
+                rd.insert(rd.end(), r2.begin(), r2.end());
+                wr.insert(wr.end(), w2.begin(), w2.end());
+            }
+        }
     }
     static bool independent(const Dispatch &a, const Dispatch &b) {
         std::vector<Place> ra, wa, rb, wb;
@@ -904,6 +924,203 @@ class Lowering {
             r.dst = w.dst;
             r.pos_last = std::max(r.pos_last, w.pos_last);
             gone[j] = 1;
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
+    // The stores of a single-column GEMV over Q / K / V (D_MULTI_GEMV or a
+    // norm-fused D_GEMV_PRO, K <= 4096) take in the dispatches that alone read
+    // its member outputs, so that the projection and the cache writes of a
+    // decode step are one launch:
+    //  * a ROPE in mode 0 of a member (one token), written as f32 / f16 rows
+    //    or into the rows of a cache (a fused SET_ROWS);
+    //  * a SET_ROWS of a member (one row) into a cache;
+    //  * a one-token paged cache write whose key (a member, or the f16 result
+    //    of a ROPE of one) and value (a member read as f32) both come from
+    //    the GEMV.
+    // The member's f32 output is then not written. An absorbed dispatch moves
+    // up to the GEMV's position, so nothing between may read what it writes
+    // or write what it reads.
+    void fuse_gemv_epilogue(std::vector<Dispatch> &d) {
+        count_readers();
+        std::vector<char> gone(d.size(), 0);
+        auto kept = [&](int32_t id) { return std::find(g_.keep.begin(), g_.keep.end(), id) != g_.keep.end(); };
+        auto readers_after = [&](size_t i, const Place &p) {
+            std::vector<size_t> who;
+            std::vector<Place> rd, wr;
+            for (size_t j = i + 1; j < d.size(); ++j) {
+                if (gone[j]) continue;
+                places(d[j], rd, wr);
+                for (const Place &r : rd)
+                    if (same_root(r, p)) {
+                        who.push_back(j);
+                        break;
+                    }
+            }
+            return who;
+        };
+        auto is_core = [](const Dispatch &x, int kind) { return x.kind == D_CORE && x.core_kind == kind; };
+        auto elems = [](const tlh_tensor &t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; };
+        auto idx_ty = [](const tlh_tensor &t) { return t.ty == TLH_TYPE_I32 || t.ty == 27 /* i64 */; };
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &f = d[i];
+            if (gone[i] || !(f.kind == D_MULTI_GEMV || (f.kind == D_GEMV_PRO && !f.has_glu && !f.has_epi))) continue;
+            const tlh_tensor &b = f.mop[0].t[1];
+            if (b.ne[0] > 4096 || b.ne[1] != 1 || b.ne[2] != 1 || b.ne[3] != 1) continue;
+            GemvEpi e;
+            Place edst[3], eidx[3], epos, eff;
+            std::vector<size_t> take[3];  // absorbed dispatch indices per member
+            const tlh_op *rope = nullptr;  // the first rotation's op (parameters shared)
+            Place rpos, rff;
+            int paged_w = -1;             // index of the absorbed paged write
+            int paged_have = 0;           // 1: key member found, 2: value member found
+            for (int k = 0; k < f.nmem; ++k) {
+                const Place P = f.mdst[k];
+                const int64_t M = f.mop[k].t[0].ne[1];
+                const tlh_tensor &y = f.mop[k].t[4];
+                if (P.buf != B_ARENA || P.off != 0 || kept(P.index) || !contiguous(y) || y.ty != TLH_TYPE_F32)
+                    continue;
+                const std::vector<size_t> who = readers_after(i, P);
+                if (who.size() != 1) continue;
+                const size_t j = who[0];
+                const Dispatch &c = d[j];
+                if (c.scratch_bytes != 0) continue;
+                if (is_core(c, TLH_CORE_ROPE) && same_place(c.src[0], P)) {
+                    const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
+                    bool ok = c.op.x[1] == 0 && x.ty == TLH_TYPE_F32 && contiguous(x) && x.ne[2] == 1 &&
+                              x.ne[3] == 1 && x.ne[0] * x.ne[1] == M && c.op.t[1].ne[0] >= 1 &&
+                              c.op.t[1].ty == TLH_TYPE_I32;
+                    if (ok && rope)
+                        ok = memcmp(rope->x, c.op.x, 9 * sizeof c.op.x[0]) == 0 && rope->t[0].ne[0] == x.ne[0] &&
+                             same_place(rpos, c.src[1]) && same_place(rff, c.src[2]);
+                    if (!ok) continue;
+                    int lay = EPI_CONTIG;
+                    std::vector<size_t> t = {j};
+                    if (c.op.x[9]) {  // into cache rows
+                        if (!idx_ty(c.op.t[3]) || o.ne[0] != M || o.nb[0] != (o.ty == TLH_TYPE_F16 ? 2 : 4)) continue;
+                        lay = EPI_CACHE_ROW;
+                        eidx[k] = c.src[3];
+                        e.idx_i64[k] = c.op.t[3].ty != TLH_TYPE_I32;
+                        e.rows[k] = o.ne[1];
+                        e.row_nb[k] = o.nb[1];
+                    } else {
+                        if (!contiguous(o) || elems(o) != M) continue;
+                        // a rotated key that only a one-token paged write reads
+                        const std::vector<size_t> w2 = readers_after(j, c.dst);
+                        if (o.ty == TLH_TYPE_F16 && w2.size() == 1 && d[w2[0]].kind == D_PAGED_WRITE &&
+                            d[w2[0]].pw[0] == 1 && !d[w2[0]].pw_f32[0] && same_place(d[w2[0]].src[0], c.dst) &&
+                            c.dst.buf == B_ARENA && !kept(c.dst.index) && (paged_w < 0 || paged_w == (int)w2[0])) {
+                            lay = EPI_PAGED_KEY;
+                            paged_w = (int)w2[0];
+                            paged_have |= 1;
+                            t.push_back(w2[0]);
+                        }
+                    }
+                    e.layout[k] = lay;
+                    e.rope[k] = 1;
+                    e.f16[k] = lay == EPI_PAGED_KEY || o.ty == TLH_TYPE_F16;
+                    if (lay != EPI_PAGED_KEY) edst[k] = c.dst;
+                    if (!rope) rope = &c.op, rpos = c.src[1], rff = c.src[2];
+                    take[k] = t;
+                } else if (is_core(c, TLH_CORE_SET_ROWS) && same_place(c.src[0], P)) {
+                    const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
+                    if (!(x.ne[0] == M && x.ne[1] == 1 && x.ne[2] == 1 && x.ne[3] == 1 && idx_ty(c.op.t[1]) &&
+                          o.ne[0] == M && (o.ty == TLH_TYPE_F16 || o.ty == TLH_TYPE_F32) &&
+                          o.nb[0] == (o.ty == TLH_TYPE_F16 ? 2 : 4)))
+                        continue;
+                    e.layout[k] = EPI_CACHE_ROW;
+                    e.f16[k] = o.ty == TLH_TYPE_F16;
+                    edst[k] = c.dst;
+                    eidx[k] = c.src[1];
+                    e.idx_i64[k] = c.op.t[1].ty != TLH_TYPE_I32;
+                    e.rows[k] = o.ne[1];
+                    e.row_nb[k] = o.nb[1];
+                    take[k] = {j};
+                } else if (c.kind == D_PAGED_WRITE && c.pw[0] == 1 && (paged_w < 0 || paged_w == (int)j)) {
+                    int side = -1;
+                    if (same_place(c.src[1], P) && c.pw_f32[1]) side = 1;
+                    else if (same_place(c.src[0], P) && c.pw_f32[0]) side = 0;
+                    if (side < 0) continue;
+                    e.layout[k] = side ? EPI_PAGED_VALUE : EPI_PAGED_KEY;
+                    e.f16[k] = 1;
+                    paged_w = (int)j;
+                    paged_have |= side ? 2 : 1;
+                    take[k] = {j};
+                }
+            }
+            // a paged write goes only with both of its operands
+            if (paged_w >= 0) {
+                const Dispatch &w = d[paged_w];
+                bool ok = paged_have == 3;
+                for (int k = 0; k < f.nmem && ok; ++k)
+                    if (e.layout[k] == EPI_PAGED_KEY || e.layout[k] == EPI_PAGED_VALUE) {
+                        ok = f.mop[k].t[0].ne[1] == (int64_t)w.pw[1] * w.pw[2];
+                        edst[k] = e.layout[k] == EPI_PAGED_KEY ? w.src[2] : w.src[3];
+                        eidx[k] = w.src[4];
+                        e.idx_i64[k] = 1;
+                        e.rows[k] = w.pw_blocks * w.pw[3];
+                    }
+                if (!ok)
+                    for (int k = 0; k < f.nmem; ++k)
+                        if (e.layout[k] == EPI_PAGED_KEY || e.layout[k] == EPI_PAGED_VALUE) {
+                            e.layout[k] = EPI_F32, e.rope[k] = 0, e.f16[k] = 0;
+                            take[k].clear();
+                        }
+                e.kvh = w.pw[1], e.hs = w.pw[2], e.bs = w.pw[3];
+            }
+            // nothing between the GEMV and an absorbed dispatch touches what
+            // the dispatch writes or writes what it reads
+            std::vector<size_t> all;
+            for (int k = 0; k < f.nmem; ++k) all.insert(all.end(), take[k].begin(), take[k].end());
+            std::sort(all.begin(), all.end());
+            all.erase(std::unique(all.begin(), all.end()), all.end());
+            if (all.empty()) continue;
+            bool ok = true;
+            std::vector<Place> rd, wr, r2, w2;
+            for (size_t j : all) {
+                places(d[j], rd, wr);
+                for (size_t t = i + 1; t < j && ok; ++t) {
+                    if (gone[t] || std::binary_search(all.begin(), all.end(), t)) continue;
+                    places(d[t], r2, w2);
+                    for (const Place &p : w2)
+                        for (const Place &q : rd) ok = ok && !same_root(p, q);
+                    for (const Place &p : wr) {
+                        for (const Place &q : r2) ok = ok && !same_root(p, q);
+                        for (const Place &q : w2) ok = ok && !same_root(p, q);
+                    }
+                }
+            }
+            if (!ok) continue;
+            if (rope) {
+                e.ne0 = rope->t[0].ne[0];
+                e.rp.n_dims = (int)rope->x[0];
+                e.rp.mode = (int)rope->x[1];
+                e.rp.freq_scale = __builtin_bit_cast(float, (int32_t)rope->x[2]);
+                e.rp.ext_factor = __builtin_bit_cast(float, (int32_t)rope->x[3]);
+                e.rp.attn_factor = __builtin_bit_cast(float, (int32_t)rope->x[4]);
+                e.rp.theta_scale = __builtin_bit_cast(float, (int32_t)rope->x[5]);
+                e.rp.corr0 = __builtin_bit_cast(float, (int32_t)rope->x[6]);
+                e.rp.corr1 = __builtin_bit_cast(float, (int32_t)rope->x[7]);
+                epos = rpos;
+                if (rope->x[8]) eff = rff;
+            }
+            e.on = 1;
+            Dispatch g = f;
+            g.kind = D_GEMV_PRO;
+            g.has_epi = 1;
+            g.epi = e;
+            for (int k = 0; k < 3; ++k) g.edst[k] = edst[k], g.eidx[k] = eidx[k];
+            g.epos = epos;
+            g.eff = eff;
+            for (size_t j : all) {
+                g.absorbed.push_back(d[j]);
+                g.pos_last = std::max(g.pos_last, d[j].pos_last);
+                gone[j] = 1;
+            }
+            d[i] = g;
         }
         std::vector<Dispatch> out;
         for (size_t i = 0; i < d.size(); ++i)
@@ -1105,17 +1322,11 @@ class Lowering {
         };
         for (const Dispatch &x : out.d) {
             if (x.pos_last == x.pos) continue;
+            std::vector<Place> rd, wr;
+            places(x, rd, wr);
             for (int64_t pos : {(int64_t)x.pos, (int64_t)x.pos_last}) {
-                for (int k = 0; k < NSRC; ++k) touch_place(x.src[k], pos);
-                touch_place(x.dst, pos);
-                for (int k = 0; k < x.nmem; ++k) touch_place(x.mdst[k], pos);
-                for (int k = 0; k < 4; ++k) touch_place(x.nsrc[k], pos);
-                touch_place(x.ndst, pos);
-                touch_place(x.gdst, pos);
-                for (int k = 0; k < x.nsub; ++k) {
-                    for (int m = 0; m < 4; ++m) touch_place(x.ssrc[k][m], pos);
-                    touch_place(x.sdst[k], pos);
-                }
+                for (const Place &p : rd) touch_place(p, pos);
+                for (const Place &p : wr) touch_place(p, pos);
             }
         }
         out.blocks.clear();
@@ -1238,6 +1449,18 @@ struct tlh_program {
 
     tlh_status enqueue(void *state, hipStream_t s) const {
         for (const Dispatch &x : low.d) {
+            const tlh_status st = launch_one(x, state, s);
+            if (st != TLH_OK) {
+                const int32_t id = low.node_ids[x.pos];
+                const std::string msg = tlh_last_error();
+                return set_error(st, "launching `%s` (tensor %d): %s", tensors[id].op, id, msg.c_str());
+            }
+        }
+        return TLH_OK;
+    }
+
+    tlh_status launch_one(const Dispatch &x, void *state, hipStream_t s) const {
+        {
             void *src[NSRC];
             for (int i = 0; i < NSRC; ++i) src[i] = resolve(x.src[i], state);
             void *dst = resolve(x.dst, state);
@@ -1342,6 +1565,15 @@ struct tlh_program {
                     pro.glu = (float *)resolve(x.gdst, state);
                     pro.glu_nb1 = x.gop.t[4].nb[1];
                 }
+                if (x.has_epi) {
+                    pro.epi = x.epi;
+                    for (int k = 0; k < 3; ++k) {
+                        pro.epi.dst[k] = (char *)resolve(x.edst[k], state);
+                        pro.epi.idx[k] = (const char *)resolve(x.eidx[k], state);
+                    }
+                    pro.epi.pos = (const int32_t *)resolve(x.epos, state);
+                    pro.epi.ff = (const float *)resolve(x.eff, state);
+                }
                 st = mul_mat_multi_pro(ops, w, dsts, x.nmem, pro, x.has_norm ? nullptr : src[1], s);
                 if (st == TLH_UNSUPPORTED) {  // the pieces one by one
                     const void *act = src[1];
@@ -1357,6 +1589,8 @@ struct tlh_program {
                             st = tlh_mul_mat(ops[k], w[k], act, dsts[k], scratch, x.scratch_bytes, s);
                     if (st == TLH_OK && x.has_glu)
                         st = tlh_core(TLH_CORE_GLU, &x.gop, dsts[0], dsts[1], nullptr, resolve(x.gdst, state), s);
+                    for (size_t k = 0; k < x.absorbed.size() && st == TLH_OK; ++k)
+                        st = launch_one(x.absorbed[k], state, s);
                 }
                 break;
             }
@@ -1369,13 +1603,8 @@ struct tlh_program {
                 }
                 break;
             }
-            if (st != TLH_OK) {
-                const int32_t id = low.node_ids[x.pos];
-                const std::string msg = tlh_last_error();
-                return set_error(st, "launching `%s` (tensor %d): %s", tensors[id].op, id, msg.c_str());
-            }
+            return st;
         }
-        return TLH_OK;
     }
 
     void drop_graph() {

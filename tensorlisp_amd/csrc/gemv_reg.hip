@@ -120,6 +120,10 @@ __device__ __forceinline__ void first_max_step(float &ba, float &bv, bool partne
 // IN_X: x with K <= 4096; IN_XL: x with K <= 16384; IN_NORM: the prologue's
 // p, q, w with K <= 4096.
 enum { IN_SCRATCH = 0, IN_X = 1, IN_NORM = 2, IN_XL = 3 };
+// OUT: how rows leave the kernel (OUT_STORE: f32 rows of dst or the
+// segments; OUT_GLU: the GemvPro SwiGLU epilogue; OUT_EPI: the GemvPro
+// store epilogue)
+enum { OUT_STORE = 0, OUT_GLU = 1, OUT_EPI = 2 };
 
 template <int IN> struct ActRegs {
     static constexpr int G = IN == IN_XL ? 4 : 1;
@@ -602,12 +606,14 @@ template <int R> struct WRegs<TLH_TYPE_Q8_0, R> {
 // quantize launch filled; IN_X: src1 rows, quantized by the workgroup into
 // LDS; IN_NORM: the GemvPro prologue's rows, likewise). GLU: the GemvPro
 // SwiGLU epilogue (rows of a wave pair gate and up rows: R / 2 of each).
-template <int WT, int NC, int R, int IN, bool PIPE, bool GLU>
+template <int WT, int NC, int R, int IN, bool PIPE, int OUT>
 __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const float *__restrict__ x,
                                                   int64_t x_row_bytes, int ksplit, int upw, const GemvPro pro) {
     constexpr int AT = vec_dot_type(WT);
     constexpr int V = R * NC;
+    constexpr bool GLU = OUT == OUT_GLU;
     static_assert(!GLU || R % 2 == 0, "GLU pairs R / 2 gate rows with R / 2 up rows");
+    static_assert(OUT != OUT_EPI || (NC == 1 && R % 2 == 0), "the store epilogue pairs rows of one column");
     __shared__ float part[4][V];
     __shared__ double shd[4];
     extern __shared__ __align__(16) char s_act[];  // IN != IN_SCRATCH: NC activation columns
@@ -730,6 +736,49 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             *(float *)(dbase + (a.n0 + n) * a.d_nb1 + m * 4) = v;
         }
     };
+    // OUT_EPI: row m (segment sg, row j of it) with value v and its pair's
+    // value o. The launcher keeps segment starts multiples of R, so a wave's
+    // rows share a segment and the selects below are on wave-uniform values.
+    auto epi_store = [&](int64_t m, float v, float o) {
+        const GemvEpi &e = pro.epi;
+        const int sg = seg_of(m);
+        const int64_t j = m - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]);
+        const int lay = sel(sg, e.layout[0], e.layout[1], e.layout[2]);
+        if (lay == EPI_F32) {
+            sel(sg, a.seg_dst[0], a.seg_dst[1], a.seg_dst[2])[j] = v;
+            return;
+        }
+        float y = v;
+        if (sel(sg, e.rope[0], e.rope[1], e.rope[2])) {
+            const int64_t el = j % e.ne0, p = el / 2;
+            if (2 * p < e.rp.n_dims) {
+                float cs, sn;
+                rope_cs_sn((float)e.pos[0], p, e.ff ? e.ff[p] : 1.0f, e.rp, cs, sn);
+                y = (el & 1) == 0 ? rope_first(v, o, cs, sn) : rope_second(o, v, cs, sn);
+            }
+        }
+        char *base = sel(sg, e.dst[0], e.dst[1], e.dst[2]);
+        const bool h16 = sel(sg, e.f16[0], e.f16[1], e.f16[2]) != 0;
+        int64_t at;  // element offset
+        if (lay == EPI_CONTIG) {
+            at = j;
+        } else {
+            const char *ip = sel(sg, e.idx[0], e.idx[1], e.idx[2]);
+            const int64_t r = sel(sg, e.idx_i64[0], e.idx_i64[1], e.idx_i64[2]) ? *(const int64_t *)ip
+                                                                                   : (int64_t)*(const int32_t *)ip;
+            if (r < 0 || r >= sel(sg, e.rows[0], e.rows[1], e.rows[2])) return;
+            if (lay == EPI_CACHE_ROW) {
+                base += r * sel(sg, e.row_nb[0], e.row_nb[1], e.row_nb[2]);
+                at = j;
+            } else {  // the paged pools' layouts: keys [blocks, kvh, hs/8, bs, 8], values [blocks, kvh, hs, bs]
+                const int64_t blk = r / e.bs, off = r % e.bs, h = j / e.hs, el = j % e.hs;
+                at = lay == EPI_PAGED_KEY ? (((blk * e.kvh + h) * (e.hs / 8) + el / 8) * e.bs + off) * 8 + el % 8
+                                          : ((blk * e.kvh + h) * e.hs + el) * e.bs + off;
+            }
+        }
+        if (h16) ((uint16_t *)base)[at] = f2h(y);
+        else ((float *)base)[at] = y;
+    };
     // products of row block rbk, their wave sums, the K slices merged, stored
     auto finish = [&](const WRegs<WT, R> &w, int64_t rbk) {
         float acc[R][NC];
@@ -776,6 +825,12 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
                 if (m0 + r < a.M && n < a.N)
                     *(float *)((char *)pro.glu + (a.n0 + n) * pro.glu_nb1 + (m0 + r) * 4) = swiglu_val(mine, up);
             }
+        } else if constexpr (OUT == OUT_EPI) {
+            // lane i stores row m0 + i; its rotation partner is row m0 + (i ^ 1)
+            float other = tot[0];
+#pragma unroll
+            for (int i = 1; i < V; ++i) other = (lane ^ 1) == i ? tot[i] : other;
+            if (emit && lane < V && m0 + lane < a.M) epi_store(m0 + lane, mine, other);
         } else {
             if (emit && lane < V) {
                 const int r = lane / NC, n = lane % NC;
@@ -836,10 +891,10 @@ template <typename Kern> static int64_t resident_blocks(Kern kern, int &cache) {
     return cache;
 }
 
-template <int WT, int NC, int R, int IN, bool PIPE, bool GLU>
+template <int WT, int NC, int R, int IN, bool PIPE, int OUT>
 static tlh_status launch_reg_pipe(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                   int ksplit, int upw, unsigned gx, hipStream_t stream) {
-    auto kern = k_gemv_reg<WT, NC, R, IN, PIPE, GLU>;
+    auto kern = k_gemv_reg<WT, NC, R, IN, PIPE, OUT>;
     const int64_t batches = a.ne12 * a.ne13;
     const size_t lds = IN == IN_SCRATCH ? 0 : (size_t)(NC * act_lds(vec_dot_type(WT), a.K).bytes);
     hipLaunchKernelGGL(kern, dim3(gx, 1, (unsigned)batches), dim3(256), lds, stream, a, x, x_row_bytes, ksplit, upw,
@@ -853,15 +908,16 @@ static tlh_status launch_reg_pipe(const MatmulArgs &a, const float *x, int64_t x
 // workgroup at least twice that in weight bytes. Once each workgroup has
 // several row blocks to walk, the double-buffered kernel keeps the weight
 // stream busy.
-template <int WT, int NC, int R, int IN, bool GLU>
+template <int WT, int NC, int R, int IN, int OUT>
 static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                  int ksplit, int upw, hipStream_t stream) {
+    constexpr bool GLU = OUT == OUT_GLU;
     static int slots = -1;
     const int groups = 4 / ksplit;
     const int64_t rows_per_block = (int64_t)groups * (GLU ? R / 2 : R);
     const int64_t row_blocks = (a.M + rows_per_block - 1) / rows_per_block;
     const int64_t batches = a.ne12 * a.ne13 > 0 ? a.ne12 * a.ne13 : 1;
-    int64_t gx = resident_blocks(k_gemv_reg<WT, NC, R, IN, false, GLU>, slots) / batches;
+    int64_t gx = resident_blocks(k_gemv_reg<WT, NC, R, IN, false, OUT>, slots) / batches;
     if (IN != IN_SCRATCH) {
         const int64_t wbytes = rows_per_block * (GLU ? 2 : 1) * (a.K / block_elems(WT)) * block_bytes(WT);
         const int64_t per_wg = (2 * 4 * a.K * NC + wbytes - 1) / wbytes;  // row blocks per workgroup, at least
@@ -869,25 +925,25 @@ static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_
     }
     gx = std::max<int64_t>(1, std::min(gx, row_blocks));
     if (row_blocks >= 2 * gx)
-        return launch_reg_pipe<WT, NC, R, IN, true, GLU>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
-    return launch_reg_pipe<WT, NC, R, IN, false, GLU>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
+        return launch_reg_pipe<WT, NC, R, IN, true, OUT>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
+    return launch_reg_pipe<WT, NC, R, IN, false, OUT>(a, x, x_row_bytes, pro, ksplit, upw, (unsigned)gx, stream);
 }
 
-template <int WT, int NC, int IN, bool GLU>
+template <int WT, int NC, int IN, int OUT>
 static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                 int ksplit, int upw, hipStream_t stream) {
     // q6_K holds 19 weight registers per row: two columns take 2 rows per wave
     constexpr int R = ((WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q5_K) && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
-    return launch_reg_cfg<WT, NC, R, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    return launch_reg_cfg<WT, NC, R, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 // N = 1 or 2 only: more columns of register-resident activations (20 VGPRs
 // per column) leave too few registers and spill.
-template <int WT, int IN, bool GLU>
+template <int WT, int IN, int OUT>
 static tlh_status launch_reg_wt(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                 int ksplit, int upw, hipStream_t stream) {
-    if (a.N == 1) return launch_reg_nc<WT, 1, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
-    return launch_reg_nc<WT, 2, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    if (OUT == OUT_EPI || a.N == 1) return launch_reg_nc<WT, 1, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    if constexpr (OUT != OUT_EPI) return launch_reg_nc<WT, 2, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 // Geometry of the register-resident GEMV for K: waves per row group and
@@ -901,15 +957,15 @@ bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw) {
     return upw <= 64;
 }
 
-template <int IN, bool GLU>
+template <int IN, int OUT>
 static tlh_status launch_reg_type(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                   int ksplit, int upw, hipStream_t stream) {
     switch (a.wtype) {
-    case TLH_TYPE_Q4_0: return launch_reg_wt<TLH_TYPE_Q4_0, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
-    case TLH_TYPE_Q8_0: return launch_reg_wt<TLH_TYPE_Q8_0, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
-    case TLH_TYPE_Q4_K: return launch_reg_wt<TLH_TYPE_Q4_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
-    case TLH_TYPE_Q5_K: return launch_reg_wt<TLH_TYPE_Q5_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
-    case TLH_TYPE_Q6_K: return launch_reg_wt<TLH_TYPE_Q6_K, IN, GLU>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q4_0: return launch_reg_wt<TLH_TYPE_Q4_0, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q8_0: return launch_reg_wt<TLH_TYPE_Q8_0, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q4_K: return launch_reg_wt<TLH_TYPE_Q4_K, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q5_K: return launch_reg_wt<TLH_TYPE_Q5_K, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
+    case TLH_TYPE_Q6_K: return launch_reg_wt<TLH_TYPE_Q6_K, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
     }
 }
@@ -918,9 +974,9 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     int ksplit = 1, upw = 64;
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     const GemvPro none;
-    if (!x) return launch_reg_type<IN_SCRATCH, false>(a, nullptr, 0, none, ksplit, upw, stream);
-    return a.K <= 4096 ? launch_reg_type<IN_X, false>(a, x, x_row_bytes, none, ksplit, upw, stream)
-                       : launch_reg_type<IN_XL, false>(a, x, x_row_bytes, none, ksplit, upw, stream);
+    if (!x) return launch_reg_type<IN_SCRATCH, OUT_STORE>(a, nullptr, 0, none, ksplit, upw, stream);
+    return a.K <= 4096 ? launch_reg_type<IN_X, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream)
+                       : launch_reg_type<IN_XL, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
 }
 
 tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
@@ -931,20 +987,49 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
     const bool glu = pro.glu != nullptr;
     if (glu && (a.nseg != 2 || a.seg_m0[1] != a.seg_m0[2] - a.seg_m0[1]))
         return set_error(TLH_INVALID, "gemv_reg: the SwiGLU epilogue needs two segments of equal rows");
+    const bool epi = pro.epi.on != 0;
+    if (epi) {
+        const GemvEpi &e = pro.epi;
+        if (glu || a.N != 1 || a.nseg < 1 || a.K > 4096)
+            return set_error(TLH_UNSUPPORTED, "gemv_reg: the store epilogue takes one column of segments, K <= 4096, "
+                                              "no SwiGLU");
+        bool rope = false;
+        for (int sg = 0; sg < a.nseg; ++sg) {
+            const int64_t rows = a.seg_m0[sg + 1] - a.seg_m0[sg];
+            if (a.seg_m0[sg] % 4 != 0)
+                return set_error(TLH_UNSUPPORTED, "gemv_reg: epilogue segments start at multiples of 4");
+            if (e.layout[sg] != EPI_F32 && !e.dst[sg]) return set_error(TLH_INVALID, "gemv_reg: epilogue without a destination");
+            if ((e.layout[sg] == EPI_CACHE_ROW || e.layout[sg] >= EPI_PAGED_KEY) && !e.idx[sg])
+                return set_error(TLH_INVALID, "gemv_reg: epilogue row or slot index missing");
+            if (e.layout[sg] >= EPI_PAGED_KEY &&
+                (!e.f16[sg] || !e.idx_i64[sg] || e.kvh < 1 || e.hs < 8 || e.hs % 8 || e.bs < 1 ||
+                 rows != (int64_t)e.kvh * e.hs))
+                return set_error(TLH_UNSUPPORTED, "gemv_reg: paged epilogue geometry");
+            if (e.rope[sg]) {
+                rope = true;
+                if (e.ne0 < 2 || e.ne0 % 2 || rows % e.ne0)
+                    return set_error(TLH_UNSUPPORTED, "gemv_reg: rotated segments are whole heads of even size");
+            }
+        }
+        if (rope && (!e.pos || e.rp.mode != 0 || e.rp.n_dims % 2 || e.rp.n_dims > e.ne0))
+            return set_error(TLH_UNSUPPORTED, "gemv_reg: the epilogue rotates in ROPE mode 0 only");
+    }
     MatmulArgs b = a;
     if (glu) b.M = a.seg_m0[1];  // rows of h
     if (pro.p) {
         if (x) return set_error(TLH_INVALID, "gemv_reg: a prologue forms the activation itself");
         if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: the norm prologue takes K <= 4096");
-        return glu ? launch_reg_type<IN_NORM, true>(b, nullptr, 0, pro, ksplit, upw, stream)
-                   : launch_reg_type<IN_NORM, false>(b, nullptr, 0, pro, ksplit, upw, stream);
+        return glu ? launch_reg_type<IN_NORM, OUT_GLU>(b, nullptr, 0, pro, ksplit, upw, stream)
+               : epi ? launch_reg_type<IN_NORM, OUT_EPI>(b, nullptr, 0, pro, ksplit, upw, stream)
+                     : launch_reg_type<IN_NORM, OUT_STORE>(b, nullptr, 0, pro, ksplit, upw, stream);
     }
     if (!x) return set_error(TLH_INVALID, "gemv_reg: no activation");
     if (a.K > 4096)
-        return glu ? launch_reg_type<IN_XL, true>(b, x, x_row_bytes, pro, ksplit, upw, stream)
-                   : launch_reg_type<IN_XL, false>(b, x, x_row_bytes, pro, ksplit, upw, stream);
-    return glu ? launch_reg_type<IN_X, true>(b, x, x_row_bytes, pro, ksplit, upw, stream)
-               : launch_reg_type<IN_X, false>(b, x, x_row_bytes, pro, ksplit, upw, stream);
+        return glu ? launch_reg_type<IN_XL, OUT_GLU>(b, x, x_row_bytes, pro, ksplit, upw, stream)
+                   : launch_reg_type<IN_XL, OUT_STORE>(b, x, x_row_bytes, pro, ksplit, upw, stream);
+    return glu ? launch_reg_type<IN_X, OUT_GLU>(b, x, x_row_bytes, pro, ksplit, upw, stream)
+           : epi ? launch_reg_type<IN_X, OUT_EPI>(b, x, x_row_bytes, pro, ksplit, upw, stream)
+                 : launch_reg_type<IN_X, OUT_STORE>(b, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 
 }  // namespace tlh

@@ -72,6 +72,33 @@ __host__ __device__ inline int64_t mm_act_rows(const MatmulArgs &a) {
 //  * Epilogue (glu != nullptr): the launch's two segments are a gate and an
 //    up matrix of equal rows; instead of their outputs the kernel stores
 //    h = silu(gate) * up (ggml_vec_swiglu_f32) at glu + n * glu_nb1 bytes.
+//  * Store epilogue (epi.on, N = 1, segments): segment s's row j goes out
+//    through epi.layout[s] instead of seg_dst[s][j], rotated first when
+//    epi.rope[s] (ROPE mode 0: rows 2p and 2p + 1 of a head of epi.ne0 rows
+//    are a pair; a wave holds both) -- the ROPE, type cast, SET_ROWS and
+//    one-token paged cache write that follow a Q / K / V projection.
+enum { EPI_F32 = 0, EPI_CONTIG = 1, EPI_CACHE_ROW = 2, EPI_PAGED_KEY = 3, EPI_PAGED_VALUE = 4 };
+struct GemvEpi {
+    int on = 0;
+    int layout[3] = {EPI_F32, EPI_F32, EPI_F32};
+    int f16[3] = {0, 0, 0};   // destination element type f16 (else f32); the paged pools are f16
+    int rope[3] = {0, 0, 0};
+    char *dst[3] = {nullptr, nullptr, nullptr};  // contiguous rows, the cache, or the paged pool
+    // EPI_CACHE_ROW: the row index (i32 or i64) and the cache's row stride and
+    // rows (an index outside them writes nothing); paged: the token's i64 slot
+    // and the pool's slots (a slot outside [0, slots) writes nothing)
+    const char *idx[3] = {nullptr, nullptr, nullptr};
+    int idx_i64[3] = {0, 0, 0};
+    int64_t row_nb[3] = {0, 0, 0};
+    int64_t rows[3] = {0, 0, 0};
+    int kvh = 0, hs = 0, bs = 0;  // paged pools: kv heads, head size, block size
+    // the rotation (one parameter set for every rotated segment): the token's
+    // position, the per-pair frequency factors (or null) and the head size
+    const int32_t *pos = nullptr;
+    const float *ff = nullptr;
+    int64_t ne0 = 0;
+    RopeParams rp;
+};
 struct GemvPro {
     const float *p = nullptr, *q = nullptr, *w = nullptr;
     float *s = nullptr;
@@ -79,6 +106,7 @@ struct GemvPro {
     float eps = 0.0f;
     float *glu = nullptr;
     int64_t glu_nb1 = 0;
+    GemvEpi epi;
 };
 
 // N <= 16. With x != nullptr (src1 rows in activation-row order, stride

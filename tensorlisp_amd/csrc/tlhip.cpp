@@ -585,6 +585,14 @@ tlh_status tlh::mul_mat_multi_pro(const tlh_op *const *ops, const void *const *w
     }
     if (glu && (((uintptr_t)pro.glu & 3) || (pro.glu_nb1 & 3)))
         return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: SwiGLU destination alignment");
+    const GemvEpi &e = pro.epi;
+    for (int i = 0; e.on && i < n; ++i) {
+        if (e.layout[i] == EPI_F32) continue;
+        const uintptr_t es = e.f16[i] ? 2 : 4, is = e.idx_i64[i] ? 8 : 4;
+        if (((uintptr_t)e.dst[i] | (uintptr_t)e.row_nb[i]) % es || (e.idx[i] && (uintptr_t)e.idx[i] % is) ||
+            (e.rope[i] && (((uintptr_t)e.pos & 3) || ((uintptr_t)e.ff & 3))))
+            return set_error(TLH_UNSUPPORTED, "mul_mat_multi_pro: epilogue pointer alignment");
+    }
     MatmulArgs m = mm_args(ops[0], s, w[0], nullptr, dst[0]);
     m.nseg = n;
     int64_t rows = 0;

@@ -282,6 +282,78 @@ def test_norm_feeding_one_gemv_is_one_launch(gpu, t):
     assert prog.stats()["launches"] == 1
 
 
+def qkv_rope_cache_graph(t, paged, norm, keep_members, E=1024, H=8, HKV=2, hd=128, n_ctx=64, bs=16, nblk=8):
+    """[RMS_NORM -> MUL ->] Q / K / V at one column, RoPE (mode 0) of Q and K,
+    then the K / V cache writes: dense f16 caches by SET_ROWS (Q stays f32), or
+    one paged-cache write of f16 casts (Q cast to f16 too), as the decoder step
+    builds them. keep_members keeps the three projections, which the store
+    epilogue fusion then refuses: the same graph runs piece by piece."""
+    b = G.Builder()
+    ekv = HKV * hd
+    x = b.input(N.F32, [E, 1])
+    pos = b.input(N.I32, [1])
+    slots = b.input(N.I32, [2]) if paged else b.input(N.I64, [1])
+    nw = b.weight(N.F32, [E])
+    wq, wk, wv = b.weight(t, [E, E]), b.weight(t, [E, ekv]), b.weight(t, [E, ekv])
+    cur = b.mul(b.rms_norm(x, 1e-5), nw) if norm else x
+    qm, km, vm = b.mul_mat(wq, cur), b.mul_mat(wk, cur), b.mul_mat(wv, cur)
+    rope = lambda a, h: b.rope_ext(b.reshape(a, hd, h, 1), pos, None, hd, 0, 4096, 500000.0, 1.0, 0.0, 1.0, 32.0,  # noqa: E731
+                                   1.0)
+    q, k = rope(qm, H), rope(km, HKV)
+    if paged:
+        n = nblk * HKV * hd * bs
+        kc, vc = b.state(N.F16, [n]), b.state(N.F16, [n])
+        q = b.cast(q, N.F16)
+        b.expand(q)
+        b.expand(b.paged_cache_write(b.cast(b.reshape(k, ekv, 1), N.F16), b.cast(vm, N.F16), kc, vc, slots, bs, HKV))
+        cache_bytes = 2 * n
+    else:
+        kc, vc = b.state(N.F16, [ekv, n_ctx]), b.state(N.F16, [ekv, n_ctx])
+        b.expand(b.set_rows(kc, b.reshape(k, ekv, 1), slots))
+        b.expand(b.set_rows(vc, vm, slots))
+        b.expand(q)
+        cache_bytes = 2 * ekv * n_ctx
+    keep = [q] + ([qm, km, vm] if keep_members else [])
+    return b, keep, q, cache_bytes, (E, ekv)
+
+
+@pytest.mark.parametrize("t", [N.Q4_K, N.Q8_0, N.Q6_K], ids=lambda t: N.TYPE_NAMES[t])
+@pytest.mark.parametrize("paged,norm,slot", [(False, True, 5), (False, False, 63), (True, True, 3 * 16 + 7),
+                                             (True, False, 0), (True, True, -1)],
+                         ids=["dense-norm", "dense", "paged-norm", "paged", "paged-skip"])
+def test_qkv_rope_cache_epilogue_is_one_launch(gpu, t, paged, norm, slot):
+    """The Q / K / V projection of a decode step with its RoPE and cache writes
+    (SET_ROWS into dense caches, or the one-token paged write, whose negative
+    slot writes nothing) runs as one register-GEMV launch, and its Q and caches
+    are bit-identical to the same graph launched piece by piece."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    outs = []
+    for keep_members in (False, True):
+        b, keep, q, cache_bytes, (E, ekv) = qkv_rope_cache_graph(t, paged, norm, keep_members)
+        nwh = (1.0 + 0.1 * synth.normal(91, (E,))).astype(np.float32)
+        ws = [dev(nwh)] + [dev(synth.random_blocks(t, 92 + i, M, E)) for i, M in enumerate((E, ekv, ekv))]
+        state = torch.zeros(2 * cache_bytes, dtype=torch.uint8, device="cuda")
+        prog = G.Program(b, keep, ws, [0, cache_bytes])
+        prog.write_input(0, dev(synth.normal(95, (1, E)) * 2 + 0.1))
+        prog.write_input(1, dev(np.array([37], np.int32)))
+        prog.write_input(2, dev(np.array([slot], np.int64).view(np.int32) if paged else np.array([slot], np.int64)))
+        prog.run(state)
+        got_q = prog.read(q, torch.int16 if paged else torch.float32, state)
+        torch.cuda.synchronize()
+        outs.append((got_q.cpu().numpy().copy(), state.cpu().numpy().copy(), prog.stats()["launches"]))
+    (fq, fs, fl), (uq, us, ul) = outs
+    np.testing.assert_array_equal(fq, uq)
+    np.testing.assert_array_equal(fs, us)
+    assert fl == 1 and ul > 1, (fl, ul)
+    if slot < 0:
+        assert not fs.any()
+    else:
+        assert fs.any()
+
+
 @pytest.mark.parametrize("n", [8192, 4100])
 def test_inplace_add_feeding_norm(gpu, n):
     """An in-place ADD (ggml_add_inplace: the sum overwrites src0) feeding
