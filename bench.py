@@ -12,14 +12,20 @@ weights in the 256 MB Infinity Cache (MALL) or L2.
 
 value  = whole-sweep algorithmic bytes (M*row_bytes + N*K*4 + N*M*4 per node)
          / wall time of the timed steps, GB/s.
-roofline = the dominant kernel (the Q4_K GEMV at N = 1 on the 128256 x 4096
-         lm_head shape): its algorithmic bytes / its mean duration from HIP
-         events on the launch stream, against 8 TB/s.
+roofline = the GEMV kernel of the sweep's heaviest node: its algorithmic bytes
+         (weights, the activation it reads, f32 outputs) / its mean duration
+         from HIP events on the launch stream, against 8 TB/s. A node above
+         N = 2 is a quantize launch and the GEMV; the GEMV is timed alone.
 cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, compiled from
-         the reference sources) on the same sweep, timed on this host.
-Also reported: an 8B Llama Q4_K bs=1 decode token rate counting only its
-matmuls (32 x (QKV, O, gate, up, down) + lm_head), from the per-node times;
-the q4_K prefill GEMM; paged-attention decode; dense
+         the reference sources) on the same sweep, timed on this host's cores
+         the GPU box allots the job (16), with the host's CPU model and count;
+         and its decode token rate on the same 8B model over a few steps.
+Also reported: configs[4] end to end through the executor -- Llama-3-8B
+shapes, random q4_K weights including the lm_head, paged KV cache, batch 1
+(the headline decode tokens/s) and batch 16 -- plus the dense-cache batch-1
+path with a q6_K lm_head; an 8B bs=1 token rate counting only the sweep's
+matmuls; the q4_K prefill GEMM alone and as the whole node with
+its quantize launch; paged-attention decode; dense
 FLASH_ATTN_EXT decode (32 sequences x 4096 keys) and a causal 512-token prefill.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -63,33 +69,118 @@ def gpu_blocks(torch, wtype, M, K, gen):
     return raw.reshape(M, (K // be) * bb)
 
 
-def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32):
-    """configs[4] at batch 1 through the executor (tlh_program_*): Llama-3-8B
-    shapes with q4_K matrices, a q4_K token embedding and a q6_K lm_head, f16 KV
-    caches written with SET_ROWS and read with FLASH_ATTN_EXT. A 512-token
-    prefill, then greedy decode steps whose next token is the previous step's
-    argmax, copied on the device into the next step's input (no host round
-    trip). Decode attends a cache view padded to 768 rows (the mask hides the
-    rows not yet written) so one program, captured once as a hipGraph, serves
-    every step. Returns a dict of timings."""
-    import numpy as np
-
-    from tensorlisp_amd import graph as G
+def decoder_weights_gpu(torch, gen, c):
+    """Random weights of the decoder `c` on the GPU, in weight-index order: RMS
+    norm weights 1 + 0.1 N(0,1); q4_K matrices drawn zero-mean (synth's
+    q4_K_model_blocks distribution, so that greedy decoding does not collapse
+    onto one token); other quantized types as structurally valid random blocks."""
     from tensorlisp_amd import native as N
+    from tensorlisp_amd import synth
 
-    c = G.DecoderConfig(n_ctx=1024)
     W = []
     for _, ty, ne in c.weight_shapes():
         if ty == N.F32:
             W.append(1.0 + 0.1 * torch.randn(ne[0], device="cuda", generator=gen))
+        elif ty == N.Q4_K:
+            W.append(synth.q4_K_model_blocks_gpu(torch, gen, ne[1], ne[0]))
         else:
             W.append(gpu_blocks(torch, ty, ne[1], ne[0], gen))
-    offs, total = c.state_bytes()
-    state = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    return W
+
+
+def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32, cpu_steps=0):
+    """configs[4] as BASELINE states it, through the executor (tlh_program_*):
+    Llama-3-8B shapes with random q4_K weights (token embedding, every matrix
+    and the lm_head), a 512-token prefill, then greedy decode steps over the
+    paged KV cache at batch 1 (the headline) and batch 16. Labelled extra: the
+    dense f16 cache (FLASH_ATTN_EXT) at batch 1 with a q6_K lm_head, as
+    Q4_K_M files have. cpu_steps > 0: ggml's CPU backend runs that many
+    decode steps of the same model (dense cache) for a CPU token rate."""
+    import dataclasses
+
+    from tensorlisp_amd import native as N
+
+    from tensorlisp_amd import graph as G
+
+    c = G.DecoderConfig(n_ctx=1024, out_type=N.Q4_K)
+    W = decoder_weights_gpu(torch, gen, c)
     weight_bytes = sum(w.numel() * w.element_size() for w in W)
     stream = torch.cuda.Stream()
-    torch.cuda.synchronize()  # weights and the zeroed state (default stream) before `stream` uses them
+    torch.cuda.synchronize()  # the weights (default stream) before `stream` uses them
     copy = lambda dst, src, n: N.check(N.lib().tlh_copy(dst, src, n, N._stream(stream)))  # noqa: E731
+    out = {"model": "Llama-3-8B shapes: 32 layers, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 128256, "
+                    "RoPE 500000; random q4_K weights (token embedding, matrices, lm_head)"}
+    for batch in (1, 16):
+        out[f"paged_bs{batch}"] = e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_tokens,
+                                                    decode_steps, batch=batch, eager_steps=eager_steps)
+    if cpu_steps > 0:
+        out["cpu_decode"] = cpu_decode(c, W, cpu_steps)
+    c6 = dataclasses.replace(c, out_type=N.Q6_K)
+    W[-1] = gpu_blocks(torch, N.Q6_K, c.n_vocab, c.n_embd, gen)
+    out["dense_bs1_q6k_lm_head"] = e2e_decoder_dense(torch, gen, c6, W, stream, copy, prefill_tokens, decode_steps,
+                                                     eager_steps)
+    del W
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_decode(c, W, steps):
+    """Decode token rate of ggml's CPU backend (oracle/_ref, compiled from the
+    reference's sources) on the same model: `steps` single-token greedy steps
+    of the dense-cache decode graph at positions 0.. (the CPU backend cannot
+    run the paged-attention nodes), each a ggml_graph_compute over the whole
+    8B model, on the threads the GPU box allots this job."""
+    import dataclasses
+
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import refs
+
+    from tensorlisp_amd import graph as G
+
+    r = refs.ref()
+    if r is None:
+        return None
+    threads = cpu_threads()
+    cc = dataclasses.replace(c, n_ctx=max(64, steps + 1))
+    hw = [w.cpu().numpy() for w in W]
+    states = [np.zeros((cc.n_ctx, cc.n_embd_kv), np.uint16) for _ in range(2 * cc.n_layer)]
+    st = G.decoder_step(cc, 1, cc.n_ctx)
+    tok, total = 1, 0.0
+    for i in range(steps + 1):  # the first step (page-ins) untimed
+        ins = [np.array([tok], np.int32), np.array([i], np.int32), np.array([i], np.int64),
+               G.causal_mask([i], cc.n_ctx)]
+        t0 = time.perf_counter()
+        _, am = r.ir_run(st.builder, hw, states, ins, [(st.logits, np.float32), (st.argmax, np.int32)],
+                         nthreads=threads)
+        if i > 0:
+            total += time.perf_counter() - t0
+        tok = int(am.reshape(-1)[0])
+    del hw
+    res = {"tokens_per_s": round(steps / total, 2), "ms_per_token": round(total / steps * 1e3, 1), "steps": steps,
+           "threads": threads, "kind": "reference",
+           "sample": f"{steps} single-token greedy decode steps at positions 1..{steps} (after one untimed step), "
+                     "dense f16 cache, the same random q4_K weights; ggml_graph_compute wall time per step"}
+    log(f"  cpu decode (ggml CPU backend, {threads} threads): {res['tokens_per_s']} tok/s over {steps} steps")
+    return res
+
+
+def e2e_decoder_dense(torch, gen, c, W, stream, copy, prefill_tokens=512, decode_steps=256, eager_steps=32):
+    """Batch 1 with the dense f16 caches written with SET_ROWS and read with
+    FLASH_ATTN_EXT: a 512-token prefill, then greedy decode steps whose next
+    token is the previous step's argmax, copied on the device into the next
+    step's input (no host round trip). Decode attends a cache view padded to
+    768 rows (the mask hides the rows not yet written) so one program, captured
+    once as a hipGraph, serves every step."""
+    import numpy as np
+
+    from tensorlisp_amd import graph as G
+
+    weight_bytes = sum(w.numel() * w.element_size() for w in W)
+    offs, total = c.state_bytes()
+    state = torch.zeros(total, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()  # the zeroed state (default stream) before `stream` uses it
 
     # prefill: 512 tokens at positions 0..511, logits of the last one
     T = prefill_tokens
@@ -144,8 +235,7 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
     kv_bytes = 2 * c.n_layer * n_kv * c.n_embd_kv * 2  # every cache row the padded view attends
     tok_bytes = weight_bytes - W[0].numel() + c.n_embd * 2 + kv_bytes  # embedding: one row
     out = {
-        "model": "Llama-3-8B shapes: 32 layers, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 128256, "
-                 "RoPE 500000; q4_K matrices and token embedding, q6_K lm_head; random weights",
+        "lm_head": "q6_K", "kv_cache": "dense f16, FLASH_ATTN_EXT over a 768-row view",
         "batch": 1, "prefill_tokens": T, "decode_steps": steps,
         "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(T / prefill_ms * 1e3, 1),
         "decode_ms_per_token_hipgraph": round(graph_ms, 4), "decode_tokens_per_s": round(1e3 / graph_ms, 1),
@@ -154,25 +244,23 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
         "decode_frac_of_hbm_peak": round(tok_bytes / graph_ms / 1e6 / HBM_PEAK_GBS, 4),
         "dispatches_per_decode_step": D.stats()["launches"],
     }
-    log(f"  e2e 8B q4_K: prefill {T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} tok/s); decode "
-        f"{graph_ms:.3f} ms/tok graph, {eager_ms:.3f} eager -> {out['decode_tokens_per_s']} tok/s, "
-        f"{out['decode_gbs']} GB/s")
+    log(f"  e2e 8B q4_K dense cache, q6_K lm_head: prefill {T} tok {prefill_ms:.1f} ms "
+        f"({out['prefill_tokens_per_s']} tok/s); decode {graph_ms:.3f} ms/tok graph, {eager_ms:.3f} eager -> "
+        f"{out['decode_tokens_per_s']} tok/s, {out['decode_gbs']} GB/s")
     del P, D, state
-    out["paged_batch16"] = e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_tokens,
-                                             decode_steps)
-    del W
-    torch.cuda.empty_cache()
     return out
 
 
 def e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_tokens=512, decode_steps=256,
-                      batch=16, block_size=16):
-    """configs[4] at batch 16 with the paged KV cache: each sequence's 512-token
-    prompt runs alone (keys and values into the pools through paged-cache-write,
-    attention over the prompt with FLASH_ATTN_EXT), then all 16 sequences decode
-    together, one token each per step, through the paged-attention node; each
-    step's next tokens are the previous step's argmax, copied on the device.
-    Blocks of a sequence are a random draw from the pool."""
+                      batch=16, block_size=16, eager_steps=32):
+    """configs[4] at `batch` sequences with the paged KV cache: each sequence's
+    512-token prompt runs alone (keys and values into the pools through
+    paged-cache-write, attention over the prompt with FLASH_ATTN_EXT), then
+    all sequences decode together, one token each per step, through the
+    paged-attention node; each step's next tokens are the previous step's
+    argmax, copied on the device (no host round trip). Blocks of a sequence
+    are a random draw from the pool. The decode program is captured once as a
+    hipGraph and replayed every step."""
     import numpy as np
 
     from tensorlisp_amd import graph as G
@@ -240,19 +328,28 @@ def e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_toke
     run_decode(steps, True)
     stream.synchronize()
     step_ms = (time.perf_counter() - t0) / steps * 1e3
-    # bytes a step reads: the weights once, every sequence's keys and values
+    t0 = time.perf_counter()
+    run_decode(min(eager_steps, steps), False)
+    stream.synchronize()
+    eager_ms = (time.perf_counter() - t0) / min(eager_steps, steps) * 1e3
+    # bytes a step reads: the weights once (one embedding row per sequence),
+    # every sequence's keys and values
     kv_rows = S * (T + (steps - 1) / 2 + 1)
     step_bytes = weight_bytes - W[0].numel() + S * c.n_embd * 2 + 2 * c.n_layer * kv_rows * c.n_embd_kv * 2
     out = {
-        "batch": S, "kv_cache": f"paged, block size {block_size}, {pc.n_blocks} blocks per layer drawn at random",
+        "batch": S, "lm_head": "q4_K",
+        "kv_cache": f"paged, block size {block_size}, {pc.n_blocks} blocks per layer drawn at random",
         "prefill_tokens_per_seq": T, "decode_steps": steps,
         "prefill_ms_all_seqs": round(prefill_ms, 1), "prefill_tokens_per_s": round(S * T / prefill_ms * 1e3, 1),
-        "decode_ms_per_step_hipgraph": round(step_ms, 4), "decode_tokens_per_s": round(S / step_ms * 1e3, 1),
-        "decode_gbs": round(step_bytes / step_ms / 1e6, 1),
+        "decode_ms_per_step_hipgraph": round(step_ms, 4), "decode_ms_per_step_eager": round(eager_ms, 4),
+        "decode_tokens_per_s": round(S / step_ms * 1e3, 1),
+        "decode_bytes_per_step": int(step_bytes), "decode_gbs": round(step_bytes / step_ms / 1e6, 1),
+        "decode_frac_of_hbm_peak": round(step_bytes / step_ms / 1e6 / HBM_PEAK_GBS, 4),
         "dispatches_per_decode_step": D.stats()["launches"],
     }
-    log(f"  e2e 8B q4_K batch {S} paged: prefill {S}x{T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} "
-        f"tok/s); decode {step_ms:.3f} ms/step -> {out['decode_tokens_per_s']} tok/s, {out['decode_gbs']} GB/s")
+    log(f"  e2e 8B q4_K paged, batch {S}: prefill {S}x{T} tok {prefill_ms:.1f} ms ({out['prefill_tokens_per_s']} "
+        f"tok/s); decode {step_ms:.3f} ms/step graph, {eager_ms:.3f} eager -> {out['decode_tokens_per_s']} tok/s, "
+        f"{out['decode_gbs']} GB/s")
     del P, D, state
     torch.cuda.empty_cache()
     return out
@@ -264,6 +361,23 @@ def algorithmic_bytes(wtype, M, K, n):
     return M * N.row_bytes(wtype, K) + n * K * 4 + n * M * 4
 
 
+def cpu_threads() -> int:
+    """Threads for the CPU legs: the cores the GPU box allots a one-GPU job
+    (OMP_NUM_THREADS there, 16), never more than the host has."""
+    n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or 16
+    return max(1, min(n, os.cpu_count() or 1))
+
+
+def cpu_model() -> str:
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(host_weights, cases, seconds: float):
     """The reference's ggml CPU backend (oracle/_ref) on the same sweep; falls back to
     our C port of it (oracle/liboracle.so) where the reference was not built."""
@@ -272,8 +386,7 @@ def cpu_baseline(host_weights, cases, seconds: float):
 
     import refs
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-    threads = max(1, min(threads, 16))
+    threads = cpu_threads()
     r = refs.ref()
     kind = "reference" if r is not None else "port"
     xs = {c: np.random.default_rng(1).standard_normal((c[3], c[2])).astype(np.float32) for c in cases}
@@ -292,8 +405,10 @@ def cpu_baseline(host_weights, cases, seconds: float):
             total_bytes += algorithmic_bytes(t, M, K, n)
         passes += 1
     return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "host": {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "threads_used": threads},
             "sample": f"{passes} pass(es) of the full 20-node sweep (same shapes, N in 1,8), "
-                      f"ggml_graph_compute wall time, {threads} threads, {total_s:.1f} s"}
+                      f"ggml_graph_compute wall time, {threads} threads (the cores the GPU box allots a one-GPU "
+                      f"job; the host reports {os.cpu_count()} CPUs, {cpu_model()}), {total_s:.1f} s"}
 
 
 def main() -> int:
@@ -306,6 +421,8 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true",
                     help="run only the end-to-end 8B decoder (configs[4]) and print its JSON")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--cpu-decode-steps", type=int, default=8,
+                    help="decode steps of the 8B model on ggml's CPU backend for the CPU token rate (0: skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -322,7 +439,8 @@ def main() -> int:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
     if args.e2e_only:
-        print(json.dumps(e2e_decoder(torch, gen, decode_steps=args.decode_steps)), flush=True)
+        print(json.dumps(e2e_decoder(torch, gen, decode_steps=args.decode_steps,
+                                     cpu_steps=0 if args.no_cpu else args.cpu_decode_steps)), flush=True)
         return 0
 
     cases = [(t, M, K, n) for t in (N.Q4_0, N.Q4_K) for (M, K) in SHAPES for n in (1, 8)]
@@ -387,8 +505,38 @@ def main() -> int:
     sweep_bytes = sum(bytes_per.values())
     value = sweep_bytes * args.steps / wall / 1e9
 
-    dom = (N.Q4_K, 128256, 4096, 1)
-    dom_gbs = bytes_per[dom] / node_ms[dom] / 1e6
+    # the roofline kernel: the GEMV of the sweep's heaviest node. A node at
+    # N <= 2 is one launch (the GEMV quantizes its activation itself); above,
+    # the node is a quantize launch and the GEMV, timed here alone (events on
+    # the launch stream around the compute launch, the activation quantized
+    # once before)
+    dom = max(cases, key=lambda c: node_ms[c])
+    dt, dM, dK, dn = dom
+    if dn <= 2:
+        dom_ms = node_ms[dom]
+        dom_bytes = bytes_per[dom]
+        dom_kernel = (f"{N.TYPE_NAMES[dt]} GEMV N={dn}, {dM}x{dK}, activation quantized in the kernel "
+                      "(tlh::k_gemv_reg), per launch")
+    else:
+        node = nodes[dom]
+        ws = weights[(dt, dM, dK)]
+        node.quantize(xs[dom], stream)
+        evs = []
+        for i in range(max(args.steps, 10)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            node.compute(ws[i % len(ws)], ys[dom], stream)
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        dom_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        # the compute launch reads the weights and the quantized activation, writes f32 rows
+        dom_bytes = dM * N.row_bytes(dt, dK) + dn * N.row_bytes(N.VEC_DOT_TYPE[dt], dK) + dn * dM * 4
+        dom_kernel = (f"{N.TYPE_NAMES[dt]} GEMV N={dn}, {dM}x{dK}: the GEMV launch of the MUL_MAT node "
+                      f"(tlh::k_gemv_mfma), after its quantize launch; node incl. quantize "
+                      f"{node_ms[dom] * 1e3:.1f} us")
+    dom_gbs = dom_bytes / dom_ms / 1e6
+    log(f"roofline kernel: {dom_kernel}: {dom_ms * 1e3:.1f} us, {dom_gbs:.0f} GB/s")
     # matmul-only decode token rate of an 8B Llama with Q4_K weights at bs = 1
     q = lambda M, K: node_ms[(N.Q4_K, M, K, 1)]  # noqa: E731
     tok_ms = 32 * (q(6144, 4096) + q(4096, 4096) + 2 * q(14336, 4096) + q(4096, 14336)) + q(128256, 4096)
@@ -414,12 +562,26 @@ def main() -> int:
                 node.compute(ws[i % len(ws)], y, stream)
                 e1.record(stream)
                 evs.append((e0, e1))
+            # the whole MUL_MAT node: the Q8_K quantize launch, then the GEMM
+            nevs = []
+            for i in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                node(ws[i % len(ws)], x, y, stream)
+                e1.record(stream)
+                nevs.append((e0, e1))
             torch.cuda.synchronize()
             ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+            node_ms_p = sum(a.elapsed_time(b) for a, b in nevs) / reps
             tflops = 2.0 * M * n * K / (ms * 1e-3) / 1e12
+            node_tflops = 2.0 * M * n * K / (node_ms_p * 1e-3) / 1e12
             prefill.append({"M": M, "K": K, "N": n, "us": round(ms * 1e3, 1), "tflops": round(tflops, 1),
-                            "frac_of_f16_mfma_peak": round(tflops / 2500.0, 4)})
-            log(f"  prefill q4_K {M}x{K} N={n}: {ms * 1e3:8.1f} us  {tflops:7.1f} TFLOP/s")
+                            "frac_of_int8_mfma_peak": round(tflops / 5000.0, 4),
+                            "frac_of_f16_mfma_peak": round(tflops / 2500.0, 4),
+                            "node_us_incl_quantize": round(node_ms_p * 1e3, 1),
+                            "node_tflops": round(node_tflops, 1)})
+            log(f"  prefill q4_K {M}x{K} N={n}: GEMM {ms * 1e3:8.1f} us  {tflops:7.1f} TFLOP/s; node with its "
+                f"quantize launch {node_ms_p * 1e3:8.1f} us  {node_tflops:7.1f} TFLOP/s")
         del ws, base
     torch.cuda.empty_cache()
 
@@ -518,7 +680,8 @@ def main() -> int:
         del fq, fk, fv, fm, fo, node
     torch.cuda.empty_cache()
 
-    e2e = e2e_decoder(torch, gen, decode_steps=args.decode_steps)
+    e2e = e2e_decoder(torch, gen, decode_steps=args.decode_steps,
+                      cpu_steps=0 if args.no_cpu else args.cpu_decode_steps)
 
     # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
     # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
@@ -543,6 +706,7 @@ def main() -> int:
         log(f"cpu baseline: ggml CPU backend on the same sweep (~{args.cpu_seconds:.0f} s)")
         host_w = {k: v[0].cpu().numpy() for k, v in weights.items()}
         cpu = cpu_baseline(host_w, cases, args.cpu_seconds)
+        cpu["decode_8b_q4k"] = e2e.get("cpu_decode")
         log(f"cpu baseline: {cpu['value']:.1f} GB/s ({cpu['kind']}, {cpu['cores']} threads)")
 
     line = {
@@ -563,7 +727,7 @@ def main() -> int:
                         "4096x14336, 128256x4096} x N {1, 8}; GGML_OP_MUL_MAT incl. Q8_0/Q8_K activation "
                         "quantization; weights rotated over >= 640 MB of HBM copies per node",
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-            "decode_tokens_per_s_8b_q4k_bs1": e2e["decode_tokens_per_s"],
+            "decode_tokens_per_s_8b_q4k_bs1": e2e["paged_bs1"]["decode_tokens_per_s"],
             "e2e_decoder_8b_q4k": e2e,
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
             "prefill_gemm_q4k": prefill,
@@ -573,8 +737,9 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "q4_K GEMV N=1 with fused Q8_K activation quantization, 128256x4096 "
-                      "(tlh::k_gemv_reg<12, 1, 4, true, true>), per launch",
+            "kernel": dom_kernel,
+            "us": round(dom_ms * 1e3, 2),
+            "bytes": int(dom_bytes),
             "achieved": round(dom_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

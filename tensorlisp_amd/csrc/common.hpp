@@ -240,19 +240,26 @@ struct RopeParams {
 // (ops.cpp:5846-5860) forms it, so the angles match the CPU's bit for bit
 // (a powf would differ in the last bits, which at positions in the
 // thousands moves the angle visibly). ff: the pair's frequency factor.
-__device__ __forceinline__ void rope_cs_sn(float pos, int64_t p, float ff, const RopeParams &r, float &cs, float &sn) {
+// The angle of pair p from tp = pos * theta_scale^p, and the magnitude scale.
+__device__ __forceinline__ float rope_theta(float tp, int64_t p, float ff, const RopeParams &r, float &mscale) {
 #pragma clang fp contract(off)
-    float tp = pos;
-    for (int64_t k = 0; k < p; ++k) tp *= r.theta_scale;
-    const float theta_extrap = tp / ff;
+    const float theta_extrap = ff == 1.0f ? tp : tp / ff;  // x / 1 is exact: the same value, no division
     float theta = r.freq_scale * theta_extrap;
-    float mscale = r.attn_factor;
+    mscale = r.attn_factor;
     if (r.ext_factor != 0.0f) {
         const float y = ((float)p - r.corr0) / fmaxf(0.001f, r.corr1 - r.corr0);
         const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * r.ext_factor;
         theta = r.freq_scale * theta_extrap * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
         mscale *= 1.0f + 0.1f * logf(1.0f / r.freq_scale);
     }
+    return theta;
+}
+__device__ __forceinline__ void rope_cs_sn(float pos, int64_t p, float ff, const RopeParams &r, float &cs, float &sn) {
+#pragma clang fp contract(off)
+    float tp = pos;
+    for (int64_t k = 0; k < p; ++k) tp *= r.theta_scale;
+    float mscale;
+    const float theta = rope_theta(tp, p, ff, r, mscale);
     cs = cosf(theta) * mscale;
     sn = sinf(theta) * mscale;
 }

@@ -1432,6 +1432,9 @@ struct tlh_program {
     std::vector<std::pair<int64_t, int64_t>> inputs;  // (io offset, bytes) per input index
     int64_t io_bytes = 0;
     char *arena = nullptr, *io = nullptr;
+    // zeroed counters the one-launch paged attention leaves zeroed (its
+    // dispatches run in stream order, so they share them)
+    unsigned *counters = nullptr;
     hipGraphExec_t exec = nullptr;
     void *exec_state = nullptr;
     hipStream_t exec_stream = nullptr;
@@ -1482,12 +1485,10 @@ struct tlh_program {
                 a.v_cache = src[2];
                 a.block_tables = (const int32_t *)src[3];
                 a.context_lens = (const int32_t *)src[4];
-                if (x.pa_f32) {
-                    a.out = nullptr;
-                    st = launch_paged_attention(a, scratch, x.scratch_bytes, s, (float *)dst);
-                } else {
-                    st = tlh_paged_attention(&a, scratch, x.scratch_bytes, s);
-                }
+                if (x.pa_f32) a.out = nullptr;
+                st = a.num_seqs == 0 ? TLH_OK
+                                     : launch_paged_attention(a, scratch, x.scratch_bytes, s,
+                                                              x.pa_f32 ? (float *)dst : nullptr, counters);
                 break;
             }
             case D_MM_COMPUTE_MULTI: {
@@ -1694,11 +1695,18 @@ tlh_status tlh_program_compile(const tlh_ir_tensor *tensors, int32_t n_tensors, 
         p->inputs[i] = {p->io_bytes, std::max<int64_t>(in_bytes[i], 0)};
         p->io_bytes += align_up(std::max<int64_t>(in_bytes[i], 1));
     }
+    size_t n_counters = 0;
+    for (const Dispatch &x : p->low.d)
+        if (x.kind == D_PAGED_ATTN) n_counters = std::max(n_counters, paged_attention_counters(x.pa));
     (void)hipGetDevice(&p->device);
     if ((st = hip_ok(hipMalloc((void **)&p->arena, (size_t)std::max<int64_t>(p->low.arena, ALIGN)), "arena")) !=
             TLH_OK ||
         (st = hip_ok(hipMalloc((void **)&p->io, (size_t)std::max<int64_t>(p->io_bytes, ALIGN)), "io buffer")) !=
-            TLH_OK) {
+            TLH_OK ||
+        (n_counters &&
+         ((st = hip_ok(hipMalloc((void **)&p->counters, n_counters * sizeof(unsigned)), "counters")) != TLH_OK ||
+          (st = hip_ok(hipMemset(p->counters, 0, n_counters * sizeof(unsigned)), "counters")) != TLH_OK ||
+          (st = hip_ok(hipStreamSynchronize(nullptr), "counters")) != TLH_OK))) {  // zero before any run's stream
         tlh_program_destroy(p);
         return st;
     }
@@ -1711,6 +1719,7 @@ tlh_status tlh_program_destroy(tlh_program *p) {
     p->drop_graph();
     if (p->arena) (void)hipFree(p->arena);
     if (p->io) (void)hipFree(p->io);
+    if (p->counters) (void)hipFree(p->counters);
     delete p;
     return TLH_OK;
 }

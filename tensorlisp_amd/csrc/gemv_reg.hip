@@ -619,19 +619,18 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     extern __shared__ __align__(16) char s_act[];  // IN != IN_SCRATCH: NC activation columns
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int groups = 4 / ksplit;
+    // The set-up is branch-free 32-bit arithmetic (the host keeps every count
+    // below 2^31): a branch splits the kernel-argument loads into rounds the
+    // kernel waits for one after another before its first weight load.
+    const int groups = ksplit == 1 ? 4 : ksplit == 2 ? 2 : 1;  // 4 / ksplit
     const int grp = wave / ksplit, kw = wave % ksplit;
     const int64_t K = a.K;
     const int64_t units = K / 64;
     const int64_t u = (int64_t)kw * upw + lane;
     const bool uvalid = lane < upw && u < units;
-    const int64_t batch = blockIdx.z;
-    int64_t i12 = 0, i13 = 0;
-    const uint8_t *W = a.w;
-    if (gridDim.z > 1) {  // 64-bit divisions only where there are batch slices
-        i12 = batch % a.ne12, i13 = batch / a.ne12;
-        W += (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
-    }
+    const uint32_t batch = blockIdx.z;
+    const uint32_t i13 = batch / (uint32_t)a.ne12, i12 = batch - i13 * (uint32_t)a.ne12;
+    const uint8_t *W = a.w + (int64_t)(i12 / (uint32_t)a.r2) * a.w_nb2 + (int64_t)(i13 / (uint32_t)a.r3) * a.w_nb3;
     const int64_t arow0 = a.n0 + a.N_total * batch;
     // output rows a workgroup covers per step (GLU: rows of h, R / 2 per wave)
     constexpr int RO = GLU ? R / 2 : R;
@@ -664,6 +663,43 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         }
     };
 
+    // OUT_EPI: the token's position, cache rows / slots and frequency
+    // factors are read before anything else (the epilogue would otherwise
+    // wait on cold loads after the products), and the pairs' cos / sin go to
+    // LDS while the weights are in flight (written before the quantization's
+    // barrier, read after it).
+    constexpr int EPI_PAIRS = OUT == OUT_EPI ? 256 : 1;
+    __shared__ float s_cs[EPI_PAIRS], s_sn[EPI_PAIRS];
+    // raw words, converted only where they are used (a conversion here would
+    // wait for the loads): row / slot k is hi:lo (i64) or lo & hi (i32, one
+    // word read twice), then the position and four frequency factors
+    int32_t e_lo[3] = {0, 0, 0}, e_hi[3] = {0, 0, 0}, e_rpos = 0, e_rff[4] = {0, 0, 0, 0};
+    const bool e_rope = OUT == OUT_EPI && (pro.epi.rope[0] | pro.epi.rope[1] | pro.epi.rope[2]);
+    if constexpr (OUT == OUT_EPI) {
+        // vector loads: a scalar load's wait would cover every scalar load in
+        // flight and stall the kernel here (the offset `z` is a zero the
+        // compiler cannot see through, so the addresses are per lane); every
+        // load is unconditional, from the weights where a pointer is absent,
+        // so no branch makes the compiler wait for it either
+        const GemvEpi &e = pro.epi;
+        const char *any = (const char *)a.seg_w[0];
+        int z;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+        auto ld32 = [z](const char *p) { return *(const int32_t *)(p + z); };
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const char *ip = e.idx[k] ? e.idx[k] : any;
+            e_lo[k] = ld32(ip);
+            e_hi[k] = ld32(ip + 4 * e.idx_i64[k]);
+        }
+        e_rpos = ld32(e.pos ? (const char *)e.pos : any);
+        const float *ffp = e.ff ? e.ff : (const float *)any;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = (threadIdx.x & 63) + 64 * i;
+            e_rff[i] = ld32((const char *)(ffp + (e.ff && p < e.ne0 / 2 ? p : 0)));
+        }
+    }
     // In-kernel activations are loaded first, then the first row block's
     // weights are requested, so quantizing waits only for the activations
     // while the weights are in flight.
@@ -684,7 +720,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     // branch would make the compiler wait for every outstanding load where the
     // branch rejoins, instead of only for the ones the next step needs.
     WRegs<WT, R> cur, nxt;
-    const int64_t nblocks = (a.M + rows_per_block - 1) / rows_per_block;
+    const int64_t nblocks = ((uint32_t)a.M + (uint32_t)rows_per_block - 1) / (uint32_t)rows_per_block;
     int64_t rb = blockIdx.x;  // the launch never has more workgroups than row blocks
     const int64_t ul = uvalid ? u : 0;
     {
@@ -726,6 +762,45 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
 #pragma unroll
         for (int n = 0; n < NC; ++n) lds_unit<AT, WT>(s_act + n * L.bytes, K, u, uvalid, act[n]);
     }
+    if constexpr (OUT == OUT_EPI) {
+        // the pairs' cos (wave 1) and sin (wave 0) into LDS while the weights
+        // land: lane l takes pairs l, l + 64, ...; the angles' chain of
+        // products runs in every lane and each lane keeps the terms of its
+        // pairs, so no lane loops on its own
+        const int np = min(pro.epi.ne0, (int64_t)pro.epi.rp.n_dims) / 2;
+        if (e_rope && wave < 2) {
+            const int l = lane;
+            const float e_pos = (float)e_rpos;
+            float cap[4] = {e_pos, e_pos, e_pos, e_pos};
+            float tp = e_pos;
+            if (np <= 64) {  // straight-line: 63 products, each kept by its lane
+                const float ts = pro.epi.rp.theta_scale;
+#pragma unroll
+                for (int k = 1; k < 64; ++k) {
+                    tp *= ts;
+                    cap[0] = k == l ? tp : cap[0];
+                }
+            } else {
+                for (int k = 1; k < np; ++k) {
+                    tp *= pro.epi.rp.theta_scale;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) cap[i] = k == l + 64 * i ? tp : cap[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = l + 64 * i;
+                if (p < np) {
+                    float mscale;
+                    const float ff = pro.epi.ff ? __builtin_bit_cast(float, e_rff[i]) : 1.0f;
+                    const float theta = rope_theta(cap[i], p, ff, pro.epi.rp, mscale);
+                    if (wave == 0) s_sn[p] = sinf(theta) * mscale;
+                    else s_cs[p] = cosf(theta) * mscale;
+                }
+            }
+        }
+        lds_barrier();
+    }
 
     char *dbase = a.nseg > 0 ? nullptr : (char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3;
     auto store = [&](int64_t m, int n, float v) {
@@ -749,11 +824,11 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
             return;
         }
         float y = v;
+        const uint32_t ju = (uint32_t)j;  // rows, heads and slots are below 2^31 (the launcher's check)
         if (sel(sg, e.rope[0], e.rope[1], e.rope[2])) {
-            const int64_t el = j % e.ne0, p = el / 2;
+            const uint32_t el = ju % (uint32_t)e.ne0, p = el / 2;
             if (2 * p < e.rp.n_dims) {
-                float cs, sn;
-                rope_cs_sn((float)e.pos[0], p, e.ff ? e.ff[p] : 1.0f, e.rp, cs, sn);
+                const float cs = s_cs[p], sn = s_sn[p];
                 y = (el & 1) == 0 ? rope_first(v, o, cs, sn) : rope_second(o, v, cs, sn);
             }
         }
@@ -763,15 +838,17 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         if (lay == EPI_CONTIG) {
             at = j;
         } else {
-            const char *ip = sel(sg, e.idx[0], e.idx[1], e.idx[2]);
-            const int64_t r = sel(sg, e.idx_i64[0], e.idx_i64[1], e.idx_i64[2]) ? *(const int64_t *)ip
-                                                                                   : (int64_t)*(const int32_t *)ip;
+            const int32_t lo = sel(sg, e_lo[0], e_lo[1], e_lo[2]), hi = sel(sg, e_hi[0], e_hi[1], e_hi[2]);
+            const int64_t r = sel(sg, e.idx_i64[0], e.idx_i64[1], e.idx_i64[2])
+                                  ? (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo)
+                                  : (int64_t)(lo & hi);
             if (r < 0 || r >= sel(sg, e.rows[0], e.rows[1], e.rows[2])) return;
             if (lay == EPI_CACHE_ROW) {
                 base += r * sel(sg, e.row_nb[0], e.row_nb[1], e.row_nb[2]);
                 at = j;
             } else {  // the paged pools' layouts: keys [blocks, kvh, hs/8, bs, 8], values [blocks, kvh, hs, bs]
-                const int64_t blk = r / e.bs, off = r % e.bs, h = j / e.hs, el = j % e.hs;
+                const uint32_t ru = (uint32_t)r, bs = (uint32_t)e.bs, hs = (uint32_t)e.hs;
+                const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, el = ju % hs;
                 at = lay == EPI_PAGED_KEY ? (((blk * e.kvh + h) * (e.hs / 8) + el / 8) * e.bs + off) * 8 + el % 8
                                           : ((blk * e.kvh + h) * e.hs + el) * e.bs + off;
             }
@@ -844,7 +921,7 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
         // in the steady state: the compiler then waits only for the older
         // buffer's loads.
         const int64_t g = gridDim.x, b0 = blockIdx.x;
-        const int64_t mine = (nblocks - b0 + g - 1) / g;  // blocks of this workgroup, >= 2
+        const int64_t mine = (uint32_t)(nblocks - b0 + g - 1) / (uint32_t)g;  // blocks of this workgroup, >= 2
         auto blk = [&](int64_t i) { return b0 + i * g; };
         int64_t i = 0;
         for (; i + 3 < mine; i += 2) {
@@ -970,7 +1047,15 @@ static tlh_status launch_reg_type(const MatmulArgs &a, const float *x, int64_t x
     }
 }
 
+// The kernel's set-up arithmetic is 32-bit.
+static bool reg_counts_ok(const MatmulArgs &a) {
+    const int64_t lim = (int64_t)1 << 31;
+    return a.M < lim && a.ne12 >= 1 && a.ne13 >= 1 && a.r2 >= 1 && a.r3 >= 1 && a.ne12 * a.ne13 < lim &&
+           a.ne12 < lim;
+}
+
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
+    if (!reg_counts_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: counts past 2^31");
     int ksplit = 1, upw = 64;
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     const GemvPro none;
@@ -982,6 +1067,7 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
 tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
                                hipStream_t stream) {
     int ksplit = 1, upw = 64;
+    if (!reg_counts_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: counts past 2^31");
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     if (a.ne12 * a.ne13 != 1) return set_error(TLH_INVALID, "gemv_reg: a prologue / epilogue takes one batch slice");
     const bool glu = pro.glu != nullptr;
@@ -1001,13 +1087,15 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
             if (e.layout[sg] != EPI_F32 && !e.dst[sg]) return set_error(TLH_INVALID, "gemv_reg: epilogue without a destination");
             if ((e.layout[sg] == EPI_CACHE_ROW || e.layout[sg] >= EPI_PAGED_KEY) && !e.idx[sg])
                 return set_error(TLH_INVALID, "gemv_reg: epilogue row or slot index missing");
+            if (e.rows[sg] >= ((int64_t)1 << 31))
+                return set_error(TLH_UNSUPPORTED, "gemv_reg: epilogue cache rows or pool slots past 2^31");
             if (e.layout[sg] >= EPI_PAGED_KEY &&
                 (!e.f16[sg] || !e.idx_i64[sg] || e.kvh < 1 || e.hs < 8 || e.hs % 8 || e.bs < 1 ||
                  rows != (int64_t)e.kvh * e.hs))
                 return set_error(TLH_UNSUPPORTED, "gemv_reg: paged epilogue geometry");
             if (e.rope[sg]) {
                 rope = true;
-                if (e.ne0 < 2 || e.ne0 % 2 || rows % e.ne0)
+                if (e.ne0 < 2 || e.ne0 % 2 || e.ne0 > 512 || rows % e.ne0)
                     return set_error(TLH_UNSUPPORTED, "gemv_reg: rotated segments are whole heads of even size");
             }
         }

@@ -187,10 +187,14 @@ tlh_status launch_core_multi(int n, const int *kinds, const tlh_op *ops, const v
 tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,
                        hipStream_t stream);
 
-// out32 != null: the f16 results are written widened to f32 there instead of a.out
+// out32 != null: the f16 results are written widened to f32 there instead of
+// a.out. counters != null: one launch that merges the partitions itself, on
+// paged_attention_counters(a) zeroed counters it leaves zeroed (launches that
+// share them must be stream-ordered); else a second launch merges them.
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
-                                  hipStream_t stream, float *out32 = nullptr);
+                                  hipStream_t stream, float *out32 = nullptr, unsigned *counters = nullptr);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
+size_t paged_attention_counters(const tlh_paged_attention_args &a);
 // key_f32 / value_f32: that source is f32 and is rounded to f16 on the way
 tlh_status launch_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
                                     const int64_t *slots, int num_tokens, int num_kv_heads, int head_size,

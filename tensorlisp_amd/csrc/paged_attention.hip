@@ -21,13 +21,17 @@
 //    touched once;
 //  * waves merge their (max, sum, acc) through LDS; partitions are merged by
 //    a second kernel (flash-decoding) into the f16 output.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace tlh {
 
-// tokens per partition (a multiple of every block size): 512, or 256 when
-// sequences x kv heads x 512-token partitions make fewer than 512 workgroups
-constexpr int PA_PART = 512;
+// tokens per partition (a multiple of every block size): 512; 256 when
+// sequences x kv heads x 512-token partitions make fewer than 512
+// workgroups; 64 when even 128-token ones would leave most of the 256 CUs
+// idle (a short batch-1 context: one 16-token tile per wave)
+constexpr int PA_PART = 512, PA_PART_SMALL = 64;
 constexpr int PA_WAVES = 4;
 
 // Scratch per (seq, head, partition): max, sum, acc[HS] (f32).
@@ -57,13 +61,57 @@ __device__ __forceinline__ f32x4_t mfma16(half4_t a, half4_t b, f32x4_t c) {
 //       dim c) 8 contiguous bytes.
 // Heads past the group (c >= gc) have zero q and are dropped; one MFMA serves
 // up to 16 query heads of a kv head, so a page is read once per group.
-template <int HS, int BS, bool PIPE, int PART>
+// Merge partitions 0 .. np-1 of (seq, head) for output dim d, f16-rounded
+// (the reduce kernel's loop, and the last partition's in the one-launch form).
+template <int HS, bool COHERENT = false>
+__device__ __forceinline__ uint16_t merge_parts(const float *base, int np, int d) {
+    constexpr int CHUNK = 16;
+    auto get = [](const float *p) {
+        if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else return *p;
+    };
+    float M = -INFINITY, lsum = 0.0f, a = 0.0f;
+    for (int p0 = 0; p0 < np; p0 += CHUNK) {
+        float m[CHUNK], l[CHUNK], v[CHUNK];
+#pragma unroll
+        for (int i = 0; i < CHUNK; ++i) {
+            const int64_t o = (int64_t)(p0 + i < np ? p0 + i : p0) * (HS + 2);
+            m[i] = get(base + o);
+            l[i] = get(base + o + 1);
+            v[i] = get(base + o + 2 + d);
+        }
+        float cm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < CHUNK; ++i) cm = fmaxf(cm, m[i]);  // repeats of p0 change nothing
+        const float Mn = fmaxf(M, cm);
+        if (Mn == -INFINITY) continue;
+        const float so = __expf(M - Mn);  // 0 while M is -inf (then lsum and a are 0)
+        lsum *= so;
+        a *= so;
+#pragma unroll
+        for (int i = 0; i < CHUNK; ++i) {
+            const float w = p0 + i < np ? __expf(m[i] - Mn) : 0.0f;
+            lsum += w * l[i];
+            a += w * v[i];
+        }
+        M = Mn;
+    }
+    return f2h(a * (1.0f / (lsum + 1e-6f)));
+}
+
+// MERGE (one launch): after writing its partial, a workgroup counts itself
+// in on its (sequence, head group) counter; the last of the sequence's
+// partitions to arrive merges them all into the output and sets the counter
+// back to zero. The counters start at zero (the caller's zeroed buffer) and
+// launches that share them must be stream-ordered.
+template <int HS, int BS, bool PIPE, int PART, bool MERGE>
 __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                                                     const uint16_t *__restrict__ vc,
                                                     const int32_t *__restrict__ tables,
                                                     const int32_t *__restrict__ lens, int num_heads, int num_kv_heads,
                                                     int gc, int max_blocks, float scale, int P,
-                                                    float *__restrict__ scratch) {
+                                                    float *__restrict__ scratch, unsigned *__restrict__ counters,
+                                                    uint16_t *__restrict__ out, float *__restrict__ out32) {
     constexpr int KS = HS / 16;  // QK steps = PV output tiles
     __shared__ int s_bt[PART / 8];
     __shared__ float s_m[PA_WAVES][16], s_l[PA_WAVES][16];
@@ -215,10 +263,44 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
             a += f * s_acc[w][h][d];
         }
         float *slotp = part_slot<HS>(scratch, seq, head0 + h, part, num_heads, P);
-        slotp[2 + d] = a;
+        // the one-launch form's partials are agent-scope stores: coherent
+        // across the XCDs' L2s without a write-back of the whole L2
+        auto put = [&](float *p, float v) {
+            if constexpr (MERGE) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *p = v;
+        };
+        put(slotp + 2 + d, a);
         if (d == 0) {
-            slotp[0] = M;
-            slotp[1] = lsum;
+            put(slotp, M);
+            put(slotp + 1, lsum);
+        }
+    }
+    if constexpr (MERGE) {
+        // Every wave's partial stores complete before the barrier (the
+        // barrier's wait), so the counter moves only after they have reached
+        // the coherent level; the last workgroup reads them back with
+        // agent-scope loads. No fence: an L2 write-back per wave, or an
+        // invalidate that drops the pages the other workgroups are reading,
+        // costs more than the merge saves.
+        __shared__ int s_last;
+        const int np = min(P, L > 0 ? (L + PART - 1) / PART : 1);  // the partitions that get here
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned *cnt = counters + (int64_t)seq * gridDim.x + blockIdx.x;
+            const unsigned before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = before + 1 == (unsigned)np;
+            if (s_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        for (int e = threadIdx.x; e < gc * HS; e += blockDim.x) {
+            const int h = e / HS, d = e % HS;
+            const uint16_t r = merge_parts<HS, true>(
+                scratch + (int64_t)(seq * num_heads + head0 + h) * P * (HS + 2), np, d);
+            const int64_t o = ((int64_t)seq * num_heads + head0 + h) * HS + d;
+            if (out32) out32[o] = h2f(r);
+            else out[o] = r;
         }
     }
 }
@@ -231,49 +313,25 @@ template <int HS, int PART>
 __global__ void __launch_bounds__(256) k_paged_attn_reduce(uint16_t *__restrict__ out, float *__restrict__ out32,
                                                            const float *__restrict__ scratch,
                                                            const int32_t *__restrict__ lens, int num_heads, int P) {
-    constexpr int CHUNK = 16;
     const int head = blockIdx.x, seq = blockIdx.y;
     const int L = lens[seq];
     // partitions holding this sequence's context (never more than were written)
     const int np = min(P, L > 0 ? (L + PART - 1) / PART : 1);
     const float *base = scratch + (int64_t)(seq * num_heads + head) * P * (HS + 2);
     for (int d = threadIdx.x; d < HS; d += blockDim.x) {
-        float M = -INFINITY, lsum = 0.0f, a = 0.0f;
-        for (int p0 = 0; p0 < np; p0 += CHUNK) {
-            float m[CHUNK], l[CHUNK], v[CHUNK];
-#pragma unroll
-            for (int i = 0; i < CHUNK; ++i) {
-                const int64_t o = (int64_t)(p0 + i < np ? p0 + i : p0) * (HS + 2);
-                m[i] = base[o];
-                l[i] = base[o + 1];
-                v[i] = base[o + 2 + d];
-            }
-            float cm = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < CHUNK; ++i) cm = fmaxf(cm, m[i]);  // repeats of p0 change nothing
-            const float Mn = fmaxf(M, cm);
-            if (Mn == -INFINITY) continue;
-            const float so = __expf(M - Mn);  // 0 while M is -inf (then lsum and a are 0)
-            lsum *= so;
-            a *= so;
-#pragma unroll
-            for (int i = 0; i < CHUNK; ++i) {
-                const float w = p0 + i < np ? __expf(m[i] - Mn) : 0.0f;
-                lsum += w * l[i];
-                a += w * v[i];
-            }
-            M = Mn;
-        }
-        const uint16_t h = f2h(a * (1.0f / (lsum + 1e-6f)));
+        const uint16_t h = merge_parts<HS>(base, np, d);
         const int64_t o = ((int64_t)seq * num_heads + head) * HS + d;
         if (out32) out32[o] = h2f(h);  // the f16 result widened (a cast to f32 fused into this store)
         else out[o] = h;
     }
 }
 
+static int64_t pa_workgroups(const tlh_paged_attention_args &a, int part) {
+    return (int64_t)a.num_seqs * a.num_kv_heads * (a.max_context_len > 0 ? (a.max_context_len + part - 1) / part : 1);
+}
 static int pa_part(const tlh_paged_attention_args &a) {
-    const int64_t p512 = a.max_context_len > 0 ? (a.max_context_len + PA_PART - 1) / PA_PART : 1;
-    return (int64_t)a.num_seqs * a.num_kv_heads * p512 < 512 ? PA_PART / 2 : PA_PART;
+    if (pa_workgroups(a, PA_PART) >= 512) return PA_PART;
+    return pa_workgroups(a, 128) >= 256 ? PA_PART / 2 : PA_PART_SMALL;
 }
 
 static int pa_partitions(const tlh_paged_attention_args &a) {
@@ -285,12 +343,22 @@ static int pa_partitions(const tlh_paged_attention_args &a) {
 // the size grows with num_seqs and max_context_len: a caller may size its
 // scratch once for its largest batch and context.
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
-    const int64_t parts = a.max_context_len > 0 ? (a.max_context_len + PA_PART / 2 - 1) / (PA_PART / 2) : 1;
-    return (size_t)a.num_seqs * a.num_heads * parts * (a.head_size + 2) * sizeof(float);
+    auto bytes = [&](int part) {
+        const int64_t parts = a.max_context_len > 0 ? (a.max_context_len + part - 1) / part : 1;
+        return (int64_t)a.num_seqs * a.num_heads * parts * (a.head_size + 2) * (int64_t)sizeof(float);
+    };
+    // 64-token partitions only while sequences x kv heads x ceil(context /
+    // 128) < 256, where sequences x heads x ceil(context / 64) <= 510 x the
+    // group size: a bounded extra term keeps the size growing with the batch
+    // and the context
+    const int64_t G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
+    const int64_t bound = 510 * G * (a.head_size + 2) * (int64_t)sizeof(float);
+    return (size_t)(bytes(PA_PART / 2) + std::min(bytes(PA_PART_SMALL), bound));
 }
 
-template <int HS, int BS>
-static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32) {
+template <int HS, int BS, int PART>
+static void launch_pa3(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
+                       unsigned *counters) {
     const int P = pa_partitions(a);
     const int G = a.num_heads / a.num_kv_heads;
     int gc = G < 16 ? G : 16;  // query heads per workgroup: a divisor of G, at most 16
@@ -298,41 +366,61 @@ static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStr
     constexpr bool PIPE = HS <= 128;  // two register sets fit
     const dim3 grid(a.num_kv_heads * (G / gc), a.num_seqs, P), rgrid(a.num_heads, a.num_seqs);
     const dim3 rblock(HS < 256 ? HS : 256);
-    if (pa_part(a) == PA_PART) {
-        hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PA_PART>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
+    if (counters) {
+        hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PART, true>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
                            (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
-                           a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch);
-        hipLaunchKernelGGL((k_paged_attn_reduce<HS, PA_PART>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
-                           (const float *)scratch, a.context_lens, a.num_heads, P);
-    } else {
-        hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PA_PART / 2>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
-                           (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
-                           a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch);
-        hipLaunchKernelGGL((k_paged_attn_reduce<HS, PA_PART / 2>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
-                           (const float *)scratch, a.context_lens, a.num_heads, P);
+                           a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch, counters,
+                           (uint16_t *)a.out, out32);
+        return;
+    }
+    hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PART, false>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
+                       (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
+                       a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch, nullptr, nullptr,
+                       nullptr);
+    hipLaunchKernelGGL((k_paged_attn_reduce<HS, PART>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
+                       (const float *)scratch, a.context_lens, a.num_heads, P);
+}
+
+template <int HS, int BS>
+static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
+                       unsigned *counters) {
+    switch (pa_part(a)) {
+    case PA_PART: launch_pa3<HS, BS, PA_PART>(a, scratch, stream, out32, counters); break;
+    case PA_PART / 2: launch_pa3<HS, BS, PA_PART / 2>(a, scratch, stream, out32, counters); break;
+    default: launch_pa3<HS, BS, PA_PART_SMALL>(a, scratch, stream, out32, counters); break;
     }
 }
 
 template <int HS>
-static void launch_pa1(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32) {
+static void launch_pa1(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
+                       unsigned *counters) {
     switch (a.block_size) {
-    case 8: launch_pa2<HS, 8>(a, scratch, stream, out32); break;
-    case 16: launch_pa2<HS, 16>(a, scratch, stream, out32); break;
-    default: launch_pa2<HS, 32>(a, scratch, stream, out32); break;
+    case 8: launch_pa2<HS, 8>(a, scratch, stream, out32, counters); break;
+    case 16: launch_pa2<HS, 16>(a, scratch, stream, out32, counters); break;
+    default: launch_pa2<HS, 32>(a, scratch, stream, out32, counters); break;
     }
 }
 
+// Counters the one-launch form takes: one per (sequence, workgroup of a kv
+// head's query heads).
+size_t paged_attention_counters(const tlh_paged_attention_args &a) {
+    const int G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
+    int gc = G < 16 ? G : 16;
+    while (gc > 1 && G % gc) --gc;
+    return (size_t)a.num_seqs * a.num_kv_heads * (G / (gc > 0 ? gc : 1));
+}
+
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t, hipStream_t stream,
-                                  float *out32) {
+                                  float *out32, unsigned *counters) {
     float *s = (float *)scratch;
     switch (a.head_size) {
-    case 64: launch_pa1<64>(a, s, stream, out32); break;
-    case 80: launch_pa1<80>(a, s, stream, out32); break;
-    case 96: launch_pa1<96>(a, s, stream, out32); break;
-    case 112: launch_pa1<112>(a, s, stream, out32); break;
-    case 128: launch_pa1<128>(a, s, stream, out32); break;
-    case 192: launch_pa1<192>(a, s, stream, out32); break;
-    case 256: launch_pa1<256>(a, s, stream, out32); break;
+    case 64: launch_pa1<64>(a, s, stream, out32, counters); break;
+    case 80: launch_pa1<80>(a, s, stream, out32, counters); break;
+    case 96: launch_pa1<96>(a, s, stream, out32, counters); break;
+    case 112: launch_pa1<112>(a, s, stream, out32, counters); break;
+    case 128: launch_pa1<128>(a, s, stream, out32, counters); break;
+    case 192: launch_pa1<192>(a, s, stream, out32, counters); break;
+    case 256: launch_pa1<256>(a, s, stream, out32, counters); break;
     default: return set_error(TLH_INVALID, "paged_attention: head_size %d", a.head_size);
     }
     return check_launch("paged_attention");

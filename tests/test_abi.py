@@ -154,14 +154,21 @@ def test_paged_attention_geometry_validation(kw, status):
     n = C.c_size_t()
     st, msg = _status(N.lib().tlh_paged_attention_scratch_bytes, C.byref(paged_args(**kw)), C.byref(n))
     assert st == status, msg
-    if status == "OK":  # partials [seqs][heads][ceil(max_ctx / 256)][head_size + 2] f32
-        assert n.value == 32 * 32 * (8192 // 256) * (128 + 2) * 4
+    if status == "OK":  # partials [seqs][heads][ceil(max_ctx / 256)][head_size + 2] f32, plus the
+        # bounded room of 64-token partitions (510 x group size rows)
+        assert n.value == 32 * 32 * (8192 // 256) * (128 + 2) * 4 + min(32 * 32 * (8192 // 64), 510 * 4) * 130 * 4
 
 
 def test_paged_attention_scratch_grows_with_batch_and_context():
-    """The scratch size never shrinks as num_seqs or max_context_len grow (it is
-    sized for the shorter of the two partition lengths the launch may pick), so
-    one buffer sized for the largest call serves every smaller one."""
+    """The scratch size never shrinks as num_seqs or max_context_len grow, so one
+    buffer sized for the largest call serves every smaller one; and it holds the
+    partials of the partition length the launch picks: 512 tokens when
+    sequences x kv heads x 512-token partitions reach 512 workgroups, else 256
+    when 128-token ones would reach 256, else 64."""
+    def need(seqs, ctx, kvh=8, heads=32):
+        parts = lambda p: -(-ctx // p)  # noqa: E731
+        part = 512 if seqs * kvh * parts(512) >= 512 else (256 if seqs * kvh * parts(128) >= 256 else 64)
+        return seqs * heads * parts(part) * 130 * 4
     def size(seqs, ctx):
         n = C.c_size_t()
         a = paged_args(num_seqs=seqs, max_context_len=ctx, max_blocks_per_seq=(ctx + 15) // 16)
@@ -171,9 +178,11 @@ def test_paged_attention_scratch_grows_with_batch_and_context():
     for ctx in (1, 255, 256, 257, 4096, 8192, 8193):
         sizes = [size(s, ctx) for s in range(1, 40)]
         assert sizes == sorted(sizes), ctx
+        assert all(sz >= need(s, ctx) for s, sz in zip(range(1, 40), sizes)), ctx
     for s in (1, 3, 4, 32):
         sizes = [size(s, c) for c in range(1, 9000, 97)]
         assert sizes == sorted(sizes), s
+        assert all(sz >= need(s, c) for c, sz in zip(range(1, 9000, 97), sizes)), s
 
 
 def _fa_op(nb=2, nh=8, nhkv=2, nq=1, L=1000, D=128, DV=None, kdt="f16", mask=True, **kw):

@@ -221,3 +221,45 @@ def test_cache_write_then_attention_matches_dense(gpu):
             p = np.exp(lg - lg.max())
             want = (p / p.sum()) @ dense_v[s][:, g, :]
             assert np.abs(got[s, h] - want).max() <= TOL * np.abs(want).max()
+
+
+@pytest.mark.parametrize("hs,bs,kvh,heads,lens", [
+    (128, 16, 8, 32, [768]),                   # a batch-1 decode step (3 partitions)
+    (128, 16, 8, 32, [512, 1, 1024, 513]),
+    (64, 8, 8, 32, [8192, 100, 3000, 511]),   # 512-token partitions
+    (128, 16, 2, 6, [0, 300, 2049]),          # an empty context, a group of 3
+])
+def test_one_launch_merge_matches_two_launches(gpu, hs, bs, kvh, heads, lens):
+    """A paged-attention node in a program runs as one launch whose last
+    partition of each (sequence, head group) merges the others (on counters it
+    leaves zeroed). Its output is bit-identical to the two-launch form of the
+    C ABI on every run, eager and replayed as a graph."""
+    import torch
+
+    from tensorlisp_amd import graph as G
+
+    q, kc, vc, tables, L = _random_paged(len(lens), heads, kvh, hs, bs, lens, 1400 + hs + len(lens))
+    scale = 1.0 / np.sqrt(hs)
+    max_ctx = int(max(1, max(lens)))
+    want = run_gpu(q, kc, vc, tables, L, kvh, bs, scale, max_ctx)
+    b = G.Builder()
+    qi = b.input(N.F16, [hs, heads, len(lens)])
+    ti = b.input(N.I32, [tables.shape[1], len(lens)])
+    li = b.input(N.I32, [len(lens)])
+    kw, vw = b.weight(N.F16, [kc.size]), b.weight(N.F16, [vc.size])
+    out = b.paged_attention(qi, kw, vw, ti, li, bs, max_ctx, scale, kvh)
+    b.expand(out)
+    prog = G.Program(b, [out], [dev(kc.view(np.int16)), dev(vc.view(np.int16))])
+    assert prog.stats()["launches"] == 1
+    ins = [dev(a) for a in (q.view(np.int16), tables, L)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    for i, a in enumerate(ins):
+        prog.write_input(i, a, stream)
+    for rep in range(5):
+        with torch.cuda.stream(stream):
+            prog.run(None, stream, graph=rep >= 2)
+            got = prog.read(out, torch.int16, None, stream)
+        stream.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16).reshape(want.shape), want,
+                                      err_msg=f"run {rep}")
