@@ -355,6 +355,81 @@ def e2e_decoder_paged(torch, gen, c, W, weight_bytes, stream, copy, prefill_toke
     return out
 
 
+def gemv_vs_floor(torch, gen, stream, shapes, pool_bytes=1200 << 20, reps=50):
+    """Cold N = 1 q4_K GEMV time (tlh_mul_mat, activation quantized in the
+    kernel) beside a plain streaming read of the same weight bytes
+    (tlh_read_floor, best of grids 256..4096 with 1 or 4 loads in flight per
+    lane), both back to back over `reps` launches that rotate through copies
+    in a 1.2 GB pool so no launch finds its bytes in MALL or L2; the launches
+    are captured as one hipGraph and timed with events around its replay."""
+    from tensorlisp_amd import native as N
+
+    pool = torch.randint(0, 256, (pool_bytes,), dtype=torch.uint8, device="cuda", generator=gen)
+    out = []
+
+    def timed(fn):
+        # the launches captured once as a graph and replayed: a Python loop of
+        # launches would leave the GPU idle between kernels of a few us
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(3):
+                fn(i, side)
+            side.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for i in range(reps):
+                    fn(i, torch.cuda.current_stream())
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(side)
+            g.replay()
+            e1.record(side)
+        e1.synchronize()
+        del g
+        return e0.elapsed_time(e1) / reps * 1e3  # us
+
+    for M, K in shapes:
+        rb = N.row_bytes(N.Q4_K, K)
+        nbytes = M * rb
+        slot = (nbytes + 4095) // 4096 * 4096
+        ncopy = min(64, pool_bytes // slot)
+        w = [synth_q4k_into(torch, gen, pool, i * slot, M, K) for i in range(ncopy)]
+        x = torch.randn((1, K), device="cuda", generator=gen)
+        y = torch.empty((1, M), dtype=torch.float32, device="cuda")
+        node = N.MulMat(N.Q4_K, M, K, 1)
+        torch.cuda.synchronize()
+        gemv_us = timed(lambda i, s: node(w[i % ncopy], x, y, s))
+        floor = []
+        for grid in (256, 512, 1024, 2048, 4096):
+            for loads in (1, 4):
+                us = timed(lambda i, s: N.check(N.lib().tlh_read_floor(
+                    pool.data_ptr() + (i % ncopy) * slot, nbytes // 16 * 16, grid, loads, N._stream(s))))
+                floor.append((us, grid, loads))
+        f_us, f_grid, f_loads = min(floor)
+        out.append({"M": M, "K": K, "weight_bytes": nbytes, "copies": ncopy, "gemv_us": round(gemv_us, 2),
+                    "read_floor_us": round(f_us, 2), "floor_grid": f_grid, "floor_loads_per_lane": f_loads,
+                    "gemv_gbs": round(nbytes / gemv_us / 1e3, 1), "floor_gbs": round(nbytes / f_us / 1e3, 1)})
+        log(f"  cold q4_K GEMV {M:6d}x{K:<5d}: {gemv_us:6.2f} us vs read floor {f_us:6.2f} us "
+            f"(grid {f_grid}, {f_loads} load(s)/lane)")
+    del pool
+    torch.cuda.empty_cache()
+    return out
+
+
+def synth_q4k_into(torch, gen, pool, offset, M, K):
+    """A [M, row_bytes] uint8 view of `pool` at `offset` holding random q4_K
+    blocks with small finite f16 scales."""
+    from tensorlisp_amd import native as N
+
+    rb = N.row_bytes(N.Q4_K, K)
+    w = pool[offset:offset + M * rb].view(M, rb)
+    blk = w.view(M * (K // 256), 144)
+    d = (torch.rand((blk.shape[0], 2), device="cuda", generator=gen) * 1e-3 + 1e-4).to(torch.float16)
+    blk[:, :4] = d.view(torch.uint8).reshape(-1, 4)
+    return w
+
+
 def algorithmic_bytes(wtype, M, K, n):
     from tensorlisp_amd import native as N
 
@@ -411,6 +486,182 @@ def cpu_baseline(host_weights, cases, seconds: float):
                       f"job; the host reports {os.cpu_count()} CPUs, {cpu_model()}), {total_s:.1f} s"}
 
 
+FLOOR_SHAPES = [(4096, 4096), (6144, 4096), (14336, 4096), (4096, 14336), (28672, 4096), (128256, 4096)]
+
+
+def copy_scale_kernel(torch):
+    """A plain device copy of known size (256 MiB): the scale for rocprof's
+    FETCH_SIZE / WRITE_SIZE counters when profiles/ derive HBM traffic per
+    launch."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def run_prefill(torch, gen, stream):
+    """the q4_K prefill GEMM on 14336x4096 and 4096x14336 at N = 512
+    and 2048, the GEMM launch alone and the whole MUL_MAT node with its
+    quantize launch, HIP events on the stream, weights rotated."""
+    from tensorlisp_amd import native as N
+
+    # prefill GEMM (configs[2]): q4_K 14336x4096 and 4096x14336, N = 512 / 2048, GEMM kernel
+    # alone (the activation quantization runs first as its own phase), rotated weights
+    prefill = []
+    for (M, K) in ((14336, 4096), (4096, 14336)):
+        base = gpu_blocks(torch, N.Q4_K, M, K, gen)
+        ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
+        for n in (512, 2048):
+            node = N.MulMat(N.Q4_K, M, K, n)
+            x = torch.randn((n, K), device="cuda", generator=gen)
+            y = torch.empty((n, M), dtype=torch.float32, device="cuda")
+            node.quantize(x, stream)
+            for i in range(2):
+                node.compute(ws[i % len(ws)], y, stream)
+            reps = 6
+            evs = []
+            for i in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                node.compute(ws[i % len(ws)], y, stream)
+                e1.record(stream)
+                evs.append((e0, e1))
+            # the whole MUL_MAT node: the Q8_K quantize launch, then the GEMM
+            nevs = []
+            for i in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                node(ws[i % len(ws)], x, y, stream)
+                e1.record(stream)
+                nevs.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+            node_ms_p = sum(a.elapsed_time(b) for a, b in nevs) / reps
+            tflops = 2.0 * M * n * K / (ms * 1e-3) / 1e12
+            node_tflops = 2.0 * M * n * K / (node_ms_p * 1e-3) / 1e12
+            prefill.append({"M": M, "K": K, "N": n, "us": round(ms * 1e3, 1), "tflops": round(tflops, 1),
+                            "frac_of_int8_mfma_peak": round(tflops / 5000.0, 4),
+                            "frac_of_f16_mfma_peak": round(tflops / 2500.0, 4),
+                            "node_us_incl_quantize": round(node_ms_p * 1e3, 1),
+                            "node_tflops": round(node_tflops, 1)})
+            log(f"  prefill q4_K {M}x{K} N={n}: GEMM {ms * 1e3:8.1f} us  {tflops:7.1f} TFLOP/s; node with its "
+                f"quantize launch {node_ms_p * 1e3:8.1f} us  {node_tflops:7.1f} TFLOP/s")
+        del ws, base
+    torch.cuda.empty_cache()
+
+    return prefill
+
+
+def run_q6_lm_head(torch, gen, stream):
+    from tensorlisp_amd import native as N
+
+    # q6_K output projection (the lm_head of Q4_K_M files), 128256 x 4096, N = 1 and 8
+    q6 = []
+    base = gpu_blocks(torch, N.Q6_K, 128256, 4096, gen)
+    ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
+    for n in (1, 8):
+        node = N.MulMat(N.Q6_K, 128256, 4096, n)
+        x = torch.randn((n, 4096), device="cuda", generator=gen)
+        y = torch.empty((n, 128256), dtype=torch.float32, device="cuda")
+        for i in range(2):
+            node(ws[i % len(ws)], x, y, stream)
+        evs = []
+        for i in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            node(ws[i % len(ws)], x, y, stream)
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        b = algorithmic_bytes(N.Q6_K, 128256, 4096, n)
+        q6.append({"M": 128256, "K": 4096, "N": n, "us": round(ms * 1e3, 1), "gbs": round(b / ms / 1e6, 1),
+                   "frac_of_hbm_peak": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)})
+        log(f"  q6_K  128256x4096  n={n}: {ms * 1e3:8.1f} us  {b / ms / 1e6:7.0f} GB/s")
+    del ws, base
+    torch.cuda.empty_cache()
+
+    return q6
+
+
+def run_attention(torch, gen, stream):
+    """configs[3] paged-attention decode, and dense FLASH_ATTN_EXT decode and
+    causal prefill."""
+    from tensorlisp_amd import native as N
+
+    # paged-attention decode (configs[3]): 32 sequences, 32 q / 8 kv heads, hs 128, 16-token
+    # pages scattered over a 65,536-page pool (2 GiB per cache), lens ~ U[512, 8192]
+    seqs, heads, kvh, hs, bs, pool = 32, 32, 8, 128, 16, 65536
+    lens = torch.randint(512, 8193, (seqs,), device="cuda", generator=gen, dtype=torch.int32)
+    maxb = 8192 // bs
+    kc = torch.randn((pool, kvh, hs // 8, bs, 8), device="cuda", generator=gen, dtype=torch.float16)
+    vc = torch.randn((pool, kvh, hs, bs), device="cuda", generator=gen, dtype=torch.float16)
+    tables = torch.randperm(pool, device="cuda", generator=gen)[: seqs * maxb].to(torch.int32).reshape(seqs, maxb)
+    qa = torch.randn((seqs, heads, hs), device="cuda", generator=gen, dtype=torch.float16)
+    oa = torch.empty_like(qa)
+    pa = N.PagedAttention(seqs, heads, kvh, hs, bs, maxb, 8192, hs ** -0.5)
+    lsum = int(lens.sum().item())
+    pages = int(((lens + bs - 1) // bs).sum().item())
+    attn_bytes = lsum * kvh * hs * 2 * 2 + 2 * seqs * heads * hs * 2 + pages * 4 + seqs * 4
+    for _ in range(2):
+        pa(oa, qa, kc, vc, tables, lens, stream)
+    evs = []
+    for _ in range(10):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        pa(oa, qa, kc, vc, tables, lens, stream)
+        e1.record(stream)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    attn_gbs = attn_bytes / attn_ms / 1e6
+    attention = {"seqs": seqs, "heads": heads, "kv_heads": kvh, "head_size": hs, "block_size": bs,
+                 "context_tokens": lsum, "bytes": attn_bytes, "us": round(attn_ms * 1e3, 1),
+                 "gbs": round(attn_gbs, 1), "frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4)}
+    log(f"  paged attention {seqs} seqs, {lsum} tokens: {attn_ms * 1e3:8.1f} us  {attn_gbs:7.0f} GB/s")
+    del kc, vc
+    torch.cuda.empty_cache()
+
+    # dense FLASH_ATTN_EXT decode: the same 32 sequences x 32 q / 8 kv heads x 128 with a
+    # per-sequence f16 cache of 4096 keys (ggml k/v [128, 4096, 8, 32]), one query each;
+    # and a causal 512-token prefill of one sequence (q [128, 512, 32, 1], mask [512, 512])
+    fa = {}
+    for name, nb, nq, L, causal in (("decode", 32, 1, 4096, False), ("prefill_causal", 1, 512, 512, True)):
+        fq = torch.randn((nb, heads, nq, hs), device="cuda", generator=gen, dtype=torch.float32)
+        fk = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
+        fv = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
+        fm = None
+        if causal:
+            fm = torch.full((nq, L), float("-inf"), device="cuda").triu(1 + L - nq).to(torch.float16)[None, None]
+            fm = fm.contiguous()
+        fo = torch.empty((nb, nq, heads, hs), device="cuda", dtype=torch.float32)
+        node = N.FlashAttnExt(fq, fk, fv, fm, fo, hs ** -0.5)
+        for _ in range(2):
+            node(fq, fk, fv, fm, fo, stream)
+        evs = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            node(fq, fk, fv, fm, fo, stream)
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        fms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        fbytes = nb * kvh * L * hs * 2 * 2 + 2 * nb * nq * heads * hs * 4 + (nq * L * 2 if causal else 0)
+        flops = 4.0 * nb * heads * nq * L * hs  # QK and PV over every key the kernel visits
+        fa[name] = {"batch": nb, "queries": nq, "keys": L, "heads": heads, "kv_heads": kvh, "head_size": hs,
+                    "causal_mask": causal, "bytes": fbytes, "us": round(fms * 1e3, 1),
+                    "gbs": round(fbytes / fms / 1e6, 1), "frac_of_hbm_peak": round(fbytes / fms / 1e6 / HBM_PEAK_GBS, 4),
+                    "tflops": round(flops / (fms * 1e-3) / 1e12, 1)}
+        log(f"  flash_attn_ext {name}: {fms * 1e3:8.1f} us  {fbytes / fms / 1e6:7.0f} GB/s  "
+            f"{flops / (fms * 1e-3) / 1e12:6.1f} TFLOP/s")
+        del fq, fk, fv, fm, fo, node
+    torch.cuda.empty_cache()
+
+    return attention, fa
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -418,6 +669,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["sweep", "floor", "prefill", "attention", "e2e"], default=None,
+                    help="run one part and print its JSON (for profiler runs); the default runs everything and "
+                         "prints the bench line")
     ap.add_argument("--e2e-only", action="store_true",
                     help="run only the end-to-end 8B decoder (configs[4]) and print its JSON")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -438,9 +692,20 @@ def main() -> int:
     log(f"device {props['name']} {props['arch']} CUs={props['compute_units']}")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
-    if args.e2e_only:
+    only = "e2e" if args.e2e_only else args.only
+    if only == "e2e":
         print(json.dumps(e2e_decoder(torch, gen, decode_steps=args.decode_steps,
                                      cpu_steps=0 if args.no_cpu else args.cpu_decode_steps)), flush=True)
+        return 0
+    if only == "floor":
+        print(json.dumps(gemv_vs_floor(torch, gen, torch.cuda.current_stream(), FLOOR_SHAPES)), flush=True)
+        return 0
+    if only == "prefill":
+        print(json.dumps(run_prefill(torch, gen, torch.cuda.current_stream())), flush=True)
+        return 0
+    if only == "attention":
+        att, fa = run_attention(torch, gen, torch.cuda.current_stream())
+        print(json.dumps({"paged_attention_decode": att, "flash_attn_ext": fa}), flush=True)
         return 0
 
     cases = [(t, M, K, n) for t in (N.Q4_0, N.Q4_K) for (M, K) in SHAPES for n in (1, 8)]
@@ -541,155 +806,21 @@ def main() -> int:
     q = lambda M, K: node_ms[(N.Q4_K, M, K, 1)]  # noqa: E731
     tok_ms = 32 * (q(6144, 4096) + q(4096, 4096) + 2 * q(14336, 4096) + q(4096, 14336)) + q(128256, 4096)
 
-    # prefill GEMM: q4_K 14336x4096 and 4096x14336, N = 512 / 2048, GEMM kernel
-    # alone (the activation quantization runs first as its own phase), rotated weights
-    prefill = []
-    for (M, K) in ((14336, 4096), (4096, 14336)):
-        base = gpu_blocks(torch, N.Q4_K, M, K, gen)
-        ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
-        for n in (512, 2048):
-            node = N.MulMat(N.Q4_K, M, K, n)
-            x = torch.randn((n, K), device="cuda", generator=gen)
-            y = torch.empty((n, M), dtype=torch.float32, device="cuda")
-            node.quantize(x, stream)
-            for i in range(2):
-                node.compute(ws[i % len(ws)], y, stream)
-            reps = 6
-            evs = []
-            for i in range(reps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                node.compute(ws[i % len(ws)], y, stream)
-                e1.record(stream)
-                evs.append((e0, e1))
-            # the whole MUL_MAT node: the Q8_K quantize launch, then the GEMM
-            nevs = []
-            for i in range(reps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                node(ws[i % len(ws)], x, y, stream)
-                e1.record(stream)
-                nevs.append((e0, e1))
-            torch.cuda.synchronize()
-            ms = sum(a.elapsed_time(b) for a, b in evs) / reps
-            node_ms_p = sum(a.elapsed_time(b) for a, b in nevs) / reps
-            tflops = 2.0 * M * n * K / (ms * 1e-3) / 1e12
-            node_tflops = 2.0 * M * n * K / (node_ms_p * 1e-3) / 1e12
-            prefill.append({"M": M, "K": K, "N": n, "us": round(ms * 1e3, 1), "tflops": round(tflops, 1),
-                            "frac_of_int8_mfma_peak": round(tflops / 5000.0, 4),
-                            "frac_of_f16_mfma_peak": round(tflops / 2500.0, 4),
-                            "node_us_incl_quantize": round(node_ms_p * 1e3, 1),
-                            "node_tflops": round(node_tflops, 1)})
-            log(f"  prefill q4_K {M}x{K} N={n}: GEMM {ms * 1e3:8.1f} us  {tflops:7.1f} TFLOP/s; node with its "
-                f"quantize launch {node_ms_p * 1e3:8.1f} us  {node_tflops:7.1f} TFLOP/s")
-        del ws, base
-    torch.cuda.empty_cache()
+    # the decode GEMV shapes cold, beside a plain streaming read of the same bytes
+    if only == "sweep":  # the sweep and its roofline kernel alone (for counter runs), then the copy scale
+        copy_scale_kernel(torch)
+        print(json.dumps({"value_gbs": round(value, 2), "roofline_kernel": dom_kernel, "us": round(dom_ms * 1e3, 2),
+                          "gbs": round(dom_gbs, 1)}), flush=True)
+        return 0
+    floor = gemv_vs_floor(torch, gen, stream, FLOOR_SHAPES)
 
-    # q6_K output projection (the lm_head of Q4_K_M files), 128256 x 4096, N = 1 and 8
-    q6 = []
-    base = gpu_blocks(torch, N.Q6_K, 128256, 4096, gen)
-    ws = [base] + [base.clone() for _ in range(max(1, math.ceil(ROTATE_BYTES / base.numel())) - 1)]
-    for n in (1, 8):
-        node = N.MulMat(N.Q6_K, 128256, 4096, n)
-        x = torch.randn((n, 4096), device="cuda", generator=gen)
-        y = torch.empty((n, 128256), dtype=torch.float32, device="cuda")
-        for i in range(2):
-            node(ws[i % len(ws)], x, y, stream)
-        evs = []
-        for i in range(10):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            node(ws[i % len(ws)], x, y, stream)
-            e1.record(stream)
-            evs.append((e0, e1))
-        torch.cuda.synchronize()
-        ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-        b = algorithmic_bytes(N.Q6_K, 128256, 4096, n)
-        q6.append({"M": 128256, "K": 4096, "N": n, "us": round(ms * 1e3, 1), "gbs": round(b / ms / 1e6, 1),
-                   "frac_of_hbm_peak": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)})
-        log(f"  q6_K  128256x4096  n={n}: {ms * 1e3:8.1f} us  {b / ms / 1e6:7.0f} GB/s")
-    del ws, base
-    torch.cuda.empty_cache()
-
-    # paged-attention decode: 32 sequences, 32 q / 8 kv heads, hs 128, 16-token
-    # pages scattered over a 65,536-page pool (2 GiB per cache), lens ~ U[512, 8192]
-    seqs, heads, kvh, hs, bs, pool = 32, 32, 8, 128, 16, 65536
-    lens = torch.randint(512, 8193, (seqs,), device="cuda", generator=gen, dtype=torch.int32)
-    maxb = 8192 // bs
-    kc = torch.randn((pool, kvh, hs // 8, bs, 8), device="cuda", generator=gen, dtype=torch.float16)
-    vc = torch.randn((pool, kvh, hs, bs), device="cuda", generator=gen, dtype=torch.float16)
-    tables = torch.randperm(pool, device="cuda", generator=gen)[: seqs * maxb].to(torch.int32).reshape(seqs, maxb)
-    qa = torch.randn((seqs, heads, hs), device="cuda", generator=gen, dtype=torch.float16)
-    oa = torch.empty_like(qa)
-    pa = N.PagedAttention(seqs, heads, kvh, hs, bs, maxb, 8192, hs ** -0.5)
-    lsum = int(lens.sum().item())
-    pages = int(((lens + bs - 1) // bs).sum().item())
-    attn_bytes = lsum * kvh * hs * 2 * 2 + 2 * seqs * heads * hs * 2 + pages * 4 + seqs * 4
-    for _ in range(2):
-        pa(oa, qa, kc, vc, tables, lens, stream)
-    evs = []
-    for _ in range(10):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        pa(oa, qa, kc, vc, tables, lens, stream)
-        e1.record(stream)
-        evs.append((e0, e1))
-    torch.cuda.synchronize()
-    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    attn_gbs = attn_bytes / attn_ms / 1e6
-    attention = {"seqs": seqs, "heads": heads, "kv_heads": kvh, "head_size": hs, "block_size": bs,
-                 "context_tokens": lsum, "bytes": attn_bytes, "us": round(attn_ms * 1e3, 1),
-                 "gbs": round(attn_gbs, 1), "frac_of_hbm_peak": round(attn_gbs / HBM_PEAK_GBS, 4)}
-    log(f"  paged attention {seqs} seqs, {lsum} tokens: {attn_ms * 1e3:8.1f} us  {attn_gbs:7.0f} GB/s")
-    del kc, vc
-    torch.cuda.empty_cache()
-
-    # dense FLASH_ATTN_EXT decode: the same 32 sequences x 32 q / 8 kv heads x 128 with a
-    # per-sequence f16 cache of 4096 keys (ggml k/v [128, 4096, 8, 32]), one query each;
-    # and a causal 512-token prefill of one sequence (q [128, 512, 32, 1], mask [512, 512])
-    fa = {}
-    for name, nb, nq, L, causal in (("decode", 32, 1, 4096, False), ("prefill_causal", 1, 512, 512, True)):
-        fq = torch.randn((nb, heads, nq, hs), device="cuda", generator=gen, dtype=torch.float32)
-        fk = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
-        fv = torch.randn((nb, kvh, L, hs), device="cuda", generator=gen, dtype=torch.float16)
-        fm = None
-        if causal:
-            fm = torch.full((nq, L), float("-inf"), device="cuda").triu(1 + L - nq).to(torch.float16)[None, None]
-            fm = fm.contiguous()
-        fo = torch.empty((nb, nq, heads, hs), device="cuda", dtype=torch.float32)
-        node = N.FlashAttnExt(fq, fk, fv, fm, fo, hs ** -0.5)
-        for _ in range(2):
-            node(fq, fk, fv, fm, fo, stream)
-        evs = []
-        for _ in range(10):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            node(fq, fk, fv, fm, fo, stream)
-            e1.record(stream)
-            evs.append((e0, e1))
-        torch.cuda.synchronize()
-        fms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-        fbytes = nb * kvh * L * hs * 2 * 2 + 2 * nb * nq * heads * hs * 4 + (nq * L * 2 if causal else 0)
-        flops = 4.0 * nb * heads * nq * L * hs  # QK and PV over every key the kernel visits
-        fa[name] = {"batch": nb, "queries": nq, "keys": L, "heads": heads, "kv_heads": kvh, "head_size": hs,
-                    "causal_mask": causal, "bytes": fbytes, "us": round(fms * 1e3, 1),
-                    "gbs": round(fbytes / fms / 1e6, 1), "frac_of_hbm_peak": round(fbytes / fms / 1e6 / HBM_PEAK_GBS, 4),
-                    "tflops": round(flops / (fms * 1e-3) / 1e12, 1)}
-        log(f"  flash_attn_ext {name}: {fms * 1e3:8.1f} us  {fbytes / fms / 1e6:7.0f} GB/s  "
-            f"{flops / (fms * 1e-3) / 1e12:6.1f} TFLOP/s")
-        del fq, fk, fv, fm, fo, node
-    torch.cuda.empty_cache()
-
+    prefill = run_prefill(torch, gen, stream)
+    q6 = run_q6_lm_head(torch, gen, stream)
+    attention, fa = run_attention(torch, gen, stream)
     e2e = e2e_decoder(torch, gen, decode_steps=args.decode_steps,
                       cpu_steps=0 if args.no_cpu else args.cpu_decode_steps)
 
-    # a plain device copy of known size (256 MiB), the scale for rocprof's FETCH_SIZE /
-    # WRITE_SIZE counters when profiles/ derive HBM traffic per launch
-    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
+    copy_scale_kernel(torch)
 
     # HBM bytes per launch of the roofline kernel, as measured by the rocprofv3 PMC runs
     # summarised in profiles/ (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size)
@@ -730,6 +861,7 @@ def main() -> int:
             "decode_tokens_per_s_8b_q4k_bs1": e2e["paged_bs1"]["decode_tokens_per_s"],
             "e2e_decoder_8b_q4k": e2e,
             "decode_tokens_per_s_8b_q4k_bs1_matmul_only": round(1e3 / tok_ms, 1),
+            "gemv_q4k_n1_cold_vs_read_floor": floor,
             "prefill_gemm_q4k": prefill,
             "gemv_q6k_lm_head": q6,
             "paged_attention_decode": attention,

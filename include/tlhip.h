@@ -361,6 +361,17 @@ tlh_status tlh_program_compile(const tlh_ir_tensor *tensors, int32_t n_tensors, 
 tlh_status tlh_program_destroy(tlh_program *p);
 /* Stream-ordered copy between any two device (or pinned host) addresses. */
 tlh_status tlh_copy(void *dst, const void *src, size_t bytes, void *stream);
+/* Stream-ordered fill of `bytes` device bytes at dst with the low 8 bits of
+   `value`, by a kernel (so it may be captured in a hipGraph). Replaces the
+   CUDA backend's cuMemsetD8Async zero fill (Backend::zero,
+   crates/kernels/src/cuda/backend.rs:334-343). */
+tlh_status tlh_memset(void *dst, int value, size_t bytes, void *stream);
+/* No counterpart in the reference: a plain streaming read of `bytes` bytes
+   (16-byte aligned; `grid` workgroups of 256 lanes, `loads` = 1 or 4 16-byte
+   loads in flight per lane) that writes nothing. For measurement only: the
+   floor a kernel that must read the same bytes cannot beat, timed beside the
+   GEMVs by bench.py. */
+tlh_status tlh_read_floor(const void *src, size_t bytes, int32_t grid, int32_t loads, void *stream);
 /* Device address and byte size of graph input i in the io buffer. */
 tlh_status tlh_program_input(const tlh_program *p, int32_t i, void **ptr, size_t *bytes);
 /* Device address of tensor `id` (any storage; `state` is the run's state buffer). */

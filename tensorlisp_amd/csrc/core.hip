@@ -14,6 +14,8 @@
 // with consecutive threads on consecutive elements, so contiguous rows are
 // read and written in full cache lines; reductions (norms, softmax, argmax)
 // give each row one workgroup and reduce in registers, then across waves.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 // The CPU backend rounds every product and sum (its x86-64 build has no FMA);
@@ -897,6 +899,65 @@ tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, con
     else
         hipLaunchKernelGGL(k_norm_chain<false>, red_grid(rows), dim3(256), 0, stream, a);
     return check_launch("norm_chain");
+}
+
+// ------------------------------------------------------------------- fill
+// bytes of dst set to one value by a kernel (a caller may capture it in a
+// hipGraph, where memset nodes are avoided): 16-byte stores from the first
+// aligned address, single bytes before and after it
+__global__ void __launch_bounds__(256) k_fill_bytes(uint8_t *__restrict__ dst, uint64_t n, uint32_t v8) {
+    const uint64_t head = (16 - ((uintptr_t)dst & 15)) & 15;
+    const uint64_t h = head < n ? head : n;
+    const uint64_t body = (n - h) / 16;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t w = v8 * 0x01010101u;
+    uint4 *b = (uint4 *)(dst + h);
+    for (uint64_t i = t; i < body; i += stride) b[i] = make_uint4(w, w, w, w);
+    const uint64_t tail0 = h + 16 * body;
+    if (t < h) dst[t] = (uint8_t)v8;
+    if (t < n - tail0) dst[tail0 + t] = (uint8_t)v8;
+}
+
+tlh_status launch_fill(void *dst, int value, size_t bytes, hipStream_t stream) {
+    const uint64_t chunks = bytes / 16 + 1;
+    const uint64_t blocks = std::min<uint64_t>((chunks + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_fill_bytes, dim3((unsigned)blocks), dim3(256), 0, stream, (uint8_t *)dst, (uint64_t)bytes,
+                       (uint32_t)(value & 0xff));
+    return check_launch("fill");
+}
+
+// -------------------------------------------------------------- read floor
+// A plain streaming read of `bytes` bytes (16-byte loads, U per lane in
+// flight, grid-stride), XOR-folded into a value that is stored only if it
+// matches an impossible pattern: the bandwidth / latency floor a kernel
+// that must read the same bytes cannot beat.
+__device__ unsigned g_read_sink;
+template <int U>
+__global__ void __launch_bounds__(256) k_read_floor(const uint4 *__restrict__ p, uint64_t n16) {
+    uint64_t i = (uint64_t)blockIdx.x * 256 * U + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * 256 * U;
+    unsigned acc = 0;
+    for (; i < n16; i += stride) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + (uint64_t)u * 256;
+            v[u] = j < n16 ? p[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u && threadIdx.x == 0x3ff) g_read_sink = acc;
+}
+
+tlh_status launch_read_floor(const void *src, size_t bytes, int grid, int loads, hipStream_t stream) {
+    const uint64_t n16 = bytes / 16;
+    if (loads == 4)
+        hipLaunchKernelGGL(k_read_floor<4>, dim3((unsigned)grid), dim3(256), 0, stream, (const uint4 *)src, n16);
+    else
+        hipLaunchKernelGGL(k_read_floor<1>, dim3((unsigned)grid), dim3(256), 0, stream, (const uint4 *)src, n16);
+    return check_launch("read_floor");
 }
 
 }  // namespace tlh

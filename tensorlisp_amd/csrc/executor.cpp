@@ -1730,6 +1730,20 @@ tlh_status tlh_copy(void *dst, const void *src, size_t bytes, void *stream) {
     return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, (hipStream_t)stream), "copy");
 }
 
+tlh_status tlh_memset(void *dst, int value, size_t bytes, void *stream) {
+    if (!bytes) return TLH_OK;
+    if (!dst) return set_error(TLH_INVALID, "memset: null pointer");
+    return launch_fill(dst, value, bytes, (hipStream_t)stream);
+}
+
+tlh_status tlh_read_floor(const void *src, size_t bytes, int32_t grid, int32_t loads, void *stream) {
+    if (!src || (uintptr_t)src % 16 || bytes % 16) return set_error(TLH_INVALID, "read_floor: 16-byte aligned bytes");
+    if (grid < 1 || grid > 65536 || (loads != 1 && loads != 4))
+        return set_error(TLH_INVALID, "read_floor: grid 1..65536, 1 or 4 loads per lane");
+    if (!bytes) return TLH_OK;
+    return launch_read_floor(src, bytes, grid, loads, (hipStream_t)stream);
+}
+
 tlh_status tlh_program_input(const tlh_program *p, int32_t i, void **ptr, size_t *bytes) {
     if (!p || !ptr) return set_error(TLH_INVALID, "program_input: null pointer");
     if (i < 0 || i >= (int32_t)p->inputs.size()) return set_error(TLH_INVALID, "program_input: no graph input %d", i);

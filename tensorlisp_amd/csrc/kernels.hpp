@@ -182,6 +182,8 @@ tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void 
 // ROPE) in one launch; srcs[k] = s0, s1, s2 and, for a ROPE whose op has x9 =
 // 1, the row index of each token (the result goes to those rows of the dst).
 bool core_multi_kind(int kind);
+tlh_status launch_fill(void *dst, int value, size_t bytes, hipStream_t stream);
+tlh_status launch_read_floor(const void *src, size_t bytes, int grid, int loads, hipStream_t stream);
 tlh_status launch_core_multi(int n, const int *kinds, const tlh_op *ops, const void *const (*srcs)[4],
                              void *const *dsts, hipStream_t stream);
 tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s1, const void *s2, void *dst,

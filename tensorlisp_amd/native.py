@@ -33,7 +33,9 @@ EXPORTS = (
     "tlh_mul_mat_noalloc", "tlh_mul_mat_quantize", "tlh_mul_mat_compute", "tlh_mul_mat_id_scratch_bytes", "tlh_mul_mat_id",
     "tlh_quantize_act", "tlh_dequantize", "tlh_flash_attn_ext_scratch_bytes", "tlh_flash_attn_ext",
     "tlh_paged_attention_scratch_bytes", "tlh_paged_attention", "tlh_reshape_and_cache",
-    "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_program_input",
+    "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_memset",
+    "tlh_read_floor",
+    "tlh_program_input",
     "tlh_program_tensor", "tlh_program_run", "tlh_program_stats", "tlh_program_plan",
     "tlh_gguf_open", "tlh_gguf_close", "tlh_gguf_counts", "tlh_gguf_tensor", "tlh_gguf_find_tensor",
     "tlh_gguf_find_key", "tlh_gguf_key", "tlh_gguf_value", "tlh_gguf_string", "tlh_gguf_layout", "tlh_gguf_upload",
@@ -109,6 +111,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
                                       C.c_int32, i64p, C.c_int32, C.POINTER(C.c_void_p)]
     L.tlh_program_destroy.argtypes = [vp]
     L.tlh_copy.argtypes = [vp, vp, C.c_size_t, vp]
+    L.tlh_memset.argtypes = [vp, C.c_int, C.c_size_t, vp]
+    L.tlh_read_floor.argtypes = [vp, C.c_size_t, C.c_int32, C.c_int32, vp]
     L.tlh_program_input.argtypes = [vp, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
     L.tlh_program_tensor.argtypes = [vp, C.c_int32, vp, C.POINTER(C.c_void_p)]
     L.tlh_program_run.argtypes = [vp, vp, vp, C.c_int32]
@@ -268,6 +272,13 @@ def quantize_act(wtype: int, x, stream=None):
     out = torch.empty((rows, row_bytes(VEC_DOT_TYPE[wtype], k)), dtype=torch.uint8, device=x.device)
     check(lib().tlh_quantize_act(wtype, _ptr(x), k, rows, x.stride(0) * 4, _ptr(out), _stream(stream)))
     return out
+
+
+def memset(t, value: int, nbytes: int = None, offset: int = 0, stream=None) -> None:
+    """Fill `nbytes` bytes of device tensor t (from byte `offset`; all of it by
+    default) with the low 8 bits of value, on `stream` (tlh_memset)."""
+    n = t.numel() * t.element_size() - offset if nbytes is None else nbytes
+    check(lib().tlh_memset(C.c_void_p(t.data_ptr() + offset), int(value), n, _stream(stream)))
 
 
 def dequantize(wtype: int, w, k: int, stream=None):

@@ -31,6 +31,17 @@ def test_library_exports_every_declared_symbol():
     assert sorted(N.EXPORTS) == decl
 
 
+def test_integration_binding_lists_every_declaration():
+    """The reference-side FFI block a maintainer would add (INTEGRATION.md's
+    `extern "C"` block) names every function the header declares, once."""
+    text = (HEADER.parents[1] / "INTEGRATION.md").read_text()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    bound = re.findall(r"pub fn (tlh_[a-z0-9_]+)\(", block)
+    assert len(bound) == len(set(bound)), sorted(f for f in bound if bound.count(f) > 1)
+    assert sorted(bound) == declared_functions()
+
+
 def test_descriptor_layout():
     assert C.sizeof(N.TlhTensor) == 72
     assert C.sizeof(N.TlhOp) == 5 * 72 + 12 * 8  # OP_BYTES of lower.rs:67
