@@ -829,7 +829,7 @@ def main() -> int:
     if tfile.exists():
         for ln in tfile.read_text().splitlines():
             key, _, val = ln.partition("=")
-            if key.strip() == "gemv_q4_K_128256x4096_n1_bytes" and val.strip().isdigit():
+            if key.strip() == f"gemv_{N.TYPE_NAMES[dt]}_{dM}x{dK}_n{dn}_bytes" and val.strip().isdigit():
                 traffic = int(val.strip())
 
     cpu = None
