@@ -9,13 +9,15 @@
 // contiguous load; for larger K, KSPLIT (2 or 4) waves of a workgroup take
 // contiguous K ranges of the same rows and merge their partials through LDS.
 //
-// FUSED: every wave quantizes its own activation slice in registers
-// from the f32 input (the rules of quantize_row_q8_0_ref, ggml-quants.c:276-297,
-// and quantize_row_q8_K_ref, :2768-2804; a q8_K super-block is 4 lanes, which
-// agree on its signed maximum with two butterflies), so a decode MUL_MAT is
-// one launch and no workgroup waits on a barrier before its first weight
-// load. Otherwise the codes come from the split scratch a quantize launch
-// wrote.
+// In-kernel activations (IN_X, IN_XL, IN_NORM): each workgroup loads its
+// activation column(s), requests its first weights, then quantizes the column
+// once into LDS with the rules of quantize_row_q8_0_ref (ggml-quants.c:276-297)
+// and quantize_row_q8_K_ref (:2768-2804), so a decode MUL_MAT is one launch.
+// IN_NORM forms the column from the executor's [ADD ->] RMS_NORM -> MUL chain
+// first. IN_SCRATCH reads the split scratch a quantize launch wrote. The
+// outputs leave as f32 rows (OUT_STORE), as SwiGLU of gate / up row pairs
+// (OUT_GLU) or through the store epilogue (OUT_EPI: RoPE, f16, cache rows,
+// paged pools).
 //
 // Block products follow the CPU's vec_dot (ggml-cpu/quants.c:225-258,
 // :451-476, :696-773): exact int32 sums on v_dot4, scaled in f32.
