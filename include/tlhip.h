@@ -51,7 +51,8 @@ enum {
     TLH_TYPE_Q6_K = 14,
     TLH_TYPE_Q8_K = 15,
     TLH_TYPE_I32 = 26,
-    TLH_TYPE_I64 = 27
+    TLH_TYPE_I64 = 27,
+    TLH_TYPE_BF16 = 30
 };
 
 /* Thread-local text of the last failure on this thread ("" if none). */
@@ -107,9 +108,11 @@ typedef struct tlh_op {
  * GGML_OP_MUL_MAT, replacing Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
  * and its mm_vec / mm_tile kernels (crates/kernels/src/cuda/native/mm.cu:16-103),
  * computed the way the ggml CPU backend does (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457):
- *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K | Q5_K | Q6_K, ne [K, M, ne02, ne03],
- *                  nb[0] = block bytes (rows must not be transposed);
- *   op->t[1] src1: f32 activations, ne [K, N, ne12, ne13], nb[0] = 4;
+ *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K | Q5_K | Q6_K | F32 | F16 | BF16,
+ *                  ne [K, M, ne02, ne03], nb[0] = block (element) bytes (rows must
+ *                  not be transposed);
+ *   op->t[1] src1: f32 activations (or, for F16 / BF16 weights, already of the
+ *                  weight type), ne [K, N, ne12, ne13], nb[0] = element bytes;
  *   op->t[4] dst:  f32 [M, N, ne12, ne13], nb[0] = 4;
  *   op->x[0] = r2 = ne12 / ne02, op->x[1] = r3 = ne13 / ne03 (broadcast).
  * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0 and
@@ -117,8 +120,12 @@ typedef struct tlh_op {
  * then N <= 16 runs the decode GEMV (register kernel for N <= 2, int8-MFMA
  * few-column kernel above), larger N the MFMA GEMM. Integer block
  * sums are exact; the f32 result agrees with the CPU backend to rounding of
- * the f32 accumulation order. TLH_UNSUPPORTED (with the reason in
- * tlh_last_error) for any other type or layout. */
+ * the f32 accumulation order. F32 / F16 / BF16 weights follow the CPU's float
+ * rows (ggml-cpu.c:215-226, :394-399): src1 rounded to the weight type, f32
+ * products summed in f32, one launch (tlh_mul_mat_scratch_bytes still counts
+ * the converted src1 rows, which only the split form below writes).
+ * TLH_UNSUPPORTED (with the reason in tlh_last_error) for any
+ * other type or layout. */
 tlh_status tlh_mul_mat_scratch_bytes(const tlh_op *op, size_t *bytes);
 tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, void *dst, void *scratch,
                        size_t scratch_bytes, void *stream);

@@ -19,7 +19,7 @@ enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q5_K_B = 17
 
 int64_t tlq_block_elems(int type) {
     switch (type) {
-    case TLQ_F32: case TLQ_F16: return 1;
+    case TLQ_F32: case TLQ_F16: case TLQ_BF16: return 1;
     case TLQ_Q4_0: case TLQ_Q8_0: return QK32;
     case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
     default: return 0;
@@ -29,7 +29,7 @@ int64_t tlq_block_elems(int type) {
 int64_t tlq_block_bytes(int type) {
     switch (type) {
     case TLQ_F32: return 4;
-    case TLQ_F16: return 2;
+    case TLQ_F16: case TLQ_BF16: return 2;
     case TLQ_Q4_0: return Q4_0_B;
     case TLQ_Q8_0: return Q8_0_B;
     case TLQ_Q4_K: return Q4_K_B;
@@ -49,6 +49,7 @@ int tlq_vec_dot_type(int wtype) {
     switch (wtype) {
     case TLQ_Q4_0: case TLQ_Q8_0: return TLQ_Q8_0;
     case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: return TLQ_Q8_K;
+    case TLQ_F32: case TLQ_F16: case TLQ_BF16: return wtype;
     default: return -1;
     }
 }
@@ -103,6 +104,15 @@ void tlq_fp16_to_fp32_row(const uint16_t *h, float *f, int64_t n) {
 
 void tlq_fp32_to_fp16_row(const float *f, uint16_t *h, int64_t n) {
     for (int64_t i = 0; i < n; ++i) h[i] = tlq_fp32_to_fp16(f[i]);
+}
+
+// ggml-impl.h:590-624
+float tlq_bf16_to_fp32(uint16_t h) { return bitsf((uint32_t)h << 16); }
+
+uint16_t tlq_fp32_to_bf16(float f) {
+    const uint32_t u = fbits(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
 // Round to nearest, ties to even, for |v| < 2^22: what ggml's nearest_int
@@ -329,6 +339,11 @@ int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k) {
     switch (tlq_vec_dot_type(wtype)) {
     case TLQ_Q8_0: tlq_quantize_row_q8_0(x, y, k); return 0;
     case TLQ_Q8_K: tlq_quantize_row_q8_K(x, y, k); return 0;
+    case TLQ_F32: memcpy(y, x, (size_t)k * 4); return 0;
+    case TLQ_F16: tlq_fp32_to_fp16_row(x, (uint16_t *)y, k); return 0;
+    case TLQ_BF16:
+        for (int64_t i = 0; i < k; ++i) ((uint16_t *)y)[i] = tlq_fp32_to_bf16(x[i]);
+        return 0;
     default: return -1;
     }
 }
@@ -583,6 +598,29 @@ float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *vx, const void *vy) {
     return sumf;
 }
 
+// ------------------------------------------------------ float dot products
+// vec.cpp:11-143 / :139-262 / :264-352 without GGML_SIMD: f32 products, double sum.
+float tlq_vec_dot_f32(int64_t k, const void *vx, const void *vy) {
+    const float *x = (const float *)vx, *y = (const float *)vy;
+    double s = 0.0;
+    for (int64_t i = 0; i < k; ++i) s += (double)(x[i] * y[i]);
+    return (float)s;
+}
+
+float tlq_vec_dot_f16(int64_t k, const void *vx, const void *vy) {
+    const uint16_t *x = (const uint16_t *)vx, *y = (const uint16_t *)vy;
+    double s = 0.0;
+    for (int64_t i = 0; i < k; ++i) s += (double)(tlq_fp16_to_fp32(x[i]) * tlq_fp16_to_fp32(y[i]));
+    return (float)s;
+}
+
+float tlq_vec_dot_bf16(int64_t k, const void *vx, const void *vy) {
+    const uint16_t *x = (const uint16_t *)vx, *y = (const uint16_t *)vy;
+    double s = 0.0;
+    for (int64_t i = 0; i < k; ++i) s += (double)(tlq_bf16_to_fp32(x[i]) * tlq_bf16_to_fp32(y[i]));
+    return (float)s;
+}
+
 // -------------------------------------------------------------- mul_mat
 typedef float (*dot_fn)(int64_t, const void *, const void *);
 
@@ -612,6 +650,9 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
     case TLQ_Q5_K: dot = tlq_vec_dot_q5_K_q8_K; break;
     case TLQ_Q6_K: dot = tlq_vec_dot_q6_K_q8_K; break;
+    case TLQ_F32: dot = tlq_vec_dot_f32; break;
+    case TLQ_F16: dot = tlq_vec_dot_f16; break;
+    case TLQ_BF16: dot = tlq_vec_dot_bf16; break;
     default: return -1;
     }
     const int at = tlq_vec_dot_type(wtype);
@@ -770,18 +811,19 @@ int tlq_flash_attn_ext(const void *q, const int64_t q_ne[4], const int64_t q_nb[
 
 // ------------------------------------------------------------ core ops
 // The ggml CPU backend's ops around MUL_MAT in a decoder step, on ggml tensors
-// given as (data, ne[4], nb[4], type). f32/f16 data, i32/i64 indices.
+// given as (data, ne[4], nb[4], type). f32/f16/bf16 data, i32/i64 indices.
 static float t_ld(const tlq_t *t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
     const char *p = (const char *)t->data + i0 * t->nb[0] + i1 * t->nb[1] + i2 * t->nb[2] + i3 * t->nb[3];
     if (t->ty == TLQ_F16) return tlq_fp16_to_fp32(rd16((const uint8_t *)p));
+    if (t->ty == TLQ_BF16) return tlq_bf16_to_fp32(rd16((const uint8_t *)p));
     float f;
     memcpy(&f, p, 4);
     return f;
 }
 static void t_st(const tlq_t *t, int64_t i0, int64_t i1, int64_t i2, int64_t i3, float v) {
     char *p = (char *)t->data + i0 * t->nb[0] + i1 * t->nb[1] + i2 * t->nb[2] + i3 * t->nb[3];
-    if (t->ty == TLQ_F16) {
-        const uint16_t h = tlq_fp32_to_fp16(v);
+    if (t->ty == TLQ_F16 || t->ty == TLQ_BF16) {
+        const uint16_t h = t->ty == TLQ_F16 ? tlq_fp32_to_fp16(v) : tlq_fp32_to_bf16(v);
         memcpy(p, &h, 2);
     } else {
         memcpy(p, &v, 4);
@@ -917,7 +959,7 @@ void tlq_core_get_rows(const tlq_t *a, const tlq_t *idx, const tlq_t *d) {
     FOR4(d) {
         const int64_t r = t_idx(idx, i1, i2, i3);
         const char *row = (const char *)a->data + r * a->nb[1] + i2 * a->nb[2] + i3 * a->nb[3];
-        if (a->ty == TLQ_F32 || a->ty == TLQ_F16) {
+        if (a->ty == TLQ_F32 || a->ty == TLQ_F16 || a->ty == TLQ_BF16) {
             for (int64_t i = 0; i < d->ne[0]; ++i) {
                 tlq_t one = *a;
                 one.data = (void *)row;
@@ -945,7 +987,7 @@ void tlq_core_cpy(const tlq_t *a, const tlq_t *d) {
     int64_t k = 0;
     FOR4(a) {
         const char *row = (const char *)a->data + i1 * a->nb[1] + i2 * a->nb[2] + i3 * a->nb[3];
-        if (a->ty == TLQ_F32 || a->ty == TLQ_F16) {
+        if (a->ty == TLQ_F32 || a->ty == TLQ_F16 || a->ty == TLQ_BF16) {
             tlq_t one = *a;
             one.data = (void *)row;
             for (int64_t i = 0; i < a->ne[0]; ++i) tmp[i] = t_ld(&one, i, 0, 0, 0);

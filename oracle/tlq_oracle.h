@@ -29,14 +29,16 @@ enum {
     TLQ_Q5_K = 13,
     TLQ_Q6_K = 14,
     TLQ_Q8_K = 15,
+    TLQ_BF16 = 30,
 };
 
 // Block geometry, vendor/ggml/src/ggml-common.h:89-90,194-198,251-255,325-337,370-375.
 int64_t tlq_block_elems(int type);
 int64_t tlq_block_bytes(int type);
 int64_t tlq_row_bytes(int type, int64_t k);
-// vec_dot_type of a weight type on x86 (ggml-cpu.c:239-319): Q8_0 for Q4_0
-// and Q8_0 weights, Q8_K for Q4_K; -1 otherwise.
+// vec_dot_type of a weight type on x86 (ggml-cpu.c:215-226,239-319,394-399):
+// Q8_0 for Q4_0 and Q8_0 weights, Q8_K for the K-quants, the weight type
+// itself for F32 / F16 / BF16; -1 otherwise.
 int tlq_vec_dot_type(int wtype);
 
 // IEEE binary16 <-> binary32 (round to nearest even), the semantics of
@@ -45,6 +47,10 @@ float tlq_fp16_to_fp32(uint16_t h);
 uint16_t tlq_fp32_to_fp16(float f);
 void tlq_fp16_to_fp32_row(const uint16_t *h, float *f, int64_t n);
 void tlq_fp32_to_fp16_row(const float *f, uint16_t *h, int64_t n);
+// bfloat16 <-> binary32: ggml_compute_bf16_to_fp32 / ggml_compute_fp32_to_bf16
+// (ggml-impl.h:590-624): round to nearest even, NaN kept and made quiet.
+float tlq_bf16_to_fp32(uint16_t h);
+uint16_t tlq_fp32_to_bf16(float f);
 
 // Weight quantizers (offline, host only; ggml_quantize_chunk with imatrix NULL):
 // quantize_row_q4_0_ref ggml-quants.c:113-147, quantize_row_q8_0_ref :276-297,
@@ -58,7 +64,9 @@ void tlq_quantize_row_q4_K(const float *x, void *y, int64_t k);
 // ggml-quants.c:2768-2804).
 void tlq_quantize_row_q8_0(const float *x, void *y, int64_t k);
 void tlq_quantize_row_q8_K(const float *x, void *y, int64_t k);
-// Quantize one activation row into the weight type's vec_dot type.
+// Quantize one activation row into the weight type's vec_dot type (for F32 /
+// F16 / BF16 weights: from_float = copy / ggml_cpu_fp32_to_fp16 /
+// ggml_cpu_fp32_to_bf16, ggml-cpu.c:3531-3536).
 int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k);
 
 // Dequantizers: dequantize_row_q4_0 ggml-quants.c:459-476, _q8_0 :553-565,
@@ -85,10 +93,19 @@ float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *x, const void *y);
 // q4_K: *sum_q = sum_s sc_s * sum_{e in s} q4_e*q8_e, *sum_m = sum_s m_s * sum_{e in s} q8_e.
 void tlq_block_ints_q4_K(const void *x_block, const void *y_block, int32_t *sum_q, int32_t *sum_m);
 
+// Dot products of float rows as an x86-64 build without -march compiles them
+// (no GGML_SIMD): each product in f32, the sum in double, rounded to f32 once
+// (ggml_vec_dot_f32 vec.cpp:11-143 scalar branch, ggml_vec_dot_bf16
+// :139-262 tail loop, ggml_vec_dot_f16 :264-352 scalar branch).
+float tlq_vec_dot_f32(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_f16(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_bf16(int64_t k, const void *x, const void *y);
+
 // GGML_OP_MUL_MAT on the CPU backend's algorithm (ggml-cpu.c:1254-1457 with
 // the one-chunk loop :1164-1252): quantize every activation column to the
 // vec_dot type, then y[n*M + m] = vec_dot(W row m, column n). `nthreads`
-// splits rows; the result does not depend on it.
+// splits rows; the result does not depend on it. Weights of F32 / F16 / BF16
+// take the float dot products above on src1 converted to the weight type.
 int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, int64_t N, float *y,
                 int nthreads);
 

@@ -47,6 +47,14 @@ __host__ __device__ constexpr int vec_dot_type(int wtype) {
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // v_cvt_f16_f32: round to nearest even, f16 denormals kept (kernel default mode).
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// bf16: the upper half of an f32; f32 -> bf16 rounds to nearest even and keeps
+// a NaN a (quiet) NaN
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
 
 // q4_K packed 6-bit scale/min of sub-block j from the 12-byte field
 // (ggml-quants.c:880-887), given the field as three little-endian words.

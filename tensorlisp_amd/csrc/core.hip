@@ -27,11 +27,15 @@ namespace tlh {
 constexpr int CORE_I32 = 26, CORE_I64 = 27;
 
 __device__ __forceinline__ float ld_f(const char *p, int ty) {
-    return ty == TLH_TYPE_F16 ? h2f(*(const uint16_t *)p) : *(const float *)p;
+    return ty == TLH_TYPE_F16    ? h2f(*(const uint16_t *)p)
+           : ty == TLH_TYPE_BF16 ? bf16_to_f32(*(const uint16_t *)p)
+                                 : *(const float *)p;
 }
 __device__ __forceinline__ void st_f(char *p, int ty, float v) {
     if (ty == TLH_TYPE_F16)
         *(uint16_t *)p = f2h(v);
+    else if (ty == TLH_TYPE_BF16)
+        *(uint16_t *)p = f32_to_bf16(v);  // ggml_compute_fp32_to_bf16's rounding
     else
         *(float *)p = v;
 }
@@ -189,7 +193,7 @@ __global__ void __launch_bounds__(256) k_core_get_rows(const CoreArgs a) {
         const int64_t i0 = e0 + 256 * u;
         if (i0 >= d.ne[0]) break;
         float v;
-        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16)
+        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16 || ST == TLH_TYPE_BF16)
             v = ld_f(xr + i0 * x.nb[0], ST);
         else
             v = dequant_elem<ST>((const uint8_t *)xr, i0);
@@ -239,7 +243,7 @@ __global__ void __launch_bounds__(256) k_core_cpy(const CoreArgs a) {
         const int64_t i0 = e0 + 256 * u;
         if (i0 >= x.ne[0]) break;
         float v;
-        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16)
+        if constexpr (ST == TLH_TYPE_F32 || ST == TLH_TYPE_F16 || ST == TLH_TYPE_BF16)
             v = ld_f(xr + i0 * x.nb[0], ST);
         else
             v = dequant_elem<ST>((const uint8_t *)xr, i0);
@@ -605,6 +609,7 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         switch (x.ty) {
         case TLH_TYPE_F32: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_F32>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_BF16: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_BF16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
@@ -627,6 +632,7 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         switch (x.ty) {
         case TLH_TYPE_F32: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_F32>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_BF16: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_BF16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;

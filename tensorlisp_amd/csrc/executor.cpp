@@ -1170,8 +1170,8 @@ class Lowering {
     // that lives until the last has run. A node that writes into the
     // activation's storage in between ends the group.
     void group_mul_mats(std::vector<Dispatch> &d) {
-        using Key = std::tuple<int, int32_t, int64_t, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                               int64_t>;
+        using Key = std::tuple<int, int32_t, int64_t, int, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                               int64_t, int64_t>;
         std::map<Key, int> open;  // key -> index of the group's first dispatch
         std::vector<Dispatch> out;
         out.reserve(d.size() * 2);
@@ -1186,8 +1186,8 @@ class Lowering {
             }
             if (x.kind != D_MUL_MAT || x.op.t[1].ne[1] <= 2) continue;
             const tlh_tensor &b = x.op.t[1];
-            const Key k{x.src[1].buf, x.src[1].index, x.src[1].off, x.op.t[0].ty, b.ne[0], b.ne[1], b.ne[2], b.ne[3],
-                        b.nb[1], b.nb[2], b.nb[3], x.op.t[0].ne[2]};
+            const Key k{x.src[1].buf, x.src[1].index, x.src[1].off, x.op.t[0].ty, b.ty, b.ne[0], b.ne[1], b.ne[2],
+                        b.ne[3], b.nb[1], b.nb[2], b.nb[3], x.op.t[0].ne[2]};
             auto it = open.find(k);
             if (it == open.end()) {
                 open[k] = (int)i;

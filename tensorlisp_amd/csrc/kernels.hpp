@@ -182,6 +182,22 @@ tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void 
 // ROPE) in one launch; srcs[k] = s0, s1, s2 and, for a ROPE whose op has x9 =
 // 1, the row index of each token (the result goes to those rows of the dst).
 bool core_multi_kind(int kind);
+// MUL_MAT with f32 / f16 / bf16 weights (mm_float.hip): w rows of wtype
+// (w_nb* byte strides), x rows of xtype (f32, or already the weight type),
+// f32 outputs; batch slice (i12, i13) reads weight slice (i12 / r2, i13 / r3).
+struct FloatMM {
+    int wtype, xtype;
+    const char *w;
+    int64_t w_nb1, w_nb2, w_nb3;
+    const char *x;
+    int64_t x_nb1, x_nb2, x_nb3;
+    float *d;
+    int64_t d_nb1, d_nb2, d_nb3;
+    int64_t M, K, N, ne12, ne13, r2, r3;
+};
+tlh_status launch_mm_float(const FloatMM &f, hipStream_t stream);
+// x rows -> contiguous rows of the weight type at out (out_row bytes apart)
+tlh_status launch_mm_float_convert(const FloatMM &f, void *out, int64_t out_row, hipStream_t stream);
 tlh_status launch_fill(void *dst, int value, size_t bytes, hipStream_t stream);
 tlh_status launch_read_floor(const void *src, size_t bytes, int grid, int loads, hipStream_t stream);
 tlh_status launch_core_multi(int n, const int *kinds, const tlh_op *ops, const void *const (*srcs)[4],

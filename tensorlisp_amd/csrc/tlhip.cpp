@@ -69,15 +69,23 @@ static const char *type_name(int t) {
 struct MulMatShape {
     int64_t K, M, N, ne12, ne13, r2, r3, act_rows;
     int wtype, act_type;
+    bool flt = false;  // f32 / f16 / bf16 weights (mm_float.hip)
 };
+
+static bool float_type(int t) { return t == TLH_TYPE_F32 || t == TLH_TYPE_F16 || t == TLH_TYPE_BF16; }
+static int float_size(int t) { return t == TLH_TYPE_F32 ? 4 : 2; }
 
 static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     if (!op) return set_error(TLH_INVALID, "mul_mat: null op");
     const tlh_tensor &a = op->t[0], &b = op->t[1], &d = op->t[4];
-    if (!weight_type_ok(a.ty))
-        return set_error(TLH_UNSUPPORTED, "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K", a.ty,
+    s.flt = float_type(a.ty);
+    if (!weight_type_ok(a.ty) && !s.flt)
+        return set_error(TLH_UNSUPPORTED,
+                         "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K, f32, f16, bf16", a.ty,
                          type_name(a.ty));
-    if (b.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: activations must be f32 (got type %d)", b.ty);
+    // src1 is f32, or (ggml's vec_dot_type rule) already the f16 / bf16 of f16 / bf16 weights
+    if (b.ty != TLH_TYPE_F32 && !(s.flt && a.ty != TLH_TYPE_F32 && b.ty == a.ty))
+        return set_error(TLH_UNSUPPORTED, "mul_mat: activations of type %d with weights of type %d", b.ty, a.ty);
     if (d.ty != TLH_TYPE_F32) return set_error(TLH_UNSUPPORTED, "mul_mat: the destination must be f32");
     for (int i = 0; i < 4; ++i)
         if (a.ne[i] < 0 || b.ne[i] < 0 || d.ne[i] < 0) return set_error(TLH_INVALID, "mul_mat: negative extent");
@@ -96,6 +104,19 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     if ((op->x[0] != 0 && op->x[0] != s.r2) || (op->x[1] != 0 && op->x[1] != s.r3))
         return set_error(TLH_INVALID, "mul_mat: broadcast factors x[0]=%lld x[1]=%lld disagree with the shapes",
                          (long long)op->x[0], (long long)op->x[1]);
+    if (s.flt) {  // element rows: any strides that keep elements aligned
+        const int64_t ea = float_size(a.ty), eb = float_size(b.ty);
+        if (a.nb[0] != ea || b.nb[0] != eb)
+            return set_error(TLH_UNSUPPORTED, "mul_mat: rows must be contiguous (nb0 = element size)");
+        for (int i = 1; i < 4; ++i)
+            if (a.nb[i] % ea || b.nb[i] % eb) return set_error(TLH_INVALID, "mul_mat: strides not element-aligned");
+        if (d.nb[0] != 4 || (d.nb[1] & 3) || (d.nb[2] & 3) || (d.nb[3] & 3))
+            return set_error(TLH_UNSUPPORTED, "mul_mat: dst must be f32 with unit element stride");
+        s.wtype = a.ty;
+        s.act_type = a.ty;
+        s.act_rows = s.N * s.ne12 * s.ne13;
+        return TLH_OK;
+    }
     const int be = block_elems(a.ty);
     if (s.K % be != 0)
         return set_error(TLH_UNSUPPORTED, "mul_mat: K=%lld is not a multiple of the %s block (%d)", (long long)s.K,
@@ -189,7 +210,7 @@ static tlh_status check_flash_attn(const tlh_op *op, bool has_mask, FlashAttnDes
 // (crates/kernels/src/cuda/lower.rs:175-500) refuse nodes, narrowed to what
 // core.hip runs: f32/f16 data, i32/i64 indices, quantized rows for GET_ROWS
 // and CPY.
-static bool data_ty(int t) { return t == TLH_TYPE_F32 || t == TLH_TYPE_F16; }
+static bool data_ty(int t) { return t == TLH_TYPE_F32 || t == TLH_TYPE_F16 || t == TLH_TYPE_BF16; }
 static bool idx_ty(int t) { return t == 26 || t == 27; }
 static bool same_shape(const tlh_tensor &a, const tlh_tensor &b) {
     for (int i = 0; i < 4; ++i)
@@ -201,7 +222,7 @@ static bool rows_of_blocks(const tlh_tensor &t) {  // quantized tensor read by w
     return weight_type_ok(t.ty) && t.ne[0] % block_elems(t.ty) == 0 && t.nb[0] == block_bytes(t.ty);
 }
 static bool elem_strides_ok(const tlh_tensor &t) {
-    const int64_t es = t.ty == TLH_TYPE_F16 ? 2 : t.ty == 27 ? 8 : 4;
+    const int64_t es = (t.ty == TLH_TYPE_F16 || t.ty == TLH_TYPE_BF16) ? 2 : t.ty == 27 ? 8 : 4;
     for (int i = 0; i < 4; ++i)
         if (t.nb[i] % es) return false;
     return true;
@@ -377,10 +398,25 @@ tlh_status tlh_stream_sync(void *stream) {
 
 // Scratch: the quantized activations, then (when the int8-MFMA few-column
 // kernel runs with K split in chunks) its partial sums.
+// float weights: src1 converted to contiguous rows of the weight type, 16-byte aligned
+static int64_t mm_float_row(const MulMatShape &s) { return align_up(s.K * float_size(s.wtype), 16); }
 static int64_t mm_act_bytes(const MulMatShape &s) {
+    if (s.flt) return align_up(s.act_rows * mm_float_row(s), 256);
     return act_layout(s.act_type, s.K, s.act_rows, act_has_f16(s.wtype, s.N)).total;
 }
+static FloatMM float_mm(const tlh_op *op, const MulMatShape &s, const void *src0, const void *x, int xtype,
+                        const int64_t (&x_nb)[4], void *dst) {
+    const tlh_tensor &a = op->t[0], &d = op->t[4];
+    FloatMM f{};
+    f.wtype = a.ty, f.xtype = xtype;
+    f.w = (const char *)src0, f.w_nb1 = a.nb[1], f.w_nb2 = a.nb[2], f.w_nb3 = a.nb[3];
+    f.x = (const char *)x, f.x_nb1 = x_nb[1], f.x_nb2 = x_nb[2], f.x_nb3 = x_nb[3];
+    f.d = (float *)dst, f.d_nb1 = d.nb[1], f.d_nb2 = d.nb[2], f.d_nb3 = d.nb[3];
+    f.M = s.M, f.K = s.K, f.N = s.N, f.ne12 = s.ne12, f.ne13 = s.ne13, f.r2 = s.r2, f.r3 = s.r3;
+    return f;
+}
 static int64_t mm_partial_bytes(const MulMatShape &s) {
+    if (s.flt) return 0;
     int ksplit, upw;
     const bool reg = s.N <= 2 && gemv_reg_geometry(s.K, ksplit, upw);
     if (s.N > 16 && has_gemm(s.wtype)) return align_up(gemm_partial_bytes(s.wtype, s.M, s.N, s.K, s.ne12 * s.ne13), 256);
@@ -409,6 +445,11 @@ static tlh_status mm_check_scratch(const MulMatShape &s, const void *scratch, si
 static tlh_status mm_quantize(const tlh_op *op, const MulMatShape &s, const void *src1, void *scratch,
                               hipStream_t hs) {
     const tlh_tensor &a = op->t[0], &b = op->t[1];
+    if (s.flt) {
+        if ((uintptr_t)src1 % float_size(b.ty)) return set_error(TLH_INVALID, "mul_mat: misaligned src1");
+        const FloatMM f = float_mm(op, s, nullptr, src1, b.ty, b.nb, nullptr);
+        return launch_mm_float_convert(f, scratch, mm_float_row(s), hs);
+    }
     if ((uintptr_t)src1 & 3) return set_error(TLH_INVALID, "mul_mat: src1 must be 4-byte aligned");
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
     if (packed)
@@ -455,6 +496,12 @@ static tlh_status mm_compute(const tlh_op *op, const MulMatShape &s, const void 
                              void *dst, hipStream_t hs) {
     if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
         return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
+    if (s.flt) {
+        if ((uintptr_t)src0 % float_size(s.wtype)) return set_error(TLH_INVALID, "mul_mat: misaligned src0");
+        const int64_t row = mm_float_row(s);
+        const int64_t x_nb[4] = {float_size(s.wtype), row, row * s.N, row * s.N * s.ne12};
+        return launch_mm_float(float_mm(op, s, src0, scratch, s.wtype, x_nb, dst), hs);
+    }
     const MatmulArgs m = mm_args(op, s, src0, scratch, dst);
     return s.N <= 16 ? launch_gemv(m, nullptr, 0, hs) : launch_gemm(m, hs);
 }
@@ -477,7 +524,7 @@ bool tlh::mul_mat_compute_multi_ok(const tlh_op *const *ops, int n) {
     MulMatShape first;
     for (int i = 0; i < n; ++i) {
         MulMatShape s;
-        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.N < 3 || s.N > 16 || s.ne12 * s.ne13 != 1)
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || s.N < 3 || s.N > 16 || s.ne12 * s.ne13 != 1)
             return false;
         if (gemv_mfma_partial_bytes(s.K, s.M, s.N, 1) != 0) return false;
         if (i < n - 1 && s.M % 16 != 0) return false;
@@ -523,7 +570,8 @@ bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
     MulMatShape first;
     for (int i = 0; i < n; ++i) {
         MulMatShape s;
-        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.N != 1 || s.ne12 * s.ne13 != 1) return false;
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || s.N != 1 || s.ne12 * s.ne13 != 1)
+            return false;
         int ks, upw;
         if (!gemv_reg_geometry(s.K, ks, upw)) return false;
         if (i == 0) first = s;
@@ -626,8 +674,13 @@ tlh_status tlh_mul_mat(const tlh_op *op, const void *src0, const void *src1, voi
     if (!src0 || !src1 || !dst) return set_error(TLH_INVALID, "mul_mat: null tensor pointer");
     if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
     const hipStream_t hs = (hipStream_t)stream;
-    // Decode with a small activation: the GEMV quantizes src1 itself (one launch).
     const tlh_tensor &b = op->t[1];
+    if (s.flt) {  // one launch that rounds src1 as it reads it
+        if ((uintptr_t)src0 % float_size(s.wtype) || (uintptr_t)src1 % float_size(b.ty) || ((uintptr_t)dst & 3))
+            return set_error(TLH_INVALID, "mul_mat: misaligned src0, src1 or dst");
+        return launch_mm_float(float_mm(op, s, src0, src1, b.ty, b.nb, dst), hs);
+    }
+    // Decode with a small activation: the GEMV quantizes src1 itself (one launch).
     const bool packed = b.nb[2] == b.nb[1] * s.N && b.nb[3] == b.nb[2] * s.ne12;
     if (s.N <= 2 && packed && !((uintptr_t)src1 & 3)) {
         const MatmulArgs m = mm_args(op, s, src0, scratch, dst);

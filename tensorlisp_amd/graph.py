@@ -23,7 +23,7 @@ from dataclasses import dataclass, field
 from . import native as N
 
 STORE_TEMP, STORE_WEIGHT, STORE_STATE, STORE_INPUT = 0, 1, 2, 3
-ELEM = {N.F32: 4, N.F16: 2, N.I32: 4, N.I64: 8}
+ELEM = {N.F32: 4, N.F16: 2, N.BF16: 2, N.I32: 4, N.I64: 8}
 
 
 class TlhIrTensor(C.Structure):

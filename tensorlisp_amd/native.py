@@ -18,10 +18,13 @@ PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libtlhip.so"
 
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
-F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
-VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
-TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 30
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292),
+         F32: (1, 4), F16: (1, 2), BF16: (1, 2)}
+# ggml's vec_dot_type: what src1 is converted to (float weights: their own type)
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, F32: F32, F16: F16, BF16: BF16}
+TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K",
+              BF16: "bf16"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 STATUS = {0: "OK", 1: "NO_DEVICE", 2: "UNSUPPORTED", 3: "INVALID", 4: "ALLOC", 5: "EXECUTION"}
@@ -179,11 +182,12 @@ def ggml_tensor(ty: int, ne, nb=None) -> TlhTensor:
 
 
 def mul_mat_op(wtype: int, M: int, K: int, N: int, ne2: int = 1, ne3: int = 1, w_ne2: int = 1,
-               w_ne3: int = 1, x_nb=None, w_nb=None, d_nb=None) -> TlhOp:
-    """The MUL_MAT descriptor of Ctx::mul_mat (lower.rs:543-571): t0 weights [K, M], t1 f32 [K, N], t4 f32 [M, N]."""
+               w_ne3: int = 1, x_nb=None, w_nb=None, d_nb=None, xtype: int = F32) -> TlhOp:
+    """The MUL_MAT descriptor of Ctx::mul_mat (lower.rs:543-571): t0 weights [K, M], t1 [K, N] (f32, or the
+    f16 / bf16 of f16 / bf16 weights), t4 f32 [M, N]."""
     op = TlhOp()
     op.t[0] = ggml_tensor(wtype, [K, M, w_ne2, w_ne3], w_nb)
-    op.t[1] = ggml_tensor(F32, [K, N, ne2, ne3], x_nb)
+    op.t[1] = ggml_tensor(xtype, [K, N, ne2, ne3], x_nb)
     op.t[4] = ggml_tensor(F32, [M, N, ne2, ne3], d_nb)
     op.x[0] = ne2 // w_ne2
     op.x[1] = ne3 // w_ne3
@@ -225,11 +229,11 @@ class MulMat:
     """One GGML_OP_MUL_MAT node with its scratch, launched many times (what a lowered
     Dispatch is in crates/kernels/src/cuda/exec.rs:186-225)."""
 
-    def __init__(self, wtype: int, M: int, K: int, N: int, device="cuda"):
+    def __init__(self, wtype: int, M: int, K: int, N: int, device="cuda", op: TlhOp = None):
         import torch
 
         self.wtype, self.M, self.K, self.N = wtype, M, K, N
-        self.op = mul_mat_op(wtype, M, K, N)
+        self.op = mul_mat_op(wtype, M, K, N) if op is None else op
         self.scratch_bytes = mul_mat_scratch_bytes(self.op)
         self.scratch = torch.empty(max(self.scratch_bytes, 256) + 256, dtype=torch.uint8, device=device)
         off = (-self.scratch.data_ptr()) % 256
@@ -261,6 +265,33 @@ def mul_mat(wtype: int, w, M: int, K: int, x, stream=None):
     y = torch.empty((N, M), dtype=torch.float32, device=x.device)
     MulMat(wtype, M, K, N, device=x.device)(w, x, y, stream)
     return y
+
+
+def mul_mat_views(w, x, out=None, stream=None, split: bool = False):
+    """ggml_mul_mat on torch views of float weights: w (w3, w2, M, K) f32 / f16 /
+    bf16, x (n3, n2, N, K) f32 or w's dtype, out (n3, n2, N, M) f32 (ggml's ne
+    reversed; fewer leading dims are 1). Any element-aligned strides with K
+    contiguous; w's batch dims broadcast over x's (r2 = n2 / w2, r3 = n3 / w3).
+    split: src1's conversion and the products as two launches
+    (tlh_mul_mat_quantize + tlh_mul_mat_compute) instead of one."""
+    import torch
+
+    wt, xt = _ggml_type(w), _ggml_type(x)
+    lead = lambda t: [1] * (4 - t.dim()) + list(t.shape[:-2])  # noqa: E731
+    n3, n2 = lead(x)[-2:]
+    if out is None:
+        out = torch.empty((n3, n2, x.shape[-2], w.shape[-2]), dtype=torch.float32, device=x.device)
+    op = TlhOp()
+    op.t[0], op.t[1], op.t[4] = tensor_desc(w, wt), tensor_desc(x, xt), tensor_desc(out, F32)
+    w3, w2 = lead(w)[-2:]
+    op.x[0], op.x[1] = n2 // max(w2, 1), n3 // max(w3, 1)
+    mm = MulMat(wt, w.shape[-2], w.shape[-1], x.shape[-2], device=x.device, op=op)
+    if split:
+        mm.quantize(x, stream)
+        mm.compute(w, out, stream)
+    else:
+        mm(w, x, out, stream)
+    return out
 
 
 def quantize_act(wtype: int, x, stream=None):
@@ -317,7 +348,7 @@ def flash_attn_params(n_head: int, scale: float, max_bias: float = 0.0, softcap:
 def _ggml_type(t) -> int:
     import torch
 
-    return {torch.float32: F32, torch.float16: F16}.get(t.dtype, -1)
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}.get(t.dtype, -1)
 
 
 def tensor_desc(t, ty: int) -> TlhTensor:
@@ -476,7 +507,8 @@ def _f32(x) -> float:
 def core_type(t) -> int:
     import torch
 
-    return {torch.float32: F32, torch.float16: F16, torch.int32: I32, torch.int64: I64}.get(t.dtype, -1)
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32,
+            torch.int64: I64}.get(t.dtype, -1)
 
 
 def quant_desc(t, wtype: int, k: int) -> TlhTensor:

@@ -17,6 +17,11 @@ these are the reference's outputs on fixed inputs, captured once:
   mul_mat.npz      one GGML_OP_MUL_MAT on the CPU backend for the reference test's
                    cases (native.rs:73-107: 96 x 256 weights from noise(seed 1),
                    x = noise(seed 10 + n), n in 1,3,5,8,9,40) per weight type
+  mul_mat_float.npz  the same cases with f32, f16 and bf16 weights (ggml_quantize_chunk
+                   of the noise matrix), plus f16 / bf16 weights against src1 already
+                   of the weight type and a ragged K = 100 (the element-wise path), and
+                   attn:sdpa's non-flash graph on refs.SDPA_CASES (inputs regenerated
+                   from seeds by refs.sdpa_inputs)
   config1.npz      BASELINE config 1 (Q8_0 4096 x 4096, N = 1, seed 0): input hashes
                    and the CPU backend's output vector
   flash_attn.npz   GGML_OP_FLASH_ATTN_EXT (ops.cpp:8468) on dense f16 K/V, the
@@ -67,7 +72,8 @@ these are the reference's outputs on fixed inputs, captured once:
                    accumulation; for refs.paged_8b_seqs, each sequence run alone, the
                    argmax and 8 largest logits of each step (f32 P.V) and how far the
                    two accumulations move that step's logits.
-Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b]   (needs oracle/_ref built)
+Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b
+     | mul_mat_float]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -83,7 +89,8 @@ sys.path.insert(0, str(HERE.parents[1]))
 
 from refs import (DECODER_8B_STEPS, decoder_8b_layer_ref, decoder_8b_ref_run, decoder_8b_slice_config,  # noqa: E402
                   decoder_8b_weights, paged_8b_ref)
-from refs import (FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
+from refs import SDPA_CASES, sdpa_graph, sdpa_inputs  # noqa: E402
+from refs import (BF16, F16, F32, FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
                   decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, mmid_case, paged_ref_run,
                   xorshift_noise)
 from tensorlisp_amd import synth  # noqa: E402
@@ -157,6 +164,47 @@ def q5_K_golden(ref) -> None:
     kquant_golden(ref, Q5_K, "q5_K", 71, 72)
 
 
+def mul_mat_float_golden(ref) -> None:
+    rows, k = 96, 256
+    wn = xorshift_noise((rows, k), 1)
+    ns = [1, 3, 5, 8, 9, 40]
+    out = {"ns": np.array(ns)}
+    for t, name in ((F32, "f32"), (F16, "f16"), (BF16, "bf16")):
+        wq = ref.quantize_weights(t, wn)
+        out[f"{name}_w"] = wq
+        for n in ns:
+            y, _ = ref.mul_mat(t, wq, rows, k, xorshift_noise((n, k), 10 + n))
+            out[f"{name}_y{n}"] = y
+    # src1 already f16 / bf16 (the graph form ggml_mul_mat takes then), through
+    # ref_ir_run: weights [k, rows], x [k, n] of the weight type
+    from tensorlisp_amd import graph as G
+
+    for t, name in ((F16, "f16"), (BF16, "bf16")):
+        for n in (1, 9):
+            b = G.Builder()
+            w = b.weight(t, [k, rows])
+            x = b.input(t, [k, n])
+            y = b.mul_mat(w, x)
+            b.expand(y)
+            xq = ref.quantize_weights(t, xorshift_noise((n, k), 20 + n)).view(np.uint16)
+            out[f"{name}_x{n}_same"] = xq
+            out[f"{name}_y{n}_same"] = ref.ir_run(b, [out[f"{name}_w"].view(np.uint16)], [], [xq],
+                                                  [(y, np.float32)])[0].reshape(n, rows)
+    # K = 100: no multiple of 8 (the element-wise path)
+    w100 = synth.normal(81, (33, 100))
+    x100 = synth.normal(82, (5, 100))
+    out["k100_x"] = x100
+    for t, name in ((F32, "f32"), (F16, "f16"), (BF16, "bf16")):
+        wq = ref.quantize_weights(t, w100)
+        out[f"k100_{name}_w"] = wq
+        out[f"k100_{name}_y"] = ref.mul_mat(t, wq, 33, 100, x100)[0]
+    # attn:sdpa's non-flash graph (float MUL_MATs of K and V) on refs.SDPA_CASES
+    for i, case in enumerate(SDPA_CASES):
+        b, merged, _ = sdpa_graph(*case)
+        out[f"sdpa{i}"] = ref.ir_run(b, [], [], sdpa_inputs(case, 300 + 10 * i), [(merged, np.float32)])[0]
+    np.savez_compressed(HERE / "mul_mat_float.npz", **out)
+
+
 def mul_mat_id_golden(ref) -> None:
     out = {}
     for case in MMID_CASES:
@@ -222,6 +270,9 @@ def main() -> None:
     ref = Ref()
     if sys.argv[1:] == ["decoder_8b"]:  # only the 8B-shaped decoder fixture
         decoder_8b_golden(ref)
+        return
+    if sys.argv[1:] == ["mul_mat_float"]:  # only the float-weight MUL_MAT fixture
+        mul_mat_float_golden(ref)
         return
     if sys.argv[1:] == ["mul_mat_id"]:  # only the MUL_MAT_ID fixture
         mul_mat_id_golden(ref)
@@ -310,6 +361,7 @@ def main() -> None:
     decoder_paged_golden(ref)
     decoder_8b_golden(ref)
     mul_mat_id_golden(ref)
+    mul_mat_float_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

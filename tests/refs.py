@@ -22,13 +22,19 @@ ORACLE_SO = ROOT / "oracle" / "liboracle.so"
 REF_SO = ROOT / "oracle" / "_ref" / "libggml_ref.so"
 
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
-F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 30
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
 VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32", F16: "f16",
+         BF16: "bf16"}
+
+
+FLOAT_BYTES = {F32: 4, F16: 2, BF16: 2}  # element sizes of the float weight types
 
 
 def row_bytes(t: int, k: int) -> int:
+    if t in FLOAT_BYTES:
+        return k * FLOAT_BYTES[t]
     be, bb = BLOCK[t]
     assert k % be == 0, (t, k)
     return k // be * bb
@@ -60,7 +66,7 @@ def _i64p(a: np.ndarray):
 
 
 I32, I64 = 26, 27
-NP_OF = {F32: np.float32, F16: np.uint16, I32: np.int32, I64: np.int64}
+NP_OF = {F32: np.float32, F16: np.uint16, BF16: np.uint16, I32: np.int32, I64: np.int64}
 
 
 class TlqT(C.Structure):
@@ -109,6 +115,13 @@ class Oracle:
             getattr(L, name).restype = C.c_float
         L.tlq_fp16_to_fp32_row.argtypes = [vp, vp, i64]
         L.tlq_fp32_to_fp16_row.argtypes = [vp, vp, i64]
+        L.tlq_bf16_to_fp32.argtypes = [C.c_uint16]
+        L.tlq_bf16_to_fp32.restype = C.c_float
+        L.tlq_fp32_to_bf16.argtypes = [C.c_float]
+        L.tlq_fp32_to_bf16.restype = C.c_uint16
+        for name in ("tlq_vec_dot_f32", "tlq_vec_dot_f16", "tlq_vec_dot_bf16"):
+            getattr(L, name).argtypes = [i64, vp, vp]
+            getattr(L, name).restype = C.c_float
         L.tlq_block_ints_q4_K.argtypes = [vp, vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
         L.tlq_mul_mat.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, C.c_int]
         L.tlq_mul_mat.restype = C.c_int
@@ -145,6 +158,15 @@ class Oracle:
         out = np.empty(f.shape, np.uint16)
         self.lib.tlq_fp32_to_fp16_row(_p(f), _p(out), f.size)
         return out
+
+    # -- bf16 (element by element through the C functions: small arrays only)
+    def f32_to_bf16(self, f) -> np.ndarray:
+        f = _f32(f)
+        return np.array([self.lib.tlq_fp32_to_bf16(float(v)) for v in f.reshape(-1)], np.uint16).reshape(f.shape)
+
+    def bf16_to_f32(self, h) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        return np.array([self.lib.tlq_bf16_to_fp32(int(v)) for v in h.reshape(-1)], np.float32).reshape(h.shape)
 
     # -- quantizers: x [rows, k] f32 -> uint8 [rows, row_bytes]
     def quantize(self, t: int, x) -> np.ndarray:
@@ -186,8 +208,9 @@ class Oracle:
         return a.value, b.value
 
     def mul_mat(self, wtype: int, w, M: int, K: int, x, nthreads: int = 8) -> np.ndarray:
-        """x [N, K] f32 -> y [N, M] f32 (ggml dst layout ne0 = M)."""
-        w = np.ascontiguousarray(w, dtype=np.uint8)
+        """x [N, K] f32 -> y [N, M] f32 (ggml dst layout ne0 = M). w: block bytes, or
+        the f32 / f16 (uint16 bits) / bf16 (uint16 bits) rows of float weights."""
+        w = np.ascontiguousarray(w).view(np.uint8)
         x = _f32(np.atleast_2d(x))
         N = x.shape[0]
         y = np.empty((N, M), np.float32)
@@ -410,7 +433,7 @@ class Ref:
 
     def mul_mat(self, wtype: int, w, M: int, K: int, x, nthreads: int = 8, reps: int = 1):
         """One GGML_OP_MUL_MAT on the CPU backend. Returns (y [N, M], seconds for `reps` runs)."""
-        w = np.ascontiguousarray(w, dtype=np.uint8)
+        w = np.ascontiguousarray(w).view(np.uint8)
         x = _f32(np.atleast_2d(x))
         N = x.shape[0]
         y = np.empty((N, M), np.float32)
@@ -1177,3 +1200,53 @@ def mmid_case(case):
         rng = np.random.default_rng(930 + seed)
         idh = np.stack([rng.permutation(n_as)[:n_used] for _ in range(n_tok)]).astype(np.int32)
     return b, y, [wh], [xh, idh]
+
+
+# ------------------------------------------------------------ attn:sdpa graphs
+# (head dim, queries, keys, heads, kv heads, K/V type, causal mask): decode and
+# prefill shapes, grouped and plain heads, an f16 cache and f32 projections
+SDPA_CASES = ((64, 7, 7, 4, 2, F16, True), (128, 1, 33, 8, 2, F16, False), (64, 5, 12, 4, 4, F32, True),
+              (128, 20, 40, 8, 8, BF16, True))
+
+
+def sdpa_graph(hd, lq, lk, heads, kvh, kvt, masked):
+    """attn:sdpa's non-flash branch (crates/tensorlisp/src/scheme/stdlib/attn.ss:75-90)
+    on split heads (attn.ss:55-60): q [hd, heads, lq] f32 and k, v [hd, kvh, lk] of
+    `kvt` permuted to [hd, L, heads]; probs = soft_max_ext(mul_mat(cont k, cont q),
+    mask, 1/sqrt(hd)); out = mul_mat(cont(permute(v, 1, 0, 2, 3)), probs), heads
+    merged back to [hd * heads, lq]. Returns (builder, output, (q, k, v, mask)).
+    Both MUL_MATs have float weights: the f16 / bf16 / f32 keys and values."""
+    from tensorlisp_amd import graph as G
+
+    b = G.Builder()
+    q = b.input(F32, [hd, heads, lq])
+    k = b.input(kvt, [hd, kvh, lk])
+    v = b.input(kvt, [hd, kvh, lk])
+    m = b.input(F16, [lk, lq]) if masked else None
+    qh, kh, vh = (b.permute(t, 0, 2, 1, 3) for t in (q, k, v))
+    kq = b.mul_mat(b.cont(kh), b.cont(qh))  # [lk, lq, heads]
+    probs = b.soft_max_ext(kq, m, float(np.float32(1.0) / np.sqrt(np.float32(hd))), 0.0)
+    out = b.mul_mat(b.cont(b.permute(vh, 1, 0, 2, 3)), probs)  # [hd, lq, heads]
+    merged = b.reshape(b.cont(b.permute(out, 0, 2, 1, 3)), hd * heads, lq)
+    b.expand(merged)
+    return b, merged, (q, k, v, m)
+
+
+def sdpa_inputs(case, seed: int):
+    """numpy inputs of an SDPA_CASES graph (ggml ne reversed; f16 / bf16 as uint16
+    bits): q, k, v and, when masked, the causal f16 mask (key j of query i is
+    visible while j <= i + lk - lq)."""
+    from tensorlisp_amd import synth
+
+    hd, lq, lk, heads, kvh, kvt, masked = case
+    q = synth.normal(seed, (lq, heads, hd))
+    kv = [synth.normal(seed + i, (lk, kvh, hd)) for i in (1, 2)]
+    if kvt == F16:
+        kv = [a.astype(np.float16).view(np.uint16) for a in kv]
+    elif kvt == BF16:
+        kv = [((a.view(np.uint32) + 0x7FFF + ((a.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16) for a in kv]
+    ins = [q] + kv
+    if masked:
+        i, j = np.arange(lq)[:, None], np.arange(lk)[None, :]
+        ins.append(np.where(j <= i + lk - lq, 0.0, -np.inf).astype(np.float16).view(np.uint16))
+    return ins

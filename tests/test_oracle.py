@@ -18,7 +18,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref, row_bytes
+from refs import (BF16, F16, F32, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref,
+                  row_bytes)
 from tensorlisp_amd import synth
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -364,6 +365,89 @@ def test_q5_K_matches_reference_live():
         assert same_bits(o.mul_mat(Q5_K, w, M, K, x), y)
         y, _ = r.mul_mat(Q5_K, wq, 8, K, x)
         assert same_bits(o.mul_mat(Q5_K, wq, 8, K, x), y)
+
+
+# ------------------------------------------------ float weights (f32 / f16 / bf16)
+FLOATS = ((F32, "f32"), (F16, "f16"), (BF16, "bf16"))
+
+
+def test_bf16_conversion_against_torch():
+    """tlq_fp32_to_bf16 rounds to nearest, ties to even, as torch's bfloat16 cast
+    does (an independent implementation), on random bit patterns, exact ties with
+    even and odd kept halves, and the rounding into infinity; a NaN stays a NaN
+    with the quiet bit set; bf16 -> f32 puts the bits in the upper half."""
+    import torch
+
+    o = oracle()
+    bits = synth.integers(91, 0, 2**32 - 1, 3000).astype(np.uint32)
+    bits = bits[(bits & 0x7F800000) != 0x7F800000]  # finite
+    ties = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7F8000, 0x7F7F7FFF, 0x00008000, 0x00018000,
+                     0x7F7FFFFF, 0x80000000, 0x00000001], np.uint32)
+    f = np.concatenate([bits, ties]).view(np.float32)
+    got = o.f32_to_bf16(f)
+    want = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, want)
+    assert list(got[-10:-6]) == [0x3F80, 0x3F82, 0xBF80, 0x7F80]  # ties to even, and into +inf
+    nan = np.array([0x7F800001, 0xFF800001, 0x7FC00000], np.uint32).view(np.float32)
+    assert list(o.f32_to_bf16(nan)) == [0x7FC0, 0xFFC0, 0x7FC0]
+    h = np.arange(0, 65536, 7, dtype=np.uint16)
+    h = h[((h & 0x7F80) != 0x7F80) | ((h & 0x7F) == 0)]  # NaNs lose their payload on the way through a double
+    np.testing.assert_array_equal(o.bf16_to_f32(h).view(np.uint32), h.astype(np.uint32) << 16)
+
+
+def test_float_mul_mat_golden_reference_cases():
+    """The reference test's cases (native.rs:73-107, 96 x 256 noise weights, n in
+    1,3,5,8,9,40) with f32 / f16 / bf16 weights, src1 already of the weight type,
+    and a ragged K = 100: bit-exact with the CPU backend (mul_mat_float.npz)."""
+    from refs import xorshift_noise
+
+    o, g = oracle(), gold("mul_mat_float")
+    for t, name in FLOATS:
+        w = g[f"{name}_w"]
+        for n in g["ns"]:
+            assert same_bits(o.mul_mat(t, w, 96, 256, xorshift_noise((int(n), 256), 10 + int(n))), g[f"{name}_y{n}"])
+        assert same_bits(o.mul_mat(t, g[f"k100_{name}_w"], 33, 100, g["k100_x"]), g[f"k100_{name}_y"])
+    for name, up in (("f16", o.f16_to_f32), ("bf16", o.bf16_to_f32)):
+        t = F16 if name == "f16" else BF16
+        for n in (1, 9):
+            x = up(g[f"{name}_x{n}_same"])  # exact in f32; the oracle's conversion back is the identity
+            assert same_bits(o.mul_mat(t, g[f"{name}_w"], 96, 256, x), g[f"{name}_y{n}_same"])
+
+
+@pytest.mark.parametrize("t,name", FLOATS, ids=[n for _, n in FLOATS])
+def test_float_mul_mat_against_f64(t, name):
+    """Every output is the f64 sum of f32 products of the weights and src1 rounded
+    to the weight type (numpy float16 / torch bfloat16 casts), to the last f32
+    rounding: an unrounded src1 (about 1e-3 relative for f16) or a dropped term fails."""
+    import torch
+
+    o = oracle()
+    M, K, N = 40, 1000, 3
+    wf, x = synth.normal(92, (M, K)), synth.normal(93, (N, K)) * 3
+    if t == F32:
+        wq, wd, xd = wf, wf, x
+    elif t == F16:
+        wq = wf.astype(np.float16).view(np.uint16)
+        wd, xd = wf.astype(np.float16).astype(np.float32), x.astype(np.float16).astype(np.float32)
+    else:
+        bf = lambda a: torch.from_numpy(a).to(torch.bfloat16).to(torch.float32).numpy()  # noqa: E731
+        wq = torch.from_numpy(wf).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        wd, xd = bf(wf), bf(x)
+    prods = wd[None, :, :] * xd[:, None, :]  # f32 products [N, M, K]
+    want = prods.astype(np.float64).sum(-1)
+    got = o.mul_mat(t, wq, M, K, x).astype(np.float64)
+    bound = np.abs(want) * 2.0**-24 + 1e-14 * np.abs(prods).astype(np.float64).sum(-1)
+    assert (np.abs(got - want) <= bound).all()
+
+
+@pytest.mark.parametrize("t,name", FLOATS, ids=[n for _, n in FLOATS])
+def test_float_mul_mat_matches_reference_live(t, name):
+    r = ref()
+    o = oracle()
+    for M, K, N in ((7, 33, 3), (64, 256, 5), (40, 4096, 17)):
+        wq = r.quantize_weights(t, synth.normal(94 + K, (M, K)))
+        x = synth.normal(95 + N, (N, K))
+        assert same_bits(o.mul_mat(t, wq, M, K, x), r.mul_mat(t, wq, M, K, x)[0])
 
 
 # ------------------------------------------------------------- MUL_MAT_ID
