@@ -15,12 +15,13 @@
 // bits, 128 nibble bytes), :362-368 (q6_K: 128 low-nibble bytes, 64 bytes of
 // 2-bit high parts, 16 int8 scales, f16 d), :370-375 (q8_K: f32 d, 256 int8,
 // 16 int16 sums).
-enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q5_K_B = 176, Q6_K_B = 210, Q8_K_B = 292 };
+enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q5_K_B = 176, Q6_K_B = 210, Q8_K_B = 292,
+       Q4_1_B = 20, Q5_0_B = 22, Q5_1_B = 24, Q8_1_B = 36 };
 
 int64_t tlq_block_elems(int type) {
     switch (type) {
     case TLQ_F32: case TLQ_F16: case TLQ_BF16: return 1;
-    case TLQ_Q4_0: case TLQ_Q8_0: return QK32;
+    case TLQ_Q4_0: case TLQ_Q8_0: case TLQ_Q4_1: case TLQ_Q5_0: case TLQ_Q5_1: case TLQ_Q8_1: return QK32;
     case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
     default: return 0;
     }
@@ -32,6 +33,10 @@ int64_t tlq_block_bytes(int type) {
     case TLQ_F16: case TLQ_BF16: return 2;
     case TLQ_Q4_0: return Q4_0_B;
     case TLQ_Q8_0: return Q8_0_B;
+    case TLQ_Q4_1: return Q4_1_B;
+    case TLQ_Q5_0: return Q5_0_B;
+    case TLQ_Q5_1: return Q5_1_B;
+    case TLQ_Q8_1: return Q8_1_B;
     case TLQ_Q4_K: return Q4_K_B;
     case TLQ_Q5_K: return Q5_K_B;
     case TLQ_Q6_K: return Q6_K_B;
@@ -47,7 +52,8 @@ int64_t tlq_row_bytes(int type, int64_t k) {
 
 int tlq_vec_dot_type(int wtype) {
     switch (wtype) {
-    case TLQ_Q4_0: case TLQ_Q8_0: return TLQ_Q8_0;
+    case TLQ_Q4_0: case TLQ_Q8_0: case TLQ_Q5_0: return TLQ_Q8_0;
+    case TLQ_Q4_1: case TLQ_Q5_1: return TLQ_Q8_1;
     case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: return TLQ_Q8_K;
     case TLQ_F32: case TLQ_F16: case TLQ_BF16: return wtype;
     default: return -1;
@@ -302,6 +308,30 @@ void tlq_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
     }
 }
 
+// ggml-quants.c:302-335 (quantize_row_q8_1_ref; the x86 entry without AVX,
+// arch/x86/quants.c:400-501): q8_0's d and codes, plus s = f16(sum of the
+// codes * the unrounded d).
+void tlq_quantize_row_q8_1(const float *x, void *vy, int64_t k) {
+    uint8_t *y = (uint8_t *)vy;
+    for (int64_t b = 0; b < k / QK32; ++b, x += QK32, y += Q8_1_B) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK32; ++j) {
+            const float a = fabsf(x[j]);
+            if (a > amax) amax = a;
+        }
+        const float d = amax / 127;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        wr16(y, tlq_fp32_to_fp16(d));
+        int sum = 0;
+        for (int j = 0; j < QK32; ++j) {
+            const int q = (int)roundf(x[j] * id);
+            y[4 + j] = (uint8_t)(int8_t)q;
+            sum += q;
+        }
+        wr16(y + 2, tlq_fp32_to_fp16((float)sum * d));
+    }
+}
+
 // ggml-quants.c:2768-2804: iscale = -127/(signed value of largest magnitude,
 // first wins), codes round-half-even clamped to 127, 16-element code sums,
 // d = 1/iscale in f32. An all-zero block stores d = 0 and zero codes; the
@@ -339,6 +369,7 @@ int tlq_quantize_act(int wtype, const float *x, void *y, int64_t k) {
     switch (tlq_vec_dot_type(wtype)) {
     case TLQ_Q8_0: tlq_quantize_row_q8_0(x, y, k); return 0;
     case TLQ_Q8_K: tlq_quantize_row_q8_K(x, y, k); return 0;
+    case TLQ_Q8_1: tlq_quantize_row_q8_1(x, y, k); return 0;
     case TLQ_F32: memcpy(y, x, (size_t)k * 4); return 0;
     case TLQ_F16: tlq_fp32_to_fp16_row(x, (uint16_t *)y, k); return 0;
     case TLQ_BF16:
@@ -439,8 +470,48 @@ void tlq_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
     }
 }
 
+// ggml-quants.c:479-498: q*d + m per element (two roundings), nibbles as q4_0.
+void tlq_dequantize_row_q4_1(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q4_1_B, y += QK32) {
+        const float d = tlq_fp16_to_fp32(rd16(x)), m = tlq_fp16_to_fp32(rd16(x + 2));
+        for (int j = 0; j < 16; ++j) {
+            y[j] = (float)(x[4 + j] & 0x0f) * d + m;
+            y[j + 16] = (float)(x[4 + j] >> 4) * d + m;
+        }
+    }
+}
+
+// The fifth bit of element j of a q5 block: bit j of the little-endian qh word.
+static inline int q5_code(const uint8_t *qh, const uint8_t *qs, int j) {
+    const uint32_t h = (uint32_t)qh[0] | (uint32_t)qh[1] << 8 | (uint32_t)qh[2] << 16 | (uint32_t)qh[3] << 24;
+    const int nib = j < 16 ? (qs[j] & 0x0f) : (qs[j - 16] >> 4);
+    return nib | (int)((h >> j) & 1u) << 4;
+}
+
+// ggml-quants.c:500-524: (q - 16) * d.
+void tlq_dequantize_row_q5_0(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q5_0_B, y += QK32) {
+        const float d = tlq_fp16_to_fp32(rd16(x));
+        for (int j = 0; j < QK32; ++j) y[j] = (float)(q5_code(x + 2, x + 6, j) - 16) * d;
+    }
+}
+
+// ggml-quants.c:526-551: q * d + m.
+void tlq_dequantize_row_q5_1(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q5_1_B, y += QK32) {
+        const float d = tlq_fp16_to_fp32(rd16(x)), m = tlq_fp16_to_fp32(rd16(x + 2));
+        for (int j = 0; j < QK32; ++j) y[j] = (float)q5_code(x + 4, x + 8, j) * d + m;
+    }
+}
+
 int tlq_dequantize_row(int type, const void *x, float *y, int64_t k) {
     switch (type) {
+    case TLQ_Q4_1: tlq_dequantize_row_q4_1(x, y, k); return 0;
+    case TLQ_Q5_0: tlq_dequantize_row_q5_0(x, y, k); return 0;
+    case TLQ_Q5_1: tlq_dequantize_row_q5_1(x, y, k); return 0;
     case TLQ_Q4_0: tlq_dequantize_row_q4_0(x, y, k); return 0;
     case TLQ_Q8_0: tlq_dequantize_row_q8_0(x, y, k); return 0;
     case TLQ_Q4_K: tlq_dequantize_row_q4_K(x, y, k); return 0;
@@ -464,6 +535,49 @@ float tlq_vec_dot_q4_0_q8_0(int64_t k, const void *vx, const void *vy) {
             s += ((x[2 + j] >> 4) - 8) * (int8_t)y[2 + 16 + j];
         }
         acc += s * tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y));
+    }
+    return acc;
+}
+
+// ggml-cpu/quants.c:262-296 (x86 entry without AVX: arch/x86/quants.c:859-915):
+// per block sumf += (dx * dy) * sumi + mx * sy.
+float tlq_vec_dot_q4_1_q8_1(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float acc = 0;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q4_1_B, y += Q8_1_B) {
+        int s = 0;
+        for (int j = 0; j < 16; ++j) {
+            s += (x[4 + j] & 0x0f) * (int8_t)y[4 + j];
+            s += (x[4 + j] >> 4) * (int8_t)y[4 + 16 + j];
+        }
+        acc += (tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y))) * (float)s +
+               tlq_fp16_to_fp32(rd16(x + 2)) * tlq_fp16_to_fp32(rd16(y + 2));
+    }
+    return acc;
+}
+
+// ggml-cpu/quants.c:365-406 (arch/x86/quants.c:1142-1219): codes q - 16,
+// sumf += (dx * dy) * sumi.
+float tlq_vec_dot_q5_0_q8_0(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float acc = 0;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q5_0_B, y += Q8_0_B) {
+        int s = 0;
+        for (int j = 0; j < QK32; ++j) s += (q5_code(x + 2, x + 6, j) - 16) * (int8_t)y[2 + j];
+        acc += (tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y))) * (float)s;
+    }
+    return acc;
+}
+
+// ggml-cpu/quants.c:408-449 (arch/x86/quants.c:1222-1305): as q4_1 with 5-bit codes.
+float tlq_vec_dot_q5_1_q8_1(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float acc = 0;
+    for (int64_t b = 0; b < k / QK32; ++b, x += Q5_1_B, y += Q8_1_B) {
+        int s = 0;
+        for (int j = 0; j < QK32; ++j) s += q5_code(x + 4, x + 8, j) * (int8_t)y[4 + j];
+        acc += (tlq_fp16_to_fp32(rd16(x)) * tlq_fp16_to_fp32(rd16(y))) * (float)s +
+               tlq_fp16_to_fp32(rd16(x + 2)) * tlq_fp16_to_fp32(rd16(y + 2));
     }
     return acc;
 }
@@ -650,6 +764,9 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
     case TLQ_Q5_K: dot = tlq_vec_dot_q5_K_q8_K; break;
     case TLQ_Q6_K: dot = tlq_vec_dot_q6_K_q8_K; break;
+    case TLQ_Q4_1: dot = tlq_vec_dot_q4_1_q8_1; break;
+    case TLQ_Q5_0: dot = tlq_vec_dot_q5_0_q8_0; break;
+    case TLQ_Q5_1: dot = tlq_vec_dot_q5_1_q8_1; break;
     case TLQ_F32: dot = tlq_vec_dot_f32; break;
     case TLQ_F16: dot = tlq_vec_dot_f16; break;
     case TLQ_BF16: dot = tlq_vec_dot_bf16; break;

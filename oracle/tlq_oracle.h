@@ -24,7 +24,11 @@ enum {
     TLQ_F32 = 0,
     TLQ_F16 = 1,
     TLQ_Q4_0 = 2,
+    TLQ_Q4_1 = 3,
+    TLQ_Q5_0 = 6,
+    TLQ_Q5_1 = 7,
     TLQ_Q8_0 = 8,
+    TLQ_Q8_1 = 9,
     TLQ_Q4_K = 12,
     TLQ_Q5_K = 13,
     TLQ_Q6_K = 14,
@@ -32,13 +36,14 @@ enum {
     TLQ_BF16 = 30,
 };
 
-// Block geometry, vendor/ggml/src/ggml-common.h:89-90,194-198,251-255,325-337,370-375.
+// Block geometry, vendor/ggml/src/ggml-common.h:89-90,194-198,201-269 (q4_1, q5_0,
+// q5_1, q8_1: 20, 22, 24, 36 bytes per 32),325-337,370-375.
 int64_t tlq_block_elems(int type);
 int64_t tlq_block_bytes(int type);
 int64_t tlq_row_bytes(int type, int64_t k);
 // vec_dot_type of a weight type on x86 (ggml-cpu.c:215-226,239-319,394-399):
-// Q8_0 for Q4_0 and Q8_0 weights, Q8_K for the K-quants, the weight type
-// itself for F32 / F16 / BF16; -1 otherwise.
+// Q8_0 for Q4_0, Q5_0 and Q8_0 weights, Q8_1 for Q4_1 and Q5_1, Q8_K for the
+// K-quants, the weight type itself for F32 / F16 / BF16; -1 otherwise.
 int tlq_vec_dot_type(int wtype);
 
 // IEEE binary16 <-> binary32 (round to nearest even), the semantics of
@@ -64,6 +69,9 @@ void tlq_quantize_row_q4_K(const float *x, void *y, int64_t k);
 // ggml-quants.c:2768-2804).
 void tlq_quantize_row_q8_0(const float *x, void *y, int64_t k);
 void tlq_quantize_row_q8_K(const float *x, void *y, int64_t k);
+// quantize_row_q8_1 -> _ref on x86 without AVX (arch/x86/quants.c:400-501,
+// ggml-quants.c:302-335): q8_0's d and codes plus s = f16(code sum * d).
+void tlq_quantize_row_q8_1(const float *x, void *y, int64_t k);
 // Quantize one activation row into the weight type's vec_dot type (for F32 /
 // F16 / BF16 weights: from_float = copy / ggml_cpu_fp32_to_fp16 /
 // ggml_cpu_fp32_to_bf16, ggml-cpu.c:3531-3536).
@@ -77,6 +85,10 @@ void tlq_dequantize_row_q4_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q5_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q8_K(const void *x, float *y, int64_t k);
+// dequantize_row_q4_1 ggml-quants.c:479-498, _q5_0 :500-524, _q5_1 :526-551.
+void tlq_dequantize_row_q4_1(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q5_0(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q5_1(const void *x, float *y, int64_t k);
 int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
 
 // Dot products of one weight row with one quantized activation row:
@@ -88,6 +100,11 @@ float tlq_vec_dot_q8_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q4_K_q8_K(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q5_K_q8_K(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *x, const void *y);
+// ggml_vec_dot_q4_1_q8_1_generic ggml-cpu/quants.c:262-296, _q5_0_q8_0_generic
+// :365-406, _q5_1_q8_1_generic :408-449 (the x86 entries without AVX call them).
+float tlq_vec_dot_q4_1_q8_1(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q5_0_q8_0(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q5_1_q8_1(int64_t k, const void *x, const void *y);
 
 // Exact integer parts of one block product (for pinning GPU partial sums):
 // q4_K: *sum_q = sum_s sc_s * sum_{e in s} q4_e*q8_e, *sum_m = sum_s m_s * sum_{e in s} q8_e.

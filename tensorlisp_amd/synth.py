@@ -75,7 +75,7 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
     """Structurally valid random blocks of a weight type, sized like weights
     quantized from N(0, std) (finite f16 scales, random codes). Used where
     quantizing full-size f32 weights on the host would dominate run time."""
-    from .native import Q4_0, Q8_0, Q4_K, Q5_K, Q6_K
+    from .native import Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K
 
     if wtype == Q8_0:
         return q8_0_config1(seed, M, K)
@@ -114,6 +114,20 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
         blocks = raw.copy()
         blocks[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
         return blocks.reshape(M, (K // 256) * 210)
+    if wtype in (Q4_1, Q5_0, Q5_1):
+        # random code bytes (nibbles and fifth bits); q5_0 a signed d as q4_0,
+        # q4_1 / q5_1 d > 0 with a min m < 0 about half the block's range
+        bb, levels = {Q4_1: (20, 15), Q5_0: (22, 16), Q5_1: (24, 31)}[wtype]
+        nb = M * (K // 32)
+        blocks = bits(seed, (nb * bb + 7) // 8).view(np.uint8)[:nb * bb].reshape(nb, bb).copy()
+        if wtype == Q5_0:
+            d = f16_bits(normal(seed + 1, (nb,), std) / np.float32(levels))
+        else:
+            d = f16_bits(np.abs(normal(seed + 1, (nb,), std)) * np.float32(3 / levels))
+            m = f16_bits(-np.abs(normal(seed + 2, (nb,), std)) * np.float32(1.5))
+            blocks[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        return blocks.reshape(M, (K // 32) * bb)
     raise ValueError(wtype)
 
 

@@ -17,6 +17,12 @@ these are the reference's outputs on fixed inputs, captured once:
   mul_mat.npz      one GGML_OP_MUL_MAT on the CPU backend for the reference test's
                    cases (native.rs:73-107: 96 x 256 weights from noise(seed 1),
                    x = noise(seed 10 + n), n in 1,3,5,8,9,40) per weight type
+  legacy_quants.npz  q4_1, q5_0 and q5_1 (the reference test's other 32-element
+                   types, native.rs:84): ggml_quantize_chunk of its 96 x 256 noise
+                   matrix, dequantize_row_*, one GGML_OP_MUL_MAT per n in 1,3,5,8,9,40;
+                   structurally random blocks (synth seeds 111, 121, 131) against x
+                   (seed + 1, 3 x 1024); quantize_row_q8_1 (src1 of q4_1 / q5_1) on the
+                   activation edge rows and random rows
   mul_mat_float.npz  the same cases with f32, f16 and bf16 weights (ggml_quantize_chunk
                    of the noise matrix), plus f16 / bf16 weights against src1 already
                    of the weight type and a ragged K = 100 (the element-wise path), and
@@ -73,7 +79,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    argmax and 8 largest logits of each step (f32 P.V) and how far the
                    two accumulations move that step's logits.
 Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b
-     | mul_mat_float]   (needs oracle/_ref built)
+     | mul_mat_float | legacy_quants]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -90,6 +96,7 @@ sys.path.insert(0, str(HERE.parents[1]))
 from refs import (DECODER_8B_STEPS, decoder_8b_layer_ref, decoder_8b_ref_run, decoder_8b_slice_config,  # noqa: E402
                   decoder_8b_weights, paged_8b_ref)
 from refs import SDPA_CASES, sdpa_graph, sdpa_inputs  # noqa: E402
+from refs import Q4_1, Q5_0, Q5_1  # noqa: E402
 from refs import (BF16, F16, F32, FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
                   decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, mmid_case, paged_ref_run,
                   xorshift_noise)
@@ -162,6 +169,27 @@ def q6_K_golden(ref) -> None:
 
 def q5_K_golden(ref) -> None:
     kquant_golden(ref, Q5_K, "q5_K", 71, 72)
+
+
+def legacy_quants_golden(ref) -> None:
+    rows, k = 96, 256
+    wn = xorshift_noise((rows, k), 1)
+    ns = [1, 3, 5, 8, 9, 40]
+    out = {"ns": np.array(ns)}
+    for t, name, seed in ((Q4_1, "q4_1", 111), (Q5_0, "q5_0", 121), (Q5_1, "q5_1", 131)):
+        q = ref.quantize_weights(t, wn)
+        out[f"{name}_w"] = q
+        out[f"{name}_deq"] = ref.dequantize(t, q, k)
+        for n in ns:
+            out[f"{name}_y{n}"] = ref.mul_mat(t, q, rows, k, xorshift_noise((n, k), 10 + n))[0]
+        rw = synth.random_blocks(t, seed, 40, 1024)
+        out[f"{name}_rand_w"] = rw
+        out[f"{name}_rand_deq8"] = ref.dequantize(t, rw[:8], 1024)  # the first 8 rows
+        out[f"{name}_rand_y"] = ref.mul_mat(t, rw, 40, 1024, synth.normal(seed + 1, (3, 1024)))[0]
+    x = np.concatenate([edge_rows_act(1024), synth.normal(141, (6, 1024))]).astype(np.float32)
+    out["act_x"] = x
+    out["q8_1"] = ref.quantize_act(Q4_1, x)
+    np.savez_compressed(HERE / "legacy_quants.npz", **out)
 
 
 def mul_mat_float_golden(ref) -> None:
@@ -271,6 +299,9 @@ def main() -> None:
     if sys.argv[1:] == ["decoder_8b"]:  # only the 8B-shaped decoder fixture
         decoder_8b_golden(ref)
         return
+    if sys.argv[1:] == ["legacy_quants"]:  # only the q4_1 / q5_0 / q5_1 fixture
+        legacy_quants_golden(ref)
+        return
     if sys.argv[1:] == ["mul_mat_float"]:  # only the float-weight MUL_MAT fixture
         mul_mat_float_golden(ref)
         return
@@ -362,6 +393,7 @@ def main() -> None:
     decoder_8b_golden(ref)
     mul_mat_id_golden(ref)
     mul_mat_float_golden(ref)
+    legacy_quants_golden(ref)
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

@@ -23,10 +23,12 @@ REF_SO = ROOT / "oracle" / "_ref" / "libggml_ref.so"
 
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 30
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
-VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+Q4_1, Q5_0, Q5_1, Q8_1 = 3, 6, 7, 9
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292),
+         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_1: (32, 36)}
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_0: Q8_0, Q5_1: Q8_1}
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32", F16: "f16",
-         BF16: "bf16"}
+         BF16: "bf16", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q8_1: "q8_1"}
 
 
 FLOAT_BYTES = {F32: 4, F16: 2, BF16: 2}  # element sizes of the float weight types
@@ -106,11 +108,13 @@ class Oracle:
         for name in ("tlq_quantize_row_q4_0", "tlq_quantize_row_q4_K", "tlq_quantize_row_q8_0",
                      "tlq_quantize_row_q8_K", "tlq_dequantize_row_q4_0", "tlq_dequantize_row_q8_0",
                      "tlq_dequantize_row_q4_K", "tlq_dequantize_row_q5_K", "tlq_dequantize_row_q6_K",
-                     "tlq_dequantize_row_q8_K"):
+                     "tlq_dequantize_row_q8_K", "tlq_quantize_row_q8_1", "tlq_dequantize_row_q4_1",
+                     "tlq_dequantize_row_q5_0", "tlq_dequantize_row_q5_1"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("tlq_vec_dot_q4_0_q8_0", "tlq_vec_dot_q8_0_q8_0", "tlq_vec_dot_q4_K_q8_K",
-                     "tlq_vec_dot_q5_K_q8_K", "tlq_vec_dot_q6_K_q8_K"):
+                     "tlq_vec_dot_q5_K_q8_K", "tlq_vec_dot_q6_K_q8_K", "tlq_vec_dot_q4_1_q8_1",
+                     "tlq_vec_dot_q5_0_q8_0", "tlq_vec_dot_q5_1_q8_1"):
             getattr(L, name).argtypes = [i64, vp, vp]
             getattr(L, name).restype = C.c_float
         L.tlq_fp16_to_fp32_row.argtypes = [vp, vp, i64]
@@ -174,7 +178,8 @@ class Oracle:
         rows, k = x.shape
         out = np.zeros((rows, row_bytes(t, k)), np.uint8)
         fn = {Q4_0: self.lib.tlq_quantize_row_q4_0, Q4_K: self.lib.tlq_quantize_row_q4_K,
-              Q8_0: self.lib.tlq_quantize_row_q8_0, Q8_K: self.lib.tlq_quantize_row_q8_K}[t]
+              Q8_0: self.lib.tlq_quantize_row_q8_0, Q8_K: self.lib.tlq_quantize_row_q8_K,
+              Q8_1: self.lib.tlq_quantize_row_q8_1}[t]
         fn(_p(x), _p(out), rows * k)
         return out
 
@@ -188,7 +193,8 @@ class Oracle:
         fn = {Q4_0: self.lib.tlq_dequantize_row_q4_0, Q8_0: self.lib.tlq_dequantize_row_q8_0,
               Q4_K: self.lib.tlq_dequantize_row_q4_K, Q5_K: self.lib.tlq_dequantize_row_q5_K,
               Q6_K: self.lib.tlq_dequantize_row_q6_K,
-              Q8_K: self.lib.tlq_dequantize_row_q8_K}[t]
+              Q8_K: self.lib.tlq_dequantize_row_q8_K, Q4_1: self.lib.tlq_dequantize_row_q4_1,
+              Q5_0: self.lib.tlq_dequantize_row_q5_0, Q5_1: self.lib.tlq_dequantize_row_q5_1}[t]
         fn(_p(q), _p(out), rows * k)
         return out
 
@@ -197,7 +203,8 @@ class Oracle:
         yrow = np.ascontiguousarray(yrow, dtype=np.uint8)
         fn = {Q4_0: self.lib.tlq_vec_dot_q4_0_q8_0, Q8_0: self.lib.tlq_vec_dot_q8_0_q8_0,
               Q4_K: self.lib.tlq_vec_dot_q4_K_q8_K, Q5_K: self.lib.tlq_vec_dot_q5_K_q8_K,
-              Q6_K: self.lib.tlq_vec_dot_q6_K_q8_K}[wtype]
+              Q6_K: self.lib.tlq_vec_dot_q6_K_q8_K, Q4_1: self.lib.tlq_vec_dot_q4_1_q8_1,
+              Q5_0: self.lib.tlq_vec_dot_q5_0_q8_0, Q5_1: self.lib.tlq_vec_dot_q5_1_q8_1}[wtype]
         return float(fn(k, _p(xrow), _p(yrow)))
 
     def block_ints_q4_K(self, xblock, yblock):
@@ -344,11 +351,13 @@ class Ref:
         vp, i64 = C.c_void_p, C.c_int64
         for name in ("quantize_row_q8_0", "quantize_row_q8_K", "quantize_row_q8_0_ref", "quantize_row_q8_K_ref",
                      "quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "dequantize_row_q4_0",
-                     "dequantize_row_q8_0", "dequantize_row_q4_K", "dequantize_row_q5_K", "dequantize_row_q6_K"):
+                     "dequantize_row_q8_0", "dequantize_row_q4_K", "dequantize_row_q5_K", "dequantize_row_q6_K",
+                     "quantize_row_q8_1", "dequantize_row_q4_1", "dequantize_row_q5_0", "dequantize_row_q5_1"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("ggml_vec_dot_q4_0_q8_0", "ggml_vec_dot_q8_0_q8_0", "ggml_vec_dot_q4_K_q8_K",
-                     "ggml_vec_dot_q5_K_q8_K", "ggml_vec_dot_q6_K_q8_K"):
+                     "ggml_vec_dot_q5_K_q8_K", "ggml_vec_dot_q6_K_q8_K", "ggml_vec_dot_q4_1_q8_1",
+                     "ggml_vec_dot_q5_0_q8_0", "ggml_vec_dot_q5_1_q8_1"):
             getattr(L, name).argtypes = [C.c_int, C.POINTER(C.c_float), C.c_size_t, vp, C.c_size_t, vp, C.c_size_t,
                                          C.c_int]
             getattr(L, name).restype = None
@@ -406,7 +415,7 @@ class Ref:
         rows, k = x.shape
         t = VEC_DOT_TYPE[wtype]
         out = np.zeros((rows, row_bytes(t, k)), np.uint8)
-        fn = self.lib.quantize_row_q8_0 if t == Q8_0 else self.lib.quantize_row_q8_K
+        fn = {Q8_0: self.lib.quantize_row_q8_0, Q8_K: self.lib.quantize_row_q8_K, Q8_1: self.lib.quantize_row_q8_1}[t]
         for r in range(rows):
             fn(_p(x[r]), out[r].ctypes.data_as(C.c_void_p), k)
         return out
@@ -417,7 +426,8 @@ class Ref:
         out = np.empty((rows, k), np.float32)
         fn = {Q4_0: self.lib.dequantize_row_q4_0, Q8_0: self.lib.dequantize_row_q8_0,
               Q4_K: self.lib.dequantize_row_q4_K, Q5_K: self.lib.dequantize_row_q5_K,
-              Q6_K: self.lib.dequantize_row_q6_K}[t]
+              Q6_K: self.lib.dequantize_row_q6_K, Q4_1: self.lib.dequantize_row_q4_1,
+              Q5_0: self.lib.dequantize_row_q5_0, Q5_1: self.lib.dequantize_row_q5_1}[t]
         fn(_p(q), _p(out), rows * k)
         return out
 
@@ -427,7 +437,8 @@ class Ref:
         s = C.c_float()
         fn = {Q4_0: self.lib.ggml_vec_dot_q4_0_q8_0, Q8_0: self.lib.ggml_vec_dot_q8_0_q8_0,
               Q4_K: self.lib.ggml_vec_dot_q4_K_q8_K, Q5_K: self.lib.ggml_vec_dot_q5_K_q8_K,
-              Q6_K: self.lib.ggml_vec_dot_q6_K_q8_K}[wtype]
+              Q6_K: self.lib.ggml_vec_dot_q6_K_q8_K, Q4_1: self.lib.ggml_vec_dot_q4_1_q8_1,
+              Q5_0: self.lib.ggml_vec_dot_q5_0_q8_0, Q5_1: self.lib.ggml_vec_dot_q5_1_q8_1}[wtype]
         fn(k, C.byref(s), 0, _p(xrow), 0, _p(yrow), 0, 1)
         return float(s.value)
 

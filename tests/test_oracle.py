@@ -18,8 +18,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import (BF16, F16, F32, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, fp16_probe_values, oracle, ref,
-                  row_bytes)
+from refs import (BF16, F16, F32, NAMES, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, Q8_1, Q8_K, fp16_probe_values,
+                  oracle, ref, row_bytes)
 from tensorlisp_amd import synth
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -365,6 +365,124 @@ def test_q5_K_matches_reference_live():
         assert same_bits(o.mul_mat(Q5_K, w, M, K, x), y)
         y, _ = r.mul_mat(Q5_K, wq, 8, K, x)
         assert same_bits(o.mul_mat(Q5_K, wq, 8, K, x), y)
+
+
+# ---------------------------------------------- q4_1 / q5_0 / q5_1 and q8_1
+# tlq_dequantize_row_q4_1 / _q5_0 / _q5_1 (ggml-quants.c:479-551),
+# tlq_quantize_row_q8_1 (:302-335) and the generic vec_dots
+# (ggml-cpu/quants.c:262-296, :365-449): pinned by the compiled reference's
+# outputs (legacy_quants.npz), bit-exact; an independent numpy unpacking of the
+# codes; q8_1's s against numpy's float16 cast; float64 brute force; the live
+# reference.
+LEGACY = ((Q4_1, "q4_1", 111), (Q5_0, "q5_0", 121), (Q5_1, "q5_1", 131))
+LEGACY_IDS = [n for _, n, _ in LEGACY]
+
+
+@pytest.mark.parametrize("t,name,seed", LEGACY, ids=LEGACY_IDS)
+def test_legacy_quants_golden(t, name, seed):
+    from refs import xorshift_noise
+
+    o, g = oracle(), gold("legacy_quants")
+    assert same_bits(o.dequantize(t, g[f"{name}_w"], 256), g[f"{name}_deq"])
+    for n in g["ns"]:
+        y = o.mul_mat(t, g[f"{name}_w"], 96, 256, xorshift_noise((int(n), 256), 10 + int(n)))
+        assert same_bits(y, g[f"{name}_y{n}"]), n
+    rw = synth.random_blocks(t, seed, 40, 1024)
+    assert np.array_equal(rw, g[f"{name}_rand_w"])  # the generator still makes the fixture's blocks
+    assert same_bits(o.dequantize(t, rw[:8], 1024), g[f"{name}_rand_deq8"])
+    assert same_bits(o.mul_mat(t, rw, 40, 1024, synth.normal(seed + 1, (3, 1024))), g[f"{name}_rand_y"])
+
+
+def test_q8_1_golden_and_against_numpy():
+    """q8_1 = q8_0's f16 d and codes, plus s = f16(code sum * the f32 d): the codes
+    and d against the (separately pinned) q8_0 quantizer, s rebuilt with
+    numpy's float16 cast from the codes and amax / 127."""
+    o, g = oracle(), gold("legacy_quants")
+    x = g["act_x"]
+    q = o.quantize(Q8_1, x)
+    assert np.array_equal(q, g["q8_1"])
+    b1, b0 = q.reshape(-1, 36), o.quantize(Q8_0, x).reshape(-1, 34)
+    assert np.array_equal(b1[:, 0:2], b0[:, 0:2]) and np.array_equal(b1[:, 4:], b0[:, 2:])
+    d32 = (np.abs(x).reshape(-1, 32).max(1) / np.float32(127)).astype(np.float32)
+    sums = b1[:, 4:].view(np.int8).astype(np.int32).sum(1).astype(np.float32)
+    with np.errstate(over="ignore"):  # the 1e4-scaled row's sums overflow f16 to inf, as ggml's do
+        want = (sums * d32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(b1[:, 2:4].copy().view(np.uint16)[:, 0], want)
+
+
+def _legacy_fields(t, w):
+    """(d, m, codes) of q4_1 / q5_0 / q5_1 blocks by numpy, from the block
+    layouts of ggml-common.h:201-249 (m = 0 for q5_0, codes with q5_0's -16)."""
+    bb = {Q4_1: 20, Q5_0: 22, Q5_1: 24}[t]
+    b = w.reshape(-1, bb)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    m = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0] if t != Q5_0 else np.zeros_like(d)
+    qs = b[:, bb - 16:].astype(np.int64)
+    codes = np.concatenate([qs & 15, qs >> 4], axis=1)
+    if t != Q4_1:
+        qh = b[:, bb - 20: bb - 16].copy().view(np.uint32)[:, 0].astype(np.int64)
+        codes |= ((qh[:, None] >> np.arange(32)) & 1) << 4
+    if t == Q5_0:
+        codes -= 16
+    return d, m, codes
+
+
+@pytest.mark.parametrize("t,name,seed", LEGACY, ids=LEGACY_IDS)
+def test_legacy_codes_against_an_independent_unpacking(t, name, seed):
+    """y = code * d (+ m) in f32 with the codes rebuilt here over whole arrays,
+    bit-exact; every code value occurs."""
+    o = oracle()
+    w = synth.random_blocks(t, seed + 5, 12, 512)
+    d, m, codes = _legacy_fields(t, w)
+    want = (codes.astype(np.float32) * d[:, None]).astype(np.float32)
+    if t != Q5_0:
+        want = (want + m[:, None]).astype(np.float32)
+    lo, hi = {Q4_1: (0, 15), Q5_0: (-16, 15), Q5_1: (0, 31)}[t]
+    assert codes.min() == lo and codes.max() == hi
+    assert same_bits(o.dequantize(t, w, 512).reshape(-1, 32), want)
+
+
+@pytest.mark.parametrize("t,name,seed", LEGACY, ids=LEGACY_IDS)
+def test_legacy_vec_dot_against_f64_bruteforce(t, name, seed):
+    """vec_dot = the float64 sum of the dequantized weights times the activation
+    values d8 * q8, up to f32 accumulation and, for q4_1 / q5_1, the f16
+    rounding of q8_1's s (m * s stands for m * d8 * sum q8): a dropped min term,
+    a wrong fifth bit or sign fails."""
+    o = oracle()
+    K = 2048
+    w = synth.random_blocks(t, seed + 6, 8, K)
+    x = synth.normal(seed + 7, (4, K))
+    xq = o.quantize_act(t, x)
+    at = Q8_1 if t != Q5_0 else Q8_0
+    ab = {Q8_1: 36, Q8_0: 34}[at]
+    yb = xq.reshape(4, -1, ab)
+    d8 = yb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    q8 = yb[:, :, ab - 32:].view(np.int8).astype(np.float64)
+    xd = (d8[:, :, None] * q8).reshape(4, K)
+    wd = o.dequantize(t, w, K).astype(np.float64)
+    want = wd @ xd.T
+    got = np.array([[o.vec_dot(t, K, w[i], xq[j]) for j in range(4)] for i in range(8)])
+    tol = 1e-6 * (np.abs(wd) @ np.abs(xd).T)
+    if at == Q8_1:
+        _, m, _ = _legacy_fields(t, w)
+        s8 = np.abs(yb[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0])
+        tol += np.abs(m.reshape(8, -1)) @ s8.T * 2.0 ** -10
+    assert np.all(np.abs(got - want) <= tol)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("t,name,seed", LEGACY, ids=LEGACY_IDS)
+def test_legacy_matches_reference_live(t, name, seed):
+    o, r = oracle(), ref()
+    M, K = 72, 1024
+    w = synth.random_blocks(t, seed + 8, M, K)
+    assert same_bits(o.dequantize(t, w, K), r.dequantize(t, w, K))
+    wq = r.quantize_weights(t, synth.normal(seed + 9, (8, K), 0.02))
+    for n in (1, 2, 9):
+        x = synth.normal(seed + 10 + n, (n, K)) * 3
+        assert np.array_equal(o.quantize_act(t, x), r.quantize_act(t, x))
+        assert same_bits(o.mul_mat(t, w, M, K, x), r.mul_mat(t, w, M, K, x)[0])
+        assert same_bits(o.mul_mat(t, wq, 8, K, x), r.mul_mat(t, wq, 8, K, x)[0])
 
 
 # ------------------------------------------------ float weights (f32 / f16 / bf16)
