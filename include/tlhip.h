@@ -45,7 +45,11 @@ enum {
     TLH_TYPE_F32 = 0,
     TLH_TYPE_F16 = 1,
     TLH_TYPE_Q4_0 = 2,
+    TLH_TYPE_Q4_1 = 3,
+    TLH_TYPE_Q5_0 = 6,
+    TLH_TYPE_Q5_1 = 7,
     TLH_TYPE_Q8_0 = 8,
+    TLH_TYPE_Q8_1 = 9,
     TLH_TYPE_Q4_K = 12,
     TLH_TYPE_Q5_K = 13,
     TLH_TYPE_Q6_K = 14,
@@ -108,15 +112,17 @@ typedef struct tlh_op {
  * GGML_OP_MUL_MAT, replacing Ctx::mul_mat (crates/kernels/src/cuda/lower.rs:543-571)
  * and its mm_vec / mm_tile kernels (crates/kernels/src/cuda/native/mm.cu:16-103),
  * computed the way the ggml CPU backend does (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1254-1457):
- *   op->t[0] src0: weights, type Q4_0 | Q8_0 | Q4_K | Q5_K | Q6_K | F32 | F16 | BF16,
+ *   op->t[0] src0: weights, type Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q4_K | Q5_K | Q6_K |
+ *                  F32 | F16 | BF16,
  *                  ne [K, M, ne02, ne03], nb[0] = block (element) bytes (rows must
  *                  not be transposed);
  *   op->t[1] src1: f32 activations (or, for F16 / BF16 weights, already of the
  *                  weight type), ne [K, N, ne12, ne13], nb[0] = element bytes;
  *   op->t[4] dst:  f32 [M, N, ne12, ne13], nb[0] = 4;
  *   op->x[0] = r2 = ne12 / ne02, op->x[1] = r3 = ne13 / ne03 (broadcast).
- * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0 and
- * Q8_0, Q8_K for Q4_K, Q5_K and Q6_K) into `scratch` (at least tlh_mul_mat_scratch_bytes);
+ * src1 is first quantized to the weight type's vec_dot type (Q8_0 for Q4_0, Q5_0
+ * and Q8_0, Q8_1 for Q4_1 and Q5_1, Q8_K for Q4_K, Q5_K and Q6_K) into `scratch`
+ * (at least tlh_mul_mat_scratch_bytes);
  * then N <= 16 runs the decode GEMV (register kernel for N <= 2, int8-MFMA
  * few-column kernel above), larger N the MFMA GEMM. Integer block
  * sums are exact; the f32 result agrees with the CPU backend to rounding of

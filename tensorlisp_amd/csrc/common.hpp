@@ -10,14 +10,18 @@
 namespace tlh {
 
 // ----------------------------------------------------------- block formats
-// vendor/ggml/src/ggml-common.h:194-198 (q4_0), :251-255 (q8_0), :325-337
-// (q4_K), :345-352 (q5_K), :362-368 (q6_K), :370-375 (q8_K). Byte sizes per
-// block and
-// elements per block.
-constexpr int QK = 32;    // q4_0 / q8_0 block
+// vendor/ggml/src/ggml-common.h:194-198 (q4_0), :201-211 (q4_1), :229-248
+// (q5_0, q5_1), :251-269 (q8_0, q8_1), :325-337 (q4_K), :345-352 (q5_K),
+// :362-368 (q6_K), :370-375 (q8_K). Byte sizes per block and elements per
+// block.
+constexpr int QK = 32;    // q4_0 / q4_1 / q5_0 / q5_1 / q8_0 / q8_1 block
 constexpr int QKK = 256;  // k-quant super-block
 constexpr int Q4_0_BYTES = 18;
 constexpr int Q8_0_BYTES = 34;
+constexpr int Q4_1_BYTES = 20;  // f16 d, f16 m, qs[16] (nibbles: elements j and j + 16)
+constexpr int Q5_0_BYTES = 22;  // f16 d, qh[4] (fifth bits, bit j of element j), qs[16]
+constexpr int Q5_1_BYTES = 24;  // f16 d, f16 m, qh[4], qs[16]
+constexpr int Q8_1_BYTES = 36;  // f16 d, f16 s (= code sum * d), qs[32]
 constexpr int Q4_K_BYTES = 144;
 constexpr int Q5_K_BYTES = 176;  // f16 d, dmin; scales[12] as q4_K; qh[32] (fifth bits); qs[128] (low nibbles)
 constexpr int Q6_K_BYTES = 210;  // ql[128] (low 4 bits), qh[64] (high 2 bits), int8 scales[16], f16 d
@@ -25,8 +29,10 @@ constexpr int Q8_K_BYTES = 292;
 
 __host__ __device__ constexpr int block_elems(int t) {
     return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K || t == TLH_TYPE_Q8_K) ? QKK
-           : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0)                      ? QK
-                                                                             : 1;
+           : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_1 || t == TLH_TYPE_Q5_0 ||
+              t == TLH_TYPE_Q5_1 || t == TLH_TYPE_Q8_1)
+               ? QK
+               : 1;
 }
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == TLH_TYPE_Q4_0   ? Q4_0_BYTES
@@ -35,12 +41,27 @@ __host__ __device__ constexpr int block_bytes(int t) {
            : t == TLH_TYPE_Q5_K ? Q5_K_BYTES
            : t == TLH_TYPE_Q6_K ? Q6_K_BYTES
            : t == TLH_TYPE_Q8_K ? Q8_K_BYTES
+           : t == TLH_TYPE_Q4_1 ? Q4_1_BYTES
+           : t == TLH_TYPE_Q5_0 ? Q5_0_BYTES
+           : t == TLH_TYPE_Q5_1 ? Q5_1_BYTES
+           : t == TLH_TYPE_Q8_1 ? Q8_1_BYTES
            : t == TLH_TYPE_F16  ? 2
                                 : 4;
 }
 // vec_dot_type on x86 (vendor/ggml/src/ggml-cpu/ggml-cpu.c:239-319).
 __host__ __device__ constexpr int vec_dot_type(int wtype) {
-    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K : TLH_TYPE_Q8_0;
+    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K
+           : (wtype == TLH_TYPE_Q4_1 || wtype == TLH_TYPE_Q5_1)                          ? TLH_TYPE_Q8_1
+                                                                                          : TLH_TYPE_Q8_0;
+}
+// 32-element block types that carry a min (q4_1, q5_1: x = q * d + m) or a
+// fifth code bit (q5_0, q5_1)
+__host__ __device__ constexpr bool has_min(int wtype) { return wtype == TLH_TYPE_Q4_1 || wtype == TLH_TYPE_Q5_1; }
+__host__ __device__ constexpr bool has_qh(int wtype) { return wtype == TLH_TYPE_Q5_0 || wtype == TLH_TYPE_Q5_1; }
+// Byte offsets in a 32-element block: the min, the fifth bits, the nibbles
+__host__ __device__ constexpr int blk_qh_off(int wtype) { return wtype == TLH_TYPE_Q5_1 ? 4 : 2; }
+__host__ __device__ constexpr int blk_qs_off(int wtype) {
+    return wtype == TLH_TYPE_Q4_1 ? 4 : wtype == TLH_TYPE_Q5_0 ? 6 : wtype == TLH_TYPE_Q5_1 ? 8 : 2;
 }
 
 // ---------------------------------------------------------- conversions
@@ -71,15 +92,33 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
+// Four bits (of a q5 block's qh word) to bit 4 of four bytes: bit i lands at
+// bit 8i by the multiply (the shifted copies never overlap), then moves up 4.
+__device__ __forceinline__ uint32_t spread4(uint32_t b4) { return ((b4 * 0x00204081u) & 0x01010101u) << 4; }
+
 // ------------------------------------------------------ element dequantizers
 // Element `col` of a row of ggml blocks of type WT, rounded as the reference's
 // dequantize_row_* rounds it (integer codes convert exactly): q4_0
 // (q-8)*d (ggml-quants.c:459-476), q8_0 q*d (:553-565), q4_K (d*sc)*q -
 // (dmin*m) (:1529-1550), q5_K the same with a fifth code bit (:1731-1756),
-// q6_K (d*sc)*q (:1939-1968).
+// q6_K (d*sc)*q (:1939-1968), q4_1 q*d + m (:479-498), q5_0 (q-16)*d
+// (:500-524), q5_1 q*d + m (:526-551).
 template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r, int64_t col) {
 #pragma clang fp contract(off)
-    if constexpr (WT == TLH_TYPE_Q4_0) {
+    if constexpr (WT == TLH_TYPE_Q4_1 || WT == TLH_TYPE_Q5_0 || WT == TLH_TYPE_Q5_1) {
+        const uint8_t *b = r + (col / QK) * block_bytes(WT);
+        const int j = (int)(col % QK);
+        const uint8_t byte = b[blk_qs_off(WT) + (j & 15)];
+        int code = j < 16 ? (byte & 0x0f) : (byte >> 4);
+        if constexpr (has_qh(WT)) {
+            uint32_t qh;
+            __builtin_memcpy(&qh, b + blk_qh_off(WT), 4);
+            code |= (int)((qh >> j) & 1u) << 4;
+        }
+        const float d = h2f(*(const uint16_t *)b);
+        if constexpr (WT == TLH_TYPE_Q5_0) return (float)(code - 16) * d;
+        else return (float)code * d + h2f(*(const uint16_t *)(b + 2));
+    } else if constexpr (WT == TLH_TYPE_Q4_0) {
         const uint8_t *b = r + (col / QK) * Q4_0_BYTES;
         const int j = (int)(col % QK);
         const float d = h2f(*(const uint16_t *)b);
@@ -127,15 +166,16 @@ template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r
 // a split layout the kernels can stream with aligned 128-bit loads: for R
 // activation rows of K values,
 //   qs  : int8  [R][K]            codes, 64-byte aligned rows
-//   d   : f32   [R][K/blk]        block scales (q8_0: the f16-rounded d as f32)
+//   d   : f32   [R][K/blk]        block scales (q8_0 / q8_1: the f16-rounded d as f32)
 //   sum : int32 [R][K/32] (q8_0)  per-block code sums
+//         f32   [R][K/32] (q8_1)  per-block s (f16-rounded code sum * d, as f32)
 //         int16 [R][K/16] (q8_K)  bsums
 //   q16 : f16   [R][K]            (GEMM launches only) the codes as f16,
 //         exact, so the MFMA operand needs no conversion
 struct ActView {
     const int8_t *qs;
     const float *d;
-    const int32_t *sum32;  // q8_0 only
+    const int32_t *sum32;  // q8_0: code sums; q8_1: the bits of s as f32
     const int16_t *bsums;  // q8_K only
     const _Float16 *q16;   // GEMM launches only
     int64_t K;

@@ -611,6 +611,9 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_BF16: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_BF16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_1: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_1>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q5_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_1: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q5_1>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;
@@ -634,6 +637,9 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_F16: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_F16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_BF16: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_BF16>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q4_1: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_1>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q5_0>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q5_1: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q5_1>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;

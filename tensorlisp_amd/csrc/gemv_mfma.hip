@@ -90,9 +90,11 @@ template <int WT> constexpr int unit_bytes() {
     return WT == TLH_TYPE_Q4_K   ? Q4_K_BYTES
            : WT == TLH_TYPE_Q5_K ? Q5_K_BYTES
            : WT == TLH_TYPE_Q6_K ? Q6_K_BYTES
-           : WT == TLH_TYPE_Q4_0 ? 8 * Q4_0_BYTES
-                                 : 8 * Q8_0_BYTES;
+                                 : 8 * block_bytes(WT);
 }
+// 32-element block types whose codes are nibbles (q5: plus a fifth bit):
+// a lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16 + 4g.. (high)
+template <int WT> constexpr bool nibble_type() { return WT == TLH_TYPE_Q4_0 || legacy_type(WT); }
 // Bytes of a unit staged through LDS (a multiple of 16): all of it, but for
 // q6_K its first 208 (ql, qh, scales; d, the last 2 bytes, is loaded apart).
 template <int WT> constexpr int staged_bytes() { return WT == TLH_TYPE_Q6_K ? 208 : unit_bytes<WT>(); }
@@ -157,27 +159,89 @@ template <> struct UnitW<TLH_TYPE_Q6_K> {
     }
 };
 
+// blk0: the unit's first block; the `nb` valid blocks of the unit are read
+// (blocks past them reread the last valid one: a row's last unit may end
+// early, and its bytes past the row are not the row's)
 template <> struct UnitW<TLH_TYPE_Q8_0> {
     uint2 q[8];
     uint16_t d[8];
-    // blk0: the unit's first block; blocks past `nb` valid ones are not read (global) / garbage (LDS)
-    __device__ __forceinline__ void load(const uint8_t *blk0, int g) {
+    __device__ __forceinline__ void load(const uint8_t *blk0, int g, int nb) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            d[j] = ldu<uint16_t>(blk0 + j * Q8_0_BYTES);
-            q[j] = ldu<uint2>(blk0 + j * Q8_0_BYTES + 2 + 8 * g);
+            const uint8_t *b = blk0 + (j < nb ? j : nb - 1) * Q8_0_BYTES;
+            d[j] = ldu<uint16_t>(b);
+            q[j] = ldu<uint2>(b + 2 + 8 * g);
         }
     }
 };
 
+// q4_1 / q5_0 / q5_1: per block the f16 d (and m) word, the fifth bits and
+// nibble bytes 4g..4g+3
+template <int WT> struct UnitWLegacy {
+    uint32_t q[8], dm[8], qh[8];
+    __device__ __forceinline__ void load(const uint8_t *blk0, int g, int nb) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t *b = blk0 + (j < nb ? j : nb - 1) * block_bytes(WT);
+            dm[j] = ldu<uint32_t>(b);
+            qh[j] = has_qh(WT) ? ldu<uint32_t>(b + blk_qh_off(WT)) : 0u;
+            q[j] = ldu<uint32_t>(b + blk_qs_off(WT) + 4 * g);
+        }
+    }
+};
+template <> struct UnitW<TLH_TYPE_Q4_1> : UnitWLegacy<TLH_TYPE_Q4_1> {};
+template <> struct UnitW<TLH_TYPE_Q5_0> : UnitWLegacy<TLH_TYPE_Q5_0> {};
+template <> struct UnitW<TLH_TYPE_Q5_1> : UnitWLegacy<TLH_TYPE_Q5_1> {};
+
+// The weight operand of one q4_1 / q5_0 / q5_1 block for lane group g from its
+// nibble bytes 4g..4g+3 (v) and qh: codes as int8 (q5_0: q - 16, no borrows
+// with the byte-wise bias trick)
+template <int WT> __device__ __forceinline__ long legacy_B(uint32_t v, uint32_t qh, int g) {
+    uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
+    if constexpr (has_qh(WT)) {
+        lo |= spread4((qh >> (4 * g)) & 0xfu);
+        hi |= spread4((qh >> (16 + 4 * g)) & 0xfu);
+    }
+    if constexpr (WT == TLH_TYPE_Q5_0) {
+        lo = ((lo | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
+        hi = ((hi | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
+    }
+    return pack2(lo, hi);
+}
+
+// One q4_1 / q5_0 / q5_1 block: y[r] += (d * d8) * sumi (+ m * s8), the CPU's
+// per-block step (ggml-cpu/quants.c:262-296, :365-449); dm: the block's f16 d
+// (and m) word; sdb / ssb: the block's activation d8 / s8 [16 columns].
+template <int WT>
+__device__ __forceinline__ void block_mma_legacy(long A, long B, uint32_t dm, const float *sdb, const float *ssb,
+                                                 int g, float (&y)[4]) {
+#pragma clang fp contract(off)
+    const v4i zero = {0, 0, 0, 0};
+    const v4i Sb = mfma_i8(A, B, zero);
+    const float dw = h2f((uint16_t)(dm & 0xffff));
+    const float4 d8 = *(const float4 *)(sdb + 4 * g);
+    const float d8r[4] = {d8.x, d8.y, d8.z, d8.w};
+    if constexpr (has_min(WT)) {
+        const float mw = h2f((uint16_t)(dm >> 16));
+        const float4 s8 = *(const float4 *)(ssb + 4 * g);
+        const float s8r[4] = {s8.x, s8.y, s8.z, s8.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] += (dw * d8r[r]) * (float)Sb[r] + mw * s8r[r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] += (dw * d8r[r]) * (float)Sb[r];
+    }
+}
+
 template <> struct UnitW<TLH_TYPE_Q4_0> {
     uint32_t q[8];
     uint16_t d[8];
-    __device__ __forceinline__ void load(const uint8_t *blk0, int g) {
+    __device__ __forceinline__ void load(const uint8_t *blk0, int g, int nb) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            d[j] = ldu<uint16_t>(blk0 + j * Q4_0_BYTES);
-            q[j] = ldu<uint32_t>(blk0 + j * Q4_0_BYTES + 2 + 4 * g);
+            const uint8_t *b = blk0 + (j < nb ? j : nb - 1) * Q4_0_BYTES;
+            d[j] = ldu<uint16_t>(b);
+            q[j] = ldu<uint32_t>(b + 2 + 4 * g);
         }
     }
 };
@@ -245,8 +309,8 @@ __device__ __forceinline__ void unit_mma_q6k(const UnitW<TLH_TYPE_Q6_K> &w, uint
 // (q4_K one slot, q4_0 / q8_0 one per block) as [slot][16 columns];
 // nvalid: blocks of the unit inside K (q4_0 / q8_0).
 template <int WT>
-__device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8], const float *sdu, int g,
-                                         int nvalid, float (&y)[4]) {
+__device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8], const float *sdu, const float *ssu,
+                                         int g, int nvalid, float (&y)[4]) {
     const v4i zero = {0, 0, 0, 0};
     if constexpr (WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K) {
         const uint4 h = w.hdr;
@@ -278,6 +342,13 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
         const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
+    } else if constexpr (legacy_type(WT)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j >= nvalid) continue;  // wave-uniform
+            block_mma_legacy<WT>(A[j], legacy_B<WT>(w.q[j], w.qh[j], g), w.dm[j], sdu + j * SK_COLS,
+                                 ssu + j * SK_COLS, g, y);
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -305,13 +376,18 @@ template <int WT, int KS> struct Stage {
     uint32_t dq;  // q6_K: the lane's row's d (KS = 1)
 };
 
-// Direct loads of KS units (prefetch set of the unstaged kernel). Units
-// past `last` reread unit `last` (their products are skipped).
+// Direct loads of KS units (prefetch set of the unstaged kernel, 32-element
+// block types). Units past `last` reread unit `last` (their products are
+// skipped); a unit reads only its blocks below `nblk`.
 template <int WT, int KS> struct DirectW {
     UnitW<WT> u[KS];
-    __device__ __forceinline__ void load(const uint8_t *row, int64_t u0, int64_t last, int g) {
+    __device__ __forceinline__ void load(const uint8_t *row, int64_t u0, int64_t last, int64_t nblk, int g) {
 #pragma unroll
-        for (int t = 0; t < KS; ++t) u[t].load(row + (u0 + t < last ? u0 + t : last) * unit_bytes<WT>(), g);
+        for (int t = 0; t < KS; ++t) {
+            const int64_t uu = u0 + t < last ? u0 + t : last;
+            const int64_t nb = nblk - 8 * uu;
+            u[t].load(row + uu * unit_bytes<WT>(), g, (int)(nb < 8 ? nb : 8));
+        }
     }
 };
 
@@ -354,9 +430,12 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // launch's scale slots [s_end - s_begin][16 columns], the outputs of up
     // to SK_OUTBUF row groups [SK_OUTBUF][256], then (STAGED) one weight
     // buffer per wave.
+    // q8_1 activations (q4_1 / q5_1) add their s values, as many slots again
+    constexpr bool S8 = AT == TLH_TYPE_Q8_1;
     float4 *red = (float4 *)sk_lds;
     float *sd = (float *)(sk_lds + 2 * nw * 64 * sizeof(float4));
-    float *obuf = sd + (s_end - s_begin) * SK_COLS;
+    float *ss = sd + (s_end - s_begin) * SK_COLS;
+    float *obuf = ss + (S8 ? (s_end - s_begin) * SK_COLS : 0);
     uint8_t *wbuf = (uint8_t *)(obuf + SK_OUTBUF * 256) + (size_t)wave * St::BUF;
 
     const int64_t groups = (a.M + 15) / 16;
@@ -411,7 +490,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     DirectW<WT, KS> da, db;
     const int64_t rg0 = rg < groups ? rg : groups - 1;
     if constexpr (STAGED) stage_load(st, rg0);
-    else da.load(wrow_of(rg0), u0, (s_end - 1) / (KQ ? 1 : 8), g);
+    else da.load(wrow_of(rg0), u0, (s_end - 1) / (KQ ? 1 : 8), s_end, g);
 
     // activation operands of this wave's units (zero past N and past the range)
     long A[KS][8];
@@ -426,7 +505,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
                 const bool ok = col_ok && e < 256 * u_end && e < K;
                 const int64_t ec = ok ? e : 0;
                 long v;
-                if constexpr (WT == TLH_TYPE_Q4_0) {
+                if constexpr (nibble_type<WT>()) {
                     // the lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16+4g.. (high)
                     v = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
                 } else {
@@ -438,6 +517,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const int64_t b = s_begin + (i >> 4);
             const int c = (int)(i & 15);
             sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
+            if constexpr (S8) ss[i] = c < N ? __int_as_float(act.sum32[(arow0 + c) * nblk + b]) : 0.0f;
         }
     }
     lds_barrier();
@@ -492,6 +572,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     };
 
     auto unit_slots = [&](int t) { return sd + (KQ ? (u0 + t - s_begin) : 8 * (u0 + t) - s_begin) * SK_COLS; };
+    const int64_t s_gap = ss - sd;  // an s slot sits this far after its d slot
     auto unit_nvalid = [&](int t) {
         const int64_t v = s_end - 8 * (u0 + t);
         return KQ ? 8 : (int)(v < 0 ? 0 : v > 8 ? 8 : v);
@@ -510,7 +591,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             } else if constexpr (KQ) {
                 UnitW<WT> w;
                 w.load_lds(wbuf + ub, g);
-                unit_mma<WT>(w, A[t], unit_slots(t), g, 8, y);
+                unit_mma<WT>(w, A[t], unit_slots(t), nullptr, g, 8, y);
             } else {
                 // block by block: the operands of one block live at a time
                 const int nv = unit_nvalid(t);
@@ -521,6 +602,14 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
                 for (int j = 0; j < 8; ++j) {
                     if (j >= nv) continue;  // wave-uniform
                     const uint32_t blk = ub + j * block_bytes(WT);
+                    if constexpr (legacy_type(WT)) {
+                        const uint32_t v = lds_u32(w32, blk + blk_qs_off(WT) + 4 * g);
+                        const uint32_t qh = has_qh(WT) ? lds_u32(w32, blk + blk_qh_off(WT)) : 0u;
+                        block_mma_legacy<WT>(A[t][j], legacy_B<WT>(v, qh, g), lds_u32(w32, blk), sdu + j * SK_COLS,
+                                             sdu + s_gap + j * SK_COLS, g, y);
+                        __builtin_amdgcn_sched_barrier(0);
+                        continue;
+                    }
                     long B;
                     if constexpr (WT == TLH_TYPE_Q4_0) {
                         const uint32_t v = lds_u32(w32, blk + 2 + 4 * g);
@@ -544,7 +633,8 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
-            if constexpr (WT != TLH_TYPE_Q6_K) unit_mma<WT>(d.u[t], A[t], unit_slots(t), g, unit_nvalid(t), y);
+            if constexpr (WT != TLH_TYPE_Q6_K)
+                unit_mma<WT>(d.u[t], A[t], unit_slots(t), unit_slots(t) + s_gap, g, unit_nvalid(t), y);
         }
         finish(y, grp, parity);
     };
@@ -571,11 +661,11 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         for (;;) {
             if (rg >= groups) break;
             const int64_t r1 = rg + gridDim.x;
-            db.load(wrow_of(r1 < groups ? r1 : rg), u0, dlast, g);
+            db.load(wrow_of(r1 < groups ? r1 : rg), u0, dlast, s_end, g);
             process_direct(da, rg, 0);
             if (r1 >= groups) break;
             const int64_t r2 = r1 + gridDim.x;
-            da.load(wrow_of(r2 < groups ? r2 : r1), u0, dlast, g);
+            da.load(wrow_of(r2 < groups ? r2 : r1), u0, dlast, s_end, g);
             process_direct(db, r1, 1);
             rg = r2;
         }
@@ -630,7 +720,8 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     if (chunks > 1 && !a.part) return set_error(TLH_INVALID, "gemv_mfma: K=%lld needs a partials buffer", (long long)a.K);
     // at least 4 waves: the first 256 threads each own one of a row group's outputs
     const int nw = (int)((share + KS - 1) / KS) > 4 ? (int)((share + KS - 1) / KS) : 4;
-    const size_t lds = (size_t)2 * nw * 64 * 16 + (size_t)(kquant<WT>() ? share : 8 * share) * SK_COLS * 4 +
+    const size_t slots = (size_t)(kquant<WT>() ? share : 8 * share) * SK_COLS * 4;
+    const size_t lds = (size_t)2 * nw * 64 * 16 + slots * (vec_dot_type(WT) == TLH_TYPE_Q8_1 ? 2 : 1) +
                        (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0);
     static int cached_nw = -1, blocks_per_cu = 1, cus = 0;
     if (cached_nw != nw) {
@@ -671,6 +762,9 @@ tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     switch (a.wtype) {
     case TLH_TYPE_Q4_0: return launch_sk_wt<TLH_TYPE_Q4_0>(a, staged, stream);
     case TLH_TYPE_Q8_0: return launch_sk_wt<TLH_TYPE_Q8_0>(a, staged, stream);
+    case TLH_TYPE_Q4_1: return launch_sk_wt<TLH_TYPE_Q4_1>(a, staged, stream);
+    case TLH_TYPE_Q5_0: return launch_sk_wt<TLH_TYPE_Q5_0>(a, staged, stream);
+    case TLH_TYPE_Q5_1: return launch_sk_wt<TLH_TYPE_Q5_1>(a, staged, stream);
     case TLH_TYPE_Q4_K: return launch_sk_wt<TLH_TYPE_Q4_K>(a, staged, stream);
     case TLH_TYPE_Q5_K: return launch_sk_wt<TLH_TYPE_Q5_K>(a, staged, stream);
     case TLH_TYPE_Q6_K: return launch_sk_wt<TLH_TYPE_Q6_K>(a, staged, stream);

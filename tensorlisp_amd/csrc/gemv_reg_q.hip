@@ -1,0 +1,29 @@
+// Decode GEMV launchers for q4_1, q5_0 and q5_1 weights: the register-resident
+// kernels of gemv_reg.hpp with plain f32 stores, reading src1 from the split
+// scratch or quantizing it in the kernel (q8_1 / q8_0). Compiled apart from the
+// other types so the two halves build in parallel; these types take no
+// prologue / epilogue fusions.
+#include "gemv_reg.hpp"
+
+namespace tlh {
+
+template <int IN>
+static tlh_status launch_q(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
+                           hipStream_t stream) {
+    const GemvPro none;
+    switch (a.wtype) {
+    case TLH_TYPE_Q4_1: return launch_reg_wt<TLH_TYPE_Q4_1, IN, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
+    case TLH_TYPE_Q5_0: return launch_reg_wt<TLH_TYPE_Q5_0, IN, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
+    case TLH_TYPE_Q5_1: return launch_reg_wt<TLH_TYPE_Q5_1, IN, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
+    default: return set_error(TLH_UNSUPPORTED, "gemv: weight type %d", a.wtype);
+    }
+}
+
+tlh_status launch_gemv_reg_legacy(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
+                                  hipStream_t stream) {
+    if (!x) return launch_q<IN_SCRATCH>(a, nullptr, 0, ksplit, upw, stream);
+    return a.K <= 4096 ? launch_q<IN_X>(a, x, x_row_bytes, ksplit, upw, stream)
+                       : launch_q<IN_XL>(a, x, x_row_bytes, ksplit, upw, stream);
+}
+
+}  // namespace tlh

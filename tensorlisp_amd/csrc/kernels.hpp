@@ -118,6 +118,12 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
 // the register GEMV with a prologue and / or epilogue (GemvPro); quantizes in-kernel
+// q4_1 / q5_0 / q5_1 register GEMV (gemv_reg_q.hip): plain stores only
+tlh_status launch_gemv_reg_legacy(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
+                                  hipStream_t stream);
+__host__ __device__ constexpr bool legacy_type(int t) {
+    return t == TLH_TYPE_Q4_1 || t == TLH_TYPE_Q5_0 || t == TLH_TYPE_Q5_1;
+}
 tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
                                hipStream_t stream);
 // few-column GEMM on int8 MFMA (gemv_mfma.hip): 1 <= N <= 16, any K, from

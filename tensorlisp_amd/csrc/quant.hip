@@ -1,6 +1,6 @@
-// Activation quantizers (f32 -> Q8_0 / Q8_K, bit-exact with the CPU backend's
-// from_float) and weight dequantizers (Q4_0 / Q8_0 / Q4_K -> f32, bit-exact
-// with ggml's dequantize_row_*), for gfx950.
+// Activation quantizers (f32 -> Q8_0 / Q8_1 / Q8_K, bit-exact with the CPU
+// backend's from_float) and weight dequantizers (every weight type -> f32,
+// bit-exact with ggml's dequantize_row_*), for gfx950.
 //
 // Bit-exactness rules kept here: no a*b+c contraction where the reference
 // rounds twice (#pragma clang fp contract(off)), IEEE-correct f32 division
@@ -19,7 +19,11 @@ namespace tlh {
 // with the multiplier taken from the unrounded f32 d.
 // `rows` rows of x (stride x_row_bytes) become activation rows row_off.. of
 // an output holding total_rows rows.
-template <bool GGML_LAYOUT>
+// Q81: quantize_row_q8_1_ref (ggml-quants.c:302-335; the x86 entry without
+// AVX, arch/x86/quants.c:400-501): the same d and codes, plus s = f16(code
+// sum * the unrounded d) (block_q8_1: d, s, codes; split layout: s as f32 in
+// the sum slot).
+template <bool GGML_LAYOUT, bool Q81>
 __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__ x, int64_t K, int64_t rows,
                                                        int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
                                                        int64_t total_rows, bool f16) {
@@ -40,21 +44,26 @@ __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__
     const int lane32 = threadIdx.x & 31;
     const int64_t blk = col / QK;
     const int64_t orow = row + row_off;
+    int s = q;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) s += __shfl_xor(s, m, 32);
+    const uint16_t sh = f2h((float)s * d);  // q8_1 only
     if (GGML_LAYOUT) {
-        uint8_t *b = (uint8_t *)out + orow * (K / QK) * Q8_0_BYTES + blk * Q8_0_BYTES;
-        b[2 + lane32] = (uint8_t)(int8_t)q;
-        if (lane32 == 0) *(uint16_t *)b = dh;
+        constexpr int BB = Q81 ? Q8_1_BYTES : Q8_0_BYTES, CO = Q81 ? 4 : 2;
+        uint8_t *b = (uint8_t *)out + orow * (K / QK) * BB + blk * BB;
+        b[CO + lane32] = (uint8_t)(int8_t)q;
+        if (lane32 == 0) {
+            *(uint16_t *)b = dh;
+            if (Q81) *(uint16_t *)(b + 2) = sh;
+        }
     } else {
-        const ActLayout L = act_layout(TLH_TYPE_Q8_0, K, total_rows, f16);
+        const ActLayout L = act_layout(Q81 ? TLH_TYPE_Q8_1 : TLH_TYPE_Q8_0, K, total_rows, f16);
         int8_t *qs = (int8_t *)out + L.qs_off;
         qs[orow * K + col] = (int8_t)q;
         if (f16) ((_Float16 *)((char *)out + L.q16_off))[orow * K + col] = (_Float16)q;
-        int s = q;
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) s += __shfl_xor(s, m, 32);
         if (lane32 == 0) {
             ((float *)((char *)out + L.d_off))[orow * (K / QK) + blk] = h2f(dh);
-            ((int32_t *)((char *)out + L.sum_off))[orow * (K / QK) + blk] = s;
+            ((int32_t *)((char *)out + L.sum_off))[orow * (K / QK) + blk] = Q81 ? __float_as_int(h2f(sh)) : s;
         }
     }
 }
@@ -157,14 +166,12 @@ static inline unsigned grid_for(int64_t threads, int per_block) {
 tlh_status launch_quantize_act(int wtype, const float *x, int64_t K, int64_t rows, int64_t x_row_bytes, void *out,
                                bool ggml_layout, int64_t row_off, int64_t total_rows, bool f16, hipStream_t stream) {
     if (rows == 0 || K == 0) return TLH_OK;
-    if (vec_dot_type(wtype) == TLH_TYPE_Q8_0) {
+    if (vec_dot_type(wtype) == TLH_TYPE_Q8_0 || vec_dot_type(wtype) == TLH_TYPE_Q8_1) {
         const unsigned g = grid_for(K * rows, 256);
-        if (ggml_layout)
-            hipLaunchKernelGGL(k_quantize_q8_0<true>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows, f16);
-        else
-            hipLaunchKernelGGL(k_quantize_q8_0<false>, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out,
-                               row_off, total_rows, f16);
+        const bool q81 = vec_dot_type(wtype) == TLH_TYPE_Q8_1;
+        auto kern = ggml_layout ? (q81 ? k_quantize_q8_0<true, true> : k_quantize_q8_0<true, false>)
+                                : (q81 ? k_quantize_q8_0<false, true> : k_quantize_q8_0<false, false>);
+        hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, stream, x, K, rows, x_row_bytes, out, row_off, total_rows, f16);
     } else {
         const unsigned g = grid_for((K / QKK) * rows * 64, 256);
         if (ggml_layout)
@@ -188,6 +195,15 @@ tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, i
         break;
     case TLH_TYPE_Q8_0:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q8_0>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q4_1:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_1>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q5_0:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q5_0>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q5_1:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q5_1>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
         break;
     case TLH_TYPE_Q4_K:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q4_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);

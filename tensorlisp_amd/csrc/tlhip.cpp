@@ -48,7 +48,8 @@ static tlh_status hip_check(hipError_t e, const char *what) {
 tlh_status noalloc_setup_current_device();
 
 static bool weight_type_ok(int t) {
-    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K;
+    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K ||
+           legacy_type(t);
 }
 
 static const char *type_name(int t) {
@@ -56,7 +57,12 @@ static const char *type_name(int t) {
     case TLH_TYPE_F32: return "f32";
     case TLH_TYPE_F16: return "f16";
     case TLH_TYPE_Q4_0: return "q4_0";
+    case TLH_TYPE_Q4_1: return "q4_1";
+    case TLH_TYPE_Q5_0: return "q5_0";
+    case TLH_TYPE_Q5_1: return "q5_1";
     case TLH_TYPE_Q8_0: return "q8_0";
+    case TLH_TYPE_Q8_1: return "q8_1";
+    case TLH_TYPE_BF16: return "bf16";
     case TLH_TYPE_Q4_K: return "q4_K";
     case TLH_TYPE_Q5_K: return "q5_K";
     case TLH_TYPE_Q6_K: return "q6_K";
@@ -81,7 +87,8 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     s.flt = float_type(a.ty);
     if (!weight_type_ok(a.ty) && !s.flt)
         return set_error(TLH_UNSUPPORTED,
-                         "mul_mat: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K, f32, f16, bf16", a.ty,
+                         "mul_mat: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q4_K, q5_K, q6_K, "
+                         "f32, f16, bf16", a.ty,
                          type_name(a.ty));
     // src1 is f32, or (ggml's vec_dot_type rule) already the f16 / bf16 of f16 / bf16 weights
     if (b.ty != TLH_TYPE_F32 && !(s.flt && a.ty != TLH_TYPE_F32 && b.ty == a.ty))
@@ -570,7 +577,9 @@ bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
     MulMatShape first;
     for (int i = 0; i < n; ++i) {
         MulMatShape s;
-        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || s.N != 1 || s.ne12 * s.ne13 != 1)
+        // q4_1 / q5_0 / q5_1 have no fused (prologue / epilogue) register kernels
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || legacy_type(s.wtype) || s.N != 1 ||
+            s.ne12 * s.ne13 != 1)
             return false;
         int ks, upw;
         if (!gemv_reg_geometry(s.K, ks, upw)) return false;
@@ -793,7 +802,8 @@ static tlh_status check_mul_mat_id(const tlh_op *op, MulMatIdShape &s) {
     if (!op) return set_error(TLH_INVALID, "mul_mat_id: null op");
     const tlh_tensor &a = op->t[0], &b = op->t[1], &ids = op->t[2], &d = op->t[4];
     if (!weight_type_ok(a.ty))
-        return set_error(TLH_UNSUPPORTED, "mul_mat_id: weights of ggml type %d (%s); have q4_0, q8_0, q4_K, q5_K, q6_K",
+        return set_error(TLH_UNSUPPORTED,
+                         "mul_mat_id: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q4_K, q5_K, q6_K",
                          a.ty, type_name(a.ty));
     if (b.ty != TLH_TYPE_F32 || d.ty != TLH_TYPE_F32 || ids.ty != TLH_TYPE_I32)
         return set_error(TLH_UNSUPPORTED, "mul_mat_id: f32 src1 and dst, i32 ids");
