@@ -13,9 +13,12 @@
 
 namespace tlh {
 
+// One launch that quantizes src1 itself: N <= 2 and K <= 4096 (longer rows
+// run a quantize launch first: every workgroup quantizing the whole column
+// costs more than that launch).
 bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_bytes) {
     int ksplit, upw;
-    return x != nullptr && a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw) && ((uintptr_t)x & 15) == 0 &&
+    return x != nullptr && a.N <= 2 && a.K <= 4096 && gemv_reg_geometry(a.K, ksplit, upw) && ((uintptr_t)x & 15) == 0 &&
            (x_row_bytes & 15) == 0;
 }
 
@@ -29,7 +32,7 @@ static bool gemv_uses_reg(const MatmulArgs &a) {
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream) {
     if (a.N < 1 || a.N > 16) return set_error(TLH_INVALID, "gemv: N=%lld outside 1..16", (long long)a.N);
     if (gemv_uses_reg(a)) return launch_gemv_reg(a, x, x_row_bytes, stream);
-    if (x != nullptr) return set_error(TLH_INVALID, "gemv: fused quantization needs N <= 2, K <= 16384, K %% 64 == 0");
+    if (x != nullptr) return set_error(TLH_INVALID, "gemv: fused quantization needs N <= 2, K <= 4096, K %% 64 == 0");
     return launch_gemv_mfma(a, stream);
 }
 

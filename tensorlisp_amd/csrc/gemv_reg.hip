@@ -42,8 +42,8 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     if (legacy_type(a.wtype)) return launch_gemv_reg_legacy(a, x, x_row_bytes, ksplit, upw, stream);
     const GemvPro none;
     if (!x) return launch_reg_type<IN_SCRATCH, OUT_STORE>(a, nullptr, 0, none, ksplit, upw, stream);
-    return a.K <= 4096 ? launch_reg_type<IN_X, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream)
-                       : launch_reg_type<IN_XL, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
+    if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: in-kernel quantization takes K <= 4096");
+    return launch_reg_type<IN_X, OUT_STORE>(a, x, x_row_bytes, none, ksplit, upw, stream);
 }
 
 tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
@@ -95,9 +95,7 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
                      : launch_reg_type<IN_NORM, OUT_STORE>(b, nullptr, 0, pro, ksplit, upw, stream);
     }
     if (!x) return set_error(TLH_INVALID, "gemv_reg: no activation");
-    if (a.K > 4096)
-        return glu ? launch_reg_type<IN_XL, OUT_GLU>(b, x, x_row_bytes, pro, ksplit, upw, stream)
-                   : launch_reg_type<IN_XL, OUT_STORE>(b, x, x_row_bytes, pro, ksplit, upw, stream);
+    if (a.K > 4096) return set_error(TLH_UNSUPPORTED, "gemv_reg: in-kernel quantization takes K <= 4096");
     return glu ? launch_reg_type<IN_X, OUT_GLU>(b, x, x_row_bytes, pro, ksplit, upw, stream)
            : epi ? launch_reg_type<IN_X, OUT_EPI>(b, x, x_row_bytes, pro, ksplit, upw, stream)
                  : launch_reg_type<IN_X, OUT_STORE>(b, x, x_row_bytes, pro, ksplit, upw, stream);

@@ -13,7 +13,7 @@
 // contiguous load; for larger K, KSPLIT (2 or 4) waves of a workgroup take
 // contiguous K ranges of the same rows and merge their partials through LDS.
 //
-// In-kernel activations (IN_X, IN_XL, IN_NORM): each workgroup loads its
+// In-kernel activations (IN_X, IN_NORM; K <= 4096): each workgroup loads its
 // activation column(s), requests its first weights, then quantizes the column
 // once into LDS with the rules of quantize_row_q8_0_ref (ggml-quants.c:276-297)
 // and quantize_row_q8_K_ref (:2768-2804), so a decode MUL_MAT is one launch.
@@ -98,8 +98,8 @@ __host__ __device__ inline ActLds act_lds(int act_type, int64_t K) {
     return L;
 }
 
-// A thread's share of one activation column: 16-element groups t, t + 256,
-// ... (G of them; K <= 4096 * G), loaded into registers before the weight
+// A thread's share of one activation column: the 16-element group t (K <=
+// 4096: one group per thread), loaded into registers before the weight
 // loads are issued, so that quantizing them does not wait for the weights
 // (vector loads complete in order). IN_X: the values of x; IN_NORM: x = p + q
 // and the norm weight w (K <= 4096).
@@ -126,16 +126,17 @@ __device__ __forceinline__ void first_max_step(float &ba, float &bv, bool partne
     if (oa > ba || (oa == ba && partner_first)) ba = oa, bv = ov;
 }
 
-// IN_X: x with K <= 4096; IN_XL: x with K <= 16384; IN_NORM: the prologue's
-// p, q, w with K <= 4096.
-enum { IN_SCRATCH = 0, IN_X = 1, IN_NORM = 2, IN_XL = 3 };
+// IN_X: x with K <= 4096; IN_NORM: the prologue's p, q, w with K <= 4096.
+// (A longer K reads the scratch of a quantize launch: quantizing a whole
+// column in every workgroup costs more there than that launch.)
+enum { IN_SCRATCH = 0, IN_X = 1, IN_NORM = 2 };
 // OUT: how rows leave the kernel (OUT_STORE: f32 rows of dst or the
 // segments; OUT_GLU: the GemvPro SwiGLU epilogue; OUT_EPI: the GemvPro
 // store epilogue)
 enum { OUT_STORE = 0, OUT_GLU = 1, OUT_EPI = 2 };
 
 template <int IN> struct ActRegs {
-    static constexpr int G = IN == IN_XL ? 4 : 1;
+    static constexpr int G = 1;
     static constexpr int NQ = IN == IN_NORM ? 16 : 1;
     float v[G][16];
     float q[NQ], w[NQ];  // IN_NORM: the ADD's second operand (or x again) and the norm weight

@@ -22,8 +22,8 @@ static tlh_status launch_q(const MatmulArgs &a, const float *x, int64_t x_row_by
 tlh_status launch_gemv_reg_legacy(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
                                   hipStream_t stream) {
     if (!x) return launch_q<IN_SCRATCH>(a, nullptr, 0, ksplit, upw, stream);
-    return a.K <= 4096 ? launch_q<IN_X>(a, x, x_row_bytes, ksplit, upw, stream)
-                       : launch_q<IN_XL>(a, x, x_row_bytes, ksplit, upw, stream);
+    if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: in-kernel quantization takes K <= 4096");
+    return launch_q<IN_X>(a, x, x_row_bytes, ksplit, upw, stream);
 }
 
 }  // namespace tlh

@@ -582,7 +582,7 @@ bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
             s.ne12 * s.ne13 != 1)
             return false;
         int ks, upw;
-        if (!gemv_reg_geometry(s.K, ks, upw)) return false;
+        if (s.K > 4096 || !gemv_reg_geometry(s.K, ks, upw)) return false;  // in-kernel quantization: K <= 4096
         if (i == 0) first = s;
         else if (s.K != first.K || s.wtype != first.wtype) return false;
     }

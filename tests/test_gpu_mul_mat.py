@@ -304,12 +304,13 @@ def tie_rows(n, K, seed):
 
 
 @pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
-@pytest.mark.parametrize("K", [256, 4096, 8192, 14336, 16384])
+@pytest.mark.parametrize("K", [256, 1024, 4096, 14336])
 def test_in_kernel_quantization_is_the_quantize_launch(gpu, t, K):
-    """For N <= 2 the GEMV quantizes src1 itself (each workgroup into LDS). Its
-    products must be bit-identical to the same GEMV reading the scratch of the
-    separate quantize launch, which is pinned bit-exact to ggml's
-    quantize_row_q8_0 / q8_K (test_gpu_quant.py): so are the in-kernel codes."""
+    """For N <= 2 and K <= 4096 the GEMV quantizes src1 itself (each workgroup
+    into LDS). Its products must be bit-identical to the same GEMV reading the
+    scratch of the separate quantize launch, which is pinned bit-exact to
+    ggml's quantize_row_q8_0 / q8_K (test_gpu_quant.py): so are the in-kernel
+    codes. (K = 14336 runs the quantize launch in both forms.)"""
     import torch
 
     M = 300
