@@ -222,6 +222,152 @@ __host__ __device__ inline ActView act_view(const void *base, int act_type, int6
     return v;
 }
 
+// ------------------------------------- activation quantizers on registers
+// Shared by the quantize launch and by kernels that quantize the rows they
+// produce (the norm chain, SwiGLU), so both write the same bytes.
+
+// q8_K (quantize_row_q8_K_ref, ggml-quants.c:2768-2804) of NB 256-element
+// blocks held by one wave, elements 4l..4l+3 of block b in v[b] of lane l:
+// the signed value of largest magnitude (the first one on ties), iscale =
+// -127/max, codes rint(iscale*x) clamped to 127, d = 1/iscale; an all-zero
+// block gets d = 0 and zero codes. packed[b]: the lane's four codes; psum[b]:
+// the sum of the codes of lanes 4k..4k+3 (bsum k of the block). The NB
+// blocks' reductions are interleaved (independent shuffle chains in flight
+// together); each block's arithmetic is the same for any NB.
+template <int NB>
+__device__ __forceinline__ void q8K_waves(const float (&v)[NB][4], int lane, uint32_t (&packed)[NB], int (&psum)[NB],
+                                          float (&d)[NB]) {
+#pragma clang fp contract(off)
+    float ba[NB], bv[NB];
+    int bi[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        ba[b] = 0.0f, bv[b] = 0.0f, bi[b] = 1 << 30;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = fabsf(v[b][i]);
+            if (a > ba[b]) { ba[b] = a; bv[b] = v[b][i]; bi[b] = 4 * lane + i; }
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float oa[NB], ov[NB];
+        int oi[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            oa[b] = __shfl_xor(ba[b], m, 64);
+            ov[b] = __shfl_xor(bv[b], m, 64);
+            oi[b] = __shfl_xor(bi[b], m, 64);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (oa[b] > ba[b] || (oa[b] == ba[b] && oi[b] < bi[b])) { ba[b] = oa[b]; bv[b] = ov[b]; bi[b] = oi[b]; }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        packed[b] = 0;
+        psum[b] = 0;
+        d[b] = 0.0f;
+        if (ba[b] != 0.0f) {  // wave-uniform
+            const float iscale = -127.0f / bv[b];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int q = (int)rintf(iscale * v[b][i]);
+                q = q > 127 ? 127 : q;
+                packed[b] |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
+                psum[b] += q;
+            }
+            d[b] = 1.0f / iscale;
+        }
+    }
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) psum[b] += __shfl_xor(psum[b], m, 64);
+}
+
+// One q8_K block (q8K_waves' results) into the split layout at activation
+// row `orow`, super-block `blk`.
+__device__ __forceinline__ void q8K_store_split(char *out, const ActLayout &L, int64_t K, int64_t orow, int64_t blk,
+                                                int lane, uint32_t packed, int psum, float d, bool f16) {
+    const int64_t e0 = orow * K + blk * QKK + 4 * lane;
+    *(uint32_t *)(out + L.qs_off + e0) = packed;
+    if (f16) {
+        uint32_t h[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c0 = (int)(int8_t)(packed >> (16 * i)), c1 = (int)(int8_t)(packed >> (16 * i + 8));
+            h[i] = (uint32_t)f2h((float)c0) | ((uint32_t)f2h((float)c1) << 16);
+        }
+        *(uint2 *)(out + L.q16_off + e0 * 2) = make_uint2(h[0], h[1]);
+    }
+    if ((lane & 3) == 0) ((int16_t *)(out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
+    if (lane == 0) ((float *)(out + L.d_off))[orow * (K / QKK) + blk] = d;
+}
+
+// q8_0 (quantize_row_q8_0_ref, ggml-quants.c:276-297) / q8_1 (:302-335) of
+// 32-element blocks held by 8 consecutive lanes (8-lane aligned), four
+// consecutive elements per lane: v[b] starts at element col[b] of activation
+// row `orow` (live[b] false: not stored; whole 8-lane groups agree): amax,
+// d = amax/127, f16(d), codes roundf(x * (1/d)) with the unrounded d; q8_1
+// also s = f16(code sum * unrounded d). Written to the split layout (d as f32
+// of its f16; the sum slot: q8_0 the code sum, q8_1 s as f32). The NB sets'
+// reductions are interleaved.
+template <int NB, bool Q81>
+__device__ __forceinline__ void q80_quads_store_split(const float (&v)[NB][4], const bool (&live)[NB], int lane,
+                                                      char *out, const ActLayout &L, int64_t K, int64_t orow,
+                                                      const int64_t (&col)[NB], bool f16) {
+#pragma clang fp contract(off)
+    float amax[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        amax[b] = fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])), fmaxf(fabsf(v[b][2]), fabsf(v[b][3])));
+#pragma unroll
+    for (int m = 4; m >= 1; m >>= 1)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], m, 64));
+    float d[NB];
+    uint32_t packed[NB];
+    int s[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        d[b] = amax[b] / 127.0f;
+        const float id = d[b] != 0.0f ? 1.0f / d[b] : 0.0f;
+        packed[b] = 0;
+        s[b] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = (int)roundf(v[b][i] * id);
+            packed[b] |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
+            s[b] += q;
+        }
+    }
+#pragma unroll
+    for (int m = 4; m >= 1; m >>= 1)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) s[b] += __shfl_xor(s[b], m, 64);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (!live[b]) continue;
+        const int64_t e0 = orow * K + col[b];
+        *(uint32_t *)(out + L.qs_off + e0) = packed[b];
+        if (f16) {
+            uint32_t h[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int c0 = (int)(int8_t)(packed[b] >> (16 * i)), c1 = (int)(int8_t)(packed[b] >> (16 * i + 8));
+                h[i] = (uint32_t)f2h((float)c0) | ((uint32_t)f2h((float)c1) << 16);
+            }
+            *(uint2 *)(out + L.q16_off + e0 * 2) = make_uint2(h[0], h[1]);
+        }
+        if ((lane & 7) == 0) {
+            const int64_t bk = orow * (K / 32) + col[b] / 32;
+            ((float *)(out + L.d_off))[bk] = h2f(f2h(d[b]));
+            ((int32_t *)(out + L.sum_off))[bk] = Q81 ? __float_as_int(h2f(f2h((float)s[b] * d[b]))) : s[b];
+        }
+    }
+}
+
 // ------------------------------------------------------- wave64 reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -303,6 +303,124 @@ __global__ void __launch_bounds__(256) k_core_glu(const CoreArgs a) {
     body_glu(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 
+// GLU whose output rows feed a MUL_MAT: the values body_glu computes, stored
+// the same way, and quantized into the MUL_MAT's activation scratch in the
+// same pass (q8K_waves / q80_quads_store_split: the quantize launch's bytes).
+// One wave per 256 elements of a row, four consecutive elements per lane
+// (a q8_K super-block, or eight 8-lane q8_0 / q8_1 blocks); row r of dst is
+// activation row r. VEC: every row 16-byte aligned (float4 loads / stores).
+struct GluQuantArgs {
+    CoreArgs c;
+    ActQuantOut qo;
+    int64_t chunks;  // 256-element chunks per row
+};
+
+template <bool VEC>
+__global__ void __launch_bounds__(256) k_glu_quantize(const GluQuantArgs a) {
+    const tlh_tensor &x = a.c.op.t[0], &y = a.c.op.t[1], &d = a.c.op.t[4];
+    const int code = (int)a.c.op.x[0];
+    const bool swapped = a.c.op.x[1] != 0;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t rows = d.ne[1] * d.ne[2] * d.ne[3];
+    if (wave >= rows * a.chunks) return;  // whole waves
+    const int64_t row = wave / a.chunks, ch = wave - row * a.chunks;
+    int64_t i1, i2, i3;
+    row_coords(row, d, i1, i2, i3);
+    const int64_t nc = d.ne[0];
+    const float *xr = (const float *)(a.c.s0 + offs(x, 0, i1, i2, i3));
+    const float *gr;
+    if (a.c.s1) {
+        gr = (const float *)(a.c.s1 + offs(y, 0, i1, i2, i3));
+    } else {
+        gr = xr + (swapped ? 0 : nc);
+        xr += swapped ? nc : 0;
+    }
+    float *dr = (float *)(a.c.dst + offs(d, 0, i1, i2, i3));
+    const int64_t c0 = 256 * ch + 4 * lane;
+    const bool live = c0 < nc;  // whole 8-lane groups: nc is a multiple of 32
+    float h[1][4];
+    if (live) {
+        float xv[4], gv[4];
+        if (VEC) {
+            const float4 a4 = *(const float4 *)(xr + c0), g4 = *(const float4 *)(gr + c0);
+            xv[0] = a4.x, xv[1] = a4.y, xv[2] = a4.z, xv[3] = a4.w;
+            gv[0] = g4.x, gv[1] = g4.y, gv[2] = g4.z, gv[3] = g4.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = xr[c0 + e], gv[e] = gr[c0 + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[0][e] = glu_val(code, xv[e], gv[e]);
+        if (VEC) {
+            *(float4 *)(dr + c0) = make_float4(h[0][0], h[0][1], h[0][2], h[0][3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dr[c0 + e] = h[0][e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[0][e] = 0.0f;
+    }
+    const ActLayout L = act_layout(a.qo.type, nc, a.qo.rows, a.qo.f16);
+    if (a.qo.type == TLH_TYPE_Q8_K) {  // nc % 256 == 0: every lane live
+        uint32_t pk[1];
+        int ps[1];
+        float dd[1];
+        q8K_waves<1>(h, lane, pk, ps, dd);
+        q8K_store_split((char *)a.qo.out, L, nc, row, ch, lane, pk[0], ps[0], dd[0], a.qo.f16);
+    } else {
+        const bool lv[1] = {live};
+        const int64_t col[1] = {c0};
+        if (a.qo.type == TLH_TYPE_Q8_1)
+            q80_quads_store_split<1, true>(h, lv, lane, (char *)a.qo.out, L, nc, row, col, a.qo.f16);
+        else
+            q80_quads_store_split<1, false>(h, lv, lane, (char *)a.qo.out, L, nc, row, col, a.qo.f16);
+    }
+}
+
+bool glu_quantize_ok(const tlh_op &op, int act_type) {
+    const tlh_tensor &x = op.t[0], &d = op.t[4];
+    const int be = act_type == TLH_TYPE_Q8_K ? QKK : act_type == TLH_TYPE_Q8_0 || act_type == TLH_TYPE_Q8_1 ? QK : 0;
+    return be > 0 && x.ty == TLH_TYPE_F32 && d.ty == TLH_TYPE_F32 && x.nb[0] == 4 && d.nb[0] == 4 &&
+           d.ne[0] > 0 && d.ne[0] % be == 0;
+}
+
+tlh_status launch_glu_quantize(const tlh_op &op, const void *src0, const void *src1, void *dst, const ActQuantOut &qo,
+                               hipStream_t stream) {
+    if (!glu_quantize_ok(op, qo.type) || (src1 && (op.t[1].ty != TLH_TYPE_F32 || op.t[1].nb[0] != 4)))
+        return set_error(TLH_INVALID, "glu_quantize: operands or row length do not fit activation type %d", qo.type);
+    const tlh_tensor &d = op.t[4];
+    const int64_t rows = d.ne[1] * d.ne[2] * d.ne[3];
+    if (!qo.out || ((uintptr_t)qo.out & 255) || qo.rows != rows)
+        return set_error(TLH_INVALID, "glu_quantize: activation scratch");
+    if (rows == 0) return TLH_OK;
+    GluQuantArgs a;
+    a.c.op = op;
+    a.c.s0 = (const char *)src0;
+    a.c.s1 = (const char *)src1;
+    a.c.s2 = nullptr;
+    a.c.s3 = nullptr;
+    a.c.dst = (char *)dst;
+    a.qo = qo;
+    a.chunks = (d.ne[0] + 255) / 256;
+    // float4 access: the three bases and every row stride 16-byte aligned
+    const tlh_tensor *ts[3] = {&op.t[0], &op.t[1], &op.t[4]};
+    const void *ps[3] = {src0, src1, dst};
+    bool vec = true;
+    for (int k = 0; k < 3 && vec; ++k) {
+        if (!ps[k]) continue;
+        vec = ((uintptr_t)ps[k] & 15) == 0;
+        for (int i = 1; i < 4; ++i) vec = vec && ts[k]->nb[i] % 16 == 0;
+    }
+    if (!src1) vec = vec && (d.ne[0] * 4) % 16 == 0;  // the second half's offset
+    const int64_t waves = rows * a.chunks;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (vec) hipLaunchKernelGGL(k_glu_quantize<true>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(k_glu_quantize<false>, grid, dim3(256), 0, stream, a);
+    return check_launch("glu_quantize");
+}
+
 // ------------------------------------------------------------ block reduces
 // (wave_sum_t and block_sum_t: common.hpp)
 __device__ __forceinline__ float block_max_f(float v, float *sh) {

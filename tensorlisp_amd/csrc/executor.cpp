@@ -66,6 +66,10 @@ struct Dispatch {
     int has_norm = 0, has_glu = 0;
     tlh_op nop, gop;
     Place nsrc[4], ndst, gdst;
+    // D_CORE GLU: also quantizes its output for a MUL_MAT (type, activation
+    // rows, f16 codes) into that MUL_MAT's scratch block
+    int nq_type = 0, nq_f16 = 0;
+    int64_t nq_rows = 0;
     int32_t pw[4] = {0, 0, 0, 0};
     int64_t pw_blocks = 0;  // D_PAGED_WRITE: blocks in the smaller pool (slots past it are dropped)
     int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
@@ -210,6 +214,7 @@ class Lowering {
         group_elementwise(out.d);
         group_mul_mats(out.d);
         merge_mm_computes(out.d);
+        fuse_glu_quantize(out.d);
         group_elementwise(out.d);  // merged computes can leave element-wise launches adjacent
         plan(out);
         return TLH_OK;
@@ -1130,7 +1135,8 @@ class Lowering {
 
     // consecutive independent element-wise dispatches -> one launch (up to 4)
     void group_elementwise(std::vector<Dispatch> &d) {
-        auto ew = [](const Dispatch &x) { return x.kind == D_CORE && core_multi_kind(x.core_kind); };
+        // (a GLU that also quantizes for a MUL_MAT keeps its own launch)
+        auto ew = [](const Dispatch &x) { return x.kind == D_CORE && core_multi_kind(x.core_kind) && !x.nq_type; };
         std::vector<Dispatch> out;
         for (size_t i = 0; i < d.size();) {
             size_t j = i + 1;
@@ -1282,6 +1288,78 @@ class Lowering {
         d.swap(out);
     }
 
+    // A MUL_MAT of 3 or more columns whose activation is a GLU's output (the
+    // SwiGLU before the down projection): the GLU launch also writes the
+    // quantized rows (the bytes the quantize launch would write) into the
+    // MUL_MAT's scratch, and the MUL_MAT keeps only its compute launch; a
+    // quantization group's leader quantize goes the same way. Needs: src1 is
+    // the GLU's whole output, contiguous f32 rows (a multiple of the block)
+    // in the same order, and nothing between the two writes that storage.
+    // The scratch then lives from the GLU on.
+    void fuse_glu_quantize(std::vector<Dispatch> &d) {
+        auto contiguous_f32 = [](const tlh_tensor &t) {
+            return t.ty == TLH_TYPE_F32 && t.nb[0] == 4 && t.nb[1] == 4 * t.ne[0] && t.nb[2] == t.nb[1] * t.ne[1] &&
+                   t.nb[3] == t.nb[2] * t.ne[2];
+        };
+        std::vector<char> gone(d.size(), 0);
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &q = d[i];
+            const bool leader = q.kind == D_MM_QUANTIZE && q.block <= -2;
+            const bool single = q.kind == D_MUL_MAT && q.block == -1 && q.scratch_bytes > 0;
+            if (!leader && !single) continue;
+            const tlh_tensor &b = q.op.t[1];
+            const int wt = q.op.t[0].ty;
+            if (wt == TLH_TYPE_F32 || wt == TLH_TYPE_F16 || wt == TLH_TYPE_BF16 || b.ne[1] < 3) continue;
+            const int at = vec_dot_type(wt);
+            const int64_t K = b.ne[0], rows = b.ne[1] * b.ne[2] * b.ne[3];
+            if (!contiguous_f32(b) || rows == 0) continue;
+            // the GLU that wrote src1, with nothing writing it since
+            int gi = -1;
+            std::vector<Place> rd, wr;
+            for (int j = (int)i - 1; j >= 0; --j) {
+                if (gone[j]) continue;
+                const Dispatch &c = d[j];
+                if (c.kind == D_CORE && c.core_kind == TLH_CORE_GLU && same_place(c.dst, q.src[1])) {
+                    gi = j;
+                    break;
+                }
+                places(c, rd, wr);
+                bool touches = false;
+                for (const Place &p : wr) touches = touches || same_root(p, q.src[1]);
+                if (touches) break;
+            }
+            if (gi < 0) continue;
+            Dispatch &g = d[gi];
+            const tlh_tensor &y = g.op.t[4];
+            if (g.block != -1 || !contiguous_f32(y) || y.ne[0] != K || y.ne[1] * y.ne[2] * y.ne[3] != rows ||
+                !glu_quantize_ok(g.op, at))
+                continue;
+            if (single) {  // a group of one: its scratch block spans GLU .. MUL_MAT
+                Group gr;
+                gr.first = q.pos;
+                gr.last = q.pos_last;
+                gr.bytes = q.scratch_bytes;
+                gr.leader = (int)i;
+                q.block = -2 - (int)groups_.size();
+                groups_.push_back(gr);
+                q.kind = D_MM_COMPUTE;
+            } else {
+                gone[i] = 1;
+            }
+            g.nq_type = at;
+            g.nq_rows = rows;
+            g.nq_f16 = act_has_f16(wt, b.ne[1]);
+            g.block = q.block;
+            g.scratch_bytes = q.scratch_bytes;
+            Group &gr = groups_[-2 - q.block];
+            gr.first = std::min<int64_t>(gr.first, g.pos);
+        }
+        std::vector<Dispatch> out;
+        for (size_t i = 0; i < d.size(); ++i)
+            if (!gone[i]) out.push_back(d[i]);
+        d.swap(out);
+    }
+
     struct Group {
         int64_t first = 0, last = 0;
         size_t bytes = 0;
@@ -1382,7 +1460,7 @@ class Lowering {
         for (size_t i = 0; i < n_tensor_blocks; ++i) out.arena_off[out.blocks[i].tensor] = out.blocks[i].off;
         out.node_scratch.assign(n, -1);
         for (const Dispatch &x : out.d) {
-            if (x.block >= 0) out.node_scratch[x.pos] = out.blocks[x.block].off;
+            if (x.block >= 0 && !x.nq_type) out.node_scratch[x.pos] = out.blocks[x.block].off;
             if (x.block >= 0 && x.kind == D_MM_COMPUTE_MULTI)
                 for (int k = 0; k < x.nmem; ++k) out.node_scratch[x.mpos[k]] = out.blocks[x.block].off;
         }
@@ -1599,6 +1677,13 @@ struct tlh_program {
                 if (x.core_kind == TLH_CORE_ROPE && x.op.x[9]) {  // rope into cache rows
                     const void *ss[1][4] = {{src[0], src[1], src[2], src[3]}};
                     st = launch_core_multi(1, &x.core_kind, &x.op, ss, &dst, s);
+                } else if (x.core_kind == TLH_CORE_GLU && x.nq_type) {  // and the next MUL_MAT's quantization
+                    ActQuantOut qo;
+                    qo.out = scratch;
+                    qo.type = x.nq_type;
+                    qo.rows = x.nq_rows;
+                    qo.f16 = x.nq_f16 != 0;
+                    st = launch_glu_quantize(x.op, src[0], src[1], dst, qo, s);
                 } else {
                     st = tlh_core(x.core_kind, &x.op, src[0], src[1], src[2], dst, s);
                 }

@@ -180,6 +180,21 @@ tlh_status mul_mat_multi_pro(const tlh_op *const *ops, const void *const *w, voi
 // op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
 tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
                              hipStream_t stream);
+// A kernel's rows quantized as it writes them: the activation scratch of a
+// MUL_MAT (split layout of `type` = q8_0 / q8_1 / q8_K for `rows` activation
+// rows, f16 codes too when `f16`), row r of the kernel's output being
+// activation row r.
+struct ActQuantOut {
+    void *out = nullptr;
+    int type = 0;
+    int64_t rows = 0;
+    bool f16 = false;
+};
+// GGML_OP_GLU (the core op's operands, f32 rows of unit element stride) that
+// also quantizes its output rows into qo (row length a multiple of qo's block).
+bool glu_quantize_ok(const tlh_op &op, int act_type);
+tlh_status launch_glu_quantize(const tlh_op &op, const void *src0, const void *src1, void *dst, const ActQuantOut &qo,
+                               hipStream_t stream);
 // ARGMAX of long rows in chunks over many workgroups (executor): scratch of
 // argmax_split_scratch_bytes; same result as the core ARGMAX.
 size_t argmax_split_scratch_bytes(const tlh_op &op);

@@ -71,9 +71,8 @@ __global__ void __launch_bounds__(256) k_quantize_q8_0(const float *__restrict__
 // ------------------------------------------------------------------ Q8_K
 // quantize_row_q8_K_ref (ggml-quants.c:2768-2804), the x86 entry
 // (arch/x86/quants.c:505-507). One wave per 256-element block, four
-// consecutive elements per lane: the signed value of largest magnitude (the
-// first one on ties), iscale = -127/max, codes rint(iscale*x) clamped to 127,
-// bsums of 16, d = 1/iscale. An all-zero block gets d = 0 and zero codes and sums.
+// consecutive elements per lane, quantized by q8K_waves (the arithmetic the
+// fused norm / SwiGLU kernels share).
 template <bool GGML_LAYOUT>
 __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__ x, int64_t K, int64_t rows,
                                                        int64_t x_row_bytes, void *__restrict__ out, int64_t row_off,
@@ -86,60 +85,22 @@ __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__
     const int64_t row = wave / nblk;
     const int64_t blk = wave - row * nblk;
     const float *src = (const float *)((const char *)x + row * x_row_bytes) + blk * QKK + 4 * lane;
-    float v[4];
+    float v[1][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = src[i];
-    float ba = 0.0f, bv = 0.0f;
-    int bi = 1 << 30;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > ba) { ba = a; bv = v[i]; bi = 4 * lane + i; }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float oa = __shfl_xor(ba, m, 64);
-        const float ov = __shfl_xor(bv, m, 64);
-        const int oi = __shfl_xor(bi, m, 64);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
-    }
-    uint32_t packed = 0;
-    int psum = 0;
-    float d = 0.0f;
-    if (ba != 0.0f) {
-        const float iscale = -127.0f / bv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int q = (int)rintf(iscale * v[i]);
-            q = q > 127 ? 127 : q;
-            packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
-            psum += q;
-        }
-        d = 1.0f / iscale;
-    }
-    psum += __shfl_xor(psum, 1, 64);
-    psum += __shfl_xor(psum, 2, 64);
+    for (int i = 0; i < 4; ++i) v[0][i] = src[i];
+    uint32_t packed[1];
+    int psum[1];
+    float d[1];
+    q8K_waves<1>(v, lane, packed, psum, d);
     const int64_t orow = row + row_off;
     if (GGML_LAYOUT) {
         uint8_t *b = (uint8_t *)out + orow * nblk * Q8_K_BYTES + blk * Q8_K_BYTES;
-        *(uint32_t *)(b + 4 + 4 * lane) = packed;
-        if ((lane & 3) == 0) *(int16_t *)(b + 4 + QKK + 2 * (lane >> 2)) = (int16_t)psum;
-        if (lane == 0) *(float *)b = d;
+        *(uint32_t *)(b + 4 + 4 * lane) = packed[0];
+        if ((lane & 3) == 0) *(int16_t *)(b + 4 + QKK + 2 * (lane >> 2)) = (int16_t)psum[0];
+        if (lane == 0) *(float *)b = d[0];
     } else {
-        const ActLayout L = act_layout(TLH_TYPE_Q8_K, K, total_rows, f16);
-        *(uint32_t *)((char *)out + L.qs_off + orow * K + blk * QKK + 4 * lane) = packed;
-        if (f16) {
-            uint32_t h[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int c0 = (int)(int8_t)(packed >> (16 * i)), c1 = (int)(int8_t)(packed >> (16 * i + 8));
-                h[i] = (uint32_t)f2h((float)c0) | ((uint32_t)f2h((float)c1) << 16);
-            }
-            *(uint2 *)((char *)out + L.q16_off + (orow * K + blk * QKK + 4 * lane) * 2) = make_uint2(h[0], h[1]);
-        }
-        if ((lane & 3) == 0)
-            ((int16_t *)((char *)out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
-        if (lane == 0) ((float *)((char *)out + L.d_off))[orow * nblk + blk] = d;
+        q8K_store_split((char *)out, act_layout(TLH_TYPE_Q8_K, K, total_rows, f16), K, orow, blk, lane, packed[0],
+                        psum[0], d[0], f16);
     }
 }
 

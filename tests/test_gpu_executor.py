@@ -164,6 +164,52 @@ def test_shared_quantization_matches_separate(gpu):
     assert prog.stats()["launches"] == 1 + 2 + 1
 
 
+GQ_TYPES = [N.Q4_K, N.Q6_K, N.Q5_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0, N.Q5_1]
+
+
+@pytest.mark.parametrize("t", GQ_TYPES, ids=[N.TYPE_NAMES[t] for t in GQ_TYPES])
+@pytest.mark.parametrize("K,n,op,group", [(14336, 16, "swiglu", False), (4096, 8, "geglu", True),
+                                          (1024, 40, "swiglu", True), (512, 3, "swiglu", False)])
+def test_glu_quantizes_for_its_mul_mats(gpu, t, K, n, op, group):
+    """A GLU feeding MUL_MATs of n >= 3 columns (the SwiGLU before the down
+    projection): the GLU kernel also writes the quantized activation (q8_K /
+    q8_0 / q8_1 codes, scales and sums; at n > 16 the q4_K / q5_K GEMM's f16
+    codes too) and no quantize launch runs. The GLU's output and every product
+    are bit-identical to the core GLU and tlh_mul_mat (its own quantize launch)
+    run one by one; K = 14336 takes the few-column kernel's K chunks."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    Ms = (256, 128) if group else (256,)
+    b = G.Builder()
+    gt = b.input(N.F32, [K, n])
+    up = b.input(N.F32, [K, n])
+    W = [b.weight(t, [K, m]) for m in Ms]
+    h = b.glu_split(gt, up, op)
+    outs = [b.mul_mat(w, h) for w in W]
+    for o in outs:
+        b.expand(o)
+    wd = [dev(synth.random_blocks(t, 102 + i, m, K)) for i, m in enumerate(Ms)]
+    prog = G.Program(b, outs + [h], wd)
+    gv, uv = dev(synth.normal(103, (n, K)) * 2), dev(synth.normal(104, (n, K)))
+    prog.write_input(0, gv)
+    prog.write_input(1, uv)
+    print(f"[glu-quant] {N.TYPE_NAMES[t]} K={K} n={n} {op} group={group}", flush=True)
+    prog.run()
+    hv = N.glu(op, gv, uv)
+    np.testing.assert_array_equal(prog.read(h, torch.float32).reshape(hv.shape).cpu().numpy(), hv.cpu().numpy())
+    for m, wdev, o in zip(Ms, wd, outs):
+        want = N.mul_mat(t, wdev, m, K, hv)
+        got = prog.read(o, torch.float32)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy().reshape(want.shape).view(np.uint32),
+                              want.cpu().numpy().view(np.uint32)), f"{N.TYPE_NAMES[t]} M={m}"
+    # dispatches: the GLU, then the products' compute launches (a group at
+    # n <= 16: one few-column launch over both matrices' rows)
+    assert prog.stats()["launches"] == 1 + (2 if group and n > 16 else 1)
+
+
 def test_program_refusals(gpu):
     c = decoder_tiny_config()
     dec = GpuDecoder(c, decoder_weights(c))
