@@ -172,17 +172,19 @@ template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r
 //         int16 [R][K/16] (q8_K)  bsums
 //   q16 : f16   [R][K]            (GEMM launches only) the codes as f16,
 //         exact, so the MFMA operand needs no conversion
+//   b16 : f16   [R][K/16]         (GEMM launches, q8_K only) the bsums as f16 (exact)
 struct ActView {
     const int8_t *qs;
     const float *d;
     const int32_t *sum32;  // q8_0: code sums; q8_1: the bits of s as f32
     const int16_t *bsums;  // q8_K only
     const _Float16 *q16;   // GEMM launches only
+    const _Float16 *b16;   // GEMM launches, q8_K only
     int64_t K;
 };
 
 struct ActLayout {
-    int64_t qs_off, d_off, sum_off, q16_off, total;
+    int64_t qs_off, d_off, sum_off, q16_off, b16_off, total;
 };
 
 // Weight types with a tiled prefill GEMM (more than 16 activation columns);
@@ -205,7 +207,9 @@ __host__ __device__ inline ActLayout act_layout(int act_type, int64_t K, int64_t
     L.sum_off = align_up(L.d_off + rows * nblk * 4, 256);
     const int64_t sum_bytes = act_type == TLH_TYPE_Q8_K ? rows * (K / 16) * 2 : rows * (K / 32) * 4;
     L.q16_off = align_up(L.sum_off + sum_bytes, 256);
-    L.total = align_up(L.q16_off + (f16 ? rows * K * 2 : 0), 256);
+    L.b16_off = align_up(L.q16_off + rows * K * 2, 256);
+    L.total = f16 ? align_up(L.b16_off + (act_type == TLH_TYPE_Q8_K ? rows * (K / 16) * 2 : 0), 256)
+                  : align_up(L.q16_off, 256);
     return L;
 }
 
@@ -218,6 +222,7 @@ __host__ __device__ inline ActView act_view(const void *base, int act_type, int6
     v.sum32 = (const int32_t *)(b + L.sum_off);
     v.bsums = (const int16_t *)(b + L.sum_off);
     v.q16 = (const _Float16 *)(b + L.q16_off);
+    v.b16 = (const _Float16 *)(b + L.b16_off);
     v.K = K;
     return v;
 }
@@ -301,7 +306,10 @@ __device__ __forceinline__ void q8K_store_split(char *out, const ActLayout &L, i
         }
         *(uint2 *)(out + L.q16_off + e0 * 2) = make_uint2(h[0], h[1]);
     }
-    if ((lane & 3) == 0) ((int16_t *)(out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
+    if ((lane & 3) == 0) {
+        ((int16_t *)(out + L.sum_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = (int16_t)psum;
+        if (f16) ((uint16_t *)(out + L.b16_off))[orow * (K / 16) + blk * 16 + (lane >> 2)] = f2h((float)psum);
+    }
     if (lane == 0) ((float *)(out + L.d_off))[orow * (K / QKK) + blk] = d;
 }
 

@@ -18,12 +18,13 @@
 //    super-block, as the CPU does (its f32 accumulation order differs).
 // Tiling: 128 (weight rows) x 128 (tokens) per workgroup of 4 waves, each
 // wave 64 x 64 as 2 x 2 MFMA tiles of 32 x 32; K advances in stages of one
-// 64-element q4_K chunk. Each stage is converted once per workgroup into f16
-// LDS tiles (nibble -> (1024 + n) * sc - 1024 * sc with one packed FMA; the
-// activation codes arrive as exact f16 from the quantize pass). LDS holds two
-// stage buffers: while the waves multiply stage s, the threads write stage
-// s + 1 (fetched one stage earlier) into the other buffer and fetch s + 2, one
-// barrier per stage.
+// 64-element q4_K chunk. LDS holds two stage buffers: while the waves
+// multiply stage s, stage s + 1 fills the other one. Its activation codes
+// (exact f16 from the quantize pass) go straight from global memory to LDS
+// (global_load_lds_dwordx4: no registers, no LDS writes); its weight codes
+// come to registers and are converted once per workgroup (nibble -> (1024 +
+// n) * sc - 1024 * sc with one packed FMA) and written after the products.
+// One barrier per stage.
 //
 // q5_K runs the same kernel with the fifth code bit OR-ed in before the f16
 // conversion (sc * q <= 63 * 31 stays exact). q8_0 / q4_0 have their own
@@ -80,16 +81,12 @@ __device__ __forceinline__ uint4 ldg16(const void *p) {
     return v;
 }
 
-// What one thread fetches from global memory for a stage: its weight row's
-// 16 code bytes (half h of the chunk) and super-block header, its token's 32
-// f16 codes (half h of the chunk); at a super-block's first chunk also the
-// token's scale and 16 bsums.
+// What one thread fetches to registers for a stage: its weight row's 16 code
+// bytes (half h of the chunk); at a super-block's first stage also its header.
 struct StageRegs {
-    uint4 wq, hdr, qh;  // qh: q5_K's fifth bits of the thread's 16 elements of each run
-    uint4 x[4];
-    uint4 bs0, bs1;
-    float dx;
+    uint4 wq, hdr, qh;  // hdr: at a super-block's first stage only; qh: q5_K's fifth bits
 };
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int WT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_gemm_q4k(const MatmulArgs a) {
@@ -113,35 +110,78 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     // staging roles: weight row / token tid >> 1, half h = tid & 1 of the 64-element chunk
     const int srow = tid >> 1, sh = tid & 1;
     const int64_t grow = m_base + srow < a.M ? m_base + srow : a.M - 1;  // clamped: loads in bounds
-    const int64_t gcol = n_base + srow < a.N ? n_base + srow : a.N - 1;
     const uint8_t *wrow = W + grow * a.w_nb1;
-    const int64_t arow = a.n0 + gcol + a.N_total * batch;
-    const _Float16 *xrow = act.q16 + arow * K;
+    // B tile rows (tokens) this lane fills by direct-to-LDS loads: instruction
+    // i of wave w fills rows 8 (4 w + i) .. + 7, lane l row + l / 8 at chunk
+    // position l % 8, i.e. the chunk (l % 8) ^ (row & 7) of the token's stage
+    const _Float16 *brow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * (4 * wave + i) + (lane >> 3);
+        const int64_t col = n_base + r < a.N ? n_base + r : a.N - 1;
+        brow[i] = act.q16 + (a.n0 + col + a.N_total * batch) * K + 8 * ((lane & 7) ^ (r & 7));
+    }
+    // the tokens' metadata of a super-block, also straight to LDS: bsums (f16
+    // from the quantize pass), wave w tokens 32 w .. + 31, lane l token
+    // 32 w + l / 2, bsums 8 (l & 1) .. + 7; scales, waves 0 and 1, 64 tokens each
+    const _Float16 *bsrow;
+    const float *dxrow;
+    {
+        const int r = 32 * wave + (lane >> 1);
+        const int64_t col = n_base + r < a.N ? n_base + r : a.N - 1;
+        bsrow = act.b16 + (a.n0 + col + a.N_total * batch) * (K / 16) + 8 * (lane & 1);
+        const int rd = 64 * (wave & 1) + lane;
+        const int64_t cold = n_base + rd < a.N ? n_base + rd : a.N - 1;
+        dxrow = act.d + (a.n0 + cold + a.N_total * batch) * nsb;
+    }
+    auto load_b = [&](int64_t stage) {
+        const int buf = (int)(stage & 1);
+        const int64_t sb = stage >> 2;
+        const int64_t off = sb * QKK + 64 * (stage & 3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(brow[i] + off), (lds_void *)&sm.B[buf][8 * (4 * wave + i)][0], 16,
+                                             0, 0);
+        if ((stage & 3) == 0) {
+            const int mb = (int)(sb & 1);
+            __builtin_amdgcn_global_load_lds((const void *)(bsrow + sb * 16), (lds_void *)&sm.Bsum[mb][32 * wave][0], 16, 0,
+                                             0);
+            if (wave < 2)
+                __builtin_amdgcn_global_load_lds((const void *)(dxrow + sb), (lds_void *)&sm.dB[mb][64 * wave], 4, 0, 0);
+        }
+    };
 
     auto fetch = [&](int64_t stage, StageRegs &r) {
         const int64_t sb = stage >> 2;
         const int j = (int)(stage & 3);
         const uint8_t *blk = wrow + sb * SB;
-        r.hdr = ldg16(blk);
+        if (j == 0) r.hdr = ldg16(blk);
         r.wq = ldg16(blk + QS + 32 * j + 16 * sh);
         if constexpr (Q5) r.qh = ldg16(blk + 16 + 16 * sh);
-        const _Float16 *xq = xrow + sb * QKK + 64 * j + 32 * sh;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r.x[i] = *(const uint4 *)(xq + 8 * i);
-        if (j == 0) {
-            r.dx = act.d[arow * nsb + sb];
-            const int16_t *bs = act.bsums + arow * (K / 16) + sb * 16;
-            r.bs0 = *(const uint4 *)bs;
-            r.bs1 = *(const uint4 *)(bs + 8);
-        }
     };
+    uint32_t scw[2] = {0, 0};  // the current super-block's 8 sub-block scales (bytes), from its header
 
     auto commit = [&](int64_t stage, const StageRegs &r) {
         const int buf = (int)(stage & 1), mb = (int)((stage >> 2) & 1);
         const int j = (int)(stage & 3);
-        int sclo, mnlo, schi, mnhi;
-        q4k_sm_g(2 * j, r.hdr.y, r.hdr.z, r.hdr.w, sclo, mnlo);
-        q4k_sm_g(2 * j + 1, r.hdr.y, r.hdr.z, r.hdr.w, schi, mnhi);
+        if (j == 0) {
+            uint32_t mv[2] = {0, 0};
+            scw[0] = scw[1] = 0;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                int sc, mn;
+                q4k_sm_g(s, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+                scw[s >> 2] |= (uint32_t)sc << (8 * (s & 3));
+                mv[s >> 2] |= (uint32_t)mn << (8 * (s & 3));
+            }
+            if (sh == 0) {
+                sm.dA[mb][srow] = h2f((uint16_t)(r.hdr.x & 0xffff));
+                sm.dminA[mb][srow] = h2f((uint16_t)(r.hdr.x >> 16));
+                *(uint2 *)&sm.Amin[mb][srow][0] = make_uint2(mv[0], mv[1]);
+            }
+        }
+        const int sclo = (int)((scw[j >> 1] >> (16 * (j & 1))) & 0xff);
+        const int schi = (int)((scw[j >> 1] >> (16 * (j & 1) + 8)) & 0xff);
         const _Float16 fl = (_Float16)sclo, fh = (_Float16)schi;
         const half2_t sl2 = {fl, fl}, sh2 = {fh, fh};
         const half2_t nsl2 = {(_Float16)(-1024 * sclo), (_Float16)(-1024 * sclo)};
@@ -165,31 +205,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         *(uint4 *)(ar + swz(srow, 2 * sh + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
         *(uint4 *)(ar + swz(srow, 4 + 2 * sh)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         *(uint4 *)(ar + swz(srow, 5 + 2 * sh)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-        _Float16 *br = sm.B[buf][srow];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *(uint4 *)(br + swz(srow, 4 * sh + i)) = r.x[i];
-        if (j == 0 && sh == 0) {
-            sm.dA[mb][srow] = h2f((uint16_t)(r.hdr.x & 0xffff));
-            sm.dminA[mb][srow] = h2f((uint16_t)(r.hdr.x >> 16));
-            uint32_t mv[2] = {0, 0};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                int sc, mn;
-                q4k_sm_g(s, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
-                mv[s >> 2] |= (uint32_t)mn << (8 * (s & 3));
-            }
-            *(uint2 *)&sm.Amin[mb][srow][0] = make_uint2(mv[0], mv[1]);
-            sm.dB[mb][srow] = r.dx;
-            const uint32_t bw[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
-            uint32_t bh[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int lo16 = (int)(int16_t)(bw[i] & 0xffff), hi16 = (int)(int16_t)(bw[i] >> 16);
-                bh[i] = (uint32_t)f2h((float)lo16) | ((uint32_t)f2h((float)hi16) << 16);
-            }
-            *(uint4 *)&sm.Bsum[mb][srow][0] = make_uint4(bh[0], bh[1], bh[2], bh[3]);
-            *(uint4 *)&sm.Bsum[mb][srow][8] = make_uint4(bh[4], bh[5], bh[6], bh[7]);
-        }
     };
 
     float16_t S[2][2], acc[2][2];
@@ -208,13 +223,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int64_t g0 = 4 * sb0, stages = 4 * sb1;
     StageRegs pre;
     if (g0 < stages) {
+        load_b(g0);
         fetch(g0, pre);
         commit(g0, pre);
-        if (g0 + 1 < stages) fetch(g0 + 1, pre);
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct-to-LDS loads landed
     lds_barrier();
     for (int64_t st = g0; st < stages; ++st) {
         const int buf = (int)(st & 1);
+        // stage st + 1: B straight to the free LDS buffer, A to registers
+        if (st + 1 < stages) {
+            load_b(st + 1);
+            fetch(st + 1, pre);
+        }
 #pragma unroll
         for (int t = 0; t < GBK / 16; ++t) {
             half8_t av[2], bv[2];
@@ -269,12 +290,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 }
             }
         }
-        // stage st + 1 goes to the other buffer (free since the last barrier),
-        // stage st + 2 is fetched behind this stage's products
-        if (st + 1 < stages) {
-            commit(st + 1, pre);
-            if (st + 2 < stages) fetch(st + 2, pre);
-        }
+        // stage st + 1's A to the other buffer (free since the last barrier)
+        if (st + 1 < stages) commit(st + 1, pre);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): stage st + 1's B landed
         lds_barrier();
     }
 
