@@ -75,7 +75,8 @@ def test_mul_mat_scratch_sizes(wt, n):
     be = N.BLOCK[at][0]
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
     sums = n * (K // 16) * 2 if at == N.Q8_K else n * (K // 32) * 4
-    f16_codes = n * K * 2 if wt == N.Q4_K and n > 16 else 0  # q4_K GEMM launches also stage f16 codes
+    # q4_K GEMM launches also stage the codes and the bsums as f16
+    f16_codes = al(n * K * 2) + n * (K // 16) * 2 if wt == N.Q4_K and n > 16 else 0
     # a GEMM of fewer 128 x 128 tiles than CUs (256) splits K into up to 512 / tiles
     # chunks of at least 4 x 256 elements (at most 16) with f32 partials [chunk][N][M]
     tiles = -(-n // 128) * -(-M // 128)
