@@ -245,11 +245,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 av[i] = *(const half8_t *)&sm.A[buf][ra][swz(ra, 2 * t + lg)];
                 bv[i] = *(const half8_t *)&sm.B[buf][rb][swz(rb, 2 * t + lg)];
             }
+            if (t == 0 && (st & 3) == 0) {  // a super-block's first products start from zero
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int jn = 0; jn < 2; ++jn)
-                    S[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[jn], S[i][jn], 0, 0, 0);
+                    for (int jn = 0; jn < 2; ++jn)
+                        S[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[jn], (float16_t){}, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int jn = 0; jn < 2; ++jn)
+                        S[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[jn], S[i][jn], 0, 0, 0);
+            }
         }
         if ((st & 3) == 3) {
             // super-block finalize: acc += dy * (d * S - dmin * Mn)
@@ -286,7 +294,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                             acc[i][jn][r] += dy * (dv[e] * S[i][jn][r] - dmv[e] * Mn[r]);
                         }
                     }
-                    S[i][jn] = (float16_t){};
                 }
             }
         }
