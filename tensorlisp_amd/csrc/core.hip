@@ -645,26 +645,39 @@ tlh_status launch_argmax_split(const tlh_op &op, const void *x, void *dst, void 
 // theta = pos * theta_scale^p / freq_factor, mixed with its interpolation by
 // the ramp over [corr0, corr1] when ext_factor != 0; dims past n_dims pass
 // through. One thread per pair.
-__device__ __forceinline__ void body_rope(const CoreArgs &a, int64_t bx, int64_t row) {
+// One token (i2, i3) per block (bx: a chunk of 256 pairs when a row has more),
+// every head i1 of it: thread t takes pair t % P of heads t / P, t / P + 256 / P,
+// ... (P = pairs per row, at most 256), so the angle's cos / sin -- the
+// position times theta_scale^p by repeated products, then cosf / sinf -- is
+// formed once per pair and token, not once per head.
+__device__ __forceinline__ void body_rope(const CoreArgs &a, int64_t bx, int64_t tok) {
     const tlh_tensor &x = a.op.t[0], &ps = a.op.t[1], &d = a.op.t[4];
     const int n_dims = (int)a.op.x[0], mode = (int)a.op.x[1];
     const float freq_scale = __int_as_float((int)a.op.x[2]), ext_factor = __int_as_float((int)a.op.x[3]);
     const float attn_factor = __int_as_float((int)a.op.x[4]), theta_scale = __int_as_float((int)a.op.x[5]);
     const float corr0 = __int_as_float((int)a.op.x[6]), corr1 = __int_as_float((int)a.op.x[7]);
     const bool has_ff = a.op.x[8] != 0;
-    if (row >= x.ne[1] * x.ne[2] * x.ne[3]) return;
-    int64_t i1, i2, i3;
-    row_coords(row, x, i1, i2, i3);
-    const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+    if (tok >= x.ne[2] * x.ne[3]) return;
+    const int64_t i2 = tok % x.ne[2], i3 = tok / x.ne[2];
+    const int64_t P = x.ne[0] / 2;
+    const int64_t per = P < 256 ? P : 256;  // pairs per pass
+    const int64_t hstep = 256 / per;          // heads per pass
+    const int64_t p = bx * 256 + threadIdx.x % per;
+    const int64_t h0 = threadIdx.x / per;
+    if (p >= P || h0 >= hstep) return;
     // x9 = 1: the rotated row of token i2 lands in row idx[i2] of a cache whose
     // rows hold every head of a token (the SET_ROWS of the reshaped result)
-    char *dr = a.op.x[9] ? a.dst + ld_idx(a.s3 + i2 * a.op.t[3].nb[0], a.op.t[3].ty) * d.nb[1] + i1 * x.ne[0] * d.nb[0]
-                         : a.dst + offs(d, 0, i1, i2, i3);
-    const int64_t p = bx * 256 + threadIdx.x;  // pair index
-    if (p >= x.ne[0] / 2) return;
+    const int64_t crow = a.op.x[9] ? ld_idx(a.s3 + i2 * a.op.t[3].nb[0], a.op.t[3].ty) : 0;
+    auto dst_row = [&](int64_t i1) {
+        return a.op.x[9] ? a.dst + crow * d.nb[1] + i1 * x.ne[0] * d.nb[0] : a.dst + offs(d, 0, i1, i2, i3);
+    };
     if (2 * p >= n_dims) {  // past the rotated dims: copy both elements of the pair
-        st_f(dr + 2 * p * d.nb[0], d.ty, ld_f(xr + 2 * p * x.nb[0], x.ty));
-        st_f(dr + (2 * p + 1) * d.nb[0], d.ty, ld_f(xr + (2 * p + 1) * x.nb[0], x.ty));
+        for (int64_t i1 = h0; i1 < x.ne[1]; i1 += hstep) {
+            const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+            char *dr = dst_row(i1);
+            st_f(dr + 2 * p * d.nb[0], d.ty, ld_f(xr + 2 * p * x.nb[0], x.ty));
+            st_f(dr + (2 * p + 1) * d.nb[0], d.ty, ld_f(xr + (2 * p + 1) * x.nb[0], x.ty));
+        }
         return;
     }
     const float ff = has_ff ? *(const float *)(a.s2 + p * 4) : 1.0f;
@@ -675,9 +688,28 @@ __device__ __forceinline__ void body_rope(const CoreArgs &a, int64_t bx, int64_t
     rope_cs_sn((float)*(const int32_t *)(a.s1 + i2 * ps.nb[0]), p, ff, rp, cs, sn);
     const int64_t ia = mode == 0 ? 2 * p : p;
     const int64_t ib = mode == 0 ? 2 * p + 1 : p + n_dims / 2;
-    const float x0 = ld_f(xr + ia * x.nb[0], x.ty), x1 = ld_f(xr + ib * x.nb[0], x.ty);
-    st_f(dr + ia * d.nb[0], d.ty, rope_first(x0, x1, cs, sn));
-    st_f(dr + ib * d.nb[0], d.ty, rope_second(x0, x1, cs, sn));
+    // heads in groups of eight: the group's loads all go out before its stores
+    for (int64_t g0 = h0; g0 < x.ne[1]; g0 += 8 * hstep) {
+        float x0[8], x1[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t i1 = g0 + k * hstep;
+            if (i1 < x.ne[1]) {
+                const char *xr = a.s0 + offs(x, 0, i1, i2, i3);
+                x0[k] = ld_f(xr + ia * x.nb[0], x.ty);
+                x1[k] = ld_f(xr + ib * x.nb[0], x.ty);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t i1 = g0 + k * hstep;
+            if (i1 < x.ne[1]) {
+                char *dr = dst_row(i1);
+                st_f(dr + ia * d.nb[0], d.ty, rope_first(x0[k], x1[k], cs, sn));
+                st_f(dr + ib * d.nb[0], d.ty, rope_second(x0[k], x1[k], cs, sn));
+            }
+        }
+    }
 }
 __global__ void __launch_bounds__(256) k_core_rope(const CoreArgs a) {
     body_rope(a, blockIdx.x, blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
@@ -791,9 +823,9 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         break;
     }
     case TLH_CORE_ROPE: {
-        const int64_t rows = nrows(x);
-        if (rows == 0 || x.ne[0] < 2) return TLH_OK;
-        hipLaunchKernelGGL(k_core_rope, row_grid((x.ne[0] / 2 + 255) / 256, rows), dim3(256), 0, stream, a);
+        const int64_t toks = x.ne[2] * x.ne[3];
+        if (nrows(x) == 0 || x.ne[0] < 2) return TLH_OK;
+        hipLaunchKernelGGL(k_core_rope, row_grid((x.ne[0] / 2 + 255) / 256, toks), dim3(256), 0, stream, a);
         break;
     }
     default: return set_error(TLH_INVALID, "core: unknown kind %d", kind);
@@ -838,7 +870,7 @@ static bool ew_grid(int kind, const tlh_op &op, int64_t &gx, int64_t &rows) {
         gx = (d.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows = nrows(d);
         return true;
     case TLH_CORE_SET_ROWS: gx = (x.ne[0] + CORE_CHUNK - 1) / CORE_CHUNK, rows = nrows(x); return true;
-    case TLH_CORE_ROPE: gx = (x.ne[0] / 2 + 255) / 256, rows = nrows(x); return true;
+    case TLH_CORE_ROPE: gx = (x.ne[0] / 2 + 255) / 256, rows = x.ne[2] * x.ne[3]; return true;  // blocks: tokens
     default: return false;
     }
 }
