@@ -921,6 +921,7 @@ struct NormChainArgs {
     tlh_op op;
     const float *p, *q, *w;
     float *s, *y;
+    ActQuantOut qo;  // qo.type != 0: y also goes to a MUL_MAT's activation scratch
 };
 
 constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows up to 4096 in one read
@@ -1022,23 +1023,58 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
 #pragma unroll
     for (int j = 0; j < NC_CACHE; ++j) {
         const int i0 = 4 * (t + 256 * j);
-        float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = ((c[j][e] - mean) * scale) * wv[j][e];
+        for (int e = 0; e < 4; ++e) c[j][e] = ((c[j][e] - mean) * scale) * wv[j][e];  // y (kept for quantizing)
         if (VEC) {
-            if (i0 < n) *(float4 *)(yr + i0) = make_float4(o[0], o[1], o[2], o[3]);
+            if (i0 < n) *(float4 *)(yr + i0) = make_float4(c[j][0], c[j][1], c[j][2], c[j][3]);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (i0 + e < n) yr[i0 + e] = o[e];
+                if (i0 + e < n) yr[i0 + e] = c[j][e];
+        }
+    }
+    if (a.qo.type) {
+        // c[j] of wave t / 64 holds elements 1024 j + 256 (t / 64) .. + 255 of
+        // the row (n <= 4096: all of it): a q8_K super-block in the quantize
+        // launch's lane layout, or four 8-lane q8_0 / q8_1 blocks
+        const int64_t row = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;  // = the activation row
+        const ActLayout QL = act_layout(a.qo.type, n, a.qo.rows, a.qo.f16);
+        const int lane = t & 63, w = t >> 6;
+        if (a.qo.type == TLH_TYPE_Q8_K) {
+            uint32_t pk[NC_CACHE];
+            int ps[NC_CACHE];
+            float d[NC_CACHE];
+            q8K_waves<NC_CACHE>(c, lane, pk, ps, d);
+#pragma unroll
+            for (int j = 0; j < NC_CACHE; ++j)
+                if (1024 * j + 256 * w < n)  // wave-uniform (n % 256 == 0)
+                    q8K_store_split((char *)a.qo.out, QL, n, row, 4 * j + w, lane, pk[j], ps[j], d[j], a.qo.f16);
+        } else {
+            bool live[NC_CACHE];
+            int64_t col[NC_CACHE];
+#pragma unroll
+            for (int j = 0; j < NC_CACHE; ++j) {
+                col[j] = 4 * (t + 256 * j);
+                live[j] = col[j] < n;  // whole 8-lane groups (n % 32 == 0)
+            }
+            if (a.qo.type == TLH_TYPE_Q8_1)
+                q80_quads_store_split<NC_CACHE, true>(c, live, lane, (char *)a.qo.out, QL, n, row, col, a.qo.f16);
+            else
+                q80_quads_store_split<NC_CACHE, false>(c, live, lane, (char *)a.qo.out, QL, n, row, col, a.qo.f16);
         }
     }
     for (int i = 4 * 256 * NC_CACHE + 4 * t; i < n; i += 4 * 256)
         for (int e = 0; e < 4 && i + e < n; ++e) yr[i + e] = ((value(i + e) - mean) * scale) * wr[i + e];
 }
 
+bool norm_chain_quantize_ok(const tlh_op &op, int act_type) {
+    const int64_t n = op.t[0].ne[0];
+    const int be = act_type == TLH_TYPE_Q8_K ? QKK : act_type == TLH_TYPE_Q8_0 || act_type == TLH_TYPE_Q8_1 ? QK : 0;
+    return be > 0 && n > 0 && n % be == 0 && n <= NORM_CHAIN_QUANT_MAX;
+}
+
 tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
-                             hipStream_t stream) {
+                             hipStream_t stream, const ActQuantOut *qo) {
     NormChainArgs a;
     a.op = op;
     a.p = (const float *)p;
@@ -1048,6 +1084,12 @@ tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, con
     a.y = (float *)y;
     const int64_t rows = nrows(op.t[0]);
     if (rows == 0) return TLH_OK;
+    if (qo && qo->type) {
+        if (!norm_chain_quantize_ok(op, qo->type) || !qo->out || ((uintptr_t)qo->out & 255) || qo->rows != rows)
+            return set_error(TLH_INVALID, "norm_chain: cannot quantize rows of %lld into type %d",
+                             (long long)op.t[0].ne[0], qo->type);
+        a.qo = *qo;
+    }
     const tlh_tensor *ts[5] = {&op.t[0], &op.t[1], &op.t[2], &op.t[3], &op.t[4]};
     const void *ps[5] = {p, q, w, s, y};
     bool vec = op.t[0].ne[0] % 4 == 0;

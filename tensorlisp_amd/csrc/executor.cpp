@@ -66,8 +66,8 @@ struct Dispatch {
     int has_norm = 0, has_glu = 0;
     tlh_op nop, gop;
     Place nsrc[4], ndst, gdst;
-    // D_CORE GLU: also quantizes its output for a MUL_MAT (type, activation
-    // rows, f16 codes) into that MUL_MAT's scratch block
+    // D_CORE GLU, D_NORM_CHAIN: also quantizes its output for a MUL_MAT (type,
+    // activation rows, f16 codes) into that MUL_MAT's scratch block
     int nq_type = 0, nq_f16 = 0;
     int64_t nq_rows = 0;
     int32_t pw[4] = {0, 0, 0, 0};
@@ -214,7 +214,7 @@ class Lowering {
         group_elementwise(out.d);
         group_mul_mats(out.d);
         merge_mm_computes(out.d);
-        fuse_glu_quantize(out.d);
+        fuse_act_quantize(out.d);
         group_elementwise(out.d);  // merged computes can leave element-wise launches adjacent
         plan(out);
         return TLH_OK;
@@ -1289,14 +1289,19 @@ class Lowering {
     }
 
     // A MUL_MAT of 3 or more columns whose activation is a GLU's output (the
-    // SwiGLU before the down projection): the GLU launch also writes the
-    // quantized rows (the bytes the quantize launch would write) into the
-    // MUL_MAT's scratch, and the MUL_MAT keeps only its compute launch; a
-    // quantization group's leader quantize goes the same way. Needs: src1 is
-    // the GLU's whole output, contiguous f32 rows (a multiple of the block)
-    // in the same order, and nothing between the two writes that storage.
-    // The scratch then lives from the GLU on.
-    void fuse_glu_quantize(std::vector<Dispatch> &d) {
+    // SwiGLU before the down projection), or a norm chain's output over at
+    // least NQ_MIN_ROWS rows (the RMS_NORM before Q / K / V and gate / up in a
+    // prefill): that launch also writes the quantized rows (the bytes the
+    // quantize launch would write) into the MUL_MAT's scratch, and the MUL_MAT
+    // keeps only its compute launch; a quantization group's leader quantize
+    // goes the same way. Needs: src1 is the producer's whole output,
+    // contiguous f32 rows (a multiple of the block) in the same order, and
+    // nothing between the two writes that storage. The scratch then lives from
+    // the producer on. (A norm chain works one row per workgroup: over few rows
+    // the quantization lengthens its one serial path by about what the
+    // separate launch costs, so there it stays apart.)
+    static constexpr int64_t NQ_MIN_ROWS = 64;
+    void fuse_act_quantize(std::vector<Dispatch> &d) {
         auto contiguous_f32 = [](const tlh_tensor &t) {
             return t.ty == TLH_TYPE_F32 && t.nb[0] == 4 && t.nb[1] == 4 * t.ne[0] && t.nb[2] == t.nb[1] * t.ne[1] &&
                    t.nb[3] == t.nb[2] * t.ne[2];
@@ -1319,7 +1324,8 @@ class Lowering {
             for (int j = (int)i - 1; j >= 0; --j) {
                 if (gone[j]) continue;
                 const Dispatch &c = d[j];
-                if (c.kind == D_CORE && c.core_kind == TLH_CORE_GLU && same_place(c.dst, q.src[1])) {
+                if (((c.kind == D_CORE && c.core_kind == TLH_CORE_GLU) || c.kind == D_NORM_CHAIN) &&
+                    same_place(c.dst, q.src[1])) {
                     gi = j;
                     break;
                 }
@@ -1331,8 +1337,10 @@ class Lowering {
             if (gi < 0) continue;
             Dispatch &g = d[gi];
             const tlh_tensor &y = g.op.t[4];
-            if (g.block != -1 || !contiguous_f32(y) || y.ne[0] != K || y.ne[1] * y.ne[2] * y.ne[3] != rows ||
-                !glu_quantize_ok(g.op, at))
+            if (g.block != -1 || !contiguous_f32(y) || y.ne[0] != K || y.ne[1] * y.ne[2] * y.ne[3] != rows)
+                continue;
+            if (g.kind == D_NORM_CHAIN ? rows < NQ_MIN_ROWS || !norm_chain_quantize_ok(g.op, at)
+                                       : !glu_quantize_ok(g.op, at))
                 continue;
             if (single) {  // a group of one: its scratch block spans GLU .. MUL_MAT
                 Group gr;
@@ -1554,7 +1562,17 @@ struct tlh_program {
             case D_FLASH_ATTN:
                 st = tlh_flash_attn_ext(&x.op, src[0], src[1], src[2], src[3], dst, scratch, x.scratch_bytes, s);
                 break;
-            case D_NORM_CHAIN: st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s); break;
+            case D_NORM_CHAIN: {
+                ActQuantOut qo;
+                if (x.nq_type) {
+                    qo.out = scratch;
+                    qo.type = x.nq_type;
+                    qo.rows = x.nq_rows;
+                    qo.f16 = x.nq_f16 != 0;
+                }
+                st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s, x.nq_type ? &qo : nullptr);
+                break;
+            }
             case D_PAGED_ATTN: {
                 tlh_paged_attention_args a = x.pa;
                 a.out = dst;

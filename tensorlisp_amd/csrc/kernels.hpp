@@ -176,10 +176,6 @@ tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *c
 // not allow it.
 tlh_status mul_mat_multi_pro(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
                              const GemvPro &pro, const void *x, hipStream_t stream);
-// [ADD ->] RMS_NORM / NORM -> MUL(weight) in one kernel (core.hip k_norm_chain);
-// op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
-tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
-                             hipStream_t stream);
 // A kernel's rows quantized as it writes them: the activation scratch of a
 // MUL_MAT (split layout of `type` = q8_0 / q8_1 / q8_K for `rows` activation
 // rows, f16 codes too when `f16`), row r of the kernel's output being
@@ -190,6 +186,14 @@ struct ActQuantOut {
     int64_t rows = 0;
     bool f16 = false;
 };
+// Longest row the norm chain quantizes (the row is held in registers).
+constexpr int64_t NORM_CHAIN_QUANT_MAX = 4096;
+// [ADD ->] RMS_NORM / NORM -> MUL(weight) in one kernel (core.hip k_norm_chain);
+// op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
+// With qo, y is also quantized into qo's scratch (norm_chain_quantize_ok).
+bool norm_chain_quantize_ok(const tlh_op &op, int act_type);
+tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
+                             hipStream_t stream, const ActQuantOut *qo = nullptr);
 // GGML_OP_GLU (the core op's operands, f32 rows of unit element stride) that
 // also quantizes its output rows into qo (row length a multiple of qo's block).
 bool glu_quantize_ok(const tlh_op &op, int act_type);

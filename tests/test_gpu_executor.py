@@ -210,6 +210,56 @@ def test_glu_quantizes_for_its_mul_mats(gpu, t, K, n, op, group):
     assert prog.stats()["launches"] == 1 + (2 if group and n > 16 else 1)
 
 
+NQ_TYPES = [N.Q4_K, N.Q6_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0]
+
+
+@pytest.mark.parametrize("t", NQ_TYPES, ids=[N.TYPE_NAMES[t] for t in NQ_TYPES])
+@pytest.mark.parametrize("K,n,add", [(4096, 64, True), (1024, 100, False), (4096, 16, True)])
+def test_norm_chain_quantizes_for_its_mul_mats(gpu, t, K, n, add):
+    """[ADD ->] RMS_NORM -> MUL feeding MUL_MATs over 64 or more rows (a
+    prefill): the norm kernel also writes the group's quantized activation
+    (q8_K / q8_0 / q8_1 codes, scales and sums; at n > 16 the q4_K GEMM's f16
+    codes and bsums too) and no quantize launch runs; over fewer rows (16) the
+    quantize launch stays. Either way the norm's outputs and every product are
+    bit-identical to the core ops and tlh_mul_mat run one by one."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    Ms = (256, 128)
+    b = G.Builder()
+    p = b.input(N.F32, [K, n])
+    q = b.input(N.F32, [K, n])
+    nw = b.weight(N.F32, [K])
+    W = [b.weight(t, [K, m]) for m in Ms]
+    s = b.add(p, q) if add else p
+    y = b.mul(b.rms_norm(s, 1e-5), nw)
+    outs = [b.mul_mat(w, y) for w in W]
+    for o in outs:
+        b.expand(o)
+    nwh = dev((1.0 + 0.1 * synth.normal(111, (K,))).astype(np.float32))
+    wd = [dev(synth.random_blocks(t, 112 + i, m, K)) for i, m in enumerate(Ms)]
+    prog = G.Program(b, outs + [y] + ([s] if add else []), [nwh] + wd)
+    pv, qv = dev(synth.normal(113, (n, K)) * 2 + 0.3), dev(synth.normal(114, (n, K)))
+    prog.write_input(0, pv)
+    prog.write_input(1, qv)
+    print(f"[norm-quant] {N.TYPE_NAMES[t]} K={K} n={n} add={add}", flush=True)
+    prog.run()
+    sv = N.add(pv, qv) if add else pv
+    yv = N.mul(N.norm(sv, 1e-5, rms=True), nwh)
+    np.testing.assert_array_equal(prog.read(y, torch.float32).reshape(yv.shape).cpu().numpy(), yv.cpu().numpy())
+    for m, wdev, o in zip(Ms, wd, outs):
+        want = N.mul_mat(t, wdev, m, K, yv)
+        got = prog.read(o, torch.float32)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy().reshape(want.shape).view(np.uint32),
+                              want.cpu().numpy().view(np.uint32)), f"{N.TYPE_NAMES[t]} M={m}"
+    # dispatches: the norm chain, the quantize launch when it stays apart, then
+    # the products (n <= 16: one few-column launch over both matrices' rows)
+    fused = n >= 64
+    assert prog.stats()["launches"] == 1 + (0 if fused else 1) + (1 if n <= 16 else 2)
+
+
 def test_program_refusals(gpu):
     c = decoder_tiny_config()
     dec = GpuDecoder(c, decoder_weights(c))
