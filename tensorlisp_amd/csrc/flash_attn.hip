@@ -158,6 +158,7 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
             int jt = j0;  // keys past the 16-byte runs, one by one
             if (a.mask_vec) {
                 const int jv = j0 + (j1 - j0) / 8 * 8;
+#pragma unroll 8
                 for (int jb = j0 + 8 * g; jb < jv; jb += 32) {
                     const uint4 w = *(const uint4 *)(mr + jb);
                     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -384,6 +385,275 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
     }
 }
 
+// Prefill form for head size 128 (D = DV), many queries: a workgroup of 8
+// waves owns 64 rows in 4 groups of 16 -- group r the 16 queries qb + 16 (r /
+// gw) .. + 15 of head hk * G + hc * gw + r % gw (gw = min(G, 4) heads of the KV
+// head's group) -- and walks the keys in 64-key tiles that every wave reads
+// from LDS: each K / V row is fetched from L2 once per 64 rows instead of once
+// per 16. Waves r and r + 4 share row group r, each taking 32 of a tile's 64
+// keys (two waves a SIMD hide each other's latencies), and merge at the end. The tiles
+// come straight from global memory (global_load_lds_dwordx4, double-buffered:
+// tile t + 1 loads while tile t is multiplied). K rows are stored with their
+// 16-byte chunks XOR-swizzled by the key (chunk q of key c at position
+// q ^ (c % 16)), so the A-operand reads of 16 keys hit distinct banks; V rows
+// as they are (the B-operand pieces of one key are contiguous). Per wave and
+// 16-key step the arithmetic is k_flash_attn's (S^T = K . Q^T, online softmax
+// on S^T's lane layout, O += P . V on 8 output tiles); no key partitions.
+constexpr int FR_TK = 64;    // keys per tile
+constexpr int FR_ROW = 256;  // bytes of a K / V row (128 f16)
+typedef __attribute__((address_space(3))) void fa_lds_void;
+
+struct FaRowsArgs {
+    FaArgs f;
+    int gw;   // heads per workgroup (waves share the query block when gw < 4)
+    int QB;   // query blocks of 64 / gw queries
+};
+
+template <bool MASK>
+__global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
+    const FaArgs &a = ra.f;
+    // two buffers as four separate arrays, each named statically where it is
+    // read or filled: the compiler then sees that the reads of one buffer do not
+    // overlap the direct-to-LDS loads into the other, and inserts no wait for
+    // those loads before every read
+    __shared__ __attribute__((aligned(16))) uint8_t K0[FR_TK][FR_ROW], K1[FR_TK][FR_ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t V0[FR_TK][FR_ROW], V1[FR_TK][FR_ROW];
+    __shared__ __attribute__((aligned(16))) uint16_t M0[64][FR_TK], M1[64][FR_TK];  // mask tiles: row 16 rg + c
+    __shared__ float Mo[4][16][128], Mm[4][16], Ml[4][16];  // the key halves' merge
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rg = wave & 3, kh = wave >> 2;  // row group, key half
+    const int g = lane >> 4, c = lane & 15;
+    const int gw = ra.gw, qpw = 64 / gw;  // queries per workgroup
+    // heavy (late) query blocks first: causal rows at the end see the most keys
+    const int qblk = ra.QB - 1 - (int)(blockIdx.x % ra.QB);
+    const int hc = (int)(blockIdx.x / ra.QB);
+    const int hk = blockIdx.y, ib = blockIdx.z;
+    const int q0 = qblk * qpw + 16 * (rg / gw);
+    const int h = hk * a.G + hc * gw + rg % gw;
+    const int iq = q0 + c;  // this lane's row (query) in S^T's layout
+    const bool rlive = iq < a.nq;
+    const int iqc = rlive ? iq : a.nq - 1;
+    const int L = a.L;
+
+    // Q^T operand of the wave's rows (row c: query iq of head h), rounded to f16
+    fa_half4 qb[8];
+    {
+        const float *qrow = (const float *)(a.q + iqc * a.q_nb1 + h * a.q_nb2 + ib * a.q_nb3);
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const int d0 = 32 * (st / 2) + 8 * g + 4 * (st % 2);
+            fa_half4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (_Float16)qrow[d0 + e];
+            qb[st] = rlive ? v : (fa_half4){};
+        }
+    }
+    float slope = 1.0f;
+    const char *mdma = nullptr;  // the mask row this lane's DMA fills: row 8 wave + lane / 8, keys 8 (lane % 8) ..
+    if constexpr (MASK) {
+        if (a.max_bias > 0.0f)
+            slope = h < a.nhl2 ? powf(a.m0, (float)(h + 1)) : powf(a.m1, (float)(2 * (h - a.nhl2) + 1));
+        const int R = 8 * wave + (lane >> 3), rgR = R >> 4, cR = R & 15;
+        const int qR = min(qblk * qpw + 16 * (rgR / gw) + cR, a.nq - 1);
+        const int hR = hk * a.G + hc * gw + rgR % gw;
+        mdma = a.mask + qR * a.m_nb1 + (int64_t)(hR % a.m_ne2) * a.m_nb2 + (int64_t)(ib % a.m_ne3) * a.m_nb3;
+    }
+    const float scale = a.scale, softcap = a.softcap;
+    const char *kb = a.k + hk * a.k_nb2 + (ib / a.rk3) * a.k_nb3;
+    const char *vb = a.v + hk * a.v_nb2 + (ib / a.rk3) * a.v_nb3;
+
+    // tile loads: instruction i of wave w fills keys 4 (2 w + i) .. + 3 of the
+    // tile, lane l key + l / 16 at chunk position l % 16 (K: the chunk
+    // (l % 16) ^ (key % 16) of the row; V: chunk l % 16). Keys past L read
+    // row L - 1 (their scores are masked).
+    const int ntiles = (L + FR_TK - 1) / FR_TK;
+    auto load_tile = [&](int t, uint8_t (&Kd)[FR_TK][FR_ROW], uint8_t (&Vd)[FR_TK][FR_ROW]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int kk = 4 * (2 * wave + i) + (lane >> 4);
+            const int key = min(FR_TK * t + kk, L - 1);
+            const int pos = lane & 15;
+            __builtin_amdgcn_global_load_lds((const void *)(kb + (int64_t)key * a.k_nb1 + 16 * (pos ^ (kk & 15))),
+                                             (fa_lds_void *)&Kd[4 * (2 * wave + i)][0], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(vb + (int64_t)key * a.v_nb1 + 16 * pos),
+                                             (fa_lds_void *)&Vd[4 * (2 * wave + i)][0], 16, 0, 0);
+        }
+    };
+    // the mask tile (64 rows x 64 keys) straight to LDS with K and V: wave w
+    // fills rows 8w .. 8w + 7, lane l 16 bytes (keys 8 (l % 8) ..) of row
+    // 8w + l / 8. L is a multiple of 8, so no 8-key chunk straddles the end;
+    // chunks past it reread the last one (those keys are masked by index).
+    auto load_mask = [&](int t, uint16_t (&Md)[64][FR_TK]) {
+        if constexpr (MASK) {
+            const int key = min(FR_TK * t + 8 * (lane & 7), L - 8);
+            __builtin_amdgcn_global_load_lds((const void *)(mdma + 2 * key), (fa_lds_void *)&Md[8 * wave][0], 16, 0, 0);
+        }
+    };
+
+    // Online softmax with lazy rescaling: m_ref, the value the exponentials are
+    // taken against, moves to the running max only when that has grown by more
+    // than 8 (then O and l are rescaled); otherwise p = exp(s - m_ref) <= e^8,
+    // well inside f16 for the P operand, and the final O / l is unchanged.
+    float m_ref = -INFINITY, l_run = 0.0f;
+    fa_f32x4 o[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[n] = (fa_f32x4){};
+
+    // tile t from (Kc, Vc) with mask values mkc, while tile t + 1 goes to
+    // (Kn, Vn) and its mask values to mkn; this wave takes the tile's keys
+    // 32 kh .. + 31 as one step of two 16-key halves
+    auto tile = [&](int t, const uint8_t (&Kc)[FR_TK][FR_ROW], const uint8_t (&Vc)[FR_TK][FR_ROW],
+                    uint8_t (&Kn)[FR_TK][FR_ROW], uint8_t (&Vn)[FR_TK][FR_ROW], const uint16_t (&Mc)[64][FR_TK],
+                    uint16_t (&Mn)[64][FR_TK]) {
+        if (t + 1 < ntiles) {  // the other buffer: free since the last barrier
+            load_tile(t + 1, Kn, Vn);
+            load_mask(t + 1, Mn);
+        }
+        const int kt = FR_TK * t + 32 * kh;  // first key of this wave's step
+        // this lane's mask values: row c of the group, keys 4g .. 4g + 3 of each half
+        uint32_t mkc[2][4];
+        if constexpr (MASK) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const uint2 mw = *(const uint2 *)&Mc[16 * rg + c][32 * kh + 16 * hf + 4 * g];
+                mkc[hf][0] = mw.x & 0xffffu, mkc[hf][1] = mw.x >> 16, mkc[hf][2] = mw.y & 0xffffu, mkc[hf][3] = mw.y >> 16;
+            }
+        }
+        // nothing live for any of the wave's rows in its 32 keys: skip (uniform)
+        bool live = kt < L;
+        if constexpr (MASK) {
+            bool any = false;
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) any = any || (mkc[st][r] != 0xfc00u && kt + 16 * st + 4 * g + r < L);
+            live = live && __builtin_amdgcn_ballot_w64(any && rlive) != 0;
+        }
+        if (live) {
+            // S^T (key 4g + r, row c) of both halves: four independent chains
+            fa_f32x4 S[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                fa_f32x4 S0 = (fa_f32x4){}, S1 = (fa_f32x4){};
+                const uint8_t *kr = &Kc[32 * kh + 16 * hf + c][0];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 kf = *(const uint4 *)(kr + 16 * ((4 * i + g) ^ c));
+                    S0 = fa_mfma(as_h4(kf.x, kf.y), qb[2 * i], S0);
+                    S1 = fa_mfma(as_h4(kf.z, kf.w), qb[2 * i + 1], S1);
+                }
+                S[hf] = S0 + S1;
+            }
+            // V pieces: keys 4g + j of each half, dims 8c .. 8c + 7
+            uint4 vf[2][4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vf[hf][j] = *(const uint4 *)&Vc[32 * kh + 16 * hf + 4 * g + j][16 * c];
+            float x[2][4], mx = -INFINITY;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float sv = S[hf][r] * scale;
+                    if (softcap != 0.0f) sv = softcap * tanhf(sv);
+                    if constexpr (MASK) {
+                        const float mv = slope * h2f((uint16_t)mkc[hf][r]);
+                        sv = mv == -INFINITY ? -INFINITY : sv + mv;
+                    }
+                    x[hf][r] = kt + 16 * hf + 4 * g + r < L ? sv : -INFINITY;
+                    mx = fmaxf(mx, x[hf][r]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            // row c's new reference when its max grew by more than 8 (or was -inf)
+            const bool grow = mx > m_ref + 8.0f || (m_ref == -INFINITY && mx != -INFINITY);
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // some row rescales: O and l of every row
+                const float m_new = grow ? mx : m_ref;
+                const float alpha = m_ref == -INFINITY ? 1.0f : __expf(m_ref - m_new);
+                m_ref = m_new;
+                l_run *= alpha;
+                float ao[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ao[r] = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+                for (int n = 0; n < 8; ++n)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[n][r] *= ao[r];
+            }
+            const bool none = m_ref == -INFINITY;
+            fa_half4 pa[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                float pr[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pr[r] = none ? 0.0f : __expf(x[hf][r] - m_ref);
+                l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+                pa[hf] = (fa_half4){(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
+            }
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const int w = n / 2;
+                const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const uint32_t lo = __builtin_amdgcn_perm(word(vf[hf][1], w), word(vf[hf][0], w), sel);
+                    const uint32_t hi = __builtin_amdgcn_perm(word(vf[hf][3], w), word(vf[hf][2], w), sel);
+                    o[n] = fa_mfma(pa[hf], as_h4(lo, hi), o[n]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile t + 1 landed
+        __syncthreads();
+    };
+
+    // even tiles in buffer 0, odd ones in buffer 1
+    if (ntiles > 0) {
+        load_tile(0, K0, V0);
+        load_mask(0, M0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {
+        tile(t, K0, V0, K1, V1, M0, M1);
+        if (t + 1 < ntiles) tile(t + 1, K1, V1, K0, V0, M1, M0);
+    }
+
+    // merge the key halves: the second wave of each row group hands its
+    // reference, sum and accumulators (rows 4g + r, dims 8c .. 8c + 7) to the
+    // first, which rescales both to the larger reference, normalizes and stores
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (kh == 1) {
+        if (g == 0) Mm[rg][c] = m_ref, Ml[rg][c] = l_run;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            *(float4 *)&Mo[rg][4 * g + r][8 * c] = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
+            *(float4 *)&Mo[rg][4 * g + r][8 * c + 4] = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
+        }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        const float m0 = __shfl(m_ref, row, 64), l0 = __shfl(l_run, row, 64);
+        const float m1 = Mm[rg][row], l1 = Ml[rg][row];
+        const float M = fmaxf(m0, m1);
+        const float f0 = m0 == -INFINITY ? 0.0f : __expf(m0 - M), f1 = m1 == -INFINITY ? 0.0f : __expf(m1 - M);
+        const float lsum = f0 * l0 + f1 * l1;
+        const int orow = q0 + row;
+        if (orow >= a.nq) continue;
+        const float inv = lsum == 0.0f ? 0.0f : 1.0f / lsum;
+        const float4 p0 = *(const float4 *)&Mo[rg][row][8 * c], p1 = *(const float4 *)&Mo[rg][row][8 * c + 4];
+        float *out = (float *)(a.dst + h * a.d_nb1 + orow * a.d_nb2 + ib * a.d_nb3) + 8 * c;
+        *(float4 *)out = make_float4((f0 * o[0][r] + f1 * p0.x) * inv, (f0 * o[1][r] + f1 * p0.y) * inv,
+                                     (f0 * o[2][r] + f1 * p0.z) * inv, (f0 * o[3][r] + f1 * p0.w) * inv);
+        *(float4 *)(out + 4) = make_float4((f0 * o[4][r] + f1 * p1.x) * inv, (f0 * o[5][r] + f1 * p1.y) * inv,
+                                           (f0 * o[6][r] + f1 * p1.z) * inv, (f0 * o[7][r] + f1 * p1.w) * inv);
+    }
+}
+
 // Merge the partitions of one (batch, head, query) row: every partition was
 // written (an empty one as max -inf, sum 0). Each thread reads the maxima,
 // sums and its dims of up to 16 partitions in one round of loads and folds
@@ -511,6 +781,26 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
     a.scale = d.scale, a.max_bias = d.max_bias, a.m0 = d.m0, a.m1 = d.m1, a.softcap = d.softcap;
     a.nhl2 = d.n_head_log2;
     const bool mask = d.mask != nullptr && d.L > 0;
+    // prefill: the 64-row form when it fills the GPU without key partitions and
+    // the K / V / dst rows allow 16-byte accesses
+    if (d.D == 128 && d.DV == 128 && d.nq >= 32 && d.L > 0) {
+        const int gw = pl.G % 4 == 0 ? 4 : pl.G % 2 == 0 ? 2 : 1;
+        const int64_t QB = (d.nq + 64 / gw - 1) / (64 / gw), HC = pl.G / gw;
+        auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+        bool ok = QB * HC * d.nhkv * d.nb >= 128 && al16(d.k) && al16(d.v) && al16(d.dst) &&
+                  (!mask || (a.mask_vec && d.L % 8 == 0));
+        for (int i = 1; i < 4; ++i) ok = ok && d.k_nb[i] % 16 == 0 && d.v_nb[i] % 16 == 0 && d.d_nb[i] % 16 == 0;
+        if (ok && QB * HC < 65536) {
+            FaRowsArgs ra;
+            ra.f = a;
+            ra.gw = gw;
+            ra.QB = (int)QB;
+            const dim3 grid((unsigned)(QB * HC), (unsigned)d.nhkv, (unsigned)d.nb);
+            if (mask) hipLaunchKernelGGL(k_flash_attn_rows<true>, grid, dim3(512), 0, stream, ra);
+            else hipLaunchKernelGGL(k_flash_attn_rows<false>, grid, dim3(512), 0, stream, ra);
+            return check_launch("flash_attn_ext (rows)");
+        }
+    }
     switch (d.D * 1000 + d.DV) {
     case 32032: launch_fa<32, 32>(a, mask, stream); break;
     case 40040: launch_fa<40, 40>(a, mask, stream); break;

@@ -250,3 +250,49 @@ def test_window_and_causal_masks_clip_key_ranges(gpu):
     q1 = np.ascontiguousarray(q[:, :, -1:])
     m1 = np.ascontiguousarray(m[:, :, -1:])
     check(run_gpu(q1, k, v, m1, 0.125), q1, k, v, m1, 0.125, what="windows, one query")
+
+
+def _causal(nb, nh, nq, L, per_head=False, window=0, pad=0):
+    """f16 bits of a causal mask (query i at position L - nq + i), optionally a
+    window of `window` keys and a padding prefix of `pad` keys in batch 1."""
+    pos = np.arange(nq)[:, None] + (L - nq)
+    j = np.arange(L)[None, :]
+    live = j <= pos
+    if window:
+        live &= j > pos - window
+    mf = np.where(live, 0.0, -np.inf).astype(np.float32)
+    mf = np.broadcast_to(mf, (nb, nh if per_head else 1, nq, L)).copy()
+    if pad:
+        mf[min(1, nb - 1), :, :, :pad] = -np.inf
+    return mf.astype(np.float16).view(np.uint16)
+
+
+# (nb, nh, nhkv, nq, L, mask kind, softcap, max_bias): head size 128, at least
+# 128 workgroups of 64 rows and (with a mask) L a multiple of 8, so these run
+# the prefill form (k_flash_attn_rows); GQA groups 4 (4 heads a workgroup), 8
+# (two head groups), 1 and 3 (one head, 64 queries), 2 (two heads, 32
+# queries), partial query blocks and key tiles, causal / window / padding
+# masks, none, soft cap and ALiBi. The last case (L = 700) takes the 16-row
+# kernel: same checks.
+ROWS_CASES = [
+    (1, 32, 8, 512, 512, "causal", 0.0, 0.0),
+    (1, 64, 8, 256, 250, "none", 0.0, 0.0),
+    (4, 8, 8, 300, 704, "window", 0.0, 0.0),
+    (2, 24, 8, 130, 400, "pad", 30.0, 4.0),
+    (8, 16, 8, 40, 1000, "causal", 0.0, 0.0),
+    (4, 8, 8, 300, 700, "window", 0.0, 0.0),
+]
+
+
+@pytest.mark.parametrize("case", ROWS_CASES, ids=[f"{c[0]}x{c[1]}/{c[2]}-q{c[3]}-L{c[4]}-{c[5]}" for c in ROWS_CASES])
+def test_prefill_rows_form(gpu, case):
+    nb, nh, nhkv, nq, L, kind, softcap, max_bias = case
+    D = 128
+    q = synth.normal(201, (nb, nh, nq, D))
+    k = synth.f16_bits(synth.normal(202, (nb, nhkv, L, D)))
+    v = synth.f16_bits(synth.normal(203, (nb, nhkv, L, D)))
+    m = {"none": None, "causal": _causal(nb, 1, nq, L), "window": _causal(nb, nh, nq, L, True, 97),
+         "pad": _causal(nb, 1, nq, L, pad=150)}[kind]
+    scale = 1.0 / np.sqrt(D)
+    print(f"[fa-rows] {case}", flush=True)
+    check(run_gpu(q, k, v, m, scale, max_bias, softcap), q, k, v, m, scale, max_bias, softcap, what=str(case))
