@@ -649,7 +649,10 @@ def run_attention(torch, gen, stream):
         torch.cuda.synchronize()
         fms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
         fbytes = nb * kvh * L * hs * 2 * 2 + 2 * nb * nq * heads * hs * 4 + (nq * L * 2 if causal else 0)
-        flops = 4.0 * nb * heads * nq * L * hs  # QK and PV over every key the kernel visits
+        # QK and PV over the (query, key) pairs the mask leaves live: query i of
+        # a causal mask sits at position L - nq + i and sees L - nq + i + 1 keys
+        live = sum(min(L, L - nq + i + 1) for i in range(nq)) if causal else nq * L
+        flops = 4.0 * nb * heads * live * hs
         fa[name] = {"batch": nb, "queries": nq, "keys": L, "heads": heads, "kv_heads": kvh, "head_size": hs,
                     "causal_mask": causal, "bytes": fbytes, "us": round(fms * 1e3, 1),
                     "gbs": round(fbytes / fms / 1e6, 1), "frac_of_hbm_peak": round(fbytes / fms / 1e6 / HBM_PEAK_GBS, 4),
