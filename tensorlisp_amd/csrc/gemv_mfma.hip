@@ -673,6 +673,159 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     flush();
 }
 
+// Tall matrices (the vocabulary projection): every wave owns whole 16-row
+// groups over all of K (K <= 4096, a multiple of 256), so no wave waits for
+// another in the main loop -- no barrier, no cross-wave sum of partials per
+// group, as the K-split form above needs. The activation operands of all K
+// (8 bytes a lane a block) and their scales are written to LDS once per
+// workgroup; each wave streams its group's weights one 256-element unit at a
+// time through its own LDS staging buffer (the next unit's loads in flight
+// while this one is multiplied) and keeps its 16 x 16 outputs in registers
+// until the group ends. Per block the arithmetic is the K-split form's
+// (block_mma / unit_mma), so the products agree bit for bit only up to the
+// f32 order of the block sums within a row, which is the same here: blocks
+// in K order.
+constexpr int GC_WAVES = 16;
+
+template <int WT>
+__global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char gc_lds[];
+    constexpr int AT = vec_dot_type(WT);
+    constexpr bool KQ = kquant<WT>();
+    constexpr int UB = unit_bytes<WT>();
+    using St = Stage<WT, 1>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, wr = lane & 15;
+    const int64_t K = a.K;
+    const int units = (int)(K / 256);
+    const int nblk = (int)(K / block_elems(AT));
+    const int slots = KQ ? units : 8 * units;
+    const ActView act = act_view(a.act, AT, K, mm_act_rows(a));
+    const int N = (int)a.N;
+    long *sA = (long *)gc_lds;                      // [8 * units][64]: block j's A operand of lane l
+    float *sd = (float *)(sA + (size_t)8 * units * 64);  // [slots][16 columns]
+    uint8_t *wbuf = (uint8_t *)(sd + (size_t)slots * SK_COLS) + (size_t)wave * St::BUF;
+
+    // A operands (zero past N) and scales of the whole K, once per workgroup
+    for (int idx = threadIdx.x; idx < 8 * units * 64; idx += blockDim.x) {
+        const int j = idx >> 6, l = idx & 63, c = l & 15, gg = l >> 4;
+        long v = 0;
+        if (c < N) {
+            const int8_t *aq = act.qs + (a.n0 + c) * K + 32 * j;
+            if constexpr (nibble_type<WT>()) v = pack2(ldu<uint32_t>(aq + 4 * gg), ldu<uint32_t>(aq + 16 + 4 * gg));
+            else v = ldu<long>(aq + 8 * gg);
+        }
+        sA[idx] = v;
+    }
+    for (int idx = threadIdx.x; idx < slots * SK_COLS; idx += blockDim.x) {
+        const int b = idx >> 4, c = idx & 15;
+        sd[idx] = c < N ? act.d[(a.n0 + c) * nblk + b] : 0.0f;
+    }
+    __syncthreads();
+
+    // staging pieces of a unit, as in the K-split form (KS = 1)
+    int pr[St::NL];
+    int poff[St::NL];
+#pragma unroll
+    for (int i = 0; i < St::NL; ++i) {
+        const int p = 64 * i + lane;
+        const int pc = p < 16 * St::PR ? p : 0;
+        pr[i] = pc / St::PR;
+        poff[i] = 16 * (pc - pr[i] * St::PR);
+    }
+    const int64_t groups = (a.M + 15) / 16;
+    auto stage_load = [&](St &s, int64_t grp, int u) {
+#pragma unroll
+        for (int i = 0; i < St::NL; ++i) {
+            const int64_t row = grp * 16 + pr[i] < a.M ? grp * 16 + pr[i] : a.M - 1;  // clamp: loads in bounds
+            s.v[i] = ldu<uint4>(a.w + row * a.w_nb1 + (int64_t)u * UB + poff[i]);
+        }
+        if constexpr (WT == TLH_TYPE_Q6_K) {
+            const int64_t row = grp * 16 + wr < a.M ? grp * 16 + wr : a.M - 1;
+            s.dq = ldu<uint16_t>(a.w + row * a.w_nb1 + (int64_t)u * UB + 208);
+        }
+    };
+
+    for (int64_t grp = (int64_t)blockIdx.x * GC_WAVES + wave; grp < groups; grp += (int64_t)gridDim.x * GC_WAVES) {
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        St st;
+        stage_load(st, grp, 0);
+        for (int u = 0; u < units; ++u) {
+            // this unit's bytes to the wave's own buffer (a wave's LDS accesses
+            // are in order: no barrier), the next unit's loads out
+#pragma unroll
+            for (int i = 0; i < St::NL; ++i) *(uint4 *)(wbuf + 1024 * i + 16 * lane) = st.v[i];
+            const uint32_t dq = st.dq;
+            if (u + 1 < units) stage_load(st, grp, u + 1);
+            long A[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) A[j] = sA[(8 * u + j) * 64 + lane];
+            const uint32_t ub = (uint32_t)(wr * St::RB);
+            const float *sdu = sd + (KQ ? u : 8 * u) * SK_COLS;
+            if constexpr (WT == TLH_TYPE_Q6_K) {
+                UnitW<WT> w;
+                w.load_lds(wbuf + ub, g);
+                unit_mma_q6k(w, dq, A, sdu, g, y);
+            } else if constexpr (KQ) {
+                UnitW<WT> w;
+                w.load_lds(wbuf + ub, g);
+                unit_mma<WT>(w, A, sdu, nullptr, g, 8, y);
+            } else {
+                const uint32_t *w32 = (const uint32_t *)wbuf;
+                const uint16_t *w16 = (const uint16_t *)wbuf;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t blk = ub + j * block_bytes(WT);
+                    long B;
+                    if constexpr (WT == TLH_TYPE_Q4_0) {
+                        const uint32_t v = lds_u32(w32, blk + 2 + 4 * g);
+                        B = pack2(nib_minus8(v & 0x0f0f0f0fu), nib_minus8((v >> 4) & 0x0f0f0f0fu));
+                    } else {
+                        const uint2 v = lds_u64(w32, blk + 2 + 8 * g);
+                        B = pack2(v.x, v.y);
+                    }
+                    block_mma<WT>(A[j], B, w16[blk >> 1], sdu + j * SK_COLS, g, y);
+                }
+            }
+        }
+        // lane (g, wr): columns 4g + r of row grp * 16 + wr
+        const int64_t row = grp * 16 + wr;
+        if (row < a.M) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int col = 4 * g + r;
+                if (col < N) *(float *)((char *)a.dst + (a.n0 + col) * a.d_nb1 + row * 4) = y[r];
+            }
+        }
+    }
+}
+
+static bool gemv_cols_ok(const MatmulArgs &a) {
+    constexpr int64_t CUS = 256;  // MI355X
+    const bool wt = a.wtype == TLH_TYPE_Q4_0 || a.wtype == TLH_TYPE_Q8_0 || a.wtype == TLH_TYPE_Q4_K ||
+                    a.wtype == TLH_TYPE_Q5_K || a.wtype == TLH_TYPE_Q6_K;
+    return wt && a.K % 256 == 0 && a.K <= 4096 && a.nseg == 0 && !a.ids && a.ne12 * a.ne13 == 1 &&
+           (a.M + 15) / 16 >= CUS * GC_WAVES;
+}
+
+template <int WT> static tlh_status launch_cols(const MatmulArgs &a, hipStream_t stream) {
+    using St = Stage<WT, 1>;
+    const int64_t units = a.K / 256;
+    const int64_t slots = kquant<WT>() ? units : 8 * units;
+    const size_t lds = (size_t)8 * units * 64 * 8 + (size_t)slots * SK_COLS * 4 + (size_t)GC_WAVES * St::BUF;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (cus < 1) cus = 1;
+    }
+    const int64_t groups = (a.M + 15) / 16;
+    const int64_t wgs = (groups + GC_WAVES - 1) / GC_WAVES;
+    hipLaunchKernelGGL(k_gemv_cols<WT>, dim3((unsigned)(wgs < cus ? wgs : cus)), dim3(64 * GC_WAVES), lds, stream, a);
+    return check_launch("gemv_cols");
+}
+
 // Units per wave: one (16 activation-operand registers); a workgroup covers
 // up to 16 units (K = 4096); longer K takes several chunks.
 template <int WT> constexpr int sk_ks() { return 1; }
@@ -757,6 +910,16 @@ template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool stage
 
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     if (!gemv_mfma_supported(a.N)) return set_error(TLH_INVALID, "gemv_mfma: N=%lld", (long long)a.N);
+    if (gemv_cols_ok(a)) {
+        switch (a.wtype) {
+        case TLH_TYPE_Q4_0: return launch_cols<TLH_TYPE_Q4_0>(a, stream);
+        case TLH_TYPE_Q8_0: return launch_cols<TLH_TYPE_Q8_0>(a, stream);
+        case TLH_TYPE_Q4_K: return launch_cols<TLH_TYPE_Q4_K>(a, stream);
+        case TLH_TYPE_Q5_K: return launch_cols<TLH_TYPE_Q5_K>(a, stream);
+        case TLH_TYPE_Q6_K: return launch_cols<TLH_TYPE_Q6_K>(a, stream);
+        default: break;
+        }
+    }
     // whole units per row: every staged piece lies inside its row
     const bool staged = a.K % 256 == 0;
     switch (a.wtype) {

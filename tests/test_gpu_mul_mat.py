@@ -96,6 +96,21 @@ def test_q6_K_lm_head_row_sample(gpu, n):
     close(y[:, rows], want, f"q6_K lm_head n={n}")
 
 
+@pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
+@pytest.mark.parametrize("M,K,n", [(65552, 4096, 8), (65545, 1024, 3), (70000, 4096, 16)])
+def test_tall_few_column_form(gpu, t, M, K, n):
+    """4096 or more 16-row groups with 3..16 columns and K <= 4096 (a multiple of
+    256): each wave owns whole row groups over all of K (k_gemv_cols). Against
+    the oracle on a row sample that includes the last rows (M not a multiple of
+    16 in one case)."""
+    w = synth.random_blocks(t, 620 + n, M, K)
+    x = synth.normal(621 + n, (n, K))
+    y = host(N.mul_mat(t, dev(w), M, K, dev(x)))
+    rows = np.unique(np.concatenate([synth.integers(622 + n, 0, M - 1, 96), np.arange(M - 20, M)]))
+    want = oracle().mul_mat(t, np.ascontiguousarray(w[rows]), len(rows), K, x, nthreads=16)
+    close(y[:, rows], want, f"tall {NAMES[t]} {M}x{K} n={n}")
+
+
 def test_config1_q8_0_4096_golden(gpu):
     g = np.load(GOLD / "config1.npz")
     w = synth.q8_0_config1(int(g["seeds"][0]), 4096, 4096)
