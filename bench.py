@@ -800,8 +800,12 @@ def main() -> int:
         dom_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
         # the compute launch reads the weights and the quantized activation, writes f32 rows
         dom_bytes = dM * N.row_bytes(dt, dK) + dn * N.row_bytes(N.VEC_DOT_TYPE[dt], dK) + dn * dM * 4
+        # tall matrices with K <= 4096 take the few-column form whose waves own
+        # whole 16-row groups (gemv_cols_ok in gemv_mfma.hip)
+        kname = ("tlh::k_gemv_cols" if dM // 16 >= 4096 and dK <= 4096 and dK % 256 == 0
+                 else "tlh::k_gemv_mfma")
         dom_kernel = (f"{N.TYPE_NAMES[dt]} GEMV N={dn}, {dM}x{dK}: the GEMV launch of the MUL_MAT node "
-                      f"(tlh::k_gemv_mfma), after its quantize launch; node incl. quantize "
+                      f"({kname}), after its quantize launch; node incl. quantize "
                       f"{node_ms[dom] * 1e3:.1f} us")
     dom_gbs = dom_bytes / dom_ms / 1e6
     log(f"roofline kernel: {dom_kernel}: {dom_ms * 1e3:.1f} us, {dom_gbs:.0f} GB/s")
