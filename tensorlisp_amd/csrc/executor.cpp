@@ -1238,9 +1238,11 @@ class Lowering {
         d.swap(out);
     }
 
-    // Compute halves of one quantization group (3..16 columns, K <= 4096)
-    // become one few-column MFMA launch over their rows, at the first one's
-    // place. A later member moves up only if nothing in between reads or
+    // Compute halves of one quantization group become one launch over their
+    // rows, at the first one's place: 3..16 columns with K <= 4096 the
+    // few-column MFMA kernel, more columns of q4_K / q5_K weights the GEMM
+    // (whose K-chunk partials over all the rows can outgrow the members'
+    // scratch: the group's block grows to fit). A later member moves up only if nothing in between reads or
     // writes its destination (its weights and the group's activation scratch
     // are written by nobody else).
     void merge_mm_computes(std::vector<Dispatch> &d) {
@@ -1282,6 +1284,15 @@ class Lowering {
                 f.mdst[k] = y.dst;
                 f.pos_last = std::max(f.pos_last, y.pos_last);
                 taken[mem[k]] = 1;
+            }
+            const tlh_op *mops[3] = {&f.mop[0], &f.mop[1], &f.mop[2]};
+            const size_t need = mul_mat_compute_multi_scratch_bytes(mops, f.nmem);
+            if (need > f.scratch_bytes) {
+                f.scratch_bytes = need;
+                if (f.block <= -2) {
+                    Group &gr = groups_[-2 - f.block];
+                    gr.bytes = std::max(gr.bytes, need);
+                }
             }
             out.push_back(f);
         }

@@ -109,8 +109,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // staging roles: weight row / token tid >> 1, half h = tid & 1 of the 64-element chunk
     const int srow = tid >> 1, sh = tid & 1;
+    // segments (a.nseg > 0, one batch slice): rows seg_m0[s] .. seg_m0[s+1] of
+    // the launch are the rows of weight matrix seg_w[s] (row stride w_nb1),
+    // written to seg_dst[s]; every segment but the last is a whole number of
+    // tiles, so a tile lies in one (sg) and its rows start at m0 in it
+    int sg = 0;
+    int64_t m0 = 0;
+    if (a.nseg > 0) {
+        sg = (int)(m_base >= a.seg_m0[1]) + (int)(a.nseg > 2 && m_base >= a.seg_m0[2]);
+        m0 = a.seg_m0[sg];
+        W = a.seg_w[sg];
+    }
     const int64_t grow = m_base + srow < a.M ? m_base + srow : a.M - 1;  // clamped: loads in bounds
-    const uint8_t *wrow = W + grow * a.w_nb1;
+    const uint8_t *wrow = W + (grow - m0) * a.w_nb1;
     // B tile rows (tokens) this lane fills by direct-to-LDS loads: instruction
     // i of wave w fills rows 8 (4 w + i) .. + 7, lane l row + l / 8 at chunk
     // position l % 8, i.e. the chunk (l % 8) ^ (row & 7) of the token's stage
@@ -313,13 +324,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int jn = 0; jn < 2; ++jn) {
             const int64_t n = n_base + 64 * wn + 32 * jn + lr;
             if (n >= a.N) continue;
-            float *drow = pbase ? pbase + n * a.M : (float *)(dbase + (a.n0 + n) * a.d_nb1);
+            // partials hold every row of the launch; a segment's own output
+            // holds its rows from m0
+            const int64_t moff = pbase ? 0 : m0;
+            float *drow = pbase      ? pbase + n * a.M
+                          : a.nseg ? (float *)((char *)a.seg_dst[sg] + (a.n0 + n) * a.seg_d_nb1[sg])
+                                   : (float *)(dbase + (a.n0 + n) * a.d_nb1);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t m = m_base + 64 * wm + 32 * i + 8 * q + 4 * lg;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (m + e < a.M) drow[m + e] = acc[i][jn][4 * q + e];
+                    if (m + e < a.M) drow[m + e - moff] = acc[i][jn][4 * q + e];
             }
         }
 }

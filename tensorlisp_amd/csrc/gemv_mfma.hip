@@ -842,6 +842,11 @@ __global__ void __launch_bounds__(256) k_gemv_mfma_reduce(const MatmulArgs a, in
     const int64_t n = r / a.M, m = r - n * a.M;
     float s = 0.0f;
     for (int c = 0; c < chunks; ++c) s += a.part[(c * batches + batch) * per_batch + r];
+    if (a.nseg > 0) {  // one batch slice; row m of the launch is row m - seg_m0[sg] of segment sg
+        const int sg = (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]);
+        *(float *)((char *)a.seg_dst[sg] + (a.n0 + n) * a.seg_d_nb1[sg] + (m - a.seg_m0[sg]) * 4) = s;
+        return;
+    }
     const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
     *(float *)((char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3 + (a.n0 + n) * a.d_nb1 + m * 4) = s;
 }

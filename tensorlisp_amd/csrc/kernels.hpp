@@ -166,6 +166,7 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
 // type and K as one register-GEMV launch (tlhip.cpp); TLH_UNSUPPORTED when the
 // pointers do not allow it.
 bool mul_mat_compute_multi_ok(const tlh_op *const *ops, int n);
+size_t mul_mat_compute_multi_scratch_bytes(const tlh_op *const *ops, int n);
 tlh_status mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
                                  const void *scratch, size_t scratch_bytes, hipStream_t stream);
 bool mul_mat_multi_ok(const tlh_op *const *ops, int n);

@@ -531,10 +531,15 @@ bool tlh::mul_mat_compute_multi_ok(const tlh_op *const *ops, int n) {
     MulMatShape first;
     for (int i = 0; i < n; ++i) {
         MulMatShape s;
-        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || s.N < 3 || s.N > 16 || s.ne12 * s.ne13 != 1)
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || s.N < 3 || s.ne12 * s.ne13 != 1)
             return false;
-        if (gemv_mfma_partial_bytes(s.K, s.M, s.N, 1) != 0) return false;
-        if (i < n - 1 && s.M % 16 != 0) return false;
+        // more than 16 columns: the q4_K / q5_K GEMM over the segments' rows
+        // (each but the last a whole number of its 128-row tiles)
+        const bool gemm = s.N > 16;
+        if (gemm ? !(s.wtype == TLH_TYPE_Q4_K || s.wtype == TLH_TYPE_Q5_K)
+                 : gemv_mfma_partial_bytes(s.K, s.M, s.N, 1) != 0)
+            return false;
+        if (i < n - 1 && s.M % (gemm ? 128 : 16) != 0) return false;
         if (i == 0) first = s;
         else if (s.K != first.K || s.wtype != first.wtype || s.N != first.N ||
                  ops[i]->t[0].nb[1] != ops[0]->t[0].nb[1] || ops[i]->t[1].nb[1] != ops[0]->t[1].nb[1])
@@ -543,15 +548,29 @@ bool tlh::mul_mat_compute_multi_ok(const tlh_op *const *ops, int n) {
     return true;
 }
 
+// The quantized activation of the first node plus, for the GEMM form, the
+// partial sums of its K chunks over all the nodes' rows.
+size_t tlh::mul_mat_compute_multi_scratch_bytes(const tlh_op *const *ops, int n) {
+    if (!mul_mat_compute_multi_ok(ops, n)) return 0;
+    MulMatShape s;
+    check_mul_mat(ops[0], s);
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) rows += ops[i]->t[0].ne[1];
+    const int64_t part = s.N > 16 ? align_up(gemm_partial_bytes(s.wtype, rows, s.N, s.K, 1), 256) : 0;
+    return (size_t)(mm_act_bytes(s) + part);
+}
+
 tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
                                       const void *scratch, size_t scratch_bytes, hipStream_t stream) {
     if (!mul_mat_compute_multi_ok(ops, n)) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: shapes");
     MulMatShape s;
     check_mul_mat(ops[0], s);
-    tlh_status st = mm_check_scratch(s, scratch, scratch_bytes);
-    if (st != TLH_OK) return st;
+    const size_t need = mul_mat_compute_multi_scratch_bytes(ops, n);
+    if (!scratch || scratch_bytes < need)
+        return set_error(TLH_INVALID, "mul_mat_compute_multi: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    if ((uintptr_t)scratch & 255) return set_error(TLH_INVALID, "mul_mat_compute_multi: scratch must be 256-byte aligned");
     MatmulArgs m = mm_args(ops[0], s, w[0], scratch, dst[0]);
-    m.part = nullptr;
+    m.part = s.N > 16 ? (float *)((char *)scratch + mm_act_bytes(s)) : nullptr;
     m.nseg = n;
     int64_t rows = 0;
     for (int i = 0; i < 3; ++i) {
@@ -569,7 +588,7 @@ tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *cons
     m.seg_m0[3] = rows;
     for (int i = n; i < 3; ++i) m.seg_m0[i] = rows;
     m.M = rows;
-    return launch_gemv_mfma(m, stream);
+    return s.N > 16 ? launch_gemm(m, stream) : launch_gemv_mfma(m, stream);
 }
 
 bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {

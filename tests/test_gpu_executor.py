@@ -164,6 +164,50 @@ def test_shared_quantization_matches_separate(gpu):
     assert prog.stats()["launches"] == 1 + 2 + 1
 
 
+@pytest.mark.parametrize("t", [N.Q4_K, N.Q5_K], ids=["q4_K", "q5_K"])
+@pytest.mark.parametrize("n", [64, 512])
+def test_prefill_qkv_one_gemm(gpu, t, n):
+    """Q / K / V of a prefill (3 matrices of 512, 128 and 128 rows reading one
+    RMS-normed activation of n >= 64 tokens): one GEMM launch over the 768 rows.
+    Its K split follows all 768 rows, so its sums may split K unlike each
+    matrix alone: every product is checked against the CPU oracle's
+    mul_mat (quants.c dot products) to 1e-4 + 1e-3 |want|, and the
+    dispatches are the norm chain (which quantizes) and the one GEMM."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    K = 4096
+    Ms = (512, 128, 128)
+    b = G.Builder()
+    x = b.input(N.F32, [K, n])
+    nw = b.weight(N.F32, [K])
+    W = [b.weight(t, [K, m]) for m in Ms]
+    y = b.mul(b.rms_norm(x, 1e-5), nw)
+    outs = [b.mul_mat(w, y) for w in W]
+    for o in outs:
+        b.expand(o)
+    nwh = dev((1.0 + 0.1 * synth.normal(121, (K,))).astype(np.float32))
+    wh = [synth.random_blocks(t, 122 + i, m, K) for i, m in enumerate(Ms)]
+    prog = G.Program(b, outs + [y], [nwh] + [dev(w) for w in wh])
+    xv = dev(synth.normal(123, (n, K)))
+    prog.write_input(0, xv)
+    print(f"[qkv-gemm] {N.TYPE_NAMES[t]} n={n}", flush=True)
+    prog.run()
+    yv = prog.read(y, torch.float32).reshape(n, K)
+    torch.cuda.synchronize()
+    yh = yv.cpu().numpy()
+    rows = slice(0, n) if n <= 64 else np.r_[0:8, n - 8:n]  # the oracle on a sample of tokens at n = 512
+    for m, w, o in zip(Ms, wh, outs):
+        got = prog.read(o, torch.float32).reshape(n, m)
+        torch.cuda.synchronize()
+        want = oracle().mul_mat(t, w, m, K, np.ascontiguousarray(yh[rows]))
+        g = got.cpu().numpy()[rows]
+        bad = np.abs(g - want) > 1e-4 + 1e-3 * np.abs(want)  # the GEMM tests' tolerance
+        assert not bad.any(), (N.TYPE_NAMES[t], m, n, float(np.abs(g - want).max()))
+    assert prog.stats()["launches"] == 2
+
+
 GQ_TYPES = [N.Q4_K, N.Q6_K, N.Q5_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0, N.Q5_1]
 
 
@@ -206,11 +250,13 @@ def test_glu_quantizes_for_its_mul_mats(gpu, t, K, n, op, group):
         assert np.array_equal(got.cpu().numpy().reshape(want.shape).view(np.uint32),
                               want.cpu().numpy().view(np.uint32)), f"{N.TYPE_NAMES[t]} M={m}"
     # dispatches: the GLU, then the products' compute launches (a group at
-    # n <= 16: one few-column launch over both matrices' rows)
-    assert prog.stats()["launches"] == 1 + (2 if group and n > 16 else 1)
+    # n <= 16: one few-column launch over both matrices' rows; above, one GEMM
+    # launch over them for q4_K / q5_K)
+    apart = group and n > 16 and t not in (N.Q4_K, N.Q5_K)
+    assert prog.stats()["launches"] == 1 + (2 if apart else 1)
 
 
-NQ_TYPES = [N.Q4_K, N.Q6_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0]
+NQ_TYPES = [N.Q4_K, N.Q5_K, N.Q6_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0]
 
 
 @pytest.mark.parametrize("t", NQ_TYPES, ids=[N.TYPE_NAMES[t] for t in NQ_TYPES])
@@ -221,12 +267,16 @@ def test_norm_chain_quantizes_for_its_mul_mats(gpu, t, K, n, add):
     (q8_K / q8_0 / q8_1 codes, scales and sums; at n > 16 the q4_K GEMM's f16
     codes and bsums too) and no quantize launch runs; over fewer rows (16) the
     quantize launch stays. Either way the norm's outputs and every product are
-    bit-identical to the core ops and tlh_mul_mat run one by one."""
+    bit-identical to the core ops and tlh_mul_mat run one by one. Over more
+    than 16 rows the q4_K / q5_K products are one GEMM launch over the three
+    matrices' rows (the first two whole 128-row tiles, the last not): its K
+    split here is the one each matrix gets alone, so the sums agree bit for
+    bit."""
     import torch
 
     from tensorlisp_amd import synth
 
-    Ms = (256, 128)
+    Ms = (256, 128, 100)
     b = G.Builder()
     p = b.input(N.F32, [K, n])
     q = b.input(N.F32, [K, n])
@@ -255,9 +305,11 @@ def test_norm_chain_quantizes_for_its_mul_mats(gpu, t, K, n, add):
         assert np.array_equal(got.cpu().numpy().reshape(want.shape).view(np.uint32),
                               want.cpu().numpy().view(np.uint32)), f"{N.TYPE_NAMES[t]} M={m}"
     # dispatches: the norm chain, the quantize launch when it stays apart, then
-    # the products (n <= 16: one few-column launch over both matrices' rows)
+    # the products (n <= 16: one few-column launch over all matrices' rows;
+    # more rows: one GEMM launch for q4_K / q5_K, else one per matrix)
     fused = n >= 64
-    assert prog.stats()["launches"] == 1 + (0 if fused else 1) + (1 if n <= 16 else 2)
+    merged = n <= 16 or t in (N.Q4_K, N.Q5_K)
+    assert prog.stats()["launches"] == 1 + (0 if fused else 1) + (1 if merged else len(Ms))
 
 
 def test_program_refusals(gpu):
