@@ -394,6 +394,23 @@ tlh_status tlh_program_run(tlh_program *p, void *state, void *stream, int32_t gr
  * per lowered node, plus one quantization per MUL_MAT group; a dispatch may
  * launch more than one kernel). */
 tlh_status tlh_program_stats(const tlh_program *p, size_t *arena_bytes, size_t *io_bytes, int32_t *launches);
+/* Per-dispatch timing, in place of the reference's TL_NATIVE_PROFILE per-op
+ * times (crates/kernels/src/cuda/exec.rs:186-216): one eager run of the program
+ * on `stream` with an event after every dispatch; ms[i] = GPU milliseconds of
+ * dispatch i (n >= the dispatch count of tlh_program_stats). Synchronous.
+ * With the environment variable TLH_NATIVE_PROFILE set, every eager
+ * tlh_program_run does the same and prints the ops with the most time to
+ * stderr, as the reference does. */
+tlh_status tlh_program_profile(tlh_program *p, void *state, void *stream, float *ms, int32_t n);
+/* One eager run of the program on `stream` that records which kernels each
+ * dispatch launched (no counterpart in the reference; its exec.rs labels
+ * dispatches only by op). `text` receives one line per dispatch:
+ * "<index>\t<ggml op of its first node>\t<launch labels, comma-separated>\n"
+ * (labels as the launch sites name them: "gemv", "gemv_mfma", "gemv_cols",
+ * "gemm_q4k", "gemm_q8", "flash_attn_ext", "flash_attn_ext (rows)",
+ * "paged_attention", "norm_chain", ...), NUL-terminated and truncated to `cap`
+ * bytes; *len (optional) = the bytes the whole text needs. Not synchronous. */
+tlh_status tlh_program_trace(tlh_program *p, void *state, void *stream, char *text, size_t cap, size_t *len);
 /* The plan without a device (for checking it): arena offset per tensor (-1 if
  * not in the arena), per-node scratch offset (-1 if none) and the arena size.
  * Scratch sizes come from the same entry points compile uses. */

@@ -10,6 +10,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -1547,16 +1549,51 @@ struct tlh_program {
         }
     }
 
+    // The ggml op of a dispatch's first node (its label in errors, traces and profiles).
+    const char *op_of(const Dispatch &x) const { return tensors[low.node_ids[x.pos]].op; }
+
     tlh_status enqueue(void *state, hipStream_t s) const {
-        for (const Dispatch &x : low.d) {
-            const tlh_status st = launch_one(x, state, s);
-            if (st != TLH_OK) {
-                const int32_t id = low.node_ids[x.pos];
-                const std::string msg = tlh_last_error();
-                return set_error(st, "launching `%s` (tensor %d): %s", tensors[id].op, id, msg.c_str());
-            }
+        for (size_t i = 0; i < low.d.size(); ++i) {
+            const tlh_status st = enqueue_one(i, state, s);
+            if (st != TLH_OK) return st;
         }
         return TLH_OK;
+    }
+
+    tlh_status enqueue_one(size_t i, void *state, hipStream_t s) const {
+        const Dispatch &x = low.d[i];
+        const tlh_status st = launch_one(x, state, s);
+        if (st != TLH_OK) {
+            const int32_t id = low.node_ids[x.pos];
+            const std::string msg = tlh_last_error();
+            return set_error(st, "launching `%s` (tensor %d): %s", op_of(x), id, msg.c_str());
+        }
+        return TLH_OK;
+    }
+
+    // Every dispatch between two events on `s` (eager launches); ms[i] is the
+    // GPU time of dispatch i. The events are created and destroyed here.
+    tlh_status profile(void *state, hipStream_t s, float *ms) const {
+        const size_t n = low.d.size();
+        std::vector<hipEvent_t> ev(n + 1, nullptr);
+        tlh_status st = TLH_OK;
+        size_t made = 0;
+        for (; made <= n && st == TLH_OK; ++made)
+            if (hipEventCreate(&ev[made]) != hipSuccess) st = set_error(TLH_EXECUTION, "profile: hipEventCreate");
+        if (st == TLH_OK && hipEventRecord(ev[0], s) != hipSuccess) st = set_error(TLH_EXECUTION, "profile: record");
+        for (size_t i = 0; i < n && st == TLH_OK; ++i) {
+            st = enqueue_one(i, state, s);
+            if (st == TLH_OK && hipEventRecord(ev[i + 1], s) != hipSuccess)
+                st = set_error(TLH_EXECUTION, "profile: record");
+        }
+        if (st == TLH_OK && hipEventSynchronize(ev[n]) != hipSuccess)
+            st = set_error(TLH_EXECUTION, "profile: hipEventSynchronize: %s", hipGetErrorString(hipGetLastError()));
+        for (size_t i = 0; i < n && st == TLH_OK; ++i)
+            if (hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]) != hipSuccess)
+                st = set_error(TLH_EXECUTION, "profile: hipEventElapsedTime");
+        for (size_t i = 0; i < made && i <= n; ++i)
+            if (ev[i]) (void)hipEventDestroy(ev[i]);
+        return st;
     }
 
     tlh_status launch_one(const Dispatch &x, void *state, hipStream_t s) const {
@@ -1887,11 +1924,41 @@ tlh_status tlh_program_tensor(const tlh_program *p, int32_t id, void *state, voi
     return TLH_OK;
 }
 
+// TLH_NATIVE_PROFILE set: an eager run times every dispatch and prints the
+// ops with the most GPU time to stderr, as the reference's executor does under
+// TL_NATIVE_PROFILE (crates/kernels/src/cuda/exec.rs:186-216; events here, not
+// a host clock around a synchronize).
+static tlh_status run_profiled(tlh_program *p, void *state, hipStream_t s) {
+    const size_t n = p->low.d.size();
+    std::vector<float> ms(n, 0.0f);
+    const tlh_status st = p->profile(state, s, ms.data());
+    if (st != TLH_OK) return st;
+    std::vector<std::tuple<std::string, double, int>> by_op;
+    double total = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const std::string op = p->op_of(p->low.d[i]);
+        auto it = std::find_if(by_op.begin(), by_op.end(), [&](const auto &e) { return std::get<0>(e) == op; });
+        if (it == by_op.end()) by_op.emplace_back(op, ms[i], 1);
+        else std::get<1>(*it) += ms[i], ++std::get<2>(*it);
+        total += ms[i];
+    }
+    std::stable_sort(by_op.begin(), by_op.end(), [](const auto &a, const auto &b) { return std::get<1>(a) > std::get<1>(b); });
+    std::string list;
+    for (size_t i = 0; i < by_op.size() && i < 6; ++i) {
+        char buf[96];
+        snprintf(buf, sizeof buf, "%s%s %.3fms/%d", i ? ", " : "", std::get<0>(by_op[i]).c_str(), std::get<1>(by_op[i]),
+                 std::get<2>(by_op[i]));
+        list += buf;
+    }
+    fprintf(stderr, "profile: %zu launches %.3f ms (events): %s\n", n, total, list.c_str());
+    return TLH_OK;
+}
+
 tlh_status tlh_program_run(tlh_program *p, void *state, void *stream, int32_t graph) {
     if (!p) return set_error(TLH_INVALID, "program_run: null program");
     if (!p->state_offsets.empty() && !state) return set_error(TLH_INVALID, "program_run: the graph has state; pass its buffer");
     const hipStream_t s = (hipStream_t)stream;
-    if (!graph) return p->enqueue(state, s);
+    if (!graph) return getenv("TLH_NATIVE_PROFILE") ? run_profiled(p, state, s) : p->enqueue(state, s);
     if (!s) return set_error(TLH_INVALID, "program_run: graph replay needs a stream other than the null stream");
     if (!p->exec || p->exec_state != state || p->exec_stream != s) {
         p->drop_graph();
@@ -1914,6 +1981,43 @@ tlh_status tlh_program_run(tlh_program *p, void *state, void *stream, int32_t gr
         p->exec_stream = s;
     }
     return hip_ok(hipGraphLaunch(p->exec, s), "hipGraphLaunch");
+}
+
+tlh_status tlh_program_profile(tlh_program *p, void *state, void *stream, float *ms, int32_t n) {
+    if (!p || (!ms && !p->low.d.empty())) return set_error(TLH_INVALID, "program_profile: null pointer");
+    if (n < (int32_t)p->low.d.size())
+        return set_error(TLH_INVALID, "program_profile: room for %d of %zu dispatches", n, p->low.d.size());
+    if (!p->state_offsets.empty() && !state)
+        return set_error(TLH_INVALID, "program_profile: the graph has state; pass its buffer");
+    return p->profile(state, (hipStream_t)stream, ms);
+}
+
+tlh_status tlh_program_trace(tlh_program *p, void *state, void *stream, char *text, size_t cap, size_t *len) {
+    if (!p || (!text && cap)) return set_error(TLH_INVALID, "program_trace: null pointer");
+    if (!p->state_offsets.empty() && !state)
+        return set_error(TLH_INVALID, "program_trace: the graph has state; pass its buffer");
+    std::string out, labels;
+    tlh_status st = TLH_OK;
+    for (size_t i = 0; i < p->low.d.size() && st == TLH_OK; ++i) {
+        labels.clear();
+        launch_trace(&labels);
+        st = p->enqueue_one(i, state, (hipStream_t)stream);
+        launch_trace(nullptr);
+        const Dispatch &x = p->low.d[i];
+        char head[64];
+        snprintf(head, sizeof head, "%zu\t%s\t", i, p->op_of(x));
+        out += head;
+        out += labels;
+        out.push_back('\n');
+    }
+    if (st != TLH_OK) return st;
+    if (len) *len = out.size() + 1;
+    if (cap) {
+        const size_t k = std::min(cap - 1, out.size());
+        memcpy(text, out.data(), k);
+        text[k] = 0;
+    }
+    return TLH_OK;
 }
 
 tlh_status tlh_program_stats(const tlh_program *p, size_t *arena_bytes, size_t *io_bytes, int32_t *launches) {

@@ -1,6 +1,8 @@
 // Internal interface between the C ABI (tlhip.cpp) and the kernel files.
 #pragma once
 
+#include <string>
+
 #include "common.hpp"
 
 namespace tlh {
@@ -8,7 +10,10 @@ namespace tlh {
 // Thread-local error text + status (defined in tlhip.cpp).
 tlh_status set_error(tlh_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // hipGetLastError after a launch, mapped to TLH_EXECUTION with `what` in the text.
+// While a trace is on (launch_trace with a sink), `what` is also appended to
+// the sink, comma-separated: the launch labels of this thread.
 tlh_status check_launch(const char *what);
+void launch_trace(std::string *sink);
 
 // rows of x (stride x_row_bytes) -> activation rows row_off.. of an output of
 // total_rows rows, in ggml's block layout or the split scratch layout.

@@ -30,9 +30,18 @@ tlh_status set_error(tlh_status s, const char *fmt, ...) {
     return s;
 }
 
+// Launch labels of this thread, recorded while a trace is on (tlh_program_trace).
+static thread_local std::string *g_trace = nullptr;
+
+void launch_trace(std::string *sink) { g_trace = sink; }
+
 tlh_status check_launch(const char *what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(TLH_EXECUTION, "%s: launch failed: %s", what, hipGetErrorString(e));
+    if (g_trace) {
+        if (!g_trace->empty()) g_trace->push_back(',');
+        g_trace->append(what);
+    }
     return TLH_OK;
 }
 

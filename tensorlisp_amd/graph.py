@@ -386,6 +386,33 @@ class Program:
         N.check(N.lib().tlh_program_stats(self.ptr, C.byref(a), C.byref(io), C.byref(n)))
         return {"arena_bytes": a.value, "io_bytes": io.value, "launches": n.value}
 
+    def trace(self, state=None, stream=None):
+        """One eager run that records the kernels each dispatch launched:
+        a list of (ggml op of the dispatch's first node, [launch labels])."""
+        st = C.c_void_p(state.data_ptr() if state is not None else None)
+        if state is not None:
+            self._order(state, stream)
+        need, cap = C.c_size_t(), 1 << 20
+        buf = C.create_string_buffer(cap)
+        N.check(N.lib().tlh_program_trace(self.ptr, st, N._stream(stream), buf, cap, C.byref(need)))
+        if need.value > cap:  # not run again: a second run would repeat the program's writes
+            raise RuntimeError(f"trace text of {need.value} bytes exceeds {cap}")
+        out = []
+        for line in buf.value.decode().splitlines():
+            _, op, labels = line.split("\t")
+            out.append((op, labels.split(",") if labels else []))
+        return out
+
+    def profile(self, state=None, stream=None):
+        """Per-dispatch GPU milliseconds of one eager run (synchronous)."""
+        n = self.stats()["launches"]
+        ms = (C.c_float * max(n, 1))()
+        st = C.c_void_p(state.data_ptr() if state is not None else None)
+        if state is not None:
+            self._order(state, stream)
+        N.check(N.lib().tlh_program_profile(self.ptr, st, N._stream(stream), ms, n))
+        return list(ms[:n])
+
 
 
 # ----------------------------------------------------------- decoder step

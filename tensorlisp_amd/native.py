@@ -41,7 +41,8 @@ EXPORTS = (
     "tlh_core_check", "tlh_core", "tlh_program_compile", "tlh_program_destroy", "tlh_copy", "tlh_memset",
     "tlh_read_floor",
     "tlh_program_input",
-    "tlh_program_tensor", "tlh_program_run", "tlh_program_stats", "tlh_program_plan",
+    "tlh_program_tensor", "tlh_program_run", "tlh_program_stats", "tlh_program_profile", "tlh_program_trace",
+    "tlh_program_plan",
     "tlh_gguf_open", "tlh_gguf_close", "tlh_gguf_counts", "tlh_gguf_tensor", "tlh_gguf_find_tensor",
     "tlh_gguf_find_key", "tlh_gguf_key", "tlh_gguf_value", "tlh_gguf_string", "tlh_gguf_layout", "tlh_gguf_upload",
 )
@@ -122,6 +123,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
     L.tlh_program_tensor.argtypes = [vp, C.c_int32, vp, C.POINTER(C.c_void_p)]
     L.tlh_program_run.argtypes = [vp, vp, vp, C.c_int32]
     L.tlh_program_stats.argtypes = [vp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]
+    L.tlh_program_profile.argtypes = [vp, vp, vp, C.POINTER(C.c_float), C.c_int32]
+    L.tlh_program_trace.argtypes = [vp, vp, vp, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]
     L.tlh_program_plan.argtypes = [vp, C.c_int32, i32p, C.c_int32, i32p, C.c_int32, i64p, i64p,
                                    C.POINTER(C.c_size_t)]
     u64p, cpp = C.POINTER(C.c_uint64), C.POINTER(C.c_char_p)

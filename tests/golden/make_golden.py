@@ -78,8 +78,19 @@ these are the reference's outputs on fixed inputs, captured once:
                    accumulation; for refs.paged_8b_seqs, each sequence run alone, the
                    argmax and 8 largest logits of each step (f32 P.V) and how far the
                    two accumulations move that step's logits.
+  decoder_8b_prefill.npz  the same slice over configs[4]'s run shape (refs.prefill_8b_steps: a
+                   512-token prompt, a 64-token chunk at position 512, two single-token
+                   steps), dense cache, P.V in f32: last-token logits per step and how far
+                   the f16 P.V run moves them; the residual stream after layer 0 (all
+                   rows) and after layer 1 (a row sample for the prompt, all rows for the
+                   later steps); the cache rows after the last step; per layer, how far
+                   f16 P.V accumulation moves that layer's output from the same input
+                   (largest, mean, 99.9th percentile and largest per-row mean |difference|);
+                   and the paged form's two decode steps after the same prompt
+                   (refs.prefill_8b_paged_steps) with their logits, residual streams and
+                   written cache rows.
 Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b
-     | mul_mat_float | legacy_quants]   (needs oracle/_ref built)
+     | decoder_8b_prefill | mul_mat_float | legacy_quants]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -95,6 +106,7 @@ sys.path.insert(0, str(HERE.parents[1]))
 
 from refs import (DECODER_8B_STEPS, decoder_8b_layer_ref, decoder_8b_ref_run, decoder_8b_slice_config,  # noqa: E402
                   decoder_8b_weights, paged_8b_ref)
+from refs import PREFILL_8B_SAMPLE, decoder_8b_run_states, prefill_8b_paged_steps, prefill_8b_steps  # noqa: E402
 from refs import SDPA_CASES, sdpa_graph, sdpa_inputs  # noqa: E402
 from refs import Q4_1, Q5_0, Q5_1  # noqa: E402
 from refs import (BF16, F16, F32, FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
@@ -294,8 +306,68 @@ def decoder_8b_golden(ref) -> None:
     np.savez_compressed(HERE / "decoder_8b.npz", **out)
 
 
+def decoder_8b_prefill_golden(ref) -> None:
+    """configs[4]'s run shape on the 8B slice: refs.prefill_8b_steps (a
+    512-token prompt, a 64-token chunk, two single-token steps) on the CPU
+    backend, dense cache, P.V accumulated in f32 and, again, in f16 (the
+    backend's default); and the paged form's two decode steps after the same
+    prompt (refs.prefill_8b_paged_steps)."""
+    c = decoder_8b_slice_config()
+    w = decoder_8b_weights(c)
+    steps, psteps = prefill_8b_steps(), prefill_8b_paged_steps()
+    zero = lambda: [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]  # noqa: E731
+    runs = {}
+    for f32v in (True, False):
+        st = zero()
+        lg, taps = decoder_8b_run_states(ref, c, w, steps[:1], st, f32v)
+        stp = [s.copy() for s in st]
+        plg, ptaps = decoder_8b_run_states(ref, c, w, psteps, stp, f32v)
+        lg2, taps2 = decoder_8b_run_states(ref, c, w, steps[1:], st, f32v)
+        runs[f32v] = (lg + lg2, taps + taps2, st, plg, ptaps, stp)
+        print(f"prefill_8b: f32 P.V {f32v} done", flush=True)
+    lg, taps, st, plg, ptaps, stp = runs[True]
+    lg16, plg16 = runs[False][0], runs[False][3]
+    rows = max(p0 + len(t) for t, p0, _, _ in steps)
+    out = {"tap0_0s": taps[0][0][:4], "tap0_1": taps[0][1], "tap0_2s": taps[0][2][PREFILL_8B_SAMPLE]}
+    for i in range(len(steps)):
+        out[f"logits{i}"] = lg[i].reshape(-1)
+        d = np.abs(lg[i] - lg16[i])
+        out[f"spread{i}"] = np.float32(d.max())
+        out[f"spreadstats{i}"] = np.array([d.mean(), np.quantile(d, 0.999)], np.float32)
+        if i:
+            out[f"tap{i}_1"], out[f"tap{i}_2"] = taps[i][1], taps[i][2]
+    for j in range(2 * c.n_layer):
+        out[f"cache{j}"] = st[j][:rows]
+        out[f"pcache{j}"] = stp[j][512:514]  # the rows the paged decode steps write
+    caches = [s[:rows] for s in st]
+    pcaches = [s[:514] for s in stp]
+    for i, step in enumerate(steps):
+        for layer in range(c.n_layer):
+            tf = decoder_8b_layer_ref(ref, c, w, caches, step, layer, taps[i][layer], False)
+            d = np.abs(tf - taps[i][layer + 1])
+            out[f"tfspread{i}_{layer}"] = np.float32(d.max())
+            out[f"tfstats{i}_{layer}"] = np.array([d.mean(), np.quantile(d, 0.999), d.mean(axis=1).max()], np.float32)
+    for k, step in enumerate(psteps):
+        out[f"plogits{k}"] = plg[k].reshape(-1)
+        d = np.abs(plg[k] - plg16[k])
+        out[f"pspread{k}"] = np.float32(d.max())
+        out[f"pspreadstats{k}"] = np.array([d.mean(), np.quantile(d, 0.999)], np.float32)
+        for layer in range(c.n_layer + 1):
+            out[f"ptap{k}_{layer}"] = ptaps[k][layer]
+        for layer in range(c.n_layer):
+            tf = decoder_8b_layer_ref(ref, c, w, pcaches, step, layer, ptaps[k][layer], False)
+            d = np.abs(tf - ptaps[k][layer + 1])
+            out[f"ptfspread{k}_{layer}"] = np.float32(d.max())
+            out[f"ptfstats{k}_{layer}"] = np.array([d.mean(), np.quantile(d, 0.999), d.mean(axis=1).max()],
+                                                   np.float32)
+    np.savez_compressed(HERE / "decoder_8b_prefill.npz", **out)
+
+
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["decoder_8b_prefill"]:  # only the 8B-shaped prefill fixture
+        decoder_8b_prefill_golden(ref)
+        return
     if sys.argv[1:] == ["decoder_8b"]:  # only the 8B-shaped decoder fixture
         decoder_8b_golden(ref)
         return
@@ -391,6 +463,7 @@ def main() -> None:
     decoder_golden(ref)
     decoder_paged_golden(ref)
     decoder_8b_golden(ref)
+    decoder_8b_prefill_golden(ref)
     mul_mat_id_golden(ref)
     mul_mat_float_golden(ref)
     legacy_quants_golden(ref)

@@ -1044,13 +1044,18 @@ def decoder_8b_weights(c, seed=300):
     from tensorlisp_amd import native as N
     from tensorlisp_amd import synth
 
-    out = []
-    for i, (_, ty, ne) in enumerate(c.weight_shapes()):
-        if ty == N.F32:
-            out.append((1.0 + 0.1 * synth.normal(seed + i, (ne[0],))).astype(np.float32))
-        else:
-            out.append(synth.q4_K_model_blocks(seed + i, ne[1], ne[0], 0.02))
-    return out
+    return [decoder_8b_weight(c, i, seed) for i in range(len(c.weight_shapes()))]
+
+
+def decoder_8b_weight(c, i, seed=300):
+    """Weight i of decoder_8b_weights alone."""
+    from tensorlisp_amd import native as N
+    from tensorlisp_amd import synth
+
+    _, ty, ne = c.weight_shapes()[i]
+    if ty == N.F32:
+        return (1.0 + 0.1 * synth.normal(seed + i, (ne[0],))).astype(np.float32)
+    return synth.q4_K_model_blocks(seed + i, ne[1], ne[0], 0.02)
 
 
 # (tokens, first position, attended cache rows, logits of every token?): a
@@ -1097,6 +1102,61 @@ def decoder_8b_layer_ref(r, c, weights, caches, step, layer, x, f32_values):
     (out,) = r.ir_run(ls.builder, weights, states, [np.ascontiguousarray(x, np.float32), pos, pos.astype(np.int64),
                                                     G.causal_mask(pos, n_kv)], [(ls.out, np.float32)])
     return out.reshape(T_, c.n_embd)
+
+
+# configs[4]'s own run shape on the 8B slice: a 512-token prompt, a 64-token
+# chunk, then two single-token steps attending a padded 584-row view (tokens
+# uniform over the vocabulary); the paged form of the same prompt decodes two
+# other tokens at positions 512 and 513
+def prefill_8b_tokens():
+    from tensorlisp_amd import synth
+
+    t = synth.integers(340, 0, 128255, 512 + 64 + 4).astype(np.int64)
+    return [int(x) for x in t[:512]], [int(x) for x in t[512:576]], [int(x) for x in t[576:]]
+
+
+def prefill_8b_steps():
+    """(tokens, first position, attended cache rows, logits of every token?) of
+    the dense run."""
+    prompt, chunk, dec = prefill_8b_tokens()
+    return [(prompt, 0, 512, False), (chunk, 512, 576, False), ([dec[0]], 576, 584, False),
+            ([dec[1]], 577, 584, False)]
+
+
+def prefill_8b_paged_steps():
+    """The paged run's decode steps after the 512-token prompt, as dense steps
+    (each attends exactly the rows it has)."""
+    prompt, _, dec = prefill_8b_tokens()
+    return [([dec[2]], 512, 513, False), ([dec[3]], 513, 514, False)]
+
+
+# rows of the 512-token prompt's last residual stream kept in the fixture
+PREFILL_8B_SAMPLE = np.concatenate([np.arange(0, 512, 16), [511]])
+
+
+def decoder_8b_run_states(r, c, weights, steps, states, f32_values):
+    """`steps` through the reference CPU backend from the dense caches `states`
+    (updated in place); per step the logits and the residual stream after the
+    embedding and each layer."""
+    from tensorlisp_amd import graph as G
+
+    logits, taps = [], []
+    for step in steps:
+        st = G.decoder_step(c, len(step[0]), step[2], last_only=not step[3], f32_values=f32_values)
+        res = r.ir_run(st.builder, weights, states, decoder_step_inputs(step),
+                       [(st.logits, np.float32)] + [(t, np.float32) for t in st.taps])
+        logits.append(res[0].reshape(-1, c.n_vocab))
+        taps.append([x.reshape(len(step[0]), c.n_embd) for x in res[1:]])
+    return logits, taps
+
+
+def embed_rows(c, weights, tokens):
+    """The token embedding rows (GET_ROWS of the q4_K table, which the CPU
+    backend forms with dequantize_row_q4_K) through the oracle's dequantizer,
+    which the quant fixtures pin bit for bit to the reference's."""
+    rb = row_bytes(Q4_K, c.n_embd)
+    tab = weights[0].reshape(c.n_vocab, rb)
+    return oracle().dequantize(Q4_K, np.ascontiguousarray(tab[np.asarray(tokens)]), c.n_embd).reshape(-1, c.n_embd)
 
 
 # 16 sequences of the 8B slice for a batched paged decode: prompts of 1..16
