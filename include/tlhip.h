@@ -50,6 +50,8 @@ enum {
     TLH_TYPE_Q5_1 = 7,
     TLH_TYPE_Q8_0 = 8,
     TLH_TYPE_Q8_1 = 9,
+    TLH_TYPE_Q2_K = 10,
+    TLH_TYPE_Q3_K = 11,
     TLH_TYPE_Q4_K = 12,
     TLH_TYPE_Q5_K = 13,
     TLH_TYPE_Q6_K = 14,

@@ -14,15 +14,17 @@
 // bytes, 128 nibble bytes), :345-352 (q5_K: q4_K's header, 32 bytes of fifth
 // bits, 128 nibble bytes), :362-368 (q6_K: 128 low-nibble bytes, 64 bytes of
 // 2-bit high parts, 16 int8 scales, f16 d), :370-375 (q8_K: f32 d, 256 int8,
-// 16 int16 sums).
+// 16 int16 sums); :298-323 (q2_K: 16 bytes of 4-bit scale | 4-bit min << 4, 64
+// bytes of 2-bit codes, f16 d, f16 dmin; q3_K: 32 bytes of high code bits, 64
+// bytes of 2-bit low code parts, 12 bytes of packed 6-bit scales, f16 d).
 enum { QK32 = 32, QKK = 256, Q4_0_B = 18, Q8_0_B = 34, Q4_K_B = 144, Q5_K_B = 176, Q6_K_B = 210, Q8_K_B = 292,
-       Q4_1_B = 20, Q5_0_B = 22, Q5_1_B = 24, Q8_1_B = 36 };
+       Q4_1_B = 20, Q5_0_B = 22, Q5_1_B = 24, Q8_1_B = 36, Q2_K_B = 84, Q3_K_B = 110 };
 
 int64_t tlq_block_elems(int type) {
     switch (type) {
     case TLQ_F32: case TLQ_F16: case TLQ_BF16: return 1;
     case TLQ_Q4_0: case TLQ_Q8_0: case TLQ_Q4_1: case TLQ_Q5_0: case TLQ_Q5_1: case TLQ_Q8_1: return QK32;
-    case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
+    case TLQ_Q2_K: case TLQ_Q3_K: case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: case TLQ_Q8_K: return QKK;
     default: return 0;
     }
 }
@@ -41,6 +43,8 @@ int64_t tlq_block_bytes(int type) {
     case TLQ_Q5_K: return Q5_K_B;
     case TLQ_Q6_K: return Q6_K_B;
     case TLQ_Q8_K: return Q8_K_B;
+    case TLQ_Q2_K: return Q2_K_B;
+    case TLQ_Q3_K: return Q3_K_B;
     default: return 0;
     }
 }
@@ -54,7 +58,7 @@ int tlq_vec_dot_type(int wtype) {
     switch (wtype) {
     case TLQ_Q4_0: case TLQ_Q8_0: case TLQ_Q5_0: return TLQ_Q8_0;
     case TLQ_Q4_1: case TLQ_Q5_1: return TLQ_Q8_1;
-    case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: return TLQ_Q8_K;
+    case TLQ_Q2_K: case TLQ_Q3_K: case TLQ_Q4_K: case TLQ_Q5_K: case TLQ_Q6_K: return TLQ_Q8_K;
     case TLQ_F32: case TLQ_F16: case TLQ_BF16: return wtype;
     default: return -1;
     }
@@ -462,6 +466,58 @@ void tlq_dequantize_row_q6_K(const void *vx, float *y, int64_t k) {
     }
 }
 
+// q2_K element i of a super-block (ggml-quants.c:961-989): per 128-element
+// half h, element 32j + l keeps its 2-bit code in byte qs[32h + l] at bit 2j;
+// sub-block i / 16 has scale = low nibble, min = high nibble of scales[i / 16].
+static int q2k_code(const uint8_t *blk, int i) {
+    const int h = i / 128, e = i % 128, j = e / 32, l = e % 32;
+    return (blk[16 + 32 * h + l] >> (2 * j)) & 3;
+}
+
+// y = (d * scale) * code - (dmin * min): two roundings, as the reference.
+void tlq_dequantize_row_q2_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q2_K_B) {
+        const float d = tlq_fp16_to_fp32(rd16(x + 80)), dmin = tlq_fp16_to_fp32(rd16(x + 82));
+        for (int i = 0; i < QKK; ++i) {
+            const uint8_t sc = x[i / 16];
+            const float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+            *y++ = dl * (float)q2k_code(x, i) - ml;
+        }
+    }
+}
+
+// q3_K element i (ggml-quants.c:1305-1351): the low 2 bits as q2_K's (qs at
+// byte 32), the third bit in hmask[l] at bit 4h + j; a clear bit subtracts 4,
+// so codes are -4..3.
+static int q3k_code(const uint8_t *blk, int i) {
+    const int h = i / 128, e = i % 128, j = e / 32, l = e % 32;
+    const int lo = (blk[32 + 32 * h + l] >> (2 * j)) & 3;
+    return lo - (((blk[l] >> (4 * h + j)) & 1) ? 0 : 4);
+}
+
+// The 6-bit scale of q3_K sub-block s minus 32, from the 12 packed bytes at
+// byte 96: low 4 bits in byte s (s < 8) or the high nibble of byte s - 8,
+// high 2 bits in byte 8 + s % 4 at bit 2 (s / 4) (the kmask unpacking of
+// ggml-quants.c:1324-1328).
+static int q3k_scale(const uint8_t *blk, int s) {
+    const uint8_t *sc = blk + 96;
+    const int lo = s < 8 ? (sc[s] & 15) : (sc[s - 8] >> 4);
+    const int hi = (sc[8 + s % 4] >> (2 * (s / 4))) & 3;
+    return (lo | hi << 4) - 32;
+}
+
+void tlq_dequantize_row_q3_K(const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q3_K_B) {
+        const float d = tlq_fp16_to_fp32(rd16(x + 108));
+        for (int i = 0; i < QKK; ++i) {
+            const float dl = d * (float)q3k_scale(x, i / 16);
+            *y++ = dl * (float)q3k_code(x, i);
+        }
+    }
+}
+
 void tlq_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
     const uint8_t *x = (const uint8_t *)vx;
     for (int64_t b = 0; b < k / QKK; ++b, x += Q8_K_B, y += QKK) {
@@ -518,6 +574,8 @@ int tlq_dequantize_row(int type, const void *x, float *y, int64_t k) {
     case TLQ_Q5_K: tlq_dequantize_row_q5_K(x, y, k); return 0;
     case TLQ_Q6_K: tlq_dequantize_row_q6_K(x, y, k); return 0;
     case TLQ_Q8_K: tlq_dequantize_row_q8_K(x, y, k); return 0;
+    case TLQ_Q2_K: tlq_dequantize_row_q2_K(x, y, k); return 0;
+    case TLQ_Q3_K: tlq_dequantize_row_q3_K(x, y, k); return 0;
     default: return -1;
     }
 }
@@ -712,6 +770,56 @@ float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *vx, const void *vy) {
     return sumf;
 }
 
+// ggml-cpu/quants.c:565-615. Per super-block: the min term as an int
+// (summs = sum_s bsums_s * min_s), the code sum isum = sum_s scale_s *
+// sum_{e in s} q8_e * code_e, then sumf += dall * isum - dmin * summs with
+// dall = d8 * d, dmin = d8 * dmin in f32, super-block by super-block.
+float tlq_vec_dot_q2_K_q8_K(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float sumf = 0;
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q2_K_B, y += Q8_K_B) {
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int summs = 0, isum = 0;
+        for (int s = 0; s < 16; ++s) {
+            const int16_t bsum = (int16_t)rd16(y + 260 + 2 * s);
+            summs += bsum * (x[s] >> 4);
+            int part = 0;
+            for (int l = 0; l < 16; ++l) part += q8[16 * s + l] * q2k_code(x, 16 * s + l);
+            isum += (x[s] & 15) * part;
+        }
+        const float d8 = rdf32(y);
+        const float dall = d8 * tlq_fp16_to_fp32(rd16(x + 80));
+        const float dmin = d8 * tlq_fp16_to_fp32(rd16(x + 82));
+        sumf += dall * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+// ggml-cpu/quants.c:617-694. Per super-block: eight int32 lane accumulators
+// (element e of each 16-element sub-block feeds lane e % 8) of (scale_s - 32)
+// * (q8 * code) with the int16 product, then sums[lane] += (d * d8) * lane,
+// and sumf = sums[0] + ... + sums[7] at the end.
+float tlq_vec_dot_q3_K_q8_K(int64_t k, const void *vx, const void *vy) {
+    const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+    float sums[8] = {0};
+    for (int64_t b = 0; b < k / QKK; ++b, x += Q3_K_B, y += Q8_K_B) {
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int32_t aux32[8] = {0};
+        for (int s = 0; s < 16; ++s) {
+            const int sc = q3k_scale(x, s);
+            for (int l = 0; l < 16; ++l) {
+                const int e = 16 * s + l;
+                aux32[l % 8] += sc * (int16_t)(q8[e] * q3k_code(x, e));
+            }
+        }
+        const float d = tlq_fp16_to_fp32(rd16(x + 108)) * rdf32(y);
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+    }
+    float sumf = 0;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
 // ------------------------------------------------------ float dot products
 // vec.cpp:11-143 / :139-262 / :264-352 without GGML_SIMD: f32 products, double sum.
 float tlq_vec_dot_f32(int64_t k, const void *vx, const void *vy) {
@@ -764,6 +872,8 @@ int tlq_mul_mat(int wtype, const void *w, int64_t M, int64_t K, const float *x, 
     case TLQ_Q4_K: dot = tlq_vec_dot_q4_K_q8_K; break;
     case TLQ_Q5_K: dot = tlq_vec_dot_q5_K_q8_K; break;
     case TLQ_Q6_K: dot = tlq_vec_dot_q6_K_q8_K; break;
+    case TLQ_Q2_K: dot = tlq_vec_dot_q2_K_q8_K; break;
+    case TLQ_Q3_K: dot = tlq_vec_dot_q3_K_q8_K; break;
     case TLQ_Q4_1: dot = tlq_vec_dot_q4_1_q8_1; break;
     case TLQ_Q5_0: dot = tlq_vec_dot_q5_0_q8_0; break;
     case TLQ_Q5_1: dot = tlq_vec_dot_q5_1_q8_1; break;

@@ -29,6 +29,8 @@ enum {
     TLQ_Q5_1 = 7,
     TLQ_Q8_0 = 8,
     TLQ_Q8_1 = 9,
+    TLQ_Q2_K = 10,
+    TLQ_Q3_K = 11,
     TLQ_Q4_K = 12,
     TLQ_Q5_K = 13,
     TLQ_Q6_K = 14,
@@ -37,13 +39,14 @@ enum {
 };
 
 // Block geometry, vendor/ggml/src/ggml-common.h:89-90,194-198,201-269 (q4_1, q5_0,
-// q5_1, q8_1: 20, 22, 24, 36 bytes per 32),325-337,370-375.
+// q5_1, q8_1: 20, 22, 24, 36 bytes per 32),298-323 (q2_K, q3_K: 84, 110 bytes
+// per 256),325-337,370-375.
 int64_t tlq_block_elems(int type);
 int64_t tlq_block_bytes(int type);
 int64_t tlq_row_bytes(int type, int64_t k);
 // vec_dot_type of a weight type on x86 (ggml-cpu.c:215-226,239-319,394-399):
 // Q8_0 for Q4_0, Q5_0 and Q8_0 weights, Q8_1 for Q4_1 and Q5_1, Q8_K for the
-// K-quants, the weight type itself for F32 / F16 / BF16; -1 otherwise.
+// K-quants (q2_K..q6_K), the weight type itself for F32 / F16 / BF16; -1 otherwise.
 int tlq_vec_dot_type(int wtype);
 
 // IEEE binary16 <-> binary32 (round to nearest even), the semantics of
@@ -89,6 +92,9 @@ void tlq_dequantize_row_q8_K(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q4_1(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q5_0(const void *x, float *y, int64_t k);
 void tlq_dequantize_row_q5_1(const void *x, float *y, int64_t k);
+// dequantize_row_q2_K ggml-quants.c:961-989, _q3_K :1305-1351.
+void tlq_dequantize_row_q2_K(const void *x, float *y, int64_t k);
+void tlq_dequantize_row_q3_K(const void *x, float *y, int64_t k);
 int tlq_dequantize_row(int type, const void *x, float *y, int64_t k);
 
 // Dot products of one weight row with one quantized activation row:
@@ -105,6 +111,10 @@ float tlq_vec_dot_q6_K_q8_K(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q4_1_q8_1(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q5_0_q8_0(int64_t k, const void *x, const void *y);
 float tlq_vec_dot_q5_1_q8_1(int64_t k, const void *x, const void *y);
+// ggml_vec_dot_q2_K_q8_K_generic ggml-cpu/quants.c:565-615, _q3_K_q8_K_generic
+// :617-694 (the x86 entries without AVX call them, arch/x86/quants.c:1762, :2034).
+float tlq_vec_dot_q2_K_q8_K(int64_t k, const void *x, const void *y);
+float tlq_vec_dot_q3_K_q8_K(int64_t k, const void *x, const void *y);
 
 // Exact integer parts of one block product (for pinning GPU partial sums):
 // q4_K: *sum_q = sum_s sc_s * sum_{e in s} q4_e*q8_e, *sum_m = sum_s m_s * sum_{e in s} q8_e.

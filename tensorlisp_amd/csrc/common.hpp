@@ -12,8 +12,8 @@ namespace tlh {
 // ----------------------------------------------------------- block formats
 // vendor/ggml/src/ggml-common.h:194-198 (q4_0), :201-211 (q4_1), :229-248
 // (q5_0, q5_1), :251-269 (q8_0, q8_1), :325-337 (q4_K), :345-352 (q5_K),
-// :362-368 (q6_K), :370-375 (q8_K). Byte sizes per block and elements per
-// block.
+// :362-368 (q6_K), :370-375 (q8_K), :298-323 (q2_K, q3_K). Byte sizes per
+// block and elements per block.
 constexpr int QK = 32;    // q4_0 / q4_1 / q5_0 / q5_1 / q8_0 / q8_1 block
 constexpr int QKK = 256;  // k-quant super-block
 constexpr int Q4_0_BYTES = 18;
@@ -26,9 +26,15 @@ constexpr int Q4_K_BYTES = 144;
 constexpr int Q5_K_BYTES = 176;  // f16 d, dmin; scales[12] as q4_K; qh[32] (fifth bits); qs[128] (low nibbles)
 constexpr int Q6_K_BYTES = 210;  // ql[128] (low 4 bits), qh[64] (high 2 bits), int8 scales[16], f16 d
 constexpr int Q8_K_BYTES = 292;
+constexpr int Q2_K_BYTES = 84;   // scales[16] (4-bit scale | 4-bit min << 4), qs[64] (2-bit codes), f16 d, dmin
+constexpr int Q3_K_BYTES = 110;  // hmask[32] (third code bits), qs[64] (2-bit low parts), scales[12] (6-bit), f16 d
+
+__host__ __device__ constexpr bool kquant_type(int t) {
+    return t == TLH_TYPE_Q2_K || t == TLH_TYPE_Q3_K || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K;
+}
 
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K || t == TLH_TYPE_Q8_K) ? QKK
+    return (kquant_type(t) || t == TLH_TYPE_Q8_K) ? QKK
            : (t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_1 || t == TLH_TYPE_Q5_0 ||
               t == TLH_TYPE_Q5_1 || t == TLH_TYPE_Q8_1)
                ? QK
@@ -45,12 +51,14 @@ __host__ __device__ constexpr int block_bytes(int t) {
            : t == TLH_TYPE_Q5_0 ? Q5_0_BYTES
            : t == TLH_TYPE_Q5_1 ? Q5_1_BYTES
            : t == TLH_TYPE_Q8_1 ? Q8_1_BYTES
+           : t == TLH_TYPE_Q2_K ? Q2_K_BYTES
+           : t == TLH_TYPE_Q3_K ? Q3_K_BYTES
            : t == TLH_TYPE_F16  ? 2
                                 : 4;
 }
 // vec_dot_type on x86 (vendor/ggml/src/ggml-cpu/ggml-cpu.c:239-319).
 __host__ __device__ constexpr int vec_dot_type(int wtype) {
-    return (wtype == TLH_TYPE_Q4_K || wtype == TLH_TYPE_Q5_K || wtype == TLH_TYPE_Q6_K) ? TLH_TYPE_Q8_K
+    return kquant_type(wtype)                                                            ? TLH_TYPE_Q8_K
            : (wtype == TLH_TYPE_Q4_1 || wtype == TLH_TYPE_Q5_1)                          ? TLH_TYPE_Q8_1
                                                                                           : TLH_TYPE_Q8_0;
 }
@@ -102,10 +110,30 @@ __device__ __forceinline__ uint32_t spread4(uint32_t b4) { return ((b4 * 0x00204
 // (q-8)*d (ggml-quants.c:459-476), q8_0 q*d (:553-565), q4_K (d*sc)*q -
 // (dmin*m) (:1529-1550), q5_K the same with a fifth code bit (:1731-1756),
 // q6_K (d*sc)*q (:1939-1968), q4_1 q*d + m (:479-498), q5_0 (q-16)*d
-// (:500-524), q5_1 q*d + m (:526-551).
+// (:500-524), q5_1 q*d + m (:526-551), q2_K (d*sc)*q - (dmin*m) (:961-989),
+// q3_K (d*(sc-32))*q (:1305-1351).
 template <int WT> __device__ __forceinline__ float dequant_elem(const uint8_t *r, int64_t col) {
 #pragma clang fp contract(off)
-    if constexpr (WT == TLH_TYPE_Q4_1 || WT == TLH_TYPE_Q5_0 || WT == TLH_TYPE_Q5_1) {
+    if constexpr (WT == TLH_TYPE_Q2_K || WT == TLH_TYPE_Q3_K) {
+        // element e = 32j + l of half h: 2-bit code in qs[32h + l] at bit 2j
+        // (q3_K: its third bit in hmask[l] at bit 4h + j, clear = minus 4)
+        constexpr bool Q3 = WT == TLH_TYPE_Q3_K;
+        const uint8_t *b = r + (col / QKK) * (Q3 ? Q3_K_BYTES : Q2_K_BYTES);
+        const int i = (int)(col % QKK);
+        const int h = i >> 7, j = (i >> 5) & 3, l = i & 31, s = i >> 4;
+        const int lo = (b[(Q3 ? 32 : 16) + 32 * h + l] >> (2 * j)) & 3;
+        if constexpr (Q3) {
+            const int code = lo - (((b[l] >> (4 * h + j)) & 1) ? 0 : 4);
+            const uint8_t *sc = b + 96;  // 6-bit scales: low 4 bits, then high 2 bits at byte 8 + s % 4
+            const int scale = ((s < 8 ? (sc[s] & 15) : (sc[s - 8] >> 4)) | (((sc[8 + (s & 3)] >> (2 * (s >> 2))) & 3) << 4)) - 32;
+            const float d = h2f((uint16_t)(b[108] | (b[109] << 8)));
+            return (d * (float)scale) * (float)code;
+        } else {
+            const float d = h2f((uint16_t)(b[80] | (b[81] << 8))), dmin = h2f((uint16_t)(b[82] | (b[83] << 8)));
+            const float dl = d * (float)(b[s] & 15), ml = dmin * (float)(b[s] >> 4);
+            return dl * (float)lo - ml;
+        }
+    } else if constexpr (WT == TLH_TYPE_Q4_1 || WT == TLH_TYPE_Q5_0 || WT == TLH_TYPE_Q5_1) {
         const uint8_t *b = r + (col / QK) * block_bytes(WT);
         const int j = (int)(col % QK);
         const uint8_t byte = b[blk_qs_off(WT) + (j & 15)];

@@ -767,6 +767,8 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q2_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q2_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q3_K: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q3_K>, g, dim3(256), 0, stream, a); break;
         default: hipLaunchKernelGGL(k_core_get_rows<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
         }
         break;
@@ -793,6 +795,8 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
         case TLH_TYPE_Q8_0: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q8_0>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q4_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q4_K>, g, dim3(256), 0, stream, a); break;
         case TLH_TYPE_Q5_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q5_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q2_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q2_K>, g, dim3(256), 0, stream, a); break;
+        case TLH_TYPE_Q3_K: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q3_K>, g, dim3(256), 0, stream, a); break;
         default: hipLaunchKernelGGL(k_core_cpy<TLH_TYPE_Q6_K>, g, dim3(256), 0, stream, a); break;
         }
         break;

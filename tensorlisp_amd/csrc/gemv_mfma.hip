@@ -86,20 +86,23 @@ __device__ __forceinline__ uint2 lds_u64(const uint32_t *base, uint32_t off) {
 }
 
 // Bytes of one row per unit (the stride between units).
-template <int WT> constexpr int unit_bytes() {
-    return WT == TLH_TYPE_Q4_K   ? Q4_K_BYTES
-           : WT == TLH_TYPE_Q5_K ? Q5_K_BYTES
-           : WT == TLH_TYPE_Q6_K ? Q6_K_BYTES
-                                 : 8 * block_bytes(WT);
-}
+template <int WT> constexpr int unit_bytes() { return kquant_type(WT) ? block_bytes(WT) : 8 * block_bytes(WT); }
 // 32-element block types whose codes are nibbles (q5: plus a fifth bit):
 // a lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16 + 4g.. (high)
 template <int WT> constexpr bool nibble_type() { return WT == TLH_TYPE_Q4_0 || legacy_type(WT); }
 // Bytes of a unit staged through LDS (a multiple of 16): all of it, but for
-// q6_K its first 208 (ql, qh, scales; d, the last 2 bytes, is loaded apart).
-template <int WT> constexpr int staged_bytes() { return WT == TLH_TYPE_Q6_K ? 208 : unit_bytes<WT>(); }
+// q6_K its first 208 (ql, qh, scales; d, the last 2 bytes, is loaded apart),
+// q2_K its first 80 (scales, qs; d and dmin loaded apart) and q3_K its first
+// 96 (hmask, qs; the 12 scale bytes and d loaded apart).
+template <int WT> constexpr int staged_bytes() {
+    return WT == TLH_TYPE_Q6_K ? 208 : WT == TLH_TYPE_Q2_K ? 80 : WT == TLH_TYPE_Q3_K ? 96 : unit_bytes<WT>();
+}
+// Types with bytes loaded beside the staged ones (one unit per wave).
+template <int WT> constexpr bool staged_extra() {
+    return WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q2_K || WT == TLH_TYPE_Q3_K;
+}
 // Types whose unit is one k-quant super-block (one activation scale slot).
-template <int WT> constexpr bool kquant() { return WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K || WT == TLH_TYPE_Q6_K; }
+template <int WT> constexpr bool kquant() { return kquant_type(WT); }
 
 // One lane's weight data of one unit in operand form: q4_K the super-block
 // header and bytes 8g..8g+7 of each 32-byte chunk; q8_0 / q4_0 per block the
@@ -156,6 +159,30 @@ template <> struct UnitW<TLH_TYPE_Q6_K> {
 #pragma unroll
         for (int h = 0; h < 2; ++h) qh[h] = *(const uint2 *)(blk + 128 + 32 * h + 8 * g);
         sc = *(const uint4 *)(blk + 192);
+    }
+};
+
+// q2_K / q3_K from the staged LDS copy: lane g's operand bytes of step m
+// (elements 32m + 8g..+7; half h = m / 4, run j = m % 4, l = 8g..8g+7) are
+// the half's qs bytes l (2-bit fields 2j) at 16 + 32h + 8g (q2_K, after the
+// 16 scale bytes) or 32 + 32h + 8g (q3_K, after the 32 hmask bytes); q3_K
+// adds hmask bytes 8g..8g+7 (bit 4h + j); q2_K keeps all 16 scale bytes.
+template <> struct UnitW<TLH_TYPE_Q2_K> {
+    uint2 q[2];  // [h]
+    uint4 sc;
+    __device__ __forceinline__ void load_lds(const uint8_t *blk, int g) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) q[h] = *(const uint2 *)(blk + 16 + 32 * h + 8 * g);
+        sc = *(const uint4 *)blk;
+    }
+};
+template <> struct UnitW<TLH_TYPE_Q3_K> {
+    uint2 q[2];  // [h]
+    uint2 hm;
+    __device__ __forceinline__ void load_lds(const uint8_t *blk, int g) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) q[h] = *(const uint2 *)(blk + 32 + 32 * h + 8 * g);
+        hm = *(const uint2 *)(blk + 8 * g);
     }
 };
 
@@ -304,6 +331,83 @@ __device__ __forceinline__ void unit_mma_q6k(const UnitW<TLH_TYPE_Q6_K> &w, uint
     for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r];
 }
 
+// q2_K super-block (vec_dot_q2_K_q8_K_generic, ggml-cpu/quants.c:565-615):
+// 16 sub-blocks of 16, scale (low nibble) and min (high nibble) per
+// sub-block. Each 32-element step runs twice with the other sub-block's lanes
+// of the weight operand zeroed (as q6_K); S = sum scale_s * S_s in int32, and
+// the min term Mn = sum_s min_s * (sum of q8 in s) is one more MFMA per step
+// whose weight operand is min_{2m} on lanes g < 2 and min_{2m+1} on g >= 2.
+// dm: the unit's f16 d (low half) and dmin (high half).
+__device__ __forceinline__ void unit_mma_q2k(const UnitW<TLH_TYPE_Q2_K> &w, uint32_t dm, const long (&A)[8],
+                                             const float *sdu, int g, float (&y)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    v4i S = {0, 0, 0, 0}, Mn = {0, 0, 0, 0};
+    const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const uint2 qv = w.q[m >> 2];
+        const int sh = 2 * (m & 3);
+        const long B = pack2((qv.x >> sh) & 0x03030303u, (qv.y >> sh) & 0x03030303u);
+        const v4i S0 = mfma_i8(A[m], g < 2 ? B : 0, zero);   // sub-block 2m
+        const v4i S1 = mfma_i8(A[m], g >= 2 ? B : 0, zero);  // sub-block 2m + 1
+        const uint32_t b2 = (scw[m >> 1] >> (16 * (m & 1))) & 0xffffu;  // scale bytes 2m, 2m + 1
+        const int s0 = (int)(b2 & 15), s1 = (int)((b2 >> 8) & 15);
+        const uint32_t mn = g < 2 ? (b2 >> 4) & 15 : (b2 >> 12) & 15;
+        const uint32_t m4 = mn * 0x01010101u;
+        Mn = mfma_i8(A[m], pack2(m4, m4), Mn);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[r] += __mul24(s0, S0[r]) + __mul24(s1, S1[r]);  // |S_s| < 2^13
+    }
+    const float d = h2f((uint16_t)(dm & 0xffff)), dmin = h2f((uint16_t)(dm >> 16));
+    const float4 d8 = *(const float4 *)(sdu + 4 * g);
+    const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
+}
+
+// q3_K super-block (vec_dot_q3_K_q8_K_generic, ggml-cpu/quants.c:617-694):
+// codes (low 2 bits | third bit << 2) - 4 as signed bytes, steps as q2_K's;
+// the 16 6-bit scales (minus 32) unpacked into four words of bytes: low 4
+// bits from scale bytes 0..7 (low nibbles: sub-blocks 0..7, high: 8..15),
+// high 2 bits of sub-block 4q + k from byte 8 + k at bit 2q. S = sum scale_s
+// * S_s in int32, scaled by d * d8. ex: block bytes 94..109 (scale bytes at
+// 2..13, d at 14..15).
+__device__ __forceinline__ void unit_mma_q3k(const UnitW<TLH_TYPE_Q3_K> &w, uint4 ex, const long (&A)[8],
+                                             const float *sdu, int g, float (&y)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    v4i S = {0, 0, 0, 0};
+    const uint32_t b0 = (ex.x >> 16) | (ex.y << 16), b1 = (ex.y >> 16) | (ex.z << 16);
+    const uint32_t b2 = (ex.z >> 16) | (ex.w << 16);
+    const uint32_t lo[4] = {b0 & 0x0f0f0f0fu, b1 & 0x0f0f0f0fu, (b0 >> 4) & 0x0f0f0f0fu, (b1 >> 4) & 0x0f0f0f0fu};
+    uint32_t scw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) scw[q] = lo[q] | (((b2 >> (2 * q)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int h = m >> 2, j = m & 3;
+        const uint2 qv = w.q[h];
+        const uint32_t hv[2] = {w.hm.x, w.hm.y}, lv[2] = {qv.x, qv.y};
+        uint32_t b[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u = ((lv[i] >> (2 * j)) & 0x03030303u) | (((hv[i] >> (4 * h + j)) & 0x01010101u) << 2);
+            b[i] = ((u | 0x80808080u) - 0x04040404u) ^ 0x80808080u;  // u - 4 per byte, no borrows
+        }
+        const long B = pack2(b[0], b[1]);
+        const v4i S0 = mfma_i8(A[m], g < 2 ? B : 0, zero);   // sub-block 2m
+        const v4i S1 = mfma_i8(A[m], g >= 2 ? B : 0, zero);  // sub-block 2m + 1
+        const uint32_t sw = (scw[m >> 1] >> (16 * (m & 1))) & 0xffffu;
+        const int s0 = (int)(sw & 0xff) - 32, s1 = (int)(sw >> 8) - 32;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[r] += __mul24(s0, S0[r]) + __mul24(s1, S1[r]);  // |S_s| < 2^13
+    }
+    const float d = h2f((uint16_t)(ex.w >> 16));
+    const float4 d8 = *(const float4 *)(sdu + 4 * g);
+    const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r];
+}
+
 // y[r] += the unit's contribution to output (column 4g + r, the lane's weight
 // row). A: the unit's activation operands; sdu: its activation scales in LDS
 // (q4_K one slot, q4_0 / q8_0 one per block) as [slot][16 columns];
@@ -367,13 +471,18 @@ __device__ __forceinline__ void unit_mma(const UnitW<WT> &w, const long (&A)[8],
 
 // Staging of one row group's slice: lane l loads pieces 64i + l (16 bytes
 // each) of the 16 rows x KS units, row-major; NL loads per lane.
+template <int WT> struct StageExtra { using T = uint32_t; };
+template <> struct StageExtra<TLH_TYPE_Q3_K> { using T = uint4; };
 template <int WT, int KS> struct Stage {
     static constexpr int RB = KS * staged_bytes<WT>();  // slice bytes per row (a multiple of 16)
     static constexpr int PR = RB / 16;                   // pieces per row
     static constexpr int NL = (16 * PR + 63) / 64;
     static constexpr int BUF = NL * 64 * 16 + 16;        // LDS bytes per wave (with read slack)
     uint4 v[NL];
-    uint32_t dq;  // q6_K: the lane's row's d (KS = 1)
+    // the lane's row's bytes loaded beside the staged ones (KS = 1): q6_K its
+    // d, q2_K d and dmin, q3_K the 12 scale bytes and d (block bytes 94..109)
+    using ExtraT = typename StageExtra<WT>::T;
+    ExtraT dq;
 };
 
 // Direct loads of KS units (prefetch set of the unstaged kernel, 32-element
@@ -397,7 +506,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     constexpr int AT = vec_dot_type(WT);
     constexpr bool KQ = kquant<WT>();
     constexpr int UB = unit_bytes<WT>();
-    static_assert(WT != TLH_TYPE_Q6_K || KS == 1, "q6_K staging keeps one d per lane");
+    static_assert(!staged_extra<WT>() || KS == 1, "q6_K / q2_K / q3_K staging keeps one unit's extra bytes per lane");
     using St = Stage<WT, KS>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
@@ -479,9 +588,12 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const uint8_t *q = pr[i] < rows_left ? gb + pofs[i] : wlast + (pofs[i] - pr[i] * a.w_nb1);
             s.v[i] = ldu<uint4>(q);
         }
-        if constexpr (WT == TLH_TYPE_Q6_K) {
+        if constexpr (staged_extra<WT>()) {
             const int64_t ud = u0 < u_end ? u0 : u_begin;  // a unit of the row (products past u_end are skipped)
-            s.dq = ldu<uint16_t>(wrow_of(grp) + ud * UB + 208);
+            const uint8_t *ub = wrow_of(grp) + ud * UB;
+            if constexpr (WT == TLH_TYPE_Q6_K) s.dq = ldu<uint16_t>(ub + 208);
+            else if constexpr (WT == TLH_TYPE_Q2_K) s.dq = ldu<uint32_t>(ub + 80);
+            else s.dq = ldu<uint4>(ub + 94);
         }
     };
 
@@ -578,7 +690,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
         return KQ ? 8 : (int)(v < 0 ? 0 : v > 8 ? 8 : v);
     };
     // multiply one row group from the wave's LDS buffer
-    auto process_staged = [&](int64_t grp, int parity, uint32_t dq) {
+    auto process_staged = [&](int64_t grp, int parity, typename St::ExtraT dq) {
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
@@ -588,6 +700,14 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
                 UnitW<WT> w;
                 w.load_lds(wbuf + ub, g);
                 unit_mma_q6k(w, dq, A[t], unit_slots(t), g, y);
+            } else if constexpr (WT == TLH_TYPE_Q2_K) {
+                UnitW<WT> w;
+                w.load_lds(wbuf + ub, g);
+                unit_mma_q2k(w, dq, A[t], unit_slots(t), g, y);
+            } else if constexpr (WT == TLH_TYPE_Q3_K) {
+                UnitW<WT> w;
+                w.load_lds(wbuf + ub, g);
+                unit_mma_q3k(w, dq, A[t], unit_slots(t), g, y);
             } else if constexpr (KQ) {
                 UnitW<WT> w;
                 w.load_lds(wbuf + ub, g);
@@ -633,7 +753,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
-            if constexpr (WT != TLH_TYPE_Q6_K)
+            if constexpr (!staged_extra<WT>())
                 unit_mma<WT>(d.u[t], A[t], unit_slots(t), unit_slots(t) + s_gap, g, unit_nvalid(t), y);
         }
         finish(y, grp, parity);
@@ -651,7 +771,7 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const int64_t r1 = rg + gridDim.x;
 #pragma unroll
             for (int i = 0; i < St::NL; ++i) *(uint4 *)(wbuf + 1024 * i + 16 * lane) = st.v[i];
-            const uint32_t dq = st.dq;  // this group's (read with its weight bytes above)
+            const auto dq = st.dq;  // this group's (read with its weight bytes above)
             stage_load(st, r1 < groups ? r1 : rg);
             process_staged(rg, it & 1, dq);
             rg = r1;
@@ -936,6 +1056,8 @@ tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream) {
     case TLH_TYPE_Q4_K: return launch_sk_wt<TLH_TYPE_Q4_K>(a, staged, stream);
     case TLH_TYPE_Q5_K: return launch_sk_wt<TLH_TYPE_Q5_K>(a, staged, stream);
     case TLH_TYPE_Q6_K: return launch_sk_wt<TLH_TYPE_Q6_K>(a, staged, stream);
+    case TLH_TYPE_Q2_K: return launch_sk_wt<TLH_TYPE_Q2_K>(a, staged, stream);
+    case TLH_TYPE_Q3_K: return launch_sk_wt<TLH_TYPE_Q3_K>(a, staged, stream);
     default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: weight type %d", a.wtype);
     }
 }

@@ -1,5 +1,6 @@
 // Decode GEMV launchers for q4_0, q8_0, q4_K, q5_K and q6_K weights (the
-// kernels are in gemv_reg.hpp); q4_1 / q5_0 / q5_1 go to gemv_reg_q.hip.
+// kernels are in gemv_reg.hpp); q4_1 / q5_0 / q5_1 / q2_K / q3_K go to
+// gemv_reg_q.hip.
 #include "gemv_reg.hpp"
 
 namespace tlh {
@@ -39,7 +40,7 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     if (!reg_counts_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: counts past 2^31");
     int ksplit = 1, upw = 64;
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
-    if (legacy_type(a.wtype)) return launch_gemv_reg_legacy(a, x, x_row_bytes, ksplit, upw, stream);
+    if (reg_plain_type(a.wtype)) return launch_gemv_reg_legacy(a, x, x_row_bytes, ksplit, upw, stream);
     const GemvPro none;
     if (!x) return launch_reg_type<IN_SCRATCH, OUT_STORE>(a, nullptr, 0, none, ksplit, upw, stream);
     if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: in-kernel quantization takes K <= 4096");
@@ -52,7 +53,7 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
     if (!reg_counts_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: counts past 2^31");
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     if (a.ne12 * a.ne13 != 1) return set_error(TLH_INVALID, "gemv_reg: a prologue / epilogue takes one batch slice");
-    if (legacy_type(a.wtype)) return set_error(TLH_UNSUPPORTED, "gemv_reg: no fused forms for weight type %d", a.wtype);
+    if (reg_plain_type(a.wtype)) return set_error(TLH_UNSUPPORTED, "gemv_reg: no fused forms for weight type %d", a.wtype);
     const bool glu = pro.glu != nullptr;
     if (glu && (a.nseg != 2 || a.seg_m0[1] != a.seg_m0[2] - a.seg_m0[1]))
         return set_error(TLH_INVALID, "gemv_reg: the SwiGLU epilogue needs two segments of equal rows");

@@ -538,6 +538,125 @@ template <int R> struct WRegs<TLH_TYPE_Q6_K, R> {
     }
 };
 
+// q2_K and q3_K: a lane's unit u = 4 * super-block + 2h + c is the 64
+// contiguous elements 128h + 64c.. of the super-block, the code runs j = 2c
+// and 2c + 1 of half h. Element 32j + l of the half keeps its 2-bit code in
+// the half's qs byte l at bit 2j, so the lane loads the half's 32 qs bytes
+// and takes bits 4c and 4c + 2 of each. Its four 16-element sub-blocks are
+// 8h + 4c .. 8h + 4c + 3.
+//
+// q2_K (vec_dot_q2_K_q8_K_generic, ggml-cpu/quants.c:565-615): sub-block s
+// has scale (low nibble) and min (high nibble) in byte s of the block; per
+// super-block the CPU forms isum = sum_s scale_s * sum(q8 * code) and summs =
+// sum_s min_s * bsum_s exactly, then (d8 * d) * isum - (d8 * dmin) * summs.
+template <int R> struct WRegs<TLH_TYPE_Q2_K, R> {
+    uint4 q0[R], q1[R];
+    uint32_t sc[R], dm[R];
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+        const int64_t sb = u >> 2;
+        const int h = (int)((u >> 1) & 1), c = (int)(u & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + sb * Q2_K_BYTES;
+            q0[r] = ldu16(blk + 16 + 32 * h);
+            q1[r] = ldu16(blk + 32 + 32 * h);
+            __builtin_memcpy(&sc[r], blk + 8 * h + 4 * c, 4);
+            __builtin_memcpy(&dm[r], blk + 80, 4);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t u, float (&acc)[R][NC]) const {
+        const int c = (int)(u & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            int code[16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                code[i] = (int)((w[i] >> (4 * c)) & 0x03030303u);
+                code[8 + i] = (int)((w[i] >> (4 * c + 2)) & 0x03030303u);
+            }
+            const float d = h2f((uint16_t)(dm[r] & 0xffff)), dmin = h2f((uint16_t)(dm[r] >> 16));
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int isum = 0, summs = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int s = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s = dot4(code[4 * k + i], act[n].q[4 * k + i], s);
+                    const int b = (int)((sc[r] >> (8 * k)) & 0xff);
+                    isum += (b & 15) * s;
+                    summs += (b >> 4) * act[n].b[k];
+                }
+                acc[r][n] += (d * act[n].d0) * (float)isum - (dmin * act[n].d0) * (float)summs;
+            }
+        }
+    }
+};
+
+// q3_K (vec_dot_q3_K_q8_K_generic, ggml-cpu/quants.c:617-694): the low 2 bits
+// as q2_K's (qs at block byte 32), the third bit of element 32j + l of half h
+// in hmask byte l at bit 4h + j; code = low | bit << 2 in 0..7 stands for
+// code - 4, applied as -4 * bsum per sub-block. Sub-block s has the 6-bit
+// scale (low 4 bits: byte s for s < 8, else the high nibble of byte s - 8;
+// high 2 bits: byte 8 + s % 4 at bit 2 (s / 4)) minus 32. Per super-block the
+// int32 sum of scale * (dot - 4 * bsum), scaled by d * d8.
+template <int R> struct WRegs<TLH_TYPE_Q3_K, R> {
+    uint4 m0[R], m1[R], q0[R], q1[R];
+    uint4 sd[R];  // block bytes 94..109: the 12 scale bytes at 2..13, d at 14..15
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
+        const int64_t sb = u >> 2;
+        const int h = (int)((u >> 1) & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = wrow[r] + sb * Q3_K_BYTES;
+            m0[r] = ldu16(blk);
+            m1[r] = ldu16(blk + 16);
+            q0[r] = ldu16(blk + 32 + 32 * h);
+            q1[r] = ldu16(blk + 48 + 32 * h);
+            sd[r] = ldu16(blk + 94);
+        }
+    }
+    template <int NC>
+    __device__ __forceinline__ void compute(const AUnit (&act)[NC], int64_t u, float (&acc)[R][NC]) const {
+        const int h = (int)((u >> 1) & 1), c = (int)(u & 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            const uint32_t m[8] = {m0[r].x, m0[r].y, m0[r].z, m0[r].w, m1[r].x, m1[r].y, m1[r].z, m1[r].w};
+            const int ba = 4 * h + 2 * c;  // hmask bit of the unit's first run
+            int code[16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                code[i] = (int)(((w[i] >> (4 * c)) & 0x03030303u) | (((m[i] >> ba) & 0x01010101u) << 2));
+                code[8 + i] = (int)(((w[i] >> (4 * c + 2)) & 0x03030303u) | (((m[i] >> (ba + 1)) & 0x01010101u) << 2));
+            }
+            // the unit's four scale bytes: low 4 bits from scale bytes 4c..4c+3
+            // (high nibbles for h = 1), high 2 bits from bytes 8..11 at bit
+            // 2 (2h + c) = ba
+            const uint32_t s0 = (sd[r].x >> 16) | (sd[r].y << 16);  // scale bytes 0..3
+            const uint32_t s1 = (sd[r].y >> 16) | (sd[r].z << 16);  // 4..7
+            const uint32_t s2 = (sd[r].z >> 16) | (sd[r].w << 16);  // 8..11
+            const uint32_t sc4 = (((c ? s1 : s0) >> (4 * h)) & 0x0f0f0f0fu) | (((s2 >> ba) & 0x03030303u) << 4);
+            const float d = h2f((uint16_t)(sd[r].w >> 16));
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                int tot = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int s = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s = dot4(code[4 * k + i], act[n].q[4 * k + i], s);
+                    const int scale = (int)((sc4 >> (8 * k)) & 0xff) - 32;
+                    tot += scale * (s - 4 * act[n].b[k]);
+                }
+                acc[r][n] += (d * act[n].d0) * (float)tot;
+            }
+        }
+    }
+};
+
 // q4_1 / q5_0 / q5_1 (vec_dot_q4_1_q8_1_generic, _q5_0_q8_0_generic,
 // _q5_1_q8_1_generic, ggml-cpu/quants.c:262-296, :365-449): the lane's two
 // blocks of 32 as q4_0's, nibble bytes 4i..4i+3 hold elements 4i.. (low) and
@@ -1094,8 +1213,10 @@ static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_
 template <int WT, int NC, int IN, int OUT>
 static tlh_status launch_reg_nc(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                 int ksplit, int upw, hipStream_t stream) {
-    // q6_K holds 19 weight registers per row: two columns take 2 rows per wave
-    constexpr int R = ((WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q5_K) && NC == 2) ? 2 : NC <= 2 ? 4 : (NC <= 4 ? 2 : 1);
+    // q6_K / q5_K / q3_K hold about 20 weight registers per row: two columns take 2 rows per wave
+    constexpr int R = ((WT == TLH_TYPE_Q6_K || WT == TLH_TYPE_Q5_K || WT == TLH_TYPE_Q3_K) && NC == 2) ? 2
+                      : NC <= 2                                                                       ? 4
+                      : (NC <= 4 ? 2 : 1);
     return launch_reg_cfg<WT, NC, R, IN, OUT>(a, x, x_row_bytes, pro, ksplit, upw, stream);
 }
 

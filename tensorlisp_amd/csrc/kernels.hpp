@@ -123,11 +123,16 @@ bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_byte
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
 // the register GEMV with a prologue and / or epilogue (GemvPro); quantizes in-kernel
-// q4_1 / q5_0 / q5_1 register GEMV (gemv_reg_q.hip): plain stores only
+// q4_1 / q5_0 / q5_1 / q2_K / q3_K register GEMV (gemv_reg_q.hip): plain stores only
 tlh_status launch_gemv_reg_legacy(const MatmulArgs &a, const float *x, int64_t x_row_bytes, int ksplit, int upw,
                                   hipStream_t stream);
 __host__ __device__ constexpr bool legacy_type(int t) {
     return t == TLH_TYPE_Q4_1 || t == TLH_TYPE_Q5_0 || t == TLH_TYPE_Q5_1;
+}
+// weight types whose register GEMV lives in gemv_reg_q.hip (plain stores, no
+// prologue / epilogue forms): q4_1 / q5_0 / q5_1, q2_K / q3_K
+__host__ __device__ constexpr bool reg_plain_type(int t) {
+    return legacy_type(t) || t == TLH_TYPE_Q2_K || t == TLH_TYPE_Q3_K;
 }
 tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const float *x, int64_t x_row_bytes,
                                hipStream_t stream);

@@ -175,6 +175,12 @@ tlh_status launch_dequantize(int type, const void *w, int64_t K, int64_t rows, i
     case TLH_TYPE_Q6_K:
         hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q6_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
         break;
+    case TLH_TYPE_Q2_K:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q2_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
+    case TLH_TYPE_Q3_K:
+        hipLaunchKernelGGL(k_dequantize<TLH_TYPE_Q3_K>, dim3(g), dim3(256), 0, stream, wb, K, rows, w_row_bytes, y);
+        break;
     default:
         return set_error(TLH_UNSUPPORTED, "dequantize: unsupported type %d", type);
     }

@@ -57,8 +57,7 @@ static tlh_status hip_check(hipError_t e, const char *what) {
 tlh_status noalloc_setup_current_device();
 
 static bool weight_type_ok(int t) {
-    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || t == TLH_TYPE_Q4_K || t == TLH_TYPE_Q5_K || t == TLH_TYPE_Q6_K ||
-           legacy_type(t);
+    return t == TLH_TYPE_Q4_0 || t == TLH_TYPE_Q8_0 || kquant_type(t) || legacy_type(t);
 }
 
 static const char *type_name(int t) {
@@ -72,6 +71,8 @@ static const char *type_name(int t) {
     case TLH_TYPE_Q8_0: return "q8_0";
     case TLH_TYPE_Q8_1: return "q8_1";
     case TLH_TYPE_BF16: return "bf16";
+    case TLH_TYPE_Q2_K: return "q2_K";
+    case TLH_TYPE_Q3_K: return "q3_K";
     case TLH_TYPE_Q4_K: return "q4_K";
     case TLH_TYPE_Q5_K: return "q5_K";
     case TLH_TYPE_Q6_K: return "q6_K";
@@ -96,8 +97,8 @@ static tlh_status check_mul_mat(const tlh_op *op, MulMatShape &s) {
     s.flt = float_type(a.ty);
     if (!weight_type_ok(a.ty) && !s.flt)
         return set_error(TLH_UNSUPPORTED,
-                         "mul_mat: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q4_K, q5_K, q6_K, "
-                         "f32, f16, bf16", a.ty,
+                         "mul_mat: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q2_K, q3_K, q4_K, "
+                         "q5_K, q6_K, f32, f16, bf16", a.ty,
                          type_name(a.ty));
     // src1 is f32, or (ggml's vec_dot_type rule) already the f16 / bf16 of f16 / bf16 weights
     if (b.ty != TLH_TYPE_F32 && !(s.flt && a.ty != TLH_TYPE_F32 && b.ty == a.ty))
@@ -276,7 +277,8 @@ static tlh_status check_core(int kind, const tlh_op *op, bool has1, bool has2) {
         return TLH_OK;
     case TLH_CORE_GET_ROWS:
         if (!(a_data || rows_of_blocks(a)) || !idx_ty(b.ty) || !elem_strides_ok(b) || !d_data)
-            return unsup("GET_ROWS: f32/f16/q4_0/q8_0/q4_K/q5_K/q6_K rows, i32/i64 indices, f32/f16 destination");
+            return unsup("GET_ROWS: f32/f16/bf16 or quantized (q4_0 ... q8_0, q2_K ... q6_K) rows, i32/i64 indices, "
+                         "f32/f16 destination");
         if (d.ne[0] != a.ne[0] || d.ne[1] != b.ne[0] || d.ne[2] != b.ne[1] || d.ne[3] != b.ne[2] ||
             a.ne[2] != b.ne[1] || a.ne[3] != b.ne[2] || (a.ne[1] == 0 && nel(d) > 0))
             return unsup("GET_ROWS: shapes");
@@ -605,8 +607,9 @@ bool tlh::mul_mat_multi_ok(const tlh_op *const *ops, int n) {
     MulMatShape first;
     for (int i = 0; i < n; ++i) {
         MulMatShape s;
-        // q4_1 / q5_0 / q5_1 have no fused (prologue / epilogue) register kernels
-        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || legacy_type(s.wtype) || s.N != 1 ||
+        // q4_1 / q5_0 / q5_1 / q2_K / q3_K have no segment or fused (prologue /
+        // epilogue) register kernels
+        if (check_mul_mat(ops[i], s) != TLH_OK || mm_empty(s) || s.flt || reg_plain_type(s.wtype) || s.N != 1 ||
             s.ne12 * s.ne13 != 1)
             return false;
         int ks, upw;
@@ -831,7 +834,8 @@ static tlh_status check_mul_mat_id(const tlh_op *op, MulMatIdShape &s) {
     const tlh_tensor &a = op->t[0], &b = op->t[1], &ids = op->t[2], &d = op->t[4];
     if (!weight_type_ok(a.ty))
         return set_error(TLH_UNSUPPORTED,
-                         "mul_mat_id: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q4_K, q5_K, q6_K",
+                         "mul_mat_id: weights of ggml type %d (%s); have q4_0, q4_1, q5_0, q5_1, q8_0, q2_K, q3_K, "
+                         "q4_K, q5_K, q6_K",
                          a.ty, type_name(a.ty));
     if (b.ty != TLH_TYPE_F32 || d.ty != TLH_TYPE_F32 || ids.ty != TLH_TYPE_I32)
         return set_error(TLH_UNSUPPORTED, "mul_mat_id: f32 src1 and dst, i32 ids");

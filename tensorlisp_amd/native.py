@@ -20,13 +20,15 @@ LIB_PATH = PKG / "libtlhip.so"
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 30
 Q4_1, Q5_0, Q5_1, Q8_1 = 3, 6, 7, 9
+Q2_K, Q3_K = 10, 11
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292),
-         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_1: (32, 36), F32: (1, 4), F16: (1, 2), BF16: (1, 2)}
+         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_1: (32, 36), F32: (1, 4), F16: (1, 2), BF16: (1, 2),
+         Q2_K: (256, 84), Q3_K: (256, 110)}
 # ggml's vec_dot_type: what src1 is converted to (float weights: their own type)
 VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_0: Q8_0, Q5_1: Q8_1,
-                F32: F32, F16: F16, BF16: BF16}
+                F32: F32, F16: F16, BF16: BF16, Q2_K: Q8_K, Q3_K: Q8_K}
 TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K",
-              BF16: "bf16", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q8_1: "q8_1"}
+              BF16: "bf16", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q8_1: "q8_1", Q2_K: "q2_K", Q3_K: "q3_K"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 STATUS = {0: "OK", 1: "NO_DEVICE", 2: "UNSUPPORTED", 3: "INVALID", 4: "ALLOC", 5: "EXECUTION"}

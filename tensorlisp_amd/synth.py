@@ -75,7 +75,7 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
     """Structurally valid random blocks of a weight type, sized like weights
     quantized from N(0, std) (finite f16 scales, random codes). Used where
     quantizing full-size f32 weights on the host would dominate run time."""
-    from .native import Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K
+    from .native import Q2_K, Q3_K, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K
 
     if wtype == Q8_0:
         return q8_0_config1(seed, M, K)
@@ -114,6 +114,24 @@ def random_blocks(wtype: int, seed: int, M: int, K: int, std: float = 0.02) -> n
         blocks = raw.copy()
         blocks[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
         return blocks.reshape(M, (K // 256) * 210)
+    if wtype == Q2_K:
+        # random 4-bit scale / min pairs and 2-bit codes; d, dmin > 0 sized so
+        # d * 15 * 3 and dmin * 15 span about the weights' range
+        nb = M * (K // 256)
+        d = f16_bits(np.abs(normal(seed + 1, (nb,), std)) / np.float32(15 * 1.5))
+        dmin = f16_bits(np.abs(normal(seed + 2, (nb,), std)) / np.float32(15))
+        blocks = bits(seed, (nb * 84 + 7) // 8).view(np.uint8)[:nb * 84].reshape(nb, 84).copy()
+        blocks[:, 80:82] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 82:84] = dmin.view(np.uint8).reshape(nb, 2)
+        return blocks.reshape(M, (K // 256) * 84)
+    if wtype == Q3_K:
+        # random high bits, 2-bit codes and packed 6-bit scales (-32..31); a
+        # signed d, as the quantizer's 1 / iscale may be
+        nb = M * (K // 256)
+        d = f16_bits(normal(seed + 1, (nb,), std) / np.float32(32 * 2))
+        blocks = bits(seed, (nb * 110 + 7) // 8).view(np.uint8)[:nb * 110].reshape(nb, 110).copy()
+        blocks[:, 108:110] = d.view(np.uint8).reshape(nb, 2)
+        return blocks.reshape(M, (K // 256) * 110)
     if wtype in (Q4_1, Q5_0, Q5_1):
         # random code bytes (nibbles and fifth bits); q5_0 a signed d as q4_0,
         # q4_1 / q5_1 d > 0 with a min m < 0 about half the block's range

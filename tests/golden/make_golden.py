@@ -17,6 +17,13 @@ these are the reference's outputs on fixed inputs, captured once:
   mul_mat.npz      one GGML_OP_MUL_MAT on the CPU backend for the reference test's
                    cases (native.rs:73-107: 96 x 256 weights from noise(seed 1),
                    x = noise(seed 10 + n), n in 1,3,5,8,9,40) per weight type
+  q2_K.npz, q3_K.npz  as q5_K.npz for the two lowest k-quants
+  decoder_lowk.npz the tiny decoder with a Q2_K model file's matrix types
+                   (refs.decoder_lowk_config: q2_K embedding and matrices, q3_K value
+                   and down projections and lm_head) over refs.LOWK_STEPS (decoder.npz's
+                   steps plus a 20-token chunk) with P.V accumulated in f32: logits,
+                   argmax, final caches, and how far the default f16 accumulation moves
+                   the logits (largest and mean |difference|) and the caches
   legacy_quants.npz  q4_1, q5_0 and q5_1 (the reference test's other 32-element
                    types, native.rs:84): ggml_quantize_chunk of its 96 x 256 noise
                    matrix, dequantize_row_*, one GGML_OP_MUL_MAT per n in 1,3,5,8,9,40;
@@ -90,7 +97,7 @@ these are the reference's outputs on fixed inputs, captured once:
                    (refs.prefill_8b_paged_steps) with their logits, residual streams and
                    written cache rows.
 Run: python tests/golden/make_golden.py [flash_attn_ext | q6_K | q5_K | core | decoder | decoder_paged | mul_mat_id | decoder_8b
-     | decoder_8b_prefill | mul_mat_float | legacy_quants]   (needs oracle/_ref built)
+     | decoder_8b_prefill | lowk | mul_mat_float | legacy_quants]   (needs oracle/_ref built)
 """
 from __future__ import annotations
 
@@ -109,6 +116,7 @@ from refs import (DECODER_8B_STEPS, decoder_8b_layer_ref, decoder_8b_ref_run, de
 from refs import PREFILL_8B_SAMPLE, decoder_8b_run_states, prefill_8b_paged_steps, prefill_8b_steps  # noqa: E402
 from refs import SDPA_CASES, sdpa_graph, sdpa_inputs  # noqa: E402
 from refs import Q4_1, Q5_0, Q5_1  # noqa: E402
+from refs import LOWK_STEPS, Q2_K, Q3_K, decoder_lowk_config  # noqa: E402
 from refs import (BF16, F16, F32, FA_CASES, MMID_CASES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref, core_cases, core_ref, decoder_ref_run,  # noqa: E402
                   decoder_tiny_config, decoder_weights, fa_case_inputs, fp16_probe_values, mmid_case, paged_ref_run,
                   xorshift_noise)
@@ -181,6 +189,27 @@ def q6_K_golden(ref) -> None:
 
 def q5_K_golden(ref) -> None:
     kquant_golden(ref, Q5_K, "q5_K", 71, 72)
+
+
+def lowk_golden(ref) -> None:
+    """q2_K.npz and q3_K.npz (as q5_K.npz), and decoder_lowk.npz: the tiny
+    decoder with a Q2_K file's matrix types (refs.decoder_lowk_config) over
+    refs.LOWK_STEPS on the CPU backend."""
+    kquant_golden(ref, Q2_K, "q2_K", 81, 82)
+    kquant_golden(ref, Q3_K, "q3_K", 91, 92)
+    c = decoder_lowk_config()
+    w = decoder_weights(c)
+    logits, ams, caches = decoder_ref_run(ref, c, w, LOWK_STEPS, f32_values=True)
+    lg16, _, c16 = decoder_ref_run(ref, c, w, LOWK_STEPS)
+    out = {f"logits{i}": lg for i, lg in enumerate(logits)}
+    out.update({f"argmax{i}": a for i, a in enumerate(ams)})
+    out.update({f"cache{i}": s for i, s in enumerate(caches)})
+    for i, (a, b) in enumerate(zip(logits, lg16)):
+        d = np.abs(a - b)
+        out[f"spread{i}"] = np.array([d.max(), d.mean()], np.float32)
+    for j, (a, b) in enumerate(zip(caches, c16)):
+        out[f"cspread{j}"] = np.float32(np.abs(ref.f16_to_f32(a) - ref.f16_to_f32(b)).max())
+    np.savez_compressed(HERE / "decoder_lowk.npz", **out)
 
 
 def legacy_quants_golden(ref) -> None:
@@ -365,6 +394,9 @@ def decoder_8b_prefill_golden(ref) -> None:
 
 def main() -> None:
     ref = Ref()
+    if sys.argv[1:] == ["lowk"]:  # only the q2_K / q3_K fixtures
+        lowk_golden(ref)
+        return
     if sys.argv[1:] == ["decoder_8b_prefill"]:  # only the 8B-shaped prefill fixture
         decoder_8b_prefill_golden(ref)
         return
@@ -459,6 +491,7 @@ def main() -> None:
     flash_attn_ext_golden(ref)
     q6_K_golden(ref)
     q5_K_golden(ref)
+    lowk_golden(ref)
     core_golden(ref)
     decoder_golden(ref)
     decoder_paged_golden(ref)

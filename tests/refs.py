@@ -24,11 +24,13 @@ REF_SO = ROOT / "oracle" / "_ref" / "libggml_ref.so"
 # ggml type numbers (vendor/ggml/include/ggml.h:390-405)
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 30
 Q4_1, Q5_0, Q5_1, Q8_1 = 3, 6, 7, 9
+Q2_K, Q3_K = 10, 11
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292),
-         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_1: (32, 36)}
-VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_0: Q8_0, Q5_1: Q8_1}
+         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_1: (32, 36), Q2_K: (256, 84), Q3_K: (256, 110)}
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_0: Q8_0, Q5_1: Q8_1,
+                Q2_K: Q8_K, Q3_K: Q8_K}
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32", F16: "f16",
-         BF16: "bf16", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q8_1: "q8_1"}
+         BF16: "bf16", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q8_1: "q8_1", Q2_K: "q2_K", Q3_K: "q3_K"}
 
 
 FLOAT_BYTES = {F32: 4, F16: 2, BF16: 2}  # element sizes of the float weight types
@@ -109,12 +111,14 @@ class Oracle:
                      "tlq_quantize_row_q8_K", "tlq_dequantize_row_q4_0", "tlq_dequantize_row_q8_0",
                      "tlq_dequantize_row_q4_K", "tlq_dequantize_row_q5_K", "tlq_dequantize_row_q6_K",
                      "tlq_dequantize_row_q8_K", "tlq_quantize_row_q8_1", "tlq_dequantize_row_q4_1",
-                     "tlq_dequantize_row_q5_0", "tlq_dequantize_row_q5_1"):
+                     "tlq_dequantize_row_q5_0", "tlq_dequantize_row_q5_1", "tlq_dequantize_row_q2_K",
+                     "tlq_dequantize_row_q3_K"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("tlq_vec_dot_q4_0_q8_0", "tlq_vec_dot_q8_0_q8_0", "tlq_vec_dot_q4_K_q8_K",
                      "tlq_vec_dot_q5_K_q8_K", "tlq_vec_dot_q6_K_q8_K", "tlq_vec_dot_q4_1_q8_1",
-                     "tlq_vec_dot_q5_0_q8_0", "tlq_vec_dot_q5_1_q8_1"):
+                     "tlq_vec_dot_q5_0_q8_0", "tlq_vec_dot_q5_1_q8_1", "tlq_vec_dot_q2_K_q8_K",
+                     "tlq_vec_dot_q3_K_q8_K"):
             getattr(L, name).argtypes = [i64, vp, vp]
             getattr(L, name).restype = C.c_float
         L.tlq_fp16_to_fp32_row.argtypes = [vp, vp, i64]
@@ -194,7 +198,8 @@ class Oracle:
               Q4_K: self.lib.tlq_dequantize_row_q4_K, Q5_K: self.lib.tlq_dequantize_row_q5_K,
               Q6_K: self.lib.tlq_dequantize_row_q6_K,
               Q8_K: self.lib.tlq_dequantize_row_q8_K, Q4_1: self.lib.tlq_dequantize_row_q4_1,
-              Q5_0: self.lib.tlq_dequantize_row_q5_0, Q5_1: self.lib.tlq_dequantize_row_q5_1}[t]
+              Q5_0: self.lib.tlq_dequantize_row_q5_0, Q5_1: self.lib.tlq_dequantize_row_q5_1,
+              Q2_K: self.lib.tlq_dequantize_row_q2_K, Q3_K: self.lib.tlq_dequantize_row_q3_K}[t]
         fn(_p(q), _p(out), rows * k)
         return out
 
@@ -204,7 +209,8 @@ class Oracle:
         fn = {Q4_0: self.lib.tlq_vec_dot_q4_0_q8_0, Q8_0: self.lib.tlq_vec_dot_q8_0_q8_0,
               Q4_K: self.lib.tlq_vec_dot_q4_K_q8_K, Q5_K: self.lib.tlq_vec_dot_q5_K_q8_K,
               Q6_K: self.lib.tlq_vec_dot_q6_K_q8_K, Q4_1: self.lib.tlq_vec_dot_q4_1_q8_1,
-              Q5_0: self.lib.tlq_vec_dot_q5_0_q8_0, Q5_1: self.lib.tlq_vec_dot_q5_1_q8_1}[wtype]
+              Q5_0: self.lib.tlq_vec_dot_q5_0_q8_0, Q5_1: self.lib.tlq_vec_dot_q5_1_q8_1,
+              Q2_K: self.lib.tlq_vec_dot_q2_K_q8_K, Q3_K: self.lib.tlq_vec_dot_q3_K_q8_K}[wtype]
         return float(fn(k, _p(xrow), _p(yrow)))
 
     def block_ints_q4_K(self, xblock, yblock):
@@ -352,12 +358,14 @@ class Ref:
         for name in ("quantize_row_q8_0", "quantize_row_q8_K", "quantize_row_q8_0_ref", "quantize_row_q8_K_ref",
                      "quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "dequantize_row_q4_0",
                      "dequantize_row_q8_0", "dequantize_row_q4_K", "dequantize_row_q5_K", "dequantize_row_q6_K",
-                     "quantize_row_q8_1", "dequantize_row_q4_1", "dequantize_row_q5_0", "dequantize_row_q5_1"):
+                     "quantize_row_q8_1", "dequantize_row_q4_1", "dequantize_row_q5_0", "dequantize_row_q5_1",
+                     "dequantize_row_q2_K", "dequantize_row_q3_K"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
         for name in ("ggml_vec_dot_q4_0_q8_0", "ggml_vec_dot_q8_0_q8_0", "ggml_vec_dot_q4_K_q8_K",
                      "ggml_vec_dot_q5_K_q8_K", "ggml_vec_dot_q6_K_q8_K", "ggml_vec_dot_q4_1_q8_1",
-                     "ggml_vec_dot_q5_0_q8_0", "ggml_vec_dot_q5_1_q8_1"):
+                     "ggml_vec_dot_q5_0_q8_0", "ggml_vec_dot_q5_1_q8_1", "ggml_vec_dot_q2_K_q8_K",
+                     "ggml_vec_dot_q3_K_q8_K"):
             getattr(L, name).argtypes = [C.c_int, C.POINTER(C.c_float), C.c_size_t, vp, C.c_size_t, vp, C.c_size_t,
                                          C.c_int]
             getattr(L, name).restype = None
@@ -427,7 +435,8 @@ class Ref:
         fn = {Q4_0: self.lib.dequantize_row_q4_0, Q8_0: self.lib.dequantize_row_q8_0,
               Q4_K: self.lib.dequantize_row_q4_K, Q5_K: self.lib.dequantize_row_q5_K,
               Q6_K: self.lib.dequantize_row_q6_K, Q4_1: self.lib.dequantize_row_q4_1,
-              Q5_0: self.lib.dequantize_row_q5_0, Q5_1: self.lib.dequantize_row_q5_1}[t]
+              Q5_0: self.lib.dequantize_row_q5_0, Q5_1: self.lib.dequantize_row_q5_1,
+              Q2_K: self.lib.dequantize_row_q2_K, Q3_K: self.lib.dequantize_row_q3_K}[t]
         fn(_p(q), _p(out), rows * k)
         return out
 
@@ -438,7 +447,8 @@ class Ref:
         fn = {Q4_0: self.lib.ggml_vec_dot_q4_0_q8_0, Q8_0: self.lib.ggml_vec_dot_q8_0_q8_0,
               Q4_K: self.lib.ggml_vec_dot_q4_K_q8_K, Q5_K: self.lib.ggml_vec_dot_q5_K_q8_K,
               Q6_K: self.lib.ggml_vec_dot_q6_K_q8_K, Q4_1: self.lib.ggml_vec_dot_q4_1_q8_1,
-              Q5_0: self.lib.ggml_vec_dot_q5_0_q8_0, Q5_1: self.lib.ggml_vec_dot_q5_1_q8_1}[wtype]
+              Q5_0: self.lib.ggml_vec_dot_q5_0_q8_0, Q5_1: self.lib.ggml_vec_dot_q5_1_q8_1,
+              Q2_K: self.lib.ggml_vec_dot_q2_K_q8_K, Q3_K: self.lib.ggml_vec_dot_q3_K_q8_K}[wtype]
         fn(k, C.byref(s), 0, _p(xrow), 0, _p(yrow), 0, 1)
         return float(s.value)
 
@@ -1002,6 +1012,22 @@ DECODER_STEPS = [([1, 7, 3, 999, 0], 0, 8, False), ([42], 5, 8, False), ([17], 6
                  ([3, 4, 5], 8, 16, True)]
 
 
+def decoder_lowk_config():
+    """The tiny decoder with the matrix types of a Q2_K model file: q2_K token
+    embedding and attention / FFN matrices, q3_K value and down projections and
+    lm_head (llama.cpp's Q2_K mix keeps those a step higher)."""
+    from tensorlisp_amd import graph as G
+
+    types = {f"l{i}.{n}": Q3_K for i in range(2) for n in ("wv", "w_down")}
+    return G.DecoderConfig(n_embd=256, n_head=4, n_head_kv=2, n_ff=512, n_layer=2, n_vocab=1000, n_ctx=64,
+                           wtype=Q2_K, embd_type=Q2_K, out_type=Q3_K, types=types)
+
+
+# DECODER_STEPS plus a 20-token chunk (more than 16 columns: the few-column
+# kernel's 16-column slabs)
+LOWK_STEPS = DECODER_STEPS + [(list(range(100, 120)), 11, 32, False)]
+
+
 def decoder_step_inputs(step):
     from tensorlisp_amd import graph as G
 
@@ -1010,15 +1036,16 @@ def decoder_step_inputs(step):
     return [np.array(toks, np.int32), pos, pos.astype(np.int64), G.causal_mask(pos, n_kv)]
 
 
-def decoder_ref_run(r, c, weights):
-    """DECODER_STEPS through the reference CPU backend; returns (logits per
-    step, argmax per step, final caches)."""
+def decoder_ref_run(r, c, weights, steps=DECODER_STEPS, f32_values=False):
+    """`steps` through the reference CPU backend; returns (logits per step,
+    argmax per step, final caches). f32_values: attention reads the cached
+    values through an f32 cast (P.V accumulated in f32)."""
     from tensorlisp_amd import graph as G
 
     states = [np.zeros((c.n_ctx, c.n_embd_kv), np.uint16) for _ in range(2 * c.n_layer)]
     logits, ams = [], []
-    for step in DECODER_STEPS:
-        st = G.decoder_step(c, len(step[0]), step[2], last_only=not step[3])
+    for step in steps:
+        st = G.decoder_step(c, len(step[0]), step[2], last_only=not step[3], f32_values=f32_values)
         lg, am = r.ir_run(st.builder, weights, states, decoder_step_inputs(step),
                           [(st.logits, np.float32), (st.argmax, np.int32)])
         logits.append(lg.reshape(-1, c.n_vocab))

@@ -104,10 +104,20 @@ def test_mul_mat_scratch_has_mfma_partials_for_long_K(wt, n, K, parts):
 
 
 def test_mul_mat_unsupported_weight_type_is_named():
+    """A weight type the reference's lowering refuses too (quant_ok,
+    crates/kernels/src/cuda/lower.rs:117-119, admits 2, 3, 6, 7, 8, 10..14 and
+    the float types): iq2_xxs (16)."""
     op = N.mul_mat_op(N.Q4_0, 64, 256, 1)
-    op.t[0].ty = 11  # q3_K
+    op.t[0].ty = 16
     st, msg, _ = scratch_status(op)
-    assert st == "UNSUPPORTED" and "type 11" in msg
+    assert st == "UNSUPPORTED" and "type 16" in msg
+
+
+def test_mul_mat_admits_the_reference_lowering_types():
+    """Every quantized type quant_ok admits (lower.rs:117-119) sizes its scratch."""
+    for t in (N.Q4_0, N.Q4_1, N.Q5_0, N.Q5_1, N.Q8_0, N.Q2_K, N.Q3_K, N.Q4_K, N.Q5_K, N.Q6_K):
+        st, msg, _ = scratch_status(N.mul_mat_op(t, 64, 512, 3))
+        assert st == "OK", (t, msg)
 
 
 def test_mul_mat_rejects_bad_shapes_and_layouts():
@@ -138,7 +148,9 @@ def test_mul_mat_null_pointers_are_invalid_not_crashes():
 
 def test_quantize_and_dequantize_validation():
     L = N.lib()
-    st, msg = _status(L.tlh_quantize_act, 11, None, 256, 1, 1024, None, None)  # q3_K
+    st, msg = _status(L.tlh_quantize_act, 16, None, 256, 1, 1024, None, None)  # iq2_xxs
+    assert st == "UNSUPPORTED"
+    st, msg = _status(L.tlh_dequantize, 16, None, 256, 1, 66, None, None)
     assert st == "UNSUPPORTED"
     st, msg = _status(L.tlh_quantize_act, N.Q4_K, None, 300, 1, 1200, None, None)
     assert st == "INVALID" and "multiple" in msg
@@ -321,7 +333,7 @@ def test_core_validation():
         (N.CORE_BIN, [f32(64, 5), f32(64, 5)], f32(64, 5), (4,), "INVALID", "BIN code"),
         (N.CORE_UNARY, [f32(9, 2)], f32(9, 2), (17,), "UNSUPPORTED", "unary op 17"),
         (N.CORE_NORM, [f16(64, 2)], f32(64, 2), (1,), "UNSUPPORTED", "NORM"),
-        (N.CORE_GET_ROWS, [N.ggml_tensor(11, [512, 40], [110, 220, 8800, 8800]), i32(7)], f32(512, 7), (),
+        (N.CORE_GET_ROWS, [N.ggml_tensor(16, [512, 40], [66, 132, 5280, 5280]), i32(7)], f32(512, 7), (),
          "UNSUPPORTED", "GET_ROWS"),
         (N.CORE_GET_ROWS, [f32(512, 40), i32(7)], f32(512, 6), (), "UNSUPPORTED", "shapes"),
         (N.CORE_SET_ROWS, [f32(512, 5), i32(4)], f32(512, 64), (), "UNSUPPORTED", "shapes"),
@@ -369,7 +381,7 @@ def test_mul_mat_id_scratch_and_validation():
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
     rows, K = 2 * 3, 512
     assert n.value == al(al(al(al(rows * K) + rows * (K // 256) * 4) + rows * (K // 16) * 2))
-    for kw in ({"n_b1": 3}, {"ids_ty": N.F32}, {"wt": 11}):
+    for kw in ({"n_b1": 3}, {"ids_ty": N.F32}, {"wt": 16}):
         st, msg = _status(L.tlh_mul_mat_id_scratch_bytes, C.byref(_mmid_op(**kw)), C.byref(n))
         assert st == "UNSUPPORTED", (kw, msg)
     op = _mmid_op()

@@ -137,7 +137,7 @@ def test_unsupported_ops_are_reported_by_name():
     with pytest.raises(N.TlhError, match=r"IM2COL x2 .*POOL_2D x1"):
         G.plan(b, [z])
     b = G.Builder()
-    w = b._new(11, [256, 8], nb=[110, 110, 880, 880], storage=G.STORE_WEIGHT, index=0)  # q3_K: not taken
+    w = b._new(15, [256, 8], nb=[292, 292, 2336, 2336], storage=G.STORE_WEIGHT, index=0)  # q8_K: no weight type
     x = b.input(N.F32, [256, 1])
     b.expand(b.mul_mat(w, x))
     with pytest.raises(N.TlhError, match="MUL_MAT x1"):

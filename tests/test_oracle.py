@@ -18,7 +18,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from refs import (BF16, F16, F32, NAMES, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, Q8_1, Q8_K, fp16_probe_values,
+from refs import (BF16, F16, F32, NAMES, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, Q8_1, Q8_K,
+                  fp16_probe_values,
                   oracle, ref, row_bytes)
 from tensorlisp_amd import synth
 
@@ -365,6 +366,131 @@ def test_q5_K_matches_reference_live():
         assert same_bits(o.mul_mat(Q5_K, w, M, K, x), y)
         y, _ = r.mul_mat(Q5_K, wq, 8, K, x)
         assert same_bits(o.mul_mat(Q5_K, wq, 8, K, x), y)
+
+
+# ---------------------------------------------------------- q2_K / q3_K
+# tlq_dequantize_row_q2_K / _q3_K (ggml-quants.c:961-989, :1305-1351) and the
+# generic vec_dots (ggml-cpu/quants.c:565-615, :617-694): pinned by the
+# compiled reference's outputs (q2_K.npz, q3_K.npz), bit-exact; an
+# independent numpy unpacking of the codes, scales and mins over whole
+# arrays; float64 brute force; the live reference.
+LOWK = ((Q2_K, "q2_K", 82), (Q3_K, "q3_K", 92))
+
+
+@pytest.mark.parametrize("t,name,xseed", LOWK, ids=[n for _, n, _ in LOWK])
+def test_lowk_golden_dequantize_and_mul_mat(t, name, xseed):
+    o, g = oracle(), gold(name)
+    assert same_bits(o.dequantize(t, g["w"], 256), g["deq"])
+    assert same_bits(o.dequantize(t, g["rand_w"], 1024), g["rand_deq"])
+    from refs import xorshift_noise
+
+    for n in g["ns"]:
+        y = o.mul_mat(t, g["w"], 96, 256, xorshift_noise((int(n), 256), 10 + int(n)))
+        assert same_bits(y, g[f"y{n}"]), n
+    assert same_bits(o.mul_mat(t, g["rand_w"], 40, 1024, synth.normal(xseed, (3, 1024))), g["rand_y"])
+
+
+def lowk_numpy_dequant(t, w):
+    """Element values of q2_K / q3_K super-blocks [nb, bytes] by whole-array
+    numpy, from the block layouts of ggml-common.h:298-323: element 32j + l of
+    half h has its 2-bit code in qs[32h + l] at bit 2j; q2_K: (d * (sc & 15))
+    * code - dmin * (sc >> 4) with sc the byte of its 16-element sub-block;
+    q3_K: (d * (scale - 32)) * (code - 4 * (1 - bit)), bit = hmask[l] >> (4h
+    + j), scale the 6-bit field (low 4 bits from bytes 0..7, high 2 bits from
+    bytes 8..11)."""
+    nb = w.shape[0]
+    e = np.arange(256)
+    h, j, l, s = e // 128, (e % 128) // 32, e % 32, e // 16
+    if t == Q2_K:
+        qs = w[:, 16:80].astype(np.int64)
+        code = (qs[:, 32 * h + l] >> (2 * j)) & 3
+        sc = w[:, s].astype(np.int64)
+        d = w[:, 80:82].copy().view(np.float16).astype(np.float32)
+        dmin = w[:, 82:84].copy().view(np.float16).astype(np.float32)
+        dl = d * (sc & 15).astype(np.float32)
+        ml = dmin * (sc >> 4).astype(np.float32)
+        return (dl * code.astype(np.float32) - ml).astype(np.float32), code
+    hm, qs = w[:, 0:32].astype(np.int64), w[:, 32:96].astype(np.int64)
+    code = ((qs[:, 32 * h + l] >> (2 * j)) & 3) - 4 * (1 - ((hm[:, l] >> (4 * h + j)) & 1))
+    b = w[:, 96:108].astype(np.int64)
+    ss = np.arange(16)
+    low = np.where(ss < 8, b[:, np.minimum(ss, 7)] & 15, b[:, np.maximum(ss - 8, 0)] >> 4)
+    high = (b[:, 8 + ss % 4] >> (2 * (ss // 4))) & 3
+    scale = (low | high << 4) - 32
+    d = w[:, 108:110].copy().view(np.float16).astype(np.float32)
+    dl = d * scale[:, s].astype(np.float32)
+    return (dl * code.astype(np.float32)).astype(np.float32), code
+
+
+@pytest.mark.parametrize("t,name,xseed", LOWK, ids=[n for _, n, _ in LOWK])
+def test_lowk_codes_against_an_independent_unpacking(t, name, xseed):
+    o = oracle()
+    w = synth.random_blocks(t, 190 + t, 6, 512)
+    bb = 84 if t == Q2_K else 110
+    want, code = lowk_numpy_dequant(t, w.reshape(-1, bb))
+    assert (code.min(), code.max()) == ((0, 3) if t == Q2_K else (-4, 3))
+    assert same_bits(o.dequantize(t, w, 512), want.reshape(6, 512))
+    # and on ggml-quantized weights (scales and mins the quantizer chose)
+    g = gold(name)
+    want, _ = lowk_numpy_dequant(t, g["w"].reshape(-1, bb))
+    assert same_bits(g["deq"], want.reshape(g["deq"].shape))
+
+
+@pytest.mark.parametrize("t,name,xseed", LOWK, ids=[n for _, n, _ in LOWK])
+def test_lowk_vec_dot_against_f64_bruteforce(t, name, xseed):
+    o = oracle()
+    K = 2048
+    w = synth.random_blocks(t, 193 + t, 8, K)
+    x = synth.normal(194, (4, K))
+    xq = o.quantize_act(t, x)
+    wd = o.dequantize(t, w, K).astype(np.float64)
+    xd = o.dequantize(Q8_K, xq, K).astype(np.float64)
+    want = wd @ xd.T
+    got = np.array([[o.vec_dot(t, K, w[i], xq[j]) for j in range(4)] for i in range(8)])
+    scale = np.abs(wd).sum(1)[:, None] * np.abs(xd).max()
+    assert np.all(np.abs(got - want) <= 1e-6 * scale)
+
+
+@pytest.mark.skipif(ref() is None, reason="oracle/_ref (compiled reference) not built here")
+@pytest.mark.parametrize("t,name,xseed", LOWK, ids=[n for _, n, _ in LOWK])
+def test_lowk_matches_reference_live(t, name, xseed):
+    o, r = oracle(), ref()
+    M, K = 120, 2048
+    w = synth.random_blocks(t, 195 + t, M, K)
+    assert same_bits(o.dequantize(t, w, K), r.dequantize(t, w, K))
+    wq = r.quantize_weights(t, synth.normal(196, (8, K), 0.02))
+    assert same_bits(o.dequantize(t, wq, K), r.dequantize(t, wq, K))
+    xq = r.quantize_act(t, synth.normal(197, (2, K)))
+    for m in range(8):
+        for n in range(2):
+            assert np.float32(o.vec_dot(t, K, wq[m], xq[n])) == np.float32(r.vec_dot(t, K, wq[m], xq[n]))
+    for n in (1, 2, 9):
+        x = synth.normal(198 + n, (n, K))
+        y, _ = r.mul_mat(t, w, M, K, x)
+        assert same_bits(o.mul_mat(t, w, M, K, x), y)
+        y, _ = r.mul_mat(t, wq, 8, K, x)
+        assert same_bits(o.mul_mat(t, wq, 8, K, x), y)
+
+
+def test_lowk_oracle_catches_planted_mistakes():
+    """The unpacking check above is sensitive to the mistakes a restatement
+    could plausibly make: a swapped nibble, the wrong hmask bit, a dropped
+    min term or a transposed scale index each change the values."""
+    w = synth.random_blocks(Q3_K, 199, 4, 256).reshape(-1, 110)
+    good, _ = lowk_numpy_dequant(Q3_K, w)
+    o = oracle()
+    assert same_bits(o.dequantize(Q3_K, w, 256), good)
+    bad = w.copy()
+    bad[:, 0:32] ^= 0x01  # one hmask bit of every element run 0
+    assert not same_bits(o.dequantize(Q3_K, bad, 256), good)
+    w2 = synth.random_blocks(Q2_K, 199, 4, 256).reshape(-1, 84)
+    good2, code = lowk_numpy_dequant(Q2_K, w2)
+    d = w2[:, 80:82].copy().view(np.float16).astype(np.float32)
+    no_min = (d * (w2[:, np.arange(256) // 16] & 15).astype(np.float32) * code.astype(np.float32)).astype(np.float32)
+    assert not same_bits(no_min, good2)
+    swapped = w2.copy()
+    swapped[:, :16] = ((w2[:, :16] & 15) << 4) | (w2[:, :16] >> 4)  # scale and min nibbles exchanged
+    assert not same_bits(o.dequantize(Q2_K, swapped, 256), good2)
 
 
 # ---------------------------------------------- q4_1 / q5_0 / q5_1 and q8_1
