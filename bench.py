@@ -115,6 +115,7 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
                                                     decode_steps, batch=batch, eager_steps=eager_steps)
     if cpu_steps > 0:
         out["cpu_decode"] = cpu_decode(c, W, cpu_steps)
+        out["cpu_decode_fast"] = cpu_decode(c, W, cpu_steps, fast=True)
     c6 = dataclasses.replace(c, out_type=N.Q6_K)
     W[-1] = gpu_blocks(torch, N.Q6_K, c.n_vocab, c.n_embd, gen)
     out["dense_bs1_q6k_lm_head"] = e2e_decoder_dense(torch, gen, c6, W, stream, copy, prefill_tokens, decode_steps,
@@ -124,12 +125,14 @@ def e2e_decoder(torch, gen, prefill_tokens=512, decode_steps=256, eager_steps=32
     return out
 
 
-def cpu_decode(c, W, steps):
+def cpu_decode(c, W, steps, fast=False):
     """Decode token rate of ggml's CPU backend (oracle/_ref, compiled from the
     reference's sources) on the same model: `steps` single-token greedy steps
     of the dense-cache decode graph at positions 0.. (the CPU backend cannot
     run the paged-attention nodes), each a ggml_graph_compute over the whole
-    8B model, on the threads the GPU box allots this job."""
+    8B model, on the threads the GPU box allots this job. fast: the fastest
+    ISA build of the same sources this host runs (x86-64-v4 / v3, ggml's SIMD
+    paths; labelled, not the parity build)."""
     import dataclasses
 
     import numpy as np
@@ -139,7 +142,7 @@ def cpu_decode(c, W, steps):
 
     from tensorlisp_amd import graph as G
 
-    r = refs.ref()
+    r, isa = refs.ref_fast() if fast else (refs.ref(), None)
     if r is None:
         return None
     threads = cpu_threads()
@@ -160,9 +163,11 @@ def cpu_decode(c, W, steps):
     del hw
     res = {"tokens_per_s": round(steps / total, 2), "ms_per_token": round(total / steps * 1e3, 1), "steps": steps,
            "threads": threads, "kind": "reference",
+           "build": f"-march=x86-64-{isa} (SIMD paths)" if fast else "no -march (the parity build: scalar paths)",
            "sample": f"{steps} single-token greedy decode steps at positions 1..{steps} (after one untimed step), "
                      "dense f16 cache, the same random q4_K weights; ggml_graph_compute wall time per step"}
-    log(f"  cpu decode (ggml CPU backend, {threads} threads): {res['tokens_per_s']} tok/s over {steps} steps")
+    log(f"  cpu decode (ggml CPU backend, {res['build']}, {threads} threads): {res['tokens_per_s']} tok/s "
+        f"over {steps} steps")
     return res
 
 
@@ -453,16 +458,20 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(host_weights, cases, seconds: float):
+def cpu_baseline(host_weights, cases, seconds: float, fast: bool = False):
     """The reference's ggml CPU backend (oracle/_ref) on the same sweep; falls back to
-    our C port of it (oracle/liboracle.so) where the reference was not built."""
+    our C port of it (oracle/liboracle.so) where the reference was not built.
+    fast: the fastest ISA build of the same sources this host runs (None if
+    there is none)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import numpy as np
 
     import refs
 
     threads = cpu_threads()
-    r = refs.ref()
+    r, isa = refs.ref_fast() if fast else (refs.ref(), None)
+    if fast and r is None:
+        return None
     kind = "reference" if r is not None else "port"
     xs = {c: np.random.default_rng(1).standard_normal((c[3], c[2])).astype(np.float32) for c in cases}
     total_bytes, total_s, passes = 0, 0.0, 0
@@ -480,6 +489,8 @@ def cpu_baseline(host_weights, cases, seconds: float):
             total_bytes += algorithmic_bytes(t, M, K, n)
         passes += 1
     return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "build": f"-march=x86-64-{isa} (ggml's SIMD paths; labelled fast build)" if fast
+            else "no -march (the parity build: ggml's scalar _ref/_generic paths, as the reference's cc build)",
             "host": {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "threads_used": threads},
             "sample": f"{passes} pass(es) of the full 20-node sweep (same shapes, N in 1,8), "
                       f"ggml_graph_compute wall time, {threads} threads (the cores the GPU box allots a one-GPU "
@@ -846,6 +857,11 @@ def main() -> int:
         cpu = cpu_baseline(host_w, cases, args.cpu_seconds)
         cpu["decode_8b_q4k"] = e2e.get("cpu_decode")
         log(f"cpu baseline: {cpu['value']:.1f} GB/s ({cpu['kind']}, {cpu['cores']} threads)")
+        fast = cpu_baseline(host_w, cases, args.cpu_seconds, fast=True)
+        if fast is not None:
+            fast["decode_8b_q4k"] = e2e.get("cpu_decode_fast")
+            log(f"cpu baseline, fast build: {fast['value']:.1f} GB/s ({fast['build']})")
+        cpu["fast_build"] = fast
 
     line = {
         "metric": METRIC,

@@ -933,13 +933,7 @@ template <int WT> static tlh_status launch_cols(const MatmulArgs &a, hipStream_t
     const int64_t units = a.K / 256;
     const int64_t slots = kquant<WT>() ? units : 8 * units;
     const size_t lds = (size_t)8 * units * 64 * 8 + (size_t)slots * SK_COLS * 4 + (size_t)GC_WAVES * St::BUF;
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (cus < 1) cus = 1;
-    }
+    const int64_t cus = device_cus();
     const int64_t groups = (a.M + 15) / 16;
     const int64_t wgs = (groups + GC_WAVES - 1) / GC_WAVES;
     hipLaunchKernelGGL(k_gemv_cols<WT>, dim3((unsigned)(wgs < cus ? wgs : cus)), dim3(64 * GC_WAVES), lds, stream, a);
@@ -1001,18 +995,12 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     const size_t slots = (size_t)(kquant<WT>() ? share : 8 * share) * SK_COLS * 4;
     const size_t lds = (size_t)2 * nw * 64 * 16 + slots * (vec_dot_type(WT) == TLH_TYPE_Q8_1 ? 2 : 1) +
                        (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0);
-    static int cached_nw = -1, blocks_per_cu = 1, cus = 0;
-    if (cached_nw != nw) {
-        int dev = 0, nb = 0;
-        (void)hipGetDevice(&dev);
-        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * nw, lds) != hipSuccess || nb < 1) nb = 1;
-        blocks_per_cu = nb;
-        cached_nw = nw;
-    }
+    // per-CU occupancy by wave count (the LDS size follows from it)
+    static std::atomic<int> bpc[SK_MAXW + 1];
+    const int nb = blocks_per_cu(kern, 64 * nw, lds, bpc[nw <= SK_MAXW ? nw : SK_MAXW]);
     const int64_t groups = (a.M + 15) / 16;
     const int64_t batches = a.ne12 * a.ne13;
-    int64_t resident = (int64_t)cus * blocks_per_cu / (batches * chunks > 0 ? batches * chunks : 1);
+    int64_t resident = (int64_t)device_cus() * nb / (batches * chunks > 0 ? batches * chunks : 1);
     if (resident < 1) resident = 1;
     const unsigned gx = (unsigned)(groups < resident ? groups : resident);
     MatmulArgs k = a;

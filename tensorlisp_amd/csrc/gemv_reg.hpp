@@ -1160,16 +1160,10 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     }
 }
 
-// Workgroups of `kern` that the device holds at once (cached per kernel).
-template <typename Kern> static int64_t resident_blocks(Kern kern, int &cache) {
-    if (cache < 0) {
-        int dev = 0, cus = 0, nb = 0;
-        (void)hipGetDevice(&dev);
-        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 256, 0) != hipSuccess || nb < 1) nb = 1;
-        cache = cus * nb;
-    }
-    return cache;
+// Workgroups of `kern` that the current device holds at once (the per-CU
+// count cached per kernel, the CU count per device).
+template <typename Kern> static int64_t resident_blocks(Kern kern, std::atomic<int> &cache) {
+    return (int64_t)device_cus() * blocks_per_cu(kern, 256, 0, cache);
 }
 
 template <int WT, int NC, int R, int IN, bool PIPE, int OUT>
@@ -1193,7 +1187,7 @@ template <int WT, int NC, int R, int IN, int OUT>
 static tlh_status launch_reg_cfg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, const GemvPro &pro,
                                  int ksplit, int upw, hipStream_t stream) {
     constexpr bool GLU = OUT == OUT_GLU;
-    static int slots = -1;
+    static std::atomic<int> slots{0};
     const int groups = 4 / ksplit;
     const int64_t rows_per_block = (int64_t)groups * (GLU ? R / 2 : R);
     const int64_t row_blocks = (a.M + rows_per_block - 1) / rows_per_block;

@@ -1,6 +1,7 @@
 // Internal interface between the C ABI (tlhip.cpp) and the kernel files.
 #pragma once
 
+#include <atomic>
 #include <string>
 
 #include "common.hpp"
@@ -14,6 +15,22 @@ tlh_status set_error(tlh_status s, const char *fmt, ...) __attribute__((format(p
 // the sink, comma-separated: the launch labels of this thread.
 tlh_status check_launch(const char *what);
 void launch_trace(std::string *sink);
+// Compute units of the current device (looked up once per device, thread-safe).
+int device_cus();
+// Workgroups of `kern` (block threads, dynamic LDS bytes) one CU holds at
+// once, looked up once into `cache` (0: not yet; thread-safe).
+template <typename Kern>
+int blocks_per_cu(Kern kern, int threads, size_t lds, std::atomic<int> &cache) {
+    int nb = cache.load(std::memory_order_relaxed);
+    if (nb == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds) != hipSuccess || nb < 1) {
+            (void)hipGetLastError();
+            nb = 1;
+        }
+        cache.store(nb, std::memory_order_relaxed);
+    }
+    return nb;
+}
 
 // rows of x (stride x_row_bytes) -> activation rows row_off.. of an output of
 // total_rows rows, in ggml's block layout or the split scratch layout.

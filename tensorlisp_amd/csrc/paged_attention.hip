@@ -282,6 +282,19 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
         // agent-scope loads. No fence: an L2 write-back per wave, or an
         // invalidate that drops the pages the other workgroups are reading,
         // costs more than the merge saves.
+        //
+        // What this ordering rests on is gfx950's code generation, not the
+        // HIP memory model: the partials, the counter and the read-back are
+        // all relaxed atomics, which the model leaves unordered. It holds
+        // because (1) relaxed agent-scope stores compile to stores that write
+        // through to the device-coherent level (MALL / HBM) rather than stay
+        // in one XCD's L2, (2) s_waitcnt(0) before the barrier makes every
+        // wave's stores complete (acknowledged at that level) before thread 0
+        // increments the counter, and (3) relaxed agent-scope loads bypass
+        // the reading XCD's L2, so the last workgroup sees the partials the
+        // counter accounts for. A target or compiler that cached agent-scope
+        // relaxed stores or loads in a non-coherent L2 would need a release
+        // fence before the increment and an acquire fence after it.
         __shared__ int s_last;
         const int np = min(P, L > 0 ? (L + PART - 1) / PART : 1);  // the partitions that get here
         __builtin_amdgcn_s_waitcnt(0);

@@ -35,6 +35,26 @@ static thread_local std::string *g_trace = nullptr;
 
 void launch_trace(std::string *sink) { g_trace = sink; }
 
+constexpr int kMaxDevices = 64;
+
+int device_cus() {
+    static std::atomic<int> cus[kMaxDevices];  // 0: not looked up yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return 256;  // MI355X
+    }
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 1) {
+            (void)hipGetLastError();
+            c = 1;
+        }
+        cus[dev].store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
+
 tlh_status check_launch(const char *what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(TLH_EXECUTION, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -372,8 +392,11 @@ tlh_status tlh_device_open(int ordinal, tlh_device_props *props) {
     if (n == 0) return set_error(TLH_NO_DEVICE, "no HIP device");
     if (ordinal < 0 || ordinal >= n) return set_error(TLH_NO_DEVICE, "device %d of %d", ordinal, n);
     st = hip_check(hipSetDevice(ordinal), "hipSetDevice");
-    if (st == TLH_OK) st = noalloc_setup_current_device();
-    if (st != TLH_OK || !props) return st;
+    if (st != TLH_OK) return st;
+    // best effort: resolving tlh_mul_mat_noalloc's array here keeps the look-up
+    // out of a later capture; if it fails, that entry point reports it itself
+    if (noalloc_setup_current_device() != TLH_OK) (void)hipGetLastError();
+    if (!props) return TLH_OK;
     hipDeviceProp_t p;
     st = hip_check(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
     if (st != TLH_OK) return st;
@@ -768,7 +791,6 @@ static __device__ __align__(256) uint8_t scratch[TLH_NOALLOC_SCRATCH_BYTES];
 
 namespace tlh {
 
-constexpr int kMaxDevices = 64;
 static std::mutex g_noalloc_mu;
 static void *g_noalloc_ptr[kMaxDevices];
 

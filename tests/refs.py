@@ -728,6 +728,36 @@ def ref():
     return _ref
 
 
+# x86-64 micro-architecture levels of the fast reference builds (oracle/Makefile
+# ref_fast) and the /proc/cpuinfo flags each needs
+ISA_LEVELS = (("v4", ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl", "avx2", "fma", "f16c", "bmi2")),
+              ("v3", ("avx2", "fma", "f16c", "bmi1", "bmi2", "movbe", "abm")))
+_ref_fast = None
+
+
+def ref_fast():
+    """(Ref, level) for the fastest ISA build of the reference this host can
+    run (x86-64-v4, else v3), or (None, None): ggml's SIMD paths, a labelled
+    speed baseline only -- parity is defined by the no -march build."""
+    global _ref_fast
+    if _ref_fast is None:
+        _ref_fast = (None, None)
+        try:
+            flags = set()
+            for ln in Path("/proc/cpuinfo").read_text().splitlines():
+                if ln.startswith("flags"):
+                    flags = set(ln.split(":", 1)[1].split())
+                    break
+        except OSError:
+            flags = set()
+        for level, need in ISA_LEVELS:
+            so = REF_SO.parent / level / REF_SO.name
+            if so.exists() and all(f in flags for f in need):
+                _ref_fast = (Ref(so), level)
+                break
+    return _ref_fast
+
+
 def fp16_probe_values() -> np.ndarray:
     """f32 inputs that pin an f32 -> f16 conversion: every midpoint between adjacent
     finite halves and its two f32 neighbours, a random sample over all exponents,

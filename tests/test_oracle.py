@@ -1016,3 +1016,34 @@ def test_core_oracle_against_the_mathematics():
     np.testing.assert_array_equal(o.core_get_rows(w, Q8_0, ids, I32, k=256), o.dequantize(Q8_0, w, 256)[ids])
     q = rng.standard_normal((2, 3, 4)).astype(np.float32)
     np.testing.assert_array_equal(o.core_cpy(q.transpose(1, 0, 2), F32, (3, 2, 4), F32), q.transpose(1, 0, 2))
+
+
+def test_fast_reference_builds_agree_with_the_parity_build():
+    """The x86-64-v3 / v4 builds of the reference (oracle/Makefile ref_fast,
+    ggml's SIMD paths) that bench.py times as a labelled fast CPU baseline
+    compute the same MUL_MAT as the parity build up to f32 rounding (the
+    north star's 1e-3 relative / 1e-4 absolute), so their speed is the speed
+    of the same work."""
+    from refs import ISA_LEVELS, REF_SO, Ref
+
+    builds = [(lv, REF_SO.parent / lv / REF_SO.name) for lv, _ in ISA_LEVELS]
+    builds = [(lv, p) for lv, p in builds if p.exists()]
+    if ref() is None or not builds:
+        pytest.skip("oracle/_ref ISA builds not built here")
+    flags = ""
+    for ln in Path("/proc/cpuinfo").read_text().splitlines():
+        if ln.startswith("flags"):
+            flags = ln
+            break
+    r = ref()
+    for lv, p in builds:
+        need = dict(ISA_LEVELS)[lv]
+        if not all(f in flags.split() for f in need):
+            continue
+        f = Ref(p)
+        for t in (Q4_0, Q8_0, Q4_K, Q6_K, Q2_K):
+            w = synth.random_blocks(t, 150 + t, 64, 1024)
+            x = synth.normal(151, (3, 1024))
+            want, _ = r.mul_mat(t, w, 64, 1024, x)
+            got, _ = f.mul_mat(t, w, 64, 1024, x)
+            assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want)), (lv, t)
