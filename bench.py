@@ -598,8 +598,13 @@ def run_q6_lm_head(torch, gen, stream):
 
 def run_attention(torch, gen, stream):
     """configs[3] paged-attention decode, and dense FLASH_ATTN_EXT decode and
-    causal prefill."""
+    causal prefill. The inputs come from a generator of their own (seed 3), so
+    `--only attention` (the profiles' command) and the full run draw the same
+    context lengths and pages."""
     from tensorlisp_amd import native as N
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
 
     # paged-attention decode (configs[3]): 32 sequences, 32 q / 8 kv heads, hs 128, 16-token
     # pages scattered over a 65,536-page pool (2 GiB per cache), lens ~ U[512, 8192]
@@ -719,6 +724,7 @@ def main() -> int:
         return 0
     if only == "attention":
         att, fa = run_attention(torch, gen, torch.cuda.current_stream())
+        copy_scale_kernel(torch)
         print(json.dumps({"paged_attention_decode": att, "flash_attn_ext": fa}), flush=True)
         return 0
 
