@@ -807,7 +807,105 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 // in K order.
 constexpr int GC_WAVES = 16;
 
+// Paired blocks (N <= 8). With at most 8 columns, half of a 16 x 16 output is
+// zero columns, yet every output takes the per-block f32 scaling. Instead
+// v_mfma_i32_16x16x64_i8 takes two 32-element blocks (q4_0 / q8_0) or
+// sub-blocks (q4_K / q5_K) 2p and 2p + 1 at once: lane group g carries 16
+// bytes of one block (groups 0, 1: block 2p, elements 16g..; groups 2, 3:
+// block 2p + 1, elements 16 (g - 2)..); the activation operand is block
+// diagonal -- lane (g, i) holds column i & 7's codes where i < 8 matches
+// g < 2, zeros elsewhere -- so output row i < 8 is column i's sum over block
+// 2p and row i >= 8 column i - 8's over block 2p + 1. A lane (g, j) then holds
+// weight row j's sums of columns 4 (g & 1) .. + 3 for one block, every output
+// useful: half the MFMAs and half the scaling per block of the unpaired form.
+// Both parities' partial sums of an output meet once per row group (lanes l
+// and l + 32). Within a parity the blocks are added in K order, so the f32
+// order of the block sums differs from the CPU's sequential loop (even and
+// odd blocks summed apart, then added).
+template <int WT> constexpr bool pair_type() {
+    return WT == TLH_TYPE_Q4_0 || WT == TLH_TYPE_Q8_0 || WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K;
+}
+__device__ __forceinline__ v4i mfma_i8_k64(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// One unit (256 elements) of a paired row group from the wave's staged LDS
+// copy at byte ub (the lane's weight row); A: the unit's four block-pair
+// activation operands; sdu: the unit's activation scales [slot][16 columns].
+// (Tried for q4_0: the nibbles as they are and 8 * the blocks' activation
+// code sums subtracted from the integer sums, which saves the bias trick's
+// three VALU operations per word but adds an LDS read per block: slower.)
 template <int WT>
+__device__ __forceinline__ void unit_mma_pair(const uint8_t *wbuf, uint32_t ub, const v4i (&A)[4], const float *sdu,
+                                              int g, float (&y)[4]) {
+    const int par = g >> 1, half = g & 1;  // block parity, 16-element half of the block
+    const v4i zero = {0, 0, 0, 0};
+    const uint32_t *w32 = (const uint32_t *)wbuf;
+    if constexpr (WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K) {
+        constexpr bool Q5 = WT == TLH_TYPE_Q5_K;
+        const uint4 h = *(const uint4 *)(wbuf + ub);
+        // the 6-bit scales / mins of sub-blocks 0..3 and 4..7 as bytes (get_scale_min_k4)
+        const uint32_t sc[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+        uint4 qh = {0, 0, 0, 0};
+        if constexpr (Q5) qh = *(const uint4 *)(wbuf + ub + 16 + 16 * half);
+        v4i S = zero, Mn = zero;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int s = 2 * p + par;  // this lane's sub-block
+            const uint4 q = *(const uint4 *)(wbuf + ub + (Q5 ? 48 : 16) + 32 * p + 16 * half);
+            const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {qh.x, qh.y, qh.z, qh.w};
+            v4i B;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t c = (qv[i] >> (4 * par)) & 0x0f0f0f0fu;
+                if constexpr (Q5) c |= ((hv[i] >> s) & 0x01010101u) << 4;
+                B[i] = (int)c;
+            }
+            const v4i Sp = mfma_i8_k64(A[p], B, zero);
+            const int scv = (int)__builtin_amdgcn_ubfe(sc[s >> 2], 8 * (s & 3), 8);
+            const uint32_t m4 = __builtin_amdgcn_perm(0u, mn[s >> 2], 0x01010101u * (uint32_t)(s & 3));
+            const v4i Bm = {(int)m4, (int)m4, (int)m4, (int)m4};
+            Mn = mfma_i8_k64(A[p], Bm, Mn);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] += __mul24(scv, Sp[r]);  // |Sp| < 2^16, sc < 64
+        }
+        const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
+        const float4 d8 = *(const float4 *)(sdu + 4 * half);
+        const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
+    } else {
+        constexpr int BB = block_bytes(WT);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t blk = ub + (2 * p + par) * BB;  // the lane's block (2-byte aligned)
+            v4i B;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (WT == TLH_TYPE_Q4_0) {  // low nibbles: elements 0..15, high: 16..31
+                    const uint32_t v = lds_u32(w32, blk + 2 + 4 * i);
+                    B[i] = (int)nib_minus8((v >> (4 * half)) & 0x0f0f0f0fu);
+                } else {
+                    B[i] = (int)lds_u32(w32, blk + 2 + 16 * half + 4 * i);
+                }
+            }
+            const v4i Sb = mfma_i8_k64(A[p], B, zero);
+            const float dw = h2f((uint16_t)lds_u32(w32, blk));
+            const float4 d8 = *(const float4 *)(sdu + (2 * p + par) * SK_COLS + 4 * half);
+            const float d8r[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (WT == TLH_TYPE_Q4_0)
+                    y[r] += ((float)Sb[r] * dw) * d8r[r];  // quants.c:255
+                else
+                    y[r] += (float)Sb[r] * (dw * d8r[r]);  // quants.c:475
+            }
+        }
+    }
+}
+
+template <int WT, bool PAIR>
 __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
     extern __shared__ __attribute__((aligned(16))) char gc_lds[];
     constexpr int AT = vec_dot_type(WT);
@@ -822,20 +920,35 @@ __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
     const int slots = KQ ? units : 8 * units;
     const ActView act = act_view(a.act, AT, K, mm_act_rows(a));
     const int N = (int)a.N;
+    static_assert(!PAIR || pair_type<WT>(), "paired blocks: q4_0, q8_0, q4_K, q5_K");
     long *sA = (long *)gc_lds;                      // [8 * units][64]: block j's A operand of lane l
+    v4i *sA2 = (v4i *)gc_lds;                       // PAIR: [4 * units][64]: block pair p's A operand of lane l
     float *sd = (float *)(sA + (size_t)8 * units * 64);  // [slots][16 columns]
     uint8_t *wbuf = (uint8_t *)(sd + (size_t)slots * SK_COLS) + (size_t)wave * St::BUF;
 
     // A operands (zero past N) and scales of the whole K, once per workgroup
-    for (int idx = threadIdx.x; idx < 8 * units * 64; idx += blockDim.x) {
-        const int j = idx >> 6, l = idx & 63, c = l & 15, gg = l >> 4;
-        long v = 0;
-        if (c < N) {
-            const int8_t *aq = act.qs + (a.n0 + c) * K + 32 * j;
-            if constexpr (nibble_type<WT>()) v = pack2(ldu<uint32_t>(aq + 4 * gg), ldu<uint32_t>(aq + 16 + 4 * gg));
-            else v = ldu<long>(aq + 8 * gg);
+    if constexpr (PAIR) {
+        for (int idx = threadIdx.x; idx < 4 * units * 64; idx += blockDim.x) {
+            const int p = idx >> 6, l = idx & 63, i = l & 15, gg = l >> 4;
+            const int c = i & 7;
+            v4i v = {0, 0, 0, 0};
+            if ((i < 8) == (gg < 2) && c < N) {  // block 2p for rows 0..7, 2p + 1 for rows 8..15
+                const uint4 q = ldu<uint4>(act.qs + (a.n0 + c) * K + 64 * p + 16 * gg);
+                v = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+            }
+            sA2[idx] = v;
         }
-        sA[idx] = v;
+    } else {
+        for (int idx = threadIdx.x; idx < 8 * units * 64; idx += blockDim.x) {
+            const int j = idx >> 6, l = idx & 63, c = l & 15, gg = l >> 4;
+            long v = 0;
+            if (c < N) {
+                const int8_t *aq = act.qs + (a.n0 + c) * K + 32 * j;
+                if constexpr (nibble_type<WT>()) v = pack2(ldu<uint32_t>(aq + 4 * gg), ldu<uint32_t>(aq + 16 + 4 * gg));
+                else v = ldu<long>(aq + 8 * gg);
+            }
+            sA[idx] = v;
+        }
     }
     for (int idx = threadIdx.x; idx < slots * SK_COLS; idx += blockDim.x) {
         const int b = idx >> 4, c = idx & 15;
@@ -877,11 +990,18 @@ __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
             for (int i = 0; i < St::NL; ++i) *(uint4 *)(wbuf + 1024 * i + 16 * lane) = st.v[i];
             const uint32_t dq = st.dq;
             if (u + 1 < units) stage_load(st, grp, u + 1);
+            const uint32_t ub = (uint32_t)(wr * St::RB);
+            const float *sdu = sd + (KQ ? u : 8 * u) * SK_COLS;
+            if constexpr (PAIR) {
+                v4i A2[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) A2[p] = sA2[(4 * u + p) * 64 + lane];
+                unit_mma_pair<WT>(wbuf, ub, A2, sdu, g, y);
+                continue;
+            }
             long A[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) A[j] = sA[(8 * u + j) * 64 + lane];
-            const uint32_t ub = (uint32_t)(wr * St::RB);
-            const float *sdu = sd + (KQ ? u : 8 * u) * SK_COLS;
             if constexpr (WT == TLH_TYPE_Q6_K) {
                 UnitW<WT> w;
                 w.load_lds(wbuf + ub, g);
@@ -908,9 +1028,14 @@ __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
                 }
             }
         }
-        // lane (g, wr): columns 4g + r of row grp * 16 + wr
+        // lane (g, wr): columns 4g + r of row grp * 16 + wr (PAIR: 4 (g & 1) + r,
+        // lanes g < 2 adding the odd blocks' sums of lane l + 32)
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] += __shfl_xor(y[r], 32);
+        }
         const int64_t row = grp * 16 + wr;
-        if (row < a.M) {
+        if (row < a.M && (!PAIR || g < 2)) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int col = 4 * g + r;
@@ -936,7 +1061,14 @@ template <int WT> static tlh_status launch_cols(const MatmulArgs &a, hipStream_t
     const int64_t cus = device_cus();
     const int64_t groups = (a.M + 15) / 16;
     const int64_t wgs = (groups + GC_WAVES - 1) / GC_WAVES;
-    hipLaunchKernelGGL(k_gemv_cols<WT>, dim3((unsigned)(wgs < cus ? wgs : cus)), dim3(64 * GC_WAVES), lds, stream, a);
+    const dim3 grid((unsigned)(wgs < cus ? wgs : cus));
+    if constexpr (pair_type<WT>()) {
+        if (a.N <= 8) {
+            hipLaunchKernelGGL((k_gemv_cols<WT, true>), grid, dim3(64 * GC_WAVES), lds, stream, a);
+            return check_launch("gemv_cols (pairs)");
+        }
+    }
+    hipLaunchKernelGGL((k_gemv_cols<WT, false>), grid, dim3(64 * GC_WAVES), lds, stream, a);
     return check_launch("gemv_cols");
 }
 
