@@ -424,6 +424,55 @@ __device__ __forceinline__ float wave_max(float v) {
 // made visible to the other waves.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Every 64-byte line of the first L * 64 bytes of the kernel arguments, read
+// by scalar loads in one round (one wait). The compiler spreads its own
+// argument loads over the set-up in several rounds, each waiting for the
+// last -- about 700 cycles each when the lines are not in the scalar cache,
+// as after a weight stream has gone through L2 -- and these then hit. The
+// loads and their wait are one statement, so no loaded register is reused
+// while its load is in flight. L must not exceed the explicit arguments.
+template <int L> __device__ __forceinline__ void kernarg_prefetch() {
+    static_assert(L >= 1 && L <= 16, "1 to 16 lines");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    int d[16];
+    if constexpr (L == 1) {
+        asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]) : "s"(kp) : "memory");
+    } else if constexpr (L == 2) {
+        asm volatile("s_load_dword %0, %2, 0x0\n\ts_load_dword %1, %2, 0x40\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]) : "s"(kp) : "memory");
+    } else if constexpr (L == 3) {
+        asm volatile("s_load_dword %0, %3, 0x0\n\ts_load_dword %1, %3, 0x40\n\ts_load_dword %2, %3, 0x80\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]) : "s"(kp) : "memory");
+    } else if constexpr (L == 4) {
+        asm volatile("s_load_dword %0, %4, 0x0\n\ts_load_dword %1, %4, 0x40\n\ts_load_dword %2, %4, 0x80\n\ts_load_dword %3, %4, 0xc0\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]) : "s"(kp) : "memory");
+    } else if constexpr (L == 5) {
+        asm volatile("s_load_dword %0, %5, 0x0\n\ts_load_dword %1, %5, 0x40\n\ts_load_dword %2, %5, 0x80\n\ts_load_dword %3, %5, 0xc0\n\ts_load_dword %4, %5, 0x100\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]) : "s"(kp) : "memory");
+    } else if constexpr (L == 6) {
+        asm volatile("s_load_dword %0, %6, 0x0\n\ts_load_dword %1, %6, 0x40\n\ts_load_dword %2, %6, 0x80\n\ts_load_dword %3, %6, 0xc0\n\ts_load_dword %4, %6, 0x100\n\ts_load_dword %5, %6, 0x140\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]) : "s"(kp) : "memory");
+    } else if constexpr (L == 7) {
+        asm volatile("s_load_dword %0, %7, 0x0\n\ts_load_dword %1, %7, 0x40\n\ts_load_dword %2, %7, 0x80\n\ts_load_dword %3, %7, 0xc0\n\ts_load_dword %4, %7, 0x100\n\ts_load_dword %5, %7, 0x140\n\ts_load_dword %6, %7, 0x180\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]) : "s"(kp) : "memory");
+    } else if constexpr (L == 8) {
+        asm volatile("s_load_dword %0, %8, 0x0\n\ts_load_dword %1, %8, 0x40\n\ts_load_dword %2, %8, 0x80\n\ts_load_dword %3, %8, 0xc0\n\ts_load_dword %4, %8, 0x100\n\ts_load_dword %5, %8, 0x140\n\ts_load_dword %6, %8, 0x180\n\ts_load_dword %7, %8, 0x1c0\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]) : "s"(kp) : "memory");
+    } else if constexpr (L == 9) {
+        asm volatile("s_load_dword %0, %9, 0x0\n\ts_load_dword %1, %9, 0x40\n\ts_load_dword %2, %9, 0x80\n\ts_load_dword %3, %9, 0xc0\n\ts_load_dword %4, %9, 0x100\n\ts_load_dword %5, %9, 0x140\n\ts_load_dword %6, %9, 0x180\n\ts_load_dword %7, %9, 0x1c0\n\ts_load_dword %8, %9, 0x200\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]) : "s"(kp) : "memory");
+    } else if constexpr (L == 10) {
+        asm volatile("s_load_dword %0, %10, 0x0\n\ts_load_dword %1, %10, 0x40\n\ts_load_dword %2, %10, 0x80\n\ts_load_dword %3, %10, 0xc0\n\ts_load_dword %4, %10, 0x100\n\ts_load_dword %5, %10, 0x140\n\ts_load_dword %6, %10, 0x180\n\ts_load_dword %7, %10, 0x1c0\n\ts_load_dword %8, %10, 0x200\n\ts_load_dword %9, %10, 0x240\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]) : "s"(kp) : "memory");
+    } else if constexpr (L == 11) {
+        asm volatile("s_load_dword %0, %11, 0x0\n\ts_load_dword %1, %11, 0x40\n\ts_load_dword %2, %11, 0x80\n\ts_load_dword %3, %11, 0xc0\n\ts_load_dword %4, %11, 0x100\n\ts_load_dword %5, %11, 0x140\n\ts_load_dword %6, %11, 0x180\n\ts_load_dword %7, %11, 0x1c0\n\ts_load_dword %8, %11, 0x200\n\ts_load_dword %9, %11, 0x240\n\ts_load_dword %10, %11, 0x280\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]) : "s"(kp) : "memory");
+    } else if constexpr (L == 12) {
+        asm volatile("s_load_dword %0, %12, 0x0\n\ts_load_dword %1, %12, 0x40\n\ts_load_dword %2, %12, 0x80\n\ts_load_dword %3, %12, 0xc0\n\ts_load_dword %4, %12, 0x100\n\ts_load_dword %5, %12, 0x140\n\ts_load_dword %6, %12, 0x180\n\ts_load_dword %7, %12, 0x1c0\n\ts_load_dword %8, %12, 0x200\n\ts_load_dword %9, %12, 0x240\n\ts_load_dword %10, %12, 0x280\n\ts_load_dword %11, %12, 0x2c0\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]), "=s"(d[11]) : "s"(kp) : "memory");
+    } else if constexpr (L == 13) {
+        asm volatile("s_load_dword %0, %13, 0x0\n\ts_load_dword %1, %13, 0x40\n\ts_load_dword %2, %13, 0x80\n\ts_load_dword %3, %13, 0xc0\n\ts_load_dword %4, %13, 0x100\n\ts_load_dword %5, %13, 0x140\n\ts_load_dword %6, %13, 0x180\n\ts_load_dword %7, %13, 0x1c0\n\ts_load_dword %8, %13, 0x200\n\ts_load_dword %9, %13, 0x240\n\ts_load_dword %10, %13, 0x280\n\ts_load_dword %11, %13, 0x2c0\n\ts_load_dword %12, %13, 0x300\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]), "=s"(d[11]), "=s"(d[12]) : "s"(kp) : "memory");
+    } else if constexpr (L == 14) {
+        asm volatile("s_load_dword %0, %14, 0x0\n\ts_load_dword %1, %14, 0x40\n\ts_load_dword %2, %14, 0x80\n\ts_load_dword %3, %14, 0xc0\n\ts_load_dword %4, %14, 0x100\n\ts_load_dword %5, %14, 0x140\n\ts_load_dword %6, %14, 0x180\n\ts_load_dword %7, %14, 0x1c0\n\ts_load_dword %8, %14, 0x200\n\ts_load_dword %9, %14, 0x240\n\ts_load_dword %10, %14, 0x280\n\ts_load_dword %11, %14, 0x2c0\n\ts_load_dword %12, %14, 0x300\n\ts_load_dword %13, %14, 0x340\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]), "=s"(d[11]), "=s"(d[12]), "=s"(d[13]) : "s"(kp) : "memory");
+    } else if constexpr (L == 15) {
+        asm volatile("s_load_dword %0, %15, 0x0\n\ts_load_dword %1, %15, 0x40\n\ts_load_dword %2, %15, 0x80\n\ts_load_dword %3, %15, 0xc0\n\ts_load_dword %4, %15, 0x100\n\ts_load_dword %5, %15, 0x140\n\ts_load_dword %6, %15, 0x180\n\ts_load_dword %7, %15, 0x1c0\n\ts_load_dword %8, %15, 0x200\n\ts_load_dword %9, %15, 0x240\n\ts_load_dword %10, %15, 0x280\n\ts_load_dword %11, %15, 0x2c0\n\ts_load_dword %12, %15, 0x300\n\ts_load_dword %13, %15, 0x340\n\ts_load_dword %14, %15, 0x380\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]), "=s"(d[11]), "=s"(d[12]), "=s"(d[13]), "=s"(d[14]) : "s"(kp) : "memory");
+    } else if constexpr (L == 16) {
+        asm volatile("s_load_dword %0, %16, 0x0\n\ts_load_dword %1, %16, 0x40\n\ts_load_dword %2, %16, 0x80\n\ts_load_dword %3, %16, 0xc0\n\ts_load_dword %4, %16, 0x100\n\ts_load_dword %5, %16, 0x140\n\ts_load_dword %6, %16, 0x180\n\ts_load_dword %7, %16, 0x1c0\n\ts_load_dword %8, %16, 0x200\n\ts_load_dword %9, %16, 0x240\n\ts_load_dword %10, %16, 0x280\n\ts_load_dword %11, %16, 0x2c0\n\ts_load_dword %12, %16, 0x300\n\ts_load_dword %13, %16, 0x340\n\ts_load_dword %14, %16, 0x380\n\ts_load_dword %15, %16, 0x3c0\n\ts_waitcnt lgkmcnt(0)" : "=s"(d[0]), "=s"(d[1]), "=s"(d[2]), "=s"(d[3]), "=s"(d[4]), "=s"(d[5]), "=s"(d[6]), "=s"(d[7]), "=s"(d[8]), "=s"(d[9]), "=s"(d[10]), "=s"(d[11]), "=s"(d[12]), "=s"(d[13]), "=s"(d[14]), "=s"(d[15]) : "s"(kp) : "memory");
+    }
+    (void)d;
+}
+// Lines of an argument block of `bytes` bytes (the last one starts inside it).
+constexpr int kernarg_lines(size_t bytes) { return (int)((bytes + 63) / 64); }
+
 // Sum over the 256 threads of a workgroup, in an order fixed by the lane and
 // wave layout (so every kernel that uses it adds the same values alike).
 template <typename T> __device__ __forceinline__ T wave_sum_t(T v) {

@@ -99,10 +99,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int wm = wave >> 1, wn = wave & 1;  // wave tile position (2 x 2)
     const int64_t K = a.K;
     const int64_t nsb = K / QKK;
-    const int64_t batches = a.ne12 * a.ne13;
-    const int64_t batch = blockIdx.z % batches, kc = blockIdx.z / batches;  // K chunk kc of gridDim.z / batches
-    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
-    const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
+    const uint32_t batches = (uint32_t)(a.ne12 * a.ne13);
+    // K chunk kc of gridDim.z / batches (one batch slice: no division)
+    const uint32_t kc = batches == 1 ? blockIdx.z : blockIdx.z / batches, batch = blockIdx.z - kc * batches;
+    const MmSlice sl = mm_slice(a, batch);
+    const int64_t i12 = sl.i12, i13 = sl.i13;
+    const uint8_t *W = sl.w;
     const ActView act = act_view(a.act, TLH_TYPE_Q8_K, K, a.N_total * a.ne12 * a.ne13);
     const int64_t m_base = (int64_t)blockIdx.y * GBM;
     const int64_t n_base = (int64_t)blockIdx.x * GBN;

@@ -502,6 +502,7 @@ template <int WT, int KS> struct DirectW {
 
 template <int WT, int KS, bool STAGED>
 __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share) {
+    kernarg_prefetch<kernarg_lines(sizeof(MatmulArgs) + 8)>();
     extern __shared__ __attribute__((aligned(16))) char sk_lds[];
     constexpr int AT = vec_dot_type(WT);
     constexpr bool KQ = kquant<WT>();
@@ -522,8 +523,9 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     const int64_t s_begin = KQ ? u_begin : 8 * u_begin;
     const int64_t s_end = KQ ? u_end : (8 * u_end < nblk ? 8 * u_end : nblk);
     const int64_t batch = blockIdx.z;
-    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
-    const uint8_t *W = a.w + (i12 / a.r2) * a.w_nb2 + (i13 / a.r3) * a.w_nb3;
+    const MmSlice sl = mm_slice(a, blockIdx.z);
+    const int64_t i12 = sl.i12, i13 = sl.i13;
+    const uint8_t *W = sl.w;
     int64_t arow0 = a.n0 + a.N_total * batch;
     bool bad_id = false;  // MUL_MAT_ID: an expert id out of range (outputs NaN, loads stay in bounds)
     if (a.ids) {
@@ -1078,28 +1080,33 @@ template <int WT> constexpr int sk_ks() { return 1; }
 bool gemv_mfma_supported(int64_t N) { return N >= 1 && N <= SK_COLS; }
 
 
-// dst (strided, columns n0..) = sum over the K chunks of the partials, in chunk order
+// dst (strided, columns n0..) = sum over the K chunks of the partials, in
+// chunk order. Grid: (rows / 256, columns, batch slices); columns past the
+// grid's y extent loop.
 __global__ void __launch_bounds__(256) k_gemv_mfma_reduce(const MatmulArgs a, int chunks) {
-    const int64_t batches = a.ne12 * a.ne13;
-    const int64_t per_batch = a.N * a.M;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= per_batch * batches) return;
-    const int64_t batch = i / per_batch, r = i - batch * per_batch;
-    const int64_t n = r / a.M, m = r - n * a.M;
-    float s = 0.0f;
-    for (int c = 0; c < chunks; ++c) s += a.part[(c * batches + batch) * per_batch + r];
-    if (a.nseg > 0) {  // one batch slice; row m of the launch is row m - seg_m0[sg] of segment sg
-        const int sg = (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]);
-        *(float *)((char *)a.seg_dst[sg] + (a.n0 + n) * a.seg_d_nb1[sg] + (m - a.seg_m0[sg]) * 4) = s;
-        return;
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (m >= a.M) return;
+    const int64_t batches = a.ne12 * a.ne13, batch = blockIdx.z;
+    const int64_t per_batch = a.N * a.M, cstride = batches * per_batch;
+    const MmSlice sl = mm_slice(a, blockIdx.z);
+    int sg = 0;
+    if (a.nseg > 0) sg = (int)(m >= a.seg_m0[1]) + (int)(a.nseg > 2 && m >= a.seg_m0[2]);
+    for (int64_t n = blockIdx.y; n < a.N; n += gridDim.y) {
+        const float *p = a.part + batch * per_batch + n * a.M + m;
+        float s = 0.0f;
+        for (int c = 0; c < chunks; ++c) s += p[c * cstride];
+        if (a.nseg > 0)  // one batch slice; row m of the launch is row m - seg_m0[sg] of segment sg
+            *(float *)((char *)a.seg_dst[sg] + (a.n0 + n) * a.seg_d_nb1[sg] + (m - a.seg_m0[sg]) * 4) = s;
+        else
+            *(float *)((char *)a.dst + sl.i12 * a.d_nb2 + sl.i13 * a.d_nb3 + (a.n0 + n) * a.d_nb1 + m * 4) = s;
     }
-    const int64_t i12 = batch % a.ne12, i13 = batch / a.ne12;
-    *(float *)((char *)a.dst + i12 * a.d_nb2 + i13 * a.d_nb3 + (a.n0 + n) * a.d_nb1 + m * 4) = s;
 }
 
 tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t stream) {
-    const int64_t total = a.N * a.M * a.ne12 * a.ne13;
-    hipLaunchKernelGGL(k_gemv_mfma_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, chunks);
+    const int64_t batches = a.ne12 * a.ne13;
+    if (a.M <= 0 || a.N <= 0 || batches <= 0) return TLH_OK;
+    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)(a.N < 65535 ? a.N : 65535), (unsigned)batches);
+    hipLaunchKernelGGL(k_gemv_mfma_reduce, grid, dim3(256), 0, stream, a, chunks);
     return check_launch("partial_reduce");
 }
 
@@ -1140,9 +1147,7 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share);
     tlh_status st = check_launch("gemv_mfma");
     if (st != TLH_OK || chunks == 1) return st;
-    const int64_t total = a.N * a.M * batches;
-    hipLaunchKernelGGL(k_gemv_mfma_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, (int)chunks);
-    return check_launch("gemv_mfma_reduce");
+    return launch_partial_reduce(a, (int)chunks, stream);
 }
 
 template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool staged, hipStream_t stream) {

@@ -833,8 +833,9 @@ __global__ void __launch_bounds__(256) k_gemv_reg(const MatmulArgs a, const floa
     const int64_t u = (int64_t)kw * upw + lane;
     const bool uvalid = lane < upw && u < units;
     const uint32_t batch = blockIdx.z;
-    const uint32_t i13 = batch / (uint32_t)a.ne12, i12 = batch - i13 * (uint32_t)a.ne12;
-    const uint8_t *W = a.w + (int64_t)(i12 / (uint32_t)a.r2) * a.w_nb2 + (int64_t)(i13 / (uint32_t)a.r3) * a.w_nb3;
+    const MmSlice sl = mm_slice(a, batch);
+    const uint32_t i12 = (uint32_t)sl.i12, i13 = (uint32_t)sl.i13;
+    const uint8_t *W = sl.w;
     const int64_t arow0 = a.n0 + a.N_total * batch;
     // output rows a workgroup covers per step (GLU: rows of h, R / 2 per wave)
     constexpr int RO = GLU ? R / 2 : R;

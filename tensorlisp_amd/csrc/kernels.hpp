@@ -78,6 +78,26 @@ struct MatmulArgs {
     int64_t ids_nb0, ids_nb1, id_b1, id_nas;
 };
 
+// Batch slice z of a MUL_MAT launch: i12 = z % ne12, i13 = z / ne12 and the
+// weight matrix it reads (broadcast by r2 / r3). Slice 0 -- the only one of a
+// single-matrix MUL_MAT -- skips the integer divisions: they are a few hundred
+// scalar instructions that every wave of the launch would otherwise issue
+// before its first weight load. The counts fit 32 bits (grid z is below 2^16).
+struct MmSlice {
+    int64_t i12, i13;
+    const uint8_t *w;
+};
+__device__ __forceinline__ MmSlice mm_slice(const MatmulArgs &a, uint32_t z) {
+    MmSlice s{0, 0, a.w};
+    if (z != 0) {
+        const uint32_t ne12 = (uint32_t)a.ne12, i13 = z / ne12, i12 = z - i13 * ne12;
+        s.i12 = i12;
+        s.i13 = i13;
+        s.w = a.w + (int64_t)(i12 / (uint32_t)a.r2) * a.w_nb2 + (int64_t)(i13 / (uint32_t)a.r3) * a.w_nb3;
+    }
+    return s;
+}
+
 // Rows of quantized activations a launch's scratch holds.
 __host__ __device__ inline int64_t mm_act_rows(const MatmulArgs &a) {
     return a.ids ? a.id_b1 * a.ne13 : a.N_total * a.ne12 * a.ne13;

@@ -97,8 +97,12 @@ __global__ void __launch_bounds__(256) k_mm_float(const FloatMM f) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t batch = blockIdx.z;
-    const int64_t i12 = batch % f.ne12, i13 = batch / f.ne12;
-    const char *W = f.w + (i12 / f.r2) * f.w_nb2 + (i13 / f.r3) * f.w_nb3;
+    int64_t i12 = 0, i13 = 0;  // batch slice 0 skips the divisions
+    const char *W = f.w;
+    if (batch != 0) {
+        i12 = batch % f.ne12, i13 = batch / f.ne12;
+        W += (i12 / f.r2) * f.w_nb2 + (i13 / f.r3) * f.w_nb3;
+    }
     const char *X = f.x + i12 * f.x_nb2 + i13 * f.x_nb3;
     const int64_t m0 = (int64_t)blockIdx.x * (4 * MMF_ROWS) + wave * MMF_ROWS;
     const int64_t n0 = (int64_t)blockIdx.y * MMF_COLS;
