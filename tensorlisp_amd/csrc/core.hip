@@ -317,6 +317,7 @@ struct GluQuantArgs {
 
 template <bool VEC>
 __global__ void __launch_bounds__(256) k_glu_quantize(const GluQuantArgs a) {
+    kernarg_prefetch<(kernarg_lines(sizeof(GluQuantArgs)))>();
     const tlh_tensor &x = a.c.op.t[0], &y = a.c.op.t[1], &d = a.c.op.t[4];
     const int code = (int)a.c.op.x[0];
     const bool swapped = a.c.op.x[1] != 0;
@@ -852,6 +853,7 @@ struct MultiArgs {
 };
 
 __global__ void __launch_bounds__(256) k_core_multi(const MultiArgs m) {
+    kernarg_prefetch<(kernarg_lines(sizeof(MultiArgs)) > 16 ? 16 : kernarg_lines(sizeof(MultiArgs)))>();
     const int64_t b = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
     int k = 0;
     while (k + 1 < m.n && b >= m.start[k + 1]) ++k;
@@ -934,6 +936,7 @@ constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows
 // element i of a row multiplies w[i].
 template <bool VEC>  // VEC: every row 16-byte aligned with n % 4 == 0, groups move as float4
 __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
+    kernarg_prefetch<(kernarg_lines(sizeof(NormChainArgs)))>();
     __shared__ double shd[4];
     const tlh_tensor &tp = a.op.t[0], &tq = a.op.t[1], &tw = a.op.t[2], &ts = a.op.t[3], &ty = a.op.t[4];
     const bool rms = a.op.x[0] != 0, add = a.op.x[2] != 0;

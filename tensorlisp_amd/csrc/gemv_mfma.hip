@@ -909,6 +909,7 @@ __device__ __forceinline__ void unit_mma_pair(const uint8_t *wbuf, uint32_t ub, 
 
 template <int WT, bool PAIR>
 __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
+    kernarg_prefetch<(kernarg_lines(sizeof(MatmulArgs)))>();
     extern __shared__ __attribute__((aligned(16))) char gc_lds[];
     constexpr int AT = vec_dot_type(WT);
     constexpr bool KQ = kquant<WT>();
@@ -1084,6 +1085,7 @@ bool gemv_mfma_supported(int64_t N) { return N >= 1 && N <= SK_COLS; }
 // chunk order. Grid: (rows / 256, columns, batch slices); columns past the
 // grid's y extent loop.
 __global__ void __launch_bounds__(256) k_gemv_mfma_reduce(const MatmulArgs a, int chunks) {
+    kernarg_prefetch<(kernarg_lines(sizeof(MatmulArgs)))>();
     const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (m >= a.M) return;
     const int64_t batches = a.ne12 * a.ne13, batch = blockIdx.z;
