@@ -72,6 +72,8 @@ struct Dispatch {
     // activation rows, f16 codes) into that MUL_MAT's scratch block
     int nq_type = 0, nq_f16 = 0;
     int64_t nq_rows = 0;
+    tlh_op nq_op;          // that MUL_MAT (its quantize launch, if the fused form is refused)
+    size_t pa_own = 0;     // D_PAGED_ATTN with nq_type: its own scratch's offset in the shared block
     int32_t pw[4] = {0, 0, 0, 0};
     int64_t pw_blocks = 0;  // D_PAGED_WRITE: blocks in the smaller pool (slots past it are dropped)
     int pw_f32[2] = {0, 0};  // D_PAGED_WRITE: key / value read as f32 (a fused cast)
@@ -1302,9 +1304,11 @@ class Lowering {
     }
 
     // A MUL_MAT of 3 or more columns whose activation is a GLU's output (the
-    // SwiGLU before the down projection), or a norm chain's output over at
-    // least NQ_MIN_ROWS rows (the RMS_NORM before Q / K / V and gate / up in a
-    // prefill): that launch also writes the quantized rows (the bytes the
+    // SwiGLU before the down projection), a norm chain's output over at least
+    // NQ_MIN_ROWS rows (the RMS_NORM before Q / K / V and gate / up in a
+    // prefill) or the one-launch paged attention's f32 output (the output
+    // projection of a batched decode step, the merge quantizing whole q8_K
+    // blocks of heads): that launch also writes the quantized rows (the bytes the
     // quantize launch would write) into the MUL_MAT's scratch, and the MUL_MAT
     // keeps only its compute launch; a quantization group's leader quantize
     // goes the same way. Needs: src1 is the producer's whole output,
@@ -1327,7 +1331,7 @@ class Lowering {
             if (!leader && !single) continue;
             const tlh_tensor &b = q.op.t[1];
             const int wt = q.op.t[0].ty;
-            if (wt == TLH_TYPE_F32 || wt == TLH_TYPE_F16 || wt == TLH_TYPE_BF16 || b.ne[1] < 3) continue;
+            if (wt == TLH_TYPE_F32 || wt == TLH_TYPE_F16 || wt == TLH_TYPE_BF16) continue;
             const int at = vec_dot_type(wt);
             const int64_t K = b.ne[0], rows = b.ne[1] * b.ne[2] * b.ne[3];
             if (!contiguous_f32(b) || rows == 0) continue;
@@ -1337,7 +1341,8 @@ class Lowering {
             for (int j = (int)i - 1; j >= 0; --j) {
                 if (gone[j]) continue;
                 const Dispatch &c = d[j];
-                if (((c.kind == D_CORE && c.core_kind == TLH_CORE_GLU) || c.kind == D_NORM_CHAIN) &&
+                if (((c.kind == D_CORE && c.core_kind == TLH_CORE_GLU) || c.kind == D_NORM_CHAIN ||
+                     (c.kind == D_PAGED_ATTN && c.pa_f32)) &&
                     same_place(c.dst, q.src[1])) {
                     gi = j;
                     break;
@@ -1349,12 +1354,26 @@ class Lowering {
             }
             if (gi < 0) continue;
             Dispatch &g = d[gi];
-            const tlh_tensor &y = g.op.t[4];
-            if (g.block != -1 || !contiguous_f32(y) || y.ne[0] != K || y.ne[1] * y.ne[2] * y.ne[3] != rows)
-                continue;
-            if (g.kind == D_NORM_CHAIN ? rows < NQ_MIN_ROWS || !norm_chain_quantize_ok(g.op, at)
-                                       : !glu_quantize_ok(g.op, at))
-                continue;
+            // paged attention (one launch, f32 output): its merge quantizes the
+            // heads it holds. Like the others only for 3 or more columns: below
+            // that the MUL_MAT quantizes in its own launch, which costs less
+            // than the merge's extra work (bs 1 decode: 1.85 -> 1.90 ms a step)
+            const bool pa = g.kind == D_PAGED_ATTN;
+            if (b.ne[1] < 3) continue;
+            if (pa) {
+                const int64_t per = (int64_t)g.pa.num_heads * g.pa.head_size;
+                if (g.block != -1 || K != per || rows != g.pa.num_seqs || !contiguous_f32(b) ||
+                    act_has_f16(wt, b.ne[1]) || !paged_attention_quantize_ok(g.pa, at))
+                    continue;
+            } else {
+                const tlh_tensor &y = g.op.t[4];
+                if (g.block != -1 || !contiguous_f32(y) || y.ne[0] != K ||
+                    y.ne[1] * y.ne[2] * y.ne[3] != rows)
+                    continue;
+                if (g.kind == D_NORM_CHAIN ? rows < NQ_MIN_ROWS || !norm_chain_quantize_ok(g.op, at)
+                                           : !glu_quantize_ok(g.op, at))
+                    continue;
+            }
             if (single) {  // a group of one: its scratch block spans GLU .. MUL_MAT
                 Group gr;
                 gr.first = q.pos;
@@ -1370,9 +1389,16 @@ class Lowering {
             g.nq_type = at;
             g.nq_rows = rows;
             g.nq_f16 = act_has_f16(wt, b.ne[1]);
+            g.nq_op = q.op;
             g.block = q.block;
-            g.scratch_bytes = q.scratch_bytes;
             Group &gr = groups_[-2 - q.block];
+            if (pa) {  // the block holds the MUL_MAT's scratch, then the attention's own
+                g.pa_own = (size_t)align_up((int64_t)q.scratch_bytes);
+                g.scratch_bytes = g.pa_own + g.scratch_bytes;
+                gr.bytes = std::max(gr.bytes, g.scratch_bytes);
+            } else {
+                g.scratch_bytes = q.scratch_bytes;
+            }
             gr.first = std::min<int64_t>(gr.first, g.pos);
         }
         std::vector<Dispatch> out;
@@ -1630,9 +1656,23 @@ struct tlh_program {
                 a.block_tables = (const int32_t *)src[3];
                 a.context_lens = (const int32_t *)src[4];
                 if (x.pa_f32) a.out = nullptr;
-                st = a.num_seqs == 0 ? TLH_OK
-                                     : launch_paged_attention(a, scratch, x.scratch_bytes, s,
-                                                              x.pa_f32 ? (float *)dst : nullptr, counters);
+                if (a.num_seqs == 0) break;
+                if (x.nq_type) {  // and the next MUL_MAT's quantized activation, at the block's start
+                    ActQuantOut qo;
+                    qo.out = scratch;
+                    qo.type = x.nq_type;
+                    qo.rows = x.nq_rows;
+                    qo.f16 = x.nq_f16 != 0;
+                    char *own = (char *)scratch + x.pa_own;
+                    st = launch_paged_attention(a, own, x.scratch_bytes - x.pa_own, s, (float *)dst, counters, &qo);
+                    if (st == TLH_UNSUPPORTED) {
+                        st = launch_paged_attention(a, own, x.scratch_bytes - x.pa_own, s, (float *)dst, counters);
+                        if (st == TLH_OK) st = tlh_mul_mat_quantize(&x.nq_op, dst, scratch, x.pa_own, s);
+                    }
+                    break;
+                }
+                st = launch_paged_attention(a, scratch, x.scratch_bytes, s, x.pa_f32 ? (float *)dst : nullptr,
+                                            counters);
                 break;
             }
             case D_MM_COMPUTE_MULTI: {

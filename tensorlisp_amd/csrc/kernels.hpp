@@ -282,8 +282,15 @@ tlh_status launch_core(int kind, const tlh_op &op, const void *s0, const void *s
 // a.out. counters != null: one launch that merges the partitions itself, on
 // paged_attention_counters(a) zeroed counters it leaves zeroed (launches that
 // share them must be stream-ordered); else a second launch merges them.
+// qo (one-launch form, paged_attention_quantize_ok): the merging workgroup
+// also quantizes its heads' outputs (as f32, whole q8_K blocks) into qo's
+// split-layout scratch, activation row = sequence, K = heads x head size --
+// the bytes the next MUL_MAT's quantize launch would write.
+struct ActQuantOut;
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t scratch_bytes,
-                                  hipStream_t stream, float *out32 = nullptr, unsigned *counters = nullptr);
+                                  hipStream_t stream, float *out32 = nullptr, unsigned *counters = nullptr,
+                                  const ActQuantOut *qo = nullptr);
+bool paged_attention_quantize_ok(const tlh_paged_attention_args &a, int act_type);
 size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a);
 size_t paged_attention_counters(const tlh_paged_attention_args &a);
 // key_f32 / value_f32: that source is f32 and is rounded to f16 on the way

@@ -111,7 +111,8 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
                                                     const int32_t *__restrict__ lens, int num_heads, int num_kv_heads,
                                                     int gc, int max_blocks, float scale, int P,
                                                     float *__restrict__ scratch, unsigned *__restrict__ counters,
-                                                    uint16_t *__restrict__ out, float *__restrict__ out32) {
+                                                    uint16_t *__restrict__ out, float *__restrict__ out32,
+                                                    void *__restrict__ qout, int64_t qrows) {
     constexpr int KS = HS / 16;  // QK steps = PV output tiles
     __shared__ int s_bt[PART / 8];
     __shared__ float s_m[PA_WAVES][16], s_l[PA_WAVES][16];
@@ -307,6 +308,9 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
         }
         __syncthreads();
         if (!s_last) return;
+        // with qout, the merged values also go to LDS (the partial sums' buffer
+        // is free by now) for the quantization below
+        float *sq = &s_acc[0][0][0];
         for (int e = threadIdx.x; e < gc * HS; e += blockDim.x) {
             const int h = e / HS, d = e % HS;
             const uint16_t r = merge_parts<HS, true>(
@@ -314,6 +318,27 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
             const int64_t o = ((int64_t)seq * num_heads + head0 + h) * HS + d;
             if (out32) out32[o] = h2f(r);
             else out[o] = r;
+            if (qout) sq[e] = h2f(r);
+        }
+        if (qout) {
+            // the heads' outputs are whole q8_K blocks of the sequence's row
+            // (the launcher's check): one wave per block, four consecutive
+            // values a lane, as the quantize launch takes them
+            __syncthreads();
+            const int64_t K = (int64_t)num_heads * HS;
+            const ActLayout QL = act_layout(TLH_TYPE_Q8_K, K, qrows, false);
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            for (int b = wave; b < gc * HS / QKK; b += PA_WAVES) {
+                float v[1][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[0][i] = sq[QKK * b + 4 * lane + i];
+                uint32_t packed[1];
+                int psum[1];
+                float dq[1];
+                q8K_waves<1>(v, lane, packed, psum, dq);
+                q8K_store_split((char *)qout, QL, K, seq, (int64_t)head0 * HS / QKK + b, lane, packed[0], psum[0],
+                                dq[0], false);
+            }
         }
     }
 }
@@ -369,9 +394,22 @@ size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
     return (size_t)(bytes(PA_PART / 2) + std::min(bytes(PA_PART_SMALL), bound));
 }
 
+// query heads per workgroup: a divisor of the group size, at most 16
+static int pa_gc(const tlh_paged_attention_args &a) {
+    const int G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
+    int gc = G < 16 ? G : 16;
+    while (gc > 1 && G % gc) --gc;
+    return gc > 0 ? gc : 1;
+}
+
+bool paged_attention_quantize_ok(const tlh_paged_attention_args &a, int act_type) {
+    return act_type == TLH_TYPE_Q8_K && ((int64_t)pa_gc(a) * a.head_size) % QKK == 0 &&
+           ((int64_t)a.num_heads * a.head_size) % QKK == 0;
+}
+
 template <int HS, int BS, int PART>
 static void launch_pa3(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
-                       unsigned *counters) {
+                       unsigned *counters, const ActQuantOut *qo) {
     const int P = pa_partitions(a);
     const int G = a.num_heads / a.num_kv_heads;
     int gc = G < 16 ? G : 16;  // query heads per workgroup: a divisor of G, at most 16
@@ -383,34 +421,34 @@ static void launch_pa3(const tlh_paged_attention_args &a, float *scratch, hipStr
         hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PART, true>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
                            (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
                            a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch, counters,
-                           (uint16_t *)a.out, out32);
+                           (uint16_t *)a.out, out32, qo ? qo->out : nullptr, qo ? qo->rows : (int64_t)0);
         return;
     }
     hipLaunchKernelGGL((k_paged_attn<HS, BS, PIPE, PART, false>), grid, dim3(256), 0, stream, (const uint16_t *)a.q,
                        (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables, a.context_lens,
                        a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, P, scratch, nullptr, nullptr,
-                       nullptr);
+                       nullptr, nullptr, (int64_t)0);
     hipLaunchKernelGGL((k_paged_attn_reduce<HS, PART>), rgrid, rblock, 0, stream, (uint16_t *)a.out, out32,
                        (const float *)scratch, a.context_lens, a.num_heads, P);
 }
 
 template <int HS, int BS>
 static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
-                       unsigned *counters) {
+                       unsigned *counters, const ActQuantOut *qo) {
     switch (pa_part(a)) {
-    case PA_PART: launch_pa3<HS, BS, PA_PART>(a, scratch, stream, out32, counters); break;
-    case PA_PART / 2: launch_pa3<HS, BS, PA_PART / 2>(a, scratch, stream, out32, counters); break;
-    default: launch_pa3<HS, BS, PA_PART_SMALL>(a, scratch, stream, out32, counters); break;
+    case PA_PART: launch_pa3<HS, BS, PA_PART>(a, scratch, stream, out32, counters, qo); break;
+    case PA_PART / 2: launch_pa3<HS, BS, PA_PART / 2>(a, scratch, stream, out32, counters, qo); break;
+    default: launch_pa3<HS, BS, PA_PART_SMALL>(a, scratch, stream, out32, counters, qo); break;
     }
 }
 
 template <int HS>
 static void launch_pa1(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
-                       unsigned *counters) {
+                       unsigned *counters, const ActQuantOut *qo) {
     switch (a.block_size) {
-    case 8: launch_pa2<HS, 8>(a, scratch, stream, out32, counters); break;
-    case 16: launch_pa2<HS, 16>(a, scratch, stream, out32, counters); break;
-    default: launch_pa2<HS, 32>(a, scratch, stream, out32, counters); break;
+    case 8: launch_pa2<HS, 8>(a, scratch, stream, out32, counters, qo); break;
+    case 16: launch_pa2<HS, 16>(a, scratch, stream, out32, counters, qo); break;
+    default: launch_pa2<HS, 32>(a, scratch, stream, out32, counters, qo); break;
     }
 }
 
@@ -424,16 +462,20 @@ size_t paged_attention_counters(const tlh_paged_attention_args &a) {
 }
 
 tlh_status launch_paged_attention(const tlh_paged_attention_args &a, void *scratch, size_t, hipStream_t stream,
-                                  float *out32, unsigned *counters) {
+                                  float *out32, unsigned *counters, const ActQuantOut *qo) {
     float *s = (float *)scratch;
+    if (qo && (!counters || !qo->out || !paged_attention_quantize_ok(a, qo->type) || qo->f16 ||
+               qo->rows < a.num_seqs))
+        return set_error(TLH_UNSUPPORTED, "paged_attention: the merge quantizes whole q8_K blocks of heads, "
+                                          "one launch, no f16 codes");
     switch (a.head_size) {
-    case 64: launch_pa1<64>(a, s, stream, out32, counters); break;
-    case 80: launch_pa1<80>(a, s, stream, out32, counters); break;
-    case 96: launch_pa1<96>(a, s, stream, out32, counters); break;
-    case 112: launch_pa1<112>(a, s, stream, out32, counters); break;
-    case 128: launch_pa1<128>(a, s, stream, out32, counters); break;
-    case 192: launch_pa1<192>(a, s, stream, out32, counters); break;
-    case 256: launch_pa1<256>(a, s, stream, out32, counters); break;
+    case 64: launch_pa1<64>(a, s, stream, out32, counters, qo); break;
+    case 80: launch_pa1<80>(a, s, stream, out32, counters, qo); break;
+    case 96: launch_pa1<96>(a, s, stream, out32, counters, qo); break;
+    case 112: launch_pa1<112>(a, s, stream, out32, counters, qo); break;
+    case 128: launch_pa1<128>(a, s, stream, out32, counters, qo); break;
+    case 192: launch_pa1<192>(a, s, stream, out32, counters, qo); break;
+    case 256: launch_pa1<256>(a, s, stream, out32, counters, qo); break;
     default: return set_error(TLH_INVALID, "paged_attention: head_size %d", a.head_size);
     }
     return check_launch("paged_attention");

@@ -282,6 +282,31 @@ def to_pool(dense_rows, table, kvh, hd, bs, kpool, vpool):
         vpool[b, :, :, o] = v[p].reshape(kvh, hd)
 
 
+def test_8b_slice_batch16_attention_merge_quantizes_for_the_output_projection(gpu, slice8b):
+    """At 16 sequences the one-launch paged attention's merge writes the output
+    projection's q8_K activation (4 query heads x 128 = two whole blocks per
+    workgroup), so that MUL_MAT launches no quantize of its own; the numbers
+    are covered by the batch-16 test above, which runs the same program."""
+    c, wd = slice8b
+    pc = G.PagedConfig(block_size=16, n_blocks=48, max_blocks=4)
+    dec = Paged(c, pc, wd)
+    st = G.decoder_decode_paged(c, pc, 16)
+    prog = G.Program(st.builder, st.keep, dec.w, dec.offs)
+    tables = np.arange(32, dtype=np.int32).reshape(16, 2)
+    tab = np.zeros((16, pc.max_blocks), np.int32)
+    tab[:, :2] = tables
+    pos = np.zeros(16, np.int32)
+    slots = np.concatenate([G.paged_slots(t, [0], pc.block_size) for t in tables])
+    for i, a in enumerate([np.zeros(16, np.int32), pos, slots, tab, pos + 1]):
+        prog.write_input(i, dev(a))
+    trace = prog.trace(dec.state)
+    att = [i for i, (_, labels) in enumerate(trace) if "paged_attention" in labels]
+    assert len(att) == c.n_layer, trace
+    for i in att:
+        nxt = next(j for j in range(i + 1, len(trace)) if trace[j][0] == "MUL_MAT")
+        assert "quantize_act" not in trace[nxt][1], (i, trace[nxt])
+
+
 def test_8b_full_32_layers_graph_and_paged_properties(gpu):
     """The whole 32-layer configs[4] model (weights drawn on the GPU, no CPU run
     at this size). A hipGraph replay of a decode step equals the eager launches
