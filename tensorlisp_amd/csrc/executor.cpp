@@ -214,10 +214,11 @@ class Lowering {
         fuse_rope_cast(out.d);
         fuse_paged_cast(out.d);
         fuse_cache_write_cast(out.d);
-        fuse_gemv_epilogue(out.d);
-        group_elementwise(out.d);
+        fuse_gemv_epilogue(out.d, false);
         group_mul_mats(out.d);
         merge_mm_computes(out.d);
+        fuse_gemv_epilogue(out.d, true);  // the batched Q / K / V projection's merged compute
+        group_elementwise(out.d);
         fuse_act_quantize(out.d);
         group_elementwise(out.d);  // merged computes can leave element-wise launches adjacent
         plan(out);
@@ -953,7 +954,11 @@ class Lowering {
     // The member's f32 output is then not written. An absorbed dispatch moves
     // up to the GEMV's position, so nothing between may read what it writes
     // or write what it reads.
-    void fuse_gemv_epilogue(std::vector<Dispatch> &d) {
+    // batched: the same for the merged compute of a few-column projection
+    // (D_MM_COMPUTE_MULTI, 3..16 columns = tokens, K <= 4096, q4_K / q5_K /
+    // q6_K: the int8-MFMA kernel's store epilogue, token n in column n), for
+    // the rotated / cast outputs and paged K / V writes (not cache rows).
+    void fuse_gemv_epilogue(std::vector<Dispatch> &d, bool batched) {
         count_readers();
         std::vector<char> gone(d.size(), 0);
         auto kept = [&](int32_t id) { return std::find(g_.keep.begin(), g_.keep.end(), id) != g_.keep.end(); };
@@ -976,9 +981,17 @@ class Lowering {
         auto idx_ty = [](const tlh_tensor &t) { return t.ty == TLH_TYPE_I32 || t.ty == 27 /* i64 */; };
         for (size_t i = 0; i < d.size(); ++i) {
             Dispatch &f = d[i];
-            if (gone[i] || !(f.kind == D_MULTI_GEMV || (f.kind == D_GEMV_PRO && !f.has_glu && !f.has_epi))) continue;
+            if (gone[i]) continue;
+            if (batched ? !(f.kind == D_MM_COMPUTE_MULTI && !f.has_epi)
+                        : !(f.kind == D_MULTI_GEMV || (f.kind == D_GEMV_PRO && !f.has_glu && !f.has_epi)))
+                continue;
             const tlh_tensor &b = f.mop[0].t[1];
-            if (b.ne[0] > 4096 || b.ne[1] != 1 || b.ne[2] != 1 || b.ne[3] != 1) continue;
+            const int wty = f.mop[0].t[0].ty;
+            if (batched && (b.ne[1] < 3 || b.ne[1] > 16 ||
+                            (wty != TLH_TYPE_Q4_K && wty != TLH_TYPE_Q5_K && wty != TLH_TYPE_Q6_K)))
+                continue;
+            const int64_t T = batched ? b.ne[1] : 1;  // tokens = columns
+            if (b.ne[0] > 4096 || b.ne[1] != T || b.ne[2] != 1 || b.ne[3] != 1) continue;
             GemvEpi e;
             Place edst[3], eidx[3], epos, eff;
             std::vector<size_t> take[3];  // absorbed dispatch indices per member
@@ -999,9 +1012,9 @@ class Lowering {
                 if (c.scratch_bytes != 0) continue;
                 if (is_core(c, TLH_CORE_ROPE) && same_place(c.src[0], P)) {
                     const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
-                    bool ok = c.op.x[1] == 0 && x.ty == TLH_TYPE_F32 && contiguous(x) && x.ne[2] == 1 &&
-                              x.ne[3] == 1 && x.ne[0] * x.ne[1] == M && c.op.t[1].ne[0] >= 1 &&
-                              c.op.t[1].ty == TLH_TYPE_I32;
+                    bool ok = c.op.x[1] == 0 && x.ty == TLH_TYPE_F32 && contiguous(x) && x.ne[2] == T &&
+                              x.ne[3] == 1 && x.ne[0] * x.ne[1] == M && c.op.t[1].ne[0] >= T &&
+                              c.op.t[1].ty == TLH_TYPE_I32 && !(batched && c.op.x[9]);
                     if (ok && rope)
                         ok = memcmp(rope->x, c.op.x, 9 * sizeof c.op.x[0]) == 0 && rope->t[0].ne[0] == x.ne[0] &&
                              same_place(rpos, c.src[1]) && same_place(rff, c.src[2]);
@@ -1016,11 +1029,11 @@ class Lowering {
                         e.rows[k] = o.ne[1];
                         e.row_nb[k] = o.nb[1];
                     } else {
-                        if (!contiguous(o) || elems(o) != M) continue;
-                        // a rotated key that only a one-token paged write reads
+                        if (!contiguous(o) || elems(o) != M * T) continue;
+                        // a rotated key that only a paged write of these tokens reads
                         const std::vector<size_t> w2 = readers_after(j, c.dst);
                         if (o.ty == TLH_TYPE_F16 && w2.size() == 1 && d[w2[0]].kind == D_PAGED_WRITE &&
-                            d[w2[0]].pw[0] == 1 && !d[w2[0]].pw_f32[0] && same_place(d[w2[0]].src[0], c.dst) &&
+                            d[w2[0]].pw[0] == T && !d[w2[0]].pw_f32[0] && same_place(d[w2[0]].src[0], c.dst) &&
                             c.dst.buf == B_ARENA && !kept(c.dst.index) && (paged_w < 0 || paged_w == (int)w2[0])) {
                             lay = EPI_PAGED_KEY;
                             paged_w = (int)w2[0];
@@ -1034,7 +1047,7 @@ class Lowering {
                     if (lay != EPI_PAGED_KEY) edst[k] = c.dst;
                     if (!rope) rope = &c.op, rpos = c.src[1], rff = c.src[2];
                     take[k] = t;
-                } else if (is_core(c, TLH_CORE_SET_ROWS) && same_place(c.src[0], P)) {
+                } else if (!batched && is_core(c, TLH_CORE_SET_ROWS) && same_place(c.src[0], P)) {
                     const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
                     if (!(x.ne[0] == M && x.ne[1] == 1 && x.ne[2] == 1 && x.ne[3] == 1 && idx_ty(c.op.t[1]) &&
                           o.ne[0] == M && (o.ty == TLH_TYPE_F16 || o.ty == TLH_TYPE_F32) &&
@@ -1048,7 +1061,7 @@ class Lowering {
                     e.rows[k] = o.ne[1];
                     e.row_nb[k] = o.nb[1];
                     take[k] = {j};
-                } else if (c.kind == D_PAGED_WRITE && c.pw[0] == 1 && (paged_w < 0 || paged_w == (int)j)) {
+                } else if (c.kind == D_PAGED_WRITE && c.pw[0] == T && (paged_w < 0 || paged_w == (int)j)) {
                     int side = -1;
                     if (same_place(c.src[1], P) && c.pw_f32[1]) side = 1;
                     else if (same_place(c.src[0], P) && c.pw_f32[0]) side = 0;
@@ -1118,7 +1131,7 @@ class Lowering {
             }
             e.on = 1;
             Dispatch g = f;
-            g.kind = D_GEMV_PRO;
+            if (!batched) g.kind = D_GEMV_PRO;
             g.has_epi = 1;
             g.epi = e;
             for (int k = 0; k < 3; ++k) g.edst[k] = edst[k], g.eidx[k] = eidx[k];
@@ -1683,6 +1696,20 @@ struct tlh_program {
                     ops[k] = &x.mop[k];
                     w[k] = resolve(x.mw[k], state);
                     dsts[k] = resolve(x.mdst[k], state);
+                }
+                if (x.has_epi) {  // the absorbed rotations / casts / paged writes at the store
+                    GemvEpi e = x.epi;
+                    for (int k = 0; k < 3; ++k) {
+                        e.dst[k] = (char *)resolve(x.edst[k], state);
+                        e.idx[k] = (const char *)resolve(x.eidx[k], state);
+                    }
+                    e.pos = (const int32_t *)resolve(x.epos, state);
+                    e.ff = (const float *)resolve(x.eff, state);
+                    st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s, &e);
+                    if (st != TLH_UNSUPPORTED) break;
+                    st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s);
+                    for (size_t k = 0; k < x.absorbed.size() && st == TLH_OK; ++k) st = launch_one(x.absorbed[k], state, s);
+                    break;
                 }
                 st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s);
                 break;

@@ -41,6 +41,8 @@
 // reads its 16-row x KS-unit slice as consecutive 16-byte pieces per lane
 // (each row's slice is contiguous), writes them to a wave-private LDS buffer
 // and reads the operand layout back from there. Other K: direct loads.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace tlh {
@@ -500,9 +502,20 @@ template <int WT, int KS> struct DirectW {
     }
 };
 
-template <int WT, int KS, bool STAGED>
-__global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share) {
-    kernarg_prefetch<kernarg_lines(sizeof(MatmulArgs) + 8)>();
+// No store epilogue (the kernel argument of the plain launches).
+struct NoEpi {
+    int unused;
+};
+
+// EP = GemvEpi: the outputs of segment s go out through ep.layout[s] at the
+// flush instead of seg_dst[s] (one K chunk, segments): the ROPE (mode 0, the
+// pair's other row is the neighbouring output of the same column), f16 cast,
+// cache-row or paged K / V write that follow a batched Q / K / V projection,
+// column n being token n (its position ep.pos[n], its row or slot ep.idx[s][n]).
+template <int WT, int KS, bool STAGED, typename EP = NoEpi>
+__global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share, const EP ep) {
+    kernarg_prefetch<kernarg_lines(sizeof(MatmulArgs) + 8 + sizeof(EP))>();
+    constexpr bool EPI = !std::is_same<EP, NoEpi>::value;
     extern __shared__ __attribute__((aligned(16))) char sk_lds[];
     constexpr int AT = vec_dot_type(WT);
     constexpr bool KQ = kquant<WT>();
@@ -657,12 +670,63 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // share one completion counter that is not in order across the two).
     int nbuf = 0;
     int64_t buf_rg = rg;
+    // EPI: output (row m, column n) with value v, its rotation partner's value o
+    auto epi_store = [&](int64_t m, int n, float v, float o) {
+        if constexpr (EPI) {
+            auto sel = [](int s, auto x0, auto x1, auto x2) { return s == 0 ? x0 : s == 1 ? x1 : x2; };
+            const int sg = seg_of(m);
+            const int64_t j = m - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]);
+            const int lay = sel(sg, ep.layout[0], ep.layout[1], ep.layout[2]);
+            if (lay == EPI_F32) {
+                *(float *)((char *)sel(sg, a.seg_dst[0], a.seg_dst[1], a.seg_dst[2]) +
+                           n * sel(sg, a.seg_d_nb1[0], a.seg_d_nb1[1], a.seg_d_nb1[2]) + j * 4) = v;
+                return;
+            }
+            float y = v;
+            if (sel(sg, ep.rope[0], ep.rope[1], ep.rope[2])) {
+                const uint32_t el = (uint32_t)j % (uint32_t)ep.ne0, pr = el / 2;  // rows below 2^31 (launcher)
+                if (2 * pr < (uint32_t)ep.rp.n_dims) {
+                    float cs, sn;
+                    rope_cs_sn((float)ep.pos[n], pr, ep.ff ? ep.ff[pr] : 1.0f, ep.rp, cs, sn);
+                    y = (el & 1) == 0 ? rope_first(v, o, cs, sn) : rope_second(o, v, cs, sn);
+                }
+            }
+            char *base = sel(sg, ep.dst[0], ep.dst[1], ep.dst[2]);
+            const bool h16 = sel(sg, ep.f16[0], ep.f16[1], ep.f16[2]) != 0;
+            int64_t at;  // element offset
+            if (lay == EPI_CONTIG) {
+                at = (int64_t)n * (sel(sg, a.seg_m0[1], a.seg_m0[2], a.seg_m0[3]) - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2])) + j;
+            } else {
+                const char *ip = sel(sg, ep.idx[0], ep.idx[1], ep.idx[2]);
+                const int64_t r = sel(sg, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2]) ? ((const int64_t *)ip)[n]
+                                                                                      : (int64_t)((const int32_t *)ip)[n];
+                if (r < 0 || r >= sel(sg, ep.rows[0], ep.rows[1], ep.rows[2])) return;
+                if (lay == EPI_CACHE_ROW) {
+                    base += r * sel(sg, ep.row_nb[0], ep.row_nb[1], ep.row_nb[2]);
+                    at = j;
+                } else {  // the paged pools' layouts: keys [blocks, kvh, hs/8, bs, 8], values [blocks, kvh, hs, bs]
+                    const uint32_t ru = (uint32_t)r, bs = (uint32_t)ep.bs, hs = (uint32_t)ep.hs, ju = (uint32_t)j;
+                    const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, el = ju % hs;
+                    at = lay == EPI_PAGED_KEY ? (((blk * ep.kvh + h) * (ep.hs / 8) + el / 8) * ep.bs + off) * 8 + el % 8
+                                              : ((blk * ep.kvh + h) * ep.hs + el) * ep.bs + off;
+                }
+            }
+            if (h16) ((uint16_t *)base)[at] = f2h(y);
+            else ((float *)base)[at] = y;
+        }
+    };
     auto flush = [&]() {
         if (threadIdx.x < 16 * SK_COLS)
             for (int k = 0; k < nbuf; ++k) {
                 const int64_t grp = buf_rg + (int64_t)k * gridDim.x;
-                if (ocol < N && grp * 16 + orow < a.M)
-                    *out_ptr(grp) = bad_id ? __builtin_nanf("") : obuf[k * 256 + threadIdx.x];
+                if (ocol < N && grp * 16 + orow < a.M) {
+                    if constexpr (EPI) {  // the pair partner: the neighbouring row, same column
+                        epi_store(grp * 16 + orow, (int)(a.n0 + ocol), obuf[k * 256 + threadIdx.x],
+                                  obuf[k * 256 + (threadIdx.x ^ 1)]);
+                    } else {
+                        *out_ptr(grp) = bad_id ? __builtin_nanf("") : obuf[k * 256 + threadIdx.x];
+                    }
+                }
             }
         nbuf = 0;
         // the stores complete here, so no later wait for loads is widened by them
@@ -1125,9 +1189,10 @@ int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches
     return chunks > 1 ? chunks * batches * (N < SK_COLS ? N : SK_COLS) * M * 4 : 0;
 }
 
-template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream) {
+template <int WT, bool STAGED, typename EP = NoEpi>
+static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream, const EP &ep = EP{}) {
     constexpr int KS = sk_ks<WT>();
-    auto kern = k_gemv_mfma<WT, KS, STAGED>;
+    auto kern = k_gemv_mfma<WT, KS, STAGED, EP>;
     int64_t chunks = 1;
     const int64_t share = sk_share(a.K, chunks);
     if (chunks > 1 && !a.part) return set_error(TLH_INVALID, "gemv_mfma: K=%lld needs a partials buffer", (long long)a.K);
@@ -1146,7 +1211,9 @@ template <int WT, bool STAGED> static tlh_status launch_sk(const MatmulArgs &a, 
     const unsigned gx = (unsigned)(groups < resident ? groups : resident);
     MatmulArgs k = a;
     if (chunks == 1) k.part = nullptr;
-    hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share);
+    if (!std::is_same<EP, NoEpi>::value && chunks != 1)
+        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes one K chunk");
+    hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share, ep);
     tlh_status st = check_launch("gemv_mfma");
     if (st != TLH_OK || chunks == 1) return st;
     return launch_partial_reduce(a, (int)chunks, stream);
@@ -1157,6 +1224,20 @@ template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool stage
         return launch_sk<WT, true>(a, stream);  // K is a multiple of 256
     } else {
         return staged ? launch_sk<WT, true>(a, stream) : launch_sk<WT, false>(a, stream);
+    }
+}
+
+// The few-column kernel with the store epilogue (segments, q4_K / q5_K / q6_K,
+// K a multiple of 256 in one chunk, rows and segment rows below 2^31).
+tlh_status launch_gemv_mfma_epi(const MatmulArgs &a, const GemvEpi &ep, hipStream_t stream) {
+    if (!gemv_mfma_supported(a.N) || a.nseg < 1 || a.K % 256 != 0 || a.M >= ((int64_t)1 << 31) || a.ids ||
+        a.ne12 * a.ne13 != 1)
+        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes segments of one batch slice");
+    switch (a.wtype) {
+    case TLH_TYPE_Q4_K: return launch_sk<TLH_TYPE_Q4_K, true, GemvEpi>(a, stream, ep);
+    case TLH_TYPE_Q5_K: return launch_sk<TLH_TYPE_Q5_K, true, GemvEpi>(a, stream, ep);
+    case TLH_TYPE_Q6_K: return launch_sk<TLH_TYPE_Q6_K, true, GemvEpi>(a, stream, ep);
+    default: return set_error(TLH_UNSUPPORTED, "gemv_mfma: no store epilogue for weight type %d", a.wtype);
     }
 }
 

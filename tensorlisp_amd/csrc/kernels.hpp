@@ -178,6 +178,10 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
 bool gemv_mfma_supported(int64_t N);
 int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches);
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
+// launch_gemv_mfma with GemvEpi's store epilogue over the columns (token n =
+// column n): segments, q4_K / q5_K / q6_K, one K chunk; TLH_UNSUPPORTED otherwise.
+struct GemvEpi;
+tlh_status launch_gemv_mfma_epi(const MatmulArgs &a, const GemvEpi &ep, hipStream_t stream);
 // Tiled prefill GEMM for q8_0 / q4_0 weights (gemm_q8.hip), any N; with
 // ksplit > 1 each K chunk writes a.part and a reduce launch sums them.
 tlh_status launch_gemm_q8(const MatmulArgs &a, int ksplit, hipStream_t stream);
@@ -215,7 +219,8 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream);
 bool mul_mat_compute_multi_ok(const tlh_op *const *ops, int n);
 size_t mul_mat_compute_multi_scratch_bytes(const tlh_op *const *ops, int n);
 tlh_status mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
-                                 const void *scratch, size_t scratch_bytes, hipStream_t stream);
+                                 const void *scratch, size_t scratch_bytes, hipStream_t stream,
+                                 const GemvEpi *epi = nullptr);
 bool mul_mat_multi_ok(const tlh_op *const *ops, int n);
 tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n, const void *x,
                          hipStream_t stream);

@@ -594,9 +594,23 @@ size_t tlh::mul_mat_compute_multi_scratch_bytes(const tlh_op *const *ops, int n)
     return (size_t)(mm_act_bytes(s) + part);
 }
 
+// With epi (the executor's batched Q / K / V projection): the few-column
+// kernel stores through the epilogue (N <= 16, one K chunk); TLH_UNSUPPORTED
+// when it cannot take the shapes or pointers (the executor then runs the
+// absorbed dispatches after a plain launch).
 tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
-                                      const void *scratch, size_t scratch_bytes, hipStream_t stream) {
+                                      const void *scratch, size_t scratch_bytes, hipStream_t stream,
+                                      const GemvEpi *epi) {
     if (!mul_mat_compute_multi_ok(ops, n)) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: shapes");
+    if (epi) {
+        for (int i = 0; i < n; ++i) {
+            if (epi->layout[i] == EPI_F32) continue;
+            const uintptr_t es = epi->f16[i] ? 2 : 4, is = epi->idx_i64[i] ? 8 : 4;
+            if (((uintptr_t)epi->dst[i] | (uintptr_t)epi->row_nb[i]) % es || (epi->idx[i] && (uintptr_t)epi->idx[i] % is) ||
+                (epi->rope[i] && (((uintptr_t)epi->pos & 3) || ((uintptr_t)epi->ff & 3))))
+                return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: epilogue pointer alignment");
+        }
+    }
     MulMatShape s;
     check_mul_mat(ops[0], s);
     const size_t need = mul_mat_compute_multi_scratch_bytes(ops, n);
@@ -622,6 +636,10 @@ tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *cons
     m.seg_m0[3] = rows;
     for (int i = n; i < 3; ++i) m.seg_m0[i] = rows;
     m.M = rows;
+    if (epi) {
+        if (s.N > 16) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: the store epilogue takes N <= 16");
+        return launch_gemv_mfma_epi(m, *epi, stream);
+    }
     return s.N > 16 ? launch_gemm(m, stream) : launch_gemv_mfma(m, stream);
 }
 
