@@ -72,6 +72,7 @@ struct Dispatch {
     // activation rows, f16 codes) into that MUL_MAT's scratch block
     int nq_type = 0, nq_f16 = 0;
     int64_t nq_rows = 0;
+    int64_t rt_off = 0;  // batched epilogue: byte offset of its rotation table in the program's table buffer
     tlh_op nq_op;          // that MUL_MAT (its quantize launch, if the fused form is refused)
     size_t pa_own = 0;     // D_PAGED_ATTN with nq_type: its own scratch's offset in the shared block
     int32_t pw[4] = {0, 0, 0, 0};
@@ -174,6 +175,7 @@ struct Lowered {
     std::vector<int64_t> node_scratch;  // per node position (-1: none)
     std::vector<int32_t> node_ids;      // tensor id per node position
     int64_t arena = 0;
+    int64_t rt_bytes = 0;  // the batched epilogues' rotation tables
 };
 
 class Lowering {
@@ -1128,6 +1130,21 @@ class Lowering {
                 e.rp.corr1 = __builtin_bit_cast(float, (int32_t)rope->x[7]);
                 epos = rpos;
                 if (rope->x[8]) eff = rff;
+                if (batched) {  // one (cos, sin) table per positions and parameters, the first launch writes it
+                    std::vector<int64_t> key = {rpos.buf, rpos.index, rpos.off, rff.buf, rff.index, rff.off, e.ne0, T};
+                    for (int q = 0; q < 9; ++q) key.push_back(rope->x[q]);
+                    auto it = rt_tables_.find(key);
+                    const int64_t pairs = std::min<int64_t>(e.rp.n_dims, e.ne0) / 2;
+                    if (it == rt_tables_.end()) {
+                        f.rt_off = rt_bytes_;
+                        rt_tables_[key] = rt_bytes_;
+                        rt_bytes_ += align_up(T * pairs * 8);
+                        e.rt_mode = 1;
+                    } else {
+                        f.rt_off = it->second;
+                        e.rt_mode = 2;
+                    }
+                }
             }
             e.on = 1;
             Dispatch g = f;
@@ -1420,6 +1437,9 @@ class Lowering {
         d.swap(out);
     }
 
+    std::map<std::vector<int64_t>, int64_t> rt_tables_;  // rotation table offset per key
+    int64_t rt_bytes_ = 0;
+
     struct Group {
         int64_t first = 0, last = 0;
         size_t bytes = 0;
@@ -1525,6 +1545,7 @@ class Lowering {
                 for (int k = 0; k < x.nmem; ++k) out.node_scratch[x.mpos[k]] = out.blocks[x.block].off;
         }
         out.arena = arena;
+        out.rt_bytes = rt_bytes_;
     }
 };
 
@@ -1573,6 +1594,10 @@ struct tlh_program {
     // zeroed counters the one-launch paged attention leaves zeroed (its
     // dispatches run in stream order, so they share them)
     unsigned *counters = nullptr;
+    float *rtab = nullptr;  // the batched epilogues' rotation tables (low.rt_bytes)
+    // per table offset: its writing launch took the epilogue (else its readers
+    // compute the rotation themselves); set as the dispatches are enqueued in order
+    mutable std::map<int64_t, bool> rt_ok;
     hipGraphExec_t exec = nullptr;
     void *exec_state = nullptr;
     hipStream_t exec_stream = nullptr;
@@ -1705,7 +1730,10 @@ struct tlh_program {
                     }
                     e.pos = (const int32_t *)resolve(x.epos, state);
                     e.ff = (const float *)resolve(x.eff, state);
+                    if (e.rt_mode) e.rt = (float *)((char *)rtab + x.rt_off);
+                    if (e.rt_mode == 2 && !rt_ok[x.rt_off]) e.rt_mode = 0;
                     st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s, &e);
+                    if (e.rt_mode == 1) rt_ok[x.rt_off] = st == TLH_OK;
                     if (st != TLH_UNSUPPORTED) break;
                     st = mul_mat_compute_multi(ops, w, dsts, x.nmem, scratch, x.scratch_bytes, s);
                     for (size_t k = 0; k < x.absorbed.size() && st == TLH_OK; ++k) st = launch_one(x.absorbed[k], state, s);
@@ -1921,6 +1949,8 @@ tlh_status tlh_program_compile(const tlh_ir_tensor *tensors, int32_t n_tensors, 
             TLH_OK ||
         (st = hip_ok(hipMalloc((void **)&p->io, (size_t)std::max<int64_t>(p->io_bytes, ALIGN)), "io buffer")) !=
             TLH_OK ||
+        (p->low.rt_bytes &&
+         (st = hip_ok(hipMalloc((void **)&p->rtab, (size_t)p->low.rt_bytes), "rotation tables")) != TLH_OK) ||
         (n_counters &&
          ((st = hip_ok(hipMalloc((void **)&p->counters, n_counters * sizeof(unsigned)), "counters")) != TLH_OK ||
           (st = hip_ok(hipMemset(p->counters, 0, n_counters * sizeof(unsigned)), "counters")) != TLH_OK ||
@@ -1938,6 +1968,7 @@ tlh_status tlh_program_destroy(tlh_program *p) {
     if (p->arena) (void)hipFree(p->arena);
     if (p->io) (void)hipFree(p->io);
     if (p->counters) (void)hipFree(p->counters);
+    if (p->rtab) (void)hipFree(p->rtab);
     delete p;
     return TLH_OK;
 }

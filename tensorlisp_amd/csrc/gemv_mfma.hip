@@ -506,6 +506,11 @@ template <int WT, int KS> struct DirectW {
 struct NoEpi {
     int unused;
 };
+// Rotated pairs per head in the epilogue's (cos, sin) table (0: none read).
+__host__ __device__ inline int epi_table_pairs(const NoEpi &) { return 0; }
+__host__ __device__ inline int epi_table_pairs(const GemvEpi &e) {
+    return e.rt_mode == 2 && (e.rope[0] | e.rope[1] | e.rope[2]) ? (int)(e.rp.n_dims < e.ne0 ? e.rp.n_dims : e.ne0) / 2 : 0;
+}
 
 // EP = GemvEpi: the outputs of segment s go out through ep.layout[s] at the
 // flush instead of seg_dst[s] (one K chunk, segments): the ROPE (mode 0, the
@@ -561,6 +566,9 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     float *ss = sd + (s_end - s_begin) * SK_COLS;
     float *obuf = ss + (S8 ? (s_end - s_begin) * SK_COLS : 0);
     uint8_t *wbuf = (uint8_t *)(obuf + SK_OUTBUF * 256) + (size_t)wave * St::BUF;
+    // EPI reading the (cos, sin) table: its columns' entries, after the weight buffers
+    const int tpairs = epi_table_pairs(ep);
+    float2 *s_rt = (float2 *)((uint8_t *)(obuf + SK_OUTBUF * 256) + (size_t)nw * (STAGED ? St::BUF : 0));
 
     const int64_t groups = (a.M + 15) / 16;
     int64_t rg = blockIdx.x;
@@ -618,6 +626,34 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     const int64_t rg0 = rg < groups ? rg : groups - 1;
     if constexpr (STAGED) stage_load(st, rg0);
     else da.load(wrow_of(rg0), u0, (s_end - 1) / (KQ ? 1 : 8), s_end, g);
+    // EPI: the flush's column (token) values, read now so that no load waits at
+    // the end of the kernel: its position and, per segment, its row or slot
+    // (raw words: i64 as two, i32 read twice)
+    float e_pos = 0.0f;
+    int32_t e_lo[3] = {0, 0, 0}, e_hi[3] = {0, 0, 0};
+    // and the rotation table's entries (at most RT_PER per thread), written to LDS before the first barrier
+    constexpr int RT_PER = 4;
+    float2 rt_v[EPI ? RT_PER : 1];
+    if constexpr (EPI) {
+        if (tpairs) {  // uniform; the loads are unconditional (clamped), so no wait where a branch rejoins
+            const int last = N * tpairs - 1;
+#pragma unroll
+            for (int k = 0; k < RT_PER; ++k) {
+                const int i = threadIdx.x + k * (int)blockDim.x;
+                rt_v[k] = ((const float2 *)ep.rt)[(int64_t)a.n0 * tpairs + (i < last ? i : last)];
+            }
+        }
+        const int ec = threadIdx.x >> 4;  // the flush's column of this thread
+        const int64_t en = a.n0 + (ec < N ? ec : 0);
+        if (ep.pos) e_pos = (float)ep.pos[en];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (ep.idx[k]) {
+                const int32_t *ip = (const int32_t *)ep.idx[k];
+                e_lo[k] = ip[ep.idx_i64[k] ? 2 * en : en];
+                e_hi[k] = ip[ep.idx_i64[k] ? 2 * en + 1 : en];
+            }
+    }
 
     // activation operands of this wave's units (zero past N and past the range)
     long A[KS][8];
@@ -645,6 +681,14 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             const int c = (int)(i & 15);
             sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
             if constexpr (S8) ss[i] = c < N ? __int_as_float(act.sum32[(arow0 + c) * nblk + b]) : 0.0f;
+        }
+    }
+    if constexpr (EPI) {
+        // the table's entries of this launch's columns, to LDS
+#pragma unroll
+        for (int k = 0; k < RT_PER; ++k) {
+            const int i = threadIdx.x + k * (int)blockDim.x;
+            if (i < N * tpairs) s_rt[i] = rt_v[k];
         }
     }
     lds_barrier();
@@ -687,7 +731,16 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
                 const uint32_t el = (uint32_t)j % (uint32_t)ep.ne0, pr = el / 2;  // rows below 2^31 (launcher)
                 if (2 * pr < (uint32_t)ep.rp.n_dims) {
                     float cs, sn;
-                    rope_cs_sn((float)ep.pos[n], pr, ep.ff ? ep.ff[pr] : 1.0f, ep.rp, cs, sn);
+                    if (tpairs) {
+                        const float2 t = s_rt[(n - a.n0) * tpairs + pr];
+                        cs = t.x, sn = t.y;
+                    } else {
+                        rope_cs_sn(e_pos, pr, ep.ff ? ep.ff[pr] : 1.0f, ep.rp, cs, sn);
+                        if (ep.rt_mode == 1 && (el & 1) == 0) {  // one writer per pair, the table's row width
+                            const int tw = (int)(ep.rp.n_dims < ep.ne0 ? ep.rp.n_dims : ep.ne0) / 2;
+                            ((float2 *)ep.rt)[(int64_t)n * tw + pr] = make_float2(cs, sn);
+                        }
+                    }
                     y = (el & 1) == 0 ? rope_first(v, o, cs, sn) : rope_second(o, v, cs, sn);
                 }
             }
@@ -697,9 +750,10 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             if (lay == EPI_CONTIG) {
                 at = (int64_t)n * (sel(sg, a.seg_m0[1], a.seg_m0[2], a.seg_m0[3]) - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2])) + j;
             } else {
-                const char *ip = sel(sg, ep.idx[0], ep.idx[1], ep.idx[2]);
-                const int64_t r = sel(sg, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2]) ? ((const int64_t *)ip)[n]
-                                                                                      : (int64_t)((const int32_t *)ip)[n];
+                const int32_t lo = sel(sg, e_lo[0], e_lo[1], e_lo[2]), hi = sel(sg, e_hi[0], e_hi[1], e_hi[2]);
+                const int64_t r = sel(sg, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2])
+                                      ? (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo)
+                                      : (int64_t)lo;
                 if (r < 0 || r >= sel(sg, ep.rows[0], ep.rows[1], ep.rows[2])) return;
                 if (lay == EPI_CACHE_ROW) {
                     base += r * sel(sg, ep.row_nb[0], ep.row_nb[1], ep.row_nb[2]);
@@ -1200,7 +1254,8 @@ static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream, const EP &e
     const int nw = (int)((share + KS - 1) / KS) > 4 ? (int)((share + KS - 1) / KS) : 4;
     const size_t slots = (size_t)(kquant<WT>() ? share : 8 * share) * SK_COLS * 4;
     const size_t lds = (size_t)2 * nw * 64 * 16 + slots * (vec_dot_type(WT) == TLH_TYPE_Q8_1 ? 2 : 1) +
-                       (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0);
+                       (size_t)SK_OUTBUF * 256 * 4 + (STAGED ? (size_t)nw * Stage<WT, KS>::BUF : 0) +
+                       (size_t)SK_COLS * epi_table_pairs(ep) * sizeof(float2);
     // per-CU occupancy by wave count (the LDS size follows from it)
     static std::atomic<int> bpc[SK_MAXW + 1];
     const int nb = blocks_per_cu(kern, 64 * nw, lds, bpc[nw <= SK_MAXW ? nw : SK_MAXW]);
@@ -1233,6 +1288,29 @@ tlh_status launch_gemv_mfma_epi(const MatmulArgs &a, const GemvEpi &ep, hipStrea
     if (!gemv_mfma_supported(a.N) || a.nseg < 1 || a.K % 256 != 0 || a.M >= ((int64_t)1 << 31) || a.ids ||
         a.ne12 * a.ne13 != 1)
         return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes segments of one batch slice");
+    bool rope = false;
+    for (int sg = 0; sg < a.nseg; ++sg) {
+        const int64_t rows = a.seg_m0[sg + 1] - a.seg_m0[sg];
+        if (ep.layout[sg] != EPI_F32 && !ep.dst[sg]) return set_error(TLH_INVALID, "gemv_mfma: epilogue without a destination");
+        if ((ep.layout[sg] == EPI_CACHE_ROW || ep.layout[sg] >= EPI_PAGED_KEY) && !ep.idx[sg])
+            return set_error(TLH_INVALID, "gemv_mfma: epilogue row or slot index missing");
+        if (ep.rows[sg] >= ((int64_t)1 << 31))
+            return set_error(TLH_UNSUPPORTED, "gemv_mfma: epilogue cache rows or pool slots past 2^31");
+        if (ep.layout[sg] >= EPI_PAGED_KEY && (!ep.f16[sg] || !ep.idx_i64[sg] || ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 ||
+                                               ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs))
+            return set_error(TLH_UNSUPPORTED, "gemv_mfma: paged epilogue geometry");
+        if (ep.rope[sg]) {
+            rope = true;
+            if (ep.ne0 < 2 || ep.ne0 % 2 || ep.ne0 > 512 || rows % ep.ne0 || a.seg_m0[sg] % 2)
+                return set_error(TLH_UNSUPPORTED, "gemv_mfma: rotated segments are whole heads of even size");
+        }
+    }
+    if (rope && (!ep.pos || ep.rp.mode != 0 || ep.rp.n_dims % 2 || ep.rp.n_dims < 0))
+        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the epilogue rotates in ROPE mode 0 only");
+    if (ep.rt_mode && (!ep.rt || ((uintptr_t)ep.rt & 7)))
+        return set_error(TLH_INVALID, "gemv_mfma: the rotation table needs an 8-byte aligned buffer");
+    if (ep.rt_mode == 2 && a.N * epi_table_pairs(ep) > 4 * 256)  // RT_PER entries a thread, at least 4 waves
+        return set_error(TLH_UNSUPPORTED, "gemv_mfma: rotation table larger than the prologue reads");
     switch (a.wtype) {
     case TLH_TYPE_Q4_K: return launch_sk<TLH_TYPE_Q4_K, true, GemvEpi>(a, stream, ep);
     case TLH_TYPE_Q5_K: return launch_sk<TLH_TYPE_Q5_K, true, GemvEpi>(a, stream, ep);

@@ -140,6 +140,13 @@ struct GemvEpi {
     const float *ff = nullptr;
     int64_t ne0 = 0;
     RopeParams rp;
+    // the few-column kernel (several tokens): the rotation's (cos, sin) per
+    // (token, pair), [tokens][pairs][2], are the same for every layer of a
+    // step. rt_mode 1: computed here and also written to rt; 2: read from rt
+    // (a launch with mode 1 of the same positions and parameters ran before);
+    // 0: computed here only
+    float *rt = nullptr;
+    int rt_mode = 0;
 };
 struct GemvPro {
     const float *p = nullptr, *q = nullptr, *w = nullptr;
