@@ -655,33 +655,45 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
             }
     }
 
-    // activation operands of this wave's units (zero past N and past the range)
+    // activation operands of this wave's units (zero past N and past the
+    // range). Every load goes out first, from clamped addresses; the masks
+    // come after the last one (a use of a loaded value waits for every load
+    // issued before it, so a mask between loads would split them in rounds).
     long A[KS][8];
     const bool col_ok = wr < N;
+    auto a_ok = [&](int t, int j) {
+        const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
+        return col_ok && e < 256 * u_end && e < K;
+    };
     {
         const int8_t *aq = act.qs + (arow0 + (col_ok ? wr : 0)) * K;
 #pragma unroll
         for (int t = 0; t < KS; ++t)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
-                const bool ok = col_ok && e < 256 * u_end && e < K;
-                const int64_t ec = ok ? e : 0;
-                long v;
+                const int64_t ec = a_ok(t, j) ? 256 * (u0 + t) + 32 * j : 0;
                 if constexpr (nibble_type<WT>()) {
                     // the lane's weight bytes 4g..4g+3 hold elements 4g.. (low) and 16+4g.. (high)
-                    v = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
+                    A[t][j] = pack2(ldu<uint32_t>(aq + ec + 4 * g), ldu<uint32_t>(aq + ec + 16 + 4 * g));
                 } else {
-                    v = ldu<long>(aq + ec + 8 * g);
+                    A[t][j] = ldu<long>(aq + ec + 8 * g);
                 }
-                A[t][j] = ok ? v : 0;
             }
         for (int64_t i = threadIdx.x; i < (s_end - s_begin) * SK_COLS; i += blockDim.x) {
             const int64_t b = s_begin + (i >> 4);
             const int c = (int)(i & 15);
-            sd[i] = c < N ? act.d[(arow0 + c) * nblk + b] : 0.0f;
-            if constexpr (S8) ss[i] = c < N ? __int_as_float(act.sum32[(arow0 + c) * nblk + b]) : 0.0f;
+            const int64_t at = (arow0 + (c < N ? c : 0)) * nblk + b;
+            const float dv = act.d[at];
+            sd[i] = c < N ? dv : 0.0f;
+            if constexpr (S8) {
+                const float sv = __int_as_float(act.sum32[at]);
+                ss[i] = c < N ? sv : 0.0f;
+            }
         }
+#pragma unroll
+        for (int t = 0; t < KS; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) A[t][j] = a_ok(t, j) ? A[t][j] : 0;
     }
     if constexpr (EPI) {
         // the table's entries of this launch's columns, to LDS
