@@ -14,8 +14,9 @@ value  = whole-sweep algorithmic bytes (M*row_bytes + N*K*4 + N*M*4 per node)
          / wall time of the timed steps, GB/s.
 roofline = the GEMV kernel of the sweep's heaviest node: its algorithmic bytes
          (weights, the activation it reads, f32 outputs) / its mean duration
-         from HIP events on the launch stream, against 8 TB/s. A node above
-         N = 2 is a quantize launch and the GEMV; the GEMV is timed alone.
+         (HIP events on the launch stream around a run of back-to-back
+         launches), against 8 TB/s. A node above N = 2 is a quantize launch
+         and the GEMV; the GEMV is timed alone.
 cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, compiled from
          the reference sources) on the same sweep, timed on this host's cores
          the GPU box allots the job (16), with the host's CPU model and count;
@@ -793,8 +794,8 @@ def main() -> int:
     # the roofline kernel: the GEMV of the sweep's heaviest node. A node at
     # N <= 2 is one launch (the GEMV quantizes its activation itself); above,
     # the node is a quantize launch and the GEMV, timed here alone (events on
-    # the launch stream around the compute launch, the activation quantized
-    # once before)
+    # the launch stream around back-to-back compute launches, the activation
+    # quantized once before)
     dom = max(cases, key=lambda c: node_ms[c])
     dt, dM, dK, dn = dom
     if dn <= 2:
@@ -806,15 +807,17 @@ def main() -> int:
         node = nodes[dom]
         ws = weights[(dt, dM, dK)]
         node.quantize(xs[dom], stream)
-        evs = []
-        for i in range(max(args.steps, 10)):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
+        # back-to-back compute launches (weights rotated) between one pair of
+        # events: the average launch duration on the stream, without a
+        # dispatch latency in every sample
+        reps = max(args.steps, 10)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
             node.compute(ws[i % len(ws)], ys[dom], stream)
-            e1.record(stream)
-            evs.append((e0, e1))
+        e1.record(stream)
         torch.cuda.synchronize()
-        dom_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        dom_ms = e0.elapsed_time(e1) / reps
         # the compute launch reads the weights and the quantized activation, writes f32 rows
         dom_bytes = dM * N.row_bytes(dt, dK) + dn * N.row_bytes(N.VEC_DOT_TYPE[dt], dK) + dn * dM * 4
         # tall matrices with K <= 4096 take the few-column form whose waves own
