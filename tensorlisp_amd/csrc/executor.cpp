@@ -86,6 +86,7 @@ struct Dispatch {
     int has_epi = 0;
     GemvEpi epi;
     Place edst[3], eidx[3], epos, eff;
+    Place edst2[3];  // the second (paged pool) store of a dual segment
     std::vector<Dispatch> absorbed;
 };
 
@@ -746,7 +747,7 @@ class Lowering {
         }
         if (x.has_glu) wr.push_back(x.gdst);
         if (x.has_epi) {
-            for (int k = 0; k < 3; ++k) wr.push_back(x.edst[k]), rd.push_back(x.eidx[k]);
+            for (int k = 0; k < 3; ++k) wr.push_back(x.edst[k]), wr.push_back(x.edst2[k]), rd.push_back(x.eidx[k]);
             rd.push_back(x.epos), rd.push_back(x.eff);
             std::vector<Place> r2, w2;
             for (const Dispatch &a : x.absorbed) {
@@ -959,7 +960,9 @@ class Lowering {
     // batched: the same for the merged compute of a few-column projection
     // (D_MM_COMPUTE_MULTI, 3..16 columns = tokens, K <= 4096, q4_K / q5_K /
     // q6_K: the int8-MFMA kernel's store epilogue, token n in column n), for
-    // the rotated / cast outputs and paged K / V writes (not cache rows).
+    // the rotated / cast outputs and paged K / V writes (not cache rows); and
+    // for a prefill's (more columns, q4_K / q5_K) when the merged GEMM splits
+    // K, through its reduce launch.
     void fuse_gemv_epilogue(std::vector<Dispatch> &d, bool batched) {
         count_readers();
         std::vector<char> gone(d.size(), 0);
@@ -989,18 +992,45 @@ class Lowering {
                 continue;
             const tlh_tensor &b = f.mop[0].t[1];
             const int wty = f.mop[0].t[0].ty;
-            if (batched && (b.ne[1] < 3 || b.ne[1] > 16 ||
-                            (wty != TLH_TYPE_Q4_K && wty != TLH_TYPE_Q5_K && wty != TLH_TYPE_Q6_K)))
-                continue;
+            bool many = false;  // a prefill's merged GEMM: its reduce stores (second paged stores allowed)
+            if (batched) {
+                // 3..16 columns: the few-column kernel's stores; more (a
+                // prefill): the reduce of a q4_K / q5_K GEMM that splits K
+                int64_t rows = 0;
+                for (int k = 0; k < f.nmem; ++k) rows += f.mop[k].t[0].ne[1];
+                const bool few = b.ne[1] >= 3 && b.ne[1] <= 16 &&
+                                 (wty == TLH_TYPE_Q4_K || wty == TLH_TYPE_Q5_K || wty == TLH_TYPE_Q6_K);
+                many = b.ne[1] > 16 && (wty == TLH_TYPE_Q4_K || wty == TLH_TYPE_Q5_K) &&
+                       gemm_ksplit(wty, rows, b.ne[1], b.ne[0], 1) > 1;
+                if (!few && !many) continue;
+            }
             const int64_t T = batched ? b.ne[1] : 1;  // tokens = columns
             if (b.ne[0] > 4096 || b.ne[1] != T || b.ne[2] != 1 || b.ne[3] != 1) continue;
             GemvEpi e;
-            Place edst[3], eidx[3], epos, eff;
+            Place edst[3], eidx[3], epos, eff, edst2[3];
             std::vector<size_t> take[3];  // absorbed dispatch indices per member
             const tlh_op *rope = nullptr;  // the first rotation's op (parameters shared)
             Place rpos, rff;
             int paged_w = -1;             // index of the absorbed paged write
             int paged_have = 0;           // 1: key member found, 2: value member found
+            // many columns: an f16 result `out` (rotated keys, cast values)
+            // that the attention reads as rows and one paged write of these
+            // tokens also reads (side 0 key, 1 value): that write becomes a
+            // second store of the segment
+            auto dual_write = [&](size_t j, const Place &out, int side) -> int {
+                if (!many || out.buf != B_ARENA || kept(out.index)) return -1;
+                const std::vector<size_t> w2 = readers_after(j, out);
+                int found = -1;
+                for (size_t q : w2)
+                    if (d[q].kind == D_PAGED_WRITE && d[q].pw[0] == T && !d[q].pw_f32[side] &&
+                        same_place(d[q].src[side], out) && !same_place(d[q].src[side ^ 1], out)) {
+                        if (found >= 0) return -1;
+                        found = (int)q;
+                    }
+                if (found < 0 || w2.size() < 2 || (paged_w >= 0 && paged_w != found)) return -1;
+                return found;
+            };
+            int dual_w[3] = {-1, -1, -1};  // per member: the paged write taken as its second store
             for (int k = 0; k < f.nmem; ++k) {
                 const Place P = f.mdst[k];
                 const int64_t M = f.mop[k].t[0].ne[1];
@@ -1041,6 +1071,15 @@ class Lowering {
                             paged_w = (int)w2[0];
                             paged_have |= 1;
                             t.push_back(w2[0]);
+                        } else if (o.ty == TLH_TYPE_F16) {
+                            const int q = dual_write(j, c.dst, 0);
+                            if (q >= 0) {
+                                e.dual[k] = EPI_PAGED_KEY;
+                                dual_w[k] = q;
+                                paged_w = q;
+                                paged_have |= 1;
+                                t.push_back((size_t)q);
+                            }
                         }
                     }
                     e.layout[k] = lay;
@@ -1048,6 +1087,26 @@ class Lowering {
                     e.f16[k] = lay == EPI_PAGED_KEY || o.ty == TLH_TYPE_F16;
                     if (lay != EPI_PAGED_KEY) edst[k] = c.dst;
                     if (!rope) rope = &c.op, rpos = c.src[1], rff = c.src[2];
+                    take[k] = t;
+                } else if (batched && is_core(c, TLH_CORE_CPY) && same_place(c.src[0], P)) {
+                    // an f32 -> f16 cast of the member (a prefill's values, also
+                    // read as rows by the attention): contiguous f16 rows
+                    const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
+                    if (!(x.ty == TLH_TYPE_F32 && o.ty == TLH_TYPE_F16 && contiguous(x) && contiguous(o) &&
+                          elems(x) == M * T && elems(o) == M * T))
+                        continue;
+                    std::vector<size_t> t = {j};
+                    e.layout[k] = EPI_CONTIG;
+                    e.f16[k] = 1;
+                    edst[k] = c.dst;
+                    const int q = dual_write(j, c.dst, 1);
+                    if (q >= 0) {
+                        e.dual[k] = EPI_PAGED_VALUE;
+                        dual_w[k] = q;
+                        paged_w = q;
+                        paged_have |= 2;
+                        t.push_back((size_t)q);
+                    }
                     take[k] = t;
                 } else if (!batched && is_core(c, TLH_CORE_SET_ROWS) && same_place(c.src[0], P)) {
                     const tlh_tensor &x = c.op.t[0], &o = c.op.t[4];
@@ -1079,20 +1138,27 @@ class Lowering {
             if (paged_w >= 0) {
                 const Dispatch &w = d[paged_w];
                 bool ok = paged_have == 3;
-                for (int k = 0; k < f.nmem && ok; ++k)
-                    if (e.layout[k] == EPI_PAGED_KEY || e.layout[k] == EPI_PAGED_VALUE) {
+                for (int k = 0; k < f.nmem && ok; ++k) {
+                    const int pl = e.dual[k] ? e.dual[k] : e.layout[k];
+                    if (pl == EPI_PAGED_KEY || pl == EPI_PAGED_VALUE) {
                         ok = f.mop[k].t[0].ne[1] == (int64_t)w.pw[1] * w.pw[2];
-                        edst[k] = e.layout[k] == EPI_PAGED_KEY ? w.src[2] : w.src[3];
+                        (e.dual[k] ? edst2[k] : edst[k]) = pl == EPI_PAGED_KEY ? w.src[2] : w.src[3];
                         eidx[k] = w.src[4];
                         e.idx_i64[k] = 1;
                         e.rows[k] = w.pw_blocks * w.pw[3];
                     }
+                }
                 if (!ok)
-                    for (int k = 0; k < f.nmem; ++k)
-                        if (e.layout[k] == EPI_PAGED_KEY || e.layout[k] == EPI_PAGED_VALUE) {
+                    for (int k = 0; k < f.nmem; ++k) {
+                        if (e.dual[k]) {  // keep the contiguous rows, leave the paged write out
+                            e.dual[k] = 0;
+                            take[k].erase(std::remove(take[k].begin(), take[k].end(), (size_t)dual_w[k]), take[k].end());
+                            eidx[k] = Place{}, e.idx_i64[k] = 0, e.rows[k] = 0;
+                        } else if (e.layout[k] == EPI_PAGED_KEY || e.layout[k] == EPI_PAGED_VALUE) {
                             e.layout[k] = EPI_F32, e.rope[k] = 0, e.f16[k] = 0;
                             take[k].clear();
                         }
+                    }
                 e.kvh = w.pw[1], e.hs = w.pw[2], e.bs = w.pw[3];
             }
             // nothing between the GEMV and an absorbed dispatch touches what
@@ -1130,7 +1196,7 @@ class Lowering {
                 e.rp.corr1 = __builtin_bit_cast(float, (int32_t)rope->x[7]);
                 epos = rpos;
                 if (rope->x[8]) eff = rff;
-                if (batched) {  // one (cos, sin) table per positions and parameters, the first launch writes it
+                if (batched && T <= 16) {  // one (cos, sin) table per positions and parameters, the first launch writes it
                     std::vector<int64_t> key = {rpos.buf, rpos.index, rpos.off, rff.buf, rff.index, rff.off, e.ne0, T};
                     for (int q = 0; q < 9; ++q) key.push_back(rope->x[q]);
                     auto it = rt_tables_.find(key);
@@ -1151,7 +1217,7 @@ class Lowering {
             if (!batched) g.kind = D_GEMV_PRO;
             g.has_epi = 1;
             g.epi = e;
-            for (int k = 0; k < 3; ++k) g.edst[k] = edst[k], g.eidx[k] = eidx[k];
+            for (int k = 0; k < 3; ++k) g.edst[k] = edst[k], g.eidx[k] = eidx[k], g.edst2[k] = edst2[k];
             g.epos = epos;
             g.eff = eff;
             for (size_t j : all) {
@@ -1727,6 +1793,7 @@ struct tlh_program {
                     for (int k = 0; k < 3; ++k) {
                         e.dst[k] = (char *)resolve(x.edst[k], state);
                         e.idx[k] = (const char *)resolve(x.eidx[k], state);
+                        e.dst2[k] = (char *)resolve(x.edst2[k], state);
                     }
                     e.pos = (const int32_t *)resolve(x.epos, state);
                     e.ff = (const float *)resolve(x.eff, state);

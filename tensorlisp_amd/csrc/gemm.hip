@@ -438,6 +438,31 @@ int64_t gemm_partial_bytes(int wtype, int64_t M, int64_t N, int64_t K, int64_t b
     return ks > 1 ? (int64_t)ks * batches * N * M * 4 : 0;
 }
 
+static tlh_status launch_gemm_q4k(const MatmulArgs &a, int ks, hipStream_t stream) {
+    const int64_t batches = a.ne12 * a.ne13;
+    // the kernel addresses the f16 activation codes by 32-bit byte offsets
+    if ((double)a.N_total * (double)batches * (double)a.K * 2.0 >= 4294967296.0)
+        return set_error(TLH_UNSUPPORTED, "gemm: activation codes of %lld x %lld x %lld exceed 4 GiB",
+                         (long long)a.N_total, (long long)batches, (long long)a.K);
+    const int nw = gemm_nw(a.N);
+    const dim3 grid((unsigned)((a.N + 32 * nw - 1) / (32 * nw)), (unsigned)((a.M + GBM - 1) / GBM), (unsigned)(batches * ks));
+    const bool q4 = a.wtype == TLH_TYPE_Q4_K;
+    if (nw == 8 && q4) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q4_K, 8>), grid, dim3(512), 0, stream, a);
+    else if (nw == 8) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q5_K, 8>), grid, dim3(512), 0, stream, a);
+    else if (q4) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q4_K, 4>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q5_K, 4>), grid, dim3(256), 0, stream, a);
+    return check_launch("gemm_q4k");
+}
+
+tlh_status launch_gemm_epi(const MatmulArgs &a, const GemvEpi &ep, hipStream_t stream) {
+    const int ks = gemm_ksplit(a.wtype, a.M, a.N, a.K, a.ne12 * a.ne13);
+    if ((a.wtype != TLH_TYPE_Q4_K && a.wtype != TLH_TYPE_Q5_K) || ks < 2 || !a.part)
+        return set_error(TLH_UNSUPPORTED, "gemm: the store epilogue rides on the reduce of a K-split q4_K / q5_K GEMM");
+    tlh_status st = reduce_epi_check(a, ep);
+    if (st == TLH_OK) st = launch_gemm_q4k(a, ks, stream);
+    return st != TLH_OK ? st : launch_partial_reduce_epi(a, ks, ep, stream);
+}
+
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
     const int64_t batches = a.ne12 * a.ne13;
     const int ks = gemm_ksplit(a.wtype, a.M, a.N, a.K, batches);
@@ -447,18 +472,7 @@ tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
         return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
     }
     if (a.wtype == TLH_TYPE_Q4_K || a.wtype == TLH_TYPE_Q5_K) {
-        // the kernel addresses the f16 activation codes by 32-bit byte offsets
-        if ((double)a.N_total * (double)batches * (double)a.K * 2.0 >= 4294967296.0)
-            return set_error(TLH_UNSUPPORTED, "gemm: activation codes of %lld x %lld x %lld exceed 4 GiB",
-                             (long long)a.N_total, (long long)batches, (long long)a.K);
-        const int nw = gemm_nw(a.N);
-        const dim3 grid((unsigned)((a.N + 32 * nw - 1) / (32 * nw)), (unsigned)((a.M + GBM - 1) / GBM), (unsigned)(batches * ks));
-        const bool q4 = a.wtype == TLH_TYPE_Q4_K;
-        if (nw == 8 && q4) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q4_K, 8>), grid, dim3(512), 0, stream, a);
-        else if (nw == 8) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q5_K, 8>), grid, dim3(512), 0, stream, a);
-        else if (q4) hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q4_K, 4>), grid, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((k_gemm_q4k<TLH_TYPE_Q5_K, 4>), grid, dim3(256), 0, stream, a);
-        const tlh_status st = check_launch("gemm_q4k");
+        const tlh_status st = launch_gemm_q4k(a, ks, stream);
         return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
     }
     for (int64_t c = 0; c < a.N; c += 16) {

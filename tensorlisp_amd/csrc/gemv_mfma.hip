@@ -1242,6 +1242,190 @@ tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t st
     return check_launch("partial_reduce");
 }
 
+// The reduce with the few-column kernel's store epilogue (GemvEpi), for a
+// K-split GEMM over Q / K / V segments at many tokens (a prefill): element
+// (m, n) = the sum of the chunks' partials in chunk order (as
+// k_gemv_mfma_reduce), then rotated with its pair partner m ^ 1 (the
+// neighbouring lane: rotated segments start at even rows), cast and stored
+// into the segment's layout for token n -- and, with ep.dual[s], also into
+// the segment's paged pool (dst2: the key or value layout). A workgroup takes
+// 256 rows x RE_TOK tokens: the tokens' rotation (cos, sin) per pair and
+// every token's sum of partials first (the CPU's chain of products, once per
+// token and pair), then token by token the row-contiguous stores; the paged stores last, from LDS,
+// with the lanes walking a value's tokens (or a key's 8-element groups)
+// fastest, so consecutive slots of a block are written together. One batch
+// slice; grid (rows / 256, columns / RE_TOK).
+constexpr int RE_PAIRS = 256;  // ne0 <= 512
+constexpr int RE_TOK = 16;
+__global__ void __launch_bounds__(256) k_reduce_epi(const MatmulArgs a, int chunks, const GemvEpi ep) {
+    kernarg_prefetch<(kernarg_lines(sizeof(MatmulArgs) + sizeof(int) + sizeof(GemvEpi)))>();
+    __shared__ float2 s_t[RE_TOK * RE_PAIRS];  // (cos, sin) of token t, pair pr at t * np + pr
+    __shared__ uint16_t s_h[RE_TOK][256];      // f16 results for the paged stores
+    __shared__ int64_t s_slot[3][RE_TOK];
+    const int tid = threadIdx.x;
+    const int64_t m = (int64_t)blockIdx.x * 256 + tid;
+    const bool mvalid = m < a.M;
+    const int64_t mc = mvalid ? m : a.M - 1;
+    const int64_t cstride = a.N * a.M;
+    const int64_t nb = (int64_t)blockIdx.y * RE_TOK;
+    const int nt = (int)(a.N - nb < RE_TOK ? a.N - nb : RE_TOK);
+    auto sel = [](int s, auto x0, auto x1, auto x2) { return s == 0 ? x0 : s == 1 ? x1 : x2; };
+    auto seg_of = [&](int64_t r) { return (int)(r >= a.seg_m0[1]) + (int)(a.nseg > 2 && r >= a.seg_m0[2]); };
+    const int sg = seg_of(mc);
+    const int64_t j = mc - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]);
+    const int lay = sel(sg, ep.layout[0], ep.layout[1], ep.layout[2]);
+    const bool rot = sel(sg, ep.rope[0], ep.rope[1], ep.rope[2]) != 0;
+    const bool h16 = sel(sg, ep.f16[0], ep.f16[1], ep.f16[2]) != 0;
+    const int64_t seg_rows = sel(sg, a.seg_m0[1], a.seg_m0[2], a.seg_m0[3]) - sel(sg, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]);
+    const bool any_rot = ep.rope[0] | ep.rope[1] | ep.rope[2];
+    const bool any_dual = ep.dual[0] | ep.dual[1] | ep.dual[2];
+    const int np = any_rot ? (int)((ep.rp.n_dims < ep.ne0 ? ep.rp.n_dims : ep.ne0) / 2) : 0;
+    // the tokens' rotations and row / slot indices
+    for (int i = tid; i < nt * np; i += 256) {
+        const int t = i / np, pr = i - t * np;
+        float cs, sn;
+        rope_cs_sn((float)ep.pos[a.n0 + nb + t], pr, ep.ff ? ep.ff[pr] : 1.0f, ep.rp, cs, sn);
+        s_t[i] = make_float2(cs, sn);
+    }
+    if (tid < 3 * RE_TOK) {
+        const int s3 = tid / RE_TOK, t = tid % RE_TOK;
+        const char *ip = sel(s3, ep.idx[0], ep.idx[1], ep.idx[2]);
+        int64_t r = -1;
+        if (ip && t < nt) {
+            const int64_t tok = a.n0 + nb + t;
+            r = sel(s3, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2]) ? ((const int64_t *)ip)[tok]
+                                                                     : (int64_t)((const int32_t *)ip)[tok];
+            if (r >= sel(s3, ep.rows[0], ep.rows[1], ep.rows[2])) r = -1;
+        }
+        s_slot[s3][t] = r;
+    }
+    // every token's sum first: the stores below may alias the partials for
+    // all the compiler knows, so loads after a store would wait for it
+    // (chunk by chunk, the tokens' loads of a chunk issued together; each sum
+    // still adds the chunks in order)
+    float vs[RE_TOK];
+#pragma unroll
+    for (int t = 0; t < RE_TOK; ++t) vs[t] = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        const float *pc = a.part + c * cstride + mc;
+#pragma unroll
+        for (int t = 0; t < RE_TOK; ++t) vs[t] += pc[(nb + (t < nt ? t : 0)) * a.M];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < RE_TOK; ++t) {
+        if (t >= nt) break;
+        const int64_t n = nb + t, tok = a.n0 + n;
+        const float v = vs[t];
+        const float o = __shfl_xor(v, 1, 64);
+        float y = v;
+        if (rot) {
+            const uint32_t el = (uint32_t)j % (uint32_t)ep.ne0, pr = el / 2;  // rows below 2^31 (launcher)
+            if ((int)pr < np) {
+                const float2 c2 = s_t[t * np + pr];
+                y = (el & 1) == 0 ? rope_first(v, o, c2.x, c2.y) : rope_second(o, v, c2.x, c2.y);
+            }
+        }
+        const uint16_t yh = f2h(y);
+        if (any_dual) s_h[t][tid] = yh;
+        if (!mvalid) continue;
+        if (lay == EPI_F32) {
+            *(float *)((char *)sel(sg, a.seg_dst[0], a.seg_dst[1], a.seg_dst[2]) +
+                       tok * sel(sg, a.seg_d_nb1[0], a.seg_d_nb1[1], a.seg_d_nb1[2]) + j * 4) = v;
+            continue;
+        }
+        char *base = sel(sg, ep.dst[0], ep.dst[1], ep.dst[2]);
+        int64_t at;  // element offset
+        if (lay == EPI_CONTIG) {
+            at = tok * seg_rows + j;
+        } else {
+            const int64_t r = s_slot[sg][t];
+            if (r < 0) continue;
+            if (lay == EPI_CACHE_ROW) {
+                base += r * sel(sg, ep.row_nb[0], ep.row_nb[1], ep.row_nb[2]);
+                at = j;
+            } else {
+                const uint32_t ru = (uint32_t)r, bs = (uint32_t)ep.bs, hs = (uint32_t)ep.hs, ju = (uint32_t)j;
+                const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, e = ju % hs;
+                at = lay == EPI_PAGED_KEY ? (((blk * ep.kvh + h) * (ep.hs / 8) + e / 8) * ep.bs + off) * 8 + e % 8
+                                          : ((blk * ep.kvh + h) * ep.hs + e) * ep.bs + off;
+            }
+        }
+        if (h16) ((uint16_t *)base)[at] = yh;
+        else ((float *)base)[at] = y;
+    }
+    if (!any_dual) return;
+    __syncthreads();
+    // the paged stores: element (row rr, token t) of the block; a key pool
+    // keeps 8 elements of a token together, a value pool a block's tokens
+    const bool keys = sel(seg_of((int64_t)blockIdx.x * 256), ep.dual[0], ep.dual[1], ep.dual[2]) == EPI_PAGED_KEY;
+    for (int idx = tid; idx < 256 * nt; idx += 256) {
+        int rr, t;
+        if (keys) {
+            const int g8 = idx / (8 * nt), w = idx - g8 * 8 * nt;
+            t = w / 8, rr = 8 * g8 + (w & 7);
+        } else {
+            rr = idx / nt, t = idx - rr * nt;
+        }
+        const int64_t mr = (int64_t)blockIdx.x * 256 + rr;
+        if (mr >= a.M) continue;
+        const int s2 = seg_of(mr);
+        const int l2 = sel(s2, ep.dual[0], ep.dual[1], ep.dual[2]);
+        const int64_t r = s_slot[s2][t];
+        if (!l2 || r < 0) continue;
+        const uint32_t ru = (uint32_t)r, bs = (uint32_t)ep.bs, hs = (uint32_t)ep.hs;
+        const uint32_t ju = (uint32_t)(mr - sel(s2, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]));
+        const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, e = ju % hs;
+        const int64_t at = l2 == EPI_PAGED_KEY ? (((blk * ep.kvh + h) * (ep.hs / 8) + e / 8) * ep.bs + off) * 8 + e % 8
+                                               : ((blk * ep.kvh + h) * ep.hs + e) * ep.bs + off;
+        ((uint16_t *)sel(s2, ep.dst2[0], ep.dst2[1], ep.dst2[2]))[at] = s_h[t][rr];
+    }
+}
+
+// What the store epilogue needs of the launch's segments and of ep (shared by
+// the few-column kernel's and the reduce's epilogues).
+static tlh_status epi_check(const MatmulArgs &a, const GemvEpi &ep, const char *who) {
+    if (a.nseg < 1 || a.M >= ((int64_t)1 << 31) || a.ids || a.ne12 * a.ne13 != 1)
+        return set_error(TLH_UNSUPPORTED, "%s: the store epilogue takes segments of one batch slice", who);
+    bool rope = false;
+    for (int sg = 0; sg < a.nseg; ++sg) {
+        const int64_t rows = a.seg_m0[sg + 1] - a.seg_m0[sg];
+        if (ep.layout[sg] != EPI_F32 && !ep.dst[sg]) return set_error(TLH_INVALID, "%s: epilogue without a destination", who);
+        if ((ep.layout[sg] == EPI_CACHE_ROW || ep.layout[sg] >= EPI_PAGED_KEY) && !ep.idx[sg])
+            return set_error(TLH_INVALID, "%s: epilogue row or slot index missing", who);
+        if (ep.rows[sg] >= ((int64_t)1 << 31))
+            return set_error(TLH_UNSUPPORTED, "%s: epilogue cache rows or pool slots past 2^31", who);
+        if (ep.layout[sg] >= EPI_PAGED_KEY && (!ep.f16[sg] || !ep.idx_i64[sg] || ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 ||
+                                               ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs))
+            return set_error(TLH_UNSUPPORTED, "%s: paged epilogue geometry", who);
+        if (ep.rope[sg]) {
+            rope = true;
+            if (ep.ne0 < 2 || ep.ne0 % 2 || ep.ne0 > 512 || rows % ep.ne0 || a.seg_m0[sg] % 2)
+                return set_error(TLH_UNSUPPORTED, "%s: rotated segments are whole heads of even size", who);
+        }
+        if (ep.dual[sg] && (ep.layout[sg] != EPI_CONTIG || !ep.f16[sg] || !ep.dst2[sg] || !ep.idx[sg] ||
+                            !ep.idx_i64[sg] || (ep.dual[sg] != EPI_PAGED_KEY && ep.dual[sg] != EPI_PAGED_VALUE) ||
+                            ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 || ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs))
+            return set_error(TLH_UNSUPPORTED, "%s: a second, paged store goes with contiguous f16 rows", who);
+    }
+    if (rope && (!ep.pos || ep.rp.mode != 0 || ep.rp.n_dims % 2 || ep.rp.n_dims < 0))
+        return set_error(TLH_UNSUPPORTED, "%s: the epilogue rotates in ROPE mode 0 only", who);
+    return TLH_OK;
+}
+
+tlh_status reduce_epi_check(const MatmulArgs &a, const GemvEpi &ep) { return epi_check(a, ep, "reduce"); }
+
+tlh_status launch_partial_reduce_epi(const MatmulArgs &a, int chunks, const GemvEpi &ep, hipStream_t stream) {
+    const tlh_status st = epi_check(a, ep, "reduce");
+    if (st != TLH_OK) return st;
+    if (a.M <= 0 || a.N <= 0) return TLH_OK;
+    if ((a.N + RE_TOK - 1) / RE_TOK >= 65536)
+        return set_error(TLH_UNSUPPORTED, "reduce: %lld columns through the store epilogue", (long long)a.N);
+    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((a.N + RE_TOK - 1) / RE_TOK), 1u);
+    hipLaunchKernelGGL(k_reduce_epi, grid, dim3(256), 0, stream, a, chunks, ep);
+    return check_launch("partial_reduce (epilogue)");
+}
+
 static int64_t sk_share(int64_t K, int64_t &chunks) {
     const int64_t units = (K + 255) / 256;
     const int64_t per = (int64_t)SK_MAXW * sk_ks<TLH_TYPE_Q4_K>();
@@ -1297,28 +1481,10 @@ template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool stage
 // The few-column kernel with the store epilogue (segments, q4_K / q5_K / q6_K,
 // K a multiple of 256 in one chunk, rows and segment rows below 2^31).
 tlh_status launch_gemv_mfma_epi(const MatmulArgs &a, const GemvEpi &ep, hipStream_t stream) {
-    if (!gemv_mfma_supported(a.N) || a.nseg < 1 || a.K % 256 != 0 || a.M >= ((int64_t)1 << 31) || a.ids ||
-        a.ne12 * a.ne13 != 1)
-        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes segments of one batch slice");
-    bool rope = false;
-    for (int sg = 0; sg < a.nseg; ++sg) {
-        const int64_t rows = a.seg_m0[sg + 1] - a.seg_m0[sg];
-        if (ep.layout[sg] != EPI_F32 && !ep.dst[sg]) return set_error(TLH_INVALID, "gemv_mfma: epilogue without a destination");
-        if ((ep.layout[sg] == EPI_CACHE_ROW || ep.layout[sg] >= EPI_PAGED_KEY) && !ep.idx[sg])
-            return set_error(TLH_INVALID, "gemv_mfma: epilogue row or slot index missing");
-        if (ep.rows[sg] >= ((int64_t)1 << 31))
-            return set_error(TLH_UNSUPPORTED, "gemv_mfma: epilogue cache rows or pool slots past 2^31");
-        if (ep.layout[sg] >= EPI_PAGED_KEY && (!ep.f16[sg] || !ep.idx_i64[sg] || ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 ||
-                                               ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs))
-            return set_error(TLH_UNSUPPORTED, "gemv_mfma: paged epilogue geometry");
-        if (ep.rope[sg]) {
-            rope = true;
-            if (ep.ne0 < 2 || ep.ne0 % 2 || ep.ne0 > 512 || rows % ep.ne0 || a.seg_m0[sg] % 2)
-                return set_error(TLH_UNSUPPORTED, "gemv_mfma: rotated segments are whole heads of even size");
-        }
-    }
-    if (rope && (!ep.pos || ep.rp.mode != 0 || ep.rp.n_dims % 2 || ep.rp.n_dims < 0))
-        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the epilogue rotates in ROPE mode 0 only");
+    if (!gemv_mfma_supported(a.N) || a.K % 256 != 0 || (ep.dual[0] | ep.dual[1] | ep.dual[2]))
+        return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes N <= 16, K %% 256 == 0, one store a row");
+    const tlh_status st = epi_check(a, ep, "gemv_mfma");
+    if (st != TLH_OK) return st;
     if (ep.rt_mode && (!ep.rt || ((uintptr_t)ep.rt & 7)))
         return set_error(TLH_INVALID, "gemv_mfma: the rotation table needs an 8-byte aligned buffer");
     if (ep.rt_mode == 2 && a.N * epi_table_pairs(ep) > 4 * 256)  // RT_PER entries a thread, at least 4 waves

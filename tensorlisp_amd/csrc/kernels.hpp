@@ -147,6 +147,12 @@ struct GemvEpi {
     // 0: computed here only
     float *rt = nullptr;
     int rt_mode = 0;
+    // the K-split GEMM's reduce only: an EPI_CONTIG f16 segment also stored
+    // into a paged pool (dual[s] = EPI_PAGED_KEY / EPI_PAGED_VALUE, dst2[s]
+    // the pool, idx / rows / kvh / hs / bs as for a paged layout): a prefill's
+    // keys and values, read as rows by its attention and kept in the pools
+    int dual[3] = {0, 0, 0};
+    char *dst2[3] = {nullptr, nullptr, nullptr};
 };
 struct GemvPro {
     const float *p = nullptr, *q = nullptr, *w = nullptr;
@@ -194,12 +200,19 @@ tlh_status launch_gemv_mfma_epi(const MatmulArgs &a, const GemvEpi &ep, hipStrea
 tlh_status launch_gemm_q8(const MatmulArgs &a, int ksplit, hipStream_t stream);
 // dst (strided, columns n0..) = sum over `chunks` partials [chunk][batch][N][M] of a.part, in chunk order
 tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t stream);
+// the same through GemvEpi's store epilogue (segments, one batch slice);
+// reduce_epi_check: TLH_OK when it takes a and ep
+tlh_status launch_partial_reduce_epi(const MatmulArgs &a, int chunks, const GemvEpi &ep, hipStream_t stream);
+tlh_status reduce_epi_check(const MatmulArgs &a, const GemvEpi &ep);
 // K chunks of the tiled prefill GEMMs: a launch of fewer 128 x 128 tiles than
 // CUs splits K into up to 512 / tiles chunks (whole stages per chunk, at least four super-blocks /
 // sixteen q8_0 blocks each), and the bytes of its partial sums.
 int gemm_ksplit(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches);
 int64_t gemm_partial_bytes(int wtype, int64_t M, int64_t N, int64_t K, int64_t batches);
 tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream);  // any N, from the scratch
+// q4_K / q5_K GEMM whose K chunks' reduce stores through ep (the launch must
+// split K); TLH_UNSUPPORTED otherwise, before anything is launched
+tlh_status launch_gemm_epi(const MatmulArgs &a, const GemvEpi &ep, hipStream_t stream);
 
 // Dense FLASH_ATTN_EXT over f16 K/V (flash_attn.hip). Strides in bytes;
 // scale already divided by softcap when softcap != 0; mask may be null.

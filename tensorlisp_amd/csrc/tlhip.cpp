@@ -595,9 +595,10 @@ size_t tlh::mul_mat_compute_multi_scratch_bytes(const tlh_op *const *ops, int n)
 }
 
 // With epi (the executor's batched Q / K / V projection): the few-column
-// kernel stores through the epilogue (N <= 16, one K chunk); TLH_UNSUPPORTED
-// when it cannot take the shapes or pointers (the executor then runs the
-// absorbed dispatches after a plain launch).
+// kernel stores through the epilogue (N <= 16, one K chunk), or above 16
+// columns the q4_K / q5_K GEMM's K-chunk reduce does (the GEMM must split K);
+// TLH_UNSUPPORTED when neither can take the shapes or pointers (the executor
+// then runs the absorbed dispatches after a plain launch).
 tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n,
                                       const void *scratch, size_t scratch_bytes, hipStream_t stream,
                                       const GemvEpi *epi) {
@@ -636,10 +637,8 @@ tlh_status tlh::mul_mat_compute_multi(const tlh_op *const *ops, const void *cons
     m.seg_m0[3] = rows;
     for (int i = n; i < 3; ++i) m.seg_m0[i] = rows;
     m.M = rows;
-    if (epi) {
-        if (s.N > 16) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_multi: the store epilogue takes N <= 16");
-        return launch_gemv_mfma_epi(m, *epi, stream);
-    }
+    if (epi)  // few columns: the GEMV's own stores; many: the K-split GEMM's reduce
+        return s.N > 16 ? launch_gemm_epi(m, *epi, stream) : launch_gemv_mfma_epi(m, *epi, stream);
     return s.N > 16 ? launch_gemm(m, stream) : launch_gemv_mfma(m, stream);
 }
 
