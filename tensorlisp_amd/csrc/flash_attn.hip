@@ -55,6 +55,25 @@ __device__ __forceinline__ fa_half4 as_h4(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(fa_half4, make_uint2(lo, hi));
 }
 
+typedef _Float16 fa_half8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ fa_f32x4 fa_mfma32(fa_half8 a, fa_half8 b, fa_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ fa_half8 as_h8(uint4 v) { return __builtin_bit_cast(fa_half8, v); }
+
+// max over lanes c, c + 16, c + 32, c + 48 (the four lane groups of a
+// 16 x 16 MFMA output column), with gfx950's lane-swap moves instead of LDS
+// permutes: permlane32_swap(v, v) gives (v[l % 32], v[32 + l % 32]) in lane l,
+// permlane16_swap(v, v) the lanes l and l ^ 16 of each 32-lane half.
+__device__ __forceinline__ float max_across_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ uint32_t word(const uint4 &v, int w) { return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w; }
 
 // Key-row geometry: full 32-dim chunks (one 16-byte load, two MFMA steps
@@ -397,11 +416,21 @@ __global__ void __launch_bounds__(256) k_flash_attn(const FaArgs a) {
 // 16-byte chunks XOR-swizzled by the key (chunk q of key c at position
 // q ^ (c % 16)), so the A-operand reads of 16 keys hit distinct banks; V rows
 // as they are (the B-operand pieces of one key are contiguous). Per wave and
-// 16-key step the arithmetic is k_flash_attn's (S^T = K . Q^T, online softmax
-// on S^T's lane layout, O += P . V on 8 output tiles); no key partitions.
+// 32-key step the products run on gfx950's v_mfma_f32_16x16x32_f16 (S^T = K .
+// Q^T, online softmax on S^T's lane layout in the log2 domain, O += P . V on 8
+// output tiles); a step whose mask values are all zero skips the mask
+// arithmetic; no key partitions.
 constexpr int FR_TK = 64;    // keys per tile
 constexpr int FR_ROW = 256;  // bytes of a K / V row (128 f16)
+constexpr int FR_KV = FR_TK * FR_ROW;           // bytes of a tile's K (or V) rows
+constexpr int FR_BUF = 2 * FR_KV + 64 * FR_TK * 2;  // a tile buffer: K, V, the f16 mask tile
 typedef __attribute__((address_space(3))) void fa_lds_void;
+
+// 16 bytes a lane from global memory straight to LDS (lane l's bytes land at
+// lds + 16 l)
+__device__ __forceinline__ void dma16(const void *g, fa_lds_void *lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
 
 struct FaRowsArgs {
     FaArgs f;
@@ -412,15 +441,16 @@ struct FaRowsArgs {
 template <bool MASK>
 __global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
     const FaArgs &a = ra.f;
-    // two buffers as four separate arrays, each named statically where it is
-    // read or filled: the compiler then sees that the reads of one buffer do not
-    // overlap the direct-to-LDS loads into the other, and inserts no wait for
-    // those loads before every read
-    __shared__ __attribute__((aligned(16))) uint8_t K0[FR_TK][FR_ROW], K1[FR_TK][FR_ROW];
-    __shared__ __attribute__((aligned(16))) uint8_t V0[FR_TK][FR_ROW], V1[FR_TK][FR_ROW];
-    __shared__ __attribute__((aligned(16))) uint16_t M0[64][FR_TK], M1[64][FR_TK];  // mask tiles: row 16 rg + c
+    // two tile buffers (K rows, V rows, then the 64 x 64 mask tile, row
+    // 16 rg + c), each a separate array named statically where it is read or
+    // filled: the compiler then sees that the reads of one buffer do not overlap
+    // the direct-to-LDS loads into the other, and inserts no wait for those
+    // loads before every read
+    __shared__ __attribute__((aligned(16))) uint8_t T0[FR_BUF], T1[FR_BUF];
     __shared__ float Mo[4][16][128], Mm[4][16], Ml[4][16];  // the key halves' merge
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index in a scalar register: the per-wave step conditions below
+    // are then scalar branches, not exec masks
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rg = wave & 3, kh = wave >> 2;  // row group, key half
     const int g = lane >> 4, c = lane & 15;
     const int gw = ra.gw, qpw = 64 / gw;  // queries per workgroup
@@ -436,18 +466,28 @@ __global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
     const int L = a.L;
 
     // Q^T operand of the wave's rows (row c: query iq of head h), rounded to f16
-    fa_half4 qb[8];
-    {
+    // (B operand of S^T = K . Q^T on v_mfma_f32_16x16x32_f16: lane (c, g) holds
+    // row c's dims 32 s + 8 g .. + 7 for step s)
+    // (loaded after the first tile's loads are issued, so the two latencies
+    // overlap; all eight loads go out before any is used. A row past nq reads
+    // row nq - 1 instead: its results are never stored)
+    fa_half8 qb[4];
+    auto load_q = [&](float4 (&qv)[4][2]) {
         const float *qrow = (const float *)(a.q + iqc * a.q_nb1 + h * a.q_nb2 + ib * a.q_nb3);
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int d0 = 32 * (st / 2) + 8 * g + 4 * (st % 2);
-            fa_half4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (_Float16)qrow[d0 + e];
-            qb[st] = rlive ? v : (fa_half4){};
+        for (int st = 0; st < 4; ++st) {
+            qv[st][0] = *(const float4 *)(qrow + 32 * st + 8 * g);
+            qv[st][1] = *(const float4 *)(qrow + 32 * st + 8 * g + 4);
         }
-    }
+    };
+    auto convert_q = [&](const float4 (&qv)[4][2]) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const float4 lo = qv[st][0], hi = qv[st][1];
+            qb[st] = (fa_half8){(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                                (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+        }
+    };
     float slope = 1.0f;
     const char *mdma = nullptr;  // the mask row this lane's DMA fills: row 8 wave + lane / 8, keys 8 (lane % 8) ..
     if constexpr (MASK) {
@@ -467,110 +507,137 @@ __global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
     // (l % 16) ^ (key % 16) of the row; V: chunk l % 16). Keys past L read
     // row L - 1 (their scores are masked).
     const int ntiles = (L + FR_TK - 1) / FR_TK;
-    auto load_tile = [&](int t, uint8_t (&Kd)[FR_TK][FR_ROW], uint8_t (&Vd)[FR_TK][FR_ROW]) {
+    auto load_tile = [&](int t, uint8_t (&Td)[FR_BUF]) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int kk = 4 * (2 * wave + i) + (lane >> 4);
             const int key = min(FR_TK * t + kk, L - 1);
             const int pos = lane & 15;
-            __builtin_amdgcn_global_load_lds((const void *)(kb + (int64_t)key * a.k_nb1 + 16 * (pos ^ (kk & 15))),
-                                             (fa_lds_void *)&Kd[4 * (2 * wave + i)][0], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void *)(vb + (int64_t)key * a.v_nb1 + 16 * pos),
-                                             (fa_lds_void *)&Vd[4 * (2 * wave + i)][0], 16, 0, 0);
+            dma16(kb + (int64_t)key * a.k_nb1 + 16 * (pos ^ (kk & 15)), (fa_lds_void *)(Td + 4 * (2 * wave + i) * FR_ROW));
+            dma16(vb + (int64_t)key * a.v_nb1 + 16 * pos, (fa_lds_void *)(Td + FR_KV + 4 * (2 * wave + i) * FR_ROW));
         }
     };
     // the mask tile (64 rows x 64 keys) straight to LDS with K and V: wave w
     // fills rows 8w .. 8w + 7, lane l 16 bytes (keys 8 (l % 8) ..) of row
     // 8w + l / 8. L is a multiple of 8, so no 8-key chunk straddles the end;
     // chunks past it reread the last one (those keys are masked by index).
-    auto load_mask = [&](int t, uint16_t (&Md)[64][FR_TK]) {
+    auto load_mask = [&](int t, uint8_t (&Td)[FR_BUF]) {
         if constexpr (MASK) {
             const int key = min(FR_TK * t + 8 * (lane & 7), L - 8);
-            __builtin_amdgcn_global_load_lds((const void *)(mdma + 2 * key), (fa_lds_void *)&Md[8 * wave][0], 16, 0, 0);
+            dma16(mdma + 2 * key, (fa_lds_void *)(Td + 2 * FR_KV + 8 * wave * FR_TK * 2));
         }
     };
 
-    // Online softmax with lazy rescaling: m_ref, the value the exponentials are
-    // taken against, moves to the running max only when that has grown by more
-    // than 8 (then O and l are rescaled); otherwise p = exp(s - m_ref) <= e^8,
-    // well inside f16 for the P operand, and the final O / l is unchanged.
+    // Online softmax with lazy rescaling, in the log2 domain (x = s * log2 e):
+    // m_ref, the value the exponentials are taken against, moves to the
+    // running max only when that has grown by more than 8 (then O and l are
+    // rescaled); otherwise p = 2^(x - m_ref) <= 2^8, well inside f16 for the P
+    // operand, and the final O / l is unchanged.
+    constexpr float LOG2E = 1.4426950408889634f;
+    const float cs = scale * LOG2E;
     float m_ref = -INFINITY, l_run = 0.0f;
     fa_f32x4 o[8];
 #pragma unroll
     for (int n = 0; n < 8; ++n) o[n] = (fa_f32x4){};
 
-    // tile t from (Kc, Vc) with mask values mkc, while tile t + 1 goes to
-    // (Kn, Vn) and its mask values to mkn; this wave takes the tile's keys
-    // 32 kh .. + 31 as one step of two 16-key halves
-    auto tile = [&](int t, const uint8_t (&Kc)[FR_TK][FR_ROW], const uint8_t (&Vc)[FR_TK][FR_ROW],
-                    uint8_t (&Kn)[FR_TK][FR_ROW], uint8_t (&Vn)[FR_TK][FR_ROW], const uint16_t (&Mc)[64][FR_TK],
-                    uint16_t (&Mn)[64][FR_TK]) {
+    // tile t from buffer Tc, while tile t + 1 goes to Tn; this
+    // wave takes the tile's keys 32 kh .. + 31 as one step of two 16-key
+    // halves. S^T of a half is four v_mfma_f32_16x16x32_f16 (lane (c, g): key
+    // c's dims 32 s + 8 g .. + 7, one 16-byte LDS read); its lane layout (key
+    // 16 hf + 4 g + r, row c) is, over both halves, exactly the A operand of
+    // O += P . V with the step's 32 keys in the order (4 g .. 4 g + 3, 16 + 4 g
+    // .. + 3) for lane group g -- and the V operand takes its keys in the same
+    // order: lane (c, g) reads those 8 keys' 16-byte pieces at dims 8 c .. + 7,
+    // and output tile m (dims 8 c + m) gets element m of each (four byte
+    // permutes).
+    auto tile = [&](int t, const uint8_t (&Tc)[FR_BUF], uint8_t (&Tn)[FR_BUF]) {
         if (t + 1 < ntiles) {  // the other buffer: free since the last barrier
-            load_tile(t + 1, Kn, Vn);
-            load_mask(t + 1, Mn);
+            load_tile(t + 1, Tn);
+            load_mask(t + 1, Tn);
         }
         const int kt = FR_TK * t + 32 * kh;  // first key of this wave's step
-        // this lane's mask values: row c of the group, keys 4g .. 4g + 3 of each half
-        uint32_t mkc[2][4];
-        if constexpr (MASK) {
+        uint4 kf[2][4];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const uint2 mw = *(const uint2 *)&Mc[16 * rg + c][32 * kh + 16 * hf + 4 * g];
-                mkc[hf][0] = mw.x & 0xffffu, mkc[hf][1] = mw.x >> 16, mkc[hf][2] = mw.y & 0xffffu, mkc[hf][3] = mw.y >> 16;
-            }
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint8_t *kr = Tc + (32 * kh + 16 * hf + c) * FR_ROW;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) kf[hf][s] = *(const uint4 *)(kr + 16 * ((4 * s + g) ^ c));
         }
-        // nothing live for any of the wave's rows in its 32 keys: skip (uniform)
-        bool live = kt < L;
+        // V pieces: keys 16 hf + 4g + j of the step, dims 8c .. 8c + 7 (read with
+        // the keys, so their latency overlaps the S^T products)
+        uint4 vf[2][4];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vf[hf][j] = *(const uint4 *)(Tc + FR_KV + (32 * kh + 16 * hf + 4 * g + j) * FR_ROW + 16 * c);
+        // this lane's mask values: row c of the group, keys 4g .. 4g + 3 of each half.
+        // A step whose keys are all inside L and whose mask values are all +-0 for
+        // every row of the wave (and no soft cap) takes the plain path: s + slope * 0
+        // is s.
+        uint2 mw[2] = {};
+        bool plain = kt + 32 <= L && softcap == 0.0f;
         if constexpr (MASK) {
-            bool any = false;
-#pragma unroll
-            for (int st = 0; st < 2; ++st)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) any = any || (mkc[st][r] != 0xfc00u && kt + 16 * st + 4 * g + r < L);
-            live = live && __builtin_amdgcn_ballot_w64(any && rlive) != 0;
-        }
-        if (live) {
-            // S^T (key 4g + r, row c) of both halves: four independent chains
-            fa_f32x4 S[2];
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                fa_f32x4 S0 = (fa_f32x4){}, S1 = (fa_f32x4){};
-                const uint8_t *kr = &Kc[32 * kh + 16 * hf + c][0];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint4 kf = *(const uint4 *)(kr + 16 * ((4 * i + g) ^ c));
-                    S0 = fa_mfma(as_h4(kf.x, kf.y), qb[2 * i], S0);
-                    S1 = fa_mfma(as_h4(kf.z, kf.w), qb[2 * i + 1], S1);
-                }
-                S[hf] = S0 + S1;
-            }
-            // V pieces: keys 4g + j of each half, dims 8c .. 8c + 7
-            uint4 vf[2][4];
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) vf[hf][j] = *(const uint4 *)&Vc[32 * kh + 16 * hf + 4 * g + j][16 * c];
-            float x[2][4], mx = -INFINITY;
+                mw[hf] = *(const uint2 *)(Tc + 2 * FR_KV + ((16 * rg + c) * FR_TK + 32 * kh + 16 * hf + 4 * g) * 2);
+            plain = plain && __builtin_amdgcn_ballot_w64(((mw[0].x | mw[0].y | mw[1].x | mw[1].y) & 0x7fff7fffu) != 0) == 0;
+        }
+        auto mk = [&](int hf, int r) -> uint32_t {
+            const uint32_t w = r < 2 ? mw[hf].x : mw[hf].y;
+            return r & 1 ? w >> 16 : w & 0xffffu;
+        };
+        // nothing live for any of the wave's rows in its 32 keys: skip (uniform)
+        bool live = kt < L;
+        if (!plain) {
+            bool any = false;
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float sv = S[hf][r] * scale;
-                    if (softcap != 0.0f) sv = softcap * tanhf(sv);
-                    if constexpr (MASK) {
-                        const float mv = slope * h2f((uint16_t)mkc[hf][r]);
-                        sv = mv == -INFINITY ? -INFINITY : sv + mv;
-                    }
-                    x[hf][r] = kt + 16 * hf + 4 * g + r < L ? sv : -INFINITY;
-                    mx = fmaxf(mx, x[hf][r]);
+                    bool k_live = kt + 16 * hf + 4 * g + r < L;
+                    if constexpr (MASK) k_live = k_live & (mk(hf, r) != 0xfc00u);
+                    any = any | k_live;
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            live = live && __builtin_amdgcn_ballot_w64(any && rlive) != 0;
+        }
+        if (live) {
+            fa_f32x4 S[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                fa_f32x4 S0 = fa_mfma32(as_h8(kf[hf][0]), qb[0], (fa_f32x4){});
+                fa_f32x4 S1 = fa_mfma32(as_h8(kf[hf][1]), qb[1], (fa_f32x4){});
+                S0 = fa_mfma32(as_h8(kf[hf][2]), qb[2], S0);
+                S1 = fa_mfma32(as_h8(kf[hf][3]), qb[3], S1);
+                S[hf] = S0 + S1;
+            }
+            float x[2][4];
+            if (plain) {
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[hf][r] = S[hf][r] * cs;
+            } else {
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float sv = S[hf][r] * scale;
+                        if (softcap != 0.0f) sv = softcap * tanhf(sv);
+                        if constexpr (MASK) {
+                            const float mv = slope * h2f((uint16_t)mk(hf, r));
+                            sv = mv == -INFINITY ? -INFINITY : sv + mv;
+                        }
+                        x[hf][r] = kt + 16 * hf + 4 * g + r < L ? sv * LOG2E : -INFINITY;
+                    }
+            }
+            float mx = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                             fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+            mx = max_across_groups(mx);
             // row c's new reference when its max grew by more than 8 (or was -inf)
             const bool grow = mx > m_ref + 8.0f || (m_ref == -INFINITY && mx != -INFINITY);
             if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // some row rescales: O and l of every row
                 const float m_new = grow ? mx : m_ref;
-                const float alpha = m_ref == -INFINITY ? 1.0f : __expf(m_ref - m_new);
+                const float alpha = m_ref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
                 m_ref = m_new;
                 l_run *= alpha;
                 float ao[4];
@@ -582,41 +649,43 @@ __global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
                     for (int r = 0; r < 4; ++r) o[n][r] *= ao[r];
             }
             const bool none = m_ref == -INFINITY;
-            fa_half4 pa[2];
+            float pr[2][4];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                float pr[4];
+            for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) pr[r] = none ? 0.0f : __expf(x[hf][r] - m_ref);
-                l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-                pa[hf] = (fa_half4){(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
-            }
+                for (int r = 0; r < 4; ++r) pr[hf][r] = none ? 0.0f : __builtin_amdgcn_exp2f(x[hf][r] - m_ref);
+            l_run += ((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) + ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]));
+            const fa_half8 pa = {(_Float16)pr[0][0], (_Float16)pr[0][1], (_Float16)pr[0][2], (_Float16)pr[0][3],
+                                 (_Float16)pr[1][0], (_Float16)pr[1][1], (_Float16)pr[1][2], (_Float16)pr[1][3]};
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
                 const int w = n / 2;
                 const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const uint32_t lo = __builtin_amdgcn_perm(word(vf[hf][1], w), word(vf[hf][0], w), sel);
-                    const uint32_t hi = __builtin_amdgcn_perm(word(vf[hf][3], w), word(vf[hf][2], w), sel);
-                    o[n] = fa_mfma(pa[hf], as_h4(lo, hi), o[n]);
-                }
+                uint4 b;
+                b.x = __builtin_amdgcn_perm(word(vf[0][1], w), word(vf[0][0], w), sel);
+                b.y = __builtin_amdgcn_perm(word(vf[0][3], w), word(vf[0][2], w), sel);
+                b.z = __builtin_amdgcn_perm(word(vf[1][1], w), word(vf[1][0], w), sel);
+                b.w = __builtin_amdgcn_perm(word(vf[1][3], w), word(vf[1][2], w), sel);
+                o[n] = fa_mfma32(pa, as_h8(b), o[n]);
             }
         }
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile t + 1 landed
-        __syncthreads();
+        lds_barrier();
     };
 
-    // even tiles in buffer 0, odd ones in buffer 1
+    // even tiles in buffer 0, odd ones in buffer 1; q's loads go out with tile 0's
     if (ntiles > 0) {
-        load_tile(0, K0, V0);
-        load_mask(0, M0);
+        load_tile(0, T0);
+        load_mask(0, T0);
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();
+    float4 qv[4][2];
+    load_q(qv);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile 0 and q landed
+    convert_q(qv);
+    lds_barrier();
     for (int t = 0; t < ntiles; t += 2) {
-        tile(t, K0, V0, K1, V1, M0, M1);
-        if (t + 1 < ntiles) tile(t + 1, K1, V1, K0, V0, M1, M0);
+        tile(t, T0, T1);
+        if (t + 1 < ntiles) tile(t + 1, T1, T0);
     }
 
     // merge the key halves: the second wave of each row group hands its
@@ -640,7 +709,8 @@ __global__ void __launch_bounds__(512) k_flash_attn_rows(const FaRowsArgs ra) {
         const float m0 = __shfl(m_ref, row, 64), l0 = __shfl(l_run, row, 64);
         const float m1 = Mm[rg][row], l1 = Ml[rg][row];
         const float M = fmaxf(m0, m1);
-        const float f0 = m0 == -INFINITY ? 0.0f : __expf(m0 - M), f1 = m1 == -INFINITY ? 0.0f : __expf(m1 - M);
+        const float f0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+        const float f1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
         const float lsum = f0 * l0 + f1 * l1;
         const int orow = q0 + row;
         if (orow >= a.nq) continue;
@@ -787,9 +857,10 @@ tlh_status launch_flash_attn(const FlashAttnDesc &d, hipStream_t stream) {
         const int gw = pl.G % 4 == 0 ? 4 : pl.G % 2 == 0 ? 2 : 1;
         const int64_t QB = (d.nq + 64 / gw - 1) / (64 / gw), HC = pl.G / gw;
         auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
-        bool ok = QB * HC * d.nhkv * d.nb >= 128 && al16(d.k) && al16(d.v) && al16(d.dst) &&
+        bool ok = QB * HC * d.nhkv * d.nb >= 128 && al16(d.q) && al16(d.k) && al16(d.v) && al16(d.dst) &&
                   (!mask || (a.mask_vec && d.L % 8 == 0));
-        for (int i = 1; i < 4; ++i) ok = ok && d.k_nb[i] % 16 == 0 && d.v_nb[i] % 16 == 0 && d.d_nb[i] % 16 == 0;
+        for (int i = 1; i < 4; ++i)
+            ok = ok && d.q_nb[i] % 16 == 0 && d.k_nb[i] % 16 == 0 && d.v_nb[i] % 16 == 0 && d.d_nb[i] % 16 == 0;
         if (ok && QB * HC < 65536) {
             FaRowsArgs ra;
             ra.f = a;
