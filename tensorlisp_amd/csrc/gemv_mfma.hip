@@ -1257,11 +1257,15 @@ tlh_status launch_partial_reduce(const MatmulArgs &a, int chunks, hipStream_t st
 // slice; grid (rows / 256, columns / RE_TOK).
 constexpr int RE_PAIRS = 256;  // ne0 <= 512
 constexpr int RE_TOK = 16;
+constexpr int RE_CH = 4;  // chunks whose partials are requested before the rotation work
 __global__ void __launch_bounds__(256) k_reduce_epi(const MatmulArgs a, int chunks, const GemvEpi ep) {
     kernarg_prefetch<(kernarg_lines(sizeof(MatmulArgs) + sizeof(int) + sizeof(GemvEpi)))>();
     __shared__ float2 s_t[RE_TOK * RE_PAIRS];  // (cos, sin) of token t, pair pr at t * np + pr
-    __shared__ uint16_t s_h[RE_TOK][256];      // f16 results for the paged stores
-    __shared__ int64_t s_slot[3][RE_TOK];
+    __shared__ __attribute__((aligned(16))) uint16_t s_h[RE_TOK][256];  // f16 results for the paged stores
+    // per thread (so every thread writes its entry: a write behind a branch
+    // lets the compiler sink the load that feeds it behind the partials')
+    __shared__ int64_t s_slot[256];  // [3][RE_TOK]: segment s's slot of token t at s * RE_TOK + t
+    __shared__ float s_ff[256], s_pos[256];
     const int tid = threadIdx.x;
     const int64_t m = (int64_t)blockIdx.x * 256 + tid;
     const bool mvalid = m < a.M;
@@ -1280,33 +1284,56 @@ __global__ void __launch_bounds__(256) k_reduce_epi(const MatmulArgs a, int chun
     const bool any_rot = ep.rope[0] | ep.rope[1] | ep.rope[2];
     const bool any_dual = ep.dual[0] | ep.dual[1] | ep.dual[2];
     const int np = any_rot ? (int)((ep.rp.n_dims < ep.ne0 ? ep.rp.n_dims : ep.ne0) / 2) : 0;
-    // the tokens' rotations and row / slot indices
+    // Loads go out in the order their values are needed (vector loads complete
+    // in order): the tokens' positions, the pairs' frequency factors and the
+    // slot indices, then the partials of up to RE_CH chunks, so the rotation
+    // work below runs while the partials land (the stores further down may
+    // alias the partials for all the compiler knows, so every load comes
+    // before them). Every load is unconditional, from a clamped address.
+    // (an absent pointer reads the partials instead; the value is dropped)
+    const int64_t tok0 = a.n0 + nb;
+    const int32_t pos_raw = (ep.pos ? ep.pos : (const int32_t *)a.part)[tok0 + (tid < nt ? tid : 0)];
+    const uint32_t ff_raw = (ep.ff ? (const uint32_t *)ep.ff : (const uint32_t *)a.part)[tid < np ? tid : 0];
+    const int s3 = tid < 3 * RE_TOK ? tid / RE_TOK : 0, t3 = tid % RE_TOK;
+    const bool i64 = sel(s3, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2]) != 0;
+    const char *ip3 = sel(s3, ep.idx[0], ep.idx[1], ep.idx[2]);
+    const char *ipl = (ip3 ? ip3 : (const char *)a.part) + (tok0 + (t3 < nt ? t3 : 0)) * (i64 ? 8 : 4);
+    const uint32_t idx_lo = *(const uint32_t *)ipl, idx_hi = *(const uint32_t *)(ipl + (i64 ? 4 : 0));
+    float pv[RE_CH][RE_TOK];
+    const int ch0 = chunks < RE_CH ? chunks : RE_CH;
+#pragma unroll
+    for (int c = 0; c < RE_CH; ++c) {
+        const float *pc = a.part + (c < ch0 ? c : 0) * cstride + mc;
+#pragma unroll
+        for (int t = 0; t < RE_TOK; ++t) pv[c][t] = pc[(nb + (t < nt ? t : 0)) * a.M];
+    }
+    // the row / slot indices, positions and factors to LDS (the waits cover
+    // those first loads only), then the tokens' rotations
+    {
+        int64_t r = i64 ? (int64_t)(((uint64_t)idx_hi << 32) | idx_lo) : (int64_t)(int32_t)idx_lo;
+        const bool bad = (tid >= 3 * RE_TOK) | (t3 >= nt) | (ip3 == nullptr) | (r >= sel(s3, ep.rows[0], ep.rows[1], ep.rows[2]));
+        s_slot[tid] = bad ? -1 : r;
+    }
+    s_pos[tid] = (float)pos_raw;
+    s_ff[tid] = ep.ff ? __uint_as_float(ff_raw) : 1.0f;
+    lds_barrier();  // LDS only: the partials stay in flight
     for (int i = tid; i < nt * np; i += 256) {
         const int t = i / np, pr = i - t * np;
         float cs, sn;
-        rope_cs_sn((float)ep.pos[a.n0 + nb + t], pr, ep.ff ? ep.ff[pr] : 1.0f, ep.rp, cs, sn);
+        rope_cs_sn(s_pos[t], pr, s_ff[pr], ep.rp, cs, sn);
         s_t[i] = make_float2(cs, sn);
     }
-    if (tid < 3 * RE_TOK) {
-        const int s3 = tid / RE_TOK, t = tid % RE_TOK;
-        const char *ip = sel(s3, ep.idx[0], ep.idx[1], ep.idx[2]);
-        int64_t r = -1;
-        if (ip && t < nt) {
-            const int64_t tok = a.n0 + nb + t;
-            r = sel(s3, ep.idx_i64[0], ep.idx_i64[1], ep.idx_i64[2]) ? ((const int64_t *)ip)[tok]
-                                                                     : (int64_t)((const int32_t *)ip)[tok];
-            if (r >= sel(s3, ep.rows[0], ep.rows[1], ep.rows[2])) r = -1;
-        }
-        s_slot[s3][t] = r;
-    }
-    // every token's sum first: the stores below may alias the partials for
-    // all the compiler knows, so loads after a store would wait for it
-    // (chunk by chunk, the tokens' loads of a chunk issued together; each sum
-    // still adds the chunks in order)
+    // every token's sum, adding the chunks in order (chunks past RE_CH, if
+    // any, load here)
     float vs[RE_TOK];
 #pragma unroll
     for (int t = 0; t < RE_TOK; ++t) vs[t] = 0.0f;
-    for (int c = 0; c < chunks; ++c) {
+#pragma unroll
+    for (int c = 0; c < RE_CH; ++c)
+#pragma unroll
+        for (int t = 0; t < RE_TOK; ++t)
+            if (c < ch0) vs[t] += pv[c][t];
+    for (int c = RE_CH; c < chunks; ++c) {
         const float *pc = a.part + c * cstride + mc;
 #pragma unroll
         for (int t = 0; t < RE_TOK; ++t) vs[t] += pc[(nb + (t < nt ? t : 0)) * a.M];
@@ -1339,7 +1366,7 @@ __global__ void __launch_bounds__(256) k_reduce_epi(const MatmulArgs a, int chun
         if (lay == EPI_CONTIG) {
             at = tok * seg_rows + j;
         } else {
-            const int64_t r = s_slot[sg][t];
+            const int64_t r = s_slot[sg * RE_TOK + t];
             if (r < 0) continue;
             if (lay == EPI_CACHE_ROW) {
                 base += r * sel(sg, ep.row_nb[0], ep.row_nb[1], ep.row_nb[2]);
@@ -1356,29 +1383,37 @@ __global__ void __launch_bounds__(256) k_reduce_epi(const MatmulArgs a, int chun
     }
     if (!any_dual) return;
     __syncthreads();
-    // the paged stores: element (row rr, token t) of the block; a key pool
-    // keeps 8 elements of a token together, a value pool a block's tokens
-    const bool keys = sel(seg_of((int64_t)blockIdx.x * 256), ep.dual[0], ep.dual[1], ep.dual[2]) == EPI_PAGED_KEY;
-    for (int idx = tid; idx < 256 * nt; idx += 256) {
-        int rr, t;
-        if (keys) {
-            const int g8 = idx / (8 * nt), w = idx - g8 * 8 * nt;
-            t = w / 8, rr = 8 * g8 + (w & 7);
-        } else {
-            rr = idx / nt, t = idx - rr * nt;
-        }
+    // the paged stores. A key pool keeps 8 elements of a token together: one
+    // 16-byte store per (8-row group, token), consecutive threads on
+    // consecutive tokens (segments start at multiples of 8 rows and head
+    // sizes are multiples of 8, so a group is 8 elements e % 8 = 0..7 of one
+    // head). A value pool keeps a block's tokens together: one element per
+    // thread, consecutive threads on consecutive tokens.
+    for (int idx = tid; idx < 32 * nt; idx += 256) {
+        const int g8 = idx / nt, t = idx - g8 * nt, rr = 8 * g8;
         const int64_t mr = (int64_t)blockIdx.x * 256 + rr;
         if (mr >= a.M) continue;
         const int s2 = seg_of(mr);
-        const int l2 = sel(s2, ep.dual[0], ep.dual[1], ep.dual[2]);
-        const int64_t r = s_slot[s2][t];
-        if (!l2 || r < 0) continue;
+        const int64_t r = s_slot[s2 * RE_TOK + t];
+        if (sel(s2, ep.dual[0], ep.dual[1], ep.dual[2]) != EPI_PAGED_KEY || r < 0) continue;
         const uint32_t ru = (uint32_t)r, bs = (uint32_t)ep.bs, hs = (uint32_t)ep.hs;
         const uint32_t ju = (uint32_t)(mr - sel(s2, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]));
         const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, e = ju % hs;
-        const int64_t at = l2 == EPI_PAGED_KEY ? (((blk * ep.kvh + h) * (ep.hs / 8) + e / 8) * ep.bs + off) * 8 + e % 8
-                                               : ((blk * ep.kvh + h) * ep.hs + e) * ep.bs + off;
-        ((uint16_t *)sel(s2, ep.dst2[0], ep.dst2[1], ep.dst2[2]))[at] = s_h[t][rr];
+        const int64_t at = (((blk * ep.kvh + h) * (ep.hs / 8) + e / 8) * ep.bs + off) * 8;
+        *(uint4 *)((uint16_t *)sel(s2, ep.dst2[0], ep.dst2[1], ep.dst2[2]) + at) = *(const uint4 *)&s_h[t][rr];
+    }
+    for (int idx = tid; idx < 256 * nt; idx += 256) {
+        const int rr = idx / nt, t = idx - rr * nt;
+        const int64_t mr = (int64_t)blockIdx.x * 256 + rr;
+        if (mr >= a.M) continue;
+        const int s2 = seg_of(mr);
+        const int64_t r = s_slot[s2 * RE_TOK + t];
+        if (sel(s2, ep.dual[0], ep.dual[1], ep.dual[2]) != EPI_PAGED_VALUE || r < 0) continue;
+        const uint32_t ru = (uint32_t)r, bs = (uint32_t)ep.bs, hs = (uint32_t)ep.hs;
+        const uint32_t ju = (uint32_t)(mr - sel(s2, a.seg_m0[0], a.seg_m0[1], a.seg_m0[2]));
+        const int64_t blk = ru / bs, off = ru % bs, h = ju / hs, e = ju % hs;
+        ((uint16_t *)sel(s2, ep.dst2[0], ep.dst2[1], ep.dst2[2]))[((blk * ep.kvh + h) * ep.hs + e) * ep.bs + off] =
+            s_h[t][rr];
     }
 }
 
@@ -1405,7 +1440,8 @@ static tlh_status epi_check(const MatmulArgs &a, const GemvEpi &ep, const char *
         }
         if (ep.dual[sg] && (ep.layout[sg] != EPI_CONTIG || !ep.f16[sg] || !ep.dst2[sg] || !ep.idx[sg] ||
                             !ep.idx_i64[sg] || (ep.dual[sg] != EPI_PAGED_KEY && ep.dual[sg] != EPI_PAGED_VALUE) ||
-                            ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 || ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs))
+                            ep.kvh < 1 || ep.hs < 8 || ep.hs % 8 || ep.bs < 1 || rows != (int64_t)ep.kvh * ep.hs ||
+                            (ep.dual[sg] == EPI_PAGED_KEY && (a.seg_m0[sg] % 8 || ((uintptr_t)ep.dst2[sg] & 15)))))
             return set_error(TLH_UNSUPPORTED, "%s: a second, paged store goes with contiguous f16 rows", who);
     }
     if (rope && (!ep.pos || ep.rp.mode != 0 || ep.rp.n_dims % 2 || ep.rp.n_dims < 0))
