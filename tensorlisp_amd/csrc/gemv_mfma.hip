@@ -517,7 +517,108 @@ __host__ __device__ inline int epi_table_pairs(const GemvEpi &e) {
 // pair's other row is the neighbouring output of the same column), f16 cast,
 // cache-row or paged K / V write that follow a batched Q / K / V projection,
 // column n being token n (its position ep.pos[n], its row or slot ep.idx[s][n]).
-template <int WT, int KS, bool STAGED, typename EP = NoEpi>
+// Paired blocks (N <= 8). With at most 8 columns, half of a 16 x 16 output is
+// zero columns, yet every output takes the per-block f32 scaling. Instead
+// v_mfma_i32_16x16x64_i8 takes two 32-element blocks (q4_0 / q8_0) or
+// sub-blocks (q4_K / q5_K) 2p and 2p + 1 at once: lane group g carries 16
+// bytes of one block (groups 0, 1: block 2p, elements 16g..; groups 2, 3:
+// block 2p + 1, elements 16 (g - 2)..); the activation operand is block
+// diagonal -- lane (g, i) holds column i & 7's codes where i < 8 matches
+// g < 2, zeros elsewhere -- so output row i < 8 is column i's sum over block
+// 2p and row i >= 8 column i - 8's over block 2p + 1. A lane (g, j) then holds
+// weight row j's sums of columns 4 (g & 1) .. + 3 for one block, every output
+// useful: half the MFMAs and half the scaling per block of the unpaired form.
+// Both parities' partial sums of an output meet once per row group (lanes l
+// and l + 32). Within a parity the blocks are added in K order, so the f32
+// order of the block sums differs from the CPU's sequential loop (even and
+// odd blocks summed apart, then added).
+template <int WT> constexpr bool pair_type() {
+    return WT == TLH_TYPE_Q4_0 || WT == TLH_TYPE_Q8_0 || WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K;
+}
+__device__ __forceinline__ v4i mfma_i8_k64(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// One unit (256 elements) of a paired row group from the wave's staged LDS
+// copy at byte ub (the lane's weight row); A: the unit's four block-pair
+// activation operands; sdu: the unit's activation scales [slot][16 columns].
+// (Tried for q4_0: the nibbles as they are and 8 * the blocks' activation
+// code sums subtracted from the integer sums, which saves the bias trick's
+// three VALU operations per word but adds an LDS read per block: slower.)
+template <int WT>
+__device__ __forceinline__ void unit_mma_pair(const uint8_t *wbuf, uint32_t ub, const v4i (&A)[4], const float *sdu,
+                                              int g, float (&y)[4]) {
+    const int par = g >> 1, half = g & 1;  // block parity, 16-element half of the block
+    const v4i zero = {0, 0, 0, 0};
+    const uint32_t *w32 = (const uint32_t *)wbuf;
+    if constexpr (WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K) {
+        constexpr bool Q5 = WT == TLH_TYPE_Q5_K;
+        const uint4 h = *(const uint4 *)(wbuf + ub);
+        // the 6-bit scales / mins of sub-blocks 0..3 and 4..7 as bytes (get_scale_min_k4)
+        const uint32_t sc[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+        uint4 qh = {0, 0, 0, 0};
+        if constexpr (Q5) qh = *(const uint4 *)(wbuf + ub + 16 + 16 * half);
+        v4i S = zero, Mn = zero;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int s = 2 * p + par;  // this lane's sub-block
+            const uint4 q = *(const uint4 *)(wbuf + ub + (Q5 ? 48 : 16) + 32 * p + 16 * half);
+            const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {qh.x, qh.y, qh.z, qh.w};
+            v4i B;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t c = (qv[i] >> (4 * par)) & 0x0f0f0f0fu;
+                if constexpr (Q5) c |= ((hv[i] >> s) & 0x01010101u) << 4;
+                B[i] = (int)c;
+            }
+            const v4i Sp = mfma_i8_k64(A[p], B, zero);
+            const int scv = (int)__builtin_amdgcn_ubfe(sc[s >> 2], 8 * (s & 3), 8);
+            const uint32_t m4 = __builtin_amdgcn_perm(0u, mn[s >> 2], 0x01010101u * (uint32_t)(s & 3));
+            const v4i Bm = {(int)m4, (int)m4, (int)m4, (int)m4};
+            Mn = mfma_i8_k64(A[p], Bm, Mn);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] += __mul24(scv, Sp[r]);  // |Sp| < 2^16, sc < 64
+        }
+        const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
+        const float4 d8 = *(const float4 *)(sdu + 4 * half);
+        const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
+    } else {
+        constexpr int BB = block_bytes(WT);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t blk = ub + (2 * p + par) * BB;  // the lane's block (2-byte aligned)
+            v4i B;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (WT == TLH_TYPE_Q4_0) {  // low nibbles: elements 0..15, high: 16..31
+                    const uint32_t v = lds_u32(w32, blk + 2 + 4 * i);
+                    B[i] = (int)nib_minus8((v >> (4 * half)) & 0x0f0f0f0fu);
+                } else {
+                    B[i] = (int)lds_u32(w32, blk + 2 + 16 * half + 4 * i);
+                }
+            }
+            const v4i Sb = mfma_i8_k64(A[p], B, zero);
+            const float dw = h2f((uint16_t)lds_u32(w32, blk));
+            const float4 d8 = *(const float4 *)(sdu + (2 * p + par) * SK_COLS + 4 * half);
+            const float d8r[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (WT == TLH_TYPE_Q4_0)
+                    y[r] += ((float)Sb[r] * dw) * d8r[r];  // quants.c:255
+                else
+                    y[r] += (float)Sb[r] * (dw * d8r[r]);  // quants.c:475
+            }
+        }
+    }
+}
+
+// PAIR (N <= 8, whole units, q4_0 / q8_0 / q4_K / q5_K): block pairs per
+// v_mfma_i32_16x16x64_i8 as in k_gemv_cols below (unit_mma_pair); the A
+// registers then hold the unit's four block-pair operands.
+template <int WT, int KS, bool STAGED, typename EP = NoEpi, bool PAIR = false>
 __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t share, const EP ep) {
     kernarg_prefetch<kernarg_lines(sizeof(MatmulArgs) + 8 + sizeof(EP))>();
     constexpr bool EPI = !std::is_same<EP, NoEpi>::value;
@@ -659,13 +760,35 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // range). Every load goes out first, from clamped addresses; the masks
     // come after the last one (a use of a loaded value waits for every load
     // issued before it, so a mask between loads would split them in rounds).
+    static_assert(!PAIR || (pair_type<WT>() && KS == 1 && STAGED), "paired blocks: one staged unit a wave");
     long A[KS][8];
     const bool col_ok = wr < N;
     auto a_ok = [&](int t, int j) {
         const int64_t e = 256 * (u0 + t) + 32 * j;  // first element of the block / sub-block
         return col_ok && e < 256 * u_end && e < K;
     };
-    {
+    if constexpr (PAIR) {
+        // lane (g, i): column i & 7's codes 16 g .. of the unit's 64-element
+        // pair p (block 2p for rows i < 8 = groups 0, 1; 2p + 1 for rows i >=
+        // 8 = groups 2, 3), zero elsewhere
+        const int c = wr & 7;
+        const bool pa_ok = ((wr < 8) == (g < 2)) && c < N && u0 < u_end;
+        const int8_t *aq = act.qs + (arow0 + (c < N ? c : 0)) * K + 256 * (u0 < u_end ? u0 : u_begin) + 16 * g;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint4 q = ldu<uint4>(aq + 64 * p);
+            A[0][2 * p] = (long)(((uint64_t)q.y << 32) | q.x);
+            A[0][2 * p + 1] = (long)(((uint64_t)q.w << 32) | q.z);
+        }
+        for (int64_t i = threadIdx.x; i < (s_end - s_begin) * SK_COLS; i += blockDim.x) {
+            const int64_t b = s_begin + (i >> 4);
+            const int c2 = (int)(i & 15);
+            const float dv = act.d[(arow0 + (c2 < N ? c2 : 0)) * nblk + b];
+            sd[i] = c2 < N ? dv : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) A[0][j] = pa_ok ? A[0][j] : 0;
+    } else {
         const int8_t *aq = act.qs + (arow0 + (col_ok ? wr : 0)) * K;
 #pragma unroll
         for (int t = 0; t < KS; ++t)
@@ -824,6 +947,22 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
     // multiply one row group from the wave's LDS buffer
     auto process_staged = [&](int64_t grp, int parity, typename St::ExtraT dq) {
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (PAIR) {
+            if (u0 < u_end) {  // wave-uniform
+                v4i A2[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint64_t lo = (uint64_t)A[0][2 * p], hi = (uint64_t)A[0][2 * p + 1];
+                    A2[p] = (v4i){(int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi, (int)(uint32_t)(hi >> 32)};
+                }
+                unit_mma_pair<WT>(wbuf, (uint32_t)(wr * St::RB), A2, unit_slots(0), g, y);
+            }
+            // lanes g < 2 (columns 4 g + r) add the odd blocks' sums of lane l + 32
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] += __shfl_xor(y[r], 32);
+            finish(y, grp, parity);
+            return;
+        }
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
             if (u0 + t >= u_end) continue;  // wave-uniform
@@ -938,104 +1077,6 @@ __global__ void __launch_bounds__(1024) k_gemv_mfma(const MatmulArgs a, int64_t 
 // f32 order of the block sums within a row, which is the same here: blocks
 // in K order.
 constexpr int GC_WAVES = 16;
-
-// Paired blocks (N <= 8). With at most 8 columns, half of a 16 x 16 output is
-// zero columns, yet every output takes the per-block f32 scaling. Instead
-// v_mfma_i32_16x16x64_i8 takes two 32-element blocks (q4_0 / q8_0) or
-// sub-blocks (q4_K / q5_K) 2p and 2p + 1 at once: lane group g carries 16
-// bytes of one block (groups 0, 1: block 2p, elements 16g..; groups 2, 3:
-// block 2p + 1, elements 16 (g - 2)..); the activation operand is block
-// diagonal -- lane (g, i) holds column i & 7's codes where i < 8 matches
-// g < 2, zeros elsewhere -- so output row i < 8 is column i's sum over block
-// 2p and row i >= 8 column i - 8's over block 2p + 1. A lane (g, j) then holds
-// weight row j's sums of columns 4 (g & 1) .. + 3 for one block, every output
-// useful: half the MFMAs and half the scaling per block of the unpaired form.
-// Both parities' partial sums of an output meet once per row group (lanes l
-// and l + 32). Within a parity the blocks are added in K order, so the f32
-// order of the block sums differs from the CPU's sequential loop (even and
-// odd blocks summed apart, then added).
-template <int WT> constexpr bool pair_type() {
-    return WT == TLH_TYPE_Q4_0 || WT == TLH_TYPE_Q8_0 || WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K;
-}
-__device__ __forceinline__ v4i mfma_i8_k64(v4i a, v4i b, v4i c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-// One unit (256 elements) of a paired row group from the wave's staged LDS
-// copy at byte ub (the lane's weight row); A: the unit's four block-pair
-// activation operands; sdu: the unit's activation scales [slot][16 columns].
-// (Tried for q4_0: the nibbles as they are and 8 * the blocks' activation
-// code sums subtracted from the integer sums, which saves the bias trick's
-// three VALU operations per word but adds an LDS read per block: slower.)
-template <int WT>
-__device__ __forceinline__ void unit_mma_pair(const uint8_t *wbuf, uint32_t ub, const v4i (&A)[4], const float *sdu,
-                                              int g, float (&y)[4]) {
-    const int par = g >> 1, half = g & 1;  // block parity, 16-element half of the block
-    const v4i zero = {0, 0, 0, 0};
-    const uint32_t *w32 = (const uint32_t *)wbuf;
-    if constexpr (WT == TLH_TYPE_Q4_K || WT == TLH_TYPE_Q5_K) {
-        constexpr bool Q5 = WT == TLH_TYPE_Q5_K;
-        const uint4 h = *(const uint4 *)(wbuf + ub);
-        // the 6-bit scales / mins of sub-blocks 0..3 and 4..7 as bytes (get_scale_min_k4)
-        const uint32_t sc[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
-        const uint32_t mn[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
-        uint4 qh = {0, 0, 0, 0};
-        if constexpr (Q5) qh = *(const uint4 *)(wbuf + ub + 16 + 16 * half);
-        v4i S = zero, Mn = zero;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int s = 2 * p + par;  // this lane's sub-block
-            const uint4 q = *(const uint4 *)(wbuf + ub + (Q5 ? 48 : 16) + 32 * p + 16 * half);
-            const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {qh.x, qh.y, qh.z, qh.w};
-            v4i B;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t c = (qv[i] >> (4 * par)) & 0x0f0f0f0fu;
-                if constexpr (Q5) c |= ((hv[i] >> s) & 0x01010101u) << 4;
-                B[i] = (int)c;
-            }
-            const v4i Sp = mfma_i8_k64(A[p], B, zero);
-            const int scv = (int)__builtin_amdgcn_ubfe(sc[s >> 2], 8 * (s & 3), 8);
-            const uint32_t m4 = __builtin_amdgcn_perm(0u, mn[s >> 2], 0x01010101u * (uint32_t)(s & 3));
-            const v4i Bm = {(int)m4, (int)m4, (int)m4, (int)m4};
-            Mn = mfma_i8_k64(A[p], Bm, Mn);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] += __mul24(scv, Sp[r]);  // |Sp| < 2^16, sc < 64
-        }
-        const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
-        const float4 d8 = *(const float4 *)(sdu + 4 * half);
-        const float dy[4] = {d8.x, d8.y, d8.z, d8.w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] += (d * dy[r]) * (float)S[r] - (dmin * dy[r]) * (float)Mn[r];
-    } else {
-        constexpr int BB = block_bytes(WT);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t blk = ub + (2 * p + par) * BB;  // the lane's block (2-byte aligned)
-            v4i B;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (WT == TLH_TYPE_Q4_0) {  // low nibbles: elements 0..15, high: 16..31
-                    const uint32_t v = lds_u32(w32, blk + 2 + 4 * i);
-                    B[i] = (int)nib_minus8((v >> (4 * half)) & 0x0f0f0f0fu);
-                } else {
-                    B[i] = (int)lds_u32(w32, blk + 2 + 16 * half + 4 * i);
-                }
-            }
-            const v4i Sb = mfma_i8_k64(A[p], B, zero);
-            const float dw = h2f((uint16_t)lds_u32(w32, blk));
-            const float4 d8 = *(const float4 *)(sdu + (2 * p + par) * SK_COLS + 4 * half);
-            const float d8r[4] = {d8.x, d8.y, d8.z, d8.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (WT == TLH_TYPE_Q4_0)
-                    y[r] += ((float)Sb[r] * dw) * d8r[r];  // quants.c:255
-                else
-                    y[r] += (float)Sb[r] * (dw * d8r[r]);  // quants.c:475
-            }
-        }
-    }
-}
 
 template <int WT, bool PAIR>
 __global__ void __launch_bounds__(1024) k_gemv_cols(const MatmulArgs a) {
@@ -1475,10 +1516,10 @@ int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches
     return chunks > 1 ? chunks * batches * (N < SK_COLS ? N : SK_COLS) * M * 4 : 0;
 }
 
-template <int WT, bool STAGED, typename EP = NoEpi>
-static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream, const EP &ep = EP{}) {
+template <int WT, bool STAGED, typename EP = NoEpi, bool PAIR = false>
+static tlh_status launch_sk_form(const MatmulArgs &a, hipStream_t stream, const EP &ep) {
     constexpr int KS = sk_ks<WT>();
-    auto kern = k_gemv_mfma<WT, KS, STAGED, EP>;
+    auto kern = k_gemv_mfma<WT, KS, STAGED, EP, PAIR>;
     int64_t chunks = 1;
     const int64_t share = sk_share(a.K, chunks);
     if (chunks > 1 && !a.part) return set_error(TLH_INVALID, "gemv_mfma: K=%lld needs a partials buffer", (long long)a.K);
@@ -1501,9 +1542,18 @@ static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream, const EP &e
     if (!std::is_same<EP, NoEpi>::value && chunks != 1)
         return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes one K chunk");
     hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share, ep);
-    tlh_status st = check_launch("gemv_mfma");
+    tlh_status st = check_launch(PAIR ? "gemv_mfma (pairs)" : "gemv_mfma");
     if (st != TLH_OK || chunks == 1) return st;
     return launch_partial_reduce(a, (int)chunks, stream);
+}
+
+// Up to 8 columns of whole units: the paired-block form.
+template <int WT, bool STAGED, typename EP = NoEpi>
+static tlh_status launch_sk(const MatmulArgs &a, hipStream_t stream, const EP &ep = EP{}) {
+    if constexpr (pair_type<WT>() && STAGED && sk_ks<WT>() == 1) {
+        if (a.N <= 8 && a.K % 256 == 0) return launch_sk_form<WT, STAGED, EP, true>(a, stream, ep);
+    }
+    return launch_sk_form<WT, STAGED, EP, false>(a, stream, ep);
 }
 
 template <int WT> static tlh_status launch_sk_wt(const MatmulArgs &a, bool staged, hipStream_t stream) {
