@@ -6,7 +6,8 @@
 // and every block is reduced as the CPU's vec_dot does: exact int32 block
 // sums, scaled in f32 (ggml-cpu/quants.c:225-258, :451-476, :696-773).
 //  * N <= 2 with K a multiple of 64 up to 16384: the register-resident GEMV
-//    (gemv_reg.hip), which can also quantize src1 itself (one launch);
+//    (gemv_reg.hip), which can also quantize src1 itself (one launch); q4_0
+//    weights there need 4-byte aligned pointers and strides;
 //  * otherwise (N 3..16, or other K): the int8-MFMA few-column kernel
 //    (gemv_mfma.hip) from the scratch a quantize launch filled.
 #include "kernels.hpp"
@@ -19,12 +20,12 @@ namespace tlh {
 bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_bytes) {
     int ksplit, upw;
     return x != nullptr && a.N <= 2 && a.K <= 4096 && gemv_reg_geometry(a.K, ksplit, upw) && ((uintptr_t)x & 15) == 0 &&
-           (x_row_bytes & 15) == 0;
+           (x_row_bytes & 15) == 0 && gemv_reg_weights_ok(a);
 }
 
 static bool gemv_uses_reg(const MatmulArgs &a) {
     int ksplit, upw;
-    return a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw);
+    return a.N <= 2 && gemv_reg_geometry(a.K, ksplit, upw) && gemv_reg_weights_ok(a);
 }
 
 // N <= 2 with K the register kernel covers: the register-resident GEMV

@@ -29,6 +29,15 @@ static tlh_status launch_reg_type(const MatmulArgs &a, const float *x, int64_t x
     }
 }
 
+// q4_0 units are loaded as dwords (WRegs<TLH_TYPE_Q4_0>): every weight
+// pointer and stride a multiple of 4 (the row bytes are, for K % 64 == 0).
+bool gemv_reg_weights_ok(const MatmulArgs &a) {
+    if (a.wtype != TLH_TYPE_Q4_0) return true;
+    uintptr_t bits = (uintptr_t)a.w | (uintptr_t)a.w_nb1 | (uintptr_t)a.w_nb2 | (uintptr_t)a.w_nb3;
+    for (int sg = 0; sg < a.nseg; ++sg) bits |= (uintptr_t)a.seg_w[sg] | (uintptr_t)a.seg_w_nb1[sg];
+    return (bits & 3) == 0;
+}
+
 // The kernel's set-up arithmetic is 32-bit.
 static bool reg_counts_ok(const MatmulArgs &a) {
     const int64_t lim = (int64_t)1 << 31;
@@ -41,6 +50,7 @@ tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_by
     int ksplit = 1, upw = 64;
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     if (reg_plain_type(a.wtype)) return launch_gemv_reg_legacy(a, x, x_row_bytes, ksplit, upw, stream);
+    if (!gemv_reg_weights_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: q4_0 weights need 4-byte alignment");
     const GemvPro none;
     if (!x) return launch_reg_type<IN_SCRATCH, OUT_STORE>(a, nullptr, 0, none, ksplit, upw, stream);
     if (a.K > 4096) return set_error(TLH_INVALID, "gemv_reg: in-kernel quantization takes K <= 4096");
@@ -54,6 +64,7 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
     if (!gemv_reg_geometry(a.K, ksplit, upw)) return set_error(TLH_INVALID, "gemv_reg: K=%lld", (long long)a.K);
     if (a.ne12 * a.ne13 != 1) return set_error(TLH_INVALID, "gemv_reg: a prologue / epilogue takes one batch slice");
     if (reg_plain_type(a.wtype)) return set_error(TLH_UNSUPPORTED, "gemv_reg: no fused forms for weight type %d", a.wtype);
+    if (!gemv_reg_weights_ok(a)) return set_error(TLH_UNSUPPORTED, "gemv_reg: q4_0 weights need 4-byte alignment");
     const bool glu = pro.glu != nullptr;
     if (glu && (a.nseg != 2 || a.seg_m0[1] != a.seg_m0[2] - a.seg_m0[1]))
         return set_error(TLH_INVALID, "gemv_reg: the SwiGLU epilogue needs two segments of equal rows");

@@ -729,17 +729,25 @@ template <int R> struct WRegs<TLH_TYPE_Q4_1, R> : WRegsLegacy<TLH_TYPE_Q4_1, R> 
 template <int R> struct WRegs<TLH_TYPE_Q5_0, R> : WRegsLegacy<TLH_TYPE_Q5_0, R> {};
 template <int R> struct WRegs<TLH_TYPE_Q5_1, R> : WRegsLegacy<TLH_TYPE_Q5_1, R> {};
 
+// A unit is two 18-byte blocks, 36 bytes at a 4-byte aligned address (the
+// launcher checks the weight pointers and strides, gemv_reg_weights_ok):
+// three dword-aligned loads, and the first block's codes (bytes 2..17)
+// shifted into place, instead of 16-byte loads at 2-byte aligned addresses
+// and separate scale loads.
 template <int R> struct WRegs<TLH_TYPE_Q4_0, R> {
     uint4 w0[R], w1[R];
     float dw0[R], dw1[R];
     __device__ __forceinline__ void load(const uint8_t *const (&wrow)[R], int64_t u) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint8_t *blk = wrow[r] + u * (2 * Q4_0_BYTES);
-            dw0[r] = h2f(*(const uint16_t *)blk);
-            w0[r] = ldu16(blk + 2);
-            dw1[r] = h2f(*(const uint16_t *)(blk + Q4_0_BYTES));
-            w1[r] = ldu16(blk + Q4_0_BYTES + 2);
+            const uint32_t *blk = (const uint32_t *)(wrow[r] + u * (2 * Q4_0_BYTES));
+            const uint4 p0 = *(const uint4 *)blk, p1 = *(const uint4 *)(blk + 4);
+            const uint32_t p2 = blk[8];
+            dw0[r] = h2f((uint16_t)(p0.x & 0xffff));
+            w0[r] = make_uint4(__builtin_amdgcn_alignbyte(p0.y, p0.x, 2), __builtin_amdgcn_alignbyte(p0.z, p0.y, 2),
+                               __builtin_amdgcn_alignbyte(p0.w, p0.z, 2), __builtin_amdgcn_alignbyte(p1.x, p0.w, 2));
+            dw1[r] = h2f((uint16_t)(p1.x >> 16));
+            w1[r] = make_uint4(p1.y, p1.z, p1.w, p2);
         }
     }
     template <int NC>

@@ -169,6 +169,7 @@ struct GemvPro {
 // not read; otherwise it reads the scratch a quantize launch filled.
 tlh_status launch_gemv(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);
 bool gemv_fuses_quantize(const MatmulArgs &a, const float *x, int64_t x_row_bytes);
+bool gemv_reg_weights_ok(const MatmulArgs &a);
 // register-resident GEMV (gemv_reg.hip): K <= 16384, K % 64 == 0
 bool gemv_reg_geometry(int64_t K, int &ksplit, int &upw);
 tlh_status launch_gemv_reg(const MatmulArgs &a, const float *x, int64_t x_row_bytes, hipStream_t stream);

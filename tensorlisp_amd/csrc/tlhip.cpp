@@ -461,7 +461,9 @@ static int64_t mm_partial_bytes(const MulMatShape &s) {
     int ksplit, upw;
     const bool reg = s.N <= 2 && gemv_reg_geometry(s.K, ksplit, upw);
     if (s.N > 16 && has_gemm(s.wtype)) return align_up(gemm_partial_bytes(s.wtype, s.M, s.N, s.K, s.ne12 * s.ne13), 256);
-    const bool mfma = s.N <= 16 ? !reg : true;
+    // (q4_0 at N <= 2 takes the MFMA form when its weights are not 4-byte
+    // aligned, which only the pointers tell: reserve its partials too)
+    const bool mfma = s.N <= 16 ? (!reg || s.wtype == TLH_TYPE_Q4_0) : true;
     return mfma ? align_up(gemv_mfma_partial_bytes(s.K, s.M, s.N, s.ne12 * s.ne13), 256) : 0;
 }
 

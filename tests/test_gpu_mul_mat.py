@@ -277,6 +277,36 @@ def test_unaligned_activation_rows_take_the_quantize_launch(gpu, t, n):
     close(host(y), oracle().mul_mat(t, w, M, K, x[:, :K]), NAMES[t])
 
 
+@pytest.mark.parametrize("K", [4096, 14336])
+@pytest.mark.parametrize("n", [1, 2])
+def test_q4_0_weights_at_two_byte_offset(gpu, n, K):
+    """The register GEMV loads q4_0 units as dwords, so it takes 4-byte aligned
+    weights; weights at a 2-byte offset (allowed by the ABI) take the int8-MFMA
+    kernel instead -- after a quantize launch, K-split above 4096 -- with the
+    same result against the oracle."""
+    import ctypes as C
+
+    import torch
+
+    M = 130
+    w = synth.random_blocks(Q4_0, 996, M, K)
+    x = synth.normal(997, (n, K))
+    op = N.mul_mat_op(Q4_0, M, K, n)
+    nbytes = N.mul_mat_scratch_bytes(op)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    raw = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    raw[2:2 + w.size] = dev(w.reshape(-1))
+    xd = dev(x)
+    want = oracle().mul_mat(Q4_0, w, M, K, x)
+    for off in (0, 2):  # the aligned copy takes the register GEMV
+        wd = raw[off:] if off else dev(w)
+        y = torch.full((n, M), float("nan"), dtype=torch.float32, device="cuda")
+        N.check(N.lib().tlh_mul_mat(C.byref(op), C.c_void_p(wd.data_ptr()), C.c_void_p(xd.data_ptr()),
+                                    C.c_void_p(y.data_ptr()), C.c_void_p(scratch.data_ptr()), nbytes,
+                                    C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        close(host(y), want, f"q4_0 weights at offset {off}")
+
+
 @pytest.mark.parametrize("t", WTYPES, ids=[NAMES[t] for t in WTYPES])
 def test_split_phases_match_fused_node(gpu, t):
     """tlh_mul_mat_quantize + tlh_mul_mat_compute (the CPU's two phases) equal the
