@@ -931,9 +931,15 @@ struct NormChainArgs {
 };
 
 constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows up to 4096 in one read
+constexpr int64_t NC_SPLIT_ROWS = 64;  // fewer rows than this (quantized) split each row over its 1024-element groups
 
 // The weight row has the norm's length (the executor fuses only then), so
 // element i of a row multiplies w[i].
+// Split (gridDim.z > 1, rows of n <= 4096 quantized for a MUL_MAT): workgroup
+// z of a row still reads the whole row for its sums, but writes s, y and the
+// quantized blocks of group z only (elements 1024 z .. + 1023), so a few rows
+// spread over 4x the workgroups and the quantization does not lengthen one
+// workgroup's path by a whole row's.
 template <bool VEC>  // VEC: every row 16-byte aligned with n % 4 == 0, groups move as float4
 __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     kernarg_prefetch<(kernarg_lines(sizeof(NormChainArgs)))>();
@@ -980,16 +986,19 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
                 wv[j][e] = i < n ? wr[i] : 0.0f;
             }
     }
+    const bool split = gridDim.z > 1;
+    const int js = (int)blockIdx.z;  // split: the group this workgroup writes
+    auto mine = [&](int j) { return !split || j == js; };
     double s1 = 0.0;
 #pragma unroll
     for (int j = 0; j < NC_CACHE; ++j) {
         const int i0 = 4 * (t + 256 * j);
-        if (VEC && add && i0 < n) *(float4 *)(sr + i0) = make_float4(c[j][0], c[j][1], c[j][2], c[j][3]);
+        if (VEC && add && i0 < n && mine(j)) *(float4 *)(sr + i0) = make_float4(c[j][0], c[j][1], c[j][2], c[j][3]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = i0 + e;
             if (i < n) {
-                if (!VEC && add) sr[i] = c[j][e];
+                if (!VEC && add && mine(j)) sr[i] = c[j][e];
                 s1 += rms ? (double)(c[j][e] * c[j][e]) : (double)c[j][e];
             }
         }
@@ -1032,6 +1041,7 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
         const int i0 = 4 * (t + 256 * j);
 #pragma unroll
         for (int e = 0; e < 4; ++e) c[j][e] = ((c[j][e] - mean) * scale) * wv[j][e];  // y (kept for quantizing)
+        if (!mine(j)) continue;
         if (VEC) {
             if (i0 < n) *(float4 *)(yr + i0) = make_float4(c[j][0], c[j][1], c[j][2], c[j][3]);
         } else {
@@ -1047,7 +1057,19 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
         const int64_t row = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;  // = the activation row
         const ActLayout QL = act_layout(a.qo.type, n, a.qo.rows, a.qo.f16);
         const int lane = t & 63, w = t >> 6;
-        if (a.qo.type == TLH_TYPE_Q8_K) {
+        if (a.qo.type == TLH_TYPE_Q8_K && split) {
+#pragma unroll
+            for (int j = 0; j < NC_CACHE; ++j) {
+                if (j != js) continue;  // uniform
+                float cj[1][4] = {{c[j][0], c[j][1], c[j][2], c[j][3]}};
+                uint32_t pk[1];
+                int ps[1];
+                float d[1];
+                q8K_waves<1>(cj, lane, pk, ps, d);
+                if (1024 * j + 256 * w < n)  // wave-uniform (n % 256 == 0)
+                    q8K_store_split((char *)a.qo.out, QL, n, row, 4 * j + w, lane, pk[0], ps[0], d[0], a.qo.f16);
+            }
+        } else if (a.qo.type == TLH_TYPE_Q8_K) {
             uint32_t pk[NC_CACHE];
             int ps[NC_CACHE];
             float d[NC_CACHE];
@@ -1062,7 +1084,7 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
 #pragma unroll
             for (int j = 0; j < NC_CACHE; ++j) {
                 col[j] = 4 * (t + 256 * j);
-                live[j] = col[j] < n;  // whole 8-lane groups (n % 32 == 0)
+                live[j] = col[j] < n && mine(j);  // whole 8-lane groups (n % 32 == 0)
             }
             if (a.qo.type == TLH_TYPE_Q8_1)
                 q80_quads_store_split<NC_CACHE, true>(c, live, lane, (char *)a.qo.out, QL, n, row, col, a.qo.f16);
@@ -1105,10 +1127,14 @@ tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, con
         vec = ((uintptr_t)ps[k] & 15) == 0;
         for (int i = 1; i < 4; ++i) vec = vec && ts[k]->nb[i] % 16 == 0;
     }
+    // few rows quantized for a MUL_MAT (a batched decode step): one workgroup
+    // per 1024-element group of a row
+    dim3 grid = red_grid(rows);
+    if (a.qo.type && rows < NC_SPLIT_ROWS && op.t[0].ne[0] <= 4 * 256 * NC_CACHE) grid.z = (unsigned)((op.t[0].ne[0] + 1023) / 1024);
     if (vec)
-        hipLaunchKernelGGL(k_norm_chain<true>, red_grid(rows), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(k_norm_chain<true>, grid, dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(k_norm_chain<false>, red_grid(rows), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(k_norm_chain<false>, grid, dim3(256), 0, stream, a);
     return check_launch("norm_chain");
 }
 

@@ -1410,10 +1410,10 @@ class Lowering {
     // goes the same way. Needs: src1 is the producer's whole output,
     // contiguous f32 rows (a multiple of the block) in the same order, and
     // nothing between the two writes that storage. The scratch then lives from
-    // the producer on. (A norm chain works one row per workgroup: over few rows
-    // the quantization lengthens its one serial path by about what the
-    // separate launch costs, so there it stays apart.)
-    static constexpr int64_t NQ_MIN_ROWS = 64;
+    // the producer on. (A norm chain over few rows -- a batched decode step --
+    // spreads each row over its 1024-element groups, so the quantization does
+    // not lengthen one workgroup's path by a whole row's.)
+    static constexpr int64_t NQ_MIN_ROWS = 3;
     void fuse_act_quantize(std::vector<Dispatch> &d) {
         auto contiguous_f32 = [](const tlh_tensor &t) {
             return t.ty == TLH_TYPE_F32 && t.nb[0] == 4 && t.nb[1] == 4 * t.ne[0] && t.nb[2] == t.nb[1] * t.ne[1] &&

@@ -260,13 +260,14 @@ NQ_TYPES = [N.Q4_K, N.Q5_K, N.Q6_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0]
 
 
 @pytest.mark.parametrize("t", NQ_TYPES, ids=[N.TYPE_NAMES[t] for t in NQ_TYPES])
-@pytest.mark.parametrize("K,n,add", [(4096, 64, True), (1024, 100, False), (4096, 16, True)])
+@pytest.mark.parametrize("K,n,add", [(4096, 64, True), (1024, 100, False), (4096, 16, True), (2048, 3, False)])
 def test_norm_chain_quantizes_for_its_mul_mats(gpu, t, K, n, add):
-    """[ADD ->] RMS_NORM -> MUL feeding MUL_MATs over 64 or more rows (a
-    prefill): the norm kernel also writes the group's quantized activation
-    (q8_K / q8_0 / q8_1 codes, scales and sums; at n > 16 the q4_K GEMM's f16
-    codes and bsums too) and no quantize launch runs; over fewer rows (16) the
-    quantize launch stays. Either way the norm's outputs and every product are
+    """[ADD ->] RMS_NORM -> MUL feeding MUL_MATs over 3 or more rows: the norm
+    kernel also writes the group's quantized activation (q8_K / q8_0 / q8_1
+    codes, scales and sums; at n > 16 the q4_K GEMM's f16 codes and bsums too)
+    and no quantize launch runs. Below 64 rows (a batched decode step) each
+    row's 1024-element groups go to workgroups of their own, each reading the
+    whole row for the sums. Either way the norm's outputs and every product are
     bit-identical to the core ops and tlh_mul_mat run one by one. Over more
     than 16 rows the q4_K / q5_K products are one GEMM launch over the three
     matrices' rows (the first two whole 128-row tiles, the last not): its K
@@ -307,7 +308,7 @@ def test_norm_chain_quantizes_for_its_mul_mats(gpu, t, K, n, add):
     # dispatches: the norm chain, the quantize launch when it stays apart, then
     # the products (n <= 16: one few-column launch over all matrices' rows;
     # more rows: one GEMM launch for q4_K / q5_K, else one per matrix)
-    fused = n >= 64
+    fused = n >= 3
     merged = n <= 16 or t in (N.Q4_K, N.Q5_K)
     assert prog.stats()["launches"] == 1 + (0 if fused else 1) + (1 if merged else len(Ms))
 
