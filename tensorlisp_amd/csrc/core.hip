@@ -928,10 +928,12 @@ struct NormChainArgs {
     const float *p, *q, *w;
     float *s, *y;
     ActQuantOut qo;  // qo.type != 0: y also goes to a MUL_MAT's activation scratch
+    NormPartials qp;  // qp.chunks > 1: q's rows are sums of a MUL_MAT's K-split partials
 };
 
 constexpr int NC_CACHE = 4;  // groups of four a thread keeps in registers: rows up to 4096 in one read
-constexpr int64_t NC_SPLIT_ROWS = 64;  // fewer rows than this (quantized) split each row over its 1024-element groups
+constexpr int64_t NC_SPLIT_ROWS = 64;
+constexpr int NC_QCH = 4;  // K-split partial chunks a thread loads at once  // fewer rows than this (quantized) split each row over its 1024-element groups
 
 // The weight row has the norm's length (the executor fuses only then), so
 // element i of a row multiplies w[i].
@@ -950,17 +952,62 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
     int64_t i1, i2, i3;
     row_coords(blockIdx.x + (int64_t)gridDim.x * blockIdx.y, tp, i1, i2, i3);
     const float *pr = (const float *)((const char *)a.p + offs(tp, 0, i1, i2, i3));
-    const float *qr = add ? (const float *)((const char *)a.q + offs(tq, 0, i1, i2, i3)) : nullptr;
+    const bool qsum = add && a.qp.chunks > 1;  // q from the partials: row r at part + r * ne0
+    const int64_t prow = blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+    const float *qr = qsum ? a.qp.part + prow * tp.ne[0]
+                      : add ? (const float *)((const char *)a.q + offs(tq, 0, i1, i2, i3)) : nullptr;
+    // element i of q: the partials' sum in chunk order from 0, as the chunk-sum
+    // kernel forms it (k_gemv_mfma_reduce), or q itself
+    auto qval = [&](int i) {
+        if (!qsum) return qr[i];
+        float v = 0.0f;
+        for (int c = 0; c < a.qp.chunks; ++c) v += qr[c * a.qp.cstride + i];
+        return v;
+    };
+    auto qval4 = [&](int i) {
+        if (!qsum) return *(const float4 *)(qr + i);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < a.qp.chunks; ++c) {
+            const float4 g = *(const float4 *)(qr + c * a.qp.cstride + i);
+            v.x += g.x, v.y += g.y, v.z += g.z, v.w += g.w;
+        }
+        return v;
+    };
     float *sr = add ? (float *)((char *)a.s + offs(ts, 0, i1, i2, i3)) : nullptr;
     const float *wr = (const float *)((const char *)a.w + offs(tw, 0, i1 % tw.ne[1], i2 % tw.ne[2], i3 % tw.ne[3]));
     float *yr = (float *)((char *)a.y + offs(ty, 0, i1, i2, i3));
     const int n = (int)tp.ne[0];
     const int t = threadIdx.x;
-    auto value = [&](int i) { return add ? pr[i] + qr[i] : pr[i]; };
+    auto value = [&](int i) { return add ? pr[i] + qval(i) : pr[i]; };
     // thread t owns groups of four: elements 4 (t + 256 j) .. + 3; the weight
     // row is fetched with the values, so its latency overlaps the reduction
     float c[NC_CACHE][4], wv[NC_CACHE][4];
-    if constexpr (VEC) {
+    if (VEC && qsum && a.qp.chunks <= NC_QCH) {
+        // every load first, from clamped addresses (n % 4 == 0), then the sums:
+        // q in chunk order from 0, then p + q
+        float4 pv[NC_CACHE], w4[NC_CACHE], qv[NC_CACHE][NC_QCH];
+#pragma unroll
+        for (int j = 0; j < NC_CACHE; ++j) {
+            const int i = min(4 * (t + 256 * j), n - 4);
+            pv[j] = *(const float4 *)(pr + i);
+            w4[j] = *(const float4 *)(wr + i);
+#pragma unroll
+            for (int k = 0; k < NC_QCH; ++k)
+                qv[j][k] = *(const float4 *)(qr + (int64_t)min(k, a.qp.chunks - 1) * a.qp.cstride + i);
+        }
+#pragma unroll
+        for (int j = 0; j < NC_CACHE; ++j) {
+            const bool in = 4 * (t + 256 * j) < n;
+            float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < NC_QCH; ++k)
+                if (k < a.qp.chunks) g.x += qv[j][k].x, g.y += qv[j][k].y, g.z += qv[j][k].z, g.w += qv[j][k].w;
+            c[j][0] = in ? pv[j].x + g.x : 0.0f, c[j][1] = in ? pv[j].y + g.y : 0.0f;
+            c[j][2] = in ? pv[j].z + g.z : 0.0f, c[j][3] = in ? pv[j].w + g.w : 0.0f;
+            wv[j][0] = in ? w4[j].x : 0.0f, wv[j][1] = in ? w4[j].y : 0.0f;
+            wv[j][2] = in ? w4[j].z : 0.0f, wv[j][3] = in ? w4[j].w : 0.0f;
+        }
+    } else if constexpr (VEC) {
 #pragma unroll
         for (int j = 0; j < NC_CACHE; ++j) {
             const int i = 4 * (t + 256 * j);
@@ -968,7 +1015,7 @@ __global__ void __launch_bounds__(256) k_norm_chain(const NormChainArgs a) {
             if (i < n) {
                 v = *(const float4 *)(pr + i);
                 if (add) {
-                    const float4 g = *(const float4 *)(qr + i);
+                    const float4 g = qval4(i);
                     v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);
                 }
                 ww = *(const float4 *)(wr + i);
@@ -1103,7 +1150,7 @@ bool norm_chain_quantize_ok(const tlh_op &op, int act_type) {
 }
 
 tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
-                             hipStream_t stream, const ActQuantOut *qo) {
+                             hipStream_t stream, const ActQuantOut *qo, const NormPartials *qp) {
     NormChainArgs a;
     a.op = op;
     a.p = (const float *)p;
@@ -1113,6 +1160,13 @@ tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, con
     a.y = (float *)y;
     const int64_t rows = nrows(op.t[0]);
     if (rows == 0) return TLH_OK;
+    if (qp && qp->chunks > 1) {
+        // the partials hold rows of ne0 contiguous elements; q's own tensor is not read
+        if (!op.x[2] || !qp->part || ((uintptr_t)qp->part & 15) || qp->cstride < rows * op.t[0].ne[0] ||
+            qp->cstride % 4)
+            return set_error(TLH_INVALID, "norm_chain: partial sums for q");
+        a.qp = *qp;
+    }
     if (qo && qo->type) {
         if (!norm_chain_quantize_ok(op, qo->type) || !qo->out || ((uintptr_t)qo->out & 255) || qo->rows != rows)
             return set_error(TLH_INVALID, "norm_chain: cannot quantize rows of %lld into type %d",

@@ -87,6 +87,13 @@ struct Dispatch {
     GemvEpi epi;
     Place edst[3], eidx[3], epos, eff;
     Place edst2[3];  // the second (paged pool) store of a dual segment
+    // D_MUL_MAT / D_MM_COMPUTE: leave the K-split partials (no chunk-sum launch)
+    // for the norm chain that adds them; D_NORM_CHAIN: q's rows are the partials
+    // of dispatch pp_disp (pp_off bytes into its scratch; pp_chunks, pp_cstride)
+    int keep_part = 0;
+    int pp_disp = -1;
+    int pp_chunks = 0;
+    int64_t pp_off = 0, pp_cstride = 0;
     std::vector<Dispatch> absorbed;
 };
 
@@ -224,6 +231,7 @@ class Lowering {
         group_elementwise(out.d);
         fuse_act_quantize(out.d);
         group_elementwise(out.d);  // merged computes can leave element-wise launches adjacent
+        fuse_partials_into_norm(out.d);  // last: it refers to dispatches by index
         plan(out);
         return TLH_OK;
     }
@@ -1503,6 +1511,73 @@ class Lowering {
         d.swap(out);
     }
 
+    // A K-split MUL_MAT product whose only reader is the ADD of a norm chain
+    // (a layer's output or down projection at a batched decode step or a
+    // prefill, then the residual ADD and the next RMS_NORM): the product leaves
+    // its chunk partials in its scratch and the norm chain adds them in chunk
+    // order as it reads q (the bits the chunk-sum launch would have written),
+    // so that launch goes. The MUL_MAT's scratch then lives until the norm
+    // chain; the MUL_MAT's own output is never written.
+    void fuse_partials_into_norm(std::vector<Dispatch> &d) {
+        count_readers();
+        for (size_t i = 0; i < d.size(); ++i) {
+            Dispatch &nc = d[i];
+            if (nc.kind != D_NORM_CHAIN || nc.op.x[2] == 0 || nc.pp_disp >= 0) continue;
+            const int32_t add_id = node_of(nc);
+            for (int k = 0; k < 2; ++k) {
+                // the producer of operand k, with nothing in between writing it
+                int j = -1;
+                std::vector<Place> rd, wr;
+                for (int jj = (int)i - 1; jj >= 0; --jj) {
+                    const Dispatch &c = d[jj];
+                    if ((c.kind == D_MUL_MAT || c.kind == D_MM_COMPUTE) && same_place(c.dst, nc.src[k])) {
+                        j = jj;
+                        break;
+                    }
+                    places(c, rd, wr);
+                    bool touches = false;
+                    for (const Place &p : wr) touches = touches || same_root(p, nc.src[k]);
+                    if (touches) break;
+                }
+                if (j < 0) continue;
+                Dispatch &mm = d[j];
+                const int32_t mm_id = node_of(mm);
+                MmPartials pp;
+                if (mm.keep_part || mm.scratch_bytes == 0 || readers_[mm_id] != 1 || reader_[mm_id] != add_id ||
+                    !mul_mat_partials(&mm.op, pp))
+                    continue;
+                const tlh_tensor &y = mm.op.t[4];
+                if (y.nb[0] != 4 || y.nb[1] != 4 * y.ne[0] || y.ne[0] != nc.op.t[0].ne[0] ||
+                    y.ne[1] != nc.op.t[0].ne[1] * nc.op.t[0].ne[2] * nc.op.t[0].ne[3] || y.ne[2] != 1 || y.ne[3] != 1 ||
+                    nc.op.t[0].ne[0] % 4 != 0)
+                    continue;
+                if (k == 0) {  // the partials become q: p + q is q + p, bit for bit
+                    std::swap(nc.src[0], nc.src[1]);
+                    std::swap(nc.op.t[0], nc.op.t[1]);
+                }
+                mm.keep_part = 1;
+                nc.pp_disp = j;
+                nc.pp_off = pp.off;
+                nc.pp_chunks = pp.chunks;
+                nc.pp_cstride = pp.cstride;
+                // the MUL_MAT's scratch lives until the norm chain
+                if (mm.block <= -2) {
+                    Group &gr = groups_[-2 - mm.block];
+                    gr.last = std::max<int64_t>(gr.last, nc.pos_last);
+                } else {
+                    Group gr;
+                    gr.first = mm.pos;
+                    gr.last = nc.pos_last;
+                    gr.bytes = mm.scratch_bytes;
+                    gr.leader = j;
+                    mm.block = -2 - (int)groups_.size();
+                    groups_.push_back(gr);
+                }
+                break;
+            }
+        }
+    }
+
     std::map<std::vector<int64_t>, int64_t> rt_tables_;  // rotation table offset per key
     int64_t rt_bytes_ = 0;
 
@@ -1734,9 +1809,15 @@ struct tlh_program {
             void *scratch = x.block >= 0 ? arena + low.blocks[x.block].off : nullptr;
             tlh_status st;
             switch (x.kind) {
-            case D_MUL_MAT: st = tlh_mul_mat(&x.op, src[0], src[1], dst, scratch, x.scratch_bytes, s); break;
+            case D_MUL_MAT:
+                st = x.keep_part ? mul_mat_compute_keep(&x.op, src[0], src[1], scratch, x.scratch_bytes, dst, s)
+                                 : tlh_mul_mat(&x.op, src[0], src[1], dst, scratch, x.scratch_bytes, s);
+                break;
             case D_MM_QUANTIZE: st = tlh_mul_mat_quantize(&x.op, src[1], scratch, x.scratch_bytes, s); break;
-            case D_MM_COMPUTE: st = tlh_mul_mat_compute(&x.op, src[0], scratch, x.scratch_bytes, dst, s); break;
+            case D_MM_COMPUTE:
+                st = x.keep_part ? mul_mat_compute_keep(&x.op, src[0], nullptr, scratch, x.scratch_bytes, dst, s)
+                                 : tlh_mul_mat_compute(&x.op, src[0], scratch, x.scratch_bytes, dst, s);
+                break;
             case D_FLASH_ATTN:
                 st = tlh_flash_attn_ext(&x.op, src[0], src[1], src[2], src[3], dst, scratch, x.scratch_bytes, s);
                 break;
@@ -1748,7 +1829,15 @@ struct tlh_program {
                     qo.rows = x.nq_rows;
                     qo.f16 = x.nq_f16 != 0;
                 }
-                st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s, x.nq_type ? &qo : nullptr);
+                NormPartials qp;
+                if (x.pp_disp >= 0) {
+                    const Dispatch &mm = low.d[x.pp_disp];
+                    qp.part = (const float *)(arena + low.blocks[mm.block].off + x.pp_off);
+                    qp.chunks = x.pp_chunks;
+                    qp.cstride = x.pp_cstride;
+                }
+                st = launch_norm_chain(x.op, src[0], src[1], src[2], src[3], dst, s, x.nq_type ? &qo : nullptr,
+                                       x.pp_disp >= 0 ? &qp : nullptr);
                 break;
             }
             case D_PAGED_ATTN: {

@@ -469,12 +469,13 @@ tlh_status launch_gemm(const MatmulArgs &a, hipStream_t stream) {
     if (ks > 1 && !a.part) return set_error(TLH_INVALID, "gemm: a K split of %d needs a partials buffer", ks);
     if (a.wtype == TLH_TYPE_Q8_0 || a.wtype == TLH_TYPE_Q4_0) {
         const tlh_status st = launch_gemm_q8(a, ks, stream);
-        return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
+        return st != TLH_OK || ks == 1 || a.keep_part ? st : launch_partial_reduce(a, ks, stream);
     }
     if (a.wtype == TLH_TYPE_Q4_K || a.wtype == TLH_TYPE_Q5_K) {
         const tlh_status st = launch_gemm_q4k(a, ks, stream);
-        return st != TLH_OK || ks == 1 ? st : launch_partial_reduce(a, ks, stream);
+        return st != TLH_OK || ks == 1 || a.keep_part ? st : launch_partial_reduce(a, ks, stream);
     }
+    if (a.keep_part) return set_error(TLH_UNSUPPORTED, "gemm: no kept partials for weight type %d", a.wtype);
     for (int64_t c = 0; c < a.N; c += 16) {
         MatmulArgs s = a;
         s.n0 = a.n0 + c;

@@ -1510,6 +1510,12 @@ static int64_t sk_share(int64_t K, int64_t &chunks) {
     return (units + chunks - 1) / chunks;  // equal shares, so no chunk is left with a sliver
 }
 
+int64_t gemv_mfma_chunks(int64_t K) {
+    int64_t chunks = 1;
+    (void)sk_share(K, chunks);
+    return chunks;
+}
+
 int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches) {
     int64_t chunks = 1;
     (void)sk_share(K, chunks);
@@ -1543,7 +1549,7 @@ static tlh_status launch_sk_form(const MatmulArgs &a, hipStream_t stream, const 
         return set_error(TLH_UNSUPPORTED, "gemv_mfma: the store epilogue takes one K chunk");
     hipLaunchKernelGGL(kern, dim3(gx, (unsigned)chunks, (unsigned)batches), dim3(64 * nw), lds, stream, k, share, ep);
     tlh_status st = check_launch(PAIR ? "gemv_mfma (pairs)" : "gemv_mfma");
-    if (st != TLH_OK || chunks == 1) return st;
+    if (st != TLH_OK || chunks == 1 || a.keep_part) return st;
     return launch_partial_reduce(a, (int)chunks, stream);
 }
 

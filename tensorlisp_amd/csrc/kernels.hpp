@@ -76,6 +76,9 @@ struct MatmulArgs {
     // into dst + e * d_nb2 + t * d_nb3. An id outside [0, id_nas) gives NaN.
     const char *ids;
     int64_t ids_nb0, ids_nb1, id_b1, id_nas;
+    // K-split launches leave their partials in `part` without the chunk-sum
+    // launch (a consumer adds them: mul_mat_compute_keep)
+    int keep_part;
 };
 
 // Batch slice z of a MUL_MAT launch: i12 = z % ne12, i13 = z / ne12 and the
@@ -191,6 +194,7 @@ tlh_status launch_gemv_reg_pro(const MatmulArgs &a, const GemvPro &pro, const fl
 // the scratch. K > 4096 needs a.part: gemv_mfma_partial_bytes of scratch.
 bool gemv_mfma_supported(int64_t N);
 int64_t gemv_mfma_partial_bytes(int64_t K, int64_t M, int64_t N, int64_t batches);
+int64_t gemv_mfma_chunks(int64_t K);  // the few-column kernel's K chunks
 tlh_status launch_gemv_mfma(const MatmulArgs &a, hipStream_t stream);
 // launch_gemv_mfma with GemvEpi's store epilogue over the columns (token n =
 // column n): segments, q4_K / q5_K / q6_K, one K chunk; TLH_UNSUPPORTED otherwise.
@@ -243,6 +247,21 @@ tlh_status mul_mat_compute_multi(const tlh_op *const *ops, const void *const *w,
                                  const void *scratch, size_t scratch_bytes, hipStream_t stream,
                                  const GemvEpi *epi = nullptr);
 bool mul_mat_multi_ok(const tlh_op *const *ops, int n);
+// Where a MUL_MAT's K-split product leaves its partial sums [chunk][N][M] in
+// the node's scratch (byte offset, chunks > 1, chunk stride in floats), for a
+// consumer that adds them itself; false when the node's product does not split
+// K in a form this covers (N 3..16 few-column, or the q8_0 / q4_0 / q4_K /
+// q5_K GEMM; one batch slice). mul_mat_compute_keep runs the node's product
+// (after quantizing src1 into the scratch when src1 is given) without the
+// chunk sum.
+struct MmPartials {
+    int64_t off = 0;
+    int chunks = 1;
+    int64_t cstride = 0;
+};
+bool mul_mat_partials(const tlh_op *op, MmPartials &pp);
+tlh_status mul_mat_compute_keep(const tlh_op *op, const void *src0, const void *src1, void *scratch,
+                                size_t scratch_bytes, void *dst, hipStream_t stream);
 tlh_status mul_mat_multi(const tlh_op *const *ops, const void *const *w, void *const *dst, int n, const void *x,
                          hipStream_t stream);
 // mul_mat_multi with a GemvPro prologue and / or SwiGLU epilogue (executor
@@ -266,8 +285,16 @@ constexpr int64_t NORM_CHAIN_QUANT_MAX = 4096;
 // op: t0 p (or x), t1 q, t2 w, t3 s, t4 y; x0 rms, x1 eps bits, x2 with the ADD.
 // With qo, y is also quantized into qo's scratch (norm_chain_quantize_ok).
 bool norm_chain_quantize_ok(const tlh_op &op, int act_type);
+// qp (chunks > 1): q is not read; its rows are the sums, in chunk order, of the
+// K-split partials a MUL_MAT left (mul_mat_compute_keep): row r element i at
+// part + c * cstride + r * ne0 + i.
+struct NormPartials {
+    const float *part = nullptr;
+    int chunks = 0;
+    int64_t cstride = 0;
+};
 tlh_status launch_norm_chain(const tlh_op &op, const void *p, const void *q, const void *w, void *s, void *y,
-                             hipStream_t stream, const ActQuantOut *qo = nullptr);
+                             hipStream_t stream, const ActQuantOut *qo = nullptr, const NormPartials *qp = nullptr);
 // GGML_OP_GLU (the core op's operands, f32 rows of unit element stride) that
 // also quantizes its output rows into qo (row length a multiple of qo's block).
 bool glu_quantize_ok(const tlh_op &op, int act_type);

@@ -787,6 +787,48 @@ tlh_status tlh_mul_mat_quantize(const tlh_op *op, const void *src1, void *scratc
 }
 
 tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *scratch, size_t scratch_bytes,
+                               void *dst, void *stream);
+
+}  // extern "C"
+
+bool tlh::mul_mat_partials(const tlh_op *op, MmPartials &pp) {
+    MulMatShape s;
+    if (check_mul_mat(op, s) != TLH_OK || mm_empty(s) || s.flt || s.ne12 * s.ne13 != 1 || s.N < 3) return false;
+    int64_t chunks;
+    if (s.N > 16) {
+        if (s.wtype != TLH_TYPE_Q8_0 && s.wtype != TLH_TYPE_Q4_0 && s.wtype != TLH_TYPE_Q4_K && s.wtype != TLH_TYPE_Q5_K)
+            return false;
+        chunks = gemm_ksplit(s.wtype, s.M, s.N, s.K, 1);
+    } else {
+        chunks = gemv_mfma_chunks(s.K);  // (the tall form takes K <= 4096: one chunk)
+    }
+    if (chunks < 2) return false;
+    pp.off = mm_act_bytes(s);
+    pp.chunks = (int)chunks;
+    pp.cstride = s.N * s.M;
+    return true;
+}
+
+tlh_status tlh::mul_mat_compute_keep(const tlh_op *op, const void *src0, const void *src1, void *scratch,
+                                     size_t scratch_bytes, void *dst, hipStream_t hs) {
+    MulMatShape s;
+    tlh_status st = check_mul_mat(op, s);
+    if (st != TLH_OK) return st;
+    MmPartials pp;
+    if (!mul_mat_partials(op, pp)) return set_error(TLH_UNSUPPORTED, "mul_mat_compute_keep: no K split here");
+    if (!src0 || !dst) return set_error(TLH_INVALID, "mul_mat_compute_keep: null tensor pointer");
+    if ((st = mm_check_scratch(s, scratch, scratch_bytes)) != TLH_OK) return st;
+    if (((uintptr_t)src0 & 1) || ((uintptr_t)dst & 3))
+        return set_error(TLH_INVALID, "mul_mat: misaligned src0 (2 bytes) or dst (4 bytes)");
+    if (src1 && (st = mm_quantize(op, s, src1, scratch, hs)) != TLH_OK) return st;
+    MatmulArgs m = mm_args(op, s, src0, scratch, dst);
+    m.keep_part = 1;
+    return s.N <= 16 ? launch_gemv(m, nullptr, 0, hs) : launch_gemm(m, hs);
+}
+
+extern "C" {
+
+tlh_status tlh_mul_mat_compute(const tlh_op *op, const void *src0, const void *scratch, size_t scratch_bytes,
                                void *dst, void *stream) {
     MulMatShape s;
     tlh_status st = check_mul_mat(op, s);

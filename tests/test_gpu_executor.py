@@ -256,6 +256,49 @@ def test_glu_quantizes_for_its_mul_mats(gpu, t, K, n, op, group):
     assert prog.stats()["launches"] == 1 + (2 if apart else 1)
 
 
+@pytest.mark.parametrize("t,K,n,order", [(N.Q4_K, 14336, 16, 0), (N.Q4_K, 14336, 8, 1), (N.Q4_0, 8192, 5, 0),
+                                         (N.Q4_K, 4096, 512, 0), (N.Q8_0, 4096, 512, 1)])
+def test_k_split_partials_summed_by_the_norm_chain(gpu, t, K, n, order):
+    """A K-split MUL_MAT whose only reader is the ADD of a norm chain (the
+    down or output projection, then the residual ADD and the next RMS_NORM)
+    leaves its chunk partials, and the norm chain adds them in chunk order as
+    it reads them: the chunk-sum launch goes. The residual sum and the norm's
+    output are bit-identical to the same graph with the product kept as an
+    output (which keeps the chunk-sum launch), with the product as either
+    operand of the ADD; few-column and GEMM forms."""
+    import torch
+
+    from tensorlisp_amd import synth
+
+    M = 4096
+    outs = {}
+    for keep in (False, True):
+        b = G.Builder()
+        x = b.input(N.F32, [M, n])
+        h = b.input(N.F32, [K, n])
+        nw = b.weight(N.F32, [M])
+        W = b.weight(t, [K, M])
+        y = b.mul_mat(W, h)
+        s = b.add(y, x) if order else b.add(x, y)
+        z = b.mul(b.rms_norm(s, 1e-5), nw)
+        b.expand(z)
+        wanted = [z, s] + ([y] if keep else [])
+        prog = G.Program(b, wanted, [dev((1.0 + 0.1 * synth.normal(121, (M,))).astype(np.float32)),
+                                     dev(synth.random_blocks(t, 122, M, K))])
+        prog.write_input(0, dev(synth.normal(123, (n, M))))
+        prog.write_input(1, dev(synth.normal(124, (n, K))))
+        print(f"[partials-norm] {N.TYPE_NAMES[t]} K={K} n={n} order={order} keep={keep}", flush=True)
+        trace = prog.trace()  # one eager run, recording each dispatch's kernel launches
+        sums = sum(labels.count("partial_reduce") for _, labels in trace)
+        outs[keep] = ([prog.read(v, torch.float32).cpu().numpy() for v in (z, s)], sums)
+        torch.cuda.synchronize()
+    (zf, sf), rf = outs[False]
+    (zk, sk), rk = outs[True]
+    assert np.array_equal(sf.view(np.uint32), sk.view(np.uint32))
+    assert np.array_equal(zf.view(np.uint32), zk.view(np.uint32))
+    assert (rf, rk) == (0, 1), (rf, rk)  # the chunk-sum launch goes only where the product is not kept
+
+
 NQ_TYPES = [N.Q4_K, N.Q5_K, N.Q6_K, N.Q4_0, N.Q8_0, N.Q4_1, N.Q5_0]
 
 
