@@ -99,13 +99,43 @@ __device__ __forceinline__ uint16_t merge_parts(const float *base, int np, int d
     return f2h(a * (1.0f / (lsum + 1e-6f)));
 }
 
+// The merged outputs of a workgroup's gc heads (f32 values of the f16
+// results, in LDS) quantized to q8_K for the output projection: the heads'
+// outputs are whole q8_K blocks of the sequence's row (the launcher's check);
+// one wave per block, four consecutive values a lane, as the quantize launch
+// takes them.
+template <int HS, int W>
+__device__ __forceinline__ void quantize_heads(const float *sq, int gc, int num_heads, int head0, int seq, void *qout,
+                                               int64_t qrows) {
+    const int64_t K = (int64_t)num_heads * HS;
+    const ActLayout QL = act_layout(TLH_TYPE_Q8_K, K, qrows, false);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int b = wave; b < gc * HS / QKK; b += W) {
+        float v[1][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[0][i] = sq[QKK * b + 4 * lane + i];
+        uint32_t packed[1];
+        int psum[1];
+        float dq[1];
+        q8K_waves<1>(v, lane, packed, psum, dq);
+        q8K_store_split((char *)qout, QL, K, seq, (int64_t)head0 * HS / QKK + b, lane, packed[0], psum[0], dq[0],
+                        false);
+    }
+}
+
 // MERGE (one launch): after writing its partial, a workgroup counts itself
 // in on its (sequence, head group) counter; the last of the sequence's
 // partitions to arrive merges them all into the output and sets the counter
 // back to zero. The counters start at zero (the caller's zeroed buffer) and
 // launches that share them must be stream-ordered.
-template <int HS, int BS, bool PIPE, int PART, bool MERGE>
-__global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
+//
+// WHOLE (W waves, one partition covering the whole context, PART >= every
+// length): the workgroup's wave merge is the final merge, so the output is
+// written straight from it (merge_parts of one partition gives the same
+// value), with no scratch, counter or read-back round trip: for short
+// contexts over few workgroups, where those round trips are most of the time.
+template <int HS, int BS, bool PIPE, int PART, bool MERGE, int W = PA_WAVES, bool WHOLE = false>
+__global__ void __launch_bounds__(64 * W) k_paged_attn(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
                                                     const uint16_t *__restrict__ vc,
                                                     const int32_t *__restrict__ tables,
                                                     const int32_t *__restrict__ lens, int num_heads, int num_kv_heads,
@@ -115,8 +145,9 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
                                                     void *__restrict__ qout, int64_t qrows) {
     constexpr int KS = HS / 16;  // QK steps = PV output tiles
     __shared__ int s_bt[PART / 8];
-    __shared__ float s_m[PA_WAVES][16], s_l[PA_WAVES][16];
-    __shared__ float s_acc[PA_WAVES][16][HS];
+    constexpr int HR = WHOLE ? 4 : 16;  // head rows kept (the one-partition form takes gc <= 4)
+    __shared__ float s_m[W][16], s_l[W][16];
+    __shared__ float s_acc[W][HR][HS];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -156,10 +187,10 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
     const int64_t kv_stride_blk = (int64_t)num_kv_heads * HS * BS;  // elements per block
     const int64_t head_off = (int64_t)kvh * HS * BS;
     const int ntiles = (t1 - t0 + 15) / 16;
-    const int my_tiles = ntiles > wave ? (ntiles - wave + PA_WAVES - 1) / PA_WAVES : 0;
-    // tile k of this wave: tokens t0 + 16 * (wave + PA_WAVES * k) ...
+    const int my_tiles = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
+    // tile k of this wave: tokens t0 + 16 * (wave + W * k) ...
     auto load_tile = [&](int k, half4_t (&ka)[KS], half4_t (&vb)[KS]) {
-        const int tk = 16 * (wave + PA_WAVES * k);  // first token of the tile, relative to t0
+        const int tk = 16 * (wave + W * k);  // first token of the tile, relative to t0
         // keys: token tk + c at slot (t0 + tk + c) % BS of partition page
         // (t0 % BS + tk + c) / BS. A tile's tokens past the context can lie on
         // a page past the sequence's last (block size 8): those read the last
@@ -178,7 +209,7 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
         for (int n = 0; n < KS; ++n) vb[n] = __builtin_bit_cast(half4_t, *(const uint2 *)(vp + 16 * n * BS));
     };
     auto compute_tile = [&](int k, const half4_t (&ka)[KS], const half4_t (&vin)[KS]) {
-        const int tk = t0 + 16 * (wave + PA_WAVES * k);
+        const int tk = t0 + 16 * (wave + W * k);
         f32x4_t S = (f32x4_t){};
 #pragma unroll
         for (int st = 0; st < KS; ++st) S = mfma16(ka[st], qb[st], S);
@@ -249,19 +280,31 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
 #pragma unroll
     for (int n = 0; n < KS; ++n)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s_acc[wave][4 * g + r][16 * n + c] = o[n][r];
+        for (int r = 0; r < 4; ++r)
+            if (HR == 16 || g == 0) s_acc[wave][4 * g + r][16 * n + c] = o[n][r];
     __syncthreads();
     for (int e = threadIdx.x; e < gc * HS; e += blockDim.x) {
         const int h = e / HS, d = e % HS;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < PA_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][h]);
         float lsum = 0.0f, a = 0.0f;
 #pragma unroll
-        for (int w = 0; w < PA_WAVES; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float f = s_m[w][h] == -INFINITY ? 0.0f : __expf(s_m[w][h] - M);
             lsum += f * s_l[w][h];
             a += f * s_acc[w][h][d];
+        }
+        if constexpr (WHOLE) {
+            // merge_parts over one partition: exp(0) = 1 weighs it, so its
+            // value is a * (1 / (lsum + 1e-6)) rounded to f16
+            const uint16_t r = f2h(a * (1.0f / (lsum + 1e-6f)));
+            const int64_t o = ((int64_t)seq * num_heads + head0 + h) * HS + d;
+            if (out32) out32[o] = h2f(r);
+            else out[o] = r;
+            // s_acc[0][h][d], read above by this thread alone
+            if (qout) s_acc[0][0][e] = h2f(r);
+            continue;
         }
         float *slotp = part_slot<HS>(scratch, seq, head0 + h, part, num_heads, P);
         // the one-launch form's partials are agent-scope stores: coherent
@@ -275,6 +318,13 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
             put(slotp, M);
             put(slotp + 1, lsum);
         }
+    }
+    if constexpr (WHOLE) {
+        if (qout) {
+            __syncthreads();
+            quantize_heads<HS, W>(&s_acc[0][0][0], gc, num_heads, head0, seq, qout, qrows);
+        }
+        return;
     }
     if constexpr (MERGE) {
         // Every wave's partial stores complete before the barrier (the
@@ -321,24 +371,8 @@ __global__ void __launch_bounds__(256) k_paged_attn(const uint16_t *__restrict__
             if (qout) sq[e] = h2f(r);
         }
         if (qout) {
-            // the heads' outputs are whole q8_K blocks of the sequence's row
-            // (the launcher's check): one wave per block, four consecutive
-            // values a lane, as the quantize launch takes them
             __syncthreads();
-            const int64_t K = (int64_t)num_heads * HS;
-            const ActLayout QL = act_layout(TLH_TYPE_Q8_K, K, qrows, false);
-            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-            for (int b = wave; b < gc * HS / QKK; b += PA_WAVES) {
-                float v[1][4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[0][i] = sq[QKK * b + 4 * lane + i];
-                uint32_t packed[1];
-                int psum[1];
-                float dq[1];
-                q8K_waves<1>(v, lane, packed, psum, dq);
-                q8K_store_split((char *)qout, QL, K, seq, (int64_t)head0 * HS / QKK + b, lane, packed[0], psum[0],
-                                dq[0], false);
-            }
+            quantize_heads<HS, W>(sq, gc, num_heads, head0, seq, qout, qrows);
         }
     }
 }
@@ -372,6 +406,25 @@ static int pa_part(const tlh_paged_attention_args &a) {
     return pa_workgroups(a, 128) >= 256 ? PA_PART / 2 : PA_PART_SMALL;
 }
 
+// query heads per workgroup: a divisor of the group size, at most 16
+static int pa_gc(const tlh_paged_attention_args &a) {
+    const int G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
+    int gc = G < 16 ? G : 16;
+    while (gc > 1 && G % gc) --gc;
+    return gc > 0 ? gc : 1;
+}
+
+// The one-partition form: contexts up to PA_WHOLE tokens, one workgroup of
+// PA_WHOLE_WAVES waves per (sequence, kv head), while those workgroups
+// number 64 to 256 (fewer leave too few CUs pulling each context) and the
+// group has at most 4 query heads.
+constexpr int PA_WHOLE = 1024, PA_WHOLE_WAVES = 8;
+static bool pa_whole(const tlh_paged_attention_args &a) {
+    const int G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
+    const int64_t wgs = (int64_t)a.num_seqs * a.num_kv_heads * (G / pa_gc(a));
+    return a.head_size <= 128 && a.max_context_len <= PA_WHOLE && pa_gc(a) <= 4 && wgs >= 64 && wgs <= 256;
+}
+
 static int pa_partitions(const tlh_paged_attention_args &a) {
     const int part = pa_part(a);
     return a.max_context_len > 0 ? (a.max_context_len + part - 1) / part : 1;
@@ -392,14 +445,6 @@ size_t paged_attention_scratch_bytes(const tlh_paged_attention_args &a) {
     const int64_t G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
     const int64_t bound = 510 * G * (a.head_size + 2) * (int64_t)sizeof(float);
     return (size_t)(bytes(PA_PART / 2) + std::min(bytes(PA_PART_SMALL), bound));
-}
-
-// query heads per workgroup: a divisor of the group size, at most 16
-static int pa_gc(const tlh_paged_attention_args &a) {
-    const int G = a.num_kv_heads > 0 ? a.num_heads / a.num_kv_heads : 1;
-    int gc = G < 16 ? G : 16;
-    while (gc > 1 && G % gc) --gc;
-    return gc > 0 ? gc : 1;
 }
 
 bool paged_attention_quantize_ok(const tlh_paged_attention_args &a, int act_type) {
@@ -435,6 +480,19 @@ static void launch_pa3(const tlh_paged_attention_args &a, float *scratch, hipStr
 template <int HS, int BS>
 static void launch_pa2(const tlh_paged_attention_args &a, float *scratch, hipStream_t stream, float *out32,
                        unsigned *counters, const ActQuantOut *qo) {
+    if constexpr (HS <= 128) {
+        if (pa_whole(a)) {  // no scratch or counters; both forms take it
+            const int gc = pa_gc(a), G = a.num_heads / a.num_kv_heads;
+            const dim3 grid(a.num_kv_heads * (G / gc), a.num_seqs, 1);
+            hipLaunchKernelGGL((k_paged_attn<HS, BS, true, PA_WHOLE, false, PA_WHOLE_WAVES, true>), grid,
+                               dim3(64 * PA_WHOLE_WAVES), 0, stream, (const uint16_t *)a.q,
+                               (const uint16_t *)a.k_cache, (const uint16_t *)a.v_cache, a.block_tables,
+                               a.context_lens, a.num_heads, a.num_kv_heads, gc, a.max_blocks_per_seq, a.scale, 1,
+                               nullptr, nullptr, (uint16_t *)a.out, out32, qo ? qo->out : nullptr,
+                               qo ? qo->rows : (int64_t)0);
+            return;
+        }
+    }
     switch (pa_part(a)) {
     case PA_PART: launch_pa3<HS, BS, PA_PART>(a, scratch, stream, out32, counters, qo); break;
     case PA_PART / 2: launch_pa3<HS, BS, PA_PART / 2>(a, scratch, stream, out32, counters, qo); break;

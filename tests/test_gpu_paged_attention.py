@@ -59,6 +59,11 @@ CASES = [
     (128, 16, 1, 4, [515, 5]),
     (128, 16, 8, 32, [512, 1, 1024, 513]),
     (128, 8, 2, 6, [77, 300]),  # group of 3 query heads per kv head
+    # 64..256 workgroups of (sequence, kv head) and contexts up to 1024 tokens:
+    # the one-partition form (8 waves over the whole context, no merge)
+    (128, 16, 8, 32, [1, 1024, 513, 37, 700, 16, 17, 300]),
+    (64, 8, 8, 24, [5, 77, 1000, 8, 9, 256, 511, 33]),  # groups of 3, 8-token pages
+    (96, 32, 16, 32, [100, 1, 900, 64, 65, 31, 32, 512]),  # groups of 2, 128 workgroups
     # 4 sequences x 8 kv heads x ceil(8192 / 512) = 512 workgroups: these take the
     # 512-token partitions (fewer workgroups would take 256-token ones), at block
     # sizes 8 and 32 and head sizes 64 and 256
@@ -228,6 +233,7 @@ def test_cache_write_then_attention_matches_dense(gpu):
     (128, 16, 8, 32, [512, 1, 1024, 513]),
     (64, 8, 8, 32, [8192, 100, 3000, 511]),   # 512-token partitions
     (128, 16, 2, 6, [0, 300, 2049]),          # an empty context, a group of 3
+    (128, 16, 8, 32, [0, 300, 1024, 5, 64, 65, 17, 900]),  # one partition (64 workgroups)
 ])
 def test_one_launch_merge_matches_two_launches(gpu, hs, bs, kvh, heads, lens):
     """A paged-attention node in a program runs as one launch whose last
