@@ -64,6 +64,7 @@ CASES = [
     (128, 16, 8, 32, [1, 1024, 513, 37, 700, 16, 17, 300]),
     (64, 8, 8, 24, [5, 77, 1000, 8, 9, 256, 511, 33]),  # groups of 3, 8-token pages
     (96, 32, 16, 32, [100, 1, 900, 64, 65, 31, 32, 512]),  # groups of 2, 128 workgroups
+    (128, 16, 8, 32, [1, 512, 300, 37, 16, 17, 255, 500]),  # contexts of at most 512 tokens
     # 4 sequences x 8 kv heads x ceil(8192 / 512) = 512 workgroups: these take the
     # 512-token partitions (fewer workgroups would take 256-token ones), at block
     # sizes 8 and 32 and head sizes 64 and 256
