@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(256) k_quantize_q8_K(const float *__restrict__
     const int lane = threadIdx.x & 63;
     const int64_t nblk = K / QKK;
     if (wave >= nblk * rows) return;
-    const int64_t row = wave / nblk;
+    const int64_t row = rows == 1 ? 0 : wave / nblk;  // one row (a decode step): no 64-bit division
     const int64_t blk = wave - row * nblk;
     const float *src = (const float *)((const char *)x + row * x_row_bytes) + blk * QKK + 4 * lane;
     float v[1][4];
